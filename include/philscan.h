@@ -1,0 +1,136 @@
+/*
+ * philscan — C ABI of the MI355X (gfx950) linear-recurrence kernels.
+ *
+ * Every entry point computes, per batch row b and step t (row-major,
+ * contiguous buffers, device pointers):
+ *
+ *     h[b,t] = A[b,t] h[b,t-1] + x[b,t],   h[b,-1] = zi[b]
+ *
+ * and writes the states after consuming x[b,t]: the exact output contract of
+ * philtorch's `philtorch::*` operators (philtorch/csrc/host_recur2.cpp:162-171).
+ * The `_bwd` entry points compute, in one fused reverse-time pass, the
+ * gradients of that output for an upstream gradient `grad_y`:
+ *
+ *     lambda[t] = grad_y[t] + A[t+1]^H lambda[t+1],  lambda[T-1] = grad_y[T-1]
+ *     grad_x[t] = lambda[t]
+ *     grad_A[t] = lambda[t] conj(h[t-1])^T   (summed where A is shared)
+ *     grad_zi   = A[0]^H lambda[0]
+ *
+ * which is what philtorch's registered backward closures compute
+ * (philtorch/__init__.py:34-148).
+ *
+ * Conventions
+ *   - `dtype` is a phs_dtype; all pointers of one call share it.
+ *   - complex values are interleaved (re, im) pairs, as torch stores them.
+ *   - every call is asynchronous on `stream` (a hipStream_t; NULL = the
+ *     default stream), never synchronises and never allocates: the caller
+ *     passes `workspace` of at least phs_workspace_size(...) bytes (a larger
+ *     one is fine; pass its full size).  The workspace must be zero-filled
+ *     once before its first use; every call leaves it ready for the next, so
+ *     nothing is cleared per call.  Calls sharing one workspace must be
+ *     ordered (same stream, or synchronised): concurrent calls on one
+ *     workspace race.
+ *   - nullable outputs of the `_bwd` calls are skipped when NULL.
+ *   - return value: PHS_OK or a phs_status error code; inputs are never
+ *     modified; a call with B == 0 or T == 0 does nothing.
+ */
+#ifndef PHILSCAN_H_
+#define PHILSCAN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum phs_dtype { PHS_F32 = 0, PHS_F64 = 1, PHS_C64 = 2, PHS_C128 = 3, PHS_I64 = 4 };
+
+enum phs_op { PHS_OP_RECUR = 0, PHS_OP_LTI_RECUR = 1, PHS_OP_RECUR2 = 2, PHS_OP_LTI_RECUR2 = 3 };
+
+enum phs_status {
+  PHS_OK = 0,
+  PHS_ERR_INVALID = 1,   /* bad size, null required pointer, unsupported combination */
+  PHS_ERR_WORKSPACE = 2, /* workspace NULL or smaller than phs_workspace_size() */
+  PHS_ERR_LAUNCH = 3,    /* the HIP runtime rejected a kernel launch */
+  PHS_ERR_DTYPE = 4      /* dtype not one of phs_dtype */
+};
+
+/* Bytes of workspace that one call of `op` needs (backward != 0 for the
+ * `_bwd` entry point).  `coef_shared` is the same flag the call receives. */
+size_t phs_workspace_size(int op, int dtype, int64_t B, int64_t T, int coef_shared, int backward);
+
+/* Human-readable text of a phs_status code (static storage). */
+const char *phs_error_string(int status);
+
+/* ABI version of this library (major*100 + minor). */
+int phs_abi_version(void);
+
+/* LPV scalar scan.  A: [B,T] (coef_shared=0) or [T] shared by all rows
+ * (coef_shared=1); zi: [B]; x, y: [B,T].
+ * Replaces philtorch::recurN with 1x1 matrices, the only native time-varying
+ * scalar scan of the reference: host_recurN.cpp:236-281 (CPU impl registered
+ * at :285); the reference's lpv.linear_recurrence (lpv/recur.py:20-101) has
+ * no native op of its own. */
+int phs_recur_fwd(int dtype, int64_t B, int64_t T, const void *A, int coef_shared, const void *zi,
+                  const void *x, void *y, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Backward of phs_recur_fwd.  y: the forward output.  grad_A: [B,T], or [T]
+ * when coef_shared (summed over rows).  grad_zi: [B].  grad_x: [B,T].
+ * Replaces the recurN autograd closure philtorch/__init__.py:34-73. */
+int phs_recur_bwd(int dtype, int64_t B, int64_t T, const void *A, int coef_shared, const void *zi,
+                  const void *y, const void *grad_y, void *grad_x, void *grad_A, void *grad_zi,
+                  void *workspace, size_t workspace_bytes, void *stream);
+
+/* LTI scalar scan.  a: [B] (coef_shared=0) or one value shared by all rows
+ * (coef_shared=1); zi: [B]; x, y: [B,T].
+ * Replaces lti_recur_cuda_impl, philtorch/csrc/lti_recur.cu:113-158
+ * (registered at :160; CPU twin host_lti_recur.cpp:42-80). */
+int phs_lti_recur_fwd(int dtype, int64_t B, int64_t T, const void *a, int coef_shared,
+                      const void *zi, const void *x, void *y, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
+/* Backward of phs_lti_recur_fwd.  grad_a: [B], or one value when
+ * coef_shared: sum_t conj(h[t-1]) lambda[t], reduced deterministically.
+ * Replaces _lti_recur_backward, philtorch/__init__.py:115-148. */
+int phs_lti_recur_bwd(int dtype, int64_t B, int64_t T, const void *a, int coef_shared,
+                      const void *zi, const void *y, const void *grad_y, void *grad_x,
+                      void *grad_a, void *grad_zi, void *workspace, size_t workspace_bytes,
+                      void *stream);
+
+/* LPV 2x2 scan.  A: [B,T,2,2] (coef_shared=0) or [T,2,2] (coef_shared=1);
+ * zi: [B,2]; x, y: [B,T,2].
+ * Replaces mat_recur_second_order_cuda_impl, philtorch/csrc/recur2.cu:69-117
+ * (registered at :119-122; CPU twin host_recurN.cpp:236-281). */
+int phs_recur2_fwd(int dtype, int64_t B, int64_t T, const void *A, int coef_shared, const void *zi,
+                   const void *x, void *y, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Backward of phs_recur2_fwd.  grad_A: [B,T,2,2], or [T,2,2] when
+ * coef_shared.  grad_zi: [B,2].  grad_x: [B,T,2].
+ * Replaces the recur2 autograd closure philtorch/__init__.py:34-73. */
+int phs_recur2_bwd(int dtype, int64_t B, int64_t T, const void *A, int coef_shared,
+                   const void *zi, const void *y, const void *grad_y, void *grad_x, void *grad_A,
+                   void *grad_zi, void *workspace, size_t workspace_bytes, void *stream);
+
+/* LTI 2x2 scan.  A: [B,2,2] (coef_shared=0) or [2,2] (coef_shared=1);
+ * zi: [B,2]; x, y: [B,T,2].
+ * Replaces lti_mat_recur_second_order_cuda_impl,
+ * philtorch/csrc/lti_recur2.cu:66-113 (registered at :115-118; CPU twin
+ * host_lti_recurN.cpp:147-192). */
+int phs_lti_recur2_fwd(int dtype, int64_t B, int64_t T, const void *A, int coef_shared,
+                       const void *zi, const void *x, void *y, void *workspace,
+                       size_t workspace_bytes, void *stream);
+
+/* Backward of phs_lti_recur2_fwd.  grad_A: [B,2,2], or [2,2] when
+ * coef_shared, sum_t lambda[t] conj(h[t-1])^T.
+ * Replaces the lti_recur2 autograd closure philtorch/__init__.py:76-112. */
+int phs_lti_recur2_bwd(int dtype, int64_t B, int64_t T, const void *A, int coef_shared,
+                       const void *zi, const void *y, const void *grad_y, void *grad_x,
+                       void *grad_A, void *grad_zi, void *workspace, size_t workspace_bytes,
+                       void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PHILSCAN_H_ */

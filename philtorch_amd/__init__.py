@@ -1,0 +1,254 @@
+"""philtorch_amd — MI355X-native linear-recurrence core with philtorch's API.
+
+Importing the package loads ``_C.so`` (the torch.library layer over the HIP
+kernels of ``libphilscan.so``), which defines the ``philtorch`` operator
+namespace: the reference's five ops (``recur2``, ``recurN``, ``lti_recur2``,
+``lti_recurN``, ``lti_recur``; philtorch/csrc/host_recur2.cpp:162-171), the new
+LPV scalar op ``recur`` and four fused backward ops.  This module then
+registers fake (meta) kernels and autograd formulas for them, as
+philtorch/__init__.py:157-268 does for its ops.
+
+Backward: without ``create_graph`` the registered formula calls the fused
+single-pass adjoint kernel (``*_backward`` ops).  With ``create_graph`` it
+falls back to the composite formula written with the same ops, which is
+differentiable again (gradgradcheck).
+
+If the extension is missing, ``EXTENSION_LOADED`` is False and the Python API
+takes philtorch's pure-PyTorch route, as the reference does
+(philtorch/__init__.py:6-12); on a machine with a GPU the import fails instead,
+so a GPU run can never silently lose its kernels
+(set PHILTORCH_AMD_ALLOW_MISSING_EXTENSION=1 to override).
+"""
+from __future__ import annotations
+
+import os
+import warnings
+from typing import Any, Optional
+
+import torch
+
+__version__ = "0.1.0"
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+OPS_LIBRARY = os.path.join(_HERE, "_C.so")
+KERNEL_LIBRARY = os.path.join(_HERE, "libphilscan.so")
+
+
+def _load_extension() -> tuple[bool, Optional[BaseException]]:
+    if not os.path.exists(OPS_LIBRARY):
+        return False, FileNotFoundError(OPS_LIBRARY)
+    try:
+        torch.ops.load_library(OPS_LIBRARY)
+    except (OSError, RuntimeError) as exc:  # pragma: no cover - depends on the build
+        return False, exc
+    return True, None
+
+
+EXTENSION_LOADED, _LOAD_ERROR = _load_extension()
+HELION_LOADED = False  # the Helion backend of the reference is out of scope
+
+if not EXTENSION_LOADED:
+    if torch.cuda.is_available() and not os.environ.get("PHILTORCH_AMD_ALLOW_MISSING_EXTENSION"):
+        raise ImportError(
+            f"philtorch_amd: the HIP extension {OPS_LIBRARY} did not load ({_LOAD_ERROR}); "
+            "build it with `python -m philtorch_amd._build`"
+        )
+    warnings.warn("Custom extension not loaded.")
+
+
+def require_extension() -> None:
+    """Raise unless the native operators are available."""
+    if not EXTENSION_LOADED:
+        raise RuntimeError(
+            f"philtorch_amd native extension not loaded ({_LOAD_ERROR}); "
+            "build it with `python -m philtorch_amd._build`"
+        )
+
+
+# --------------------------------------------------------------------------
+# composite backward formulas (used when create_graph=True)
+#
+# Adjoint of h[t] = A[t] h[t-1] + x[t]:
+#   lambda[t] = g[t] + A[t+1]^H lambda[t+1],  lambda[T-1] = g[T-1]
+#   grad_x = lambda,  grad_zi = A[0]^H lambda[0],  grad_A[t] = lambda[t] conj(h[t-1])^T
+# (philtorch/__init__.py:34-148).  lambda is one more forward scan over the
+# time-reversed sequence with coefficient A[t+1]^H and zero initial state.
+
+
+def _shifted_states(zi: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    """h[t-1] for every t: the initial state followed by all but the last output."""
+    return torch.cat([zi.unsqueeze(1), y[:, :-1]], dim=1)
+
+
+def _recur_composite(A, zi, y, gy, needs):
+    # scalar LPV: A [B, T] or shared [T]
+    coef = torch.roll(A.conj_physical(), -1, dims=-1).flip(-1)
+    lam = torch.ops.philtorch.recur(coef, torch.zeros_like(zi), gy.flip(1)).flip(1)
+    gA = gzi = gx = None
+    if needs[1]:
+        gzi = A.conj_physical()[..., 0] * lam[:, 0]
+    if needs[2]:
+        gx = lam
+    if needs[0]:
+        per_step = lam * _shifted_states(zi, y).conj_physical()
+        gA = per_step if A.dim() == 2 else per_step.sum(0)
+    return gA, gzi, gx
+
+
+def _recurN_composite(A, zi, y, gy, needs):
+    # LPV M x M: A [B, T, M, M] or shared [T, M, M]
+    AH = A.mT.conj_physical()
+    coef = torch.roll(AH, -1, dims=-3).flip(-3)
+    lam = MatrixOps.recur(coef, torch.zeros_like(zi), gy.flip(1)).flip(1)
+    gA = gzi = gx = None
+    if needs[1]:
+        gzi = (AH[..., 0, :, :] @ lam[:, 0, :, None]).squeeze(-1)
+    if needs[2]:
+        gx = lam
+    if needs[0]:
+        per_step = lam.unsqueeze(-1) * _shifted_states(zi, y).conj_physical().unsqueeze(-2)
+        gA = per_step if A.dim() == 4 else per_step.sum(0)
+    return gA, gzi, gx
+
+
+def _lti_recur_composite(A, zi, y, gy, needs):
+    # scalar LTI: A [B] (per row) or a single shared value
+    a_conj = A.conj_physical()
+    lam = torch.ops.philtorch.lti_recur(a_conj, torch.zeros_like(zi), gy.flip(1)).flip(1)
+    gA = gzi = gx = None
+    batched = A.dim() == 1 and A.numel() == gy.size(0)
+    if needs[1]:
+        gzi = lam[:, 0] * (a_conj if batched else a_conj.reshape(()))
+    if needs[2]:
+        gx = lam
+    if needs[0]:
+        per_row = torch.linalg.vecdot(_shifted_states(zi, y), lam)  # sum_t conj(h[t-1]) lambda[t]
+        gA = per_row if batched else per_row.sum().reshape(A.shape)
+    return gA, gzi, gx
+
+
+def _lti_recurN_composite(A, zi, y, gy, needs):
+    # LTI M x M: A [B, M, M] or shared [M, M]
+    AH = A.mT.conj_physical()
+    lam = MatrixOps.lti_recur(AH, torch.zeros_like(zi), gy.flip(1)).flip(1)
+    gA = gzi = gx = None
+    if needs[1]:
+        gzi = (AH @ lam[:, 0, :, None]).squeeze(-1)
+    if needs[2]:
+        gx = lam
+    if needs[0]:
+        hp = _shifted_states(zi, y).conj_physical()
+        per_row = lam.mT @ hp  # [B, M, M]: sum_t lambda[t] conj(h[t-1])^T
+        gA = per_row if A.dim() == 3 else per_row.sum(0)
+    return gA, gzi, gx
+
+
+class MatrixOps:
+    """Routes an M x M scan to the op the reference would call for that M."""
+
+    @staticmethod
+    def recur(A, zi, x):
+        if x.size(-1) == 2:
+            return torch.ops.philtorch.recur2(A, zi, x)
+        return torch.ops.philtorch.recurN(A, zi, x)
+
+    @staticmethod
+    def lti_recur(A, zi, x):
+        if x.size(-1) == 2:
+            return torch.ops.philtorch.lti_recur2(A, zi, x)
+        return torch.ops.philtorch.lti_recurN(A, zi, x)
+
+
+def _setup_context(ctx: Any, inputs: tuple, output: torch.Tensor) -> None:
+    A, zi, _ = inputs
+    ctx.save_for_backward(A, zi, output)
+
+
+def _make_backward(fused_name: str, composite):
+    def backward(ctx: Any, grad_y: torch.Tensor):
+        A, zi, y = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        if torch.is_grad_enabled():
+            gA, gzi, gx = composite(A, zi, y, grad_y, needs)
+        else:
+            fused = getattr(torch.ops.philtorch, fused_name)
+            gA, gzi, gx = fused(A, zi, y, grad_y)
+        return (gA if needs[0] else None, gzi if needs[1] else None, gx if needs[2] else None)
+
+    return backward
+
+
+if EXTENSION_LOADED:
+
+    def _fake_like(x):
+        return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+    @torch.library.register_fake("philtorch::recur")
+    def _(A, zi, x):
+        torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
+        torch._check(A.ndim in (1, 2), lambda: "A must be 1D (shared) or 2D.")
+        torch._check(A.shape[-1] == x.shape[1], lambda: "A's last dimension must match x's time dimension")
+        torch._check(zi.ndim == 1 and zi.shape[0] == x.shape[0], lambda: "x and zi must have the same batch size.")
+        if A.ndim == 2:
+            torch._check(A.shape[0] == x.shape[0], lambda: "If A is 2D, its first dimension must match x's batch size.")
+        return _fake_like(x)
+
+    def _fake_recurN(A, zi, x, square2: bool):
+        if square2:
+            torch._check(A.shape[-1] == A.shape[-2] == 2, lambda: "A must be square.")
+        else:
+            torch._check(A.shape[-1] == A.shape[-2] == x.shape[2], lambda: "A must be square.")
+        torch._check(A.ndim in (3, 4), lambda: "A must be 3D or 4D.")
+        torch._check(zi.shape[1] == x.shape[2], lambda: "zi's last dimension must match x's.")
+        torch._check(x.shape[1] == A.shape[-3], lambda: "x's second dimension must match A's last-3 dimension.")
+        torch._check(x.shape[0] == zi.shape[0], lambda: "x and zi must have the same batch size.")
+        if A.ndim == 4:
+            torch._check(A.shape[0] == x.shape[0], lambda: "If A is 4D, its first dimension must match x's batch size.")
+        return _fake_like(x)
+
+    def _fake_lti_recurN(A, zi, x, square2: bool):
+        if square2:
+            torch._check(A.shape[-1] == A.shape[-2] == 2, lambda: "A must be square.")
+        else:
+            torch._check(A.shape[-1] == A.shape[-2] == x.shape[2], lambda: "A must be square.")
+        torch._check(A.ndim in (2, 3), lambda: "A must be 2D or 3D.")
+        torch._check(zi.shape[1] == x.shape[2], lambda: "zi's last dimension must match x's.")
+        torch._check(x.shape[0] == zi.shape[0], lambda: "x and zi must have the same batch size.")
+        if A.ndim == 3:
+            torch._check(A.shape[0] == x.shape[0], lambda: "If A is 3D, its first dimension must match x's batch size.")
+        return _fake_like(x)
+
+    torch.library.register_fake("philtorch::recur2")(lambda A, zi, x: _fake_recurN(A, zi, x, True))
+    torch.library.register_fake("philtorch::recurN")(lambda A, zi, x: _fake_recurN(A, zi, x, False))
+    torch.library.register_fake("philtorch::lti_recur2")(lambda A, zi, x: _fake_lti_recurN(A, zi, x, True))
+    torch.library.register_fake("philtorch::lti_recurN")(lambda A, zi, x: _fake_lti_recurN(A, zi, x, False))
+
+    @torch.library.register_fake("philtorch::lti_recur")
+    def _(A, zi, x):
+        torch._check(A.ndim <= 1, lambda: "A must be 1D or scalar.")
+        torch._check(zi.shape[0] == x.shape[0], lambda: "x and zi must have the same batch size.")
+        if A.ndim == 1 and A.shape[0] != 1:
+            torch._check(A.shape[0] == x.shape[0], lambda: "If A is 1D, its length must match x's batch size.")
+        return _fake_like(x)
+
+    def _fake_backward(A, zi, y, grad_y):
+        return _fake_like(A), _fake_like(zi), _fake_like(y)
+
+    for _name in ("recur_backward", "recurN_backward", "lti_recur_backward", "lti_recurN_backward"):
+        torch.library.register_fake(f"philtorch::{_name}")(_fake_backward)
+
+    for _op, _fused, _comp in (
+        ("recur", "recur_backward", _recur_composite),
+        ("recur2", "recurN_backward", _recurN_composite),
+        ("recurN", "recurN_backward", _recurN_composite),
+        ("lti_recur", "lti_recur_backward", _lti_recur_composite),
+        ("lti_recur2", "lti_recurN_backward", _lti_recurN_composite),
+        ("lti_recurN", "lti_recurN_backward", _lti_recurN_composite),
+    ):
+        torch.library.register_autograd(
+            f"philtorch::{_op}", _make_backward(_fused, _comp), setup_context=_setup_context
+        )
+
+from . import mat  # noqa: E402,F401
+from . import lti  # noqa: E402,F401
+from . import lpv  # noqa: E402,F401

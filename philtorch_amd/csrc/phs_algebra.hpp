@@ -1,0 +1,266 @@
+// Element algebra of the linear-recurrence scans.
+//
+// A step of `h[t] = A[t] h[t-1] + x[t]` is the affine map  h -> A h + x.
+// Maps compose associatively:  (first p, then q) = (q.A p.A, q.A p.x + q.x),
+// which is the operator the reference scans with Thrust
+// (philtorch/csrc/lti_recur.cu:19-31 for the scalar case,
+//  philtorch/csrc/recur2.cuh:7-21 for the 2x2 case).  Everything here is
+// written for gfx950 wave64 code: values are moved between lanes as 32-bit
+// words with ds_bpermute (`__shfl`) or v_readlane.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace phs {
+
+// ---------------------------------------------------------------- scalars
+struct c64 {
+  float re, im;
+};
+struct c128 {
+  double re, im;
+};
+
+template <typename T>
+struct Num;
+
+template <>
+struct Num<float> {
+  using acc = double;
+  static __device__ __forceinline__ float zero() { return 0.f; }
+  static __device__ __forceinline__ float one() { return 1.f; }
+};
+template <>
+struct Num<double> {
+  using acc = double;
+  static __device__ __forceinline__ double zero() { return 0.0; }
+  static __device__ __forceinline__ double one() { return 1.0; }
+};
+template <>
+struct Num<int64_t> {
+  using acc = int64_t;
+  static __device__ __forceinline__ int64_t zero() { return 0; }
+  static __device__ __forceinline__ int64_t one() { return 1; }
+};
+template <>
+struct Num<c64> {
+  using acc = c128;
+  static __device__ __forceinline__ c64 zero() { return {0.f, 0.f}; }
+  static __device__ __forceinline__ c64 one() { return {1.f, 0.f}; }
+};
+template <>
+struct Num<c128> {
+  using acc = c128;
+  static __device__ __forceinline__ c128 zero() { return {0.0, 0.0}; }
+  static __device__ __forceinline__ c128 one() { return {1.0, 0.0}; }
+};
+
+// real arithmetic
+__device__ __forceinline__ float mul(float a, float b) { return a * b; }
+__device__ __forceinline__ double mul(double a, double b) { return a * b; }
+__device__ __forceinline__ int64_t mul(int64_t a, int64_t b) { return a * b; }
+__device__ __forceinline__ float add(float a, float b) { return a + b; }
+__device__ __forceinline__ double add(double a, double b) { return a + b; }
+__device__ __forceinline__ int64_t add(int64_t a, int64_t b) { return a + b; }
+// a*b + c
+__device__ __forceinline__ float mad(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ double mad(double a, double b, double c) { return __builtin_fma(a, b, c); }
+__device__ __forceinline__ int64_t mad(int64_t a, int64_t b, int64_t c) { return a * b + c; }
+__device__ __forceinline__ float cj(float a) { return a; }
+__device__ __forceinline__ double cj(double a) { return a; }
+__device__ __forceinline__ int64_t cj(int64_t a) { return a; }
+
+// complex arithmetic
+template <typename C, typename R>
+__device__ __forceinline__ C cmul(C a, C b) {
+  C r;
+  r.re = mad(a.re, b.re, -(a.im * b.im));
+  r.im = mad(a.re, b.im, a.im * b.re);
+  return r;
+}
+template <typename C>
+__device__ __forceinline__ C cmad(C a, C b, C c) {
+  C r;
+  r.re = mad(a.re, b.re, mad(-a.im, b.im, c.re));
+  r.im = mad(a.re, b.im, mad(a.im, b.re, c.im));
+  return r;
+}
+__device__ __forceinline__ c64 mul(c64 a, c64 b) { return cmul<c64, float>(a, b); }
+__device__ __forceinline__ c128 mul(c128 a, c128 b) { return cmul<c128, double>(a, b); }
+__device__ __forceinline__ c64 add(c64 a, c64 b) { return {a.re + b.re, a.im + b.im}; }
+__device__ __forceinline__ c128 add(c128 a, c128 b) { return {a.re + b.re, a.im + b.im}; }
+__device__ __forceinline__ c64 mad(c64 a, c64 b, c64 c) { return cmad(a, b, c); }
+__device__ __forceinline__ c128 mad(c128 a, c128 b, c128 c) { return cmad(a, b, c); }
+__device__ __forceinline__ c64 cj(c64 a) { return {a.re, -a.im}; }
+__device__ __forceinline__ c128 cj(c128 a) { return {a.re, -a.im}; }
+
+// widening into the reduction accumulator type
+__device__ __forceinline__ double widen(float v) { return (double)v; }
+__device__ __forceinline__ double widen(double v) { return v; }
+__device__ __forceinline__ int64_t widen(int64_t v) { return v; }
+__device__ __forceinline__ c128 widen(c64 v) { return {(double)v.re, (double)v.im}; }
+__device__ __forceinline__ c128 widen(c128 v) { return v; }
+__device__ __forceinline__ void narrow(double v, float &o) { o = (float)v; }
+__device__ __forceinline__ void narrow(double v, double &o) { o = v; }
+__device__ __forceinline__ void narrow(int64_t v, int64_t &o) { o = v; }
+__device__ __forceinline__ void narrow(c128 v, c64 &o) { o = {(float)v.re, (float)v.im}; }
+__device__ __forceinline__ void narrow(c128 v, c128 &o) { o = v; }
+
+// ---------------------------------------------------------------- 2x2 blocks
+template <typename T>
+struct Mat2 {
+  T m00, m01, m10, m11;
+};
+template <typename T>
+struct Vec2 {
+  T v0, v1;
+};
+
+// ---------------------------------------------------------------- algebras
+// Scalar first-order scan: coefficient and state are both T.
+template <typename T>
+struct Scalar {
+  using elem = T;
+  using coef = T;
+  using state = T;
+  using acc_coef = typename Num<T>::acc;
+  static constexpr int kCoefElems = 1;   // scalars of T per coefficient
+  static constexpr int kStateElems = 1;  // scalars of T per state
+
+  static __device__ __forceinline__ coef cone() { return Num<T>::one(); }
+  static __device__ __forceinline__ coef czero() { return Num<T>::zero(); }
+  static __device__ __forceinline__ state szero() { return Num<T>::zero(); }
+  // q * p  (apply p first)
+  static __device__ __forceinline__ coef cmul(coef q, coef p) { return mul(q, p); }
+  // A h + x
+  static __device__ __forceinline__ state affine(coef A, state h, state x) { return mad(A, h, x); }
+  static __device__ __forceinline__ state sadd(state a, state b) { return add(a, b); }
+  // A^H (conjugate transpose)
+  static __device__ __forceinline__ coef adjoint(coef A) { return cj(A); }
+  // lambda conj(y)^T : the per-step gradient of the coefficient
+  static __device__ __forceinline__ coef outer(state lam, state y) { return mul(lam, cj(y)); }
+  static __device__ __forceinline__ acc_coef acc_zero() { return widen(Num<T>::zero()); }
+  static __device__ __forceinline__ acc_coef acc_add(acc_coef s, coef v) { return add(s, widen(v)); }
+  static __device__ __forceinline__ acc_coef acc_sum(acc_coef a, acc_coef b) { return add(a, b); }
+  static __device__ __forceinline__ coef acc_narrow(acc_coef s) {
+    coef o;
+    narrow(s, o);
+    return o;
+  }
+};
+
+// 2x2 state-space recursion (biquad sections): coefficient Mat2, state Vec2.
+template <typename T>
+struct Block2 {
+  using elem = T;
+  using coef = Mat2<T>;
+  using state = Vec2<T>;
+  using acc_t = typename Num<T>::acc;
+  using acc_coef = Mat2<acc_t>;
+  static constexpr int kCoefElems = 4;
+  static constexpr int kStateElems = 2;
+
+  static __device__ __forceinline__ coef cone() {
+    return {Num<T>::one(), Num<T>::zero(), Num<T>::zero(), Num<T>::one()};
+  }
+  static __device__ __forceinline__ coef czero() {
+    return {Num<T>::zero(), Num<T>::zero(), Num<T>::zero(), Num<T>::zero()};
+  }
+  static __device__ __forceinline__ state szero() { return {Num<T>::zero(), Num<T>::zero()}; }
+  static __device__ __forceinline__ coef cmul(coef q, coef p) {
+    coef r;
+    r.m00 = mad(q.m00, p.m00, mul(q.m01, p.m10));
+    r.m01 = mad(q.m00, p.m01, mul(q.m01, p.m11));
+    r.m10 = mad(q.m10, p.m00, mul(q.m11, p.m10));
+    r.m11 = mad(q.m10, p.m01, mul(q.m11, p.m11));
+    return r;
+  }
+  static __device__ __forceinline__ state affine(coef A, state h, state x) {
+    state r;
+    r.v0 = mad(A.m00, h.v0, mad(A.m01, h.v1, x.v0));
+    r.v1 = mad(A.m10, h.v0, mad(A.m11, h.v1, x.v1));
+    return r;
+  }
+  static __device__ __forceinline__ state sadd(state a, state b) {
+    return {add(a.v0, b.v0), add(a.v1, b.v1)};
+  }
+  static __device__ __forceinline__ coef adjoint(coef A) {
+    return {cj(A.m00), cj(A.m10), cj(A.m01), cj(A.m11)};
+  }
+  static __device__ __forceinline__ coef outer(state lam, state y) {
+    T y0 = cj(y.v0), y1 = cj(y.v1);
+    return {mul(lam.v0, y0), mul(lam.v0, y1), mul(lam.v1, y0), mul(lam.v1, y1)};
+  }
+  static __device__ __forceinline__ acc_coef acc_zero() {
+    acc_t z = widen(Num<T>::zero());
+    return {z, z, z, z};
+  }
+  static __device__ __forceinline__ acc_coef acc_add(acc_coef s, coef v) {
+    return {add(s.m00, widen(v.m00)), add(s.m01, widen(v.m01)), add(s.m10, widen(v.m10)),
+            add(s.m11, widen(v.m11))};
+  }
+  static __device__ __forceinline__ acc_coef acc_sum(acc_coef a, acc_coef b) {
+    return {add(a.m00, b.m00), add(a.m01, b.m01), add(a.m10, b.m10), add(a.m11, b.m11)};
+  }
+  static __device__ __forceinline__ coef acc_narrow(acc_coef s) {
+    coef o;
+    narrow(s.m00, o.m00);
+    narrow(s.m01, o.m01);
+    narrow(s.m10, o.m10);
+    narrow(s.m11, o.m11);
+    return o;
+  }
+};
+
+// Affine map h -> A h + x.
+template <class Alg>
+struct Map {
+  typename Alg::coef A;
+  typename Alg::state x;
+};
+
+template <class Alg>
+__device__ __forceinline__ Map<Alg> map_identity() {
+  return {Alg::cone(), Alg::szero()};
+}
+// first p, then q
+template <class Alg>
+__device__ __forceinline__ Map<Alg> compose(const Map<Alg> &p, const Map<Alg> &q) {
+  return {Alg::cmul(q.A, p.A), Alg::affine(q.A, p.x, q.x)};
+}
+template <class Alg>
+__device__ __forceinline__ typename Alg::state apply(const Map<Alg> &m, const typename Alg::state &h) {
+  return Alg::affine(m.A, h, m.x);
+}
+
+// ---------------------------------------------------------------- lane moves
+template <typename X>
+__device__ __forceinline__ X shfl_from(const X &v, int src) {
+  static_assert(sizeof(X) % 4 == 0, "32-bit granular types only");
+  constexpr int n = sizeof(X) / 4;
+  union {
+    X x;
+    int w[n];
+  } in, out;
+  in.x = v;
+#pragma unroll
+  for (int i = 0; i < n; ++i) out.w[i] = __shfl(in.w[i], src, 64);
+  return out.x;
+}
+
+// Value of `v` held by lane `lane` (must be wave-uniform); result is uniform.
+template <typename X>
+__device__ __forceinline__ X read_lane(const X &v, int lane) {
+  constexpr int n = sizeof(X) / 4;
+  union {
+    X x;
+    int w[n];
+  } in, out;
+  in.x = v;
+#pragma unroll
+  for (int i = 0; i < n; ++i) out.w[i] = __builtin_amdgcn_readlane(in.w[i], lane);
+  return out.x;
+}
+
+}  // namespace phs

@@ -1,0 +1,202 @@
+// C ABI entry points of libphilscan (declared in include/philscan.h).
+// Host side: argument checks, workspace carving, and the launch of
+//   scan_kernel [-> reduce kernel]
+// on the caller's stream.  No allocation, no synchronisation, no globals.
+// Workspace layout: [0, 256) header (tile counter, finished blocks, epoch),
+// then the tile status words, then (backward only) per-tile partial sums or
+// per-step scratch.
+#include <hip/hip_runtime.h>
+
+#include "../../include/philscan.h"
+#include "phs_scan.hpp"
+
+namespace phs {
+namespace {
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct Layout {
+  int64_t tiles_per_row = 0;
+  size_t status_off = 0, status_words = 0;  // header lives at offset 0
+  size_t partials_off = 0, scratch_off = 0, total = 0;
+};
+
+// TV: coefficient varies with time; shared: one coefficient set for all rows.
+template <class Alg>
+Layout make_layout(int64_t B, int64_t T, bool TV, bool shared, bool backward) {
+  using Sh = Shape<Alg>;
+  Layout L;
+  L.tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
+  L.status_off = kAlign;
+  L.status_words = size_t(B) * size_t(L.tiles_per_row) * Sh::kStride;
+  size_t off = align_up(L.status_off + L.status_words * sizeof(uint64_t));
+  if (backward && !TV) {  // per-tile coefficient-gradient partial sums
+    L.partials_off = off;
+    off = align_up(off + size_t(B) * size_t(L.tiles_per_row) * sizeof(typename Alg::acc_coef));
+  }
+  if (backward && TV && shared) {  // per-step gradients before the batch sum
+    L.scratch_off = off;
+    off = align_up(off + size_t(B) * size_t(T) * sizeof(typename Alg::coef));
+  }
+  L.total = off;
+  return L;
+}
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <class Alg>
+int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void *coef,
+           const void *zi, const void *x, const void *y, void *out, void *gcoef, void *gzi,
+           void *workspace, size_t ws_bytes, hipStream_t stream) {
+  using E = typename Alg::elem;
+  using Sh = Shape<Alg>;
+  if (B < 0 || T < 0) return PHS_ERR_INVALID;
+  if (B == 0 || T == 0) return PHS_OK;
+  if (!coef || !zi || !x || (backward ? !y : !out)) return PHS_ERR_INVALID;
+  const Layout L = make_layout<Alg>(B, T, TV, shared, backward);
+  if (double(B) * double(L.tiles_per_row) >= 4294967295.0) return PHS_ERR_INVALID;
+  if (!workspace || ws_bytes < L.total) return PHS_ERR_WORKSPACE;
+
+  char *ws = static_cast<char *>(workspace);
+  ScanArgs<Alg> a;
+  a.coef = static_cast<const E *>(coef);
+  a.coef_row_stride = shared ? 0 : (TV ? T : 1);
+  a.zi = static_cast<const E *>(zi);
+  a.x = static_cast<const E *>(x);
+  a.y = static_cast<const E *>(y);
+  a.out = static_cast<E *>(out);
+  a.gcoef = nullptr;
+  a.partials = nullptr;
+  a.gzi = static_cast<E *>(gzi);
+  a.B = B;
+  a.T_len = T;
+  a.tiles_per_row = L.tiles_per_row;
+  a.header = reinterpret_cast<unsigned *>(ws);
+  a.status = reinterpret_cast<uint64_t *>(ws + L.status_off);
+  a.status_capacity = int64_t((ws_bytes - L.status_off) / sizeof(uint64_t));
+  if (backward && gcoef) {
+    if (TV)
+      a.gcoef = shared ? reinterpret_cast<E *>(ws + L.scratch_off) : static_cast<E *>(gcoef);
+    else
+      a.partials = ws + L.partials_off;
+  }
+  bool vec = (size_t(T) * sizeof(typename Alg::state)) % 16 == 0 && aligned16(x) && aligned16(y) &&
+             aligned16(out) && aligned16(a.gcoef) && (!TV || aligned16(coef));
+  a.vec_ok = vec ? 1 : 0;
+
+  const unsigned tiles = unsigned(B * L.tiles_per_row);
+  if (TV) {
+    if (backward)
+      hipLaunchKernelGGL((scan_kernel<Alg, true, true>), dim3(tiles), dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((scan_kernel<Alg, true, false>), dim3(tiles), dim3(kThreads), 0, stream, a);
+  } else {
+    if (backward)
+      hipLaunchKernelGGL((scan_kernel<Alg, false, true>), dim3(tiles), dim3(kThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL((scan_kernel<Alg, false, false>), dim3(tiles), dim3(kThreads), 0, stream, a);
+  }
+  if (backward && gcoef) {
+    if (TV && shared) {
+      const int blocks = int(std::min<int64_t>((T + kThreads - 1) / kThreads, 4096));
+      hipLaunchKernelGGL(reduce_batch_kernel<Alg>, dim3(blocks), dim3(kThreads), 0, stream,
+                         static_cast<const E *>(a.gcoef), B, T, static_cast<E *>(gcoef));
+    } else if (!TV) {
+      const int64_t rows = shared ? 1 : B;
+      const int64_t count = shared ? B * L.tiles_per_row : L.tiles_per_row;
+      hipLaunchKernelGGL(reduce_rows_kernel<Alg>, dim3(unsigned(rows)), dim3(kThreads), 0, stream,
+                         static_cast<const void *>(a.partials), count, static_cast<E *>(gcoef));
+    }
+  }
+  return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
+}
+
+template <template <class> class AlgT, class F>
+int dispatch(int dtype, F &&f) {
+  switch (dtype) {
+    case PHS_F32: return f(AlgT<float>{});
+    case PHS_F64: return f(AlgT<double>{});
+    case PHS_C64: return f(AlgT<c64>{});
+    case PHS_C128: return f(AlgT<c128>{});
+    case PHS_I64: return f(AlgT<int64_t>{});
+    default: return PHS_ERR_DTYPE;
+  }
+}
+
+template <template <class> class AlgT>
+size_t ws_size(int dtype, int64_t B, int64_t T, bool TV, bool shared, bool backward) {
+  size_t out = 0;
+  if (B <= 0 || T <= 0) return 0;
+  dispatch<AlgT>(dtype, [&](auto alg) {
+    using Alg = decltype(alg);
+    out = make_layout<Alg>(B, T, TV, shared, backward).total;
+    return 0;
+  });
+  return out;
+}
+
+}  // namespace
+}  // namespace phs
+
+using phs::Block2;
+using phs::dispatch;
+using phs::Scalar;
+
+extern "C" {
+
+size_t phs_workspace_size(int op, int dtype, int64_t B, int64_t T, int coef_shared, int backward) {
+  const bool sh = coef_shared != 0, bw = backward != 0;
+  switch (op) {
+    case PHS_OP_RECUR: return phs::ws_size<Scalar>(dtype, B, T, true, sh, bw);
+    case PHS_OP_LTI_RECUR: return phs::ws_size<Scalar>(dtype, B, T, false, sh, bw);
+    case PHS_OP_RECUR2: return phs::ws_size<Block2>(dtype, B, T, true, sh, bw);
+    case PHS_OP_LTI_RECUR2: return phs::ws_size<Block2>(dtype, B, T, false, sh, bw);
+    default: return 0;
+  }
+}
+
+const char *phs_error_string(int status) {
+  switch (status) {
+    case PHS_OK: return "ok";
+    case PHS_ERR_INVALID: return "invalid argument (size, null pointer or unsupported combination)";
+    case PHS_ERR_WORKSPACE: return "workspace missing or smaller than phs_workspace_size()";
+    case PHS_ERR_LAUNCH: return "HIP kernel launch failed";
+    case PHS_ERR_DTYPE: return "unsupported dtype";
+    default: return "unknown philscan status";
+  }
+}
+
+int phs_abi_version(void) { return 100; }
+
+#define PHS_FWD(NAME, ALGT, TV)                                                                    \
+  int NAME(int dtype, int64_t B, int64_t T, const void *A, int coef_shared, const void *zi,        \
+           const void *x, void *y, void *workspace, size_t workspace_bytes, void *stream) {        \
+    return dispatch<ALGT>(dtype, [&](auto alg) {                                                    \
+      return phs::launch<decltype(alg)>(B, T, TV, coef_shared != 0, false, A, zi, x, nullptr, y,   \
+                                        nullptr, nullptr, workspace, workspace_bytes,              \
+                                        static_cast<hipStream_t>(stream));                         \
+    });                                                                                            \
+  }
+
+#define PHS_BWD(NAME, ALGT, TV)                                                                    \
+  int NAME(int dtype, int64_t B, int64_t T, const void *A, int coef_shared, const void *zi,        \
+           const void *y, const void *grad_y, void *grad_x, void *grad_A, void *grad_zi,           \
+           void *workspace, size_t workspace_bytes, void *stream) {                                \
+    return dispatch<ALGT>(dtype, [&](auto alg) {                                                    \
+      return phs::launch<decltype(alg)>(B, T, TV, coef_shared != 0, true, A, zi, grad_y, y,        \
+                                        grad_x, grad_A, grad_zi, workspace, workspace_bytes,       \
+                                        static_cast<hipStream_t>(stream));                         \
+    });                                                                                            \
+  }
+
+PHS_FWD(phs_recur_fwd, Scalar, true)
+PHS_BWD(phs_recur_bwd, Scalar, true)
+PHS_FWD(phs_lti_recur_fwd, Scalar, false)
+PHS_BWD(phs_lti_recur_bwd, Scalar, false)
+PHS_FWD(phs_recur2_fwd, Block2, true)
+PHS_BWD(phs_recur2_bwd, Block2, true)
+PHS_FWD(phs_lti_recur2_fwd, Block2, false)
+PHS_BWD(phs_lti_recur2_bwd, Block2, false)
+
+}  // extern "C"

@@ -1,0 +1,347 @@
+// torch.library layer of philtorch_amd: owns the `philtorch` operator
+// namespace with the reference's schemas (philtorch/csrc/host_recur2.cpp:162-171)
+// plus the new LPV scalar op `recur` and four fused backward ops, and binds
+// the HIP device key (PyTorch-ROCm names it CUDA) to the C ABI of
+// libphilscan.  No CPU kernels are registered: CPU tensors raise, and the
+// Python API keeps the reference's pure-PyTorch route for them.
+#include <ATen/ATen.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/library.h>
+
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+#include "../../include/philscan.h"
+
+namespace {
+
+using at::Tensor;
+using Triple = std::tuple<Tensor, Tensor, Tensor>;
+
+int phs_dtype_of(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat: return PHS_F32;
+    case at::kDouble: return PHS_F64;
+    case at::kComplexFloat: return PHS_C64;
+    case at::kComplexDouble: return PHS_C128;
+    case at::kLong: return PHS_I64;
+    default: return -1;
+  }
+}
+
+bool is_half(at::ScalarType t) { return t == at::kHalf || t == at::kBFloat16; }
+
+void check_status(int rc, const char *op) {
+  TORCH_CHECK(rc == PHS_OK, "philtorch::", op, ": ", phs_error_string(rc));
+}
+
+void check_common(const char *op, const Tensor &A, const Tensor &zi, const Tensor &x) {
+  // message texts follow host_recurN.cpp:240-248 / host_lti_recur.cpp:45-50
+  TORCH_CHECK(zi.scalar_type() == x.scalar_type(), "zi must have the same scalar type as input");
+  TORCH_CHECK(A.scalar_type() == x.scalar_type(), "A must have the same scalar type as input");
+  TORCH_CHECK(x.is_cuda() && A.is_cuda() && zi.is_cuda(), "philtorch::", op,
+              ": philtorch_amd runs on HIP devices only (got ", x.device(), ")");
+  TORCH_CHECK(A.device() == x.device() && zi.device() == x.device(), "philtorch::", op,
+              ": all tensors must be on the same device");
+  TORCH_CHECK(is_half(x.scalar_type()) || phs_dtype_of(x.scalar_type()) >= 0, "philtorch::", op,
+              ": unsupported dtype ", x.scalar_type());
+}
+
+void *stream_of(const Tensor &t) {
+  return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream();
+}
+
+// The kernels' workspace is self-resetting: zero-filled once, then every call
+// leaves it ready for the next one on the same stream.  One buffer is kept per
+// (device, stream) and grown geometrically; a replaced buffer goes back to the
+// caching allocator, whose stream-ordered reuse keeps in-flight kernels safe.
+// The cache is intentionally leaked at exit (no HIP calls during teardown).
+struct Workspace {
+  void *ptr;
+  size_t bytes;
+};
+
+Workspace workspace_for(const Tensor &like, size_t bytes, void *stream) {
+  static auto *mu = new std::mutex;
+  static auto *cache = new std::map<std::pair<int, void *>, Tensor>;
+  std::lock_guard<std::mutex> lock(*mu);
+  const auto key = std::make_pair(int(like.device().index()), stream);
+  auto it = cache->find(key);
+  if (it == cache->end() || size_t(it->second.numel()) < bytes) {
+    size_t cap = size_t(1) << 16;
+    if (it != cache->end()) cap = std::max(cap, size_t(it->second.numel()) * 2);
+    while (cap < bytes) cap *= 2;
+    Tensor buf = at::zeros({int64_t(cap)}, like.options().dtype(at::kByte));
+    it = cache->insert_or_assign(key, buf).first;
+  }
+  return {it->second.mutable_data_ptr(), size_t(it->second.numel())};
+}
+
+using FwdFn = int (*)(int, int64_t, int64_t, const void *, int, const void *, const void *, void *,
+                      void *, size_t, void *);
+using BwdFn = int (*)(int, int64_t, int64_t, const void *, int, const void *, const void *,
+                      const void *, void *, void *, void *, void *, size_t, void *);
+
+// y = op(A, zi, x); A/zi/x already validated, x is [B, T, ...]
+Tensor run_fwd(const char *name, FwdFn fn, int op, const Tensor &A, bool shared, const Tensor &zi,
+               const Tensor &x) {
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  const int64_t B = x.size(0), T = x.size(1);
+  Tensor Ac = A.contiguous(), zc = zi.contiguous(), xc = x.contiguous();
+  Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  void *stream = stream_of(x);
+  const Workspace ws = workspace_for(x, phs_workspace_size(op, dt, B, T, shared ? 1 : 0, 0), stream);
+  check_status(fn(dt, B, T, Ac.const_data_ptr(), shared ? 1 : 0, zc.const_data_ptr(),
+                  xc.const_data_ptr(), y.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+               name);
+  return y;
+}
+
+Triple run_bwd(const char *name, BwdFn fn, int op, const Tensor &A, bool shared, const Tensor &zi,
+               const Tensor &y, const Tensor &gy) {
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(y.device());
+  const int dt = phs_dtype_of(y.scalar_type());
+  const int64_t B = y.size(0), T = y.size(1);
+  Tensor Ac = A.contiguous(), zc = zi.contiguous(), yc = y.contiguous(), gc = gy.contiguous();
+  Tensor gA = at::empty(A.sizes(), A.options());
+  Tensor gzi = at::empty(zi.sizes(), zi.options());
+  Tensor gx = at::empty(y.sizes(), y.options());
+  void *stream = stream_of(y);
+  const Workspace ws = workspace_for(y, phs_workspace_size(op, dt, B, T, shared ? 1 : 0, 1), stream);
+  check_status(fn(dt, B, T, Ac.const_data_ptr(), shared ? 1 : 0, zc.const_data_ptr(),
+                  yc.const_data_ptr(), gc.const_data_ptr(), gx.mutable_data_ptr(),
+                  gA.mutable_data_ptr(), gzi.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+               name);
+  if (B == 0 || T == 0) {  // nothing was launched: gradients are zero
+    gA.zero_();
+    gzi.zero_();
+    gx.zero_();
+  }
+  return {gA, gzi, gx};
+}
+
+Triple to_dtype(const Triple &t, at::ScalarType dt) {
+  return {std::get<0>(t).to(dt), std::get<1>(t).to(dt), std::get<2>(t).to(dt)};
+}
+
+// ------------------------------------------------------------ LPV scalar
+void check_recur(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  TORCH_CHECK(x.dim() == 2, "x must be a 2D tensor (batch, time)");
+  TORCH_CHECK(zi.dim() == 1 && zi.size(0) == x.size(0), "zi must be a vector with x's batch size");
+  TORCH_CHECK(A.dim() == 1 || A.dim() == 2, "A must be a 1D (shared) or 2D tensor");
+  TORCH_CHECK(A.size(-1) == x.size(1), "A's last dimension must match x's time dimension");
+  if (A.dim() == 2) TORCH_CHECK(A.size(0) == x.size(0), "If A is 2D, its first dimension must match x's batch size.");
+}
+
+Tensor recur_hip(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  check_common("recur", A, zi, x);
+  check_recur(A, zi, x);
+  if (is_half(x.scalar_type()))
+    return recur_hip(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
+  return run_fwd("recur", phs_recur_fwd, PHS_OP_RECUR, A, A.dim() == 1, zi, x);
+}
+
+Triple recur_backward_hip(const Tensor &A, const Tensor &zi, const Tensor &y, const Tensor &gy) {
+  check_common("recur_backward", A, zi, y);
+  check_recur(A, zi, y);
+  TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
+  if (is_half(y.scalar_type()))
+    return to_dtype(recur_backward_hip(A.to(at::kFloat), zi.to(at::kFloat), y.to(at::kFloat),
+                                       gy.to(at::kFloat)),
+                    y.scalar_type());
+  return run_bwd("recur_backward", phs_recur_bwd, PHS_OP_RECUR, A, A.dim() == 1, zi, y,
+                 gy.to(y.scalar_type()));
+}
+
+// ------------------------------------------------------------ LPV MxM (M = 1, 2)
+void check_recurN(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  // host_recurN.cpp:244-248 and the fake kernel philtorch/__init__.py:179-198
+  TORCH_CHECK(A.dim() == 3 || A.dim() == 4, "A must be a 3D or 4D tensor");
+  TORCH_CHECK(x.dim() == 3, "x must be a 3D tensor (batch, time, order)");
+  TORCH_CHECK(x.size(2) == A.size(-1), "Last dimension of x must match last dimension of A");
+  TORCH_CHECK(A.size(-1) == A.size(-2), "Last two dimensions of A must be equal");
+  TORCH_CHECK(zi.dim() == 2 && zi.size(1) == x.size(2) && zi.size(0) == x.size(0),
+              "zi must be (batch, order)");
+  TORCH_CHECK(x.size(1) == A.size(-3), "x's second dimension must match A's last-3 dimension.");
+  if (A.dim() == 4)
+    TORCH_CHECK(A.size(0) == x.size(0), "If A is 4D, its first dimension must match x's batch size.");
+}
+
+// [B,T,1,1] -> [B,T]; shared [T,1,1] -> [T]
+std::vector<int64_t> scalar_coef_shape(const Tensor &A, bool shared) {
+  return shared ? std::vector<int64_t>{A.size(0)} : std::vector<int64_t>{A.size(0), A.size(1)};
+}
+
+Tensor recurN_hip(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  check_common("recurN", A, zi, x);
+  check_recurN(A, zi, x);
+  if (is_half(x.scalar_type()))
+    return recurN_hip(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
+  const int64_t M = A.size(-1);
+  const bool shared = A.dim() == 3;
+  if (M == 1)
+    return run_fwd("recurN", phs_recur_fwd, PHS_OP_RECUR, A.reshape(scalar_coef_shape(A, shared)),
+                   shared, zi.reshape({zi.size(0)}), x.reshape({x.size(0), x.size(1)}))
+        .view(x.sizes());
+  TORCH_CHECK(M == 2, "philtorch::recurN on HIP devices supports 1x1 and 2x2 matrices, got ", M, "x", M);
+  return run_fwd("recurN", phs_recur2_fwd, PHS_OP_RECUR2, A, shared, zi, x);
+}
+
+Tensor recur2_hip(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  TORCH_CHECK(A.dim() >= 2 && A.size(-1) == 2 && A.size(-2) == 2, "A must be square.");
+  return recurN_hip(A, zi, x);
+}
+
+Triple recurN_backward_hip(const Tensor &A, const Tensor &zi, const Tensor &y, const Tensor &gy) {
+  check_common("recurN_backward", A, zi, y);
+  check_recurN(A, zi, y);
+  TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
+  if (is_half(y.scalar_type()))
+    return to_dtype(recurN_backward_hip(A.to(at::kFloat), zi.to(at::kFloat), y.to(at::kFloat),
+                                        gy.to(at::kFloat)),
+                    y.scalar_type());
+  const int64_t M = A.size(-1);
+  const bool shared = A.dim() == 3;
+  const Tensor g = gy.to(y.scalar_type());
+  if (M == 1) {
+    auto r = run_bwd("recurN_backward", phs_recur_bwd, PHS_OP_RECUR,
+                     A.reshape(scalar_coef_shape(A, shared)),
+                     shared, zi.reshape({zi.size(0)}), y.reshape({y.size(0), y.size(1)}),
+                     g.reshape({y.size(0), y.size(1)}));
+    return {std::get<0>(r).view(A.sizes()), std::get<1>(r).view(zi.sizes()),
+            std::get<2>(r).view(y.sizes())};
+  }
+  TORCH_CHECK(M == 2, "philtorch::recurN on HIP devices supports 1x1 and 2x2 matrices, got ", M, "x", M);
+  return run_bwd("recurN_backward", phs_recur2_bwd, PHS_OP_RECUR2, A, shared, zi, y, g);
+}
+
+// ------------------------------------------------------------ LTI scalar
+void check_lti_recur(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  // host_lti_recur.cpp:49-50 and philtorch/__init__.py:233-244
+  TORCH_CHECK(A.dim() <= 1, "A must be a vector or a scalar");
+  TORCH_CHECK(zi.dim() == 1, "zi must be a vector");
+  TORCH_CHECK(x.dim() == 2, "x must be a 2D tensor (batch, time)");
+  TORCH_CHECK(zi.size(0) == x.size(0), "x and zi must have the same batch size.");
+  const bool batched = A.dim() == 1 && A.numel() == x.size(0);
+  TORCH_CHECK(batched || A.numel() == 1, "If A is 1D, its length must match x's batch size.");
+}
+
+bool lti_shared(const Tensor &A, const Tensor &x) { return !(A.dim() == 1 && A.numel() == x.size(0)); }
+
+Tensor lti_recur_hip(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  check_common("lti_recur", A, zi, x);
+  check_lti_recur(A, zi, x);
+  if (is_half(x.scalar_type()))
+    return lti_recur_hip(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
+  return run_fwd("lti_recur", phs_lti_recur_fwd, PHS_OP_LTI_RECUR, A, lti_shared(A, x), zi, x);
+}
+
+Triple lti_recur_backward_hip(const Tensor &A, const Tensor &zi, const Tensor &y, const Tensor &gy) {
+  check_common("lti_recur_backward", A, zi, y);
+  check_lti_recur(A, zi, y);
+  TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
+  if (is_half(y.scalar_type()))
+    return to_dtype(lti_recur_backward_hip(A.to(at::kFloat), zi.to(at::kFloat), y.to(at::kFloat),
+                                           gy.to(at::kFloat)),
+                    y.scalar_type());
+  return run_bwd("lti_recur_backward", phs_lti_recur_bwd, PHS_OP_LTI_RECUR, A, lti_shared(A, y), zi,
+                 y, gy.to(y.scalar_type()));
+}
+
+// ------------------------------------------------------------ LTI MxM (M = 1, 2)
+void check_lti_recurN(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  // host_lti_recurN.cpp:155-159 and philtorch/__init__.py:200-231
+  TORCH_CHECK(A.dim() == 2 || A.dim() == 3, "A must be a 2D or 3D tensor");
+  TORCH_CHECK(x.dim() == 3, "x must be a 3D tensor (batch, time, order)");
+  TORCH_CHECK(x.size(2) == A.size(-1), "Last dimension of x must match last dimension of A");
+  TORCH_CHECK(A.size(-1) == A.size(-2), "Last two dimensions of A must be equal");
+  TORCH_CHECK(zi.dim() == 2 && zi.size(1) == x.size(2) && zi.size(0) == x.size(0),
+              "zi must be (batch, order)");
+  if (A.dim() == 3)
+    TORCH_CHECK(A.size(0) == x.size(0), "If A is 3D, its first dimension must match x's batch size.");
+}
+
+Tensor lti_recurN_hip(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  check_common("lti_recurN", A, zi, x);
+  check_lti_recurN(A, zi, x);
+  if (is_half(x.scalar_type()))
+    return lti_recurN_hip(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
+  const int64_t M = A.size(-1);
+  const bool shared = A.dim() == 2;
+  if (M == 1)
+    return run_fwd("lti_recurN", phs_lti_recur_fwd, PHS_OP_LTI_RECUR,
+                   shared ? A.reshape({1}) : A.reshape({A.size(0)}), shared,
+                   zi.reshape({zi.size(0)}), x.reshape({x.size(0), x.size(1)}))
+        .view(x.sizes());
+  TORCH_CHECK(M == 2, "philtorch::lti_recurN on HIP devices supports 1x1 and 2x2 matrices, got ", M, "x", M);
+  return run_fwd("lti_recurN", phs_lti_recur2_fwd, PHS_OP_LTI_RECUR2, A, shared, zi, x);
+}
+
+Tensor lti_recur2_hip(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  TORCH_CHECK(A.dim() >= 2 && A.size(-1) == 2 && A.size(-2) == 2, "A must be square.");
+  return lti_recurN_hip(A, zi, x);
+}
+
+Triple lti_recurN_backward_hip(const Tensor &A, const Tensor &zi, const Tensor &y,
+                               const Tensor &gy) {
+  check_common("lti_recurN_backward", A, zi, y);
+  check_lti_recurN(A, zi, y);
+  TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
+  if (is_half(y.scalar_type()))
+    return to_dtype(lti_recurN_backward_hip(A.to(at::kFloat), zi.to(at::kFloat),
+                                            y.to(at::kFloat), gy.to(at::kFloat)),
+                    y.scalar_type());
+  const int64_t M = A.size(-1);
+  const bool shared = A.dim() == 2;
+  const Tensor g = gy.to(y.scalar_type());
+  if (M == 1) {
+    auto r = run_bwd("lti_recurN_backward", phs_lti_recur_bwd, PHS_OP_LTI_RECUR,
+                     shared ? A.reshape({1}) : A.reshape({A.size(0)}), shared,
+                     zi.reshape({zi.size(0)}), y.reshape({y.size(0), y.size(1)}),
+                     g.reshape({y.size(0), y.size(1)}));
+    return {std::get<0>(r).view(A.sizes()), std::get<1>(r).view(zi.sizes()),
+            std::get<2>(r).view(y.sizes())};
+  }
+  TORCH_CHECK(M == 2, "philtorch::lti_recurN on HIP devices supports 1x1 and 2x2 matrices, got ", M, "x", M);
+  return run_bwd("lti_recurN_backward", phs_lti_recur2_bwd, PHS_OP_LTI_RECUR2, A, shared, zi, y, g);
+}
+
+}  // namespace
+
+TORCH_LIBRARY(philtorch, m) {
+  // the reference's five schemas, philtorch/csrc/host_recur2.cpp:164-170
+  m.def("recur2(Tensor A, Tensor zi, Tensor x) -> Tensor", {at::Tag::pt2_compliant_tag});
+  m.def("recurN(Tensor A, Tensor zi, Tensor x) -> Tensor", {at::Tag::pt2_compliant_tag});
+  m.def("lti_recur2(Tensor A, Tensor zi, Tensor x) -> Tensor", {at::Tag::pt2_compliant_tag});
+  m.def("lti_recurN(Tensor A, Tensor zi, Tensor x) -> Tensor", {at::Tag::pt2_compliant_tag});
+  m.def("lti_recur(Tensor A, Tensor zi, Tensor x) -> Tensor", {at::Tag::pt2_compliant_tag});
+  // new: the LPV scalar scan behind lpv.linear_recurrence (A [B,T] or [T])
+  m.def("recur(Tensor A, Tensor zi, Tensor x) -> Tensor", {at::Tag::pt2_compliant_tag});
+  // new: fused adjoint passes returning (grad_A, grad_zi, grad_x)
+  m.def("recur_backward(Tensor A, Tensor zi, Tensor y, Tensor grad_y) -> (Tensor, Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
+  m.def("recurN_backward(Tensor A, Tensor zi, Tensor y, Tensor grad_y) -> (Tensor, Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
+  m.def("lti_recur_backward(Tensor A, Tensor zi, Tensor y, Tensor grad_y) -> (Tensor, Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
+  m.def("lti_recurN_backward(Tensor A, Tensor zi, Tensor y, Tensor grad_y) -> (Tensor, Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
+}
+
+TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
+  m.impl("recur2", &recur2_hip);
+  m.impl("recurN", &recurN_hip);
+  m.impl("lti_recur2", &lti_recur2_hip);
+  m.impl("lti_recurN", &lti_recurN_hip);
+  m.impl("lti_recur", &lti_recur_hip);
+  m.impl("recur", &recur_hip);
+  m.impl("recur_backward", &recur_backward_hip);
+  m.impl("recurN_backward", &recurN_backward_hip);
+  m.impl("lti_recur_backward", &lti_recur_backward_hip);
+  m.impl("lti_recurN_backward", &lti_recurN_backward_hip);
+}

@@ -1,0 +1,85 @@
+"""Seeded synthetic inputs and the parity bar shared by the tests.
+
+Inputs are generated on the CPU with numpy's PCG64 so the oracle and the GPU
+see identical bits.  The bar: fp32/complex64
+``max|got - ref| <= 1e-4 * max|ref|``; fp64/complex128 ``<= 1e-10 * max|ref|``;
+int64 exact.  ``|.|`` is the complex modulus.
+"""
+from __future__ import annotations
+
+import zlib
+
+import numpy as np
+
+REAL = {np.float32: np.float32, np.float64: np.float64, np.complex64: np.float32, np.complex128: np.float64}
+
+
+def rng(seed: int) -> np.random.Generator:
+    return np.random.default_rng(seed)
+
+
+def seed_of(*key) -> int:
+    """Process-independent seed for a test case (unlike hash(), never salted)."""
+    return zlib.crc32(repr(key).encode())
+
+
+def normal(g, shape, dtype):
+    dtype = np.dtype(dtype)
+    if dtype.kind == "c":
+        return (g.standard_normal(shape) + 1j * g.standard_normal(shape)).astype(dtype)
+    return g.standard_normal(shape).astype(dtype)
+
+
+def coef(g, shape, dtype, rmax=0.99):
+    """Stable scalar coefficients: U(-rmax, rmax) real, r e^{i theta} complex."""
+    dtype = np.dtype(dtype)
+    if dtype.kind == "c":
+        r = g.uniform(0.5, rmax, shape)
+        th = g.uniform(0, np.pi, shape)
+        return (r * np.exp(1j * th)).astype(dtype)
+    return g.uniform(-rmax, rmax, shape).astype(dtype)
+
+
+def biquad_A(g, shape, dtype, rlo=0.5, rhi=0.98):
+    """2x2 transposed-companion matrices [[-a1, 1], [-a2, 0]] of stable biquads.
+
+    Poles r e^{+-i theta}: a1 = -2 r cos(theta), a2 = r^2 (the TDF-II state
+    matrix that philtorch's lfilter builds, philtorch/lti/filtering.py:304-317).
+    For complex dtypes a random phase is applied to the whole matrix.
+    """
+    dtype = np.dtype(dtype)
+    r = g.uniform(rlo, rhi, shape)
+    th = g.uniform(0, np.pi, shape)
+    a1, a2 = -2 * r * np.cos(th), r * r
+    A = np.zeros(shape + (2, 2))
+    A[..., 0, 0] = -a1
+    A[..., 0, 1] = 1.0
+    A[..., 1, 0] = -a2
+    if dtype.kind == "c":
+        ph = np.exp(1j * g.uniform(-0.3, 0.3, shape))[..., None, None]
+        return (A * ph).astype(dtype)
+    return A.astype(dtype)
+
+
+def tol(dtype) -> float:
+    dtype = np.dtype(dtype)
+    if dtype in (np.dtype(np.float32), np.dtype(np.complex64)):
+        return 1e-4
+    if dtype in (np.dtype(np.float64), np.dtype(np.complex128)):
+        return 1e-10
+    return 0.0
+
+
+def check(got, ref, name="", dtype=None):
+    got = np.asarray(got)
+    ref = np.asarray(ref)
+    assert got.shape == ref.shape, f"{name}: shape {got.shape} != {ref.shape}"
+    dtype = dtype or ref.dtype
+    if np.dtype(dtype).kind in "iu":
+        np.testing.assert_array_equal(got, ref, err_msg=name)
+        return 0.0
+    err = float(np.max(np.abs(got.astype(np.complex128) - ref.astype(np.complex128)))) if ref.size else 0.0
+    scale = float(np.max(np.abs(ref))) if ref.size else 0.0
+    bound = tol(dtype) * max(scale, np.finfo(np.float64).tiny)
+    assert err <= bound, f"{name}: max|d|={err:.3e} > {tol(dtype):.0e} * max|ref| ({scale:.3e})"
+    return err / max(scale, 1e-300)
