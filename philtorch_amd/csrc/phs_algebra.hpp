@@ -118,19 +118,59 @@ struct Vec2 {
 };
 
 // ---------------------------------------------------------------- algebras
-// Scalar first-order scan: coefficient and state are both T.
+// Storage vs compute precision: data move in the caller's dtype, but every
+// scan operation (lane folds, map compositions, look-back payloads and
+// reductions) runs in the wide type below.  The path is bandwidth-bound, so
+// fp64 arithmetic costs no throughput, and it keeps the parallel
+// reassociation far inside the fp32 parity bar even for non-normal 2x2
+// sections with poles near the unit circle.
+template <typename T>
+struct Wide {
+  using type = T;
+};
+template <>
+struct Wide<float> {
+  using type = double;
+};
+template <>
+struct Wide<c64> {
+  using type = c128;
+};
+
+template <typename T>
+__device__ __forceinline__ typename Wide<T>::type up(T v) {
+  return widen(v);
+}
+template <typename T>
+__device__ __forceinline__ T down(typename Wide<T>::type v) {
+  T o;
+  narrow(v, o);
+  return o;
+}
+
+// Scalar first-order scan: coefficient and state are both one scalar.
 template <typename T>
 struct Scalar {
-  using elem = T;
-  using coef = T;
-  using state = T;
-  using acc_coef = typename Num<T>::acc;
-  static constexpr int kCoefElems = 1;   // scalars of T per coefficient
-  static constexpr int kStateElems = 1;  // scalars of T per state
+  using elem = T;                       // storage scalar
+  using ct = typename Wide<T>::type;    // compute scalar
+  using s_coef = T;                     // coefficient as stored
+  using s_state = T;                    // state as stored
+  using coef = ct;
+  using state = ct;
+  using acc_coef = ct;
+  static constexpr int kCoefElems = 1;
+  static constexpr int kStateElems = 1;
+  static constexpr int kRounds = 4;
 
-  static __device__ __forceinline__ coef cone() { return Num<T>::one(); }
-  static __device__ __forceinline__ coef czero() { return Num<T>::zero(); }
-  static __device__ __forceinline__ state szero() { return Num<T>::zero(); }
+  static __device__ __forceinline__ coef load_c(s_coef v) { return up(v); }
+  static __device__ __forceinline__ state load_s(s_state v) { return up(v); }
+  static __device__ __forceinline__ s_coef store_c(coef v) { return down<T>(v); }
+  static __device__ __forceinline__ s_state store_s(state v) { return down<T>(v); }
+  static __device__ __forceinline__ s_coef s_czero() { return Num<T>::zero(); }
+  static __device__ __forceinline__ s_state s_szero() { return Num<T>::zero(); }
+
+  static __device__ __forceinline__ coef cone() { return Num<ct>::one(); }
+  static __device__ __forceinline__ state szero() { return Num<ct>::zero(); }
   // q * p  (apply p first)
   static __device__ __forceinline__ coef cmul(coef q, coef p) { return mul(q, p); }
   // A h + x
@@ -140,34 +180,42 @@ struct Scalar {
   static __device__ __forceinline__ coef adjoint(coef A) { return cj(A); }
   // lambda conj(y)^T : the per-step gradient of the coefficient
   static __device__ __forceinline__ coef outer(state lam, state y) { return mul(lam, cj(y)); }
-  static __device__ __forceinline__ acc_coef acc_zero() { return widen(Num<T>::zero()); }
-  static __device__ __forceinline__ acc_coef acc_add(acc_coef s, coef v) { return add(s, widen(v)); }
+  static __device__ __forceinline__ acc_coef acc_zero() { return Num<ct>::zero(); }
+  static __device__ __forceinline__ acc_coef acc_add(acc_coef s, coef v) { return add(s, v); }
   static __device__ __forceinline__ acc_coef acc_sum(acc_coef a, acc_coef b) { return add(a, b); }
-  static __device__ __forceinline__ coef acc_narrow(acc_coef s) {
-    coef o;
-    narrow(s, o);
-    return o;
-  }
 };
 
 // 2x2 state-space recursion (biquad sections): coefficient Mat2, state Vec2.
 template <typename T>
 struct Block2 {
   using elem = T;
-  using coef = Mat2<T>;
-  using state = Vec2<T>;
-  using acc_t = typename Num<T>::acc;
-  using acc_coef = Mat2<acc_t>;
+  using ct = typename Wide<T>::type;
+  using s_coef = Mat2<T>;
+  using s_state = Vec2<T>;
+  using coef = Mat2<ct>;
+  using state = Vec2<ct>;
+  using acc_coef = Mat2<ct>;
   static constexpr int kCoefElems = 4;
   static constexpr int kStateElems = 2;
+  static constexpr int kRounds = 2;
 
-  static __device__ __forceinline__ coef cone() {
-    return {Num<T>::one(), Num<T>::zero(), Num<T>::zero(), Num<T>::one()};
+  static __device__ __forceinline__ coef load_c(s_coef v) {
+    return {up(v.m00), up(v.m01), up(v.m10), up(v.m11)};
   }
-  static __device__ __forceinline__ coef czero() {
+  static __device__ __forceinline__ state load_s(s_state v) { return {up(v.v0), up(v.v1)}; }
+  static __device__ __forceinline__ s_coef store_c(coef v) {
+    return {down<T>(v.m00), down<T>(v.m01), down<T>(v.m10), down<T>(v.m11)};
+  }
+  static __device__ __forceinline__ s_state store_s(state v) { return {down<T>(v.v0), down<T>(v.v1)}; }
+  static __device__ __forceinline__ s_coef s_czero() {
     return {Num<T>::zero(), Num<T>::zero(), Num<T>::zero(), Num<T>::zero()};
   }
-  static __device__ __forceinline__ state szero() { return {Num<T>::zero(), Num<T>::zero()}; }
+  static __device__ __forceinline__ s_state s_szero() { return {Num<T>::zero(), Num<T>::zero()}; }
+
+  static __device__ __forceinline__ coef cone() {
+    return {Num<ct>::one(), Num<ct>::zero(), Num<ct>::zero(), Num<ct>::one()};
+  }
+  static __device__ __forceinline__ state szero() { return {Num<ct>::zero(), Num<ct>::zero()}; }
   static __device__ __forceinline__ coef cmul(coef q, coef p) {
     coef r;
     r.m00 = mad(q.m00, p.m00, mul(q.m01, p.m10));
@@ -189,27 +237,17 @@ struct Block2 {
     return {cj(A.m00), cj(A.m10), cj(A.m01), cj(A.m11)};
   }
   static __device__ __forceinline__ coef outer(state lam, state y) {
-    T y0 = cj(y.v0), y1 = cj(y.v1);
+    ct y0 = cj(y.v0), y1 = cj(y.v1);
     return {mul(lam.v0, y0), mul(lam.v0, y1), mul(lam.v1, y0), mul(lam.v1, y1)};
   }
   static __device__ __forceinline__ acc_coef acc_zero() {
-    acc_t z = widen(Num<T>::zero());
-    return {z, z, z, z};
+    return {Num<ct>::zero(), Num<ct>::zero(), Num<ct>::zero(), Num<ct>::zero()};
   }
   static __device__ __forceinline__ acc_coef acc_add(acc_coef s, coef v) {
-    return {add(s.m00, widen(v.m00)), add(s.m01, widen(v.m01)), add(s.m10, widen(v.m10)),
-            add(s.m11, widen(v.m11))};
+    return {add(s.m00, v.m00), add(s.m01, v.m01), add(s.m10, v.m10), add(s.m11, v.m11)};
   }
   static __device__ __forceinline__ acc_coef acc_sum(acc_coef a, acc_coef b) {
     return {add(a.m00, b.m00), add(a.m01, b.m01), add(a.m10, b.m10), add(a.m11, b.m11)};
-  }
-  static __device__ __forceinline__ coef acc_narrow(acc_coef s) {
-    coef o;
-    narrow(s.m00, o.m00);
-    narrow(s.m01, o.m01);
-    narrow(s.m10, o.m10);
-    narrow(s.m11, o.m11);
-    return o;
   }
 };
 

@@ -37,7 +37,7 @@ Layout make_layout(int64_t B, int64_t T, bool TV, bool shared, bool backward) {
   }
   if (backward && TV && shared) {  // per-step gradients before the batch sum
     L.scratch_off = off;
-    off = align_up(off + size_t(B) * size_t(T) * sizeof(typename Alg::coef));
+    off = align_up(off + size_t(B) * size_t(T) * sizeof(typename Alg::s_coef));
   }
   L.total = off;
   return L;
@@ -81,7 +81,7 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
     else
       a.partials = ws + L.partials_off;
   }
-  bool vec = (size_t(T) * sizeof(typename Alg::state)) % 16 == 0 && aligned16(x) && aligned16(y) &&
+  bool vec = (size_t(T) * sizeof(typename Alg::s_state)) % 16 == 0 && aligned16(x) && aligned16(y) &&
              aligned16(out) && aligned16(a.gcoef) && (!TV || aligned16(coef));
   a.vec_ok = vec ? 1 : 0;
 

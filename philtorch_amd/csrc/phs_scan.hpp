@@ -49,10 +49,11 @@ constexpr int kWaves = kThreads / 64;
 
 template <class Alg>
 struct Shape {
-  using coef = typename Alg::coef;
   using state = typename Alg::state;
-  static constexpr int K = sizeof(state) >= 16 ? 1 : int(16 / sizeof(state));
-  static constexpr int R = sizeof(Map<Alg>) > 32 ? 2 : 4;
+  using s_state = typename Alg::s_state;
+  // steps per lane and round: one 16-byte vector of stored states (or more)
+  static constexpr int K = sizeof(s_state) >= 16 ? 1 : int(16 / sizeof(s_state));
+  static constexpr int R = Alg::kRounds;
   static constexpr int kWaveSeg = 64 * K * R;
   static constexpr int kTile = kWaves * kWaveSeg;
   static constexpr int kIncWords = sizeof(state) / 4;
@@ -244,8 +245,10 @@ __device__ __forceinline__ void store_chunk(X *row, int64_t t0, int64_t T, bool 
 //       grad_x, lambda[t] conj(y[t-1])^T the coefficient grad, nu[0] grad_zi.
 template <class Alg, bool TV, bool REV>
 __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs<Alg> a) {
-  using C = typename Alg::coef;
+  using C = typename Alg::coef;      // compute types
   using S = typename Alg::state;
+  using SC = typename Alg::s_coef;   // storage types
+  using SS = typename Alg::s_state;
   using M = Map<Alg>;
   using Sh = Shape<Alg>;
   constexpr int K = Sh::K, R = Sh::R;
@@ -271,31 +274,43 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs<Alg> a) {
   const int64_t seg0 = qf * Sh::kTile + int64_t(w) * Sh::kWaveSeg;
   const bool vec = a.vec_ok != 0;
 
-  const S *xrow = reinterpret_cast<const S *>(a.x) + b * T;
-  const C *crow = reinterpret_cast<const C *>(a.coef) + b * a.coef_row_stride;
+  const SS *xrow = reinterpret_cast<const SS *>(a.x) + b * T;
+  const SC *crow = reinterpret_cast<const SC *>(a.coef) + b * a.coef_row_stride;
+  const SS *yrow_in = reinterpret_cast<const SS *>(a.y) + b * T;
   const S zero_s = Alg::szero();
   // Steps past the end of the row load a zero coefficient and a zero input.
   // Forward they follow every valid step, so they only touch the aggregate of
   // the row's last tile, which nobody reads.  Backward they come first, where
   // the carry is zero anyway, and keep it zero.
-  const C zero_c = Alg::czero();
+  const SC zero_sc = Alg::s_czero();
+  const SS zero_ss = Alg::s_szero();
 
   // ---- loads (all rounds issued up front)
-  S X[R][K];
-  C A[TV ? R : 1][TV ? K : 1];
-  S Y[REV ? R : 1][REV ? K : 1];
-  C a_row = zero_c;
-  if (!TV) a_row = crow[0];
+  SS X[R][K];
+  SC A[TV ? R : 1][TV ? K : 1];
+  SS Y[REV ? R : 1][REV ? K : 1];
+  SS Yfirst[REV ? R : 1];  // backward: y[t-1] for lane 0 of each round
+  C a_row = Alg::load_c(zero_sc);
+  if (!TV) a_row = Alg::load_c(crow[0]);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t t0 = seg0 + int64_t(r) * 64 * K + int64_t(lane) * K;
-    load_chunk<S, K>(xrow, t0, T, vec, X[r], zero_s);
-    if constexpr (TV) load_chunk<C, K>(crow, t0, T, vec, A[r], zero_c);
-    if constexpr (REV) load_chunk<S, K>(reinterpret_cast<const S *>(a.y) + b * T, t0, T, vec, Y[r], zero_s);
+    load_chunk<SS, K>(xrow, t0, T, vec, X[r], zero_ss);
+    if constexpr (TV) load_chunk<SC, K>(crow, t0, T, vec, A[r], zero_sc);
+    if constexpr (REV) {
+      load_chunk<SS, K>(yrow_in, t0, T, vec, Y[r], zero_ss);
+      Yfirst[r] = zero_ss;
+      if (lane == 0) {
+        if (t0 == 0)
+          Yfirst[r] = reinterpret_cast<const SS *>(a.zi)[b];
+        else if (t0 - 1 < T)
+          Yfirst[r] = yrow_in[t0 - 1];
+      }
+    }
   }
   auto coef_at = [&](int r, int k) -> C {
     if constexpr (TV) {
-      C v = A[r][k];
+      const C v = Alg::load_c(A[r][k]);
       return REV ? Alg::adjoint(v) : v;
     } else {
       return REV ? Alg::adjoint(a_row) : a_row;
@@ -313,9 +328,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs<Alg> a) {
     for (int kk = 0; kk < K; ++kk) {
       const int k = REV ? K - 1 - kk : kk;
       const C c = coef_at(r, k);
+      const S xv = Alg::load_s(X[r][k]);
       M e;
       e.A = c;
-      e.x = REV ? Alg::affine(c, X[r][k], zero_s) : X[r][k];
+      e.x = REV ? Alg::affine(c, xv, zero_s) : xv;
       m = compose<Alg>(m, e);
     }
     // inclusive scan over lanes in scan order
@@ -347,7 +363,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs<Alg> a) {
   // ---- look-back (wave 0)
   if (w == 0) {
     uint64_t *row_status = a.status + b * a.tiles_per_row * Sh::kStride;
-    const S virt = REV ? zero_s : reinterpret_cast<const S *>(a.zi)[b];
+    const S virt = REV ? zero_s : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
     S yin;
     if (qs == 0) {
       yin = virt;
@@ -364,28 +380,22 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs<Alg> a) {
 
   // ---- pass 2
   if constexpr (!REV) {
-    S *yrow = reinterpret_cast<S *>(a.out) + b * T;
+    SS *yrow = reinterpret_cast<SS *>(a.out) + b * T;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t t0 = seg0 + int64_t(r) * 64 * K + int64_t(lane) * K;
       S h = apply<Alg>(Ex[r], hw);
-      S O[K];
+      SS O[K];
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        h = Alg::affine(coef_at(r, k), h, X[r][k]);
-        O[k] = h;
+        h = Alg::affine(coef_at(r, k), h, Alg::load_s(X[r][k]));
+        O[k] = Alg::store_s(h);
       }
-      store_chunk<S, K>(yrow, t0, T, vec, O);
+      store_chunk<SS, K>(yrow, t0, T, vec, O);
     }
   } else {
-    // y[t-1] for the first step of the wave segment
-    S yseg = zero_s;
-    if (seg0 == 0)
-      yseg = reinterpret_cast<const S *>(a.zi)[b];
-    else if (seg0 - 1 < T)
-      yseg = reinterpret_cast<const S *>(a.y)[b * T + seg0 - 1];
-    S *gxrow = a.out ? reinterpret_cast<S *>(a.out) + b * T : nullptr;
-    C *gcrow = a.gcoef ? reinterpret_cast<C *>(a.gcoef) + b * T : nullptr;
+    SS *gxrow = a.out ? reinterpret_cast<SS *>(a.out) + b * T : nullptr;
+    SC *gcrow = a.gcoef ? reinterpret_cast<SC *>(a.gcoef) + b * T : nullptr;
     typename Alg::acc_coef acc = Alg::acc_zero();
     const bool want_acc = a.partials != nullptr;
     // the rounds are walked from the end of the segment towards its start
@@ -393,32 +403,29 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs<Alg> a) {
     for (int rr = 0; rr < R; ++rr) {
       const int r = R - 1 - rr;
       const int64_t t0 = seg0 + int64_t(r) * 64 * K + int64_t(lane) * K;
-      S yprev[K];
-#pragma unroll
-      for (int k = 1; k < K; ++k) yprev[k] = Y[r][k - 1];
-      {
-        S nb = shfl_from(Y[r][K - 1], lane - 1);
-        if (lane == 0) nb = (r == 0) ? yseg : read_lane(Y[r > 0 ? r - 1 : 0][K - 1], 63);
-        yprev[0] = nb;
-      }
+      // y[t-1] for each of this lane's steps: own registers, the previous
+      // lane's last step, or (lane 0) the value loaded from memory
+      SS yp0 = shfl_from(Y[r][K - 1], lane - 1);
+      if (lane == 0) yp0 = Yfirst[r];
       S nu = apply<Alg>(Ex[r], hw);
-      S GX[K];
-      C GC[K];
+      SS GX[K];
+      SC GC[K];
 #pragma unroll
       for (int kk = 0; kk < K; ++kk) {
         const int k = K - 1 - kk;
         const C c = coef_at(r, k);
-        const S lam = Alg::sadd(X[r][k], nu);
-        GX[k] = lam;
-        const C g = Alg::outer(lam, yprev[k]);
-        GC[k] = g;
+        const S lam = Alg::sadd(Alg::load_s(X[r][k]), nu);
+        GX[k] = Alg::store_s(lam);
+        const S yprev = Alg::load_s(k == 0 ? yp0 : Y[r][k > 0 ? k - 1 : 0]);
+        const C g = Alg::outer(lam, yprev);
+        GC[k] = Alg::store_c(g);
         if (want_acc && t0 + k < T) acc = Alg::acc_add(acc, g);
         nu = Alg::affine(c, lam, zero_s);
-        if (t0 + k == 0 && a.gzi) reinterpret_cast<S *>(a.gzi)[b] = nu;
+        if (t0 + k == 0 && a.gzi) reinterpret_cast<SS *>(a.gzi)[b] = Alg::store_s(nu);
       }
-      if (gxrow) store_chunk<S, K>(gxrow, t0, T, vec, GX);
+      if (gxrow) store_chunk<SS, K>(gxrow, t0, T, vec, GX);
       if constexpr (TV) {
-        if (gcrow) store_chunk<C, K>(gcrow, t0, T, vec, GC);
+        if (gcrow) store_chunk<SC, K>(gcrow, t0, T, vec, GC);
       }
     }
     if (want_acc) {
@@ -428,10 +435,10 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs<Alg> a) {
       if (lane == 0) s_acc[w] = acc;
       __syncthreads();
       if (tid == 0) {
-        typename Alg::acc_coef s = s_acc[0];
+        typename Alg::acc_coef sum = s_acc[0];
 #pragma unroll
-        for (int i = 1; i < kWaves; ++i) s = Alg::acc_sum(s, s_acc[i]);
-        reinterpret_cast<typename Alg::acc_coef *>(a.partials)[b * a.tiles_per_row + qf] = s;
+        for (int i = 1; i < kWaves; ++i) sum = Alg::acc_sum(sum, s_acc[i]);
+        reinterpret_cast<typename Alg::acc_coef *>(a.partials)[b * a.tiles_per_row + qf] = sum;
       }
     }
   }
@@ -455,7 +462,7 @@ __global__ __launch_bounds__(kThreads) void reduce_rows_kernel(const void *parti
     __syncthreads();
   }
   if (threadIdx.x == 0)
-    reinterpret_cast<typename Alg::coef *>(out)[blockIdx.x] = Alg::acc_narrow(s[0]);
+    reinterpret_cast<typename Alg::s_coef *>(out)[blockIdx.x] = Alg::store_c(s[0]);
 }
 
 // out[t] = sum_b per_step[b, t]  (LPV coefficient shared across the batch).
@@ -463,13 +470,13 @@ template <class Alg>
 __global__ __launch_bounds__(kThreads) void reduce_batch_kernel(const typename Alg::elem *per_step,
                                                                  int64_t B, int64_t T,
                                                                  typename Alg::elem *out) {
-  using C = typename Alg::coef;
-  const C *p = reinterpret_cast<const C *>(per_step);
+  using SC = typename Alg::s_coef;
+  const SC *p = reinterpret_cast<const SC *>(per_step);
   for (int64_t t = blockIdx.x * int64_t(kThreads) + threadIdx.x; t < T;
        t += int64_t(gridDim.x) * kThreads) {
     typename Alg::acc_coef acc = Alg::acc_zero();
-    for (int64_t b = 0; b < B; ++b) acc = Alg::acc_add(acc, p[b * T + t]);
-    reinterpret_cast<C *>(out)[t] = Alg::acc_narrow(acc);
+    for (int64_t b = 0; b < B; ++b) acc = Alg::acc_add(acc, Alg::load_c(p[b * T + t]));
+    reinterpret_cast<SC *>(out)[t] = Alg::store_c(acc);
   }
 }
 
