@@ -9,8 +9,10 @@ the GPU before timing.
 One step = the hot path over that batch: the forward scan
 ``torch.ops.philtorch.recur`` and the fused adjoint pass
 ``torch.ops.philtorch.recur_backward`` (grad w.r.t. a, x and y0).  Before
-every step a 512 MiB buffer is overwritten so the 256 MB Infinity Cache holds
-none of the step's operands; that write is outside the timed events.
+every step a 512 MiB buffer is read end to end so the 256 MB Infinity Cache
+holds none of the step's operands (a read sweep, not a write: a write would
+leave dirty lines whose write-back then competes with the step); the sweep
+is outside the timed events.
 
 Output: one JSON line (the driver's contract) with
   value        GSamples/s = B*T / (t_fwd + t_bwd), whole job (one GPU)
@@ -114,13 +116,14 @@ def main() -> int:
     a_c, x_c, y0_c, g_c = make_inputs(B, T, dtype)
     dev = torch.device("cuda", 0)
     a, x, y0, gy = (t.to(dev) for t in (a_c, x_c, y0_c, g_c))
-    evict = None if args.no_evict else torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    evict = None if args.no_evict else torch.ones(128 << 20, dtype=torch.float32, device=dev)
+    evict_sink = torch.empty((), dtype=torch.float32, device=dev)
     recur = torch.ops.philtorch.recur
     recur_bwd = torch.ops.philtorch.recur_backward
 
     def step(evs=None):
         if evict is not None:
-            evict.fill_(1)
+            torch.sum(evict, dim=0, out=evict_sink)
         if evs:
             evs[0].record()
         y = recur(a, y0, x)

@@ -66,6 +66,14 @@ const char *phs_error_string(int status);
 /* ABI version of this library (major*100 + minor). */
 int phs_abi_version(void);
 
+/* Testing hook, no counterpart in the reference.  Sets the number of
+ * look-back polls a tile makes before it stops waiting for its predecessors
+ * and computes its entry state from the inputs itself (0 restores the
+ * default, about 0.1 s of waiting).  A tiny value forces that fallback path
+ * so tests can check it; results are identical either way.  Process-wide;
+ * takes effect for calls issued afterwards. */
+void phs_debug_set_spin_limit(unsigned polls);
+
 /* LPV scalar scan.  A: [B,T] (coef_shared=0) or [T] shared by all rows
  * (coef_shared=1); zi: [B]; x, y: [B,T].
  * Replaces philtorch::recurN with 1x1 matrices, the only native time-varying

@@ -57,7 +57,7 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 def _kernel_cmd() -> list[str]:
     tmp = KERNEL_LIB + ".tmp"
-    return [HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "phs_capi.hip"), "-o", tmp]
+    return [HIPCC, *HIP_FLAGS, "-shared", "-Wl,-soname,libphilscan.so", os.path.join(CSRC, "phs_capi.hip"), "-o", tmp]
 
 
 def _ops_cmds() -> tuple[list[str], list[str]]:

@@ -160,7 +160,11 @@ struct Scalar {
   using acc_coef = ct;
   static constexpr int kCoefElems = 1;
   static constexpr int kStateElems = 1;
-  static constexpr int kRounds = 4;
+  static constexpr int kVecsPerLane = 2;
+  static constexpr int kRounds = 2;
+  static constexpr int kWavesPerBlock = 8;
+  // occupancy floor: 4 waves per SIMD keeps 4 tiles resident per CU
+  static constexpr int kMinWavesPerEU = 1;
 
   static __device__ __forceinline__ coef load_c(s_coef v) { return up(v); }
   static __device__ __forceinline__ state load_s(s_state v) { return up(v); }
@@ -168,6 +172,13 @@ struct Scalar {
   static __device__ __forceinline__ s_state store_s(state v) { return down<T>(v); }
   static __device__ __forceinline__ s_coef s_czero() { return Num<T>::zero(); }
   static __device__ __forceinline__ s_state s_szero() { return Num<T>::zero(); }
+
+  // steps of pass 2 run in storage precision from a wide entry state
+  static __device__ __forceinline__ s_state s_affine(s_coef A, s_state h, s_state x) { return mad(A, h, x); }
+  static __device__ __forceinline__ s_coef s_cmul(s_coef q, s_coef p) { return mul(q, p); }
+  static __device__ __forceinline__ s_state s_add(s_state a, s_state b) { return add(a, b); }
+  static __device__ __forceinline__ s_coef s_adjoint(s_coef A) { return cj(A); }
+  static __device__ __forceinline__ s_coef s_outer(s_state lam, s_state y) { return mul(lam, cj(y)); }
 
   static __device__ __forceinline__ coef cone() { return Num<ct>::one(); }
   static __device__ __forceinline__ state szero() { return Num<ct>::zero(); }
@@ -197,7 +208,10 @@ struct Block2 {
   using acc_coef = Mat2<ct>;
   static constexpr int kCoefElems = 4;
   static constexpr int kStateElems = 2;
+  static constexpr int kVecsPerLane = 1;
   static constexpr int kRounds = 2;
+  static constexpr int kWavesPerBlock = 4;
+  static constexpr int kMinWavesPerEU = 1;
 
   static __device__ __forceinline__ coef load_c(s_coef v) {
     return {up(v.m00), up(v.m01), up(v.m10), up(v.m11)};
@@ -211,6 +225,24 @@ struct Block2 {
     return {Num<T>::zero(), Num<T>::zero(), Num<T>::zero(), Num<T>::zero()};
   }
   static __device__ __forceinline__ s_state s_szero() { return {Num<T>::zero(), Num<T>::zero()}; }
+
+  static __device__ __forceinline__ s_state s_affine(s_coef A, s_state h, s_state x) {
+    return {mad(A.m00, h.v0, mad(A.m01, h.v1, x.v0)), mad(A.m10, h.v0, mad(A.m11, h.v1, x.v1))};
+  }
+  static __device__ __forceinline__ s_state s_add(s_state a, s_state b) {
+    return {add(a.v0, b.v0), add(a.v1, b.v1)};
+  }
+  static __device__ __forceinline__ s_coef s_cmul(s_coef q, s_coef p) {
+    return {mad(q.m00, p.m00, mul(q.m01, p.m10)), mad(q.m00, p.m01, mul(q.m01, p.m11)),
+            mad(q.m10, p.m00, mul(q.m11, p.m10)), mad(q.m10, p.m01, mul(q.m11, p.m11))};
+  }
+  static __device__ __forceinline__ s_coef s_adjoint(s_coef A) {
+    return {cj(A.m00), cj(A.m10), cj(A.m01), cj(A.m11)};
+  }
+  static __device__ __forceinline__ s_coef s_outer(s_state lam, s_state y) {
+    T y0 = cj(y.v0), y1 = cj(y.v1);
+    return {mul(lam.v0, y0), mul(lam.v0, y1), mul(lam.v1, y0), mul(lam.v1, y1)};
+  }
 
   static __device__ __forceinline__ coef cone() {
     return {Num<ct>::one(), Num<ct>::zero(), Num<ct>::zero(), Num<ct>::one()};
@@ -258,6 +290,13 @@ struct Map {
   typename Alg::state x;
 };
 
+// The same map in storage precision (a lane's few steps are folded in it).
+template <class Alg>
+struct SMap {
+  typename Alg::s_coef A;
+  typename Alg::s_state x;
+};
+
 template <class Alg>
 __device__ __forceinline__ Map<Alg> map_identity() {
   return {Alg::cone(), Alg::szero()};
@@ -285,6 +324,55 @@ __device__ __forceinline__ X shfl_from(const X &v, int src) {
 #pragma unroll
   for (int i = 0; i < n; ++i) out.w[i] = __shfl(in.w[i], src, 64);
   return out.x;
+}
+
+// DPP lane move of every 32-bit word of `v` (gfx9 DPP control `CTRL`,
+// rows enabled by `ROW_MASK`).  Lanes without a source, or in disabled rows,
+// keep their own value.
+template <int CTRL, int ROW_MASK, typename X>
+__device__ __forceinline__ X dpp_move(const X &v) {
+  constexpr int n = sizeof(X) / 4;
+  union {
+    X x;
+    int w[n];
+  } in, out;
+  in.x = v;
+#pragma unroll
+  for (int i = 0; i < n; ++i) out.w[i] = __builtin_amdgcn_update_dpp(in.w[i], in.w[i], CTRL, ROW_MASK, 0xF, false);
+  return out.x;
+}
+
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+constexpr int kDppWaveShr1 = 0x138;
+
+// Inclusive wave64 scan of `v` under the associative, non-commutative `op`
+// (op(earlier, later)), lane 0 first: four row_shr steps inside each
+// 16-lane row, then row_bcast:15 and row_bcast:31 across rows.
+template <typename X, typename Op>
+__device__ __forceinline__ X wave_scan_incl(X v, int lane, Op op) {
+  const int r = lane & 15;
+  X o;
+  o = dpp_move<kDppRowShr1, 0xF>(v);
+  if (r >= 1) v = op(o, v);
+  o = dpp_move<kDppRowShr2, 0xF>(v);
+  if (r >= 2) v = op(o, v);
+  o = dpp_move<kDppRowShr4, 0xF>(v);
+  if (r >= 4) v = op(o, v);
+  o = dpp_move<kDppRowShr8, 0xF>(v);
+  if (r >= 8) v = op(o, v);
+  o = dpp_move<kDppRowBcast15, 0xA>(v);
+  if (lane & 16) v = op(o, v);
+  o = dpp_move<kDppRowBcast31, 0xC>(v);
+  if (lane >= 32) v = op(o, v);
+  return v;
+}
+
+// Value of the previous lane (lane 0 gets `first`).
+template <typename X>
+__device__ __forceinline__ X wave_shift_up(const X &v, int lane, const X &first) {
+  X o = dpp_move<kDppWaveShr1, 0xF>(v);
+  return lane == 0 ? first : o;
 }
 
 // Value of `v` held by lane `lane` (must be wave-uniform); result is uniform.

@@ -2,10 +2,12 @@
 // Host side: argument checks, workspace carving, and the launch of
 //   scan_kernel [-> reduce kernel]
 // on the caller's stream.  No allocation, no synchronisation, no globals.
-// Workspace layout: [0, 256) header (tile counter, finished blocks, epoch),
+// Workspace layout: [0, 2048) header (16 striped {epoch, claim count} words),
 // then the tile status words, then (backward only) per-tile partial sums or
 // per-step scratch.
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 
 #include "../../include/philscan.h"
 #include "phs_scan.hpp"
@@ -14,6 +16,10 @@ namespace phs {
 namespace {
 
 constexpr size_t kAlign = 256;
+// Look-back polls before a tile computes its entry state itself; about 0.1 s
+// of waiting, far beyond any schedule in which predecessors make progress.
+constexpr unsigned kDefaultSpinLimit = 1u << 16;
+std::atomic<unsigned> g_spin_limit{0};  // testing hook, 0 = default
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
@@ -28,7 +34,7 @@ Layout make_layout(int64_t B, int64_t T, bool TV, bool shared, bool backward) {
   using Sh = Shape<Alg>;
   Layout L;
   L.tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
-  L.status_off = kAlign;
+  L.status_off = align_up(kHeaderBytes);
   L.status_words = size_t(B) * size_t(L.tiles_per_row) * Sh::kStride;
   size_t off = align_up(L.status_off + L.status_words * sizeof(uint64_t));
   if (backward && !TV) {  // per-tile coefficient-gradient partial sums
@@ -55,7 +61,7 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
   if (B == 0 || T == 0) return PHS_OK;
   if (!coef || !zi || !x || (backward ? !y : !out)) return PHS_ERR_INVALID;
   const Layout L = make_layout<Alg>(B, T, TV, shared, backward);
-  if (double(B) * double(L.tiles_per_row) >= 4294967295.0) return PHS_ERR_INVALID;
+  if (double(B) * double(L.tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
   if (!workspace || ws_bytes < L.total) return PHS_ERR_WORKSPACE;
 
   char *ws = static_cast<char *>(workspace);
@@ -72,9 +78,13 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
   a.B = B;
   a.T_len = T;
   a.tiles_per_row = L.tiles_per_row;
-  a.header = reinterpret_cast<unsigned *>(ws);
+  a.claims = reinterpret_cast<unsigned long long *>(ws);
   a.status = reinterpret_cast<uint64_t *>(ws + L.status_off);
-  a.status_capacity = int64_t((ws_bytes - L.status_off) / sizeof(uint64_t));
+  const unsigned tiles = unsigned(B * L.tiles_per_row);
+  a.tiles = tiles;
+  a.per_stripe = (tiles + kStripes - 1) / kStripes;
+  const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
+  a.spin_limit = sl ? sl : kDefaultSpinLimit;
   if (backward && gcoef) {
     if (TV)
       a.gcoef = shared ? reinterpret_cast<E *>(ws + L.scratch_off) : static_cast<E *>(gcoef);
@@ -85,27 +95,27 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
              aligned16(out) && aligned16(a.gcoef) && (!TV || aligned16(coef));
   a.vec_ok = vec ? 1 : 0;
 
-  const unsigned tiles = unsigned(B * L.tiles_per_row);
+  const unsigned grid = a.per_stripe * kStripes;
   if (TV) {
     if (backward)
-      hipLaunchKernelGGL((scan_kernel<Alg, true, true>), dim3(tiles), dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((scan_kernel<Alg, true, true>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
     else
-      hipLaunchKernelGGL((scan_kernel<Alg, true, false>), dim3(tiles), dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((scan_kernel<Alg, true, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
   } else {
     if (backward)
-      hipLaunchKernelGGL((scan_kernel<Alg, false, true>), dim3(tiles), dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((scan_kernel<Alg, false, true>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
     else
-      hipLaunchKernelGGL((scan_kernel<Alg, false, false>), dim3(tiles), dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((scan_kernel<Alg, false, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
   }
   if (backward && gcoef) {
     if (TV && shared) {
-      const int blocks = int(std::min<int64_t>((T + kThreads - 1) / kThreads, 4096));
-      hipLaunchKernelGGL(reduce_batch_kernel<Alg>, dim3(blocks), dim3(kThreads), 0, stream,
+      const int blocks = int(std::min<int64_t>((T + kReduceThreads - 1) / kReduceThreads, 4096));
+      hipLaunchKernelGGL(reduce_batch_kernel<Alg>, dim3(blocks), dim3(kReduceThreads), 0, stream,
                          static_cast<const E *>(a.gcoef), B, T, static_cast<E *>(gcoef));
     } else if (!TV) {
       const int64_t rows = shared ? 1 : B;
       const int64_t count = shared ? B * L.tiles_per_row : L.tiles_per_row;
-      hipLaunchKernelGGL(reduce_rows_kernel<Alg>, dim3(unsigned(rows)), dim3(kThreads), 0, stream,
+      hipLaunchKernelGGL(reduce_rows_kernel<Alg>, dim3(unsigned(rows)), dim3(kReduceThreads), 0, stream,
                          static_cast<const void *>(a.partials), count, static_cast<E *>(gcoef));
     }
   }
@@ -168,6 +178,8 @@ const char *phs_error_string(int status) {
 }
 
 int phs_abi_version(void) { return 100; }
+
+void phs_debug_set_spin_limit(unsigned polls) { phs::g_spin_limit.store(polls, std::memory_order_relaxed); }
 
 #define PHS_FWD(NAME, ALGT, TV)                                                                    \
   int NAME(int dtype, int64_t B, int64_t T, const void *A, int coef_shared, const void *zi,        \

@@ -11,8 +11,9 @@
 //     a round is one contiguous 64*K*sizeof(step) byte run (K*sizeof(state)
 //     is 16 B or more: one dwordx4 per lane and array);
 //   * pass 1: each lane folds its K steps into one affine map; a wave64
-//     Hillis-Steele scan (ds_bpermute) turns lane maps into exclusive maps;
-//     rounds are chained inside the wave; the 4 wave aggregates meet in LDS;
+//     DPP scan (row_shr 1/2/4/8, row_bcast 15/31, wave_shr 1) turns lane
+//     maps into exclusive maps; rounds are chained inside the wave; the 4
+//     wave aggregates meet in LDS;
 //   * look-back (wave 0): the tile publishes its aggregate map, then lane i
 //     polls the status words of predecessor tile q-1-i; the nearest
 //     predecessor with an inclusive state ends the search and the aggregates
@@ -25,37 +26,46 @@
 // accepts a value only when every one of its words carries this call's tag,
 // so payload and flag can never tear and no fence is needed.
 //
-// Self-resetting workspace: the workspace starts with a header
-// {tile counter, finished-block counter, epoch}.  A call tags its words with
-// epoch+1; the last workgroup to finish (it sees the finished counter reach
-// gridDim-1 after every wave of every block has drained its memory traffic)
-// zeroes both counters and stores the new epoch.  Words left by earlier calls
-// carry older tags and are ignored, so the workspace needs zero-filling only
-// once, when it is allocated, and no clearing kernel runs per call.  When the
-// 32-bit tag space wraps, that last workgroup also zeroes the whole status
-// area.  Consecutive calls sharing a workspace must be stream-ordered.
+// Self-resetting workspace: the workspace starts with kStripes 64-bit claim
+// words {epoch (high 32 bits), claim count (low 32 bits)}, one per 128-byte
+// line.  Workgroup g claims from stripe g % kStripes with one atomic add,
+// which returns its claim index c and the epoch; its tile is c*kStripes + g%
+// kStripes (the grid is padded to whole stripes, surplus workgroups exit).
+// Striping keeps same-address atomics from serialising the launch.  The call
+// tags its status words with epoch+1.  The last claimer of each stripe
+// re-arms it with {epoch+1, 0}: every claim on that stripe has happened by
+// then.  Words left by earlier calls carry older tags and are ignored, so the
+// workspace is zero-filled only when allocated (and by its owner again every
+// 2^31 calls, before the 32-bit tags could repeat); no clearing kernel and no
+// end-of-kernel bookkeeping run per call.  Consecutive calls sharing a
+// workspace must be stream-ordered.
 //
-// Tiles are claimed through an atomic counter in launch order, mapped
-// q-major (id = q*B + b): a tile's predecessor always holds a smaller id, so
-// it has been claimed by a running or finished workgroup and every wait ends.
+// Forward progress does not depend on the order in which the hardware starts
+// workgroups: the look-back polls a bounded number of times, and a tile whose
+// predecessors have not all published by then computes its entry state
+// itself, folding every earlier step of its row straight from the inputs.
+// Claims are mapped q-major (id = q*B + b), so in practice predecessors are
+// claimed first and that path is only taken by the tests that force it.
 #pragma once
 
 #include "phs_algebra.hpp"
 
 namespace phs {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-
 template <class Alg>
 struct Shape {
+  static constexpr int kWaves = Alg::kWavesPerBlock;
+  static constexpr int kThreads = 64 * kWaves;
   using state = typename Alg::state;
   using s_state = typename Alg::s_state;
-  // steps per lane and round: one 16-byte vector of stored states (or more)
-  static constexpr int K = sizeof(s_state) >= 16 ? 1 : int(16 / sizeof(s_state));
+  // steps per lane and round: kVecs 16-byte vectors of stored states (one
+  // state per lane when a state is 16 bytes or wider)
+  static constexpr int K =
+      sizeof(s_state) >= 16 ? 1 : Alg::kVecsPerLane * int(16 / sizeof(s_state));
   static constexpr int R = Alg::kRounds;
   static constexpr int kWaveSeg = 64 * K * R;
   static constexpr int kTile = kWaves * kWaveSeg;
+  static_assert(kWaves >= 1 && kWaves <= 16, "1..16 waves per workgroup");
   static constexpr int kIncWords = sizeof(state) / 4;
   static constexpr int kAggWords = sizeof(Map<Alg>) / 4;
   static constexpr int kStride = kIncWords + kAggWords;  // 64-bit words per tile
@@ -74,13 +84,29 @@ struct ScanArgs {
   void *partials;           // backward, LTI: per-tile coefficient-grad sums (nullable)
   T *gzi;                   // backward: grad of zi (nullable)
   int64_t B, T_len, tiles_per_row;
-  unsigned *header;          // [0] tile counter, [1] finished blocks, [2] epoch
+  unsigned long long *claims;  // kStripes claim words, 128 bytes apart (workspace offset 0)
+  unsigned tiles;              // B * tiles_per_row
+  unsigned per_stripe;         // claims per stripe (grid = per_stripe * kStripes)
+  unsigned spin_limit;         // look-back polls before the self-compute fallback
   uint64_t *status;          // status words of this call
-  int64_t status_capacity;   // 64-bit words available from `status` on
   int vec_ok;
 };
 
-enum : int { kHdrCounter = 0, kHdrDone = 1, kHdrEpoch = 2 };
+constexpr int kStripes = 16;
+constexpr int kStripeWords = 16;  // 128 bytes between claim words
+constexpr size_t kHeaderBytes = kStripes * kStripeWords * sizeof(unsigned long long);
+
+__device__ __forceinline__ void claim_tile(unsigned long long *claims, unsigned per_stripe, unsigned &id,
+                                           unsigned &tag) {
+  const unsigned j = blockIdx.x % kStripes;
+  unsigned long long *w = claims + j * kStripeWords;
+  const unsigned long long v = __hip_atomic_fetch_add(w, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned epoch = unsigned(v >> 32), c = unsigned(v);
+  id = c * kStripes + j;
+  tag = epoch + 1u;
+  if (c == per_stripe - 1u)
+    __hip_atomic_store(w, (unsigned long long)(epoch + 1u) << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // ------------------------------------------------------------ status words
 template <typename X>
@@ -117,15 +143,18 @@ __device__ __forceinline__ bool try_read(uint64_t *src, X &v, unsigned tag) {
 
 // Wave-level look-back.  `row_status` points at tile 0 of this row's status;
 // `q` is this tile's position in scan order; `virt` is the state entering
-// the row (zi forward, 0 backward).  Returns the state entering tile q.
+// the row (zi forward, 0 backward).  On success stores the state entering
+// tile q in `out` and returns true; returns false after `spin_limit` polls
+// found some predecessor still unpublished.
 template <class Alg>
-__device__ typename Alg::state lookback(uint64_t *row_status, int64_t q,
-                                        const typename Alg::state &virt, int lane, unsigned tag) {
+__device__ bool lookback(uint64_t *row_status, int64_t q, const typename Alg::state &virt, int lane,
+                         unsigned tag, unsigned spin_limit, typename Alg::state &out) {
   using S = typename Alg::state;
   using M = Map<Alg>;
   using Sh = Shape<Alg>;
   M acc = map_identity<Alg>();
   int64_t base = q - 1;
+  unsigned polls = 0;
   while (true) {
     const int64_t p = base - lane;
     M mv = map_identity<Alg>();
@@ -150,6 +179,7 @@ __device__ typename Alg::state lookback(uint64_t *row_status, int64_t q,
       const uint64_t low = (k >= 64) ? ~0ull : ((1ull << k) - 1ull);
       const uint64_t waiting = __ballot(st == 0) & low;
       if (waiting == 0) break;
+      if (++polls >= spin_limit) return false;
       __builtin_amdgcn_s_sleep(1);
     }
     // lanes [0, k) hold aggregates of tiles q-1-lane (newest at lane 0);
@@ -163,36 +193,11 @@ __device__ typename Alg::state lookback(uint64_t *row_status, int64_t q,
     const M F = read_lane(m, 0);
     if (k < 64) {
       const S yk = read_lane(sv, k);
-      return apply<Alg>(compose<Alg>(F, acc), yk);
+      out = apply<Alg>(compose<Alg>(F, acc), yk);
+      return true;
     }
     acc = compose<Alg>(F, acc);
     base -= 64;
-  }
-}
-
-// End of a workgroup: count it as finished; the last one resets the header
-// for the next call on this workspace (see "Self-resetting workspace").
-__device__ __forceinline__ void retire_block(unsigned *header, uint64_t *status, int64_t capacity,
-                                             unsigned tag, int &s_last) {
-  // every wave drains its outstanding memory operations first, so no status
-  // read of this block can still be in flight when the last block resets
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev =
-        __hip_atomic_fetch_add(header + kHdrDone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == gridDim.x - 1) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  const bool wrap = (tag == 0xFFFFFFFFu);
-  if (wrap)
-    for (int64_t i = threadIdx.x; i < capacity; i += blockDim.x)
-      __hip_atomic_store(status + i, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (threadIdx.x == 0) {
-    __hip_atomic_store(header + kHdrCounter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(header + kHdrDone, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(header + kHdrEpoch, wrap ? 0u : tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -238,40 +243,81 @@ __device__ __forceinline__ void store_chunk(X *row, int64_t t0, int64_t T, bool 
   }
 }
 
+// A lane's K steps folded into one map: in storage precision (the error of
+// a handful of steps is a few ulps), then widened for every later level.
+// Forward step t is (A[t], x[t]); backward it is (A[t]^H, A[t]^H g[t]) and the
+// lane walks its chunk downwards.
+template <class Alg, bool TV, bool REV, int K>
+__device__ __forceinline__ Map<Alg> lane_map(const typename Alg::s_coef (&Ac)[TV ? K : 1],
+                                             const typename Alg::s_state (&Xc)[K],
+                                             const typename Alg::s_coef &a_row) {
+  using SC = typename Alg::s_coef;
+  using SS = typename Alg::s_state;
+  const SS zero_ss = Alg::s_szero();
+  SMap<Alg> f;
+#pragma unroll
+  for (int kk = 0; kk < K; ++kk) {
+    const int k = REV ? K - 1 - kk : kk;
+    const SC raw = TV ? Ac[TV ? k : 0] : a_row;
+    const SC c = REV ? Alg::s_adjoint(raw) : raw;
+    const SS e = REV ? Alg::s_affine(c, Xc[k], zero_ss) : Xc[k];
+    if (kk == 0) {
+      f.A = c;
+      f.x = e;
+    } else {
+      f.A = Alg::s_cmul(c, f.A);
+      f.x = Alg::s_affine(c, f.x, e);
+    }
+  }
+  Map<Alg> m;
+  m.A = Alg::load_c(f.A);
+  m.x = Alg::load_s(f.x);
+  return m;
+}
+
 // ------------------------------------------------------------ the kernel
 // TV  : the coefficient varies along time (LPV); otherwise one per row (LTI).
 // REV : backward adjoint scan, nu[t] = A[t]^H (g[t] + nu[t+1]), run from the
 //       end of the row towards its start; lambda[t] = g[t] + nu[t+1] is
 //       grad_x, lambda[t] conj(y[t-1])^T the coefficient grad, nu[0] grad_zi.
+//
+// Scan order is always ascending in (wave, round, lane); REV mirrors the
+// placement of waves, rounds and lanes in memory instead, so one DPP scan
+// serves both directions.  Inside a lane's K steps REV walks downwards.
 template <class Alg, bool TV, bool REV>
-__global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs<Alg> a) {
+__global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void scan_kernel(ScanArgs<Alg> a) {
   using C = typename Alg::coef;      // compute types
   using S = typename Alg::state;
   using SC = typename Alg::s_coef;   // storage types
   using SS = typename Alg::s_state;
   using M = Map<Alg>;
   using Sh = Shape<Alg>;
-  constexpr int K = Sh::K, R = Sh::R;
+  constexpr int K = Sh::K, R = Sh::R, kWaves = Sh::kWaves;
 
   __shared__ M s_wagg[kWaves];
+  __shared__ M s_wpre[kWaves];
   __shared__ S s_in;
   __shared__ unsigned s_id, s_tag;
-  __shared__ int s_last;
   __shared__ typename Alg::acc_coef s_acc[kWaves];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  if (tid == 0) {
-    s_id = __hip_atomic_fetch_add(a.header + kHdrCounter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_tag = __hip_atomic_load(a.header + kHdrEpoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-  }
+  if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
   __syncthreads();
+  if (s_id >= a.tiles) return;  // padding of the last stripe round
   const int64_t id = s_id;
   const unsigned tag = s_tag;
   const int64_t qs = id / a.B;         // position in scan order
   const int64_t b = id - qs * a.B;
   const int64_t qf = REV ? a.tiles_per_row - 1 - qs : qs;  // position along time
   const int64_t T = a.T_len;
-  const int64_t seg0 = qf * Sh::kTile + int64_t(w) * Sh::kWaveSeg;
+  // memory placement of this wave's segment and of this lane's chunk
+  const int pw = REV ? kWaves - 1 - w : w;
+  const int pl = REV ? 63 - lane : lane;
+  const int64_t seg0 = qf * Sh::kTile + int64_t(pw) * Sh::kWaveSeg;
+  auto chunk0 = [&](int r) -> int64_t {
+    const int pr = REV ? R - 1 - r : r;
+    return seg0 + int64_t(pr) * 64 * K + int64_t(pl) * K;
+  };
   const bool vec = a.vec_ok != 0;
 
   const SS *xrow = reinterpret_cast<const SS *>(a.x) + b * T;
@@ -289,79 +335,50 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs<Alg> a) {
   SS X[R][K];
   SC A[TV ? R : 1][TV ? K : 1];
   SS Y[REV ? R : 1][REV ? K : 1];
-  SS Yfirst[REV ? R : 1];  // backward: y[t-1] for lane 0 of each round
-  C a_row = Alg::load_c(zero_sc);
-  if (!TV) a_row = Alg::load_c(crow[0]);
+  SS Ylow[REV ? R : 1];  // backward: y[t0-1] below the chunk of lane 63
+  const SC a_row_s = TV ? zero_sc : crow[0];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int64_t t0 = seg0 + int64_t(r) * 64 * K + int64_t(lane) * K;
+    const int64_t t0 = chunk0(r);
     load_chunk<SS, K>(xrow, t0, T, vec, X[r], zero_ss);
     if constexpr (TV) load_chunk<SC, K>(crow, t0, T, vec, A[r], zero_sc);
     if constexpr (REV) {
       load_chunk<SS, K>(yrow_in, t0, T, vec, Y[r], zero_ss);
-      Yfirst[r] = zero_ss;
-      if (lane == 0) {
+      Ylow[r] = zero_ss;
+      if (lane == 63) {
         if (t0 == 0)
-          Yfirst[r] = reinterpret_cast<const SS *>(a.zi)[b];
+          Ylow[r] = reinterpret_cast<const SS *>(a.zi)[b];
         else if (t0 - 1 < T)
-          Yfirst[r] = yrow_in[t0 - 1];
+          Ylow[r] = yrow_in[t0 - 1];
       }
     }
   }
-  auto coef_at = [&](int r, int k) -> C {
-    if constexpr (TV) {
-      const C v = Alg::load_c(A[r][k]);
-      return REV ? Alg::adjoint(v) : v;
-    } else {
-      return REV ? Alg::adjoint(a_row) : a_row;
-    }
-  };
+  auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
 
   // ---- pass 1: lane maps, wave scans, round chaining
   M Ex[R];
   M carry = map_identity<Alg>();
 #pragma unroll
-  for (int rr = 0; rr < R; ++rr) {
-    const int r = REV ? R - 1 - rr : rr;
-    M m = map_identity<Alg>();
-#pragma unroll
-    for (int kk = 0; kk < K; ++kk) {
-      const int k = REV ? K - 1 - kk : kk;
-      const C c = coef_at(r, k);
-      const S xv = Alg::load_s(X[r][k]);
-      M e;
-      e.A = c;
-      e.x = REV ? Alg::affine(c, xv, zero_s) : xv;
-      m = compose<Alg>(m, e);
-    }
-    // inclusive scan over lanes in scan order
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int src = REV ? lane + d : lane - d;
-      M o = shfl_from(m, src);
-      if (REV ? (lane + d < 64) : (lane >= d)) m = compose<Alg>(o, m);
-    }
-    M ex = shfl_from(m, REV ? lane + 1 : lane - 1);
-    if (lane == (REV ? 63 : 0)) ex = map_identity<Alg>();
-    const M tot = read_lane(m, REV ? 0 : 63);
+  for (int r = 0; r < R; ++r) {
+    M m = lane_map<Alg, TV, REV, K>(A[TV ? r : 0], X[r], a_row_s);
+    m = wave_scan_incl(m, lane, op);
+    const M ex = wave_shift_up(m, lane, map_identity<Alg>());
+    const M tot = read_lane(m, 63);
     Ex[r] = compose<Alg>(carry, ex);
     carry = compose<Alg>(carry, tot);
   }
 
-  // ---- block: wave aggregates in scan order
+  // ---- block: wave aggregates in scan order, combined by wave 0
   if (lane == 0) s_wagg[w] = carry;
   __syncthreads();
-  M wpre = map_identity<Alg>();
-  M tagg = map_identity<Alg>();
-#pragma unroll
-  for (int i = 0; i < kWaves; ++i) {
-    const int wi = REV ? kWaves - 1 - i : i;
-    if (REV ? (wi > w) : (wi < w)) wpre = compose<Alg>(wpre, s_wagg[wi]);
-    tagg = compose<Alg>(tagg, s_wagg[wi]);
-  }
 
   // ---- look-back (wave 0)
   if (w == 0) {
+    M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
+    v = wave_scan_incl(v, lane, op);
+    const M wex = wave_shift_up(v, lane, map_identity<Alg>());
+    if (lane < kWaves) s_wpre[lane] = wex;
+    const M tagg = read_lane(v, kWaves - 1);
     uint64_t *row_status = a.status + b * a.tiles_per_row * Sh::kStride;
     const S virt = REV ? zero_s : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
     S yin;
@@ -369,66 +386,83 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs<Alg> a) {
       yin = virt;
     } else {
       if (lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
-      yin = lookback<Alg>(row_status, qs, virt, lane, tag);
+      if (!lookback<Alg>(row_status, qs, virt, lane, tag, a.spin_limit, yin)) {
+        // fallback: fold every step of this row that precedes the tile in
+        // scan order, 64*K steps per wave iteration, straight from the inputs
+        M acc = map_identity<Alg>();
+        const int64_t span = qs * Sh::kTile;
+        const int64_t row_end = a.tiles_per_row * Sh::kTile;
+        for (int64_t off = 0; off < span; off += 64 * K) {
+          const int64_t c0 = REV ? row_end - off - int64_t(lane + 1) * K : off + int64_t(lane) * K;
+          SS xs[K];
+          SC cs[TV ? K : 1];
+          load_chunk<SS, K>(xrow, c0, T, vec, xs, zero_ss);
+          if constexpr (TV) load_chunk<SC, K>(crow, c0, T, vec, cs, zero_sc);
+          M m = lane_map<Alg, TV, REV, K>(cs, xs, a_row_s);
+          m = wave_scan_incl(m, lane, op);
+          acc = compose<Alg>(acc, read_lane(m, 63));
+        }
+        yin = apply<Alg>(acc, virt);
+      }
     }
     if (qs + 1 < a.tiles_per_row && lane == 0)
       publish(row_status + qs * Sh::kStride, apply<Alg>(tagg, yin), tag);
     if (lane == 0) s_in = yin;
   }
   __syncthreads();
-  const S hw = apply<Alg>(wpre, s_in);
+  const S hw = apply<Alg>(s_wpre[w], s_in);
 
   // ---- pass 2
   if constexpr (!REV) {
     SS *yrow = reinterpret_cast<SS *>(a.out) + b * T;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t t0 = seg0 + int64_t(r) * 64 * K + int64_t(lane) * K;
-      S h = apply<Alg>(Ex[r], hw);
+      SS h = Alg::store_s(apply<Alg>(Ex[r], hw));
       SS O[K];
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        h = Alg::affine(coef_at(r, k), h, Alg::load_s(X[r][k]));
-        O[k] = Alg::store_s(h);
+        h = Alg::s_affine(TV ? A[r][TV ? k : 0] : a_row_s, h, X[r][k]);
+        O[k] = h;
       }
-      store_chunk<SS, K>(yrow, t0, T, vec, O);
+      store_chunk<SS, K>(yrow, chunk0(r), T, vec, O);
     }
   } else {
     SS *gxrow = a.out ? reinterpret_cast<SS *>(a.out) + b * T : nullptr;
     SC *gcrow = a.gcoef ? reinterpret_cast<SC *>(a.gcoef) + b * T : nullptr;
+    // only LTI coefficients reduce their gradient inside the kernel
+    constexpr bool kAcc = !TV;
     typename Alg::acc_coef acc = Alg::acc_zero();
-    const bool want_acc = a.partials != nullptr;
-    // the rounds are walked from the end of the segment towards its start
+    const bool want_acc = kAcc && a.partials != nullptr;
 #pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-      const int r = R - 1 - rr;
-      const int64_t t0 = seg0 + int64_t(r) * 64 * K + int64_t(lane) * K;
-      // y[t-1] for each of this lane's steps: own registers, the previous
-      // lane's last step, or (lane 0) the value loaded from memory
-      SS yp0 = shfl_from(Y[r][K - 1], lane - 1);
-      if (lane == 0) yp0 = Yfirst[r];
-      S nu = apply<Alg>(Ex[r], hw);
+    for (int r = 0; r < R; ++r) {
+      const int64_t t0 = chunk0(r);
+      // y[t0-1] sits in the last step of the next lane's chunk (lanes are
+      // mirrored), or below the round for lane 63
+      SS ybelow = shfl_from(Y[r][K - 1], lane + 1);
+      if (lane == 63) ybelow = Ylow[r];
+      SS nu = Alg::store_s(apply<Alg>(Ex[r], hw));
       SS GX[K];
       SC GC[K];
 #pragma unroll
       for (int kk = 0; kk < K; ++kk) {
         const int k = K - 1 - kk;
-        const C c = coef_at(r, k);
-        const S lam = Alg::sadd(Alg::load_s(X[r][k]), nu);
-        GX[k] = Alg::store_s(lam);
-        const S yprev = Alg::load_s(k == 0 ? yp0 : Y[r][k > 0 ? k - 1 : 0]);
-        const C g = Alg::outer(lam, yprev);
-        GC[k] = Alg::store_c(g);
-        if (want_acc && t0 + k < T) acc = Alg::acc_add(acc, g);
-        nu = Alg::affine(c, lam, zero_s);
-        if (t0 + k == 0 && a.gzi) reinterpret_cast<SS *>(a.gzi)[b] = Alg::store_s(nu);
+        const SC c = Alg::s_adjoint(TV ? A[r][TV ? k : 0] : a_row_s);
+        const SS lam = Alg::s_add(X[r][k], nu);
+        GX[k] = lam;
+        const SC g = Alg::s_outer(lam, k == 0 ? ybelow : Y[r][k > 0 ? k - 1 : 0]);
+        GC[k] = g;
+        if constexpr (kAcc) {
+          if (want_acc && t0 + k < T) acc = Alg::acc_add(acc, Alg::load_c(g));
+        }
+        nu = Alg::s_affine(c, lam, zero_ss);
+        if (t0 + k == 0 && a.gzi) reinterpret_cast<SS *>(a.gzi)[b] = nu;
       }
       if (gxrow) store_chunk<SS, K>(gxrow, t0, T, vec, GX);
       if constexpr (TV) {
         if (gcrow) store_chunk<SC, K>(gcrow, t0, T, vec, GC);
       }
     }
-    if (want_acc) {
+    if (kAcc && want_acc) {
       // deterministic block reduction of the per-tile coefficient gradient
 #pragma unroll
       for (int d = 32; d >= 1; d >>= 1) acc = Alg::acc_sum(acc, shfl_from(acc, lane ^ d));
@@ -442,22 +476,23 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs<Alg> a) {
       }
     }
   }
-  retire_block(a.header, a.status, a.status_capacity, tag, s_last);
 }
 
 // ------------------------------------------------------------ helpers
+constexpr int kReduceThreads = 256;
+
 // out[i] = sum_{j < count} partials[i*count + j], fixed order, one block per i.
 template <class Alg>
-__global__ __launch_bounds__(kThreads) void reduce_rows_kernel(const void *partials, int64_t count,
+__global__ __launch_bounds__(kReduceThreads) void reduce_rows_kernel(const void *partials, int64_t count,
                                                                 typename Alg::elem *out) {
   using AC = typename Alg::acc_coef;
-  __shared__ AC s[kThreads];
+  __shared__ AC s[kReduceThreads];
   const AC *p = reinterpret_cast<const AC *>(partials) + blockIdx.x * count;
   AC acc = Alg::acc_zero();
-  for (int64_t j = threadIdx.x; j < count; j += kThreads) acc = Alg::acc_sum(acc, p[j]);
+  for (int64_t j = threadIdx.x; j < count; j += kReduceThreads) acc = Alg::acc_sum(acc, p[j]);
   s[threadIdx.x] = acc;
   __syncthreads();
-  for (int h = kThreads / 2; h > 0; h >>= 1) {
+  for (int h = kReduceThreads / 2; h > 0; h >>= 1) {
     if (threadIdx.x < h) s[threadIdx.x] = Alg::acc_sum(s[threadIdx.x], s[threadIdx.x + h]);
     __syncthreads();
   }
@@ -467,13 +502,13 @@ __global__ __launch_bounds__(kThreads) void reduce_rows_kernel(const void *parti
 
 // out[t] = sum_b per_step[b, t]  (LPV coefficient shared across the batch).
 template <class Alg>
-__global__ __launch_bounds__(kThreads) void reduce_batch_kernel(const typename Alg::elem *per_step,
+__global__ __launch_bounds__(kReduceThreads) void reduce_batch_kernel(const typename Alg::elem *per_step,
                                                                  int64_t B, int64_t T,
                                                                  typename Alg::elem *out) {
   using SC = typename Alg::s_coef;
   const SC *p = reinterpret_cast<const SC *>(per_step);
-  for (int64_t t = blockIdx.x * int64_t(kThreads) + threadIdx.x; t < T;
-       t += int64_t(gridDim.x) * kThreads) {
+  for (int64_t t = blockIdx.x * int64_t(kReduceThreads) + threadIdx.x; t < T;
+       t += int64_t(gridDim.x) * kReduceThreads) {
     typename Alg::acc_coef acc = Alg::acc_zero();
     for (int64_t b = 0; b < B; ++b) acc = Alg::acc_add(acc, Alg::load_c(p[b * T + t]));
     reinterpret_cast<SC *>(out)[t] = Alg::store_c(acc);

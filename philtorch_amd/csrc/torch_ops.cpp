@@ -59,26 +59,35 @@ void *stream_of(const Tensor &t) {
 // leaves it ready for the next one on the same stream.  One buffer is kept per
 // (device, stream) and grown geometrically; a replaced buffer goes back to the
 // caching allocator, whose stream-ordered reuse keeps in-flight kernels safe.
+// Status words carry a 32-bit per-call tag, so the buffer is zeroed again
+// every 2^31 calls, long before a tag could repeat.
 // The cache is intentionally leaked at exit (no HIP calls during teardown).
 struct Workspace {
   void *ptr;
   size_t bytes;
 };
 
+struct CachedWorkspace {
+  Tensor buf;
+  uint64_t calls = 0;
+};
+
 Workspace workspace_for(const Tensor &like, size_t bytes, void *stream) {
   static auto *mu = new std::mutex;
-  static auto *cache = new std::map<std::pair<int, void *>, Tensor>;
+  static auto *cache = new std::map<std::pair<int, void *>, CachedWorkspace>;
   std::lock_guard<std::mutex> lock(*mu);
-  const auto key = std::make_pair(int(like.device().index()), stream);
-  auto it = cache->find(key);
-  if (it == cache->end() || size_t(it->second.numel()) < bytes) {
+  CachedWorkspace &entry = (*cache)[std::make_pair(int(like.device().index()), stream)];
+  if (!entry.buf.defined() || size_t(entry.buf.numel()) < bytes) {
     size_t cap = size_t(1) << 16;
-    if (it != cache->end()) cap = std::max(cap, size_t(it->second.numel()) * 2);
+    if (entry.buf.defined()) cap = std::max(cap, size_t(entry.buf.numel()) * 2);
     while (cap < bytes) cap *= 2;
-    Tensor buf = at::zeros({int64_t(cap)}, like.options().dtype(at::kByte));
-    it = cache->insert_or_assign(key, buf).first;
+    entry.buf = at::zeros({int64_t(cap)}, like.options().dtype(at::kByte));
+    entry.calls = 0;
+  } else if (++entry.calls >= (uint64_t(1) << 31)) {
+    entry.buf.zero_();
+    entry.calls = 0;
   }
-  return {it->second.mutable_data_ptr(), size_t(it->second.numel())};
+  return {entry.buf.mutable_data_ptr(), size_t(entry.buf.numel())};
 }
 
 using FwdFn = int (*)(int, int64_t, int64_t, const void *, int, const void *, const void *, void *,

@@ -1,0 +1,51 @@
+"""ctypes binding of libphilscan's C ABI (include/philscan.h), for the tests.
+
+Loads the in-tree library; on a GPU machine torch must be imported first so
+that the HIP runtime torch uses is the one the library binds to.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(REPO, "philtorch_amd", "libphilscan.so")
+HEADER = os.path.join(REPO, "include", "philscan.h")
+
+PHS_OK, PHS_ERR_INVALID, PHS_ERR_WORKSPACE, PHS_ERR_LAUNCH, PHS_ERR_DTYPE = range(5)
+OPS = {"recur": 0, "lti_recur": 1, "recur2": 2, "lti_recur2": 3}
+DTYPES = {np.dtype(np.float32): 0, np.dtype(np.float64): 1, np.dtype(np.complex64): 2,
+          np.dtype(np.complex128): 3, np.dtype(np.int64): 4}
+
+_FWD_ARGS = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+_BWD_ARGS = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+
+
+def declared_symbols() -> list[str]:
+    """Function names declared in include/philscan.h."""
+    import re
+
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(phs_[a-z0-9_]+)\s*\(", text)))
+
+
+def load() -> ctypes.CDLL:
+    lib = ctypes.CDLL(LIB_PATH)
+    for op in OPS:
+        getattr(lib, f"phs_{op}_fwd").argtypes = _FWD_ARGS
+        getattr(lib, f"phs_{op}_fwd").restype = ctypes.c_int
+        getattr(lib, f"phs_{op}_bwd").argtypes = _BWD_ARGS
+        getattr(lib, f"phs_{op}_bwd").restype = ctypes.c_int
+    lib.phs_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                       ctypes.c_int]
+    lib.phs_workspace_size.restype = ctypes.c_size_t
+    lib.phs_error_string.argtypes = [ctypes.c_int]
+    lib.phs_error_string.restype = ctypes.c_char_p
+    lib.phs_debug_set_spin_limit.argtypes = [ctypes.c_uint]
+    lib.phs_debug_set_spin_limit.restype = None
+    return lib

@@ -1,0 +1,74 @@
+"""Write golden vectors from the reference's own CPU extension.
+
+Runs philtorch's CPU operators, compiled from /root/reference/philtorch/csrc by
+oracle/build_ref.py into oracle/_ref/ref_C.so, on small seeded inputs and
+stores inputs and outputs in tests/golden/ref_vectors.npz.  Only data is
+committed; the reference itself never travels with the repository.
+
+    python oracle/build_ref.py && python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, REPO)
+
+from oracle import ref_runner  # noqa: E402
+
+
+def cases():
+    g = np.random.default_rng(20261201)
+    out = []
+    for dt in (np.float32, np.float64, np.complex64, np.complex128):
+        cplx = np.dtype(dt).kind == "c"
+
+        def rnd(*shape):
+            v = g.standard_normal(shape)
+            if cplx:
+                v = v + 1j * g.standard_normal(shape)
+            return v.astype(dt)
+
+        def coef(*shape):
+            v = g.uniform(-0.95, 0.95, shape)
+            if cplx:
+                v = v * np.exp(1j * g.uniform(0, np.pi, shape))
+            return v.astype(dt)
+
+        B, T = 3, 37
+        # recurN with M = 1 (LPV scalar), batched and shared coefficient
+        out.append(("recurN", coef(B, T, 1, 1), rnd(B, 1), rnd(B, T, 1)))
+        out.append(("recurN", coef(T, 1, 1), rnd(B, 1), rnd(B, T, 1)))
+        # recurN with M = 2 (the recur2 math)
+        out.append(("recurN", 0.6 * coef(B, T, 2, 2), rnd(B, 2), rnd(B, T, 2)))
+        out.append(("recurN", 0.6 * coef(T, 2, 2), rnd(B, 2), rnd(B, T, 2)))
+        # LTI scalar: per-row and shared a
+        out.append(("lti_recur", coef(B), rnd(B), rnd(B, T)))
+        out.append(("lti_recur", coef(1), rnd(B), rnd(B, T)))
+        # LTI 2x2: per-row and shared A
+        out.append(("lti_recurN", 0.6 * coef(B, 2, 2), rnd(B, 2), rnd(B, T, 2)))
+        out.append(("lti_recurN", 0.6 * coef(2, 2), rnd(B, 2), rnd(B, T, 2)))
+    # README Fibonacci known answer through lti_recurN in int64
+    x = np.zeros((1, 10, 2), np.int64)
+    x[0, 0, 0] = 1
+    out.append(("lti_recurN", np.array([[1, 1], [1, 0]], np.int64), np.zeros((1, 2), np.int64), x))
+    return out
+
+
+def main() -> None:
+    arrays = {}
+    for i, (op, A, zi, x) in enumerate(cases()):
+        y = ref_runner.run(op, A, zi, x)
+        arrays[f"{i}_op"] = np.array(op)
+        arrays[f"{i}_A"], arrays[f"{i}_zi"], arrays[f"{i}_x"], arrays[f"{i}_y"] = A, zi, x, y
+    path = os.path.join(HERE, "ref_vectors.npz")
+    np.savez_compressed(path, **arrays)
+    print(f"wrote {len(arrays) // 5} cases to {path}")
+
+
+if __name__ == "__main__":
+    main()

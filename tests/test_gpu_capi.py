@@ -1,0 +1,168 @@
+"""GPU parity through the C ABI itself (ctypes -> libphilscan -> HIP kernels).
+
+Device memory comes from torch; every call passes raw device pointers, sizes
+and the current stream exactly as a C/C++ caller of include/philscan.h would.
+Also covers the self-compute fallback of the look-back (forced with a tiny
+poll budget through phs_debug_set_spin_limit), workspace reuse across calls of
+different shapes, and the error codes.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from tests import _data as D
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def api(hip):
+    import torch
+
+    from tests import capi
+
+    lib = capi.load()
+    dev = torch.device("cuda", 0)
+    # one workspace for every call of this module, zero-filled once
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+    yield lib, ws, capi
+    lib.phs_debug_set_spin_limit(0)
+
+
+def _dev(x):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream():
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _run(api, op, A, shared, zi, x, gy):
+    """Forward + backward of one op through the C ABI; returns numpy results."""
+    import torch
+
+    lib, ws, capi = api
+    dt = capi.DTYPES[np.dtype(x.dtype)]
+    B, T = x.shape[:2]
+    tA, tz, tx, tg = _dev(A), _dev(zi), _dev(x), _dev(gy)
+    y = torch.empty_like(tx)
+    need = lib.phs_workspace_size(capi.OPS[op], dt, B, T, int(shared), 1)
+    assert need <= ws.numel()
+    rc = getattr(lib, f"phs_{op}_fwd")(dt, B, T, _p(tA), int(shared), _p(tz), _p(tx), _p(y), _p(ws), ws.numel(),
+                                       _stream())
+    assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+    gA, gz, gx = torch.empty_like(tA), torch.empty_like(tz), torch.empty_like(tx)
+    rc = getattr(lib, f"phs_{op}_bwd")(dt, B, T, _p(tA), int(shared), _p(tz), _p(y), _p(tg), _p(gx), _p(gA),
+                                       _p(gz), _p(ws), ws.numel(), _stream())
+    assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+    torch.cuda.synchronize()
+    return [t.cpu().numpy() for t in (y, gA, gz, gx)]
+
+
+def _case(op, B, T, dtype, shared, seed):
+    g = D.rng(seed)
+    if op == "recur":
+        A = D.coef(g, (T,) if shared else (B, T), dtype)
+        zi, x, gy = D.normal(g, (B,), dtype), D.normal(g, (B, T), dtype), D.normal(g, (B, T), dtype)
+    elif op == "lti_recur":
+        A = D.coef(g, (1,) if shared else (B,), dtype)
+        zi, x, gy = D.normal(g, (B,), dtype), D.normal(g, (B, T), dtype), D.normal(g, (B, T), dtype)
+    elif op == "recur2":
+        A = D.biquad_A(g, (T,) if shared else (B, T), dtype)
+        zi, x, gy = D.normal(g, (B, 2), dtype), D.normal(g, (B, T, 2), dtype), D.normal(g, (B, T, 2), dtype)
+    else:
+        A = D.biquad_A(g, () if shared else (B,), dtype)
+        zi, x, gy = D.normal(g, (B, 2), dtype), D.normal(g, (B, T, 2), dtype), D.normal(g, (B, T, 2), dtype)
+    return A, zi, x, gy
+
+
+def _oracle(op, A, zi, x, gy):
+    import oracle
+
+    if op == "recur":
+        y = oracle.recur(A, zi, x)
+        return [y, *oracle.recur_bwd(A, zi, y, gy)]
+    if op == "lti_recur":
+        y = oracle.lti_recur(A, zi, x)
+        return [y, *oracle.lti_recur_bwd(A, zi, y, gy)]
+    if op == "recur2":
+        y = oracle.recurN(A, zi, x)
+        return [y, *oracle.recurN_bwd(A, zi, y, gy)]
+    y = oracle.lti_recurN(A, zi, x)
+    return [y, *oracle.lti_recurN_bwd(A, zi, y, gy)]
+
+
+def _check(got, ref):
+    for name, a, b in zip(("y", "grad_A", "grad_zi", "grad_x"), got, ref):
+        D.check(a.reshape(b.shape), b, name)
+
+
+CASES = [
+    ("recur", 3, 20000, np.float32, False),
+    ("recur", 2, 9001, np.float64, True),
+    ("recur", 2, 5000, np.complex64, False),
+    ("lti_recur", 4, 30000, np.complex64, False),
+    ("lti_recur", 3, 7000, np.float64, True),
+    ("recur2", 2, 6000, np.float32, False),
+    ("recur2", 2, 3000, np.float64, True),
+    ("lti_recur2", 3, 9000, np.float32, False),
+    ("lti_recur2", 2, 4000, np.complex128, True),
+]
+
+
+@pytest.mark.parametrize("op,B,T,dtype,shared", CASES)
+def test_capi_parity(api, op, B, T, dtype, shared):
+    A, zi, x, gy = _case(op, B, T, dtype, shared, D.seed_of("capi", op, B, T, np.dtype(dtype).str, shared))
+    _check(_run(api, op, A, zi=zi, x=x, gy=gy, shared=shared), _oracle(op, A, zi, x, gy))
+
+
+@pytest.mark.parametrize("op,B,T,dtype,shared", CASES[::2] + [("recur", 2, 1 << 20, np.float32, False)])
+def test_capi_lookback_fallback(api, op, B, T, dtype, shared):
+    """With a poll budget of 1, waiting tiles fold their row's prefix from the
+    inputs themselves; results must not change."""
+    lib = api[0]
+    A, zi, x, gy = _case(op, B, T, dtype, shared, D.seed_of("fallback", op, B, T, np.dtype(dtype).str))
+    lib.phs_debug_set_spin_limit(1)
+    try:
+        got = _run(api, op, A, zi=zi, x=x, gy=gy, shared=shared)
+    finally:
+        lib.phs_debug_set_spin_limit(0)
+    _check(got, _oracle(op, A, zi, x, gy))
+
+
+def test_capi_workspace_reuse_many_calls(api):
+    """One workspace, many calls of changing shapes: the per-call tags must
+    keep every call independent of the status words left by earlier ones."""
+    for i, (B, T) in enumerate([(4, 70000), (1, 3), (7, 8193), (4, 70000), (2, 200000), (3, 5)]):
+        A, zi, x, gy = _case("recur", B, T, np.float32, False, 500 + i)
+        _check(_run(api, "recur", A, zi=zi, x=x, gy=gy, shared=False), _oracle("recur", A, zi, x, gy))
+
+
+def test_capi_errors(api):
+    import torch
+
+    lib, ws, capi = api
+    x = torch.zeros(2, 100, device="cuda")
+    z = torch.zeros(2, device="cuda")
+    y = torch.empty_like(x)
+    s = _stream()
+    need = lib.phs_workspace_size(0, 0, 2, 100, 0, 0)
+    assert need > 0
+    assert lib.phs_recur_fwd(0, 2, 100, _p(x), 0, _p(z), _p(x), _p(y), _p(ws), need - 1, s) == capi.PHS_ERR_WORKSPACE
+    assert lib.phs_recur_fwd(0, 2, 100, _p(x), 0, _p(z), _p(x), _p(y), None, 0, s) == capi.PHS_ERR_WORKSPACE
+    assert lib.phs_recur_fwd(9, 2, 100, _p(x), 0, _p(z), _p(x), _p(y), _p(ws), ws.numel(), s) == capi.PHS_ERR_DTYPE
+    assert lib.phs_recur_fwd(0, -1, 100, _p(x), 0, _p(z), _p(x), _p(y), _p(ws), ws.numel(), s) == capi.PHS_ERR_INVALID
+    assert lib.phs_recur_fwd(0, 2, 100, None, 0, _p(z), _p(x), _p(y), _p(ws), ws.numel(), s) == capi.PHS_ERR_INVALID
+    # empty problems are a no-op
+    assert lib.phs_recur_fwd(0, 0, 100, None, 0, None, None, None, None, 0, s) == capi.PHS_OK
+    assert lib.phs_recur_fwd(0, 2, 0, None, 0, None, None, None, None, 0, s) == capi.PHS_OK
+    assert b"workspace" in lib.phs_error_string(capi.PHS_ERR_WORKSPACE)

@@ -1,0 +1,155 @@
+"""Host-side checks that need no GPU: the C ABI library, the op registrations
+and fake kernels, and the pure-PyTorch routes of the Python API."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import _data as D
+from tests import capi
+
+
+# ------------------------------------------------------------ C ABI library
+def test_capi_exports_every_declared_symbol():
+    lib = ctypes.CDLL(capi.LIB_PATH)
+    declared = capi.declared_symbols()
+    assert len(declared) >= 12
+    missing = [name for name in declared if not hasattr(lib, name)]
+    assert not missing, f"declared in include/philscan.h but not exported: {missing}"
+
+
+def test_capi_host_only_calls():
+    lib = capi.load()
+    assert lib.phs_abi_version() == 100
+    for op in capi.OPS.values():
+        for dt in capi.DTYPES.values():
+            fwd = lib.phs_workspace_size(op, dt, 64, 65536, 0, 0)
+            bwd = lib.phs_workspace_size(op, dt, 64, 65536, 0, 1)
+            assert 0 < fwd <= bwd
+    assert lib.phs_workspace_size(0, 0, 0, 10, 0, 0) == 0
+    assert lib.phs_workspace_size(7, 0, 4, 10, 0, 0) == 0
+    assert lib.phs_workspace_size(0, 9, 4, 10, 0, 0) == 0
+    # shared LPV backward needs per-step scratch for the batch reduction
+    assert lib.phs_workspace_size(0, 0, 8, 1 << 20, 1, 1) > lib.phs_workspace_size(0, 0, 8, 1 << 20, 0, 1) + 8 * 4 * (1 << 20) - 4096
+    for code in range(5):
+        assert lib.phs_error_string(code)
+    # argument errors are reported before anything is launched
+    dummy = ctypes.c_void_p(16)
+    assert lib.phs_recur_fwd(9, 2, 100, dummy, 0, dummy, dummy, dummy, dummy, 1 << 20, None) == capi.PHS_ERR_DTYPE
+    assert lib.phs_recur_fwd(0, -1, 100, dummy, 0, dummy, dummy, dummy, dummy, 1 << 20, None) == capi.PHS_ERR_INVALID
+    assert lib.phs_recur_fwd(0, 2, 100, None, 0, dummy, dummy, dummy, dummy, 1 << 20, None) == capi.PHS_ERR_INVALID
+    assert lib.phs_recur_fwd(0, 2, 100, dummy, 0, dummy, dummy, dummy, None, 0, None) == capi.PHS_ERR_WORKSPACE
+    assert lib.phs_recur_bwd(0, 2, 100, dummy, 0, dummy, None, dummy, dummy, dummy, dummy, dummy, 1 << 20,
+                             None) == capi.PHS_ERR_INVALID
+    assert lib.phs_recur_fwd(0, 0, 100, None, 0, None, None, None, None, 0, None) == capi.PHS_OK
+
+
+# ------------------------------------------------------------ op registration
+def test_ops_registered_with_reference_schemas():
+    import philtorch_amd  # noqa: F401
+
+    for name in ("recur2", "recurN", "lti_recur2", "lti_recurN", "lti_recur", "recur"):
+        schema = getattr(torch.ops.philtorch, name).default._schema
+        assert str(schema) == f"philtorch::{name}(Tensor A, Tensor zi, Tensor x) -> Tensor"
+        assert torch.Tag.pt2_compliant_tag in getattr(torch.ops.philtorch, name).default.tags
+    for name in ("recur_backward", "recurN_backward", "lti_recur_backward", "lti_recurN_backward"):
+        schema = str(getattr(torch.ops.philtorch, name).default._schema)
+        assert schema.endswith("-> (Tensor, Tensor, Tensor)")
+
+
+def test_cpu_tensors_raise():
+    import philtorch_amd  # noqa: F401
+
+    with pytest.raises(NotImplementedError):
+        torch.ops.philtorch.recur(torch.zeros(2, 3), torch.zeros(2), torch.zeros(2, 3))
+
+
+@pytest.mark.parametrize(
+    "op,A,zi,x",
+    [
+        ("recur", (4, 100), (4,), (4, 100)),
+        ("recur", (100,), (4,), (4, 100)),
+        ("recurN", (4, 100, 2, 2), (4, 2), (4, 100, 2)),
+        ("recur2", (100, 2, 2), (4, 2), (4, 100, 2)),
+        ("lti_recur", (4,), (4,), (4, 100)),
+        ("lti_recur", (), (4,), (4, 100)),
+        ("lti_recur2", (4, 2, 2), (4, 2), (4, 100, 2)),
+        ("lti_recurN", (3, 3), (4, 3), (4, 100, 3)),
+    ],
+)
+def test_fake_kernels_shapes(op, A, zi, x):
+    import philtorch_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        fa, fz, fx = torch.empty(A), torch.empty(zi), torch.empty(x)
+        y = getattr(torch.ops.philtorch, op)(fa, fz, fx)
+        assert y.shape == fx.shape and y.is_contiguous()
+
+
+def test_fake_kernel_rejects_mismatch():
+    import philtorch_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        with pytest.raises(RuntimeError):
+            torch.ops.philtorch.recur2(torch.empty(5, 99, 2, 2), torch.empty(5, 2), torch.empty(5, 100, 2))
+
+
+# ------------------------------------------------------------ Python API, CPU route
+@pytest.mark.parametrize("unroll", [1, 7, 64])
+@pytest.mark.parametrize("shared", [False, True])
+def test_lpv_linear_recurrence_cpu_route(unroll, shared):
+    from philtorch_amd import lpv
+
+    g = D.rng(10)
+    B, T = 3, 301
+    a = D.coef(g, (T,) if shared else (B, T), np.float64)
+    x, zi = D.normal(g, (B, T), np.float64), D.normal(g, (B,), np.float64)
+    y = lpv.linear_recurrence(torch.from_numpy(a), torch.from_numpy(zi), torch.from_numpy(x), unroll_factor=unroll)
+    a_full = np.broadcast_to(a, (B, T)) if shared else a
+    np.testing.assert_allclose(y.numpy(), oracle.recur(np.ascontiguousarray(a_full), zi, x), rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("unroll", [1, 5, 32])
+def test_lti_linear_recurrence_cpu_route(unroll):
+    from philtorch_amd import lti
+
+    g = D.rng(11)
+    B, T = 3, 257
+    a = D.coef(g, (B,), np.complex128)
+    x, zi = D.normal(g, (B, T), np.complex128), D.normal(g, (B,), np.complex128)
+    y = lti.linear_recurrence(torch.from_numpy(a), torch.from_numpy(zi), torch.from_numpy(x), unroll_factor=unroll)
+    np.testing.assert_allclose(y.numpy(), oracle.lti_recur(a, zi, x), rtol=1e-10, atol=1e-10)
+
+
+def test_linear_recurrence_argument_errors():
+    from philtorch_amd import lpv, lti
+
+    x = torch.zeros(2, 10)
+    with pytest.raises(ValueError):
+        lpv.linear_recurrence(torch.zeros(10), torch.zeros(2), x, unroll_factor=0)
+    with pytest.raises(ValueError):
+        lpv.linear_recurrence(torch.zeros(9), torch.zeros(2), x)
+    with pytest.raises(ValueError):
+        lpv.linear_recurrence(torch.zeros(10), torch.zeros(3), x)
+    with pytest.raises(ValueError):
+        lti.linear_recurrence(torch.zeros(3), torch.zeros(2), x)
+    with pytest.raises(AssertionError):
+        lti.linear_recurrence(torch.zeros(2, 2), torch.zeros(2), x)
+
+
+def test_extension_flag_and_loader():
+    import philtorch_amd
+
+    assert philtorch_amd.EXTENSION_LOADED
+    assert philtorch_amd.HELION_LOADED is False
+    philtorch_amd.require_extension()
+
+
+def test_graft_entry_points_importable():
+    import __graft_entry__
+
+    assert callable(__graft_entry__.build) and callable(__graft_entry__.smoke)

@@ -1,0 +1,243 @@
+"""Pins of the CPU oracle (CPU only).
+
+The oracle restates philtorch's CPU extension and backward closures; these
+tests make sure a plausible slip in that restatement (dropped term, wrong
+index or sign, transposed operand) cannot survive:
+
+* golden vectors written by the reference's own CPU operators
+  (tests/golden/ref_vectors.npz, from oracle/_ref/ref_C.so built from the
+  reference sources) — the forward must match them bit for bit;
+* the same comparison live against oracle/_ref when that library is present;
+* closed forms: a = 0, a = 1 (cumsum), x = 0 (cumprod), constant a against
+  scipy.signal.lfilter;
+* an explicit product formula and explicit matrix products on small inputs;
+* the README Fibonacci known answer in int64;
+* backward: central finite differences (fp64) and the adjoint identity
+  <g, J d> = <J^T g, d> with J applied through the (independently pinned)
+  forward.
+"""
+import os
+
+import numpy as np
+import pytest
+import scipy.signal
+
+import oracle
+from tests import _data as D
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz")
+FLOATS = [np.float32, np.float64, np.complex64, np.complex128]
+
+
+def _oracle_fwd(op, A, zi, x):
+    if op == "recurN":
+        return oracle.recurN(A, zi, x)
+    if op == "lti_recurN":
+        return oracle.lti_recurN(A, zi, x)
+    return oracle.lti_recur(A, zi, x)
+
+
+def _golden_cases():
+    data = np.load(GOLDEN)
+    n = len([k for k in data.files if k.endswith("_op")])
+    return [(str(data[f"{i}_op"]), data[f"{i}_A"], data[f"{i}_zi"], data[f"{i}_x"], data[f"{i}_y"]) for i in range(n)]
+
+
+@pytest.mark.parametrize("case", range(33))
+def test_oracle_matches_reference_golden_vectors(case):
+    op, A, zi, x, y = _golden_cases()[case]
+    got = _oracle_fwd(op, A, zi, x)
+    assert got.dtype == y.dtype and got.shape == y.shape
+    np.testing.assert_array_equal(got, y)  # same operations in the same order
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(os.path.dirname(oracle.__file__), "_ref", "ref_C.so")),
+                    reason="oracle/_ref not built (needs the reference sources)")
+@pytest.mark.parametrize("dtype", [np.float32, np.complex128])
+def test_oracle_matches_live_reference_build(dtype):
+    from oracle import ref_runner
+
+    g = D.rng(77)
+    B, T = 4, 513
+    A = D.biquad_A(g, (B, T), dtype)
+    zi, x = D.normal(g, (B, 2), dtype), D.normal(g, (B, T, 2), dtype)
+    np.testing.assert_array_equal(oracle.recurN(A, zi, x), ref_runner.run("recurN", A, zi, x))
+    a = D.coef(g, (B,), dtype)
+    zs, xs = D.normal(g, (B,), dtype), D.normal(g, (B, T), dtype)
+    np.testing.assert_array_equal(oracle.lti_recur(a, zs, xs), ref_runner.run("lti_recur", a, zs, xs))
+
+
+# ------------------------------------------------------------ closed forms
+@pytest.mark.parametrize("dtype", FLOATS)
+def test_closed_forms_scalar(dtype):
+    g = D.rng(1)
+    B, T = 3, 200
+    x, zi = D.normal(g, (B, T), dtype), D.normal(g, (B,), dtype)
+    zero, one = np.zeros((B, T), dtype), np.ones((B, T), dtype)
+    np.testing.assert_allclose(oracle.recur(zero, zi, x), x)  # a = 0: y = x
+    rtol = 1e-4 if np.dtype(dtype) in (np.dtype(np.float32), np.dtype(np.complex64)) else 1e-12
+    np.testing.assert_allclose(oracle.recur(one, zi, x), np.cumsum(x, axis=1) + zi[:, None], rtol=rtol, atol=rtol * 20)
+    a = D.coef(g, (B, T), dtype)
+    np.testing.assert_allclose(oracle.recur(a, zi, np.zeros_like(x)), zi[:, None] * np.cumprod(a, axis=1),
+                               rtol=rtol, atol=1e-30)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.complex128])
+def test_constant_coefficient_matches_scipy_lfilter(dtype):
+    g = D.rng(2)
+    B, T = 4, 500
+    a = D.coef(g, (B,), dtype)
+    x, zi = D.normal(g, (B, T), dtype), D.normal(g, (B,), dtype)
+    for b in range(B):
+        # y[t] = a y[t-1] + x[t], y[-1] = zi  <=>  lfilter([1], [1, -a], x, zi=[a zi])
+        ref, _ = scipy.signal.lfilter([1.0], [1.0, -a[b]], x[b], zi=[a[b] * zi[b]])
+        np.testing.assert_allclose(oracle.lti_recur(a, zi, x)[b], ref, rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(oracle.recur(np.broadcast_to(a[:, None], (B, T)), zi, x)[b], ref, rtol=1e-12,
+                                   atol=1e-12)
+
+
+def test_explicit_product_formula():
+    """y[t] = (prod_{s<=t} a_s) zi + sum_{s<=t} (prod_{s<u<=t} a_u) x_s."""
+    g = D.rng(3)
+    B, T = 2, 9
+    a, x, zi = D.coef(g, (B, T), np.float64), D.normal(g, (B, T), np.float64), D.normal(g, (B,), np.float64)
+    ref = np.zeros((B, T))
+    for b in range(B):
+        for t in range(T):
+            acc = np.prod(a[b, : t + 1]) * zi[b]
+            for s in range(t + 1):
+                acc += np.prod(a[b, s + 1 : t + 1]) * x[b, s]
+            ref[b, t] = acc
+    np.testing.assert_allclose(oracle.recur(a, zi, x), ref, rtol=1e-13, atol=1e-13)
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_matrix_recursion_explicit_products(shared):
+    """h[t] = A[t] h[t-1] + x[t] by explicit numpy matrix-vector products;
+    catches a transposed A (row vs column contraction)."""
+    g = D.rng(4)
+    B, T = 3, 11
+    A = g.standard_normal((T, 2, 2) if shared else (B, T, 2, 2)) * 0.7
+    x, zi = g.standard_normal((B, T, 2)), g.standard_normal((B, 2))
+    ref = np.zeros((B, T, 2))
+    for b in range(B):
+        h = zi[b]
+        for t in range(T):
+            h = (A[t] if shared else A[b, t]) @ h + x[b, t]
+            ref[b, t] = h
+    np.testing.assert_allclose(oracle.recurN(A, zi, x), ref, rtol=1e-13, atol=1e-13)
+    # LTI: time-invariant A equals LPV with A repeated along time
+    A0 = A[0] if shared else A[:, 0]
+    At = np.broadcast_to(A0[..., None, :, :] if not shared else A0, (B, T, 2, 2) if not shared else (T, 2, 2))
+    np.testing.assert_allclose(oracle.lti_recurN(A0, zi, x), oracle.recurN(np.ascontiguousarray(At), zi, x),
+                               rtol=1e-13, atol=1e-13)
+
+
+def test_biquad_tdf2_matches_scipy():
+    """A transposed-direct-form-II biquad as a 2x2 LTI recursion equals
+    scipy.signal.lfilter, with initial state and output y = h[t-1][0] + b0 x."""
+    g = D.rng(5)
+    T = 400
+    b = np.array([0.3, -0.2, 0.5])
+    a = np.array([1.0, -1.2, 0.5])
+    x = g.standard_normal(T)
+    zi = g.standard_normal(2)
+    A = np.array([[-a[1], 1.0], [-a[2], 0.0]])  # companion(a)^T
+    Bv = b[1:] - b[0] * a[1:]
+    h = oracle.lti_recurN(A, zi[None], (x[:, None] * Bv)[None])[0]
+    prev = np.vstack([zi[None], h[:-1]])
+    y = prev[:, 0] + b[0] * x
+    ref, zf = scipy.signal.lfilter(b, a, x, zi=zi)
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(h[-1], zf, rtol=1e-12, atol=1e-12)
+
+
+def test_fibonacci_known_answer():
+    """philtorch README.md:143-159: lti_recur2 with [[1,1],[1,0]] in int64."""
+    A = np.array([[1, 1], [1, 0]], np.int64)
+    x = np.zeros((1, 10, 2), np.int64)
+    x[0, 0, 0] = 1
+    y = oracle.lti_recurN(A, np.zeros((1, 2), np.int64), x)
+    assert y[0, :, 0].tolist() == [1, 1, 2, 3, 5, 8, 13, 21, 34, 55]
+
+
+# ------------------------------------------------------------ backward
+def _fd_grad(f, v, eps=1e-6):
+    """Central differences of the scalar f(v) for real v (fp64)."""
+    g = np.zeros_like(v)
+    it = np.nditer(v, flags=["multi_index"])
+    for _ in it:
+        i = it.multi_index
+        vp, vm = v.copy(), v.copy()
+        vp[i] += eps
+        vm[i] -= eps
+        g[i] = (f(vp) - f(vm)) / (2 * eps)
+    return g
+
+
+@pytest.mark.parametrize("kind", ["recur", "recur_shared", "lti", "lti_shared", "recurN", "recurN_shared",
+                                  "lti_recurN", "lti_recurN_shared"])
+def test_backward_finite_differences(kind):
+    g = D.rng(D.seed_of("fd", kind))
+    B, T = 2, 6
+    if kind.startswith("recurN"):
+        A = g.standard_normal((T, 2, 2) if kind.endswith("shared") else (B, T, 2, 2)) * 0.6
+        zi, x, gy = g.standard_normal((B, 2)), g.standard_normal((B, T, 2)), g.standard_normal((B, T, 2))
+        fwd, bwd = oracle.recurN, oracle.recurN_bwd
+    elif kind.startswith("lti_recurN"):
+        A = g.standard_normal((2, 2) if kind.endswith("shared") else (B, 2, 2)) * 0.6
+        zi, x, gy = g.standard_normal((B, 2)), g.standard_normal((B, T, 2)), g.standard_normal((B, T, 2))
+        fwd, bwd = oracle.lti_recurN, oracle.lti_recurN_bwd
+    elif kind.startswith("lti"):
+        A = g.uniform(-0.9, 0.9, (1,) if kind.endswith("shared") else (B,))
+        zi, x, gy = g.standard_normal(B), g.standard_normal((B, T)), g.standard_normal((B, T))
+        fwd, bwd = oracle.lti_recur, oracle.lti_recur_bwd
+    else:
+        A = g.uniform(-0.9, 0.9, (T,) if kind.endswith("shared") else (B, T))
+        zi, x, gy = g.standard_normal(B), g.standard_normal((B, T)), g.standard_normal((B, T))
+        fwd, bwd = oracle.recur, oracle.recur_bwd
+    y = fwd(A, zi, x)
+    gA, gzi, gx = bwd(A, zi, y, gy)
+    loss = lambda A_, zi_, x_: float(np.sum(fwd(A_, zi_, x_) * gy))  # noqa: E731
+    np.testing.assert_allclose(gA, _fd_grad(lambda v: loss(v, zi, x), A).reshape(gA.shape), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(gzi, _fd_grad(lambda v: loss(A, v, x), zi), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(gx, _fd_grad(lambda v: loss(A, zi, v), x), rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.complex128])
+def test_backward_adjoint_identity(dtype):
+    """For fixed A the forward is linear in (zi, x): J d = recur(A, dzi, dx).
+    Then <g, J d> must equal <grad_zi, dzi> + <grad_x, dx> (real inner
+    products; complex uses Re<u, v> with the conjugate-linear convention)."""
+    g = D.rng(6)
+    B, T = 3, 300
+    A = D.coef(g, (B, T), dtype)
+    zi, x, gy = D.normal(g, (B,), dtype), D.normal(g, (B, T), dtype), D.normal(g, (B, T), dtype)
+    dzi, dx = D.normal(g, (B,), dtype), D.normal(g, (B, T), dtype)
+    y = oracle.recur(A, zi, x)
+    _, gzi, gx = oracle.recur_bwd(A, zi, y, gy)
+    Jd = oracle.recur(A, dzi, dx)
+    lhs = np.real(np.vdot(gy, Jd))
+    rhs = np.real(np.vdot(gzi, dzi)) + np.real(np.vdot(gx, dx))
+    assert abs(lhs - rhs) <= 1e-10 * max(1.0, abs(lhs))
+
+
+def test_complex_coefficient_gradient_convention():
+    """grad_A = lambda conj(h[t-1]): the Wirtinger convention torch uses for
+    complex autograd; checked against torch.autograd on a tiny fp64 loop."""
+    import torch
+
+    g = D.rng(7)
+    B, T = 2, 5
+    A = D.coef(g, (B, T), np.complex128)
+    zi, x, gy = D.normal(g, (B,), np.complex128), D.normal(g, (B, T), np.complex128), D.normal(g, (B, T), np.complex128)
+    tA = torch.tensor(A, requires_grad=True)
+    h = torch.tensor(zi)
+    outs = []
+    for t in range(T):
+        h = tA[:, t] * h + torch.tensor(x[:, t])
+        outs.append(h)
+    torch.stack(outs, 1).backward(torch.tensor(gy))
+    y = oracle.recur(A, zi, x)
+    gA, _, _ = oracle.recur_bwd(A, zi, y, gy)
+    np.testing.assert_allclose(gA, tA.grad.numpy(), rtol=1e-12, atol=1e-12)
