@@ -15,10 +15,13 @@ leave dirty lines whose write-back then competes with the step); the sweep
 is outside the timed events.
 
 Output: one JSON line (the driver's contract) with
-  value        GSamples/s = B*T / (t_fwd + t_bwd), whole job (one GPU)
+  value        GSamples/s = B*T / t_step, whole job (one GPU); t_step is the
+               mean over the K timed steps of one HIP-event pair around the
+               forward and backward launches
   roofline     the dominant kernel (the backward scan): algorithmic bytes per
                launch (20 B/sample: read a, g, y; write grad_x, grad_a) over
-               its mean HIP-event duration, against 8 TB/s
+               its mean HIP-event duration from a second pass that puts an
+               event between the two launches, against 8 TB/s
   cpu_baseline the oracle (a C restatement of the reference CPU extension and
                its composite backward, OpenMP over the batch) on a bounded
                sample of the same workload, on this host's cores
@@ -121,36 +124,46 @@ def main() -> int:
     recur = torch.ops.philtorch.recur
     recur_bwd = torch.ops.philtorch.recur_backward
 
-    def step(evs=None):
+    def evict_caches():
         if evict is not None:
             torch.sum(evict, dim=0, out=evict_sink)
-        if evs:
-            evs[0].record()
+
+    def step():
         y = recur(a, y0, x)
-        if evs:
-            evs[1].record()
-        out = recur_bwd(a, y0, y, gy)
-        if evs:
-            evs[2].record()
-        return out
+        return recur_bwd(a, y0, y, gy)
 
     for _ in range(args.warmup):
+        evict_caches()
         step()
     torch.cuda.synchronize()
 
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    # timed region: K steps, each bracketed by one event pair (the cache
+    # eviction before each step stays outside the events)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     for i in range(args.steps):
-        step(events[i])
+        evict_caches()
+        ev[i][0].record()
+        step()
+        ev[i][1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
+    ms_per_step = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
 
-    t_fwd = [e[0].elapsed_time(e[1]) for e in events]  # ms
-    t_bwd = [e[1].elapsed_time(e[2]) for e in events]
-    mean_fwd = sum(t_fwd) / len(t_fwd)
-    mean_bwd = sum(t_bwd) / len(t_bwd)
-    ms_per_step = mean_fwd + mean_bwd
+    # roofline pass: the same steps with an event between the two kernels,
+    # giving each kernel's mean launch duration on the stream it runs on
+    kev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for i in range(args.steps):
+        evict_caches()
+        kev[i][0].record()
+        y = recur(a, y0, x)
+        kev[i][1].record()
+        recur_bwd(a, y0, y, gy)
+        kev[i][2].record()
+    torch.cuda.synchronize()
+    mean_fwd = sum(e[0].elapsed_time(e[1]) for e in kev) / args.steps
+    mean_bwd = sum(e[1].elapsed_time(e[2]) for e in kev) / args.steps
     samples = B * T
     esize = 4 if dtype == "float32" else 8
     bwd_bytes = 5 * esize * samples  # read a, g, y; write grad_x, grad_a
@@ -179,8 +192,8 @@ def main() -> int:
             "cache_evicted_between_steps": evict is not None,
         },
         "detail": {
-            "ms_fwd": round(mean_fwd, 5),
-            "ms_bwd": round(mean_bwd, 5),
+            "ms_fwd_kernel": round(mean_fwd, 5),
+            "ms_bwd_kernel": round(mean_bwd, 5),
             "fwd_GBs_algorithmic": round(fwd_bytes / (mean_fwd * 1e-3) / 1e9, 1),
             "bwd_GBs_algorithmic": round(bwd_bytes / (mean_bwd * 1e-3) / 1e9, 1),
             "wall_s_timed_region": round(wall, 4),

@@ -1,0 +1,353 @@
+"""Time-varying (LPV) state-space recursion and models (philtorch/lpv/ssm.py).
+
+``MatrixRecurrence`` is the autograd Function over ``philtorch::recur2`` /
+``philtorch::recurN`` (reference philtorch/lpv/ssm.py:34-115).  On a HIP
+device with ``unroll_factor == 1`` the recursion runs as one native scan;
+elsewhere the reference's pure-PyTorch routes are kept: a per-step loop, or a
+two-level blocked scan for ``unroll_factor > 1``.
+
+The M = 1 case of ``_ext_ss_recur`` calls the native scalar scan
+``philtorch::recur``; the reference sends it to the third-party
+``torchlpc.sample_wise_lpc`` (philtorch/lpv/ssm.py:188-195), which computes
+the same recurrence with the coefficient negated.
+"""
+from __future__ import annotations
+
+from typing import Any, Optional
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+from torch.autograd import Function
+
+from .. import EXTENSION_LOADED, HELION_LOADED
+
+
+def extension_backend_indicator(x: Tensor, M: int) -> bool:
+    """True when the native scan serves this input: extension loaded, the
+    tensor on a HIP device, and a scalar or 2x2 state (philtorch/lpv/ssm.py:20-26)."""
+    return EXTENSION_LOADED and x.is_cuda and M <= 2
+
+
+class MatrixRecurrence(Function):
+    """Autograd Function of the native M x M LPV scan ``h[t] = A[t] h[t-1] + x[t]``.
+
+    A: ``[T, M, M]`` (shared) or ``[B, T, M, M]``; zi: ``[B, M]``; x: ``[B, T, M]``.
+    backward: fused adjoint kernel without ``create_graph``, otherwise the
+    composite formula through this Function (reference lpv/ssm.py:64-99).
+    jvp: one more scan with input ``dx + dA h[t-1]`` (lpv/ssm.py:101-115).
+    """
+
+    @staticmethod
+    def forward(A: Tensor, zi: Tensor, x: Tensor) -> Tensor:
+        if x.size(-1) == 2:
+            return torch.ops.philtorch.recur2(A, zi, x)
+        return torch.ops.philtorch.recurN(A, zi, x)
+
+    @staticmethod
+    def setup_context(ctx: Any, inputs: tuple, output: Tensor) -> None:
+        A, zi, _ = inputs
+        ctx.save_for_backward(A, zi, output)
+        ctx.save_for_forward(A, zi, output)
+
+    @staticmethod
+    def backward(ctx: Any, grad_y: Tensor):
+        A, zi, y = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        if not torch.is_grad_enabled():
+            gA, gzi, gx = torch.ops.philtorch.recurN_backward(A, zi, y, grad_y)
+            return (gA if needs[0] else None, gzi if needs[1] else None, gx if needs[2] else None)
+        AH = A.mT.conj_physical()
+        coef = torch.roll(AH, -1, dims=-3).flip(-3)
+        lam = MatrixRecurrence.apply(coef, torch.zeros_like(zi), grad_y.flip(1)).flip(1)
+        grad_A = grad_zi = grad_x = None
+        if needs[1]:
+            grad_zi = (AH[..., 0, :, :] @ lam[:, 0, :, None]).squeeze(-1)
+        if needs[2]:
+            grad_x = lam
+        if needs[0]:
+            prev = torch.cat([zi.unsqueeze(1), y[:, :-1]], dim=1).conj_physical()
+            per_step = lam.unsqueeze(-1) * prev.unsqueeze(-2)
+            grad_A = per_step if A.dim() == 4 else per_step.sum(0)
+        return grad_A, grad_zi, grad_x
+
+    @staticmethod
+    def jvp(ctx: Any, grad_A: Optional[Tensor], grad_zi: Optional[Tensor], grad_x: Optional[Tensor]) -> Tensor:
+        A, zi, y = ctx.saved_tensors
+        t_zi = grad_zi if grad_zi is not None else torch.zeros_like(zi)
+        t_x = grad_x if grad_x is not None else torch.zeros_like(y)
+        if grad_A is not None:
+            prev = torch.cat([zi.unsqueeze(1), y[:, :-1]], dim=1)
+            t_x = t_x + (grad_A @ prev.unsqueeze(-1)).squeeze(-1)
+        return MatrixRecurrence.apply(A, t_zi, t_x)
+
+
+def _widen(x: Tensor, M: int) -> Tensor:
+    """``[B, T]`` input driving the first state only -> ``[B, T, M]``."""
+    return torch.cat([x.unsqueeze(-1), x.new_zeros(*x.shape, M - 1)], dim=-1)
+
+
+def _recursion_loop(A: Tensor, zi: Tensor, x: Tensor, out_idx: Optional[int] = None) -> Tensor:
+    """Per-step PyTorch loop (philtorch/lpv/ssm.py:118-164)."""
+    assert x.size(1) == A.size(-3), (
+        f"State matrix A must have the same time dimension as x, got A: {A.size(-3)}, x: {x.size(1)}"
+    )
+    if x.dim() == 2:
+        x = _widen(x, A.size(-1))
+    h = zi
+    outs = []
+    for t in range(x.size(1)):
+        At = A[t] if A.dim() == 3 else A[:, t]
+        h = (At @ h.unsqueeze(-1)).squeeze(-1) + x[:, t]
+        outs.append(h if out_idx is None else h[:, out_idx])
+    return torch.stack(outs, dim=1)
+
+
+def _ext_ss_recur(A: Tensor, zi: Tensor, x: Tensor, *, out_idx: Optional[int] = None, **_) -> Tensor:
+    """Native recursion (philtorch/lpv/ssm.py:167-205)."""
+    assert EXTENSION_LOADED or HELION_LOADED, "Compiled extension or the Helion backend is not available"
+    M = A.size(-1)
+    if M == 1:
+        xs = x if x.dim() == 2 else x.squeeze(-1)
+        coef = A[..., 0, 0]  # [T] shared or [B, T]
+        y = torch.ops.philtorch.recur(coef, zi.reshape(-1), xs).unsqueeze(-1)
+    else:
+        if x.dim() == 2:
+            x = _widen(x, M)
+        y = MatrixRecurrence.apply(A, zi, x)
+    if out_idx is not None and y.dim() == 3:
+        y = y[:, :, out_idx]
+    return y
+
+
+def _prefix_products(A: Tensor) -> Tensor:
+    """P[..., i, :, :] = A[i] ... A[1] A[0] along dim -3."""
+    out = [A[..., 0, :, :]]
+    for i in range(1, A.size(-3)):
+        out.append(A[..., i, :, :] @ out[-1])
+    return torch.stack(out, dim=-3)
+
+
+def state_space_recursion(
+    A: Tensor, zi: Tensor, x: Tensor, *, unroll_factor: int = 1, out_idx: Optional[int] = None
+) -> Tensor:
+    """States of ``h[t] = A[t] h[t-1] + x[t]`` (philtorch/lpv/ssm.py:208-334).
+
+    Args:
+        A: ``[N, M, M]`` or ``[B, N, M, M]``.
+        zi: ``[B, M]`` initial states.
+        x: ``[B, N, M]`` or ``[B, N]`` (drives the first state).
+        unroll_factor: 1 = native scan on a HIP device (per-step loop on the
+            CPU); ``k > 1`` = blocked PyTorch scan with blocks of ``k`` steps.
+        out_idx: return only this state index.
+    Returns:
+        ``[B, N, M]`` (or ``[B, N]`` with ``out_idx``).
+    """
+    assert x.dim() in (2, 3), f"Input signal must be 2D or 3D (batch, time, [features]), got {x.shape}"
+    assert A.dim() in (3, 4), f"State matrix A must be 3D or 4D, got {A.shape}"
+    assert A.size(-2) == A.size(-1), f"State matrix A must be square, got {A.shape}"
+    assert A.size(-3) == x.size(1), (
+        f"State matrix A must have the same time dimension as x, got A: {A.size(-3)}, x: {x.size(1)}"
+    )
+    if A.dim() == 4:
+        assert x.size(0) == A.size(0), (
+            f"Batch size of A must match batch size of x, got A: {A.size(0)}, x: {x.size(0)}"
+        )
+    if x.dim() == 3:
+        assert A.size(-1) == x.size(-1), (
+            f"Last dimension of A must match last dimension of x, got A: {A.size(-1)}, x: {x.size(-1)}"
+        )
+    batch, N = x.size(0), x.size(1)
+    M = A.size(-1)
+    assert zi.dim() == 2, f"Initial conditions zi must be 2D, got {zi.shape}"
+    assert zi.size(0) == batch, f"Batch size of zi must match batch size of x, got zi: {zi.size(0)}, x: {batch}"
+    assert zi.size(1) == M, f"Last dimension of zi must match last dimension of A, got zi: {zi.size(1)}, A: {M}"
+    if unroll_factor < 1:
+        raise ValueError("Unroll factor must be >= 1")
+    k = unroll_factor
+
+    if k == 1 or k >= N:
+        if k == 1 and extension_backend_indicator(x, M):
+            return _ext_ss_recur(A, zi, x, out_idx=out_idx)
+        return _recursion_loop(A, zi, x, out_idx=out_idx)
+
+    if x.dim() == 2:
+        x = _widen(x, M)
+    pad = (-N) % k
+    if pad:
+        x = F.pad(x, (0, 0, 0, pad))
+        A = F.pad(A, (0, 0, 0, 0, 0, pad))
+    xb = x.unflatten(1, (-1, k))  # [B, n, k, M]
+    Ab = A.unflatten(-3, (-1, k))  # [n, k, M, M] or [B, n, k, M, M]
+    # block-local scans from a zero state, k vectorised steps
+    h = torch.zeros_like(xb[:, :, 0])
+    cols = []
+    for i in range(k):
+        h = (Ab[..., i, :, :] @ h.unsqueeze(-1)).squeeze(-1) + xb[:, :, i]
+        cols.append(h)
+    local = torch.stack(cols, dim=2)  # [B, n, k, M]
+    gains = _prefix_products(Ab)  # [.., n, k, M, M]
+    carries = state_space_recursion(gains[..., -1, :, :], zi, local[:, :, -1], unroll_factor=k)  # [B, n, M]
+    prev = torch.cat([zi.unsqueeze(1), carries[:, :-1]], dim=1)  # state entering each block
+    out = local + (gains @ prev.unsqueeze(2).unsqueeze(-1)).squeeze(-1)
+    out = out.flatten(1, 2)[:, :N]
+    return out if out_idx is None else out[..., out_idx]
+
+
+def _apply_B(x: Tensor, B: Optional[Tensor], batch: int, N: int, M: int, features: int) -> Tensor:
+    """Input matrix shapes of philtorch/lpv/ssm.py:413-454."""
+    if B is None:
+        return x
+    shape = tuple(B.shape)
+    if shape == (M,):
+        assert x.dim() == 2, f"Input signal x must be 2D when B is of shape {M,}, got {x.shape}"
+        return x.unsqueeze(-1) * B
+    if len(shape) == 2 and shape == (M, features):
+        return x @ B.T
+    if len(shape) == 2 and shape == (N, M):
+        assert x.dim() == 2
+        return x.unsqueeze(-1) * B
+    if len(shape) == 2 and shape == (batch, M):
+        assert x.dim() == 2
+        return x.unsqueeze(-1) * B.unsqueeze(1)
+    if len(shape) == 3 and shape == (N, M, features):
+        return torch.linalg.vecdot(B.conj(), x.unsqueeze(-2))
+    if len(shape) == 3 and shape == (batch, N, M):
+        assert x.dim() == 2
+        return x.unsqueeze(-1) * B
+    if len(shape) == 3 and shape == (batch, M, features):
+        return torch.linalg.vecdot(B.unsqueeze(1).conj(), x.unsqueeze(-2))
+    if len(shape) == 4 and shape == (batch, N, M, features):
+        return torch.linalg.vecdot(B.conj(), x.unsqueeze(-2))
+    raise ValueError(
+        f"Input matrix B must be of shape ({M},), ({M, features}), ({N, M}), ({batch, M}), "
+        f"({N, M, features}), ({batch, N, M}), ({batch, M, features}), or ({batch, N, M, features}), got {B.shape}"
+    )
+
+
+def _apply_D(x: Tensor, D: Optional[Tensor], batch: int, N: int, features: int) -> Optional[Tensor]:
+    """Feedthrough shapes (the common subset of philtorch/lpv/ssm.py:480-547)."""
+    if D is None:
+        return None
+    shape = tuple(D.shape)
+    if shape in ((), (1,)):
+        return x * D
+    if len(shape) == 1:
+        if shape[0] == features:
+            return x @ D
+        if shape[0] == N and x.dim() == 2:
+            return D * x
+        if shape[0] == batch and x.dim() == 2:
+            return D.unsqueeze(1) * x
+        assert x.dim() == 2, f"Input signal x must be 2D when D is of shape {D.shape}, got {x.shape}"
+        return x.unsqueeze(-1) * D
+    if len(shape) == 2:
+        if shape == (N, features):
+            return torch.linalg.vecdot(D.conj(), x)
+        if shape == (batch, features):
+            return torch.linalg.vecdot(D.conj().unsqueeze(1), x)
+        if shape == (batch, N) and x.dim() == 2:
+            return D * x
+        if shape[0] == batch and x.dim() == 2:
+            return D.unsqueeze(1) * x.unsqueeze(-1)
+        if shape[0] == N and x.dim() == 2:
+            return D * x.unsqueeze(-1)
+        if shape[1] == features:
+            return x @ D.T
+    if len(shape) == 3:
+        if shape == (batch, N, features):
+            return torch.linalg.vecdot(D.conj(), x)
+        if shape[0] == batch and shape[2] == features:
+            return x @ D.mT
+        if shape[0] == N and shape[2] == features:
+            return torch.linalg.vecdot(D.conj(), x.unsqueeze(-2))
+        if shape[:2] == (batch, N) and x.dim() == 2:
+            return D * x.unsqueeze(-1)
+    if len(shape) == 4 and shape[0] == batch and shape[1] == N and shape[3] == features:
+        return torch.linalg.vecdot(D.conj(), x.unsqueeze(-2))
+    raise ValueError(f"Unsupported feedthrough matrix D of shape {D.shape}")
+
+
+def _apply_C(h: Tensor, C: Optional[Tensor], batch: int, N: int, M: int) -> Tensor:
+    """Output matrix shapes of philtorch/lpv/ssm.py:549-573."""
+    if C is None:
+        return h
+    shape = tuple(C.shape)
+    if shape == (M,):
+        return h @ C
+    if len(shape) == 2 and shape == (N, M):
+        return torch.linalg.vecdot(C.conj(), h)
+    if len(shape) == 2 and shape == (batch, M):
+        return torch.linalg.vecdot(C.unsqueeze(1).conj(), h)
+    if len(shape) == 2 and shape[1] == M:
+        return h @ C.T
+    if len(shape) == 3 and shape[0] == N and shape[2] == M:
+        return torch.linalg.vecdot(C.conj(), h.unsqueeze(-2))
+    if len(shape) == 3 and shape == (batch, N, M):
+        return torch.linalg.vecdot(C.conj(), h)
+    if len(shape) == 3 and shape[0] == batch and shape[2] == M:
+        return h @ C.mT
+    if len(shape) == 4 and shape[0] == batch and shape[1] == N and shape[3] == M:
+        return torch.linalg.vecdot(C.conj(), h.unsqueeze(-2))
+    raise ValueError(
+        f"Output matrix C must be of shape ({M,}), ({N, M}), ({batch, M}), ({batch, N, M}), or ({batch, N, '_', M}), "
+        f"got {C.shape}"
+    )
+
+
+def state_space(
+    A: Tensor,
+    x: Tensor,
+    B: Optional[Tensor] = None,
+    C: Optional[Tensor] = None,
+    D: Optional[Tensor] = None,
+    zi: Optional[Tensor] = None,
+    unroll_factor: Optional[int] = None,
+    out_idx: Optional[int] = None,
+):
+    """Outputs of ``h[t+1] = A[t] h[t] + B x[t]``, ``y[t] = C h[t] + D x[t]``.
+
+    Mirrors philtorch/lpv/ssm.py:337-581: when ``zi`` is given, returns
+    ``(y, zf)``.  ``unroll_factor=None`` means ``round(sqrt(N))`` (the
+    blocked PyTorch route); ``unroll_factor=1`` on a HIP device runs the
+    native scan.
+    """
+    assert x.dim() in (2, 3), f"Input signal must be 2D or 3D (batch, time, [features]), got {x.shape}"
+    assert A.dim() in (3, 4), f"State matrix A must be 3D or 4D, got {A.shape}"
+    assert A.size(-2) == A.size(-1), f"State matrix A must be square, got {A.shape}"
+    assert A.size(-3) == x.size(1), (
+        f"State matrix A must have the same time dimension as x, got A: {A.size(-3)}, x: {x.size(1)}"
+    )
+    if not (C is None or out_idx is None):
+        raise ValueError("C and out_idx cannot be used together. Use either C or out_idx.")
+    batch, N = x.size(0), x.size(1)
+    M = A.size(-1)
+    return_zf = zi is not None
+    if zi is None:
+        zi = x.new_zeros(batch, M)
+    elif zi.dim() == 1:
+        zi = zi.unsqueeze(0).expand(batch, -1)
+    if unroll_factor is None:
+        unroll_factor = round(N**0.5)
+    features = -1 if x.dim() == 2 else x.size(-1)
+    Bx = _apply_B(x, B, batch, N, M, features)
+
+    native = extension_backend_indicator(x, M) and unroll_factor in (None, 1)
+    runner = _ext_ss_recur if native else state_space_recursion
+    if return_zf or out_idx is None:
+        h = runner(A, zi, Bx, unroll_factor=unroll_factor, out_idx=None)
+        zf = h[:, -1, :] if return_zf else None
+        if out_idx is None:
+            h = torch.cat([zi.unsqueeze(1), h[:, :-1]], dim=1)
+        else:
+            h = torch.cat([zi[:, None, out_idx], h[:, :-1, out_idx]], dim=1)
+    else:
+        zf = None
+        h = runner(A, zi, Bx, unroll_factor=unroll_factor, out_idx=out_idx)
+        h = torch.cat([zi[:, None, out_idx], h[:, :-1]], dim=1)
+
+    Dx = _apply_D(x, D, batch, N, features)
+    y = _apply_C(h, C, batch, N, M)
+    if Dx is not None:
+        y = y + Dx
+    return (y, zf) if return_zf else y
