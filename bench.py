@@ -1,27 +1,33 @@
 #!/usr/bin/env python3
-"""Throughput of the first-order LPV scan, forward + backward, on one MI355X.
+"""Throughput of the linear-recurrence core, forward + backward, on one MI355X.
 
-Workload (the metric's config): a[B,T]~U(-0.99,0.99),
-x[B,T]~N(0,1), y0[B]~N(0,1), upstream grad g[B,T]~N(0,1), B=64, T=65536,
-fp32, generated on the CPU with torch.Generator().manual_seed(1) and copied to
-the GPU before timing.
+Default workload (the metric's config): the
+first-order LPV scan, a[B,T]~U(-0.99,0.99), x[B,T]~N(0,1), y0[B]~N(0,1),
+upstream grad g[B,T]~N(0,1), B=64, T=65536, fp32, generated on the CPU with
+torch.Generator().manual_seed(1) and copied to the GPU before timing.  The
+other BASELINE configs run with --config c2|c3|c4|c5|c5_f64 (same output
+format, their own metric string).
 
-One step = the hot path over that batch: the forward scan
-``torch.ops.philtorch.recur`` and the fused adjoint pass
-``torch.ops.philtorch.recur_backward`` (grad w.r.t. a, x and y0).  Before
-every step a 512 MiB buffer is read end to end so the 256 MB Infinity Cache
-holds none of the step's operands (a read sweep, not a write: a write would
-leave dirty lines whose write-back then competes with the step); the sweep
-is outside the timed events.
+One step = the hot path over one batch: the forward scan op and the fused
+adjoint op (grads w.r.t. the coefficients, the input and the initial state):
+  c1, c5  philtorch::recur + recur_backward                 (LPV scalar)
+  c2      philtorch::lti_recur + lti_recur_backward         (LTI scalar, complex64)
+  c3      philtorch::recur2 + recurN_backward               (LPV 2x2)
+  c4      8 x (philtorch::lti_recur2 + lti_recurN_backward) (LTI biquad cascade)
+Before every step a 512 MiB buffer is read end to end so the 256 MB Infinity
+Cache holds none of the step's operands (a read sweep, not a write: a write
+would leave dirty lines whose write-back then competes with the step); the
+sweep is outside the timed events.
 
 Output: one JSON line (the driver's contract) with
-  value        GSamples/s = B*T / t_step, whole job (one GPU); t_step is the
-               mean over the K timed steps of one HIP-event pair around the
-               forward and backward launches
+  value        GSamples/s = samples / t_step, whole job (one GPU); t_step is
+               the mean over the K timed steps of one HIP-event pair around
+               the step's launches
   roofline     the dominant kernel (the backward scan): algorithmic bytes per
-               launch (20 B/sample: read a, g, y; write grad_x, grad_a) over
-               its mean HIP-event duration from a second pass that puts an
-               event between the two launches, against 8 TB/s
+               launch over its mean HIP-event duration from a second pass that
+               puts events between the launches, against 8 TB/s; `traffic` is
+               the measured HBM bytes per launch from the rocprofv3 --pmc
+               summary under profiles/ when one exists for the config
   cpu_baseline the oracle (a C restatement of the reference CPU extension and
                its composite backward, OpenMP over the batch) on a bounded
                sample of the same workload, on this host's cores
@@ -35,56 +41,285 @@ import sys
 import time
 
 PEAK_HBM_GBS = 8000.0
-CONFIGS = {
-    # name: (B, T, dtype)
-    "c1": (64, 65536, "float32"),
-    "c5": (8, 1 << 24, "float32"),
-    "c5_f64": (8, 1 << 24, "float64"),
-}
+REPO = os.path.dirname(os.path.abspath(__file__))
 
 
-def make_inputs(B, T, dtype, seed=1):
-    import torch
+# ----------------------------------------------------------------------------
+# workloads
+class Workload:
+    """Inputs on the CPU (for the oracle) and on the GPU, plus the step."""
 
-    g = torch.Generator().manual_seed(seed)
-    dt = getattr(torch, dtype)
-    a = (torch.rand(B, T, generator=g, dtype=torch.float64) * 1.98 - 0.99).to(dt)
-    x = torch.randn(B, T, generator=g, dtype=torch.float64).to(dt)
-    y0 = torch.randn(B, generator=g, dtype=torch.float64).to(dt)
-    gy = torch.randn(B, T, generator=g, dtype=torch.float64).to(dt)
-    return a, x, y0, gy
+    name = ""
+    metric = ""
+    dtype_tag = "f32"
+    samples = 0
+    fwd_bytes = 0  # algorithmic bytes of one forward launch
+    bwd_bytes = 0  # algorithmic bytes of one backward launch
+    launches = 1  # forward (and backward) launches per step
+
+    def step_fwd(self):
+        raise NotImplementedError
+
+    def step_bwd(self, y):
+        raise NotImplementedError
+
+    def cpu_step(self, rows, steps, nthreads):
+        raise NotImplementedError
 
 
-def cpu_baseline(a, x, y0, gy, budget_s=10.0):
+class LpvScalar(Workload):
+    def __init__(self, name, B, T, dtype):
+        import torch
+
+        self.name, self.B, self.T = name, B, T
+        self.dtype_tag = "f32" if dtype == "float32" else "f64"
+        self.metric = (
+            "GSamples/s fwd+bwd and % of HBM peak, 1st-order LPV scan B=64 T=65536 fp32"
+            if name == "c1"
+            else f"GSamples/s fwd+bwd, 1st-order LPV scan B={B} T={T} {dtype}"
+        )
+        g = torch.Generator().manual_seed(1 if name == "c1" else 5)
+        dt = getattr(torch, dtype)
+        if name == "c1":
+            a = torch.rand(B, T, generator=g, dtype=torch.float64) * 1.98 - 0.99
+        else:  # c5: a = 0.999 tanh(z), z ~ N(0, 2)
+            a = 0.999 * torch.tanh(2.0 * torch.randn(B, T, generator=g, dtype=torch.float64))
+        x = torch.randn(B, T, generator=g, dtype=torch.float64)
+        y0 = torch.randn(B, generator=g, dtype=torch.float64)
+        gy = torch.randn(B, T, generator=g, dtype=torch.float64)
+        self.cpu = [v.to(dt) for v in (a, x, y0, gy)]
+        self.dev = [v.cuda() for v in self.cpu]
+        es = 4 if dtype == "float32" else 8
+        self.samples = B * T
+        self.fwd_bytes = 3 * es * B * T  # read a, x; write y
+        self.bwd_bytes = 5 * es * B * T  # read a, g, y; write grad_x, grad_a
+
+    def step_fwd(self):
+        import torch
+
+        a, x, y0, _ = self.dev
+        return torch.ops.philtorch.recur(a, y0, x)
+
+    def step_bwd(self, y):
+        import torch
+
+        a, _, y0, gy = self.dev
+        return torch.ops.philtorch.recur_backward(a, y0, y, gy)
+
+    def cpu_step(self, rows, steps, nthreads):
+        import oracle
+
+        a, x, y0, gy = (v.numpy()[:rows, ..., :steps] if v.dim() > 1 else v.numpy()[:rows] for v in self.cpu)
+        y = oracle.recur(a, y0, x, nthreads=nthreads)
+        oracle.recur_bwd(a, y0, y, gy, nthreads=nthreads)
+
+
+class LtiComplex(Workload):
+    """c2: per-channel complex pole p = r e^{i theta}, the diag_state_space call."""
+
+    def __init__(self):
+        import torch
+
+        C, T = 1024, 262144
+        self.name, self.B, self.T = "c2", C, T
+        self.dtype_tag = "c64"
+        self.metric = f"GSamples/s fwd+bwd, LTI diagonal scan complex64 C={C} T={T}"
+        g = torch.Generator().manual_seed(2)
+        r = torch.rand(C, generator=g, dtype=torch.float64) * 0.099 + 0.9
+        th = torch.rand(C, generator=g, dtype=torch.float64) * torch.pi
+        p = torch.polar(r, th)
+        x = torch.complex(torch.randn(C, T, generator=g), torch.randn(C, T, generator=g))
+        zi = torch.complex(torch.randn(C, generator=g), torch.randn(C, generator=g))
+        gy = torch.complex(torch.randn(C, T, generator=g), torch.randn(C, T, generator=g))
+        self.cpu = [p.to(torch.complex64), x, zi, gy]
+        self.dev = [v.cuda() for v in self.cpu]
+        self.samples = C * T
+        self.fwd_bytes = 16 * C * T  # read x, write y (8 B each)
+        self.bwd_bytes = 24 * C * T  # read g, y; write grad_x
+
+    def step_fwd(self):
+        import torch
+
+        p, x, zi, _ = self.dev
+        return torch.ops.philtorch.lti_recur(p, zi, x)
+
+    def step_bwd(self, y):
+        import torch
+
+        p, _, zi, gy = self.dev
+        return torch.ops.philtorch.lti_recur_backward(p, zi, y, gy)
+
+    def cpu_step(self, rows, steps, nthreads):
+        import oracle
+
+        p, x, zi, gy = (v.numpy() for v in self.cpu)
+        y = oracle.lti_recur(p[:rows], zi[:rows], x[:rows, :steps], nthreads=nthreads)
+        oracle.lti_recur_bwd(p[:rows], zi[:rows], y, gy[:rows, :steps], nthreads=nthreads)
+
+
+class LpvBiquad(Workload):
+    """c3: per-sample biquad denominators (TDF-II 2x2 companion), smoothed poles."""
+
+    def __init__(self):
+        import torch
+        import torch.nn.functional as F
+
+        B, T = 32, 1 << 20
+        self.name, self.B, self.T = "c3", B, T
+        self.metric = f"GSamples/s fwd+bwd, 2nd-order LPV state_space_recursion B={B} T={T} fp32"
+        g = torch.Generator().manual_seed(3)
+        r = torch.rand(B, T + 63, generator=g, dtype=torch.float64) * 0.48 + 0.5
+        th = torch.rand(B, T + 63, generator=g, dtype=torch.float64) * torch.pi
+        kern = torch.full((1, 1, 64), 1 / 64, dtype=torch.float64)
+        r = F.conv1d(r.unsqueeze(1), kern).squeeze(1)
+        th = F.conv1d(th.unsqueeze(1), kern).squeeze(1)
+        a1, a2 = -2 * r * torch.cos(th), r * r
+        A = torch.zeros(B, T, 2, 2, dtype=torch.float64)
+        A[..., 0, 0], A[..., 0, 1], A[..., 1, 0] = -a1, 1.0, -a2
+        x = torch.randn(B, T, generator=g, dtype=torch.float64)
+        xw = torch.stack([x, torch.zeros_like(x)], -1)
+        zi = torch.randn(B, 2, generator=g, dtype=torch.float64)
+        gy = torch.randn(B, T, 2, generator=g, dtype=torch.float64)
+        self.cpu = [v.float() for v in (A, xw, zi, gy)]
+        self.dev = [v.cuda() for v in self.cpu]
+        self.samples = B * T
+        self.fwd_bytes = 32 * B * T  # read A (16), x (8); write y (8)
+        self.bwd_bytes = 56 * B * T  # read A, g, y; write grad_x (8), grad_A (16)
+
+    def step_fwd(self):
+        import torch
+
+        A, x, zi, _ = self.dev
+        return torch.ops.philtorch.recur2(A, zi, x)
+
+    def step_bwd(self, y):
+        import torch
+
+        A, _, zi, gy = self.dev
+        return torch.ops.philtorch.recurN_backward(A, zi, y, gy)
+
+    def cpu_step(self, rows, steps, nthreads):
+        import oracle
+
+        A, x, zi, gy = (v.numpy() for v in self.cpu)
+        y = oracle.recurN(A[:rows, :steps], zi[:rows], x[:rows, :steps], nthreads=nthreads)
+        oracle.recurN_bwd(A[:rows, :steps], zi[:rows], y, gy[:rows, :steps], nthreads=nthreads)
+
+
+class SosCascade(Workload):
+    """c4: 8 biquad sections per batch item, each one TDF-II 2x2 LTI scan."""
+
+    def __init__(self):
+        import torch
+
+        B, S, T = 16, 8, 480000
+        self.name, self.B, self.T, self.S = "c4", B, T, S
+        self.metric = f"GSamples/s fwd+bwd, LTI lfilter cascaded SOS x{S} B={B} T={T} fp32 (op level)"
+        g = torch.Generator().manual_seed(4)
+        r = torch.rand(B, S, generator=g, dtype=torch.float64) * 0.48 + 0.5
+        th = torch.rand(B, S, generator=g, dtype=torch.float64) * torch.pi
+        a1, a2 = -2 * r * torch.cos(th), r * r
+        A = torch.zeros(B, S, 2, 2, dtype=torch.float64)
+        A[..., 0, 0], A[..., 0, 1], A[..., 1, 0] = -a1, 1.0, -a2  # companion(a)^T (TDF-II)
+        x = torch.randn(B, T, 2, generator=g, dtype=torch.float64)  # B x[t] of the first section
+        zi = torch.zeros(B, 2, dtype=torch.float64)
+        gy = torch.randn(B, T, 2, generator=g, dtype=torch.float64)
+        self.cpu = [v.float() for v in (A, x, zi, gy)]
+        self.dev = [v.cuda() for v in self.cpu]
+        self.samples = B * T  # input samples through the whole cascade
+        self.fwd_bytes = 16 * B * T  # per section: read x, write y
+        self.bwd_bytes = 24 * B * T  # per section: read g, y; write grad_x
+        self.launches = S
+
+    def step_fwd(self):
+        import torch
+
+        A, x, zi, _ = self.dev
+        ys = []
+        for s in range(self.S):
+            ys.append(torch.ops.philtorch.lti_recur2(A[:, s], zi, x if s == 0 else ys[-1]))
+        return ys
+
+    def step_bwd(self, ys):
+        import torch
+
+        A, x, zi, gy = self.dev
+        g = gy
+        for s in reversed(range(self.S)):
+            _, _, g = torch.ops.philtorch.lti_recurN_backward(A[:, s], zi, ys[s], g)
+        return g
+
+    def cpu_step(self, rows, steps, nthreads):
+        import oracle
+
+        A, x, zi, gy = (v.numpy() for v in self.cpu)
+        ys, h = [], x[:rows, :steps]
+        for s in range(self.S):
+            h = oracle.lti_recurN(A[:rows, s], zi[:rows], h, nthreads=nthreads)
+            ys.append(h)
+        g = gy[:rows, :steps]
+        for s in reversed(range(self.S)):
+            _, _, g = oracle.lti_recurN_bwd(A[:rows, s], zi[:rows], ys[s], g, nthreads=nthreads)
+
+
+def make_workload(name):
+    if name == "c1":
+        return LpvScalar("c1", 64, 65536, "float32")
+    if name == "c5":
+        return LpvScalar("c5", 8, 1 << 24, "float32")
+    if name == "c5_f64":
+        return LpvScalar("c5_f64", 8, 1 << 24, "float64")
+    if name == "c2":
+        return LtiComplex()
+    if name == "c3":
+        return LpvBiquad()
+    if name == "c4":
+        return SosCascade()
+    raise ValueError(name)
+
+
+CONFIGS = ("c1", "c2", "c3", "c4", "c5", "c5_f64")
+
+
+# ----------------------------------------------------------------------------
+def cpu_baseline(w: Workload, budget_s=10.0):
     """Time the oracle's forward + backward on a bounded sample of rows."""
-    import numpy as np
-    import oracle
+    import statistics
 
     cores = len(os.sched_getaffinity(0))
-    B, T = a.shape
-    a_n, x_n, y0_n, g_n = (t.numpy() for t in (a, x, y0, gy))
-    rows = min(B, max(cores, 1))
-    # one probe on the sample to size the timed repetitions
+    rows = min(w.B, max(cores, 1))  # the reference parallelises over rows only
+    # bound one repetition: all sampled rows over a prefix of the time axis
+    steps = int(min(w.T, 64e6 // (rows * w.launches)))
     t0 = time.perf_counter()
-    y = oracle.recur(a_n[:rows], y0_n[:rows], x_n[:rows], nthreads=cores)
-    oracle.recur_bwd(a_n[:rows], y0_n[:rows], y, g_n[:rows], nthreads=cores)
+    w.cpu_step(rows, steps, cores)
     probe = time.perf_counter() - t0
     reps = int(max(1, min(50, budget_s / max(probe, 1e-6))))
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        y = oracle.recur(a_n[:rows], y0_n[:rows], x_n[:rows], nthreads=cores)
-        oracle.recur_bwd(a_n[:rows], y0_n[:rows], y, g_n[:rows], nthreads=cores)
+        w.cpu_step(rows, steps, cores)
         times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    med = float(statistics.median(times))
     return {
-        "value": rows * T / med / 1e9,
+        "value": rows * steps / med / 1e9,
         "unit": "GSamples/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"{rows} of {B} rows x T={T}, fwd+bwd, median of {reps} reps "
+        "sample": f"{rows} of {w.B} rows x the first {steps} of T={w.T} steps, fwd+bwd, median of {reps} reps "
         f"(oracle/phs_oracle.c, OpenMP over rows, {cores} threads)",
     }
+
+
+def _measured_traffic(config):
+    """HBM bytes per launch of the dominant kernel, from the rocprofv3 --pmc
+    summary committed under profiles/ (FETCH_SIZE + WRITE_SIZE, each scaled by
+    the same counter on a plain copy of known size), or None."""
+    path = os.path.join(REPO, "profiles", f"traffic_{config}.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["bwd_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def main() -> int:
@@ -92,9 +327,12 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c1", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c1", choices=CONFIGS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-evict", action="store_true", help="keep operands cache-resident (diagnostic)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="after timing, run one plain 256 MiB device copy (reads and writes 256 MiB) so "
+                    "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE of this run can be scaled to bytes")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -107,7 +345,7 @@ def main() -> int:
 
     import torch
 
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, REPO)
     import philtorch_amd
 
     philtorch_amd.require_extension()
@@ -115,26 +353,18 @@ def main() -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
 
-    B, T, dtype = CONFIGS[args.config]
-    a_c, x_c, y0_c, g_c = make_inputs(B, T, dtype)
+    w = make_workload(args.config)
     dev = torch.device("cuda", 0)
-    a, x, y0, gy = (t.to(dev) for t in (a_c, x_c, y0_c, g_c))
     evict = None if args.no_evict else torch.ones(128 << 20, dtype=torch.float32, device=dev)
     evict_sink = torch.empty((), dtype=torch.float32, device=dev)
-    recur = torch.ops.philtorch.recur
-    recur_bwd = torch.ops.philtorch.recur_backward
 
     def evict_caches():
         if evict is not None:
             torch.sum(evict, dim=0, out=evict_sink)
 
-    def step():
-        y = recur(a, y0, x)
-        return recur_bwd(a, y0, y, gy)
-
     for _ in range(args.warmup):
         evict_caches()
-        step()
+        w.step_bwd(w.step_fwd())
     torch.cuda.synchronize()
 
     # timed region: K steps, each bracketed by one event pair (the cache
@@ -145,35 +375,34 @@ def main() -> int:
     for i in range(args.steps):
         evict_caches()
         ev[i][0].record()
-        step()
+        w.step_bwd(w.step_fwd())
         ev[i][1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms_per_step = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
 
-    # roofline pass: the same steps with an event between the two kernels,
-    # giving each kernel's mean launch duration on the stream it runs on
+    # roofline pass: the same steps with an event between forward and
+    # backward, giving each kernel's mean launch duration on its stream
     kev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     for i in range(args.steps):
         evict_caches()
         kev[i][0].record()
-        y = recur(a, y0, x)
+        y = w.step_fwd()
         kev[i][1].record()
-        recur_bwd(a, y0, y, gy)
+        w.step_bwd(y)
         kev[i][2].record()
     torch.cuda.synchronize()
-    mean_fwd = sum(e[0].elapsed_time(e[1]) for e in kev) / args.steps
-    mean_bwd = sum(e[1].elapsed_time(e[2]) for e in kev) / args.steps
-    samples = B * T
-    esize = 4 if dtype == "float32" else 8
-    bwd_bytes = 5 * esize * samples  # read a, g, y; write grad_x, grad_a
-    fwd_bytes = 3 * esize * samples  # read a, x; write y
-    dominant = ("backward", bwd_bytes, mean_bwd) if mean_bwd >= mean_fwd else ("forward", fwd_bytes, mean_fwd)
+    mean_fwd = sum(e[0].elapsed_time(e[1]) for e in kev) / args.steps / w.launches
+    mean_bwd = sum(e[1].elapsed_time(e[2]) for e in kev) / args.steps / w.launches
+    if mean_bwd >= mean_fwd:
+        dominant = ("backward", w.bwd_bytes, mean_bwd)
+    else:
+        dominant = ("forward", w.fwd_bytes, mean_fwd)
     achieved = dominant[1] / (dominant[2] * 1e-3) / 1e9
 
     result = {
-        "metric": "GSamples/s fwd+bwd and % of HBM peak, 1st-order LPV scan B=64 T=65536 fp32",
-        "value": round(samples / (ms_per_step * 1e-3) / 1e9, 3),
+        "metric": w.metric,
+        "value": round(w.samples / (ms_per_step * 1e-3) / 1e9, 3),
         "unit": "GSamples/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -182,20 +411,27 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if dtype == "float32" else "f64",
+        "dtype": w.dtype_tag,
         "data": "synthetic (seeded torch.Generator, CPU-generated, copied to HBM before timing)",
         "config": {
-            "workload": f"lpv_scan_fwd_bwd_{args.config}",
-            "B": B,
-            "T": T,
-            "op": "philtorch::recur + philtorch::recur_backward",
+            "workload": {
+                "c1": "lpv_scan_fwd_bwd_B64_T65536_f32",
+                "c2": "lti_diag_scan_fwd_bwd_C1024_T262144_c64",
+                "c3": "lpv_2x2_scan_fwd_bwd_B32_T1048576_f32",
+                "c4": "lti_sos8_cascade_fwd_bwd_B16_T480000_f32",
+                "c5": "lpv_scan_fwd_bwd_B8_T16777216_f32",
+                "c5_f64": "lpv_scan_fwd_bwd_B8_T16777216_f64",
+            }[w.name],
+            "B": w.B,
+            "T": w.T,
             "cache_evicted_between_steps": evict is not None,
         },
         "detail": {
+            "launches_per_direction": w.launches,
             "ms_fwd_kernel": round(mean_fwd, 5),
             "ms_bwd_kernel": round(mean_bwd, 5),
-            "fwd_GBs_algorithmic": round(fwd_bytes / (mean_fwd * 1e-3) / 1e9, 1),
-            "bwd_GBs_algorithmic": round(bwd_bytes / (mean_bwd * 1e-3) / 1e9, 1),
+            "fwd_GBs_algorithmic": round(w.fwd_bytes / (mean_fwd * 1e-3) / 1e9, 1),
+            "bwd_GBs_algorithmic": round(w.bwd_bytes / (mean_bwd * 1e-3) / 1e9, 1),
             "wall_s_timed_region": round(wall, 4),
         },
         "roofline": {
@@ -205,11 +441,19 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": _measured_traffic(w.name),
         },
     }
+    if args.calib_copy:
+        csrc = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        cdst = torch.empty_like(csrc)
+        torch.cuda.synchronize()
+        evict_caches()
+        cdst.copy_(csrc)
+        torch.cuda.synchronize()
+        result["detail"]["calib_copy_bytes_each_way"] = 256 << 20
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(a_c, x_c, y0_c, g_c)
+        result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)
     return 0
 
