@@ -27,30 +27,35 @@ struct Num;
 
 template <>
 struct Num<float> {
+  static constexpr bool kComplex = false;
   using acc = double;
   static __device__ __forceinline__ float zero() { return 0.f; }
   static __device__ __forceinline__ float one() { return 1.f; }
 };
 template <>
 struct Num<double> {
+  static constexpr bool kComplex = false;
   using acc = double;
   static __device__ __forceinline__ double zero() { return 0.0; }
   static __device__ __forceinline__ double one() { return 1.0; }
 };
 template <>
 struct Num<int64_t> {
+  static constexpr bool kComplex = false;
   using acc = int64_t;
   static __device__ __forceinline__ int64_t zero() { return 0; }
   static __device__ __forceinline__ int64_t one() { return 1; }
 };
 template <>
 struct Num<c64> {
+  static constexpr bool kComplex = true;
   using acc = c128;
   static __device__ __forceinline__ c64 zero() { return {0.f, 0.f}; }
   static __device__ __forceinline__ c64 one() { return {1.f, 0.f}; }
 };
 template <>
 struct Num<c128> {
+  static constexpr bool kComplex = true;
   using acc = c128;
   static __device__ __forceinline__ c128 zero() { return {0.0, 0.0}; }
   static __device__ __forceinline__ c128 one() { return {1.0, 0.0}; }
@@ -162,9 +167,12 @@ struct Scalar {
   static constexpr int kStateElems = 1;
   static constexpr int kVecsPerLane = 2;
   static constexpr int kRounds = 2;
-  static constexpr int kWavesPerBlock = 8;
-  // occupancy floor: 4 waves per SIMD keeps 4 tiles resident per CU
-  static constexpr int kMinWavesPerEU = 1;
+  // Real scans: 8-wave tiles with a floor of 4 waves per SIMD (at most 128
+  // VGPRs), so two tiles stay resident per CU.  Complex scans need more
+  // registers than that floor allows without spilling; they use 4-wave tiles
+  // at 3 waves per SIMD (three tiles per CU) instead.
+  static constexpr int kWavesPerBlock = Num<T>::kComplex ? 4 : 8;
+  static constexpr int kMinWavesPerEU = Num<T>::kComplex ? 1 : 4;
 
   static __device__ __forceinline__ coef load_c(s_coef v) { return up(v); }
   static __device__ __forceinline__ state load_s(s_state v) { return up(v); }
@@ -211,7 +219,9 @@ struct Block2 {
   static constexpr int kVecsPerLane = 1;
   static constexpr int kRounds = 2;
   static constexpr int kWavesPerBlock = 4;
-  static constexpr int kMinWavesPerEU = 1;
+  // real 2x2 scans: floor of 3 waves per SIMD (at most 168 VGPRs); complex
+  // ones would spill heavily under it
+  static constexpr int kMinWavesPerEU = Num<T>::kComplex ? 1 : 3;
 
   static __device__ __forceinline__ coef load_c(s_coef v) {
     return {up(v.m00), up(v.m01), up(v.m10), up(v.m11)};

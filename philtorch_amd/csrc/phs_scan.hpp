@@ -14,10 +14,12 @@
 //     DPP scan (row_shr 1/2/4/8, row_bcast 15/31, wave_shr 1) turns lane
 //     maps into exclusive maps; rounds are chained inside the wave; the 4
 //     wave aggregates meet in LDS;
-//   * look-back (wave 0): the tile publishes its aggregate map, then lane i
-//     polls the status words of predecessor tile q-1-i; the nearest
-//     predecessor with an inclusive state ends the search and the aggregates
-//     in between are reduced in one wave operation;
+//   * look-back (wave 0): the tile publishes its aggregate map, then the wave
+//     reads the status entries of its 64 nearest predecessors, which are
+//     contiguous, with coalesced loads (64 consecutive words per
+//     instruction), stages them in LDS, and lane i takes the entry of tile
+//     q-1-i; the nearest predecessor with an inclusive state ends the search
+//     and the aggregates in between are reduced in one wave operation;
 //   * pass 2: each lane re-runs its K steps from its now-known entry state and
 //     writes results with vector stores.
 //
@@ -69,6 +71,11 @@ struct Shape {
   static constexpr int kIncWords = sizeof(state) / 4;
   static constexpr int kAggWords = sizeof(Map<Alg>) / 4;
   static constexpr int kStride = kIncWords + kAggWords;  // 64-bit words per tile
+  // LDS staging of a 64-tile look-back window: one entry per tile, padded to
+  // an odd number of words so that lanes reading successive entries spread
+  // over the banks
+  static constexpr int kLookPitch = kStride | 1;
+  static constexpr int kLookWords = 64 * kLookPitch;
 };
 
 template <class Alg>
@@ -123,8 +130,10 @@ __device__ __forceinline__ void publish(uint64_t *dst, const X &v, unsigned tag)
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Decodes a value from status words already read; true when every word
+// carries `tag`.
 template <typename X>
-__device__ __forceinline__ bool try_read(uint64_t *src, X &v, unsigned tag) {
+__device__ __forceinline__ bool unpack(const uint64_t *src, X &v, unsigned tag) {
   constexpr int n = sizeof(X) / 4;
   union {
     X x;
@@ -133,7 +142,7 @@ __device__ __forceinline__ bool try_read(uint64_t *src, X &v, unsigned tag) {
   bool ok = true;
 #pragma unroll
   for (int i = 0; i < n; ++i) {
-    uint64_t word = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t word = src[i];
     ok = ok & (unsigned(word >> 32) == tag);
     u.w[i] = uint32_t(word);
   }
@@ -141,39 +150,75 @@ __device__ __forceinline__ bool try_read(uint64_t *src, X &v, unsigned tag) {
   return ok;
 }
 
+// Orders one wave's LDS accesses across its lanes (LDS operations of a wave
+// execute in issue order; the fences keep the compiler from moving them).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Wave-level look-back.  `row_status` points at tile 0 of this row's status;
 // `q` is this tile's position in scan order; `virt` is the state entering
-// the row (zi forward, 0 backward).  On success stores the state entering
-// tile q in `out` and returns true; returns false after `spin_limit` polls
-// found some predecessor still unpublished.
+// the row (zi forward, 0 backward); `s_look` is LDS for one window.  On
+// success stores the state entering tile q in `out` and returns true;
+// returns false after `spin_limit` polls found some predecessor still
+// unpublished.
+//
+// A window is the n = min(64, base+1) tiles [base+1-n, base]; their entries
+// are the words [(base+1-n)*kStride, (base+1)*kStride) of the row, read 64
+// consecutive words per instruction from one base address.  (Reading entry-per-lane instead costs 64 separate
+// requests per word and competes with the co-resident tiles' data loads.)
 template <class Alg>
-__device__ bool lookback(uint64_t *row_status, int64_t q, const typename Alg::state &virt, int lane,
-                         unsigned tag, unsigned spin_limit, typename Alg::state &out) {
+__device__ bool lookback(const uint64_t *row_status, int64_t q, const typename Alg::state &virt,
+                         int lane, unsigned tag, unsigned spin_limit, uint64_t *s_look,
+                         typename Alg::state &out) {
   using S = typename Alg::state;
   using M = Map<Alg>;
   using Sh = Shape<Alg>;
+  constexpr int kS = Sh::kStride, kP = Sh::kLookPitch;
+  constexpr int kBatch = kS < 8 ? kS : 8;  // words in flight per lane
   M acc = map_identity<Alg>();
   int64_t base = q - 1;
   unsigned polls = 0;
   while (true) {
-    const int64_t p = base - lane;
+    const int n = base >= 63 ? 64 : int(base + 1);  // tiles in the window
+    const uint64_t *win = row_status + (base + 1 - n) * kS + lane;
+    const int64_t p = base - lane;  // lane < n: window entry n-1-lane
     M mv = map_identity<Alg>();
     S sv = Alg::szero();
     int k;
     while (true) {
+      // all loads of a batch are issued before any LDS store: atomic loads
+      // are ordered against other memory operations, so interleaving them
+      // with the stores would serialise one round trip per word
+#pragma unroll
+      for (int i0 = 0; i0 < kS; i0 += kBatch) {
+        uint64_t words[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          words[i] = 0;
+          if (i0 + i < kS && (i0 + i) * 64 + lane < n * kS)  // word (i0+i)*64+lane of the window
+            words[i] = __hip_atomic_load(win + (i0 + i) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          const int j = (i0 + i) * 64 + lane;
+          if (i0 + i < kS) s_look[(j / kS) * kP + (j % kS)] = words[i];
+        }
+      }
+      wave_sync();
       int st;
       if (p < 0) {
         st = 2;
         sv = (p == -1) ? virt : Alg::szero();
       } else {
-        uint64_t *s = row_status + p * Sh::kStride;
-        if (try_read(s, sv, tag))
-          st = 2;
-        else if (try_read(s + Sh::kIncWords, mv, tag))
-          st = 1;
-        else
-          st = 0;
+        const uint64_t *e = s_look + (n - 1 - lane) * kP;
+        const bool inc_ok = unpack(e, sv, tag);
+        const bool agg_ok = unpack(e + Sh::kIncWords, mv, tag);
+        st = inc_ok ? 2 : (agg_ok ? 1 : 0);
       }
+      wave_sync();
       const uint64_t incm = __ballot(st == 2);
       k = incm ? __builtin_ctzll(incm) : 64;
       const uint64_t low = (k >= 64) ? ~0ull : ((1ull << k) - 1ull);
@@ -299,6 +344,7 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
   __shared__ S s_in;
   __shared__ unsigned s_id, s_tag;
   __shared__ typename Alg::acc_coef s_acc[kWaves];
+  __shared__ uint64_t s_look[Sh::kLookWords];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
@@ -386,7 +432,7 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
       yin = virt;
     } else {
       if (lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
-      if (!lookback<Alg>(row_status, qs, virt, lane, tag, a.spin_limit, yin)) {
+      if (!lookback<Alg>(row_status, qs, virt, lane, tag, a.spin_limit, s_look, yin)) {
         // fallback: fold every step of this row that precedes the tile in
         // scan order, 64*K steps per wave iteration, straight from the inputs
         M acc = map_identity<Alg>();

@@ -3,7 +3,7 @@
 Every case draws seeded inputs on the CPU, runs the op on cuda:0 and the
 oracle (a restatement of philtorch's CPU extension and backward closures) on
 the same bits, and applies the north-star bar from tests/_data.py.  Shapes
-cover single steps, tile edges (tiles are 1024..4096 steps), partial tiles,
+cover single steps, tile edges (tiles are 512..8192 steps), partial tiles,
 T not divisible by the vector width, shared coefficients and rows long enough
 for look-back windows of more than 64 predecessor tiles.
 """
@@ -15,7 +15,8 @@ from tests import _data as D
 pytestmark = pytest.mark.gpu
 
 FLOATS = [np.float32, np.float64, np.complex64, np.complex128]
-SHAPES = [(1, 1), (3, 1), (2, 5), (4, 4095), (4, 4096), (3, 4097), (2, 3 * 4096 + 17), (5, 20001)]
+SHAPES = [(1, 1), (3, 1), (2, 5), (4, 4095), (4, 4096), (3, 4097), (2, 8192), (1, 8193), (2, 3 * 4096 + 17),
+          (5, 20001)]
 
 
 def _t(x):
