@@ -167,11 +167,13 @@ struct Scalar {
   static constexpr int kStateElems = 1;
   static constexpr int kVecsPerLane = 2;
   static constexpr int kRounds = 2;
-  // Real scans: 8-wave tiles with a floor of 4 waves per SIMD (at most 128
-  // VGPRs), so two tiles stay resident per CU.  Complex scans need more
-  // registers than that floor allows without spilling; they use 4-wave tiles
-  // at 3 waves per SIMD (three tiles per CU) instead.
-  static constexpr int kWavesPerBlock = Num<T>::kComplex ? 4 : 8;
+  // Real scans: 8 data waves that also do the look-back, with a floor of 4
+  // waves per SIMD (at most 128 VGPRs): two tiles resident per CU.  Complex
+  // scans: 3 data waves plus a look-back wave, so the look-back's registers
+  // do not add to the data path's (workgroups stay whole multiples of 4
+  // waves, which the wave-slot allocation favours).
+  static constexpr bool kLookbackWave = Num<T>::kComplex;
+  static constexpr int kWavesPerBlock = Num<T>::kComplex ? 3 : 8;
   static constexpr int kMinWavesPerEU = Num<T>::kComplex ? 1 : 4;
 
   static __device__ __forceinline__ coef load_c(s_coef v) { return up(v); }
@@ -216,11 +218,13 @@ struct Block2 {
   using acc_coef = Mat2<ct>;
   static constexpr int kCoefElems = 4;
   static constexpr int kStateElems = 2;
-  static constexpr int kVecsPerLane = 1;
+  static constexpr int kVecsPerLane = 2;
   static constexpr int kRounds = 2;
-  static constexpr int kWavesPerBlock = 4;
-  // real 2x2 scans: floor of 3 waves per SIMD (at most 168 VGPRs); complex
-  // ones would spill heavily under it
+  // 3 data waves plus a look-back wave (see Scalar); real 2x2 scans keep a
+  // floor of 3 waves per SIMD (at most 168 VGPRs), complex ones would spill
+  // heavily under it
+  static constexpr bool kLookbackWave = true;
+  static constexpr int kWavesPerBlock = 3;
   static constexpr int kMinWavesPerEU = Num<T>::kComplex ? 1 : 3;
 
   static __device__ __forceinline__ coef load_c(s_coef v) {

@@ -5,21 +5,24 @@
 // adjoint backward (REV=true).
 //
 // Work decomposition (per tile of one batch row; tiles never span rows):
-//   * 256 threads = 4 waves; a wave owns a contiguous segment of 64*K*R steps;
+//   * a workgroup is W data waves, plus one look-back wave for some
+//     algebras; a data wave owns a contiguous segment of 64*K*R steps;
 //   * the segment is read in R "rounds" of 64*K contiguous steps, lane l
 //     holding steps [l*K, l*K+K) of the round, so every vector load/store of
 //     a round is one contiguous 64*K*sizeof(step) byte run (K*sizeof(state)
 //     is 16 B or more: one dwordx4 per lane and array);
 //   * pass 1: each lane folds its K steps into one affine map; a wave64
 //     DPP scan (row_shr 1/2/4/8, row_bcast 15/31, wave_shr 1) turns lane
-//     maps into exclusive maps; rounds are chained inside the wave; the 4
+//     maps into exclusive maps; rounds are chained inside the wave; the W
 //     wave aggregates meet in LDS;
-//   * look-back (wave 0): the tile publishes its aggregate map, then the wave
-//     reads the status entries of its 64 nearest predecessors, which are
-//     contiguous, with coalesced loads (64 consecutive words per
-//     instruction), stages them in LDS, and lane i takes the entry of tile
-//     q-1-i; the nearest predecessor with an inclusive state ends the search
-//     and the aggregates in between are reduced in one wave operation;
+//   * look-back (the extra wave, or data wave 0 where the algebra has no
+//     look-back wave): it combines the wave aggregates, publishes
+//     the tile's aggregate map, then reads the status entries of its 64
+//     nearest predecessors, which are contiguous, with coalesced loads (64
+//     consecutive words per instruction), stages them in LDS, and lane i
+//     takes the entry of tile q-1-i; the nearest predecessor with an
+//     inclusive state ends the search and the aggregates in between are
+//     reduced in one wave operation;
 //   * pass 2: each lane re-runs its K steps from its now-known entry state and
 //     writes results with vector stores.
 //
@@ -56,8 +59,9 @@ namespace phs {
 
 template <class Alg>
 struct Shape {
-  static constexpr int kWaves = Alg::kWavesPerBlock;
-  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kWaves = Alg::kWavesPerBlock;  // data waves
+  static constexpr bool kLookbackWave = Alg::kLookbackWave;
+  static constexpr int kThreads = 64 * (kWaves + (kLookbackWave ? 1 : 0));
   using state = typename Alg::state;
   using s_state = typename Alg::s_state;
   // steps per lane and round: kVecs 16-byte vectors of stored states (one
@@ -320,6 +324,78 @@ __device__ __forceinline__ Map<Alg> lane_map(const typename Alg::s_coef (&Ac)[TV
   return m;
 }
 
+// ------------------------------------------------------------ look-back fallback
+// State entering tile (scan position qs) of a row, folded straight from the
+// inputs: every step of the row that precedes the tile in scan order, 64*K
+// steps per wave iteration.  Taken only when predecessors did not publish
+// within the poll budget; kept out of line so that this cold loop does not
+// shape the register allocation and schedule of the hot path.
+template <class Alg, bool TV, bool REV>
+__device__ __noinline__ typename Alg::state row_prefix_fallback(const typename Alg::s_state *xrow,
+                                                               const typename Alg::s_coef *crow, int64_t T,
+                                                               bool vec, int64_t span, int64_t row_end,
+                                                               int lane, typename Alg::state virt) {
+  using SC = typename Alg::s_coef;
+  using SS = typename Alg::s_state;
+  using M = Map<Alg>;
+  constexpr int K = Shape<Alg>::K;
+  auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
+  const SC zero_sc = Alg::s_czero();
+  const SS zero_ss = Alg::s_szero();
+  const SC a_row_s = TV ? zero_sc : crow[0];
+  M acc = map_identity<Alg>();
+  for (int64_t off = 0; off < span; off += 64 * K) {
+    const int64_t c0 = REV ? row_end - off - int64_t(lane + 1) * K : off + int64_t(lane) * K;
+    SS xs[K];
+    SC cs[TV ? K : 1];
+    load_chunk<SS, K>(xrow, c0, T, vec, xs, zero_ss);
+    if constexpr (TV) load_chunk<SC, K>(crow, c0, T, vec, cs, zero_sc);
+    M m = lane_map<Alg, TV, REV, K>(cs, xs, a_row_s);
+    m = wave_scan_incl(m, lane, op);
+    acc = compose<Alg>(acc, read_lane(m, 63));
+  }
+  return apply<Alg>(acc, virt);
+}
+
+// ------------------------------------------------------------ tile look-back
+// Look-back of tile (row b, scan position qs), run by one wave between the
+// "wave aggregates ready" and "entry state ready" barriers: combine the wave
+// aggregates from s_wagg (exclusive prefixes to s_wpre), publish the tile's
+// aggregate, find the state entering the tile (s_in), publish the inclusive
+// state.
+template <class Alg, bool TV, bool REV>
+__device__ __forceinline__ void tile_lookback(const ScanArgs<Alg> &a, int64_t qs, int64_t b, unsigned tag,
+                                              int lane, const Map<Alg> *s_wagg, Map<Alg> *s_wpre,
+                                              typename Alg::state *s_in, uint64_t *s_look) {
+  using S = typename Alg::state;
+  using SC = typename Alg::s_coef;
+  using SS = typename Alg::s_state;
+  using M = Map<Alg>;
+  using Sh = Shape<Alg>;
+  constexpr int K = Sh::K, kWaves = Sh::kWaves;
+  auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
+  M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
+  v = wave_scan_incl(v, lane, op);
+  const M wex = wave_shift_up(v, lane, map_identity<Alg>());
+  if (lane < kWaves) s_wpre[lane] = wex;
+  const M tagg = read_lane(v, kWaves - 1);
+  uint64_t *row_status = a.status + b * a.tiles_per_row * Sh::kStride;
+  const S virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
+  S yin;
+  if (qs == 0) {
+    yin = virt;
+  } else {
+    if (lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
+    if (!lookback<Alg>(row_status, qs, virt, lane, tag, a.spin_limit, s_look, yin))
+      yin = row_prefix_fallback<Alg, TV, REV>(reinterpret_cast<const SS *>(a.x) + b * a.T_len,
+                                              reinterpret_cast<const SC *>(a.coef) + b * a.coef_row_stride,
+                                              a.T_len, a.vec_ok != 0, qs * Sh::kTile,
+                                              a.tiles_per_row * Sh::kTile, lane, virt);
+  }
+  if (qs + 1 < a.tiles_per_row && lane == 0) publish(row_status + qs * Sh::kStride, apply<Alg>(tagg, yin), tag);
+  if (lane == 0) *s_in = yin;
+}
+
 // ------------------------------------------------------------ the kernel
 // TV  : the coefficient varies along time (LPV); otherwise one per row (LTI).
 // REV : backward adjoint scan, nu[t] = A[t]^H (g[t] + nu[t+1]), run from the
@@ -329,10 +405,19 @@ __device__ __forceinline__ Map<Alg> lane_map(const typename Alg::s_coef (&Ac)[TV
 // Scan order is always ascending in (wave, round, lane); REV mirrors the
 // placement of waves, rounds and lanes in memory instead, so one DPP scan
 // serves both directions.  Inside a lane's K steps REV walks downwards.
+//
+// Where the algebra asks for it (Alg::kLookbackWave), the look-back runs in
+// a wave of its own that holds no tile data.  Run by data wave 0 instead, its
+// staging words and folded maps are live on top of that wave's loaded chunk
+// and scan maps; split into roles, the kernel needs the larger of the two
+// register sets, not their sum.  That pays where the data path is
+// register-heavy (2x2 and complex scans); for real scalar scans a ninth wave
+// per tile costs more than it saves.  Either way the waves meet at the same
+// barriers: claim, wave aggregates ready, entry state ready (and, backward
+// for LTI, the gradient reduction).
 template <class Alg, bool TV, bool REV>
 __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void scan_kernel(ScanArgs<Alg> a) {
-  using C = typename Alg::coef;      // compute types
-  using S = typename Alg::state;
+  using S = typename Alg::state;     // compute type
   using SC = typename Alg::s_coef;   // storage types
   using SS = typename Alg::s_state;
   using M = Map<Alg>;
@@ -346,7 +431,10 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
   __shared__ typename Alg::acc_coef s_acc[kWaves];
   __shared__ uint64_t s_look[Sh::kLookWords];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // wave index as a scalar: the role branches below are scalar branches, so a
+  // wave only ever executes the barriers of its own role
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
   __syncthreads();
   if (s_id >= a.tiles) return;  // padding of the last stripe round
@@ -356,6 +444,51 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
   const int64_t b = id - qs * a.B;
   const int64_t qf = REV ? a.tiles_per_row - 1 - qs : qs;  // position along time
   const int64_t T = a.T_len;
+  const bool vec = a.vec_ok != 0;
+
+  const SS *xrow = reinterpret_cast<const SS *>(a.x) + b * T;
+  const SC *crow = reinterpret_cast<const SC *>(a.coef) + b * a.coef_row_stride;
+  // Steps past the end of the row load a zero coefficient and a zero input.
+  // Forward they follow every valid step, so they only touch the aggregate of
+  // the row's last tile, which nobody reads.  Backward they come first, where
+  // the carry is zero anyway, and keep it zero.
+  const SC zero_sc = Alg::s_czero();
+  const SS zero_ss = Alg::s_szero();
+  const SC a_row_s = TV ? zero_sc : crow[0];
+  auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
+  // only LTI coefficients reduce their gradient inside the kernel (backward)
+  constexpr bool kAcc = REV && !TV;
+  const bool want_acc = kAcc && a.partials != nullptr;
+
+  if (Sh::kLookbackWave && w == kWaves) {
+    // ================= look-back wave
+    __syncthreads();  // wave aggregates are in s_wagg
+    // tile_lookback written out in place: this copy measured faster for the
+    // complex and 2x2 backward scans than the inlined call
+    M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
+    v = wave_scan_incl(v, lane, op);
+    const M wex = wave_shift_up(v, lane, map_identity<Alg>());
+    if (lane < kWaves) s_wpre[lane] = wex;
+    const M tagg = read_lane(v, kWaves - 1);
+    uint64_t *row_status = a.status + b * a.tiles_per_row * Sh::kStride;
+    const S virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
+    S yin;
+    if (qs == 0) {
+      yin = virt;
+    } else {
+      if (lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
+      if (!lookback<Alg>(row_status, qs, virt, lane, tag, a.spin_limit, s_look, yin))
+        yin = row_prefix_fallback<Alg, TV, REV>(xrow, crow, T, vec, qs * Sh::kTile, a.tiles_per_row * Sh::kTile,
+                                                lane, virt);
+    }
+    if (qs + 1 < a.tiles_per_row && lane == 0) publish(row_status + qs * Sh::kStride, apply<Alg>(tagg, yin), tag);
+    if (lane == 0) s_in = yin;
+    __syncthreads();  // entry state published to the data waves
+    if (want_acc) __syncthreads();  // the data waves' gradient reduction
+    return;
+  }
+
+  // ================= data waves
   // memory placement of this wave's segment and of this lane's chunk
   const int pw = REV ? kWaves - 1 - w : w;
   const int pl = REV ? 63 - lane : lane;
@@ -364,25 +497,13 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
     const int pr = REV ? R - 1 - r : r;
     return seg0 + int64_t(pr) * 64 * K + int64_t(pl) * K;
   };
-  const bool vec = a.vec_ok != 0;
-
-  const SS *xrow = reinterpret_cast<const SS *>(a.x) + b * T;
-  const SC *crow = reinterpret_cast<const SC *>(a.coef) + b * a.coef_row_stride;
   const SS *yrow_in = reinterpret_cast<const SS *>(a.y) + b * T;
-  const S zero_s = Alg::szero();
-  // Steps past the end of the row load a zero coefficient and a zero input.
-  // Forward they follow every valid step, so they only touch the aggregate of
-  // the row's last tile, which nobody reads.  Backward they come first, where
-  // the carry is zero anyway, and keep it zero.
-  const SC zero_sc = Alg::s_czero();
-  const SS zero_ss = Alg::s_szero();
 
   // ---- loads (all rounds issued up front)
   SS X[R][K];
   SC A[TV ? R : 1][TV ? K : 1];
   SS Y[REV ? R : 1][REV ? K : 1];
   SS Ylow[REV ? R : 1];  // backward: y[t0-1] below the chunk of lane 63
-  const SC a_row_s = TV ? zero_sc : crow[0];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t t0 = chunk0(r);
@@ -399,7 +520,6 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
       }
     }
   }
-  auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
 
   // ---- pass 1: lane maps, wave scans, round chaining
   M Ex[R];
@@ -413,49 +533,10 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
     Ex[r] = compose<Alg>(carry, ex);
     carry = compose<Alg>(carry, tot);
   }
-
-  // ---- block: wave aggregates in scan order, combined by wave 0
   if (lane == 0) s_wagg[w] = carry;
-  __syncthreads();
-
-  // ---- look-back (wave 0)
-  if (w == 0) {
-    M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
-    v = wave_scan_incl(v, lane, op);
-    const M wex = wave_shift_up(v, lane, map_identity<Alg>());
-    if (lane < kWaves) s_wpre[lane] = wex;
-    const M tagg = read_lane(v, kWaves - 1);
-    uint64_t *row_status = a.status + b * a.tiles_per_row * Sh::kStride;
-    const S virt = REV ? zero_s : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
-    S yin;
-    if (qs == 0) {
-      yin = virt;
-    } else {
-      if (lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
-      if (!lookback<Alg>(row_status, qs, virt, lane, tag, a.spin_limit, s_look, yin)) {
-        // fallback: fold every step of this row that precedes the tile in
-        // scan order, 64*K steps per wave iteration, straight from the inputs
-        M acc = map_identity<Alg>();
-        const int64_t span = qs * Sh::kTile;
-        const int64_t row_end = a.tiles_per_row * Sh::kTile;
-        for (int64_t off = 0; off < span; off += 64 * K) {
-          const int64_t c0 = REV ? row_end - off - int64_t(lane + 1) * K : off + int64_t(lane) * K;
-          SS xs[K];
-          SC cs[TV ? K : 1];
-          load_chunk<SS, K>(xrow, c0, T, vec, xs, zero_ss);
-          if constexpr (TV) load_chunk<SC, K>(crow, c0, T, vec, cs, zero_sc);
-          M m = lane_map<Alg, TV, REV, K>(cs, xs, a_row_s);
-          m = wave_scan_incl(m, lane, op);
-          acc = compose<Alg>(acc, read_lane(m, 63));
-        }
-        yin = apply<Alg>(acc, virt);
-      }
-    }
-    if (qs + 1 < a.tiles_per_row && lane == 0)
-      publish(row_status + qs * Sh::kStride, apply<Alg>(tagg, yin), tag);
-    if (lane == 0) s_in = yin;
-  }
-  __syncthreads();
+  __syncthreads();  // wave aggregates are in s_wagg
+  if (!Sh::kLookbackWave && w == 0) tile_lookback<Alg, TV, REV>(a, qs, b, tag, lane, s_wagg, s_wpre, &s_in, s_look);
+  __syncthreads();  // entry state is in s_in
   const S hw = apply<Alg>(s_wpre[w], s_in);
 
   // ---- pass 2
@@ -475,10 +556,7 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
   } else {
     SS *gxrow = a.out ? reinterpret_cast<SS *>(a.out) + b * T : nullptr;
     SC *gcrow = a.gcoef ? reinterpret_cast<SC *>(a.gcoef) + b * T : nullptr;
-    // only LTI coefficients reduce their gradient inside the kernel
-    constexpr bool kAcc = !TV;
     typename Alg::acc_coef acc = Alg::acc_zero();
-    const bool want_acc = kAcc && a.partials != nullptr;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t t0 = chunk0(r);
@@ -508,7 +586,7 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
         if (gcrow) store_chunk<SC, K>(gcrow, t0, T, vec, GC);
       }
     }
-    if (kAcc && want_acc) {
+    if (want_acc) {
       // deterministic block reduction of the per-tile coefficient gradient
 #pragma unroll
       for (int d = 32; d >= 1; d >>= 1) acc = Alg::acc_sum(acc, shfl_from(acc, lane ^ d));
