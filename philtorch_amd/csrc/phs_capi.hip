@@ -1,13 +1,19 @@
 // C ABI entry points of libphilscan (declared in include/philscan.h).
 // Host side: argument checks, workspace carving, and the launch of
 //   scan_kernel [-> reduce kernel]
-// on the caller's stream.  No allocation, no synchronisation, no globals.
+// on the caller's stream.  No allocation and no synchronisation; the only
+// global state is the spin-limit testing hook and a per-device cache of how
+// many workgroups of each kernel are resident at once.
 // Workspace layout: [0, 2048) header (16 striped {epoch, claim count} words),
 // then the tile status words, then (backward only) per-tile partial sums or
 // per-step scratch.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "../../include/philscan.h"
 #include "phs_scan.hpp"
@@ -50,6 +56,31 @@ Layout make_layout(int64_t B, int64_t T, bool TV, bool shared, bool backward) {
 }
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Workgroups of `kernel` resident at once on the current device (occupancy
+// per CU times CUs), cached per (kernel, device); 0 if the query fails.
+int64_t resident_groups(const void *kernel, int threads) {
+  static std::mutex mu;
+  static std::map<std::pair<const void *, int>, int64_t> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(kernel, dev);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  const int64_t n = int64_t(std::max(per_cu, 0)) * std::max(cus, 0);
+  cache[key] = n;
+  return n;
+}
+
+template <class Alg, bool TV, bool REV>
+void launch_scan(const ScanArgs<Alg> &a, unsigned grid, hipStream_t stream) {
+  hipLaunchKernelGGL((scan_kernel<Alg, TV, REV>), dim3(grid), dim3(Shape<Alg>::kThreads), 0, stream, a);
+}
 
 template <class Alg>
 int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void *coef,
@@ -95,17 +126,32 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
              aligned16(out) && aligned16(a.gcoef) && (!TV || aligned16(coef));
   a.vec_ok = vec ? 1 : 0;
 
+  const void *kernel = TV ? (backward ? reinterpret_cast<const void *>(scan_kernel<Alg, true, true>)
+                                       : reinterpret_cast<const void *>(scan_kernel<Alg, true, false>))
+                          : (backward ? reinterpret_cast<const void *>(scan_kernel<Alg, false, true>)
+                                      : reinterpret_cast<const void *>(scan_kernel<Alg, false, false>));
+  // Tiles are claimed q-major, so a tile's predecessor in its row was claimed
+  // B claims earlier, i.e. B/resident tile lifetimes earlier.  From half a
+  // lifetime on it has published at least its aggregate, and the look-back
+  // wave can poll for it while the data waves are still loading; with
+  // smaller B those early polls mostly fail and only add status traffic.
+  a.early_polls = 0;
+  if (Sh::kLookbackWave) {
+    const int64_t resident = resident_groups(kernel, Sh::kThreads);
+    if (resident > 0 && 2 * B >= resident) a.early_polls = a.spin_limit;
+  }
+
   const unsigned grid = a.per_stripe * kStripes;
   if (TV) {
     if (backward)
-      hipLaunchKernelGGL((scan_kernel<Alg, true, true>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
+      launch_scan<Alg, true, true>(a, grid, stream);
     else
-      hipLaunchKernelGGL((scan_kernel<Alg, true, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
+      launch_scan<Alg, true, false>(a, grid, stream);
   } else {
     if (backward)
-      hipLaunchKernelGGL((scan_kernel<Alg, false, true>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
+      launch_scan<Alg, false, true>(a, grid, stream);
     else
-      hipLaunchKernelGGL((scan_kernel<Alg, false, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
+      launch_scan<Alg, false, false>(a, grid, stream);
   }
   if (backward && gcoef) {
     if (TV && shared) {

@@ -96,6 +96,10 @@ struct ScanArgs {
   T *gzi;                   // backward: grad of zi (nullable)
   int64_t B, T_len, tiles_per_row;
   unsigned long long *claims;  // kStripes claim words, 128 bytes apart (workspace offset 0)
+  // look-back wave: polls allowed before the tile's own aggregate is known
+  // (0: wait for it; the host enables early polling when a row's
+  // predecessor tile is claimed a whole resident grid earlier)
+  unsigned early_polls;
   unsigned tiles;              // B * tiles_per_row
   unsigned per_stripe;         // claims per stripe (grid = per_stripe * kStripes)
   unsigned spin_limit;         // look-back polls before the self-compute fallback
@@ -163,75 +167,86 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 // Wave-level look-back.  `row_status` points at tile 0 of this row's status;
-// `q` is this tile's position in scan order; `virt` is the state entering
-// the row (zi forward, 0 backward); `s_look` is LDS for one window.  On
-// success stores the state entering tile q in `out` and returns true;
-// returns false after `spin_limit` polls found some predecessor still
-// unpublished.
+// `virt` is the state entering the row (zi forward, 0 backward); `s_look` is
+// LDS for one window.
 //
 // A window is the n = min(64, base+1) tiles [base+1-n, base]; their entries
 // are the words [(base+1-n)*kStride, (base+1)*kStride) of the row, read 64
-// consecutive words per instruction from one base address.  (Reading entry-per-lane instead costs 64 separate
-// requests per word and competes with the co-resident tiles' data loads.)
+// consecutive words per instruction from one base address.  (Reading
+// entry-per-lane instead costs 64 separate requests per word and competes
+// with the co-resident tiles' data loads.)
+
+// Progress of one tile's look-back, kept across polls.
 template <class Alg>
-__device__ bool lookback(const uint64_t *row_status, int64_t q, const typename Alg::state &virt,
-                         int lane, unsigned tag, unsigned spin_limit, uint64_t *s_look,
-                         typename Alg::state &out) {
+struct Lookback {
+  Map<Alg> acc;    // fold of the windows already passed
+  int64_t base;    // newest tile of the current window
+  unsigned polls;  // polls that found some predecessor still unpublished
+};
+
+template <class Alg>
+__device__ __forceinline__ Lookback<Alg> lookback_start(int64_t q) {
+  return {map_identity<Alg>(), q - 1, 0u};
+}
+
+// One poll.  When every tile between the nearest inclusive predecessor and
+// this tile has published its aggregate, stores the state entering the tile
+// in `out` and returns true (a window of aggregates only is folded into
+// lb.acc and the next window read straight away).  Otherwise counts the poll
+// and returns false.
+template <class Alg>
+__device__ bool lookback_poll(const uint64_t *row_status, const typename Alg::state &virt, int lane,
+                              unsigned tag, uint64_t *s_look, Lookback<Alg> &lb, typename Alg::state &out) {
   using S = typename Alg::state;
   using M = Map<Alg>;
   using Sh = Shape<Alg>;
   constexpr int kS = Sh::kStride, kP = Sh::kLookPitch;
   constexpr int kBatch = kS < 8 ? kS : 8;  // words in flight per lane
-  M acc = map_identity<Alg>();
-  int64_t base = q - 1;
-  unsigned polls = 0;
   while (true) {
+    const int64_t base = lb.base;
     const int n = base >= 63 ? 64 : int(base + 1);  // tiles in the window
     const uint64_t *win = row_status + (base + 1 - n) * kS + lane;
     const int64_t p = base - lane;  // lane < n: window entry n-1-lane
     M mv = map_identity<Alg>();
     S sv = Alg::szero();
-    int k;
-    while (true) {
-      // all loads of a batch are issued before any LDS store: atomic loads
-      // are ordered against other memory operations, so interleaving them
-      // with the stores would serialise one round trip per word
+    // all loads of a batch are issued before any LDS store: atomic loads are
+    // ordered against other memory operations, so interleaving them with the
+    // stores would serialise one round trip per word
 #pragma unroll
-      for (int i0 = 0; i0 < kS; i0 += kBatch) {
-        uint64_t words[kBatch];
+    for (int i0 = 0; i0 < kS; i0 += kBatch) {
+      uint64_t words[kBatch];
 #pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-          words[i] = 0;
-          if (i0 + i < kS && (i0 + i) * 64 + lane < n * kS)  // word (i0+i)*64+lane of the window
-            words[i] = __hip_atomic_load(win + (i0 + i) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-          const int j = (i0 + i) * 64 + lane;
-          if (i0 + i < kS) s_look[(j / kS) * kP + (j % kS)] = words[i];
-        }
+      for (int i = 0; i < kBatch; ++i) {
+        words[i] = 0;
+        if (i0 + i < kS && (i0 + i) * 64 + lane < n * kS)  // word (i0+i)*64+lane of the window
+          words[i] = __hip_atomic_load(win + (i0 + i) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      wave_sync();
-      int st;
-      if (p < 0) {
-        st = 2;
-        sv = (p == -1) ? virt : Alg::szero();
-      } else {
-        const uint64_t *e = s_look + (n - 1 - lane) * kP;
-        const bool inc_ok = unpack(e, sv, tag);
-        const bool agg_ok = unpack(e + Sh::kIncWords, mv, tag);
-        st = inc_ok ? 2 : (agg_ok ? 1 : 0);
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int j = (i0 + i) * 64 + lane;
+        if (i0 + i < kS) s_look[(j / kS) * kP + (j % kS)] = words[i];
       }
-      wave_sync();
-      const uint64_t incm = __ballot(st == 2);
-      k = incm ? __builtin_ctzll(incm) : 64;
-      const uint64_t low = (k >= 64) ? ~0ull : ((1ull << k) - 1ull);
-      const uint64_t waiting = __ballot(st == 0) & low;
-      if (waiting == 0) break;
-      if (++polls >= spin_limit) return false;
-      __builtin_amdgcn_s_sleep(1);
     }
-    // lanes [0, k) hold aggregates of tiles q-1-lane (newest at lane 0);
+    wave_sync();
+    int st;
+    if (p < 0) {
+      st = 2;
+      sv = (p == -1) ? virt : Alg::szero();
+    } else {
+      const uint64_t *e = s_look + (n - 1 - lane) * kP;
+      const bool inc_ok = unpack(e, sv, tag);
+      const bool agg_ok = unpack(e + Sh::kIncWords, mv, tag);
+      st = inc_ok ? 2 : (agg_ok ? 1 : 0);
+    }
+    wave_sync();
+    const uint64_t incm = __ballot(st == 2);
+    const int k = incm ? __builtin_ctzll(incm) : 64;
+    const uint64_t low = (k >= 64) ? ~0ull : ((1ull << k) - 1ull);
+    if (__ballot(st == 0) & low) {
+      ++lb.polls;
+      return false;
+    }
+    // lanes [0, k) hold aggregates of tiles base-lane (newest at lane 0);
     // fold them oldest-first into lane 0.
     M m = (lane < k) ? mv : map_identity<Alg>();
 #pragma unroll
@@ -242,12 +257,24 @@ __device__ bool lookback(const uint64_t *row_status, int64_t q, const typename A
     const M F = read_lane(m, 0);
     if (k < 64) {
       const S yk = read_lane(sv, k);
-      out = apply<Alg>(compose<Alg>(F, acc), yk);
+      out = apply<Alg>(compose<Alg>(F, lb.acc), yk);
       return true;
     }
-    acc = compose<Alg>(F, acc);
-    base -= 64;
+    lb.acc = compose<Alg>(F, lb.acc);
+    lb.base = base - 64;
   }
+}
+
+// Blocking look-back: polls until the entry state is known (true), or
+// returns false once lb.polls reaches spin_limit.
+template <class Alg>
+__device__ bool lookback(const uint64_t *row_status, const typename Alg::state &virt, int lane, unsigned tag,
+                         unsigned spin_limit, uint64_t *s_look, Lookback<Alg> &lb, typename Alg::state &out) {
+  while (!lookback_poll<Alg>(row_status, virt, lane, tag, s_look, lb, out)) {
+    if (lb.polls >= spin_limit) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return true;
 }
 
 // ------------------------------------------------------------ chunk I/O
@@ -386,7 +413,8 @@ __device__ __forceinline__ void tile_lookback(const ScanArgs<Alg> &a, int64_t qs
     yin = virt;
   } else {
     if (lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
-    if (!lookback<Alg>(row_status, qs, virt, lane, tag, a.spin_limit, s_look, yin))
+    Lookback<Alg> lb = lookback_start<Alg>(qs);
+    if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
       yin = row_prefix_fallback<Alg, TV, REV>(reinterpret_cast<const SS *>(a.x) + b * a.T_len,
                                               reinterpret_cast<const SC *>(a.coef) + b * a.coef_row_stride,
                                               a.T_len, a.vec_ok != 0, qs * Sh::kTile,
@@ -430,12 +458,16 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
   __shared__ unsigned s_id, s_tag;
   __shared__ typename Alg::acc_coef s_acc[kWaves];
   __shared__ uint64_t s_look[Sh::kLookWords];
+  __shared__ unsigned s_ready;  // data waves whose aggregate is in s_wagg
 
   const int tid = threadIdx.x, lane = tid & 63;
   // wave index as a scalar: the role branches below are scalar branches, so a
   // wave only ever executes the barriers of its own role
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
+  if (tid == 0) {
+    claim_tile(a.claims, a.per_stripe, s_id, s_tag);
+    s_ready = 0;
+  }
   __syncthreads();
   if (s_id >= a.tiles) return;  // padding of the last stripe round
   const int64_t id = s_id;
@@ -462,22 +494,29 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
 
   if (Sh::kLookbackWave && w == kWaves) {
     // ================= look-back wave
+    uint64_t *row_status = a.status + b * a.tiles_per_row * Sh::kStride;
+    const S virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
+    Lookback<Alg> lb = lookback_start<Alg>(qs);
+    S yin = virt;
+    bool known = qs == 0;
+    // The entry state does not depend on this tile: where the predecessor is
+    // expected to have finished (a.early_polls > 0), poll while the data
+    // waves load and scan, until it is known or their aggregates are all in.
+    while (!known && lb.polls < a.early_polls) {
+      known = lookback_poll<Alg>(row_status, virt, lane, tag, s_look, lb, yin);
+      if (known || __hip_atomic_load(&s_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == unsigned(kWaves))
+        break;
+      __builtin_amdgcn_s_sleep(1);
+    }
     __syncthreads();  // wave aggregates are in s_wagg
-    // tile_lookback written out in place: this copy measured faster for the
-    // complex and 2x2 backward scans than the inlined call
     M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
     v = wave_scan_incl(v, lane, op);
     const M wex = wave_shift_up(v, lane, map_identity<Alg>());
     if (lane < kWaves) s_wpre[lane] = wex;
     const M tagg = read_lane(v, kWaves - 1);
-    uint64_t *row_status = a.status + b * a.tiles_per_row * Sh::kStride;
-    const S virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
-    S yin;
-    if (qs == 0) {
-      yin = virt;
-    } else {
+    if (!known) {
       if (lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
-      if (!lookback<Alg>(row_status, qs, virt, lane, tag, a.spin_limit, s_look, yin))
+      if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
         yin = row_prefix_fallback<Alg, TV, REV>(xrow, crow, T, vec, qs * Sh::kTile, a.tiles_per_row * Sh::kTile,
                                                 lane, virt);
     }
@@ -533,7 +572,10 @@ __global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void sca
     Ex[r] = compose<Alg>(carry, ex);
     carry = compose<Alg>(carry, tot);
   }
-  if (lane == 0) s_wagg[w] = carry;
+  if (lane == 0) {
+    s_wagg[w] = carry;
+    if (Sh::kLookbackWave) __hip_atomic_fetch_add(&s_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
   __syncthreads();  // wave aggregates are in s_wagg
   if (!Sh::kLookbackWave && w == 0) tile_lookback<Alg, TV, REV>(a, qs, b, tag, lane, s_wagg, s_wpre, &s_in, s_look);
   __syncthreads();  // entry state is in s_in

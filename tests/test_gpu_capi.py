@@ -139,6 +139,37 @@ def test_capi_lookback_fallback(api, op, B, T, dtype, shared):
     _check(got, _oracle(op, A, zi, x, gy))
 
 
+# Thousands of rows: a row's predecessor tile is claimed more than half a
+# resident grid earlier, so the look-back wave of the complex and 2x2 scans
+# polls for it while the tile is still loading (early look-back).
+MANY_ROWS = [
+    ("lti_recur", 2048, 6000, np.complex64, False),
+    ("recur", 2048, 5000, np.complex128, False),
+    ("recur2", 1536, 4000, np.float32, False),
+    ("lti_recur2", 2048, 5000, np.float64, True),
+]
+
+
+@pytest.mark.parametrize("op,B,T,dtype,shared", MANY_ROWS)
+def test_capi_many_rows_early_lookback(api, op, B, T, dtype, shared):
+    A, zi, x, gy = _case(op, B, T, dtype, shared, D.seed_of("rows", op, B, T, np.dtype(dtype).str, shared))
+    _check(_run(api, op, A, zi=zi, x=x, gy=gy, shared=shared), _oracle(op, A, zi, x, gy))
+
+
+@pytest.mark.parametrize("op,B,T,dtype,shared", MANY_ROWS[::2])
+def test_capi_many_rows_fallback(api, op, B, T, dtype, shared):
+    """Early look-back with a poll budget of 1: tiles fall back to folding
+    their row prefix from the inputs."""
+    lib = api[0]
+    A, zi, x, gy = _case(op, B, T, dtype, shared, D.seed_of("rows-fb", op, B, T, np.dtype(dtype).str))
+    lib.phs_debug_set_spin_limit(1)
+    try:
+        got = _run(api, op, A, zi=zi, x=x, gy=gy, shared=shared)
+    finally:
+        lib.phs_debug_set_spin_limit(0)
+    _check(got, _oracle(op, A, zi, x, gy))
+
+
 def test_capi_workspace_reuse_many_calls(api):
     """One workspace, many calls of changing shapes: the per-call tags must
     keep every call independent of the status words left by earlier ones."""
