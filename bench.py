@@ -226,6 +226,9 @@ class SosCascade(Workload):
         gy = torch.randn(B, T, 2, generator=g, dtype=torch.float64)
         self.cpu = [v.float() for v in (A, x, zi, gy)]
         self.dev = [v.cuda() for v in self.cpu]
+        # each section's coefficients as a tensor of its own, as a cascade
+        # holds them (a strided A[:, s] view would add a copy per call)
+        self.A_sec = [self.dev[0][:, s].contiguous() for s in range(S)]
         self.samples = B * T  # input samples through the whole cascade
         self.fwd_bytes = 16 * B * T  # per section: read x, write y
         self.bwd_bytes = 24 * B * T  # per section: read g, y; write grad_x
@@ -234,19 +237,19 @@ class SosCascade(Workload):
     def step_fwd(self):
         import torch
 
-        A, x, zi, _ = self.dev
+        _, x, zi, _ = self.dev
         ys = []
         for s in range(self.S):
-            ys.append(torch.ops.philtorch.lti_recur2(A[:, s], zi, x if s == 0 else ys[-1]))
+            ys.append(torch.ops.philtorch.lti_recur2(self.A_sec[s], zi, x if s == 0 else ys[-1]))
         return ys
 
     def step_bwd(self, ys):
         import torch
 
-        A, x, zi, gy = self.dev
+        _, _, zi, gy = self.dev
         g = gy
         for s in reversed(range(self.S)):
-            _, _, g = torch.ops.philtorch.lti_recurN_backward(A[:, s], zi, ys[s], g)
+            _, _, g = torch.ops.philtorch.lti_recurN_backward(self.A_sec[s], zi, ys[s], g)
         return g
 
     def cpu_step(self, rows, steps, nthreads):
