@@ -46,7 +46,14 @@ extern "C" {
 
 enum phs_dtype { PHS_F32 = 0, PHS_F64 = 1, PHS_C64 = 2, PHS_C128 = 3, PHS_I64 = 4 };
 
-enum phs_op { PHS_OP_RECUR = 0, PHS_OP_LTI_RECUR = 1, PHS_OP_RECUR2 = 2, PHS_OP_LTI_RECUR2 = 3 };
+enum phs_op {
+  PHS_OP_RECUR = 0,
+  PHS_OP_LTI_RECUR = 1,
+  PHS_OP_RECUR2 = 2,
+  PHS_OP_LTI_RECUR2 = 3,
+  PHS_OP_RECURN = 4,    /* order-M ops, phs_workspace_size_n only */
+  PHS_OP_LTI_RECURN = 5
+};
 
 enum phs_status {
   PHS_OK = 0,
@@ -59,6 +66,12 @@ enum phs_status {
 /* Bytes of workspace that one call of `op` needs (backward != 0 for the
  * `_bwd` entry point).  `coef_shared` is the same flag the call receives. */
 size_t phs_workspace_size(int op, int dtype, int64_t B, int64_t T, int coef_shared, int backward);
+
+/* phs_workspace_size for an op of state order M.  PHS_OP_RECURN and
+ * PHS_OP_LTI_RECURN take M = 1..4; the fixed-order ops accept only their own
+ * order (1 for PHS_OP_RECUR / PHS_OP_LTI_RECUR, 2 for the *2 ops).  Returns 0
+ * for an unsupported combination. */
+size_t phs_workspace_size_n(int op, int dtype, int M, int64_t B, int64_t T, int coef_shared, int backward);
 
 /* Human-readable text of a phs_status code (static storage). */
 const char *phs_error_string(int status);
@@ -124,7 +137,7 @@ int phs_recur2_bwd(int dtype, int64_t B, int64_t T, const void *A, int coef_shar
  * zi: [B,2]; x, y: [B,T,2].
  * Replaces lti_mat_recur_second_order_cuda_impl,
  * philtorch/csrc/lti_recur2.cu:66-113 (registered at :115-118; CPU twin
- * host_lti_recurN.cpp:147-192). */
+ * host_lti_recurN.cpp:63-108). */
 int phs_lti_recur2_fwd(int dtype, int64_t B, int64_t T, const void *A, int coef_shared,
                        const void *zi, const void *x, void *y, void *workspace,
                        size_t workspace_bytes, void *stream);
@@ -136,6 +149,37 @@ int phs_lti_recur2_bwd(int dtype, int64_t B, int64_t T, const void *A, int coef_
                        const void *zi, const void *y, const void *grad_y, void *grad_x,
                        void *grad_A, void *grad_zi, void *workspace, size_t workspace_bytes,
                        void *stream);
+
+/* LPV MxM scan of state order M = 1..4.  A: [B,T,M,M] (coef_shared=0) or
+ * [T,M,M] (coef_shared=1), row-major matrices; zi: [B,M]; x, y: [B,T,M].
+ * Replaces philtorch::recurN, whose only implementation in the reference is
+ * the CPU one, host_recurN.cpp:236-281 (registered at :285).  M = 1 and 2 run
+ * the kernels of phs_recur_fwd and phs_recur2_fwd. */
+int phs_recurN_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int coef_shared, const void *zi,
+                   const void *x, void *y, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Backward of phs_recurN_fwd.  grad_A: [B,T,M,M], or [T,M,M] when
+ * coef_shared.  grad_zi: [B,M].  grad_x: [B,T,M].
+ * Replaces the recurN autograd closure philtorch/__init__.py:34-73. */
+int phs_recurN_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int coef_shared, const void *zi,
+                   const void *y, const void *grad_y, void *grad_x, void *grad_A, void *grad_zi,
+                   void *workspace, size_t workspace_bytes, void *stream);
+
+/* LTI MxM scan of state order M = 1..4.  A: [B,M,M] (coef_shared=0) or
+ * [M,M] (coef_shared=1); zi: [B,M]; x, y: [B,T,M].
+ * Replaces philtorch::lti_recurN, CPU-only in the reference:
+ * host_lti_recurN.cpp:63-108 (registered at :110-113).  M = 1 and 2 run the
+ * kernels of phs_lti_recur_fwd and phs_lti_recur2_fwd. */
+int phs_lti_recurN_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int coef_shared,
+                       const void *zi, const void *x, void *y, void *workspace, size_t workspace_bytes,
+                       void *stream);
+
+/* Backward of phs_lti_recurN_fwd.  grad_A: [B,M,M], or [M,M] when
+ * coef_shared, sum_t lambda[t] conj(h[t-1])^T.
+ * Replaces the lti_recurN autograd closure philtorch/__init__.py:76-112. */
+int phs_lti_recurN_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int coef_shared,
+                       const void *zi, const void *y, const void *grad_y, void *grad_x, void *grad_A,
+                       void *grad_zi, void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -80,7 +80,7 @@ def recur(A, zi, x, nthreads=None):
 
 
 def lti_recurN(A, zi, x, nthreads=None):
-    """philtorch::lti_recurN / lti_recur2 CPU (host_lti_recurN.cpp:147-192).
+    """philtorch::lti_recurN / lti_recur2 CPU (host_lti_recurN.cpp:5-108).
     A [B,M,M] or shared [M,M]; zi [B,M]; x [B,T,M]."""
     dt = x.dtype
     x = _c(x, dt); zi = _c(zi, dt); A = _c(A, dt)

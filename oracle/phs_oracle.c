@@ -16,8 +16,8 @@
  *               first step off (:279).  M = 1 is the LPV scalar scan; M = 2 is recur2.
  *   lti_recur   philtorch/csrc/host_lti_recur.cpp:42-80 (batched a[b] :4-22,
  *               shared scalar a :24-40).
- *   lti_recurN  philtorch/csrc/host_lti_recurN.cpp:147-192 (batched :88-117,
- *               shared :119-145).  M = 2 is lti_recur2.
+ *   lti_recurN  philtorch/csrc/host_lti_recurN.cpp:63-108 (batched :5-33,
+ *               shared :36-61).  M = 2 is lti_recur2.
  *
  * Backward closures (reverse-time scan of the same form):
  *   recurN      philtorch/__init__.py:34-73  (_recurN_backward)
@@ -107,7 +107,7 @@ static void set_threads(int nthreads) {
     return 0;                                                                     \
   }                                                                               \
                                                                                   \
-  /* host_lti_recurN.cpp:147-192 (A [M,M] shared or [B,M,M]). */                  \
+  /* host_lti_recurN.cpp:5-61 (A [M,M] shared or [B,M,M]). */                     \
   int oracle_lti_recurN_##SFX(int64_t B, int64_t T, int64_t M, const S *A,        \
                               int A_batched, const S *zi, const S *x, S *y,       \
                               int nthreads) {                                     \

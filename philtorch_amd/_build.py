@@ -4,12 +4,14 @@ Two shared objects, both written next to this file so that they travel with
 the repository tree:
 
 * ``libphilscan.so`` — the HIP kernels and their C ABI (include/philscan.h),
-  compiled by hipcc for gfx950 only.  It has no torch dependency.
+  compiled by hipcc for gfx950 only from four units compiled in parallel
+  (fixed-order and order-M entry points, the order-3 and order-4 kernels).
+  It has no torch dependency.
 * ``_C.so`` — the torch.library operator layer (csrc/torch_ops.cpp), host C++
   linked against libtorch and libphilscan (found through ``$ORIGIN``).
 
 No hipify step, no JIT cache: ``python -m philtorch_amd._build`` or
-``__graft_entry__.build()`` runs both compiles in parallel.
+``__graft_entry__.build()`` runs the compiles in parallel.
 """
 from __future__ import annotations
 
@@ -55,9 +57,23 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(out, flush=True)
 
 
-def _kernel_cmd() -> list[str]:
-    tmp = KERNEL_LIB + ".tmp"
-    return [HIPCC, *HIP_FLAGS, "-shared", "-Wl,-soname,libphilscan.so", os.path.join(CSRC, "phs_capi.hip"), "-o", tmp]
+# (source, extra flags, object): the fixed-order and order-M entry points,
+# and the generic BlockN kernels once per order
+KERNEL_UNITS = (
+    ("phs_capi.hip", [], "phs_capi.o"),
+    ("phs_capi_n.hip", [], "phs_capi_n.o"),
+    ("phs_blockn.hip", ["-DPHS_BLOCKN_ORDER=3"], "phs_blockn3.o"),
+    ("phs_blockn.hip", ["-DPHS_BLOCKN_ORDER=4"], "phs_blockn4.o"),
+)
+
+
+def _kernel_cmds() -> tuple[list[list[str]], list[str]]:
+    """(per-unit compile commands, link command) of libphilscan."""
+    objs = [os.path.join(HERE, o) for _, _, o in KERNEL_UNITS]
+    compiles = [[HIPCC, *HIP_FLAGS, *flags, "-c", os.path.join(CSRC, src), "-o", o]
+                for (src, flags, _), o in zip(KERNEL_UNITS, objs)]
+    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-Wl,-soname,libphilscan.so", *objs, "-o", KERNEL_LIB + ".tmp"]
+    return compiles, link
 
 
 def _ops_cmds() -> tuple[list[str], list[str]]:
@@ -87,10 +103,14 @@ def _ops_cmds() -> tuple[list[str], list[str]]:
 def build(verbose: bool = False) -> list[str]:
     """Compile both libraries; returns their paths.  Always recompiles."""
     compile_cmd, link_cmd = _ops_cmds()
-    with ThreadPoolExecutor(max_workers=2) as ex:
-        futs = [ex.submit(_run, _kernel_cmd(), verbose), ex.submit(_run, compile_cmd, verbose)]
+    kernel_compiles, kernel_link = _kernel_cmds()
+    with ThreadPoolExecutor(max_workers=len(kernel_compiles) + 1) as ex:
+        futs = [ex.submit(_run, c, verbose) for c in kernel_compiles] + [ex.submit(_run, compile_cmd, verbose)]
         for f in futs:
             f.result()
+    _run(kernel_link, verbose)
+    for c in kernel_compiles:
+        os.remove(c[-1])
     os.replace(KERNEL_LIB + ".tmp", KERNEL_LIB)
     _run(link_cmd, verbose)
     os.replace(OPS_LIB + ".tmp", OPS_LIB)

@@ -297,6 +297,173 @@ struct Block2 {
   }
 };
 
+// M x M state-space recursion for small orders (M = 3, 4): coefficient MatN
+// (row-major, as torch stores [..., M, M]), state VecN.  The generic
+// counterpart of Block2, which stays hand-unrolled for the biquad hot path.
+template <typename T, int M>
+struct MatN {
+  T m[M * M];
+};
+template <typename T, int M>
+struct VecN {
+  T v[M];
+};
+
+template <typename T, int M>
+struct BlockN {
+  using elem = T;
+  using ct = typename Wide<T>::type;
+  using s_coef = MatN<T, M>;
+  using s_state = VecN<T, M>;
+  using coef = MatN<ct, M>;
+  using state = VecN<ct, M>;
+  using acc_coef = MatN<ct, M>;
+  static constexpr int kCoefElems = M * M;
+  static constexpr int kStateElems = M;
+  static constexpr int kVecsPerLane = 1;
+  static constexpr int kRounds = 2;
+  // 3 data waves plus a look-back wave, as Block2; no register floor (the
+  // maps are large and complex orders would spill under one)
+  static constexpr bool kLookbackWave = true;
+  static constexpr int kWavesPerBlock = 3;
+  static constexpr int kMinWavesPerEU = 1;
+
+  template <typename D, typename S, int N>
+  static __device__ __forceinline__ void conv_up(D (&d)[N], const S (&s)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) d[i] = up(s[i]);
+  }
+  template <typename D, typename S, int N>
+  static __device__ __forceinline__ void conv_down(D (&d)[N], const S (&s)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) d[i] = down<T>(s[i]);
+  }
+  template <typename U>
+  static __device__ __forceinline__ MatN<U, M> mat_zero() {
+    MatN<U, M> r;
+#pragma unroll
+    for (int i = 0; i < M * M; ++i) r.m[i] = Num<U>::zero();
+    return r;
+  }
+  template <typename U>
+  static __device__ __forceinline__ VecN<U, M> vec_zero() {
+    VecN<U, M> r;
+#pragma unroll
+    for (int i = 0; i < M; ++i) r.v[i] = Num<U>::zero();
+    return r;
+  }
+  // q p (apply p first)
+  template <typename U>
+  static __device__ __forceinline__ MatN<U, M> mat_mul(const MatN<U, M> &q, const MatN<U, M> &p) {
+    MatN<U, M> r;
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+#pragma unroll
+      for (int j = 0; j < M; ++j) {
+        U acc = mul(q.m[i * M + M - 1], p.m[(M - 1) * M + j]);
+#pragma unroll
+        for (int k = M - 2; k >= 0; --k) acc = mad(q.m[i * M + k], p.m[k * M + j], acc);
+        r.m[i * M + j] = acc;
+      }
+    return r;
+  }
+  // A h + x
+  template <typename U>
+  static __device__ __forceinline__ VecN<U, M> mat_affine(const MatN<U, M> &A, const VecN<U, M> &h,
+                                                         const VecN<U, M> &x) {
+    VecN<U, M> r;
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+      U acc = x.v[i];
+#pragma unroll
+      for (int k = M - 1; k >= 0; --k) acc = mad(A.m[i * M + k], h.v[k], acc);
+      r.v[i] = acc;
+    }
+    return r;
+  }
+  template <typename U>
+  static __device__ __forceinline__ VecN<U, M> vec_add(const VecN<U, M> &a, const VecN<U, M> &b) {
+    VecN<U, M> r;
+#pragma unroll
+    for (int i = 0; i < M; ++i) r.v[i] = add(a.v[i], b.v[i]);
+    return r;
+  }
+  template <typename U>
+  static __device__ __forceinline__ MatN<U, M> mat_adjoint(const MatN<U, M> &A) {
+    MatN<U, M> r;
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+#pragma unroll
+      for (int j = 0; j < M; ++j) r.m[i * M + j] = cj(A.m[j * M + i]);
+    return r;
+  }
+  // lam conj(y)^T
+  template <typename U>
+  static __device__ __forceinline__ MatN<U, M> vec_outer(const VecN<U, M> &lam, const VecN<U, M> &y) {
+    MatN<U, M> r;
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+#pragma unroll
+      for (int j = 0; j < M; ++j) r.m[i * M + j] = mul(lam.v[i], cj(y.v[j]));
+    return r;
+  }
+
+  static __device__ __forceinline__ coef load_c(const s_coef &v) {
+    coef r;
+    conv_up(r.m, v.m);
+    return r;
+  }
+  static __device__ __forceinline__ state load_s(const s_state &v) {
+    state r;
+    conv_up(r.v, v.v);
+    return r;
+  }
+  static __device__ __forceinline__ s_coef store_c(const coef &v) {
+    s_coef r;
+    conv_down(r.m, v.m);
+    return r;
+  }
+  static __device__ __forceinline__ s_state store_s(const state &v) {
+    s_state r;
+    conv_down(r.v, v.v);
+    return r;
+  }
+  static __device__ __forceinline__ s_coef s_czero() { return mat_zero<T>(); }
+  static __device__ __forceinline__ s_state s_szero() { return vec_zero<T>(); }
+  static __device__ __forceinline__ s_state s_affine(const s_coef &A, const s_state &h, const s_state &x) {
+    return mat_affine<T>(A, h, x);
+  }
+  static __device__ __forceinline__ s_state s_add(const s_state &a, const s_state &b) { return vec_add<T>(a, b); }
+  static __device__ __forceinline__ s_coef s_cmul(const s_coef &q, const s_coef &p) { return mat_mul<T>(q, p); }
+  static __device__ __forceinline__ s_coef s_adjoint(const s_coef &A) { return mat_adjoint<T>(A); }
+  static __device__ __forceinline__ s_coef s_outer(const s_state &lam, const s_state &y) {
+    return vec_outer<T>(lam, y);
+  }
+
+  static __device__ __forceinline__ coef cone() {
+    coef r = mat_zero<ct>();
+#pragma unroll
+    for (int i = 0; i < M; ++i) r.m[i * M + i] = Num<ct>::one();
+    return r;
+  }
+  static __device__ __forceinline__ state szero() { return vec_zero<ct>(); }
+  static __device__ __forceinline__ coef cmul(const coef &q, const coef &p) { return mat_mul<ct>(q, p); }
+  static __device__ __forceinline__ state affine(const coef &A, const state &h, const state &x) {
+    return mat_affine<ct>(A, h, x);
+  }
+  static __device__ __forceinline__ state sadd(const state &a, const state &b) { return vec_add<ct>(a, b); }
+  static __device__ __forceinline__ coef adjoint(const coef &A) { return mat_adjoint<ct>(A); }
+  static __device__ __forceinline__ coef outer(const state &lam, const state &y) { return vec_outer<ct>(lam, y); }
+  static __device__ __forceinline__ acc_coef acc_zero() { return mat_zero<ct>(); }
+  static __device__ __forceinline__ acc_coef acc_add(const acc_coef &s, const coef &v) {
+    acc_coef r;
+#pragma unroll
+    for (int i = 0; i < M * M; ++i) r.m[i] = add(s.m[i], v.m[i]);
+    return r;
+  }
+  static __device__ __forceinline__ acc_coef acc_sum(const acc_coef &a, const acc_coef &b) { return acc_add(a, b); }
+};
+
 // Affine map h -> A h + x.
 template <class Alg>
 struct Map {

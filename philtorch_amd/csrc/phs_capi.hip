@@ -1,198 +1,10 @@
-// C ABI entry points of libphilscan (declared in include/philscan.h).
-// Host side: argument checks, workspace carving, and the launch of
-//   scan_kernel [-> reduce kernel]
-// on the caller's stream.  No allocation and no synchronisation; the only
-// global state is the spin-limit testing hook and a per-device cache of how
-// many workgroups of each kernel are resident at once.
-// Workspace layout: [0, 2048) header (16 striped {epoch, claim count} words),
-// then the tile status words, then (backward only) per-tile partial sums or
-// per-step scratch.
-#include <hip/hip_runtime.h>
-
-#include <algorithm>
-#include <atomic>
-#include <map>
-#include <mutex>
-#include <utility>
-
-#include "../../include/philscan.h"
-#include "phs_scan.hpp"
+// C ABI entry points of libphilscan (declared in include/philscan.h) for the
+// fixed-order ops: scalar (recur, lti_recur) and 2x2 (recur2, lti_recur2).
+// The order-M entry points live in phs_capi_n.hip; both share phs_launch.hpp.
+#include "phs_launch.hpp"
 
 namespace phs {
-namespace {
-
-constexpr size_t kAlign = 256;
-// Look-back polls before a tile computes its entry state itself; about 0.1 s
-// of waiting, far beyond any schedule in which predecessors make progress.
-constexpr unsigned kDefaultSpinLimit = 1u << 16;
-std::atomic<unsigned> g_spin_limit{0};  // testing hook, 0 = default
-inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
-
-struct Layout {
-  int64_t tiles_per_row = 0;
-  size_t status_off = 0, status_words = 0;  // header lives at offset 0
-  size_t partials_off = 0, scratch_off = 0, total = 0;
-};
-
-// TV: coefficient varies with time; shared: one coefficient set for all rows.
-template <class Alg>
-Layout make_layout(int64_t B, int64_t T, bool TV, bool shared, bool backward) {
-  using Sh = Shape<Alg>;
-  Layout L;
-  L.tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
-  L.status_off = align_up(kHeaderBytes);
-  L.status_words = size_t(B) * size_t(L.tiles_per_row) * Sh::kStride;
-  size_t off = align_up(L.status_off + L.status_words * sizeof(uint64_t));
-  if (backward && !TV) {  // per-tile coefficient-gradient partial sums
-    L.partials_off = off;
-    off = align_up(off + size_t(B) * size_t(L.tiles_per_row) * sizeof(typename Alg::acc_coef));
-  }
-  if (backward && TV && shared) {  // per-step gradients before the batch sum
-    L.scratch_off = off;
-    off = align_up(off + size_t(B) * size_t(T) * sizeof(typename Alg::s_coef));
-  }
-  L.total = off;
-  return L;
-}
-
-inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-// Workgroups of `kernel` resident at once on the current device (occupancy
-// per CU times CUs), cached per (kernel, device); 0 if the query fails.
-int64_t resident_groups(const void *kernel, int threads) {
-  static std::mutex mu;
-  static std::map<std::pair<const void *, int>, int64_t> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_pair(kernel, dev);
-  auto it = cache.find(key);
-  if (it != cache.end()) return it->second;
-  int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 0;
-  const int64_t n = int64_t(std::max(per_cu, 0)) * std::max(cus, 0);
-  cache[key] = n;
-  return n;
-}
-
-template <class Alg, bool TV, bool REV>
-void launch_scan(const ScanArgs<Alg> &a, unsigned grid, hipStream_t stream) {
-  hipLaunchKernelGGL((scan_kernel<Alg, TV, REV>), dim3(grid), dim3(Shape<Alg>::kThreads), 0, stream, a);
-}
-
-template <class Alg>
-int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void *coef,
-           const void *zi, const void *x, const void *y, void *out, void *gcoef, void *gzi,
-           void *workspace, size_t ws_bytes, hipStream_t stream) {
-  using E = typename Alg::elem;
-  using Sh = Shape<Alg>;
-  if (B < 0 || T < 0) return PHS_ERR_INVALID;
-  if (B == 0 || T == 0) return PHS_OK;
-  if (!coef || !zi || !x || (backward ? !y : !out)) return PHS_ERR_INVALID;
-  const Layout L = make_layout<Alg>(B, T, TV, shared, backward);
-  if (double(B) * double(L.tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
-  if (!workspace || ws_bytes < L.total) return PHS_ERR_WORKSPACE;
-
-  char *ws = static_cast<char *>(workspace);
-  ScanArgs<Alg> a;
-  a.coef = static_cast<const E *>(coef);
-  a.coef_row_stride = shared ? 0 : (TV ? T : 1);
-  a.zi = static_cast<const E *>(zi);
-  a.x = static_cast<const E *>(x);
-  a.y = static_cast<const E *>(y);
-  a.out = static_cast<E *>(out);
-  a.gcoef = nullptr;
-  a.partials = nullptr;
-  a.gzi = static_cast<E *>(gzi);
-  a.B = B;
-  a.T_len = T;
-  a.tiles_per_row = L.tiles_per_row;
-  a.claims = reinterpret_cast<unsigned long long *>(ws);
-  a.status = reinterpret_cast<uint64_t *>(ws + L.status_off);
-  const unsigned tiles = unsigned(B * L.tiles_per_row);
-  a.tiles = tiles;
-  a.per_stripe = (tiles + kStripes - 1) / kStripes;
-  const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
-  a.spin_limit = sl ? sl : kDefaultSpinLimit;
-  if (backward && gcoef) {
-    if (TV)
-      a.gcoef = shared ? reinterpret_cast<E *>(ws + L.scratch_off) : static_cast<E *>(gcoef);
-    else
-      a.partials = ws + L.partials_off;
-  }
-  bool vec = (size_t(T) * sizeof(typename Alg::s_state)) % 16 == 0 && aligned16(x) && aligned16(y) &&
-             aligned16(out) && aligned16(a.gcoef) && (!TV || aligned16(coef));
-  a.vec_ok = vec ? 1 : 0;
-
-  const void *kernel = TV ? (backward ? reinterpret_cast<const void *>(scan_kernel<Alg, true, true>)
-                                       : reinterpret_cast<const void *>(scan_kernel<Alg, true, false>))
-                          : (backward ? reinterpret_cast<const void *>(scan_kernel<Alg, false, true>)
-                                      : reinterpret_cast<const void *>(scan_kernel<Alg, false, false>));
-  // Tiles are claimed q-major, so a tile's predecessor in its row was claimed
-  // B claims earlier, i.e. B/resident tile lifetimes earlier.  From half a
-  // lifetime on it has published at least its aggregate, and the look-back
-  // wave can poll for it while the data waves are still loading; with
-  // smaller B those early polls mostly fail and only add status traffic.
-  a.early_polls = 0;
-  if (Sh::kLookbackWave) {
-    const int64_t resident = resident_groups(kernel, Sh::kThreads);
-    if (resident > 0 && 2 * B >= resident) a.early_polls = a.spin_limit;
-  }
-
-  const unsigned grid = a.per_stripe * kStripes;
-  if (TV) {
-    if (backward)
-      launch_scan<Alg, true, true>(a, grid, stream);
-    else
-      launch_scan<Alg, true, false>(a, grid, stream);
-  } else {
-    if (backward)
-      launch_scan<Alg, false, true>(a, grid, stream);
-    else
-      launch_scan<Alg, false, false>(a, grid, stream);
-  }
-  if (backward && gcoef) {
-    if (TV && shared) {
-      const int blocks = int(std::min<int64_t>((T + kReduceThreads - 1) / kReduceThreads, 4096));
-      hipLaunchKernelGGL(reduce_batch_kernel<Alg>, dim3(blocks), dim3(kReduceThreads), 0, stream,
-                         static_cast<const E *>(a.gcoef), B, T, static_cast<E *>(gcoef));
-    } else if (!TV) {
-      const int64_t rows = shared ? 1 : B;
-      const int64_t count = shared ? B * L.tiles_per_row : L.tiles_per_row;
-      hipLaunchKernelGGL(reduce_rows_kernel<Alg>, dim3(unsigned(rows)), dim3(kReduceThreads), 0, stream,
-                         static_cast<const void *>(a.partials), count, static_cast<E *>(gcoef));
-    }
-  }
-  return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
-}
-
-template <template <class> class AlgT, class F>
-int dispatch(int dtype, F &&f) {
-  switch (dtype) {
-    case PHS_F32: return f(AlgT<float>{});
-    case PHS_F64: return f(AlgT<double>{});
-    case PHS_C64: return f(AlgT<c64>{});
-    case PHS_C128: return f(AlgT<c128>{});
-    case PHS_I64: return f(AlgT<int64_t>{});
-    default: return PHS_ERR_DTYPE;
-  }
-}
-
-template <template <class> class AlgT>
-size_t ws_size(int dtype, int64_t B, int64_t T, bool TV, bool shared, bool backward) {
-  size_t out = 0;
-  if (B <= 0 || T <= 0) return 0;
-  dispatch<AlgT>(dtype, [&](auto alg) {
-    using Alg = decltype(alg);
-    out = make_layout<Alg>(B, T, TV, shared, backward).total;
-    return 0;
-  });
-  return out;
-}
-
-}  // namespace
+std::atomic<unsigned> g_spin_limit{0};
 }  // namespace phs
 
 using phs::Block2;
@@ -223,7 +35,7 @@ const char *phs_error_string(int status) {
   }
 }
 
-int phs_abi_version(void) { return 100; }
+int phs_abi_version(void) { return 101; }
 
 void phs_debug_set_spin_limit(unsigned polls) { phs::g_spin_limit.store(polls, std::memory_order_relaxed); }
 

@@ -57,6 +57,8 @@
 
 namespace phs {
 
+constexpr size_t gcd16(size_t n) { return n % 16 == 0 ? 16 : n % 8 == 0 ? 8 : n % 4 == 0 ? 4 : n % 2 == 0 ? 2 : 1; }
+
 template <class Alg>
 struct Shape {
   static constexpr int kWaves = Alg::kWavesPerBlock;  // data waves
@@ -64,10 +66,13 @@ struct Shape {
   static constexpr int kThreads = 64 * (kWaves + (kLookbackWave ? 1 : 0));
   using state = typename Alg::state;
   using s_state = typename Alg::s_state;
-  // steps per lane and round: kVecs 16-byte vectors of stored states (one
-  // state per lane when a state is 16 bytes or wider)
-  static constexpr int K =
-      sizeof(s_state) >= 16 ? 1 : Alg::kVecsPerLane * int(16 / sizeof(s_state));
+  // steps per lane and round: a whole number of 16-byte vectors of stored
+  // states, kVecsPerLane vectors' worth where a state is under 16 bytes
+  static constexpr int kMinSteps = 16 / int(gcd16(sizeof(s_state)));  // smallest K with K*size % 16 == 0
+  static constexpr int K = sizeof(s_state) >= 16 || Alg::kVecsPerLane * 16 < int(kMinSteps * sizeof(s_state))
+                               ? kMinSteps
+                               : Alg::kVecsPerLane * int(16 / sizeof(s_state)) / kMinSteps * kMinSteps;
+  static_assert(K >= 1 && (K * sizeof(s_state)) % 16 == 0, "chunks must be whole 16-byte vectors");
   static constexpr int R = Alg::kRounds;
   static constexpr int kWaveSeg = 64 * K * R;
   static constexpr int kTile = kWaves * kWaveSeg;

@@ -90,29 +90,36 @@ Workspace workspace_for(const Tensor &like, size_t bytes, void *stream) {
   return {entry.buf.mutable_data_ptr(), size_t(entry.buf.numel())};
 }
 
+// Largest state order with native kernels (the C ABI's phs_*N_* entry points).
+constexpr int64_t kMaxOrder = 4;
+
 using FwdFn = int (*)(int, int64_t, int64_t, const void *, int, const void *, const void *, void *,
                       void *, size_t, void *);
 using BwdFn = int (*)(int, int64_t, int64_t, const void *, int, const void *, const void *,
                       const void *, void *, void *, void *, void *, size_t, void *);
 
-// y = op(A, zi, x); A/zi/x already validated, x is [B, T, ...]
-Tensor run_fwd(const char *name, FwdFn fn, int op, const Tensor &A, bool shared, const Tensor &zi,
-               const Tensor &x) {
+// y = op(A, zi, x); A/zi/x already validated, x is [B, T, ...].
+// launch(dt, B, T, A, shared, zi, x, y, ws, bytes, stream) runs the entry
+// point; ws_size(dt, B, T, shared, backward) sizes its workspace.
+template <class Launch, class Size>
+Tensor run_fwd_with(const char *name, Launch &&launch, Size &&ws_size, const Tensor &A, bool shared,
+                    const Tensor &zi, const Tensor &x) {
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
   const int dt = phs_dtype_of(x.scalar_type());
   const int64_t B = x.size(0), T = x.size(1);
   Tensor Ac = A.contiguous(), zc = zi.contiguous(), xc = x.contiguous();
   Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
   void *stream = stream_of(x);
-  const Workspace ws = workspace_for(x, phs_workspace_size(op, dt, B, T, shared ? 1 : 0, 0), stream);
-  check_status(fn(dt, B, T, Ac.const_data_ptr(), shared ? 1 : 0, zc.const_data_ptr(),
-                  xc.const_data_ptr(), y.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+  const Workspace ws = workspace_for(x, ws_size(dt, B, T, shared ? 1 : 0, 0), stream);
+  check_status(launch(dt, B, T, Ac.const_data_ptr(), shared ? 1 : 0, zc.const_data_ptr(), xc.const_data_ptr(),
+                      y.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
                name);
   return y;
 }
 
-Triple run_bwd(const char *name, BwdFn fn, int op, const Tensor &A, bool shared, const Tensor &zi,
-               const Tensor &y, const Tensor &gy) {
+template <class Launch, class Size>
+Triple run_bwd_with(const char *name, Launch &&launch, Size &&ws_size, const Tensor &A, bool shared,
+                    const Tensor &zi, const Tensor &y, const Tensor &gy) {
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(y.device());
   const int dt = phs_dtype_of(y.scalar_type());
   const int64_t B = y.size(0), T = y.size(1);
@@ -121,10 +128,10 @@ Triple run_bwd(const char *name, BwdFn fn, int op, const Tensor &A, bool shared,
   Tensor gzi = at::empty(zi.sizes(), zi.options());
   Tensor gx = at::empty(y.sizes(), y.options());
   void *stream = stream_of(y);
-  const Workspace ws = workspace_for(y, phs_workspace_size(op, dt, B, T, shared ? 1 : 0, 1), stream);
-  check_status(fn(dt, B, T, Ac.const_data_ptr(), shared ? 1 : 0, zc.const_data_ptr(),
-                  yc.const_data_ptr(), gc.const_data_ptr(), gx.mutable_data_ptr(),
-                  gA.mutable_data_ptr(), gzi.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+  const Workspace ws = workspace_for(y, ws_size(dt, B, T, shared ? 1 : 0, 1), stream);
+  check_status(launch(dt, B, T, Ac.const_data_ptr(), shared ? 1 : 0, zc.const_data_ptr(), yc.const_data_ptr(),
+                      gc.const_data_ptr(), gx.mutable_data_ptr(), gA.mutable_data_ptr(), gzi.mutable_data_ptr(),
+                      ws.ptr, ws.bytes, stream),
                name);
   if (B == 0 || T == 0) {  // nothing was launched: gradients are zero
     gA.zero_();
@@ -132,6 +139,44 @@ Triple run_bwd(const char *name, BwdFn fn, int op, const Tensor &A, bool shared,
     gx.zero_();
   }
   return {gA, gzi, gx};
+}
+
+// fixed-order entry points (op: a phs_op of order 1 or 2)
+Tensor run_fwd(const char *name, FwdFn fn, int op, const Tensor &A, bool shared, const Tensor &zi,
+               const Tensor &x) {
+  return run_fwd_with(
+      name, fn, [op](int dt, int64_t B, int64_t T, int sh, int bw) { return phs_workspace_size(op, dt, B, T, sh, bw); },
+      A, shared, zi, x);
+}
+
+Triple run_bwd(const char *name, BwdFn fn, int op, const Tensor &A, bool shared, const Tensor &zi,
+               const Tensor &y, const Tensor &gy) {
+  return run_bwd_with(
+      name, fn, [op](int dt, int64_t B, int64_t T, int sh, int bw) { return phs_workspace_size(op, dt, B, T, sh, bw); },
+      A, shared, zi, y, gy);
+}
+
+// order-M entry points (phs_recurN_* / phs_lti_recurN_*, op PHS_OP_RECURN or
+// PHS_OP_LTI_RECURN)
+using FwdFnN = int (*)(int, int, int64_t, int64_t, const void *, int, const void *, const void *, void *,
+                       void *, size_t, void *);
+using BwdFnN = int (*)(int, int, int64_t, int64_t, const void *, int, const void *, const void *,
+                       const void *, void *, void *, void *, void *, size_t, void *);
+
+Tensor run_fwd_n(const char *name, FwdFnN fn, int op, int M, const Tensor &A, bool shared, const Tensor &zi,
+                 const Tensor &x) {
+  return run_fwd_with(
+      name, [fn, M](int dt, auto... rest) { return fn(dt, M, rest...); },
+      [op, M](int dt, int64_t B, int64_t T, int sh, int bw) { return phs_workspace_size_n(op, dt, M, B, T, sh, bw); },
+      A, shared, zi, x);
+}
+
+Triple run_bwd_n(const char *name, BwdFnN fn, int op, int M, const Tensor &A, bool shared, const Tensor &zi,
+                 const Tensor &y, const Tensor &gy) {
+  return run_bwd_with(
+      name, [fn, M](int dt, auto... rest) { return fn(dt, M, rest...); },
+      [op, M](int dt, int64_t B, int64_t T, int sh, int bw) { return phs_workspace_size_n(op, dt, M, B, T, sh, bw); },
+      A, shared, zi, y, gy);
 }
 
 Triple to_dtype(const Triple &t, at::ScalarType dt) {
@@ -197,8 +242,10 @@ Tensor recurN_hip(const Tensor &A, const Tensor &zi, const Tensor &x) {
     return run_fwd("recurN", phs_recur_fwd, PHS_OP_RECUR, A.reshape(scalar_coef_shape(A, shared)),
                    shared, zi.reshape({zi.size(0)}), x.reshape({x.size(0), x.size(1)}))
         .view(x.sizes());
-  TORCH_CHECK(M == 2, "philtorch::recurN on HIP devices supports 1x1 and 2x2 matrices, got ", M, "x", M);
-  return run_fwd("recurN", phs_recur2_fwd, PHS_OP_RECUR2, A, shared, zi, x);
+  if (M == 2) return run_fwd("recurN", phs_recur2_fwd, PHS_OP_RECUR2, A, shared, zi, x);
+  TORCH_CHECK(M <= kMaxOrder, "philtorch::recurN on HIP devices supports M x M matrices up to M = ", kMaxOrder,
+              ", got ", M, "x", M);
+  return run_fwd_n("recurN", phs_recurN_fwd, PHS_OP_RECURN, int(M), A, shared, zi, x);
 }
 
 Tensor recur2_hip(const Tensor &A, const Tensor &zi, const Tensor &x) {
@@ -225,8 +272,10 @@ Triple recurN_backward_hip(const Tensor &A, const Tensor &zi, const Tensor &y, c
     return {std::get<0>(r).view(A.sizes()), std::get<1>(r).view(zi.sizes()),
             std::get<2>(r).view(y.sizes())};
   }
-  TORCH_CHECK(M == 2, "philtorch::recurN on HIP devices supports 1x1 and 2x2 matrices, got ", M, "x", M);
-  return run_bwd("recurN_backward", phs_recur2_bwd, PHS_OP_RECUR2, A, shared, zi, y, g);
+  if (M == 2) return run_bwd("recurN_backward", phs_recur2_bwd, PHS_OP_RECUR2, A, shared, zi, y, g);
+  TORCH_CHECK(M <= kMaxOrder, "philtorch::recurN on HIP devices supports M x M matrices up to M = ", kMaxOrder,
+              ", got ", M, "x", M);
+  return run_bwd_n("recurN_backward", phs_recurN_bwd, PHS_OP_RECURN, int(M), A, shared, zi, y, g);
 }
 
 // ------------------------------------------------------------ LTI scalar
@@ -264,7 +313,7 @@ Triple lti_recur_backward_hip(const Tensor &A, const Tensor &zi, const Tensor &y
 
 // ------------------------------------------------------------ LTI MxM (M = 1, 2)
 void check_lti_recurN(const Tensor &A, const Tensor &zi, const Tensor &x) {
-  // host_lti_recurN.cpp:155-159 and philtorch/__init__.py:200-231
+  // host_lti_recurN.cpp:67-75 and philtorch/__init__.py:200-231
   TORCH_CHECK(A.dim() == 2 || A.dim() == 3, "A must be a 2D or 3D tensor");
   TORCH_CHECK(x.dim() == 3, "x must be a 3D tensor (batch, time, order)");
   TORCH_CHECK(x.size(2) == A.size(-1), "Last dimension of x must match last dimension of A");
@@ -287,8 +336,10 @@ Tensor lti_recurN_hip(const Tensor &A, const Tensor &zi, const Tensor &x) {
                    shared ? A.reshape({1}) : A.reshape({A.size(0)}), shared,
                    zi.reshape({zi.size(0)}), x.reshape({x.size(0), x.size(1)}))
         .view(x.sizes());
-  TORCH_CHECK(M == 2, "philtorch::lti_recurN on HIP devices supports 1x1 and 2x2 matrices, got ", M, "x", M);
-  return run_fwd("lti_recurN", phs_lti_recur2_fwd, PHS_OP_LTI_RECUR2, A, shared, zi, x);
+  if (M == 2) return run_fwd("lti_recurN", phs_lti_recur2_fwd, PHS_OP_LTI_RECUR2, A, shared, zi, x);
+  TORCH_CHECK(M <= kMaxOrder, "philtorch::lti_recurN on HIP devices supports M x M matrices up to M = ", kMaxOrder,
+              ", got ", M, "x", M);
+  return run_fwd_n("lti_recurN", phs_lti_recurN_fwd, PHS_OP_LTI_RECURN, int(M), A, shared, zi, x);
 }
 
 Tensor lti_recur2_hip(const Tensor &A, const Tensor &zi, const Tensor &x) {
@@ -316,8 +367,10 @@ Triple lti_recurN_backward_hip(const Tensor &A, const Tensor &zi, const Tensor &
     return {std::get<0>(r).view(A.sizes()), std::get<1>(r).view(zi.sizes()),
             std::get<2>(r).view(y.sizes())};
   }
-  TORCH_CHECK(M == 2, "philtorch::lti_recurN on HIP devices supports 1x1 and 2x2 matrices, got ", M, "x", M);
-  return run_bwd("lti_recurN_backward", phs_lti_recur2_bwd, PHS_OP_LTI_RECUR2, A, shared, zi, y, g);
+  if (M == 2) return run_bwd("lti_recurN_backward", phs_lti_recur2_bwd, PHS_OP_LTI_RECUR2, A, shared, zi, y, g);
+  TORCH_CHECK(M <= kMaxOrder, "philtorch::lti_recurN on HIP devices supports M x M matrices up to M = ", kMaxOrder,
+              ", got ", M, "x", M);
+  return run_bwd_n("lti_recurN_backward", phs_lti_recurN_bwd, PHS_OP_LTI_RECURN, int(M), A, shared, zi, y, g);
 }
 
 }  // namespace

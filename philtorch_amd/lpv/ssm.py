@@ -25,8 +25,9 @@ from .. import EXTENSION_LOADED, HELION_LOADED
 
 def extension_backend_indicator(x: Tensor, M: int) -> bool:
     """True when the native scan serves this input: extension loaded, the
-    tensor on a HIP device, and a scalar or 2x2 state (philtorch/lpv/ssm.py:20-26)."""
-    return EXTENSION_LOADED and x.is_cuda and M <= 2
+    tensor on a HIP device, and a state of order M <= 4 (the reference,
+    philtorch/lpv/ssm.py:20-26, has GPU kernels for M <= 2 only)."""
+    return EXTENSION_LOADED and x.is_cuda and M <= 4
 
 
 class MatrixRecurrence(Function):

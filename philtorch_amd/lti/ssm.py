@@ -22,10 +22,11 @@ from .recur import LTIRecurrence, linear_recurrence
 
 
 def extension_backend_indicator(x: Tensor, M: int) -> bool:
-    """True when the native scan serves this input (philtorch/lti/ssm.py:13-25):
-    extension loaded, tensor on a HIP device, 2x2 state (M = 1 goes through
-    ``LTIRecurrence``)."""
-    return EXTENSION_LOADED and x.is_cuda and M == 2
+    """True when the native scan serves this input: extension loaded, tensor
+    on a HIP device, state of order 2 <= M <= 4 (M = 1 goes through
+    ``LTIRecurrence``).  The reference, philtorch/lti/ssm.py:13-25, has a GPU
+    kernel for M = 2 only."""
+    return EXTENSION_LOADED and x.is_cuda and 2 <= M <= 4
 
 
 def helion_backend_indicator(x: Tensor) -> bool:

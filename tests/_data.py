@@ -61,6 +61,17 @@ def biquad_A(g, shape, dtype, rlo=0.5, rhi=0.98):
     return A.astype(dtype)
 
 
+def stable_matrix(g, shape, M, dtype, rmax=0.95):
+    """Random M x M matrices (complex where dtype is) scaled to spectral norm
+    U(0.5, rmax), so that every step contracts the state."""
+    dtype = np.dtype(dtype)
+    A = g.standard_normal(shape + (M, M))
+    if dtype.kind == "c":
+        A = A + 1j * g.standard_normal(shape + (M, M))
+    norm = np.linalg.norm(A, ord=2, axis=(-2, -1))[..., None, None]
+    return (A / norm * g.uniform(0.5, rmax, shape)[..., None, None]).astype(dtype)
+
+
 def tol(dtype) -> float:
     dtype = np.dtype(dtype)
     if dtype in (np.dtype(np.float32), np.dtype(np.complex64)):

@@ -16,6 +16,7 @@ HEADER = os.path.join(REPO, "include", "philscan.h")
 
 PHS_OK, PHS_ERR_INVALID, PHS_ERR_WORKSPACE, PHS_ERR_LAUNCH, PHS_ERR_DTYPE = range(5)
 OPS = {"recur": 0, "lti_recur": 1, "recur2": 2, "lti_recur2": 3}
+OPS_N = {"recurN": 4, "lti_recurN": 5}  # order-M ops (entry points take M after dtype)
 DTYPES = {np.dtype(np.float32): 0, np.dtype(np.float64): 1, np.dtype(np.complex64): 2,
           np.dtype(np.complex128): 3, np.dtype(np.int64): 4}
 
@@ -44,6 +45,14 @@ def load() -> ctypes.CDLL:
     lib.phs_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                        ctypes.c_int]
     lib.phs_workspace_size.restype = ctypes.c_size_t
+    for op in OPS_N:
+        getattr(lib, f"phs_{op}_fwd").argtypes = [_FWD_ARGS[0], ctypes.c_int, *_FWD_ARGS[1:]]
+        getattr(lib, f"phs_{op}_fwd").restype = ctypes.c_int
+        getattr(lib, f"phs_{op}_bwd").argtypes = [_BWD_ARGS[0], ctypes.c_int, *_BWD_ARGS[1:]]
+        getattr(lib, f"phs_{op}_bwd").restype = ctypes.c_int
+    lib.phs_workspace_size_n.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                         ctypes.c_int, ctypes.c_int]
+    lib.phs_workspace_size_n.restype = ctypes.c_size_t
     lib.phs_error_string.argtypes = [ctypes.c_int]
     lib.phs_error_string.restype = ctypes.c_char_p
     lib.phs_debug_set_spin_limit.argtypes = [ctypes.c_uint]

@@ -56,6 +56,31 @@ def cases():
     x = np.zeros((1, 10, 2), np.int64)
     x[0, 0, 0] = 1
     out.append(("lti_recurN", np.array([[1, 1], [1, 0]], np.int64), np.zeros((1, 2), np.int64), x))
+    # orders 3 and 4 (recurN / lti_recurN beyond 2x2), batched and shared
+    # coefficients; a generator of their own keeps the cases above unchanged
+    g3 = np.random.default_rng(20261202)
+    for dt in (np.float32, np.float64, np.complex64, np.complex128):
+        cplx = np.dtype(dt).kind == "c"
+
+        def rnd3(*shape):
+            v = g3.standard_normal(shape)
+            if cplx:
+                v = v + 1j * g3.standard_normal(shape)
+            return v.astype(dt)
+
+        def coef3(M, *shape):
+            # entries below 0.9/M in modulus: every row sums below 0.9, a contraction
+            v = g3.uniform(-0.9 / M, 0.9 / M, shape)
+            if cplx:
+                v = v * np.exp(1j * g3.uniform(0, np.pi, shape))
+            return v.astype(dt)
+
+        B, T = 3, 37
+        for M in (3, 4):
+            out.append(("recurN", coef3(M, B, T, M, M), rnd3(B, M), rnd3(B, T, M)))
+            out.append(("recurN", coef3(M, T, M, M), rnd3(B, M), rnd3(B, T, M)))
+            out.append(("lti_recurN", coef3(M, B, M, M), rnd3(B, M), rnd3(B, T, M)))
+            out.append(("lti_recurN", coef3(M, M, M), rnd3(B, M), rnd3(B, T, M)))
     return out
 
 

@@ -99,6 +99,26 @@ def test_state_space_lpv_native_equals_cpu(hip):
     _close(zg, zc, np.float64, "zf")
 
 
+def test_state_space_lti_order3_native_equals_cpu(hip):
+    """A third-order LTI system through state_space: native order-M scan on
+    the GPU, the reference's pure-PyTorch route on the CPU."""
+    from philtorch_amd import lti
+
+    g = D.rng(34)
+    B, T = 3, 5000
+    A = D.stable_matrix(g, (), 3, np.float64)
+    x = D.normal(g, (B, T), np.float64)
+    zi = D.normal(g, (B, 3), np.float64)
+    Bm = np.array([1.0, -0.5, 0.25])
+    C = np.array([0.4, -1.1, 0.7])
+    yc, zc = lti.state_space(torch.from_numpy(A), torch.from_numpy(x), B=torch.from_numpy(Bm), C=torch.from_numpy(C),
+                             zi=torch.from_numpy(zi), unroll_factor=1)
+    yg, zg = lti.state_space(torch.from_numpy(A).cuda(), torch.from_numpy(x).cuda(), B=torch.from_numpy(Bm).cuda(),
+                             C=torch.from_numpy(C).cuda(), zi=torch.from_numpy(zi).cuda(), unroll_factor=1)
+    _close(yg, yc, np.float64, "y")
+    _close(zg, zc, np.float64, "zf")
+
+
 def test_diag_state_space_complex_native_equals_cpu(hip):
     """Config 2's call: per-channel complex poles through LTIRecurrence."""
     from philtorch_amd import lti
@@ -127,9 +147,15 @@ def _grad_inputs(g, kind, dtype, B=3, T=11, shared=False):
     elif kind == "lpv2":
         A = D.biquad_A(g, (T,) if shared else (B, T), dtype)
         zi, x = D.normal(g, (B, 2), dtype), D.normal(g, (B, T, 2), dtype)
-    else:
+    elif kind == "lti2":
         A = D.biquad_A(g, () if shared else (B,), dtype)
         zi, x = D.normal(g, (B, 2), dtype), D.normal(g, (B, T, 2), dtype)
+    elif kind == "lpv3":  # order-M kernels (M = 3, 4)
+        A = D.stable_matrix(g, (T,) if shared else (B, T), 3, dtype)
+        zi, x = D.normal(g, (B, 3), dtype), D.normal(g, (B, T, 3), dtype)
+    else:  # lti4
+        A = D.stable_matrix(g, () if shared else (B,), 4, dtype)
+        zi, x = D.normal(g, (B, 4), dtype), D.normal(g, (B, T, 4), dtype)
     return [torch.from_numpy(np.ascontiguousarray(v)).to(dev).requires_grad_(True) for v in (A, zi, x)]
 
 
@@ -142,10 +168,12 @@ def _fn(kind):
         "lti": LTIRecurrence.apply,
         "lpv2": MatrixRecurrence.apply,
         "lti2": LTIMatrixRecurrence.apply,
+        "lpv3": MatrixRecurrence.apply,
+        "lti4": LTIMatrixRecurrence.apply,
     }[kind]
 
 
-@pytest.mark.parametrize("kind", ["lpv", "lti", "lpv2", "lti2"])
+@pytest.mark.parametrize("kind", ["lpv", "lti", "lpv2", "lti2", "lpv3", "lti4"])
 @pytest.mark.parametrize("dtype", [np.float64, np.complex128])
 @pytest.mark.parametrize("shared", [False, True])
 def test_gradcheck_gradgradcheck(hip, kind, dtype, shared):
@@ -157,16 +185,16 @@ def test_gradcheck_gradgradcheck(hip, kind, dtype, shared):
     assert torch.autograd.gradgradcheck(f, inputs, check_fwd_over_rev=fwd_ad)
 
 
-@pytest.mark.parametrize("op", ["recur", "recur2", "recurN", "lti_recur", "lti_recur2", "lti_recurN"])
-def test_opcheck(hip, op):
-    g = D.rng(D.seed_of("opcheck", op))
-    kind = {"recur": "lpv", "recur2": "lpv2", "recurN": "lpv2", "lti_recur": "lti", "lti_recur2": "lti2",
-            "lti_recurN": "lti2"}[op]
+@pytest.mark.parametrize("op,kind", [("recur", "lpv"), ("recur2", "lpv2"), ("recurN", "lpv2"), ("recurN", "lpv3"),
+                                     ("lti_recur", "lti"), ("lti_recur2", "lti2"), ("lti_recurN", "lti2"),
+                                     ("lti_recurN", "lti4")])
+def test_opcheck(hip, op, kind):
+    g = D.rng(D.seed_of("opcheck", op, kind))
     A, zi, x = _grad_inputs(g, kind, np.float64, B=2, T=40)
     torch.library.opcheck(getattr(torch.ops.philtorch, op), (A, zi, x))
 
 
-@pytest.mark.parametrize("kind", ["lpv", "lti", "lpv2", "lti2"])
+@pytest.mark.parametrize("kind", ["lpv", "lti", "lpv2", "lti2", "lpv3", "lti4"])
 def test_fused_backward_equals_composite(hip, kind):
     """Large enough for many tiles: the fused kernel (no create_graph) and the
     composite formula (create_graph) give the same gradients."""

@@ -46,8 +46,9 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def _run(api, op, A, shared, zi, x, gy):
-    """Forward + backward of one op through the C ABI; returns numpy results."""
+def _run(api, op, A, shared, zi, x, gy, M=None):
+    """Forward + backward of one op through the C ABI; returns numpy results.
+    M: the state order, for the order-M ops (recurN, lti_recurN)."""
     import torch
 
     lib, ws, capi = api
@@ -55,14 +56,23 @@ def _run(api, op, A, shared, zi, x, gy):
     B, T = x.shape[:2]
     tA, tz, tx, tg = _dev(A), _dev(zi), _dev(x), _dev(gy)
     y = torch.empty_like(tx)
-    need = lib.phs_workspace_size(capi.OPS[op], dt, B, T, int(shared), 1)
-    assert need <= ws.numel()
-    rc = getattr(lib, f"phs_{op}_fwd")(dt, B, T, _p(tA), int(shared), _p(tz), _p(tx), _p(y), _p(ws), ws.numel(),
-                                       _stream())
+    order = () if M is None else (M,)
+
+    def size(backward):
+        if M is None:
+            return lib.phs_workspace_size(capi.OPS[op], dt, B, T, int(shared), backward)
+        return lib.phs_workspace_size_n(capi.OPS_N[op], dt, M, B, T, int(shared), backward)
+
+    need = size(1)
+    need_fwd = lambda: size(0)  # noqa: E731
+    assert 0 < need <= ws.numel()
+    # the call gets exactly the reported size: an under-reported size fails it
+    rc = getattr(lib, f"phs_{op}_fwd")(dt, *order, B, T, _p(tA), int(shared), _p(tz), _p(tx), _p(y), _p(ws),
+                                       need_fwd(), _stream())
     assert rc == capi.PHS_OK, lib.phs_error_string(rc)
     gA, gz, gx = torch.empty_like(tA), torch.empty_like(tz), torch.empty_like(tx)
-    rc = getattr(lib, f"phs_{op}_bwd")(dt, B, T, _p(tA), int(shared), _p(tz), _p(y), _p(tg), _p(gx), _p(gA),
-                                       _p(gz), _p(ws), ws.numel(), _stream())
+    rc = getattr(lib, f"phs_{op}_bwd")(dt, *order, B, T, _p(tA), int(shared), _p(tz), _p(y), _p(tg), _p(gx),
+                                       _p(gA), _p(gz), _p(ws), need, _stream())
     assert rc == capi.PHS_OK, lib.phs_error_string(rc)
     torch.cuda.synchronize()
     return [t.cpu().numpy() for t in (y, gA, gz, gx)]
@@ -168,6 +178,51 @@ def test_capi_many_rows_fallback(api, op, B, T, dtype, shared):
     finally:
         lib.phs_debug_set_spin_limit(0)
     _check(got, _oracle(op, A, zi, x, gy))
+
+
+# Order-M entry points (M = 3, 4).  600 rows put the look-back wave in its
+# early-polling mode; the others run the chain mode.
+CASES_N = [
+    ("recurN", 3, 3, 5000, np.float32, False),
+    ("recurN", 4, 2, 3000, np.complex128, True),
+    ("lti_recurN", 3, 600, 2000, np.float64, False),
+    ("lti_recurN", 4, 2, 4000, np.complex64, True),
+    ("recurN", 4, 600, 700, np.float32, False),
+]
+
+
+def _case_n(op, M, B, T, dtype, shared, seed):
+    g = D.rng(seed)
+    shape = ((T,) if shared else (B, T)) if op == "recurN" else (() if shared else (B,))
+    A = D.stable_matrix(g, shape, M, dtype)
+    return A, D.normal(g, (B, M), dtype), D.normal(g, (B, T, M), dtype), D.normal(g, (B, T, M), dtype)
+
+
+def _oracle_n(op, A, zi, x, gy):
+    import oracle
+
+    fwd, bwd = (oracle.recurN, oracle.recurN_bwd) if op == "recurN" else (oracle.lti_recurN, oracle.lti_recurN_bwd)
+    y = fwd(A, zi, x)
+    return [y, *bwd(A, zi, y, gy)]
+
+
+@pytest.mark.parametrize("op,M,B,T,dtype,shared", CASES_N)
+def test_capi_order_n_parity(api, op, M, B, T, dtype, shared):
+    A, zi, x, gy = _case_n(op, M, B, T, dtype, shared, D.seed_of("capi-n", op, M, B, T, np.dtype(dtype).str))
+    _check(_run(api, op, A, zi=zi, x=x, gy=gy, shared=shared, M=M), _oracle_n(op, A, zi, x, gy))
+
+
+@pytest.mark.parametrize("op,M,B,T,dtype,shared", CASES_N[::2])
+def test_capi_order_n_fallback(api, op, M, B, T, dtype, shared):
+    """Order-M scans with a poll budget of 1 (look-back fallback)."""
+    lib = api[0]
+    A, zi, x, gy = _case_n(op, M, B, T, dtype, shared, D.seed_of("capi-n-fb", op, M, B, T, np.dtype(dtype).str))
+    lib.phs_debug_set_spin_limit(1)
+    try:
+        got = _run(api, op, A, zi=zi, x=x, gy=gy, shared=shared, M=M)
+    finally:
+        lib.phs_debug_set_spin_limit(0)
+    _check(got, _oracle_n(op, A, zi, x, gy))
 
 
 def test_capi_workspace_reuse_many_calls(api):

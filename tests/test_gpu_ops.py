@@ -147,6 +147,64 @@ def test_lti_recur2_fwd_bwd(hip, dtype, shape, shared):
         D.check(_n(a), b, name)
 
 
+# ----------------------------------------------------------------- recurN / lti_recurN, M = 3, 4
+SHAPES_N = [(1, 1), (2, 7), (3, 1025), (2, 3001)]
+
+
+@pytest.mark.parametrize("M", [3, 4])
+@pytest.mark.parametrize("dtype", FLOATS)
+@pytest.mark.parametrize("shape", SHAPES_N)
+@pytest.mark.parametrize("shared", [False, True])
+def test_recurN_order_fwd_bwd(hip, M, dtype, shape, shared):
+    import torch
+    import oracle
+
+    B, T = shape
+    g = D.rng(D.seed_of('recurN', M, B, T, shared, np.dtype(dtype).str))
+    A = D.stable_matrix(g, (T,) if shared else (B, T), M, dtype)
+    zi = D.normal(g, (B, M), dtype)
+    x = D.normal(g, (B, T, M), dtype)
+    gy = D.normal(g, (B, T, M), dtype)
+    y_ref = oracle.recurN(A, zi, x)
+    y = torch.ops.philtorch.recurN(_t(A), _t(zi), _t(x))
+    D.check(_n(y), y_ref, "y")
+    ref = oracle.recurN_bwd(A, zi, y_ref, gy)
+    got = torch.ops.philtorch.recurN_backward(_t(A), _t(zi), y, _t(gy))
+    for name, a, b in zip(("grad_A", "grad_zi", "grad_x"), got, ref):
+        D.check(_n(a), b, name)
+
+
+@pytest.mark.parametrize("M", [3, 4])
+@pytest.mark.parametrize("dtype", FLOATS)
+@pytest.mark.parametrize("shape", SHAPES_N)
+@pytest.mark.parametrize("shared", [False, True])
+def test_lti_recurN_order_fwd_bwd(hip, M, dtype, shape, shared):
+    import torch
+    import oracle
+
+    B, T = shape
+    g = D.rng(D.seed_of('lti_recurN', M, B, T, shared, np.dtype(dtype).str))
+    A = D.stable_matrix(g, () if shared else (B,), M, dtype)
+    zi = D.normal(g, (B, M), dtype)
+    x = D.normal(g, (B, T, M), dtype)
+    gy = D.normal(g, (B, T, M), dtype)
+    y_ref = oracle.lti_recurN(A, zi, x)
+    y = torch.ops.philtorch.lti_recurN(_t(A), _t(zi), _t(x))
+    D.check(_n(y), y_ref, "y")
+    ref = oracle.lti_recurN_bwd(A, zi, y_ref, gy)
+    got = torch.ops.philtorch.lti_recurN_backward(_t(A), _t(zi), y, _t(gy))
+    for name, a, b in zip(("grad_A", "grad_zi", "grad_x"), got, ref):
+        D.check(_n(a), b, name)
+
+
+def test_recurN_order_above_native_raises(hip):
+    import torch
+
+    A = torch.zeros(2, 5, 5, 5, device="cuda")
+    with pytest.raises(RuntimeError, match="up to M = 4"):
+        torch.ops.philtorch.recurN(A, torch.zeros(2, 5, device="cuda"), torch.zeros(2, 5, 5, device="cuda"))
+
+
 def test_fibonacci_int64(hip):
     """README known answer (philtorch README.md:143-159) through lti_recur2 in int64."""
     import torch

@@ -22,7 +22,7 @@ def test_capi_exports_every_declared_symbol():
 
 def test_capi_host_only_calls():
     lib = capi.load()
-    assert lib.phs_abi_version() == 100
+    assert lib.phs_abi_version() == 101
     for op in capi.OPS.values():
         for dt in capi.DTYPES.values():
             fwd = lib.phs_workspace_size(op, dt, 64, 65536, 0, 0)
@@ -44,6 +44,62 @@ def test_capi_host_only_calls():
     assert lib.phs_recur_bwd(0, 2, 100, dummy, 0, dummy, None, dummy, dummy, dummy, dummy, dummy, 1 << 20,
                              None) == capi.PHS_ERR_INVALID
     assert lib.phs_recur_fwd(0, 0, 100, None, 0, None, None, None, None, 0, None) == capi.PHS_OK
+
+
+def test_capi_workspace_size_is_exact():
+    """Each entry point accepts exactly the size phs_workspace_size(_n)
+    reports and refuses one byte less.  Runs without a GPU only: with one,
+    the accepted call would launch on dummy pointers."""
+    if torch.cuda.device_count() > 0:
+        pytest.skip("calls entry points with dummy pointers; CPU-only check")
+    lib = capi.load()
+    d = ctypes.c_void_p(16)
+    fixed = [(name, code, None) for name, code in capi.OPS.items()]
+    orders = [(name, code, M) for name, code in capi.OPS_N.items() for M in (1, 2, 3, 4)]
+    for name, code, M in fixed + orders:
+        for dt in capi.DTYPES.values():
+            for shared in (0, 1):
+                for B, T in ((3, 11), (5, 40000)):
+                    order = () if M is None else (M,)
+                    for bw in (0, 1):
+                        if M is None:
+                            n = lib.phs_workspace_size(code, dt, B, T, shared, bw)
+                        else:
+                            n = lib.phs_workspace_size_n(code, dt, M, B, T, shared, bw)
+                        if bw:
+                            call = lambda size: getattr(lib, f"phs_{name}_bwd")(  # noqa: E731
+                                dt, *order, B, T, d, shared, d, d, d, d, d, d, d, size, None)
+                        else:
+                            call = lambda size: getattr(lib, f"phs_{name}_fwd")(  # noqa: E731
+                                dt, *order, B, T, d, shared, d, d, d, d, size, None)
+                        assert call(n - 1) == capi.PHS_ERR_WORKSPACE, (name, M, dt, shared, B, T, bw)
+                        assert call(n) == capi.PHS_ERR_LAUNCH, (name, M, dt, shared, B, T, bw)  # no device here
+
+
+def test_capi_order_n_host_only_calls():
+    lib = capi.load()
+    RECURN, LTI_RECURN = capi.OPS_N["recurN"], capi.OPS_N["lti_recurN"]
+    for dt in capi.DTYPES.values():
+        for bw in (0, 1):
+            # orders 1 and 2 size exactly as the fixed-order ops
+            assert lib.phs_workspace_size_n(RECURN, dt, 1, 8, 5000, 0, bw) == lib.phs_workspace_size(0, dt, 8, 5000, 0, bw)
+            assert lib.phs_workspace_size_n(LTI_RECURN, dt, 2, 8, 5000, 1, bw) == lib.phs_workspace_size(3, dt, 8, 5000, 1, bw)
+            for M in (3, 4):
+                for op in (RECURN, LTI_RECURN):
+                    assert lib.phs_workspace_size_n(op, dt, M, 8, 5000, 0, bw) > 0
+        assert lib.phs_workspace_size_n(RECURN, dt, 5, 8, 5000, 0, 0) == 0
+        assert lib.phs_workspace_size_n(RECURN, dt, 0, 8, 5000, 0, 0) == 0
+    assert lib.phs_workspace_size_n(0, 0, 2, 8, 5000, 0, 0) == 0  # fixed-order op, wrong order
+    assert lib.phs_workspace_size_n(2, 0, 2, 8, 5000, 0, 0) == lib.phs_workspace_size(2, 0, 8, 5000, 0, 0)
+    assert lib.phs_workspace_size_n(RECURN, 0, 3, 0, 5000, 0, 0) == 0
+    dummy = ctypes.c_void_p(16)
+    for M in (0, 5):
+        assert lib.phs_recurN_fwd(0, M, 2, 100, dummy, 0, dummy, dummy, dummy, dummy, 1 << 20, None) == capi.PHS_ERR_INVALID
+        assert lib.phs_lti_recurN_bwd(0, M, 2, 100, dummy, 0, dummy, dummy, dummy, dummy, dummy, dummy, dummy,
+                                      1 << 20, None) == capi.PHS_ERR_INVALID
+    assert lib.phs_recurN_fwd(9, 3, 2, 100, dummy, 0, dummy, dummy, dummy, dummy, 1 << 20, None) == capi.PHS_ERR_DTYPE
+    assert lib.phs_lti_recurN_fwd(0, 4, 2, 100, dummy, 0, dummy, dummy, dummy, None, 0, None) == capi.PHS_ERR_WORKSPACE
+    assert lib.phs_recurN_fwd(0, 3, 0, 100, None, 0, None, None, None, None, 0, None) == capi.PHS_OK
 
 
 # ------------------------------------------------------------ op registration

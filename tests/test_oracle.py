@@ -43,7 +43,10 @@ def _golden_cases():
     return [(str(data[f"{i}_op"]), data[f"{i}_A"], data[f"{i}_zi"], data[f"{i}_x"], data[f"{i}_y"]) for i in range(n)]
 
 
-@pytest.mark.parametrize("case", range(33))
+N_GOLDEN = len([k for k in np.load(GOLDEN).files if k.endswith("_op")])
+
+
+@pytest.mark.parametrize("case", range(N_GOLDEN))
 def test_oracle_matches_reference_golden_vectors(case):
     op, A, zi, x, y = _golden_cases()[case]
     got = _oracle_fwd(op, A, zi, x)
@@ -176,17 +179,20 @@ def _fd_grad(f, v, eps=1e-6):
 
 
 @pytest.mark.parametrize("kind", ["recur", "recur_shared", "lti", "lti_shared", "recurN", "recurN_shared",
-                                  "lti_recurN", "lti_recurN_shared"])
+                                  "lti_recurN", "lti_recurN_shared", "recurN3", "recurN4_shared", "lti_recurN3_shared",
+                                  "lti_recurN4"])
 def test_backward_finite_differences(kind):
     g = D.rng(D.seed_of("fd", kind))
     B, T = 2, 6
+    base = kind.replace("_shared", "")
+    M = int(base[-1]) if base[-1].isdigit() else 2  # matrix order of the recurN / lti_recurN kinds
     if kind.startswith("recurN"):
-        A = g.standard_normal((T, 2, 2) if kind.endswith("shared") else (B, T, 2, 2)) * 0.6
-        zi, x, gy = g.standard_normal((B, 2)), g.standard_normal((B, T, 2)), g.standard_normal((B, T, 2))
+        A = g.standard_normal((T, M, M) if kind.endswith("shared") else (B, T, M, M)) * 0.6 / M ** 0.5
+        zi, x, gy = g.standard_normal((B, M)), g.standard_normal((B, T, M)), g.standard_normal((B, T, M))
         fwd, bwd = oracle.recurN, oracle.recurN_bwd
     elif kind.startswith("lti_recurN"):
-        A = g.standard_normal((2, 2) if kind.endswith("shared") else (B, 2, 2)) * 0.6
-        zi, x, gy = g.standard_normal((B, 2)), g.standard_normal((B, T, 2)), g.standard_normal((B, T, 2))
+        A = g.standard_normal((M, M) if kind.endswith("shared") else (B, M, M)) * 0.6 / M ** 0.5
+        zi, x, gy = g.standard_normal((B, M)), g.standard_normal((B, T, M)), g.standard_normal((B, T, M))
         fwd, bwd = oracle.lti_recurN, oracle.lti_recurN_bwd
     elif kind.startswith("lti"):
         A = g.uniform(-0.9, 0.9, (1,) if kind.endswith("shared") else (B,))
