@@ -166,6 +166,9 @@ struct Scalar {
   static constexpr int kCoefElems = 1;
   static constexpr int kStateElems = 1;
   static constexpr int kVecsPerLane = 2;
+  // LTI scans load no coefficients: complex lanes then carry twice the steps
+  // in the registers the coefficients would take
+  static constexpr int kVecsPerLaneLTI = Num<T>::kComplex ? 4 : 2;
   static constexpr int kRounds = 2;
   // Real scans: 8 data waves that also do the look-back, with a floor of 4
   // waves per SIMD (at most 128 VGPRs): two tiles resident per CU.  Complex
@@ -219,6 +222,7 @@ struct Block2 {
   static constexpr int kCoefElems = 4;
   static constexpr int kStateElems = 2;
   static constexpr int kVecsPerLane = 2;
+  static constexpr int kVecsPerLaneLTI = 4;  // LTI: no per-step coefficients to hold (see Scalar)
   static constexpr int kRounds = 2;
   // 3 data waves plus a look-back wave (see Scalar); real 2x2 scans keep a
   // floor of 3 waves per SIMD (at most 168 VGPRs), complex ones would spill
@@ -321,6 +325,7 @@ struct BlockN {
   static constexpr int kCoefElems = M * M;
   static constexpr int kStateElems = M;
   static constexpr int kVecsPerLane = 1;
+  static constexpr int kVecsPerLaneLTI = 1;
   static constexpr int kRounds = 2;
   // 3 data waves plus a look-back wave, as Block2; no register floor (the
   // maps are large and complex orders would spill under one)

@@ -38,11 +38,11 @@ struct Layout {
 // TV: coefficient varies with time; shared: one coefficient set for all rows.
 template <class Alg>
 Layout make_layout(int64_t B, int64_t T, bool TV, bool shared, bool backward) {
-  using Sh = Shape<Alg>;
+  const int64_t tile = TV ? Shape<Alg, true>::kTile : Shape<Alg, false>::kTile;
   Layout L;
-  L.tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
+  L.tiles_per_row = (T + tile - 1) / tile;
   L.status_off = align_up(kHeaderBytes);
-  L.status_words = size_t(B) * size_t(L.tiles_per_row) * Sh::kStride;
+  L.status_words = size_t(B) * size_t(L.tiles_per_row) * StatusShape<Alg>::kStride;
   size_t off = align_up(L.status_off + L.status_words * sizeof(uint64_t));
   if (backward && !TV) {  // per-tile coefficient-gradient partial sums
     L.partials_off = off;
@@ -80,7 +80,7 @@ inline int64_t resident_groups(const void *kernel, int threads) {
 
 template <class Alg, bool TV, bool REV>
 void launch_scan(const ScanArgs<Alg> &a, unsigned grid, hipStream_t stream) {
-  hipLaunchKernelGGL((scan_kernel<Alg, TV, REV>), dim3(grid), dim3(Shape<Alg>::kThreads), 0, stream, a);
+  hipLaunchKernelGGL((scan_kernel<Alg, TV, REV>), dim3(grid), dim3(Shape<Alg, TV>::kThreads), 0, stream, a);
 }
 
 template <class Alg>
@@ -88,7 +88,6 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
            const void *zi, const void *x, const void *y, void *out, void *gcoef, void *gzi,
            void *workspace, size_t ws_bytes, hipStream_t stream) {
   using E = typename Alg::elem;
-  using Sh = Shape<Alg>;
   if (B < 0 || T < 0) return PHS_ERR_INVALID;
   if (B == 0 || T == 0) return PHS_OK;
   if (!coef || !zi || !x || (backward ? !y : !out)) return PHS_ERR_INVALID;
@@ -137,8 +136,9 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
   // wave can poll for it while the data waves are still loading; with
   // smaller B those early polls mostly fail and only add status traffic.
   a.early_polls = 0;
-  if (Sh::kLookbackWave) {
-    const int64_t resident = resident_groups(kernel, Sh::kThreads);
+  if (Alg::kLookbackWave) {
+    const int threads = TV ? Shape<Alg, true>::kThreads : Shape<Alg, false>::kThreads;
+    const int64_t resident = resident_groups(kernel, threads);
     if (resident > 0 && 2 * B >= resident) a.early_polls = a.spin_limit;
   }
 

@@ -59,25 +59,11 @@ namespace phs {
 
 constexpr size_t gcd16(size_t n) { return n % 16 == 0 ? 16 : n % 8 == 0 ? 8 : n % 4 == 0 ? 4 : n % 2 == 0 ? 2 : 1; }
 
+// Per-tile status record of the look-back: an inclusive prefix and an
+// aggregate map in 64-bit (tag, word) pairs.  Independent of the tile shape.
 template <class Alg>
-struct Shape {
-  static constexpr int kWaves = Alg::kWavesPerBlock;  // data waves
-  static constexpr bool kLookbackWave = Alg::kLookbackWave;
-  static constexpr int kThreads = 64 * (kWaves + (kLookbackWave ? 1 : 0));
-  using state = typename Alg::state;
-  using s_state = typename Alg::s_state;
-  // steps per lane and round: a whole number of 16-byte vectors of stored
-  // states, kVecsPerLane vectors' worth where a state is under 16 bytes
-  static constexpr int kMinSteps = 16 / int(gcd16(sizeof(s_state)));  // smallest K with K*size % 16 == 0
-  static constexpr int K = sizeof(s_state) >= 16 || Alg::kVecsPerLane * 16 < int(kMinSteps * sizeof(s_state))
-                               ? kMinSteps
-                               : Alg::kVecsPerLane * int(16 / sizeof(s_state)) / kMinSteps * kMinSteps;
-  static_assert(K >= 1 && (K * sizeof(s_state)) % 16 == 0, "chunks must be whole 16-byte vectors");
-  static constexpr int R = Alg::kRounds;
-  static constexpr int kWaveSeg = 64 * K * R;
-  static constexpr int kTile = kWaves * kWaveSeg;
-  static_assert(kWaves >= 1 && kWaves <= 16, "1..16 waves per workgroup");
-  static constexpr int kIncWords = sizeof(state) / 4;
+struct StatusShape {
+  static constexpr int kIncWords = sizeof(typename Alg::state) / 4;
   static constexpr int kAggWords = sizeof(Map<Alg>) / 4;
   static constexpr int kStride = kIncWords + kAggWords;  // 64-bit words per tile
   // LDS staging of a 64-tile look-back window: one entry per tile, padded to
@@ -85,6 +71,30 @@ struct Shape {
   // over the banks
   static constexpr int kLookPitch = kStride | 1;
   static constexpr int kLookWords = 64 * kLookPitch;
+};
+
+// Tile shape of one scan mode (TV: per-step coefficients; LTI: one
+// coefficient per row).  LTI scans load no coefficients, so their lanes can
+// carry more steps in the same registers (Alg::kVecsPerLaneLTI).
+template <class Alg, bool TV>
+struct Shape : StatusShape<Alg> {
+  static constexpr int kWaves = Alg::kWavesPerBlock;  // data waves
+  static constexpr bool kLookbackWave = Alg::kLookbackWave;
+  static constexpr int kThreads = 64 * (kWaves + (kLookbackWave ? 1 : 0));
+  using state = typename Alg::state;
+  using s_state = typename Alg::s_state;
+  // steps per lane and round: a whole number of 16-byte vectors of stored
+  // states, kVecs vectors' worth where a state is under 16 bytes
+  static constexpr int kVecs = TV ? Alg::kVecsPerLane : Alg::kVecsPerLaneLTI;
+  static constexpr int kMinSteps = 16 / int(gcd16(sizeof(s_state)));  // smallest K with K*size % 16 == 0
+  static constexpr int K = sizeof(s_state) >= 16 || kVecs * 16 < int(kMinSteps * sizeof(s_state))
+                               ? kMinSteps
+                               : kVecs * int(16 / sizeof(s_state)) / kMinSteps * kMinSteps;
+  static_assert(K >= 1 && (K * sizeof(s_state)) % 16 == 0, "chunks must be whole 16-byte vectors");
+  static constexpr int R = Alg::kRounds;
+  static constexpr int kWaveSeg = 64 * K * R;
+  static constexpr int kTile = kWaves * kWaveSeg;
+  static_assert(kWaves >= 1 && kWaves <= 16, "1..16 waves per workgroup");
 };
 
 template <class Alg>
@@ -204,7 +214,7 @@ __device__ bool lookback_poll(const uint64_t *row_status, const typename Alg::st
                               unsigned tag, uint64_t *s_look, Lookback<Alg> &lb, typename Alg::state &out) {
   using S = typename Alg::state;
   using M = Map<Alg>;
-  using Sh = Shape<Alg>;
+  using Sh = StatusShape<Alg>;
   constexpr int kS = Sh::kStride, kP = Sh::kLookPitch;
   constexpr int kBatch = kS < 8 ? kS : 8;  // words in flight per lane
   while (true) {
@@ -370,7 +380,7 @@ __device__ __noinline__ typename Alg::state row_prefix_fallback(const typename A
   using SC = typename Alg::s_coef;
   using SS = typename Alg::s_state;
   using M = Map<Alg>;
-  constexpr int K = Shape<Alg>::K;
+  constexpr int K = Shape<Alg, TV>::K;
   auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
   const SC zero_sc = Alg::s_czero();
   const SS zero_ss = Alg::s_szero();
@@ -403,7 +413,7 @@ __device__ __forceinline__ void tile_lookback(const ScanArgs<Alg> &a, int64_t qs
   using SC = typename Alg::s_coef;
   using SS = typename Alg::s_state;
   using M = Map<Alg>;
-  using Sh = Shape<Alg>;
+  using Sh = Shape<Alg, TV>;
   constexpr int K = Sh::K, kWaves = Sh::kWaves;
   auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
   M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
@@ -449,12 +459,12 @@ __device__ __forceinline__ void tile_lookback(const ScanArgs<Alg> &a, int64_t qs
 // barriers: claim, wave aggregates ready, entry state ready (and, backward
 // for LTI, the gradient reduction).
 template <class Alg, bool TV, bool REV>
-__global__ __launch_bounds__(Shape<Alg>::kThreads, Alg::kMinWavesPerEU) void scan_kernel(ScanArgs<Alg> a) {
+__global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) void scan_kernel(ScanArgs<Alg> a) {
   using S = typename Alg::state;     // compute type
   using SC = typename Alg::s_coef;   // storage types
   using SS = typename Alg::s_state;
   using M = Map<Alg>;
-  using Sh = Shape<Alg>;
+  using Sh = Shape<Alg, TV>;
   constexpr int K = Sh::K, R = Sh::R, kWaves = Sh::kWaves;
 
   __shared__ M s_wagg[kWaves];
