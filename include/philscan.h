@@ -181,6 +181,44 @@ int phs_lti_recurN_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, in
                        const void *zi, const void *y, const void *grad_y, void *grad_x, void *grad_A,
                        void *grad_zi, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- Cascade of second-order sections (biquads), fused.
+ * No counterpart op in the reference: it replaces the caller pattern of one
+ * philtorch lfilter(form="tdf2") per section (philtorch/lti/filtering.py:
+ * 211-333, each section a philtorch::lti_recur2 with its Bx and C/D glue) by
+ * one pass over all sections.  Semantics of scipy.signal.sosfilt: section s
+ * of row b, sos[.., s, :] = (b0, b1, b2, a0 = 1, a1, a2), transposed direct
+ * form II,
+ *     y[t] = h[t-1].0 + b0 u[t],  h[t] = [[-a1, 1], [-a2, 0]] h[t-1] + (b1 - b0 a1, b2 - b0 a2) u[t],
+ * h[-1] = zi[b, s], zf[b, s] = h[T-1]; section 0 reads x, section s+1 reads
+ * section s's output, y is section S-1's output.  dtype PHS_F32 or PHS_F64;
+ * S = 1..8 per call (a longer cascade is a chain of calls, each over its own
+ * sections); sos: [B,S,6] (sos_shared=0) or [S,6] (sos_shared=1), the a0
+ * entries are not read (callers normalise them to 1); x, y: [B,T];
+ * zi, zf: [B,S,2]. */
+
+/* Workspace bytes of phs_sosfilt_fwd (backward=0) or of either call
+ * (backward!=0); 0 for unsupported arguments. */
+size_t phs_sosfilt_workspace_size(int dtype, int64_t B, int64_t T, int S, int backward);
+
+/* Bytes of the state checkpoints the forward writes for the backward's
+ * coefficient gradients (every 512th step of every section, in fp64). */
+size_t phs_sosfilt_ckpt_size(int dtype, int64_t B, int64_t T, int S);
+
+/* Forward.  zi NULL = zero initial states; zf and ckpt are skipped when NULL.
+ * ckpt (phs_sosfilt_ckpt_size bytes) is required later by the backward when
+ * it computes grad_sos. */
+int phs_sosfilt_fwd(int dtype, int64_t B, int64_t T, int S, const void *sos, int sos_shared, const void *zi,
+                    const void *x, void *y, void *zf, void *ckpt, void *workspace, size_t workspace_bytes,
+                    void *stream);
+
+/* Backward: the adjoint cascade (sections in reverse order, time reversed).
+ * grad_zf NULL = zero.  grad_x [B,T], grad_zi [B,S,2] are skipped when NULL.
+ * grad_sos ([B,S,6], or [S,6] summed over rows when sos_shared; the a0 entries
+ * are 0) needs x and the forward's ckpt; when NULL they are not read. */
+int phs_sosfilt_bwd(int dtype, int64_t B, int64_t T, int S, const void *sos, int sos_shared, const void *x,
+                    const void *ckpt, const void *grad_y, const void *grad_zf, void *grad_x, void *grad_sos,
+                    void *grad_zi, void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

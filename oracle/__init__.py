@@ -152,3 +152,106 @@ def lti_recur_bwd(a, zi, y, gy, nthreads=None):
             _ptr(ga), _ptr(gzi), _ptr(gx), _threads(nthreads))
     assert rc == 0
     return ga, gzi, gx
+
+
+# ------------------------------------------------------------------ SOS cascade
+# philtorch has no cascade op: a cascade of second-order sections is one
+# lfilter(form="tdf2") per section.  Each section is the state-space model
+# _ssm_lfilter builds (philtorch/lti/filtering.py:273-333; companion matrix
+# philtorch/mat.py:42-62) run through state_space with out_idx=0
+# (philtorch/lti/ssm.py:386-510): Bx = x Bv, h = lti_recurN(A, zi, Bx),
+# y = [zi.0, h[:-1].0] + b0 x, zf = h[-1].  The backward is the chain rule of
+# that graph around _lti_recurN_backward (philtorch/__init__.py:76-112).
+def _tdf2_section(sos_s):
+    """(A [R,2,2], Bv [R,2], b0 [R], a [R,2]) of sections sos_s [R,6] with a0 = 1:
+    A = companion(a).mT = [[-a1, 1], [-a2, 0]], Bv = b[1:] - b0 a."""
+    b0, b1, b2, a1, a2 = sos_s[:, 0], sos_s[:, 1], sos_s[:, 2], sos_s[:, 4], sos_s[:, 5]
+    A = np.zeros((sos_s.shape[0], 2, 2), dtype=sos_s.dtype)
+    A[:, 0, 0] = -a1
+    A[:, 0, 1] = 1
+    A[:, 1, 0] = -a2
+    Bv = np.stack([b1 - b0 * a1, b2 - b0 * a2], axis=-1)
+    return A, Bv, b0, np.stack([a1, a2], axis=-1)
+
+
+def _sos_rows(sos, B):
+    """sos [S,6] (shared) or [B,S,6] -> per-row view [B,S,6] and the shared flag."""
+    sos = np.asarray(sos)
+    if sos.ndim == 2:
+        return np.broadcast_to(sos, (B,) + sos.shape), True
+    return sos, False
+
+
+def _sos_section_fwd(A, Bv, b0, zi, u, nthreads):
+    Bx = u[..., None] * Bv[:, None, :]
+    h = lti_recurN(A, zi, Bx, nthreads)
+    y = np.concatenate([zi[:, None, 0], h[:, :-1, 0]], axis=1) + b0[:, None] * u
+    return y, h
+
+
+def sosfilt(sos, x, zi=None, nthreads=None):
+    """Cascade of second-order sections, sos [S,6] or [B,S,6] with a0 = 1;
+    x [B,T]; zi [B,S,2] or None.  Returns (y [B,T], zf [B,S,2])."""
+    dt = np.asarray(x).dtype
+    x = _c(x, dt)
+    B, T = x.shape
+    rows, _ = _sos_rows(_c(sos, dt), B)
+    S = rows.shape[1]
+    zi = np.zeros((B, S, 2), dtype=dt) if zi is None else _c(zi, dt)
+    zf = np.empty((B, S, 2), dtype=dt)
+    u = x
+    for s in range(S):
+        A, Bv, b0, _ = _tdf2_section(_c(rows[:, s], dt))
+        u, h = _sos_section_fwd(A, Bv, b0, _c(zi[:, s], dt), u, nthreads)
+        zf[:, s] = h[:, -1] if T > 0 else zi[:, s]
+    return u, zf
+
+
+def sosfilt_bwd(sos, x, zi, gy, gzf=None, nthreads=None):
+    """Backward of sosfilt for upstream gradients gy [B,T] and gzf [B,S,2]
+    (None = 0).  Returns (grad_sos, grad_zi, grad_x); grad_sos has sos's
+    shape (summed over rows when shared; the a0 column is 0)."""
+    dt = np.asarray(x).dtype
+    x = _c(x, dt)
+    B, T = x.shape
+    rows, shared = _sos_rows(_c(sos, dt), B)
+    S = rows.shape[1]
+    zi = np.zeros((B, S, 2), dtype=dt) if zi is None else _c(zi, dt)
+    gzf = np.zeros((B, S, 2), dtype=dt) if gzf is None else _c(gzf, dt)
+    secs, ins, hs = [], [], []
+    u = x
+    for s in range(S):
+        sec = _tdf2_section(_c(rows[:, s], dt))
+        ins.append(u)
+        u, h = _sos_section_fwd(*sec[:3], _c(zi[:, s], dt), u, nthreads)
+        secs.append(sec)
+        hs.append(h)
+    g = _c(gy, dt)
+    gsos = np.zeros((B, S, 6), dtype=dt)
+    gzi = np.zeros((B, S, 2), dtype=dt)
+    for s in reversed(range(S)):
+        A, Bv, b0, a = secs[s]
+        u, h = ins[s], hs[s]
+        # y = shift(h).0 + b0 u
+        gh = np.zeros_like(h)
+        gh[:, :-1, 0] = g[:, 1:]
+        gh[:, -1] += gzf[:, s]
+        gzi_s = np.zeros((B, 2), dtype=dt)
+        gzi_s[:, 0] = g[:, 0]
+        gb0 = np.sum(g * u, axis=1)
+        gu = b0[:, None] * g
+        gA, gz, gBx = lti_recurN_bwd(A, _c(zi[:, s], dt), h, gh, nthreads)
+        gzi_s += gz
+        gu = gu + np.sum(gBx * Bv[:, None, :], axis=-1)
+        gBv = np.sum(gBx * u[..., None], axis=1)
+        # Bv = b[1:] - b0 a;  A = [[-a1, 1], [-a2, 0]]
+        gsos[:, s, 0] = gb0 - np.sum(a * gBv, axis=-1)
+        gsos[:, s, 1] = gBv[:, 0]
+        gsos[:, s, 2] = gBv[:, 1]
+        gsos[:, s, 4] = -gA[:, 0, 0] - b0 * gBv[:, 0]
+        gsos[:, s, 5] = -gA[:, 1, 0] - b0 * gBv[:, 1]
+        gzi[:, s] = gzi_s
+        g = gu
+    if shared:
+        gsos = gsos.sum(axis=0)
+    return gsos, gzi, g

@@ -4,7 +4,9 @@ Importing the package loads ``_C.so`` (the torch.library layer over the HIP
 kernels of ``libphilscan.so``), which defines the ``philtorch`` operator
 namespace: the reference's five ops (``recur2``, ``recurN``, ``lti_recur2``,
 ``lti_recurN``, ``lti_recur``; philtorch/csrc/host_recur2.cpp:162-171), the new
-LPV scalar op ``recur`` and four fused backward ops.  This module then
+LPV scalar op ``recur``, four fused backward ops, and the fused cascade of
+second-order sections ``sosfilt`` / ``sosfilt_backward`` (no reference
+counterpart; ``lti.sosfilt`` is its API).  This module then
 registers fake (meta) kernels and autograd formulas for them, as
 philtorch/__init__.py:157-268 does for its ops.
 
@@ -248,6 +250,52 @@ if EXTENSION_LOADED:
         torch.library.register_autograd(
             f"philtorch::{_op}", _make_backward(_fused, _comp), setup_context=_setup_context
         )
+
+
+def _has_op(name: str) -> bool:
+    try:
+        getattr(torch.ops.philtorch, name)
+        return True
+    except (AttributeError, RuntimeError):
+        return False
+
+
+# (a _C.so built before the cascade ops existed lacks them; the in-tree build
+# imports this package before it rebuilds that library)
+if EXTENSION_LOADED and _has_op("sosfilt"):
+    # fused cascade of second-order sections: (y, zf, ckpt); ckpt holds the
+    # forward's state checkpoints (every 512th step, fp64) for the backward
+    @torch.library.register_fake("philtorch::sosfilt")
+    def _(sos, zi, x):
+        torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
+        torch._check(sos.ndim in (2, 3) and sos.shape[-1] == 6, lambda: "sos must be (sections, 6) or (batch, sections, 6)")
+        torch._check(1 <= sos.shape[-2] <= 8, lambda: "1 to 8 sections per call")
+        if sos.ndim == 3:
+            torch._check(sos.shape[0] == x.shape[0], lambda: "a 3D sos must have x's batch size")
+        B, T, S = x.shape[0], x.shape[1], sos.shape[-2]
+        if zi is not None:
+            torch._check(tuple(zi.shape) == (B, S, 2), lambda: "zi must be (batch, sections, 2)")
+        return (_fake_like(x), x.new_empty((B, S, 2)), x.new_empty((B, S, (T + 511) // 512, 2), dtype=torch.float64))
+
+    @torch.library.register_fake("philtorch::sosfilt_backward")
+    def _(sos, x, ckpt, grad_y, grad_zf, need_sos):
+        return _fake_like(x), sos.new_empty(sos.shape), x.new_empty((x.shape[0], sos.shape[-2], 2))
+
+    def _sosfilt_setup(ctx, inputs, output):
+        sos, zi, x = inputs
+        ctx.save_for_backward(sos, x, output[2])
+        ctx.has_zi = zi is not None
+
+    def _sosfilt_backward(ctx, gy, gzf, _gckpt):
+        sos, x, ckpt = ctx.saved_tensors
+        need_sos = bool(ctx.needs_input_grad[0])
+        if gy is None:
+            gy = torch.zeros_like(x)
+        gx, gsos, gzi = torch.ops.philtorch.sosfilt_backward(sos, x, ckpt, gy, gzf, need_sos)
+        needs = ctx.needs_input_grad
+        return (gsos if needs[0] else None, gzi if ctx.has_zi and needs[1] else None, gx if needs[2] else None)
+
+    torch.library.register_autograd("philtorch::sosfilt", _sosfilt_backward, setup_context=_sosfilt_setup)
 
 from . import mat  # noqa: E402,F401
 from . import lti  # noqa: E402,F401

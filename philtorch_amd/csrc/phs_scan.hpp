@@ -414,7 +414,7 @@ __device__ __forceinline__ void tile_lookback(const ScanArgs<Alg> &a, int64_t qs
   using SS = typename Alg::s_state;
   using M = Map<Alg>;
   using Sh = Shape<Alg, TV>;
-  constexpr int K = Sh::K, kWaves = Sh::kWaves;
+  constexpr int kWaves = Sh::kWaves;
   auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
   M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
   v = wave_scan_incl(v, lane, op);

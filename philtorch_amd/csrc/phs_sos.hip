@@ -1,0 +1,179 @@
+// C ABI of the fused second-order-section cascade (declared in
+// include/philscan.h): argument checks, workspace carving and the launches of
+// sos_kernel [-> sos_grad_reduce_kernel] on the caller's stream.  No
+// allocation and no synchronisation.
+// Workspace layout: [0, 2048) claim header, then the status words of every
+// (row, section, tile), then (gradient backward only) per-tile, per-wave
+// coefficient sums.
+#include "phs_launch.hpp"
+#include "phs_sos.hpp"
+
+namespace phs {
+namespace {
+
+// Forward tiles carry four 16-byte vectors per lane and round; the gradient
+// backward keeps four arrays of a lane's steps live, so it takes two.
+template <typename E>
+using SosFwd = SosShape<E, int(64 / sizeof(E)), 2>;
+template <typename E>
+using SosBwd = SosShape<E, int(32 / sizeof(E)), 2>;
+
+struct SosLayout {
+  int64_t tiles_per_row = 0;
+  size_t status_off = 0, partials_off = 0, total = 0;
+};
+
+template <typename E, class Sh>
+SosLayout sos_layout(int64_t B, int64_t T, int S, bool grad) {
+  using Alg = Block2<E>;
+  SosLayout L;
+  L.tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
+  L.status_off = align_up(kHeaderBytes);
+  const size_t words = size_t(B) * size_t(S) * size_t(L.tiles_per_row) * StatusShape<Alg>::kStride;
+  size_t off = align_up(L.status_off + words * sizeof(uint64_t));
+  if (grad) {
+    L.partials_off = off;
+    off = align_up(off + size_t(B) * size_t(S) * size_t(L.tiles_per_row) * Sh::kWaves * 5 *
+                             sizeof(typename Wide<E>::type));
+  }
+  L.total = off;
+  return L;
+}
+
+inline int64_t n_ckpt(int64_t T) { return (T + kSosCkpt - 1) / kSosCkpt; }
+
+template <typename E>
+size_t ws_bytes_for(int64_t B, int64_t T, int S, bool backward) {
+  const size_t f = sos_layout<E, SosFwd<E>>(B, T, S, false).total;
+  if (!backward) return f;
+  return std::max(f, sos_layout<E, SosBwd<E>>(B, T, S, true).total);
+}
+
+bool sizes_ok(int64_t B, int64_t T, int S) { return B >= 0 && T >= 0 && S >= 1 && S <= kSosMaxSections; }
+
+template <typename E, class Sh>
+void fill_common(SosArgs<E> &a, const SosLayout &L, int64_t B, int64_t T, int S, const void *sos, bool shared,
+                 char *ws) {
+  a.sos = static_cast<const E *>(sos);
+  a.sos_row_stride = shared ? 0 : int64_t(S) * 6;
+  a.B = B;
+  a.T_len = T;
+  a.tiles_per_row = L.tiles_per_row;
+  a.n_ckpt = n_ckpt(T);
+  a.S = S;
+  a.claims = reinterpret_cast<unsigned long long *>(ws);
+  a.status = reinterpret_cast<uint64_t *>(ws + L.status_off);
+  a.tiles = unsigned(B * L.tiles_per_row);
+  a.per_stripe = (a.tiles + kStripes - 1) / kStripes;
+  const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
+  a.spin_limit = sl ? sl : kDefaultSpinLimit;
+}
+
+template <typename E>
+int sos_fwd(int64_t B, int64_t T, int S, const void *sos, bool shared, const void *zi, const void *x, void *y,
+            void *zf, void *ckpt, void *workspace, size_t ws_bytes, hipStream_t stream) {
+  using Sh = SosFwd<E>;
+  if (!sizes_ok(B, T, S)) return PHS_ERR_INVALID;
+  if (B == 0 || T == 0) return PHS_OK;
+  if (!sos || !x || !y) return PHS_ERR_INVALID;
+  const SosLayout L = sos_layout<E, Sh>(B, T, S, false);
+  if (double(B) * double(L.tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
+  if (!workspace || ws_bytes < L.total) return PHS_ERR_WORKSPACE;
+  SosArgs<E> a{};
+  fill_common<E, Sh>(a, L, B, T, S, sos, shared, static_cast<char *>(workspace));
+  a.in = static_cast<const E *>(x);
+  a.out = static_cast<E *>(y);
+  a.virt = static_cast<const E *>(zi);
+  a.fin = static_cast<E *>(zf);
+  a.ckpt = static_cast<Vec2<typename Wide<E>::type> *>(ckpt);
+  a.vec_ok = (size_t(T) * sizeof(E)) % 16 == 0 && aligned16(x) && aligned16(y);
+  const unsigned grid = a.per_stripe * kStripes;
+  hipLaunchKernelGGL((sos_kernel<E, Sh, false, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
+  return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
+}
+
+template <typename E>
+int sos_bwd(int64_t B, int64_t T, int S, const void *sos, bool shared, const void *x, const void *ckpt,
+            const void *gy, const void *gzf, void *gx, void *gsos, void *gzi, void *workspace, size_t ws_bytes,
+            hipStream_t stream) {
+  using Sh = SosBwd<E>;
+  if (!sizes_ok(B, T, S)) return PHS_ERR_INVALID;
+  if (B == 0 || T == 0) return PHS_OK;
+  const bool grad = gsos != nullptr;
+  if (!sos || !gy || (grad && (!x || !ckpt))) return PHS_ERR_INVALID;
+  const SosLayout L = sos_layout<E, Sh>(B, T, S, grad);
+  if (double(B) * double(L.tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
+  if (!workspace || ws_bytes < L.total) return PHS_ERR_WORKSPACE;
+  char *ws = static_cast<char *>(workspace);
+  SosArgs<E> a{};
+  fill_common<E, Sh>(a, L, B, T, S, sos, shared, ws);
+  a.in = static_cast<const E *>(gy);
+  a.out = static_cast<E *>(gx);
+  a.virt = static_cast<const E *>(gzf);
+  a.fin = static_cast<E *>(gzi);
+  a.ckpt = const_cast<Vec2<typename Wide<E>::type> *>(static_cast<const Vec2<typename Wide<E>::type> *>(ckpt));
+  a.x = static_cast<const E *>(x);
+  a.partials = grad ? reinterpret_cast<typename Wide<E>::type *>(ws + L.partials_off) : nullptr;
+  a.vec_ok = (size_t(T) * sizeof(E)) % 16 == 0 && aligned16(gy) && aligned16(gx) && (!grad || aligned16(x));
+  const unsigned grid = a.per_stripe * kStripes;
+  if (grad) {
+    const size_t lds = size_t(S) * Sh::kWaves * Sh::R * 64 * sizeof(Vec2<E>);
+    hipLaunchKernelGGL((sos_kernel<E, Sh, true, true>), dim3(grid), dim3(Sh::kThreads), lds, stream, a);
+    if (hipGetLastError() != hipSuccess) return PHS_ERR_LAUNCH;
+    const int64_t rows = shared ? 1 : B;
+    hipLaunchKernelGGL((sos_grad_reduce_kernel<E, Sh>), dim3(unsigned(rows * S)), dim3(kSosReduceThreads), 0,
+                       stream, a, static_cast<E *>(gsos), rows);
+  } else {
+    hipLaunchKernelGGL((sos_kernel<E, Sh, true, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
+  }
+  return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
+}
+
+}  // namespace
+}  // namespace phs
+
+extern "C" {
+
+size_t phs_sosfilt_workspace_size(int dtype, int64_t B, int64_t T, int S, int backward) {
+  if (!phs::sizes_ok(B, T, S)) return 0;
+  switch (dtype) {
+    case PHS_F32: return phs::ws_bytes_for<float>(B, T, S, backward != 0);
+    case PHS_F64: return phs::ws_bytes_for<double>(B, T, S, backward != 0);
+    default: return 0;
+  }
+}
+
+size_t phs_sosfilt_ckpt_size(int dtype, int64_t B, int64_t T, int S) {
+  if (!phs::sizes_ok(B, T, S) || (dtype != PHS_F32 && dtype != PHS_F64)) return 0;
+  return size_t(B) * size_t(S) * size_t(phs::n_ckpt(T)) * 2 * sizeof(double);
+}
+
+int phs_sosfilt_fwd(int dtype, int64_t B, int64_t T, int S, const void *sos, int sos_shared, const void *zi,
+                    const void *x, void *y, void *zf, void *ckpt, void *workspace, size_t workspace_bytes,
+                    void *stream) {
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case PHS_F32:
+      return phs::sos_fwd<float>(B, T, S, sos, sos_shared != 0, zi, x, y, zf, ckpt, workspace, workspace_bytes, st);
+    case PHS_F64:
+      return phs::sos_fwd<double>(B, T, S, sos, sos_shared != 0, zi, x, y, zf, ckpt, workspace, workspace_bytes, st);
+    default: return PHS_ERR_DTYPE;
+  }
+}
+
+int phs_sosfilt_bwd(int dtype, int64_t B, int64_t T, int S, const void *sos, int sos_shared, const void *x,
+                    const void *ckpt, const void *grad_y, const void *grad_zf, void *grad_x, void *grad_sos,
+                    void *grad_zi, void *workspace, size_t workspace_bytes, void *stream) {
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case PHS_F32:
+      return phs::sos_bwd<float>(B, T, S, sos, sos_shared != 0, x, ckpt, grad_y, grad_zf, grad_x, grad_sos,
+                                 grad_zi, workspace, workspace_bytes, st);
+    case PHS_F64:
+      return phs::sos_bwd<double>(B, T, S, sos, sos_shared != 0, x, ckpt, grad_y, grad_zf, grad_x, grad_sos,
+                                  grad_zi, workspace, workspace_bytes, st);
+    default: return PHS_ERR_DTYPE;
+  }
+}
+
+}  // extern "C"

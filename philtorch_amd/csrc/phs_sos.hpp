@@ -1,0 +1,691 @@
+// Fused cascade of second-order sections (biquads), forward and adjoint, in
+// one single-pass kernel per direction, for gfx950.
+//
+// Section s of row b has coefficients (b0, b1, b2, a1, a2) (a0 = 1) and runs
+// the transposed direct form II of philtorch's lfilter(form="tdf2")
+// (philtorch/lti/filtering.py:273-333 building state_space, lti/ssm.py:386-510):
+//   y[t] = h[t-1].0 + b0 u[t],     h[t] = A h[t-1] + c u[t],
+//   A = [[-a1, 1], [-a2, 0]],      c = (b1 - b0 a1, b2 - b0 a2),
+// with h[-1] = zi[b, s] and zf[b, s] = h[T-1]; section s+1 filters section s's
+// output.  The adjoint of the cascade is the transposed cascade, run backwards
+// in time with the sections in reverse order:
+//   mu[t] = A^T mu[t+1] + e0 g[t],   gu[t] = c . mu[t+1] + b0 g[t],
+// where mu[t+1] = dL/dh[t], mu[T] = dL/dzf and mu[0] = dL/dzi.  It needs no
+// forward values, so one kernel template serves both directions.
+// Coefficient gradients pair mu with the forward input u and state h, which
+// the backward recomputes inside its tile from x and the states the forward
+// kernel checkpoints every kSosCkpt steps.
+//
+// Per tile and section (tile layout as in phs_scan.hpp: data waves own
+// contiguous segments of R rounds of 64*K steps; the backward mirrors waves,
+// rounds and lanes in memory so that scan order is always ascending):
+//   * pass 1: each lane folds its K steps from a zero state into the vector
+//     part of an affine map; the matrix part is A^K for every lane, so a wave
+//     scan of vector parts alone (DPP row shifts with the uniform multipliers
+//     A^(K 2^j) inside 16-lane rows, then row totals with per-lane powers
+//     of A^K computed once per section) gives each lane's exclusive prefix;
+//   * the look-back wave combines the wave aggregates, publishes the tile's
+//     aggregate of this section and resolves the section's entry state by
+//     decoupled look-back over that section's own status row (the protocol,
+//     tags and fallback of phs_scan.hpp);
+//   * pass 2: every lane re-runs its steps from its exact entry state, and the
+//     outputs replace the inputs in registers for the next section.
+// Tile q's section s waits on tile q-1's section s, which in turn only needs
+// tile q-1's sections below s: the dependence is a wavefront S sections deep,
+// not a chain along the row.
+#pragma once
+
+#include "phs_scan.hpp"
+
+namespace phs {
+
+constexpr int kSosCkpt = 512;          // steps between forward state checkpoints
+constexpr int kSosMaxSections = 8;     // sections per launch (LDS of the gradient backward)
+
+// Tile shape: W data waves plus one look-back wave; K steps per lane and
+// round (a power of two dividing kSosCkpt), R rounds (1 or 2).
+template <typename E, int K_, int R_>
+struct SosShape {
+  static constexpr int kWaves = 3;
+  static constexpr int kThreads = 64 * (kWaves + 1);
+  static constexpr int K = K_;
+  static constexpr int R = R_;
+  static constexpr int kWaveSeg = 64 * K * R;
+  static constexpr int kTile = kWaves * kWaveSeg;
+  // multipliers A^(K 2^j), j = 0..5 for the wave scan, 6 for a round, and
+  // the last one for a whole wave segment (A^(64 K R))
+  static constexpr int kPowers = R == 1 ? 7 : 8;
+  static_assert(R == 1 || R == 2, "one or two rounds");
+  static_assert((K & (K - 1)) == 0 && kSosCkpt % K == 0, "K must be a power of two dividing kSosCkpt");
+  static_assert(kTile % kSosCkpt == 0, "tiles start on checkpoints");
+  static_assert((K * sizeof(E)) % 16 == 0, "chunks must be whole 16-byte vectors");
+};
+
+template <typename E>
+struct SosArgs {
+  using C = typename Wide<E>::type;
+  const E *sos;            // [rows, S, 6]: b0 b1 b2 a0 a1 a2 (a0 = 1)
+  int64_t sos_row_stride;  // elements between rows (0 = one set for all rows)
+  const E *in;             // forward: x;  backward: grad of y
+  E *out;                  // forward: y;  backward: grad of x (nullable)
+  const E *virt;           // forward: zi;  backward: grad of zf  ([B, S, 2], nullable = zeros)
+  E *fin;                  // forward: zf;  backward: grad of zi  ([B, S, 2], nullable)
+  Vec2<C> *ckpt;           // [B, S, n_ckpt] states entering every kSosCkpt-th step:
+                           // written forward (nullable), read by the gradient backward
+  const E *x;              // gradient backward: the forward input
+  C *partials;             // gradient backward: [B, S, tiles, kWaves, 5] coefficient sums
+  int64_t B, T_len, tiles_per_row, n_ckpt;
+  int S;
+  unsigned long long *claims;  // kStripes claim words (workspace offset 0)
+  unsigned tiles;              // B * tiles_per_row
+  unsigned per_stripe;         // claims per stripe (grid = per_stripe * kStripes)
+  unsigned spin_limit;         // look-back polls before the self-compute fallback
+  uint64_t *status;            // [B, S, tiles, kStride] status words of this call
+  int vec_ok;
+};
+
+// One section, in the form the steps use.
+template <typename E>
+struct SosSec {
+  E b0, c0, c1, na1, na2;  // c = b[1:] - b0 a;  na = -a
+};
+
+template <typename E>
+__device__ __forceinline__ SosSec<E> load_sec(const E *row, int s) {
+  const E *p = row + 6 * s;
+  const E b0 = p[0], b1 = p[1], b2 = p[2], a1 = p[4], a2 = p[5];
+  return {b0, b1 - b0 * a1, b2 - b0 * a2, -a1, -a2};
+}
+
+// Section matrix in compute precision: A forward, A^T for the adjoint.
+template <typename E, bool REV>
+__device__ __forceinline__ Mat2<typename Wide<E>::type> sec_matrix(const SosSec<E> &q) {
+  using C = typename Wide<E>::type;
+  const C one = C(1), zero = C(0);
+  if constexpr (REV)
+    return {up(q.na1), up(q.na2), one, zero};
+  else
+    return {up(q.na1), one, up(q.na2), zero};
+}
+
+// P[0] = A^K, P[j] = A^(K 2^j).
+template <typename E, int K, int NP>
+__device__ __forceinline__ void sec_powers(const Mat2<typename Wide<E>::type> &A,
+                                           Mat2<typename Wide<E>::type> (&P)[NP]) {
+  using Alg = Block2<E>;
+  Mat2<typename Wide<E>::type> m = A;
+#pragma unroll
+  for (int k = 1; k < K; k <<= 1) m = Alg::cmul(m, m);
+  P[0] = m;
+#pragma unroll
+  for (int j = 1; j < NP; ++j) P[j] = Alg::cmul(P[j - 1], P[j - 1]);
+}
+
+// A^(K cnt) for cnt in [0, 64), from P (powers of one matrix commute).
+template <typename E, int NP>
+__device__ __forceinline__ Mat2<typename Wide<E>::type> lane_power(const Mat2<typename Wide<E>::type> (&P)[NP],
+                                                                   int cnt) {
+  using Alg = Block2<E>;
+  Mat2<typename Wide<E>::type> r = Alg::cone();
+#pragma unroll
+  for (int j = 0; j < 6; ++j)
+    if ((cnt >> j) & 1) r = Alg::cmul(P[j], r);
+  return r;
+}
+
+constexpr int kDppRowShl1 = 0x101, kDppRowShl2 = 0x102, kDppRowShl4 = 0x104, kDppRowShl8 = 0x108;
+constexpr int kDppWaveShl1 = 0x130;
+
+// Per-lane multipliers of the two cross-row steps of lti_scan (computed once
+// per section): after the in-row steps a lane at row position r holds its
+// row's prefix up to itself (UP) or its suffix from itself (!UP); the row
+// total it then adds sits n = r+1 (UP) or 16-r (!UP) lanes away, and in the
+// second step n or n+16 lanes away.
+template <typename C>
+struct RowMul {
+  Mat2<C> q1, q2;
+};
+
+template <bool UP, typename E, int NP>
+__device__ __forceinline__ RowMul<typename Wide<E>::type> row_mul(const Mat2<typename Wide<E>::type> (&P)[NP],
+                                                                 int lane) {
+  using Alg = Block2<E>;
+  const int r = lane & 15;
+  const Mat2<typename Wide<E>::type> q1 = lane_power<E, NP>(P, UP ? r + 1 : 16 - r);
+  const bool far = UP ? (lane & 16) != 0 : (lane & 16) == 0;
+  return {q1, far ? Alg::cmul(P[4], q1) : q1};
+}
+
+// Inclusive scan of the vector parts of maps (P[0], v) over the wave, lane 0
+// first (UP) or lane 63 first (!UP): v_i <- v_i + A^(K d) v_(i -+ d) for
+// d = 1, 2, 4, 8 inside each 16-lane row (DPP row shifts), then the total of
+// the preceding row (rows 1 and 3 from rows 0 and 2), then that of the
+// preceding pair of rows, each times the lane's own power from `mul` (UP:
+// DPP row_bcast 15/31; !UP: the mirrored lanes through bpermute).
+template <bool UP, typename C, int NP>
+__device__ __forceinline__ Vec2<C> lti_scan(Vec2<C> v, int lane, const Mat2<C> (&P)[NP], const RowMul<C> &mul) {
+  using V = Vec2<C>;
+  auto step = [](const Mat2<C> &A, const V &o, const V &x) -> V {
+    return {mad(A.m00, o.v0, mad(A.m01, o.v1, x.v0)), mad(A.m10, o.v0, mad(A.m11, o.v1, x.v1))};
+  };
+  const int r = lane & 15;
+  V o;
+  o = dpp_move<UP ? kDppRowShr1 : kDppRowShl1, 0xF>(v);
+  if (UP ? r >= 1 : r <= 14) v = step(P[0], o, v);
+  o = dpp_move<UP ? kDppRowShr2 : kDppRowShl2, 0xF>(v);
+  if (UP ? r >= 2 : r <= 13) v = step(P[1], o, v);
+  o = dpp_move<UP ? kDppRowShr4 : kDppRowShl4, 0xF>(v);
+  if (UP ? r >= 4 : r <= 11) v = step(P[2], o, v);
+  o = dpp_move<UP ? kDppRowShr8 : kDppRowShl8, 0xF>(v);
+  if (UP ? r >= 8 : r <= 7) v = step(P[3], o, v);
+  if constexpr (UP) {
+    o = dpp_move<kDppRowBcast15, 0xA>(v);
+    if (lane & 16) v = step(mul.q1, o, v);
+    o = dpp_move<kDppRowBcast31, 0xC>(v);
+    if (lane >= 32) v = step(mul.q2, o, v);
+  } else {
+    o = shfl_from(v, ((lane | 15) + 1) & 63);
+    if ((lane & 16) == 0) v = step(mul.q1, o, v);
+    o = shfl_from(v, 32);
+    if (lane < 32) v = step(mul.q2, o, v);
+  }
+  return v;
+}
+
+// Value of the previous lane in scan order (the first lane gets `first`).
+template <bool UP, typename X>
+__device__ __forceinline__ X lane_prev(const X &v, int lane, const X &first) {
+  X o = dpp_move<UP ? kDppWaveShr1 : kDppWaveShl1, 0xF>(v);
+  return (UP ? lane == 0 : lane == 63) ? first : o;
+}
+
+// ------------------------------------------------------------ lane steps
+// Forward fold of steps [t0, t0+K) from a zero state (pass 1).  Steps past the
+// row end read zero inputs and follow every valid step: they only change
+// states nobody reads.
+template <typename E, int K>
+__device__ __forceinline__ Vec2<typename Wide<E>::type> fold_fwd(const SosSec<E> &q, const E (&u)[K]) {
+  E v0 = E(0), v1 = E(0);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const E x = u[k];
+    const E n0 = fma(q.na1, v0, fma(q.c0, x, v1));
+    v1 = fma(q.na2, v0, q.c1 * x);
+    v0 = n0;
+  }
+  return {up(v0), up(v1)};
+}
+
+// Forward run of steps [t0, t0+K) from state h (pass 2): outputs replace the
+// inputs, zero past the row end; zf (nullable) receives h[T-1].
+template <typename E, int K>
+__device__ __forceinline__ void run_fwd(const SosSec<E> &q, Vec2<E> h, E (&u)[K], int64_t t0, int64_t T, E *zf) {
+  if (t0 + K <= T) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const E x = u[k];
+      u[k] = fma(q.b0, x, h.v0);
+      const E n0 = fma(q.na1, h.v0, fma(q.c0, x, h.v1));
+      h.v1 = fma(q.na2, h.v0, q.c1 * x);
+      h.v0 = n0;
+    }
+    if (zf && t0 + K == T) {
+      zf[0] = h.v0;
+      zf[1] = h.v1;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const E x = u[k];
+      if (t0 + k < T) {
+        u[k] = fma(q.b0, x, h.v0);
+        const E n0 = fma(q.na1, h.v0, fma(q.c0, x, h.v1));
+        h.v1 = fma(q.na2, h.v0, q.c1 * x);
+        h.v0 = n0;
+        if (zf && t0 + k == T - 1) {
+          zf[0] = h.v0;
+          zf[1] = h.v1;
+        }
+      } else {
+        u[k] = E(0);
+      }
+    }
+  }
+}
+
+// Adjoint fold of steps t0+K-1 down to t0 from a zero state.  Past the row end
+// the gradient is zero; the step at t = T (present when the row does not end on
+// a tile boundary) injects dL/dzf, so that mu[T] = dL/dzf exactly.
+template <typename E, int K>
+__device__ __forceinline__ Vec2<typename Wide<E>::type> fold_adj(const SosSec<E> &q, const E (&g)[K], int64_t t0,
+                                                                 int64_t T, const Vec2<E> &gzf) {
+  E m0 = E(0), m1 = E(0);
+  if (t0 + K <= T) {
+#pragma unroll
+    for (int kk = 0; kk < K; ++kk) {
+      const int k = K - 1 - kk;
+      const E n0 = fma(q.na1, m0, fma(q.na2, m1, g[k]));
+      m1 = m0;
+      m0 = n0;
+    }
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < K; ++kk) {
+      const int k = K - 1 - kk;
+      const int64_t t = t0 + k;
+      if (t < T) {
+        const E n0 = fma(q.na1, m0, fma(q.na2, m1, g[k]));
+        m1 = m0;
+        m0 = n0;
+      } else if (t == T) {
+        m0 = gzf.v0;
+        m1 = gzf.v1;
+      }
+    }
+  }
+  return {up(m0), up(m1)};
+}
+
+// Coefficient-gradient sums of one section (per lane, then per wave):
+// a1: sum mu0 h0,  a2: sum mu1 h0,  c0: sum mu0 u,  c1: sum mu1 u,  b0: sum g u,
+// with mu = mu[t+1] = dL/dh[t], h0 = h[t-1].0 = y[t] - b0 u[t].
+template <typename C>
+struct SosAcc {
+  C a1, a2, c0, c1, b0;
+};
+
+// Adjoint run of steps t0+K-1 down to t0 from mu (pass 2): grad of the
+// section input replaces g (zero past the row end); gzi (nullable) receives
+// mu[0].  With GRAD, u/y are the forward input and output of the section and
+// the sums go to acc.
+template <typename E, int K, bool GRAD>
+__device__ __forceinline__ void run_adj(const SosSec<E> &q, Vec2<E> mu, E (&g)[K], int64_t t0, int64_t T,
+                                        const Vec2<E> &gzf, E *gzi, const E (&u)[GRAD ? K : 1],
+                                        const E (&y)[GRAD ? K : 1], SosAcc<E> &acc) {
+  auto step = [&](int k) {
+    const E gk = g[k];
+    if constexpr (GRAD) {
+      const E uk = u[k];
+      const E h0 = fma(-q.b0, uk, y[k]);
+      acc.a1 = fma(mu.v0, h0, acc.a1);
+      acc.a2 = fma(mu.v1, h0, acc.a2);
+      acc.c0 = fma(mu.v0, uk, acc.c0);
+      acc.c1 = fma(mu.v1, uk, acc.c1);
+      acc.b0 = fma(gk, uk, acc.b0);
+    }
+    g[k] = fma(q.c0, mu.v0, fma(q.c1, mu.v1, q.b0 * gk));
+    const E n0 = fma(q.na1, mu.v0, fma(q.na2, mu.v1, gk));
+    mu.v1 = mu.v0;
+    mu.v0 = n0;
+  };
+  if (t0 + K <= T) {
+#pragma unroll
+    for (int kk = 0; kk < K; ++kk) step(K - 1 - kk);
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < K; ++kk) {
+      const int k = K - 1 - kk;
+      const int64_t t = t0 + k;
+      if (t < T) {
+        step(k);
+      } else {
+        if (t == T) mu = gzf;
+        g[k] = E(0);
+      }
+    }
+  }
+  if (gzi && t0 == 0) {
+    gzi[0] = mu.v0;
+    gzi[1] = mu.v1;
+  }
+}
+
+template <typename E>
+__device__ __forceinline__ Vec2<E> load_pair(const E *p, bool valid) {
+  return valid ? Vec2<E>{p[0], p[1]} : Vec2<E>{E(0), E(0)};
+}
+
+// ------------------------------------------------------------ look-back fallback
+// State entering scan positions [span, ...) of section s_target in row b,
+// computed by one wave straight from the inputs: the cascade (forward) or the
+// adjoint cascade (REV) over the whole row prefix in scan order, 64*K steps
+// per iteration, every section up to s_target carrying its state across
+// iterations in LDS (`carry`, one entry per section).  Taken only when
+// predecessors did not publish within the poll budget.
+template <typename E, class Sh, bool REV>
+__device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const SosArgs<E> &a, int64_t b,
+                                                                        int s_target, int64_t span, int lane,
+                                                                        Vec2<typename Wide<E>::type> *carry) {
+  using Alg = Block2<E>;
+  using C = typename Wide<E>::type;
+  using V = Vec2<C>;
+  using Mt = Mat2<C>;
+  constexpr int K = Sh::K, NP = Sh::kPowers;
+  const int S = a.S;
+  const int64_t T = a.T_len;
+  const int64_t row_end = a.tiles_per_row * Sh::kTile;
+  const int n = REV ? S - s_target : s_target + 1;  // sections in processing order
+  const E *sosrow = a.sos + b * a.sos_row_stride;
+  const E *inrow = a.in + b * T;
+  const bool row_virt = !REV || (T % Sh::kTile) == 0;
+  wave_sync();
+  if (lane == 0)
+    for (int i = 0; i < n; ++i) {
+      const int s = REV ? S - 1 - i : i;
+      const Vec2<E> v = load_pair(a.virt + (b * S + s) * 2, a.virt != nullptr && row_virt);
+      carry[i] = {up(v.v0), up(v.v1)};
+    }
+  wave_sync();
+  const E zero = E(0);
+  const SosAcc<E> none{};
+  for (int64_t off = 0; off < span; off += 64 * K) {
+    const int64_t t0 = REV ? row_end - off - int64_t(lane + 1) * K : off + int64_t(lane) * K;
+    E u[K];
+    load_chunk<E, K>(inrow, t0, T, a.vec_ok != 0, u, zero);
+    for (int i = 0; i < n; ++i) {
+      const int s = REV ? S - 1 - i : i;
+      const SosSec<E> q = load_sec(sosrow, s);
+      Mt P[NP];
+      sec_powers<E, K, NP>(sec_matrix<E, REV>(q), P);
+      const Mt pw = lane_power<E, NP>(P, lane);
+      const RowMul<C> mul = row_mul<true, E, NP>(P, lane);
+      const Vec2<E> gzf = load_pair(a.virt + (b * S + s) * 2, REV && a.virt != nullptr);
+      V v = REV ? fold_adj<E, K>(q, u, t0, T, gzf) : fold_fwd<E, K>(q, u);
+      v = lti_scan<true>(v, lane, P, mul);
+      const V tot = read_lane(v, 63);
+      const V ex = lane_prev<true>(v, lane, Alg::szero());
+      const V c = carry[i];
+      const Vec2<E> h = Alg::store_s(Alg::affine(pw, c, ex));
+      if constexpr (REV) {
+        SosAcc<E> acc = none;
+        const E unused[1] = {zero};
+        run_adj<E, K, false>(q, h, u, t0, T, gzf, nullptr, unused, unused, acc);
+      } else {
+        run_fwd<E, K>(q, h, u, t0, T, nullptr);
+      }
+      wave_sync();
+      if (lane == 0) carry[i] = Alg::affine(P[6], c, tot);
+      wave_sync();
+    }
+  }
+  const V out = carry[n - 1];
+  wave_sync();
+  return out;
+}
+
+// ------------------------------------------------------------ the kernel
+// REV : adjoint cascade (backward); GRAD: also the coefficient gradients
+// (backward only: recomputes the forward inside the tile from a.x and a.ckpt).
+// Barriers: claim; with GRAD, one per section while the forward is
+// recomputed; then two per section (wave aggregates ready, entry state ready).
+template <typename E, class Sh, bool REV, bool GRAD>
+__global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
+  using Alg = Block2<E>;
+  using C = typename Wide<E>::type;
+  using V = Vec2<C>;
+  using Mt = Mat2<C>;
+  using M = Map<Alg>;
+  using SV = Vec2<E>;
+  constexpr int K = Sh::K, R = Sh::R, W = Sh::kWaves, NP = Sh::kPowers;
+  constexpr int kS = StatusShape<Alg>::kStride;
+  static_assert(!GRAD || REV, "coefficient gradients come with the backward");
+
+  __shared__ M s_wagg[W];
+  __shared__ M s_wpre[W];
+  __shared__ V s_in;
+  __shared__ unsigned s_id, s_tag;
+  __shared__ uint64_t s_look[StatusShape<Alg>::kLookWords];
+  __shared__ M s_fagg[GRAD ? 2 : 1][W];  // forward recompute: wave aggregates, two sections in flight
+  extern __shared__ __align__(16) unsigned char sos_dyn[];  // GRAD: lane entry states [S][W][R][64]
+  SV *s_laneh = reinterpret_cast<SV *>(sos_dyn);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
+  __syncthreads();
+  if (s_id >= a.tiles) return;  // padding of the last stripe round
+  const int64_t id = s_id;
+  const unsigned tag = s_tag;
+  const int64_t qs = id / a.B;  // position in scan order
+  const int64_t b = id - qs * a.B;
+  const int64_t tiles = a.tiles_per_row;
+  const int64_t qf = REV ? tiles - 1 - qs : qs;  // position along time
+  const int64_t T = a.T_len;
+  const int S = a.S;
+  const bool vec = a.vec_ok != 0;
+  const E *sosrow = a.sos + b * a.sos_row_stride;
+  // the row's state before its first step in scan order; backward it is
+  // dL/dzf only when no padded step t = T carries it
+  const bool row_virt = !REV || (T % Sh::kTile) == 0;
+
+  if (w == W) {
+    // ================= look-back wave
+    if constexpr (GRAD)
+      for (int i = 0; i < S; ++i) __syncthreads();  // forward recompute barriers
+    auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
+    for (int i = 0; i < S; ++i) {
+      const int s = REV ? S - 1 - i : i;
+      uint64_t *row_status = a.status + ((b * S + s) * tiles) * kS;
+      const SV vs = load_pair(a.virt + (b * S + s) * 2, a.virt != nullptr && row_virt);
+      const V virt = {up(vs.v0), up(vs.v1)};
+      __syncthreads();  // wave aggregates are in s_wagg
+      M v = lane < W ? s_wagg[lane] : map_identity<Alg>();
+      v = wave_scan_incl(v, lane, op);
+      const M wex = wave_shift_up(v, lane, map_identity<Alg>());
+      if (lane < W) s_wpre[lane] = wex;
+      const M tagg = read_lane(v, W - 1);
+      V yin = virt;
+      if (qs > 0) {
+        if (lane == 0) publish(row_status + qs * kS + StatusShape<Alg>::kIncWords, tagg, tag);
+        Lookback<Alg> lb = lookback_start<Alg>(qs);
+        if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
+          yin = sos_prefix_fallback<E, Sh, REV>(a, b, s, qs * Sh::kTile, lane, reinterpret_cast<V *>(s_look));
+      }
+      if (qs + 1 < tiles && lane == 0) publish(row_status + qs * kS, apply<Alg>(tagg, yin), tag);
+      if (lane == 0) s_in = yin;
+      __syncthreads();  // entry state is in s_in
+    }
+    return;
+  }
+
+  // ================= data waves
+  const int pw = REV ? W - 1 - w : w;
+  const int pl = REV ? 63 - lane : lane;
+  const int64_t seg0 = qf * Sh::kTile + int64_t(pw) * Sh::kWaveSeg;
+  auto chunk0 = [&](int r) -> int64_t {  // r in scan order
+    const int pr = REV ? R - 1 - r : r;
+    return seg0 + int64_t(pr) * 64 * K + int64_t(pl) * K;
+  };
+  const E zero = E(0);
+
+  E U[R][K];  // forward: input of the current section;  backward: its upstream gradient
+#pragma unroll
+  for (int r = 0; r < R; ++r) load_chunk<E, K>(a.in + b * T, chunk0(r), T, vec, U[r], zero);
+
+  // ---- backward with coefficient gradients: recompute the forward cascade
+  // over the tile from its checkpoints (time order is descending scan order),
+  // keeping every lane's entry state of every section in LDS
+  E X[GRAD ? R : 1][GRAD ? K : 1];
+  E F[GRAD ? R : 1][GRAD ? K : 1];  // forward values of the current section
+  if constexpr (GRAD) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      load_chunk<E, K>(a.x + b * T, chunk0(r), T, vec, X[r], zero);
+#pragma unroll
+      for (int k = 0; k < K; ++k) F[r][k] = X[r][k];
+    }
+    const int64_t ck0 = (qf * Sh::kTile) / kSosCkpt;
+    for (int s = 0; s < S; ++s) {
+      const SosSec<E> q = load_sec(sosrow, s);
+      Mt P[NP];
+      sec_powers<E, K, NP>(sec_matrix<E, false>(q), P);
+      const RowMul<C> mul = row_mul<false, E, NP>(P, lane);
+      V ex[R], tot[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        V v = fold_fwd<E, K>(q, F[r]);
+        v = lti_scan<false>(v, lane, P, mul);
+        tot[r] = read_lane(v, 0);
+        ex[r] = lane_prev<false>(v, lane, Alg::szero());
+      }
+      V agg = tot[R - 1];
+#pragma unroll
+      for (int r = R - 2; r >= 0; --r) agg = Alg::affine(P[6], agg, tot[r]);
+      if (lane == 0) s_fagg[s & 1][w] = M{P[NP - 1], agg};
+      __syncthreads();  // forward wave aggregates of section s
+      V H = a.ckpt[(b * S + s) * a.n_ckpt + ck0];
+      for (int w2 = W - 1; w2 > w; --w2) H = apply<Alg>(s_fagg[s & 1][w2], H);
+      const Mt pwr = lane_power<E, NP>(P, 63 - lane);
+#pragma unroll
+      for (int r = R - 1; r >= 0; --r) {
+        const SV h = Alg::store_s(Alg::affine(pwr, H, ex[r]));
+        s_laneh[((s * W + w) * R + r) * 64 + lane] = h;
+        run_fwd<E, K>(q, h, F[r], chunk0(r), T, nullptr);
+        H = Alg::affine(P[6], H, tot[r]);
+      }
+    }
+    // F now holds the cascade output: the forward output of section S-1
+  }
+
+  for (int i = 0; i < S; ++i) {
+    const int s = REV ? S - 1 - i : i;
+    const SosSec<E> q = load_sec(sosrow, s);
+    Mt P[NP];
+    sec_powers<E, K, NP>(sec_matrix<E, REV>(q), P);
+    const SV gzf = load_pair(a.virt + (b * S + s) * 2, REV && a.virt != nullptr);
+
+    // forward input of section s, recomputed from x through sections < s
+    // (F keeps its output, the previous iteration's input)
+    E Uf[GRAD ? R : 1][GRAD ? K : 1];
+    if constexpr (GRAD) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int k = 0; k < K; ++k) Uf[r][k] = X[r][k];
+      for (int j = 0; j < s; ++j) {
+        const SosSec<E> qj = load_sec(sosrow, j);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          run_fwd<E, K>(qj, s_laneh[((j * W + w) * R + r) * 64 + lane], Uf[r], chunk0(r), T, nullptr);
+      }
+    }
+
+    // ---- pass 1: lane folds, wave scan, round chaining
+    const RowMul<C> mul = row_mul<true, E, NP>(P, lane);
+    V ex[R], tot[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      V v = REV ? fold_adj<E, K>(q, U[r], chunk0(r), T, gzf) : fold_fwd<E, K>(q, U[r]);
+      v = lti_scan<true>(v, lane, P, mul);
+      tot[r] = read_lane(v, 63);
+      ex[r] = lane_prev<true>(v, lane, Alg::szero());
+    }
+    V agg = tot[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r) agg = Alg::affine(P[6], agg, tot[r]);
+    if (lane == 0) s_wagg[w] = M{P[NP - 1], agg};
+    __syncthreads();  // wave aggregates are in s_wagg
+    __syncthreads();  // entry state is in s_in
+    V H = apply<Alg>(s_wpre[w], s_in);
+    const Mt pwr = lane_power<E, NP>(P, lane);
+
+    // ---- pass 2
+    SosAcc<E> acc{};
+    SosAcc<C> wacc{};
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t t0 = chunk0(r);
+      const V hc = Alg::affine(pwr, H, ex[r]);
+      const SV h = Alg::store_s(hc);
+      if constexpr (REV) {
+        acc = SosAcc<E>{};
+        run_adj<E, K, GRAD>(q, h, U[r], t0, T, gzf, a.fin ? a.fin + (b * S + s) * 2 : nullptr,
+                            Uf[GRAD ? r : 0], F[GRAD ? r : 0], acc);
+        if constexpr (GRAD) {
+          wacc.a1 += up(acc.a1);
+          wacc.a2 += up(acc.a2);
+          wacc.c0 += up(acc.c0);
+          wacc.c1 += up(acc.c1);
+          wacc.b0 += up(acc.b0);
+        }
+      } else {
+        if (a.ckpt && (t0 % kSosCkpt) == 0 && t0 < T) a.ckpt[(b * S + s) * a.n_ckpt + t0 / kSosCkpt] = hc;
+        run_fwd<E, K>(q, h, U[r], t0, T, a.fin ? a.fin + (b * S + s) * 2 : nullptr);
+      }
+      H = Alg::affine(P[6], H, tot[r]);
+    }
+    if constexpr (GRAD) {
+      auto sum = [](const SosAcc<C> &p, const SosAcc<C> &o) -> SosAcc<C> {
+        return {p.a1 + o.a1, p.a2 + o.a2, p.c0 + o.c0, p.c1 + o.c1, p.b0 + o.b0};
+      };
+      wacc = wave_scan_incl(wacc, lane, sum);
+      if (lane == 63) {
+        C *dst = a.partials + ((((b * S + s) * tiles + qf) * W) + w) * 5;
+        dst[0] = wacc.a1;
+        dst[1] = wacc.a2;
+        dst[2] = wacc.c0;
+        dst[3] = wacc.c1;
+        dst[4] = wacc.b0;
+      }
+      // the next (lower) section's forward output is this section's input
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int k = 0; k < K; ++k) F[r][k] = Uf[r][k];
+    }
+  }
+
+  if (a.out) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) store_chunk<E, K>(a.out + b * T, chunk0(r), T, vec, U[r]);
+  }
+}
+
+// ------------------------------------------------------------ coefficient gradient
+// One block per (coefficient row, section): sums the per-tile, per-wave
+// partials (over every batch row when the coefficients are shared) in a fixed
+// order and applies the chain rule to (b0, b1, b2, a0, a1, a2):
+//   d c0/d b1 = 1, d c0/d b0 = -a1, d c0/d a1 = -b0, d A00/d a1 = -1 (same
+//   pattern for c1, a2), d y/d b0 = u; a0 is not a free parameter (zero).
+constexpr int kSosReduceThreads = 256;
+
+template <typename E, class Sh>
+__global__ __launch_bounds__(kSosReduceThreads) void sos_grad_reduce_kernel(const SosArgs<E> a, E *gsos,
+                                                                         int64_t coef_rows) {
+  using C = typename Wide<E>::type;
+  __shared__ C s_sum[5][kSosReduceThreads];
+  const int64_t row = blockIdx.x / a.S;
+  const int s = int(blockIdx.x - row * a.S);
+  const int64_t per_b = a.tiles_per_row * Sh::kWaves;
+  const int64_t b_lo = coef_rows == 1 ? 0 : row, b_hi = coef_rows == 1 ? a.B : row + 1;
+  C acc[5] = {C(0), C(0), C(0), C(0), C(0)};
+  for (int64_t bb = b_lo; bb < b_hi; ++bb) {
+    const C *p = a.partials + ((bb * a.S + s) * per_b) * 5;
+    for (int64_t j = threadIdx.x; j < per_b; j += kSosReduceThreads)
+#pragma unroll
+      for (int c = 0; c < 5; ++c) acc[c] += p[j * 5 + c];
+  }
+#pragma unroll
+  for (int c = 0; c < 5; ++c) s_sum[c][threadIdx.x] = acc[c];
+  __syncthreads();
+  for (int h = kSosReduceThreads / 2; h > 0; h >>= 1) {
+    if (int(threadIdx.x) < h)
+#pragma unroll
+      for (int c = 0; c < 5; ++c) s_sum[c][threadIdx.x] += s_sum[c][threadIdx.x + h];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const E *p = a.sos + row * a.sos_row_stride + 6 * s;
+    const C b0 = up(p[0]), a1 = up(p[4]), a2 = up(p[5]);
+    const C Sa1 = s_sum[0][0], Sa2 = s_sum[1][0], Sc0 = s_sum[2][0], Sc1 = s_sum[3][0], Sb0 = s_sum[4][0];
+    E *g = gsos + row * int64_t(a.S) * 6 + 6 * s;
+    g[0] = down<E>(Sb0 - a1 * Sc0 - a2 * Sc1);
+    g[1] = down<E>(Sc0);
+    g[2] = down<E>(Sc1);
+    g[3] = E(0);
+    g[4] = down<E>(-Sa1 - b0 * Sc0);
+    g[5] = down<E>(-Sa2 - b0 * Sc1);
+  }
+}
+
+}  // namespace phs

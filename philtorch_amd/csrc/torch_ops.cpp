@@ -1,6 +1,7 @@
 // torch.library layer of philtorch_amd: owns the `philtorch` operator
 // namespace with the reference's schemas (philtorch/csrc/host_recur2.cpp:162-171)
-// plus the new LPV scalar op `recur` and four fused backward ops, and binds
+// plus the new LPV scalar op `recur`, four fused backward ops and the fused
+// second-order-section cascade (`sosfilt`, `sosfilt_backward`), and binds
 // the HIP device key (PyTorch-ROCm names it CUDA) to the C ABI of
 // libphilscan.  No CPU kernels are registered: CPU tensors raise, and the
 // Python API keeps the reference's pure-PyTorch route for them.
@@ -12,6 +13,7 @@
 #include <algorithm>
 #include <map>
 #include <mutex>
+#include <optional>
 #include <tuple>
 #include <vector>
 
@@ -373,6 +375,99 @@ Triple lti_recurN_backward_hip(const Tensor &A, const Tensor &zi, const Tensor &
   return run_bwd_n("lti_recurN_backward", phs_lti_recurN_bwd, PHS_OP_LTI_RECURN, int(M), A, shared, zi, y, g);
 }
 
+// ------------------------------------------------------------ SOS cascade
+// sosfilt: fused cascade of second-order sections (scipy.signal.sosfilt
+// semantics, phs_sosfilt_* in philscan.h); no counterpart op in the reference.
+constexpr int64_t kSosMaxSections = 8;
+constexpr int64_t kSosCkptInterval = 512;  // steps between forward checkpoints
+
+void check_sos(const char *op, const Tensor &sos, const Tensor &x) {
+  TORCH_CHECK(x.dim() == 2, "philtorch::", op, ": x must be a 2D tensor (batch, time)");
+  TORCH_CHECK((sos.dim() == 2 || sos.dim() == 3) && sos.size(-1) == 6, "philtorch::", op,
+              ": sos must be (sections, 6) or (batch, sections, 6)");
+  if (sos.dim() == 3)
+    TORCH_CHECK(sos.size(0) == x.size(0), "philtorch::", op, ": a 3D sos must have x's batch size");
+  const int64_t S = sos.size(-2);
+  TORCH_CHECK(S >= 1 && S <= kSosMaxSections, "philtorch::", op, ": 1 to ", kSosMaxSections,
+              " sections per call, got ", S);
+  TORCH_CHECK(sos.scalar_type() == x.scalar_type(), "sos must have the same scalar type as input");
+  TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble, "philtorch::", op,
+              ": float32 or float64 only, got ", x.scalar_type());
+  TORCH_CHECK(x.is_cuda() && sos.is_cuda(), "philtorch::", op, ": philtorch_amd runs on HIP devices only (got ",
+              x.device(), ")");
+  TORCH_CHECK(sos.device() == x.device(), "philtorch::", op, ": all tensors must be on the same device");
+}
+
+void check_states(const char *op, const char *what, const Tensor &z, const Tensor &x, int64_t S) {
+  TORCH_CHECK(z.dim() == 3 && z.size(0) == x.size(0) && z.size(1) == S && z.size(2) == 2, "philtorch::", op,
+              ": ", what, " must be (batch, sections, 2)");
+  TORCH_CHECK(z.scalar_type() == x.scalar_type(), "philtorch::", op, ": ", what, " must have x's scalar type");
+  TORCH_CHECK(z.device() == x.device(), "philtorch::", op, ": all tensors must be on the same device");
+}
+
+int64_t sos_n_ckpt(int64_t T) { return (T + kSosCkptInterval - 1) / kSosCkptInterval; }
+
+Triple sosfilt_hip(const Tensor &sos, const std::optional<Tensor> &zi, const Tensor &x) {
+  check_sos("sosfilt", sos, x);
+  const int64_t B = x.size(0), T = x.size(1), S = sos.size(-2);
+  if (zi) check_states("sosfilt", "zi", *zi, x, S);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor sc = sos.contiguous(), xc = x.contiguous();
+  Tensor zc = zi ? zi->contiguous() : Tensor();
+  Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  Tensor zf = at::empty({B, S, 2}, x.options());
+  Tensor ckpt = at::empty({B, S, sos_n_ckpt(T), 2}, x.options().dtype(at::kDouble));
+  TORCH_CHECK(size_t(ckpt.numel()) * sizeof(double) == phs_sosfilt_ckpt_size(dt, B, T, int(S)),
+              "philtorch::sosfilt: checkpoint layout mismatch with libphilscan");
+  if (B == 0 || T == 0) {
+    if (zi) zf.copy_(zc); else zf.zero_();
+    return {y, zf, ckpt};
+  }
+  void *stream = stream_of(x);
+  const Workspace ws = workspace_for(x, phs_sosfilt_workspace_size(dt, B, T, int(S), 0), stream);
+  check_status(phs_sosfilt_fwd(dt, B, T, int(S), sc.const_data_ptr(), sos.dim() == 2 ? 1 : 0,
+                               zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(), y.mutable_data_ptr(),
+                               zf.mutable_data_ptr(), ckpt.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+               "sosfilt");
+  return {y, zf, ckpt};
+}
+
+// Returns (grad_x, grad_sos, grad_zi); grad_sos is zero unless need_sos.
+Triple sosfilt_backward_hip(const Tensor &sos, const Tensor &x, const Tensor &ckpt, const Tensor &gy,
+                            const std::optional<Tensor> &gzf, bool need_sos) {
+  check_sos("sosfilt_backward", sos, x);
+  const int64_t B = x.size(0), T = x.size(1), S = sos.size(-2);
+  TORCH_CHECK(gy.sizes() == x.sizes(), "philtorch::sosfilt_backward: grad_y must have x's shape");
+  TORCH_CHECK(gy.device() == x.device(), "philtorch::sosfilt_backward: all tensors must be on the same device");
+  if (gzf) check_states("sosfilt_backward", "grad_zf", *gzf, x, S);
+  TORCH_CHECK(ckpt.scalar_type() == at::kDouble && ckpt.dim() == 4 && ckpt.size(0) == B && ckpt.size(1) == S &&
+                  ckpt.size(2) == sos_n_ckpt(T) && ckpt.size(3) == 2 && ckpt.device() == x.device(),
+              "philtorch::sosfilt_backward: ckpt must be the forward's checkpoint tensor");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor sc = sos.contiguous(), xc = x.contiguous(), gc = gy.to(x.scalar_type()).contiguous();
+  Tensor cc = ckpt.contiguous();
+  Tensor gzc = gzf ? gzf->contiguous() : Tensor();
+  Tensor gx = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  Tensor gsos = need_sos ? at::empty(sos.sizes(), sos.options()) : at::zeros(sos.sizes(), sos.options());
+  Tensor gzi = at::empty({B, S, 2}, x.options());
+  if (B == 0 || T == 0) {
+    if (need_sos) gsos.zero_();
+    if (gzf) gzi.copy_(gzc); else gzi.zero_();
+    return {gx, gsos, gzi};
+  }
+  void *stream = stream_of(x);
+  const Workspace ws = workspace_for(x, phs_sosfilt_workspace_size(dt, B, T, int(S), 1), stream);
+  check_status(phs_sosfilt_bwd(dt, B, T, int(S), sc.const_data_ptr(), sos.dim() == 2 ? 1 : 0,
+                               need_sos ? xc.const_data_ptr() : nullptr, need_sos ? cc.const_data_ptr() : nullptr,
+                               gc.const_data_ptr(), gzf ? gzc.const_data_ptr() : nullptr, gx.mutable_data_ptr(),
+                               need_sos ? gsos.mutable_data_ptr() : nullptr, gzi.mutable_data_ptr(), ws.ptr,
+                               ws.bytes, stream),
+               "sosfilt_backward");
+  return {gx, gsos, gzi};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(philtorch, m) {
@@ -393,6 +488,12 @@ TORCH_LIBRARY(philtorch, m) {
         {at::Tag::pt2_compliant_tag});
   m.def("lti_recurN_backward(Tensor A, Tensor zi, Tensor y, Tensor grad_y) -> (Tensor, Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
+  // new: fused cascade of second-order sections, returning (y, zf, ckpt), and
+  // its backward returning (grad_x, grad_sos, grad_zi)
+  m.def("sosfilt(Tensor sos, Tensor? zi, Tensor x) -> (Tensor, Tensor, Tensor)", {at::Tag::pt2_compliant_tag});
+  m.def("sosfilt_backward(Tensor sos, Tensor x, Tensor ckpt, Tensor grad_y, Tensor? grad_zf, bool need_sos)"
+        " -> (Tensor, Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
@@ -406,4 +507,6 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("recurN_backward", &recurN_backward_hip);
   m.impl("lti_recur_backward", &lti_recur_backward_hip);
   m.impl("lti_recurN_backward", &lti_recurN_backward_hip);
+  m.impl("sosfilt", &sosfilt_hip);
+  m.impl("sosfilt_backward", &sosfilt_backward_hip);
 }

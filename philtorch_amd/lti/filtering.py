@@ -5,7 +5,9 @@ it through ``state_space`` (transposed direct form II by default), so with
 ``unroll_factor=1`` on a HIP device every biquad section is one native 2x2
 scan (``philtorch::lti_recur2``).  ``filtfilt`` and ``lfilter_zi`` follow the
 reference and SciPy.  Cascaded second-order sections are composed by the
-caller, one ``lfilter`` per section, as in the reference (it has no SOS API).
+caller, one ``lfilter`` per section, as in the reference (it has no SOS API),
+or all at once by ``sosfilt``, which on a HIP device runs the whole cascade in
+one fused kernel per direction.
 """
 from __future__ import annotations
 
@@ -141,3 +143,81 @@ def filtfilt(
     if edge > 0:
         y = y[..., edge:-edge]
     return y.flip(-1)
+
+
+# sections per fused launch (the backward keeps every section's lane states in LDS)
+_SOS_SECTIONS_PER_CALL = 8
+
+
+def sosfilt(sos: Tensor, x: Tensor, zi: Optional[Tensor] = None, **kwargs) -> Union[Tensor, tuple[Tensor, Tensor]]:
+    """Cascade of second-order sections with ``scipy.signal.sosfilt``'s
+    semantics (transposed direct form II, filtering along the last axis).
+
+    philtorch has no cascade API; its users chain one ``lfilter(b, a, y,
+    form="tdf2")`` per section (philtorch/lti/filtering.py:211-333), which is
+    what this computes.  On a HIP device every group of up to 8 sections
+    runs in one fused kernel per direction (``philtorch::sosfilt``):
+    the intermediate sections' signals never reach memory.  Elsewhere it
+    takes that per-section ``lfilter`` route (``**kwargs`` are forwarded to it,
+    e.g. ``unroll_factor``).
+
+    Args:
+        sos: ``(S, 6)`` or ``(B, S, 6)`` rows ``(b0, b1, b2, a0, a1, a2)``;
+            every section is normalised by its ``a0``.
+        x: ``(N,)`` or ``(B, N)`` input.
+        zi: optional initial states in scipy's layout, ``(S, 2)`` for a 1D
+            ``x`` or ``(S, B, 2)``; when given, ``(y, zf)`` is returned with
+            ``zf`` in the same layout.
+    """
+    assert sos.dim() in (2, 3) and sos.size(-1) == 6, "sos must be (sections, 6) or (batch, sections, 6)."
+    assert x.dim() in (1, 2), "Input signal x must be 1D or 2D."
+    squeeze = x.dim() == 1
+    xb = x.unsqueeze(0) if squeeze else x
+    batch, S = xb.size(0), sos.size(-2)
+    if sos.dim() == 3:
+        assert sos.size(0) == batch, "A 3D sos must have x's batch size."
+    sos = sos / sos[..., 3:4]
+    zb = None
+    if zi is not None:
+        want = (S, 2) if squeeze else (S, batch, 2)
+        assert tuple(zi.shape) == want, f"zi must have shape {want}, got {tuple(zi.shape)}"
+        zb = (zi.unsqueeze(1) if squeeze else zi).transpose(0, 1)  # (B, S, 2)
+    if xb.is_cuda:
+        y, zf = _sosfilt_fused(sos, xb, zb)
+    else:
+        y, zf = _sosfilt_sections(sos, xb, zb, **kwargs)
+    if squeeze:
+        y = y.squeeze(0)
+    if zi is None:
+        return y
+    zf = zf.transpose(0, 1)
+    return y, (zf.squeeze(1) if squeeze else zf)
+
+
+def _sosfilt_fused(sos: Tensor, x: Tensor, zi: Optional[Tensor]) -> tuple[Tensor, Tensor]:
+    from .. import require_extension
+
+    require_extension()
+    dtype = x.dtype
+    if dtype in (torch.float16, torch.bfloat16):
+        x, sos = x.float(), sos.float()
+        zi = None if zi is None else zi.float()
+    else:
+        sos = sos.to(dtype)
+    y, zfs = x, []
+    for s0 in range(0, sos.size(-2), _SOS_SECTIONS_PER_CALL):
+        part = sos[..., s0:s0 + _SOS_SECTIONS_PER_CALL, :]
+        zpart = None if zi is None else zi[:, s0:s0 + part.size(-2)].contiguous()
+        y, zf, _ = torch.ops.philtorch.sosfilt(part.contiguous(), zpart, y.contiguous())
+        zfs.append(zf)
+    return y.to(dtype), torch.cat(zfs, dim=1).to(dtype)
+
+
+def _sosfilt_sections(sos: Tensor, x: Tensor, zi: Optional[Tensor], **kwargs) -> tuple[Tensor, Tensor]:
+    y, zfs = x, []
+    for s in range(sos.size(-2)):
+        b, a = sos[..., s, 0:3], sos[..., s, 4:6]
+        z = x.new_zeros(x.size(0), 2) if zi is None else zi[:, s]
+        y, zf = lfilter(b, a, y, zi=z, form="tdf2", **kwargs)
+        zfs.append(zf)
+    return y, torch.stack(zfs, dim=1)

@@ -81,7 +81,7 @@ def tol(dtype) -> float:
     return 0.0
 
 
-def check(got, ref, name="", dtype=None):
+def check(got, ref, name="", dtype=None, scale=None):
     got = np.asarray(got)
     ref = np.asarray(ref)
     assert got.shape == ref.shape, f"{name}: shape {got.shape} != {ref.shape}"
@@ -90,7 +90,20 @@ def check(got, ref, name="", dtype=None):
         np.testing.assert_array_equal(got, ref, err_msg=name)
         return 0.0
     err = float(np.max(np.abs(got.astype(np.complex128) - ref.astype(np.complex128)))) if ref.size else 0.0
-    scale = float(np.max(np.abs(ref))) if ref.size else 0.0
+    own = float(np.max(np.abs(ref))) if ref.size else 0.0
+    scale = own if scale is None else max(own, float(scale))
     bound = tol(dtype) * max(scale, np.finfo(np.float64).tiny)
     assert err <= bound, f"{name}: max|d|={err:.3e} > {tol(dtype):.0e} * max|ref| ({scale:.3e})"
     return err / max(scale, 1e-300)
+
+
+def sos_coefs(g, lead, S, dtype, rlo=0.5, rhi=0.95, rz=1.2):
+    """Second-order sections (b0, b1, b2, 1, a1, a2) of shape lead + (S, 6):
+    poles r e^{+-i theta}, r ~ U(rlo, rhi), zeros r_z e^{+-i phi},
+    r_z ~ U(0, rz), gain b0 ~ U(0.5, 1.5) (the C4 recipe of the benchmark)."""
+    shape = tuple(lead) + (S,)
+    r, th = g.uniform(rlo, rhi, shape), g.uniform(0, np.pi, shape)
+    z, ph = g.uniform(0, rz, shape), g.uniform(0, np.pi, shape)
+    k = g.uniform(0.5, 1.5, shape)
+    sos = np.stack([k, -2 * z * np.cos(ph) * k, z * z * k, np.ones(shape), -2 * r * np.cos(th), r * r], axis=-1)
+    return sos.astype(dtype)

@@ -57,4 +57,20 @@ def load() -> ctypes.CDLL:
     lib.phs_error_string.restype = ctypes.c_char_p
     lib.phs_debug_set_spin_limit.argtypes = [ctypes.c_uint]
     lib.phs_debug_set_spin_limit.restype = None
+    # fused cascade of second-order sections
+    lib.phs_sosfilt_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                               ctypes.c_int]
+    lib.phs_sosfilt_workspace_size.restype = ctypes.c_size_t
+    lib.phs_sosfilt_ckpt_size.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
+    lib.phs_sosfilt_ckpt_size.restype = ctypes.c_size_t
+    lib.phs_sosfilt_fwd.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
+                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                    ctypes.c_void_p]
+    lib.phs_sosfilt_fwd.restype = ctypes.c_int
+    lib.phs_sosfilt_bwd.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
+                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                    ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.phs_sosfilt_bwd.restype = ctypes.c_int
     return lib

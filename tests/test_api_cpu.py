@@ -95,6 +95,23 @@ def test_sos_cascade_matches_scipy_sosfilt():
     np.testing.assert_allclose(y[0].numpy(), scipy.signal.sosfilt(sos, x), rtol=1e-9, atol=1e-9)
 
 
+def test_sosfilt_cpu_route_matches_scipy():
+    """lti.sosfilt on CPU tensors (one lfilter(tdf2) per section), scipy's
+    layout of zi/zf, a0 normalisation, 1D and 2D inputs."""
+    g = D.rng(25)
+    sos = D.sos_coefs(g, (), 3, np.float64)
+    sos[1] *= 2.0  # a0 = 2 for one section
+    x = g.standard_normal((2, 400))
+    zi = g.standard_normal((3, 2, 2))
+    y, zf = lti.sosfilt(torch.from_numpy(sos), torch.from_numpy(x), zi=torch.from_numpy(zi))
+    sos_n = sos / sos[:, 3:4]  # scipy takes normalised sections only
+    ry, rzf = scipy.signal.sosfilt(sos_n, x, axis=-1, zi=zi)
+    np.testing.assert_allclose(y.numpy(), ry, rtol=1e-9, atol=1e-9)
+    np.testing.assert_allclose(zf.numpy(), rzf, rtol=1e-9, atol=1e-9)
+    y1 = lti.sosfilt(torch.from_numpy(sos), torch.from_numpy(x[0]))
+    np.testing.assert_allclose(y1.numpy(), scipy.signal.sosfilt(sos_n, x[0]), rtol=1e-9, atol=1e-9)
+
+
 @pytest.mark.parametrize("unroll", [1, 4, 13])
 @pytest.mark.parametrize("batched", [False, True])
 def test_lti_state_space_recursion_unrolled_equals_loop(unroll, batched):

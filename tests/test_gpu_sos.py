@@ -1,0 +1,271 @@
+"""GPU parity of the fused second-order-section cascade.
+
+The C ABI entry points phs_sosfilt_fwd / phs_sosfilt_bwd (ctypes, raw device
+pointers, the caller's stream) against the oracle's cascade, which chains one
+philtorch lfilter(form="tdf2") per section (oracle.sosfilt / sosfilt_bwd,
+pinned to scipy.signal.sosfilt and to autograd of a serial loop in
+tests/test_oracle.py), evaluated in fp64 on the GPU's exact inputs.  Covers rows that end inside a tile, on a tile, and
+shorter than a lane's chunk; one to eight sections (more through the API, which chains launches); shared and per-row
+coefficients; initial states and a zf gradient; the forced look-back
+fallback in both directions; the torch API (philtorch_amd.lti.sosfilt) against
+scipy and the per-section lfilter route, at the benchmark's full C4 size.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from tests import _data as D
+
+pytestmark = pytest.mark.gpu
+
+# float32 tiles are 6144 steps forward, 3072 backward; float64 3072 / 1536
+SHAPES = [(1, 1), (2, 17), (3, 1536), (2, 3071), (2, 6144), (3, 6145), (2, 20000)]
+SECTIONS = [1, 3, 8]
+FLOATS = [np.float32, np.float64]
+
+
+@pytest.fixture(scope="module")
+def api(hip):
+    import torch
+
+    from tests import capi
+
+    lib = capi.load()
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+    yield lib, ws, capi
+    lib.phs_debug_set_spin_limit(0)
+
+
+def _dev(x):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream():
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _case(dtype, B, T, S, shared, with_zi, with_gzf, seed):
+    g = D.rng(seed)
+    sos = D.sos_coefs(g, () if shared else (B,), S, dtype)
+    x = D.normal(g, (B, T), dtype)
+    zi = D.normal(g, (B, S, 2), dtype) if with_zi else None
+    gy = D.normal(g, (B, T), dtype)
+    gzf = D.normal(g, (B, S, 2), dtype) if with_gzf else None
+    return sos, x, zi, gy, gzf
+
+
+def _run(api, sos, x, zi, gy, gzf, grad=True):
+    """Forward + backward through the C ABI; numpy (y, zf, gsos, gzi, gx)."""
+    import torch
+
+    lib, ws, capi = api
+    dt = capi.DTYPES[np.dtype(x.dtype)]
+    B, T = x.shape
+    S = sos.shape[-2]
+    shared = int(sos.ndim == 2)
+    ts, tx, tg = _dev(sos), _dev(x), _dev(gy)
+    tz = _dev(zi) if zi is not None else None
+    tgz = _dev(gzf) if gzf is not None else None
+    need_f = lib.phs_sosfilt_workspace_size(dt, B, T, S, 0)
+    need = lib.phs_sosfilt_workspace_size(dt, B, T, S, 1)
+    assert 0 < need_f <= need <= ws.numel()
+    ck = torch.empty(lib.phs_sosfilt_ckpt_size(dt, B, T, S), dtype=torch.uint8, device="cuda")
+    y = torch.empty_like(tx)
+    zf = torch.empty((B, S, 2), dtype=tx.dtype, device="cuda")
+    rc = lib.phs_sosfilt_fwd(dt, B, T, S, _p(ts), shared, _p(tz), _p(tx), _p(y), _p(zf), _p(ck), _p(ws), need_f,
+                             _stream())
+    assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+    gx, gzi = torch.empty_like(tx), torch.empty((B, S, 2), dtype=tx.dtype, device="cuda")
+    gs = torch.empty_like(ts) if grad else None
+    rc = lib.phs_sosfilt_bwd(dt, B, T, S, _p(ts), shared, _p(tx) if grad else None, _p(ck) if grad else None,
+                             _p(tg), _p(tgz), _p(gx), _p(gs), _p(gzi), _p(ws), need, _stream())
+    assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+    torch.cuda.synchronize()
+    out = [y, zf, gs, gzi, gx]
+    return [None if t is None else t.cpu().numpy() for t in out]
+
+
+def _exact(*arrays):
+    """fp32 inputs widened to fp64: the oracle then evaluates the reference's
+    algorithm on exactly the GPU's inputs without fp32 rounding.  A high-gain
+    8-section cascade leaves ~1e-4 of rounding in the fp32 reference's own
+    coefficient gradients, so two fp32 evaluations may differ by twice the bar
+    while each is within it of this value."""
+    return [None if a is None else np.asarray(a, dtype=np.float64) for a in arrays]
+
+
+def _check_all(got, sos, x, zi, gy, gzf, dtype, name):
+    y, zf, gs, gzi, gx = got
+    sos, x, zi, gy, gzf = _exact(sos, x, zi, gy, gzf)
+    ry, rzf = oracle.sosfilt(sos, x, zi)
+    D.check(y, ry, f"{name} y", dtype=dtype)
+    # final states and their gradients on the scale of the signal they end
+    D.check(zf, rzf, f"{name} zf", dtype=dtype, scale=np.max(np.abs(ry)))
+    rgs, rgzi, rgx = oracle.sosfilt_bwd(sos, x, zi, gy, gzf)
+    D.check(gx, rgx, f"{name} grad_x", dtype=dtype)
+    D.check(gzi, rgzi, f"{name} grad_zi", dtype=dtype, scale=np.max(np.abs(rgx)))
+    if gs is not None:
+        rgs[..., 3] = 0
+        D.check(gs, rgs, f"{name} grad_sos", dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("B,T", SHAPES)
+@pytest.mark.parametrize("S", SECTIONS)
+def test_sosfilt_capi_parity(api, dtype, B, T, S):
+    for shared, with_zi, with_gzf in ((False, True, True), (True, False, False)):
+        case = _case(dtype, B, T, S, shared, with_zi, with_gzf, D.seed_of("sos", dtype, B, T, S, shared))
+        _check_all(_run(api, *case), *case, dtype, f"S={S} B={B} T={T} shared={shared}")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_sosfilt_capi_no_coef_grad(api, dtype):
+    sos, x, zi, gy, gzf = _case(dtype, 3, 7000, 4, False, True, True, D.seed_of("sos-nograd", dtype))
+    y, zf, gs, gzi, gx = _run(api, sos, x, zi, gy, gzf, grad=False)
+    assert gs is None
+    _, rgzi, rgx = oracle.sosfilt_bwd(*_exact(sos, x, zi, gy, gzf))
+    D.check(gx, rgx, "grad_x", dtype=dtype)
+    D.check(gzi, rgzi, "grad_zi", dtype=dtype, scale=np.max(np.abs(rgx)))
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_sosfilt_capi_forced_fallback(api, dtype):
+    """A one-poll budget makes tiles compute their entry states from the row
+    prefix (forward cascade) or suffix (adjoint cascade) themselves."""
+    lib = api[0]
+    case = _case(dtype, 2, 20000, 5, False, True, True, D.seed_of("sos-fallback", dtype))
+    lib.phs_debug_set_spin_limit(1)
+    try:
+        got = _run(api, *case)
+    finally:
+        lib.phs_debug_set_spin_limit(0)
+    _check_all(got, *case, dtype, "fallback")
+
+
+def test_sosfilt_capi_errors(api):
+    import torch
+
+    lib, ws, capi = api
+    x = torch.zeros((2, 100), device="cuda")
+    y = torch.empty_like(x)
+    sos = torch.zeros((3, 6), device="cuda")
+    args = (_p(sos), 1, None, _p(x), _p(y), None, None, _p(ws), ws.numel(), _stream())
+    assert lib.phs_sosfilt_fwd(0, 2, 100, 0, *args) == capi.PHS_ERR_INVALID
+    assert lib.phs_sosfilt_fwd(0, 2, 100, 9, *args) == capi.PHS_ERR_INVALID
+    assert lib.phs_sosfilt_fwd(2, 2, 100, 3, *args) == capi.PHS_ERR_DTYPE
+    need = lib.phs_sosfilt_workspace_size(0, 2, 100, 3, 0)
+    assert lib.phs_sosfilt_fwd(0, 2, 100, 3, _p(sos), 1, None, _p(x), _p(y), None, None, _p(ws), need - 1,
+                               _stream()) == capi.PHS_ERR_WORKSPACE
+    # grad_sos without the forward's checkpoints
+    assert lib.phs_sosfilt_bwd(0, 2, 100, 3, _p(sos), 1, _p(x), None, _p(x), None, _p(y), _p(sos), None, _p(ws),
+                               ws.numel(), _stream()) == capi.PHS_ERR_INVALID
+    assert lib.phs_sosfilt_workspace_size(0, 2, 100, 0, 0) == 0
+    assert lib.phs_sosfilt_ckpt_size(2, 2, 100, 3) == 0
+
+
+# ---------------------------------------------------------------- torch API
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_sosfilt_api_matches_scipy(hip, dtype):
+    import scipy.signal as sg
+    import torch
+
+    g = D.rng(D.seed_of("sos-api", dtype))
+    for S, shape in ((4, (3, 5000)), (20, (2, 9000)), (2, (777,))):
+        sos = D.sos_coefs(g, (), S, np.float64)
+        sos[:, :3] *= 0.7
+        sos[:, 3:] *= 1.3  # a0 != 1: normalised per section
+        x = g.standard_normal(shape)
+        zi = g.standard_normal((S,) + shape[:-1] + (2,))
+        ry, rzf = sg.sosfilt(sos / sos[:, 3:4], x, axis=-1, zi=zi)
+        y, zf = hip.lti.sosfilt(torch.tensor(sos, dtype=torch.float64 if dtype == np.float64 else torch.float32,
+                                             device="cuda"),
+                                torch.tensor(x.astype(dtype), device="cuda"),
+                                zi=torch.tensor(zi.astype(dtype), device="cuda"))
+        D.check(y.cpu().numpy(), ry.astype(dtype), f"y S={S}")
+        D.check(zf.cpu().numpy(), rzf.astype(dtype), f"zf S={S}")
+
+
+def test_sosfilt_api_grad_matches_oracle(hip):
+    import torch
+
+    g = D.rng(D.seed_of("sos-api-grad"))
+    B, T, S = 3, 9000, 6
+    sos = D.sos_coefs(g, (B,), S, np.float64)
+    x = g.standard_normal((B, T))
+    zi = g.standard_normal((S, B, 2))
+    gy = g.standard_normal((B, T))
+    gzf = g.standard_normal((S, B, 2))
+    ts = torch.tensor(sos, device="cuda", requires_grad=True)
+    tx = torch.tensor(x, device="cuda", requires_grad=True)
+    tz = torch.tensor(zi, device="cuda", requires_grad=True)
+    y, zf = hip.lti.sosfilt(ts, tx, zi=tz)
+    ((y * torch.tensor(gy, device="cuda")).sum() + (zf * torch.tensor(gzf, device="cuda")).sum()).backward()
+    zi_b = np.transpose(zi, (1, 0, 2))
+    rgs, rgzi, rgx = oracle.sosfilt_bwd(sos, x, zi_b, gy, np.transpose(gzf, (1, 0, 2)))
+    # the API normalises by a0: d/d a0 of (sos / a0) at a0 = 1 is -sum of the row's other grads
+    rgs[..., 3] = -np.sum(rgs * sos, axis=-1) + rgs[..., 3] * sos[..., 3]
+    D.check(ts.grad.cpu().numpy(), rgs, "grad_sos")
+    D.check(tz.grad.cpu().numpy(), np.transpose(rgzi, (1, 0, 2)), "grad_zi")
+    D.check(tx.grad.cpu().numpy(), rgx, "grad_x")
+
+
+def test_sosfilt_gradcheck(hip):
+    import torch
+
+    g = D.rng(D.seed_of("sos-gradcheck"))
+    sos = torch.tensor(D.sos_coefs(g, (2,), 3, np.float64), device="cuda", requires_grad=True)
+    x = torch.tensor(g.standard_normal((2, 40)), device="cuda", requires_grad=True)
+    zi = torch.tensor(g.standard_normal((3, 2, 2)), device="cuda", requires_grad=True)
+    assert torch.autograd.gradcheck(lambda s, a, z: hip.lti.sosfilt(s, a, zi=z), (sos, x, zi))
+
+
+def test_sosfilt_opcheck(hip):
+    import torch
+
+    g = D.rng(D.seed_of("sos-opcheck"))
+    sos = torch.tensor(D.sos_coefs(g, (), 3, np.float32), device="cuda", requires_grad=True)
+    x = torch.tensor(g.standard_normal((2, 700)).astype(np.float32), device="cuda", requires_grad=True)
+    zi = torch.tensor(g.standard_normal((2, 3, 2)).astype(np.float32), device="cuda", requires_grad=True)
+    torch.library.opcheck(torch.ops.philtorch.sosfilt.default, (sos, zi, x))
+    torch.library.opcheck(torch.ops.philtorch.sosfilt.default, (sos, None, x))
+
+
+def test_sosfilt_c4_size_matches_lfilter_chain(hip):
+    """At the benchmark's C4 size (B=16, T=480000, 8 sections, fp32) the fused
+    cascade agrees with one lfilter(tdf2) per section on the native 2x2 scan,
+    forward and backward."""
+    import torch
+
+    g = D.rng(D.seed_of("sos-c4"))
+    B, T, S = 16, 480000, 8
+    sos_np = D.sos_coefs(g, (B,), S, np.float32, rhi=0.98)
+    x_np = g.standard_normal((B, T)).astype(np.float32)
+    gy = torch.tensor(g.standard_normal((B, T)).astype(np.float32), device="cuda")
+    res = []
+    for fused in (True, False):
+        sos = torch.tensor(sos_np, device="cuda", requires_grad=True)
+        x = torch.tensor(x_np, device="cuda", requires_grad=True)
+        if fused:
+            y = hip.lti.sosfilt(sos, x)
+        else:
+            y = x
+            for s in range(S):
+                y = hip.lti.lfilter(sos[:, s, :3], sos[:, s, 4:], y, form="tdf2", unroll_factor=1)
+        (y * gy).sum().backward()
+        res.append((y.detach().cpu().numpy(), x.grad.cpu().numpy(), sos.grad.cpu().numpy()))
+        del y, sos, x
+    (y1, gx1, gs1), (y2, gx2, gs2) = res
+    D.check(y1, y2, "y")
+    D.check(gx1, gx2, "grad_x")
+    gs2[..., 3] = gs1[..., 3]  # the lfilter chain does not differentiate a0
+    D.check(gs1, gs2, "grad_sos")

@@ -22,7 +22,7 @@ def test_capi_exports_every_declared_symbol():
 
 def test_capi_host_only_calls():
     lib = capi.load()
-    assert lib.phs_abi_version() == 101
+    assert lib.phs_abi_version() == 102
     for op in capi.OPS.values():
         for dt in capi.DTYPES.values():
             fwd = lib.phs_workspace_size(op, dt, 64, 65536, 0, 0)
@@ -209,3 +209,29 @@ def test_graft_entry_points_importable():
     import __graft_entry__
 
     assert callable(__graft_entry__.build) and callable(__graft_entry__.smoke)
+
+
+def test_capi_sosfilt_host_only_calls():
+    """Sizes and argument errors of the cascade entry points (nothing launches)."""
+    lib = capi.load()
+    for dt in (0, 1):
+        fwd = lib.phs_sosfilt_workspace_size(dt, 16, 480000, 8, 0)
+        bwd = lib.phs_sosfilt_workspace_size(dt, 16, 480000, 8, 1)
+        assert 0 < fwd <= bwd
+        # one fp64 pair per section and every 512th step
+        assert lib.phs_sosfilt_ckpt_size(dt, 16, 480000, 8) == 16 * 8 * ((480000 + 511) // 512) * 16
+    for bad in ((0, 16, 100, 0), (0, 16, 100, 9), (2, 16, 100, 8), (0, -1, 100, 8)):
+        assert lib.phs_sosfilt_workspace_size(*bad, 0) == 0
+        assert lib.phs_sosfilt_ckpt_size(*bad) == 0
+    d = ctypes.c_void_p(16)
+    ws = 1 << 30
+    assert lib.phs_sosfilt_fwd(2, 2, 100, 3, d, 0, None, d, d, None, None, d, ws, None) == capi.PHS_ERR_DTYPE
+    assert lib.phs_sosfilt_fwd(0, 2, 100, 0, d, 0, None, d, d, None, None, d, ws, None) == capi.PHS_ERR_INVALID
+    assert lib.phs_sosfilt_fwd(0, 2, 100, 3, None, 0, None, d, d, None, None, d, ws, None) == capi.PHS_ERR_INVALID
+    assert lib.phs_sosfilt_fwd(0, 2, 100, 3, d, 0, None, d, d, None, None, None, 0, None) == capi.PHS_ERR_WORKSPACE
+    need = lib.phs_sosfilt_workspace_size(0, 2, 100, 3, 0)
+    assert lib.phs_sosfilt_fwd(0, 2, 100, 3, d, 0, None, d, d, None, None, d, need - 1, None) == capi.PHS_ERR_WORKSPACE
+    # coefficient gradients need x and the forward's checkpoints
+    assert lib.phs_sosfilt_bwd(0, 2, 100, 3, d, 0, None, d, d, None, d, d, None, d, ws, None) == capi.PHS_ERR_INVALID
+    assert lib.phs_sosfilt_bwd(1, 2, 100, 3, d, 0, d, None, d, None, d, d, None, d, ws, None) == capi.PHS_ERR_INVALID
+    assert lib.phs_sosfilt_fwd(0, 0, 100, 3, None, 0, None, None, None, None, None, None, 0, None) == capi.PHS_OK

@@ -247,3 +247,66 @@ def test_complex_coefficient_gradient_convention():
     y = oracle.recur(A, zi, x)
     gA, _, _ = oracle.recur_bwd(A, zi, y, gy)
     np.testing.assert_allclose(gA, tA.grad.numpy(), rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- SOS cascade
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("batched", [False, True])
+def test_sosfilt_matches_scipy(dtype, batched):
+    """oracle.sosfilt (one lfilter(tdf2) per section through the oracle's
+    lti_recurN) against scipy.signal.sosfilt, with initial states."""
+    g = D.rng(D.seed_of("oracle-sos", dtype, batched))
+    B, T, S = 3, 700, 5
+    sos = D.sos_coefs(g, (B,) if batched else (), S, np.float64)
+    x = g.standard_normal((B, T))
+    zi = g.standard_normal((B, S, 2))
+    y, zf = oracle.sosfilt(sos.astype(dtype), x.astype(dtype), zi.astype(dtype))
+    for b in range(B):
+        ry, rzf = scipy.signal.sosfilt(sos[b] if batched else sos, x[b], zi=zi[b])
+        D.check(y[b], ry.astype(dtype), f"y row {b}")
+        # zf on the signal's scale: fp32 arithmetic (the reference's own) leaves
+        # ~1e-5 of max|y| on the final states of the later sections
+        err = np.max(np.abs(zf[b] - rzf))
+        assert err <= D.tol(dtype) * max(np.max(np.abs(ry)), np.max(np.abs(rzf))), f"zf row {b}: {err}"
+
+
+def _sos_serial_loop(sos, x, zi):
+    """The TDF-II difference equations of each section, written step by step
+    in torch (y = b0 u + z1; z1 = b1 u - a1 y + z2; z2 = b2 u - a2 y), so that
+    autograd derives the cascade's gradient independently of the oracle."""
+    import torch
+
+    u, zfs = x, []
+    for s in range(sos.shape[-2]):
+        b0, b1, b2, a1, a2 = (sos[..., s, i] for i in (0, 1, 2, 4, 5))
+        z1, z2 = zi[:, s, 0], zi[:, s, 1]
+        ys = []
+        for t in range(x.shape[1]):
+            yt = b0 * u[:, t] + z1
+            z1, z2 = b1 * u[:, t] - a1 * yt + z2, b2 * u[:, t] - a2 * yt
+            ys.append(yt)
+        u = torch.stack(ys, 1)
+        zfs.append(torch.stack([z1, z2], -1))
+    return u, torch.stack(zfs, 1)
+
+
+@pytest.mark.parametrize("batched", [False, True])
+def test_sosfilt_backward_matches_serial_autograd(batched):
+    import torch
+
+    g = D.rng(D.seed_of("oracle-sos-bwd", batched))
+    B, T, S = 3, 30, 4
+    sos = D.sos_coefs(g, (B,) if batched else (), S, np.float64)
+    x = g.standard_normal((B, T))
+    zi = g.standard_normal((B, S, 2))
+    gy = g.standard_normal((B, T))
+    gzf = g.standard_normal((B, S, 2))
+    ts, tx, tz = (torch.tensor(v, requires_grad=True) for v in (sos, x, zi))
+    y, zf = _sos_serial_loop(ts, tx, tz)
+    ((y * torch.tensor(gy)).sum() + (zf * torch.tensor(gzf)).sum()).backward()
+    gs, gzi, gx = oracle.sosfilt_bwd(sos, x, zi, gy, gzf)
+    ref_gs = ts.grad.numpy().copy()
+    ref_gs[..., 3] = 0  # a0 appears in no difference equation
+    D.check(gs, ref_gs, "grad_sos")
+    D.check(gzi, tz.grad.numpy(), "grad_zi")
+    D.check(gx, tx.grad.numpy(), "grad_x")
