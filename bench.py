@@ -14,6 +14,7 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c2      philtorch::lti_recur + lti_recur_backward         (LTI scalar, complex64)
   c3      philtorch::recur2 + recurN_backward               (LPV 2x2)
   c4      8 x (philtorch::lti_recur2 + lti_recurN_backward) (LTI biquad cascade)
+  c4_fused  philtorch::sosfilt + sosfilt_backward              (the same cascade, fused)
 Before every step a 512 MiB buffer is read end to end so the 256 MB Infinity
 Cache holds none of the step's operands (a read sweep, not a write: a write
 would leave dirty lines whose write-back then competes with the step); the
@@ -265,6 +266,52 @@ class SosCascade(Workload):
             _, _, g = oracle.lti_recurN_bwd(A[:rows, s], zi[:rows], ys[s], g, nthreads=nthreads)
 
 
+class SosFused(Workload):
+    """c4_fused: the C4 cascade (16 rows, 8 biquads, T=480000, fp32) through
+    the fused cascade op: philtorch::sosfilt + sosfilt_backward, gradients
+    w.r.t. x and every section's coefficients (b, a)."""
+
+    def __init__(self):
+        import torch
+
+        B, S, T = 16, 8, 480000
+        self.name, self.B, self.T, self.S = "c4_fused", B, T, S
+        self.metric = f"GSamples/s fwd+bwd, fused SOS cascade x{S} (grad x, b, a) B={B} T={T} fp32"
+        g = torch.Generator().manual_seed(4)
+        r = torch.rand(B, S, generator=g, dtype=torch.float64) * 0.48 + 0.5
+        th = torch.rand(B, S, generator=g, dtype=torch.float64) * torch.pi
+        rz = torch.rand(B, S, generator=g, dtype=torch.float64) * 1.2
+        thz = torch.rand(B, S, generator=g, dtype=torch.float64) * torch.pi
+        one = torch.ones(B, S, dtype=torch.float64)
+        sos = torch.stack([one, -2 * rz * torch.cos(thz), rz * rz, one, -2 * r * torch.cos(th), r * r], dim=-1)
+        x = torch.randn(B, T, generator=g, dtype=torch.float64)
+        gy = torch.randn(B, T, generator=g, dtype=torch.float64)
+        self.cpu = [v.float() for v in (sos, x, gy)]
+        self.dev = [v.cuda() for v in self.cpu]
+        self.samples = B * T
+        self.fwd_bytes = 8 * B * T  # read x, write y (state checkpoints: 1/32 of that)
+        self.bwd_bytes = 12 * B * T  # read x and grad y, write grad x
+        self.launches = 1
+
+    def step_fwd(self):
+        import torch
+
+        sos, x, _ = self.dev
+        return torch.ops.philtorch.sosfilt(sos, None, x)
+
+    def step_bwd(self, out):
+        import torch
+
+        sos, x, gy = self.dev
+        return torch.ops.philtorch.sosfilt_backward(sos, x, out[2], gy, None, True)
+
+    def cpu_step(self, rows, steps, nthreads):
+        import oracle
+
+        sos, x, gy = (v.numpy() for v in self.cpu)
+        oracle.sosfilt_bwd(sos[:rows], x[:rows, :steps], None, gy[:rows, :steps], nthreads=nthreads)
+
+
 def make_workload(name):
     if name == "c1":
         return LpvScalar("c1", 64, 65536, "float32")
@@ -278,10 +325,12 @@ def make_workload(name):
         return LpvBiquad()
     if name == "c4":
         return SosCascade()
+    if name == "c4_fused":
+        return SosFused()
     raise ValueError(name)
 
 
-CONFIGS = ("c1", "c2", "c3", "c4", "c5", "c5_f64")
+CONFIGS = ("c1", "c2", "c3", "c4", "c4_fused", "c5", "c5_f64")
 
 
 # ----------------------------------------------------------------------------
@@ -422,6 +471,7 @@ def main() -> int:
                 "c2": "lti_diag_scan_fwd_bwd_C1024_T262144_c64",
                 "c3": "lpv_2x2_scan_fwd_bwd_B32_T1048576_f32",
                 "c4": "lti_sos8_cascade_fwd_bwd_B16_T480000_f32",
+                "c4_fused": "lti_sos8_cascade_fused_fwd_bwd_B16_T480000_f32",
                 "c5": "lpv_scan_fwd_bwd_B8_T16777216_f32",
                 "c5_f64": "lpv_scan_fwd_bwd_B8_T16777216_f64",
             }[w.name],
@@ -439,7 +489,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"scan_kernel ({dominant[0]})",
+            "kernel": f"{'sos_kernel' if w.name == 'c4_fused' else 'scan_kernel'} ({dominant[0]})",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

@@ -14,9 +14,9 @@ namespace {
 // Forward tiles carry four 16-byte vectors per lane and round; the gradient
 // backward keeps four arrays of a lane's steps live, so it takes two.
 template <typename E>
-using SosFwd = SosShape<E, int(64 / sizeof(E)), 2>;
+using SosFwd = SosShape<E, int(64 / sizeof(E)), 2, 3>;
 template <typename E>
-using SosBwd = SosShape<E, int(32 / sizeof(E)), 2>;
+using SosBwd = SosShape<E, int(32 / sizeof(E)), 2, 3>;
 
 struct SosLayout {
   int64_t tiles_per_row = 0;

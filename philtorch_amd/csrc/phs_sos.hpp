@@ -44,9 +44,9 @@ constexpr int kSosMaxSections = 8;     // sections per launch (LDS of the gradie
 
 // Tile shape: W data waves plus one look-back wave; K steps per lane and
 // round (a power of two dividing kSosCkpt), R rounds (1 or 2).
-template <typename E, int K_, int R_>
+template <typename E, int K_, int R_, int W_>
 struct SosShape {
-  static constexpr int kWaves = 3;
+  static constexpr int kWaves = W_;
   static constexpr int kThreads = 64 * (kWaves + 1);
   static constexpr int K = K_;
   static constexpr int R = R_;
