@@ -8,15 +8,19 @@
 #include "phs_launch.hpp"
 #include "phs_sos.hpp"
 
+#include <type_traits>
+
 namespace phs {
 namespace {
 
-// Forward tiles carry four 16-byte vectors per lane and round; the gradient
-// backward keeps four arrays of a lane's steps live, so it takes two.
+// Forward tiles carry eight 16-byte vectors per lane and round (fewer, longer
+// tiles: each section is a row-wide synchronisation of the tiles); the gradient
+// backward keeps four arrays of a lane's steps live, so it takes two, and in
+// fp64 one round (its LDS table of lane states is per lane and round).
 template <typename E>
-using SosFwd = SosShape<E, int(64 / sizeof(E)), 2, 3>;
+using SosFwd = SosShape<E, int(128 / sizeof(E)), 2, 3>;
 template <typename E>
-using SosBwd = SosShape<E, int(32 / sizeof(E)), 2, 3>;
+using SosBwd = std::conditional_t<sizeof(E) == 4, SosShape<E, 8, 2, 3>, SosShape<E, 8, 1, 3>>;
 
 struct SosLayout {
   int64_t tiles_per_row = 0;

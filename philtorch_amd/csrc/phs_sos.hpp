@@ -52,9 +52,6 @@ struct SosShape {
   static constexpr int R = R_;
   static constexpr int kWaveSeg = 64 * K * R;
   static constexpr int kTile = kWaves * kWaveSeg;
-  // multipliers A^(K 2^j), j = 0..5 for the wave scan, 6 for a round, and
-  // the last one for a whole wave segment (A^(64 K R))
-  static constexpr int kPowers = R == 1 ? 7 : 8;
   static_assert(R == 1 || R == 2, "one or two rounds");
   static_assert((K & (K - 1)) == 0 && kSosCkpt % K == 0, "K must be a power of two dividing kSosCkpt");
   static_assert(kTile % kSosCkpt == 0, "tiles start on checkpoints");
@@ -97,15 +94,11 @@ __device__ __forceinline__ SosSec<E> load_sec(const E *row, int s) {
   return {b0, b1 - b0 * a1, b2 - b0 * a2, -a1, -a2};
 }
 
-// Section matrix in compute precision: A forward, A^T for the adjoint.
-template <typename E, bool REV>
+// Section matrix A in compute precision.
+template <typename E>
 __device__ __forceinline__ Mat2<typename Wide<E>::type> sec_matrix(const SosSec<E> &q) {
   using C = typename Wide<E>::type;
-  const C one = C(1), zero = C(0);
-  if constexpr (REV)
-    return {up(q.na1), up(q.na2), one, zero};
-  else
-    return {up(q.na1), one, up(q.na2), zero};
+  return {up(q.na1), C(1), up(q.na2), C(0)};
 }
 
 // P[0] = A^K, P[j] = A^(K 2^j).
@@ -133,61 +126,77 @@ __device__ __forceinline__ Mat2<typename Wide<E>::type> lane_power(const Mat2<ty
   return r;
 }
 
+// Powers of one section's matrix, built by one wave into LDS once per tile
+// and section: pw[n] = A^(K n) for n = 0..64, and seg = A^(64 K R), the
+// matrix part of a whole wave segment.  Every multiplier the lane scans need
+// is one of them, and their transposes serve the adjoint ((A^T)^n = (A^n)^T).
+template <typename C>
+struct SecPowers {
+  Mat2<C> pw[65];
+  Mat2<C> seg;
+};
+
+template <typename E, int K, int R>
+__device__ __forceinline__ void build_powers(SecPowers<typename Wide<E>::type> *t, const SosSec<E> &q, int lane) {
+  using Alg = Block2<E>;
+  Mat2<typename Wide<E>::type> P[7];
+  sec_powers<E, K, 7>(sec_matrix(q), P);
+  t->pw[lane] = lane_power<E, 7>(P, lane);
+  if (lane == 0) {
+    t->pw[64] = P[6];
+    t->seg = R == 2 ? Alg::cmul(P[6], P[6]) : P[6];
+  }
+}
+
+// A o + x (TR: A^T o + x)
+template <bool TR, typename C>
+__device__ __forceinline__ Vec2<C> mva(const Mat2<C> &A, const Vec2<C> &o, const Vec2<C> &x) {
+  if constexpr (TR)
+    return {mad(A.m00, o.v0, mad(A.m10, o.v1, x.v0)), mad(A.m01, o.v0, mad(A.m11, o.v1, x.v1))};
+  else
+    return {mad(A.m00, o.v0, mad(A.m01, o.v1, x.v0)), mad(A.m10, o.v0, mad(A.m11, o.v1, x.v1))};
+}
+
+template <bool TR, typename C>
+__device__ __forceinline__ Mat2<C> maybe_transpose(const Mat2<C> &A) {
+  if constexpr (TR)
+    return {A.m00, A.m10, A.m01, A.m11};
+  else
+    return A;
+}
+
 constexpr int kDppRowShl1 = 0x101, kDppRowShl2 = 0x102, kDppRowShl4 = 0x104, kDppRowShl8 = 0x108;
 constexpr int kDppWaveShl1 = 0x130;
 
-// Per-lane multipliers of the two cross-row steps of lti_scan (computed once
-// per section): after the in-row steps a lane at row position r holds its
-// row's prefix up to itself (UP) or its suffix from itself (!UP); the row
-// total it then adds sits n = r+1 (UP) or 16-r (!UP) lanes away, and in the
-// second step n or n+16 lanes away.
-template <typename C>
-struct RowMul {
-  Mat2<C> q1, q2;
-};
-
-template <bool UP, typename E, int NP>
-__device__ __forceinline__ RowMul<typename Wide<E>::type> row_mul(const Mat2<typename Wide<E>::type> (&P)[NP],
-                                                                 int lane) {
-  using Alg = Block2<E>;
+// Inclusive scan of the vector parts of maps (B^K, v) over the wave, lane 0
+// first (UP) or lane 63 first (!UP), B = A (TR: A^T), multipliers from t:
+// v_i <- v_i + B^(K d) v_(i -+ d) for d = 1, 2, 4, 8 inside each 16-lane row
+// (DPP row shifts); a lane at row position r then holds its row's prefix up
+// to itself (UP) or suffix from itself (!UP), and adds the preceding row's
+// total, r+1 (UP) or 16-r (!UP) lanes away, then that of the preceding pair
+// of rows (UP: DPP row_bcast 15/31; !UP: bpermute from the mirrored lanes).
+template <bool UP, bool TR, typename C>
+__device__ __forceinline__ Vec2<C> lti_scan(Vec2<C> v, int lane, const SecPowers<C> &t) {
   const int r = lane & 15;
-  const Mat2<typename Wide<E>::type> q1 = lane_power<E, NP>(P, UP ? r + 1 : 16 - r);
-  const bool far = UP ? (lane & 16) != 0 : (lane & 16) == 0;
-  return {q1, far ? Alg::cmul(P[4], q1) : q1};
-}
-
-// Inclusive scan of the vector parts of maps (P[0], v) over the wave, lane 0
-// first (UP) or lane 63 first (!UP): v_i <- v_i + A^(K d) v_(i -+ d) for
-// d = 1, 2, 4, 8 inside each 16-lane row (DPP row shifts), then the total of
-// the preceding row (rows 1 and 3 from rows 0 and 2), then that of the
-// preceding pair of rows, each times the lane's own power from `mul` (UP:
-// DPP row_bcast 15/31; !UP: the mirrored lanes through bpermute).
-template <bool UP, typename C, int NP>
-__device__ __forceinline__ Vec2<C> lti_scan(Vec2<C> v, int lane, const Mat2<C> (&P)[NP], const RowMul<C> &mul) {
-  using V = Vec2<C>;
-  auto step = [](const Mat2<C> &A, const V &o, const V &x) -> V {
-    return {mad(A.m00, o.v0, mad(A.m01, o.v1, x.v0)), mad(A.m10, o.v0, mad(A.m11, o.v1, x.v1))};
-  };
-  const int r = lane & 15;
-  V o;
+  Vec2<C> o;
   o = dpp_move<UP ? kDppRowShr1 : kDppRowShl1, 0xF>(v);
-  if (UP ? r >= 1 : r <= 14) v = step(P[0], o, v);
+  if (UP ? r >= 1 : r <= 14) v = mva<TR>(t.pw[1], o, v);
   o = dpp_move<UP ? kDppRowShr2 : kDppRowShl2, 0xF>(v);
-  if (UP ? r >= 2 : r <= 13) v = step(P[1], o, v);
+  if (UP ? r >= 2 : r <= 13) v = mva<TR>(t.pw[2], o, v);
   o = dpp_move<UP ? kDppRowShr4 : kDppRowShl4, 0xF>(v);
-  if (UP ? r >= 4 : r <= 11) v = step(P[2], o, v);
+  if (UP ? r >= 4 : r <= 11) v = mva<TR>(t.pw[4], o, v);
   o = dpp_move<UP ? kDppRowShr8 : kDppRowShl8, 0xF>(v);
-  if (UP ? r >= 8 : r <= 7) v = step(P[3], o, v);
+  if (UP ? r >= 8 : r <= 7) v = mva<TR>(t.pw[8], o, v);
   if constexpr (UP) {
     o = dpp_move<kDppRowBcast15, 0xA>(v);
-    if (lane & 16) v = step(mul.q1, o, v);
+    if (lane & 16) v = mva<TR>(t.pw[r + 1], o, v);
     o = dpp_move<kDppRowBcast31, 0xC>(v);
-    if (lane >= 32) v = step(mul.q2, o, v);
+    if (lane >= 32) v = mva<TR>(t.pw[(lane & 31) + 1], o, v);
   } else {
     o = shfl_from(v, ((lane | 15) + 1) & 63);
-    if ((lane & 16) == 0) v = step(mul.q1, o, v);
+    if ((lane & 16) == 0) v = mva<TR>(t.pw[16 - r], o, v);
     o = shfl_from(v, 32);
-    if (lane < 32) v = step(mul.q2, o, v);
+    if (lane < 32) v = mva<TR>(t.pw[32 - (lane & 31)], o, v);
   }
   return v;
 }
@@ -350,17 +359,19 @@ __device__ __forceinline__ Vec2<E> load_pair(const E *p, bool valid) {
 // computed by one wave straight from the inputs: the cascade (forward) or the
 // adjoint cascade (REV) over the whole row prefix in scan order, 64*K steps
 // per iteration, every section up to s_target carrying its state across
-// iterations in LDS (`carry`, one entry per section).  Taken only when
-// predecessors did not publish within the poll budget.
+// iterations.  `lds` (the look-back staging area, free by then) holds the
+// carries and the section's powers.  Taken only when predecessors did not
+// publish within the poll budget.
 template <typename E, class Sh, bool REV>
 __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const SosArgs<E> &a, int64_t b,
                                                                         int s_target, int64_t span, int lane,
-                                                                        Vec2<typename Wide<E>::type> *carry) {
+                                                                        uint64_t *lds) {
   using Alg = Block2<E>;
   using C = typename Wide<E>::type;
   using V = Vec2<C>;
-  using Mt = Mat2<C>;
-  constexpr int K = Sh::K, NP = Sh::kPowers;
+  constexpr int K = Sh::K;
+  V *carry = reinterpret_cast<V *>(lds);
+  SecPowers<C> *tab = reinterpret_cast<SecPowers<C> *>(lds + kSosMaxSections * (sizeof(V) / sizeof(uint64_t)));
   const int S = a.S;
   const int64_t T = a.T_len;
   const int64_t row_end = a.tiles_per_row * Sh::kTile;
@@ -385,17 +396,17 @@ __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const S
     for (int i = 0; i < n; ++i) {
       const int s = REV ? S - 1 - i : i;
       const SosSec<E> q = load_sec(sosrow, s);
-      Mt P[NP];
-      sec_powers<E, K, NP>(sec_matrix<E, REV>(q), P);
-      const Mt pw = lane_power<E, NP>(P, lane);
-      const RowMul<C> mul = row_mul<true, E, NP>(P, lane);
+      wave_sync();
+      build_powers<E, K, Sh::R>(tab, q, lane);
+      wave_sync();
       const Vec2<E> gzf = load_pair(a.virt + (b * S + s) * 2, REV && a.virt != nullptr);
       V v = REV ? fold_adj<E, K>(q, u, t0, T, gzf) : fold_fwd<E, K>(q, u);
-      v = lti_scan<true>(v, lane, P, mul);
+      v = lti_scan<true, REV>(v, lane, *tab);
       const V tot = read_lane(v, 63);
       const V ex = lane_prev<true>(v, lane, Alg::szero());
       const V c = carry[i];
-      const Vec2<E> h = Alg::store_s(Alg::affine(pw, c, ex));
+      const Vec2<E> h = Alg::store_s(mva<REV>(tab->pw[lane], c, ex));
+      const V cn = mva<REV>(tab->pw[64], c, tot);
       if constexpr (REV) {
         SosAcc<E> acc = none;
         const E unused[1] = {zero};
@@ -404,7 +415,7 @@ __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const S
         run_fwd<E, K>(q, h, u, t0, T, nullptr);
       }
       wave_sync();
-      if (lane == 0) carry[i] = Alg::affine(P[6], c, tot);
+      if (lane == 0) carry[i] = cn;
       wave_sync();
     }
   }
@@ -416,17 +427,22 @@ __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const S
 // ------------------------------------------------------------ the kernel
 // REV : adjoint cascade (backward); GRAD: also the coefficient gradients
 // (backward only: recomputes the forward inside the tile from a.x and a.ckpt).
-// Barriers: claim; with GRAD, one per section while the forward is
-// recomputed; then two per section (wave aggregates ready, entry state ready).
+//
+// The tile visits its sections in order (backward: in reverse order, after,
+// with GRAD, a forward visit of every section).  The look-back wave builds
+// each visit's matrix powers two visits ahead into one of three LDS buffers
+// (keeping the data waves' registers free of matrices) and resolves each
+// section's entry state.  Barriers: claim; powers of the first two visits; one per
+// forward-recompute visit (GRAD); two per look-back visit (wave aggregates
+// ready, entry state ready).
 template <typename E, class Sh, bool REV, bool GRAD>
 __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
   using Alg = Block2<E>;
   using C = typename Wide<E>::type;
   using V = Vec2<C>;
-  using Mt = Mat2<C>;
   using M = Map<Alg>;
   using SV = Vec2<E>;
-  constexpr int K = Sh::K, R = Sh::R, W = Sh::kWaves, NP = Sh::kPowers;
+  constexpr int K = Sh::K, R = Sh::R, W = Sh::kWaves;
   constexpr int kS = StatusShape<Alg>::kStride;
   static_assert(!GRAD || REV, "coefficient gradients come with the backward");
 
@@ -435,7 +451,8 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
   __shared__ V s_in;
   __shared__ unsigned s_id, s_tag;
   __shared__ uint64_t s_look[StatusShape<Alg>::kLookWords];
-  __shared__ M s_fagg[GRAD ? 2 : 1][W];  // forward recompute: wave aggregates, two sections in flight
+  __shared__ M s_fagg[GRAD ? 2 : 1][W];  // forward recompute: wave aggregates, two visits in flight
+  __shared__ SecPowers<C> s_pow[3];
   extern __shared__ __align__(16) unsigned char sos_dyn[];  // GRAD: lane entry states [S][W][R][64]
   SV *s_laneh = reinterpret_cast<SV *>(sos_dyn);
 
@@ -457,33 +474,47 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
   // the row's state before its first step in scan order; backward it is
   // dL/dzf only when no padded step t = T carries it
   const bool row_virt = !REV || (T % Sh::kTile) == 0;
+  // visit v -> section: forward 0..S-1; backward S-1..0, after 0..S-1 with GRAD
+  const int nvis = GRAD ? 2 * S : S;
+  auto vis_sec = [S](int v) { return GRAD ? (v < S ? v : 2 * S - 1 - v) : (REV ? S - 1 - v : v); };
 
   if (w == W) {
     // ================= look-back wave
-    if constexpr (GRAD)
-      for (int i = 0; i < S; ++i) __syncthreads();  // forward recompute barriers
+    build_powers<E, K, R>(&s_pow[0], load_sec(sosrow, vis_sec(0)), lane);
+    if (nvis > 1) build_powers<E, K, R>(&s_pow[1], load_sec(sosrow, vis_sec(1)), lane);
+    __syncthreads();  // powers of the first two visits
+    int v = 0;
+    if constexpr (GRAD) {
+      for (; v < S; ++v) {
+        __syncthreads();  // forward recompute: wave aggregates of visit v
+        if (v + 2 < nvis) build_powers<E, K, R>(&s_pow[(v + 2) % 3], load_sec(sosrow, vis_sec(v + 2)), lane);
+      }
+    }
     auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
-    for (int i = 0; i < S; ++i) {
-      const int s = REV ? S - 1 - i : i;
+    for (; v < nvis; ++v) {
+      const int s = vis_sec(v);
       uint64_t *row_status = a.status + ((b * S + s) * tiles) * kS;
       const SV vs = load_pair(a.virt + (b * S + s) * 2, a.virt != nullptr && row_virt);
       const V virt = {up(vs.v0), up(vs.v1)};
-      __syncthreads();  // wave aggregates are in s_wagg
-      M v = lane < W ? s_wagg[lane] : map_identity<Alg>();
-      v = wave_scan_incl(v, lane, op);
-      const M wex = wave_shift_up(v, lane, map_identity<Alg>());
-      if (lane < W) s_wpre[lane] = wex;
-      const M tagg = read_lane(v, W - 1);
+      // (polling for the predecessors before the aggregates are in measured
+      // slower: a tile's predecessors reach each section about when it does)
       V yin = virt;
+      __syncthreads();  // wave aggregates are in s_wagg
+      M m = lane < W ? s_wagg[lane] : map_identity<Alg>();
+      m = wave_scan_incl(m, lane, op);
+      const M wex = wave_shift_up(m, lane, map_identity<Alg>());
+      if (lane < W) s_wpre[lane] = wex;
+      const M tagg = read_lane(m, W - 1);
       if (qs > 0) {
         if (lane == 0) publish(row_status + qs * kS + StatusShape<Alg>::kIncWords, tagg, tag);
         Lookback<Alg> lb = lookback_start<Alg>(qs);
         if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
-          yin = sos_prefix_fallback<E, Sh, REV>(a, b, s, qs * Sh::kTile, lane, reinterpret_cast<V *>(s_look));
+          yin = sos_prefix_fallback<E, Sh, REV>(a, b, s, qs * Sh::kTile, lane, s_look);
       }
       if (qs + 1 < tiles && lane == 0) publish(row_status + qs * kS, apply<Alg>(tagg, yin), tag);
       if (lane == 0) s_in = yin;
       __syncthreads();  // entry state is in s_in
+      if (v + 2 < nvis) build_powers<E, K, R>(&s_pow[(v + 2) % 3], load_sec(sosrow, vis_sec(v + 2)), lane);
     }
     return;
   }
@@ -501,61 +532,62 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
   E U[R][K];  // forward: input of the current section;  backward: its upstream gradient
 #pragma unroll
   for (int r = 0; r < R; ++r) load_chunk<E, K>(a.in + b * T, chunk0(r), T, vec, U[r], zero);
-
-  // ---- backward with coefficient gradients: recompute the forward cascade
-  // over the tile from its checkpoints (time order is descending scan order),
-  // keeping every lane's entry state of every section in LDS
   E X[GRAD ? R : 1][GRAD ? K : 1];
   E F[GRAD ? R : 1][GRAD ? K : 1];  // forward values of the current section
   if constexpr (GRAD) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      load_chunk<E, K>(a.x + b * T, chunk0(r), T, vec, X[r], zero);
+    for (int r = 0; r < R; ++r) load_chunk<E, K>(a.x + b * T, chunk0(r), T, vec, X[r], zero);
+  }
+  __syncthreads();  // powers of the first two visits
+  int v = 0;
+
+  // ---- backward with coefficient gradients: recompute the forward cascade
+  // over the tile from its checkpoints (time order is descending scan order),
+  // keeping every lane's entry state of every section in LDS
+  if constexpr (GRAD) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int k = 0; k < K; ++k) F[r][k] = X[r][k];
-    }
     const int64_t ck0 = (qf * Sh::kTile) / kSosCkpt;
-    for (int s = 0; s < S; ++s) {
+    for (; v < S; ++v) {
+      const int s = v;
       const SosSec<E> q = load_sec(sosrow, s);
-      Mt P[NP];
-      sec_powers<E, K, NP>(sec_matrix<E, false>(q), P);
-      const RowMul<C> mul = row_mul<false, E, NP>(P, lane);
+      const SecPowers<C> &t = s_pow[v % 3];
       V ex[R], tot[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        V v = fold_fwd<E, K>(q, F[r]);
-        v = lti_scan<false>(v, lane, P, mul);
-        tot[r] = read_lane(v, 0);
-        ex[r] = lane_prev<false>(v, lane, Alg::szero());
+        V x = fold_fwd<E, K>(q, F[r]);
+        x = lti_scan<false, false>(x, lane, t);
+        tot[r] = read_lane(x, 0);
+        ex[r] = lane_prev<false>(x, lane, Alg::szero());
       }
       V agg = tot[R - 1];
 #pragma unroll
-      for (int r = R - 2; r >= 0; --r) agg = Alg::affine(P[6], agg, tot[r]);
-      if (lane == 0) s_fagg[s & 1][w] = M{P[NP - 1], agg};
-      __syncthreads();  // forward wave aggregates of section s
+      for (int r = R - 2; r >= 0; --r) agg = mva<false>(t.pw[64], agg, tot[r]);
+      if (lane == 0) s_fagg[s & 1][w] = M{t.seg, agg};
+      __syncthreads();  // forward wave aggregates of visit v
       V H = a.ckpt[(b * S + s) * a.n_ckpt + ck0];
       for (int w2 = W - 1; w2 > w; --w2) H = apply<Alg>(s_fagg[s & 1][w2], H);
-      const Mt pwr = lane_power<E, NP>(P, 63 - lane);
 #pragma unroll
       for (int r = R - 1; r >= 0; --r) {
-        const SV h = Alg::store_s(Alg::affine(pwr, H, ex[r]));
+        const SV h = Alg::store_s(mva<false>(t.pw[63 - lane], H, ex[r]));
         s_laneh[((s * W + w) * R + r) * 64 + lane] = h;
         run_fwd<E, K>(q, h, F[r], chunk0(r), T, nullptr);
-        H = Alg::affine(P[6], H, tot[r]);
+        H = mva<false>(t.pw[64], H, tot[r]);
       }
     }
     // F now holds the cascade output: the forward output of section S-1
   }
 
-  for (int i = 0; i < S; ++i) {
-    const int s = REV ? S - 1 - i : i;
+  for (; v < nvis; ++v) {
+    const int s = vis_sec(v);
     const SosSec<E> q = load_sec(sosrow, s);
-    Mt P[NP];
-    sec_powers<E, K, NP>(sec_matrix<E, REV>(q), P);
+    const SecPowers<C> &t = s_pow[v % 3];
     const SV gzf = load_pair(a.virt + (b * S + s) * 2, REV && a.virt != nullptr);
 
     // forward input of section s, recomputed from x through sections < s
-    // (F keeps its output, the previous iteration's input)
+    // (F keeps its output, the previous visit's input)
     E Uf[GRAD ? R : 1][GRAD ? K : 1];
     if constexpr (GRAD) {
 #pragma unroll
@@ -571,23 +603,21 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
     }
 
     // ---- pass 1: lane folds, wave scan, round chaining
-    const RowMul<C> mul = row_mul<true, E, NP>(P, lane);
     V ex[R], tot[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      V v = REV ? fold_adj<E, K>(q, U[r], chunk0(r), T, gzf) : fold_fwd<E, K>(q, U[r]);
-      v = lti_scan<true>(v, lane, P, mul);
-      tot[r] = read_lane(v, 63);
-      ex[r] = lane_prev<true>(v, lane, Alg::szero());
+      V x = REV ? fold_adj<E, K>(q, U[r], chunk0(r), T, gzf) : fold_fwd<E, K>(q, U[r]);
+      x = lti_scan<true, REV>(x, lane, t);
+      tot[r] = read_lane(x, 63);
+      ex[r] = lane_prev<true>(x, lane, Alg::szero());
     }
     V agg = tot[0];
 #pragma unroll
-    for (int r = 1; r < R; ++r) agg = Alg::affine(P[6], agg, tot[r]);
-    if (lane == 0) s_wagg[w] = M{P[NP - 1], agg};
+    for (int r = 1; r < R; ++r) agg = mva<REV>(t.pw[64], agg, tot[r]);
+    if (lane == 0) s_wagg[w] = M{maybe_transpose<REV>(t.seg), agg};
     __syncthreads();  // wave aggregates are in s_wagg
     __syncthreads();  // entry state is in s_in
     V H = apply<Alg>(s_wpre[w], s_in);
-    const Mt pwr = lane_power<E, NP>(P, lane);
 
     // ---- pass 2
     SosAcc<E> acc{};
@@ -595,7 +625,7 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int64_t t0 = chunk0(r);
-      const V hc = Alg::affine(pwr, H, ex[r]);
+      const V hc = mva<REV>(t.pw[lane], H, ex[r]);
       const SV h = Alg::store_s(hc);
       if constexpr (REV) {
         acc = SosAcc<E>{};
@@ -612,7 +642,7 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
         if (a.ckpt && (t0 % kSosCkpt) == 0 && t0 < T) a.ckpt[(b * S + s) * a.n_ckpt + t0 / kSosCkpt] = hc;
         run_fwd<E, K>(q, h, U[r], t0, T, a.fin ? a.fin + (b * S + s) * 2 : nullptr);
       }
-      H = Alg::affine(P[6], H, tot[r]);
+      H = mva<REV>(t.pw[64], H, tot[r]);
     }
     if constexpr (GRAD) {
       auto sum = [](const SosAcc<C> &p, const SosAcc<C> &o) -> SosAcc<C> {
