@@ -13,12 +13,13 @@
 namespace phs {
 namespace {
 
-// Forward tiles carry eight 16-byte vectors per lane and round (fewer, longer
-// tiles: each section is a row-wide synchronisation of the tiles); the gradient
-// backward keeps four arrays of a lane's steps live, so it takes two, and in
-// fp64 one round (its LDS table of lane states is per lane and round).
+// Forward tiles carry four 16-byte vectors per lane and round and four rounds,
+// whose step chains run interleaved (fewer, longer tiles: each section is a
+// row-wide synchronisation of the tiles); the gradient backward keeps four
+// arrays of a lane's steps live, so it takes two vectors per round, and in fp64
+// one round (its LDS table of lane states is per lane and round).
 template <typename E>
-using SosFwd = SosShape<E, int(128 / sizeof(E)), 2, 3>;
+using SosFwd = SosShape<E, int(64 / sizeof(E)), 4, 3>;
 template <typename E>
 using SosBwd = std::conditional_t<sizeof(E) == 4, SosShape<E, 8, 2, 3>, SosShape<E, 8, 1, 3>>;
 

@@ -43,7 +43,7 @@ constexpr int kSosCkpt = 512;          // steps between forward state checkpoint
 constexpr int kSosMaxSections = 8;     // sections per launch (LDS of the gradient backward)
 
 // Tile shape: W data waves plus one look-back wave; K steps per lane and
-// round (a power of two dividing kSosCkpt), R rounds (1 or 2).
+// round (a power of two dividing kSosCkpt), R rounds (a power of two).
 template <typename E, int K_, int R_, int W_>
 struct SosShape {
   static constexpr int kWaves = W_;
@@ -52,7 +52,7 @@ struct SosShape {
   static constexpr int R = R_;
   static constexpr int kWaveSeg = 64 * K * R;
   static constexpr int kTile = kWaves * kWaveSeg;
-  static_assert(R == 1 || R == 2, "one or two rounds");
+  static_assert(R >= 1 && (R & (R - 1)) == 0, "a power-of-two number of rounds");
   static_assert((K & (K - 1)) == 0 && kSosCkpt % K == 0, "K must be a power of two dividing kSosCkpt");
   static_assert(kTile % kSosCkpt == 0, "tiles start on checkpoints");
   static_assert((K * sizeof(E)) % 16 == 0, "chunks must be whole 16-byte vectors");
@@ -144,7 +144,10 @@ __device__ __forceinline__ void build_powers(SecPowers<typename Wide<E>::type> *
   t->pw[lane] = lane_power<E, 7>(P, lane);
   if (lane == 0) {
     t->pw[64] = P[6];
-    t->seg = R == 2 ? Alg::cmul(P[6], P[6]) : P[6];
+    Mat2<typename Wide<E>::type> seg = P[6];
+#pragma unroll
+    for (int r = 1; r < R; r <<= 1) seg = Alg::cmul(seg, seg);
+    t->seg = seg;
   }
 }
 
@@ -168,37 +171,56 @@ __device__ __forceinline__ Mat2<C> maybe_transpose(const Mat2<C> &A) {
 constexpr int kDppRowShl1 = 0x101, kDppRowShl2 = 0x102, kDppRowShl4 = 0x104, kDppRowShl8 = 0x108;
 constexpr int kDppWaveShl1 = 0x130;
 
-// Inclusive scan of the vector parts of maps (B^K, v) over the wave, lane 0
+// Inclusive scans of the vector parts of maps (B^K, v[n]) over the wave, for
+// N independent values at once (their latency chains interleave), lane 0
 // first (UP) or lane 63 first (!UP), B = A (TR: A^T), multipliers from t:
 // v_i <- v_i + B^(K d) v_(i -+ d) for d = 1, 2, 4, 8 inside each 16-lane row
 // (DPP row shifts); a lane at row position r then holds its row's prefix up
 // to itself (UP) or suffix from itself (!UP), and adds the preceding row's
 // total, r+1 (UP) or 16-r (!UP) lanes away, then that of the preceding pair
 // of rows (UP: DPP row_bcast 15/31; !UP: bpermute from the mirrored lanes).
-template <bool UP, bool TR, typename C>
-__device__ __forceinline__ Vec2<C> lti_scan(Vec2<C> v, int lane, const SecPowers<C> &t) {
+template <bool UP, bool TR, typename C, int N>
+__device__ __forceinline__ void lti_scan(Vec2<C> (&v)[N], int lane, const SecPowers<C> &t) {
   const int r = lane & 15;
-  Vec2<C> o;
-  o = dpp_move<UP ? kDppRowShr1 : kDppRowShl1, 0xF>(v);
-  if (UP ? r >= 1 : r <= 14) v = mva<TR>(t.pw[1], o, v);
-  o = dpp_move<UP ? kDppRowShr2 : kDppRowShl2, 0xF>(v);
-  if (UP ? r >= 2 : r <= 13) v = mva<TR>(t.pw[2], o, v);
-  o = dpp_move<UP ? kDppRowShr4 : kDppRowShl4, 0xF>(v);
-  if (UP ? r >= 4 : r <= 11) v = mva<TR>(t.pw[4], o, v);
-  o = dpp_move<UP ? kDppRowShr8 : kDppRowShl8, 0xF>(v);
-  if (UP ? r >= 8 : r <= 7) v = mva<TR>(t.pw[8], o, v);
-  if constexpr (UP) {
-    o = dpp_move<kDppRowBcast15, 0xA>(v);
-    if (lane & 16) v = mva<TR>(t.pw[r + 1], o, v);
-    o = dpp_move<kDppRowBcast31, 0xC>(v);
-    if (lane >= 32) v = mva<TR>(t.pw[(lane & 31) + 1], o, v);
-  } else {
-    o = shfl_from(v, ((lane | 15) + 1) & 63);
-    if ((lane & 16) == 0) v = mva<TR>(t.pw[16 - r], o, v);
-    o = shfl_from(v, 32);
-    if (lane < 32) v = mva<TR>(t.pw[32 - (lane & 31)], o, v);
+  Vec2<C> o[N];
+#define PHS_SOS_LEVEL(CTRL_UP, CTRL_DOWN, COND_UP, COND_DOWN, MAT)            \
+  {                                                                           \
+    _Pragma("unroll") for (int n = 0; n < N; ++n) o[n] = dpp_move<UP ? CTRL_UP : CTRL_DOWN, 0xF>(v[n]); \
+    if (UP ? (COND_UP) : (COND_DOWN)) {                                       \
+      const Mat2<C> m = (MAT);                                                \
+      _Pragma("unroll") for (int n = 0; n < N; ++n) v[n] = mva<TR>(m, o[n], v[n]); \
+    }                                                                         \
   }
-  return v;
+  PHS_SOS_LEVEL(kDppRowShr1, kDppRowShl1, r >= 1, r <= 14, t.pw[1])
+  PHS_SOS_LEVEL(kDppRowShr2, kDppRowShl2, r >= 2, r <= 13, t.pw[2])
+  PHS_SOS_LEVEL(kDppRowShr4, kDppRowShl4, r >= 4, r <= 11, t.pw[4])
+  PHS_SOS_LEVEL(kDppRowShr8, kDppRowShl8, r >= 8, r <= 7, t.pw[8])
+#undef PHS_SOS_LEVEL
+  if constexpr (UP) {
+    const Mat2<C> m1 = t.pw[r + 1], m2 = t.pw[(lane & 31) + 1];
+#pragma unroll
+    for (int n = 0; n < N; ++n) o[n] = dpp_move<kDppRowBcast15, 0xA>(v[n]);
+    if (lane & 16)
+#pragma unroll
+      for (int n = 0; n < N; ++n) v[n] = mva<TR>(m1, o[n], v[n]);
+#pragma unroll
+    for (int n = 0; n < N; ++n) o[n] = dpp_move<kDppRowBcast31, 0xC>(v[n]);
+    if (lane >= 32)
+#pragma unroll
+      for (int n = 0; n < N; ++n) v[n] = mva<TR>(m2, o[n], v[n]);
+  } else {
+    const Mat2<C> m1 = t.pw[16 - r], m2 = t.pw[32 - (lane & 31)];
+#pragma unroll
+    for (int n = 0; n < N; ++n) o[n] = shfl_from(v[n], ((lane | 15) + 1) & 63);
+    if ((lane & 16) == 0)
+#pragma unroll
+      for (int n = 0; n < N; ++n) v[n] = mva<TR>(m1, o[n], v[n]);
+#pragma unroll
+    for (int n = 0; n < N; ++n) o[n] = shfl_from(v[n], 32);
+    if (lane < 32)
+#pragma unroll
+      for (int n = 0; n < N; ++n) v[n] = mva<TR>(m2, o[n], v[n]);
+  }
 }
 
 // Value of the previous lane in scan order (the first lane gets `first`).
@@ -349,6 +371,125 @@ __device__ __forceinline__ void run_adj(const SosSec<E> &q, Vec2<E> mu, E (&g)[K
   }
 }
 
+// The same over N chunks of one lane at once (independent chains, so their
+// latencies overlap); chunk n starts at t0[n].  Only when a chunk reaches past
+// the row end does a chunk take the single-chunk path with its bounds checks.
+template <typename E, int K, int N>
+__device__ __forceinline__ bool chunks_full(const int64_t (&t0)[N], int64_t T) {
+  bool full = true;
+#pragma unroll
+  for (int n = 0; n < N; ++n) full = full && t0[n] + K <= T;
+  return full;
+}
+
+template <typename E, int K, int N>
+__device__ __forceinline__ void fold_fwd_n(const SosSec<E> &q, const E (&u)[N][K],
+                                           Vec2<typename Wide<E>::type> (&out)[N]) {
+  E v0[N], v1[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) v0[n] = v1[n] = E(0);
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const E x = u[n][k];
+      const E n0 = fma(q.na1, v0[n], fma(q.c0, x, v1[n]));
+      v1[n] = fma(q.na2, v0[n], q.c1 * x);
+      v0[n] = n0;
+    }
+#pragma unroll
+  for (int n = 0; n < N; ++n) out[n] = {up(v0[n]), up(v1[n])};
+}
+
+template <typename E, int K, int N>
+__device__ __forceinline__ void run_fwd_n(const SosSec<E> &q, Vec2<E> (&h)[N], E (&u)[N][K],
+                                          const int64_t (&t0)[N], int64_t T, E *zf) {
+  if (chunks_full<E, K, N>(t0, T)) {
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const E x = u[n][k];
+        u[n][k] = fma(q.b0, x, h[n].v0);
+        const E n0 = fma(q.na1, h[n].v0, fma(q.c0, x, h[n].v1));
+        h[n].v1 = fma(q.na2, h[n].v0, q.c1 * x);
+        h[n].v0 = n0;
+      }
+    if (zf)
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+        if (t0[n] + K == T) {
+          zf[0] = h[n].v0;
+          zf[1] = h[n].v1;
+        }
+  } else {
+#pragma unroll
+    for (int n = 0; n < N; ++n) run_fwd<E, K>(q, h[n], u[n], t0[n], T, zf);
+  }
+}
+
+template <typename E, int K, int N>
+__device__ __forceinline__ void fold_adj_n(const SosSec<E> &q, const E (&g)[N][K], const int64_t (&t0)[N],
+                                           int64_t T, const Vec2<E> &gzf, Vec2<typename Wide<E>::type> (&out)[N]) {
+  if (chunks_full<E, K, N>(t0, T)) {
+    E m0[N], m1[N];
+#pragma unroll
+    for (int n = 0; n < N; ++n) m0[n] = m1[n] = E(0);
+#pragma unroll
+    for (int kk = 0; kk < K; ++kk)
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const E n0 = fma(q.na1, m0[n], fma(q.na2, m1[n], g[n][K - 1 - kk]));
+        m1[n] = m0[n];
+        m0[n] = n0;
+      }
+#pragma unroll
+    for (int n = 0; n < N; ++n) out[n] = {up(m0[n]), up(m1[n])};
+  } else {
+#pragma unroll
+    for (int n = 0; n < N; ++n) out[n] = fold_adj<E, K>(q, g[n], t0[n], T, gzf);
+  }
+}
+
+template <typename E, int K, int N, bool GRAD>
+__device__ __forceinline__ void run_adj_n(const SosSec<E> &q, Vec2<E> (&mu)[N], E (&g)[N][K],
+                                          const int64_t (&t0)[N], int64_t T, const Vec2<E> &gzf, E *gzi,
+                                          const E (&u)[GRAD ? N : 1][GRAD ? K : 1],
+                                          const E (&y)[GRAD ? N : 1][GRAD ? K : 1], SosAcc<E> (&acc)[N]) {
+  if (chunks_full<E, K, N>(t0, T)) {
+#pragma unroll
+    for (int kk = 0; kk < K; ++kk)
+#pragma unroll
+      for (int n = 0; n < N; ++n) {
+        const int k = K - 1 - kk;
+        const E gk = g[n][k];
+        if constexpr (GRAD) {
+          const E uk = u[n][k];
+          const E h0 = fma(-q.b0, uk, y[n][k]);
+          acc[n].a1 = fma(mu[n].v0, h0, acc[n].a1);
+          acc[n].a2 = fma(mu[n].v1, h0, acc[n].a2);
+          acc[n].c0 = fma(mu[n].v0, uk, acc[n].c0);
+          acc[n].c1 = fma(mu[n].v1, uk, acc[n].c1);
+          acc[n].b0 = fma(gk, uk, acc[n].b0);
+        }
+        g[n][k] = fma(q.c0, mu[n].v0, fma(q.c1, mu[n].v1, q.b0 * gk));
+        const E n0 = fma(q.na1, mu[n].v0, fma(q.na2, mu[n].v1, gk));
+        mu[n].v1 = mu[n].v0;
+        mu[n].v0 = n0;
+      }
+    if (gzi)
+#pragma unroll
+      for (int n = 0; n < N; ++n)
+        if (t0[n] == 0) {
+          gzi[0] = mu[n].v0;
+          gzi[1] = mu[n].v1;
+        }
+  } else {
+#pragma unroll
+    for (int n = 0; n < N; ++n) run_adj<E, K, GRAD>(q, mu[n], g[n], t0[n], T, gzf, gzi, u[GRAD ? n : 0], y[GRAD ? n : 0], acc[n]);
+  }
+}
+
 template <typename E>
 __device__ __forceinline__ Vec2<E> load_pair(const E *p, bool valid) {
   return valid ? Vec2<E>{p[0], p[1]} : Vec2<E>{E(0), E(0)};
@@ -391,8 +532,9 @@ __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const S
   const SosAcc<E> none{};
   for (int64_t off = 0; off < span; off += 64 * K) {
     const int64_t t0 = REV ? row_end - off - int64_t(lane + 1) * K : off + int64_t(lane) * K;
-    E u[K];
-    load_chunk<E, K>(inrow, t0, T, a.vec_ok != 0, u, zero);
+    const int64_t t0s[1] = {t0};
+    E u[1][K];
+    load_chunk<E, K>(inrow, t0, T, a.vec_ok != 0, u[0], zero);
     for (int i = 0; i < n; ++i) {
       const int s = REV ? S - 1 - i : i;
       const SosSec<E> q = load_sec(sosrow, s);
@@ -400,19 +542,23 @@ __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const S
       build_powers<E, K, Sh::R>(tab, q, lane);
       wave_sync();
       const Vec2<E> gzf = load_pair(a.virt + (b * S + s) * 2, REV && a.virt != nullptr);
-      V v = REV ? fold_adj<E, K>(q, u, t0, T, gzf) : fold_fwd<E, K>(q, u);
-      v = lti_scan<true, REV>(v, lane, *tab);
-      const V tot = read_lane(v, 63);
-      const V ex = lane_prev<true>(v, lane, Alg::szero());
+      V v[1];
+      if constexpr (REV)
+        fold_adj_n<E, K, 1>(q, u, t0s, T, gzf, v);
+      else
+        fold_fwd_n<E, K, 1>(q, u, v);
+      lti_scan<true, REV>(v, lane, *tab);
+      const V tot = read_lane(v[0], 63);
+      const V ex = lane_prev<true>(v[0], lane, Alg::szero());
       const V c = carry[i];
-      const Vec2<E> h = Alg::store_s(mva<REV>(tab->pw[lane], c, ex));
+      Vec2<E> h[1] = {Alg::store_s(mva<REV>(tab->pw[lane], c, ex))};
       const V cn = mva<REV>(tab->pw[64], c, tot);
       if constexpr (REV) {
-        SosAcc<E> acc = none;
-        const E unused[1] = {zero};
-        run_adj<E, K, false>(q, h, u, t0, T, gzf, nullptr, unused, unused, acc);
+        SosAcc<E> acc[1] = {none};
+        const E unused[1][1] = {{zero}};
+        run_adj_n<E, K, 1, false>(q, h, u, t0s, T, gzf, nullptr, unused, unused, acc);
       } else {
-        run_fwd<E, K>(q, h, u, t0, T, nullptr);
+        run_fwd_n<E, K, 1>(q, h, u, t0s, T, nullptr);
       }
       wave_sync();
       if (lane == 0) carry[i] = cn;
@@ -528,6 +674,9 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
     return seg0 + int64_t(pr) * 64 * K + int64_t(pl) * K;
   };
   const E zero = E(0);
+  int64_t t0s[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) t0s[r] = chunk0(r);
 
   E U[R][K];  // forward: input of the current section;  backward: its upstream gradient
 #pragma unroll
@@ -554,13 +703,13 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
       const int s = v;
       const SosSec<E> q = load_sec(sosrow, s);
       const SecPowers<C> &t = s_pow[v % 3];
-      V ex[R], tot[R];
+      V ex[R], tot[R], x[R];
+      fold_fwd_n<E, K, R>(q, F, x);
+      lti_scan<false, false>(x, lane, t);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        V x = fold_fwd<E, K>(q, F[r]);
-        x = lti_scan<false, false>(x, lane, t);
-        tot[r] = read_lane(x, 0);
-        ex[r] = lane_prev<false>(x, lane, Alg::szero());
+        tot[r] = read_lane(x[r], 0);
+        ex[r] = lane_prev<false>(x[r], lane, Alg::szero());
       }
       V agg = tot[R - 1];
 #pragma unroll
@@ -569,13 +718,14 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
       __syncthreads();  // forward wave aggregates of visit v
       V H = a.ckpt[(b * S + s) * a.n_ckpt + ck0];
       for (int w2 = W - 1; w2 > w; --w2) H = apply<Alg>(s_fagg[s & 1][w2], H);
+      SV h[R];
 #pragma unroll
       for (int r = R - 1; r >= 0; --r) {
-        const SV h = Alg::store_s(mva<false>(t.pw[63 - lane], H, ex[r]));
-        s_laneh[((s * W + w) * R + r) * 64 + lane] = h;
-        run_fwd<E, K>(q, h, F[r], chunk0(r), T, nullptr);
+        h[r] = Alg::store_s(mva<false>(t.pw[63 - lane], H, ex[r]));
+        s_laneh[((s * W + w) * R + r) * 64 + lane] = h[r];
         H = mva<false>(t.pw[64], H, tot[r]);
       }
+      run_fwd_n<E, K, R>(q, h, F, t0s, T, nullptr);
     }
     // F now holds the cascade output: the forward output of section S-1
   }
@@ -596,20 +746,24 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
         for (int k = 0; k < K; ++k) Uf[r][k] = X[r][k];
       for (int j = 0; j < s; ++j) {
         const SosSec<E> qj = load_sec(sosrow, j);
+        SV hj[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-          run_fwd<E, K>(qj, s_laneh[((j * W + w) * R + r) * 64 + lane], Uf[r], chunk0(r), T, nullptr);
+        for (int r = 0; r < R; ++r) hj[r] = s_laneh[((j * W + w) * R + r) * 64 + lane];
+        run_fwd_n<E, K, R>(qj, hj, Uf, t0s, T, nullptr);
       }
     }
 
     // ---- pass 1: lane folds, wave scan, round chaining
-    V ex[R], tot[R];
+    V ex[R], tot[R], x[R];
+    if constexpr (REV)
+      fold_adj_n<E, K, R>(q, U, t0s, T, gzf, x);
+    else
+      fold_fwd_n<E, K, R>(q, U, x);
+    lti_scan<true, REV>(x, lane, t);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      V x = REV ? fold_adj<E, K>(q, U[r], chunk0(r), T, gzf) : fold_fwd<E, K>(q, U[r]);
-      x = lti_scan<true, REV>(x, lane, t);
-      tot[r] = read_lane(x, 63);
-      ex[r] = lane_prev<true>(x, lane, Alg::szero());
+      tot[r] = read_lane(x[r], 63);
+      ex[r] = lane_prev<true>(x[r], lane, Alg::szero());
     }
     V agg = tot[0];
 #pragma unroll
@@ -619,30 +773,36 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
     __syncthreads();  // entry state is in s_in
     V H = apply<Alg>(s_wpre[w], s_in);
 
-    // ---- pass 2
-    SosAcc<E> acc{};
-    SosAcc<C> wacc{};
+    // ---- pass 2: entry states of every round, then all rounds' steps at once
+    SV h[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t t0 = chunk0(r);
       const V hc = mva<REV>(t.pw[lane], H, ex[r]);
-      const SV h = Alg::store_s(hc);
-      if constexpr (REV) {
-        acc = SosAcc<E>{};
-        run_adj<E, K, GRAD>(q, h, U[r], t0, T, gzf, a.fin ? a.fin + (b * S + s) * 2 : nullptr,
-                            Uf[GRAD ? r : 0], F[GRAD ? r : 0], acc);
-        if constexpr (GRAD) {
-          wacc.a1 += up(acc.a1);
-          wacc.a2 += up(acc.a2);
-          wacc.c0 += up(acc.c0);
-          wacc.c1 += up(acc.c1);
-          wacc.b0 += up(acc.b0);
-        }
-      } else {
-        if (a.ckpt && (t0 % kSosCkpt) == 0 && t0 < T) a.ckpt[(b * S + s) * a.n_ckpt + t0 / kSosCkpt] = hc;
-        run_fwd<E, K>(q, h, U[r], t0, T, a.fin ? a.fin + (b * S + s) * 2 : nullptr);
+      h[r] = Alg::store_s(hc);
+      if constexpr (!REV) {
+        if (a.ckpt && (t0s[r] % kSosCkpt) == 0 && t0s[r] < T)
+          a.ckpt[(b * S + s) * a.n_ckpt + t0s[r] / kSosCkpt] = hc;
       }
       H = mva<REV>(t.pw[64], H, tot[r]);
+    }
+    SosAcc<C> wacc{};
+    if constexpr (REV) {
+      SosAcc<E> acc[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = SosAcc<E>{};
+      run_adj_n<E, K, R, GRAD>(q, h, U, t0s, T, gzf, a.fin ? a.fin + (b * S + s) * 2 : nullptr, Uf, F, acc);
+      if constexpr (GRAD) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          wacc.a1 += up(acc[r].a1);
+          wacc.a2 += up(acc[r].a2);
+          wacc.c0 += up(acc[r].c0);
+          wacc.c1 += up(acc[r].c1);
+          wacc.b0 += up(acc[r].b0);
+        }
+      }
+    } else {
+      run_fwd_n<E, K, R>(q, h, U, t0s, T, a.fin ? a.fin + (b * S + s) * 2 : nullptr);
     }
     if constexpr (GRAD) {
       auto sum = [](const SosAcc<C> &p, const SosAcc<C> &o) -> SosAcc<C> {
