@@ -30,11 +30,10 @@ struct SosLayout {
 
 template <typename E, class Sh>
 SosLayout sos_layout(int64_t B, int64_t T, int S, bool grad) {
-  using Alg = Block2<E>;
   SosLayout L;
   L.tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
   L.status_off = align_up(kHeaderBytes);
-  const size_t words = size_t(B) * size_t(S) * size_t(L.tiles_per_row) * StatusShape<Alg>::kStride;
+  const size_t words = size_t(B) * size_t(S) * size_t(L.tiles_per_row) * kSosStatusWords;
   size_t off = align_up(L.status_off + words * sizeof(uint64_t));
   if (grad) {
     L.partials_off = off;

@@ -495,6 +495,105 @@ __device__ __forceinline__ Vec2<E> load_pair(const E *p, bool valid) {
   return valid ? Vec2<E>{p[0], p[1]} : Vec2<E>{E(0), E(0)};
 }
 
+// ------------------------------------------------------------ look-back
+// Every tile aggregate of an LTI section has the same matrix part, the tile
+// matrix G = B^(tile steps) (B = A forward, A^T for the adjoint), so a status
+// entry carries vectors only: the inclusive state (words 0-3) and the tile's
+// zero-entry aggregate (words 4-7), each 32-bit chunk a tagged 64-bit word as
+// in phs_scan.hpp.  With lane i looking at tile q-1-i and k the first lane
+// holding an inclusive state,
+//   state entering tile q = sum_{i<k} G^i agg(q-1-i) + G^k inc(q-1-k),
+// one matrix-vector product per lane and a wave sum; windows of 64 tiles
+// further back are weighted by G^64 each.
+constexpr int kSosStatusWords = 8;
+constexpr int kSosLookPitch = kSosStatusWords + 1;  // odd LDS pitch: no bank conflicts
+constexpr int kSosLookWords = 64 * kSosLookPitch;
+
+// Tile-level powers for one section: gl = G^lane and g64 = G^64.
+template <typename C>
+struct TilePowers {
+  Mat2<C> gl, g64;
+};
+
+template <typename E>
+__device__ __forceinline__ TilePowers<typename Wide<E>::type> tile_powers(const Mat2<typename Wide<E>::type> &G,
+                                                                         int lane) {
+  using Alg = Block2<E>;
+  Mat2<typename Wide<E>::type> g[7];
+  g[0] = G;
+#pragma unroll
+  for (int j = 1; j < 7; ++j) g[j] = Alg::cmul(g[j - 1], g[j - 1]);
+  return {lane_power<E, 7>(g, lane), g[6]};
+}
+
+// One section's look-back for tile q of a row: polls until the entry state is
+// known (true, in `out`) or `spin_limit` polls found a predecessor still
+// unpublished (false).  `virt` is the state before the row's first tile.
+template <typename E>
+__device__ bool sos_lookback(const uint64_t *row_status, const Vec2<typename Wide<E>::type> &virt, int lane,
+                             unsigned tag, unsigned spin_limit, uint64_t *s_look,
+                             const TilePowers<typename Wide<E>::type> &tp, int64_t q,
+                             Vec2<typename Wide<E>::type> &out) {
+  using Alg = Block2<E>;
+  using C = typename Wide<E>::type;
+  using V = Vec2<C>;
+  constexpr int kS = kSosStatusWords, kP = kSosLookPitch;
+  V acc = Alg::szero();
+  Mat2<C> gm = Alg::cone();
+  int64_t base = q - 1;
+  unsigned polls = 0;
+  auto add = [](const V &p, const V &o) -> V { return {p.v0 + o.v0, p.v1 + o.v1}; };
+  while (true) {
+    const int n = base >= 63 ? 64 : int(base + 1);  // tiles in the window
+    const uint64_t *win = row_status + (base + 1 - n) * kS + lane;
+    uint64_t words[kS];
+#pragma unroll
+    for (int i = 0; i < kS; ++i) {
+      words[i] = 0;
+      if (i * 64 + lane < n * kS)  // word i*64+lane of the window
+        words[i] = __hip_atomic_load(win + i * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int i = 0; i < kS; ++i) {
+      const int j = i * 64 + lane;
+      s_look[(j / kS) * kP + (j % kS)] = words[i];
+    }
+    wave_sync();
+    const int64_t p = base - lane;  // lane < n: window entry n-1-lane
+    V inc = Alg::szero(), agg = Alg::szero();
+    int st;
+    if (p < 0) {
+      st = 2;
+      inc = (p == -1) ? virt : Alg::szero();
+    } else {
+      const uint64_t *e = s_look + (n - 1 - lane) * kP;
+      const bool inc_ok = unpack(e, inc, tag);
+      const bool agg_ok = unpack(e + 4, agg, tag);
+      st = inc_ok ? 2 : (agg_ok ? 1 : 0);
+    }
+    wave_sync();
+    const uint64_t incm = __ballot(st == 2);
+    const int k = incm ? __builtin_ctzll(incm) : 64;
+    const uint64_t low = (k >= 64) ? ~0ull : ((1ull << k) - 1ull);
+    if (__ballot(st == 0) & low) {
+      if (++polls >= spin_limit) return false;
+      __builtin_amdgcn_s_sleep(1);
+      continue;
+    }
+    V c = Alg::szero();
+    if (lane < k) c = Alg::affine(tp.gl, agg, Alg::szero());
+    if (lane == k) c = Alg::affine(tp.gl, inc, Alg::szero());
+    const V sum = read_lane(wave_scan_incl(c, lane, add), 63);
+    acc = Alg::affine(gm, sum, acc);
+    if (k < 64) {
+      out = acc;
+      return true;
+    }
+    gm = Alg::cmul(tp.g64, gm);
+    base -= 64;
+  }
+}
+
 // ------------------------------------------------------------ look-back fallback
 // State entering scan positions [span, ...) of section s_target in row b,
 // computed by one wave straight from the inputs: the cascade (forward) or the
@@ -589,14 +688,14 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
   using M = Map<Alg>;
   using SV = Vec2<E>;
   constexpr int K = Sh::K, R = Sh::R, W = Sh::kWaves;
-  constexpr int kS = StatusShape<Alg>::kStride;
+  using Mt = Mat2<C>;
   static_assert(!GRAD || REV, "coefficient gradients come with the backward");
 
   __shared__ M s_wagg[W];
   __shared__ M s_wpre[W];
   __shared__ V s_in;
   __shared__ unsigned s_id, s_tag;
-  __shared__ uint64_t s_look[StatusShape<Alg>::kLookWords];
+  __shared__ uint64_t s_look[kSosLookWords];
   __shared__ M s_fagg[GRAD ? 2 : 1][W];  // forward recompute: wave aggregates, two visits in flight
   __shared__ SecPowers<C> s_pow[3];
   extern __shared__ __align__(16) unsigned char sos_dyn[];  // GRAD: lane entry states [S][W][R][64]
@@ -636,28 +735,37 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
         if (v + 2 < nvis) build_powers<E, K, R>(&s_pow[(v + 2) % 3], load_sec(sosrow, vis_sec(v + 2)), lane);
       }
     }
-    auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
     for (; v < nvis; ++v) {
       const int s = vis_sec(v);
-      uint64_t *row_status = a.status + ((b * S + s) * tiles) * kS;
+      uint64_t *row_status = a.status + ((b * S + s) * tiles) * kSosStatusWords;
       const SV vs = load_pair(a.virt + (b * S + s) * 2, a.virt != nullptr && row_virt);
       const V virt = {up(vs.v0), up(vs.v1)};
+      // matrices of this section, before the aggregates are in: one wave
+      // segment (Mw), its powers up to the tile matrix G, and G's powers
+      const Mt Mw = maybe_transpose<REV>(s_pow[v % 3].seg);
+      Mt Mp[W + 1];
+      Mp[0] = Alg::cone();
+#pragma unroll
+      for (int j = 1; j <= W; ++j) Mp[j] = Alg::cmul(Mw, Mp[j - 1]);
+      const TilePowers<C> tp = tile_powers<E>(Mp[W], lane);
       // (polling for the predecessors before the aggregates are in measured
       // slower: a tile's predecessors reach each section about when it does)
       V yin = virt;
       __syncthreads();  // wave aggregates are in s_wagg
-      M m = lane < W ? s_wagg[lane] : map_identity<Alg>();
-      m = wave_scan_incl(m, lane, op);
-      const M wex = wave_shift_up(m, lane, map_identity<Alg>());
-      if (lane < W) s_wpre[lane] = wex;
-      const M tagg = read_lane(m, W - 1);
+      // exclusive wave prefixes and the tile aggregate: every wave aggregate
+      // has the matrix part Mw
+      V pv = Alg::szero();
+#pragma unroll
+      for (int j = 0; j < W; ++j) {
+        if (lane == 0) s_wpre[j] = M{Mp[j], pv};
+        pv = Alg::affine(Mw, pv, s_wagg[j].x);
+      }
       if (qs > 0) {
-        if (lane == 0) publish(row_status + qs * kS + StatusShape<Alg>::kIncWords, tagg, tag);
-        Lookback<Alg> lb = lookback_start<Alg>(qs);
-        if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
+        if (lane == 0) publish(row_status + qs * kSosStatusWords + 4, pv, tag);
+        if (!sos_lookback<E>(row_status, virt, lane, tag, a.spin_limit, s_look, tp, qs, yin))
           yin = sos_prefix_fallback<E, Sh, REV>(a, b, s, qs * Sh::kTile, lane, s_look);
       }
-      if (qs + 1 < tiles && lane == 0) publish(row_status + qs * kS, apply<Alg>(tagg, yin), tag);
+      if (qs + 1 < tiles && lane == 0) publish(row_status + qs * kSosStatusWords, Alg::affine(Mp[W], yin, pv), tag);
       if (lane == 0) s_in = yin;
       __syncthreads();  // entry state is in s_in
       if (v + 2 < nvis) build_powers<E, K, R>(&s_pow[(v + 2) % 3], load_sec(sosrow, vis_sec(v + 2)), lane);
