@@ -283,16 +283,39 @@ if EXTENSION_LOADED and _has_op("sosfilt"):
 
     def _sosfilt_setup(ctx, inputs, output):
         sos, zi, x = inputs
-        ctx.save_for_backward(sos, x, output[2])
+        ctx.save_for_backward(sos, x, output[2], zi)
         ctx.has_zi = zi is not None
 
+    def _sosfilt_composite(sos, zi, x, gy, gzf, needs):
+        """Gradient through the per-section lfilter(tdf2) chain on the native
+        2x2 scan ops, whose own backward is differentiable: used under
+        create_graph (double backward)."""
+        from .lti.filtering import _sosfilt_sections
+
+        wrt = [t for t, n in zip((sos, zi, x), needs) if n and t is not None]
+        with torch.enable_grad():
+            zb = zi if zi is not None else x.new_zeros(x.size(0), sos.size(-2), 2)
+            y, zf = _sosfilt_sections(sos, x, zb, unroll_factor=1)
+            outs, grads = [y], [gy]
+            if gzf is not None:
+                outs.append(zf)
+                grads.append(gzf)
+            res = list(torch.autograd.grad(outs, wrt, grads, create_graph=True, allow_unused=True))
+        out = []
+        for t, n in zip((sos, zi, x), needs):
+            g = res.pop(0) if (n and t is not None) else None
+            out.append(torch.zeros_like(t) if (g is None and n and t is not None) else g)
+        return tuple(out)
+
     def _sosfilt_backward(ctx, gy, gzf, _gckpt):
-        sos, x, ckpt = ctx.saved_tensors
-        need_sos = bool(ctx.needs_input_grad[0])
+        sos, x, ckpt, zi = ctx.saved_tensors
+        needs = ctx.needs_input_grad
         if gy is None:
             gy = torch.zeros_like(x)
+        if torch.is_grad_enabled():  # create_graph: a differentiable gradient
+            return _sosfilt_composite(sos, zi, x, gy, gzf, needs)
+        need_sos = bool(needs[0])
         gx, gsos, gzi = torch.ops.philtorch.sosfilt_backward(sos, x, ckpt, gy, gzf, need_sos)
-        needs = ctx.needs_input_grad
         return (gsos if needs[0] else None, gzi if ctx.has_zi and needs[1] else None, gx if needs[2] else None)
 
     torch.library.register_autograd("philtorch::sosfilt", _sosfilt_backward, setup_context=_sosfilt_setup)

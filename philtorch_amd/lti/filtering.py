@@ -2,8 +2,10 @@
 
 ``lfilter`` builds the companion-form state-space model of ``b / a`` and runs
 it through ``state_space`` (transposed direct form II by default), so with
-``unroll_factor=1`` on a HIP device every biquad section is one native 2x2
-scan (``philtorch::lti_recur2``).  ``filtfilt`` and ``lfilter_zi`` follow the
+``unroll_factor=1`` on a HIP device every filter is one native scan
+(``philtorch::lti_recur2`` for a biquad); a biquad in TDF-II form runs the
+fused cascade kernel instead (Bx, scan, state shift and output in one pass),
+unless forward-mode AD is active.  ``filtfilt`` and ``lfilter_zi`` follow the
 reference and SciPy.  Cascaded second-order sections are composed by the
 caller, one ``lfilter`` per section, as in the reference (it has no SOS API),
 or all at once by ``sosfilt``, which on a HIP device runs the whole cascade in
@@ -69,6 +71,40 @@ def _ssm_lfilter(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor] = None, f
     return filt(x)
 
 
+def _fused_biquad_applies(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor], form: str, kwargs) -> bool:
+    """A second-order TDF-II filter on a HIP device with the native route
+    requested (``unroll_factor=1``): the fused cascade kernel computes the same
+    filter in one pass (Bx, the scan, the state shift and C h + D x), with
+    first- and second-order reverse-mode gradients.  Forward-mode AD keeps the
+    reference's route."""
+    from .. import EXTENSION_LOADED
+
+    if not (EXTENSION_LOADED and x.is_cuda and form == "tdf2" and set(kwargs) == {"unroll_factor"}
+            and kwargs["unroll_factor"] == 1):
+        return False
+    if a.size(-1) != 2 or b.size(-1) > 3 or x.dtype not in (torch.float32, torch.float64):
+        return False
+    if b.dtype != x.dtype or a.dtype != x.dtype or (zi is not None and zi.dtype != x.dtype):
+        return False
+    if b.dim() != a.dim() or (b.dim() == 2 and not (b.size(0) == a.size(0) == x.size(0))):
+        return False
+    if zi is not None and not (zi.dim() == 1 or (zi.dim() == 2 and zi.size(0) == x.size(0))):
+        return False
+    if not hasattr(torch.ops.philtorch, "sosfilt"):
+        return False
+    import torch.autograd.forward_ad as fwad
+
+    return all(t is None or fwad.unpack_dual(t).tangent is None for t in (b, a, x, zi))
+
+
+def _fused_biquad(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor]):
+    """lfilter(b, a, x, zi, form="tdf2") of one biquad through philtorch::sosfilt."""
+    sos = torch.cat([F.pad(b, (0, 3 - b.size(-1))), torch.ones_like(a[..., :1]), a], dim=-1).unsqueeze(-2)
+    zb = None if zi is None else zi.expand(x.size(0), 2).unsqueeze(1).contiguous()
+    y, zf, _ = torch.ops.philtorch.sosfilt(sos.contiguous(), zb, x.contiguous())
+    return y if zi is None else (y, zf[:, 0])
+
+
 def lfilter(
     b: Tensor,
     a: Tensor,
@@ -100,7 +136,10 @@ def lfilter(
     assert a.dim() in (1, 2), "Denominator coefficients a must be 1D or 2D."
     if backend != "ssm":
         raise ValueError(f"Unknown backend: {backend}")
-    y = _ssm_lfilter(b, a, x, zi, form=form, **kwargs)
+    if _fused_biquad_applies(b, a, x, zi, form, kwargs):
+        y = _fused_biquad(b, a, x, zi)
+    else:
+        y = _ssm_lfilter(b, a, x, zi, form=form, **kwargs)
     if isinstance(y, tuple):
         y, zf = y
         if squeeze_first:
@@ -214,10 +253,11 @@ def _sosfilt_fused(sos: Tensor, x: Tensor, zi: Optional[Tensor]) -> tuple[Tensor
 
 
 def _sosfilt_sections(sos: Tensor, x: Tensor, zi: Optional[Tensor], **kwargs) -> tuple[Tensor, Tensor]:
+    """One lfilter(tdf2) per section on the reference's state-space route."""
     y, zfs = x, []
     for s in range(sos.size(-2)):
         b, a = sos[..., s, 0:3], sos[..., s, 4:6]
         z = x.new_zeros(x.size(0), 2) if zi is None else zi[:, s]
-        y, zf = lfilter(b, a, y, zi=z, form="tdf2", **kwargs)
+        y, zf = _ssm_lfilter(b, a, y, z, form="tdf2", **kwargs)
         zfs.append(zf)
     return y, torch.stack(zfs, dim=1)

@@ -269,3 +269,68 @@ def test_sosfilt_c4_size_matches_lfilter_chain(hip):
     D.check(gx1, gx2, "grad_x")
     gs2[..., 3] = gs1[..., 3]  # the lfilter chain does not differentiate a0
     D.check(gs1, gs2, "grad_sos")
+
+
+# ---------------------------------------------------------------- lfilter route
+def _biquad(g, lead, dtype):
+    sos = D.sos_coefs(g, lead, 1, np.float64)[..., 0, :]
+    return sos[..., 0:3].astype(dtype), sos[..., 4:6].astype(dtype)
+
+
+def test_lfilter_tdf2_biquad_takes_fused_route(hip):
+    import torch
+
+    from philtorch_amd.lti import filtering
+
+    g = D.rng(D.seed_of("lfilter-route"))
+    b, a = (torch.tensor(v, device="cuda") for v in _biquad(g, (3,), np.float32))
+    x = torch.randn(3, 100, device="cuda")
+    assert filtering._fused_biquad_applies(b, a, x, None, "tdf2", {"unroll_factor": 1})
+    assert not filtering._fused_biquad_applies(b, a, x, None, "df2", {"unroll_factor": 1})
+    assert not filtering._fused_biquad_applies(b, a, x, None, "tdf2", {})
+    assert not filtering._fused_biquad_applies(b, a, x.cpu(), None, "tdf2", {"unroll_factor": 1})
+
+
+@pytest.mark.parametrize("batched", [False, True])
+def test_lfilter_fused_route_matches_reference_route(hip, batched):
+    """lfilter(tdf2, unroll_factor=1) on HIP (fused kernel) against the same
+    call on CPU (the reference's pure-PyTorch route), with zi/zf, and filtfilt
+    built on it."""
+    import torch
+
+    g = D.rng(D.seed_of("lfilter-fused", batched))
+    b, a = _biquad(g, (4,) if batched else (), np.float64)
+    x = g.standard_normal((4, 7000))
+    zi = g.standard_normal((4, 2))
+    tb, ta, tx, tz = (torch.tensor(v) for v in (b, a, x, zi))
+    yg, zfg = hip.lti.lfilter(tb.cuda(), ta.cuda(), tx.cuda(), zi=tz.cuda(), unroll_factor=1)
+    yc, zfc = hip.lti.lfilter(tb, ta, tx, zi=tz, unroll_factor=1)
+    D.check(yg.cpu().numpy(), yc.numpy(), "y")
+    D.check(zfg.cpu().numpy(), zfc.numpy(), "zf", scale=np.max(np.abs(yc.numpy())))
+    fg = hip.lti.filtfilt(tb.cuda(), ta.cuda(), tx.cuda(), unroll_factor=1)
+    fc = hip.lti.filtfilt(tb, ta, tx, unroll_factor=1)
+    D.check(fg.cpu().numpy(), fc.numpy(), "filtfilt")
+
+
+def test_lfilter_fused_route_second_order_gradients(hip):
+    """Double backward through the fused route (its create_graph fallback is
+    the differentiable per-section chain) and forward-mode AD (which keeps
+    the reference's route)."""
+    import torch
+    import torch.autograd.forward_ad as fwad
+
+    g = D.rng(D.seed_of("lfilter-fused-grad"))
+    b, a = (torch.tensor(v, device="cuda", requires_grad=True) for v in _biquad(g, (2,), np.float64))
+    x = torch.tensor(g.standard_normal((2, 30)), device="cuda", requires_grad=True)
+    zi = torch.tensor(g.standard_normal((2, 2)), device="cuda", requires_grad=True)
+    f = lambda b_, a_, x_, z_: hip.lti.lfilter(b_, a_, x_, zi=z_, unroll_factor=1)  # noqa: E731
+    assert torch.autograd.gradcheck(f, (b, a, x, zi))
+    assert torch.autograd.gradgradcheck(f, (b, a, x, zi))
+    sos = torch.tensor(D.sos_coefs(g, (), 2, np.float64), device="cuda", requires_grad=True)
+    assert torch.autograd.gradgradcheck(lambda s_, x_: hip.lti.sosfilt(s_, x_), (sos, x))
+    with fwad.dual_level():
+        xd = fwad.make_dual(x.detach(), torch.ones_like(x))
+        y = hip.lti.lfilter(b.detach(), a.detach(), xd, unroll_factor=1)
+        tangent = fwad.unpack_dual(y).tangent
+    ref = hip.lti.lfilter(b.detach(), a.detach(), torch.ones_like(x), unroll_factor=1)
+    D.check(tangent.cpu().numpy(), ref.cpu().numpy(), "jvp")
