@@ -15,6 +15,7 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c3      philtorch::recur2 + recurN_backward               (LPV 2x2)
   c4      8 x (philtorch::lti_recur2 + lti_recurN_backward) (LTI biquad cascade)
   c4_fused  philtorch::sosfilt + sosfilt_backward              (the same cascade, fused)
+  c4_api  8 x lti.lfilter(tdf2, unroll_factor=1) + autograd   (the caller pattern, API level)
 Before every step a 512 MiB buffer is read end to end so the 256 MB Infinity
 Cache holds none of the step's operands (a read sweep, not a write: a write
 would leave dirty lines whose write-back then competes with the step); the
@@ -312,6 +313,38 @@ class SosFused(Workload):
         oracle.sosfilt_bwd(sos[:rows], x[:rows, :steps], None, gy[:rows, :steps], nthreads=nthreads)
 
 
+class SosApi(SosFused):
+    """c4_api: the C4 caller pattern through philtorch's API exactly as
+    SURVEY's C4 states it, ``for s in range(8): y = lti.lfilter(b[:, s],
+    a[:, s], y, form="tdf2", unroll_factor=1)``, then autograd w.r.t. x, b and
+    a (every biquad runs the fused kernel on a HIP device)."""
+
+    def __init__(self):
+        super().__init__()
+        self.name = "c4_api"
+        self.metric = f"GSamples/s fwd+bwd, lti.lfilter cascade x{self.S} (grad x, b, a) B={self.B} T={self.T} fp32 (API)"
+        self.launches = self.S
+
+    def step_fwd(self):
+        import torch
+        from philtorch_amd import lti
+
+        sos, x, _ = self.dev
+        b = sos[..., 0:3].clone().requires_grad_(True)
+        a = sos[..., 4:6].clone().requires_grad_(True)
+        xr = x.detach().requires_grad_(True)
+        y = xr
+        for s in range(self.S):
+            y = lti.lfilter(b[:, s], a[:, s], y, form="tdf2", unroll_factor=1)
+        return y, (xr, b, a)
+
+    def step_bwd(self, out):
+        import torch
+
+        y, inputs = out
+        return torch.autograd.grad(y, inputs, self.dev[2])
+
+
 def make_workload(name):
     if name == "c1":
         return LpvScalar("c1", 64, 65536, "float32")
@@ -327,10 +360,12 @@ def make_workload(name):
         return SosCascade()
     if name == "c4_fused":
         return SosFused()
+    if name == "c4_api":
+        return SosApi()
     raise ValueError(name)
 
 
-CONFIGS = ("c1", "c2", "c3", "c4", "c4_fused", "c5", "c5_f64")
+CONFIGS = ("c1", "c2", "c3", "c4", "c4_fused", "c4_api", "c5", "c5_f64")
 
 
 # ----------------------------------------------------------------------------
@@ -472,6 +507,7 @@ def main() -> int:
                 "c3": "lpv_2x2_scan_fwd_bwd_B32_T1048576_f32",
                 "c4": "lti_sos8_cascade_fwd_bwd_B16_T480000_f32",
                 "c4_fused": "lti_sos8_cascade_fused_fwd_bwd_B16_T480000_f32",
+                "c4_api": "lti_lfilter8_cascade_api_fwd_bwd_B16_T480000_f32",
                 "c5": "lpv_scan_fwd_bwd_B8_T16777216_f32",
                 "c5_f64": "lpv_scan_fwd_bwd_B8_T16777216_f64",
             }[w.name],
@@ -489,7 +525,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{'sos_kernel' if w.name == 'c4_fused' else 'scan_kernel'} ({dominant[0]})",
+            "kernel": f"{'sos_kernel' if w.name.startswith('c4_') else 'scan_kernel'} ({dominant[0]})",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
