@@ -601,9 +601,10 @@ __device__ bool sos_lookback(const uint64_t *row_status, const Vec2<typename Wid
 // per iteration, every section up to s_target carrying its state across
 // iterations.  `lds` (the look-back staging area, free by then) holds the
 // carries and the section's powers.  Taken only when predecessors did not
-// publish within the poll budget.
+// publish within the poll budget.  The arguments come by value: a reference
+// would make every thread of the kernel keep a private copy of them.
 template <typename E, class Sh, bool REV>
-__device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const SosArgs<E> &a, int64_t b,
+__device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const SosArgs<E> a, int64_t b,
                                                                         int s_target, int64_t span, int lane,
                                                                         uint64_t *lds) {
   using Alg = Block2<E>;
