@@ -197,11 +197,17 @@ struct Lookback {
   Map<Alg> acc;    // fold of the windows already passed
   int64_t base;    // newest tile of the current window
   unsigned polls;  // polls that found some predecessor still unpublished
+  int span;        // tiles per window: kLookFirst first, then 64
 };
+
+// The nearest inclusive predecessor is almost always among the last few
+// tiles, so the first window reads only that many entries (a full window is
+// 64 entries of status words, read again at every poll).
+constexpr int kLookFirst = 8;
 
 template <class Alg>
 __device__ __forceinline__ Lookback<Alg> lookback_start(int64_t q) {
-  return {map_identity<Alg>(), q - 1, 0u};
+  return {map_identity<Alg>(), q - 1, 0u, kLookFirst};
 }
 
 // One poll.  When every tile between the nearest inclusive predecessor and
@@ -219,7 +225,7 @@ __device__ bool lookback_poll(const uint64_t *row_status, const typename Alg::st
   constexpr int kBatch = kS < 8 ? kS : 8;  // words in flight per lane
   while (true) {
     const int64_t base = lb.base;
-    const int n = base >= 63 ? 64 : int(base + 1);  // tiles in the window
+    const int n = base + 1 > lb.span ? lb.span : int(base + 1);  // tiles in the window
     const uint64_t *win = row_status + (base + 1 - n) * kS + lane;
     const int64_t p = base - lane;  // lane < n: window entry n-1-lane
     M mv = map_identity<Alg>();
@@ -243,15 +249,18 @@ __device__ bool lookback_poll(const uint64_t *row_status, const typename Alg::st
       }
     }
     wave_sync();
-    int st;
-    if (p < 0) {
-      st = 2;
-      sv = (p == -1) ? virt : Alg::szero();
-    } else {
+    // st: 2 inclusive (or the row's virtual entry at p = -1), 1 aggregate
+    // only, 0 unpublished, 3 outside the window (identity, never inclusive)
+    int st = 3;
+    if (lane < n) {
       const uint64_t *e = s_look + (n - 1 - lane) * kP;
       const bool inc_ok = unpack(e, sv, tag);
       const bool agg_ok = unpack(e + Sh::kIncWords, mv, tag);
       st = inc_ok ? 2 : (agg_ok ? 1 : 0);
+      if (!agg_ok) mv = map_identity<Alg>();
+    } else if (p == -1) {
+      st = 2;
+      sv = virt;
     }
     wave_sync();
     const uint64_t incm = __ballot(st == 2);
@@ -262,7 +271,8 @@ __device__ bool lookback_poll(const uint64_t *row_status, const typename Alg::st
       return false;
     }
     // lanes [0, k) hold aggregates of tiles base-lane (newest at lane 0);
-    // fold them oldest-first into lane 0.
+    // fold them oldest-first into lane 0 (lanes outside the window carry the
+    // identity).
     M m = (lane < k) ? mv : map_identity<Alg>();
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -276,7 +286,8 @@ __device__ bool lookback_poll(const uint64_t *row_status, const typename Alg::st
       return true;
     }
     lb.acc = compose<Alg>(F, lb.acc);
-    lb.base = base - 64;
+    lb.base = base - n;
+    lb.span = 64;
   }
 }
 

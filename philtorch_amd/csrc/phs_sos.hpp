@@ -503,16 +503,18 @@ __device__ __forceinline__ Vec2<E> load_pair(const E *p, bool valid) {
 // in phs_scan.hpp.  With lane i looking at tile q-1-i and k the first lane
 // holding an inclusive state,
 //   state entering tile q = sum_{i<k} G^i agg(q-1-i) + G^k inc(q-1-k),
-// one matrix-vector product per lane and a wave sum; windows of 64 tiles
-// further back are weighted by G^64 each.
+// one matrix-vector product per lane and a wave sum.  The first window holds
+// the kLookFirst nearest tiles (the inclusive state is almost always among
+// them), further windows 64; a window's sum is weighted by G^(tiles passed).
 constexpr int kSosStatusWords = 8;
 constexpr int kSosLookPitch = kSosStatusWords + 1;  // odd LDS pitch: no bank conflicts
 constexpr int kSosLookWords = 64 * kSosLookPitch;
 
-// Tile-level powers for one section: gl = G^lane and g64 = G^64.
+// Tile-level powers for one section: gl = G^lane, gfirst = G^kLookFirst and
+// g64 = G^64 (the weights of the windows passed).
 template <typename C>
 struct TilePowers {
-  Mat2<C> gl, g64;
+  Mat2<C> gl, gfirst, g64;
 };
 
 template <typename E>
@@ -523,7 +525,8 @@ __device__ __forceinline__ TilePowers<typename Wide<E>::type> tile_powers(const 
   g[0] = G;
 #pragma unroll
   for (int j = 1; j < 7; ++j) g[j] = Alg::cmul(g[j - 1], g[j - 1]);
-  return {lane_power<E, 7>(g, lane), g[6]};
+  static_assert(kLookFirst == 8, "gfirst is G^8");
+  return {lane_power<E, 7>(g, lane), g[3], g[6]};
 }
 
 // One section's look-back for tile q of a row: polls until the entry state is
@@ -542,9 +545,10 @@ __device__ bool sos_lookback(const uint64_t *row_status, const Vec2<typename Wid
   Mat2<C> gm = Alg::cone();
   int64_t base = q - 1;
   unsigned polls = 0;
+  int span = kLookFirst;
   auto add = [](const V &p, const V &o) -> V { return {p.v0 + o.v0, p.v1 + o.v1}; };
   while (true) {
-    const int n = base >= 63 ? 64 : int(base + 1);  // tiles in the window
+    const int n = base + 1 > span ? span : int(base + 1);  // tiles in the window
     const uint64_t *win = row_status + (base + 1 - n) * kS + lane;
     uint64_t words[kS];
 #pragma unroll
@@ -561,15 +565,15 @@ __device__ bool sos_lookback(const uint64_t *row_status, const Vec2<typename Wid
     wave_sync();
     const int64_t p = base - lane;  // lane < n: window entry n-1-lane
     V inc = Alg::szero(), agg = Alg::szero();
-    int st;
-    if (p < 0) {
-      st = 2;
-      inc = (p == -1) ? virt : Alg::szero();
-    } else {
+    int st = 3;  // outside the window: no contribution, never inclusive
+    if (lane < n) {
       const uint64_t *e = s_look + (n - 1 - lane) * kP;
       const bool inc_ok = unpack(e, inc, tag);
       const bool agg_ok = unpack(e + 4, agg, tag);
       st = inc_ok ? 2 : (agg_ok ? 1 : 0);
+    } else if (p == -1) {
+      st = 2;
+      inc = virt;
     }
     wave_sync();
     const uint64_t incm = __ballot(st == 2);
@@ -581,7 +585,7 @@ __device__ bool sos_lookback(const uint64_t *row_status, const Vec2<typename Wid
       continue;
     }
     V c = Alg::szero();
-    if (lane < k) c = Alg::affine(tp.gl, agg, Alg::szero());
+    if (lane < k && lane < n) c = Alg::affine(tp.gl, agg, Alg::szero());
     if (lane == k) c = Alg::affine(tp.gl, inc, Alg::szero());
     const V sum = read_lane(wave_scan_incl(c, lane, add), 63);
     acc = Alg::affine(gm, sum, acc);
@@ -589,8 +593,9 @@ __device__ bool sos_lookback(const uint64_t *row_status, const Vec2<typename Wid
       out = acc;
       return true;
     }
-    gm = Alg::cmul(tp.g64, gm);
-    base -= 64;
+    gm = Alg::cmul(n == 64 ? tp.g64 : tp.gfirst, gm);
+    base -= n;
+    span = 64;
   }
 }
 

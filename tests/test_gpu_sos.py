@@ -129,6 +129,14 @@ def test_sosfilt_capi_parity(api, dtype, B, T, S):
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_sosfilt_capi_long_rows(api, dtype):
+    """Rows of 80+ tiles: look-backs that fold a first window of 8 tiles and
+    further windows of 64 when the inclusive states are not yet published."""
+    case = _case(dtype, 2, 1_000_003, 3, False, True, True, D.seed_of("sos-long", dtype))
+    _check_all(_run(api, *case), *case, dtype, "long rows")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
 def test_sosfilt_capi_no_coef_grad(api, dtype):
     sos, x, zi, gy, gzf = _case(dtype, 3, 7000, 4, False, True, True, D.seed_of("sos-nograd", dtype))
     y, zf, gs, gzi, gx = _run(api, sos, x, zi, gy, gzf, grad=False)
