@@ -304,9 +304,13 @@ __device__ bool lookback(const uint64_t *row_status, const typename Alg::state &
 }
 
 // ------------------------------------------------------------ chunk I/O
+// The bounds-checked tail assigns in branches: `c ? row[t] : fill` with both
+// operands lvalues is an lvalue, compiled as a select between a global and a
+// private address, and every thread of the kernel then keeps a copy of
+// `fill` in scratch memory.
 template <typename X, int K>
 __device__ __forceinline__ void load_chunk(const X *row, int64_t t0, int64_t T, bool vec, X (&out)[K],
-                                           const X &fill) {
+                                           const X fill) {
   if (vec && t0 + K <= T) {
     constexpr int nv = int(K * sizeof(X) / 16);
     static_assert(K * sizeof(X) % 16 == 0, "chunk must be 16-byte granular");
@@ -321,7 +325,12 @@ __device__ __forceinline__ void load_chunk(const X *row, int64_t t0, int64_t T, 
     for (int k = 0; k < K; ++k) out[k] = u.x[k];
   } else {
 #pragma unroll
-    for (int k = 0; k < K; ++k) out[k] = (t0 + k < T) ? row[t0 + k] : fill;
+    for (int k = 0; k < K; ++k) {
+      if (t0 + k < T)
+        out[k] = row[t0 + k];
+      else
+        out[k] = fill;
+    }
   }
 }
 
