@@ -178,6 +178,11 @@ struct Scalar {
   static constexpr bool kLookbackWave = Num<T>::kComplex;
   static constexpr int kWavesPerBlock = Num<T>::kComplex ? 3 : 8;
   static constexpr int kMinWavesPerEU = Num<T>::kComplex ? 1 : 4;
+  // tiles in the first look-back window (later windows hold 64): scalar
+  // status entries are short and the nearest inclusive predecessor is usually
+  // among the last 8 tiles (C5 fp32: 8 tiles 134, 16 tiles 125, 64 tiles 128
+  // GSamples/s)
+  static constexpr int kLookFirst = 8;
 
   static __device__ __forceinline__ coef load_c(s_coef v) { return up(v); }
   static __device__ __forceinline__ state load_s(s_state v) { return up(v); }
@@ -230,6 +235,9 @@ struct Block2 {
   static constexpr bool kLookbackWave = true;
   static constexpr int kWavesPerBlock = 3;
   static constexpr int kMinWavesPerEU = Num<T>::kComplex ? 1 : 3;
+  // a full first look-back window: a short one costs 2x2 scans a second poll
+  // too often (C3: 8 tiles 40.7, 16 tiles 38.8, 64 tiles 45.5 GSamples/s)
+  static constexpr int kLookFirst = 64;
 
   static __device__ __forceinline__ coef load_c(s_coef v) {
     return {up(v.m00), up(v.m01), up(v.m10), up(v.m11)};
@@ -332,6 +340,7 @@ struct BlockN {
   static constexpr bool kLookbackWave = true;
   static constexpr int kWavesPerBlock = 3;
   static constexpr int kMinWavesPerEU = 1;
+  static constexpr int kLookFirst = 64;  // as Block2
 
   template <typename D, typename S, int N>
   static __device__ __forceinline__ void conv_up(D (&d)[N], const S (&s)[N]) {

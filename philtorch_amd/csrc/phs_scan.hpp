@@ -197,17 +197,16 @@ struct Lookback {
   Map<Alg> acc;    // fold of the windows already passed
   int64_t base;    // newest tile of the current window
   unsigned polls;  // polls that found some predecessor still unpublished
-  int span;        // tiles per window: kLookFirst first, then 64
+  int span;        // tiles per window: Alg::kLookFirst first, then 64
 };
 
-// The nearest inclusive predecessor is almost always among the last few
-// tiles, so the first window reads only that many entries (a full window is
-// 64 entries of status words, read again at every poll).
-constexpr int kLookFirst = 8;
-
+// The first window reads Alg::kLookFirst entries: a full window is 64
+// entries of status words, read again at every poll, and where the nearest
+// inclusive predecessor is usually close a narrow first read saves most of it.
 template <class Alg>
 __device__ __forceinline__ Lookback<Alg> lookback_start(int64_t q) {
-  return {map_identity<Alg>(), q - 1, 0u, kLookFirst};
+  static_assert(Alg::kLookFirst >= 1 && Alg::kLookFirst <= 64, "a window is at most one wave of entries");
+  return {map_identity<Alg>(), q - 1, 0u, Alg::kLookFirst};
 }
 
 // One poll.  When every tile between the nearest inclusive predecessor and

@@ -504,13 +504,14 @@ __device__ __forceinline__ Vec2<E> load_pair(const E *p, bool valid) {
 // holding an inclusive state,
 //   state entering tile q = sum_{i<k} G^i agg(q-1-i) + G^k inc(q-1-k),
 // one matrix-vector product per lane and a wave sum.  The first window holds
-// the kLookFirst nearest tiles (the inclusive state is almost always among
+// the kSosLookFirst nearest tiles (the inclusive state is almost always among
 // them), further windows 64; a window's sum is weighted by G^(tiles passed).
+constexpr int kSosLookFirst = 8;
 constexpr int kSosStatusWords = 8;
 constexpr int kSosLookPitch = kSosStatusWords + 1;  // odd LDS pitch: no bank conflicts
 constexpr int kSosLookWords = 64 * kSosLookPitch;
 
-// Tile-level powers for one section: gl = G^lane, gfirst = G^kLookFirst and
+// Tile-level powers for one section: gl = G^lane, gfirst = G^kSosLookFirst and
 // g64 = G^64 (the weights of the windows passed).
 template <typename C>
 struct TilePowers {
@@ -525,7 +526,7 @@ __device__ __forceinline__ TilePowers<typename Wide<E>::type> tile_powers(const 
   g[0] = G;
 #pragma unroll
   for (int j = 1; j < 7; ++j) g[j] = Alg::cmul(g[j - 1], g[j - 1]);
-  static_assert(kLookFirst == 8, "gfirst is G^8");
+  static_assert(kSosLookFirst == 8, "gfirst is G^8");
   return {lane_power<E, 7>(g, lane), g[3], g[6]};
 }
 
@@ -545,7 +546,7 @@ __device__ bool sos_lookback(const uint64_t *row_status, const Vec2<typename Wid
   Mat2<C> gm = Alg::cone();
   int64_t base = q - 1;
   unsigned polls = 0;
-  int span = kLookFirst;
+  int span = kSosLookFirst;
   auto add = [](const V &p, const V &o) -> V { return {p.v0 + o.v0, p.v1 + o.v1}; };
   while (true) {
     const int n = base + 1 > span ? span : int(base + 1);  // tiles in the window
