@@ -16,6 +16,7 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c4      8 x (philtorch::lti_recur2 + lti_recurN_backward) (LTI biquad cascade)
   c4_fused  philtorch::sosfilt + sosfilt_backward              (the same cascade, fused)
   c4_api  8 x lti.lfilter(tdf2, unroll_factor=1) + autograd   (the caller pattern, API level)
+  c4_filtfilt  8 x lti.filtfilt(replicate, padlen 9), forward only (philtorch::filtfilt)
 Before every step a 512 MiB buffer is read end to end so the 256 MB Infinity
 Cache holds none of the step's operands (a read sweep, not a write: a write
 would leave dirty lines whose write-back then competes with the step); the
@@ -345,6 +346,44 @@ class SosApi(SosFused):
         return torch.autograd.grad(y, inputs, self.dev[2])
 
 
+class FiltfiltApi(SosFused):
+    """c4_filtfilt: the filtfilt half of the C4 caller pattern, forward only,
+    ``for s in range(8): y = lti.filtfilt(b[:, s], a[:, s], y,
+    padmode="replicate", padlen=9, unroll_factor=1)`` (each call runs
+    philtorch::filtfilt: two cascade passes and two edge kernels)."""
+
+    def __init__(self):
+        super().__init__()
+        self.name = "c4_filtfilt"
+        self.metric = (f"GSamples/s fwd, lti.filtfilt x{self.S} sections (replicate, padlen 9) "
+                       f"B={self.B} T={self.T} fp32 (API)")
+        self.fwd_bytes = 16 * self.B * self.T  # per filtfilt: two passes, each reads and writes the row
+        self.bwd_bytes = 0
+        self.launches = self.S
+        sos = self.dev[0]
+        self.b = [sos[:, s, 0:3].contiguous() for s in range(self.S)]
+        self.a = [sos[:, s, 4:6].contiguous() for s in range(self.S)]
+
+    def step_fwd(self):
+        from philtorch_amd import lti
+
+        y = self.dev[1]
+        for s in range(self.S):
+            y = lti.filtfilt(self.b[s], self.a[s], y, padmode="replicate", padlen=9, unroll_factor=1)
+        return y
+
+    def step_bwd(self, out):
+        return out
+
+    def cpu_step(self, rows, steps, nthreads):
+        import oracle
+
+        sos, x, _ = (v.numpy() for v in self.cpu)
+        y = x[:rows, :steps]
+        for s in range(self.S):
+            y = oracle.filtfilt(sos[:rows, s], y, padmode="replicate", padlen=9, nthreads=nthreads)
+
+
 def make_workload(name):
     if name == "c1":
         return LpvScalar("c1", 64, 65536, "float32")
@@ -362,10 +401,12 @@ def make_workload(name):
         return SosFused()
     if name == "c4_api":
         return SosApi()
+    if name == "c4_filtfilt":
+        return FiltfiltApi()
     raise ValueError(name)
 
 
-CONFIGS = ("c1", "c2", "c3", "c4", "c4_fused", "c4_api", "c5", "c5_f64")
+CONFIGS = ("c1", "c2", "c3", "c4", "c4_fused", "c4_api", "c4_filtfilt", "c5", "c5_f64")
 
 
 # ----------------------------------------------------------------------------
@@ -392,7 +433,7 @@ def cpu_baseline(w: Workload, budget_s=10.0):
         "unit": "GSamples/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"{rows} of {w.B} rows x the first {steps} of T={w.T} steps, fwd+bwd, median of {reps} reps "
+        "sample": f"{rows} of {w.B} rows x the first {steps} of T={w.T} steps, {'fwd+bwd' if w.bwd_bytes else 'fwd'}, median of {reps} reps "
         f"(oracle/phs_oracle.c, OpenMP over rows, {cores} threads)",
     }
 
@@ -481,7 +522,7 @@ def main() -> int:
     torch.cuda.synchronize()
     mean_fwd = sum(e[0].elapsed_time(e[1]) for e in kev) / args.steps / w.launches
     mean_bwd = sum(e[1].elapsed_time(e[2]) for e in kev) / args.steps / w.launches
-    if mean_bwd >= mean_fwd:
+    if w.bwd_bytes and mean_bwd >= mean_fwd:
         dominant = ("backward", w.bwd_bytes, mean_bwd)
     else:
         dominant = ("forward", w.fwd_bytes, mean_fwd)
@@ -508,6 +549,7 @@ def main() -> int:
                 "c4": "lti_sos8_cascade_fwd_bwd_B16_T480000_f32",
                 "c4_fused": "lti_sos8_cascade_fused_fwd_bwd_B16_T480000_f32",
                 "c4_api": "lti_lfilter8_cascade_api_fwd_bwd_B16_T480000_f32",
+                "c4_filtfilt": "lti_filtfilt8_api_fwd_B16_T480000_f32",
                 "c5": "lpv_scan_fwd_bwd_B8_T16777216_f32",
                 "c5_f64": "lpv_scan_fwd_bwd_B8_T16777216_f64",
             }[w.name],
@@ -520,7 +562,7 @@ def main() -> int:
             "ms_fwd_kernel": round(mean_fwd, 5),
             "ms_bwd_kernel": round(mean_bwd, 5),
             "fwd_GBs_algorithmic": round(w.fwd_bytes / (mean_fwd * 1e-3) / 1e9, 1),
-            "bwd_GBs_algorithmic": round(w.bwd_bytes / (mean_bwd * 1e-3) / 1e9, 1),
+            "bwd_GBs_algorithmic": round(w.bwd_bytes / (mean_bwd * 1e-3) / 1e9, 1) if w.bwd_bytes else None,
             "wall_s_timed_region": round(wall, 4),
         },
         "roofline": {

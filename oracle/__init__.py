@@ -255,3 +255,43 @@ def sosfilt_bwd(sos, x, zi, gy, gzf=None, nthreads=None):
     if shared:
         gsos = gsos.sum(axis=0)
     return gsos, gzi, g
+
+
+# torch.nn.functional.pad mode -> numpy.pad mode
+_NP_PAD = {"constant": "constant", "replicate": "edge", "reflect": "reflect", "circular": "wrap"}
+
+
+def lfilter_zi(sos_rows):
+    """Steady state of TDF-II biquads sos_rows [R,6] (a0 = 1) for a unit
+    input: solve((I - A), Bv) as philtorch's lfilter_zi does
+    (philtorch/lti/filtering.py:107-142, transpose=True)."""
+    A, Bv, _, _ = _tdf2_section(np.asarray(sos_rows))
+    I_minus_A = np.eye(2, dtype=A.dtype)[None] - A
+    return np.linalg.solve(I_minus_A, Bv[..., None])[..., 0]
+
+
+def filtfilt(sos, x, padmode="replicate", padlen=None, nthreads=None):
+    """philtorch.lti.filtfilt of one biquad per row
+    (philtorch/lti/filtering.py:413-484): sos [6] (shared) or [B,6] with
+    a0 = 1; x [B,T].  Pads by `padlen` (default 3 * ntaps = 9) with
+    torch.nn.functional.pad's `padmode` (None: no padding), filters forward
+    from lfilter_zi * ext[:, 0], filters the reversed output from
+    lfilter_zi * y[:, -1], trims and flips back; each pass is one
+    lfilter(tdf2) (sosfilt with one section)."""
+    dt = np.asarray(x).dtype
+    x = _c(x, dt)
+    B, T = x.shape
+    rows = np.broadcast_to(_c(sos, dt), (B, 6)) if np.ndim(sos) == 1 else _c(sos, dt)
+    edge = 0 if padmode is None else (9 if padlen is None else int(padlen))
+    assert T > edge, f"Input signal length {T} must be greater than pad length {edge}."
+    ext = np.pad(x, ((0, 0), (edge, edge)), mode=_NP_PAD[padmode]) if edge > 0 else x
+    ext = np.ascontiguousarray(ext)
+    zi = lfilter_zi(rows).astype(dt)
+    sec = np.ascontiguousarray(rows[:, None, :])
+    y, _ = sosfilt(sec, ext, np.ascontiguousarray((zi * ext[:, :1])[:, None, :]), nthreads)
+    yr = np.ascontiguousarray(y[:, ::-1])
+    y, _ = sosfilt(sec, yr, np.ascontiguousarray((zi * yr[:, :1])[:, None, :]), nthreads)
+    if edge > 0:
+        y = y[:, edge:-edge]
+    return np.ascontiguousarray(y[:, ::-1])
+

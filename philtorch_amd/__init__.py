@@ -6,7 +6,8 @@ namespace: the reference's five ops (``recur2``, ``recurN``, ``lti_recur2``,
 ``lti_recurN``, ``lti_recur``; philtorch/csrc/host_recur2.cpp:162-171), the new
 LPV scalar op ``recur``, four fused backward ops, and the fused cascade of
 second-order sections ``sosfilt`` / ``sosfilt_backward`` (no reference
-counterpart; ``lti.sosfilt`` is its API).  This module then
+counterpart; ``lti.sosfilt`` is its API) and the forward-only zero-phase
+``filtfilt`` of filters up to second order (behind ``lti.filtfilt``).  This module then
 registers fake (meta) kernels and autograd formulas for them, as
 philtorch/__init__.py:157-268 does for its ops.
 
@@ -319,6 +320,17 @@ if EXTENSION_LOADED and _has_op("sosfilt"):
         return (gsos if needs[0] else None, gzi if ctx.has_zi and needs[1] else None, gx if needs[2] else None)
 
     torch.library.register_autograd("philtorch::sosfilt", _sosfilt_backward, setup_context=_sosfilt_setup)
+
+if EXTENSION_LOADED and _has_op("filtfilt"):
+    # zero-phase biquad filter, forward only (lti.filtfilt takes it when no
+    # gradient is needed)
+    @torch.library.register_fake("philtorch::filtfilt")
+    def _(b, a, x, padmode, padlen):
+        torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
+        torch._check(b.ndim == a.ndim and b.ndim in (1, 2), lambda: "b and a must both be 1D or both 2D")
+        torch._check(1 <= b.shape[-1] <= 3 and 1 <= a.shape[-1] <= 2, lambda: "second order at most")
+        torch._check(0 <= padlen < x.shape[1], lambda: "0 <= padlen < T")
+        return _fake_like(x)
 
 from . import mat  # noqa: E402,F401
 from . import lti  # noqa: E402,F401

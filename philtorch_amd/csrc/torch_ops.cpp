@@ -468,6 +468,45 @@ Triple sosfilt_backward_hip(const Tensor &sos, const Tensor &x, const Tensor &ck
   return {gx, gsos, gzi};
 }
 
+// Zero-phase filter of second order at most (phs_filtfilt_fwd;
+// philtorch/lti/filtering.py:413-484): b (nb,) or (batch, nb), nb <= 3; a
+// (na,) or (batch, na), the denominator after its leading 1, na <= 2;
+// padmode a phs_padmode code.  Forward only: callers that need gradients
+// compose lfilter passes instead.
+Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t padmode, int64_t padlen) {
+  TORCH_CHECK(x.dim() == 2, "philtorch::filtfilt: x must be a 2D tensor (batch, time)");
+  TORCH_CHECK(b.dim() == a.dim() && (b.dim() == 1 || b.dim() == 2), "philtorch::filtfilt: b and a must both be 1D "
+              "(shared) or both 2D (batch, taps)");
+  const int64_t B = x.size(0), T = x.size(1);
+  if (b.dim() == 2)
+    TORCH_CHECK(b.size(0) == B && a.size(0) == B, "philtorch::filtfilt: 2D b and a must have x's batch size");
+  const int64_t nb = b.size(-1), na = a.size(-1);
+  TORCH_CHECK(nb >= 1 && nb <= 3 && na >= 1 && na <= 2, "philtorch::filtfilt: filters of second order at most "
+              "(b: 1 to 3 taps, a: 1 or 2 after the leading 1)");
+  TORCH_CHECK(b.scalar_type() == x.scalar_type() && a.scalar_type() == x.scalar_type(),
+              "philtorch::filtfilt: b, a and x must have the same scalar type");
+  TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,
+              "philtorch::filtfilt: float32 or float64 only, got ", x.scalar_type());
+  TORCH_CHECK(x.is_cuda() && b.device() == x.device() && a.device() == x.device(),
+              "philtorch::filtfilt: philtorch_amd runs on HIP devices only, all tensors on one device");
+  TORCH_CHECK(padmode >= PHS_PAD_CONSTANT && padmode <= PHS_PAD_CIRCULAR, "philtorch::filtfilt: unknown padmode ",
+              padmode);
+  TORCH_CHECK(padlen >= 0 && T > padlen, "Input signal length ", T, " must be greater than pad length ", padlen, ".");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor bc = b.contiguous(), ac = a.contiguous(), xc = x.contiguous();
+  Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  if (B == 0) return y;
+  Tensor mid = at::empty({int64_t(phs_filtfilt_mid_size(dt, B, T))}, x.options().dtype(at::kByte));
+  void *stream = stream_of(x);
+  const Workspace ws = workspace_for(x, phs_filtfilt_workspace_size(dt, B, T), stream);
+  check_status(phs_filtfilt_fwd(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
+                                b.dim() == 1 ? 1 : 0, int(padmode), padlen, xc.const_data_ptr(), y.mutable_data_ptr(),
+                                mid.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+               "filtfilt");
+  return y;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(philtorch, m) {
@@ -494,6 +533,8 @@ TORCH_LIBRARY(philtorch, m) {
   m.def("sosfilt_backward(Tensor sos, Tensor x, Tensor ckpt, Tensor grad_y, Tensor? grad_zf, bool need_sos)"
         " -> (Tensor, Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
+  // new: zero-phase filtering, filters of second order at most (forward only)
+  m.def("filtfilt(Tensor b, Tensor a, Tensor x, int padmode, int padlen) -> Tensor", {at::Tag::pt2_compliant_tag});
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
@@ -509,4 +550,5 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("lti_recurN_backward", &lti_recurN_backward_hip);
   m.impl("sosfilt", &sosfilt_hip);
   m.impl("sosfilt_backward", &sosfilt_backward_hip);
+  m.impl("filtfilt", &filtfilt_hip);
 }

@@ -6,7 +6,8 @@ it through ``state_space`` (transposed direct form II by default), so with
 (``philtorch::lti_recur2`` for a biquad); a biquad in TDF-II form runs the
 fused cascade kernel instead (Bx, scan, state shift and output in one pass),
 unless forward-mode AD is active.  ``filtfilt`` and ``lfilter_zi`` follow the
-reference and SciPy.  Cascaded second-order sections are composed by the
+reference and SciPy; a biquad ``filtfilt`` with no gradient wanted runs both
+passes in philtorch::filtfilt.  Cascaded second-order sections are composed by the
 caller, one ``lfilter`` per section, as in the reference (it has no SOS API),
 or all at once by ``sosfilt``, which on a HIP device runs the whole cascade in
 one fused kernel per direction.
@@ -148,6 +149,48 @@ def lfilter(
     return y.squeeze(0) if squeeze_first else y
 
 
+# torch.nn.functional.pad modes with a fused filtfilt (PHS_PAD_* codes)
+_PAD_CODES = {"constant": 0, "replicate": 1, "reflect": 2, "circular": 3}
+
+
+def _fused_filtfilt_applies(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[str], form: str, kwargs) -> bool:
+    """A filter of second order at most on a HIP device with the native route
+    requested (``unroll_factor=1``) and no gradient wanted: philtorch::filtfilt
+    runs both passes with the padding, the flips and the trim folded in.  Its
+    output is the same for the ``tdf2`` and ``df2`` forms (each pass starts
+    from the steady state of the same transfer function)."""
+    from .. import EXTENSION_LOADED
+
+    if not (EXTENSION_LOADED and x.is_cuda and form in ("tdf2", "df2") and set(kwargs) == {"unroll_factor"}
+            and kwargs["unroll_factor"] == 1):
+        return False
+    if padmode is not None and padmode not in _PAD_CODES:
+        return False
+    if not (1 <= a.size(-1) <= 2 and 1 <= b.size(-1) <= 3) or x.dtype not in (torch.float32, torch.float64):
+        return False
+    if b.dtype != x.dtype or a.dtype != x.dtype or x.dim() not in (1, 2):
+        return False
+    if b.dim() != a.dim() or b.dim() not in (1, 2):
+        return False
+    if b.dim() == 2 and not (x.dim() == 2 and b.size(0) == a.size(0) == x.size(0)):
+        return False
+    if not hasattr(torch.ops.philtorch, "filtfilt"):
+        return False
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (b, a, x)):
+        return False
+    import torch.autograd.forward_ad as fwad
+
+    return all(fwad.unpack_dual(t).tangent is None for t in (b, a, x))
+
+
+def _fused_filtfilt(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[str], edge: int) -> Tensor:
+    """filtfilt of a filter of second order at most through philtorch::filtfilt."""
+    x2 = x.reshape(-1, x.size(-1))
+    code = _PAD_CODES[padmode] if padmode is not None else 0
+    y = torch.ops.philtorch.filtfilt(b, a, x2, code, edge if padmode is not None else 0)
+    return y.reshape(x.shape)
+
+
 def filtfilt(
     b: Tensor,
     a: Tensor,
@@ -161,7 +204,11 @@ def filtfilt(
 ) -> Tensor:
     """Zero-phase filtering: a forward and a reversed ``lfilter`` pass with
     edge padding and steady-state initial conditions
-    (philtorch/lti/filtering.py:413-484)."""
+    (philtorch/lti/filtering.py:413-484).  A biquad on a HIP device with
+    ``unroll_factor=1`` and no gradient wanted runs philtorch::filtfilt (two
+    cascade passes and two small edge kernels, no padded copy, no flips and no
+    host synchronisation); otherwise the passes are composed as in the
+    reference, each biquad pass on the fused lfilter route."""
     assert method in ("pad", "gust"), "Method must be either 'pad' or 'gust'."
     if method == "gust":
         raise NotImplementedError("Gustafsson's method is not implemented yet.")
@@ -170,6 +217,8 @@ def filtfilt(
     ntaps = max(b.size(-1), a.size(-1) + 1)
     edge = 3 * ntaps if padlen is None else padlen
     assert x.size(-1) > edge, f"Input signal length {x.size(-1)} must be greater than pad length {edge}."
+    if _fused_filtfilt_applies(b, a, x, padmode, form, kwargs):
+        return _fused_filtfilt(b, a, x, padmode, edge)
     if edge > 0 and padmode is not None:
         ext = F.pad(x.view(-1, x.size(-1)), (edge, edge), mode=padmode)
         if x.dim() == 1:

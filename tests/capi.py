@@ -15,6 +15,8 @@ LIB_PATH = os.path.join(REPO, "philtorch_amd", "libphilscan.so")
 HEADER = os.path.join(REPO, "include", "philscan.h")
 
 PHS_OK, PHS_ERR_INVALID, PHS_ERR_WORKSPACE, PHS_ERR_LAUNCH, PHS_ERR_DTYPE = range(5)
+# phs_padmode codes (torch.nn.functional.pad modes)
+PADMODES = {"constant": 0, "replicate": 1, "reflect": 2, "circular": 3}
 OPS = {"recur": 0, "lti_recur": 1, "recur2": 2, "lti_recur2": 3}
 OPS_N = {"recurN": 4, "lti_recurN": 5}  # order-M ops (entry points take M after dtype)
 DTYPES = {np.dtype(np.float32): 0, np.dtype(np.float64): 1, np.dtype(np.complex64): 2,
@@ -73,4 +75,14 @@ def load() -> ctypes.CDLL:
                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                     ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.phs_sosfilt_bwd.restype = ctypes.c_int
+    # zero-phase biquad filter
+    lib.phs_filtfilt_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
+    lib.phs_filtfilt_workspace_size.restype = ctypes.c_size_t
+    lib.phs_filtfilt_mid_size.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
+    lib.phs_filtfilt_mid_size.restype = ctypes.c_size_t
+    lib.phs_filtfilt_fwd.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                     ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_size_t, ctypes.c_void_p]
+    lib.phs_filtfilt_fwd.restype = ctypes.c_int
     return lib

@@ -1,0 +1,264 @@
+"""GPU parity of the zero-phase filter (phs_filtfilt_fwd, op
+philtorch::filtfilt, the fused route of philtorch_amd.lti.filtfilt for
+filters of first and second order).
+
+The C ABI entry point (ctypes, raw device pointers, the caller's stream)
+against oracle.filtfilt, which follows the reference's filtfilt step by step
+(pad, lfilter_zi, lfilter, flip, lfilter, trim, flip; pinned to
+scipy.signal.filtfilt in tests/test_oracle.py), evaluated in fp64 on the GPU's
+exact inputs.  Covers every pad mode at padlen 0, 9, an intermediate length
+and the largest allowed (T - 1); rows shorter than a lane's chunk, on and
+around a tile (6144 steps) and a cascade forward tile (12288), of odd length (scalar loads)
+and of a million steps; shared and per-row sections; the forced look-back
+fallback of both passes.  Through the torch API: scipy (second- and
+first-order filters), the composed route
+(each pass an lfilter) at the benchmark's C4 size, the route choice, and
+gradients (which take the composed route).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from tests import _data as D
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1), (2, 17), (3, 6143), (2, 6144), (2, 12287), (3, 12288), (2, 12289), (2, 6145), (1, 40000), (2, 30001)]
+FLOATS = [np.float32, np.float64]
+MODES = ["constant", "replicate", "reflect", "circular"]
+
+
+@pytest.fixture(scope="module")
+def api(hip):
+    import torch
+
+    from tests import capi
+
+    lib = capi.load()
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+    yield lib, ws, capi
+    lib.phs_debug_set_spin_limit(0)
+
+
+def _dev(x):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream():
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _run(api, sos, x, padmode, padlen):
+    """phs_filtfilt_fwd through the C ABI; numpy y."""
+    import torch
+
+    lib, ws, capi = api
+    dt = capi.DTYPES[np.dtype(x.dtype)]
+    B, T = x.shape
+    need = lib.phs_filtfilt_workspace_size(dt, B, T)
+    assert 0 < need <= ws.numel()
+    mid = torch.empty(lib.phs_filtfilt_mid_size(dt, B, T), dtype=torch.uint8, device="cuda")
+    tb, ta, tx = _dev(sos[..., 0:3]), _dev(sos[..., 4:6]), _dev(x)
+    y = torch.full_like(tx, float("nan"))
+    rc = lib.phs_filtfilt_fwd(dt, B, T, _p(tb), 3, _p(ta), 2, int(sos.ndim == 1), capi.PADMODES[padmode], padlen,
+                              _p(tx), _p(y), _p(mid), _p(ws), need, _stream())
+    assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def _case(dtype, B, T, shared, seed):
+    g = D.rng(seed)
+    sos = D.sos_coefs(g, () if shared else (B,), 1, dtype, rhi=0.98)[..., 0, :]
+    x = D.normal(g, (B, T), dtype)
+    return sos, x
+
+
+def _check(y, sos, x, padmode, padlen, dtype, name):
+    ref = oracle.filtfilt(np.asarray(sos, np.float64), np.asarray(x, np.float64), padmode=padmode, padlen=padlen)
+    D.check(y, ref, name, dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("B,T", SHAPES)
+def test_filtfilt_capi_parity(api, dtype, B, T):
+    for shared in (False, True):
+        sos, x = _case(dtype, B, T, shared, D.seed_of("filtfilt", dtype, B, T, shared))
+        for mode in MODES:
+            for padlen in sorted({0, min(9, T - 1), T // 3, T - 1}):
+                y = _run(api, sos, x, mode, padlen)
+                _check(y, sos, x, mode, padlen, dtype, f"B={B} T={T} shared={shared} {mode} padlen={padlen}")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_filtfilt_capi_long_rows(api, dtype):
+    sos, x = _case(dtype, 2, 1_000_003, False, D.seed_of("filtfilt-long", dtype))
+    for mode, padlen in (("replicate", 9), ("reflect", 4097)):
+        _check(_run(api, sos, x, mode, padlen), sos, x, mode, padlen, dtype, f"long rows {mode}")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_filtfilt_capi_forced_fallback(api, dtype):
+    """A one-poll budget makes the tiles of both passes compute their entry
+    states from the row prefix (pass 1) or suffix (pass 2) themselves."""
+    lib = api[0]
+    sos, x = _case(dtype, 3, 40000, False, D.seed_of("filtfilt-fallback", dtype))
+    lib.phs_debug_set_spin_limit(1)
+    try:
+        y = _run(api, sos, x, "replicate", 9)
+    finally:
+        lib.phs_debug_set_spin_limit(0)
+    _check(y, sos, x, "replicate", 9, dtype, "fallback")
+
+
+def test_filtfilt_capi_constant_row_full_size(api):
+    """At the C4 size a constant row comes out scaled by H(1)^2 for every
+    edge-value pad: both passes start in, and stay in, their steady state."""
+    B, T = 16, 480000
+    g = D.rng(D.seed_of("filtfilt-dc"))
+    sos = D.sos_coefs(g, (B,), 1, np.float64, rhi=0.98)[:, 0, :]
+    h1 = sos[:, :3].sum(-1) / (1 + sos[:, 4] + sos[:, 5])
+    x = np.full((B, T), 0.75)
+    for mode in ("replicate", "reflect", "circular"):
+        y = _run(api, sos, x, mode, 9)
+        D.check(y, np.broadcast_to((h1 * h1 * 0.75)[:, None], (B, T)), f"constant row {mode}", dtype=np.float64)
+
+
+def test_filtfilt_capi_linearity_full_size(api):
+    """filtfilt is linear in x for a fixed filter and pad mode (the edge
+    states scale with the row): f(2u - 3v) = 2 f(u) - 3 f(v) at the C4 size."""
+    B, T = 16, 480000
+    g = D.rng(D.seed_of("filtfilt-linear"))
+    sos = D.sos_coefs(g, (B,), 1, np.float64, rhi=0.98)[:, 0, :]
+    u, v = g.standard_normal((B, T)), g.standard_normal((B, T))
+    for mode in MODES:
+        lhs = _run(api, sos, 2 * u - 3 * v, mode, 9)
+        rhs = 2 * _run(api, sos, u, mode, 9) - 3 * _run(api, sos, v, mode, 9)
+        D.check(lhs, rhs, f"linearity {mode}", dtype=np.float64)
+
+
+# ---------------------------------------------------------------- torch API
+def _biquad(g, lead, dtype):
+    sos = D.sos_coefs(g, lead, 1, np.float64, rhi=0.98)[..., 0, :]
+    return sos[..., 0:3].astype(dtype), sos[..., 4:6].astype(dtype)
+
+
+def test_filtfilt_route_choice(hip):
+    import torch
+
+    from philtorch_amd.lti import filtering
+
+    g = D.rng(D.seed_of("filtfilt-route"))
+    b, a = (torch.tensor(v, device="cuda") for v in _biquad(g, (3,), np.float32))
+    x = torch.randn(3, 100, device="cuda")
+    ok = {"unroll_factor": 1}
+    assert filtering._fused_filtfilt_applies(b, a, x, "replicate", "tdf2", ok)
+    assert filtering._fused_filtfilt_applies(b, a, x, None, "df2", ok)
+    assert filtering._fused_filtfilt_applies(b[0], a[0], x[0], "circular", "tdf2", ok)
+    assert not filtering._fused_filtfilt_applies(b, a, x, "replicate", "tdf2", {})
+    assert not filtering._fused_filtfilt_applies(b, a, x, "odd", "tdf2", ok)
+    assert not filtering._fused_filtfilt_applies(b, a, x[:2], "replicate", "tdf2", ok)
+    assert filtering._fused_filtfilt_applies(b[:, :2], a[:, :1], x, "replicate", "tdf2", ok)
+    assert not filtering._fused_filtfilt_applies(torch.ones(3, 4, device="cuda"), a, x, "replicate", "tdf2", ok)
+    assert not filtering._fused_filtfilt_applies(b, a, x.requires_grad_(), "replicate", "tdf2", ok)
+    with torch.no_grad():
+        assert filtering._fused_filtfilt_applies(b, a, x, "replicate", "tdf2", ok)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_filtfilt_api_matches_scipy(hip, dtype):
+    import scipy.signal as sg
+    import torch
+
+    from philtorch_amd.lti import filtering
+
+    g = D.rng(D.seed_of("filtfilt-api", dtype))
+    for shape, batched, order in (((3, 5000), False, 2), ((3, 5000), True, 2), ((777,), False, 2),
+                                  ((3, 5000), True, 1), ((3, 5000), False, 1)):
+        b, a = _biquad(g, (shape[0],) if batched else (), np.float64)
+        if order == 1:  # b0 + b1 z^-1 over 1 + a1 z^-1, pole in (-0.95, 0.95)
+            b, a = b[..., :2], np.clip(a[..., :1], -0.95, 0.95)
+        x = g.standard_normal(shape)
+        tb, ta, tx = (torch.tensor(v.astype(dtype), device="cuda") for v in (b, a, x))
+        for padmode, padlen, padtype in (("replicate", None, "constant"), ("reflect", 100, "even"),
+                                         (None, None, None)):
+            for form in ("tdf2", "df2"):
+                assert filtering._fused_filtfilt_applies(tb, ta, tx, padmode, form, {"unroll_factor": 1})
+                y = hip.lti.filtfilt(tb, ta, tx, padmode=padmode, padlen=padlen, form=form, unroll_factor=1)
+                if batched:
+                    ref = np.stack([sg.filtfilt(b[r], np.r_[1.0, a[r]], x[r], padtype=padtype,
+                                                padlen=padlen if padtype else None)
+                                    for r in range(shape[0])])
+                else:
+                    ref = sg.filtfilt(b, np.r_[1.0, a], x, axis=-1, padtype=padtype,
+                                      padlen=padlen if padtype else None)
+                D.check(y.cpu().numpy(), ref.astype(dtype), f"{shape} {batched} {padmode} {form}")
+
+
+def test_filtfilt_api_c4_size_matches_composed_route(hip):
+    """The benchmark's filtfilt pattern at the C4 size (B=16, T=480000, fp32,
+    one filtfilt per section, padmode replicate, padlen 9): the fused route
+    against the composed one (padding, two lfilter passes, flips), which the
+    same call takes when x requires a gradient."""
+    import torch
+
+    g = D.rng(D.seed_of("filtfilt-c4"))
+    B, T, S = 16, 480000, 8
+    sos = torch.tensor(D.sos_coefs(g, (B,), S, np.float32, rhi=0.98), device="cuda")
+    x = torch.tensor(g.standard_normal((B, T)).astype(np.float32), device="cuda")
+    outs = []
+    for grad in (False, True):
+        y = x.clone().requires_grad_(grad)
+        for s in range(S):
+            y = hip.lti.filtfilt(sos[:, s, :3], sos[:, s, 4:], y, padmode="replicate", padlen=9, unroll_factor=1)
+        outs.append(y.detach().cpu().numpy())
+    D.check(outs[0], outs[1], "8 filtfilts")
+
+
+def test_filtfilt_api_gradients_take_composed_route(hip):
+    import torch
+
+    g = D.rng(D.seed_of("filtfilt-grad"))
+    b, a = (torch.tensor(v, device="cuda", requires_grad=True) for v in _biquad(g, (2,), np.float64))
+    x = torch.tensor(g.standard_normal((2, 40)), device="cuda", requires_grad=True)
+    f = lambda b_, a_, x_: hip.lti.filtfilt(b_, a_, x_, padlen=5, unroll_factor=1)  # noqa: E731
+    assert torch.autograd.gradcheck(f, (b, a, x))
+    with torch.no_grad():
+        fused = f(b, a, x)
+    D.check(fused.cpu().numpy(), f(b, a, x).detach().cpu().numpy(), "no-grad vs grad route")
+
+
+def test_filtfilt_api_errors(hip):
+    import torch
+
+    b, a = torch.tensor([0.5, 0.2, 0.1], device="cuda"), torch.tensor([-0.5, 0.2], device="cuda")
+    with pytest.raises(AssertionError, match="must be greater than pad length"):
+        hip.lti.filtfilt(b, a, torch.randn(2, 9, device="cuda"), unroll_factor=1)
+    with pytest.raises(RuntimeError, match="must be greater than pad length"):
+        torch.ops.philtorch.filtfilt(b, a, torch.randn(2, 9, device="cuda"), 1, 9)
+    with pytest.raises(RuntimeError, match="second order at most"):
+        torch.ops.philtorch.filtfilt(torch.ones(4, device="cuda"), a, torch.randn(2, 90, device="cuda"), 1, 9)
+
+
+def test_filtfilt_opcheck(hip):
+    import torch
+
+    g = D.rng(D.seed_of("filtfilt-opcheck"))
+    sos = torch.tensor(D.sos_coefs(g, (), 1, np.float32), device="cuda")
+    x = torch.tensor(g.standard_normal((2, 700)).astype(np.float32), device="cuda")
+    b, a = sos[0, :3].contiguous(), sos[0, 4:].contiguous()
+    torch.library.opcheck(torch.ops.philtorch.filtfilt.default, (b, a, x, 1, 9),
+                          test_utils=("test_schema", "test_faketensor"))
+    torch.library.opcheck(torch.ops.philtorch.filtfilt.default,
+                          (b.expand(2, 3).contiguous(), a[:1].expand(2, 1).contiguous(), x, 2, 0),
+                          test_utils=("test_schema", "test_faketensor"))

@@ -22,7 +22,7 @@ def test_capi_exports_every_declared_symbol():
 
 def test_capi_host_only_calls():
     lib = capi.load()
-    assert lib.phs_abi_version() == 102
+    assert lib.phs_abi_version() == 103
     for op in capi.OPS.values():
         for dt in capi.DTYPES.values():
             fwd = lib.phs_workspace_size(op, dt, 64, 65536, 0, 0)
@@ -235,3 +235,41 @@ def test_capi_sosfilt_host_only_calls():
     assert lib.phs_sosfilt_bwd(0, 2, 100, 3, d, 0, None, d, d, None, d, d, None, d, ws, None) == capi.PHS_ERR_INVALID
     assert lib.phs_sosfilt_bwd(1, 2, 100, 3, d, 0, d, None, d, None, d, d, None, d, ws, None) == capi.PHS_ERR_INVALID
     assert lib.phs_sosfilt_fwd(0, 0, 100, 3, None, 0, None, None, None, None, None, None, 0, None) == capi.PHS_OK
+
+
+def test_capi_filtfilt_host_only_calls():
+    """Sizes and argument errors of the zero-phase filter entry point (nothing
+    launches)."""
+    lib = capi.load()
+    for dt, esz in ((0, 4), (1, 8)):
+        assert lib.phs_filtfilt_workspace_size(dt, 16, 480000) > 0
+        # pass 1's output, three [B, 2] state arrays and the [B, 6] section rows
+        assert lib.phs_filtfilt_mid_size(dt, 16, 480000) >= 16 * 480000 * esz + 3 * 16 * 2 * esz + 16 * 6 * esz
+    for bad in ((2, 16, 100), (0, -1, 100), (0, 16, 0)):
+        assert lib.phs_filtfilt_workspace_size(*bad) == 0
+        assert lib.phs_filtfilt_mid_size(*bad) == 0
+    d = ctypes.c_void_p(16)
+    ws = 1 << 30
+    rep = capi.PADMODES["replicate"]
+
+    def call(dt=0, T=100, nb=3, na=2, mode=rep, padlen=9, mid=d, wsb=ws, B=2, b=d):
+        return lib.phs_filtfilt_fwd(dt, B, T, b, nb, d, na, 0, mode, padlen, d, d, mid, d, wsb, None)
+
+    assert call(dt=2) == capi.PHS_ERR_DTYPE
+    assert call(padlen=100) == capi.PHS_ERR_INVALID  # the reference asserts T > padlen
+    assert call(padlen=-1) == capi.PHS_ERR_INVALID
+    assert call(T=0, padlen=0) == capi.PHS_ERR_INVALID
+    assert call(mode=4) == capi.PHS_ERR_INVALID
+    assert call(nb=4) == capi.PHS_ERR_INVALID and call(nb=0) == capi.PHS_ERR_INVALID
+    assert call(na=3) == capi.PHS_ERR_INVALID and call(na=0) == capi.PHS_ERR_INVALID
+    assert call(mid=None) == capi.PHS_ERR_INVALID and call(b=None) == capi.PHS_ERR_INVALID
+    need = lib.phs_filtfilt_workspace_size(0, 2, 100)
+    assert call(wsb=need - 1) == capi.PHS_ERR_WORKSPACE
+    assert lib.phs_filtfilt_fwd(0, 0, 100, None, 3, None, 2, 0, rep, 9, None, None, None, None, 0, None) == capi.PHS_OK
+
+
+def test_filtfilt_fused_route_not_taken_on_cpu():
+    from philtorch_amd.lti import filtering
+
+    b, a, x = torch.tensor([0.5, 0.2, 0.1]), torch.tensor([-0.5, 0.2]), torch.randn(2, 50)
+    assert not filtering._fused_filtfilt_applies(b, a, x, "replicate", "tdf2", {"unroll_factor": 1})

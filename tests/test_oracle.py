@@ -310,3 +310,60 @@ def test_sosfilt_backward_matches_serial_autograd(batched):
     D.check(gs, ref_gs, "grad_sos")
     D.check(gzi, tz.grad.numpy(), "grad_zi")
     D.check(gx, tx.grad.numpy(), "grad_x")
+
+
+# ---------------------------------------------------------------- filtfilt
+def _scipy_filtfilt_composed(b, a, x, np_mode, edge):
+    """filtfilt step by step on scipy's lfilter_zi and lfilter, with numpy's
+    padding (for the pad modes scipy.signal.filtfilt has no padtype for)."""
+    den = np.r_[1.0, a]
+    ext = np.pad(x, (edge, edge), mode=np_mode) if edge else x
+    zi = scipy.signal.lfilter_zi(b, den)
+    y, _ = scipy.signal.lfilter(b, den, ext, zi=zi * ext[0])
+    y2, _ = scipy.signal.lfilter(b, den, y[::-1], zi=zi * y[-1])
+    return (y2[edge:-edge] if edge else y2)[::-1]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("batched", [False, True])
+def test_filtfilt_matches_scipy(dtype, batched):
+    """oracle.filtfilt against scipy.signal.filtfilt: F.pad's "replicate" is
+    scipy's padtype "constant" (edge values), "reflect" is "even", and no
+    padding is padtype None; "constant" (zeros) and "circular" against the
+    same steps on scipy's lfilter_zi / lfilter and numpy's padding."""
+    g = D.rng(D.seed_of("oracle-filtfilt", dtype, batched))
+    B, T = 3, 500
+    sos = D.sos_coefs(g, (B,) if batched else (), 1, np.float64, rhi=0.98)[..., 0, :]
+    x = g.standard_normal((B, T))
+    cases = [("replicate", 9, "constant"), ("reflect", 9, "even"), ("replicate", 40, "constant"),
+             ("reflect", T - 1, "even"), (None, None, None)]
+    for padmode, padlen, padtype in cases:
+        y = oracle.filtfilt(sos.astype(dtype), x.astype(dtype), padmode=padmode, padlen=padlen)
+        for r in range(B):
+            s = sos[r] if batched else sos
+            ref = scipy.signal.filtfilt(s[:3], np.r_[1.0, s[4:]], x[r], padtype=padtype,
+                                        padlen=padlen if padtype else None)
+            D.check(y[r], ref.astype(dtype), f"{padmode} {padlen} row {r}")
+    for padmode, np_mode in (("constant", "constant"), ("circular", "wrap")):
+        for padlen in (9, T - 1):
+            y = oracle.filtfilt(sos.astype(dtype), x.astype(dtype), padmode=padmode, padlen=padlen)
+            for r in range(B):
+                s = sos[r] if batched else sos
+                ref = _scipy_filtfilt_composed(s[:3], s[4:], x[r], np_mode, padlen)
+                D.check(y[r], ref.astype(dtype), f"{padmode} {padlen} row {r}")
+
+
+def test_filtfilt_steady_state_and_lfilter_zi():
+    """A constant row comes out scaled by H(1)^2 for every edge-value pad (the
+    padded row is constant and both passes start in their steady state), and
+    lfilter_zi is the fixed point of one TDF-II step."""
+    g = D.rng(D.seed_of("oracle-filtfilt-dc"))
+    sos = D.sos_coefs(g, (4,), 1, np.float64)[:, 0, :]
+    h1 = sos[:, :3].sum(-1) / (1 + sos[:, 4] + sos[:, 5])
+    x = np.full((4, 300), 2.5)
+    for padmode in ("replicate", "reflect", "circular", None):
+        y = oracle.filtfilt(sos, x, padmode=padmode)
+        np.testing.assert_allclose(y, (h1 * h1 * 2.5)[:, None] * np.ones((1, 300)), rtol=1e-12)
+    zi = oracle.lfilter_zi(sos)
+    A, Bv, _, _ = oracle._tdf2_section(sos)
+    np.testing.assert_allclose(np.einsum("rij,rj->ri", A, zi) + Bv, zi, rtol=1e-12)
