@@ -17,6 +17,7 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c4_fused  philtorch::sosfilt + sosfilt_backward              (the same cascade, fused)
   c4_api  8 x lti.lfilter(tdf2, unroll_factor=1) + autograd   (the caller pattern, API level)
   c4_filtfilt  8 x lti.filtfilt(replicate, padlen 9), forward only (philtorch::filtfilt)
+  c4_lfilter4  4 x lti.lfilter of order 4 (tdf2), forward only (philtorch::lti_ss)
 Before every step a 512 MiB buffer is read end to end so the 256 MB Infinity
 Cache holds none of the step's operands (a read sweep, not a write: a write
 would leave dirty lines whose write-back then competes with the step); the
@@ -384,6 +385,60 @@ class FiltfiltApi(SosFused):
             y = oracle.filtfilt(sos[:rows, s], y, padmode="replicate", padlen=9, nthreads=nthreads)
 
 
+class Lfilter4Api(SosFused):
+    """c4_lfilter4: the C4 signal through order-4 filters, forward only: the
+    eight C4 biquads of each row multiplied pairwise into four order-4
+    filters, ``for s in range(4): y = lti.lfilter(b4[:, s], a4[:, s], y,
+    unroll_factor=1)`` (each call runs philtorch::lti_ss: B x, the 4x4 scan,
+    the state shift and C h + D x in one pass)."""
+
+    def __init__(self):
+        import numpy as np
+        import torch
+
+        super().__init__()
+        self.name = "c4_lfilter4"
+        self.S4 = self.S // 2
+        self.metric = (f"GSamples/s fwd, lti.lfilter order-4 x{self.S4} (tdf2) B={self.B} T={self.T} fp32 (API)")
+        sos = self.cpu[0].double()
+        self.b4, self.a4 = [], []
+        for s in range(self.S4):
+            p, q = sos[:, 2 * s], sos[:, 2 * s + 1]
+            b4 = torch.stack([torch.tensor(np.polymul(p[r, :3].numpy(), q[r, :3].numpy())) for r in range(self.B)])
+            a4 = torch.stack([torch.tensor(np.polymul(p[r, 3:].numpy(), q[r, 3:].numpy())) for r in range(self.B)])
+            a4 = a4[:, 1:]
+            self.b4.append(b4.float().cuda().contiguous())
+            self.a4.append(a4.float().cuda().contiguous())
+        self.fwd_bytes = 8 * self.B * self.T  # per lfilter: read x, write y
+        self.bwd_bytes = 0
+        self.launches = self.S4
+
+    def step_fwd(self):
+        from philtorch_amd import lti
+
+        y = self.dev[1]
+        for s in range(self.S4):
+            y = lti.lfilter(self.b4[s], self.a4[s], y, form="tdf2", unroll_factor=1)
+        return y
+
+    def step_bwd(self, out):
+        return out
+
+    def cpu_step(self, rows, steps, nthreads):
+        import numpy as np
+
+        import oracle
+
+        x = self.cpu[1].numpy()[:rows, :steps]
+        for s in range(self.S4):
+            b, a = self.b4[s].cpu().numpy()[:rows], self.a4[s].cpu().numpy()[:rows]
+            A = np.zeros((rows, 4, 4), dtype=x.dtype)
+            A[:, :, 0] = -a
+            A[:, np.arange(3), np.arange(1, 4)] = 1.0  # companion(a)^T (TDF-II)
+            x, _ = oracle.lti_state_space(A, x, b[:, 1:] - b[:, :1] * a, None, b[:, 0], None, out_idx=0,
+                                          nthreads=nthreads)
+
+
 def make_workload(name):
     if name == "c1":
         return LpvScalar("c1", 64, 65536, "float32")
@@ -403,10 +458,12 @@ def make_workload(name):
         return SosApi()
     if name == "c4_filtfilt":
         return FiltfiltApi()
+    if name == "c4_lfilter4":
+        return Lfilter4Api()
     raise ValueError(name)
 
 
-CONFIGS = ("c1", "c2", "c3", "c4", "c4_fused", "c4_api", "c4_filtfilt", "c5", "c5_f64")
+CONFIGS = ("c1", "c2", "c3", "c4", "c4_fused", "c4_api", "c4_filtfilt", "c4_lfilter4", "c5", "c5_f64")
 
 
 # ----------------------------------------------------------------------------
@@ -550,6 +607,7 @@ def main() -> int:
                 "c4_fused": "lti_sos8_cascade_fused_fwd_bwd_B16_T480000_f32",
                 "c4_api": "lti_lfilter8_cascade_api_fwd_bwd_B16_T480000_f32",
                 "c4_filtfilt": "lti_filtfilt8_api_fwd_B16_T480000_f32",
+                "c4_lfilter4": "lti_lfilter_order4_x4_api_fwd_B16_T480000_f32",
                 "c5": "lpv_scan_fwd_bwd_B8_T16777216_f32",
                 "c5_f64": "lpv_scan_fwd_bwd_B8_T16777216_f64",
             }[w.name],
@@ -567,7 +625,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{'sos_kernel' if w.name.startswith('c4_') else 'scan_kernel'} ({dominant[0]})",
+            "kernel": f"{'ss_kernel' if w.name == 'c4_lfilter4' else 'sos_kernel' if w.name.startswith('c4_') else 'scan_kernel'} ({dominant[0]})",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

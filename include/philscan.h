@@ -252,6 +252,26 @@ int phs_filtfilt_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, con
                      int coef_shared, int padmode, int64_t padlen, const void *x, void *y, void *mid, void *workspace,
                      size_t workspace_bytes, void *stream);
 
+/* ---- Single-input, single-output LTI state space of order M = 1..4, fused
+ * (forward).  Replaces philtorch.lti.state_space (philtorch/lti/ssm.py:
+ * 386-510 with _ssm_C_D :513-589) for a 2D input x, B an M-vector (or
+ * absent: the input enters state 0, as _ext_ss_recur pads it, :186-191), C
+ * an M-vector or out_idx, D one value per row (or absent):
+ *     h[0] = zi,  y[t] = c . h[t] + d x[t],  h[t+1] = A h[t] + b x[t],  zf = h[T]
+ * in one pass, instead of the B x product, the scan, the shifted copy and
+ * C h + D x (the route of lfilter in companion form, lti/filtering.py:
+ * 273-333).  dtype PHS_F32 or PHS_F64; A: [B,M,M] or [M,M] (A_shared);
+ * b, c: [B,M] or [M] (*_shared), b NULL = e0, c NULL = e_out_idx; d: [B] or
+ * one value (d_shared), NULL = 0; zi [B,M] (NULL = zeros); x, y [B,T];
+ * zf [B,M] (skipped when NULL). */
+
+/* Workspace bytes of phs_lti_ss_fwd; 0 for unsupported arguments. */
+size_t phs_lti_ss_workspace_size(int dtype, int M, int64_t B, int64_t T);
+
+int phs_lti_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b, int b_shared,
+                   const void *c, int c_shared, int out_idx, const void *d, int d_shared, const void *zi,
+                   const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

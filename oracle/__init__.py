@@ -295,3 +295,33 @@ def filtfilt(sos, x, padmode="replicate", padlen=None, nthreads=None):
         y = y[:, edge:-edge]
     return np.ascontiguousarray(y[:, ::-1])
 
+
+
+def lti_state_space(A, x, B=None, C=None, D=None, zi=None, out_idx=None, nthreads=None):
+    """philtorch.lti.state_space for a 2D input and a single output
+    (philtorch/lti/ssm.py:386-589): Bx = x b (b an M-vector per row or shared;
+    None = the input enters state 0, as _ext_ss_recur pads it), the scan
+    lti_recurN, the state sequence shifted by one step behind zi, then
+    y = C h + D x (C an M-vector per row or shared, or state out_idx; D one
+    value or one per row).  Returns (y [B,T], zf [B,M])."""
+    dt = np.asarray(x).dtype
+    x = _c(x, dt)
+    Bn, T = x.shape
+    A = _c(np.broadcast_to(A, (Bn,) + np.shape(A)[-2:]), dt)
+    M = A.shape[-1]
+    zi = np.zeros((Bn, M), dtype=dt) if zi is None else _c(np.broadcast_to(zi, (Bn, M)), dt)
+    if B is None:
+        Bx = np.zeros((Bn, T, M), dtype=dt)
+        Bx[..., 0] = x
+    else:
+        Bx = x[..., None] * np.broadcast_to(np.asarray(B, dtype=dt), (Bn, M))[:, None, :]
+    h = lti_recurN(A, zi, _c(Bx, dt), nthreads)
+    zf = h[:, -1] if T > 0 else zi.copy()
+    hprev = np.concatenate([zi[:, None, :], h[:, :-1]], axis=1)
+    if C is None:
+        y = hprev[..., out_idx].copy()
+    else:
+        y = np.einsum("btm,bm->bt", hprev, np.broadcast_to(np.asarray(C, dtype=dt), (Bn, M)))
+    if D is not None:
+        y = y + np.broadcast_to(np.asarray(D, dtype=dt).reshape(-1), (Bn,))[:, None] * x
+    return _c(y, dt), _c(zf, dt)

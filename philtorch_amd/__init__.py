@@ -6,8 +6,10 @@ namespace: the reference's five ops (``recur2``, ``recurN``, ``lti_recur2``,
 ``lti_recurN``, ``lti_recur``; philtorch/csrc/host_recur2.cpp:162-171), the new
 LPV scalar op ``recur``, four fused backward ops, and the fused cascade of
 second-order sections ``sosfilt`` / ``sosfilt_backward`` (no reference
-counterpart; ``lti.sosfilt`` is its API) and the forward-only zero-phase
-``filtfilt`` of filters up to second order (behind ``lti.filtfilt``).  This module then
+counterpart; ``lti.sosfilt`` is its API), the forward-only zero-phase
+``filtfilt`` of filters up to second order (behind ``lti.filtfilt``) and the
+fused single-input single-output state space ``lti_ss`` (behind
+``lti.state_space`` and so ``lti.lfilter``).  This module then
 registers fake (meta) kernels and autograd formulas for them, as
 philtorch/__init__.py:157-268 does for its ops.
 
@@ -331,6 +333,43 @@ if EXTENSION_LOADED and _has_op("filtfilt"):
         torch._check(1 <= b.shape[-1] <= 3 and 1 <= a.shape[-1] <= 2, lambda: "second order at most")
         torch._check(0 <= padlen < x.shape[1], lambda: "0 <= padlen < T")
         return _fake_like(x)
+
+if EXTENSION_LOADED and _has_op("lti_ss"):
+    # single-input single-output LTI state space of order <= 4: (y, zf)
+    @torch.library.register_fake("philtorch::lti_ss")
+    def _(A, B, C, D, zi, x, out_idx):
+        torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
+        torch._check(A.ndim in (2, 3) and A.shape[-1] == A.shape[-2], lambda: "A must be (M, M) or (batch, M, M)")
+        return _fake_like(x), x.new_empty((x.shape[0], A.shape[-1]))
+
+    def _lti_ss_setup(ctx, inputs, output):
+        A, B, C, D, zi, x, out_idx = inputs
+        ctx.out_idx = out_idx
+        ctx.save_for_backward(A, B, C, D, zi, x)
+
+    def _lti_ss_backward(ctx, gy, gzf):
+        """Gradient of the composite the fused kernel replaces (B x, the native
+        scan, the state shift, C h + D x; philtorch/lti/ssm.py:386-589),
+        recomputed from the inputs; differentiable again under create_graph."""
+        from .lti.ssm import _state_space_composite
+
+        inputs = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
+        with torch.enable_grad():
+            y, zf = _state_space_composite(*inputs, out_idx=ctx.out_idx)
+            outs, grads = [y], [gy if gy is not None else torch.zeros_like(y)]
+            if gzf is not None:
+                outs.append(zf)
+                grads.append(gzf)
+            res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=torch.is_grad_enabled(),
+                                      allow_unused=True)
+        out = [None] * 7
+        for i, g in zip(wrt, res):
+            out[i] = g if g is not None else torch.zeros_like(inputs[i])
+        return tuple(out)
+
+    torch.library.register_autograd("philtorch::lti_ss", _lti_ss_backward, setup_context=_lti_ss_setup)
 
 from . import mat  # noqa: E402,F401
 from . import lti  # noqa: E402,F401

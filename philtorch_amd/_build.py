@@ -4,9 +4,10 @@ Two shared objects, both written next to this file so that they travel with
 the repository tree:
 
 * ``libphilscan.so`` — the HIP kernels and their C ABI (include/philscan.h),
-  compiled by hipcc for gfx950 only from five units compiled in parallel
+  compiled by hipcc for gfx950 only from six units compiled in parallel
   (fixed-order and order-M entry points, the order-3 and order-4 kernels,
-  the fused second-order-section cascade).
+  the fused second-order-section cascade with filtfilt, the fused
+  single-input single-output state space).
   It has no torch dependency.
 * ``_C.so`` — the torch.library operator layer (csrc/torch_ops.cpp), host C++
   linked against libtorch and libphilscan (found through ``$ORIGIN``).
@@ -59,13 +60,15 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 # (source, extra flags, object): the fixed-order and order-M entry points,
-# the generic BlockN kernels once per order, and the SOS cascade
+# the generic BlockN kernels once per order, the SOS cascade (and filtfilt),
+# and the single-input single-output state space
 KERNEL_UNITS = (
     ("phs_capi.hip", [], "phs_capi.o"),
     ("phs_capi_n.hip", [], "phs_capi_n.o"),
     ("phs_blockn.hip", ["-DPHS_BLOCKN_ORDER=3"], "phs_blockn3.o"),
     ("phs_blockn.hip", ["-DPHS_BLOCKN_ORDER=4"], "phs_blockn4.o"),
     ("phs_sos.hip", [], "phs_sos.o"),
+    ("phs_ss.hip", [], "phs_ss.o"),
 )
 
 

@@ -507,6 +507,72 @@ Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t p
   return y;
 }
 
+// Single-input single-output LTI state space of order <= 4, fused
+// (phs_lti_ss_fwd; philtorch/lti/ssm.py:386-589 for a 2D x): returns (y, zf).
+// A (M, M) or (batch, M, M); B, C None, (M,) or (batch, M); D None, one value
+// or (batch,); zi None or (batch, M); out_idx selects the output state when
+// C is None.
+std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
+                                      const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
+                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx) {
+  TORCH_CHECK(x.dim() == 2, "philtorch::lti_ss: x must be a 2D tensor (batch, time)");
+  TORCH_CHECK((A.dim() == 2 || A.dim() == 3) && A.size(-1) == A.size(-2),
+              "philtorch::lti_ss: A must be (M, M) or (batch, M, M)");
+  const int64_t B = x.size(0), T = x.size(1), M = A.size(-1);
+  TORCH_CHECK(M >= 1 && M <= kMaxOrder, "philtorch::lti_ss: state order 1 to ", kMaxOrder, ", got ", M);
+  if (A.dim() == 3) TORCH_CHECK(A.size(0) == B, "philtorch::lti_ss: a 3D A must have x's batch size");
+  TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,
+              "philtorch::lti_ss: float32 or float64 only, got ", x.scalar_type());
+  TORCH_CHECK(x.is_cuda(), "philtorch::lti_ss: philtorch_amd runs on HIP devices only (got ", x.device(), ")");
+  auto same = [&](const Tensor &t, const char *what) {
+    TORCH_CHECK(t.scalar_type() == x.scalar_type(), "philtorch::lti_ss: ", what, " must have x's scalar type");
+    TORCH_CHECK(t.device() == x.device(), "philtorch::lti_ss: all tensors must be on the same device");
+  };
+  same(A, "A");
+  auto vec_ok = [&](const Tensor &t) { return (t.dim() == 1 && t.size(0) == M) || (t.dim() == 2 && t.size(0) == B && t.size(1) == M); };
+  if (Bm) {
+    same(*Bm, "B");
+    TORCH_CHECK(vec_ok(*Bm), "philtorch::lti_ss: B must be (M,) or (batch, M)");
+  }
+  if (Cm) {
+    same(*Cm, "C");
+    TORCH_CHECK(vec_ok(*Cm), "philtorch::lti_ss: C must be (M,) or (batch, M)");
+  } else {
+    TORCH_CHECK(out_idx >= 0 && out_idx < M, "philtorch::lti_ss: out_idx must be in [0, ", M, ") when C is None");
+  }
+  if (Dm) {
+    same(*Dm, "D");
+    TORCH_CHECK(Dm->numel() == 1 || (Dm->dim() == 1 && Dm->size(0) == B),
+                "philtorch::lti_ss: D must hold one value or (batch,)");
+  }
+  if (zi) {
+    same(*zi, "zi");
+    TORCH_CHECK(zi->dim() == 2 && zi->size(0) == B && zi->size(1) == M, "philtorch::lti_ss: zi must be (batch, M)");
+  }
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor Ac = A.contiguous(), xc = x.contiguous();
+  Tensor bc = Bm ? Bm->contiguous() : Tensor(), cc = Cm ? Cm->contiguous() : Tensor();
+  Tensor dc = Dm ? Dm->contiguous() : Tensor(), zc = zi ? zi->contiguous() : Tensor();
+  Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  Tensor zf = at::empty({B, M}, x.options());
+  if (B == 0) return {y, zf};
+  if (T == 0) {
+    if (zi) zf.copy_(zc); else zf.zero_();
+    return {y, zf};
+  }
+  void *stream = stream_of(x);
+  const Workspace ws = workspace_for(x, phs_lti_ss_workspace_size(dt, int(M), B, T), stream);
+  check_status(phs_lti_ss_fwd(dt, int(M), B, T, Ac.const_data_ptr(), A.dim() == 2 ? 1 : 0,
+                              Bm ? bc.const_data_ptr() : nullptr, Bm && Bm->dim() == 1 ? 1 : 0,
+                              Cm ? cc.const_data_ptr() : nullptr, Cm && Cm->dim() == 1 ? 1 : 0, int(out_idx),
+                              Dm ? dc.const_data_ptr() : nullptr, Dm && Dm->numel() == 1 ? 1 : 0,
+                              zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(), y.mutable_data_ptr(),
+                              zf.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+               "lti_ss");
+  return {y, zf};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(philtorch, m) {
@@ -535,6 +601,9 @@ TORCH_LIBRARY(philtorch, m) {
         {at::Tag::pt2_compliant_tag});
   // new: zero-phase filtering, filters of second order at most (forward only)
   m.def("filtfilt(Tensor b, Tensor a, Tensor x, int padmode, int padlen) -> Tensor", {at::Tag::pt2_compliant_tag});
+  // new: single-input single-output LTI state space of order <= 4, fused: (y, zf)
+  m.def("lti_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx) -> (Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
@@ -551,4 +620,5 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("sosfilt", &sosfilt_hip);
   m.impl("sosfilt_backward", &sosfilt_backward_hip);
   m.impl("filtfilt", &filtfilt_hip);
+  m.impl("lti_ss", &lti_ss_hip);
 }

@@ -220,6 +220,51 @@ def _ssm_C_D(h: Tensor, x: Tensor, C: Optional[Tensor], D: Optional[Tensor], bat
     return Ch + Dx if Dx is not None else Ch
 
 
+def _fused_ss_applies(A: Tensor, x: Tensor, B, C, D, zi, unroll_factor, out_idx) -> bool:
+    """A single-input single-output model of order <= 4 (2D x; B, C an
+    M-vector per model or shared, or C replaced by out_idx; D one value per
+    row or shared) on a HIP device with the native route requested
+    (``unroll_factor=1``) and no gradient wanted: philtorch::lti_ss runs B x,
+    the scan, the state shift and C h + D x in one pass.  Where a gradient is
+    wanted the composed route runs (the op's own gradient recomputes that
+    route, so taking the op there would only add its forward); forward-mode
+    AD keeps the composed route too."""
+    from .. import EXTENSION_LOADED
+
+    if not (EXTENSION_LOADED and x.is_cuda and unroll_factor == 1 and x.dim() == 2):
+        return False
+    if not hasattr(torch.ops.philtorch, "lti_ss"):
+        return False
+    batch, M = x.size(0), A.size(-1)
+    if M > 4 or x.dtype not in (torch.float32, torch.float64):
+        return False
+    if any(t is not None and t.dtype != x.dtype for t in (A, B, C, D, zi)):
+        return False
+    if C is None and out_idx is None:
+        return False
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (A, B, C, D, zi, x)):
+        return False
+
+    def is_vec(t):
+        return tuple(t.shape) in ((M,), (batch, M))
+
+    if (B is not None and not is_vec(B)) or (C is not None and not is_vec(C)):
+        return False
+    if D is not None and not ((D.dim() <= 1 and D.numel() == 1) or tuple(D.shape) == (batch,)):
+        return False
+    import torch.autograd.forward_ad as fwad
+
+    return all(t is None or fwad.unpack_dual(t).tangent is None for t in (A, B, C, D, zi, x))
+
+
+def _state_space_composite(A, B, C, D, zi, x, out_idx=None):
+    """(y, zf) of the composed route (B x, the native scan, the shifted state
+    sequence, C h + D x) for what philtorch::lti_ss computes fused: its
+    autograd formula differentiates this."""
+    zi = x.new_zeros(x.size(0), A.size(-1)) if zi is None else zi
+    return _state_space(A, x, B, C, D, zi, 1, None if C is not None else out_idx, fused=False)
+
+
 def state_space(
     A: Tensor,
     x: Tensor,
@@ -235,8 +280,13 @@ def state_space(
     Mirrors philtorch/lti/ssm.py:386-510; returns ``(y, zf)`` when ``zi`` is
     given.  ``unroll_factor=None`` means ``round(sqrt(N))`` (blocked PyTorch
     route) as in the reference; ``unroll_factor=1`` on a HIP device runs the
-    native scan.
+    native scan, and a single-input single-output model of order <= 4 the
+    fused philtorch::lti_ss.
     """
+    return _state_space(A, x, B, C, D, zi, unroll_factor, out_idx, fused=True)
+
+
+def _state_space(A, x, B, C, D, zi, unroll_factor, out_idx, fused):
     assert x.dim() in (2, 3), f"Input signal must be 2D or 3D (batch, time, [features]), got {x.shape}"
     assert A.dim() in (2, 3), f"State matrix A must be 2D or 3D, got {A.shape}"
     assert A.size(-2) == A.size(-1), f"State matrix A must be square, got {A.shape}"
@@ -253,6 +303,10 @@ def state_space(
         zi = zi.unsqueeze(0).expand(batch, -1)
     if unroll_factor is None:
         unroll_factor = round(N**0.5)
+    if fused and _fused_ss_applies(A, x, B, C, D, zi, unroll_factor, out_idx):
+        y, zf = torch.ops.philtorch.lti_ss(A, B, C, D, zi.contiguous() if return_zf else None, x,
+                                           out_idx if C is None else 0)
+        return (y, zf) if return_zf else y
     features = -1 if x.dim() == 2 else x.size(-1)
     if B is not None:
         shape = tuple(B.shape)

@@ -1,0 +1,270 @@
+"""GPU parity of the fused single-input single-output LTI state space
+(phs_lti_ss_fwd, op philtorch::lti_ss, the route of philtorch_amd.lti.
+state_space and so of lti.lfilter for models of order <= 4).
+
+The C ABI entry point (ctypes, raw device pointers, the caller's stream)
+against oracle.lti_state_space (B x, the oracle's lti_recurN, the shifted
+state sequence and C h + D x, as philtorch composes them; pinned to
+scipy.signal.dlsim in tests/test_oracle.py), evaluated in fp64 on the GPU's
+exact inputs.  Orders 1 to 4; dense stable A (a companion matrix in a random
+basis); shared and per-row A, b, c, d; b absent (input into state 0), c
+absent (out_idx), d absent; initial and final states; rows shorter than a
+lane's chunk, on and around a tile (3072 fp32 steps, 1536 fp64), of odd
+length and of a million steps; the forced look-back fallback.  Through the
+torch API: lfilter of orders 1, 3 and 4 in both forms against the CPU
+(reference) route, state_space against its composed route, gradients
+(first and second order, through the composite formula), the route choice
+and opcheck.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from tests import _data as D
+from tests.test_oracle import _stable_model
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1), (2, 7), (3, 1535), (2, 1536), (2, 3071), (3, 3072), (2, 3073), (2, 20001)]
+FLOATS = [np.float32, np.float64]
+ORDERS = [1, 2, 3, 4]
+
+
+@pytest.fixture(scope="module")
+def api(hip):
+    import torch
+
+    from tests import capi
+
+    lib = capi.load()
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+    yield lib, ws, capi
+    lib.phs_debug_set_spin_limit(0)
+
+
+def _dev(x):
+    import torch
+
+    return None if x is None else torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream():
+    import torch
+
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _run(api, A, b, c, d, zi, x, out_idx=0, want_zf=True):
+    """phs_lti_ss_fwd through the C ABI; numpy (y, zf)."""
+    import torch
+
+    lib, ws, capi = api
+    dt = capi.DTYPES[np.dtype(x.dtype)]
+    Bn, T = x.shape
+    M = A.shape[-1]
+    need = lib.phs_lti_ss_workspace_size(dt, M, Bn, T)
+    assert 0 < need <= ws.numel()
+    tA, tb, tc, td, tz, tx = (_dev(v) for v in (A, b, c, d, zi, x))
+    y = torch.full_like(tx, float("nan"))
+    zf = torch.full((Bn, M), float("nan"), dtype=tx.dtype, device="cuda") if want_zf else None
+    sh = lambda v, nd: int(v is not None and np.ndim(v) == nd)  # noqa: E731
+    rc = lib.phs_lti_ss_fwd(dt, M, Bn, T, _p(tA), sh(A, 2), _p(tb), sh(b, 1), _p(tc), sh(c, 1), out_idx, _p(td),
+                            int(d is not None and np.size(d) == 1), _p(tz), _p(tx), _p(y), _p(zf), _p(ws), need,
+                            _stream())
+    assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+    torch.cuda.synchronize()
+    return y.cpu().numpy(), None if zf is None else zf.cpu().numpy()
+
+
+def _case(dtype, M, Bn, T, shared, seed):
+    g = D.rng(seed)
+    A, b, c, d = _stable_model(g, M, () if shared else (Bn,))
+    x = g.standard_normal((Bn, T))
+    zi = g.standard_normal((Bn, M))
+    cast = lambda v: None if v is None else np.asarray(v).astype(dtype)  # noqa: E731
+    return [cast(v) for v in (A, b, c, np.reshape(d, (1,)) if shared else d, zi, x)]
+
+
+def _check(got, A, b, c, d, zi, x, out_idx, dtype, name):
+    y, zf = got
+    w = lambda v: None if v is None else np.asarray(v, np.float64)  # noqa: E731
+    ry, rzf = oracle.lti_state_space(w(A), w(x), w(b), w(c), w(d), w(zi), out_idx=out_idx)
+    D.check(y, ry, f"{name} y", dtype=dtype)
+    if zf is not None:
+        D.check(zf, rzf, f"{name} zf", dtype=dtype, scale=np.max(np.abs(ry)) if ry.size else None)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("M", ORDERS)
+@pytest.mark.parametrize("Bn,T", SHAPES)
+def test_lti_ss_capi_parity(api, dtype, M, Bn, T):
+    for shared in (False, True):
+        A, b, c, d, zi, x = _case(dtype, M, Bn, T, shared, D.seed_of("ss", dtype, M, Bn, T, shared))
+        name = f"M={M} B={Bn} T={T} shared={shared}"
+        _check(_run(api, A, b, c, d, zi, x), A, b, c, d, zi, x, None, dtype, name)
+        # b absent (input into state 0), c absent (out_idx), d absent, zi absent
+        idx = M - 1
+        _check(_run(api, A, None, None, None, None, x, out_idx=idx), A, None, None, None, None, x, idx, dtype,
+               name + " e0/out_idx")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("M", [1, 4])
+def test_lti_ss_capi_long_rows(api, dtype, M):
+    A, b, c, d, zi, x = _case(dtype, M, 2, 1_000_003, False, D.seed_of("ss-long", dtype, M))
+    _check(_run(api, A, b, c, d, zi, x), A, b, c, d, zi, x, None, dtype, "long rows")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("M", [2, 3])
+def test_lti_ss_capi_forced_fallback(api, dtype, M):
+    lib = api[0]
+    A, b, c, d, zi, x = _case(dtype, M, 3, 20000, False, D.seed_of("ss-fallback", dtype, M))
+    lib.phs_debug_set_spin_limit(1)
+    try:
+        got = _run(api, A, b, c, d, zi, x)
+    finally:
+        lib.phs_debug_set_spin_limit(0)
+    _check(got, A, b, c, d, zi, x, None, dtype, "fallback")
+
+
+def test_lti_ss_capi_errors(api):
+    import torch
+
+    lib, ws, capi = api
+    x = torch.zeros((2, 100), device="cuda")
+    A = torch.zeros((3, 3), device="cuda")
+
+    def call(dt=0, M=3, out_idx=0, c=None, wsb=ws.numel(), a=A):
+        return lib.phs_lti_ss_fwd(dt, M, 2, 100, _p(a), 1, None, 0, _p(c), 1, out_idx, None, 0, None, _p(x), _p(x),
+                                  None, _p(ws), wsb, _stream())
+
+    assert call(dt=2) == capi.PHS_ERR_DTYPE
+    assert call(M=5) == capi.PHS_ERR_INVALID and call(M=0) == capi.PHS_ERR_INVALID
+    assert call(out_idx=3) == capi.PHS_ERR_INVALID and call(out_idx=-1) == capi.PHS_ERR_INVALID
+    assert call(a=None) == capi.PHS_ERR_INVALID
+    assert call(wsb=lib.phs_lti_ss_workspace_size(0, 3, 2, 100) - 1) == capi.PHS_ERR_WORKSPACE
+    assert lib.phs_lti_ss_workspace_size(0, 5, 2, 100) == 0
+
+
+# ---------------------------------------------------------------- torch API
+def _filter(g, order, lead=(), dtype=np.float64):
+    """b (order+1 taps), a (order, after the leading 1) with poles of radius < 0.95."""
+    A, _, _, _ = _stable_model(g, order, lead)
+    a = np.real(np.apply_along_axis(np.poly, -1, np.linalg.eigvals(A).reshape(-1, order))).reshape(
+        tuple(lead) + (order + 1,))[..., 1:]
+    b = g.standard_normal(tuple(lead) + (order + 1,))
+    return b.astype(dtype), a.astype(dtype)
+
+
+@pytest.mark.parametrize("order", [1, 3, 4])
+@pytest.mark.parametrize("form", ["tdf2", "df2"])
+@pytest.mark.parametrize("batched", [False, True])
+def test_lfilter_orders_take_fused_route(hip, monkeypatch, order, form, batched):
+    """lfilter of orders 1, 3, 4 on HIP (philtorch::lti_ss) against the same
+    call on CPU (the reference's pure-PyTorch route), with zi/zf."""
+    import torch
+
+    from philtorch_amd.lti import ssm
+
+    taken = []
+    orig = ssm._fused_ss_applies
+    monkeypatch.setattr(ssm, "_fused_ss_applies", lambda *a: taken.append(orig(*a)) or taken[-1])
+    g = D.rng(D.seed_of("ss-lfilter", order, form, batched))
+    b, a = _filter(g, order, (4,) if batched else ())
+    x = g.standard_normal((4, 5000))
+    zi = g.standard_normal((4, order))
+    tb, ta, tx, tz = (torch.tensor(v) for v in (b, a, x, zi))
+    yg, zfg = hip.lti.lfilter(tb.cuda(), ta.cuda(), tx.cuda(), zi=tz.cuda(), form=form, unroll_factor=1)
+    assert taken == [True]
+    yc, zfc = hip.lti.lfilter(tb, ta, tx, zi=tz, form=form, unroll_factor=1)
+    D.check(yg.cpu().numpy(), yc.numpy(), "y")
+    D.check(zfg.cpu().numpy(), zfc.numpy(), "zf", scale=np.max(np.abs(yc.numpy())))
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_state_space_fused_matches_composed(hip, dtype):
+    import torch
+
+    from philtorch_amd.lti import ssm
+
+    g = D.rng(D.seed_of("ss-api", dtype))
+    Bn, T, M = 3, 7000, 3
+    A, b, c, d = _stable_model(g, M, (Bn,))
+    x = g.standard_normal((Bn, T))
+    zi = g.standard_normal((Bn, M))
+    t = lambda v: torch.tensor(np.asarray(v).astype(dtype), device="cuda")  # noqa: E731
+    cases = [
+        dict(A=t(A), B=t(b), C=t(c), D=t(d), zi=t(zi)),
+        dict(A=t(A[0]), B=t(b[0]), C=t(c[0]), D=t(d[:1]), zi=t(zi[0])),
+        dict(A=t(A), B=None, C=None, D=t(d[0]), zi=None, out_idx=1),
+        dict(A=t(A[0]), B=t(b), C=t(c[0]), D=None, zi=t(zi)),
+    ]
+    for kw in cases:
+        out_idx = kw.pop("out_idx", None)
+        assert ssm._fused_ss_applies(kw["A"], t(x), kw["B"], kw["C"], kw["D"], kw["zi"], 1, out_idx)
+        got = hip.lti.state_space(x=t(x), unroll_factor=1, out_idx=out_idx, **kw)
+        zi_full = None if kw["zi"] is None else kw["zi"].expand(Bn, M)
+        ref = ssm._state_space(kw["A"], t(x), kw["B"], kw["C"], kw["D"], zi_full, 1, out_idx, fused=False)
+        got = got if isinstance(got, tuple) else (got,)
+        ref = ref if isinstance(ref, tuple) else (ref,)
+        for gv, rv in zip(got, ref):
+            D.check(gv.cpu().numpy(), rv.cpu().numpy(), f"{sorted(kw)} {out_idx}", dtype=dtype,
+                    scale=np.max(np.abs(ref[0].cpu().numpy())))
+
+
+def test_state_space_fused_gradients(hip):
+    import torch
+
+    g = D.rng(D.seed_of("ss-grad"))
+    Bn, T, M = 2, 25, 3
+    A, b, c, d = _stable_model(g, M, (Bn,))
+    t = lambda v: torch.tensor(np.asarray(v, np.float64), device="cuda", requires_grad=True)  # noqa: E731
+    args = (t(A), t(b), t(c), t(d), t(g.standard_normal((Bn, M))), t(g.standard_normal((Bn, T))))
+    # the op itself (lti.state_space takes the composed route when a gradient is wanted)
+    f = lambda A_, b_, c_, d_, z_, x_: torch.ops.philtorch.lti_ss(A_, b_, c_, d_, z_, x_, 0)  # noqa: E731
+    assert torch.autograd.gradcheck(f, args)
+    assert torch.autograd.gradgradcheck(f, args)
+    assert torch.autograd.gradcheck(lambda *a: hip.lti.state_space(a[0], a[5], a[1], a[2], a[3], zi=a[4],
+                                                                   unroll_factor=1), args)
+    bf, af = (torch.tensor(v, device="cuda", requires_grad=True) for v in _filter(g, 4, (Bn,)))
+    xf = args[-1]
+    assert torch.autograd.gradcheck(lambda b_, a_, x_: hip.lti.lfilter(b_, a_, x_, unroll_factor=1), (bf, af, xf))
+
+
+def test_state_space_route_choice(hip):
+    import torch
+
+    from philtorch_amd.lti import ssm
+
+    x = torch.randn(3, 50, device="cuda")
+    A = torch.randn(3, 3, device="cuda")
+    v = torch.randn(3, device="cuda")
+    assert ssm._fused_ss_applies(A, x, v, v, None, None, 1, None)
+    assert not ssm._fused_ss_applies(A, x, v, v, None, None, 7, None)  # blocked PyTorch route requested
+    assert not ssm._fused_ss_applies(A, x, v, None, None, None, 1, None)  # all states out
+    assert not ssm._fused_ss_applies(A, x.unsqueeze(-1), v, v, None, None, 1, None)  # features
+    assert not ssm._fused_ss_applies(torch.randn(5, 5, device="cuda"), x, None, None, None, None, 1, 0)
+    assert not ssm._fused_ss_applies(A, x, v, v, torch.randn(2, device="cuda"), None, 1, None)
+    assert not ssm._fused_ss_applies(A, x.cpu(), v, v, None, None, 1, None)
+    assert not ssm._fused_ss_applies(A.double(), x, v, v, None, None, 1, None)
+    assert not ssm._fused_ss_applies(A, x.requires_grad_(), v, v, None, None, 1, None)
+    with torch.no_grad():
+        assert ssm._fused_ss_applies(A, x, v, v, None, None, 1, None)
+
+
+def test_lti_ss_opcheck(hip):
+    import torch
+
+    g = D.rng(D.seed_of("ss-opcheck"))
+    A, b, c, d = _stable_model(g, 3, (2,))
+    t = lambda v: torch.tensor(np.asarray(v, np.float32), device="cuda")  # noqa: E731
+    x = t(g.standard_normal((2, 700)))
+    torch.library.opcheck(torch.ops.philtorch.lti_ss.default, (t(A), t(b), t(c), t(d), t(g.standard_normal((2, 3))), x, 0))
+    torch.library.opcheck(torch.ops.philtorch.lti_ss.default, (t(A[0]), None, None, None, None, x, 2))

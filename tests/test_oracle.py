@@ -367,3 +367,47 @@ def test_filtfilt_steady_state_and_lfilter_zi():
     zi = oracle.lfilter_zi(sos)
     A, Bv, _, _ = oracle._tdf2_section(sos)
     np.testing.assert_allclose(np.einsum("rij,rj->ri", A, zi) + Bv, zi, rtol=1e-12)
+
+
+# ---------------------------------------------------------------- SISO state space
+def _stable_model(g, M, lead=()):
+    """A dense A with a stable spectrum (a companion matrix of poles of radius
+    < 0.97, conjugated by a well-conditioned random basis), B, C, D."""
+    shape = tuple(lead)
+    r = g.uniform(0.3, 0.97, shape + (M,))
+    th = g.uniform(0, np.pi, shape + (M,))
+    poles = r * np.exp(1j * th)
+    poles[..., 1::2] = np.conj(poles[..., 0::2][..., : M // 2])
+    if M % 2:
+        poles[..., -1] = r[..., -1] * np.sign(g.uniform(-1, 1, shape))
+    a = np.real(np.apply_along_axis(np.poly, -1, poles.reshape(-1, M)).reshape(shape + (M + 1,)))[..., 1:]
+    comp = np.zeros(shape + (M, M))
+    comp[..., 0, :] = -a
+    comp[..., np.arange(1, M), np.arange(M - 1)] = 1.0
+    V = np.eye(M) + 0.3 * g.standard_normal(shape + (M, M))
+    A = V @ comp @ np.linalg.inv(V)
+    return A, g.standard_normal(shape + (M,)), g.standard_normal(shape + (M,)), g.standard_normal(shape)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_lti_state_space_matches_scipy_dlsim(M):
+    """oracle.lti_state_space (B x, lti_recurN, shift, C h + D x) against
+    scipy.signal.dlsim (x[k+1] = A x[k] + B u[k], y[k] = C x[k] + D u[k]), per
+    row, with initial states; and its B = None / out_idx forms."""
+    g = D.rng(D.seed_of("oracle-ss", M))
+    Bn, T = 3, 400
+    A, Bv, Cv, Dv = _stable_model(g, M, (Bn,))
+    x = g.standard_normal((Bn, T))
+    zi = g.standard_normal((Bn, M))
+    y, zf = oracle.lti_state_space(A, x, Bv, Cv, Dv, zi)
+    for r in range(Bn):
+        _, ry, rx = scipy.signal.dlsim((A[r], Bv[r][:, None], Cv[r][None, :], [[Dv[r]]], 1), x[r], x0=zi[r])
+        D.check(y[r], ry[:, 0], f"y row {r}")
+        rzf = A[r] @ rx[-1] + Bv[r] * x[r, -1]
+        D.check(zf[r], rzf, f"zf row {r}", scale=np.max(np.abs(ry)))
+    e0 = np.eye(M)[0]
+    idx = M - 1
+    y2, _ = oracle.lti_state_space(A[0], x, None, None, None, zi, out_idx=idx)
+    for r in range(Bn):
+        _, ry, _ = scipy.signal.dlsim((A[0], e0[:, None], np.eye(M)[idx][None, :], [[0.0]], 1), x[r], x0=zi[r])
+        D.check(y2[r], ry[:, 0], f"out_idx row {r}")
