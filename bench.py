@@ -495,14 +495,16 @@ def cpu_baseline(w: Workload, budget_s=10.0):
     }
 
 
-def _measured_traffic(config):
-    """HBM bytes per launch of the dominant kernel, from the rocprofv3 --pmc
-    summary committed under profiles/ (FETCH_SIZE + WRITE_SIZE, each scaled by
-    the same counter on a plain copy of known size), or None."""
+def _measured_traffic(config, direction="backward"):
+    """HBM bytes per launch of the dominant kernel (per call of the timed
+    unit where that is several kernels), from the rocprofv3 --pmc summary
+    committed under profiles/ (FETCH_SIZE + WRITE_SIZE, each scaled by the
+    same counter on a plain copy of known size), or None."""
     path = os.path.join(REPO, "profiles", f"traffic_{config}.json")
+    key = "bwd_bytes_per_launch" if direction == "backward" else "fwd_bytes_per_launch"
     try:
         with open(path) as f:
-            return json.load(f)["bwd_bytes_per_launch"]
+            return json.load(f)[key]
     except (OSError, KeyError, ValueError):
         return None
 
@@ -630,7 +632,7 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": _measured_traffic(w.name),
+            "traffic": _measured_traffic(w.name, dominant[0]),
         },
     }
     if args.calib_copy:
