@@ -12,7 +12,7 @@ namespace {
 template <class Alg>
 size_t ss_ws_bytes(int64_t B, int64_t T) {
   const int64_t tiles = (T + SsShape<Alg>::kTile - 1) / SsShape<Alg>::kTile;
-  return align_up(align_up(kHeaderBytes) + size_t(B) * size_t(tiles) * StatusShape<Alg>::kStride * sizeof(uint64_t));
+  return align_up(align_up(kHeaderBytes) + size_t(B) * size_t(tiles) * SsStatus<Alg>::kStride * sizeof(uint64_t));
 }
 
 template <class Alg>

@@ -166,50 +166,187 @@ __device__ __forceinline__ typename Alg::state ss_lane_fold(const SsModel<Alg> &
   return Alg::load_s(h);
 }
 
-// State entering scan position `span` of a row, folded straight from the
-// inputs (the look-back's bounded-wait fallback; out of line, cold).
-template <class Alg, class Sh>
-__device__ __noinline__ typename Alg::state ss_prefix_fallback(SsArgs<Alg> a, int64_t b, int64_t span, int lane,
-                                                              typename Alg::state virt) {
-  using E = typename Alg::elem;
-  using M = Map<Alg>;
-  constexpr int K = Sh::K;
-  const SsModel<Alg> m = ss_model<Alg>(a, b);
-  const typename Alg::coef AK = ss_pow2<Alg>(m.A, __builtin_ctz(K));
-  auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
-  const E *xrow = a.x + b * a.T_len;
-  M acc = map_identity<Alg>();
-  for (int64_t off = 0; off < span; off += 64 * K) {
-    E xs[K];
-    load_chunk<E, K>(xrow, off + int64_t(lane) * K, a.T_len, a.vec_ok != 0, xs, E(0));
-    M v = wave_scan_incl(M{AK, ss_lane_fold<Alg, K>(m, xs)}, lane, op);
-    acc = compose<Alg>(acc, read_lane(v, 63));
+// Status entries carry vectors only: every tile aggregate has the matrix
+// part G = A^(tile steps), so an entry is the inclusive state (words
+// [0, kVecWords)) and the tile's zero-entry aggregate (the next kVecWords),
+// each 32-bit chunk one tagged 64-bit word as in phs_scan.hpp.
+template <class Alg>
+struct SsStatus {
+  static constexpr int kVecWords = int(sizeof(typename Alg::state) / 4);
+  static constexpr int kStride = 2 * kVecWords;
+  static constexpr int kLookPitch = kStride | 1;  // odd LDS pitch: no bank conflicts
+  static constexpr int kLookWords = 64 * kLookPitch;
+};
+
+// Power tables the look-back wave builds in LDS before the data waves scan:
+// pw[i] = A^(K 2^i) (i < 6) for the lane scan, pw[6] = A^(64 K) between
+// rounds, pw[7] = A^(64 K R) per wave segment; gp[j] = G^(2^j) (j < 7) for
+// the look-back, G = A^(tile steps).
+template <class Alg>
+struct SsPowers {
+  typename Alg::coef pw[8];
+  typename Alg::coef gp[7];
+};
+
+// The power tables live in LDS and are read where they are used: a compiler
+// barrier at the top of each loop keeps their loads from being hoisted out
+// of it, where up to six M x M matrices would sit in registers at once.
+__device__ __forceinline__ void ss_reload_tables() { asm volatile("" ::: "memory"); }
+
+// v[r] <- P^n v[r] for a table P[j] = P^(2^j) and 0 <= n < 2^bits, level by
+// level so that one matrix serves every vector (powers of one matrix
+// commute, so the order of the factors is free).
+template <class Alg, int Bits, int N>
+__device__ __forceinline__ void ss_pow_apply(const typename Alg::coef *P, int n, typename Alg::state (&v)[N]) {
+#pragma unroll
+  for (int j = 0; j < Bits; ++j) {
+    if ((n >> j) & 1) {
+      const typename Alg::coef Pj = P[j];
+#pragma unroll
+      for (int r = 0; r < N; ++r) v[r] = Alg::affine(Pj, v[r], Alg::szero());
+    }
   }
-  return apply<Alg>(acc, virt);
 }
 
-// At least two waves per SIMD (two workgroups per CU): order 4 otherwise
-// takes 315 VGPRs, mostly the look-back wave's 4x4 maps, and holds one tile
-// per CU.
+// Inclusive scans of N rounds of lane vectors, v_L = sum_{j <= L}
+// A^(K (L-j)) s_j: Kogge-Stone, level i combines with the lane 2^i below at
+// A^(K 2^i), level by level across the rounds.
+template <class Alg, int N>
+__device__ __forceinline__ void ss_lane_scan(typename Alg::state (&v)[N], int lane, const typename Alg::coef *pw) {
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const int d = 1 << i;
+    typename Alg::state o[N];
+#pragma unroll
+    for (int r = 0; r < N; ++r) o[r] = shfl_from(v[r], lane - d);
+    if (lane >= d) {
+      const typename Alg::coef P = pw[i];
+#pragma unroll
+      for (int r = 0; r < N; ++r) v[r] = Alg::affine(P, o[r], v[r]);
+    }
+  }
+}
+
+// State entering scan position `span` of a row, folded straight from the
+// inputs (the look-back's bounded-wait fallback; out of line, cold): chunk
+// by chunk of 64 K steps, st <- A^(64 K) st + chunk total.
+template <class Alg, class Sh>
+__device__ __noinline__ typename Alg::state ss_prefix_fallback(SsArgs<Alg> a, int64_t b, int64_t span, int lane,
+                                                              typename Alg::state st, const SsPowers<Alg> *tab) {
+  using E = typename Alg::elem;
+  constexpr int K = Sh::K;
+  const SsModel<Alg> m = ss_model<Alg>(a, b);
+  const E *xrow = a.x + b * a.T_len;
+  for (int64_t off = 0; off < span; off += 64 * K) {
+    ss_reload_tables();
+    E xs[K];
+    load_chunk<E, K>(xrow, off + int64_t(lane) * K, a.T_len, a.vec_ok != 0, xs, E(0));
+    typename Alg::state v[1] = {ss_lane_fold<Alg, K>(m, xs)};
+    ss_lane_scan<Alg, 1>(v, lane, tab->pw);
+    st = Alg::affine(tab->pw[6], st, read_lane(v[0], 63));
+  }
+  return st;
+}
+
+// One tile's look-back over vector entries: with lane i looking at tile
+// q-1-i and k the first lane holding an inclusive state, the state entering
+// tile q is sum_{i<k} G^i agg(q-1-i) + G^k inc(q-1-k) (windows further back
+// weighted by G^(tiles passed)).  The first window holds Alg::kLookFirst
+// tiles, later ones 64.  Polls until the state is known (true, in `out`) or
+// `spin_limit` polls found a predecessor still unpublished (false).
+template <class Alg>
+__device__ bool ss_lookback(const uint64_t *row_status, const typename Alg::state &virt, int lane, unsigned tag,
+                            unsigned spin_limit, uint64_t *s_look, const SsPowers<Alg> *tab, int64_t q,
+                            typename Alg::state &out) {
+  using S = typename Alg::state;
+  using Mt = typename Alg::coef;
+  using St = SsStatus<Alg>;
+  constexpr int kS = St::kStride, kP = St::kLookPitch, kV = St::kVecWords;
+  constexpr int kBatch = kS < 8 ? kS : 8;  // words in flight per lane
+  S acc = Alg::szero();
+  Mt gm = Alg::cone();
+  int64_t base = q - 1;
+  unsigned polls = 0;
+  int span = Alg::kLookFirst;
+  auto add = [](const S &p, const S &o) { return Alg::sadd(p, o); };
+  while (true) {
+    ss_reload_tables();
+    const int n = base + 1 > span ? span : int(base + 1);  // tiles in the window
+    const uint64_t *win = row_status + (base + 1 - n) * kS + lane;
+    // all loads of a batch are issued before any LDS store (atomic loads are
+    // ordered against other memory operations)
+#pragma unroll
+    for (int i0 = 0; i0 < kS; i0 += kBatch) {
+      uint64_t words[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        words[i] = 0;
+        if (i0 + i < kS && (i0 + i) * 64 + lane < n * kS)  // word (i0+i)*64+lane of the window
+          words[i] = __hip_atomic_load(win + (i0 + i) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int j = (i0 + i) * 64 + lane;
+        if (i0 + i < kS) s_look[(j / kS) * kP + (j % kS)] = words[i];
+      }
+    }
+    wave_sync();
+    const int64_t p = base - lane;  // lane < n: window entry n-1-lane
+    S inc = Alg::szero(), agg = Alg::szero();
+    int st = 3;  // outside the window: no contribution, never inclusive
+    if (lane < n) {
+      const uint64_t *e = s_look + (n - 1 - lane) * kP;
+      const bool inc_ok = unpack(e, inc, tag);
+      const bool agg_ok = unpack(e + kV, agg, tag);
+      st = inc_ok ? 2 : (agg_ok ? 1 : 0);
+    } else if (p == -1) {
+      st = 2;
+      inc = virt;
+    }
+    wave_sync();
+    const uint64_t incm = __ballot(st == 2);
+    const int k = incm ? __builtin_ctzll(incm) : 64;
+    const uint64_t low = (k >= 64) ? ~0ull : ((1ull << k) - 1ull);
+    if (__ballot(st == 0) & low) {
+      if (++polls >= spin_limit) return false;
+      __builtin_amdgcn_s_sleep(1);
+      continue;
+    }
+    S c[1] = {Alg::szero()};
+    if (lane < k && lane < n) c[0] = agg;
+    if (lane == k) c[0] = inc;
+    ss_pow_apply<Alg, 6, 1>(tab->gp, lane, c);
+    const S sum = read_lane(wave_scan_incl(c[0], lane, add), 63);
+    acc = Alg::affine(gm, sum, acc);
+    if (k < 64) {
+      out = acc;
+      return true;
+    }
+    // G^n for the window just passed (n = kLookFirst or 64, a power of two)
+    gm = Alg::cmul(n == 64 ? tab->gp[6] : tab->gp[__builtin_ctz(unsigned(n))], gm);
+    base -= n;
+    span = 64;
+  }
+}
+
+// At least two waves per SIMD (two workgroups per CU).
 template <class Alg>
 __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Alg> a) {
   using E = typename Alg::elem;
   using S = typename Alg::state;
   using SS = typename Alg::s_state;
-  using M = Map<Alg>;
   using V = SsView<Alg>;
   using Sh = SsShape<Alg>;
-  using St = StatusShape<Alg>;
+  using St = SsStatus<Alg>;
   constexpr int K = Sh::K, R = Sh::R, kWaves = Sh::kWaves;
+  static_assert(Alg::kLookFirst == 8 || Alg::kLookFirst == 64, "window weights are table entries");
 
-  __shared__ M s_wagg[kWaves];
-  __shared__ M s_wpre[kWaves];
+  __shared__ S s_wagg[kWaves];  // wave aggregates (matrix part A^(64 K R))
+  __shared__ S s_wpre[kWaves];  // exclusive wave prefixes (matrix part A^(64 K R w))
   __shared__ S s_in;
   __shared__ unsigned s_id, s_tag;
   __shared__ uint64_t s_look[St::kLookWords];
-  // matrix parts, all powers of A: s_pw[i] = A^(K 2^i) for the lane scan
-  // (i < 6), s_pw[6] = A^(64 K) between rounds, s_pw[7] = A^(64 K R) per wave
-  __shared__ typename Alg::coef s_pw[8];
+  __shared__ SsPowers<Alg> s_tab;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -221,39 +358,47 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
   const int64_t q = id / a.B;  // tile position along the row
   const int64_t b = id - q * a.B;
   const int64_t T = a.T_len;
-  auto op = [](const M &p, const M &o) { return compose<Alg>(p, o); };
 
   if (w == kWaves) {
-    // ================= look-back wave
+    // ================= look-back wave: power tables, then the look-back
     {
-      typename Alg::coef P = ss_pow2<Alg>(SsView<Alg>::load_mat(a.A + b * a.A_stride), __builtin_ctz(K));
+      typename Alg::coef P = ss_pow2<Alg>(V::load_mat(a.A + b * a.A_stride), __builtin_ctz(K));
 #pragma unroll
       for (int i = 0; i < 6; ++i) {
-        if (lane == 0) s_pw[i] = P;
+        if (lane == 0) s_tab.pw[i] = P;
         P = Alg::cmul(P, P);
       }
-      if (lane == 0) s_pw[6] = P;
+      if (lane == 0) s_tab.pw[6] = P;
 #pragma unroll
       for (int r = 1; r < R; r <<= 1) P = Alg::cmul(P, P);
-      if (lane == 0) s_pw[7] = P;
+      if (lane == 0) s_tab.pw[7] = P;
+      P = Alg::cmul(P, Alg::cmul(P, P));  // G = A^(3 * 64 K R)
+      static_assert(kWaves == 3, "G is the wave power cubed");
+#pragma unroll
+      for (int j = 0; j < 7; ++j) {
+        if (lane == 0) s_tab.gp[j] = P;
+        P = Alg::cmul(P, P);
+      }
     }
-    __syncthreads();  // power table
+    __syncthreads();  // power tables
     uint64_t *row_status = a.status + b * a.tiles_per_row * St::kStride;
     const S virt = a.zi ? Alg::load_s(V::load_vec(a.zi + b * V::M)) : Alg::szero();
     S yin = virt;
     __syncthreads();  // wave aggregates are in s_wagg
-    M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
-    v = wave_scan_incl(v, lane, op);
-    const M wex = wave_shift_up(v, lane, map_identity<Alg>());
-    if (lane < kWaves) s_wpre[lane] = wex;
-    const M tagg = read_lane(v, kWaves - 1);
-    if (q > 0) {
-      if (lane == 0) publish(row_status + q * St::kStride + St::kIncWords, tagg, tag);
-      Lookback<Alg> lb = lookback_start<Alg>(q);
-      if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
-        yin = ss_prefix_fallback<Alg, Sh>(a, b, q * Sh::kTile, lane, virt);
+    // exclusive wave prefixes and the tile aggregate (every lane, uniformly)
+    S tagg = Alg::szero();
+#pragma unroll
+    for (int j = 0; j < kWaves; ++j) {
+      if (lane == 0) s_wpre[j] = tagg;
+      tagg = Alg::affine(s_tab.pw[7], tagg, s_wagg[j]);
     }
-    if (q + 1 < a.tiles_per_row && lane == 0) publish(row_status + q * St::kStride, apply<Alg>(tagg, yin), tag);
+    if (q > 0) {
+      if (lane == 0) publish(row_status + q * St::kStride + St::kVecWords, tagg, tag);
+      if (!ss_lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, &s_tab, q, yin))
+        yin = ss_prefix_fallback<Alg, Sh>(a, b, q * Sh::kTile, lane, virt, &s_tab);
+    }
+    if (q + 1 < a.tiles_per_row && lane == 0)
+      publish(row_status + q * St::kStride, Alg::affine(s_tab.gp[0], yin, tagg), tag);
     if (lane == 0) s_in = yin;
     __syncthreads();  // entry state is in s_in
     return;
@@ -271,46 +416,49 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
     t0s[r] = seg0 + int64_t(r) * 64 * K + int64_t(lane) * K;
     load_chunk<E, K>(xrow, t0s[r], T, vec, X[r], E(0));
   }
-  __syncthreads();  // power table
+  __syncthreads();  // power tables
 
   // ---- pass 1: every map's matrix part is a known power of A, so only the
-  // vector parts are scanned (Kogge-Stone over the lanes, multiplier
-  // A^(K 2^i) at level i).  Steps past the row's end take a zero input and
-  // only touch the aggregate of its last tile, which nobody reads.
+  // vector parts are scanned.  Steps past the row's end take a zero input
+  // and only touch the aggregate of its last tile, which nobody reads.
   S ex[R], tot[R];
+  {
+    S v[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    S v = ss_lane_fold<Alg, K>(m, X[r]);
+    for (int r = 0; r < R; ++r) v[r] = ss_lane_fold<Alg, K>(m, X[r]);
+    ss_lane_scan<Alg, R>(v, lane, s_tab.pw);
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      const int d = 1 << i;
-      const S o = shfl_from(v, lane - d);
-      if (lane >= d) v = Alg::affine(s_pw[i], o, v);
+    for (int r = 0; r < R; ++r) {
+      tot[r] = read_lane(v[r], 63);
+      const S prev = shfl_from(v[r], lane - 1);
+      ex[r] = lane > 0 ? prev : Alg::szero();
     }
-    tot[r] = read_lane(v, 63);
-    const S prev = shfl_from(v, lane - 1);
-    ex[r] = lane > 0 ? prev : Alg::szero();
   }
   if (lane == 0) {
     S agg = tot[0];
 #pragma unroll
-    for (int r = 1; r < R; ++r) agg = Alg::affine(s_pw[6], agg, tot[r]);
-    s_wagg[w] = M{s_pw[7], agg};
+    for (int r = 1; r < R; ++r) agg = Alg::affine(s_tab.pw[6], agg, tot[r]);
+    s_wagg[w] = agg;
   }
   __syncthreads();  // wave aggregates are in s_wagg
   __syncthreads();  // entry state is in s_in
-  S st = apply<Alg>(s_wpre[w], s_in);
+  // the wave's entry state: A^(64 K R w) s_in + its exclusive prefix
+  S st = s_in;
+  for (int j = 0; j < w; ++j) st = Alg::affine(s_tab.pw[7], st, Alg::szero());
+  st = Alg::sadd(st, s_wpre[w]);
 
-  // ---- pass 2: a lane enters round r at A^(K lane) st + ex, then
+  // ---- pass 2: round r of the wave starts at st[r] (st[r+1] = A^(64 K)
+  // st[r] + tot[r]); a lane enters it at A^(K lane) st[r] + ex[r], then
   // y = c . h + d x and the step
+  S ent[R];
+  ent[0] = st;
+#pragma unroll
+  for (int r = 1; r < R; ++r) ent[r] = Alg::affine(s_tab.pw[6], ent[r - 1], tot[r - 1]);
+  ss_pow_apply<Alg, 6, R>(s_tab.pw, lane, ent);
   E *yrow = a.y + b * T;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    S e = st;
-#pragma unroll
-    for (int i = 0; i < 6; ++i)
-      if ((lane >> i) & 1) e = Alg::affine(s_pw[i], e, Alg::szero());
-    SS h = Alg::store_s(Alg::sadd(e, ex[r]));
+    SS h = Alg::store_s(Alg::sadd(ent[r], ex[r]));
     E O[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -327,7 +475,6 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
       }
     }
     store_chunk<E, K>(yrow, t0s[r], T, vec, O);
-    st = Alg::affine(s_pw[6], st, tot[r]);
   }
 }
 
