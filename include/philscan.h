@@ -272,6 +272,23 @@ int phs_lti_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
                    const void *c, int c_shared, int out_idx, const void *d, int d_shared, const void *zi,
                    const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- lfilter of order M = max(nb - 1, na) = 1..4 in one pass (forward).
+ * Replaces philtorch.lti.lfilter (philtorch/lti/filtering.py:211-333) in
+ * the companion-form state space it builds (_ssm_lfilter :273-333) for forms
+ * "tdf2" (A = companion(a)^T, B = b[1:] - b0 a, out_idx 0, D = b0) and "df2"
+ * (A = companion(a), input into state 0, C = b[1:] - b0 a, D = b0), b and
+ * a zero-padded to order M; the companion matrix and the B/C vectors are
+ * built inside the kernel from b and a.  dtype PHS_F32 or PHS_F64; b [B,nb]
+ * or [nb], a [B,na] or [na] (the denominator after its leading 1;
+ * coef_shared for the 1D forms); form a phs_form code; zi [B,M] in the
+ * form's state coordinates (NULL = zeros); x, y [B,T]; zf [B,M] (skipped
+ * when NULL).  Workspace: phs_lti_ss_workspace_size(dtype, M, B, T). */
+enum phs_form { PHS_FORM_TDF2 = 0, PHS_FORM_DF2 = 1 };
+
+int phs_lfilter_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na, int coef_shared,
+                    int form, const void *zi, const void *x, void *y, void *zf, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,7 +9,8 @@ second-order sections ``sosfilt`` / ``sosfilt_backward`` (no reference
 counterpart; ``lti.sosfilt`` is its API), the forward-only zero-phase
 ``filtfilt`` of filters up to second order (behind ``lti.filtfilt``) and the
 fused single-input single-output state space ``lti_ss`` (behind
-``lti.state_space`` and so ``lti.lfilter``).  This module then
+``lti.state_space``) and ``lfilter_ss``, ``lfilter`` of order <= 4 from b and
+a in one pass (behind ``lti.lfilter``).  This module then
 registers fake (meta) kernels and autograd formulas for them, as
 philtorch/__init__.py:157-268 does for its ops.
 
@@ -370,6 +371,44 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
         return tuple(out)
 
     torch.library.register_autograd("philtorch::lti_ss", _lti_ss_backward, setup_context=_lti_ss_setup)
+
+if EXTENSION_LOADED and _has_op("lfilter_ss"):
+    # lfilter of order <= 4 from b and a in one pass: (y, zf)
+    @torch.library.register_fake("philtorch::lfilter_ss")
+    def _(b, a, zi, x, form):
+        torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
+        M = max(b.shape[-1] - 1, a.shape[-1])
+        torch._check(1 <= M <= 4, lambda: "filters of order 1 to 4")
+        return _fake_like(x), x.new_empty((x.shape[0], M))
+
+    def _lfilter_ss_setup(ctx, inputs, output):
+        b, a, zi, x, form = inputs
+        ctx.form = form
+        ctx.save_for_backward(b, a, zi, x)
+
+    def _lfilter_ss_backward(ctx, gy, gzf):
+        """Gradient of the companion-form route the kernel replaces
+        (philtorch/lti/filtering.py:273-333), recomputed from the inputs."""
+        from .lti.filtering import _ssm_lfilter
+
+        b, a, zi, x = inputs = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
+        with torch.enable_grad():
+            z = zi if zi is not None else x.new_zeros(x.size(0), max(b.size(-1) - 1, a.size(-1)))
+            y, zf = _ssm_lfilter(b, a, x, z, form=("tdf2", "df2")[ctx.form], unroll_factor=1)
+            outs, grads = [y], [gy if gy is not None else torch.zeros_like(y)]
+            if gzf is not None:
+                outs.append(zf)
+                grads.append(gzf)
+            res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=torch.is_grad_enabled(),
+                                      allow_unused=True)
+        out = [None] * 5
+        for i, g in zip(wrt, res):
+            out[i] = g if g is not None else torch.zeros_like(inputs[i])
+        return tuple(out)
+
+    torch.library.register_autograd("philtorch::lfilter_ss", _lfilter_ss_backward, setup_context=_lfilter_ss_setup)
 
 from . import mat  # noqa: E402,F401
 from . import lti  # noqa: E402,F401

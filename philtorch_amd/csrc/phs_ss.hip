@@ -15,16 +15,27 @@ size_t ss_ws_bytes(int64_t B, int64_t T) {
   return align_up(align_up(kHeaderBytes) + size_t(B) * size_t(tiles) * SsStatus<Alg>::kStride * sizeof(uint64_t));
 }
 
+// Filter mode of the model (SsArgs::filt_form and friends): none, or
+// lfilter(b, a) in companion form.
+struct SsFilter {
+  const void *b = nullptr, *a = nullptr;
+  int nb = 0, na = 0, form = 0;
+  bool shared = false;
+};
+
 template <class Alg>
 int ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, const void *bv, bool b_sh, const void *cv, bool c_sh,
-           int out_idx, const void *d, bool d_sh, const void *zi, const void *x, void *y, void *zf, void *workspace,
-           size_t ws_bytes, hipStream_t stream) {
+           int out_idx, const void *d, bool d_sh, const SsFilter &f, const void *zi, const void *x, void *y, void *zf,
+           void *workspace, size_t ws_bytes, hipStream_t stream) {
   using E = typename Alg::elem;
   using Sh = SsShape<Alg>;
   constexpr int M = SsView<Alg>::M;
-  if (B < 0 || T < 0 || (!cv && (out_idx < 0 || out_idx >= M))) return PHS_ERR_INVALID;
+  if (B < 0 || T < 0) return PHS_ERR_INVALID;
+  if (f.form == 0 && !cv && (out_idx < 0 || out_idx >= M)) return PHS_ERR_INVALID;
+  if (f.form != 0 && (f.nb < 1 || f.nb > M + 1 || f.na < 1 || f.na > M || (f.nb - 1 != M && f.na != M)))
+    return PHS_ERR_INVALID;
   if (B == 0 || T == 0) return PHS_OK;
-  if (!A || !x || !y) return PHS_ERR_INVALID;
+  if ((f.form == 0 ? !A : (!f.b || !f.a)) || !x || !y) return PHS_ERR_INVALID;
   const int64_t tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
   if (double(B) * double(tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
   if (!workspace || ws_bytes < ss_ws_bytes<Alg>(B, T)) return PHS_ERR_WORKSPACE;
@@ -39,6 +50,13 @@ int ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, const void *bv, bool 
   a.d = static_cast<const E *>(d);
   a.d_stride = d_sh ? 0 : 1;
   a.out_idx = out_idx;
+  a.fb = static_cast<const E *>(f.b);
+  a.fa = static_cast<const E *>(f.a);
+  a.nb = f.nb;
+  a.na = f.na;
+  a.filt_form = f.form;
+  a.f_stride_b = f.shared ? 0 : f.nb;
+  a.f_stride_a = f.shared ? 0 : f.na;
   a.zi = static_cast<const E *>(zi);
   a.x = static_cast<const E *>(x);
   a.y = static_cast<E *>(y);
@@ -92,7 +110,27 @@ int phs_lti_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return phs::ss_dispatch(dtype, M, [&](auto alg) {
     return phs::ss_fwd<decltype(alg)>(B, T, A, A_shared != 0, b, b_shared != 0, c, c_shared != 0, out_idx, d,
-                                      d_shared != 0, zi, x, y, zf, workspace, workspace_bytes, st);
+                                      d_shared != 0, phs::SsFilter{}, zi, x, y, zf, workspace, workspace_bytes, st);
+  });
+}
+
+int phs_lfilter_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na, int coef_shared,
+                    int form, const void *zi, const void *x, void *y, void *zf, void *workspace,
+                    size_t workspace_bytes, void *stream) {
+  if (form != PHS_FORM_TDF2 && form != PHS_FORM_DF2) return PHS_ERR_INVALID;
+  const int M = nb - 1 > na ? nb - 1 : na;
+  if (M < 1 || M > 4) return PHS_ERR_INVALID;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  phs::SsFilter f;
+  f.b = b;
+  f.a = a;
+  f.nb = nb;
+  f.na = na;
+  f.form = form == PHS_FORM_TDF2 ? 1 : 2;
+  f.shared = coef_shared != 0;
+  return phs::ss_dispatch(dtype, M, [&](auto alg) {
+    return phs::ss_fwd<decltype(alg)>(B, T, nullptr, false, nullptr, false, nullptr, false, 0, nullptr, false, f, zi,
+                                      x, y, zf, workspace, workspace_bytes, st);
   });
 }
 

@@ -37,6 +37,15 @@ struct SsArgs {
   const E *d;         // [rows]; nullptr: no feedthrough
   int64_t d_stride;
   int out_idx;
+  // filter mode (filt_form != 0: A, bv, cv, d are not read): the model of
+  // lfilter(fb, fa) in companion form, fb [rows, nb] (nb <= M + 1) and fa
+  // [rows, na] (the denominator after its leading 1, na <= M), both
+  // zero-padded to order M (philtorch/lti/filtering.py:273-333):
+  //   1 TDF-II: A = companion(a)^T, b = fb[1:] - fb[0] a, c = e0, d = fb[0]
+  //   2 DF-II:  A = companion(a),   b = e0, c = fb[1:] - fb[0] a, d = fb[0]
+  const E *fb, *fa;
+  int nb, na, filt_form;
+  int64_t f_stride_b, f_stride_a;  // 0 = shared
   const E *zi;        // [B, M]; nullptr: zeros
   const E *x;         // [B, T]
   E *y;               // [B, T]
@@ -138,11 +147,42 @@ template <class Alg>
 __device__ __forceinline__ SsModel<Alg> ss_model(const SsArgs<Alg> &a, int64_t row) {
   using V = SsView<Alg>;
   using E = typename Alg::elem;
+  constexpr int M = V::M;
   SsModel<Alg> m;
-  m.A = V::load_mat(a.A + row * a.A_stride);
-  m.b = a.bv ? V::load_vec(a.bv + row * a.b_stride) : V::unit(0);
-  m.c = a.cv ? V::load_vec(a.cv + row * a.c_stride) : V::unit(a.out_idx);
-  m.d = a.d ? a.d[row * a.d_stride] : E(0);
+  if (a.filt_form == 0) {
+    m.A = V::load_mat(a.A + row * a.A_stride);
+    m.b = a.bv ? V::load_vec(a.bv + row * a.b_stride) : V::unit(0);
+    m.c = a.cv ? V::load_vec(a.cv + row * a.c_stride) : V::unit(a.out_idx);
+    m.d = a.d ? a.d[row * a.d_stride] : E(0);
+    return m;
+  }
+  const E *fb = a.fb + row * a.f_stride_b, *fa = a.fa + row * a.f_stride_a;
+  union {
+    typename Alg::s_coef s;
+    E e[M * M];
+  } A;
+  union {
+    typename Alg::s_state s;
+    E e[M];
+  } g;
+  const E b0 = fb[0];
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    const E ai = i < a.na ? fa[i] : E(0);
+    const E bi = i + 1 < a.nb ? fb[i + 1] : E(0);
+    g.e[i] = bi - b0 * ai;
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+      // companion(a): row 0 = -a, ones below the diagonal
+      const E comp_ij = i == 0 ? -(j < a.na ? fa[j] : E(0)) : (j == i - 1 ? E(1) : E(0));
+      const E comp_ji = j == 0 ? -ai : (i == j - 1 ? E(1) : E(0));
+      A.e[i * M + j] = a.filt_form == 1 ? comp_ji : comp_ij;
+    }
+  }
+  m.A = A.s;
+  m.b = a.filt_form == 1 ? g.s : V::unit(0);
+  m.c = a.filt_form == 1 ? V::unit(0) : g.s;
+  m.d = b0;
   return m;
 }
 
@@ -362,7 +402,7 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
   if (w == kWaves) {
     // ================= look-back wave: power tables, then the look-back
     {
-      typename Alg::coef P = ss_pow2<Alg>(V::load_mat(a.A + b * a.A_stride), __builtin_ctz(K));
+      typename Alg::coef P = ss_pow2<Alg>(ss_model<Alg>(a, b).A, __builtin_ctz(K));
 #pragma unroll
       for (int i = 0; i < 6; ++i) {
         if (lane == 0) s_tab.pw[i] = P;

@@ -573,6 +573,53 @@ std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tenso
   return {y, zf};
 }
 
+// lfilter of order <= 4 from b and a directly (phs_lfilter_fwd;
+// philtorch/lti/filtering.py:211-333 in its companion-form state space):
+// returns (y, zf).  b (nb,) or (batch, nb); a (na,) or (batch, na), the
+// denominator after its leading 1; form 0 "tdf2", 1 "df2"; zi None or
+// (batch, max(nb - 1, na)).
+std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, const std::optional<Tensor> &zi,
+                                          const Tensor &x, int64_t form) {
+  TORCH_CHECK(x.dim() == 2, "philtorch::lfilter_ss: x must be a 2D tensor (batch, time)");
+  TORCH_CHECK(b.dim() == a.dim() && (b.dim() == 1 || b.dim() == 2),
+              "philtorch::lfilter_ss: b and a must both be 1D (shared) or both 2D (batch, taps)");
+  const int64_t B = x.size(0), T = x.size(1), nb = b.size(-1), na = a.size(-1);
+  if (b.dim() == 2)
+    TORCH_CHECK(b.size(0) == B && a.size(0) == B, "philtorch::lfilter_ss: 2D b and a must have x's batch size");
+  const int64_t M = std::max(nb - 1, na);
+  TORCH_CHECK(nb >= 1 && na >= 1 && M <= kMaxOrder, "philtorch::lfilter_ss: filters of order 1 to ", kMaxOrder);
+  TORCH_CHECK(form == PHS_FORM_TDF2 || form == PHS_FORM_DF2, "philtorch::lfilter_ss: form 0 (tdf2) or 1 (df2)");
+  TORCH_CHECK(b.scalar_type() == x.scalar_type() && a.scalar_type() == x.scalar_type(),
+              "philtorch::lfilter_ss: b, a and x must have the same scalar type");
+  TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,
+              "philtorch::lfilter_ss: float32 or float64 only, got ", x.scalar_type());
+  TORCH_CHECK(x.is_cuda() && b.device() == x.device() && a.device() == x.device(),
+              "philtorch::lfilter_ss: philtorch_amd runs on HIP devices only, all tensors on one device");
+  if (zi) {
+    TORCH_CHECK(zi->dim() == 2 && zi->size(0) == B && zi->size(1) == M && zi->scalar_type() == x.scalar_type() &&
+                    zi->device() == x.device(),
+                "philtorch::lfilter_ss: zi must be (batch, order) with x's scalar type");
+  }
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor bc = b.contiguous(), ac = a.contiguous(), xc = x.contiguous(), zc = zi ? zi->contiguous() : Tensor();
+  Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  Tensor zf = at::empty({B, M}, x.options());
+  if (B == 0) return {y, zf};
+  if (T == 0) {
+    if (zi) zf.copy_(zc); else zf.zero_();
+    return {y, zf};
+  }
+  void *stream = stream_of(x);
+  const Workspace ws = workspace_for(x, phs_lti_ss_workspace_size(dt, int(M), B, T), stream);
+  check_status(phs_lfilter_fwd(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
+                               b.dim() == 1 ? 1 : 0, int(form), zi ? zc.const_data_ptr() : nullptr,
+                               xc.const_data_ptr(), y.mutable_data_ptr(), zf.mutable_data_ptr(), ws.ptr, ws.bytes,
+                               stream),
+               "lfilter_ss");
+  return {y, zf};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(philtorch, m) {
@@ -604,6 +651,9 @@ TORCH_LIBRARY(philtorch, m) {
   // new: single-input single-output LTI state space of order <= 4, fused: (y, zf)
   m.def("lti_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
+  // new: lfilter of order <= 4 from b and a (companion model built in the kernel): (y, zf)
+  m.def("lfilter_ss(Tensor b, Tensor a, Tensor? zi, Tensor x, int form) -> (Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
@@ -621,4 +671,5 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("sosfilt_backward", &sosfilt_backward_hip);
   m.impl("filtfilt", &filtfilt_hip);
   m.impl("lti_ss", &lti_ss_hip);
+  m.impl("lfilter_ss", &lfilter_ss_hip);
 }

@@ -5,7 +5,9 @@ it through ``state_space`` (transposed direct form II by default), so with
 ``unroll_factor=1`` on a HIP device every filter is one native scan
 (``philtorch::lti_recur2`` for a biquad); a biquad in TDF-II form runs the
 fused cascade kernel instead (Bx, scan, state shift and output in one pass),
-unless forward-mode AD is active.  ``filtfilt`` and ``lfilter_zi`` follow the
+unless forward-mode AD is active; every other filter of order <= 4 with no
+gradient wanted runs philtorch::lfilter_ss (the companion model built inside
+the kernel).  ``filtfilt`` and ``lfilter_zi`` follow the
 reference and SciPy; a biquad ``filtfilt`` with no gradient wanted runs both
 passes in philtorch::filtfilt.  Cascaded second-order sections are composed by the
 caller, one ``lfilter`` per section, as in the reference (it has no SOS API),
@@ -106,6 +108,44 @@ def _fused_biquad(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor]):
     return y if zi is None else (y, zf[:, 0])
 
 
+def _fused_lfilter_applies(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor], form: str, kwargs) -> bool:
+    """A filter of order 1 to 4 on a HIP device with the native route
+    requested (``unroll_factor=1``) and no gradient wanted: philtorch::
+    lfilter_ss builds the companion model from b and a inside the kernel and
+    runs B x, the scan, the state shift and C h + D x in one pass (the TDF-II
+    biquad takes the cascade kernel first).  Where a gradient is wanted the
+    composed route runs, as in the reference."""
+    from .. import EXTENSION_LOADED
+
+    if not (EXTENSION_LOADED and x.is_cuda and form in ("tdf2", "df2") and set(kwargs) == {"unroll_factor"}
+            and kwargs["unroll_factor"] == 1 and x.dim() == 2):
+        return False
+    M = max(b.size(-1) - 1, a.size(-1))
+    if not (1 <= M <= 4 and a.size(-1) >= 1) or x.dtype not in (torch.float32, torch.float64):
+        return False
+    if b.dtype != x.dtype or a.dtype != x.dtype or (zi is not None and zi.dtype != x.dtype):
+        return False
+    if b.dim() != a.dim() or (b.dim() == 2 and not (b.size(0) == a.size(0) == x.size(0))):
+        return False
+    if zi is not None and not (tuple(zi.shape) in ((M,), (x.size(0), M))):
+        return False
+    if not hasattr(torch.ops.philtorch, "lfilter_ss"):
+        return False
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (b, a, x, zi)):
+        return False
+    import torch.autograd.forward_ad as fwad
+
+    return all(t is None or fwad.unpack_dual(t).tangent is None for t in (b, a, x, zi))
+
+
+def _fused_lfilter(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor], form: str):
+    """lfilter(b, a, x, zi, form) through philtorch::lfilter_ss."""
+    M = max(b.size(-1) - 1, a.size(-1))
+    zb = None if zi is None else zi.expand(x.size(0), M).contiguous()
+    y, zf = torch.ops.philtorch.lfilter_ss(b, a, zb, x, 0 if form == "tdf2" else 1)
+    return y if zi is None else (y, zf)
+
+
 def lfilter(
     b: Tensor,
     a: Tensor,
@@ -139,6 +179,8 @@ def lfilter(
         raise ValueError(f"Unknown backend: {backend}")
     if _fused_biquad_applies(b, a, x, zi, form, kwargs):
         y = _fused_biquad(b, a, x, zi)
+    elif _fused_lfilter_applies(b, a, x, zi, form, kwargs):
+        y = _fused_lfilter(b, a, x, zi, form)
     else:
         y = _ssm_lfilter(b, a, x, zi, form=form, **kwargs)
     if isinstance(y, tuple):

@@ -273,3 +273,32 @@ def test_filtfilt_fused_route_not_taken_on_cpu():
 
     b, a, x = torch.tensor([0.5, 0.2, 0.1]), torch.tensor([-0.5, 0.2]), torch.randn(2, 50)
     assert not filtering._fused_filtfilt_applies(b, a, x, "replicate", "tdf2", {"unroll_factor": 1})
+
+
+def test_capi_state_space_host_only_calls():
+    """Sizes and argument errors of the single-input single-output state space
+    and lfilter entry points (nothing launches)."""
+    lib = capi.load()
+    for dt in (0, 1):
+        for M in (1, 2, 3, 4):
+            assert lib.phs_lti_ss_workspace_size(dt, M, 16, 480000) > 0
+    for bad in ((2, 2, 16, 100), (0, 5, 16, 100), (0, 0, 16, 100), (0, 2, -1, 100)):
+        assert lib.phs_lti_ss_workspace_size(*bad) == 0
+    d = ctypes.c_void_p(16)
+    ws = 1 << 30
+
+    def ss(dt=0, M=3, out_idx=0, a=d):
+        return lib.phs_lti_ss_fwd(dt, M, 2, 100, a, 1, None, 0, None, 1, out_idx, None, 0, None, d, d, None, d, ws,
+                                  None)
+
+    assert ss(dt=2) == capi.PHS_ERR_DTYPE
+    assert ss(M=5) == capi.PHS_ERR_INVALID and ss(out_idx=3) == capi.PHS_ERR_INVALID and ss(a=None) == capi.PHS_ERR_INVALID
+
+    def lf(dt=0, nb=3, na=2, form=0, wsb=ws, b=d):
+        return lib.phs_lfilter_fwd(dt, 2, 100, b, nb, d, na, 0, form, None, d, d, None, d, wsb, None)
+
+    assert lf(dt=2) == capi.PHS_ERR_DTYPE
+    assert lf(form=2) == capi.PHS_ERR_INVALID
+    assert lf(nb=6) == capi.PHS_ERR_INVALID and lf(na=5) == capi.PHS_ERR_INVALID and lf(na=0) == capi.PHS_ERR_INVALID
+    assert lf(b=None) == capi.PHS_ERR_INVALID
+    assert lf(wsb=lib.phs_lti_ss_workspace_size(0, 2, 2, 100) - 1) == capi.PHS_ERR_WORKSPACE
