@@ -57,15 +57,20 @@ struct SsArgs {
   int vec_ok;
 };
 
-// 3 data waves and a look-back wave; 2 rounds of two 16-byte vectors of
-// inputs per lane (8 fp32 or 4 fp64 steps).
+// 3 data waves and a look-back wave.  Orders 1-2: 4 rounds of two 16-byte
+// vectors of inputs per lane (8 fp32 or 4 fp64 steps); orders 3-4: 2 rounds
+// of four vectors, which halves the scan levels per step where each level
+// is an M x M product (6144-step fp32 tiles either way; at the C4 shape,
+// order 4 takes 53 us per launch against 67 with the other split and 74
+// with 3072-step tiles, order 1 25 against 28).
 template <class Alg>
 struct SsShape {
   using E = typename Alg::elem;
+  static constexpr int M = int(sizeof(typename Alg::s_state) / sizeof(E));
   static constexpr int kWaves = 3;
   static constexpr int kThreads = 64 * (kWaves + 1);
-  static constexpr int K = int(32 / sizeof(E));
-  static constexpr int R = 2;
+  static constexpr int K = int((M <= 2 ? 32 : 64) / sizeof(E));
+  static constexpr int R = M <= 2 ? 4 : 2;
   static constexpr int kWaveSeg = 64 * K * R;
   static constexpr int kTile = kWaves * kWaveSeg;
   static_assert((K & (K - 1)) == 0, "K is a power of two (the lane matrix is A^K by squaring)");

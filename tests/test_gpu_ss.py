@@ -9,7 +9,7 @@ scipy.signal.dlsim in tests/test_oracle.py), evaluated in fp64 on the GPU's
 exact inputs.  Orders 1 to 4; dense stable A (a companion matrix in a random
 basis); shared and per-row A, b, c, d; b absent (input into state 0), c
 absent (out_idx), d absent; initial and final states; rows shorter than a
-lane's chunk, on and around a tile (3072 fp32 steps, 1536 fp64), of odd
+lane's chunk, on and around a tile (6144 fp32 steps, 3072 fp64), of odd
 length and of a million steps; the forced look-back fallback.  Through the
 torch API: lfilter of orders 1, 3 and 4 in both forms against the CPU
 (reference) route, state_space against its composed route, gradients
@@ -27,7 +27,7 @@ from tests.test_oracle import _stable_model
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(1, 1), (2, 7), (3, 1535), (2, 1536), (2, 3071), (3, 3072), (2, 3073), (2, 20001)]
+SHAPES = [(1, 1), (2, 7), (3, 3071), (2, 3072), (2, 6143), (3, 6144), (2, 6145), (2, 20001)]
 FLOATS = [np.float32, np.float64]
 ORDERS = [1, 2, 3, 4]
 
