@@ -349,13 +349,26 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
         ctx.save_for_backward(A, B, C, D, zi, x)
 
     def _lti_ss_backward(ctx, gy, gzf):
-        """Gradient of the composite the fused kernel replaces (B x, the native
-        scan, the state shift, C h + D x; philtorch/lti/ssm.py:386-589),
-        recomputed from the inputs; differentiable again under create_graph."""
+        """With A, B, C, D constant: the adjoint model (A^T, input vector C,
+        output vector B, D) run backwards in time from dL/dzf gives grad_x
+        and grad_zi in one more lti_ss pass over the reversed grad_y.
+        Otherwise the gradient of the composite the fused kernel replaces
+        (B x, the native scan, the state shift, C h + D x;
+        philtorch/lti/ssm.py:386-589), recomputed from the inputs.  Both are
+        differentiable again under create_graph."""
         from .lti.ssm import _state_space_composite
 
         inputs = ctx.saved_tensors
         needs = ctx.needs_input_grad
+        A, B, C, D, zi, x = inputs
+        if not any(needs[:4]):
+            M = A.size(-1)
+            unit = lambda i: torch.nn.functional.one_hot(torch.tensor(i, device=x.device), M).to(x.dtype)  # noqa: E731
+            g = gy if gy is not None else torch.zeros_like(x)
+            gxr, gzi = torch.ops.philtorch.lti_ss(A.mT.contiguous(), C if C is not None else unit(ctx.out_idx),
+                                                  B if B is not None else unit(0), D, gzf, g.flip(-1), 0)
+            return (None, None, None, None, gzi if zi is not None and needs[4] else None,
+                    gxr.flip(-1) if needs[5] else None, None)
         wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
         with torch.enable_grad():
             y, zf = _state_space_composite(*inputs, out_idx=ctx.out_idx)
@@ -387,12 +400,22 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
         ctx.save_for_backward(b, a, zi, x)
 
     def _lfilter_ss_backward(ctx, gy, gzf):
-        """Gradient of the companion-form route the kernel replaces
-        (philtorch/lti/filtering.py:273-333), recomputed from the inputs."""
+        """With b and a constant: the adjoint of a companion-form filter is
+        the other companion form of the same filter run backwards in time
+        (TDF-II <-> DF-II: A^T, with the input and output vectors swapped),
+        from dL/dzf, so grad_x and grad_zi are one more lfilter_ss pass over
+        the reversed grad_y.  Otherwise the gradient of the companion-form
+        route the kernel replaces (philtorch/lti/filtering.py:273-333),
+        recomputed from the inputs."""
         from .lti.filtering import _ssm_lfilter
 
         b, a, zi, x = inputs = ctx.saved_tensors
         needs = ctx.needs_input_grad
+        if not (needs[0] or needs[1]):
+            g = gy if gy is not None else torch.zeros_like(x)
+            gxr, gzi = torch.ops.philtorch.lfilter_ss(b, a, gzf, g.flip(-1), 1 - ctx.form)
+            return (None, None, gzi if zi is not None and needs[2] else None, gxr.flip(-1) if needs[3] else None,
+                    None)
         wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
         with torch.enable_grad():
             z = zi if zi is not None else x.new_zeros(x.size(0), max(b.size(-1) - 1, a.size(-1)))

@@ -110,10 +110,11 @@ def _fused_biquad(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor]):
 
 def _fused_lfilter_applies(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor], form: str, kwargs) -> bool:
     """A filter of order 1 to 4 on a HIP device with the native route
-    requested (``unroll_factor=1``) and no gradient wanted: philtorch::
-    lfilter_ss builds the companion model from b and a inside the kernel and
-    runs B x, the scan, the state shift and C h + D x in one pass (the TDF-II
-    biquad takes the cascade kernel first).  Where a gradient is wanted the
+    requested (``unroll_factor=1``) and no gradient wanted for b or a:
+    philtorch::lfilter_ss builds the companion model from b and a inside the
+    kernel and runs B x, the scan, the state shift and C h + D x in one pass
+    (the TDF-II biquad takes the cascade kernel first); gradients for x and zi
+    are one more pass of the adjoint form.  Where b or a need a gradient the
     composed route runs, as in the reference."""
     from .. import EXTENSION_LOADED
 
@@ -131,7 +132,7 @@ def _fused_lfilter_applies(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor]
         return False
     if not hasattr(torch.ops.philtorch, "lfilter_ss"):
         return False
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (b, a, x, zi)):
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (b, a)):
         return False
     import torch.autograd.forward_ad as fwad
 

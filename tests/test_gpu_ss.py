@@ -255,7 +255,8 @@ def test_state_space_route_choice(hip):
     assert not ssm._fused_ss_applies(A, x, v, v, torch.randn(2, device="cuda"), None, 1, None)
     assert not ssm._fused_ss_applies(A, x.cpu(), v, v, None, None, 1, None)
     assert not ssm._fused_ss_applies(A.double(), x, v, v, None, None, 1, None)
-    assert not ssm._fused_ss_applies(A, x.requires_grad_(), v, v, None, None, 1, None)
+    assert ssm._fused_ss_applies(A, x.requires_grad_(), v, v, None, None, 1, None)  # grad_x by the adjoint
+    assert not ssm._fused_ss_applies(A.requires_grad_(), x, v, v, None, None, 1, None)
     with torch.no_grad():
         assert ssm._fused_ss_applies(A, x, v, v, None, None, 1, None)
 
@@ -361,4 +362,58 @@ def test_lfilter_ss_op_gradients_and_opcheck(hip):
     torch.library.opcheck(torch.ops.philtorch.lfilter_ss.default, (t(bf), t(af), None, t(g.standard_normal((2, 500))), 0))
     torch.library.opcheck(torch.ops.philtorch.lfilter_ss.default,
                           (t(bf[:2]), t(af), t(g.standard_normal((2, 4))), t(g.standard_normal((2, 500))), 1))
+
+
+# ---------------------------------------------------------------- adjoint (grad w.r.t. x and zi)
+@pytest.mark.parametrize("order", [1, 3, 4])
+@pytest.mark.parametrize("form", ["tdf2", "df2"])
+def test_lfilter_signal_gradient_takes_adjoint_pass(hip, monkeypatch, order, form):
+    """lfilter with only x and zi requiring grad runs the fused route forward
+    and its adjoint (the other companion form, reversed in time) backward;
+    gradients against the CPU (reference) route's autograd."""
+    import torch
+
+    from philtorch_amd.lti import filtering
+
+    taken = []
+    orig = filtering._fused_lfilter_applies
+    monkeypatch.setattr(filtering, "_fused_lfilter_applies", lambda *a: taken.append(orig(*a)) or taken[-1])
+    g = D.rng(D.seed_of("ss-adjoint", order, form))
+    b, a = _filter(g, order, (3,))
+    x = g.standard_normal((3, 4000))
+    zi = g.standard_normal((3, order))
+    gy = g.standard_normal((3, 4000))
+    gzf = g.standard_normal((3, order))
+    res = []
+    for dev in ("cuda", "cpu"):
+        tx = torch.tensor(x, device=dev, requires_grad=True)
+        tz = torch.tensor(zi, device=dev, requires_grad=True)
+        y, zf = hip.lti.lfilter(torch.tensor(b, device=dev), torch.tensor(a, device=dev), tx, zi=tz, form=form,
+                                unroll_factor=1)
+        ((y * torch.tensor(gy, device=dev)).sum() + (zf * torch.tensor(gzf, device=dev)).sum()).backward()
+        res.append((tx.grad.cpu().numpy(), tz.grad.cpu().numpy()))
+    assert taken[0] is True
+    D.check(res[0][0], res[1][0], "grad_x")
+    D.check(res[0][1], res[1][1], "grad_zi", scale=np.max(np.abs(res[1][0])))
+
+
+def test_adjoint_passes_gradcheck(hip):
+    import torch
+
+    g = D.rng(D.seed_of("ss-adjoint-gradcheck"))
+    Bn, T = 2, 25
+    A, b, c, d = _stable_model(g, 3, (Bn,))
+    t = lambda v, rg=False: torch.tensor(np.asarray(v, np.float64), device="cuda", requires_grad=rg)  # noqa: E731
+    x, zi = t(g.standard_normal((Bn, T)), True), t(g.standard_normal((Bn, 3)), True)
+    f = lambda z_, x_: torch.ops.philtorch.lti_ss(t(A), t(b), t(c), t(d), z_, x_, 0)  # noqa: E731
+    assert torch.autograd.gradcheck(f, (zi, x))
+    assert torch.autograd.gradgradcheck(f, (zi, x))
+    f2 = lambda z_, x_: torch.ops.philtorch.lti_ss(t(A[0]), None, None, None, z_, x_, 2)  # noqa: E731
+    assert torch.autograd.gradcheck(f2, (zi, x))
+    bf, af = (t(v) for v in _filter(g, 4, (Bn,)))
+    z4 = t(g.standard_normal((Bn, 4)), True)
+    for form in (0, 1):
+        f3 = lambda z_, x_: torch.ops.philtorch.lfilter_ss(bf, af, z_, x_, form)  # noqa: E731
+        assert torch.autograd.gradcheck(f3, (z4, x))
+        assert torch.autograd.gradgradcheck(f3, (z4, x))
 
