@@ -15,15 +15,16 @@
 namespace phs {
 namespace {
 
-// Forward tiles carry four 16-byte vectors per lane and round and four rounds,
-// whose step chains run interleaved (fewer, longer tiles: each section is a
-// row-wide synchronisation of the tiles).  The gradient backward keeps four
+// Forward tiles: fp32 16 steps per lane in two rounds (6144-step tiles:
+// 110 us for C4's eight sections against 120 with four rounds and 119-151
+// for 8- or 32-step lanes), fp64 8 steps in four rounds; a lane's rounds are
+// independent chains and run interleaved.  The gradient backward keeps four
 // arrays of a lane's steps live and an LDS table of lane states per lane and
 // round: fp32 takes 32 steps in one round (236 VGPRs, no spills; 4% faster
 // at C4 than 16 steps in two rounds, which cost a second table entry and a
 // second round of multipliers), fp64 8 steps in one round.
 template <typename E>
-using SosFwd = SosShape<E, int(64 / sizeof(E)), 4, 3>;
+using SosFwd = std::conditional_t<sizeof(E) == 4, SosShape<E, 16, 2, 3>, SosShape<E, 8, 4, 3>>;
 template <typename E>
 using SosBwd = std::conditional_t<sizeof(E) == 4, SosShape<E, 32, 1, 3>, SosShape<E, 8, 1, 3>>;
 

@@ -20,7 +20,7 @@ from tests import _data as D
 
 pytestmark = pytest.mark.gpu
 
-# tiles: float32 12288 steps forward, 6144 backward; float64 6144 / 1536
+# tiles: float32 6144 steps forward and backward; float64 6144 / 1536
 SHAPES = [(1, 1), (2, 17), (3, 1536), (2, 3071), (2, 6144), (3, 6145), (2, 12288), (2, 20000), (1, 40000)]
 SECTIONS = [1, 3, 8]
 FLOATS = [np.float32, np.float64]
