@@ -351,7 +351,8 @@ class FiltfiltApi(SosFused):
     """c4_filtfilt: the filtfilt half of the C4 caller pattern, forward only,
     ``for s in range(8): y = lti.filtfilt(b[:, s], a[:, s], y,
     padmode="replicate", padlen=9, unroll_factor=1)`` (each call runs
-    philtorch::filtfilt: two cascade passes and two edge kernels)."""
+    philtorch::filtfilt: two state-space passes, the second in reversed
+    time, their entry states derived in the kernel)."""
 
     def __init__(self):
         super().__init__()
@@ -627,7 +628,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{'ss_kernel' if w.name == 'c4_lfilter4' else 'sos_kernel' if w.name.startswith('c4_') else 'scan_kernel'} ({dominant[0]})",
+            "kernel": f"{'ss_kernel' if w.name in ('c4_lfilter4', 'c4_filtfilt') else 'sos_kernel' if w.name.startswith('c4_') else 'scan_kernel'} ({dominant[0]})",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

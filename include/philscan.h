@@ -219,33 +219,34 @@ int phs_sosfilt_bwd(int dtype, int64_t B, int64_t T, int S, const void *sos, int
                     const void *ckpt, const void *grad_y, const void *grad_zf, void *grad_x, void *grad_sos,
                     void *grad_zi, void *workspace, size_t workspace_bytes, void *stream);
 
-/* ---- Zero-phase filtering with one biquad per row (forward only).
- * Replaces philtorch.lti.filtering.filtfilt (philtorch/lti/filtering.py:
- * 413-484, with lfilter_zi :107-142) for a second-order filter b / a:
+/* ---- Zero-phase filtering with a filter of order 1..4 per row (forward
+ * only).  Replaces philtorch.lti.filtering.filtfilt (philtorch/lti/
+ * filtering.py:413-484, with lfilter_zi :107-142) for a filter b / a:
  *     ext = F.pad(x, (padlen, padlen), mode=padmode)
  *     y1  = lfilter(b, a, ext, zi = lfilter_zi(a, b) * ext[:, 0])
  *     y2  = lfilter(b, a, flip(y1), zi = lfilter_zi(a, b) * y1[:, -1])
  *     y   = flip(y2[:, padlen : padlen + T])
- * computed as four kernels and no copies: the padded row, the flips and the
- * trim are never materialised and lfilter_zi is solved in closed form (the
- * reference's linalg.solve synchronises with the host; a section with a pole
- * at z = 1, 1 + a1 + a2 = 0, raises there and gives non-finite output here).
+ * computed as two state-space launches (one per pass; the second runs in
+ * reversed time) and no copies: the padded row, the flips and the trim are
+ * never materialised, and each pass's entry state is derived inside the
+ * kernel from the row's edge, with lfilter_zi in closed form (the
+ * reference's linalg.solve synchronises with the host; a filter with a pole
+ * at z = 1, 1 + sum(a) = 0, raises there and gives non-finite output here).
  * The output is the same for form "tdf2" and "df2": both start every pass
  * from the steady state of the same transfer function.  dtype PHS_F32 or
- * PHS_F64; b: [B,nb] (coef_shared=0) or [nb] (coef_shared=1), nb = 1..3;
- * a: [B,na] or [na], the denominator after its leading 1, na = 1..2 (as
- * philtorch's b and a; a first-order filter runs as a biquad with
- * b2 = a2 = 0); x, y: [B,T]; 0 <= padlen < T (T >= 1); padmode a
- * phs_padmode code; padlen 0 means no padding, whatever the mode. */
+ * PHS_F64; b: [B,nb] (coef_shared=0) or [nb] (coef_shared=1), nb = 1..5;
+ * a: [B,na] or [na], the denominator after its leading 1, na = 1..4 (as
+ * philtorch's b and a; the order is max(nb - 1, na)); x, y: [B,T];
+ * 0 <= padlen < T (T >= 1); padmode a phs_padmode code; padlen 0 means no
+ * padding, whatever the mode. */
 enum phs_padmode { PHS_PAD_CONSTANT = 0, PHS_PAD_REPLICATE = 1, PHS_PAD_REFLECT = 2, PHS_PAD_CIRCULAR = 3 };
 
 /* Workspace bytes of phs_filtfilt_fwd (self-resetting, like every other
  * workspace here); 0 for unsupported arguments. */
 size_t phs_filtfilt_workspace_size(int dtype, int64_t B, int64_t T);
 
-/* Bytes of phs_filtfilt_fwd's scratch buffer `mid` (the first pass's output,
- * three [B,2] state arrays and the [B,6] section rows; any contents, 16-byte
- * aligned). */
+/* Bytes of phs_filtfilt_fwd's scratch buffer `mid` (the first pass's output
+ * and its [B,4] final states; any contents, 16-byte aligned). */
 size_t phs_filtfilt_mid_size(int dtype, int64_t B, int64_t T);
 
 int phs_filtfilt_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,

@@ -297,6 +297,61 @@ def filtfilt(sos, x, padmode="replicate", padlen=None, nthreads=None):
 
 
 
+def _tdf2_companion(b, a):
+    """TDF-II model of lfilter(b, a) per row (philtorch/lti/filtering.py:
+    107-142 and :273-333, transpose=True): b [R,nb], a [R,na] (after the
+    leading 1) zero-padded to order M = max(nb - 1, na); A = companion(a)^T
+    [R,M,M], g = b[1:] - b[0] a [R,M], b0 [R]; y = h[0] + b0 u."""
+    b = np.asarray(b, np.float64)
+    a = np.asarray(a, np.float64)
+    M = max(b.shape[-1] - 1, a.shape[-1])
+    bp = np.zeros(b.shape[:-1] + (M + 1,))
+    bp[..., : b.shape[-1]] = b
+    ap = np.zeros(a.shape[:-1] + (M,))
+    ap[..., : a.shape[-1]] = a
+    A = np.zeros(a.shape[:-1] + (M, M))
+    A[..., :, 0] = -ap
+    A[..., np.arange(M - 1), np.arange(1, M)] = 1.0
+    return A, bp[..., 1:] - bp[..., :1] * ap, bp[..., 0]
+
+
+def lfilter_zi_ba(b, a):
+    """lfilter_zi(a, b) of philtorch (filtering.py:107-142, transpose=True):
+    solve(I - A, g) on the TDF-II model of each row of b [R,nb], a [R,na]."""
+    A, g, _ = _tdf2_companion(b, a)
+    return np.linalg.solve(np.eye(A.shape[-1]) - A, g[..., None])[..., 0]
+
+
+def filtfilt_ba(b, a, x, padmode="replicate", padlen=None, nthreads=None):
+    """philtorch.lti.filtfilt (philtorch/lti/filtering.py:413-484) for a
+    filter of any order: b [nb] or [B,nb], a [na] or [B,na] (after the
+    leading 1), x [B,T].  Pads by `padlen` (default 3 * max(nb, na + 1)) with
+    F.pad's `padmode` (None: no padding), runs lfilter(tdf2) -- the TDF-II
+    model through lti_state_space -- from lfilter_zi * ext[:, 0], again over
+    the reversed output from lfilter_zi * y[:, -1], trims and flips back."""
+    dt = np.asarray(x).dtype
+    x = _c(x, dt)
+    B, T = x.shape
+    b = np.broadcast_to(np.asarray(b, np.float64), (B, np.shape(b)[-1])).astype(dt).astype(np.float64)
+    a = np.broadcast_to(np.asarray(a, np.float64), (B, np.shape(a)[-1])).astype(dt).astype(np.float64)
+    ntaps = max(b.shape[-1], a.shape[-1] + 1)
+    edge = 0 if padmode is None else (3 * ntaps if padlen is None else int(padlen))
+    assert T > edge, f"Input signal length {T} must be greater than pad length {edge}."
+    ext = np.pad(x, ((0, 0), (edge, edge)), mode=_NP_PAD[padmode]) if edge > 0 else x
+    ext = np.ascontiguousarray(ext)
+    A, g, b0 = _tdf2_companion(b, a)
+    M = A.shape[-1]
+    zi = lfilter_zi_ba(b, a)
+    e0 = np.eye(M)[0]
+    A, g, b0, zi = (v.astype(dt) for v in (A, g, b0, zi))
+    y, _ = lti_state_space(A, ext, B=g, C=e0, D=b0, zi=zi * ext[:, :1], nthreads=nthreads)
+    yr = np.ascontiguousarray(y[:, ::-1])
+    y, _ = lti_state_space(A, yr, B=g, C=e0, D=b0, zi=zi * yr[:, :1], nthreads=nthreads)
+    if edge > 0:
+        y = y[:, edge:-edge]
+    return np.ascontiguousarray(y[:, ::-1])
+
+
 def lti_state_space(A, x, B=None, C=None, D=None, zi=None, out_idx=None, nthreads=None):
     """philtorch.lti.state_space for a 2D input and a single output
     (philtorch/lti/ssm.py:386-589): Bx = x b (b an M-vector per row or shared;

@@ -7,7 +7,7 @@ namespace: the reference's five ops (``recur2``, ``recurN``, ``lti_recur2``,
 LPV scalar op ``recur``, four fused backward ops, and the fused cascade of
 second-order sections ``sosfilt`` / ``sosfilt_backward`` (no reference
 counterpart; ``lti.sosfilt`` is its API), the forward-only zero-phase
-``filtfilt`` of filters up to second order (behind ``lti.filtfilt``) and the
+``filtfilt`` of filters up to order 4 (behind ``lti.filtfilt``) and the
 fused single-input single-output state space ``lti_ss`` (behind
 ``lti.state_space``) and ``lfilter_ss``, ``lfilter`` of order <= 4 from b and
 a in one pass (behind ``lti.lfilter``).  This module then
@@ -331,7 +331,7 @@ if EXTENSION_LOADED and _has_op("filtfilt"):
     def _(b, a, x, padmode, padlen):
         torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
         torch._check(b.ndim == a.ndim and b.ndim in (1, 2), lambda: "b and a must both be 1D or both 2D")
-        torch._check(1 <= b.shape[-1] <= 3 and 1 <= a.shape[-1] <= 2, lambda: "second order at most")
+        torch._check(1 <= b.shape[-1] <= 5 and 1 <= a.shape[-1] <= 4, lambda: "order 4 at most")
         torch._check(0 <= padlen < x.shape[1], lambda: "0 <= padlen < T")
         return _fake_like(x)
 

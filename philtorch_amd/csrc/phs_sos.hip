@@ -1,13 +1,11 @@
-// C ABI of the fused second-order-section cascade and of the zero-phase
-// biquad filter built on it (declared in include/philscan.h): argument
-// checks, workspace carving and the launches of sos_kernel
-// [-> sos_grad_reduce_kernel], or of filtfilt's four kernels, on the caller's
-// stream.  No allocation and no synchronisation.
+// C ABI of the fused second-order-section cascade (declared in
+// include/philscan.h): argument checks, workspace carving and the launches of
+// sos_kernel [-> sos_grad_reduce_kernel] on the caller's stream.  No
+// allocation and no synchronisation.
 // Workspace layout: [0, 2048) claim header, then the status words of every
 // (row, section, tile), then (gradient backward only) per-tile, per-wave
 // coefficient sums.
 #include "phs_launch.hpp"
-#include "phs_filtfilt.hpp"
 #include "phs_sos.hpp"
 
 #include <type_traits>
@@ -138,89 +136,6 @@ int sos_bwd(int64_t B, int64_t T, int S, const void *sos, bool shared, const voi
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
-// filtfilt's scratch buffer ("mid"): pass 1's output [B, T], three [B, 2]
-// state arrays (pass 1 entry state, pass 1 final state, pass 2 entry state)
-// and the [B, 6] section rows.  Kept out of the self-resetting workspace,
-// whose status words must never be overwritten with data.
-struct FiltfiltMid {
-  size_t y1 = 0, h1 = 0, zf1 = 0, m2 = 0, sos = 0, total = 0;
-};
-
-inline FiltfiltMid filtfilt_mid(size_t esz, int64_t B, int64_t T) {
-  FiltfiltMid M;
-  const size_t st = align_up(size_t(B) * 2 * esz);
-  M.h1 = align_up(size_t(B) * size_t(T) * esz);
-  M.zf1 = M.h1 + st;
-  M.m2 = M.zf1 + st;
-  M.sos = M.m2 + st;
-  M.total = M.sos + align_up(size_t(B) * 6 * esz);
-  return M;
-}
-
-bool filtfilt_sizes_ok(int64_t B, int64_t T, int nb, int na, int mode, int64_t padlen) {
-  return B >= 0 && T >= 1 && nb >= 1 && nb <= 3 && na >= 1 && na <= 2 && padlen >= 0 && padlen < T &&
-         mode >= kPadConstant && mode <= kPadCircular;
-}
-
-// Both passes of one section take 8 steps per lane and round, 4 rounds
-// (6144-step tiles): with one section a tile's latency, not its arithmetic,
-// sets the pace, and the smaller tiles keep more of them resident (C4's
-// filtfilt pattern: 13.0 GSamples/s against 10.9 with the cascade's forward
-// tiles; K = 4 or 2 rounds, 1, 2 or 7 data waves all measured slower).
-template <typename E>
-using FiltfiltShape = SosShape<E, 8, 4, 3>;
-
-template <typename E>
-int filtfilt_fwd(int64_t B, int64_t T, const void *bc, int nb, const void *ac, int na, bool shared, int mode,
-                 int64_t e, const void *x, void *y, void *mid, void *workspace, size_t ws_bytes, hipStream_t stream) {
-  using Sh = FiltfiltShape<E>;
-  if (!filtfilt_sizes_ok(B, T, nb, na, mode, e)) return PHS_ERR_INVALID;
-  if (B == 0) return PHS_OK;
-  if (!bc || !ac || !x || !y || !mid) return PHS_ERR_INVALID;
-  const SosLayout L = sos_layout<E, Sh>(B, T, 1, false);
-  if (double(B) * double(L.tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
-  if (!workspace || ws_bytes < L.total) return PHS_ERR_WORKSPACE;
-  char *ws = static_cast<char *>(workspace);
-  const FiltfiltMid M = filtfilt_mid(sizeof(E), B, T);
-  char *m = static_cast<char *>(mid);
-  E *y1 = reinterpret_cast<E *>(m + M.y1);
-  E *h1 = reinterpret_cast<E *>(m + M.h1);
-  E *zf1 = reinterpret_cast<E *>(m + M.zf1);
-  E *m2 = reinterpret_cast<E *>(m + M.m2);
-  E *sos = reinterpret_cast<E *>(m + M.sos);
-  const bool vec_len = (size_t(T) * sizeof(E)) % 16 == 0;
-  const unsigned edge_grid = unsigned((B + 255) / 256);
-
-  FiltfiltEdge<E> ed{static_cast<const E *>(bc), static_cast<const E *>(ac), nb, na, sos, shared ? 1 : B,
-                     static_cast<const E *>(x), y1, zf1, h1, B, T, e, mode};
-  hipLaunchKernelGGL(filtfilt_pre_kernel<E>, dim3(edge_grid), dim3(256), 0, stream, ed);
-  if (hipGetLastError() != hipSuccess) return PHS_ERR_LAUNCH;
-
-  SosArgs<E> p1{};
-  fill_common<E, Sh>(p1, L, B, T, 1, sos, shared, ws);
-  p1.in = static_cast<const E *>(x);
-  p1.out = y1;
-  p1.virt = h1;
-  p1.fin = zf1;
-  p1.vec_ok = vec_len && aligned16(x) && aligned16(y1);
-  const unsigned grid = p1.per_stripe * kStripes;
-  hipLaunchKernelGGL((sos_kernel<E, Sh, false, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, p1);
-  if (hipGetLastError() != hipSuccess) return PHS_ERR_LAUNCH;
-
-  ed.state = m2;
-  hipLaunchKernelGGL(filtfilt_mid_kernel<E>, dim3(edge_grid), dim3(256), 0, stream, ed);
-  if (hipGetLastError() != hipSuccess) return PHS_ERR_LAUNCH;
-
-  SosArgs<E> p2{};
-  fill_common<E, Sh>(p2, L, B, T, 1, sos, shared, ws);
-  p2.in = y1;
-  p2.out = static_cast<E *>(y);
-  p2.virt = m2;
-  p2.vec_ok = vec_len && aligned16(y1) && aligned16(y);
-  hipLaunchKernelGGL((sos_kernel<E, Sh, true, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, p2);
-  return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
-}
-
 }  // namespace
 }  // namespace phs
 
@@ -264,39 +179,6 @@ int phs_sosfilt_bwd(int dtype, int64_t B, int64_t T, int S, const void *sos, int
     case PHS_F64:
       return phs::sos_bwd<double>(B, T, S, sos, sos_shared != 0, x, ckpt, grad_y, grad_zf, grad_x, grad_sos,
                                   grad_zi, workspace, workspace_bytes, st);
-    default: return PHS_ERR_DTYPE;
-  }
-}
-
-size_t phs_filtfilt_workspace_size(int dtype, int64_t B, int64_t T) {
-  if (B < 0 || T < 1) return 0;
-  switch (dtype) {
-    case PHS_F32: return phs::sos_layout<float, phs::FiltfiltShape<float>>(B, T, 1, false).total;
-    case PHS_F64: return phs::sos_layout<double, phs::FiltfiltShape<double>>(B, T, 1, false).total;
-    default: return 0;
-  }
-}
-
-size_t phs_filtfilt_mid_size(int dtype, int64_t B, int64_t T) {
-  if (B < 0 || T < 1) return 0;
-  switch (dtype) {
-    case PHS_F32: return phs::filtfilt_mid(sizeof(float), B, T).total;
-    case PHS_F64: return phs::filtfilt_mid(sizeof(double), B, T).total;
-    default: return 0;
-  }
-}
-
-int phs_filtfilt_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
-                     int coef_shared, int padmode, int64_t padlen, const void *x, void *y, void *mid, void *workspace,
-                     size_t workspace_bytes, void *stream) {
-  const hipStream_t st = static_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case PHS_F32:
-      return phs::filtfilt_fwd<float>(B, T, b, nb, a, na, coef_shared != 0, padmode, padlen, x, y, mid, workspace,
-                                      workspace_bytes, st);
-    case PHS_F64:
-      return phs::filtfilt_fwd<double>(B, T, b, nb, a, na, coef_shared != 0, padmode, padlen, x, y, mid,
-                                       workspace, workspace_bytes, st);
     default: return PHS_ERR_DTYPE;
   }
 }

@@ -1,6 +1,7 @@
-// C ABI of the fused single-input, single-output LTI state space (declared in
-// include/philscan.h): argument checks, workspace carving and the launch of
-// ss_kernel on the caller's stream.  No allocation and no synchronisation.
+// C ABI of the fused single-input, single-output LTI state space and of the
+// zero-phase filter built on it (declared in include/philscan.h): argument
+// checks, workspace carving and the launches of ss_kernel on the caller's
+// stream (one per pass).  No allocation and no synchronisation.
 // Workspace layout: [0, 2048) claim header, then the status words of every
 // (row, tile).
 #include "phs_launch.hpp"
@@ -23,33 +24,16 @@ struct SsFilter {
   bool shared = false;
 };
 
+// The launch arguments of one pass over [B, T] (workspace carved as above);
+// false if the workspace is short.
 template <class Alg>
-int ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, const void *bv, bool b_sh, const void *cv, bool c_sh,
-           int out_idx, const void *d, bool d_sh, const SsFilter &f, const void *zi, const void *x, void *y, void *zf,
-           void *workspace, size_t ws_bytes, hipStream_t stream) {
+bool ss_args(int64_t B, int64_t T, const SsFilter &f, const void *zi, const void *x, void *y, void *zf,
+             void *workspace, size_t ws_bytes, SsArgs<Alg> &a) {
   using E = typename Alg::elem;
   using Sh = SsShape<Alg>;
-  constexpr int M = SsView<Alg>::M;
-  if (B < 0 || T < 0) return PHS_ERR_INVALID;
-  if (f.form == 0 && !cv && (out_idx < 0 || out_idx >= M)) return PHS_ERR_INVALID;
-  if (f.form != 0 && (f.nb < 1 || f.nb > M + 1 || f.na < 1 || f.na > M || (f.nb - 1 != M && f.na != M)))
-    return PHS_ERR_INVALID;
-  if (B == 0 || T == 0) return PHS_OK;
-  if ((f.form == 0 ? !A : (!f.b || !f.a)) || !x || !y) return PHS_ERR_INVALID;
   const int64_t tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
-  if (double(B) * double(tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
-  if (!workspace || ws_bytes < ss_ws_bytes<Alg>(B, T)) return PHS_ERR_WORKSPACE;
+  if (!workspace || ws_bytes < ss_ws_bytes<Alg>(B, T)) return false;
   char *ws = static_cast<char *>(workspace);
-  SsArgs<Alg> a{};
-  a.A = static_cast<const E *>(A);
-  a.A_stride = A_sh ? 0 : M * M;
-  a.bv = static_cast<const E *>(bv);
-  a.b_stride = b_sh ? 0 : M;
-  a.cv = static_cast<const E *>(cv);
-  a.c_stride = c_sh ? 0 : M;
-  a.d = static_cast<const E *>(d);
-  a.d_stride = d_sh ? 0 : 1;
-  a.out_idx = out_idx;
   a.fb = static_cast<const E *>(f.b);
   a.fa = static_cast<const E *>(f.a);
   a.nb = f.nb;
@@ -71,8 +55,93 @@ int ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, const void *bv, bool 
   const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
   a.spin_limit = sl ? sl : kDefaultSpinLimit;
   a.vec_ok = (size_t(T) * sizeof(E)) % 16 == 0 && aligned16(x) && aligned16(y);
-  hipLaunchKernelGGL(ss_kernel<Alg>, dim3(a.per_stripe * kStripes), dim3(Sh::kThreads), 0, stream, a);
+  return true;
+}
+
+template <class Alg, bool REV>
+int ss_launch(const SsArgs<Alg> &a, hipStream_t stream) {
+  hipLaunchKernelGGL((ss_kernel<Alg, REV>), dim3(a.per_stripe * kStripes), dim3(SsShape<Alg>::kThreads), 0, stream,
+                     a);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
+}
+
+bool ss_grid_ok(int64_t B, int64_t T, int64_t kTile) {
+  return double(B) * double((T + kTile - 1) / kTile) < 2147483648.0;
+}
+
+bool ss_filter_ok(const SsFilter &f, int M) {
+  return f.nb >= 1 && f.nb <= M + 1 && f.na >= 1 && f.na <= M && (f.nb - 1 == M || f.na == M);
+}
+
+template <class Alg>
+int ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, const void *bv, bool b_sh, const void *cv, bool c_sh,
+           int out_idx, const void *d, bool d_sh, const SsFilter &f, const void *zi, const void *x, void *y, void *zf,
+           void *workspace, size_t ws_bytes, hipStream_t stream) {
+  using E = typename Alg::elem;
+  constexpr int M = SsView<Alg>::M;
+  if (B < 0 || T < 0) return PHS_ERR_INVALID;
+  if (f.form == 0 && !cv && (out_idx < 0 || out_idx >= M)) return PHS_ERR_INVALID;
+  if (f.form != 0 && !ss_filter_ok(f, M)) return PHS_ERR_INVALID;
+  if (B == 0 || T == 0) return PHS_OK;
+  if ((f.form == 0 ? !A : (!f.b || !f.a)) || !x || !y) return PHS_ERR_INVALID;
+  if (!ss_grid_ok(B, T, SsShape<Alg>::kTile)) return PHS_ERR_INVALID;
+  SsArgs<Alg> a{};
+  if (!ss_args<Alg>(B, T, f, zi, x, y, zf, workspace, ws_bytes, a)) return PHS_ERR_WORKSPACE;
+  a.A = static_cast<const E *>(A);
+  a.A_stride = A_sh ? 0 : M * M;
+  a.bv = static_cast<const E *>(bv);
+  a.b_stride = b_sh ? 0 : M;
+  a.cv = static_cast<const E *>(cv);
+  a.c_stride = c_sh ? 0 : M;
+  a.d = static_cast<const E *>(d);
+  a.d_stride = d_sh ? 0 : 1;
+  a.out_idx = out_idx;
+  return ss_launch<Alg, false>(a, stream);
+}
+
+// filtfilt's scratch buffer ("mid"): pass 1's output [B, T] and final state
+// [B, 4] (order 4 at most).  Kept out of the self-resetting workspace, whose
+// status words must never be overwritten with data.
+inline size_t filtfilt_zf_offset(size_t esz, int64_t B, int64_t T) { return align_up(size_t(B) * size_t(T) * esz); }
+inline size_t filtfilt_mid_bytes(size_t esz, int64_t B, int64_t T) {
+  return filtfilt_zf_offset(esz, B, T) + align_up(size_t(B) * 4 * esz);
+}
+
+// The workspace of either pass at any order (the tile length is the same
+// for every order of a precision; the status entries grow with it).
+template <typename E>
+size_t filtfilt_ws_bytes(int64_t B, int64_t T) {
+  size_t m = ss_ws_bytes<Scalar<E>>(B, T);
+  m = std::max(m, ss_ws_bytes<Block2<E>>(B, T));
+  m = std::max(m, ss_ws_bytes<BlockN<E, 3>>(B, T));
+  return std::max(m, ss_ws_bytes<BlockN<E, 4>>(B, T));
+}
+
+// Zero-phase filter: pass 1 forward over x from the edge-derived state into
+// mid (output and final state), pass 2 in reversed time over mid into y.
+template <class Alg>
+int ss_filtfilt(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e, const void *x, void *y, void *mid,
+                void *workspace, size_t ws_bytes, hipStream_t stream) {
+  using E = typename Alg::elem;
+  if (ws_bytes < filtfilt_ws_bytes<E>(B, T)) return PHS_ERR_WORKSPACE;  // the documented size, any order
+  char *m = static_cast<char *>(mid);
+  E *y1 = reinterpret_cast<E *>(m);
+  E *zf1 = reinterpret_cast<E *>(m + filtfilt_zf_offset(sizeof(E), B, T));
+  SsArgs<Alg> p{};
+  if (!ss_args<Alg>(B, T, f, nullptr, x, y1, zf1, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+  p.virt_mode = 1;
+  p.xpad = static_cast<const E *>(x);
+  p.pad_mode = mode;
+  p.pad_len = e;
+  int rc = ss_launch<Alg, false>(p, stream);
+  if (rc != PHS_OK) return rc;
+  if (!ss_args<Alg>(B, T, f, nullptr, y1, y, nullptr, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+  p.virt_mode = 2;
+  p.xpad = static_cast<const E *>(x);
+  p.zf_prev = zf1;
+  p.pad_mode = mode;
+  p.pad_len = e;
+  return ss_launch<Alg, true>(p, stream);
 }
 
 // f(Alg{}) for one of the eight (dtype, M) models
@@ -131,6 +200,49 @@ int phs_lfilter_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, cons
   return phs::ss_dispatch(dtype, M, [&](auto alg) {
     return phs::ss_fwd<decltype(alg)>(B, T, nullptr, false, nullptr, false, nullptr, false, 0, nullptr, false, f, zi,
                                       x, y, zf, workspace, workspace_bytes, st);
+  });
+}
+
+size_t phs_filtfilt_workspace_size(int dtype, int64_t B, int64_t T) {
+  if (B < 0 || T < 1) return 0;
+  switch (dtype) {
+    case PHS_F32: return phs::filtfilt_ws_bytes<float>(B, T);
+    case PHS_F64: return phs::filtfilt_ws_bytes<double>(B, T);
+    default: return 0;
+  }
+}
+
+size_t phs_filtfilt_mid_size(int dtype, int64_t B, int64_t T) {
+  if (B < 0 || T < 1) return 0;
+  switch (dtype) {
+    case PHS_F32: return phs::filtfilt_mid_bytes(sizeof(float), B, T);
+    case PHS_F64: return phs::filtfilt_mid_bytes(sizeof(double), B, T);
+    default: return 0;
+  }
+}
+
+int phs_filtfilt_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
+                     int coef_shared, int padmode, int64_t padlen, const void *x, void *y, void *mid, void *workspace,
+                     size_t workspace_bytes, void *stream) {
+  if (dtype != PHS_F32 && dtype != PHS_F64) return PHS_ERR_DTYPE;
+  const int M = nb - 1 > na ? nb - 1 : na;
+  if (B < 0 || T < 1 || nb < 1 || nb > 5 || na < 1 || na > 4 || padlen < 0 || padlen >= T ||
+      padmode < PHS_PAD_CONSTANT || padmode > PHS_PAD_CIRCULAR)
+    return PHS_ERR_INVALID;
+  if (B == 0) return PHS_OK;
+  if (!b || !a || !x || !y || !mid) return PHS_ERR_INVALID;
+  const int64_t tile = dtype == PHS_F32 ? phs::SsShape<phs::Scalar<float>>::kTile : phs::SsShape<phs::Scalar<double>>::kTile;
+  if (!phs::ss_grid_ok(B, T, tile)) return PHS_ERR_INVALID;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  phs::SsFilter f;
+  f.b = b;
+  f.a = a;
+  f.nb = nb;
+  f.na = na;
+  f.form = 1;  // TDF-II (ss_filtfilt_entry)
+  f.shared = coef_shared != 0;
+  return phs::ss_dispatch(dtype, M, [&](auto alg) {
+    return phs::ss_filtfilt<decltype(alg)>(B, T, f, padmode, padlen, x, y, mid, workspace, workspace_bytes, st);
   });
 }
 

@@ -17,8 +17,15 @@
 // Every map's matrix part is a power of A known in advance, so the data
 // waves scan vectors only against a table of A^(K 2^i) in LDS (the look-back
 // wave builds it while they load): M^2 work and registers per level instead
-// of the M^3 of composing maps.  Forward only: the gradient is the composite
-// on the native recurrence ops.
+// of the M^3 of composing maps.  The gradients with respect to x and zi are
+// this kernel on the adjoint model; those of the coefficients are the
+// composite on the native recurrence ops.
+//
+// The same kernel runs both passes of a zero-phase filter (philtorch/lti/
+// filtering.py:413-484 filtfilt): scan positions map to descending time
+// (REV), and a row's entry state is derived in the kernel from the edge of
+// the row (ss_filtfilt_entry), so that neither the padded copy nor the flips
+// exist.
 #pragma once
 
 #include "phs_scan.hpp"
@@ -47,9 +54,19 @@ struct SsArgs {
   int nb, na, filt_form;
   int64_t f_stride_b, f_stride_a;  // 0 = shared
   const E *zi;        // [B, M]; nullptr: zeros
+  // The rows' entry states (virt_mode): 0 zi above; 1 and 2 the two passes
+  // of a zero-phase filter (ss_filtfilt_entry below): 1 the steady state of
+  // the padded row's first sample, stepped over the front pad of xpad; 2 the
+  // state pass 1 (final state zf_prev) reaches over the back pad, carried
+  // into the time-reversed pass
+  int virt_mode;
+  const E *xpad;      // [B, T] the zero-phase filter's input (pad values)
+  const E *zf_prev;   // [B, M] pass 1's final state (virt_mode 2)
+  int pad_mode;
+  int64_t pad_len;
   const E *x;         // [B, T]
   E *y;               // [B, T]
-  E *zf;              // [B, M]; nullable
+  E *zf;              // [B, M]; nullable (scan order: the state after the last step scanned)
   int64_t B, T_len, tiles_per_row;
   unsigned long long *claims;
   unsigned tiles, per_stripe, spin_limit;
@@ -75,6 +92,84 @@ struct SsShape {
   static constexpr int kTile = kWaves * kWaveSeg;
   static_assert((K & (K - 1)) == 0, "K is a power of two (the lane matrix is A^K by squaring)");
 };
+
+// Chunk I/O in scan order: forward, scan position s is time s; reversed
+// (REV), it is time T-1-s, so a lane's K steps are the K samples below
+// T - s0, read (and written) in descending time.  Positions past the row
+// read 0 and are not written.  The bounds-checked paths assign in branches
+// (no select between a global and a private address).
+template <bool REV, typename E, int K>
+__device__ __forceinline__ void ss_load(const E *row, int64_t s0, int64_t T, bool vec, E (&out)[K]) {
+  if constexpr (!REV) {
+    load_chunk<E, K>(row, s0, T, vec, out, E(0));
+  } else {
+    const int64_t base = T - s0 - K;  // lowest time of the chunk
+    if (vec && base >= 0) {
+      E tmp[K];
+      load_chunk<E, K>(row, base, T, true, tmp, E(0));
+#pragma unroll
+      for (int k = 0; k < K; ++k) out[k] = tmp[K - 1 - k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int64_t t = T - 1 - s0 - k;
+        if (t >= 0)
+          out[k] = row[t];
+        else
+          out[k] = E(0);
+      }
+    }
+  }
+}
+
+template <bool REV, typename E, int K>
+__device__ __forceinline__ void ss_store(E *row, int64_t s0, int64_t T, bool vec, const E (&v)[K]) {
+  if constexpr (!REV) {
+    store_chunk<E, K>(row, s0, T, vec, v);
+  } else {
+    const int64_t base = T - s0 - K;
+    if (vec && base >= 0) {
+      E tmp[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) tmp[k] = v[K - 1 - k];
+      store_chunk<E, K>(row, base, T, true, tmp);
+    } else {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int64_t t = T - 1 - s0 - k;
+        if (t >= 0) row[t] = v[k];
+      }
+    }
+  }
+}
+
+// padmode codes (PHS_PAD_* in philscan.h): torch.nn.functional.pad modes
+constexpr int kPadConstant = 0;   // zeros
+constexpr int kPadReplicate = 1;  // edge value
+constexpr int kPadReflect = 2;    // mirror without repeating the edge
+constexpr int kPadCircular = 3;   // wrap around
+
+// ext[j] for j in [0, e): the front pad of a row of T samples (e < T)
+template <typename E>
+__device__ __forceinline__ E pad_front(const E *x, int64_t T, int64_t e, int mode, int64_t j) {
+  switch (mode) {
+    case kPadReplicate: return x[0];
+    case kPadReflect: return x[e - j];
+    case kPadCircular: return x[T - e + j];
+    default: return E(0);
+  }
+}
+
+// ext[T + e + j] for j in [0, e): the back pad (e < T)
+template <typename E>
+__device__ __forceinline__ E pad_back(const E *x, int64_t T, int mode, int64_t j) {
+  switch (mode) {
+    case kPadReplicate: return x[T - 1];
+    case kPadReflect: return x[T - 2 - j];
+    case kPadCircular: return x[j];
+    default: return E(0);
+  }
+}
 
 // The element view of a state or coefficient (Scalar: one value, Block2 and
 // BlockN: contiguous fields in index order).
@@ -191,6 +286,119 @@ __device__ __forceinline__ SsModel<Alg> ss_model(const SsArgs<Alg> &a, int64_t r
   return m;
 }
 
+// Entry state of row b for the two passes of a zero-phase filter
+// (virt_mode 1 and 2), in double, on the TDF-II model of lfilter(fb, fa) of
+// order M (filter form 1: h' = A h + g u with A = companion(a)^T, g = b[1:]
+// - b0 a, y = h0 + b0 u).  Both passes run that one model whatever form the
+// caller names: each starts from the steady state of the same transfer
+// function, so the outputs are the same (the reference runs its `form`).
+//
+//  * steady state for a unit input, z = (I - A)^-1 g (lfilter_zi,
+//    philtorch/lti/filtering.py:107-142): from the companion structure,
+//    z0 = H(1) - b0 with H(1) = sum(b) / (1 + sum(a)), and
+//    z(i+1) = z(i) + a_i z0 - g_i;
+//  * pass 1 starts at z ext[0] before the e front-pad samples of xpad, so
+//    its entry state is that stepped over them (filtering.py:466-470);
+//  * pass 2 filters the reversed pass-1 output over the padded row, whose
+//    first e samples are the back pad's outputs yb[e-1..0] (pass 1 stepped
+//    on from its final state zf_prev over the back pad of xpad), from
+//    z yb[e-1] (z y1[T-1] if e = 0; filtering.py:472-474).  Folded:
+//        h = A^e z y0 + sum_j A^j g yb[j].
+// A filter with a pole at z = 1 (1 + sum(a) = 0) has no steady state: the
+// reference's linalg.solve raises, here the output is not finite.
+// Tile 0 of a row derives it while its data loads (and the look-back's
+// fallback), every lane the same: the pad samples are loaded 64 at a time,
+// one per lane, so the serial steps wait on one load latency per batch
+// rather than one per sample.
+template <class Alg>
+__device__ __forceinline__ typename Alg::state ss_filtfilt_entry(const SsArgs<Alg> &a, int64_t b, int lane) {
+  using E = typename Alg::elem;
+  constexpr int M = SsView<Alg>::M;
+  const E *fb = a.fb + b * a.f_stride_b, *fa = a.fa + b * a.f_stride_a;
+  const double b0 = double(fb[0]);
+  double am[M], g[M], z[M], h[M];
+  double sb = b0, sa = 1.0;
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    am[i] = i < a.na ? double(fa[i]) : 0.0;
+    const double bi = i + 1 < a.nb ? double(fb[i + 1]) : 0.0;
+    g[i] = bi - b0 * am[i];
+    sb += bi;
+    sa += am[i];
+  }
+  z[0] = sb / sa - b0;
+#pragma unroll
+  for (int i = 0; i + 1 < M; ++i) z[i + 1] = z[i] + am[i] * z[0] - g[i];
+  // h <- A h + g u (ascending i reads h[i+1] before it changes)
+  auto step = [&](double (&v)[M], double u) {
+    const double v0 = v[0];
+#pragma unroll
+    for (int i = 0; i < M; ++i) v[i] = -am[i] * v0 + (i + 1 < M ? v[i + 1] : 0.0) + g[i] * u;
+  };
+  const int64_t T = a.T_len, e = a.pad_len;
+  const E *xp = a.xpad + b * T;
+  if (a.virt_mode == 1) {
+    const double u0 = double(e > 0 ? pad_front(xp, T, e, a.pad_mode, 0) : xp[0]);
+#pragma unroll
+    for (int i = 0; i < M; ++i) h[i] = z[i] * u0;
+    for (int64_t j0 = 0; j0 < e; j0 += 64) {
+      const int64_t jl = j0 + lane;
+      const double ul = jl < e ? double(pad_front(xp, T, e, a.pad_mode, jl)) : 0.0;
+      const int n = e - j0 < 64 ? int(e - j0) : 64;
+      for (int j = 0; j < n; ++j) step(h, read_lane(ul, j));
+    }
+  } else {
+    double P[M][M], acc[M], ul = 0.0;
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+      h[i] = double(a.zf_prev[b * M + i]);
+      acc[i] = 0.0;
+#pragma unroll
+      for (int k = 0; k < M; ++k) P[i][k] = i == k ? 1.0 : 0.0;
+    }
+    double y0 = e > 0 ? 0.0 : double(a.x[b * T + T - 1]);
+    for (int64_t j = 0; j < e; ++j) {
+      if ((j & 63) == 0) {  // the next batch of back-pad samples, one per lane
+        const int64_t jl = j + lane;
+        ul = jl < e ? double(pad_back(xp, T, a.pad_mode, jl)) : 0.0;
+      }
+      const double u = read_lane(ul, int(j & 63));
+      const double yb = h[0] + b0 * u;
+      // acc += A^j g yb, then P = A^(j+1) (row i: -a_i P[0] + P[i+1])
+#pragma unroll
+      for (int i = 0; i < M; ++i) {
+        double t = 0.0;
+#pragma unroll
+        for (int k = 0; k < M; ++k) t += P[i][k] * g[k];
+        acc[i] += t * yb;
+      }
+      double p0[M];
+#pragma unroll
+      for (int k = 0; k < M; ++k) p0[k] = P[0][k];
+#pragma unroll
+      for (int i = 0; i < M; ++i)
+#pragma unroll
+        for (int k = 0; k < M; ++k) P[i][k] = -am[i] * p0[k] + (i + 1 < M ? P[i + 1][k] : 0.0);
+      step(h, u);
+      y0 = yb;
+    }
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+      double t = acc[i];
+#pragma unroll
+      for (int k = 0; k < M; ++k) t += P[i][k] * z[k] * y0;
+      h[i] = t;
+    }
+  }
+  union {
+    typename Alg::s_state s;
+    E e[M];
+  } u;
+#pragma unroll
+  for (int i = 0; i < M; ++i) u.e[i] = E(h[i]);
+  return Alg::load_s(u.s);
+}
+
 // A^(2^n) in compute precision.
 template <class Alg>
 __device__ __forceinline__ typename Alg::coef ss_pow2(const typename Alg::s_coef &A, int n) {
@@ -253,18 +461,32 @@ __device__ __forceinline__ void ss_pow_apply(const typename Alg::coef *P, int n,
   }
 }
 
+// A lane's place in the scan order.  FLIP (the reversed pass) numbers the
+// lanes from 63 down, so that lanes in ascending order still read and write
+// ascending addresses when scan positions run down in time; the scans below
+// then combine with the lane above rather than below.
+template <bool FLIP>
+__device__ __forceinline__ int ss_scan_lane(int lane) {
+  return FLIP ? 63 - lane : lane;
+}
+template <bool FLIP>
+__device__ __forceinline__ int ss_last_lane() {
+  return FLIP ? 0 : 63;
+}
+
 // Inclusive scans of N rounds of lane vectors, v_L = sum_{j <= L}
-// A^(K (L-j)) s_j: Kogge-Stone, level i combines with the lane 2^i below at
-// A^(K 2^i), level by level across the rounds.
-template <class Alg, int N>
+// A^(K (L-j)) s_j over scan lanes L: Kogge-Stone, level i combines with the
+// scan lane 2^i below at A^(K 2^i), level by level across the rounds.
+template <class Alg, int N, bool FLIP>
 __device__ __forceinline__ void ss_lane_scan(typename Alg::state (&v)[N], int lane, const typename Alg::coef *pw) {
+  const int sl = ss_scan_lane<FLIP>(lane);
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
     const int d = 1 << i;
     typename Alg::state o[N];
 #pragma unroll
-    for (int r = 0; r < N; ++r) o[r] = shfl_from(v[r], lane - d);
-    if (lane >= d) {
+    for (int r = 0; r < N; ++r) o[r] = shfl_from(v[r], FLIP ? lane + d : lane - d);
+    if (sl >= d) {
       const typename Alg::coef P = pw[i];
 #pragma unroll
       for (int r = 0; r < N; ++r) v[r] = Alg::affine(P, o[r], v[r]);
@@ -274,21 +496,23 @@ __device__ __forceinline__ void ss_lane_scan(typename Alg::state (&v)[N], int la
 
 // State entering scan position `span` of a row, folded straight from the
 // inputs (the look-back's bounded-wait fallback; out of line, cold): chunk
-// by chunk of 64 K steps, st <- A^(64 K) st + chunk total.
-template <class Alg, class Sh>
+// by chunk of 64 K steps, st <- A^(64 K) st + chunk total, from the row's
+// entry state st (derived here for a zero-phase pass).
+template <class Alg, class Sh, bool REV>
 __device__ __noinline__ typename Alg::state ss_prefix_fallback(SsArgs<Alg> a, int64_t b, int64_t span, int lane,
                                                               typename Alg::state st, const SsPowers<Alg> *tab) {
   using E = typename Alg::elem;
   constexpr int K = Sh::K;
   const SsModel<Alg> m = ss_model<Alg>(a, b);
   const E *xrow = a.x + b * a.T_len;
+  if (a.virt_mode != 0) st = ss_filtfilt_entry<Alg>(a, b, lane);
   for (int64_t off = 0; off < span; off += 64 * K) {
     ss_reload_tables();
     E xs[K];
-    load_chunk<E, K>(xrow, off + int64_t(lane) * K, a.T_len, a.vec_ok != 0, xs, E(0));
+    ss_load<REV, E, K>(xrow, off + int64_t(ss_scan_lane<REV>(lane)) * K, a.T_len, a.vec_ok != 0, xs);
     typename Alg::state v[1] = {ss_lane_fold<Alg, K>(m, xs)};
-    ss_lane_scan<Alg, 1>(v, lane, tab->pw);
-    st = Alg::affine(tab->pw[6], st, read_lane(v[0], 63));
+    ss_lane_scan<Alg, 1, REV>(v, lane, tab->pw);
+    st = Alg::affine(tab->pw[6], st, read_lane(v[0], ss_last_lane<REV>()));
   }
   return st;
 }
@@ -375,7 +599,7 @@ __device__ bool ss_lookback(const uint64_t *row_status, const typename Alg::stat
 }
 
 // At least two waves per SIMD (two workgroups per CU).
-template <class Alg>
+template <class Alg, bool REV>
 __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Alg> a) {
   using E = typename Alg::elem;
   using S = typename Alg::state;
@@ -427,7 +651,15 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
     }
     __syncthreads();  // power tables
     uint64_t *row_status = a.status + b * a.tiles_per_row * St::kStride;
-    const S virt = a.zi ? Alg::load_s(V::load_vec(a.zi + b * V::M)) : Alg::szero();
+    // The row's entry state.  A zero-phase pass derives it from the row's
+    // edge, which only tile 0 needs: tile 0 publishes inclusive states only,
+    // so a look-back from a later tile never passes it (the fallback does).
+    S virt = Alg::szero();
+    if (a.virt_mode == 0) {
+      if (a.zi) virt = Alg::load_s(V::load_vec(a.zi + b * V::M));
+    } else if (q == 0) {
+      virt = ss_filtfilt_entry<Alg>(a, b, lane);
+    }
     S yin = virt;
     __syncthreads();  // wave aggregates are in s_wagg
     // exclusive wave prefixes and the tile aggregate (every lane, uniformly)
@@ -440,7 +672,7 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
     if (q > 0) {
       if (lane == 0) publish(row_status + q * St::kStride + St::kVecWords, tagg, tag);
       if (!ss_lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, &s_tab, q, yin))
-        yin = ss_prefix_fallback<Alg, Sh>(a, b, q * Sh::kTile, lane, virt, &s_tab);
+        yin = ss_prefix_fallback<Alg, Sh, REV>(a, b, q * Sh::kTile, lane, virt, &s_tab);
     }
     if (q + 1 < a.tiles_per_row && lane == 0)
       publish(row_status + q * St::kStride, Alg::affine(s_tab.gp[0], yin, tagg), tag);
@@ -454,12 +686,13 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
   const bool vec = a.vec_ok != 0;
   const E *xrow = a.x + b * T;
   const int64_t seg0 = q * Sh::kTile + int64_t(w) * Sh::kWaveSeg;
+  const int sl = ss_scan_lane<REV>(lane);
   int64_t t0s[R];
   E X[R][K];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    t0s[r] = seg0 + int64_t(r) * 64 * K + int64_t(lane) * K;
-    load_chunk<E, K>(xrow, t0s[r], T, vec, X[r], E(0));
+    t0s[r] = seg0 + int64_t(r) * 64 * K + int64_t(sl) * K;
+    ss_load<REV, E, K>(xrow, t0s[r], T, vec, X[r]);
   }
   __syncthreads();  // power tables
 
@@ -471,12 +704,12 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
     S v[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) v[r] = ss_lane_fold<Alg, K>(m, X[r]);
-    ss_lane_scan<Alg, R>(v, lane, s_tab.pw);
+    ss_lane_scan<Alg, R, REV>(v, lane, s_tab.pw);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      tot[r] = read_lane(v[r], 63);
-      const S prev = shfl_from(v[r], lane - 1);
-      ex[r] = lane > 0 ? prev : Alg::szero();
+      tot[r] = read_lane(v[r], ss_last_lane<REV>());
+      const S prev = shfl_from(v[r], REV ? lane + 1 : lane - 1);
+      ex[r] = sl > 0 ? prev : Alg::szero();
     }
   }
   if (lane == 0) {
@@ -493,13 +726,13 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
   st = Alg::sadd(st, s_wpre[w]);
 
   // ---- pass 2: round r of the wave starts at st[r] (st[r+1] = A^(64 K)
-  // st[r] + tot[r]); a lane enters it at A^(K lane) st[r] + ex[r], then
+  // st[r] + tot[r]); a lane enters it at A^(K sl) st[r] + ex[r], then
   // y = c . h + d x and the step
   S ent[R];
   ent[0] = st;
 #pragma unroll
   for (int r = 1; r < R; ++r) ent[r] = Alg::affine(s_tab.pw[6], ent[r - 1], tot[r - 1]);
-  ss_pow_apply<Alg, 6, R>(s_tab.pw, lane, ent);
+  ss_pow_apply<Alg, 6, R>(s_tab.pw, sl, ent);
   E *yrow = a.y + b * T;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -519,7 +752,7 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
         for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = u.e[i];
       }
     }
-    store_chunk<E, K>(yrow, t0s[r], T, vec, O);
+    ss_store<REV, E, K>(yrow, t0s[r], T, vec, O);
   }
 }
 

@@ -468,9 +468,9 @@ Triple sosfilt_backward_hip(const Tensor &sos, const Tensor &x, const Tensor &ck
   return {gx, gsos, gzi};
 }
 
-// Zero-phase filter of second order at most (phs_filtfilt_fwd;
-// philtorch/lti/filtering.py:413-484): b (nb,) or (batch, nb), nb <= 3; a
-// (na,) or (batch, na), the denominator after its leading 1, na <= 2;
+// Zero-phase filter of order 4 at most (phs_filtfilt_fwd;
+// philtorch/lti/filtering.py:413-484): b (nb,) or (batch, nb), nb <= 5; a
+// (na,) or (batch, na), the denominator after its leading 1, na <= 4;
 // padmode a phs_padmode code.  Forward only: callers that need gradients
 // compose lfilter passes instead.
 Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t padmode, int64_t padlen) {
@@ -481,8 +481,8 @@ Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t p
   if (b.dim() == 2)
     TORCH_CHECK(b.size(0) == B && a.size(0) == B, "philtorch::filtfilt: 2D b and a must have x's batch size");
   const int64_t nb = b.size(-1), na = a.size(-1);
-  TORCH_CHECK(nb >= 1 && nb <= 3 && na >= 1 && na <= 2, "philtorch::filtfilt: filters of second order at most "
-              "(b: 1 to 3 taps, a: 1 or 2 after the leading 1)");
+  TORCH_CHECK(nb >= 1 && nb <= 5 && na >= 1 && na <= 4, "philtorch::filtfilt: filters of order 4 at most "
+              "(b: 1 to 5 taps, a: 1 to 4 after the leading 1)");
   TORCH_CHECK(b.scalar_type() == x.scalar_type() && a.scalar_type() == x.scalar_type(),
               "philtorch::filtfilt: b, a and x must have the same scalar type");
   TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,

@@ -197,7 +197,7 @@ _PAD_CODES = {"constant": 0, "replicate": 1, "reflect": 2, "circular": 3}
 
 
 def _fused_filtfilt_applies(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[str], form: str, kwargs) -> bool:
-    """A filter of second order at most on a HIP device with the native route
+    """A filter of order 4 at most on a HIP device with the native route
     requested (``unroll_factor=1``) and no gradient wanted: philtorch::filtfilt
     runs both passes with the padding, the flips and the trim folded in.  Its
     output is the same for the ``tdf2`` and ``df2`` forms (each pass starts
@@ -209,7 +209,7 @@ def _fused_filtfilt_applies(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[s
         return False
     if padmode is not None and padmode not in _PAD_CODES:
         return False
-    if not (1 <= a.size(-1) <= 2 and 1 <= b.size(-1) <= 3) or x.dtype not in (torch.float32, torch.float64):
+    if not (1 <= a.size(-1) <= 4 and 1 <= b.size(-1) <= 5) or x.dtype not in (torch.float32, torch.float64):
         return False
     if b.dtype != x.dtype or a.dtype != x.dtype or x.dim() not in (1, 2):
         return False
@@ -227,7 +227,7 @@ def _fused_filtfilt_applies(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[s
 
 
 def _fused_filtfilt(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[str], edge: int) -> Tensor:
-    """filtfilt of a filter of second order at most through philtorch::filtfilt."""
+    """filtfilt of a filter of order 4 at most through philtorch::filtfilt."""
     x2 = x.reshape(-1, x.size(-1))
     code = _PAD_CODES[padmode] if padmode is not None else 0
     y = torch.ops.philtorch.filtfilt(b, a, x2, code, edge if padmode is not None else 0)
@@ -247,11 +247,12 @@ def filtfilt(
 ) -> Tensor:
     """Zero-phase filtering: a forward and a reversed ``lfilter`` pass with
     edge padding and steady-state initial conditions
-    (philtorch/lti/filtering.py:413-484).  A biquad on a HIP device with
-    ``unroll_factor=1`` and no gradient wanted runs philtorch::filtfilt (two
-    cascade passes and two small edge kernels, no padded copy, no flips and no
+    (philtorch/lti/filtering.py:413-484).  A filter of order 4 at most on a
+    HIP device with ``unroll_factor=1`` and no gradient wanted runs
+    philtorch::filtfilt (two state-space passes, the second in reversed time,
+    their entry states derived in the kernel: no padded copy, no flips and no
     host synchronisation); otherwise the passes are composed as in the
-    reference, each biquad pass on the fused lfilter route."""
+    reference, each pass on the fused lfilter route."""
     assert method in ("pad", "gust"), "Method must be either 'pad' or 'gust'."
     if method == "gust":
         raise NotImplementedError("Gustafsson's method is not implemented yet.")

@@ -107,3 +107,27 @@ def sos_coefs(g, lead, S, dtype, rlo=0.5, rhi=0.95, rz=1.2):
     k = g.uniform(0.5, 1.5, shape)
     sos = np.stack([k, -2 * z * np.cos(ph) * k, z * z * k, np.ones(shape), -2 * r * np.cos(th), r * r], axis=-1)
     return sos.astype(dtype)
+
+
+def ba_coefs(g, lead, order, dtype, rlo=0.5, rhi=0.95):
+    """A filter of the given order as philtorch's (b, a): b lead + (order + 1,),
+    a lead + (order,) after the leading 1.  The product of order // 2
+    sections of sos_coefs and, for an odd order, a first-order section with a
+    real pole of radius U(rlo, rhi) and either sign, a real zero and gain."""
+    lead = tuple(lead)
+    n = int(np.prod(lead)) if lead else 1
+    sos = sos_coefs(g, (n,), order // 2, np.float64, rlo, rhi).reshape(n, order // 2, 6)
+    p = g.uniform(rlo, rhi, n) * np.where(g.uniform(size=n) < 0.5, -1.0, 1.0)
+    z, k = g.uniform(-1.2, 1.2, n), g.uniform(0.5, 1.5, n)
+    bs, as_ = [], []
+    for r in range(n):
+        bn, ad = np.ones(1), np.ones(1)
+        for s in range(order // 2):
+            bn, ad = np.convolve(bn, sos[r, s, :3]), np.convolve(ad, sos[r, s, 3:])
+        if order % 2:
+            bn, ad = np.convolve(bn, [k[r], -k[r] * z[r]]), np.convolve(ad, [1.0, -p[r]])
+        bs.append(bn)
+        as_.append(ad[1:])
+    b = np.array(bs).reshape(lead + (order + 1,))
+    a = np.array(as_).reshape(lead + (order,))
+    return b.astype(dtype), a.astype(dtype)

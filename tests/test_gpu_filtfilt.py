@@ -1,19 +1,21 @@
 """GPU parity of the zero-phase filter (phs_filtfilt_fwd, op
 philtorch::filtfilt, the fused route of philtorch_amd.lti.filtfilt for
-filters of first and second order).
+filters of order 1 to 4: two state-space passes, the second in reversed
+time, their entry states derived in the kernel).
 
 The C ABI entry point (ctypes, raw device pointers, the caller's stream)
-against oracle.filtfilt, which follows the reference's filtfilt step by step
-(pad, lfilter_zi, lfilter, flip, lfilter, trim, flip; pinned to
+against oracle.filtfilt_ba, which follows the reference's filtfilt step by
+step (pad, lfilter_zi, lfilter, flip, lfilter, trim, flip; pinned to
 scipy.signal.filtfilt in tests/test_oracle.py), evaluated in fp64 on the GPU's
-exact inputs.  Covers every pad mode at padlen 0, 9, an intermediate length
-and the largest allowed (T - 1); rows shorter than a lane's chunk, on and
-around a tile (6144 steps) and a cascade forward tile (12288), of odd length (scalar loads)
-and of a million steps; shared and per-row sections; the forced look-back
-fallback of both passes.  Through the torch API: scipy (second- and
-first-order filters), the composed route
-(each pass an lfilter) at the benchmark's C4 size, the route choice, and
-gradients (which take the composed route).
+exact inputs.  Covers orders 1-4 and unequal numerator / denominator lengths,
+every pad mode at padlen 0, 9, an intermediate length and the largest
+allowed (T - 1); rows shorter than a lane's chunk, on and around a tile
+(6144 fp32 or 3072 fp64 steps) and two, of odd length (scalar loads) and of a
+million steps; shared and per-row coefficients; the forced look-back fallback
+of both passes; a constant row and linearity at the benchmark's C4 size.
+Through the torch API: scipy (orders 1-4), the composed route (each pass an
+lfilter) at the C4 size, the route choice, and gradients (which take the
+composed route).
 """
 import ctypes
 
@@ -25,7 +27,9 @@ from tests import _data as D
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(1, 1), (2, 17), (3, 6143), (2, 6144), (2, 12287), (3, 12288), (2, 12289), (2, 6145), (1, 40000), (2, 30001)]
+SHAPES = [(1, 1), (2, 17), (2, 3071), (3, 3073), (3, 6143), (2, 6144), (2, 6145), (2, 12287), (3, 12288),
+          (1, 40000), (2, 30001)]
+ORDERS = [1, 2, 3, 4]
 FLOATS = [np.float32, np.float64]
 MODES = ["constant", "replicate", "reflect", "circular"]
 
@@ -58,7 +62,7 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def _run(api, sos, x, padmode, padlen):
+def _run(api, b, a, x, padmode, padlen):
     """phs_filtfilt_fwd through the C ABI; numpy y."""
     import torch
 
@@ -68,69 +72,94 @@ def _run(api, sos, x, padmode, padlen):
     need = lib.phs_filtfilt_workspace_size(dt, B, T)
     assert 0 < need <= ws.numel()
     mid = torch.empty(lib.phs_filtfilt_mid_size(dt, B, T), dtype=torch.uint8, device="cuda")
-    tb, ta, tx = _dev(sos[..., 0:3]), _dev(sos[..., 4:6]), _dev(x)
+    tb, ta, tx = _dev(b), _dev(a), _dev(x)
     y = torch.full_like(tx, float("nan"))
-    rc = lib.phs_filtfilt_fwd(dt, B, T, _p(tb), 3, _p(ta), 2, int(sos.ndim == 1), capi.PADMODES[padmode], padlen,
-                              _p(tx), _p(y), _p(mid), _p(ws), need, _stream())
+    print(f"filtfilt capi B={B} T={T} nb={b.shape[-1]} na={a.shape[-1]} {padmode} {padlen}", flush=True)
+    rc = lib.phs_filtfilt_fwd(dt, B, T, _p(tb), b.shape[-1], _p(ta), a.shape[-1], int(b.ndim == 1),
+                              capi.PADMODES[padmode], padlen, _p(tx), _p(y), _p(mid), _p(ws), need, _stream())
     assert rc == capi.PHS_OK, lib.phs_error_string(rc)
     torch.cuda.synchronize()
     return y.cpu().numpy()
 
 
-def _case(dtype, B, T, shared, seed):
+def _case(dtype, B, T, shared, seed, order=2):
     g = D.rng(seed)
-    sos = D.sos_coefs(g, () if shared else (B,), 1, dtype, rhi=0.98)[..., 0, :]
+    b, a = D.ba_coefs(g, () if shared else (B,), order, dtype, rhi=0.98)
     x = D.normal(g, (B, T), dtype)
-    return sos, x
+    return b, a, x
 
 
-def _check(y, sos, x, padmode, padlen, dtype, name):
-    ref = oracle.filtfilt(np.asarray(sos, np.float64), np.asarray(x, np.float64), padmode=padmode, padlen=padlen)
+def _check(y, b, a, x, padmode, padlen, dtype, name):
+    f64 = lambda v: np.asarray(v, np.float64)  # noqa: E731
+    ref = oracle.filtfilt_ba(f64(b), f64(a), f64(x), padmode=padmode, padlen=padlen)
     D.check(y, ref, name, dtype=dtype)
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("order", ORDERS)
 @pytest.mark.parametrize("B,T", SHAPES)
-def test_filtfilt_capi_parity(api, dtype, B, T):
+def test_filtfilt_capi_parity(api, dtype, order, B, T):
     for shared in (False, True):
-        sos, x = _case(dtype, B, T, shared, D.seed_of("filtfilt", dtype, B, T, shared))
+        b, a, x = _case(dtype, B, T, shared, D.seed_of("filtfilt", dtype, order, B, T, shared), order)
         for mode in MODES:
             for padlen in sorted({0, min(9, T - 1), T // 3, T - 1}):
-                y = _run(api, sos, x, mode, padlen)
-                _check(y, sos, x, mode, padlen, dtype, f"B={B} T={T} shared={shared} {mode} padlen={padlen}")
+                y = _run(api, b, a, x, mode, padlen)
+                _check(y, b, a, x, mode, padlen, dtype, f"order {order} B={B} T={T} shared={shared} {mode} "
+                       f"padlen={padlen}")
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
-def test_filtfilt_capi_long_rows(api, dtype):
-    sos, x = _case(dtype, 2, 1_000_003, False, D.seed_of("filtfilt-long", dtype))
+def test_filtfilt_capi_unequal_lengths(api, dtype):
+    """Numerator and denominator of different lengths: the order is
+    max(nb - 1, na), the shorter one zero-padded (an FIR, an all-pole
+    filter and mixed cases)."""
+    g = D.rng(D.seed_of("filtfilt-nbna", dtype))
+    x = D.normal(g, (3, 7001), dtype)
+    for nb, na in ((5, 1), (1, 4), (2, 3), (4, 2), (3, 1), (1, 1), (2, 4)):
+        order = max(nb - 1, na)
+        bf, af = D.ba_coefs(g, (3,), order, np.float64, rhi=0.98)
+        b = g.standard_normal((3, nb)) if nb != order + 1 else bf
+        a = af[:, :na] if na == order else D.ba_coefs(g, (3,), na, np.float64, rhi=0.98)[1]
+        b, a = b.astype(dtype), a.astype(dtype)
+        for mode, padlen in (("replicate", 3 * (order + 1)), ("reflect", 40), ("constant", 0)):
+            _check(_run(api, b, a, x, mode, padlen), b, a, x, mode, padlen, dtype, f"nb={nb} na={na} {mode}")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("order", [2, 4])
+def test_filtfilt_capi_long_rows(api, dtype, order):
+    b, a, x = _case(dtype, 2, 1_000_003, False, D.seed_of("filtfilt-long", dtype, order), order)
     for mode, padlen in (("replicate", 9), ("reflect", 4097)):
-        _check(_run(api, sos, x, mode, padlen), sos, x, mode, padlen, dtype, f"long rows {mode}")
+        _check(_run(api, b, a, x, mode, padlen), b, a, x, mode, padlen, dtype, f"long rows {mode}")
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
-def test_filtfilt_capi_forced_fallback(api, dtype):
+@pytest.mark.parametrize("order", ORDERS)
+def test_filtfilt_capi_forced_fallback(api, dtype, order):
     """A one-poll budget makes the tiles of both passes compute their entry
-    states from the row prefix (pass 1) or suffix (pass 2) themselves."""
+    states from the row's edge and prefix (pass 1) or suffix (pass 2)
+    themselves."""
     lib = api[0]
-    sos, x = _case(dtype, 3, 40000, False, D.seed_of("filtfilt-fallback", dtype))
+    b, a, x = _case(dtype, 3, 40000, False, D.seed_of("filtfilt-fallback", dtype, order), order)
     lib.phs_debug_set_spin_limit(1)
     try:
-        y = _run(api, sos, x, "replicate", 9)
+        y = _run(api, b, a, x, "replicate", 9)
     finally:
         lib.phs_debug_set_spin_limit(0)
-    _check(y, sos, x, "replicate", 9, dtype, "fallback")
+    _check(y, b, a, x, "replicate", 9, dtype, "fallback")
 
 
-def test_filtfilt_capi_constant_row_full_size(api):
+@pytest.mark.parametrize("order", [2, 4])
+def test_filtfilt_capi_constant_row_full_size(api, order):
     """At the C4 size a constant row comes out scaled by H(1)^2 for every
     edge-value pad: both passes start in, and stay in, their steady state."""
     B, T = 16, 480000
-    g = D.rng(D.seed_of("filtfilt-dc"))
-    sos = D.sos_coefs(g, (B,), 1, np.float64, rhi=0.98)[:, 0, :]
-    h1 = sos[:, :3].sum(-1) / (1 + sos[:, 4] + sos[:, 5])
+    g = D.rng(D.seed_of("filtfilt-dc", order))
+    b, a = D.ba_coefs(g, (B,), order, np.float64, rhi=0.98)
+    h1 = b.sum(-1) / (1 + a.sum(-1))
     x = np.full((B, T), 0.75)
     for mode in ("replicate", "reflect", "circular"):
-        y = _run(api, sos, x, mode, 9)
+        y = _run(api, b, a, x, mode, 9)
         D.check(y, np.broadcast_to((h1 * h1 * 0.75)[:, None], (B, T)), f"constant row {mode}", dtype=np.float64)
 
 
@@ -139,11 +168,11 @@ def test_filtfilt_capi_linearity_full_size(api):
     states scale with the row): f(2u - 3v) = 2 f(u) - 3 f(v) at the C4 size."""
     B, T = 16, 480000
     g = D.rng(D.seed_of("filtfilt-linear"))
-    sos = D.sos_coefs(g, (B,), 1, np.float64, rhi=0.98)[:, 0, :]
+    b, a = D.ba_coefs(g, (B,), 3, np.float64, rhi=0.98)
     u, v = g.standard_normal((B, T)), g.standard_normal((B, T))
     for mode in MODES:
-        lhs = _run(api, sos, 2 * u - 3 * v, mode, 9)
-        rhs = 2 * _run(api, sos, u, mode, 9) - 3 * _run(api, sos, v, mode, 9)
+        lhs = _run(api, b, a, 2 * u - 3 * v, mode, 9)
+        rhs = 2 * _run(api, b, a, u, mode, 9) - 3 * _run(api, b, a, v, mode, 9)
         D.check(lhs, rhs, f"linearity {mode}", dtype=np.float64)
 
 
@@ -169,7 +198,11 @@ def test_filtfilt_route_choice(hip):
     assert not filtering._fused_filtfilt_applies(b, a, x, "odd", "tdf2", ok)
     assert not filtering._fused_filtfilt_applies(b, a, x[:2], "replicate", "tdf2", ok)
     assert filtering._fused_filtfilt_applies(b[:, :2], a[:, :1], x, "replicate", "tdf2", ok)
-    assert not filtering._fused_filtfilt_applies(torch.ones(3, 4, device="cuda"), a, x, "replicate", "tdf2", ok)
+    b4, a4 = (torch.tensor(v, device="cuda") for v in D.ba_coefs(g, (3,), 4, np.float32))
+    assert filtering._fused_filtfilt_applies(b4, a4, x, "replicate", "tdf2", ok)
+    assert filtering._fused_filtfilt_applies(torch.ones(3, 5, device="cuda"), a, x, "replicate", "tdf2", ok)
+    assert not filtering._fused_filtfilt_applies(torch.ones(3, 6, device="cuda"), a, x, "replicate", "tdf2", ok)
+    assert not filtering._fused_filtfilt_applies(b, torch.ones(3, 5, device="cuda"), x, "replicate", "tdf2", ok)
     assert not filtering._fused_filtfilt_applies(b, a, x.requires_grad_(), "replicate", "tdf2", ok)
     with torch.no_grad():
         assert filtering._fused_filtfilt_applies(b, a, x, "replicate", "tdf2", ok)
@@ -184,10 +217,9 @@ def test_filtfilt_api_matches_scipy(hip, dtype):
 
     g = D.rng(D.seed_of("filtfilt-api", dtype))
     for shape, batched, order in (((3, 5000), False, 2), ((3, 5000), True, 2), ((777,), False, 2),
-                                  ((3, 5000), True, 1), ((3, 5000), False, 1)):
-        b, a = _biquad(g, (shape[0],) if batched else (), np.float64)
-        if order == 1:  # b0 + b1 z^-1 over 1 + a1 z^-1, pole in (-0.95, 0.95)
-            b, a = b[..., :2], np.clip(a[..., :1], -0.95, 0.95)
+                                  ((3, 5000), True, 1), ((3, 5000), False, 1), ((3, 5000), True, 3),
+                                  ((3, 5000), False, 4), ((3, 5000), True, 4)):
+        b, a = D.ba_coefs(g, (shape[0],) if batched else (), order, np.float64, rhi=0.98)
         x = g.standard_normal(shape)
         tb, ta, tx = (torch.tensor(v.astype(dtype), device="cuda") for v in (b, a, x))
         for padmode, padlen, padtype in (("replicate", None, "constant"), ("reflect", 100, "even"),
@@ -246,8 +278,10 @@ def test_filtfilt_api_errors(hip):
         hip.lti.filtfilt(b, a, torch.randn(2, 9, device="cuda"), unroll_factor=1)
     with pytest.raises(RuntimeError, match="must be greater than pad length"):
         torch.ops.philtorch.filtfilt(b, a, torch.randn(2, 9, device="cuda"), 1, 9)
-    with pytest.raises(RuntimeError, match="second order at most"):
-        torch.ops.philtorch.filtfilt(torch.ones(4, device="cuda"), a, torch.randn(2, 90, device="cuda"), 1, 9)
+    with pytest.raises(RuntimeError, match="order 4 at most"):
+        torch.ops.philtorch.filtfilt(torch.ones(6, device="cuda"), a, torch.randn(2, 90, device="cuda"), 1, 9)
+    with pytest.raises(RuntimeError, match="order 4 at most"):
+        torch.ops.philtorch.filtfilt(b, torch.ones(5, device="cuda"), torch.randn(2, 90, device="cuda"), 1, 9)
 
 
 def test_filtfilt_opcheck(hip):
@@ -261,4 +295,7 @@ def test_filtfilt_opcheck(hip):
                           test_utils=("test_schema", "test_faketensor"))
     torch.library.opcheck(torch.ops.philtorch.filtfilt.default,
                           (b.expand(2, 3).contiguous(), a[:1].expand(2, 1).contiguous(), x, 2, 0),
+                          test_utils=("test_schema", "test_faketensor"))
+    b4, a4 = (torch.tensor(v, device="cuda") for v in D.ba_coefs(g, (2,), 4, np.float32))
+    torch.library.opcheck(torch.ops.philtorch.filtfilt.default, (b4, a4, x, 3, 15),
                           test_utils=("test_schema", "test_faketensor"))

@@ -22,7 +22,7 @@ def test_capi_exports_every_declared_symbol():
 
 def test_capi_host_only_calls():
     lib = capi.load()
-    assert lib.phs_abi_version() == 103
+    assert lib.phs_abi_version() == 104
     for op in capi.OPS.values():
         for dt in capi.DTYPES.values():
             fwd = lib.phs_workspace_size(op, dt, 64, 65536, 0, 0)
@@ -243,8 +243,10 @@ def test_capi_filtfilt_host_only_calls():
     lib = capi.load()
     for dt, esz in ((0, 4), (1, 8)):
         assert lib.phs_filtfilt_workspace_size(dt, 16, 480000) > 0
-        # pass 1's output, three [B, 2] state arrays and the [B, 6] section rows
-        assert lib.phs_filtfilt_mid_size(dt, 16, 480000) >= 16 * 480000 * esz + 3 * 16 * 2 * esz + 16 * 6 * esz
+        # pass 1's output and its [B, 4] final states
+        assert lib.phs_filtfilt_mid_size(dt, 16, 480000) >= 16 * 480000 * esz + 16 * 4 * esz
+        # one workspace serves every order: at least the order-4 state-space one
+        assert lib.phs_filtfilt_workspace_size(dt, 16, 480000) >= lib.phs_lti_ss_workspace_size(dt, 4, 16, 480000)
     for bad in ((2, 16, 100), (0, -1, 100), (0, 16, 0)):
         assert lib.phs_filtfilt_workspace_size(*bad) == 0
         assert lib.phs_filtfilt_mid_size(*bad) == 0
@@ -260,11 +262,12 @@ def test_capi_filtfilt_host_only_calls():
     assert call(padlen=-1) == capi.PHS_ERR_INVALID
     assert call(T=0, padlen=0) == capi.PHS_ERR_INVALID
     assert call(mode=4) == capi.PHS_ERR_INVALID
-    assert call(nb=4) == capi.PHS_ERR_INVALID and call(nb=0) == capi.PHS_ERR_INVALID
-    assert call(na=3) == capi.PHS_ERR_INVALID and call(na=0) == capi.PHS_ERR_INVALID
+    assert call(nb=6) == capi.PHS_ERR_INVALID and call(nb=0) == capi.PHS_ERR_INVALID
+    assert call(na=5) == capi.PHS_ERR_INVALID and call(na=0) == capi.PHS_ERR_INVALID
     assert call(mid=None) == capi.PHS_ERR_INVALID and call(b=None) == capi.PHS_ERR_INVALID
     need = lib.phs_filtfilt_workspace_size(0, 2, 100)
-    assert call(wsb=need - 1) == capi.PHS_ERR_WORKSPACE
+    for nb, na in ((3, 2), (2, 1), (5, 4)):
+        assert call(wsb=need - 1, nb=nb, na=na) == capi.PHS_ERR_WORKSPACE
     assert lib.phs_filtfilt_fwd(0, 0, 100, None, 3, None, 2, 0, rep, 9, None, None, None, None, 0, None) == capi.PHS_OK
 
 

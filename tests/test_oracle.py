@@ -369,6 +369,57 @@ def test_filtfilt_steady_state_and_lfilter_zi():
     np.testing.assert_allclose(np.einsum("rij,rj->ri", A, zi) + Bv, zi, rtol=1e-12)
 
 
+@pytest.mark.parametrize("order", [1, 2, 3, 4])
+@pytest.mark.parametrize("batched", [False, True])
+def test_filtfilt_ba_matches_scipy(order, batched):
+    """oracle.filtfilt_ba (any order, the TDF-II companion model through
+    lti_state_space) against scipy.signal.filtfilt for the edge-value pads
+    and no padding, and against the same steps on scipy's lfilter_zi /
+    lfilter for zeros and circular padding; its default pad length is
+    3 * max(nb, na + 1), as the reference's."""
+    g = D.rng(D.seed_of("oracle-filtfilt-ba", order, batched))
+    B, T = 3, 400
+    b, a = D.ba_coefs(g, (B,) if batched else (), order, np.float64, rhi=0.97)
+    x = g.standard_normal((B, T))
+    ntaps = order + 1
+    for padmode, padlen, padtype in (("replicate", None, "constant"), ("reflect", 25, "even"),
+                                     ("replicate", T - 1, "constant"), (None, None, None)):
+        y = oracle.filtfilt_ba(b, a, x, padmode=padmode, padlen=padlen)
+        for r in range(B):
+            br, ar = (b[r], a[r]) if batched else (b, a)
+            pl = (3 * ntaps if padlen is None else padlen) if padtype else None
+            ref = scipy.signal.filtfilt(br, np.r_[1.0, ar], x[r], padtype=padtype, padlen=pl)
+            D.check(y[r], ref, f"order {order} {padmode} {padlen} row {r}")
+    for padmode, np_mode in (("constant", "constant"), ("circular", "wrap")):
+        for padlen in (7, T - 1):
+            y = oracle.filtfilt_ba(b, a, x, padmode=padmode, padlen=padlen)
+            for r in range(B):
+                br, ar = (b[r], a[r]) if batched else (b, a)
+                ref = _scipy_filtfilt_composed(br, ar, x[r], np_mode, padlen)
+                D.check(y[r], ref, f"order {order} {padmode} {padlen} row {r}")
+
+
+def test_filtfilt_ba_agrees_with_biquad_oracle_and_steady_state():
+    """filtfilt_ba of a biquad is oracle.filtfilt of its section (the cascade
+    route); lfilter_zi_ba is the fixed point of one TDF-II step at every
+    order; a constant row comes out scaled by H(1)^2."""
+    g = D.rng(D.seed_of("oracle-filtfilt-ba-x"))
+    sos = D.sos_coefs(g, (3,), 1, np.float64)[:, 0, :]
+    x = g.standard_normal((3, 300))
+    for padmode in ("replicate", "reflect", "constant", "circular", None):
+        D.check(oracle.filtfilt_ba(sos[:, :3], sos[:, 4:], x, padmode=padmode),
+                oracle.filtfilt(sos, x, padmode=padmode), f"biquad {padmode}")
+    for order in (1, 2, 3, 4):
+        b, a = D.ba_coefs(g, (4,), order, np.float64)
+        A, gv, _ = oracle._tdf2_companion(b, a)
+        zi = oracle.lfilter_zi_ba(b, a)
+        np.testing.assert_allclose(np.einsum("rij,rj->ri", A, zi) + gv, zi, rtol=1e-12, atol=1e-12)
+        h1 = b.sum(-1) / (1 + a.sum(-1))
+        for padmode in ("replicate", "reflect", "circular"):
+            y = oracle.filtfilt_ba(b, a, np.full((4, 200), -1.5), padmode=padmode)
+            np.testing.assert_allclose(y, np.broadcast_to((h1 * h1 * -1.5)[:, None], (4, 200)), rtol=1e-10)
+
+
 # ---------------------------------------------------------------- SISO state space
 def _stable_model(g, M, lead=()):
     """A dense A with a stable spectrum (a companion matrix of poles of radius
