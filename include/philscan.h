@@ -273,6 +273,15 @@ int phs_lti_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
                    const void *c, int c_shared, int out_idx, const void *d, int d_shared, const void *zi,
                    const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream);
 
+/* The same model run backwards in time (no counterpart in the reference,
+ * which flips: it equals flipping x, running phs_lti_ss_fwd and flipping y):
+ * h[T] = zi, y[t] = c . h[t+1] + d x[t], h[t] = A h[t+1] + b x[t],
+ * zf = h[0].  The adjoint of the forward model is this one on (A^T, c, b, d)
+ * from dL/dzf, so a gradient pass needs no flipped copies. */
+int phs_lti_ss_rev(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b, int b_shared,
+                   const void *c, int c_shared, int out_idx, const void *d, int d_shared, const void *zi,
+                   const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- lfilter of order M = max(nb - 1, na) = 1..4 in one pass (forward).
  * Replaces philtorch.lti.lfilter (philtorch/lti/filtering.py:211-333) in
  * the companion-form state space it builds (_ssm_lfilter :273-333) for forms
@@ -287,6 +296,13 @@ int phs_lti_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
 enum phs_form { PHS_FORM_TDF2 = 0, PHS_FORM_DF2 = 1 };
 
 int phs_lfilter_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na, int coef_shared,
+                    int form, const void *zi, const void *x, void *y, void *zf, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+/* The same filter run backwards in time, as phs_lti_ss_rev (flip, filter,
+ * flip without the copies; zi the state before x[T-1], zf the state after
+ * x[0]).  The adjoint of a companion form is the other form run this way. */
+int phs_lfilter_rev(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na, int coef_shared,
                     int form, const void *zi, const void *x, void *y, void *zf, void *workspace,
                     size_t workspace_bytes, void *stream);
 

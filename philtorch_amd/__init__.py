@@ -338,20 +338,22 @@ if EXTENSION_LOADED and _has_op("filtfilt"):
 if EXTENSION_LOADED and _has_op("lti_ss"):
     # single-input single-output LTI state space of order <= 4: (y, zf)
     @torch.library.register_fake("philtorch::lti_ss")
-    def _(A, B, C, D, zi, x, out_idx):
+    def _(A, B, C, D, zi, x, out_idx, reverse=False):
         torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
         torch._check(A.ndim in (2, 3) and A.shape[-1] == A.shape[-2], lambda: "A must be (M, M) or (batch, M, M)")
         return _fake_like(x), x.new_empty((x.shape[0], A.shape[-1]))
 
     def _lti_ss_setup(ctx, inputs, output):
-        A, B, C, D, zi, x, out_idx = inputs
+        A, B, C, D, zi, x, out_idx = inputs[:7]
         ctx.out_idx = out_idx
+        ctx.reverse = bool(inputs[7]) if len(inputs) > 7 else False
         ctx.save_for_backward(A, B, C, D, zi, x)
 
     def _lti_ss_backward(ctx, gy, gzf):
         """With A, B, C, D constant: the adjoint model (A^T, input vector C,
-        output vector B, D) run backwards in time from dL/dzf gives grad_x
-        and grad_zi in one more lti_ss pass over the reversed grad_y.
+        output vector B, D) run in the opposite time direction from dL/dzf
+        gives grad_x and grad_zi in one more lti_ss pass (the reversed mode
+        for a forward call and the other way round: no flipped copies).
         Otherwise the gradient of the composite the fused kernel replaces
         (B x, the native scan, the state shift, C h + D x;
         philtorch/lti/ssm.py:386-589), recomputed from the inputs.  Both are
@@ -365,20 +367,24 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
             M = A.size(-1)
             unit = lambda i: torch.nn.functional.one_hot(torch.tensor(i, device=x.device), M).to(x.dtype)  # noqa: E731
             g = gy if gy is not None else torch.zeros_like(x)
-            gxr, gzi = torch.ops.philtorch.lti_ss(A.mT.contiguous(), C if C is not None else unit(ctx.out_idx),
-                                                  B if B is not None else unit(0), D, gzf, g.flip(-1), 0)
+            gx, gzi = torch.ops.philtorch.lti_ss(A.mT.contiguous(), C if C is not None else unit(ctx.out_idx),
+                                                 B if B is not None else unit(0), D, gzf, g, 0, not ctx.reverse)
             return (None, None, None, None, gzi if zi is not None and needs[4] else None,
-                    gxr.flip(-1) if needs[5] else None, None)
+                    gx if needs[5] else None, None, None)
         wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
         with torch.enable_grad():
-            y, zf = _state_space_composite(*inputs, out_idx=ctx.out_idx)
+            if ctx.reverse:
+                y, zf = _state_space_composite(A, B, C, D, zi, x.flip(-1), out_idx=ctx.out_idx)
+                y = y.flip(-1)
+            else:
+                y, zf = _state_space_composite(*inputs, out_idx=ctx.out_idx)
             outs, grads = [y], [gy if gy is not None else torch.zeros_like(y)]
             if gzf is not None:
                 outs.append(zf)
                 grads.append(gzf)
             res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=torch.is_grad_enabled(),
                                       allow_unused=True)
-        out = [None] * 7
+        out = [None] * 8
         for i, g in zip(wrt, res):
             out[i] = g if g is not None else torch.zeros_like(inputs[i])
         return tuple(out)
@@ -388,23 +394,25 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
 if EXTENSION_LOADED and _has_op("lfilter_ss"):
     # lfilter of order <= 4 from b and a in one pass: (y, zf)
     @torch.library.register_fake("philtorch::lfilter_ss")
-    def _(b, a, zi, x, form):
+    def _(b, a, zi, x, form, reverse=False):
         torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
         M = max(b.shape[-1] - 1, a.shape[-1])
         torch._check(1 <= M <= 4, lambda: "filters of order 1 to 4")
         return _fake_like(x), x.new_empty((x.shape[0], M))
 
     def _lfilter_ss_setup(ctx, inputs, output):
-        b, a, zi, x, form = inputs
+        b, a, zi, x, form = inputs[:5]
         ctx.form = form
+        ctx.reverse = bool(inputs[5]) if len(inputs) > 5 else False
         ctx.save_for_backward(b, a, zi, x)
 
     def _lfilter_ss_backward(ctx, gy, gzf):
         """With b and a constant: the adjoint of a companion-form filter is
-        the other companion form of the same filter run backwards in time
-        (TDF-II <-> DF-II: A^T, with the input and output vectors swapped),
-        from dL/dzf, so grad_x and grad_zi are one more lfilter_ss pass over
-        the reversed grad_y.  Otherwise the gradient of the companion-form
+        the other companion form of the same filter run in the opposite time
+        direction (TDF-II <-> DF-II: A^T, with the input and output vectors
+        swapped), from dL/dzf, so grad_x and grad_zi are one more lfilter_ss
+        pass (the reversed mode for a forward call and the other way round:
+        no flipped copies).  Otherwise the gradient of the companion-form
         route the kernel replaces (philtorch/lti/filtering.py:273-333),
         recomputed from the inputs."""
         from .lti.filtering import _ssm_lfilter
@@ -413,20 +421,22 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
         needs = ctx.needs_input_grad
         if not (needs[0] or needs[1]):
             g = gy if gy is not None else torch.zeros_like(x)
-            gxr, gzi = torch.ops.philtorch.lfilter_ss(b, a, gzf, g.flip(-1), 1 - ctx.form)
-            return (None, None, gzi if zi is not None and needs[2] else None, gxr.flip(-1) if needs[3] else None,
-                    None)
+            gx, gzi = torch.ops.philtorch.lfilter_ss(b, a, gzf, g, 1 - ctx.form, not ctx.reverse)
+            return (None, None, gzi if zi is not None and needs[2] else None, gx if needs[3] else None, None, None)
         wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
         with torch.enable_grad():
             z = zi if zi is not None else x.new_zeros(x.size(0), max(b.size(-1) - 1, a.size(-1)))
-            y, zf = _ssm_lfilter(b, a, x, z, form=("tdf2", "df2")[ctx.form], unroll_factor=1)
+            xs = x.flip(-1) if ctx.reverse else x
+            y, zf = _ssm_lfilter(b, a, xs, z, form=("tdf2", "df2")[ctx.form], unroll_factor=1)
+            if ctx.reverse:
+                y = y.flip(-1)
             outs, grads = [y], [gy if gy is not None else torch.zeros_like(y)]
             if gzf is not None:
                 outs.append(zf)
                 grads.append(gzf)
             res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=torch.is_grad_enabled(),
                                       allow_unused=True)
-        out = [None] * 5
+        out = [None] * 6
         for i, g in zip(wrt, res):
             out[i] = g if g is not None else torch.zeros_like(inputs[i])
         return tuple(out)

@@ -76,7 +76,7 @@ bool ss_filter_ok(const SsFilter &f, int M) {
 template <class Alg>
 int ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, const void *bv, bool b_sh, const void *cv, bool c_sh,
            int out_idx, const void *d, bool d_sh, const SsFilter &f, const void *zi, const void *x, void *y, void *zf,
-           void *workspace, size_t ws_bytes, hipStream_t stream) {
+           void *workspace, size_t ws_bytes, bool rev, hipStream_t stream) {
   using E = typename Alg::elem;
   constexpr int M = SsView<Alg>::M;
   if (B < 0 || T < 0) return PHS_ERR_INVALID;
@@ -96,7 +96,7 @@ int ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, const void *bv, bool 
   a.d = static_cast<const E *>(d);
   a.d_stride = d_sh ? 0 : 1;
   a.out_idx = out_idx;
-  return ss_launch<Alg, false>(a, stream);
+  return rev ? ss_launch<Alg, true>(a, stream) : ss_launch<Alg, false>(a, stream);
 }
 
 // filtfilt's scratch buffer ("mid"): pass 1's output [B, T] and final state
@@ -173,19 +173,22 @@ size_t phs_lti_ss_workspace_size(int dtype, int M, int64_t B, int64_t T) {
   return rc == PHS_OK ? out : 0;
 }
 
-int phs_lti_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b, int b_shared,
-                   const void *c, int c_shared, int out_idx, const void *d, int d_shared, const void *zi,
-                   const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream) {
+namespace {
+
+int lti_ss_call(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b, int b_shared,
+                const void *c, int c_shared, int out_idx, const void *d, int d_shared, const void *zi, const void *x,
+                void *y, void *zf, void *workspace, size_t workspace_bytes, bool rev, void *stream) {
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return phs::ss_dispatch(dtype, M, [&](auto alg) {
     return phs::ss_fwd<decltype(alg)>(B, T, A, A_shared != 0, b, b_shared != 0, c, c_shared != 0, out_idx, d,
-                                      d_shared != 0, phs::SsFilter{}, zi, x, y, zf, workspace, workspace_bytes, st);
+                                      d_shared != 0, phs::SsFilter{}, zi, x, y, zf, workspace, workspace_bytes, rev,
+                                      st);
   });
 }
 
-int phs_lfilter_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na, int coef_shared,
-                    int form, const void *zi, const void *x, void *y, void *zf, void *workspace,
-                    size_t workspace_bytes, void *stream) {
+int lfilter_call(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na, int coef_shared,
+                 int form, const void *zi, const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes,
+                 bool rev, void *stream) {
   if (form != PHS_FORM_TDF2 && form != PHS_FORM_DF2) return PHS_ERR_INVALID;
   const int M = nb - 1 > na ? nb - 1 : na;
   if (M < 1 || M > 4) return PHS_ERR_INVALID;
@@ -199,8 +202,38 @@ int phs_lfilter_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, cons
   f.shared = coef_shared != 0;
   return phs::ss_dispatch(dtype, M, [&](auto alg) {
     return phs::ss_fwd<decltype(alg)>(B, T, nullptr, false, nullptr, false, nullptr, false, 0, nullptr, false, f, zi,
-                                      x, y, zf, workspace, workspace_bytes, st);
+                                      x, y, zf, workspace, workspace_bytes, rev, st);
   });
+}
+
+}  // namespace
+
+int phs_lti_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b, int b_shared,
+                   const void *c, int c_shared, int out_idx, const void *d, int d_shared, const void *zi,
+                   const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream) {
+  return lti_ss_call(dtype, M, B, T, A, A_shared, b, b_shared, c, c_shared, out_idx, d, d_shared, zi, x, y, zf,
+                     workspace, workspace_bytes, false, stream);
+}
+
+int phs_lti_ss_rev(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b, int b_shared,
+                   const void *c, int c_shared, int out_idx, const void *d, int d_shared, const void *zi,
+                   const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream) {
+  return lti_ss_call(dtype, M, B, T, A, A_shared, b, b_shared, c, c_shared, out_idx, d, d_shared, zi, x, y, zf,
+                     workspace, workspace_bytes, true, stream);
+}
+
+int phs_lfilter_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na, int coef_shared,
+                    int form, const void *zi, const void *x, void *y, void *zf, void *workspace,
+                    size_t workspace_bytes, void *stream) {
+  return lfilter_call(dtype, B, T, b, nb, a, na, coef_shared, form, zi, x, y, zf, workspace, workspace_bytes, false,
+                      stream);
+}
+
+int phs_lfilter_rev(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na, int coef_shared,
+                    int form, const void *zi, const void *x, void *y, void *zf, void *workspace,
+                    size_t workspace_bytes, void *stream) {
+  return lfilter_call(dtype, B, T, b, nb, a, na, coef_shared, form, zi, x, y, zf, workspace, workspace_bytes, true,
+                      stream);
 }
 
 size_t phs_filtfilt_workspace_size(int dtype, int64_t B, int64_t T) {

@@ -511,10 +511,11 @@ Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t p
 // (phs_lti_ss_fwd; philtorch/lti/ssm.py:386-589 for a 2D x): returns (y, zf).
 // A (M, M) or (batch, M, M); B, C None, (M,) or (batch, M); D None, one value
 // or (batch,); zi None or (batch, M); out_idx selects the output state when
-// C is None.
+// C is None; reverse runs the model backwards in time (phs_lti_ss_rev).
 std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
                                       const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
-                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx) {
+                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
+                                      bool reverse) {
   TORCH_CHECK(x.dim() == 2, "philtorch::lti_ss: x must be a 2D tensor (batch, time)");
   TORCH_CHECK((A.dim() == 2 || A.dim() == 3) && A.size(-1) == A.size(-2),
               "philtorch::lti_ss: A must be (M, M) or (batch, M, M)");
@@ -563,7 +564,7 @@ std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tenso
   }
   void *stream = stream_of(x);
   const Workspace ws = workspace_for(x, phs_lti_ss_workspace_size(dt, int(M), B, T), stream);
-  check_status(phs_lti_ss_fwd(dt, int(M), B, T, Ac.const_data_ptr(), A.dim() == 2 ? 1 : 0,
+  check_status((reverse ? phs_lti_ss_rev : phs_lti_ss_fwd)(dt, int(M), B, T, Ac.const_data_ptr(), A.dim() == 2 ? 1 : 0,
                               Bm ? bc.const_data_ptr() : nullptr, Bm && Bm->dim() == 1 ? 1 : 0,
                               Cm ? cc.const_data_ptr() : nullptr, Cm && Cm->dim() == 1 ? 1 : 0, int(out_idx),
                               Dm ? dc.const_data_ptr() : nullptr, Dm && Dm->numel() == 1 ? 1 : 0,
@@ -577,9 +578,10 @@ std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tenso
 // philtorch/lti/filtering.py:211-333 in its companion-form state space):
 // returns (y, zf).  b (nb,) or (batch, nb); a (na,) or (batch, na), the
 // denominator after its leading 1; form 0 "tdf2", 1 "df2"; zi None or
-// (batch, max(nb - 1, na)).
+// (batch, max(nb - 1, na)); reverse runs the filter backwards in time
+// (phs_lfilter_rev).
 std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, const std::optional<Tensor> &zi,
-                                          const Tensor &x, int64_t form) {
+                                          const Tensor &x, int64_t form, bool reverse) {
   TORCH_CHECK(x.dim() == 2, "philtorch::lfilter_ss: x must be a 2D tensor (batch, time)");
   TORCH_CHECK(b.dim() == a.dim() && (b.dim() == 1 || b.dim() == 2),
               "philtorch::lfilter_ss: b and a must both be 1D (shared) or both 2D (batch, taps)");
@@ -612,7 +614,7 @@ std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, cons
   }
   void *stream = stream_of(x);
   const Workspace ws = workspace_for(x, phs_lti_ss_workspace_size(dt, int(M), B, T), stream);
-  check_status(phs_lfilter_fwd(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
+  check_status((reverse ? phs_lfilter_rev : phs_lfilter_fwd)(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
                                b.dim() == 1 ? 1 : 0, int(form), zi ? zc.const_data_ptr() : nullptr,
                                xc.const_data_ptr(), y.mutable_data_ptr(), zf.mutable_data_ptr(), ws.ptr, ws.bytes,
                                stream),
@@ -649,10 +651,10 @@ TORCH_LIBRARY(philtorch, m) {
   // new: zero-phase filtering, filters of second order at most (forward only)
   m.def("filtfilt(Tensor b, Tensor a, Tensor x, int padmode, int padlen) -> Tensor", {at::Tag::pt2_compliant_tag});
   // new: single-input single-output LTI state space of order <= 4, fused: (y, zf)
-  m.def("lti_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx) -> (Tensor, Tensor)",
+  m.def("lti_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx, bool reverse=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
   // new: lfilter of order <= 4 from b and a (companion model built in the kernel): (y, zf)
-  m.def("lfilter_ss(Tensor b, Tensor a, Tensor? zi, Tensor x, int form) -> (Tensor, Tensor)",
+  m.def("lfilter_ss(Tensor b, Tensor a, Tensor? zi, Tensor x, int form, bool reverse=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
 }
 

@@ -99,4 +99,7 @@ def load() -> ctypes.CDLL:
                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                     ctypes.c_size_t, ctypes.c_void_p]
     lib.phs_lfilter_fwd.restype = ctypes.c_int
+    for rev, fwd in (("phs_lti_ss_rev", "phs_lti_ss_fwd"), ("phs_lfilter_rev", "phs_lfilter_fwd")):
+        getattr(lib, rev).argtypes = getattr(lib, fwd).argtypes
+        getattr(lib, rev).restype = ctypes.c_int
     return lib

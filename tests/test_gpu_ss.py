@@ -60,8 +60,8 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def _run(api, A, b, c, d, zi, x, out_idx=0, want_zf=True):
-    """phs_lti_ss_fwd through the C ABI; numpy (y, zf)."""
+def _run(api, A, b, c, d, zi, x, out_idx=0, want_zf=True, rev=False):
+    """phs_lti_ss_fwd (phs_lti_ss_rev) through the C ABI; numpy (y, zf)."""
     import torch
 
     lib, ws, capi = api
@@ -74,9 +74,10 @@ def _run(api, A, b, c, d, zi, x, out_idx=0, want_zf=True):
     y = torch.full_like(tx, float("nan"))
     zf = torch.full((Bn, M), float("nan"), dtype=tx.dtype, device="cuda") if want_zf else None
     sh = lambda v, nd: int(v is not None and np.ndim(v) == nd)  # noqa: E731
-    rc = lib.phs_lti_ss_fwd(dt, M, Bn, T, _p(tA), sh(A, 2), _p(tb), sh(b, 1), _p(tc), sh(c, 1), out_idx, _p(td),
-                            int(d is not None and np.size(d) == 1), _p(tz), _p(tx), _p(y), _p(zf), _p(ws), need,
-                            _stream())
+    fn = lib.phs_lti_ss_rev if rev else lib.phs_lti_ss_fwd
+    print(f"lti_ss capi M={M} B={Bn} T={T} rev={rev}", flush=True)
+    rc = fn(dt, M, Bn, T, _p(tA), sh(A, 2), _p(tb), sh(b, 1), _p(tc), sh(c, 1), out_idx, _p(td),
+            int(d is not None and np.size(d) == 1), _p(tz), _p(tx), _p(y), _p(zf), _p(ws), need, _stream())
     assert rc == capi.PHS_OK, lib.phs_error_string(rc)
     torch.cuda.synchronize()
     return y.cpu().numpy(), None if zf is None else zf.cpu().numpy()
@@ -91,10 +92,14 @@ def _case(dtype, M, Bn, T, shared, seed):
     return [cast(v) for v in (A, b, c, np.reshape(d, (1,)) if shared else d, zi, x)]
 
 
-def _check(got, A, b, c, d, zi, x, out_idx, dtype, name):
+def _check(got, A, b, c, d, zi, x, out_idx, dtype, name, rev=False):
+    """Against the oracle; rev: the model over the flipped row, flipped back."""
     y, zf = got
     w = lambda v: None if v is None else np.asarray(v, np.float64)  # noqa: E731
-    ry, rzf = oracle.lti_state_space(w(A), w(x), w(b), w(c), w(d), w(zi), out_idx=out_idx)
+    xs = np.ascontiguousarray(w(x)[:, ::-1]) if rev else w(x)
+    ry, rzf = oracle.lti_state_space(w(A), xs, w(b), w(c), w(d), w(zi), out_idx=out_idx)
+    if rev:
+        ry = np.ascontiguousarray(ry[:, ::-1])
     D.check(y, ry, f"{name} y", dtype=dtype)
     if zf is not None:
         D.check(zf, rzf, f"{name} zf", dtype=dtype, scale=np.max(np.abs(ry)) if ry.size else None)
@@ -112,6 +117,35 @@ def test_lti_ss_capi_parity(api, dtype, M, Bn, T):
         idx = M - 1
         _check(_run(api, A, None, None, None, None, x, out_idx=idx), A, None, None, None, None, x, idx, dtype,
                name + " e0/out_idx")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("M", ORDERS)
+@pytest.mark.parametrize("Bn,T", [(1, 1), (2, 17), (3, 3073), (2, 6144), (2, 6145), (2, 12289), (1, 30001)])
+def test_lti_ss_capi_reversed(api, dtype, M, Bn, T):
+    """phs_lti_ss_rev: the model run backwards in time (zi the state before
+    the last sample, zf after the first) is the forward model over the
+    flipped row, flipped back; odd lengths take the scalar loads."""
+    for shared in (False, True):
+        A, b, c, d, zi, x = _case(dtype, M, Bn, T, shared, D.seed_of("ss-rev", dtype, M, Bn, T, shared))
+        name = f"rev M={M} B={Bn} T={T} shared={shared}"
+        _check(_run(api, A, b, c, d, zi, x, rev=True), A, b, c, d, zi, x, None, dtype, name, rev=True)
+        idx = M - 1
+        _check(_run(api, A, None, None, None, None, x, out_idx=idx, rev=True), A, None, None, None, None, x, idx,
+               dtype, name + " e0/out_idx", rev=True)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("M", [2, 4])
+def test_lti_ss_capi_reversed_forced_fallback(api, dtype, M):
+    lib = api[0]
+    A, b, c, d, zi, x = _case(dtype, M, 3, 20000, False, D.seed_of("ss-rev-fallback", dtype, M))
+    lib.phs_debug_set_spin_limit(1)
+    try:
+        got = _run(api, A, b, c, d, zi, x, rev=True)
+    finally:
+        lib.phs_debug_set_spin_limit(0)
+    _check(got, A, b, c, d, zi, x, None, dtype, "rev fallback", rev=True)
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
@@ -291,7 +325,8 @@ def _companion_model(b, a, form):
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
 @pytest.mark.parametrize("nb,na", [(2, 1), (1, 2), (3, 1), (4, 3), (5, 4), (2, 4), (5, 2)])
 @pytest.mark.parametrize("form", ["tdf2", "df2"])
-def test_lfilter_capi_parity(api, dtype, nb, na, form):
+@pytest.mark.parametrize("rev", [False, True])
+def test_lfilter_capi_parity(api, dtype, nb, na, form, rev):
     """phs_lfilter_fwd (companion model built in the kernel from b and a,
     zero-padded to the order) against the oracle's state space of the
     companion model, shared and per row, at tile boundaries and beyond."""
@@ -312,14 +347,18 @@ def test_lfilter_capi_parity(api, dtype, nb, na, form):
         y = torch.full_like(tx, float("nan"))
         zf = torch.full((Bn, M), float("nan"), dtype=tx.dtype, device="cuda")
         need = lib.phs_lti_ss_workspace_size(dt, M, Bn, T)
-        rc = lib.phs_lfilter_fwd(dt, Bn, T, _p(tb), nb, _p(ta), na, int(shared), 0 if form == "tdf2" else 1, _p(tz),
-                                 _p(tx), _p(y), _p(zf), _p(ws), need, _stream())
+        fn = lib.phs_lfilter_rev if rev else lib.phs_lfilter_fwd
+        rc = fn(dt, Bn, T, _p(tb), nb, _p(ta), na, int(shared), 0 if form == "tdf2" else 1, _p(tz), _p(tx), _p(y),
+                _p(zf), _p(ws), need, _stream())
         assert rc == capi.PHS_OK, lib.phs_error_string(rc)
         torch.cuda.synchronize()
         A, Bv, Cv, Dv, idx = _companion_model(np.asarray(bb, np.float64), np.asarray(aa, np.float64), form)
-        ry, rzf = oracle.lti_state_space(A, np.asarray(x, np.float64), Bv, Cv, Dv, np.asarray(zi, np.float64),
-                                         out_idx=idx)
-        name = f"nb={nb} na={na} {form} B={Bn} T={T} shared={shared}"
+        xs = np.asarray(x, np.float64)
+        ry, rzf = oracle.lti_state_space(A, np.ascontiguousarray(xs[:, ::-1]) if rev else xs, Bv, Cv, Dv,
+                                         np.asarray(zi, np.float64), out_idx=idx)
+        if rev:
+            ry = np.ascontiguousarray(ry[:, ::-1])
+        name = f"nb={nb} na={na} {form} rev={rev} B={Bn} T={T} shared={shared}"
         D.check(y.cpu().numpy(), ry, name + " y", dtype=dtype)
         D.check(zf.cpu().numpy(), rzf, name + " zf", dtype=dtype, scale=np.max(np.abs(ry)))
 
@@ -416,4 +455,48 @@ def test_adjoint_passes_gradcheck(hip):
         f3 = lambda z_, x_: torch.ops.philtorch.lfilter_ss(bf, af, z_, x_, form)  # noqa: E731
         assert torch.autograd.gradcheck(f3, (z4, x))
         assert torch.autograd.gradgradcheck(f3, (z4, x))
+
+
+def test_reversed_ops_gradients_and_opcheck(hip):
+    """lti_ss and lfilter_ss with reverse=True: values are the forward op
+    over the flipped row, flipped back; gradients (the adjoint pass forward
+    in time, or the composite when a coefficient needs one) pass gradcheck
+    and gradgradcheck; opcheck's schema and fake-tensor checks."""
+    import torch
+
+    g = D.rng(D.seed_of("ss-rev-grad"))
+    Bn, T = 2, 25
+    A, b, c, d = _stable_model(g, 3, (Bn,))
+    t = lambda v, rg=False: torch.tensor(np.asarray(v, np.float64), device="cuda", requires_grad=rg)  # noqa: E731
+    x, zi = t(g.standard_normal((Bn, T)), True), t(g.standard_normal((Bn, 3)), True)
+    y, zf = torch.ops.philtorch.lti_ss(t(A), t(b), t(c), t(d), zi, x, 0, True)
+    yr, zfr = torch.ops.philtorch.lti_ss(t(A), t(b), t(c), t(d), zi, x.flip(-1), 0)
+    D.check(y.detach().cpu().numpy(), yr.flip(-1).detach().cpu().numpy(), "lti_ss reverse y")
+    D.check(zf.detach().cpu().numpy(), zfr.detach().cpu().numpy(), "lti_ss reverse zf")
+    f = lambda z_, x_: torch.ops.philtorch.lti_ss(t(A), t(b), t(c), t(d), z_, x_, 0, True)  # noqa: E731
+    assert torch.autograd.gradcheck(f, (zi, x))
+    assert torch.autograd.gradgradcheck(f, (zi, x))
+    Ag, bg = t(A, True), t(b, True)
+    fA = lambda A_, b_, x_: torch.ops.philtorch.lti_ss(A_, b_, t(c), t(d), None, x_, 0, True)[0]  # noqa: E731
+    assert torch.autograd.gradcheck(fA, (Ag, bg, x))
+    bf, af = (t(v) for v in _filter(g, 4, (Bn,)))
+    z4 = t(g.standard_normal((Bn, 4)), True)
+    for form in (0, 1):
+        y, zf = torch.ops.philtorch.lfilter_ss(bf, af, z4, x, form, True)
+        yr, zfr = torch.ops.philtorch.lfilter_ss(bf, af, z4, x.flip(-1), form)
+        D.check(y.detach().cpu().numpy(), yr.flip(-1).detach().cpu().numpy(), f"lfilter_ss reverse y {form}")
+        D.check(zf.detach().cpu().numpy(), zfr.detach().cpu().numpy(), f"lfilter_ss reverse zf {form}")
+        f3 = lambda z_, x_: torch.ops.philtorch.lfilter_ss(bf, af, z_, x_, form, True)  # noqa: E731
+        assert torch.autograd.gradcheck(f3, (z4, x))
+        assert torch.autograd.gradgradcheck(f3, (z4, x))
+        bg4, ag4 = t(bf.detach().cpu().numpy(), True), t(af.detach().cpu().numpy(), True)
+        f4 = lambda b_, a_, x_: torch.ops.philtorch.lfilter_ss(b_, a_, None, x_, form, True)[0]  # noqa: E731
+        assert torch.autograd.gradcheck(f4, (bg4, ag4, x))
+    s = lambda v: torch.tensor(np.asarray(v, np.float32), device="cuda")  # noqa: E731
+    bf, af = _filter(g, 4)
+    torch.library.opcheck(torch.ops.philtorch.lfilter_ss.default,
+                          (s(bf), s(af), None, s(g.standard_normal((2, 500))), 0, True))
+    torch.library.opcheck(torch.ops.philtorch.lti_ss.default,
+                          (s(A[0]), s(b[0]), None, None, s(g.standard_normal((2, 3))), s(g.standard_normal((2, 500))),
+                           1, True))
 
