@@ -297,6 +297,36 @@ def filtfilt(sos, x, padmode="replicate", padlen=None, nthreads=None):
 
 
 
+def lpv_state_space(A, x, B=None, C=None, D=None, zi=None, out_idx=None, nthreads=None):
+    """philtorch.lpv.state_space for a 2D input and a single output
+    (philtorch/lpv/ssm.py:337-581) on operands broadcast to per row and
+    step: A [T,M,M] or [B,T,M,M]; B, C [1|B, 1|T, M] (B None: the input
+    enters state 0; C None: state out_idx); D [1|B, 1|T] or None.  B x, the
+    LPV scan recurN, the state sequence shifted by one step behind zi, then
+    y = c[t] . h + d[t] x.  Returns (y [B,T], zf [B,M])."""
+    dt = np.asarray(x).dtype
+    x = _c(x, dt)
+    Bn, T = x.shape
+    M = np.shape(A)[-1]
+    A = _c(np.broadcast_to(A, (Bn, T, M, M)), dt)
+    zi = np.zeros((Bn, M), dtype=dt) if zi is None else _c(np.broadcast_to(zi, (Bn, M)), dt)
+    if B is None:
+        Bx = np.zeros((Bn, T, M), dtype=dt)
+        Bx[..., 0] = x
+    else:
+        Bx = x[..., None] * np.broadcast_to(np.asarray(B, dtype=dt), (Bn, T, M))
+    h = recurN(A, zi, _c(Bx, dt), nthreads)
+    zf = h[:, -1] if T > 0 else zi.copy()
+    hprev = np.concatenate([zi[:, None, :], h[:, :-1]], axis=1)
+    if C is None:
+        y = hprev[..., out_idx].copy()
+    else:
+        y = np.einsum("btm,btm->bt", hprev, np.broadcast_to(np.asarray(C, dtype=dt), (Bn, T, M)))
+    if D is not None:
+        y = y + np.broadcast_to(np.asarray(D, dtype=dt), (Bn, T)) * x
+    return _c(y, dt), _c(zf, dt)
+
+
 def _tdf2_companion(b, a):
     """TDF-II model of lfilter(b, a) per row (philtorch/lti/filtering.py:
     107-142 and :273-333, transpose=True): b [R,nb], a [R,na] (after the

@@ -9,8 +9,10 @@ second-order sections ``sosfilt`` / ``sosfilt_backward`` (no reference
 counterpart; ``lti.sosfilt`` is its API), the forward-only zero-phase
 ``filtfilt`` of filters up to order 4 (behind ``lti.filtfilt``) and the
 fused single-input single-output state space ``lti_ss`` (behind
-``lti.state_space``) and ``lfilter_ss``, ``lfilter`` of order <= 4 from b and
-a in one pass (behind ``lti.lfilter``).  This module then
+``lti.state_space``), ``lfilter_ss``, ``lfilter`` of order <= 4 from b and
+a in one pass (behind ``lti.lfilter``), and ``lpv_ss``, the time-varying
+single-input single-output state space of order <= 2 (behind
+``lpv.state_space``).  This module then
 registers fake (meta) kernels and autograd formulas for them, as
 philtorch/__init__.py:157-268 does for its ops.
 
@@ -442,6 +444,46 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
         return tuple(out)
 
     torch.library.register_autograd("philtorch::lfilter_ss", _lfilter_ss_backward, setup_context=_lfilter_ss_setup)
+
+if EXTENSION_LOADED and _has_op("lpv_ss"):
+    # single-input single-output LPV state space of order <= 2: (y, zf)
+    @torch.library.register_fake("philtorch::lpv_ss")
+    def _(A, B, C, D, zi, x, out_idx):
+        torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
+        torch._check(A.ndim in (3, 4) and A.shape[-1] == A.shape[-2], lambda: "A must be (T, M, M) or (batch, T, M, M)")
+        return _fake_like(x), x.new_empty((x.shape[0], A.shape[-1]))
+
+    def _lpv_ss_setup(ctx, inputs, output):
+        A, B, C, D, zi, x, out_idx = inputs
+        ctx.out_idx = out_idx
+        ctx.save_for_backward(A, B, C, D, zi, x)
+
+    def _lpv_ss_backward(ctx, gy, gzf):
+        """The gradient of the composite the fused kernel replaces (B x, the
+        native LPV scan, the state shift, C h + D x; philtorch/lpv/ssm.py:
+        337-581), recomputed from the inputs; differentiable again under
+        create_graph."""
+        from .lpv.ssm import _lpv_state_space_composite
+
+        inputs = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
+        out = [None] * 7
+        if not wrt:
+            return tuple(out)
+        with torch.enable_grad():
+            y, zf = _lpv_state_space_composite(*inputs, out_idx=ctx.out_idx)
+            outs, grads = [y], [gy if gy is not None else torch.zeros_like(y)]
+            if gzf is not None:
+                outs.append(zf)
+                grads.append(gzf)
+            res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=torch.is_grad_enabled(),
+                                      allow_unused=True)
+        for i, g in zip(wrt, res):
+            out[i] = g if g is not None else torch.zeros_like(inputs[i])
+        return tuple(out)
+
+    torch.library.register_autograd("philtorch::lpv_ss", _lpv_ss_backward, setup_context=_lpv_ss_setup)
 
 from . import mat  # noqa: E402,F401
 from . import lti  # noqa: E402,F401

@@ -69,6 +69,7 @@ KERNEL_UNITS = (
     ("phs_blockn.hip", ["-DPHS_BLOCKN_ORDER=4"], "phs_blockn4.o"),
     ("phs_sos.hip", [], "phs_sos.o"),
     ("phs_ss.hip", [], "phs_ss.o"),
+    ("phs_lpvss.hip", [], "phs_lpvss.o"),
 )
 
 

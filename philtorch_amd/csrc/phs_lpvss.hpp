@@ -1,0 +1,257 @@
+// Fused single-input, single-output LPV (time-varying) state space of order
+// M <= 2 in one pass (philtorch/lpv/ssm.py:337-581: state_space with a 2D
+// input, B an M-vector per row and/or per step or absent, C an M-vector per
+// row and/or per step or out_idx, D per row and/or per step or absent; the
+// glue of lpv/ssm.py:413-577 folded into the scan):
+//     h[0] = zi,  y[t] = c[t] . h[t] + d[t] x[t],  h[t+1] = A[t] h[t] + b[t] x[t],
+//     zf = h[T]
+// Per step the kernel reads A[t], x[t] and whichever of b[t], c[t], d[t] vary
+// along time, and writes y[t]; the reference route writes and reads B x, the
+// state sequence, its shifted copy, C h and D x.
+//
+// The scan is the generic one (phs_scan.hpp) in its time-varying mode: a lane
+// folds its K steps (A[t], b[t] x[t]) into a map, wave scans chain the lanes,
+// a look-back wave resolves the tile's entry state over the row's status
+// words, and pass 2 re-runs the steps from each lane's entry state, writing
+// c[t] . h + d[t] x[t] instead of h.  Forward only: the gradients are those of
+// the composite route, recomputed from the inputs.
+#pragma once
+
+#include "phs_ss.hpp"
+
+namespace phs {
+
+// A per-row and/or per-step operand: element (row, t, i) at
+// p + row * row_stride + t * t_stride + i (a stride 0 shares that axis).
+template <typename E>
+struct LpvOperand {
+  const E *p;
+  int64_t row_stride, t_stride;
+};
+
+template <class Alg>
+struct LpvSsArgs {
+  using E = typename Alg::elem;
+  const E *A;            // [rows, T, M, M]
+  int64_t A_row_stride;  // elements between rows (0 = shared)
+  LpvOperand<E> bv;      // [., ., M]; p nullptr: the input enters state 0
+  LpvOperand<E> cv;      // [., ., M]; p nullptr: y is state out_idx
+  LpvOperand<E> d;       // [., .]; p nullptr: no feedthrough
+  int out_idx;
+  const E *zi;  // [B, M]; nullptr: zeros
+  const E *x;   // [B, T]
+  E *y;         // [B, T]
+  E *zf;        // [B, M]; nullable
+  int64_t B, T_len, tiles_per_row;
+  unsigned long long *claims;
+  unsigned tiles, per_stripe, spin_limit;
+  uint64_t *status;
+  int vec_ok;
+};
+
+// 3 data waves and a look-back wave; the time-varying scan's steps per lane
+// and rounds (Shape<Alg, true>).
+template <class Alg>
+struct LpvSsShape {
+  static constexpr int kWaves = 3;
+  static constexpr int kThreads = 64 * (kWaves + 1);
+  static constexpr int K = Shape<Alg, true>::K;
+  static constexpr int R = Shape<Alg, true>::R;
+  static constexpr int kTile = kWaves * 64 * K * R;
+};
+
+// K scalars from row[t0..t0+K) (zeros past T): 16-byte loads where the chunk
+// is a whole number of them.
+template <typename E, int K>
+__device__ __forceinline__ void lpv_load_elems(const E *row, int64_t t0, int64_t T, bool vec, E (&out)[K]) {
+  if constexpr ((K * sizeof(E)) % 16 == 0) {
+    load_chunk<E, K>(row, t0, T, vec, out, E(0));
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (t0 + k < T)
+        out[k] = row[t0 + k];
+      else
+        out[k] = E(0);
+    }
+  }
+}
+
+template <typename E, int K>
+__device__ __forceinline__ void lpv_store_elems(E *row, int64_t t0, int64_t T, bool vec, const E (&v)[K]) {
+  if constexpr ((K * sizeof(E)) % 16 == 0) {
+    store_chunk<E, K>(row, t0, T, vec, v);
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (t0 + k < T) row[t0 + k] = v[k];
+  }
+}
+
+// b[t] x[t] for the K steps from t0 (b absent: x[t] into state 0).
+template <class Alg, int K>
+__device__ __forceinline__ void lpv_inputs(const LpvSsArgs<Alg> &a, int64_t b, int64_t t0, const typename Alg::elem (&u)[K],
+                                           typename Alg::s_state (&X)[K]) {
+  using V = SsView<Alg>;
+  using E = typename Alg::elem;
+  const E *bp = a.bv.p ? a.bv.p + b * a.bv.row_stride : nullptr;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int64_t t = t0 + k < a.T_len ? t0 + k : a.T_len - 1;  // past the row: u is 0
+    X[k] = V::scale(bp ? V::load_vec(bp + t * a.bv.t_stride) : V::unit(0), u[k]);
+  }
+}
+
+// State entering tile position `span` of a row, folded from the inputs (the
+// look-back's bounded-wait fallback; out of line, cold).
+template <class Alg>
+__device__ __noinline__ typename Alg::state lpv_prefix_fallback(LpvSsArgs<Alg> a, int64_t b, int64_t span, int lane,
+                                                               typename Alg::state virt) {
+  using E = typename Alg::elem;
+  using SC = typename Alg::s_coef;
+  using SS = typename Alg::s_state;
+  using M = Map<Alg>;
+  constexpr int K = LpvSsShape<Alg>::K;
+  auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
+  const SC *crow = reinterpret_cast<const SC *>(a.A + b * a.A_row_stride);
+  const E *xrow = a.x + b * a.T_len;
+  const SC dummy = Alg::s_czero();
+  M acc = map_identity<Alg>();
+  for (int64_t off = 0; off < span; off += 64 * K) {
+    const int64_t c0 = off + int64_t(lane) * K;
+    E u[K];
+    SS xs[K];
+    SC cs[K];
+    lpv_load_elems<E, K>(xrow, c0, a.T_len, a.vec_ok != 0, u);
+    load_chunk<SC, K>(crow, c0, a.T_len, a.vec_ok != 0, cs, Alg::s_czero());
+    lpv_inputs<Alg, K>(a, b, c0, u, xs);
+    M m = lane_map<Alg, true, false, K>(cs, xs, dummy);
+    m = wave_scan_incl(m, lane, op);
+    acc = compose<Alg>(acc, read_lane(m, 63));
+  }
+  return apply<Alg>(acc, virt);
+}
+
+template <class Alg>
+__global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(LpvSsArgs<Alg> a) {
+  using E = typename Alg::elem;
+  using S = typename Alg::state;
+  using SC = typename Alg::s_coef;
+  using SS = typename Alg::s_state;
+  using M = Map<Alg>;
+  using V = SsView<Alg>;
+  using Sh = LpvSsShape<Alg>;
+  using St = StatusShape<Alg>;
+  constexpr int K = Sh::K, R = Sh::R, kWaves = Sh::kWaves;
+
+  __shared__ M s_wagg[kWaves];
+  __shared__ M s_wpre[kWaves];
+  __shared__ S s_in;
+  __shared__ unsigned s_id, s_tag;
+  __shared__ uint64_t s_look[St::kLookWords];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
+  __syncthreads();
+  if (s_id >= a.tiles) return;  // padding of the last stripe round
+  const int64_t id = s_id;
+  const unsigned tag = s_tag;
+  const int64_t q = id / a.B;  // tile position along the row
+  const int64_t b = id - q * a.B;
+  const int64_t T = a.T_len;
+  const bool vec = a.vec_ok != 0;
+  auto op = [](const M &p, const M &q2) { return compose<Alg>(p, q2); };
+
+  if (w == kWaves) {
+    // ================= look-back wave
+    uint64_t *row_status = a.status + b * a.tiles_per_row * St::kStride;
+    const S virt = a.zi ? Alg::load_s(V::load_vec(a.zi + b * V::M)) : Alg::szero();
+    __syncthreads();  // wave aggregates are in s_wagg
+    M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
+    v = wave_scan_incl(v, lane, op);
+    const M wex = wave_shift_up(v, lane, map_identity<Alg>());
+    if (lane < kWaves) s_wpre[lane] = wex;
+    const M tagg = read_lane(v, kWaves - 1);
+    S yin = virt;
+    if (q > 0) {
+      if (lane == 0) publish(row_status + q * St::kStride + St::kIncWords, tagg, tag);
+      Lookback<Alg> lb = lookback_start<Alg>(q);
+      if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
+        yin = lpv_prefix_fallback<Alg>(a, b, q * Sh::kTile, lane, virt);
+    }
+    if (q + 1 < a.tiles_per_row && lane == 0) publish(row_status + q * St::kStride, apply<Alg>(tagg, yin), tag);
+    if (lane == 0) s_in = yin;
+    __syncthreads();  // entry state is in s_in
+    return;
+  }
+
+  // ================= data waves
+  const SC *crow = reinterpret_cast<const SC *>(a.A + b * a.A_row_stride);
+  const E *xrow = a.x + b * T;
+  const int64_t seg0 = q * Sh::kTile + int64_t(w) * 64 * K * R;
+  auto chunk0 = [&](int r) -> int64_t { return seg0 + int64_t(r) * 64 * K + int64_t(lane) * K; };
+  const SC dummy = Alg::s_czero();
+  E U[R][K];
+  SC A[R][K];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    lpv_load_elems<E, K>(xrow, chunk0(r), T, vec, U[r]);
+    load_chunk<SC, K>(crow, chunk0(r), T, vec, A[r], Alg::s_czero());
+  }
+
+  // ---- pass 1: lane maps of (A[t], b[t] x[t]), wave scans, round chaining.
+  // Steps past the row's end take a zero coefficient and input and only
+  // touch the aggregate of its last tile, which nobody reads.
+  M Ex[R];
+  M carry = map_identity<Alg>();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    SS X[K];
+    lpv_inputs<Alg, K>(a, b, chunk0(r), U[r], X);
+    M m = lane_map<Alg, true, false, K>(A[r], X, dummy);
+    m = wave_scan_incl(m, lane, op);
+    const M ex = wave_shift_up(m, lane, map_identity<Alg>());
+    const M tot = read_lane(m, 63);
+    Ex[r] = compose<Alg>(carry, ex);
+    carry = compose<Alg>(carry, tot);
+  }
+  if (lane == 0) s_wagg[w] = carry;
+  __syncthreads();  // wave aggregates are in s_wagg
+  __syncthreads();  // entry state is in s_in
+  const S hw = apply<Alg>(s_wpre[w], s_in);
+
+  // ---- pass 2: y = c[t] . h + d[t] x[t], then the step
+  E *yrow = a.y + b * T;
+  const E *cp = a.cv.p ? a.cv.p + b * a.cv.row_stride : nullptr;
+  const E *dp = a.d.p ? a.d.p + b * a.d.row_stride : nullptr;
+  const SS c_fixed = V::unit(a.out_idx);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t t0 = chunk0(r);
+    SS X[K];
+    lpv_inputs<Alg, K>(a, b, t0, U[r], X);
+    SS h = Alg::store_s(apply<Alg>(Ex[r], hw));
+    E O[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int64_t t = t0 + k < T ? t0 + k : T - 1;
+      const SS c = cp ? V::load_vec(cp + t * a.cv.t_stride) : c_fixed;
+      const E dv = dp ? dp[t * a.d.t_stride] : E(0);
+      O[k] = fma(dv, U[r][k], V::dot(c, h));
+      h = Alg::s_affine(A[r][k], h, X[k]);
+      if (a.zf && t0 + k == T - 1) {
+        union {
+          SS s;
+          E e[V::M];
+        } zu;
+        zu.s = h;
+#pragma unroll
+        for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = zu.e[i];
+      }
+    }
+    lpv_store_elems<E, K>(yrow, t0, T, vec, O);
+  }
+}
+
+}  // namespace phs

@@ -622,6 +622,79 @@ std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, cons
   return {y, zf};
 }
 
+// Single-input single-output LPV state space of order <= 2, fused
+// (phs_lpv_ss_fwd; philtorch/lpv/ssm.py:337-581 for a 2D x): returns (y, zf).
+// A (T, M, M) or (batch, T, M, M); B, C None or (1 | batch, 1 | T, M); D None
+// or (1 | batch, 1 | T) (a size-1 axis is shared); zi None or (batch, M);
+// out_idx selects the output state when C is None.
+std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
+                                      const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
+                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx) {
+  TORCH_CHECK(x.dim() == 2, "philtorch::lpv_ss: x must be a 2D tensor (batch, time)");
+  const int64_t B = x.size(0), T = x.size(1);
+  TORCH_CHECK((A.dim() == 3 || A.dim() == 4) && A.size(-1) == A.size(-2) && A.size(-3) == T,
+              "philtorch::lpv_ss: A must be (T, M, M) or (batch, T, M, M)");
+  const int64_t M = A.size(-1);
+  TORCH_CHECK(M >= 1 && M <= 2, "philtorch::lpv_ss: state order 1 or 2, got ", M);
+  if (A.dim() == 4) TORCH_CHECK(A.size(0) == B, "philtorch::lpv_ss: a 4D A must have x's batch size");
+  TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,
+              "philtorch::lpv_ss: float32 or float64 only, got ", x.scalar_type());
+  TORCH_CHECK(x.is_cuda(), "philtorch::lpv_ss: philtorch_amd runs on HIP devices only (got ", x.device(), ")");
+  auto same = [&](const Tensor &t, const char *what) {
+    TORCH_CHECK(t.scalar_type() == x.scalar_type(), "philtorch::lpv_ss: ", what, " must have x's scalar type");
+    TORCH_CHECK(t.device() == x.device(), "philtorch::lpv_ss: all tensors must be on the same device");
+  };
+  same(A, "A");
+  auto vec_ok = [&](const Tensor &t) {
+    return t.dim() == 3 && (t.size(0) == 1 || t.size(0) == B) && (t.size(1) == 1 || t.size(1) == T) &&
+           t.size(2) == M;
+  };
+  if (Bm) {
+    same(*Bm, "B");
+    TORCH_CHECK(vec_ok(*Bm), "philtorch::lpv_ss: B must be (1 or batch, 1 or T, M)");
+  }
+  if (Cm) {
+    same(*Cm, "C");
+    TORCH_CHECK(vec_ok(*Cm), "philtorch::lpv_ss: C must be (1 or batch, 1 or T, M)");
+  } else {
+    TORCH_CHECK(out_idx >= 0 && out_idx < M, "philtorch::lpv_ss: out_idx must be in [0, ", M, ") when C is None");
+  }
+  if (Dm) {
+    same(*Dm, "D");
+    TORCH_CHECK(Dm->dim() == 2 && (Dm->size(0) == 1 || Dm->size(0) == B) && (Dm->size(1) == 1 || Dm->size(1) == T),
+                "philtorch::lpv_ss: D must be (1 or batch, 1 or T)");
+  }
+  if (zi) {
+    same(*zi, "zi");
+    TORCH_CHECK(zi->dim() == 2 && zi->size(0) == B && zi->size(1) == M, "philtorch::lpv_ss: zi must be (batch, M)");
+  }
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor Ac = A.contiguous(), xc = x.contiguous();
+  Tensor bc = Bm ? Bm->contiguous() : Tensor(), cc = Cm ? Cm->contiguous() : Tensor();
+  Tensor dc = Dm ? Dm->contiguous() : Tensor(), zc = zi ? zi->contiguous() : Tensor();
+  Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  Tensor zf = at::empty({B, M}, x.options());
+  if (B == 0) return {y, zf};
+  if (T == 0) {
+    if (zi) zf.copy_(zc); else zf.zero_();
+    return {y, zf};
+  }
+  // element strides of a (rows, steps, width) operand with broadcast axes
+  auto rs = [](const Tensor &t, int64_t width) { return t.size(0) == 1 ? int64_t(0) : t.size(1) * width; };
+  auto ts = [](const Tensor &t, int64_t width) { return t.size(1) == 1 ? int64_t(0) : width; };
+  void *stream = stream_of(x);
+  const Workspace ws = workspace_for(x, phs_lpv_ss_workspace_size(dt, int(M), B, T), stream);
+  check_status(phs_lpv_ss_fwd(dt, int(M), B, T, Ac.const_data_ptr(), A.dim() == 3 ? 1 : 0,
+                              Bm ? bc.const_data_ptr() : nullptr, Bm ? rs(bc, M) : 0, Bm ? ts(bc, M) : 0,
+                              Cm ? cc.const_data_ptr() : nullptr, Cm ? rs(cc, M) : 0, Cm ? ts(cc, M) : 0,
+                              int(out_idx), Dm ? dc.const_data_ptr() : nullptr, Dm ? rs(dc, 1) : 0,
+                              Dm ? ts(dc, 1) : 0, zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(),
+                              y.mutable_data_ptr(), zf.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+               "lpv_ss");
+  return {y, zf};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(philtorch, m) {
@@ -656,6 +729,8 @@ TORCH_LIBRARY(philtorch, m) {
   // new: lfilter of order <= 4 from b and a (companion model built in the kernel): (y, zf)
   m.def("lfilter_ss(Tensor b, Tensor a, Tensor? zi, Tensor x, int form, bool reverse=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
+  m.def("lpv_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx) -> (Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
@@ -674,4 +749,5 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("filtfilt", &filtfilt_hip);
   m.impl("lti_ss", &lti_ss_hip);
   m.impl("lfilter_ss", &lfilter_ss_hip);
+  m.impl("lpv_ss", &lpv_ss_hip);
 }

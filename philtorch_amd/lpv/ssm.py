@@ -296,6 +296,94 @@ def _apply_C(h: Tensor, C: Optional[Tensor], batch: int, N: int, M: int) -> Tens
     )
 
 
+def _lpv_siso_operands(x: Tensor, B, C, D, out_idx, batch: int, N: int, M: int):
+    """B, C as (1 | batch, 1 | N, M) and D as (1 | batch, 1 | N) views when the
+    model has one input and one output, following the shape cases of
+    philtorch/lpv/ssm.py:413-454 (B), :480-547 (D) and :549-573 (C) in their
+    order; None when it has not (a state or multi-output y, features)."""
+    if x.dim() != 2:
+        return None
+    if B is not None:
+        s = tuple(B.shape)
+        if s == (M,):
+            B = B.reshape(1, 1, M)
+        elif s == (N, M):
+            B = B.reshape(1, N, M)
+        elif s == (batch, M):
+            B = B.reshape(batch, 1, M)
+        elif s == (batch, N, M):
+            pass
+        else:
+            return None
+    if C is None:
+        if out_idx is None:
+            return None
+    else:
+        s = tuple(C.shape)
+        if s == (M,):
+            C = C.reshape(1, 1, M)
+        elif s == (N, M):
+            C = C.reshape(1, N, M)
+        elif s == (batch, M):
+            C = C.reshape(batch, 1, M)
+        elif len(s) == 3 and s[0] != N and s == (batch, N, M):
+            pass
+        else:
+            return None
+    if D is not None:
+        s = tuple(D.shape)
+        if s in ((), (1,)):
+            D = D.reshape(1, 1)
+        elif len(s) == 1 and s[0] == N:
+            D = D.reshape(1, N)
+        elif len(s) == 1 and s[0] == batch:
+            D = D.reshape(batch, 1)
+        elif s == (batch, N):
+            pass
+        else:
+            return None
+    return B, C, D
+
+
+def _lpv_state_space_composite(A, B, C, D, zi, x, out_idx=0):
+    """The route philtorch::lpv_ss replaces, on canonical operands (B, C as
+    (1 | batch, 1 | N, M), D as (1 | batch, 1 | N)): B x, the native LPV
+    scan, the state shift, C h + D x; returns (y, zf).  Differentiable."""
+    batch, N = x.shape
+    M = A.size(-1)
+    z = zi if zi is not None else x.new_zeros(batch, M)
+    Bx = x.unsqueeze(-1) * B if B is not None else _widen(x, M)
+    h = _ext_ss_recur(A, z, Bx)
+    zf = h[:, -1] if N > 0 else z
+    hp = torch.cat([z.unsqueeze(1), h[:, :-1]], dim=1)
+    y = (hp * C).sum(-1) if C is not None else hp[..., out_idx]
+    if D is not None:
+        y = y + D * x
+    return y, zf
+
+
+def _fused_lpv_ss_applies(A: Tensor, x: Tensor, zi: Optional[Tensor], ops, native: bool) -> bool:
+    """A model of order <= 2 with one input and one output on a HIP device,
+    the native route requested and no gradient or tangent wanted:
+    philtorch::lpv_ss runs it in one pass."""
+    from .. import EXTENSION_LOADED
+
+    if not (native and EXTENSION_LOADED and x.is_cuda and ops is not None and hasattr(torch.ops.philtorch, "lpv_ss")):
+        return False
+    if x.dtype not in (torch.float32, torch.float64) or A.size(-1) > 2:
+        return False
+    tensors = [A, x] + [t for t in (zi, *ops) if t is not None]
+    if any(t.dtype != x.dtype or t.device != x.device for t in tensors):
+        return False
+    if A.dim() == 4 and A.size(0) != x.size(0):
+        return False
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+        return False
+    import torch.autograd.forward_ad as fwad
+
+    return all(fwad.unpack_dual(t).tangent is None for t in tensors)
+
+
 def state_space(
     A: Tensor,
     x: Tensor,
@@ -311,7 +399,10 @@ def state_space(
     Mirrors philtorch/lpv/ssm.py:337-581: when ``zi`` is given, returns
     ``(y, zf)``.  ``unroll_factor=None`` means ``round(sqrt(N))`` (the
     blocked PyTorch route); ``unroll_factor=1`` on a HIP device runs the
-    native scan.
+    native scan.  A model of order <= 2 with one input and one output (2D x;
+    B, C per row and/or per step or absent / out_idx; D per row and/or per
+    step) with no gradient wanted runs philtorch::lpv_ss: B x, the scan, the
+    state shift and C h + D x in one pass.
     """
     assert x.dim() in (2, 3), f"Input signal must be 2D or 3D (batch, time, [features]), got {x.shape}"
     assert A.dim() in (3, 4), f"State matrix A must be 3D or 4D, got {A.shape}"
@@ -331,9 +422,14 @@ def state_space(
     if unroll_factor is None:
         unroll_factor = round(N**0.5)
     features = -1 if x.dim() == 2 else x.size(-1)
+    native = extension_backend_indicator(x, M) and unroll_factor in (None, 1)
+    ops = _lpv_siso_operands(x, B, C, D, out_idx, batch, N, M)
+    if _fused_lpv_ss_applies(A, x, zi if return_zf else None, ops, native):
+        y, zf = torch.ops.philtorch.lpv_ss(A, ops[0], ops[1], ops[2], zi.contiguous() if return_zf else None, x,
+                                           0 if out_idx is None else out_idx)
+        return (y, zf) if return_zf else y
     Bx = _apply_B(x, B, batch, N, M, features)
 
-    native = extension_backend_indicator(x, M) and unroll_factor in (None, 1)
     runner = _ext_ss_recur if native else state_space_recursion
     if return_zf or out_idx is None:
         h = runner(A, zi, Bx, unroll_factor=unroll_factor, out_idx=None)

@@ -462,3 +462,40 @@ def test_lti_state_space_matches_scipy_dlsim(M):
     for r in range(Bn):
         _, ry, _ = scipy.signal.dlsim((A[0], e0[:, None], np.eye(M)[idx][None, :], [[0.0]], 1), x[r], x0=zi[r])
         D.check(y2[r], ry[:, 0], f"out_idx row {r}")
+
+
+# ---------------------------------------------------------------- LPV SISO state space
+@pytest.mark.parametrize("M", [1, 2])
+def test_lpv_state_space_matches_loop_and_lti(M):
+    """oracle.lpv_state_space against the textbook per-step loop of
+    h[t+1] = A[t] h[t] + b[t] x[t], y[t] = c[t] . h[t] + d[t] x[t] (per-row
+    and per-step operands, shared ones, B / C absent), and against
+    lti_state_space when A, b, c, d do not vary along time."""
+    g = D.rng(D.seed_of("oracle-lpv-ss", M))
+    Bn, T = 3, 60
+    A = 0.6 * g.standard_normal((Bn, T, M, M)) / np.sqrt(M)
+    x = g.standard_normal((Bn, T))
+    zi = g.standard_normal((Bn, M))
+    Bv, Cv, Dv = g.standard_normal((Bn, T, M)), g.standard_normal((1, T, M)), g.standard_normal((Bn, 1))
+    y, zf = oracle.lpv_state_space(A, x, Bv, Cv, Dv, zi)
+    for r in range(Bn):
+        h = zi[r].copy()
+        for t in range(T):
+            ref = Cv[0, t] @ h + Dv[r, 0] * x[r, t]
+            assert abs(y[r, t] - ref) <= 1e-12 * (1 + abs(ref))
+            h = A[r, t] @ h + Bv[r, t] * x[r, t]
+        np.testing.assert_allclose(zf[r], h, rtol=1e-12, atol=1e-12)
+    y2, _ = oracle.lpv_state_space(A, x, None, None, None, zi, out_idx=M - 1)
+    for r in range(Bn):
+        h = zi[r].copy()
+        for t in range(T):
+            assert abs(y2[r, t] - h[M - 1]) <= 1e-12 * (1 + abs(h[M - 1]))
+            e = np.zeros(M)
+            e[0] = x[r, t]
+            h = A[r, t] @ h + e
+    A0, b0, c0, d0 = _stable_model(g, M, (Bn,))
+    yl, zl = oracle.lpv_state_space(np.broadcast_to(A0[:, None], (Bn, T, M, M)), x, b0[:, None], c0[:, None],
+                                    d0[:, None], zi)
+    yr, zr = oracle.lti_state_space(A0, x, b0, c0, d0, zi)
+    D.check(yl, yr, "lpv vs lti y")
+    D.check(zl, zr, "lpv vs lti zf")
