@@ -13,6 +13,7 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c1, c5  philtorch::recur + recur_backward                 (LPV scalar)
   c2      philtorch::lti_recur + lti_recur_backward         (LTI scalar, complex64)
   c3      philtorch::recur2 + recurN_backward               (LPV 2x2)
+  c3_lpv_ss  lpv.state_space of a time-varying biquad (tdf2, one output), forward only (philtorch::lpv_ss)
   c4      8 x (philtorch::lti_recur2 + lti_recurN_backward) (LTI biquad cascade)
   c4_fused  philtorch::sosfilt + sosfilt_backward              (the same cascade, fused)
   c4_api  8 x lti.lfilter(tdf2, unroll_factor=1) + autograd   (the caller pattern, API level)
@@ -440,6 +441,57 @@ class Lfilter4Api(SosFused):
                                           nthreads=nthreads)
 
 
+class LpvSsApi(LpvBiquad):
+    """c3_lpv_ss: the C3 signal through a time-varying biquad as
+    ``lpv.state_space(A, x, B=b, D=d, zi, unroll_factor=1, out_idx=0)``,
+    forward only: A the C3 companion matrices, b[t] = bn[t, 1:] - bn[t, 0] a[t]
+    and d[t] = bn[t, 0] for smoothed time-varying zeros (lpv.lfilter's TDF-II
+    model; philtorch/lpv/filtering.py:288-333).  Runs philtorch::lpv_ss: B x,
+    the scan, the state shift and C h + D x in one pass."""
+
+    def __init__(self):
+        import torch
+        import torch.nn.functional as F
+
+        super().__init__()
+        B, T = self.B, self.T
+        self.name = "c3_lpv_ss"
+        self.metric = f"GSamples/s fwd, LPV biquad lpv.state_space (tdf2, one output) B={B} T={T} fp32 (API)"
+        g = torch.Generator().manual_seed(33)
+        rz = torch.rand(B, T + 63, generator=g, dtype=torch.float64) * 1.2
+        thz = torch.rand(B, T + 63, generator=g, dtype=torch.float64) * torch.pi
+        kern = torch.full((1, 1, 64), 1 / 64, dtype=torch.float64)
+        rz = F.conv1d(rz.unsqueeze(1), kern).squeeze(1)
+        thz = F.conv1d(thz.unsqueeze(1), kern).squeeze(1)
+        bn = torch.stack([torch.ones_like(rz), -2 * rz * torch.cos(thz), rz * rz], -1)
+        A = self.cpu[0].double()
+        a = torch.stack([-A[..., 0, 0], -A[..., 1, 0]], -1)  # (a1, a2) per step
+        bv = bn[..., 1:] - bn[..., :1] * a
+        d = bn[..., 0]
+        x = self.cpu[1][..., 0].double()
+        zi = self.cpu[2].double()
+        self.cpu = [v.float().contiguous() for v in (A, x, bv, d, zi)]
+        self.dev = [v.cuda() for v in self.cpu]
+        self.fwd_bytes = 36 * B * T  # read A (16), x, b (8), d; write y
+        self.bwd_bytes = 0
+
+    def step_fwd(self):
+        from philtorch_amd import lpv
+
+        A, x, bv, d, zi = self.dev
+        return lpv.state_space(A, x, B=bv, D=d, zi=zi, unroll_factor=1, out_idx=0)
+
+    def step_bwd(self, out):
+        return out
+
+    def cpu_step(self, rows, steps, nthreads):
+        import oracle
+
+        A, x, bv, d, zi = (v.numpy() for v in self.cpu)
+        oracle.lpv_state_space(A[:rows, :steps], x[:rows, :steps], bv[:rows, :steps], None, d[:rows, :steps],
+                               zi[:rows], out_idx=0, nthreads=nthreads)
+
+
 def make_workload(name):
     if name == "c1":
         return LpvScalar("c1", 64, 65536, "float32")
@@ -461,10 +513,12 @@ def make_workload(name):
         return FiltfiltApi()
     if name == "c4_lfilter4":
         return Lfilter4Api()
+    if name == "c3_lpv_ss":
+        return LpvSsApi()
     raise ValueError(name)
 
 
-CONFIGS = ("c1", "c2", "c3", "c4", "c4_fused", "c4_api", "c4_filtfilt", "c4_lfilter4", "c5", "c5_f64")
+CONFIGS = ("c1", "c2", "c3", "c3_lpv_ss", "c4", "c4_fused", "c4_api", "c4_filtfilt", "c4_lfilter4", "c5", "c5_f64")
 
 
 # ----------------------------------------------------------------------------
@@ -611,6 +665,7 @@ def main() -> int:
                 "c4_api": "lti_lfilter8_cascade_api_fwd_bwd_B16_T480000_f32",
                 "c4_filtfilt": "lti_filtfilt8_api_fwd_B16_T480000_f32",
                 "c4_lfilter4": "lti_lfilter_order4_x4_api_fwd_B16_T480000_f32",
+                "c3_lpv_ss": "lpv_biquad_state_space_api_fwd_B32_T1048576_f32",
                 "c5": "lpv_scan_fwd_bwd_B8_T16777216_f32",
                 "c5_f64": "lpv_scan_fwd_bwd_B8_T16777216_f64",
             }[w.name],
@@ -628,7 +683,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{'ss_kernel' if w.name in ('c4_lfilter4', 'c4_filtfilt') else 'sos_kernel' if w.name.startswith('c4_') else 'scan_kernel'} ({dominant[0]})",
+            "kernel": f"{'ss_kernel' if w.name in ('c4_lfilter4', 'c4_filtfilt') else 'lpv_ss_kernel' if w.name == 'c3_lpv_ss' else 'sos_kernel' if w.name.startswith('c4_') else 'scan_kernel'} ({dominant[0]})",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

@@ -205,11 +205,11 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
   // touch the aggregate of its last tile, which nobody reads.
   M Ex[R];
   M carry = map_identity<Alg>();
+  SS X[R][K];  // b[t] x[t], kept for pass 2 (b is read once)
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    SS X[K];
-    lpv_inputs<Alg, K>(a, b, chunk0(r), U[r], X);
-    M m = lane_map<Alg, true, false, K>(A[r], X, dummy);
+    lpv_inputs<Alg, K>(a, b, chunk0(r), U[r], X[r]);
+    M m = lane_map<Alg, true, false, K>(A[r], X[r], dummy);
     m = wave_scan_incl(m, lane, op);
     const M ex = wave_shift_up(m, lane, map_identity<Alg>());
     const M tot = read_lane(m, 63);
@@ -229,8 +229,6 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t t0 = chunk0(r);
-    SS X[K];
-    lpv_inputs<Alg, K>(a, b, t0, U[r], X);
     SS h = Alg::store_s(apply<Alg>(Ex[r], hw));
     E O[K];
 #pragma unroll
@@ -239,7 +237,7 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
       const SS c = cp ? V::load_vec(cp + t * a.cv.t_stride) : c_fixed;
       const E dv = dp ? dp[t * a.d.t_stride] : E(0);
       O[k] = fma(dv, U[r][k], V::dot(c, h));
-      h = Alg::s_affine(A[r][k], h, X[k]);
+      h = Alg::s_affine(A[r][k], h, X[r][k]);
       if (a.zf && t0 + k == T - 1) {
         union {
           SS s;
