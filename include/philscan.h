@@ -307,7 +307,7 @@ int phs_lfilter_rev(int dtype, int64_t B, int64_t T, const void *b, int nb, cons
                     size_t workspace_bytes, void *stream);
 
 /* ---- Single-input, single-output LPV (time-varying) state space of order
- * M = 1..2, fused (forward).  Replaces philtorch.lpv.state_space
+ * M = 1..4, fused (forward).  Replaces philtorch.lpv.state_space
  * (philtorch/lpv/ssm.py:337-581, the glue :413-577) for a 2D input x:
  *     h[0] = zi,  y[t] = c[t] . h[t] + d[t] x[t],
  *     h[t+1] = A[t] h[t] + b[t] x[t],  zf = h[T]

@@ -11,7 +11,7 @@ counterpart; ``lti.sosfilt`` is its API), the forward-only zero-phase
 fused single-input single-output state space ``lti_ss`` (behind
 ``lti.state_space``), ``lfilter_ss``, ``lfilter`` of order <= 4 from b and
 a in one pass (behind ``lti.lfilter``), and ``lpv_ss``, the time-varying
-single-input single-output state space of order <= 2 (behind
+single-input single-output state space of order <= 4 (behind
 ``lpv.state_space``).  This module then
 registers fake (meta) kernels and autograd formulas for them, as
 philtorch/__init__.py:157-268 does for its ops.
@@ -446,7 +446,7 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
     torch.library.register_autograd("philtorch::lfilter_ss", _lfilter_ss_backward, setup_context=_lfilter_ss_setup)
 
 if EXTENSION_LOADED and _has_op("lpv_ss"):
-    # single-input single-output LPV state space of order <= 2: (y, zf)
+    # single-input single-output LPV state space of order <= 4: (y, zf)
     @torch.library.register_fake("philtorch::lpv_ss")
     def _(A, B, C, D, zi, x, out_idx):
         torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")

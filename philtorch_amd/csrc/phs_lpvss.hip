@@ -64,6 +64,8 @@ int lpv_dispatch(int dtype, int M, F &&f) {
   switch (M) {
     case 1: return f32 ? f(Scalar<float>{}) : f(Scalar<double>{});
     case 2: return f32 ? f(Block2<float>{}) : f(Block2<double>{});
+    case 3: return f32 ? f(BlockN<float, 3>{}) : f(BlockN<double, 3>{});
+    case 4: return f32 ? f(BlockN<float, 4>{}) : f(BlockN<double, 4>{});
     default: return PHS_ERR_INVALID;
   }
 }

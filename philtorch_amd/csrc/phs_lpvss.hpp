@@ -1,5 +1,5 @@
 // Fused single-input, single-output LPV (time-varying) state space of order
-// M <= 2 in one pass (philtorch/lpv/ssm.py:337-581: state_space with a 2D
+// M <= 4 in one pass (philtorch/lpv/ssm.py:337-581: state_space with a 2D
 // input, B an M-vector per row and/or per step or absent, C an M-vector per
 // row and/or per step or out_idx, D per row and/or per step or absent; the
 // glue of lpv/ssm.py:413-577 folded into the scan):

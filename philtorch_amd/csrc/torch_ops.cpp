@@ -622,7 +622,7 @@ std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, cons
   return {y, zf};
 }
 
-// Single-input single-output LPV state space of order <= 2, fused
+// Single-input single-output LPV state space of order <= 4, fused
 // (phs_lpv_ss_fwd; philtorch/lpv/ssm.py:337-581 for a 2D x): returns (y, zf).
 // A (T, M, M) or (batch, T, M, M); B, C None or (1 | batch, 1 | T, M); D None
 // or (1 | batch, 1 | T) (a size-1 axis is shared); zi None or (batch, M);
@@ -635,7 +635,7 @@ std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tenso
   TORCH_CHECK((A.dim() == 3 || A.dim() == 4) && A.size(-1) == A.size(-2) && A.size(-3) == T,
               "philtorch::lpv_ss: A must be (T, M, M) or (batch, T, M, M)");
   const int64_t M = A.size(-1);
-  TORCH_CHECK(M >= 1 && M <= 2, "philtorch::lpv_ss: state order 1 or 2, got ", M);
+  TORCH_CHECK(M >= 1 && M <= kMaxOrder, "philtorch::lpv_ss: state order 1 to ", kMaxOrder, ", got ", M);
   if (A.dim() == 4) TORCH_CHECK(A.size(0) == B, "philtorch::lpv_ss: a 4D A must have x's batch size");
   TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,
               "philtorch::lpv_ss: float32 or float64 only, got ", x.scalar_type());

@@ -363,14 +363,14 @@ def _lpv_state_space_composite(A, B, C, D, zi, x, out_idx=0):
 
 
 def _fused_lpv_ss_applies(A: Tensor, x: Tensor, zi: Optional[Tensor], ops, native: bool) -> bool:
-    """A model of order <= 2 with one input and one output on a HIP device,
+    """A model of order <= 4 with one input and one output on a HIP device,
     the native route requested and no gradient or tangent wanted:
     philtorch::lpv_ss runs it in one pass."""
     from .. import EXTENSION_LOADED
 
     if not (native and EXTENSION_LOADED and x.is_cuda and ops is not None and hasattr(torch.ops.philtorch, "lpv_ss")):
         return False
-    if x.dtype not in (torch.float32, torch.float64) or A.size(-1) > 2:
+    if x.dtype not in (torch.float32, torch.float64) or A.size(-1) > 4:
         return False
     tensors = [A, x] + [t for t in (zi, *ops) if t is not None]
     if any(t.dtype != x.dtype or t.device != x.device for t in tensors):
@@ -399,7 +399,7 @@ def state_space(
     Mirrors philtorch/lpv/ssm.py:337-581: when ``zi`` is given, returns
     ``(y, zf)``.  ``unroll_factor=None`` means ``round(sqrt(N))`` (the
     blocked PyTorch route); ``unroll_factor=1`` on a HIP device runs the
-    native scan.  A model of order <= 2 with one input and one output (2D x;
+    native scan.  A model of order <= 4 with one input and one output (2D x;
     B, C per row and/or per step or absent / out_idx; D per row and/or per
     step) with no gradient wanted runs philtorch::lpv_ss: B x, the scan, the
     state shift and C h + D x in one pass.

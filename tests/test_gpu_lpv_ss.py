@@ -1,12 +1,12 @@
 """GPU parity of the fused single-input, single-output LPV state space
 (phs_lpv_ss_fwd, op philtorch::lpv_ss, the route of philtorch_amd.lpv.
-state_space for such models of order <= 2 when no gradient is wanted).
+state_space for such models of order <= 4 when no gradient is wanted).
 
 The C ABI entry point (ctypes, raw device pointers, the caller's stream)
 against oracle.lpv_state_space (B x, the LPV scan, the state shift,
 C h + D x; pinned to the per-step loop and to the LTI model in
 tests/test_oracle.py), evaluated in fp64 on the GPU's exact inputs: orders 1
-and 2, fp32 and fp64, every layout of b, c and d (shared, per row, per step,
+to 4, fp32 and fp64, every layout of b, c and d (shared, per row, per step,
 per row and step, absent / out_idx), shared and per-row A, rows shorter than
 a lane's chunk, on and around tile edges and of a million steps, the forced
 look-back fallback.  Through the torch API: the reference's shape cases
@@ -79,17 +79,26 @@ def _run(api, A, b, c, d, zi, x, out_idx=0):
 
 
 def _model(g, M, Bn, T, A_shared):
-    """Stable time-varying A: rotation-scaled per step, radius < 0.98."""
+    """Stable time-varying A: per step a block diagonal of scaled 2x2
+    rotations (and a real pole for odd M), radius < 0.98, turned dense by a
+    fixed orthogonal basis for M > 2 (orthogonal similarity keeps every
+    step's norm below 1)."""
     lead = (T,) if A_shared else (Bn, T)
     if M == 1:
         return g.uniform(-0.98, 0.98, lead + (1, 1))
-    r = g.uniform(0.5, 0.98, lead)
-    th = g.uniform(0, np.pi, lead)
-    A = np.empty(lead + (2, 2))
-    A[..., 0, 0] = r * np.cos(th)
-    A[..., 0, 1] = -r * np.sin(th)
-    A[..., 1, 0] = r * np.sin(th)
-    A[..., 1, 1] = r * np.cos(th)
+    A = np.zeros(lead + (M, M))
+    for i in range(0, M - 1, 2):
+        r = g.uniform(0.5, 0.98, lead)
+        th = g.uniform(0, np.pi, lead)
+        A[..., i, i] = r * np.cos(th)
+        A[..., i, i + 1] = -r * np.sin(th)
+        A[..., i + 1, i] = r * np.sin(th)
+        A[..., i + 1, i + 1] = r * np.cos(th)
+    if M % 2:
+        A[..., M - 1, M - 1] = g.uniform(-0.98, 0.98, lead)
+    if M > 2:
+        Q, _ = np.linalg.qr(g.standard_normal((M, M)))
+        A = Q @ A @ Q.T
     return A
 
 
@@ -106,7 +115,7 @@ def _check(got, A, b, c, d, zi, x, out_idx, dtype, name):
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 @pytest.mark.parametrize("Bn,T", SHAPES)
 def test_lpv_ss_capi_parity(api, dtype, M, Bn, T):
     g = D.rng(D.seed_of("lpv-ss", dtype, M, Bn, T))
@@ -126,7 +135,7 @@ def test_lpv_ss_capi_parity(api, dtype, M, Bn, T):
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_lpv_ss_capi_long_rows_and_fallback(api, dtype, M):
     lib = api[0]
     g = D.rng(D.seed_of("lpv-ss-long", dtype, M))
@@ -155,7 +164,7 @@ def test_lpv_ss_capi_errors(api):
                                   wsb, None)
 
     assert call(dt=2) == capi.PHS_ERR_DTYPE
-    assert call(M=3) == capi.PHS_ERR_INVALID
+    assert call(M=5) == capi.PHS_ERR_INVALID
     assert call(c=None, out_idx=2) == capi.PHS_ERR_INVALID
     assert call(rs=-1) == capi.PHS_ERR_INVALID
     assert call(wsb=lib.phs_lpv_ss_workspace_size(0, 2, 2, 100) - 1) == capi.PHS_ERR_WORKSPACE

@@ -465,7 +465,7 @@ def test_lti_state_space_matches_scipy_dlsim(M):
 
 
 # ---------------------------------------------------------------- LPV SISO state space
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_lpv_state_space_matches_loop_and_lti(M):
     """oracle.lpv_state_space against the textbook per-step loop of
     h[t+1] = A[t] h[t] + b[t] x[t], y[t] = c[t] . h[t] + d[t] x[t] (per-row
