@@ -243,16 +243,19 @@ def _apply_D(x: Tensor, D: Optional[Tensor], batch: int, N: int, features: int) 
         assert x.dim() == 2, f"Input signal x must be 2D when D is of shape {D.shape}, got {x.shape}"
         return x.unsqueeze(-1) * D
     if len(shape) == 2:
+        # the reference's case order: (N, F), (batch, F), (N, _), (batch, N),
+        # (batch, _), (_, F); so (N, _) wins over (batch, N) when batch == N
         if shape == (N, features):
             return torch.linalg.vecdot(D.conj(), x)
         if shape == (batch, features):
             return torch.linalg.vecdot(D.conj().unsqueeze(1), x)
+        if shape[0] == N:
+            assert x.dim() == 2, f"Input signal x must be 2D when D is of shape ({N, features}), got {x.shape}"
+            return D * x.unsqueeze(-1)
         if shape == (batch, N) and x.dim() == 2:
             return D * x
         if shape[0] == batch and x.dim() == 2:
             return D.unsqueeze(1) * x.unsqueeze(-1)
-        if shape[0] == N and x.dim() == 2:
-            return D * x.unsqueeze(-1)
         if shape[1] == features:
             return x @ D.T
     if len(shape) == 3:
@@ -338,7 +341,7 @@ def _lpv_siso_operands(x: Tensor, B, C, D, out_idx, batch: int, N: int, M: int):
             D = D.reshape(1, N)
         elif len(s) == 1 and s[0] == batch:
             D = D.reshape(batch, 1)
-        elif s == (batch, N):
+        elif len(s) == 2 and s[0] != N and s == (batch, N):
             pass
         else:
             return None
