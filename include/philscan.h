@@ -325,6 +325,16 @@ int phs_lpv_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
                    int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
                    const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream);
 
+/* The same model run backwards in time (no counterpart in the reference,
+ * which flips): h[T] = zi, y[t] = c[t] . h[t+1] + d[t] x[t],
+ * h[t] = A[t] h[t+1] + b[t] x[t], zf = h[0].  The adjoint of the forward
+ * model is this one on (A[t]^T, input vector c[t], output vector b[t], d[t])
+ * from dL/dzf: y = grad_x, zf = grad_zi. */
+int phs_lpv_ss_rev(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+                   int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
+                   int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
+                   const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,7 +35,7 @@ const char *phs_error_string(int status) {
   }
 }
 
-int phs_abi_version(void) { return 106; }
+int phs_abi_version(void) { return 107; }
 
 void phs_debug_set_spin_limit(unsigned polls) { phs::g_spin_limit.store(polls, std::memory_order_relaxed); }
 

@@ -18,7 +18,7 @@ size_t lpv_ss_ws_bytes(int64_t B, int64_t T) {
 template <class Alg>
 int lpv_ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, LpvOperand<typename Alg::elem> bv,
                LpvOperand<typename Alg::elem> cv, int out_idx, LpvOperand<typename Alg::elem> d, const void *zi,
-               const void *x, void *y, void *zf, void *workspace, size_t ws_bytes, hipStream_t stream) {
+               const void *x, void *y, void *zf, void *workspace, size_t ws_bytes, bool rev, hipStream_t stream) {
   using E = typename Alg::elem;
   using Sh = LpvSsShape<Alg>;
   constexpr int M = SsView<Alg>::M;
@@ -53,7 +53,10 @@ int lpv_ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, LpvOperand<typena
   const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
   a.spin_limit = sl ? sl : kDefaultSpinLimit;
   a.vec_ok = (size_t(T) * sizeof(E)) % 16 == 0 && aligned16(x) && aligned16(y) && aligned16(A);
-  hipLaunchKernelGGL(lpv_ss_kernel<Alg>, dim3(a.per_stripe * kStripes), dim3(Sh::kThreads), 0, stream, a);
+  if (rev)
+    hipLaunchKernelGGL((lpv_ss_kernel<Alg, true>), dim3(a.per_stripe * kStripes), dim3(Sh::kThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((lpv_ss_kernel<Alg, false>), dim3(a.per_stripe * kStripes), dim3(Sh::kThreads), 0, stream, a);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
@@ -85,10 +88,12 @@ size_t phs_lpv_ss_workspace_size(int dtype, int M, int64_t B, int64_t T) {
   return rc == PHS_OK ? out : 0;
 }
 
-int phs_lpv_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
-                   int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
-                   int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
-                   const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream) {
+namespace {
+
+int lpv_ss_call(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+                int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
+                int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi, const void *x,
+                void *y, void *zf, void *workspace, size_t workspace_bytes, bool rev, void *stream) {
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return phs::lpv_dispatch(dtype, M, [&](auto alg) {
     using E = typename decltype(alg)::elem;
@@ -96,8 +101,26 @@ int phs_lpv_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
     const phs::LpvOperand<E> co{static_cast<const E *>(c), c_row_stride, c_t_stride};
     const phs::LpvOperand<E> dd{static_cast<const E *>(d), d_row_stride, d_t_stride};
     return phs::lpv_ss_fwd<decltype(alg)>(B, T, A, A_shared != 0, bo, co, out_idx, dd, zi, x, y, zf, workspace,
-                                          workspace_bytes, st);
+                                          workspace_bytes, rev, st);
   });
+}
+
+}  // namespace
+
+int phs_lpv_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+                   int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
+                   int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
+                   const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream) {
+  return lpv_ss_call(dtype, M, B, T, A, A_shared, b, b_row_stride, b_t_stride, c, c_row_stride, c_t_stride, out_idx,
+                     d, d_row_stride, d_t_stride, zi, x, y, zf, workspace, workspace_bytes, false, stream);
+}
+
+int phs_lpv_ss_rev(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+                   int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
+                   int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
+                   const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream) {
+  return lpv_ss_call(dtype, M, B, T, A, A_shared, b, b_row_stride, b_t_stride, c, c_row_stride, c_t_stride, out_idx,
+                     d, d_row_stride, d_t_stride, zi, x, y, zf, workspace, workspace_bytes, true, stream);
 }
 
 }  // extern "C"

@@ -13,8 +13,9 @@
 // folds its K steps (A[t], b[t] x[t]) into a map, wave scans chain the lanes,
 // a look-back wave resolves the tile's entry state over the row's status
 // words, and pass 2 re-runs the steps from each lane's entry state, writing
-// c[t] . h + d[t] x[t] instead of h.  Forward only: the gradients are those of
-// the composite route, recomputed from the inputs.
+// c[t] . h + d[t] x[t] instead of h.  A reversed mode runs the model
+// backwards in time: the gradients w.r.t. x and zi are that mode on the
+// adjoint model; those of A, b, c, d are the composite route's.
 #pragma once
 
 #include "phs_ss.hpp"
@@ -64,51 +65,98 @@ struct LpvSsShape {
   static constexpr int kTile = kWaves * 64 * K * R;
 };
 
-// K scalars from row[t0..t0+K) (zeros past T): 16-byte loads where the chunk
-// is a whole number of them.
-template <typename E, int K>
-__device__ __forceinline__ void lpv_load_elems(const E *row, int64_t t0, int64_t T, bool vec, E (&out)[K]) {
-  if constexpr ((K * sizeof(E)) % 16 == 0) {
-    load_chunk<E, K>(row, t0, T, vec, out, E(0));
-  } else {
+// K items of a row in scan order from scan position s0: forward, position s
+// is time s; reversed (REV), time T-1-s, so the chunk is the K items below
+// T - s0 read in descending time.  Positions past the row read `fill`.
+template <bool REV, typename X, int K>
+__device__ __forceinline__ void lpv_load(const X *row, int64_t s0, int64_t T, bool vec, X (&out)[K], const X fill) {
+  constexpr bool kVec = (K * sizeof(X)) % 16 == 0;
+  if constexpr (!REV) {
+    if constexpr (kVec) {
+      load_chunk<X, K>(row, s0, T, vec, out, fill);
+    } else {
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      if (t0 + k < T)
-        out[k] = row[t0 + k];
-      else
-        out[k] = E(0);
+      for (int k = 0; k < K; ++k) {
+        if (s0 + k < T)
+          out[k] = row[s0 + k];
+        else
+          out[k] = fill;
+      }
+    }
+  } else {
+    const int64_t base = T - s0 - K;
+    if (kVec && vec && base >= 0) {
+      X tmp[K];
+      if constexpr (kVec) load_chunk<X, K>(row, base, T, true, tmp, fill);
+#pragma unroll
+      for (int k = 0; k < K; ++k) out[k] = tmp[K - 1 - k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int64_t t = T - 1 - s0 - k;
+        if (t >= 0)
+          out[k] = row[t];
+        else
+          out[k] = fill;
+      }
     }
   }
 }
 
-template <typename E, int K>
-__device__ __forceinline__ void lpv_store_elems(E *row, int64_t t0, int64_t T, bool vec, const E (&v)[K]) {
-  if constexpr ((K * sizeof(E)) % 16 == 0) {
-    store_chunk<E, K>(row, t0, T, vec, v);
-  } else {
+template <bool REV, typename X, int K>
+__device__ __forceinline__ void lpv_store(X *row, int64_t s0, int64_t T, bool vec, const X (&v)[K]) {
+  constexpr bool kVec = (K * sizeof(X)) % 16 == 0;
+  if constexpr (!REV) {
+    if constexpr (kVec) {
+      store_chunk<X, K>(row, s0, T, vec, v);
+    } else {
 #pragma unroll
-    for (int k = 0; k < K; ++k)
-      if (t0 + k < T) row[t0 + k] = v[k];
+      for (int k = 0; k < K; ++k)
+        if (s0 + k < T) row[s0 + k] = v[k];
+    }
+  } else {
+    const int64_t base = T - s0 - K;
+    if (kVec && vec && base >= 0) {
+      X tmp[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) tmp[k] = v[K - 1 - k];
+      if constexpr (kVec) store_chunk<X, K>(row, base, T, true, tmp);
+    } else {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int64_t t = T - 1 - s0 - k;
+        if (t >= 0) row[t] = v[k];
+      }
+    }
   }
 }
 
-// b[t] x[t] for the K steps from t0 (b absent: x[t] into state 0).
-template <class Alg, int K>
-__device__ __forceinline__ void lpv_inputs(const LpvSsArgs<Alg> &a, int64_t b, int64_t t0, const typename Alg::elem (&u)[K],
+// Time of scan position s (clamped into the row: positions past it carry a
+// zero input and coefficient, and their outputs are not stored).
+template <bool REV>
+__device__ __forceinline__ int64_t lpv_time(int64_t s, int64_t T) {
+  const int64_t t = REV ? T - 1 - s : s;
+  return t < 0 ? 0 : (t >= T ? T - 1 : t);
+}
+
+// b[t] x[t] for the K steps from scan position s0 (b absent: x[t] into
+// state 0).
+template <class Alg, bool REV, int K>
+__device__ __forceinline__ void lpv_inputs(const LpvSsArgs<Alg> &a, int64_t b, int64_t s0, const typename Alg::elem (&u)[K],
                                            typename Alg::s_state (&X)[K]) {
   using V = SsView<Alg>;
   using E = typename Alg::elem;
   const E *bp = a.bv.p ? a.bv.p + b * a.bv.row_stride : nullptr;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const int64_t t = t0 + k < a.T_len ? t0 + k : a.T_len - 1;  // past the row: u is 0
+    const int64_t t = lpv_time<REV>(s0 + k, a.T_len);
     X[k] = V::scale(bp ? V::load_vec(bp + t * a.bv.t_stride) : V::unit(0), u[k]);
   }
 }
 
 // State entering tile position `span` of a row, folded from the inputs (the
 // look-back's bounded-wait fallback; out of line, cold).
-template <class Alg>
+template <class Alg, bool REV>
 __device__ __noinline__ typename Alg::state lpv_prefix_fallback(LpvSsArgs<Alg> a, int64_t b, int64_t span, int lane,
                                                                typename Alg::state virt) {
   using E = typename Alg::elem;
@@ -126,9 +174,9 @@ __device__ __noinline__ typename Alg::state lpv_prefix_fallback(LpvSsArgs<Alg> a
     E u[K];
     SS xs[K];
     SC cs[K];
-    lpv_load_elems<E, K>(xrow, c0, a.T_len, a.vec_ok != 0, u);
-    load_chunk<SC, K>(crow, c0, a.T_len, a.vec_ok != 0, cs, Alg::s_czero());
-    lpv_inputs<Alg, K>(a, b, c0, u, xs);
+    lpv_load<REV, E, K>(xrow, c0, a.T_len, a.vec_ok != 0, u, E(0));
+    lpv_load<REV, SC, K>(crow, c0, a.T_len, a.vec_ok != 0, cs, Alg::s_czero());
+    lpv_inputs<Alg, REV, K>(a, b, c0, u, xs);
     M m = lane_map<Alg, true, false, K>(cs, xs, dummy);
     m = wave_scan_incl(m, lane, op);
     acc = compose<Alg>(acc, read_lane(m, 63));
@@ -136,7 +184,10 @@ __device__ __noinline__ typename Alg::state lpv_prefix_fallback(LpvSsArgs<Alg> a
   return apply<Alg>(acc, virt);
 }
 
-template <class Alg>
+// REV runs the model backwards in time: scan position s is time T-1-s (zi
+// the state before the last sample, zf after the first), the form of the
+// adjoint pass.
+template <class Alg, bool REV>
 __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(LpvSsArgs<Alg> a) {
   using E = typename Alg::elem;
   using S = typename Alg::state;
@@ -182,7 +233,7 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
       if (lane == 0) publish(row_status + q * St::kStride + St::kIncWords, tagg, tag);
       Lookback<Alg> lb = lookback_start<Alg>(q);
       if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
-        yin = lpv_prefix_fallback<Alg>(a, b, q * Sh::kTile, lane, virt);
+        yin = lpv_prefix_fallback<Alg, REV>(a, b, q * Sh::kTile, lane, virt);
     }
     if (q + 1 < a.tiles_per_row && lane == 0) publish(row_status + q * St::kStride, apply<Alg>(tagg, yin), tag);
     if (lane == 0) s_in = yin;
@@ -200,8 +251,8 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
   SC A[R][K];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    lpv_load_elems<E, K>(xrow, chunk0(r), T, vec, U[r]);
-    load_chunk<SC, K>(crow, chunk0(r), T, vec, A[r], Alg::s_czero());
+    lpv_load<REV, E, K>(xrow, chunk0(r), T, vec, U[r], E(0));
+    lpv_load<REV, SC, K>(crow, chunk0(r), T, vec, A[r], Alg::s_czero());
   }
 
   // ---- pass 1: lane maps of (A[t], b[t] x[t]), wave scans, round chaining.
@@ -212,7 +263,7 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
   SS X[R][K];  // b[t] x[t], kept for pass 2 (b is read once)
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    lpv_inputs<Alg, K>(a, b, chunk0(r), U[r], X[r]);
+    lpv_inputs<Alg, REV, K>(a, b, chunk0(r), U[r], X[r]);
     M m = lane_map<Alg, true, false, K>(A[r], X[r], dummy);
     m = wave_scan_incl(m, lane, op);
     const M ex = wave_shift_up(m, lane, map_identity<Alg>());
@@ -237,7 +288,7 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
     E O[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      const int64_t t = t0 + k < T ? t0 + k : T - 1;
+      const int64_t t = lpv_time<REV>(t0 + k, T);
       const SS c = cp ? V::load_vec(cp + t * a.cv.t_stride) : c_fixed;
       const E dv = dp ? dp[t * a.d.t_stride] : E(0);
       O[k] = fma(dv, U[r][k], V::dot(c, h));
@@ -252,7 +303,7 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
         for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = zu.e[i];
       }
     }
-    lpv_store_elems<E, K>(yrow, t0, T, vec, O);
+    lpv_store<REV, E, K>(yrow, t0, T, vec, O);
   }
 }
 

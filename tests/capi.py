@@ -105,6 +105,8 @@ def load() -> ctypes.CDLL:
     lib.phs_lpv_ss_fwd.argtypes = [ctypes.c_int, ctypes.c_int, i64, i64, vp, ctypes.c_int, vp, i64, i64, vp, i64, i64,
                                    ctypes.c_int, vp, i64, i64, vp, vp, vp, vp, vp, ctypes.c_size_t, vp]
     lib.phs_lpv_ss_fwd.restype = ctypes.c_int
+    lib.phs_lpv_ss_rev.argtypes = lib.phs_lpv_ss_fwd.argtypes
+    lib.phs_lpv_ss_rev.restype = ctypes.c_int
     for rev, fwd in (("phs_lti_ss_rev", "phs_lti_ss_fwd"), ("phs_lfilter_rev", "phs_lfilter_fwd")):
         getattr(lib, rev).argtypes = getattr(lib, fwd).argtypes
         getattr(lib, rev).restype = ctypes.c_int

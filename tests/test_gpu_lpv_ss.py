@@ -57,7 +57,7 @@ def _strides(v, T, width):
     return (0 if rows == 1 else steps * width), (0 if steps == 1 else width)
 
 
-def _run(api, A, b, c, d, zi, x, out_idx=0):
+def _run(api, A, b, c, d, zi, x, out_idx=0, rev=False):
     import torch
 
     lib, ws, capi = api
@@ -69,8 +69,8 @@ def _run(api, A, b, c, d, zi, x, out_idx=0):
     tA, tb, tc, td, tz, tx = (_dev(v) for v in (A, b, c, d, zi, x))
     y = torch.full_like(tx, float("nan"))
     zf = torch.full((Bn, M), float("nan"), dtype=tx.dtype, device="cuda")
-    print(f"lpv_ss capi M={M} B={Bn} T={T}", flush=True)
-    rc = lib.phs_lpv_ss_fwd(dt, M, Bn, T, _p(tA), int(A.ndim == 3), _p(tb), *_strides(b, T, M), _p(tc),
+    print(f"lpv_ss capi M={M} B={Bn} T={T} rev={rev}", flush=True)
+    rc = (lib.phs_lpv_ss_rev if rev else lib.phs_lpv_ss_fwd)(dt, M, Bn, T, _p(tA), int(A.ndim == 3), _p(tb), *_strides(b, T, M), _p(tc),
                             *_strides(c, T, M), out_idx, _p(td), *_strides(d, T, 1), _p(tz), _p(tx), _p(y), _p(zf),
                             _p(ws), need, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == capi.PHS_OK, lib.phs_error_string(rc)
@@ -107,9 +107,16 @@ def _layout(g, kind, Bn, T, width):
     return g.standard_normal(shape + ((width,) if width else ()))
 
 
-def _check(got, A, b, c, d, zi, x, out_idx, dtype, name):
+def _check(got, A, b, c, d, zi, x, out_idx, dtype, name, rev=False):
+    """Against the oracle; rev: the model over the time-flipped row and
+    operands, flipped back."""
     w = lambda v: None if v is None else np.asarray(v, np.float64)  # noqa: E731
+    if rev:
+        ft = lambda v, ax: v if v is None or v.shape[ax] == 1 else np.ascontiguousarray(np.flip(v, ax))  # noqa: E731
+        A, b, c, d, x = ft(A, -3), ft(b, 1), ft(c, 1), ft(d, 1), np.ascontiguousarray(np.flip(x, 1))
     ry, rzf = oracle.lpv_state_space(w(A), w(x), w(b), w(c), w(d), w(zi), out_idx=out_idx)
+    if rev:
+        ry = np.ascontiguousarray(ry[:, ::-1])
     D.check(got[0], ry, f"{name} y", dtype=dtype)
     D.check(got[1], rzf, f"{name} zf", dtype=dtype, scale=np.max(np.abs(ry)) if ry.size else None)
 
@@ -132,6 +139,8 @@ def test_lpv_ss_capi_parity(api, dtype, M, Bn, T):
         idx = M - 1
         name = f"M={M} B={Bn} T={T} A_shared={A_shared} b={kb} c={kc} d={kd}"
         _check(_run(api, A, b, c, d, zi, x, out_idx=idx), A, b, c, d, zi, x, idx, dtype, name)
+        _check(_run(api, A, b, c, d, zi, x, out_idx=idx, rev=True), A, b, c, d, zi, x, idx, dtype, name + " rev",
+               rev=True)
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
@@ -150,9 +159,11 @@ def test_lpv_ss_capi_long_rows_and_fallback(api, dtype, M):
     lib.phs_debug_set_spin_limit(1)
     try:
         got = _run(api, As, bs, cs, ds, zi, xs)
+        got_rev = _run(api, As, bs, cs, ds, zi, xs, rev=True)
     finally:
         lib.phs_debug_set_spin_limit(0)
     _check(got, As, bs, cs, ds, zi, xs, 0, dtype, "fallback")
+    _check(got_rev, As, bs, cs, ds, zi, xs, 0, dtype, "rev fallback", rev=True)
 
 
 def test_lpv_ss_capi_errors(api):
@@ -213,6 +224,63 @@ def test_lpv_state_space_api_routes_and_shapes(hip, monkeypatch):
     assert taken[-1] is False
 
 
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_lpv_state_space_signal_gradient_takes_adjoint_pass(hip, monkeypatch, M):
+    """lpv.state_space with only x and zi requiring grad runs the fused
+    route forward and its adjoint (A[t]^T, c and b swapped, reversed in
+    time) backward; gradients against the composed route's autograd."""
+    import torch
+
+    from philtorch_amd.lpv import ssm
+
+    g = D.rng(D.seed_of("lpv-ss-adjoint", M))
+    Bn, T = 3, 5000
+    t = lambda v: torch.tensor(np.asarray(v, np.float64), device="cuda")  # noqa: E731
+    A = t(_model(g, M, Bn, T, False))
+    b, c, d = t(g.standard_normal((Bn, T, M))), t(g.standard_normal(M)), t(g.standard_normal((Bn, T)))
+    x0, z0 = g.standard_normal((Bn, T)), g.standard_normal((Bn, M))
+    gy, gzf = t(g.standard_normal((Bn, T))), t(g.standard_normal((Bn, M)))
+    taken = []
+    orig = ssm._fused_lpv_ss_applies
+    res = []
+    for fused in (True, False):
+        monkeypatch.setattr(ssm, "_fused_lpv_ss_applies",
+                            (lambda *a: taken.append(orig(*a)) or taken[-1]) if fused else (lambda *a: False))
+        for kw in (dict(C=c), dict(out_idx=M - 1)):
+            x, z = t(x0).requires_grad_(True), t(z0).requires_grad_(True)
+            y, zf = hip.lpv.state_space(A, x, B=b, D=d, zi=z, unroll_factor=1, **kw)
+            ((y * gy).sum() + (zf * gzf).sum()).backward()
+            res.append((x.grad.cpu().numpy(), z.grad.cpu().numpy()))
+    assert taken == [True, True]
+    for i in range(2):
+        D.check(res[i][0], res[i + 2][0], f"grad_x {i}")
+        D.check(res[i][1], res[i + 2][1], f"grad_zi {i}", scale=np.max(np.abs(res[i + 2][0])))
+
+
+def test_lpv_ss_reversed_op_gradients(hip):
+    import torch
+
+    g = D.rng(D.seed_of("lpv-ss-rev-grad"))
+    Bn, T, M = 2, 20, 2
+    t = lambda v, rg=False: torch.tensor(np.asarray(v, np.float64), device="cuda", requires_grad=rg)  # noqa: E731
+    A = t(_model(g, M, Bn, T, False))
+    b, c, d = t(g.standard_normal((Bn, T, M))), t(g.standard_normal((1, 1, M))), t(g.standard_normal((Bn, 1)))
+    x, zi = t(g.standard_normal((Bn, T)), True), t(g.standard_normal((Bn, M)), True)
+    for rev in (False, True):
+        f = lambda z_, x_: torch.ops.philtorch.lpv_ss(A, b, c, d, z_, x_, 0, rev)  # noqa: E731
+        assert torch.autograd.gradcheck(f, (zi, x))
+        assert torch.autograd.gradgradcheck(f, (zi, x))
+        f2 = lambda z_, x_: torch.ops.philtorch.lpv_ss(A, None, None, d, z_, x_, 1, rev)  # noqa: E731
+        assert torch.autograd.gradcheck(f2, (zi, x))
+    Ag, bg = A.clone().requires_grad_(True), b.clone().requires_grad_(True)
+    fA = lambda A_, b_, x_: torch.ops.philtorch.lpv_ss(A_, b_, c, d, None, x_, 0, True)[0]  # noqa: E731
+    assert torch.autograd.gradcheck(fA, (Ag, bg, x))
+    y, zf = torch.ops.philtorch.lpv_ss(A, b, c, d, zi, x, 0, True)
+    yr, zfr = torch.ops.philtorch.lpv_ss(A.flip(-3), b.flip(1), c, d, zi, x.flip(-1), 0)
+    D.check(y.detach().cpu().numpy(), yr.flip(-1).detach().cpu().numpy(), "reverse y")
+    D.check(zf.detach().cpu().numpy(), zfr.detach().cpu().numpy(), "reverse zf")
+
+
 def test_lpv_ss_op_gradients_and_opcheck(hip):
     import torch
 
@@ -231,4 +299,8 @@ def test_lpv_ss_op_gradients_and_opcheck(hip):
     torch.library.opcheck(torch.ops.philtorch.lpv_ss.default,
                           (s(_model(g, M, Bn, 500, True)), s(g.standard_normal((1, 500, M))), None,
                            s(g.standard_normal((1, 1))), None, s(g.standard_normal((Bn, 500))), 1),
+                          test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
+    torch.library.opcheck(torch.ops.philtorch.lpv_ss.default,
+                          (s(_model(g, M, Bn, 500, False)), None, s(g.standard_normal((Bn, 1, M))), None,
+                           s(g.standard_normal((Bn, M))), s(g.standard_normal((Bn, 500))), 0, True),
                           test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
