@@ -61,6 +61,11 @@ class Workload:
     fwd_bytes = 0  # algorithmic bytes of one forward launch
     bwd_bytes = 0  # algorithmic bytes of one backward launch
     launches = 1  # forward (and backward) launches per step
+    # streaming-probe equivalents of one forward / backward launch: (arrays
+    # read, arrays written, fp32 elements per array), or None where the
+    # launch's traffic is not a set of equal-length arrays
+    probe_fwd = None
+    probe_bwd = None
 
     def step_fwd(self):
         raise NotImplementedError
@@ -98,6 +103,8 @@ class LpvScalar(Workload):
         self.samples = B * T
         self.fwd_bytes = 3 * es * B * T  # read a, x; write y
         self.bwd_bytes = 5 * es * B * T  # read a, g, y; write grad_x, grad_a
+        self.probe_fwd = (2, 1, B * T * es // 4)
+        self.probe_bwd = (3, 2, B * T * es // 4)
 
     def step_fwd(self):
         import torch
@@ -141,6 +148,8 @@ class LtiComplex(Workload):
         self.samples = C * T
         self.fwd_bytes = 16 * C * T  # read x, write y (8 B each)
         self.bwd_bytes = 24 * C * T  # read g, y; write grad_x
+        self.probe_fwd = (1, 1, 2 * C * T)
+        self.probe_bwd = (2, 1, 2 * C * T)
 
     def step_fwd(self):
         import torch
@@ -522,6 +531,18 @@ CONFIGS = ("c1", "c2", "c3", "c3_lpv_ss", "c4", "c4_fused", "c4_api", "c4_filtfi
 
 
 # ----------------------------------------------------------------------------
+def cpu_model() -> str:
+    """The host CPU's model name (first `model name` line of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(w: Workload, budget_s=10.0):
     """Time the oracle's forward + backward on a bounded sample of rows."""
     import statistics
@@ -545,6 +566,7 @@ def cpu_baseline(w: Workload, budget_s=10.0):
         "unit": "GSamples/s",
         "cores": cores,
         "kind": "port",
+        "cpu_model": cpu_model(),
         "sample": f"{rows} of {w.B} rows x the first {steps} of T={w.T} steps, {'fwd+bwd' if w.bwd_bytes else 'fwd'}, median of {reps} reps "
         f"(oracle/phs_oracle.c, OpenMP over rows, {cores} threads)",
     }
@@ -562,6 +584,110 @@ def _measured_traffic(config, direction="backward"):
             return json.load(f)[key]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def _kernel_lib():
+    """libphilscan through ctypes (the process's already loaded copy) for its
+    measurement hook and streaming probe."""
+    import ctypes
+
+    import philtorch_amd
+
+    lib = ctypes.CDLL(philtorch_amd.KERNEL_LIBRARY)
+    lib.phs_debug_time_next_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.phs_debug_time_next_launch.restype = None
+    lib.phs_stream_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p]
+    lib.phs_stream_probe.restype = ctypes.c_int
+    return lib
+
+
+def _fresh_events():
+    """Two timing events, created (recorded once) so that their handles exist
+    before the launch hook records them around a kernel."""
+    import torch
+
+    ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    for e in ev:
+        e.record()
+    return ev
+
+
+def _ceiling(lib, w, steps, evict_caches, dev):
+    """The streaming probe (phs_stream_probe) moving one step's bytes: the
+    forward launch's arrays, then the backward's, with the same cache
+    eviction before every step.  Reports the step time, each kernel's own
+    duration (launch hook) and the scan step's fraction of it; the tile shape
+    of the scalar scan (shape 0) and a flat one-vector-per-lane shape (shape
+    1) are both timed and the faster is reported.  None where the workload's
+    launches are not equal-length array streams."""
+    import ctypes
+
+    import torch
+
+    if w.probe_fwd is None or w.probe_bwd is None:
+        return None
+    if any(p[2] % 8192 for p in (w.probe_fwd, w.probe_bwd)):
+        return None
+    bufs = {}
+
+    def arrays(n_in, n_out, n, tag):
+        key = (tag, n)
+        if key not in bufs:
+            bufs[key] = [torch.ones(n, dtype=torch.float32, device=dev) for _ in range(3)] + \
+                        [torch.empty(n, dtype=torch.float32, device=dev) for _ in range(2)]
+        b = bufs[key]
+        ins = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in b[:3]])
+        outs = (ctypes.c_void_p * 2)(*[t.data_ptr() for t in b[3:]])
+        return ins, outs
+
+    calls = [(w.probe_fwd, arrays(*w.probe_fwd, "f")), (w.probe_bwd, arrays(*w.probe_bwd, "b"))]
+    results = {}
+    for shape in (0, 1):
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+        def probe_step(timed=None):
+            for j, ((n_in, n_out, n), (ins, outs)) in enumerate(calls):
+                if timed is not None:
+                    lib.phs_debug_time_next_launch(timed[j][0].cuda_event, timed[j][1].cuda_event)
+                rc = lib.phs_stream_probe(shape, n_in, n_out, n, ins, outs, stream)
+                if rc != 0:
+                    raise RuntimeError(f"phs_stream_probe returned {rc}")
+
+        for _ in range(3):
+            evict_caches()
+            probe_step()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for i in range(steps):
+            evict_caches()
+            ev[i][0].record()
+            probe_step()
+            ev[i][1].record()
+        kev = []
+        for i in range(steps):
+            evict_caches()
+            k = [_fresh_events(), _fresh_events()]
+            probe_step(k)
+            kev.append(k)
+        lib.phs_debug_time_next_launch(None, None)
+        torch.cuda.synchronize()
+        results[shape] = (
+            sum(a.elapsed_time(b) for a, b in ev) / steps,
+            sum(k[0][0].elapsed_time(k[0][1]) for k in kev) / steps,
+            sum(k[1][0].elapsed_time(k[1][1]) for k in kev) / steps,
+        )
+    best = min(results, key=lambda sh: results[sh][0])
+    ms_step, ms_f, ms_b = results[best]
+    step_bytes = (w.fwd_bytes + w.bwd_bytes) * w.launches
+    return {
+        "kernel": f"phs_stream_probe shape {best} ({'scan tile geometry' if best == 0 else 'one float4 per lane'})",
+        "ms_per_step": round(ms_step, 5),
+        "ms_fwd_kernel": round(ms_f, 5),
+        "ms_bwd_kernel": round(ms_b, 5),
+        "step_GBs": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "step_frac_of_peak": round(step_bytes / (ms_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "shapes_ms_per_step": {str(k): round(v[0], 5) for k, v in results.items()},
+    }
 
 
 def main() -> int:
@@ -623,24 +749,32 @@ def main() -> int:
     wall = time.perf_counter() - wall0
     ms_per_step = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
 
-    # roofline pass: the same steps with an event between forward and
-    # backward, giving each kernel's mean launch duration on its stream
-    kev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    # kernel pass: the same steps, each forward and backward main kernel
+    # timed by the library's launch hook (events recorded around the kernel
+    # itself, as rocprofv3's kernel trace measures it), first launch of each
+    # direction per step
+    lib = _kernel_lib()
+    kev = []
     for i in range(args.steps):
         evict_caches()
-        kev[i][0].record()
+        fe, be = _fresh_events(), _fresh_events()
+        lib.phs_debug_time_next_launch(fe[0].cuda_event, fe[1].cuda_event)
         y = w.step_fwd()
-        kev[i][1].record()
+        if w.bwd_bytes:
+            lib.phs_debug_time_next_launch(be[0].cuda_event, be[1].cuda_event)
         w.step_bwd(y)
-        kev[i][2].record()
+        kev.append((fe, be))
+    lib.phs_debug_time_next_launch(None, None)
     torch.cuda.synchronize()
-    mean_fwd = sum(e[0].elapsed_time(e[1]) for e in kev) / args.steps / w.launches
-    mean_bwd = sum(e[1].elapsed_time(e[2]) for e in kev) / args.steps / w.launches
+    mean_fwd = sum(f[0].elapsed_time(f[1]) for f, _ in kev) / args.steps
+    mean_bwd = sum(b[0].elapsed_time(b[1]) for _, b in kev) / args.steps if w.bwd_bytes else 0.0
     if w.bwd_bytes and mean_bwd >= mean_fwd:
         dominant = ("backward", w.bwd_bytes, mean_bwd)
     else:
         dominant = ("forward", w.fwd_bytes, mean_fwd)
     achieved = dominant[1] / (dominant[2] * 1e-3) / 1e9
+    step_bytes = (w.fwd_bytes + w.bwd_bytes) * w.launches
+    ceiling = _ceiling(lib, w, args.steps, evict_caches, dev)
 
     result = {
         "metric": w.metric,
@@ -676,9 +810,12 @@ def main() -> int:
         "detail": {
             "launches_per_direction": w.launches,
             "ms_fwd_kernel": round(mean_fwd, 5),
-            "ms_bwd_kernel": round(mean_bwd, 5),
+            "ms_bwd_kernel": round(mean_bwd, 5) if w.bwd_bytes else None,
+            "kernel_timing": "library launch hook: events recorded around the kernel by hipExtLaunchKernelGGL",
             "fwd_GBs_algorithmic": round(w.fwd_bytes / (mean_fwd * 1e-3) / 1e9, 1),
             "bwd_GBs_algorithmic": round(w.bwd_bytes / (mean_bwd * 1e-3) / 1e9, 1) if w.bwd_bytes else None,
+            "fwd_frac": round(w.fwd_bytes / (mean_fwd * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "bwd_frac": round(w.bwd_bytes / (mean_bwd * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if w.bwd_bytes else None,
             "wall_s_timed_region": round(wall, 4),
         },
         "roofline": {
@@ -689,8 +826,13 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": _measured_traffic(w.name, dominant[0]),
+            "step_GBs_algorithmic": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+            "step_frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "ceiling": ceiling,
         },
     }
+    if ceiling is not None:
+        ceiling["scan_step_frac_of_ceiling"] = round(ceiling["ms_per_step"] / ms_per_step, 4)
     if args.calib_copy:
         csrc = torch.ones(64 << 20, dtype=torch.float32, device=dev)
         cdst = torch.empty_like(csrc)

@@ -87,6 +87,26 @@ int phs_abi_version(void);
  * takes effect for calls issued afterwards. */
 void phs_debug_set_spin_limit(unsigned polls);
 
+/* Testing hook, no counterpart in the reference.  With `on` != 0, every tile
+ * after the first of its row publishes only its aggregate, never the state
+ * leaving it, and no look-back polls early: each look-back then folds its
+ * way back to the row's first tile, window after window of 64 aggregates,
+ * which normal runs reach only when more than a window of predecessors are
+ * still unresolved.  Every tile still publishes before it waits, so every
+ * kernel completes; results are unchanged.  0 restores normal publishing.
+ * Process-wide; takes effect for calls issued afterwards. */
+void phs_debug_set_aggregates_only(int on);
+
+/* Measurement hook, no counterpart in the reference.  The next main-kernel
+ * launch of this library (the scan, cascade, state-space or probe kernel of
+ * the next call; not a follow-up reduction) records `start_event` and
+ * `stop_event` (hipEvent_t, either may be NULL) around the kernel itself
+ * through hipExtLaunchKernelGGL, so their elapsed time is that kernel's
+ * duration from dispatch to completion, as a profiler's kernel trace
+ * measures it, without the event packets' own overhead.  The hook is
+ * consumed by that launch; NULL, NULL disarms it.  Process-wide. */
+void phs_debug_time_next_launch(void *start_event, void *stop_event);
+
 /* LPV scalar scan.  A: [B,T] (coef_shared=0) or [T] shared by all rows
  * (coef_shared=1); zi: [B]; x, y: [B,T].
  * Replaces philtorch::recurN with 1x1 matrices, the only native time-varying
@@ -334,6 +354,20 @@ int phs_lpv_ss_rev(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
                    int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
                    int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
                    const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- Measurement helper, no counterpart in the reference.  A streaming
+ * kernel with no scan: out_j[i] = (j + 1) * sum_k in_k[i] over n fp32
+ * elements, n_in = 1..3 input arrays and n_out = 1..2 output arrays (16-byte
+ * aligned; n a multiple of 8192).  It moves the bytes of a scan launch with
+ * nothing else to do, so its duration is the achievable floor for that
+ * traffic (the forward scalar scan reads 2 arrays and writes 1, its
+ * backward reads 3 and writes 2).  shape 0: the fp32 scalar scan's tile
+ * geometry (8 waves, two rounds of 8 floats per lane and array, 8192
+ * elements per workgroup); shape 1: one float4 per lane and array, 2048
+ * elements per workgroup; shape 2: shape 0's grid with no memory access
+ * (launch and drain only). */
+int phs_stream_probe(int shape, int n_in, int n_out, int64_t n, const void *const *in, void *const *out,
+                     void *stream);
 
 #ifdef __cplusplus
 }

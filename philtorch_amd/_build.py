@@ -4,10 +4,11 @@ Two shared objects, both written next to this file so that they travel with
 the repository tree:
 
 * ``libphilscan.so`` — the HIP kernels and their C ABI (include/philscan.h),
-  compiled by hipcc for gfx950 only from six units compiled in parallel
+  compiled by hipcc for gfx950 only from units compiled in parallel
   (fixed-order and order-M entry points, the order-3 and order-4 kernels,
-  the fused second-order-section cascade with filtfilt, the fused
-  single-input single-output state space).
+  the fused second-order-section cascade, the fused single-input
+  single-output LTI state space with filtfilt, the LPV state space, and the
+  streaming probe the bench times beside the scans).
   It has no torch dependency.
 * ``_C.so`` — the torch.library operator layer (csrc/torch_ops.cpp), host C++
   linked against libtorch and libphilscan (found through ``$ORIGIN``).
@@ -31,7 +32,10 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # hipcc-only flags: no packed-FP32 instructions are generated (a correctness
-# guard for this hardware pool); code object v5 loads under every ROCm 6/7 runtime.
+# guard for this hardware pool); code object v5 loads under every ROCm 6/7
+# runtime; the atomic optimizer is off: every atomic here is issued by one
+# lane already, and the optimizer's rewrite waits for the result at once,
+# which would put the tile claim's round trip in front of the tile's loads.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -39,6 +43,7 @@ HIP_FLAGS = [
     "-fPIC",
     "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall", "-Wno-unused-local-typedef", "-Wno-unknown-pragmas",
 ]
 
@@ -70,6 +75,7 @@ KERNEL_UNITS = (
     ("phs_sos.hip", [], "phs_sos.o"),
     ("phs_ss.hip", [], "phs_ss.o"),
     ("phs_lpvss.hip", [], "phs_lpvss.o"),
+    ("phs_probe.hip", [], "phs_probe.o"),
 )
 
 

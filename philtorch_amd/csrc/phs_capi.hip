@@ -5,6 +5,8 @@
 
 namespace phs {
 std::atomic<unsigned> g_spin_limit{0};
+std::atomic<bool> g_agg_only{false};
+TimingHook g_timing;
 }  // namespace phs
 
 using phs::Block2;
@@ -39,6 +41,15 @@ int phs_abi_version(void) { return 107; }
 
 void phs_debug_set_spin_limit(unsigned polls) { phs::g_spin_limit.store(polls, std::memory_order_relaxed); }
 
+void phs_debug_set_aggregates_only(int on) { phs::g_agg_only.store(on != 0, std::memory_order_relaxed); }
+
+void phs_debug_time_next_launch(void *start_event, void *stop_event) {
+  std::lock_guard<std::mutex> lock(phs::g_timing.mu);
+  phs::g_timing.start = static_cast<hipEvent_t>(start_event);
+  phs::g_timing.stop = static_cast<hipEvent_t>(stop_event);
+  phs::g_timing.armed.store(start_event != nullptr || stop_event != nullptr, std::memory_order_release);
+}
+
 #define PHS_FWD(NAME, ALGT, TV)                                                                    \
   int NAME(int dtype, int64_t B, int64_t T, const void *A, int coef_shared, const void *zi,        \
            const void *x, void *y, void *workspace, size_t workspace_bytes, void *stream) {        \
@@ -70,3 +81,4 @@ PHS_FWD(phs_lti_recur2_fwd, Block2, false)
 PHS_BWD(phs_lti_recur2_bwd, Block2, false)
 
 }  // extern "C"
+

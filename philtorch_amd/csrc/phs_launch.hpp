@@ -9,6 +9,7 @@
 // per-step scratch.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -27,7 +28,40 @@ inline constexpr size_t kAlign = 256;
 // of waiting, far beyond any schedule in which predecessors make progress.
 inline constexpr unsigned kDefaultSpinLimit = 1u << 16;
 extern std::atomic<unsigned> g_spin_limit;  // testing hook, 0 = default (phs_capi.hip)
+extern std::atomic<bool> g_agg_only;        // testing hook (phs_capi.hip)
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+// Measurement hook (phs_debug_time_next_launch): a pair of events that the
+// next main-kernel launch of the library records around the kernel itself
+// (hipExtLaunchKernelGGL), so their elapsed time is that kernel's own
+// duration, dispatch to completion, with no event packets in between.  Taken
+// (and cleared) by that launch.
+struct TimingHook {
+  std::atomic<bool> armed{false};
+  std::mutex mu;
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+extern TimingHook g_timing;  // phs_capi.hip
+
+inline bool take_timing(hipEvent_t &start, hipEvent_t &stop) {
+  if (!g_timing.armed.load(std::memory_order_acquire)) return false;
+  std::lock_guard<std::mutex> lock(g_timing.mu);
+  if (!g_timing.armed.load(std::memory_order_relaxed)) return false;
+  start = g_timing.start;
+  stop = g_timing.stop;
+  g_timing.armed.store(false, std::memory_order_relaxed);
+  return true;
+}
+
+// Launch of a library kernel on `stream`, timed when the hook is armed.
+template <typename F, typename... Args>
+void launch_kernel(F kernel, dim3 grid, dim3 block, unsigned lds, hipStream_t stream, Args... args) {
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (take_timing(start, stop))
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, start, stop, 0u, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+}
 
 struct Layout {
   int64_t tiles_per_row = 0;
@@ -80,7 +114,7 @@ inline int64_t resident_groups(const void *kernel, int threads) {
 
 template <class Alg, bool TV, bool REV>
 void launch_scan(const ScanArgs<Alg> &a, unsigned grid, hipStream_t stream) {
-  hipLaunchKernelGGL((scan_kernel<Alg, TV, REV>), dim3(grid), dim3(Shape<Alg, TV>::kThreads), 0, stream, a);
+  launch_kernel(scan_kernel<Alg, TV, REV>, dim3(grid), dim3(Shape<Alg, TV>::kThreads), 0, stream, a);
 }
 
 template <class Alg>
@@ -116,6 +150,7 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
   a.per_stripe = (tiles + kStripes - 1) / kStripes;
   const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
   a.spin_limit = sl ? sl : kDefaultSpinLimit;
+  a.agg_only = g_agg_only.load(std::memory_order_relaxed) ? 1u : 0u;
   if (backward && gcoef) {
     if (TV)
       a.gcoef = shared ? reinterpret_cast<E *>(ws + L.scratch_off) : static_cast<E *>(gcoef);
@@ -136,7 +171,7 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
   // wave can poll for it while the data waves are still loading; with
   // smaller B those early polls mostly fail and only add status traffic.
   a.early_polls = 0;
-  if (Alg::kLookbackWave) {
+  if (Alg::kLookbackWave && !a.agg_only) {
     const int threads = TV ? Shape<Alg, true>::kThreads : Shape<Alg, false>::kThreads;
     const int64_t resident = resident_groups(kernel, threads);
     if (resident > 0 && 2 * B >= resident) a.early_polls = a.spin_limit;

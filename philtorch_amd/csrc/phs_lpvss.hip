@@ -52,11 +52,12 @@ int lpv_ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, LpvOperand<typena
   a.per_stripe = (a.tiles + kStripes - 1) / kStripes;
   const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
   a.spin_limit = sl ? sl : kDefaultSpinLimit;
+  a.agg_only = g_agg_only.load(std::memory_order_relaxed) ? 1u : 0u;
   a.vec_ok = (size_t(T) * sizeof(E)) % 16 == 0 && aligned16(x) && aligned16(y) && aligned16(A);
   if (rev)
-    hipLaunchKernelGGL((lpv_ss_kernel<Alg, true>), dim3(a.per_stripe * kStripes), dim3(Sh::kThreads), 0, stream, a);
+    launch_kernel((lpv_ss_kernel<Alg, true>), dim3(a.per_stripe * kStripes), dim3(Sh::kThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL((lpv_ss_kernel<Alg, false>), dim3(a.per_stripe * kStripes), dim3(Sh::kThreads), 0, stream, a);
+    launch_kernel((lpv_ss_kernel<Alg, false>), dim3(a.per_stripe * kStripes), dim3(Sh::kThreads), 0, stream, a);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 

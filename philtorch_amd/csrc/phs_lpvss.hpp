@@ -46,6 +46,7 @@ struct LpvSsArgs {
   int64_t B, T_len, tiles_per_row;
   unsigned long long *claims;
   unsigned tiles, per_stripe, spin_limit;
+  unsigned agg_only;  // testing: tiles after a row's first publish no inclusive state
   uint64_t *status;
   int vec_ok;
 };
@@ -235,7 +236,8 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
       if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
         yin = lpv_prefix_fallback<Alg, REV>(a, b, q * Sh::kTile, lane, virt);
     }
-    if (q + 1 < a.tiles_per_row && lane == 0) publish(row_status + q * St::kStride, apply<Alg>(tagg, yin), tag);
+    if (q + 1 < a.tiles_per_row && lane == 0 && !(a.agg_only && q > 0))
+      publish(row_status + q * St::kStride, apply<Alg>(tagg, yin), tag);
     if (lane == 0) s_in = yin;
     __syncthreads();  // entry state is in s_in
     return;

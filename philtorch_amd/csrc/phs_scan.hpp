@@ -118,6 +118,7 @@ struct ScanArgs {
   unsigned tiles;              // B * tiles_per_row
   unsigned per_stripe;         // claims per stripe (grid = per_stripe * kStripes)
   unsigned spin_limit;         // look-back polls before the self-compute fallback
+  unsigned agg_only;           // testing: tiles after a row's first publish no inclusive state
   uint64_t *status;          // status words of this call
   int vec_ok;
 };
@@ -419,43 +420,40 @@ __device__ __noinline__ typename Alg::state row_prefix_fallback(const typename A
 }
 
 // ------------------------------------------------------------ tile look-back
-// Look-back of tile (row b, scan position qs), run by one wave between the
-// "wave aggregates ready" and "entry state ready" barriers: combine the wave
-// aggregates from s_wagg (exclusive prefixes to s_wpre), publish the tile's
-// aggregate, find the state entering the tile (s_in), publish the inclusive
-// state.
+// The tile's aggregate: the wave aggregates of s_wagg folded in wave order.
+template <class Alg, int kWaves>
+__device__ __forceinline__ Map<Alg> tile_aggregate(const Map<Alg> *s_wagg) {
+  Map<Alg> t = s_wagg[0];
+#pragma unroll
+  for (int j = 1; j < kWaves; ++j) t = compose<Alg>(t, s_wagg[j]);
+  return t;
+}
+
+// State entering tile qs of row b (scan order), found by one wave after the
+// tile's aggregate `tagg` is known: publish it, look back over the
+// predecessors (or fold the row prefix from the inputs once the poll budget
+// is spent), publish the inclusive state.  `known`: the state is already in
+// `yin` (the row's first tile, or an early look-back that resolved).
 template <class Alg, bool TV, bool REV>
-__device__ __forceinline__ void tile_lookback(const ScanArgs<Alg> &a, int64_t qs, int64_t b, unsigned tag,
-                                              int lane, const Map<Alg> *s_wagg, Map<Alg> *s_wpre,
-                                              typename Alg::state *s_in, uint64_t *s_look) {
-  using S = typename Alg::state;
+__device__ __forceinline__ typename Alg::state tile_entry(const ScanArgs<Alg> &a, int64_t qs, int64_t b,
+                                                          unsigned tag, int lane, const Map<Alg> &tagg, bool known,
+                                                          typename Alg::state yin, Lookback<Alg> &lb,
+                                                          uint64_t *s_look) {
   using SC = typename Alg::s_coef;
   using SS = typename Alg::s_state;
-  using M = Map<Alg>;
   using Sh = Shape<Alg, TV>;
-  constexpr int kWaves = Sh::kWaves;
-  auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
-  M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
-  v = wave_scan_incl(v, lane, op);
-  const M wex = wave_shift_up(v, lane, map_identity<Alg>());
-  if (lane < kWaves) s_wpre[lane] = wex;
-  const M tagg = read_lane(v, kWaves - 1);
   uint64_t *row_status = a.status + b * a.tiles_per_row * Sh::kStride;
-  const S virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
-  S yin;
-  if (qs == 0) {
-    yin = virt;
-  } else {
-    if (lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
-    Lookback<Alg> lb = lookback_start<Alg>(qs);
+  const typename Alg::state virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
+  if (!known) {
     if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
       yin = row_prefix_fallback<Alg, TV, REV>(reinterpret_cast<const SS *>(a.x) + b * a.T_len,
                                               reinterpret_cast<const SC *>(a.coef) + b * a.coef_row_stride,
-                                              a.T_len, a.vec_ok != 0, qs * Sh::kTile,
-                                              a.tiles_per_row * Sh::kTile, lane, virt);
+                                              a.T_len, a.vec_ok != 0, qs * Sh::kTile, a.tiles_per_row * Sh::kTile,
+                                              lane, virt);
   }
-  if (qs + 1 < a.tiles_per_row && lane == 0) publish(row_status + qs * Sh::kStride, apply<Alg>(tagg, yin), tag);
-  if (lane == 0) *s_in = yin;
+  if (qs + 1 < a.tiles_per_row && lane == 0 && !(a.agg_only && qs > 0))
+    publish(row_status + qs * Sh::kStride, apply<Alg>(tagg, yin), tag);
+  return yin;
 }
 
 // ------------------------------------------------------------ the kernel
@@ -467,6 +465,22 @@ __device__ __forceinline__ void tile_lookback(const ScanArgs<Alg> &a, int64_t qs
 // Scan order is always ascending in (wave, round, lane); REV mirrors the
 // placement of waves, rounds and lanes in memory instead, so one DPP scan
 // serves both directions.  Inside a lane's K steps REV walks downwards.
+//
+// Speculative pass 2 (Alg::kSpeculate).  Right after round r's wave scan a
+// lane knows the map E from the start of its wave's segment to the start of
+// its chunk; the true start state is store_s(E.A h + E.x) for the state h
+// entering the segment, which the look-back and the other waves' aggregates
+// fix only later.  Where E.A is negligible (Alg::negligible: below the
+// storage precision's rounding for states of ordinary size) the lane runs
+// pass 2 from store_s(E.x) at once and writes the round's outputs while the
+// later rounds are still loading; once h is known it recomputes only its
+// start state and runs pass 2 again, rewriting its outputs, if and only if
+// that start state differs in any bit.  The memory then holds exactly what
+// pass 2 from the true entry state writes, whatever was speculated.  For
+// contractive recurrences (|a| < 1, products decaying along the segment)
+// only the first steps of each wave's segment wait for the look-back, so
+// the tile streams: round r's stores overlap round r+1's loads, and the
+// look-back's latency overlaps both.
 //
 // Where the algebra asks for it (Alg::kLookbackWave), the look-back runs in
 // a wave of its own that holds no tile data.  Run by data wave 0 instead, its
@@ -483,14 +497,14 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
   using SC = typename Alg::s_coef;   // storage types
   using SS = typename Alg::s_state;
   using M = Map<Alg>;
+  using AC = typename Alg::acc_coef;
   using Sh = Shape<Alg, TV>;
   constexpr int K = Sh::K, R = Sh::R, kWaves = Sh::kWaves;
 
   __shared__ M s_wagg[kWaves];
-  __shared__ M s_wpre[kWaves];
   __shared__ S s_in;
   __shared__ unsigned s_id, s_tag;
-  __shared__ typename Alg::acc_coef s_acc[kWaves];
+  __shared__ AC s_acc[kWaves];
   __shared__ uint64_t s_look[Sh::kLookWords];
   __shared__ unsigned s_ready;  // data waves whose aggregate is in s_wagg
 
@@ -525,10 +539,10 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
   // only LTI coefficients reduce their gradient inside the kernel (backward)
   constexpr bool kAcc = REV && !TV;
   const bool want_acc = kAcc && a.partials != nullptr;
+  uint64_t *row_status = a.status + b * a.tiles_per_row * Sh::kStride;
 
   if (Sh::kLookbackWave && w == kWaves) {
     // ================= look-back wave
-    uint64_t *row_status = a.status + b * a.tiles_per_row * Sh::kStride;
     const S virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
     Lookback<Alg> lb = lookback_start<Alg>(qs);
     S yin = virt;
@@ -543,18 +557,9 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
       __builtin_amdgcn_s_sleep(1);
     }
     __syncthreads();  // wave aggregates are in s_wagg
-    M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
-    v = wave_scan_incl(v, lane, op);
-    const M wex = wave_shift_up(v, lane, map_identity<Alg>());
-    if (lane < kWaves) s_wpre[lane] = wex;
-    const M tagg = read_lane(v, kWaves - 1);
-    if (!known) {
-      if (lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
-      if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
-        yin = row_prefix_fallback<Alg, TV, REV>(xrow, crow, T, vec, qs * Sh::kTile, a.tiles_per_row * Sh::kTile,
-                                                lane, virt);
-    }
-    if (qs + 1 < a.tiles_per_row && lane == 0) publish(row_status + qs * Sh::kStride, apply<Alg>(tagg, yin), tag);
+    const M tagg = tile_aggregate<Alg, kWaves>(s_wagg);
+    if (!known && lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
+    yin = tile_entry<Alg, TV, REV>(a, qs, b, tag, lane, tagg, known, yin, lb, s_look);
     if (lane == 0) s_in = yin;
     __syncthreads();  // entry state published to the data waves
     if (want_acc) __syncthreads();  // the data waves' gradient reduction
@@ -594,53 +599,27 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
     }
   }
 
-  // ---- pass 1: lane maps, wave scans, round chaining
-  M Ex[R];
-  M carry = map_identity<Alg>();
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    M m = lane_map<Alg, TV, REV, K>(A[TV ? r : 0], X[r], a_row_s);
-    m = wave_scan_incl(m, lane, op);
-    const M ex = wave_shift_up(m, lane, map_identity<Alg>());
-    const M tot = read_lane(m, 63);
-    Ex[r] = compose<Alg>(carry, ex);
-    carry = compose<Alg>(carry, tot);
-  }
-  if (lane == 0) {
-    s_wagg[w] = carry;
-    if (Sh::kLookbackWave) __hip_atomic_fetch_add(&s_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  __syncthreads();  // wave aggregates are in s_wagg
-  if (!Sh::kLookbackWave && w == 0) tile_lookback<Alg, TV, REV>(a, qs, b, tag, lane, s_wagg, s_wpre, &s_in, s_look);
-  __syncthreads();  // entry state is in s_in
-  const S hw = apply<Alg>(s_wpre[w], s_in);
-
-  // ---- pass 2
-  if constexpr (!REV) {
-    SS *yrow = reinterpret_cast<SS *>(a.out) + b * T;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      SS h = Alg::store_s(apply<Alg>(Ex[r], hw));
+  // ---- pass 2 of round r from the stored start state h, writing its outputs
+  SS *yrow = REV ? nullptr : reinterpret_cast<SS *>(a.out) + b * T;
+  SS *gxrow = (REV && a.out) ? reinterpret_cast<SS *>(a.out) + b * T : nullptr;
+  SC *gcrow = (REV && a.gcoef) ? reinterpret_cast<SC *>(a.gcoef) + b * T : nullptr;
+  // backward: y[t0-1] of each round sits in the last step of the next lane's
+  // chunk (lanes are mirrored), or below the round for lane 63 (set, by a
+  // shuffle, outside the per-lane branches of pass 2)
+  SS Ybelow[REV ? R : 1];
+  auto pass2 = [&](int r, SS h) -> AC {
+    AC acc = Alg::acc_zero();
+    const int64_t t0 = chunk0(r);
+    if constexpr (!REV) {
       SS O[K];
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         h = Alg::s_affine(TV ? A[r][TV ? k : 0] : a_row_s, h, X[r][k]);
         O[k] = h;
       }
-      store_chunk<SS, K>(yrow, chunk0(r), T, vec, O);
-    }
-  } else {
-    SS *gxrow = a.out ? reinterpret_cast<SS *>(a.out) + b * T : nullptr;
-    SC *gcrow = a.gcoef ? reinterpret_cast<SC *>(a.gcoef) + b * T : nullptr;
-    typename Alg::acc_coef acc = Alg::acc_zero();
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t t0 = chunk0(r);
-      // y[t0-1] sits in the last step of the next lane's chunk (lanes are
-      // mirrored), or below the round for lane 63
-      SS ybelow = shfl_from(Y[r][K - 1], lane + 1);
-      if (lane == 63) ybelow = Ylow[r];
-      SS nu = Alg::store_s(apply<Alg>(Ex[r], hw));
+      store_chunk<SS, K>(yrow, t0, T, vec, O);
+    } else {
+      SS nu = h;
       SS GX[K];
       SC GC[K];
 #pragma unroll
@@ -649,7 +628,7 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
         const SC c = Alg::s_adjoint(TV ? A[r][TV ? k : 0] : a_row_s);
         const SS lam = Alg::s_add(X[r][k], nu);
         GX[k] = lam;
-        const SC g = Alg::s_outer(lam, k == 0 ? ybelow : Y[r][k > 0 ? k - 1 : 0]);
+        const SC g = Alg::s_outer(lam, k == 0 ? Ybelow[r] : Y[r][k > 0 ? k - 1 : 0]);
         GC[k] = g;
         if constexpr (kAcc) {
           if (want_acc && t0 + k < T) acc = Alg::acc_add(acc, Alg::load_c(g));
@@ -662,18 +641,75 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
         if (gcrow) store_chunk<SC, K>(gcrow, t0, T, vec, GC);
       }
     }
-    if (want_acc) {
-      // deterministic block reduction of the per-tile coefficient gradient
+    return acc;
+  };
+
+  // ---- pass 1: lane maps, wave scans, round chaining; speculative pass 2
+  // of each round as soon as its wave scan is done
+  constexpr bool kSpec = Alg::kSpeculate;
+  M E[R];  // map from the wave's start to this lane's chunk of round r
+  bool spec[R];
+  SS hs[R];
+  AC acc_s[kAcc ? R : 1];
+  M carry = map_identity<Alg>();
 #pragma unroll
-      for (int d = 32; d >= 1; d >>= 1) acc = Alg::acc_sum(acc, shfl_from(acc, lane ^ d));
-      if (lane == 0) s_acc[w] = acc;
-      __syncthreads();
-      if (tid == 0) {
-        typename Alg::acc_coef sum = s_acc[0];
+  for (int r = 0; r < R; ++r) {
+    M m = lane_map<Alg, TV, REV, K>(A[TV ? r : 0], X[r], a_row_s);
+    m = wave_scan_incl(m, lane, op);
+    const M ex = wave_shift_up(m, lane, map_identity<Alg>());
+    const M tot = read_lane(m, 63);
+    E[r] = compose<Alg>(carry, ex);
+    carry = compose<Alg>(carry, tot);
+    if constexpr (REV) {
+      Ybelow[r] = shfl_from(Y[r][K - 1], lane + 1);
+      if (lane == 63) Ybelow[r] = Ylow[r];
+    }
+    spec[r] = kSpec && Alg::negligible(E[r].A);
+    hs[r] = Alg::store_s(E[r].x);
+    AC v = Alg::acc_zero();
+    if (spec[r]) v = pass2(r, hs[r]);
+    if constexpr (kAcc) acc_s[r] = v;
+  }
+  if (lane == 0) {
+    s_wagg[w] = carry;
+    if (Sh::kLookbackWave) __hip_atomic_fetch_add(&s_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  __syncthreads();  // wave aggregates are in s_wagg
+  if (!Sh::kLookbackWave && w == 0) {
+    // look-back by data wave 0: publish the tile's aggregate, find its entry
+    const M tagg = tile_aggregate<Alg, kWaves>(s_wagg);
+    if (qs > 0 && lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
+    Lookback<Alg> lb = lookback_start<Alg>(qs);
+    const S virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
+    const S yin = tile_entry<Alg, TV, REV>(a, qs, b, tag, lane, tagg, qs == 0, virt, lb, s_look);
+    if (lane == 0) s_in = yin;
+  }
+  // the wave's exclusive prefix in the tile, folded by every wave itself
+  M wpre = map_identity<Alg>();
+  for (int j = 0; j < w; ++j) wpre = compose<Alg>(wpre, s_wagg[j]);
+  __syncthreads();  // entry state is in s_in
+
+  // ---- pass 2 from the true entry state where the speculation missed
+  const S hin = apply<Alg>(wpre, s_in);  // state entering this wave's segment
+  AC acc = Alg::acc_zero();
 #pragma unroll
-        for (int i = 1; i < kWaves; ++i) sum = Alg::acc_sum(sum, s_acc[i]);
-        reinterpret_cast<typename Alg::acc_coef *>(a.partials)[b * a.tiles_per_row + qf] = sum;
-      }
+  for (int r = 0; r < R; ++r) {
+    const SS h = Alg::store_s(apply<Alg>(E[r], hin));
+    AC v = kAcc ? acc_s[kAcc ? r : 0] : Alg::acc_zero();
+    if (!(spec[r] && same_bits(h, hs[r]))) v = pass2(r, h);
+    if constexpr (kAcc) acc = Alg::acc_sum(acc, v);
+  }
+  if (want_acc) {
+    // deterministic block reduction of the per-tile coefficient gradient
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) acc = Alg::acc_sum(acc, shfl_from(acc, lane ^ d));
+    if (lane == 0) s_acc[w] = acc;
+    __syncthreads();
+    if (tid == 0) {
+      AC sum = s_acc[0];
+#pragma unroll
+      for (int i = 1; i < kWaves; ++i) sum = Alg::acc_sum(sum, s_acc[i]);
+      reinterpret_cast<AC *>(a.partials)[b * a.tiles_per_row + qf] = sum;
     }
   }
 }

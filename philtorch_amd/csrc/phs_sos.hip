@@ -74,6 +74,7 @@ void fill_common(SosArgs<E> &a, const SosLayout &L, int64_t B, int64_t T, int S,
   a.per_stripe = (a.tiles + kStripes - 1) / kStripes;
   const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
   a.spin_limit = sl ? sl : kDefaultSpinLimit;
+  a.agg_only = g_agg_only.load(std::memory_order_relaxed) ? 1u : 0u;
 }
 
 template <typename E>
@@ -95,7 +96,7 @@ int sos_fwd(int64_t B, int64_t T, int S, const void *sos, bool shared, const voi
   a.ckpt = static_cast<Vec2<typename Wide<E>::type> *>(ckpt);
   a.vec_ok = (size_t(T) * sizeof(E)) % 16 == 0 && aligned16(x) && aligned16(y);
   const unsigned grid = a.per_stripe * kStripes;
-  hipLaunchKernelGGL((sos_kernel<E, Sh, false, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
+  launch_kernel((sos_kernel<E, Sh, false, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
@@ -125,13 +126,13 @@ int sos_bwd(int64_t B, int64_t T, int S, const void *sos, bool shared, const voi
   const unsigned grid = a.per_stripe * kStripes;
   if (grad) {
     const size_t lds = size_t(S) * Sh::kWaves * Sh::R * 64 * sizeof(Vec2<E>);
-    hipLaunchKernelGGL((sos_kernel<E, Sh, true, true>), dim3(grid), dim3(Sh::kThreads), lds, stream, a);
+    launch_kernel((sos_kernel<E, Sh, true, true>), dim3(grid), dim3(Sh::kThreads), lds, stream, a);
     if (hipGetLastError() != hipSuccess) return PHS_ERR_LAUNCH;
     const int64_t rows = shared ? 1 : B;
     hipLaunchKernelGGL((sos_grad_reduce_kernel<E, Sh>), dim3(unsigned(rows * S)), dim3(kSosReduceThreads), 0,
                        stream, a, static_cast<E *>(gsos), rows);
   } else {
-    hipLaunchKernelGGL((sos_kernel<E, Sh, true, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
+    launch_kernel((sos_kernel<E, Sh, true, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
   }
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }

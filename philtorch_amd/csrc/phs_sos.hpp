@@ -77,6 +77,7 @@ struct SosArgs {
   unsigned tiles;              // B * tiles_per_row
   unsigned per_stripe;         // claims per stripe (grid = per_stripe * kStripes)
   unsigned spin_limit;         // look-back polls before the self-compute fallback
+  unsigned agg_only;           // testing: tiles after a row's first publish no inclusive state
   uint64_t *status;            // [B, S, tiles, kStride] status words of this call
   int vec_ok;
 };
@@ -772,7 +773,8 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
         if (!sos_lookback<E>(row_status, virt, lane, tag, a.spin_limit, s_look, tp, qs, yin))
           yin = sos_prefix_fallback<E, Sh, REV>(a, b, s, qs * Sh::kTile, lane, s_look);
       }
-      if (qs + 1 < tiles && lane == 0) publish(row_status + qs * kSosStatusWords, Alg::affine(Mp[W], yin, pv), tag);
+      if (qs + 1 < tiles && lane == 0 && !(a.agg_only && qs > 0))
+        publish(row_status + qs * kSosStatusWords, Alg::affine(Mp[W], yin, pv), tag);
       if (lane == 0) s_in = yin;
       __syncthreads();  // entry state is in s_in
       if (v + 2 < nvis) build_powers<E, K, R>(&s_pow[(v + 2) % 3], load_sec(sosrow, vis_sec(v + 2)), lane);

@@ -54,13 +54,14 @@ bool ss_args(int64_t B, int64_t T, const SsFilter &f, const void *zi, const void
   a.per_stripe = (a.tiles + kStripes - 1) / kStripes;
   const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
   a.spin_limit = sl ? sl : kDefaultSpinLimit;
+  a.agg_only = g_agg_only.load(std::memory_order_relaxed) ? 1u : 0u;
   a.vec_ok = (size_t(T) * sizeof(E)) % 16 == 0 && aligned16(x) && aligned16(y);
   return true;
 }
 
 template <class Alg, bool REV>
 int ss_launch(const SsArgs<Alg> &a, hipStream_t stream) {
-  hipLaunchKernelGGL((ss_kernel<Alg, REV>), dim3(a.per_stripe * kStripes), dim3(SsShape<Alg>::kThreads), 0, stream,
+  launch_kernel((ss_kernel<Alg, REV>), dim3(a.per_stripe * kStripes), dim3(SsShape<Alg>::kThreads), 0, stream,
                      a);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }

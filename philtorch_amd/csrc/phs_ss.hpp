@@ -70,6 +70,7 @@ struct SsArgs {
   int64_t B, T_len, tiles_per_row;
   unsigned long long *claims;
   unsigned tiles, per_stripe, spin_limit;
+  unsigned agg_only;  // testing: tiles after a row's first publish no inclusive state
   uint64_t *status;
   int vec_ok;
 };
@@ -674,7 +675,7 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
       if (!ss_lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, &s_tab, q, yin))
         yin = ss_prefix_fallback<Alg, Sh, REV>(a, b, q * Sh::kTile, lane, virt, &s_tab);
     }
-    if (q + 1 < a.tiles_per_row && lane == 0)
+    if (q + 1 < a.tiles_per_row && lane == 0 && !(a.agg_only && q > 0))
       publish(row_status + q * St::kStride, Alg::affine(s_tab.gp[0], yin, tagg), tag);
     if (lane == 0) s_in = yin;
     __syncthreads();  // entry state is in s_in

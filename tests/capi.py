@@ -59,6 +59,13 @@ def load() -> ctypes.CDLL:
     lib.phs_error_string.restype = ctypes.c_char_p
     lib.phs_debug_set_spin_limit.argtypes = [ctypes.c_uint]
     lib.phs_debug_set_spin_limit.restype = None
+    lib.phs_debug_set_aggregates_only.argtypes = [ctypes.c_int]
+    lib.phs_debug_set_aggregates_only.restype = None
+    lib.phs_debug_time_next_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.phs_debug_time_next_launch.restype = None
+    lib.phs_stream_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p]
+    lib.phs_stream_probe.restype = ctypes.c_int
     # fused cascade of second-order sections
     lib.phs_sosfilt_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                                ctypes.c_int]

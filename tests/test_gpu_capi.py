@@ -252,3 +252,46 @@ def test_capi_errors(api):
     assert lib.phs_recur_fwd(0, 0, 100, None, 0, None, None, None, None, 0, s) == capi.PHS_OK
     assert lib.phs_recur_fwd(0, 2, 0, None, 0, None, None, None, None, 0, s) == capi.PHS_OK
     assert b"workspace" in lib.phs_error_string(capi.PHS_ERR_WORKSPACE)
+
+
+# Look-back past the first window: with phs_debug_set_aggregates_only every
+# tile after a row's first publishes only its aggregate, so tile q folds all
+# q - 1 aggregates back to tile 0's state, window after window (64 entries
+# each, after a first window of 8 for scalar scans).  Rows of 100-170 tiles
+# per algebra and tile shape.
+AGG_ONLY = [
+    ("recur", 2, 100 * 8192 + 5, np.float32, False),         # scalar LPV: 8192-step tiles
+    ("recur", 2, 150 * 1536 + 7, np.complex64, False),       # complex LPV: 1536
+    ("lti_recur", 2, 120 * 3072 + 1, np.complex64, False),   # complex LTI: 3072
+    ("lti_recur", 3, 170 * 4096, np.float64, True),          # fp64 scalar: 4096
+    ("recur2", 2, 150 * 1536 + 3, np.float32, False),        # 2x2 LPV: 1536
+    ("lti_recur2", 2, 140 * 3072 + 9, np.float32, True),     # 2x2 LTI: 3072
+    ("lti_recur2", 2, 170 * 384 + 1, np.complex128, False),  # complex 2x2: 384
+]
+
+
+@pytest.mark.parametrize("op,B,T,dtype,shared", AGG_ONLY)
+def test_capi_aggregates_only_multi_window(api, op, B, T, dtype, shared):
+    lib = api[0]
+    A, zi, x, gy = _case(op, B, T, dtype, shared, D.seed_of("agg-only", op, B, T, np.dtype(dtype).str))
+    print(f"aggregates-only {op} B={B} T={T} {np.dtype(dtype).name}", flush=True)
+    lib.phs_debug_set_aggregates_only(1)
+    try:
+        got = _run(api, op, A, zi=zi, x=x, gy=gy, shared=shared)
+    finally:
+        lib.phs_debug_set_aggregates_only(0)
+    _check(got, _oracle(op, A, zi, x, gy))
+
+
+@pytest.mark.parametrize("op,M,B,T,dtype", [("recurN", 3, 2, 100 * 1536 + 1, np.float32),
+                                            ("lti_recurN", 4, 2, 130 * 768 + 3, np.complex64)])
+def test_capi_order_n_aggregates_only(api, op, M, B, T, dtype):
+    lib = api[0]
+    A, zi, x, gy = _case_n(op, M, B, T, dtype, False, D.seed_of("agg-only-n", op, M, B, T))
+    print(f"aggregates-only {op} M={M} B={B} T={T} {np.dtype(dtype).name}", flush=True)
+    lib.phs_debug_set_aggregates_only(1)
+    try:
+        got = _run(api, op, A, zi=zi, x=x, gy=gy, shared=False, M=M)
+    finally:
+        lib.phs_debug_set_aggregates_only(0)
+    _check(got, _oracle_n(op, A, zi, x, gy))

@@ -304,3 +304,25 @@ def test_lpv_ss_op_gradients_and_opcheck(hip):
                           (s(_model(g, M, Bn, 500, False)), None, s(g.standard_normal((Bn, 1, M))), None,
                            s(g.standard_normal((Bn, M))), s(g.standard_normal((Bn, 500))), 0, True),
                           test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_lpv_ss_capi_aggregates_only_multi_window(api, dtype, M):
+    """Tiles after a row's first publish aggregates only (testing hook): every
+    look-back folds back to tile 0 through several 64-tile windows."""
+    lib = api[0]
+    g = D.rng(D.seed_of("lpv-ss-agg-only", dtype, M))
+    Bn, T = 2, 300_007
+    A = _model(g, M, Bn, T, False).astype(dtype)
+    b, c, d = (_layout(g, "rowstep", Bn, T, w).astype(dtype) for w in (M, M, 0))
+    x = g.standard_normal((Bn, T)).astype(dtype)
+    zi = g.standard_normal((Bn, M)).astype(dtype)
+    lib.phs_debug_set_aggregates_only(1)
+    try:
+        got = _run(api, A, b, c, d, zi, x)
+        got_rev = _run(api, A, b, c, d, zi, x, rev=True)
+    finally:
+        lib.phs_debug_set_aggregates_only(0)
+    _check(got, A, b, c, d, zi, x, 0, dtype, "aggregates only")
+    _check(got_rev, A, b, c, d, zi, x, 0, dtype, "aggregates only rev", rev=True)

@@ -342,3 +342,18 @@ def test_lfilter_fused_route_second_order_gradients(hip):
         tangent = fwad.unpack_dual(y).tangent
     ref = hip.lti.lfilter(b.detach(), a.detach(), torch.ones_like(x), unroll_factor=1)
     D.check(tangent.cpu().numpy(), ref.cpu().numpy(), "jvp")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_sosfilt_capi_aggregates_only_multi_window(api, dtype):
+    """Tiles after a row's first publish aggregates only (testing hook): every
+    section's look-back folds back to tile 0 through windows of 64 entries
+    (110+ tiles per row), forward cascade and adjoint cascade."""
+    lib = api[0]
+    case = _case(dtype, 2, 110 * 6144 + 3, 3, False, True, True, D.seed_of("sos-agg-only", dtype))
+    lib.phs_debug_set_aggregates_only(1)
+    try:
+        got = _run(api, *case)
+    finally:
+        lib.phs_debug_set_aggregates_only(0)
+    _check_all(got, *case, dtype, "aggregates only")

@@ -500,3 +500,21 @@ def test_reversed_ops_gradients_and_opcheck(hip):
                           (s(A[0]), s(b[0]), None, None, s(g.standard_normal((2, 3))), s(g.standard_normal((2, 500))),
                            1, True))
 
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("M", [2, 4])
+def test_lti_ss_capi_aggregates_only_multi_window(api, dtype, M):
+    """Tiles after a row's first publish aggregates only (testing hook), so
+    every look-back folds back to tile 0 through windows of 64 entries: 110
+    tiles of 6144 (fp32) or fewer steps per row, both time directions."""
+    lib = api[0]
+    A, b, c, d, zi, x = _case(dtype, M, 2, 110 * 6144 + 5, False, D.seed_of("ss-agg-only", dtype, M))
+    lib.phs_debug_set_aggregates_only(1)
+    try:
+        got = _run(api, A, b, c, d, zi, x)
+        got_rev = _run(api, A, b, c, d, zi, x, rev=True)
+    finally:
+        lib.phs_debug_set_aggregates_only(0)
+    _check(got, A, b, c, d, zi, x, None, dtype, "aggregates only")
+    _check(got_rev, A, b, c, d, zi, x, None, dtype, "aggregates only rev", rev=True)
