@@ -60,7 +60,8 @@ enum phs_status {
   PHS_ERR_INVALID = 1,   /* bad size, null required pointer, unsupported combination */
   PHS_ERR_WORKSPACE = 2, /* workspace NULL or smaller than phs_workspace_size() */
   PHS_ERR_LAUNCH = 3,    /* the HIP runtime rejected a kernel launch */
-  PHS_ERR_DTYPE = 4      /* dtype not one of phs_dtype */
+  PHS_ERR_DTYPE = 4,     /* dtype not one of phs_dtype */
+  PHS_ERR_TOO_LARGE = 5  /* beyond PHS_NOALLOC_SCRATCH_BYTES (phs_recur_fwd_noalloc only) */
 };
 
 /* Bytes of workspace that one call of `op` needs (backward != 0 for the
@@ -115,6 +116,22 @@ void phs_debug_time_next_launch(void *start_event, void *stop_event);
  * no native op of its own. */
 int phs_recur_fwd(int dtype, int64_t B, int64_t T, const void *A, int coef_shared, const void *zi,
                   const void *x, void *y, void *workspace, size_t workspace_bytes, void *stream);
+
+/* phs_recur_fwd without a workspace argument: allocates nothing, takes no
+ * workspace.  No counterpart in the reference; for callers that cannot
+ * allocate or hand over device memory: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  Its workspace is a static
+ * device array of PHS_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends (at most B * ceil(T / tile) tiles of 48 bytes for fp32/fp64 after a
+ * 2 KiB header: about 716 M fp32 samples in 8192-step tiles); larger
+ * problems return PHS_ERR_TOO_LARGE without launching anything.  The array
+ * is cleared by a kernel on the first call on each device (and every 2^30
+ * calls); every call on one GPU shares it and leaves it ready for the next,
+ * so calls on one GPU must be ordered (one stream, or synchronised):
+ * overlapping calls race.  Results are bit-identical to phs_recur_fwd's. */
+#define PHS_NOALLOC_SCRATCH_BYTES (4u << 20)
+int phs_recur_fwd_noalloc(int dtype, int64_t B, int64_t T, const void *A, int coef_shared, const void *zi,
+                          const void *x, void *y, void *stream);
 
 /* Backward of phs_recur_fwd.  y: the forward output.  grad_A: [B,T], or [T]
  * when coef_shared (summed over rows).  grad_zi: [B].  grad_x: [B,T].

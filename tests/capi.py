@@ -14,7 +14,7 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(REPO, "philtorch_amd", "libphilscan.so")
 HEADER = os.path.join(REPO, "include", "philscan.h")
 
-PHS_OK, PHS_ERR_INVALID, PHS_ERR_WORKSPACE, PHS_ERR_LAUNCH, PHS_ERR_DTYPE = range(5)
+PHS_OK, PHS_ERR_INVALID, PHS_ERR_WORKSPACE, PHS_ERR_LAUNCH, PHS_ERR_DTYPE, PHS_ERR_TOO_LARGE = range(6)
 # phs_padmode codes (torch.nn.functional.pad modes)
 PADMODES = {"constant": 0, "replicate": 1, "reflect": 2, "circular": 3}
 OPS = {"recur": 0, "lti_recur": 1, "recur2": 2, "lti_recur2": 3}
@@ -66,6 +66,9 @@ def load() -> ctypes.CDLL:
     lib.phs_stream_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p,
                                      ctypes.c_void_p, ctypes.c_void_p]
     lib.phs_stream_probe.restype = ctypes.c_int
+    lib.phs_recur_fwd_noalloc.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.phs_recur_fwd_noalloc.restype = ctypes.c_int
     # fused cascade of second-order sections
     lib.phs_sosfilt_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                                ctypes.c_int]
