@@ -1,11 +1,16 @@
 // torch.library layer of philtorch_amd: owns the `philtorch` operator
 // namespace with the reference's schemas (philtorch/csrc/host_recur2.cpp:162-171)
 // plus the new LPV scalar op `recur`, four fused backward ops and the fused
-// second-order-section cascade (`sosfilt`, `sosfilt_backward`), and binds
-// the HIP device key (PyTorch-ROCm names it CUDA) to the C ABI of
-// libphilscan.  No CPU kernels are registered: CPU tensors raise, and the
-// Python API keeps the reference's pure-PyTorch route for them.
+// filter ops (`sosfilt`, `filtfilt`, `lti_ss`, `lfilter_ss`, `lpv_ss`), and
+// binds the HIP device key (PyTorch-ROCm names it CUDA) to the C ABI of
+// libphilscan.  The CPU key serves the reference's five ops, `recur` and the
+// backward ops with the CPU kernels of phs_cpu.hpp, as the reference's CPU
+// extension does for its ops (host_recurN.cpp:283-287, host_lti_recur.cpp:
+// 82-85, host_lti_recurN.cpp:110-114); the filter ops are HIP-only (the
+// Python API composes them from the basic ops on CPU tensors).
 #include <ATen/ATen.h>
+#include <ATen/Dispatch.h>
+#include <ATen/Parallel.h>
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
@@ -18,6 +23,7 @@
 #include <vector>
 
 #include "../../include/philscan.h"
+#include "phs_cpu.hpp"
 
 namespace {
 
@@ -45,8 +51,6 @@ void check_common(const char *op, const Tensor &A, const Tensor &zi, const Tenso
   // message texts follow host_recurN.cpp:240-248 / host_lti_recur.cpp:45-50
   TORCH_CHECK(zi.scalar_type() == x.scalar_type(), "zi must have the same scalar type as input");
   TORCH_CHECK(A.scalar_type() == x.scalar_type(), "A must have the same scalar type as input");
-  TORCH_CHECK(x.is_cuda() && A.is_cuda() && zi.is_cuda(), "philtorch::", op,
-              ": philtorch_amd runs on HIP devices only (got ", x.device(), ")");
   TORCH_CHECK(A.device() == x.device() && zi.device() == x.device(), "philtorch::", op,
               ": all tensors must be on the same device");
   TORCH_CHECK(is_half(x.scalar_type()) || phs_dtype_of(x.scalar_type()) >= 0, "philtorch::", op,
@@ -697,6 +701,151 @@ std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tenso
   return {y, zf};
 }
 
+// ------------------------------------------------------------ CPU key
+// The reference's CPU extension registers its ops for the CPU key; these
+// run phs_cpu.hpp on contiguous copies, in parallel over rows (torch's
+// intra-op thread pool), serially in time.  Half and bfloat16 compute in fp32.
+template <class F>
+void parallel_rows(int64_t n, F &&f) {
+  at::parallel_for(0, n, 1, [&](int64_t begin, int64_t end) {
+    for (int64_t i = begin; i < end; ++i) f(i);
+  });
+}
+
+void check_cpu(const char *op, const Tensor &x) {
+  TORCH_CHECK(x.is_cpu(), "philtorch::", op, ": CPU kernel called with a ", x.device(), " tensor");
+}
+
+// y = scan(A, zi, x); x [B, T] or [B, T, M]; A laid out as L says.
+Tensor cpu_fwd(const Tensor &A, const Tensor &zi, const Tensor &x, phs_cpu::Layout L) {
+  Tensor Ac = A.contiguous(), zc = zi.contiguous(), xc = x.contiguous();
+  Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  if (L.B == 0 || L.T == 0) return y;
+  AT_DISPATCH_FLOATING_AND_COMPLEX_TYPES_AND1(at::kLong, x.scalar_type(), "philtorch_cpu_fwd", [&] {
+    phs_cpu::scan_fwd<scalar_t>(L, Ac.const_data_ptr<scalar_t>(), zc.const_data_ptr<scalar_t>(),
+                                xc.const_data_ptr<scalar_t>(), y.mutable_data_ptr<scalar_t>(),
+                                [](int64_t n, auto &&f) { parallel_rows(n, f); });
+  });
+  return y;
+}
+
+// (grad_A in A's shape, grad_zi, grad_x) of cpu_fwd for upstream grad gy.
+Triple cpu_bwd(const Tensor &A, const Tensor &zi, const Tensor &y, const Tensor &gy, phs_cpu::Layout L) {
+  Tensor Ac = A.contiguous(), zc = zi.contiguous(), yc = y.contiguous(), gc = gy.contiguous();
+  Tensor gA = at::empty(A.sizes(), A.options());
+  Tensor gzi = at::empty(zi.sizes(), zi.options());
+  Tensor gx = at::empty(y.sizes(), y.options());
+  if (L.B == 0 || L.T == 0) return {gA.zero_(), gzi.zero_(), gx.zero_()};
+  AT_DISPATCH_FLOATING_AND_COMPLEX_TYPES_AND1(at::kLong, y.scalar_type(), "philtorch_cpu_bwd", [&] {
+    phs_cpu::scan_bwd<scalar_t>(L, Ac.const_data_ptr<scalar_t>(), zc.const_data_ptr<scalar_t>(),
+                                yc.const_data_ptr<scalar_t>(), gc.const_data_ptr<scalar_t>(),
+                                gx.mutable_data_ptr<scalar_t>(), gA.mutable_data_ptr<scalar_t>(),
+                                gzi.mutable_data_ptr<scalar_t>(),
+                                [](int64_t n, auto &&f) { parallel_rows(n, f); });
+  });
+  return {gA, gzi, gx};
+}
+
+Tensor recur_cpu(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  check_common("recur", A, zi, x);
+  check_recur(A, zi, x);
+  check_cpu("recur", x);
+  if (is_half(x.scalar_type()))
+    return recur_cpu(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
+  const int64_t B = x.size(0), T = x.size(1);
+  return cpu_fwd(A, zi, x, {B, T, 1, A.dim() == 1 ? 0 : T, 1, false});
+}
+
+Triple recur_backward_cpu(const Tensor &A, const Tensor &zi, const Tensor &y, const Tensor &gy) {
+  check_common("recur_backward", A, zi, y);
+  check_recur(A, zi, y);
+  check_cpu("recur_backward", y);
+  TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
+  if (is_half(y.scalar_type()))
+    return to_dtype(recur_backward_cpu(A.to(at::kFloat), zi.to(at::kFloat), y.to(at::kFloat), gy.to(at::kFloat)),
+                    y.scalar_type());
+  const int64_t B = y.size(0), T = y.size(1);
+  return cpu_bwd(A, zi, y, gy.to(y.scalar_type()), {B, T, 1, A.dim() == 1 ? 0 : T, 1, false});
+}
+
+Tensor recurN_cpu(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  check_common("recurN", A, zi, x);
+  check_recurN(A, zi, x);
+  check_cpu("recurN", x);
+  if (is_half(x.scalar_type()))
+    return recurN_cpu(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
+  const int64_t B = x.size(0), T = x.size(1), M = A.size(-1);
+  return cpu_fwd(A, zi, x, {B, T, M, A.dim() == 3 ? 0 : T * M * M, M * M, false});
+}
+
+Tensor recur2_cpu(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  TORCH_CHECK(A.dim() >= 2 && A.size(-1) == 2 && A.size(-2) == 2, "A must be square.");
+  return recurN_cpu(A, zi, x);
+}
+
+Triple recurN_backward_cpu(const Tensor &A, const Tensor &zi, const Tensor &y, const Tensor &gy) {
+  check_common("recurN_backward", A, zi, y);
+  check_recurN(A, zi, y);
+  check_cpu("recurN_backward", y);
+  TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
+  if (is_half(y.scalar_type()))
+    return to_dtype(recurN_backward_cpu(A.to(at::kFloat), zi.to(at::kFloat), y.to(at::kFloat), gy.to(at::kFloat)),
+                    y.scalar_type());
+  const int64_t B = y.size(0), T = y.size(1), M = A.size(-1);
+  return cpu_bwd(A, zi, y, gy.to(y.scalar_type()), {B, T, M, A.dim() == 3 ? 0 : T * M * M, M * M, false});
+}
+
+Tensor lti_recur_cpu(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  check_common("lti_recur", A, zi, x);
+  check_lti_recur(A, zi, x);
+  check_cpu("lti_recur", x);
+  if (is_half(x.scalar_type()))
+    return lti_recur_cpu(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
+  const int64_t B = x.size(0), T = x.size(1);
+  return cpu_fwd(A, zi, x, {B, T, 1, lti_shared(A, x) ? 0 : 1, 0, true});
+}
+
+Triple lti_recur_backward_cpu(const Tensor &A, const Tensor &zi, const Tensor &y, const Tensor &gy) {
+  check_common("lti_recur_backward", A, zi, y);
+  check_lti_recur(A, zi, y);
+  check_cpu("lti_recur_backward", y);
+  TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
+  if (is_half(y.scalar_type()))
+    return to_dtype(lti_recur_backward_cpu(A.to(at::kFloat), zi.to(at::kFloat), y.to(at::kFloat),
+                                           gy.to(at::kFloat)),
+                    y.scalar_type());
+  const int64_t B = y.size(0), T = y.size(1);
+  return cpu_bwd(A, zi, y, gy.to(y.scalar_type()), {B, T, 1, lti_shared(A, y) ? 0 : 1, 0, true});
+}
+
+Tensor lti_recurN_cpu(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  check_common("lti_recurN", A, zi, x);
+  check_lti_recurN(A, zi, x);
+  check_cpu("lti_recurN", x);
+  if (is_half(x.scalar_type()))
+    return lti_recurN_cpu(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
+  const int64_t B = x.size(0), T = x.size(1), M = A.size(-1);
+  return cpu_fwd(A, zi, x, {B, T, M, A.dim() == 2 ? 0 : M * M, 0, false});
+}
+
+Tensor lti_recur2_cpu(const Tensor &A, const Tensor &zi, const Tensor &x) {
+  TORCH_CHECK(A.dim() >= 2 && A.size(-1) == 2 && A.size(-2) == 2, "A must be square.");
+  return lti_recurN_cpu(A, zi, x);
+}
+
+Triple lti_recurN_backward_cpu(const Tensor &A, const Tensor &zi, const Tensor &y, const Tensor &gy) {
+  check_common("lti_recurN_backward", A, zi, y);
+  check_lti_recurN(A, zi, y);
+  check_cpu("lti_recurN_backward", y);
+  TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
+  if (is_half(y.scalar_type()))
+    return to_dtype(lti_recurN_backward_cpu(A.to(at::kFloat), zi.to(at::kFloat), y.to(at::kFloat),
+                                            gy.to(at::kFloat)),
+                    y.scalar_type());
+  const int64_t B = y.size(0), T = y.size(1), M = A.size(-1);
+  return cpu_bwd(A, zi, y, gy.to(y.scalar_type()), {B, T, M, A.dim() == 2 ? 0 : M * M, 0, false});
+}
+
 }  // namespace
 
 TORCH_LIBRARY(philtorch, m) {
@@ -752,4 +901,17 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("lti_ss", &lti_ss_hip);
   m.impl("lfilter_ss", &lfilter_ss_hip);
   m.impl("lpv_ss", &lpv_ss_hip);
+}
+
+TORCH_LIBRARY_IMPL(philtorch, CPU, m) {
+  m.impl("recur2", &recur2_cpu);
+  m.impl("recurN", &recurN_cpu);
+  m.impl("lti_recur2", &lti_recur2_cpu);
+  m.impl("lti_recurN", &lti_recurN_cpu);
+  m.impl("lti_recur", &lti_recur_cpu);
+  m.impl("recur", &recur_cpu);
+  m.impl("recur_backward", &recur_backward_cpu);
+  m.impl("recurN_backward", &recurN_backward_cpu);
+  m.impl("lti_recur_backward", &lti_recur_backward_cpu);
+  m.impl("lti_recurN_backward", &lti_recurN_backward_cpu);
 }

@@ -18,7 +18,8 @@ from .. import EXTENSION_LOADED
 
 
 def _native_ok(a: Tensor, init: Tensor, x: Tensor) -> bool:
-    return EXTENSION_LOADED and x.is_cuda and a.is_cuda and init.is_cuda
+    """The native scan serves CPU and HIP tensors (all on one device)."""
+    return EXTENSION_LOADED and (x.is_cpu or x.is_cuda) and a.device == x.device and init.device == x.device
 
 
 def _scalar_recursion_loop(a: Tensor, init: Tensor, x: Tensor) -> Tensor:

@@ -24,10 +24,11 @@ from .. import EXTENSION_LOADED, HELION_LOADED
 
 
 def extension_backend_indicator(x: Tensor, M: int) -> bool:
-    """True when the native scan serves this input: extension loaded, the
-    tensor on a HIP device, and a state of order M <= 4 (the reference,
-    philtorch/lpv/ssm.py:20-26, has GPU kernels for M <= 2 only)."""
-    return EXTENSION_LOADED and x.is_cuda and M <= 4
+    """True when the native scan serves this input: extension loaded, and
+    the tensor on the CPU (any order) or on a HIP device with a state of
+    order M <= 4 (the reference, philtorch/lpv/ssm.py:20-26, takes the CPU
+    for any order and the GPU for M <= 2)."""
+    return EXTENSION_LOADED and (x.is_cpu or (x.is_cuda and M <= 4))
 
 
 class MatrixRecurrence(Function):

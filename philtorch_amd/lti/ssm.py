@@ -22,11 +22,12 @@ from .recur import LTIRecurrence, linear_recurrence
 
 
 def extension_backend_indicator(x: Tensor, M: int) -> bool:
-    """True when the native scan serves this input: extension loaded, tensor
-    on a HIP device, state of order 2 <= M <= 4 (M = 1 goes through
-    ``LTIRecurrence``).  The reference, philtorch/lti/ssm.py:13-25, has a GPU
-    kernel for M = 2 only."""
-    return EXTENSION_LOADED and x.is_cuda and 2 <= M <= 4
+    """True when the native matrix scan serves this input: extension loaded,
+    state of order M >= 2 (M = 1 goes through ``LTIRecurrence``), on the CPU
+    (any order) or on a HIP device (M <= 4).  The reference,
+    philtorch/lti/ssm.py:13-25, takes the CPU for M >= 2 and the GPU for
+    M = 2 only."""
+    return EXTENSION_LOADED and M >= 2 and (x.is_cpu or (x.is_cuda and M <= 4))
 
 
 def helion_backend_indicator(x: Tensor) -> bool:
@@ -145,7 +146,7 @@ def state_space_recursion(
         raise ValueError("Unroll factor must be >= 1")
     k = unroll_factor
     if k == 1 or k >= N:
-        if k == 1 and EXTENSION_LOADED and x.is_cuda and M <= 2:
+        if k == 1 and EXTENSION_LOADED and (x.is_cpu or (x.is_cuda and M <= 4)):
             return _ext_ss_recur(A, zi, x, out_idx=out_idx)
         return _recursion_loop(A, zi, x, out_idx=out_idx)
 
@@ -428,7 +429,7 @@ def diag_state_space(
     else:
         VBx = x @ Vinv.mT
 
-    native = EXTENSION_LOADED and x.is_cuda and unroll_factor in (None, 1)
+    native = EXTENSION_LOADED and (x.is_cpu or x.is_cuda) and unroll_factor in (None, 1)
     runner = LTIRecurrence.apply if native else partial(linear_recurrence, unroll_factor=unroll_factor)
     coef = L.broadcast_to((batch, M)).flatten(0, 1)
     if native:

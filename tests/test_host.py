@@ -115,11 +115,16 @@ def test_ops_registered_with_reference_schemas():
         assert schema.endswith("-> (Tensor, Tensor, Tensor)")
 
 
-def test_cpu_tensors_raise():
+def test_cpu_key_serves_the_scan_ops_only():
+    """The reference's ops, recur and the backward ops have CPU kernels (as
+    the reference registers its CPU extension); the fused filter ops are
+    HIP-only and raise on CPU tensors."""
     import philtorch_amd  # noqa: F401
 
+    y = torch.ops.philtorch.recur(torch.zeros(2, 3), torch.ones(2), torch.ones(2, 3))
+    assert y.tolist() == [[1.0, 1.0, 1.0]] * 2
     with pytest.raises(NotImplementedError):
-        torch.ops.philtorch.recur(torch.zeros(2, 3), torch.zeros(2), torch.zeros(2, 3))
+        torch.ops.philtorch.sosfilt(torch.zeros(1, 6), None, torch.zeros(2, 3))
 
 
 @pytest.mark.parametrize(
