@@ -343,21 +343,28 @@ int phs_lfilter_rev(int dtype, int64_t B, int64_t T, const void *b, int nb, cons
                     int form, const void *zi, const void *x, void *y, void *zf, void *workspace,
                     size_t workspace_bytes, void *stream);
 
+/* Flags of the A argument of phs_lpv_ss_fwd / phs_lpv_ss_rev (A_flags):
+ * PHS_LPV_A_SHARED, A is [T,M,M] and shared by the rows; PHS_LPV_A_TRANSPOSED,
+ * every step's matrix is read transposed, so the adjoint model's A[t]^T
+ * needs no transposed copy of A. */
+#define PHS_LPV_A_SHARED 1
+#define PHS_LPV_A_TRANSPOSED 2
+
 /* ---- Single-input, single-output LPV (time-varying) state space of order
  * M = 1..4, fused (forward).  Replaces philtorch.lpv.state_space
  * (philtorch/lpv/ssm.py:337-581, the glue :413-577) for a 2D input x:
  *     h[0] = zi,  y[t] = c[t] . h[t] + d[t] x[t],
  *     h[t+1] = A[t] h[t] + b[t] x[t],  zf = h[T]
  * in one pass: per step A[t], x[t] and the time-varying ones of b, c, d are
- * read and y[t] written.  dtype PHS_F32 or PHS_F64; A [B,T,M,M] (A_shared=0)
- * or [T,M,M]; b, c element (row, t, i) at ptr + row * row_stride +
+ * read and y[t] written.  dtype PHS_F32 or PHS_F64; A [B,T,M,M], or [T,M,M]
+ * with PHS_LPV_A_SHARED in A_flags (PHS_LPV_A_TRANSPOSED: use A[t]^T); b, c element (row, t, i) at ptr + row * row_stride +
  * t * t_stride + i and d element (row, t) at ptr + row * row_stride +
  * t * t_stride (strides in elements, >= 0; 0 shares that axis); b NULL: the
  * input enters state 0; c NULL: y is state out_idx; d NULL: no feedthrough;
  * zi [B,M] (NULL = zeros); x, y [B,T]; zf [B,M] (skipped when NULL). */
 size_t phs_lpv_ss_workspace_size(int dtype, int M, int64_t B, int64_t T);
 
-int phs_lpv_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+int phs_lpv_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_flags, const void *b,
                    int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
                    int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
                    const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream);
@@ -367,7 +374,7 @@ int phs_lpv_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
  * h[t] = A[t] h[t+1] + b[t] x[t], zf = h[0].  The adjoint of the forward
  * model is this one on (A[t]^T, input vector c[t], output vector b[t], d[t])
  * from dL/dzf: y = grad_x, zf = grad_zi. */
-int phs_lpv_ss_rev(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+int phs_lpv_ss_rev(int dtype, int M, int64_t B, int64_t T, const void *A, int A_flags, const void *b,
                    int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
                    int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
                    const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream);

@@ -448,7 +448,7 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
 if EXTENSION_LOADED and _has_op("lpv_ss"):
     # single-input single-output LPV state space of order <= 4: (y, zf)
     @torch.library.register_fake("philtorch::lpv_ss")
-    def _(A, B, C, D, zi, x, out_idx, reverse=False):
+    def _(A, B, C, D, zi, x, out_idx, reverse=False, transpose_A=False):
         torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
         torch._check(A.ndim in (3, 4) and A.shape[-1] == A.shape[-2], lambda: "A must be (T, M, M) or (batch, T, M, M)")
         return _fake_like(x), x.new_empty((x.shape[0], A.shape[-1]))
@@ -457,12 +457,14 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         A, B, C, D, zi, x, out_idx = inputs[:7]
         ctx.out_idx = out_idx
         ctx.reverse = bool(inputs[7]) if len(inputs) > 7 else False
+        ctx.transpose_A = bool(inputs[8]) if len(inputs) > 8 else False
         ctx.save_for_backward(A, B, C, D, zi, x)
 
     def _lpv_ss_backward(ctx, gy, gzf):
         """With A, B, C, D constant: the adjoint model (A[t]^T, input vector
         c[t], output vector b[t], d[t]) run in the opposite time direction
-        from dL/dzf gives grad_x and grad_zi in one more lpv_ss pass.
+        from dL/dzf gives grad_x and grad_zi in one more lpv_ss pass, which
+        reads A transposed where it lies (transpose_A; no copy of A).
         Otherwise the gradient of the composite the fused kernel replaces
         (B x, the native LPV scan, the state shift, C h + D x;
         philtorch/lpv/ssm.py:337-581), recomputed from the inputs.  Both are
@@ -472,7 +474,7 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         inputs = ctx.saved_tensors
         needs = ctx.needs_input_grad
         A, B, C, D, zi, x = inputs
-        out = [None] * 8
+        out = [None] * 9
         if not any(needs[:4]):
             M = A.size(-1)
             c_in = C
@@ -480,7 +482,8 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
                 c_in = x.new_zeros(1, 1, M)
                 c_in[..., ctx.out_idx] = 1
             g = gy if gy is not None else torch.zeros_like(x)
-            gx, gzi = torch.ops.philtorch.lpv_ss(A.mT.contiguous(), c_in, B, D, gzf, g, 0, not ctx.reverse)
+            gx, gzi = torch.ops.philtorch.lpv_ss(A, c_in, B, D, gzf, g, 0, not ctx.reverse,
+                                              not ctx.transpose_A)
             if zi is not None and needs[4]:
                 out[4] = gzi
             if needs[5]:
@@ -490,14 +493,15 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         if not wrt:
             return tuple(out)
         with torch.enable_grad():
+            Am = A.mT if ctx.transpose_A else A  # the model's matrices
             if ctx.reverse:
                 # the forward model over the time-flipped row and operands
                 ft = lambda t, d: t if t is None or t.size(d) == 1 else t.flip(d)  # noqa: E731
-                y, zf = _lpv_state_space_composite(A.flip(-3), ft(B, 1), ft(C, 1), ft(D, 1), zi, x.flip(-1),
+                y, zf = _lpv_state_space_composite(Am.flip(-3), ft(B, 1), ft(C, 1), ft(D, 1), zi, x.flip(-1),
                                                    out_idx=ctx.out_idx)
                 y = y.flip(-1)
             else:
-                y, zf = _lpv_state_space_composite(*inputs, out_idx=ctx.out_idx)
+                y, zf = _lpv_state_space_composite(Am, B, C, D, zi, x, out_idx=ctx.out_idx)
             outs, grads = [y], [gy if gy is not None else torch.zeros_like(y)]
             if gzf is not None:
                 outs.append(zf)

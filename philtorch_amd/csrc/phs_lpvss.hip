@@ -16,7 +16,7 @@ size_t lpv_ss_ws_bytes(int64_t B, int64_t T) {
 }
 
 template <class Alg>
-int lpv_ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, LpvOperand<typename Alg::elem> bv,
+int lpv_ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, bool A_tr, LpvOperand<typename Alg::elem> bv,
                LpvOperand<typename Alg::elem> cv, int out_idx, LpvOperand<typename Alg::elem> d, const void *zi,
                const void *x, void *y, void *zf, void *workspace, size_t ws_bytes, bool rev, hipStream_t stream) {
   using E = typename Alg::elem;
@@ -35,6 +35,7 @@ int lpv_ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, LpvOperand<typena
   LpvSsArgs<Alg> a{};
   a.A = static_cast<const E *>(A);
   a.A_row_stride = A_sh ? 0 : T * M * M;
+  a.A_trans = A_tr ? 1 : 0;
   a.bv = bv;
   a.cv = cv;
   a.d = d;
@@ -91,36 +92,38 @@ size_t phs_lpv_ss_workspace_size(int dtype, int M, int64_t B, int64_t T) {
 
 namespace {
 
-int lpv_ss_call(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+int lpv_ss_call(int dtype, int M, int64_t B, int64_t T, const void *A, int A_flags, const void *b,
                 int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
                 int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi, const void *x,
                 void *y, void *zf, void *workspace, size_t workspace_bytes, bool rev, void *stream) {
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (A_flags & ~(PHS_LPV_A_SHARED | PHS_LPV_A_TRANSPOSED)) return PHS_ERR_INVALID;
   return phs::lpv_dispatch(dtype, M, [&](auto alg) {
     using E = typename decltype(alg)::elem;
     const phs::LpvOperand<E> bo{static_cast<const E *>(b), b_row_stride, b_t_stride};
     const phs::LpvOperand<E> co{static_cast<const E *>(c), c_row_stride, c_t_stride};
     const phs::LpvOperand<E> dd{static_cast<const E *>(d), d_row_stride, d_t_stride};
-    return phs::lpv_ss_fwd<decltype(alg)>(B, T, A, A_shared != 0, bo, co, out_idx, dd, zi, x, y, zf, workspace,
-                                          workspace_bytes, rev, st);
+    return phs::lpv_ss_fwd<decltype(alg)>(B, T, A, (A_flags & PHS_LPV_A_SHARED) != 0,
+                                          (A_flags & PHS_LPV_A_TRANSPOSED) != 0, bo, co, out_idx, dd, zi, x, y, zf,
+                                          workspace, workspace_bytes, rev, st);
   });
 }
 
 }  // namespace
 
-int phs_lpv_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+int phs_lpv_ss_fwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_flags, const void *b,
                    int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
                    int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
                    const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream) {
-  return lpv_ss_call(dtype, M, B, T, A, A_shared, b, b_row_stride, b_t_stride, c, c_row_stride, c_t_stride, out_idx,
+  return lpv_ss_call(dtype, M, B, T, A, A_flags, b, b_row_stride, b_t_stride, c, c_row_stride, c_t_stride, out_idx,
                      d, d_row_stride, d_t_stride, zi, x, y, zf, workspace, workspace_bytes, false, stream);
 }
 
-int phs_lpv_ss_rev(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+int phs_lpv_ss_rev(int dtype, int M, int64_t B, int64_t T, const void *A, int A_flags, const void *b,
                    int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
                    int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
                    const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream) {
-  return lpv_ss_call(dtype, M, B, T, A, A_shared, b, b_row_stride, b_t_stride, c, c_row_stride, c_t_stride, out_idx,
+  return lpv_ss_call(dtype, M, B, T, A, A_flags, b, b_row_stride, b_t_stride, c, c_row_stride, c_t_stride, out_idx,
                      d, d_row_stride, d_t_stride, zi, x, y, zf, workspace, workspace_bytes, true, stream);
 }
 

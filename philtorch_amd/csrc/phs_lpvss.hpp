@@ -35,6 +35,7 @@ struct LpvSsArgs {
   using E = typename Alg::elem;
   const E *A;            // [rows, T, M, M]
   int64_t A_row_stride;  // elements between rows (0 = shared)
+  int A_trans;           // read each step's matrix transposed (the adjoint model's A[t]^T)
   LpvOperand<E> bv;      // [., ., M]; p nullptr: the input enters state 0
   LpvOperand<E> cv;      // [., ., M]; p nullptr: y is state out_idx
   LpvOperand<E> d;       // [., .]; p nullptr: no feedthrough
@@ -177,6 +178,10 @@ __device__ __noinline__ typename Alg::state lpv_prefix_fallback(LpvSsArgs<Alg> a
     SC cs[K];
     lpv_load<REV, E, K>(xrow, c0, a.T_len, a.vec_ok != 0, u, E(0));
     lpv_load<REV, SC, K>(crow, c0, a.T_len, a.vec_ok != 0, cs, Alg::s_czero());
+    if (a.A_trans) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) cs[k] = Alg::s_adjoint(cs[k]);  // real: the transpose
+    }
     lpv_inputs<Alg, REV, K>(a, b, c0, u, xs);
     M m = lane_map<Alg, true, false, K>(cs, xs, dummy);
     m = wave_scan_incl(m, lane, op);
@@ -255,6 +260,10 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
   for (int r = 0; r < R; ++r) {
     lpv_load<REV, E, K>(xrow, chunk0(r), T, vec, U[r], E(0));
     lpv_load<REV, SC, K>(crow, chunk0(r), T, vec, A[r], Alg::s_czero());
+    if (a.A_trans) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) A[r][k] = Alg::s_adjoint(A[r][k]);  // real: the transpose
+    }
   }
 
   // ---- pass 1: lane maps of (A[t], b[t] x[t]), wave scans, round chaining.

@@ -631,11 +631,12 @@ std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, cons
 // A (T, M, M) or (batch, T, M, M); B, C None or (1 | batch, 1 | T, M); D None
 // or (1 | batch, 1 | T) (a size-1 axis is shared); zi None or (batch, M);
 // out_idx selects the output state when C is None; reverse runs the model
-// backwards in time (phs_lpv_ss_rev).
+// backwards in time (phs_lpv_ss_rev); transpose_A uses A[t]^T in place of
+// A[t] (the adjoint model, read without a transposed copy).
 std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
                                       const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
                                       const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
-                                      bool reverse) {
+                                      bool reverse, bool transpose_A) {
   TORCH_CHECK(x.dim() == 2, "philtorch::lpv_ss: x must be a 2D tensor (batch, time)");
   const int64_t B = x.size(0), T = x.size(1);
   TORCH_CHECK((A.dim() == 3 || A.dim() == 4) && A.size(-1) == A.size(-2) && A.size(-3) == T,
@@ -691,7 +692,8 @@ std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tenso
   auto ts = [](const Tensor &t, int64_t width) { return t.size(1) == 1 ? int64_t(0) : width; };
   void *stream = stream_of(x);
   const Workspace ws = workspace_for(x, phs_lpv_ss_workspace_size(dt, int(M), B, T), stream);
-  check_status((reverse ? phs_lpv_ss_rev : phs_lpv_ss_fwd)(dt, int(M), B, T, Ac.const_data_ptr(), A.dim() == 3 ? 1 : 0,
+  const int A_flags = (A.dim() == 3 ? PHS_LPV_A_SHARED : 0) | (transpose_A ? PHS_LPV_A_TRANSPOSED : 0);
+  check_status((reverse ? phs_lpv_ss_rev : phs_lpv_ss_fwd)(dt, int(M), B, T, Ac.const_data_ptr(), A_flags,
                               Bm ? bc.const_data_ptr() : nullptr, Bm ? rs(bc, M) : 0, Bm ? ts(bc, M) : 0,
                               Cm ? cc.const_data_ptr() : nullptr, Cm ? rs(cc, M) : 0, Cm ? ts(cc, M) : 0,
                               int(out_idx), Dm ? dc.const_data_ptr() : nullptr, Dm ? rs(dc, 1) : 0,
@@ -880,7 +882,8 @@ TORCH_LIBRARY(philtorch, m) {
   // new: lfilter of order <= 4 from b and a (companion model built in the kernel): (y, zf)
   m.def("lfilter_ss(Tensor b, Tensor a, Tensor? zi, Tensor x, int form, bool reverse=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
-  m.def("lpv_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx, bool reverse=False) -> (Tensor, Tensor)",
+  m.def("lpv_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx, bool reverse=False, "
+        "bool transpose_A=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
 }
 

@@ -57,7 +57,7 @@ def _strides(v, T, width):
     return (0 if rows == 1 else steps * width), (0 if steps == 1 else width)
 
 
-def _run(api, A, b, c, d, zi, x, out_idx=0, rev=False):
+def _run(api, A, b, c, d, zi, x, out_idx=0, rev=False, transposed=False):
     import torch
 
     lib, ws, capi = api
@@ -69,8 +69,9 @@ def _run(api, A, b, c, d, zi, x, out_idx=0, rev=False):
     tA, tb, tc, td, tz, tx = (_dev(v) for v in (A, b, c, d, zi, x))
     y = torch.full_like(tx, float("nan"))
     zf = torch.full((Bn, M), float("nan"), dtype=tx.dtype, device="cuda")
-    print(f"lpv_ss capi M={M} B={Bn} T={T} rev={rev}", flush=True)
-    rc = (lib.phs_lpv_ss_rev if rev else lib.phs_lpv_ss_fwd)(dt, M, Bn, T, _p(tA), int(A.ndim == 3), _p(tb), *_strides(b, T, M), _p(tc),
+    flags = (capi.PHS_LPV_A_SHARED if A.ndim == 3 else 0) | (capi.PHS_LPV_A_TRANSPOSED if transposed else 0)
+    print(f"lpv_ss capi M={M} B={Bn} T={T} rev={rev} A_flags={flags}", flush=True)
+    rc = (lib.phs_lpv_ss_rev if rev else lib.phs_lpv_ss_fwd)(dt, M, Bn, T, _p(tA), flags, _p(tb), *_strides(b, T, M), _p(tc),
                             *_strides(c, T, M), out_idx, _p(td), *_strides(d, T, 1), _p(tz), _p(tx), _p(y), _p(zf),
                             _p(ws), need, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == capi.PHS_OK, lib.phs_error_string(rc)
@@ -224,18 +225,20 @@ def test_lpv_state_space_api_routes_and_shapes(hip, monkeypatch):
     assert taken[-1] is False
 
 
-@pytest.mark.parametrize("M", [1, 2, 4])
-def test_lpv_state_space_signal_gradient_takes_adjoint_pass(hip, monkeypatch, M):
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_lpv_state_space_signal_gradient_takes_adjoint_pass(hip, monkeypatch, dtype, M):
     """lpv.state_space with only x and zi requiring grad runs the fused
-    route forward and its adjoint (A[t]^T, c and b swapped, reversed in
-    time) backward; gradients against the composed route's autograd."""
+    route forward and its adjoint (A[t]^T read in place, c and b swapped,
+    reversed in time) backward; gradients against the composed route's
+    autograd."""
     import torch
 
     from philtorch_amd.lpv import ssm
 
-    g = D.rng(D.seed_of("lpv-ss-adjoint", M))
+    g = D.rng(D.seed_of("lpv-ss-adjoint", dtype, M))
     Bn, T = 3, 5000
-    t = lambda v: torch.tensor(np.asarray(v, np.float64), device="cuda")  # noqa: E731
+    t = lambda v: torch.tensor(np.asarray(v, dtype), device="cuda")  # noqa: E731
     A = t(_model(g, M, Bn, T, False))
     b, c, d = t(g.standard_normal((Bn, T, M))), t(g.standard_normal(M)), t(g.standard_normal((Bn, T)))
     x0, z0 = g.standard_normal((Bn, T)), g.standard_normal((Bn, M))
@@ -253,15 +256,40 @@ def test_lpv_state_space_signal_gradient_takes_adjoint_pass(hip, monkeypatch, M)
             res.append((x.grad.cpu().numpy(), z.grad.cpu().numpy()))
     assert taken == [True, True]
     for i in range(2):
-        D.check(res[i][0], res[i + 2][0], f"grad_x {i}")
-        D.check(res[i][1], res[i + 2][1], f"grad_zi {i}", scale=np.max(np.abs(res[i + 2][0])))
+        D.check(res[i][0], res[i + 2][0], f"grad_x {i}", dtype=dtype)
+        D.check(res[i][1], res[i + 2][1], f"grad_zi {i}", dtype=dtype, scale=np.max(np.abs(res[i + 2][0])))
 
 
-def test_lpv_ss_reversed_op_gradients(hip):
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("rev", [False, True])
+def test_lpv_ss_capi_transposed_A(api, dtype, M, rev):
+    """PHS_LPV_A_TRANSPOSED reads each step's matrix transposed where it
+    lies: bit for bit the result of passing the transposed copy, per-row and
+    shared A, through the look-back (T spans many tiles), and against the
+    oracle on the transposed model."""
+    g = D.rng(D.seed_of("lpv-ss-transposed", dtype, M, rev))
+    Bn, T = 3, 40_001
+    x = g.standard_normal((Bn, T)).astype(dtype)
+    zi = g.standard_normal((Bn, M)).astype(dtype)
+    b, c, d = _layout(g, "rowstep", Bn, T, M), _layout(g, "row", Bn, T, M), _layout(g, "step", Bn, T, 0)
+    b, c, d = (v.astype(dtype) for v in (b, c, d))
+    for shared in (False, True):
+        A = _model(g, M, Bn, T, shared).astype(dtype)  # rotations: A^T != A for M > 1
+        At = np.ascontiguousarray(np.swapaxes(A, -1, -2))
+        got = _run(api, A, b, c, d, zi, x, rev=rev, transposed=True)
+        ref = _run(api, At, b, c, d, zi, x, rev=rev)
+        np.testing.assert_array_equal(got[0], ref[0])
+        np.testing.assert_array_equal(got[1], ref[1])
+        _check(got, At, b, c, d, zi, x, 0, dtype, f"transposed shared={shared}", rev=rev)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_lpv_ss_reversed_op_gradients(hip, M):
     import torch
 
-    g = D.rng(D.seed_of("lpv-ss-rev-grad"))
-    Bn, T, M = 2, 20, 2
+    g = D.rng(D.seed_of("lpv-ss-rev-grad", M))
+    Bn, T = 2, 20
     t = lambda v, rg=False: torch.tensor(np.asarray(v, np.float64), device="cuda", requires_grad=rg)  # noqa: E731
     A = t(_model(g, M, Bn, T, False))
     b, c, d = t(g.standard_normal((Bn, T, M))), t(g.standard_normal((1, 1, M))), t(g.standard_normal((Bn, 1)))
@@ -270,11 +298,20 @@ def test_lpv_ss_reversed_op_gradients(hip):
         f = lambda z_, x_: torch.ops.philtorch.lpv_ss(A, b, c, d, z_, x_, 0, rev)  # noqa: E731
         assert torch.autograd.gradcheck(f, (zi, x))
         assert torch.autograd.gradgradcheck(f, (zi, x))
-        f2 = lambda z_, x_: torch.ops.philtorch.lpv_ss(A, None, None, d, z_, x_, 1, rev)  # noqa: E731
+        f2 = lambda z_, x_: torch.ops.philtorch.lpv_ss(A, None, None, d, z_, x_, M - 1, rev)  # noqa: E731
         assert torch.autograd.gradcheck(f2, (zi, x))
+        # the transposed model: the adjoint pass then reads A as it lies
+        f3 = lambda z_, x_: torch.ops.philtorch.lpv_ss(A, b, c, d, z_, x_, 0, rev, True)  # noqa: E731
+        assert torch.autograd.gradcheck(f3, (zi, x))
+        assert torch.autograd.gradgradcheck(f3, (zi, x))
     Ag, bg = A.clone().requires_grad_(True), b.clone().requires_grad_(True)
     fA = lambda A_, b_, x_: torch.ops.philtorch.lpv_ss(A_, b_, c, d, None, x_, 0, True)[0]  # noqa: E731
     assert torch.autograd.gradcheck(fA, (Ag, bg, x))
+    fAt = lambda A_, b_, x_: torch.ops.philtorch.lpv_ss(A_, b_, c, d, None, x_, 0, False, True)[0]  # noqa: E731
+    assert torch.autograd.gradcheck(fAt, (Ag, bg, x))
+    yt, zft = torch.ops.philtorch.lpv_ss(A, b, c, d, zi, x, 0, False, True)
+    yc, zfc = torch.ops.philtorch.lpv_ss(A.mT.contiguous(), b, c, d, zi, x, 0)
+    assert torch.equal(yt, yc) and torch.equal(zft, zfc)
     y, zf = torch.ops.philtorch.lpv_ss(A, b, c, d, zi, x, 0, True)
     yr, zfr = torch.ops.philtorch.lpv_ss(A.flip(-3), b.flip(1), c, d, zi, x.flip(-1), 0)
     D.check(y.detach().cpu().numpy(), yr.flip(-1).detach().cpu().numpy(), "reverse y")
