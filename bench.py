@@ -14,11 +14,15 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c2      philtorch::lti_recur + lti_recur_backward         (LTI scalar, complex64)
   c3      philtorch::recur2 + recurN_backward               (LPV 2x2)
   c3_lpv_ss  lpv.state_space of a time-varying biquad (tdf2, one output), forward only (philtorch::lpv_ss)
+  c3_lpv_ss_grad  the same plus gradients w.r.t. x and zi (a reversed lpv_ss pass over the adjoint model)
   c4      8 x (philtorch::lti_recur2 + lti_recurN_backward) (LTI biquad cascade)
   c4_fused  philtorch::sosfilt + sosfilt_backward              (the same cascade, fused)
   c4_api  8 x lti.lfilter(tdf2, unroll_factor=1) + autograd   (the caller pattern, API level)
   c4_filtfilt  8 x lti.filtfilt(replicate, padlen 9), forward only (philtorch::filtfilt)
   c4_lfilter4  4 x lti.lfilter of order 4 (tdf2), forward only (philtorch::lti_ss)
+--composed runs an API config (c3_lpv_ss*, c4_api, c4_filtfilt, c4_lfilter4)
+through the reference's composed route instead of the fused kernels, for the
+comparison.
 Before every step a 512 MiB buffer is read end to end so the 256 MB Infinity
 Cache holds none of the step's operands (a read sweep, not a write: a write
 would leave dirty lines whose write-back then competes with the step); the
@@ -61,9 +65,11 @@ class Workload:
     fwd_bytes = 0  # algorithmic bytes of one forward launch
     bwd_bytes = 0  # algorithmic bytes of one backward launch
     launches = 1  # forward (and backward) launches per step
-    # streaming-probe equivalents of one forward / backward launch: (arrays
-    # read, arrays written, fp32 elements per array), or None where the
-    # launch's traffic is not a set of equal-length arrays
+    # streaming-probe equivalents of one forward / backward launch: (names of
+    # the arrays read, names of the arrays written, fp32 elements per array),
+    # or None where the launch's traffic is not a set of equal-length arrays.
+    # A name the forward writes and the backward reads is one buffer, as in
+    # the step (the backward reads the forward's output and coefficients)
     probe_fwd = None
     probe_bwd = None
 
@@ -103,8 +109,8 @@ class LpvScalar(Workload):
         self.samples = B * T
         self.fwd_bytes = 3 * es * B * T  # read a, x; write y
         self.bwd_bytes = 5 * es * B * T  # read a, g, y; write grad_x, grad_a
-        self.probe_fwd = (2, 1, B * T * es // 4)
-        self.probe_bwd = (3, 2, B * T * es // 4)
+        self.probe_fwd = (("a", "x"), ("y",), B * T * es // 4)
+        self.probe_bwd = (("a", "y", "g"), ("grad_a", "grad_x"), B * T * es // 4)
 
     def step_fwd(self):
         import torch
@@ -148,8 +154,8 @@ class LtiComplex(Workload):
         self.samples = C * T
         self.fwd_bytes = 16 * C * T  # read x, write y (8 B each)
         self.bwd_bytes = 24 * C * T  # read g, y; write grad_x
-        self.probe_fwd = (1, 1, 2 * C * T)
-        self.probe_bwd = (2, 1, 2 * C * T)
+        self.probe_fwd = (("x",), ("y",), 2 * C * T)
+        self.probe_bwd = (("y", "g"), ("grad_x",), 2 * C * T)
 
     def step_fwd(self):
         import torch
@@ -501,6 +507,58 @@ class LpvSsApi(LpvBiquad):
                                zi[:rows], out_idx=0, nthreads=nthreads)
 
 
+class LpvSsGrad(LpvSsApi):
+    """c3_lpv_ss_grad: c3_lpv_ss plus the gradients w.r.t. x and zi
+    (torch.autograd.grad of y against a seeded upstream gradient).  The
+    backward is one more philtorch::lpv_ss pass: the adjoint model
+    (A[t]^T read in place, input vector e_0, output vector b[t], d[t]) in
+    reversed time."""
+
+    def __init__(self):
+        import torch
+
+        super().__init__()
+        B, T = self.B, self.T
+        self.name = "c3_lpv_ss_grad"
+        self.metric = (f"GSamples/s fwd+bwd(x, zi), LPV biquad lpv.state_space (tdf2, one output) B={B} T={T} "
+                       "fp32 (API)")
+        g = torch.Generator().manual_seed(34)
+        self.gy_cpu = torch.randn(B, T, generator=g)
+        self.gy = self.gy_cpu.cuda()
+        self.bwd_bytes = 36 * B * T  # read A (16), b (8), d, g; write grad_x
+
+    def step_fwd(self):
+        from philtorch_amd import lpv
+
+        A, x, bv, d, zi = self.dev
+        x, zi = x.detach().requires_grad_(True), zi.detach().requires_grad_(True)
+        y, _ = lpv.state_space(A, x, B=bv, D=d, zi=zi, unroll_factor=1, out_idx=0)
+        return y, x, zi
+
+    def step_bwd(self, out):
+        import torch
+
+        y, x, zi = out
+        return torch.autograd.grad(y, (x, zi), self.gy)
+
+    def cpu_step(self, rows, steps, nthreads):
+        import numpy as np
+
+        import oracle
+
+        A, x, bv, d, zi = (v.numpy() for v in self.cpu)
+        A, x, bv, d, zi = A[:rows, :steps], x[:rows, :steps], bv[:rows, :steps], d[:rows, :steps], zi[:rows]
+        gy = self.gy_cpu.numpy()[:rows, :steps]
+        oracle.lpv_state_space(A, x, bv, None, d, zi, out_idx=0, nthreads=nthreads)
+        # the adjoint model over reversed time: state lambda[T - s], input
+        # g[T-1-s], A[T-1-s]^T, input vector e_0, output vector b[T-1-s]
+        M = A.shape[-1]
+        e0 = np.zeros((1, 1, M), dtype=x.dtype)
+        e0[..., 0] = 1
+        fl = lambda v: np.ascontiguousarray(v[:, ::-1])  # noqa: E731
+        oracle.lpv_state_space(fl(np.swapaxes(A, -1, -2)), fl(gy), e0, fl(bv), fl(d), None, nthreads=nthreads)
+
+
 def make_workload(name):
     if name == "c1":
         return LpvScalar("c1", 64, 65536, "float32")
@@ -524,10 +582,13 @@ def make_workload(name):
         return Lfilter4Api()
     if name == "c3_lpv_ss":
         return LpvSsApi()
+    if name == "c3_lpv_ss_grad":
+        return LpvSsGrad()
     raise ValueError(name)
 
 
-CONFIGS = ("c1", "c2", "c3", "c3_lpv_ss", "c4", "c4_fused", "c4_api", "c4_filtfilt", "c4_lfilter4", "c5", "c5_f64")
+API_CONFIGS = ("c3_lpv_ss", "c3_lpv_ss_grad", "c4_api", "c4_filtfilt", "c4_lfilter4")
+CONFIGS = ("c1", "c2", "c3", "c3_lpv_ss", "c3_lpv_ss_grad", "c4", "c4_fused", "c4_api", "c4_filtfilt", "c4_lfilter4", "c5", "c5_f64")
 
 
 # ----------------------------------------------------------------------------
@@ -615,8 +676,9 @@ def _fresh_events():
 
 def _ceiling(lib, w, steps, evict_caches, dev):
     """The streaming probe (phs_stream_probe) moving one step's bytes: the
-    forward launch's arrays, then the backward's, with the same cache
-    eviction before every step.  Reports the step time, each kernel's own
+    forward launch's arrays, then the backward's over the same buffers the
+    step uses (the backward re-reads the forward's coefficients and output),
+    with the same cache eviction before every step.  Reports the step time, each kernel's own
     duration (launch hook) and the scan step's fraction of it; the tile shape
     of the scalar scan (shape 0) and a flat one-vector-per-lane shape (shape
     1) are both timed and the faster is reported.  None where the workload's
@@ -631,17 +693,15 @@ def _ceiling(lib, w, steps, evict_caches, dev):
         return None
     bufs = {}
 
-    def arrays(n_in, n_out, n, tag):
-        key = (tag, n)
-        if key not in bufs:
-            bufs[key] = [torch.ones(n, dtype=torch.float32, device=dev) for _ in range(3)] + \
-                        [torch.empty(n, dtype=torch.float32, device=dev) for _ in range(2)]
-        b = bufs[key]
-        ins = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in b[:3]])
-        outs = (ctypes.c_void_p * 2)(*[t.data_ptr() for t in b[3:]])
+    def arrays(ins_named, outs_named, n):
+        for nm in ins_named + outs_named:
+            if nm not in bufs:
+                bufs[nm] = torch.ones(n, dtype=torch.float32, device=dev)
+        ins = (ctypes.c_void_p * 3)(*[bufs[nm].data_ptr() for nm in ins_named])
+        outs = (ctypes.c_void_p * 2)(*[bufs[nm].data_ptr() for nm in outs_named])
         return ins, outs
 
-    calls = [(w.probe_fwd, arrays(*w.probe_fwd, "f")), (w.probe_bwd, arrays(*w.probe_bwd, "b"))]
+    calls = [((len(p[0]), len(p[1]), p[2]), arrays(*p)) for p in (w.probe_fwd, w.probe_bwd)]
     results = {}
     for shape in (0, 1):
         stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -701,7 +761,12 @@ def main() -> int:
     ap.add_argument("--calib-copy", action="store_true",
                     help="after timing, run one plain 256 MiB device copy (reads and writes 256 MiB) so "
                     "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE of this run can be scaled to bytes")
+    ap.add_argument("--composed", action="store_true",
+                    help=f"run an API config ({', '.join(API_CONFIGS)}) through the reference's composed route "
+                    "(the fused state-space, lfilter, biquad and filtfilt routes switched off), for comparison")
     args = ap.parse_args()
+    if args.composed and args.config not in API_CONFIGS:
+        ap.error(f"--composed applies to {', '.join(API_CONFIGS)}")
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
@@ -722,6 +787,16 @@ def main() -> int:
         return 2
 
     w = make_workload(args.config)
+    if args.composed:
+        from philtorch_amd.lpv import ssm as lpv_ssm
+        from philtorch_amd.lti import filtering, ssm as lti_ssm
+
+        off = lambda *a, **k: False  # noqa: E731
+        for mod, fn in ((lpv_ssm, "_fused_lpv_ss_applies"), (lti_ssm, "_fused_ss_applies"),
+                        (filtering, "_fused_biquad_applies"), (filtering, "_fused_lfilter_applies"),
+                        (filtering, "_fused_filtfilt_applies")):
+            setattr(mod, fn, off)
+        w.metric += " [composed route]"
     dev = torch.device("cuda", 0)
     evict = None if args.no_evict else torch.ones(128 << 20, dtype=torch.float32, device=dev)
     evict_sink = torch.empty((), dtype=torch.float32, device=dev)
@@ -800,6 +875,7 @@ def main() -> int:
                 "c4_filtfilt": "lti_filtfilt8_api_fwd_B16_T480000_f32",
                 "c4_lfilter4": "lti_lfilter_order4_x4_api_fwd_B16_T480000_f32",
                 "c3_lpv_ss": "lpv_biquad_state_space_api_fwd_B32_T1048576_f32",
+                "c3_lpv_ss_grad": "lpv_biquad_state_space_api_fwd_bwd_x_zi_B32_T1048576_f32",
                 "c5": "lpv_scan_fwd_bwd_B8_T16777216_f32",
                 "c5_f64": "lpv_scan_fwd_bwd_B8_T16777216_f64",
             }[w.name],
@@ -808,6 +884,7 @@ def main() -> int:
             "cache_evicted_between_steps": evict is not None,
         },
         "detail": {
+            "route": "composed" if args.composed else "fused",
             "launches_per_direction": w.launches,
             "ms_fwd_kernel": round(mean_fwd, 5),
             "ms_bwd_kernel": round(mean_bwd, 5) if w.bwd_bytes else None,
@@ -820,12 +897,12 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{'ss_kernel' if w.name in ('c4_lfilter4', 'c4_filtfilt') else 'lpv_ss_kernel' if w.name == 'c3_lpv_ss' else 'sos_kernel' if w.name.startswith('c4_') else 'scan_kernel'} ({dominant[0]})",
+            "kernel": f"{'ss_kernel' if w.name in ('c4_lfilter4', 'c4_filtfilt') else 'lpv_ss_kernel' if w.name.startswith('c3_lpv_ss') else 'sos_kernel' if w.name.startswith('c4_') else 'scan_kernel'} ({dominant[0]})",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": _measured_traffic(w.name, dominant[0]),
+            "traffic": None if args.composed else _measured_traffic(w.name, dominant[0]),
             "step_GBs_algorithmic": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 1),
             "step_frac": round(step_bytes / (ms_per_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "ceiling": ceiling,
