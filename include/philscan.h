@@ -343,6 +343,42 @@ int phs_lfilter_rev(int dtype, int64_t B, int64_t T, const void *b, int nb, cons
                     int form, const void *zi, const void *x, void *y, void *zf, void *workspace,
                     size_t workspace_bytes, void *stream);
 
+/* ---- Gradients of phs_lti_ss_fwd (reverse = 0) or phs_lti_ss_rev
+ * (reverse = 1) w.r.t. x, zi and every coefficient, in two passes and two
+ * small reductions.  Replaces the autograd of the composed state space the
+ * reference differentiates (philtorch/lti/ssm.py:386-589; B x, the scan, the
+ * state shift, C h + D x):
+ *     dL/dA = sum_t lambda[t+1] h[t]^T,  dL/db = sum_t lambda[t+1] x[t],
+ *     dL/dc = sum_t g[t] h[t],           dL/dd = sum_t g[t] x[t],
+ * with g = dL/dy, lambda[t] = dL/dh[t] = A^T lambda[t+1] + c g[t] from
+ * lambda[T] = dL/dzf; dL/dx[t] = b . lambda[t+1] + d g[t], dL/dzi =
+ * lambda[0].  The model's arguments are phs_lti_ss_fwd's (same shapes and
+ * sharing); gy [B,T] = dL/dy; gzf [B,M] or NULL (zero); outputs gx [B,T],
+ * gzi [B,M], gA, gb, gc, gd shaped like A, b, c, d (one for a shared
+ * operand: summed over the rows), each nullable (gb, gc, gd must be NULL
+ * when their operand is).  The first pass runs the model again and keeps
+ * its states (B*T*M values) in `scratch` (phs_lti_ss_bwd_scratch_size
+ * bytes, with the partial sums; any contents); `workspace` is
+ * phs_lti_ss_workspace_size bytes, as for the forward. */
+size_t phs_lti_ss_bwd_scratch_size(int dtype, int M, int64_t B, int64_t T);
+
+int phs_lti_ss_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b, int b_shared,
+                   const void *c, int c_shared, int out_idx, const void *d, int d_shared, const void *zi,
+                   const void *x, const void *gy, const void *gzf, void *gx, void *gzi, void *gA, void *gb, void *gc,
+                   void *gd, int reverse, void *scratch, size_t scratch_bytes, void *workspace,
+                   size_t workspace_bytes, void *stream);
+
+/* Gradients of phs_lfilter_fwd / phs_lfilter_rev w.r.t. x, zi, b [.., nb]
+ * and a [.., na] (gb, ga shaped like b and a, summed over the rows when
+ * coef_shared), by the chain rule through the companion model (replaces the
+ * autograd of philtorch/lti/filtering.py:273-333).  Scratch and workspace:
+ * phs_lti_ss_bwd_scratch_size and phs_lti_ss_workspace_size at
+ * M = max(nb - 1, na). */
+int phs_lfilter_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na, int coef_shared,
+                    int form, const void *zi, const void *x, const void *gy, const void *gzf, void *gx, void *gzi,
+                    void *gb, void *ga, int reverse, void *scratch, size_t scratch_bytes, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
 /* Flags of the A argument of phs_lpv_ss_fwd / phs_lpv_ss_rev (A_flags):
  * PHS_LPV_A_SHARED, A is [T,M,M] and shared by the rows; PHS_LPV_A_TRANSPOSED,
  * every step's matrix is read transposed, so the adjoint model's A[t]^T

@@ -345,6 +345,13 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
         torch._check(A.ndim in (2, 3) and A.shape[-1] == A.shape[-2], lambda: "A must be (M, M) or (batch, M, M)")
         return _fake_like(x), x.new_empty((x.shape[0], A.shape[-1]))
 
+    if _has_op("lti_ss_backward"):
+
+        @torch.library.register_fake("philtorch::lti_ss_backward")
+        def _(A, B, C, D, zi, x, grad_y, grad_zf, out_idx, reverse=False):
+            e = lambda t: x.new_empty(t.shape) if t is not None else x.new_empty((0,))  # noqa: E731
+            return [e(A), e(B), e(C), e(D), x.new_empty((x.shape[0], A.shape[-1])), _fake_like(x)]
+
     def _lti_ss_setup(ctx, inputs, output):
         A, B, C, D, zi, x, out_idx = inputs[:7]
         ctx.out_idx = out_idx
@@ -356,15 +363,25 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
         output vector B, D) run in the opposite time direction from dL/dzf
         gives grad_x and grad_zi in one more lti_ss pass (the reversed mode
         for a forward call and the other way round: no flipped copies).
-        Otherwise the gradient of the composite the fused kernel replaces
-        (B x, the native scan, the state shift, C h + D x;
-        philtorch/lti/ssm.py:386-589), recomputed from the inputs.  Both are
-        differentiable again under create_graph."""
+        With a coefficient gradient wanted: philtorch::lti_ss_backward, the
+        forward again keeping its states, then the adjoint pass summing
+        lambda h^T, lambda x, g h and g x.  Under create_graph: the gradient
+        of the composite the fused kernel replaces (B x, the native scan,
+        the state shift, C h + D x; philtorch/lti/ssm.py:386-589),
+        recomputed from the inputs and differentiable again."""
         from .lti.ssm import _state_space_composite
 
         inputs = ctx.saved_tensors
         needs = ctx.needs_input_grad
         A, B, C, D, zi, x = inputs
+        if any(needs[:4]) and not torch.is_grad_enabled() and _has_op("lti_ss_backward"):
+            g = gy if gy is not None else torch.zeros_like(x)
+            res = torch.ops.philtorch.lti_ss_backward(A, B, C, D, zi, x, g, gzf, ctx.out_idx, ctx.reverse)
+            out = [None] * 8
+            for i, t in enumerate(inputs[:5] + (x,)):
+                if t is not None and needs[i]:
+                    out[i] = res[i]
+            return tuple(out)
         if not any(needs[:4]):
             M = A.size(-1)
             unit = lambda i: torch.nn.functional.one_hot(torch.tensor(i, device=x.device), M).to(x.dtype)  # noqa: E731
@@ -402,6 +419,13 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
         torch._check(1 <= M <= 4, lambda: "filters of order 1 to 4")
         return _fake_like(x), x.new_empty((x.shape[0], M))
 
+    if _has_op("lfilter_ss_backward"):
+
+        @torch.library.register_fake("philtorch::lfilter_ss_backward")
+        def _(b, a, zi, x, grad_y, grad_zf, form, reverse=False):
+            M = max(b.shape[-1] - 1, a.shape[-1])
+            return [b.new_empty(b.shape), a.new_empty(a.shape), x.new_empty((x.shape[0], M)), _fake_like(x)]
+
     def _lfilter_ss_setup(ctx, inputs, output):
         b, a, zi, x, form = inputs[:5]
         ctx.form = form
@@ -414,13 +438,21 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
         direction (TDF-II <-> DF-II: A^T, with the input and output vectors
         swapped), from dL/dzf, so grad_x and grad_zi are one more lfilter_ss
         pass (the reversed mode for a forward call and the other way round:
-        no flipped copies).  Otherwise the gradient of the companion-form
-        route the kernel replaces (philtorch/lti/filtering.py:273-333),
-        recomputed from the inputs."""
+        no flipped copies).  With a gradient of b or a wanted:
+        philtorch::lfilter_ss_backward (the forward again keeping its
+        states, the adjoint pass with the model's gradient sums, the chain
+        rule to b and a).  Under create_graph: the gradient of the
+        companion-form route the kernel replaces (philtorch/lti/
+        filtering.py:273-333), recomputed from the inputs."""
         from .lti.filtering import _ssm_lfilter
 
         b, a, zi, x = inputs = ctx.saved_tensors
         needs = ctx.needs_input_grad
+        if (needs[0] or needs[1]) and not torch.is_grad_enabled() and _has_op("lfilter_ss_backward"):
+            g = gy if gy is not None else torch.zeros_like(x)
+            gb, ga, gzi, gx = torch.ops.philtorch.lfilter_ss_backward(b, a, zi, x, g, gzf, ctx.form, ctx.reverse)
+            return (gb if needs[0] else None, ga if needs[1] else None,
+                    gzi if zi is not None and needs[2] else None, gx if needs[3] else None, None, None)
         if not (needs[0] or needs[1]):
             g = gy if gy is not None else torch.zeros_like(x)
             gx, gzi = torch.ops.philtorch.lfilter_ss(b, a, gzf, g, 1 - ctx.form, not ctx.reverse)

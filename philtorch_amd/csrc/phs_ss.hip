@@ -3,7 +3,10 @@
 // checks, workspace carving and the launches of ss_kernel on the caller's
 // stream (one per pass).  No allocation and no synchronisation.
 // Workspace layout: [0, 2048) claim header, then the status words of every
-// (row, tile).
+// (row, tile).  The coefficient-gradient backward takes a scratch buffer of
+// its own for the per-wave partial sums, the row sums and the forward's
+// states [B, T, M] (data must never land on the self-resetting status
+// words).
 #include "phs_launch.hpp"
 #include "phs_ss.hpp"
 
@@ -59,11 +62,29 @@ bool ss_args(int64_t B, int64_t T, const SsFilter &f, const void *zi, const void
   return true;
 }
 
-template <class Alg, bool REV>
+template <class Alg, bool REV, int MODE = kSsPlain>
 int ss_launch(const SsArgs<Alg> &a, hipStream_t stream) {
-  launch_kernel((ss_kernel<Alg, REV>), dim3(a.per_stripe * kStripes), dim3(SsShape<Alg>::kThreads), 0, stream,
-                     a);
+  launch_kernel((ss_kernel<Alg, REV, MODE>), dim3(a.per_stripe * kStripes), dim3(SsShape<Alg>::kThreads), 0, stream,
+                a);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
+}
+
+// The coefficient-gradient backward's scratch: the per-wave partial sums,
+// the row sums and the states.
+template <class Alg>
+struct SsBwdLayout {
+  size_t partials = 0, rowsum = 0, states = 0, total = 0;
+};
+template <class Alg>
+SsBwdLayout<Alg> ss_bwd_layout(int64_t B, int64_t T) {
+  using C = typename Wide<typename Alg::elem>::type;
+  const int64_t tiles = (T + SsShape<Alg>::kTile - 1) / SsShape<Alg>::kTile;
+  SsBwdLayout<Alg> L;
+  L.partials = 0;
+  L.rowsum = align_up(L.partials + size_t(B) * size_t(tiles) * SsShape<Alg>::kWaves * SsGrad<Alg>::kN * sizeof(C));
+  L.states = align_up(L.rowsum + size_t(B) * SsGrad<Alg>::kN * sizeof(C));
+  L.total = align_up(L.states + size_t(B) * size_t(T) * sizeof(typename Alg::s_state));
+  return L;
 }
 
 bool ss_grid_ok(int64_t B, int64_t T, int64_t kTile) {
@@ -98,6 +119,94 @@ int ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, const void *bv, bool 
   a.d_stride = d_sh ? 0 : 1;
   a.out_idx = out_idx;
   return rev ? ss_launch<Alg, true>(a, stream) : ss_launch<Alg, false>(a, stream);
+}
+
+// The explicit model's operands (SsArgs fields of a model with filt_form 0).
+template <typename E>
+struct SsModelArgs {
+  const void *A = nullptr, *b = nullptr, *c = nullptr, *d = nullptr;
+  bool A_sh = false, b_sh = false, c_sh = false, d_sh = false;
+  int out_idx = 0;
+};
+
+// Gradients of y = model(x) (and zf) w.r.t. x, zi and the coefficients:
+// the forward again writing its states (kSsStates), the adjoint model in
+// the opposite time direction from grad_zf with the coefficient sums
+// (kSsGrad; explicit model: A^T, input vector c, output vector b; filter:
+// the other companion form of the same b and a), then the row sums and the
+// outputs.  gx, gzi and every coefficient output may be null.
+template <class Alg>
+int ss_bwd(int64_t B, int64_t T, const SsModelArgs<typename Alg::elem> &mo, const SsFilter &f, const void *zi,
+           const void *x, const void *gy, const void *gzf, void *gx, void *gzi, SsGradOut<typename Alg::elem> out,
+           void *scratch, size_t scratch_bytes, void *workspace, size_t ws_bytes, bool rev, hipStream_t stream) {
+  using E = typename Alg::elem;
+  using C = typename Wide<E>::type;
+  using SS = typename Alg::s_state;
+  constexpr int M = SsView<Alg>::M;
+  if (B < 0 || T < 0) return PHS_ERR_INVALID;
+  if (f.form == 0 && !mo.c && (mo.out_idx < 0 || mo.out_idx >= M)) return PHS_ERR_INVALID;
+  if (f.form != 0 && !ss_filter_ok(f, M)) return PHS_ERR_INVALID;
+  if (B == 0) return PHS_OK;
+  if ((f.form == 0 ? !mo.A : (!f.b || !f.a)) || (T > 0 && (!x || !gy))) return PHS_ERR_INVALID;
+  if (f.form == 0 && ((out.gb && !mo.b) || (out.gc && !mo.c) || (out.gd && !mo.d))) return PHS_ERR_INVALID;
+  if (!ss_grid_ok(B, T, SsShape<Alg>::kTile)) return PHS_ERR_INVALID;
+  const SsBwdLayout<Alg> L = ss_bwd_layout<Alg>(B, T);
+  if (!scratch || scratch_bytes < L.total) return PHS_ERR_WORKSPACE;
+  if (T > 0 && (!workspace || ws_bytes < ss_ws_bytes<Alg>(B, T))) return PHS_ERR_WORKSPACE;
+  char *sc = static_cast<char *>(scratch);
+  C *gpart = reinterpret_cast<C *>(sc + L.partials);
+  C *rowsum = reinterpret_cast<C *>(sc + L.rowsum);
+  E *states = reinterpret_cast<E *>(sc + L.states);
+  const int64_t tiles = (T + SsShape<Alg>::kTile - 1) / SsShape<Alg>::kTile;
+  auto set_model = [&](SsArgs<Alg> &a, bool adjoint) {
+    a.A = static_cast<const E *>(mo.A);
+    a.A_stride = mo.A_sh ? 0 : M * M;
+    a.A_trans = adjoint ? 1 : 0;
+    a.d = static_cast<const E *>(mo.d);
+    a.d_stride = mo.d_sh ? 0 : 1;
+    const E *bp = static_cast<const E *>(mo.b), *cp = static_cast<const E *>(mo.c);
+    if (!adjoint) {
+      a.bv = bp, a.b_stride = mo.b_sh ? 0 : M, a.in_idx = 0;
+      a.cv = cp, a.c_stride = mo.c_sh ? 0 : M, a.out_idx = mo.out_idx;
+    } else {  // input vector c (or e_out_idx), output vector b (or e_0)
+      a.bv = cp, a.b_stride = mo.c_sh ? 0 : M, a.in_idx = mo.out_idx;
+      a.cv = bp, a.c_stride = mo.b_sh ? 0 : M, a.out_idx = 0;
+    }
+  };
+  if (T > 0) {
+    SsArgs<Alg> p{};
+    if (!ss_args<Alg>(B, T, f, zi, x, nullptr, nullptr, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+    set_model(p, false);
+    p.hs = states;
+    p.vec_hs = aligned16(states) && (size_t(T) * sizeof(SS)) % 16 == 0 && aligned16(x) &&
+               (size_t(T) * sizeof(E)) % 16 == 0;
+    int rc = rev ? ss_launch<Alg, true, kSsStates>(p, stream) : ss_launch<Alg, false, kSsStates>(p, stream);
+    if (rc != PHS_OK) return rc;
+    SsFilter fa = f;
+    if (f.form != 0) fa.form = 3 - f.form;  // TDF-II <-> DF-II: the adjoint of a companion form
+    if (!ss_args<Alg>(B, T, fa, gzf, gy, gx, gzi, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+    set_model(p, true);
+    p.hs_fwd = states;
+    p.x_fwd = static_cast<const E *>(x);
+    p.gpart = gpart;
+    p.vec_hs = aligned16(states) && (size_t(T) * sizeof(SS)) % 16 == 0 && aligned16(x) &&
+               (size_t(T) * sizeof(E)) % 16 == 0;
+    rc = rev ? ss_launch<Alg, false, kSsGrad>(p, stream) : ss_launch<Alg, true, kSsGrad>(p, stream);
+    if (rc != PHS_OK) return rc;
+  }
+  out.fb = static_cast<const E *>(f.b);
+  out.fa = static_cast<const E *>(f.a);
+  out.nb = f.nb;
+  out.na = f.na;
+  out.form = f.form;
+  out.f_sh = f.shared;
+  out.gzi = T == 0 ? static_cast<E *>(gzi) : nullptr;
+  out.gzf = static_cast<const E *>(gzf);
+  hipLaunchKernelGGL(ss_grad_rows_kernel<Alg>, dim3(unsigned(B)), dim3(kSsReduceThreads), 0, stream,
+                     static_cast<const C *>(gpart), tiles * SsShape<Alg>::kWaves, rowsum);
+  hipLaunchKernelGGL(ss_grad_finish_kernel<Alg>, dim3(1), dim3(kSsReduceThreads), 0, stream,
+                     static_cast<const C *>(rowsum), B, T, out);
+  return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
 // filtfilt's scratch buffer ("mid"): pass 1's output [B, T] and final state
@@ -235,6 +344,63 @@ int phs_lfilter_rev(int dtype, int64_t B, int64_t T, const void *b, int nb, cons
                     size_t workspace_bytes, void *stream) {
   return lfilter_call(dtype, B, T, b, nb, a, na, coef_shared, form, zi, x, y, zf, workspace, workspace_bytes, true,
                       stream);
+}
+
+size_t phs_lti_ss_bwd_scratch_size(int dtype, int M, int64_t B, int64_t T) {
+  if (B < 0 || T < 0) return 0;
+  size_t out = 0;
+  const int rc = phs::ss_dispatch(dtype, M, [&](auto alg) {
+    out = phs::ss_bwd_layout<decltype(alg)>(B, T).total;
+    return PHS_OK;
+  });
+  return rc == PHS_OK ? out : 0;
+}
+
+int phs_lti_ss_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b, int b_shared,
+                   const void *c, int c_shared, int out_idx, const void *d, int d_shared, const void *zi,
+                   const void *x, const void *gy, const void *gzf, void *gx, void *gzi, void *gA, void *gb, void *gc,
+                   void *gd, int reverse, void *scratch, size_t scratch_bytes, void *workspace,
+                   size_t workspace_bytes, void *stream) {
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return phs::ss_dispatch(dtype, M, [&](auto alg) {
+    using Alg = decltype(alg);
+    using E = typename Alg::elem;
+    phs::SsModelArgs<E> mo;
+    mo.A = A, mo.b = b, mo.c = c, mo.d = d;
+    mo.A_sh = A_shared != 0, mo.b_sh = b_shared != 0, mo.c_sh = c_shared != 0, mo.d_sh = d_shared != 0;
+    mo.out_idx = out_idx;
+    phs::SsGradOut<E> o{};
+    o.gA = static_cast<E *>(gA), o.gb = static_cast<E *>(gb), o.gc = static_cast<E *>(gc), o.gd = static_cast<E *>(gd);
+    o.A_sh = mo.A_sh, o.b_sh = mo.b_sh, o.c_sh = mo.c_sh, o.d_sh = mo.d_sh;
+    return phs::ss_bwd<Alg>(B, T, mo, phs::SsFilter{}, zi, x, gy, gzf, gx, gzi, o, scratch, scratch_bytes, workspace,
+                            workspace_bytes, reverse != 0, st);
+  });
+}
+
+int phs_lfilter_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na, int coef_shared,
+                    int form, const void *zi, const void *x, const void *gy, const void *gzf, void *gx, void *gzi,
+                    void *gb, void *ga, int reverse, void *scratch, size_t scratch_bytes, void *workspace,
+                    size_t workspace_bytes, void *stream) {
+  if (form != PHS_FORM_TDF2 && form != PHS_FORM_DF2) return PHS_ERR_INVALID;
+  const int M = nb - 1 > na ? nb - 1 : na;
+  if (M < 1 || M > 4 || !gb || !ga) return PHS_ERR_INVALID;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  phs::SsFilter f;
+  f.b = b;
+  f.a = a;
+  f.nb = nb;
+  f.na = na;
+  f.form = form == PHS_FORM_TDF2 ? 1 : 2;
+  f.shared = coef_shared != 0;
+  return phs::ss_dispatch(dtype, M, [&](auto alg) {
+    using Alg = decltype(alg);
+    using E = typename Alg::elem;
+    phs::SsGradOut<E> o{};
+    o.gfb = static_cast<E *>(gb);
+    o.gfa = static_cast<E *>(ga);
+    return phs::ss_bwd<Alg>(B, T, phs::SsModelArgs<E>{}, f, zi, x, gy, gzf, gx, gzi, o, scratch, scratch_bytes,
+                            workspace, workspace_bytes, reverse != 0, st);
+  });
 }
 
 size_t phs_filtfilt_workspace_size(int dtype, int64_t B, int64_t T) {

@@ -18,8 +18,17 @@
 // waves scan vectors only against a table of A^(K 2^i) in LDS (the look-back
 // wave builds it while they load): M^2 work and registers per level instead
 // of the M^3 of composing maps.  The gradients with respect to x and zi are
-// this kernel on the adjoint model; those of the coefficients are the
-// composite on the native recurrence ops.
+// this kernel on the adjoint model (A^T, input vector c, output vector b, d,
+// run in the opposite time direction from dL/dzf).  Those of the
+// coefficients take two launches (ss_grad_* below): a forward that writes
+// the state before every step (kSsStates), then the adjoint pass
+// (kSsGrad), which at every step also has the adjoint state lambda[t+1]
+// = dL/dh[t+1], the upstream gradient g[t], the forward state h[t] and the
+// input x[t] in hand and sums, per wave,
+//     dL/dA = sum_t lambda[t+1] h[t]^T,  dL/db = sum_t lambda[t+1] x[t],
+//     dL/dc = sum_t g[t] h[t],           dL/dd = sum_t g[t] x[t],
+// the gradient of the composed graph the reference differentiates
+// (philtorch/lti/ssm.py:467-589, filtering.py:273-333).
 //
 // The same kernel runs both passes of a zero-phase filter (philtorch/lti/
 // filtering.py:413-484 filtfilt): scan positions map to descending time
@@ -37,8 +46,10 @@ struct SsArgs {
   using E = typename Alg::elem;
   const E *A;         // [rows, M, M] row-major
   int64_t A_stride;   // elements between rows (0 = shared)
-  const E *bv;        // [rows, M]; nullptr: the input enters state 0
+  int A_trans;        // use A^T (the adjoint model of an explicit A)
+  const E *bv;        // [rows, M]; nullptr: the input enters state in_idx
   int64_t b_stride;
+  int in_idx;
   const E *cv;        // [rows, M]; nullptr: y is state out_idx
   int64_t c_stride;
   const E *d;         // [rows]; nullptr: no feedthrough
@@ -67,6 +78,14 @@ struct SsArgs {
   const E *x;         // [B, T]
   E *y;               // [B, T]
   E *zf;              // [B, M]; nullable (scan order: the state after the last step scanned)
+  // kSsStates: the state before every step, [B, T, M] at its time index
+  // (y is not written); kSsGrad: the forward's states and input, read at
+  // every step, and the per-wave coefficient-gradient sums
+  // [B, tiles_per_row, kWaves, SsGradN] in compute precision
+  E *hs;
+  const E *hs_fwd, *x_fwd;
+  typename Wide<E>::type *gpart;
+  int vec_hs;         // 16-byte state chunks (T M sizeof(E) % 16 == 0, aligned)
   int64_t B, T_len, tiles_per_row;
   unsigned long long *claims;
   unsigned tiles, per_stripe, spin_limit;
@@ -102,12 +121,12 @@ struct SsShape {
 template <bool REV, typename E, int K>
 __device__ __forceinline__ void ss_load(const E *row, int64_t s0, int64_t T, bool vec, E (&out)[K]) {
   if constexpr (!REV) {
-    load_chunk<E, K>(row, s0, T, vec, out, E(0));
+    load_chunk<E, K>(row, s0, T, vec, out, E{});
   } else {
     const int64_t base = T - s0 - K;  // lowest time of the chunk
     if (vec && base >= 0) {
       E tmp[K];
-      load_chunk<E, K>(row, base, T, true, tmp, E(0));
+      load_chunk<E, K>(row, base, T, true, tmp, E{});
 #pragma unroll
       for (int k = 0; k < K; ++k) out[k] = tmp[K - 1 - k];
     } else {
@@ -117,7 +136,7 @@ __device__ __forceinline__ void ss_load(const E *row, int64_t s0, int64_t T, boo
         if (t >= 0)
           out[k] = row[t];
         else
-          out[k] = E(0);
+          out[k] = E{};
       }
     }
   }
@@ -252,7 +271,8 @@ __device__ __forceinline__ SsModel<Alg> ss_model(const SsArgs<Alg> &a, int64_t r
   SsModel<Alg> m;
   if (a.filt_form == 0) {
     m.A = V::load_mat(a.A + row * a.A_stride);
-    m.b = a.bv ? V::load_vec(a.bv + row * a.b_stride) : V::unit(0);
+    if (a.A_trans) m.A = Alg::s_adjoint(m.A);  // real: the transpose
+    m.b = a.bv ? V::load_vec(a.bv + row * a.b_stride) : V::unit(a.in_idx);
     m.c = a.cv ? V::load_vec(a.cv + row * a.c_stride) : V::unit(a.out_idx);
     m.d = a.d ? a.d[row * a.d_stride] : E(0);
     return m;
@@ -599,8 +619,61 @@ __device__ bool ss_lookback(const uint64_t *row_status, const typename Alg::stat
   }
 }
 
+// Kernel modes: the model's output (plain), the states of a forward for the
+// coefficient gradients (kSsStates: h[t] before every step, no y), the
+// adjoint pass with the coefficient-gradient sums (kSsGrad).
+constexpr int kSsPlain = 0, kSsStates = 1, kSsGrad = 2;
+
+// Coefficient-gradient sums of one model: dL/dA (M x M row-major), dL/db
+// (M), dL/dc (M), dL/dd; a lane sums its own steps in storage precision
+// (32 fp32 or 16 fp64 steps), everything above it in compute precision.
+template <class Alg, typename V = typename Wide<typename Alg::elem>::type>
+struct SsGrad {
+  static constexpr int M = SsView<Alg>::M;
+  static constexpr int kA = 0, kB = M * M, kC = M * M + M, kD = M * M + 2 * M, kN = M * M + 2 * M + 1;
+  V v[kN];
+};
+
+// Steps per group of state loads and stores: at most 64 bytes of states
+// and whole 16-byte vectors of states and inputs (bounds the registers a
+// K-step chunk of order-4 states would take).
+template <class Alg>
+constexpr int ss_state_group() {
+  constexpr int K = SsShape<Alg>::K;
+  constexpr int bytes = int(sizeof(typename Alg::s_state));
+  int g = 1;
+  while (2 * g <= K && 2 * g * bytes <= 64) g *= 2;
+  return g;
+}
+
+// One step's contribution: lambda = dL/dh[t+1] (the adjoint state before
+// the step), hf = h[t], xf = x[t], g = dL/dy[t].
+template <class Alg>
+__device__ __forceinline__ void ss_grad_step(SsGrad<Alg, typename Alg::elem> &acc,
+                                             const typename Alg::s_state &lambda, const typename Alg::s_state &hf,
+                                             typename Alg::elem xf, typename Alg::elem g) {
+  using E = typename Alg::elem;
+  using G = SsGrad<Alg, E>;
+  constexpr int M = G::M;
+  union {
+    typename Alg::s_state s;
+    E e[M];
+  } ul, uh;
+  ul.s = lambda;
+  uh.s = hf;
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    const E li = ul.e[i];
+#pragma unroll
+    for (int j = 0; j < M; ++j) acc.v[G::kA + i * M + j] = fma(li, uh.e[j], acc.v[G::kA + i * M + j]);
+    acc.v[G::kB + i] = fma(li, xf, acc.v[G::kB + i]);
+    acc.v[G::kC + i] = fma(g, uh.e[i], acc.v[G::kC + i]);
+  }
+  acc.v[G::kD] = fma(g, xf, acc.v[G::kD]);
+}
+
 // At least two waves per SIMD (two workgroups per CU).
-template <class Alg, bool REV>
+template <class Alg, bool REV, int MODE>
 __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Alg> a) {
   using E = typename Alg::elem;
   using S = typename Alg::state;
@@ -734,26 +807,198 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
 #pragma unroll
   for (int r = 1; r < R; ++r) ent[r] = Alg::affine(s_tab.pw[6], ent[r - 1], tot[r - 1]);
   ss_pow_apply<Alg, 6, R>(s_tab.pw, sl, ent);
-  E *yrow = a.y + b * T;
+  constexpr int G = ss_state_group<Alg>();
+  const bool vh = a.vec_hs != 0;
+  SsGrad<Alg, E> lacc;
+  if constexpr (MODE == kSsGrad) {
+#pragma unroll
+    for (int j = 0; j < SsGrad<Alg>::kN; ++j) lacc.v[j] = E(0);
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     SS h = Alg::store_s(Alg::sadd(ent[r], ex[r]));
     E O[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      O[k] = fma(m.d, X[r][k], V::dot(m.c, h));
-      h = Alg::s_affine(m.A, h, V::scale(m.b, X[r][k]));
-      if (a.zf && t0s[r] + k == T - 1) {
-        union {
-          SS s;
-          E e[V::M];
-        } u;
-        u.s = h;
+    for (int g0 = 0; g0 < K; g0 += G) {
+      SS Hg[G];
+      E Xg[G];
+      if constexpr (MODE == kSsGrad) {
+        ss_load<REV, SS, G>(reinterpret_cast<const SS *>(a.hs_fwd) + b * T, t0s[r] + g0, T, vh, Hg);
+        ss_load<REV, E, G>(a.x_fwd + b * T, t0s[r] + g0, T, vh, Xg);
+      }
 #pragma unroll
-        for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = u.e[i];
+      for (int k2 = 0; k2 < G; ++k2) {
+        const int k = g0 + k2;
+        if constexpr (MODE == kSsStates) {
+          Hg[k2] = h;
+        } else {
+          O[k] = fma(m.d, X[r][k], V::dot(m.c, h));
+          if constexpr (MODE == kSsGrad) ss_grad_step<Alg>(lacc, h, Hg[k2], Xg[k2], X[r][k]);
+        }
+        h = Alg::s_affine(m.A, h, V::scale(m.b, X[r][k]));
+        if (MODE != kSsStates && a.zf && t0s[r] + k == T - 1) {
+          union {
+            SS s;
+            E e[V::M];
+          } u;
+          u.s = h;
+#pragma unroll
+          for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = u.e[i];
+        }
+      }
+      if constexpr (MODE == kSsStates)
+        ss_store<REV, SS, G>(reinterpret_cast<SS *>(a.hs) + b * T, t0s[r] + g0, T, vh, Hg);
+    }
+    if (MODE != kSsStates && a.y) ss_store<REV, E, K>(a.y + b * T, t0s[r], T, vec, O);
+  }
+  if constexpr (MODE == kSsGrad) {
+    // the wave's sums, in a fixed order, one partial per (row, tile, wave)
+    auto add = [](const SsGrad<Alg> &p, const SsGrad<Alg> &o) {
+      SsGrad<Alg> r;
+#pragma unroll
+      for (int j = 0; j < SsGrad<Alg>::kN; ++j) r.v[j] = p.v[j] + o.v[j];
+      return r;
+    };
+    SsGrad<Alg> gacc;
+#pragma unroll
+    for (int j = 0; j < SsGrad<Alg>::kN; ++j) gacc.v[j] = up(lacc.v[j]);
+    gacc = wave_scan_incl(gacc, lane, add);
+    if (lane == 63) {
+      auto *dst = a.gpart + ((b * a.tiles_per_row + q) * kWaves + w) * SsGrad<Alg>::kN;
+#pragma unroll
+      for (int j = 0; j < SsGrad<Alg>::kN; ++j) dst[j] = gacc.v[j];
+    }
+  }
+}
+
+// ------------------------------------------------------------ coefficient gradients
+// Where the sums go: the explicit model's dL/dA, dL/db, dL/dc, dL/dd (each
+// nullable; one per row, or one in all for a shared operand), or the
+// filter's dL/dfb, dL/dfa by the chain rule through its companion model.
+template <typename E>
+struct SsGradOut {
+  E *gA, *gb, *gc, *gd;
+  bool A_sh, b_sh, c_sh, d_sh;
+  E *gfb, *gfa;  // filter mode (form != 0)
+  const E *fb, *fa;
+  int nb, na, form;
+  bool f_sh;
+  // T == 0: grad_zi = grad_zf (or 0), written here
+  E *gzi;
+  const E *gzf;
+};
+
+constexpr int kSsReduceThreads = 256;
+
+// Row b's sums over its per-wave partials (fixed order): rowsum[b, j].
+template <class Alg>
+__global__ __launch_bounds__(kSsReduceThreads) void ss_grad_rows_kernel(
+    const typename Wide<typename Alg::elem>::type *gpart, int64_t per_row,
+    typename Wide<typename Alg::elem>::type *rowsum) {
+  using C = typename Wide<typename Alg::elem>::type;
+  constexpr int N = SsGrad<Alg>::kN;
+  __shared__ C s[kSsReduceThreads];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
+  for (int j = 0; j < N; ++j) {
+    C acc = 0;
+    for (int64_t i = tid; i < per_row; i += kSsReduceThreads) acc += gpart[(b * per_row + i) * N + j];
+    s[tid] = acc;
+    __syncthreads();
+    for (int h = kSsReduceThreads / 2; h > 0; h >>= 1) {
+      if (tid < h) s[tid] += s[tid + h];
+      __syncthreads();
+    }
+    if (tid == 0) rowsum[b * N + j] = s[0];
+    __syncthreads();
+  }
+}
+
+// dL/dfb, dL/dfa of one filter from its model's sums G (chain rule through
+// the companion model of ss_model: TDF-II b = fb[1:] - fb[0] a, A[i][0] =
+// -a_i; DF-II c = fb[1:] - fb[0] a, A[0][j] = -a_j; d = fb[0]).
+template <class Alg>
+__device__ void ss_filter_chain(const typename Wide<typename Alg::elem>::type *Gs, const SsGradOut<typename Alg::elem> &o,
+                                const typename Alg::elem *fb, const typename Alg::elem *fa, typename Alg::elem *gfb,
+                                typename Alg::elem *gfa) {
+  using E = typename Alg::elem;
+  using C = typename Wide<E>::type;
+  using G = SsGrad<Alg>;
+  constexpr int M = G::M;
+  const C b0 = C(fb[0]);
+  const int vec_at = o.form == 1 ? G::kB : G::kC;  // the vector that carries fb[1:] - fb[0] a
+  C g0 = Gs[G::kD];
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    const C ai = i < o.na ? C(fa[i]) : C(0);
+    const C gv = Gs[vec_at + i];
+    g0 -= ai * gv;
+    if (i + 1 < o.nb) gfb[i + 1] = E(gv);
+    const C gA = o.form == 1 ? Gs[G::kA + i * M] : Gs[G::kA + i];  // A[i][0] or A[0][i]
+    if (i < o.na) gfa[i] = E(-gA - b0 * gv);
+  }
+  gfb[0] = E(g0);
+}
+
+// Every output from the row sums: shared operands summed over the rows (a
+// tree over the block, fixed order), the filter's chain rule per row or
+// once.  One block.
+template <class Alg>
+__global__ __launch_bounds__(kSsReduceThreads) void ss_grad_finish_kernel(
+    const typename Wide<typename Alg::elem>::type *rowsum, int64_t B, int64_t T, SsGradOut<typename Alg::elem> o) {
+  using E = typename Alg::elem;
+  using C = typename Wide<E>::type;
+  using G = SsGrad<Alg>;
+  constexpr int M = G::M, N = G::kN;
+  __shared__ C s[kSsReduceThreads];
+  __shared__ C tot[N];
+  const int tid = threadIdx.x;
+  if (T == 0 && o.gzi) {
+    for (int64_t i = tid; i < B * M; i += kSsReduceThreads) o.gzi[i] = o.gzf ? o.gzf[i] : E(0);
+  }
+  auto total = [&](int j) {
+    C acc = 0;
+    for (int64_t b = tid; b < B; b += kSsReduceThreads) acc += rowsum[b * N + j];
+    s[tid] = acc;
+    __syncthreads();
+    for (int h = kSsReduceThreads / 2; h > 0; h >>= 1) {
+      if (tid < h) s[tid] += s[tid + h];
+      __syncthreads();
+    }
+    if (tid == 0) tot[j] = s[0];
+    __syncthreads();
+  };
+  if (o.form != 0) {
+    if (o.f_sh) {
+      for (int j = 0; j < N; ++j) total(j);
+      if (tid == 0) ss_filter_chain<Alg>(tot, o, o.fb, o.fa, o.gfb, o.gfa);
+    } else {
+      for (int64_t b = tid; b < B; b += kSsReduceThreads)
+        ss_filter_chain<Alg>(rowsum + b * N, o, o.fb + b * o.nb, o.fa + b * o.na, o.gfb + b * o.nb,
+                             o.gfa + b * o.na);
+    }
+    return;
+  }
+  struct Part {
+    E *dst;
+    bool sh;
+    int off, n;
+  };
+  const Part parts[4] = {{o.gA, o.A_sh, G::kA, M * M}, {o.gb, o.b_sh, G::kB, M}, {o.gc, o.c_sh, G::kC, M},
+                         {o.gd, o.d_sh, G::kD, 1}};
+  for (int p = 0; p < 4; ++p) {
+    const Part pt = parts[p];
+    if (!pt.dst) continue;
+    if (pt.sh) {
+      for (int j = 0; j < pt.n; ++j) total(pt.off + j);
+      if (tid < pt.n) pt.dst[tid] = E(tot[pt.off + tid]);
+      __syncthreads();
+    } else {
+      for (int64_t i = tid; i < B * pt.n; i += kSsReduceThreads) {
+        const int64_t b = i / pt.n;
+        pt.dst[i] = E(rowsum[b * N + pt.off + int(i - b * pt.n)]);
       }
     }
-    ss_store<REV, E, K>(yrow, t0s[r], T, vec, O);
   }
 }
 

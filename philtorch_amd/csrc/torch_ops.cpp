@@ -516,14 +516,14 @@ Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t p
 // A (M, M) or (batch, M, M); B, C None, (M,) or (batch, M); D None, one value
 // or (batch,); zi None or (batch, M); out_idx selects the output state when
 // C is None; reverse runs the model backwards in time (phs_lti_ss_rev).
-std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
-                                      const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
-                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
-                                      bool reverse) {
+// lti_ss's argument checks (shared by its backward); returns M.
+int64_t lti_ss_meta_check(const Tensor &A, const std::optional<Tensor> &Bm, const std::optional<Tensor> &Cm,
+                          const std::optional<Tensor> &Dm, const std::optional<Tensor> &zi, const Tensor &x,
+                          int64_t out_idx) {
   TORCH_CHECK(x.dim() == 2, "philtorch::lti_ss: x must be a 2D tensor (batch, time)");
   TORCH_CHECK((A.dim() == 2 || A.dim() == 3) && A.size(-1) == A.size(-2),
               "philtorch::lti_ss: A must be (M, M) or (batch, M, M)");
-  const int64_t B = x.size(0), T = x.size(1), M = A.size(-1);
+  const int64_t B = x.size(0), M = A.size(-1);
   TORCH_CHECK(M >= 1 && M <= kMaxOrder, "philtorch::lti_ss: state order 1 to ", kMaxOrder, ", got ", M);
   if (A.dim() == 3) TORCH_CHECK(A.size(0) == B, "philtorch::lti_ss: a 3D A must have x's batch size");
   TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,
@@ -554,6 +554,15 @@ std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tenso
     same(*zi, "zi");
     TORCH_CHECK(zi->dim() == 2 && zi->size(0) == B && zi->size(1) == M, "philtorch::lti_ss: zi must be (batch, M)");
   }
+  return M;
+}
+
+std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
+                                      const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
+                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
+                                      bool reverse) {
+  const int64_t M = lti_ss_meta_check(A, Bm, Cm, Dm, zi, x, out_idx);
+  const int64_t B = x.size(0), T = x.size(1);
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
   const int dt = phs_dtype_of(x.scalar_type());
   Tensor Ac = A.contiguous(), xc = x.contiguous();
@@ -584,12 +593,13 @@ std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tenso
 // denominator after its leading 1; form 0 "tdf2", 1 "df2"; zi None or
 // (batch, max(nb - 1, na)); reverse runs the filter backwards in time
 // (phs_lfilter_rev).
-std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, const std::optional<Tensor> &zi,
-                                          const Tensor &x, int64_t form, bool reverse) {
+// lfilter_ss's argument checks (shared by its backward); returns the order.
+int64_t lfilter_ss_meta_check(const Tensor &b, const Tensor &a, const std::optional<Tensor> &zi, const Tensor &x,
+                              int64_t form) {
   TORCH_CHECK(x.dim() == 2, "philtorch::lfilter_ss: x must be a 2D tensor (batch, time)");
   TORCH_CHECK(b.dim() == a.dim() && (b.dim() == 1 || b.dim() == 2),
               "philtorch::lfilter_ss: b and a must both be 1D (shared) or both 2D (batch, taps)");
-  const int64_t B = x.size(0), T = x.size(1), nb = b.size(-1), na = a.size(-1);
+  const int64_t B = x.size(0), nb = b.size(-1), na = a.size(-1);
   if (b.dim() == 2)
     TORCH_CHECK(b.size(0) == B && a.size(0) == B, "philtorch::lfilter_ss: 2D b and a must have x's batch size");
   const int64_t M = std::max(nb - 1, na);
@@ -606,6 +616,13 @@ std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, cons
                     zi->device() == x.device(),
                 "philtorch::lfilter_ss: zi must be (batch, order) with x's scalar type");
   }
+  return M;
+}
+
+std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, const std::optional<Tensor> &zi,
+                                          const Tensor &x, int64_t form, bool reverse) {
+  const int64_t M = lfilter_ss_meta_check(b, a, zi, x, form);
+  const int64_t B = x.size(0), T = x.size(1), nb = b.size(-1), na = a.size(-1);
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
   const int dt = phs_dtype_of(x.scalar_type());
   Tensor bc = b.contiguous(), ac = a.contiguous(), xc = x.contiguous(), zc = zi ? zi->contiguous() : Tensor();
@@ -624,6 +641,97 @@ std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, cons
                                stream),
                "lfilter_ss");
   return {y, zf};
+}
+
+// Gradients of lti_ss w.r.t. every input (phs_lti_ss_bwd): returns
+// (grad_A, grad_B, grad_C, grad_D, grad_zi, grad_x), each shaped like its
+// input (a shared operand's gradient summed over the rows; an absent
+// operand's an empty tensor; grad_zi (batch, M) whether zi was given or
+// not).  grad_zf None is zero.  Replaces the autograd of the composed state
+// space (philtorch/lti/ssm.py:386-589).
+std::vector<Tensor> lti_ss_backward_hip(const Tensor &A, const std::optional<Tensor> &Bm,
+                                        const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
+                                        const std::optional<Tensor> &zi, const Tensor &x, const Tensor &gy,
+                                        const std::optional<Tensor> &gzf, int64_t out_idx, bool reverse) {
+  // the forward's argument checks
+  (void)lti_ss_meta_check(A, Bm, Cm, Dm, zi, x, out_idx);
+  const int64_t B = x.size(0), T = x.size(1), M = A.size(-1);
+  TORCH_CHECK(gy.sizes() == x.sizes() && gy.device() == x.device(),
+              "philtorch::lti_ss_backward: grad_y must have x's shape and device");
+  if (gzf)
+    TORCH_CHECK(gzf->dim() == 2 && gzf->size(0) == B && gzf->size(1) == M && gzf->device() == x.device(),
+                "philtorch::lti_ss_backward: grad_zf must be (batch, M)");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor Ac = A.contiguous(), xc = x.contiguous(), gc = gy.to(x.scalar_type()).contiguous();
+  Tensor bc = Bm ? Bm->contiguous() : Tensor(), cc = Cm ? Cm->contiguous() : Tensor();
+  Tensor dc = Dm ? Dm->contiguous() : Tensor(), zc = zi ? zi->contiguous() : Tensor();
+  Tensor gzc = gzf ? gzf->to(x.scalar_type()).contiguous() : Tensor();
+  Tensor gA = at::empty(A.sizes(), A.options());
+  Tensor gB = Bm ? at::empty(Bm->sizes(), Bm->options()) : at::empty({0}, x.options());
+  Tensor gC = Cm ? at::empty(Cm->sizes(), Cm->options()) : at::empty({0}, x.options());
+  Tensor gD = Dm ? at::empty(Dm->sizes(), Dm->options()) : at::empty({0}, x.options());
+  Tensor gzi = at::empty({B, M}, x.options());
+  Tensor gx = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  if (B == 0) {
+    gA.zero_(), gB.zero_(), gC.zero_(), gD.zero_();
+    return {gA, gB, gC, gD, gzi, gx};
+  }
+  void *stream = stream_of(x);
+  Tensor scratch = at::empty({int64_t(phs_lti_ss_bwd_scratch_size(dt, int(M), B, T))}, x.options().dtype(at::kByte));
+  const Workspace ws = workspace_for(x, phs_lti_ss_workspace_size(dt, int(M), B, T), stream);
+  check_status(phs_lti_ss_bwd(dt, int(M), B, T, Ac.const_data_ptr(), A.dim() == 2 ? 1 : 0,
+                              Bm ? bc.const_data_ptr() : nullptr, Bm && Bm->dim() == 1 ? 1 : 0,
+                              Cm ? cc.const_data_ptr() : nullptr, Cm && Cm->dim() == 1 ? 1 : 0, int(out_idx),
+                              Dm ? dc.const_data_ptr() : nullptr, Dm && Dm->numel() == 1 ? 1 : 0,
+                              zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(), gc.const_data_ptr(),
+                              gzf ? gzc.const_data_ptr() : nullptr, gx.mutable_data_ptr(), gzi.mutable_data_ptr(),
+                              gA.mutable_data_ptr(), Bm ? gB.mutable_data_ptr() : nullptr,
+                              Cm ? gC.mutable_data_ptr() : nullptr, Dm ? gD.mutable_data_ptr() : nullptr,
+                              reverse ? 1 : 0, scratch.mutable_data_ptr(), size_t(scratch.numel()), ws.ptr, ws.bytes,
+                              stream),
+               "lti_ss_backward");
+  return {gA, gB, gC, gD, gzi, gx};
+}
+
+// Gradients of lfilter_ss w.r.t. (b, a, zi, x) (phs_lfilter_bwd): returns
+// (grad_b, grad_a, grad_zi, grad_x) shaped like the inputs (grad_zi (batch,
+// order) whether zi was given or not); grad_zf None is zero.  Replaces the
+// autograd of the companion-form route (philtorch/lti/filtering.py:273-333).
+std::vector<Tensor> lfilter_ss_backward_hip(const Tensor &b, const Tensor &a, const std::optional<Tensor> &zi,
+                                            const Tensor &x, const Tensor &gy, const std::optional<Tensor> &gzf,
+                                            int64_t form, bool reverse) {
+  (void)lfilter_ss_meta_check(b, a, zi, x, form);
+  const int64_t B = x.size(0), T = x.size(1), nb = b.size(-1), na = a.size(-1);
+  const int64_t M = std::max(nb - 1, na);
+  TORCH_CHECK(gy.sizes() == x.sizes() && gy.device() == x.device(),
+              "philtorch::lfilter_ss_backward: grad_y must have x's shape and device");
+  if (gzf)
+    TORCH_CHECK(gzf->dim() == 2 && gzf->size(0) == B && gzf->size(1) == M && gzf->device() == x.device(),
+                "philtorch::lfilter_ss_backward: grad_zf must be (batch, order)");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor bc = b.contiguous(), ac = a.contiguous(), xc = x.contiguous(), zc = zi ? zi->contiguous() : Tensor();
+  Tensor gc = gy.to(x.scalar_type()).contiguous();
+  Tensor gzc = gzf ? gzf->to(x.scalar_type()).contiguous() : Tensor();
+  Tensor gb = at::empty(b.sizes(), b.options()), ga = at::empty(a.sizes(), a.options());
+  Tensor gzi = at::empty({B, M}, x.options());
+  Tensor gx = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  if (B == 0) {
+    gb.zero_(), ga.zero_();
+    return {gb, ga, gzi, gx};
+  }
+  void *stream = stream_of(x);
+  Tensor scratch = at::empty({int64_t(phs_lti_ss_bwd_scratch_size(dt, int(M), B, T))}, x.options().dtype(at::kByte));
+  const Workspace ws = workspace_for(x, phs_lti_ss_workspace_size(dt, int(M), B, T), stream);
+  check_status(phs_lfilter_bwd(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
+                               b.dim() == 1 ? 1 : 0, int(form), zi ? zc.const_data_ptr() : nullptr,
+                               xc.const_data_ptr(), gc.const_data_ptr(), gzf ? gzc.const_data_ptr() : nullptr,
+                               gx.mutable_data_ptr(), gzi.mutable_data_ptr(), gb.mutable_data_ptr(),
+                               ga.mutable_data_ptr(), reverse ? 1 : 0, scratch.mutable_data_ptr(),
+                               size_t(scratch.numel()), ws.ptr, ws.bytes, stream),
+               "lfilter_ss_backward");
+  return {gb, ga, gzi, gx};
 }
 
 // Single-input single-output LPV state space of order <= 4, fused
@@ -882,6 +990,13 @@ TORCH_LIBRARY(philtorch, m) {
   // new: lfilter of order <= 4 from b and a (companion model built in the kernel): (y, zf)
   m.def("lfilter_ss(Tensor b, Tensor a, Tensor? zi, Tensor x, int form, bool reverse=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
+  // new: their fused gradients w.r.t. every input (coefficients included)
+  m.def("lti_ss_backward(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, Tensor grad_y, "
+        "Tensor? grad_zf, int out_idx, bool reverse=False) -> Tensor[]",
+        {at::Tag::pt2_compliant_tag});
+  m.def("lfilter_ss_backward(Tensor b, Tensor a, Tensor? zi, Tensor x, Tensor grad_y, Tensor? grad_zf, int form, "
+        "bool reverse=False) -> Tensor[]",
+        {at::Tag::pt2_compliant_tag});
   m.def("lpv_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx, bool reverse=False, "
         "bool transpose_A=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
@@ -903,6 +1018,8 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("filtfilt", &filtfilt_hip);
   m.impl("lti_ss", &lti_ss_hip);
   m.impl("lfilter_ss", &lfilter_ss_hip);
+  m.impl("lti_ss_backward", &lti_ss_backward_hip);
+  m.impl("lfilter_ss_backward", &lfilter_ss_backward_hip);
   m.impl("lpv_ss", &lpv_ss_hip);
 }
 

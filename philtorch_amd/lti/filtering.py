@@ -110,12 +110,12 @@ def _fused_biquad(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor]):
 
 def _fused_lfilter_applies(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor], form: str, kwargs) -> bool:
     """A filter of order 1 to 4 on a HIP device with the native route
-    requested (``unroll_factor=1``) and no gradient wanted for b or a:
-    philtorch::lfilter_ss builds the companion model from b and a inside the
-    kernel and runs B x, the scan, the state shift and C h + D x in one pass
-    (the TDF-II biquad takes the cascade kernel first); gradients for x and zi
-    are one more pass of the adjoint form.  Where b or a need a gradient the
-    composed route runs, as in the reference."""
+    requested (``unroll_factor=1``): philtorch::lfilter_ss builds the
+    companion model from b and a inside the kernel and runs B x, the scan,
+    the state shift and C h + D x in one pass (the TDF-II biquad takes the
+    cascade kernel first); gradients for x and zi are one more pass of the
+    adjoint form, those of b and a two fused passes
+    (philtorch::lfilter_ss_backward)."""
     from .. import EXTENSION_LOADED
 
     if not (EXTENSION_LOADED and x.is_cuda and form in ("tdf2", "df2") and set(kwargs) == {"unroll_factor"}
@@ -131,8 +131,6 @@ def _fused_lfilter_applies(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor]
     if zi is not None and not (tuple(zi.shape) in ((M,), (x.size(0), M))):
         return False
     if not hasattr(torch.ops.philtorch, "lfilter_ss"):
-        return False
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (b, a)):
         return False
     import torch.autograd.forward_ad as fwad
 

@@ -225,12 +225,11 @@ def _fused_ss_applies(A: Tensor, x: Tensor, B, C, D, zi, unroll_factor, out_idx)
     """A single-input single-output model of order <= 4 (2D x; B, C an
     M-vector per model or shared, or C replaced by out_idx; D one value per
     row or shared) on a HIP device with the native route requested
-    (``unroll_factor=1``) and no gradient wanted for A, B, C or D:
-    philtorch::lti_ss runs B x, the scan, the state shift and C h + D x in one
-    pass, and gradients for x and zi are one pass of the adjoint model.  Where
-    a coefficient needs a gradient the composed route runs (the op's own
-    gradient would recompute that route, so taking the op there would only
-    add its forward); forward-mode AD keeps the composed route too."""
+    (``unroll_factor=1``): philtorch::lti_ss runs B x, the scan, the state
+    shift and C h + D x in one pass; gradients for x and zi are one pass of
+    the adjoint model, and those of A, B, C, D two fused passes
+    (philtorch::lti_ss_backward).  Forward-mode AD keeps the composed
+    route."""
     from .. import EXTENSION_LOADED
 
     if not (EXTENSION_LOADED and x.is_cuda and unroll_factor == 1 and x.dim() == 2):
@@ -243,8 +242,6 @@ def _fused_ss_applies(A: Tensor, x: Tensor, B, C, D, zi, unroll_factor, out_idx)
     if any(t is not None and t.dtype != x.dtype for t in (A, B, C, D, zi)):
         return False
     if C is None and out_idx is None:
-        return False
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (A, B, C, D)):
         return False
 
     def is_vec(t):

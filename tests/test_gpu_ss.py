@@ -290,7 +290,8 @@ def test_state_space_route_choice(hip):
     assert not ssm._fused_ss_applies(A, x.cpu(), v, v, None, None, 1, None)
     assert not ssm._fused_ss_applies(A.double(), x, v, v, None, None, 1, None)
     assert ssm._fused_ss_applies(A, x.requires_grad_(), v, v, None, None, 1, None)  # grad_x by the adjoint
-    assert not ssm._fused_ss_applies(A.requires_grad_(), x, v, v, None, None, 1, None)
+    # coefficient gradients: the fused backward (philtorch::lti_ss_backward)
+    assert ssm._fused_ss_applies(A.requires_grad_(), x, v, v, None, None, 1, None)
     with torch.no_grad():
         assert ssm._fused_ss_applies(A, x, v, v, None, None, 1, None)
 
