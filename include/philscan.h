@@ -415,6 +415,38 @@ int phs_lpv_ss_rev(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
                    int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
                    const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- Gradients of phs_lpv_ss_fwd (reverse = 0) or phs_lpv_ss_rev
+ * (reverse = 1) w.r.t. x, zi and every coefficient, in two passes (the
+ * forward again keeping its states, then the adjoint model in the opposite
+ * time direction).  Replaces the autograd of the composed LPV state space
+ * (philtorch/lpv/ssm.py:337-581):
+ *     dL/dA[t] = lambda[t+1] h[t]^T,  dL/db[t] = lambda[t+1] x[t],
+ *     dL/dc[t] = g[t] h[t],           dL/dd[t] = g[t] x[t],
+ * lambda[t] = A[t]^T lambda[t+1] + c[t] g[t] from lambda[T] = dL/dzf,
+ * summed over the axes an operand shares.  The model's arguments are
+ * phs_lpv_ss_fwd's; gy [B,T]; gzf [B,M] or NULL; outputs gx [B,T], gzi [B,M]
+ * and gA, gb, gc, gd contiguous in their operand's shape (A [B|1,T,M,M]
+ * without the row axis when shared; b, c [1|B, 1|T, M]; d [1|B, 1|T]; a
+ * stride-0 axis of the operand has extent 1), each nullable (gb, gc, gd NULL
+ * when their operand is).  `scratch`: phs_lpv_ss_bwd_scratch_size bytes for
+ * the same step_shared, the PHS_LPV_GRAD_* bits of the operands that vary
+ * along time and are shared by the rows (A with PHS_LPV_A_SHARED, b, c, d
+ * with row stride 0 and time stride not 0), any contents; `workspace`:
+ * phs_lpv_ss_workspace_size bytes. */
+#define PHS_LPV_GRAD_A 1
+#define PHS_LPV_GRAD_B 2
+#define PHS_LPV_GRAD_C 4
+#define PHS_LPV_GRAD_D 8
+
+size_t phs_lpv_ss_bwd_scratch_size(int dtype, int M, int64_t B, int64_t T, int step_shared);
+
+int phs_lpv_ss_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_flags, const void *b,
+                   int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
+                   int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi,
+                   const void *x, const void *gy, const void *gzf, void *gx, void *gzi, void *gA, void *gb, void *gc,
+                   void *gd, int reverse, void *scratch, size_t scratch_bytes, void *workspace,
+                   size_t workspace_bytes, void *stream);
+
 /* ---- Measurement helper, no counterpart in the reference.  A streaming
  * kernel with no scan: out_j[i] = (j + 1) * sum_k in_k[i] over n fp32
  * elements, n_in = 1..3 input arrays and n_out = 1..2 output arrays (16-byte

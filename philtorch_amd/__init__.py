@@ -485,6 +485,13 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         torch._check(A.ndim in (3, 4) and A.shape[-1] == A.shape[-2], lambda: "A must be (T, M, M) or (batch, T, M, M)")
         return _fake_like(x), x.new_empty((x.shape[0], A.shape[-1]))
 
+    if _has_op("lpv_ss_backward"):
+
+        @torch.library.register_fake("philtorch::lpv_ss_backward")
+        def _(A, B, C, D, zi, x, grad_y, grad_zf, out_idx, reverse=False, transpose_A=False):
+            e = lambda t: x.new_empty(t.shape) if t is not None else x.new_empty((0,))  # noqa: E731
+            return [e(A), e(B), e(C), e(D), x.new_empty((x.shape[0], A.shape[-1])), _fake_like(x)]
+
     def _lpv_ss_setup(ctx, inputs, output):
         A, B, C, D, zi, x, out_idx = inputs[:7]
         ctx.out_idx = out_idx
@@ -496,17 +503,28 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         """With A, B, C, D constant: the adjoint model (A[t]^T, input vector
         c[t], output vector b[t], d[t]) run in the opposite time direction
         from dL/dzf gives grad_x and grad_zi in one more lpv_ss pass, which
-        reads A transposed where it lies (transpose_A; no copy of A).
-        Otherwise the gradient of the composite the fused kernel replaces
-        (B x, the native LPV scan, the state shift, C h + D x;
-        philtorch/lpv/ssm.py:337-581), recomputed from the inputs.  Both are
-        differentiable again under create_graph."""
+        reads A transposed where it lies (transpose_A; no copy of A).  With
+        a coefficient gradient wanted: philtorch::lpv_ss_backward (the
+        forward again keeping its states, then the adjoint pass writing
+        lambda[t+1] h[t]^T, lambda[t+1] x[t], g[t] h[t], g[t] x[t] per step,
+        summed over the axes an operand shares).  Under create_graph: the
+        gradient of the composite the fused kernel replaces (B x, the native
+        LPV scan, the state shift, C h + D x; philtorch/lpv/ssm.py:337-581),
+        recomputed from the inputs and differentiable again."""
         from .lpv.ssm import _lpv_state_space_composite
 
         inputs = ctx.saved_tensors
         needs = ctx.needs_input_grad
         A, B, C, D, zi, x = inputs
         out = [None] * 9
+        if any(needs[:4]) and not torch.is_grad_enabled() and _has_op("lpv_ss_backward"):
+            g = gy if gy is not None else torch.zeros_like(x)
+            res = torch.ops.philtorch.lpv_ss_backward(A, B, C, D, zi, x, g, gzf, ctx.out_idx, ctx.reverse,
+                                                      ctx.transpose_A)
+            for i, t in enumerate(inputs):
+                if t is not None and needs[i]:
+                    out[i] = res[i]
+            return tuple(out)
         if not any(needs[:4]):
             M = A.size(-1)
             c_in = C

@@ -15,7 +15,14 @@
 // words, and pass 2 re-runs the steps from each lane's entry state, writing
 // c[t] . h + d[t] x[t] instead of h.  A reversed mode runs the model
 // backwards in time: the gradients w.r.t. x and zi are that mode on the
-// adjoint model; those of A, b, c, d are the composite route's.
+// adjoint model.  Those of A, b, c, d take two launches, as for the LTI
+// model (phs_ss.hpp): the forward again writing its states (kSsStates),
+// then the adjoint pass (kSsGrad), which at every step writes
+//     dL/dA[t] = lambda[t+1] h[t]^T, dL/db[t] = lambda[t+1] x[t],
+//     dL/dc[t] = g[t] h[t],          dL/dd[t] = g[t] x[t]
+// for the operands that vary along time (into a per-row scratch where the
+// rows share them, summed over the rows afterwards) and sums them per wave
+// for those constant in time.
 #pragma once
 
 #include "phs_ss.hpp"
@@ -36,14 +43,27 @@ struct LpvSsArgs {
   const E *A;            // [rows, T, M, M]
   int64_t A_row_stride;  // elements between rows (0 = shared)
   int A_trans;           // read each step's matrix transposed (the adjoint model's A[t]^T)
-  LpvOperand<E> bv;      // [., ., M]; p nullptr: the input enters state 0
+  LpvOperand<E> bv;      // [., ., M]; p nullptr: the input enters state in_idx
   LpvOperand<E> cv;      // [., ., M]; p nullptr: y is state out_idx
   LpvOperand<E> d;       // [., .]; p nullptr: no feedthrough
-  int out_idx;
+  int out_idx, in_idx;
   const E *zi;  // [B, M]; nullptr: zeros
   const E *x;   // [B, T]
   E *y;         // [B, T]
   E *zf;        // [B, M]; nullable
+  // kSsStates: the state before every step [B, T, M] (no y); kSsGrad: the
+  // forward's states and input, the per-(row, step) gradients of the
+  // operands that vary along time ([B, T, M*M], [B, T, M], [B, T, M],
+  // [B, T]; each nullable; dL/dA[t] written transposed with gA_trans, for
+  // a forward that read A transposed) and the per-wave sums of b, c, d where
+  // they are constant in time ([B, tiles, kWaves, SsGrad::kN])
+  E *hs;
+  const E *hs_fwd, *x_fwd;
+  int vec_hs;
+  E *gA_step, *gb_step, *gc_step, *gd_step;
+  int gA_trans;
+  int sum_b, sum_c, sum_d;
+  typename Wide<E>::type *gpart;
   int64_t B, T_len, tiles_per_row;
   unsigned long long *claims;
   unsigned tiles, per_stripe, spin_limit;
@@ -152,8 +172,57 @@ __device__ __forceinline__ void lpv_inputs(const LpvSsArgs<Alg> &a, int64_t b, i
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const int64_t t = lpv_time<REV>(s0 + k, a.T_len);
-    X[k] = V::scale(bp ? V::load_vec(bp + t * a.bv.t_stride) : V::unit(0), u[k]);
+    X[k] = V::scale(bp ? V::load_vec(bp + t * a.bv.t_stride) : V::unit(a.in_idx), u[k]);
   }
+}
+
+// One step of the adjoint pass's coefficient gradients at time t of row b
+// (valid: t inside the row): lambda = dL/dh[t+1] (the adjoint state before
+// the step), g = dL/dy[t], hf = h[t], xf = x[t].
+template <class Alg>
+__device__ __forceinline__ void lpv_grad_step(const LpvSsArgs<Alg> &a, int64_t b, int64_t t, bool valid,
+                                              const typename Alg::s_state &lambda, typename Alg::elem g,
+                                              const typename Alg::s_state &hf, typename Alg::elem xf,
+                                              SsGrad<Alg, typename Alg::elem> &acc) {
+  using E = typename Alg::elem;
+  using G = SsGrad<Alg, E>;
+  constexpr int M = G::M;
+  union {
+    typename Alg::s_state s;
+    E e[M];
+  } ul, uh;
+  ul.s = lambda;
+  uh.s = hf;
+  const int64_t rt = b * a.T_len + t;
+  if (valid && a.gA_step) {
+    union {
+      typename Alg::s_coef s;
+      E e[M * M];
+    } u;
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+#pragma unroll
+      for (int j = 0; j < M; ++j) u.e[i * M + j] = a.gA_trans ? uh.e[i] * ul.e[j] : ul.e[i] * uh.e[j];
+    reinterpret_cast<typename Alg::s_coef *>(a.gA_step)[rt] = u.s;
+  }
+  if (valid && a.gb_step) {
+#pragma unroll
+    for (int i = 0; i < M; ++i) a.gb_step[rt * M + i] = ul.e[i] * xf;
+  }
+  if (valid && a.gc_step) {
+#pragma unroll
+    for (int i = 0; i < M; ++i) a.gc_step[rt * M + i] = g * uh.e[i];
+  }
+  if (valid && a.gd_step) a.gd_step[rt] = g * xf;
+  if (a.sum_b) {
+#pragma unroll
+    for (int i = 0; i < M; ++i) acc.v[G::kB + i] = fma(ul.e[i], xf, acc.v[G::kB + i]);
+  }
+  if (a.sum_c) {
+#pragma unroll
+    for (int i = 0; i < M; ++i) acc.v[G::kC + i] = fma(g, uh.e[i], acc.v[G::kC + i]);
+  }
+  if (a.sum_d) acc.v[G::kD] = fma(g, xf, acc.v[G::kD]);
 }
 
 // State entering tile position `span` of a row, folded from the inputs (the
@@ -192,8 +261,8 @@ __device__ __noinline__ typename Alg::state lpv_prefix_fallback(LpvSsArgs<Alg> a
 
 // REV runs the model backwards in time: scan position s is time T-1-s (zi
 // the state before the last sample, zf after the first), the form of the
-// adjoint pass.
-template <class Alg, bool REV>
+// adjoint pass.  MODE as ss_kernel's.
+template <class Alg, bool REV, int MODE>
 __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(LpvSsArgs<Alg> a) {
   using E = typename Alg::elem;
   using S = typename Alg::state;
@@ -288,23 +357,39 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
   const S hw = apply<Alg>(s_wpre[w], s_in);
 
   // ---- pass 2: y = c[t] . h + d[t] x[t], then the step
-  E *yrow = a.y + b * T;
   const E *cp = a.cv.p ? a.cv.p + b * a.cv.row_stride : nullptr;
   const E *dp = a.d.p ? a.d.p + b * a.d.row_stride : nullptr;
   const SS c_fixed = V::unit(a.out_idx);
+  const bool vh = a.vec_hs != 0;
+  SsGrad<Alg, E> lacc;
+  if constexpr (MODE == kSsGrad) {
+#pragma unroll
+    for (int j = 0; j < SsGrad<Alg>::kN; ++j) lacc.v[j] = E(0);
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t t0 = chunk0(r);
     SS h = Alg::store_s(apply<Alg>(Ex[r], hw));
+    SS Hf[K];
+    E Xf[K];
+    if constexpr (MODE == kSsGrad) {
+      lpv_load<REV, SS, K>(reinterpret_cast<const SS *>(a.hs_fwd) + b * T, t0, T, vh, Hf, SS{});
+      lpv_load<REV, E, K>(a.x_fwd + b * T, t0, T, vh, Xf, E(0));
+    }
     E O[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int64_t t = lpv_time<REV>(t0 + k, T);
-      const SS c = cp ? V::load_vec(cp + t * a.cv.t_stride) : c_fixed;
-      const E dv = dp ? dp[t * a.d.t_stride] : E(0);
-      O[k] = fma(dv, U[r][k], V::dot(c, h));
+      if constexpr (MODE == kSsStates) {
+        Hf[k] = h;
+      } else {
+        const SS c = cp ? V::load_vec(cp + t * a.cv.t_stride) : c_fixed;
+        const E dv = dp ? dp[t * a.d.t_stride] : E(0);
+        O[k] = fma(dv, U[r][k], V::dot(c, h));
+        if constexpr (MODE == kSsGrad) lpv_grad_step<Alg>(a, b, t, t0 + k < T, h, U[r][k], Hf[k], Xf[k], lacc);
+      }
       h = Alg::s_affine(A[r][k], h, X[r][k]);
-      if (a.zf && t0 + k == T - 1) {
+      if (MODE != kSsStates && a.zf && t0 + k == T - 1) {
         union {
           SS s;
           E e[V::M];
@@ -314,7 +399,41 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
         for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = zu.e[i];
       }
     }
-    lpv_store<REV, E, K>(yrow, t0, T, vec, O);
+    if constexpr (MODE == kSsStates)
+      lpv_store<REV, SS, K>(reinterpret_cast<SS *>(a.hs) + b * T, t0, T, vh, Hf);
+    else if (a.y)
+      lpv_store<REV, E, K>(a.y + b * T, t0, T, vec, O);
+  }
+  if constexpr (MODE == kSsGrad) {
+    if (a.gpart) {  // the wave's sums of the operands constant in time
+      auto add = [](const SsGrad<Alg> &p, const SsGrad<Alg> &o) {
+        SsGrad<Alg> r;
+#pragma unroll
+        for (int j = 0; j < SsGrad<Alg>::kN; ++j) r.v[j] = p.v[j] + o.v[j];
+        return r;
+      };
+      SsGrad<Alg> gacc;
+#pragma unroll
+      for (int j = 0; j < SsGrad<Alg>::kN; ++j) gacc.v[j] = up(lacc.v[j]);
+      gacc = wave_scan_incl(gacc, lane, add);
+      if (lane == 63) {
+        auto *dst = a.gpart + ((b * a.tiles_per_row + q) * kWaves + w) * SsGrad<Alg>::kN;
+#pragma unroll
+        for (int j = 0; j < SsGrad<Alg>::kN; ++j) dst[j] = gacc.v[j];
+      }
+    }
+  }
+}
+
+// dst[i] = sum over the rows of src[row, i] (i < n), in row order, for the
+// per-step gradients of an operand the rows share.
+template <typename E>
+__global__ __launch_bounds__(256) void lpv_grad_batch_kernel(const E *src, int64_t rows, int64_t n, E *dst) {
+  using C = typename Wide<E>::type;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256) {
+    C acc = 0;
+    for (int64_t r = 0; r < rows; ++r) acc += up(src[r * n + i]);
+    dst[i] = down<E>(acc);
   }
 }
 

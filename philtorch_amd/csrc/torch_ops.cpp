@@ -741,10 +741,10 @@ std::vector<Tensor> lfilter_ss_backward_hip(const Tensor &b, const Tensor &a, co
 // out_idx selects the output state when C is None; reverse runs the model
 // backwards in time (phs_lpv_ss_rev); transpose_A uses A[t]^T in place of
 // A[t] (the adjoint model, read without a transposed copy).
-std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
-                                      const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
-                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
-                                      bool reverse, bool transpose_A) {
+// lpv_ss's argument checks (shared by its backward); returns M.
+int64_t lpv_ss_meta_check(const Tensor &A, const std::optional<Tensor> &Bm, const std::optional<Tensor> &Cm,
+                          const std::optional<Tensor> &Dm, const std::optional<Tensor> &zi, const Tensor &x,
+                          int64_t out_idx) {
   TORCH_CHECK(x.dim() == 2, "philtorch::lpv_ss: x must be a 2D tensor (batch, time)");
   const int64_t B = x.size(0), T = x.size(1);
   TORCH_CHECK((A.dim() == 3 || A.dim() == 4) && A.size(-1) == A.size(-2) && A.size(-3) == T,
@@ -783,6 +783,19 @@ std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tenso
     same(*zi, "zi");
     TORCH_CHECK(zi->dim() == 2 && zi->size(0) == B && zi->size(1) == M, "philtorch::lpv_ss: zi must be (batch, M)");
   }
+  return M;
+}
+
+// element strides of a (rows, steps, width) lpv_ss operand with broadcast axes
+int64_t lpv_row_stride(const Tensor &t, int64_t width) { return t.size(0) == 1 ? int64_t(0) : t.size(1) * width; }
+int64_t lpv_t_stride(const Tensor &t, int64_t width) { return t.size(1) == 1 ? int64_t(0) : width; }
+
+std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
+                                      const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
+                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
+                                      bool reverse, bool transpose_A) {
+  const int64_t M = lpv_ss_meta_check(A, Bm, Cm, Dm, zi, x, out_idx);
+  const int64_t B = x.size(0), T = x.size(1);
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
   const int dt = phs_dtype_of(x.scalar_type());
   Tensor Ac = A.contiguous(), xc = x.contiguous();
@@ -795,9 +808,7 @@ std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tenso
     if (zi) zf.copy_(zc); else zf.zero_();
     return {y, zf};
   }
-  // element strides of a (rows, steps, width) operand with broadcast axes
-  auto rs = [](const Tensor &t, int64_t width) { return t.size(0) == 1 ? int64_t(0) : t.size(1) * width; };
-  auto ts = [](const Tensor &t, int64_t width) { return t.size(1) == 1 ? int64_t(0) : width; };
+  const auto rs = lpv_row_stride, ts = lpv_t_stride;
   void *stream = stream_of(x);
   const Workspace ws = workspace_for(x, phs_lpv_ss_workspace_size(dt, int(M), B, T), stream);
   const int A_flags = (A.dim() == 3 ? PHS_LPV_A_SHARED : 0) | (transpose_A ? PHS_LPV_A_TRANSPOSED : 0);
@@ -809,6 +820,65 @@ std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tenso
                               y.mutable_data_ptr(), zf.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
                "lpv_ss");
   return {y, zf};
+}
+
+// Gradients of lpv_ss w.r.t. every input (phs_lpv_ss_bwd): returns (grad_A,
+// grad_B, grad_C, grad_D, grad_zi, grad_x), each shaped like its input
+// (summed over the axes the operand broadcasts; an absent operand's an empty
+// tensor; grad_zi (batch, M) whether zi was given or not); grad_zf None is
+// zero.  Replaces the autograd of the composed LPV state space
+// (philtorch/lpv/ssm.py:337-581).
+std::vector<Tensor> lpv_ss_backward_hip(const Tensor &A, const std::optional<Tensor> &Bm,
+                                        const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
+                                        const std::optional<Tensor> &zi, const Tensor &x, const Tensor &gy,
+                                        const std::optional<Tensor> &gzf, int64_t out_idx, bool reverse,
+                                        bool transpose_A) {
+  const int64_t M = lpv_ss_meta_check(A, Bm, Cm, Dm, zi, x, out_idx);
+  const int64_t B = x.size(0), T = x.size(1);
+  TORCH_CHECK(gy.sizes() == x.sizes() && gy.device() == x.device(),
+              "philtorch::lpv_ss_backward: grad_y must have x's shape and device");
+  if (gzf)
+    TORCH_CHECK(gzf->dim() == 2 && gzf->size(0) == B && gzf->size(1) == M && gzf->device() == x.device(),
+                "philtorch::lpv_ss_backward: grad_zf must be (batch, M)");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor Ac = A.contiguous(), xc = x.contiguous(), gc = gy.to(x.scalar_type()).contiguous();
+  Tensor bc = Bm ? Bm->contiguous() : Tensor(), cc = Cm ? Cm->contiguous() : Tensor();
+  Tensor dc = Dm ? Dm->contiguous() : Tensor(), zc = zi ? zi->contiguous() : Tensor();
+  Tensor gzc = gzf ? gzf->to(x.scalar_type()).contiguous() : Tensor();
+  Tensor gA = at::empty(A.sizes(), A.options());
+  Tensor gB = Bm ? at::empty(Bm->sizes(), Bm->options()) : at::empty({0}, x.options());
+  Tensor gC = Cm ? at::empty(Cm->sizes(), Cm->options()) : at::empty({0}, x.options());
+  Tensor gD = Dm ? at::empty(Dm->sizes(), Dm->options()) : at::empty({0}, x.options());
+  Tensor gzi = at::empty({B, M}, x.options());
+  Tensor gx = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  if (B == 0) {
+    gA.zero_(), gB.zero_(), gC.zero_(), gD.zero_();
+    return {gA, gB, gC, gD, gzi, gx};
+  }
+  const auto rs = lpv_row_stride, ts = lpv_t_stride;
+  auto tv_shared = [&](const std::optional<Tensor> &t, const Tensor &c, int64_t w) {
+    return t && rs(c, w) == 0 && ts(c, w) != 0;
+  };
+  const int step_shared = (A.dim() == 3 ? PHS_LPV_GRAD_A : 0) | (tv_shared(Bm, bc, M) ? PHS_LPV_GRAD_B : 0) |
+                          (tv_shared(Cm, cc, M) ? PHS_LPV_GRAD_C : 0) | (tv_shared(Dm, dc, 1) ? PHS_LPV_GRAD_D : 0);
+  void *stream = stream_of(x);
+  Tensor scratch =
+      at::empty({int64_t(phs_lpv_ss_bwd_scratch_size(dt, int(M), B, T, step_shared))}, x.options().dtype(at::kByte));
+  const Workspace ws = workspace_for(x, phs_lpv_ss_workspace_size(dt, int(M), B, T), stream);
+  const int A_flags = (A.dim() == 3 ? PHS_LPV_A_SHARED : 0) | (transpose_A ? PHS_LPV_A_TRANSPOSED : 0);
+  check_status(phs_lpv_ss_bwd(dt, int(M), B, T, Ac.const_data_ptr(), A_flags, Bm ? bc.const_data_ptr() : nullptr,
+                              Bm ? rs(bc, M) : 0, Bm ? ts(bc, M) : 0, Cm ? cc.const_data_ptr() : nullptr,
+                              Cm ? rs(cc, M) : 0, Cm ? ts(cc, M) : 0, int(out_idx),
+                              Dm ? dc.const_data_ptr() : nullptr, Dm ? rs(dc, 1) : 0, Dm ? ts(dc, 1) : 0,
+                              zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(), gc.const_data_ptr(),
+                              gzf ? gzc.const_data_ptr() : nullptr, gx.mutable_data_ptr(), gzi.mutable_data_ptr(),
+                              gA.mutable_data_ptr(), Bm ? gB.mutable_data_ptr() : nullptr,
+                              Cm ? gC.mutable_data_ptr() : nullptr, Dm ? gD.mutable_data_ptr() : nullptr,
+                              reverse ? 1 : 0, scratch.mutable_data_ptr(), size_t(scratch.numel()), ws.ptr, ws.bytes,
+                              stream),
+               "lpv_ss_backward");
+  return {gA, gB, gC, gD, gzi, gx};
 }
 
 // ------------------------------------------------------------ CPU key
@@ -1000,6 +1070,9 @@ TORCH_LIBRARY(philtorch, m) {
   m.def("lpv_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx, bool reverse=False, "
         "bool transpose_A=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
+  m.def("lpv_ss_backward(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, Tensor grad_y, "
+        "Tensor? grad_zf, int out_idx, bool reverse=False, bool transpose_A=False) -> Tensor[]",
+        {at::Tag::pt2_compliant_tag});
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
@@ -1021,6 +1094,7 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("lti_ss_backward", &lti_ss_backward_hip);
   m.impl("lfilter_ss_backward", &lfilter_ss_backward_hip);
   m.impl("lpv_ss", &lpv_ss_hip);
+  m.impl("lpv_ss_backward", &lpv_ss_backward_hip);
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CPU, m) {

@@ -368,9 +368,9 @@ def _lpv_state_space_composite(A, B, C, D, zi, x, out_idx=0):
 
 def _fused_lpv_ss_applies(A: Tensor, x: Tensor, zi: Optional[Tensor], ops, native: bool) -> bool:
     """A model of order <= 4 with one input and one output on a HIP device,
-    the native route requested, no gradient wanted for A, B, C, D and no
-    tangent: philtorch::lpv_ss runs it in one pass (gradients w.r.t. x and
-    zi are one more pass of its adjoint)."""
+    the native route requested and no tangent: philtorch::lpv_ss runs it in
+    one pass; gradients w.r.t. x and zi are one more pass of its adjoint,
+    those of A, B, C, D two fused passes (philtorch::lpv_ss_backward)."""
     from .. import EXTENSION_LOADED
 
     if not (native and EXTENSION_LOADED and x.is_cuda and ops is not None and hasattr(torch.ops.philtorch, "lpv_ss")):
@@ -381,9 +381,6 @@ def _fused_lpv_ss_applies(A: Tensor, x: Tensor, zi: Optional[Tensor], ops, nativ
     if any(t.dtype != x.dtype or t.device != x.device for t in tensors):
         return False
     if A.dim() == 4 and A.size(0) != x.size(0):
-        return False
-    coefs = [A] + [t for t in ops if t is not None]
-    if torch.is_grad_enabled() and any(t.requires_grad for t in coefs):
         return False
     import torch.autograd.forward_ad as fwad
 
@@ -407,9 +404,9 @@ def state_space(
     blocked PyTorch route); ``unroll_factor=1`` on a HIP device runs the
     native scan.  A model of order <= 4 with one input and one output (2D x;
     B, C per row and/or per step or absent / out_idx; D per row and/or per
-    step) with no gradient wanted for A, B, C, D runs philtorch::lpv_ss: B x,
-    the scan, the state shift and C h + D x in one pass, and its adjoint for
-    the gradients w.r.t. x and zi.
+    step) runs philtorch::lpv_ss: B x, the scan, the state shift and
+    C h + D x in one pass; its adjoint gives the gradients w.r.t. x and zi,
+    and philtorch::lpv_ss_backward those of A, B, C, D.
     """
     assert x.dim() in (2, 3), f"Input signal must be 2D or 3D (batch, time, [features]), got {x.shape}"
     assert A.dim() in (3, 4), f"State matrix A must be 3D or 4D, got {A.shape}"
