@@ -15,11 +15,13 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c3      philtorch::recur2 + recurN_backward               (LPV 2x2)
   c3_lpv_ss  lpv.state_space of a time-varying biquad (tdf2, one output), forward only (philtorch::lpv_ss)
   c3_lpv_ss_grad  the same plus gradients w.r.t. x and zi (a reversed lpv_ss pass over the adjoint model)
+  c3_lpv_ss_coef  the same plus gradients w.r.t. A[t], b[t], d[t] too (philtorch::lpv_ss_backward)
   c4      8 x (philtorch::lti_recur2 + lti_recurN_backward) (LTI biquad cascade)
   c4_fused  philtorch::sosfilt + sosfilt_backward              (the same cascade, fused)
   c4_api  8 x lti.lfilter(tdf2, unroll_factor=1) + autograd   (the caller pattern, API level)
   c4_filtfilt  8 x lti.filtfilt(replicate, padlen 9), forward only (philtorch::filtfilt)
   c4_lfilter4  4 x lti.lfilter of order 4 (tdf2), forward only (philtorch::lti_ss)
+  c4_lfilter4_grad  the same plus gradients w.r.t. x, b and a (philtorch::lfilter_ss_backward)
 --composed runs an API config (c3_lpv_ss*, c4_api, c4_filtfilt, c4_lfilter4)
 through the reference's composed route instead of the fused kernels, for the
 comparison.
@@ -559,6 +561,76 @@ class LpvSsGrad(LpvSsApi):
         oracle.lpv_state_space(fl(np.swapaxes(A, -1, -2)), fl(gy), e0, fl(bv), fl(d), None, nthreads=nthreads)
 
 
+class Lfilter4Grad(Lfilter4Api):
+    """c4_lfilter4_grad: c4_lfilter4 with the gradients w.r.t. x and every
+    filter's b and a (torch.autograd.grad against a seeded upstream
+    gradient).  Each lfilter's backward is philtorch::lfilter_ss_backward:
+    the forward again keeping its states, then the adjoint pass with the
+    coefficient sums."""
+
+    def __init__(self):
+        import torch
+
+        super().__init__()
+        self.name = "c4_lfilter4_grad"
+        self.metric = (f"GSamples/s fwd+bwd(x, b, a), lti.lfilter order-4 x{self.S4} (tdf2) B={self.B} T={self.T} "
+                       "fp32 (API)")
+        g = torch.Generator().manual_seed(44)
+        self.gy = torch.randn(self.B, self.T, generator=g).cuda()
+        # per lfilter: states pass (read x, write 4 states) + adjoint (read g, x, 4 states; write grad_x)
+        self.bwd_bytes = (4 + 16) * self.B * self.T + (4 + 4 + 16 + 4) * self.B * self.T
+
+    def step_fwd(self):
+        from philtorch_amd import lti
+
+        x = self.dev[1].detach().requires_grad_(True)
+        coefs = [t.detach().requires_grad_(True) for t in self.b4 + self.a4]
+        y = x
+        for s in range(self.S4):
+            y = lti.lfilter(coefs[s], coefs[self.S4 + s], y, form="tdf2", unroll_factor=1)
+        return y, x, coefs
+
+    def step_bwd(self, out):
+        import torch
+
+        y, x, coefs = out
+        return torch.autograd.grad(y, [x] + coefs, self.gy)
+
+    cpu_step = None  # the oracle restates no coefficient gradients of lfilter
+
+
+class LpvSsCoefGrad(LpvSsGrad):
+    """c3_lpv_ss_coef: c3_lpv_ss_grad with the gradients of the time-varying
+    A[t], b[t] and d[t] too (philtorch::lpv_ss_backward: the forward again
+    keeping its states, then the adjoint pass writing the per-step
+    coefficient gradients)."""
+
+    def __init__(self):
+        super().__init__()
+        B, T = self.B, self.T
+        self.name = "c3_lpv_ss_coef"
+        self.metric = (f"GSamples/s fwd+bwd(x, zi, A, b, d), LPV biquad lpv.state_space (tdf2, one output) B={B} "
+                       f"T={T} fp32 (API)")
+        # states pass: read A (16), x, b (8), write 2 states (8); adjoint: read A, b, d, g, x, states (8),
+        # write grad_x, grad_A (16), grad_b (8), grad_d
+        self.bwd_bytes = (16 + 4 + 8 + 8) * B * T + (16 + 8 + 4 + 4 + 4 + 8 + 4 + 16 + 8 + 4) * B * T
+
+    def step_fwd(self):
+        from philtorch_amd import lpv
+
+        A, x, bv, d, zi = (t.detach().requires_grad_(True) for t in self.dev)
+        y, _ = lpv.state_space(A, x, B=bv, D=d, zi=zi, unroll_factor=1, out_idx=0)
+        return y, (A, x, bv, d, zi)
+
+    def step_bwd(self, out):
+        import torch
+
+        y, leaves = out
+        return torch.autograd.grad(y, leaves, self.gy)
+
+    cpu_step = None  # the oracle restates no coefficient gradients of the LPV state space
+
+
 def make_workload(name):
     if name == "c1":
         return LpvScalar("c1", 64, 65536, "float32")
@@ -584,11 +656,16 @@ def make_workload(name):
         return LpvSsApi()
     if name == "c3_lpv_ss_grad":
         return LpvSsGrad()
+    if name == "c3_lpv_ss_coef":
+        return LpvSsCoefGrad()
+    if name == "c4_lfilter4_grad":
+        return Lfilter4Grad()
     raise ValueError(name)
 
 
-API_CONFIGS = ("c3_lpv_ss", "c3_lpv_ss_grad", "c4_api", "c4_filtfilt", "c4_lfilter4")
-CONFIGS = ("c1", "c2", "c3", "c3_lpv_ss", "c3_lpv_ss_grad", "c4", "c4_fused", "c4_api", "c4_filtfilt", "c4_lfilter4", "c5", "c5_f64")
+API_CONFIGS = ("c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4_api", "c4_filtfilt", "c4_lfilter4",
+               "c4_lfilter4_grad")
+CONFIGS = ("c1", "c2", "c3", "c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4", "c4_lfilter4_grad", "c4_fused", "c4_api", "c4_filtfilt", "c4_lfilter4", "c5", "c5_f64")
 
 
 # ----------------------------------------------------------------------------
@@ -605,9 +682,12 @@ def cpu_model() -> str:
 
 
 def cpu_baseline(w: Workload, budget_s=10.0):
-    """Time the oracle's forward + backward on a bounded sample of rows."""
+    """Time the oracle's forward + backward on a bounded sample of rows
+    (None where the oracle has no restatement of the config's backward)."""
     import statistics
 
+    if w.cpu_step is None:
+        return None
     cores = len(os.sched_getaffinity(0))
     rows = min(w.B, max(cores, 1))  # the reference parallelises over rows only
     # bound one repetition: all sampled rows over a prefix of the time axis
@@ -876,6 +956,8 @@ def main() -> int:
                 "c4_lfilter4": "lti_lfilter_order4_x4_api_fwd_B16_T480000_f32",
                 "c3_lpv_ss": "lpv_biquad_state_space_api_fwd_B32_T1048576_f32",
                 "c3_lpv_ss_grad": "lpv_biquad_state_space_api_fwd_bwd_x_zi_B32_T1048576_f32",
+                "c3_lpv_ss_coef": "lpv_biquad_state_space_api_fwd_bwd_all_B32_T1048576_f32",
+                "c4_lfilter4_grad": "lti_lfilter_order4_x4_api_fwd_bwd_x_b_a_B16_T480000_f32",
                 "c5": "lpv_scan_fwd_bwd_B8_T16777216_f32",
                 "c5_f64": "lpv_scan_fwd_bwd_B8_T16777216_f64",
             }[w.name],

@@ -46,7 +46,7 @@ struct LpvSsArgs {
   LpvOperand<E> bv;      // [., ., M]; p nullptr: the input enters state in_idx
   LpvOperand<E> cv;      // [., ., M]; p nullptr: y is state out_idx
   LpvOperand<E> d;       // [., .]; p nullptr: no feedthrough
-  int out_idx, in_idx;
+  int out_idx, in_idx;  // in_idx: read in kSsGrad only (the other modes take 0)
   const E *zi;  // [B, M]; nullptr: zeros
   const E *x;   // [B, T]
   E *y;         // [B, T]
@@ -162,17 +162,26 @@ __device__ __forceinline__ int64_t lpv_time(int64_t s, int64_t T) {
 }
 
 // b[t] x[t] for the K steps from scan position s0 (b absent: x[t] into
-// state 0).
+// state in_idx, 0 but in the adjoint of a model with its output state
+// selected).
 template <class Alg, bool REV, int K>
 __device__ __forceinline__ void lpv_inputs(const LpvSsArgs<Alg> &a, int64_t b, int64_t s0, const typename Alg::elem (&u)[K],
-                                           typename Alg::s_state (&X)[K]) {
+                                           typename Alg::s_state (&X)[K], int in_idx) {
   using V = SsView<Alg>;
   using E = typename Alg::elem;
-  const E *bp = a.bv.p ? a.bv.p + b * a.bv.row_stride : nullptr;
+  // (one uniform branch for the chunk, no per-step select between a load
+  // and a constant)
+  if (a.bv.p) {
+    const E *bp = a.bv.p + b * a.bv.row_stride;
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int64_t t = lpv_time<REV>(s0 + k, a.T_len);
-    X[k] = V::scale(bp ? V::load_vec(bp + t * a.bv.t_stride) : V::unit(a.in_idx), u[k]);
+    for (int k = 0; k < K; ++k) {
+      const int64_t t = lpv_time<REV>(s0 + k, a.T_len);
+      X[k] = V::scale(V::load_vec(bp + t * a.bv.t_stride), u[k]);
+    }
+  } else {
+    const typename Alg::s_state e = V::unit(in_idx);
+#pragma unroll
+    for (int k = 0; k < K; ++k) X[k] = V::scale(e, u[k]);
   }
 }
 
@@ -228,8 +237,9 @@ __device__ __forceinline__ void lpv_grad_step(const LpvSsArgs<Alg> &a, int64_t b
 // State entering tile position `span` of a row, folded from the inputs (the
 // look-back's bounded-wait fallback; out of line, cold).
 template <class Alg, bool REV>
-__device__ __noinline__ typename Alg::state lpv_prefix_fallback(LpvSsArgs<Alg> a, int64_t b, int64_t span, int lane,
-                                                               typename Alg::state virt) {
+__device__ __noinline__ typename Alg::state lpv_prefix_fallback(const LpvSsArgs<Alg> *ap, int64_t b, int64_t span,
+                                                               int lane, typename Alg::state virt, int in_idx) {
+  const LpvSsArgs<Alg> &a = *ap;
   using E = typename Alg::elem;
   using SC = typename Alg::s_coef;
   using SS = typename Alg::s_state;
@@ -251,7 +261,7 @@ __device__ __noinline__ typename Alg::state lpv_prefix_fallback(LpvSsArgs<Alg> a
 #pragma unroll
       for (int k = 0; k < K; ++k) cs[k] = Alg::s_adjoint(cs[k]);  // real: the transpose
     }
-    lpv_inputs<Alg, REV, K>(a, b, c0, u, xs);
+    lpv_inputs<Alg, REV, K>(a, b, c0, u, xs, in_idx);
     M m = lane_map<Alg, true, false, K>(cs, xs, dummy);
     m = wave_scan_incl(m, lane, op);
     acc = compose<Alg>(acc, read_lane(m, 63));
@@ -308,7 +318,8 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
       if (lane == 0) publish(row_status + q * St::kStride + St::kIncWords, tagg, tag);
       Lookback<Alg> lb = lookback_start<Alg>(q);
       if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
-        yin = lpv_prefix_fallback<Alg, REV>(a, b, q * Sh::kTile, lane, virt);
+        yin = lpv_prefix_fallback<Alg, REV>(kernel_args<LpvSsArgs<Alg>>(), b, q * Sh::kTile, lane, virt,
+                                            MODE == kSsGrad ? a.in_idx : 0);
     }
     if (q + 1 < a.tiles_per_row && lane == 0 && !(a.agg_only && q > 0))
       publish(row_status + q * St::kStride, apply<Alg>(tagg, yin), tag);
@@ -343,7 +354,7 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
   SS X[R][K];  // b[t] x[t], kept for pass 2 (b is read once)
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    lpv_inputs<Alg, REV, K>(a, b, chunk0(r), U[r], X[r]);
+    lpv_inputs<Alg, REV, K>(a, b, chunk0(r), U[r], X[r], MODE == kSsGrad ? a.in_idx : 0);
     M m = lane_map<Alg, true, false, K>(A[r], X[r], dummy);
     m = wave_scan_incl(m, lane, op);
     const M ex = wave_shift_up(m, lane, map_identity<Alg>());
@@ -401,7 +412,7 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
     }
     if constexpr (MODE == kSsStates)
       lpv_store<REV, SS, K>(reinterpret_cast<SS *>(a.hs) + b * T, t0, T, vh, Hf);
-    else if (a.y)
+    else if (MODE == kSsPlain || a.y)
       lpv_store<REV, E, K>(a.y + b * T, t0, T, vec, O);
   }
   if constexpr (MODE == kSsGrad) {

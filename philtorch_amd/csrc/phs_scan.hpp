@@ -419,6 +419,15 @@ __device__ __noinline__ typename Alg::state row_prefix_fallback(const typename A
   return apply<Alg>(acc, virt);
 }
 
+// The running kernel's argument block where it lies in the kernarg segment
+// (a kernel whose one parameter is an Args).  Out-of-line cold paths take it
+// by this pointer: a by-value copy of a large argument struct is spilled to
+// scratch by every wave on entry, on the hot path.
+template <class Args>
+__device__ __forceinline__ const Args *kernel_args() {
+  return (const Args *)__builtin_amdgcn_kernarg_segment_ptr();
+}
+
 // ------------------------------------------------------------ tile look-back
 // The tile's aggregate: the wave aggregates of s_wagg folded in wave order.
 template <class Alg, int kWaves>

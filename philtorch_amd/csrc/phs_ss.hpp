@@ -263,7 +263,9 @@ struct SsModel {
   E d;
 };
 
-template <class Alg>
+// kAdjoint: honour A_trans and in_idx (set only for the adjoint pass of the
+// coefficient gradients; the other modes read A as it lies, input state 0).
+template <class Alg, bool kAdjoint = false>
 __device__ __forceinline__ SsModel<Alg> ss_model(const SsArgs<Alg> &a, int64_t row) {
   using V = SsView<Alg>;
   using E = typename Alg::elem;
@@ -271,8 +273,8 @@ __device__ __forceinline__ SsModel<Alg> ss_model(const SsArgs<Alg> &a, int64_t r
   SsModel<Alg> m;
   if (a.filt_form == 0) {
     m.A = V::load_mat(a.A + row * a.A_stride);
-    if (a.A_trans) m.A = Alg::s_adjoint(m.A);  // real: the transpose
-    m.b = a.bv ? V::load_vec(a.bv + row * a.b_stride) : V::unit(a.in_idx);
+    if (kAdjoint && a.A_trans) m.A = Alg::s_adjoint(m.A);  // real: the transpose
+    m.b = a.bv ? V::load_vec(a.bv + row * a.b_stride) : V::unit(kAdjoint ? a.in_idx : 0);
     m.c = a.cv ? V::load_vec(a.cv + row * a.c_stride) : V::unit(a.out_idx);
     m.d = a.d ? a.d[row * a.d_stride] : E(0);
     return m;
@@ -519,12 +521,14 @@ __device__ __forceinline__ void ss_lane_scan(typename Alg::state (&v)[N], int la
 // inputs (the look-back's bounded-wait fallback; out of line, cold): chunk
 // by chunk of 64 K steps, st <- A^(64 K) st + chunk total, from the row's
 // entry state st (derived here for a zero-phase pass).
-template <class Alg, class Sh, bool REV>
-__device__ __noinline__ typename Alg::state ss_prefix_fallback(SsArgs<Alg> a, int64_t b, int64_t span, int lane,
-                                                              typename Alg::state st, const SsPowers<Alg> *tab) {
+template <class Alg, class Sh, bool REV, bool kAdjoint>
+__device__ __noinline__ typename Alg::state ss_prefix_fallback(const SsArgs<Alg> *ap, int64_t b, int64_t span,
+                                                              int lane, typename Alg::state st,
+                                                              const SsPowers<Alg> *tab) {
+  const SsArgs<Alg> &a = *ap;
   using E = typename Alg::elem;
   constexpr int K = Sh::K;
-  const SsModel<Alg> m = ss_model<Alg>(a, b);
+  const SsModel<Alg> m = ss_model<Alg, kAdjoint>(a, b);
   const E *xrow = a.x + b * a.T_len;
   if (a.virt_mode != 0) st = ss_filtfilt_entry<Alg>(a, b, lane);
   for (int64_t off = 0; off < span; off += 64 * K) {
@@ -705,7 +709,7 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
   if (w == kWaves) {
     // ================= look-back wave: power tables, then the look-back
     {
-      typename Alg::coef P = ss_pow2<Alg>(ss_model<Alg>(a, b).A, __builtin_ctz(K));
+      typename Alg::coef P = ss_pow2<Alg>(ss_model<Alg, MODE == kSsGrad>(a, b).A, __builtin_ctz(K));
 #pragma unroll
       for (int i = 0; i < 6; ++i) {
         if (lane == 0) s_tab.pw[i] = P;
@@ -746,7 +750,8 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
     if (q > 0) {
       if (lane == 0) publish(row_status + q * St::kStride + St::kVecWords, tagg, tag);
       if (!ss_lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, &s_tab, q, yin))
-        yin = ss_prefix_fallback<Alg, Sh, REV>(a, b, q * Sh::kTile, lane, virt, &s_tab);
+        yin = ss_prefix_fallback<Alg, Sh, REV, MODE == kSsGrad>(kernel_args<SsArgs<Alg>>(), b, q * Sh::kTile, lane,
+                                                                virt, &s_tab);
     }
     if (q + 1 < a.tiles_per_row && lane == 0 && !(a.agg_only && q > 0))
       publish(row_status + q * St::kStride, Alg::affine(s_tab.gp[0], yin, tagg), tag);
@@ -756,7 +761,7 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
   }
 
   // ================= data waves
-  const SsModel<Alg> m = ss_model<Alg>(a, b);
+  const SsModel<Alg> m = ss_model<Alg, MODE == kSsGrad>(a, b);
   const bool vec = a.vec_ok != 0;
   const E *xrow = a.x + b * T;
   const int64_t seg0 = q * Sh::kTile + int64_t(w) * Sh::kWaveSeg;
@@ -807,7 +812,7 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
 #pragma unroll
   for (int r = 1; r < R; ++r) ent[r] = Alg::affine(s_tab.pw[6], ent[r - 1], tot[r - 1]);
   ss_pow_apply<Alg, 6, R>(s_tab.pw, sl, ent);
-  constexpr int G = ss_state_group<Alg>();
+  constexpr int G = MODE == kSsPlain ? K : ss_state_group<Alg>();
   const bool vh = a.vec_hs != 0;
   SsGrad<Alg, E> lacc;
   if constexpr (MODE == kSsGrad) {
@@ -849,7 +854,7 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
       if constexpr (MODE == kSsStates)
         ss_store<REV, SS, G>(reinterpret_cast<SS *>(a.hs) + b * T, t0s[r] + g0, T, vh, Hg);
     }
-    if (MODE != kSsStates && a.y) ss_store<REV, E, K>(a.y + b * T, t0s[r], T, vec, O);
+    if (MODE == kSsPlain || (MODE == kSsGrad && a.y)) ss_store<REV, E, K>(a.y + b * T, t0s[r], T, vec, O);
   }
   if constexpr (MODE == kSsGrad) {
     // the wave's sums, in a fixed order, one partial per (row, tile, wave)
@@ -890,28 +895,37 @@ struct SsGradOut {
 
 constexpr int kSsReduceThreads = 256;
 
-// Row b's sums over its per-wave partials (fixed order): rowsum[b, j].
+// Row b's sums over its per-wave partials (fixed order): rowsum[b, j].  Each
+// thread sums a strided share of the partials for every component, then one
+// tree over the block.
 template <class Alg>
 __global__ __launch_bounds__(kSsReduceThreads) void ss_grad_rows_kernel(
     const typename Wide<typename Alg::elem>::type *gpart, int64_t per_row,
     typename Wide<typename Alg::elem>::type *rowsum) {
   using C = typename Wide<typename Alg::elem>::type;
   constexpr int N = SsGrad<Alg>::kN;
-  __shared__ C s[kSsReduceThreads];
+  __shared__ C s[N][kSsReduceThreads];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
-  for (int j = 0; j < N; ++j) {
-    C acc = 0;
-    for (int64_t i = tid; i < per_row; i += kSsReduceThreads) acc += gpart[(b * per_row + i) * N + j];
-    s[tid] = acc;
-    __syncthreads();
-    for (int h = kSsReduceThreads / 2; h > 0; h >>= 1) {
-      if (tid < h) s[tid] += s[tid + h];
-      __syncthreads();
+  C acc[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) acc[j] = 0;
+  for (int64_t i = tid; i < per_row; i += kSsReduceThreads) {
+    const C *p = gpart + (b * per_row + i) * N;
+#pragma unroll
+    for (int j = 0; j < N; ++j) acc[j] += p[j];
+  }
+#pragma unroll
+  for (int j = 0; j < N; ++j) s[j][tid] = acc[j];
+  __syncthreads();
+  for (int h = kSsReduceThreads / 2; h > 0; h >>= 1) {
+    if (tid < h) {
+#pragma unroll
+      for (int j = 0; j < N; ++j) s[j][tid] += s[j][tid + h];
     }
-    if (tid == 0) rowsum[b * N + j] = s[0];
     __syncthreads();
   }
+  if (tid < N) rowsum[b * N + tid] = s[tid][0];
 }
 
 // dL/dfb, dL/dfa of one filter from its model's sums G (chain rule through
