@@ -256,6 +256,24 @@ int phs_sosfilt_bwd(int dtype, int64_t B, int64_t T, int S, const void *sos, int
                     const void *ckpt, const void *grad_y, const void *grad_zf, void *grad_x, void *grad_sos,
                     void *grad_zi, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- One biquad given as lfilter's b and a where they lie (the cascade
+ * kernel at S = 1 without an sos array; lfilter(b, a, x, form="tdf2"),
+ * philtorch/lti/filtering.py:211-333, for a second-order filter): b [B, nb]
+ * (nb = 1..3, missing taps zero) and a [B, 2] (after the leading 1), each
+ * row at its own stride in elements (0 = one filter for all rows, inner
+ * stride 1); zi, zf [B, 2]; ckpt as phs_sosfilt_fwd's at S = 1; workspace
+ * phs_sosfilt_workspace_size at S = 1.  The backward writes grad_b [B|1, nb]
+ * and grad_a [B|1, 2] (one row when both strides are 0; both NULL for no
+ * coefficient gradient, then x and ckpt may be NULL). */
+int phs_biquad_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_t b_row_stride, const void *a,
+                   int64_t a_row_stride, const void *zi, const void *x, void *y, void *zf, void *ckpt,
+                   void *workspace, size_t workspace_bytes, void *stream);
+
+int phs_biquad_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_t b_row_stride, const void *a,
+                   int64_t a_row_stride, const void *x, const void *ckpt, const void *grad_y, const void *grad_zf,
+                   void *grad_x, void *grad_b, void *grad_a, void *grad_zi, void *workspace, size_t workspace_bytes,
+                   void *stream);
+
 /* ---- Zero-phase filtering with a filter of order 1..4 per row (forward
  * only).  Replaces philtorch.lti.filtering.filtfilt (philtorch/lti/
  * filtering.py:413-484, with lfilter_zi :107-142) for a filter b / a:

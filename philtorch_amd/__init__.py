@@ -291,6 +291,7 @@ if EXTENSION_LOADED and _has_op("sosfilt"):
         sos, zi, x = inputs
         ctx.save_for_backward(sos, x, output[2], zi)
         ctx.has_zi = zi is not None
+        ctx.set_materialize_grads(False)  # no zero gradients for the checkpoints or an unused zf
 
     def _sosfilt_composite(sos, zi, x, gy, gzf, needs):
         """Gradient through the per-section lfilter(tdf2) chain on the native
@@ -326,6 +327,56 @@ if EXTENSION_LOADED and _has_op("sosfilt"):
 
     torch.library.register_autograd("philtorch::sosfilt", _sosfilt_backward, setup_context=_sosfilt_setup)
 
+if EXTENSION_LOADED and _has_op("biquad"):
+    # one biquad from lfilter's b and a on the cascade kernel: (y, zf, ckpt)
+    @torch.library.register_fake("philtorch::biquad")
+    def _(b, a, zi, x):
+        torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
+        torch._check(b.ndim == a.ndim and b.ndim in (1, 2), lambda: "b and a must both be 1D or both 2D")
+        torch._check(1 <= b.shape[-1] <= 3 and a.shape[-1] == 2, lambda: "a biquad")
+        B, T = x.shape
+        return _fake_like(x), x.new_empty((B, 2)), x.new_empty((B, 1, (T + 511) // 512, 2), dtype=torch.float64)
+
+    @torch.library.register_fake("philtorch::biquad_backward")
+    def _(b, a, x, ckpt, grad_y, grad_zf, need_coef):
+        return [_fake_like(x), b.new_empty(b.shape), a.new_empty(a.shape), x.new_empty((x.shape[0], 2))]
+
+    def _biquad_setup(ctx, inputs, output):
+        b, a, zi, x = inputs
+        ctx.save_for_backward(b, a, x, output[2], zi)
+        ctx.has_zi = zi is not None
+        # the checkpoints and an unused final state need no zero gradients
+        ctx.set_materialize_grads(False)
+
+    def _biquad_backward(ctx, gy, gzf, _gckpt):
+        """philtorch::biquad_backward: the cascade kernel's adjoint pass at
+        one section, with the coefficient sums where b or a needs a
+        gradient.  Under create_graph: the gradient of the section as
+        philtorch's lfilter composes it (a differentiable composite)."""
+        b, a, x, ckpt, zi = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        if gy is None:
+            gy = torch.zeros_like(x)
+        if torch.is_grad_enabled():
+            sos = torch.cat([torch.nn.functional.pad(b, (0, 3 - b.size(-1))), torch.ones_like(a[..., :1]), a],
+                            dim=-1).unsqueeze(-2)
+            zs = None if zi is None else zi.unsqueeze(1)
+            res = _sosfilt_composite(sos, zs, x, gy, None if gzf is None else gzf.unsqueeze(1),
+                                     (needs[0] or needs[1], needs[2], needs[3]))
+            gsos, gz, gx = res
+            gb = ga = None
+            if gsos is not None:
+                gb = gsos[..., 0, : b.size(-1)]
+                ga = gsos[..., 0, 4:6]
+            return (gb if needs[0] else None, ga if needs[1] else None,
+                    gz[:, 0] if (gz is not None and ctx.has_zi and needs[2]) else None, gx if needs[3] else None)
+        need_coef = bool(needs[0] or needs[1])
+        gx, gb, ga, gzi = torch.ops.philtorch.biquad_backward(b, a, x, ckpt, gy, gzf, need_coef)
+        return (gb if needs[0] else None, ga if needs[1] else None, gzi if ctx.has_zi and needs[2] else None,
+                gx if needs[3] else None)
+
+    torch.library.register_autograd("philtorch::biquad", _biquad_backward, setup_context=_biquad_setup)
+
 if EXTENSION_LOADED and _has_op("filtfilt"):
     # zero-phase biquad filter, forward only (lti.filtfilt takes it when no
     # gradient is needed)
@@ -357,6 +408,7 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
         ctx.out_idx = out_idx
         ctx.reverse = bool(inputs[7]) if len(inputs) > 7 else False
         ctx.save_for_backward(A, B, C, D, zi, x)
+        ctx.set_materialize_grads(False)
 
     def _lti_ss_backward(ctx, gy, gzf):
         """With A, B, C, D constant: the adjoint model (A^T, input vector C,
@@ -431,6 +483,7 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
         ctx.form = form
         ctx.reverse = bool(inputs[5]) if len(inputs) > 5 else False
         ctx.save_for_backward(b, a, zi, x)
+        ctx.set_materialize_grads(False)
 
     def _lfilter_ss_backward(ctx, gy, gzf):
         """With b and a constant: the adjoint of a companion-form filter is
@@ -498,6 +551,7 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         ctx.reverse = bool(inputs[7]) if len(inputs) > 7 else False
         ctx.transpose_A = bool(inputs[8]) if len(inputs) > 8 else False
         ctx.save_for_backward(A, B, C, D, zi, x)
+        ctx.set_materialize_grads(False)
 
     def _lpv_ss_backward(ctx, gy, gzf):
         """With A, B, C, D constant: the adjoint model (A[t]^T, input vector

@@ -58,11 +58,28 @@ size_t ws_bytes_for(int64_t B, int64_t T, int S, bool backward) {
 
 bool sizes_ok(int64_t B, int64_t T, int S) { return B >= 0 && T >= 0 && S >= 1 && S <= kSosMaxSections; }
 
+// Where the coefficients lie: a [rows, S, 6] sos array (shared: one row
+// for all), or one biquad as lfilter's b [rows, nb] and a [rows, 2] at their
+// own row strides (0 = shared).
+struct SosCoefs {
+  const void *sos = nullptr;
+  bool shared = false;
+  const void *b = nullptr, *a = nullptr;
+  int64_t b_row_stride = 0, a_row_stride = 0;
+  int nb = 0;
+  bool coef_shared() const { return b ? (b_row_stride == 0 && a_row_stride == 0) : shared; }
+  bool ok() const { return b ? (a && nb >= 1 && nb <= 3 && b_row_stride >= 0 && a_row_stride >= 0) : sos != nullptr; }
+};
+
 template <typename E, class Sh>
-void fill_common(SosArgs<E> &a, const SosLayout &L, int64_t B, int64_t T, int S, const void *sos, bool shared,
-                 char *ws) {
-  a.sos = static_cast<const E *>(sos);
-  a.sos_row_stride = shared ? 0 : int64_t(S) * 6;
+void fill_common(SosArgs<E> &a, const SosLayout &L, int64_t B, int64_t T, int S, const SosCoefs &k, char *ws) {
+  a.sos = static_cast<const E *>(k.sos);
+  a.sos_row_stride = k.shared ? 0 : int64_t(S) * 6;
+  a.fb = static_cast<const E *>(k.b);
+  a.fa = static_cast<const E *>(k.a);
+  a.fb_row_stride = k.b_row_stride;
+  a.fa_row_stride = k.a_row_stride;
+  a.nb = k.nb;
   a.B = B;
   a.T_len = T;
   a.tiles_per_row = L.tiles_per_row;
@@ -78,17 +95,17 @@ void fill_common(SosArgs<E> &a, const SosLayout &L, int64_t B, int64_t T, int S,
 }
 
 template <typename E>
-int sos_fwd(int64_t B, int64_t T, int S, const void *sos, bool shared, const void *zi, const void *x, void *y,
-            void *zf, void *ckpt, void *workspace, size_t ws_bytes, hipStream_t stream) {
+int sos_fwd(int64_t B, int64_t T, int S, const SosCoefs &k, const void *zi, const void *x, void *y, void *zf,
+            void *ckpt, void *workspace, size_t ws_bytes, hipStream_t stream) {
   using Sh = SosFwd<E>;
-  if (!sizes_ok(B, T, S)) return PHS_ERR_INVALID;
+  if (!sizes_ok(B, T, S) || (k.b && S != 1)) return PHS_ERR_INVALID;
   if (B == 0 || T == 0) return PHS_OK;
-  if (!sos || !x || !y) return PHS_ERR_INVALID;
+  if (!k.ok() || !x || !y) return PHS_ERR_INVALID;
   const SosLayout L = sos_layout<E, Sh>(B, T, S, false);
   if (double(B) * double(L.tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
   if (!workspace || ws_bytes < L.total) return PHS_ERR_WORKSPACE;
   SosArgs<E> a{};
-  fill_common<E, Sh>(a, L, B, T, S, sos, shared, static_cast<char *>(workspace));
+  fill_common<E, Sh>(a, L, B, T, S, k, static_cast<char *>(workspace));
   a.in = static_cast<const E *>(x);
   a.out = static_cast<E *>(y);
   a.virt = static_cast<const E *>(zi);
@@ -100,21 +117,24 @@ int sos_fwd(int64_t B, int64_t T, int S, const void *sos, bool shared, const voi
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
+// gsos (sos layout) or gb, ga (biquad layout): the coefficient gradients,
+// null for none.
 template <typename E>
-int sos_bwd(int64_t B, int64_t T, int S, const void *sos, bool shared, const void *x, const void *ckpt,
-            const void *gy, const void *gzf, void *gx, void *gsos, void *gzi, void *workspace, size_t ws_bytes,
+int sos_bwd(int64_t B, int64_t T, int S, const SosCoefs &k, const void *x, const void *ckpt, const void *gy,
+            const void *gzf, void *gx, void *gsos, void *gb, void *ga, void *gzi, void *workspace, size_t ws_bytes,
             hipStream_t stream) {
   using Sh = SosBwd<E>;
-  if (!sizes_ok(B, T, S)) return PHS_ERR_INVALID;
+  if (!sizes_ok(B, T, S) || (k.b && S != 1)) return PHS_ERR_INVALID;
   if (B == 0 || T == 0) return PHS_OK;
-  const bool grad = gsos != nullptr;
-  if (!sos || !gy || (grad && (!x || !ckpt))) return PHS_ERR_INVALID;
+  if (k.b ? (gsos != nullptr || (gb == nullptr) != (ga == nullptr)) : (gb || ga)) return PHS_ERR_INVALID;
+  const bool grad = k.b ? gb != nullptr : gsos != nullptr;
+  if (!k.ok() || !gy || (grad && (!x || !ckpt))) return PHS_ERR_INVALID;
   const SosLayout L = sos_layout<E, Sh>(B, T, S, grad);
   if (double(B) * double(L.tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
   if (!workspace || ws_bytes < L.total) return PHS_ERR_WORKSPACE;
   char *ws = static_cast<char *>(workspace);
   SosArgs<E> a{};
-  fill_common<E, Sh>(a, L, B, T, S, sos, shared, ws);
+  fill_common<E, Sh>(a, L, B, T, S, k, ws);
   a.in = static_cast<const E *>(gy);
   a.out = static_cast<E *>(gx);
   a.virt = static_cast<const E *>(gzf);
@@ -128,9 +148,9 @@ int sos_bwd(int64_t B, int64_t T, int S, const void *sos, bool shared, const voi
     const size_t lds = size_t(S) * Sh::kWaves * Sh::R * 64 * sizeof(Vec2<E>);
     launch_kernel((sos_kernel<E, Sh, true, true>), dim3(grid), dim3(Sh::kThreads), lds, stream, a);
     if (hipGetLastError() != hipSuccess) return PHS_ERR_LAUNCH;
-    const int64_t rows = shared ? 1 : B;
+    const int64_t rows = k.coef_shared() ? 1 : B;
     hipLaunchKernelGGL((sos_grad_reduce_kernel<E, Sh>), dim3(unsigned(rows * S)), dim3(kSosReduceThreads), 0,
-                       stream, a, static_cast<E *>(gsos), rows);
+                       stream, a, static_cast<E *>(gsos), rows, static_cast<E *>(gb), static_cast<E *>(ga));
   } else {
     launch_kernel((sos_kernel<E, Sh, true, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
   }
@@ -160,11 +180,12 @@ int phs_sosfilt_fwd(int dtype, int64_t B, int64_t T, int S, const void *sos, int
                     const void *x, void *y, void *zf, void *ckpt, void *workspace, size_t workspace_bytes,
                     void *stream) {
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  phs::SosCoefs k;
+  k.sos = sos;
+  k.shared = sos_shared != 0;
   switch (dtype) {
-    case PHS_F32:
-      return phs::sos_fwd<float>(B, T, S, sos, sos_shared != 0, zi, x, y, zf, ckpt, workspace, workspace_bytes, st);
-    case PHS_F64:
-      return phs::sos_fwd<double>(B, T, S, sos, sos_shared != 0, zi, x, y, zf, ckpt, workspace, workspace_bytes, st);
+    case PHS_F32: return phs::sos_fwd<float>(B, T, S, k, zi, x, y, zf, ckpt, workspace, workspace_bytes, st);
+    case PHS_F64: return phs::sos_fwd<double>(B, T, S, k, zi, x, y, zf, ckpt, workspace, workspace_bytes, st);
     default: return PHS_ERR_DTYPE;
   }
 }
@@ -173,13 +194,57 @@ int phs_sosfilt_bwd(int dtype, int64_t B, int64_t T, int S, const void *sos, int
                     const void *ckpt, const void *grad_y, const void *grad_zf, void *grad_x, void *grad_sos,
                     void *grad_zi, void *workspace, size_t workspace_bytes, void *stream) {
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  phs::SosCoefs k;
+  k.sos = sos;
+  k.shared = sos_shared != 0;
   switch (dtype) {
     case PHS_F32:
-      return phs::sos_bwd<float>(B, T, S, sos, sos_shared != 0, x, ckpt, grad_y, grad_zf, grad_x, grad_sos,
-                                 grad_zi, workspace, workspace_bytes, st);
+      return phs::sos_bwd<float>(B, T, S, k, x, ckpt, grad_y, grad_zf, grad_x, grad_sos, nullptr, nullptr, grad_zi,
+                                 workspace, workspace_bytes, st);
     case PHS_F64:
-      return phs::sos_bwd<double>(B, T, S, sos, sos_shared != 0, x, ckpt, grad_y, grad_zf, grad_x, grad_sos,
-                                  grad_zi, workspace, workspace_bytes, st);
+      return phs::sos_bwd<double>(B, T, S, k, x, ckpt, grad_y, grad_zf, grad_x, grad_sos, nullptr, nullptr, grad_zi,
+                                  workspace, workspace_bytes, st);
+    default: return PHS_ERR_DTYPE;
+  }
+}
+
+namespace {
+phs::SosCoefs biquad_coefs(const void *b, int nb, int64_t b_row_stride, const void *a, int64_t a_row_stride) {
+  phs::SosCoefs k;
+  k.b = b;
+  k.a = a;
+  k.nb = nb;
+  k.b_row_stride = b_row_stride;
+  k.a_row_stride = a_row_stride;
+  return k;
+}
+}  // namespace
+
+int phs_biquad_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_t b_row_stride, const void *a,
+                   int64_t a_row_stride, const void *zi, const void *x, void *y, void *zf, void *ckpt,
+                   void *workspace, size_t workspace_bytes, void *stream) {
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const phs::SosCoefs k = biquad_coefs(b, nb, b_row_stride, a, a_row_stride);
+  switch (dtype) {
+    case PHS_F32: return phs::sos_fwd<float>(B, T, 1, k, zi, x, y, zf, ckpt, workspace, workspace_bytes, st);
+    case PHS_F64: return phs::sos_fwd<double>(B, T, 1, k, zi, x, y, zf, ckpt, workspace, workspace_bytes, st);
+    default: return PHS_ERR_DTYPE;
+  }
+}
+
+int phs_biquad_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_t b_row_stride, const void *a,
+                   int64_t a_row_stride, const void *x, const void *ckpt, const void *grad_y, const void *grad_zf,
+                   void *grad_x, void *grad_b, void *grad_a, void *grad_zi, void *workspace, size_t workspace_bytes,
+                   void *stream) {
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const phs::SosCoefs k = biquad_coefs(b, nb, b_row_stride, a, a_row_stride);
+  switch (dtype) {
+    case PHS_F32:
+      return phs::sos_bwd<float>(B, T, 1, k, x, ckpt, grad_y, grad_zf, grad_x, nullptr, grad_b, grad_a, grad_zi,
+                                 workspace, workspace_bytes, st);
+    case PHS_F64:
+      return phs::sos_bwd<double>(B, T, 1, k, x, ckpt, grad_y, grad_zf, grad_x, nullptr, grad_b, grad_a, grad_zi,
+                                  workspace, workspace_bytes, st);
     default: return PHS_ERR_DTYPE;
   }
 }

@@ -63,6 +63,12 @@ struct SosArgs {
   using C = typename Wide<E>::type;
   const E *sos;            // [rows, S, 6]: b0 b1 b2 a0 a1 a2 (a0 = 1)
   int64_t sos_row_stride;  // elements between rows (0 = one set for all rows)
+  // one biquad given as lfilter's b and a where they lie (S = 1; sos unused):
+  // b [rows, nb] (nb <= 3, missing taps zero), a [rows, 2] (after the
+  // leading 1), each row at its own stride (0 = shared)
+  const E *fb, *fa;
+  int64_t fb_row_stride, fa_row_stride;
+  int nb;
   const E *in;             // forward: x;  backward: grad of y
   E *out;                  // forward: y;  backward: grad of x (nullable)
   const E *virt;           // forward: zi;  backward: grad of zf  ([B, S, 2], nullable = zeros)
@@ -88,11 +94,26 @@ struct SosSec {
   E b0, c0, c1, na1, na2;  // c = b[1:] - b0 a;  na = -a
 };
 
+// Coefficients (b0, b1, b2, a1, a2) of section s of row r.
 template <typename E>
-__device__ __forceinline__ SosSec<E> load_sec(const E *row, int s) {
-  const E *p = row + 6 * s;
-  const E b0 = p[0], b1 = p[1], b2 = p[2], a1 = p[4], a2 = p[5];
-  return {b0, b1 - b0 * a1, b2 - b0 * a2, -a1, -a2};
+struct SosCoef {
+  E b0, b1, b2, a1, a2;
+};
+
+template <typename E>
+__device__ __forceinline__ SosCoef<E> sec_coef(const SosArgs<E> &a, int64_t r, int s) {
+  if (a.fb) {
+    const E *pb = a.fb + r * a.fb_row_stride, *pa = a.fa + r * a.fa_row_stride;
+    return {pb[0], a.nb > 1 ? pb[1] : E(0), a.nb > 2 ? pb[2] : E(0), pa[0], pa[1]};
+  }
+  const E *p = a.sos + r * a.sos_row_stride + 6 * s;
+  return {p[0], p[1], p[2], p[4], p[5]};
+}
+
+template <typename E>
+__device__ __forceinline__ SosSec<E> load_sec(const SosArgs<E> &a, int64_t r, int s) {
+  const SosCoef<E> k = sec_coef(a, r, s);
+  return {k.b0, k.b1 - k.b0 * k.a1, k.b2 - k.b0 * k.a2, -k.a1, -k.a2};
 }
 
 // Section matrix A in compute precision.
@@ -624,7 +645,6 @@ __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const S
   const int64_t T = a.T_len;
   const int64_t row_end = a.tiles_per_row * Sh::kTile;
   const int n = REV ? S - s_target : s_target + 1;  // sections in processing order
-  const E *sosrow = a.sos + b * a.sos_row_stride;
   const E *inrow = a.in + b * T;
   const bool row_virt = !REV || (T % Sh::kTile) == 0;
   wave_sync();
@@ -644,7 +664,7 @@ __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const S
     load_chunk<E, K>(inrow, t0, T, a.vec_ok != 0, u[0], zero);
     for (int i = 0; i < n; ++i) {
       const int s = REV ? S - 1 - i : i;
-      const SosSec<E> q = load_sec(sosrow, s);
+      const SosSec<E> q = load_sec(a, b, s);
       wave_sync();
       build_powers<E, K, Sh::R>(tab, q, lane);
       wave_sync();
@@ -723,7 +743,6 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
   const int64_t T = a.T_len;
   const int S = a.S;
   const bool vec = a.vec_ok != 0;
-  const E *sosrow = a.sos + b * a.sos_row_stride;
   // the row's state before its first step in scan order; backward it is
   // dL/dzf only when no padded step t = T carries it
   const bool row_virt = !REV || (T % Sh::kTile) == 0;
@@ -733,14 +752,14 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
 
   if (w == W) {
     // ================= look-back wave
-    build_powers<E, K, R>(&s_pow[0], load_sec(sosrow, vis_sec(0)), lane);
-    if (nvis > 1) build_powers<E, K, R>(&s_pow[1], load_sec(sosrow, vis_sec(1)), lane);
+    build_powers<E, K, R>(&s_pow[0], load_sec(a, b, vis_sec(0)), lane);
+    if (nvis > 1) build_powers<E, K, R>(&s_pow[1], load_sec(a, b, vis_sec(1)), lane);
     __syncthreads();  // powers of the first two visits
     int v = 0;
     if constexpr (GRAD) {
       for (; v < S; ++v) {
         __syncthreads();  // forward recompute: wave aggregates of visit v
-        if (v + 2 < nvis) build_powers<E, K, R>(&s_pow[(v + 2) % 3], load_sec(sosrow, vis_sec(v + 2)), lane);
+        if (v + 2 < nvis) build_powers<E, K, R>(&s_pow[(v + 2) % 3], load_sec(a, b, vis_sec(v + 2)), lane);
       }
     }
     for (; v < nvis; ++v) {
@@ -777,7 +796,7 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
         publish(row_status + qs * kSosStatusWords, Alg::affine(Mp[W], yin, pv), tag);
       if (lane == 0) s_in = yin;
       __syncthreads();  // entry state is in s_in
-      if (v + 2 < nvis) build_powers<E, K, R>(&s_pow[(v + 2) % 3], load_sec(sosrow, vis_sec(v + 2)), lane);
+      if (v + 2 < nvis) build_powers<E, K, R>(&s_pow[(v + 2) % 3], load_sec(a, b, vis_sec(v + 2)), lane);
     }
     return;
   }
@@ -818,7 +837,7 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
     const int64_t ck0 = (qf * Sh::kTile) / kSosCkpt;
     for (; v < S; ++v) {
       const int s = v;
-      const SosSec<E> q = load_sec(sosrow, s);
+      const SosSec<E> q = load_sec(a, b, s);
       const SecPowers<C> &t = s_pow[v % 3];
       V ex[R], tot[R], x[R];
       fold_fwd_n<E, K, R>(q, F, x);
@@ -849,7 +868,7 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
 
   for (; v < nvis; ++v) {
     const int s = vis_sec(v);
-    const SosSec<E> q = load_sec(sosrow, s);
+    const SosSec<E> q = load_sec(a, b, s);
     const SecPowers<C> &t = s_pow[v % 3];
     const SV gzf = load_pair(a.virt + (b * S + s) * 2, REV && a.virt != nullptr);
 
@@ -862,7 +881,7 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
 #pragma unroll
         for (int k = 0; k < K; ++k) Uf[r][k] = X[r][k];
       for (int j = 0; j < s; ++j) {
-        const SosSec<E> qj = load_sec(sosrow, j);
+        const SosSec<E> qj = load_sec(a, b, j);
         SV hj[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) hj[r] = s_laneh[((j * W + w) * R + r) * 64 + lane];
@@ -954,11 +973,13 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
 // order and applies the chain rule to (b0, b1, b2, a0, a1, a2):
 //   d c0/d b1 = 1, d c0/d b0 = -a1, d c0/d a1 = -b0, d A00/d a1 = -1 (same
 //   pattern for c1, a2), d y/d b0 = u; a0 is not a free parameter (zero).
+// gsos: [coef_rows, S, 6]; for a biquad given as b and a (a.fb), gb
+// [coef_rows, nb] and ga [coef_rows, 2] instead (gsos unused).
 constexpr int kSosReduceThreads = 256;
 
 template <typename E, class Sh>
 __global__ __launch_bounds__(kSosReduceThreads) void sos_grad_reduce_kernel(const SosArgs<E> a, E *gsos,
-                                                                         int64_t coef_rows) {
+                                                                         int64_t coef_rows, E *gb, E *ga) {
   using C = typename Wide<E>::type;
   __shared__ C s_sum[5][kSosReduceThreads];
   const int64_t row = blockIdx.x / a.S;
@@ -982,16 +1003,19 @@ __global__ __launch_bounds__(kSosReduceThreads) void sos_grad_reduce_kernel(cons
     __syncthreads();
   }
   if (threadIdx.x == 0) {
-    const E *p = a.sos + row * a.sos_row_stride + 6 * s;
-    const C b0 = up(p[0]), a1 = up(p[4]), a2 = up(p[5]);
+    const SosCoef<E> k = sec_coef(a, row, s);
+    const C b0 = up(k.b0), a1 = up(k.a1), a2 = up(k.a2);
     const C Sa1 = s_sum[0][0], Sa2 = s_sum[1][0], Sc0 = s_sum[2][0], Sc1 = s_sum[3][0], Sb0 = s_sum[4][0];
-    E *g = gsos + row * int64_t(a.S) * 6 + 6 * s;
-    g[0] = down<E>(Sb0 - a1 * Sc0 - a2 * Sc1);
-    g[1] = down<E>(Sc0);
-    g[2] = down<E>(Sc1);
-    g[3] = E(0);
-    g[4] = down<E>(-Sa1 - b0 * Sc0);
-    g[5] = down<E>(-Sa2 - b0 * Sc1);
+    const C g[6] = {Sb0 - a1 * Sc0 - a2 * Sc1, Sc0, Sc1, C(0), -Sa1 - b0 * Sc0, -Sa2 - b0 * Sc1};
+    if (a.fb) {
+      for (int j = 0; j < a.nb; ++j) gb[row * a.nb + j] = down<E>(g[j]);
+      ga[row * 2] = down<E>(g[4]);
+      ga[row * 2 + 1] = down<E>(g[5]);
+    } else {
+      E *o = gsos + row * int64_t(a.S) * 6 + 6 * s;
+#pragma unroll
+      for (int j = 0; j < 6; ++j) o[j] = down<E>(g[j]);
+    }
   }
 }
 

@@ -472,6 +472,107 @@ Triple sosfilt_backward_hip(const Tensor &sos, const Tensor &x, const Tensor &ck
   return {gx, gsos, gzi};
 }
 
+// One biquad as lfilter(b, a, x, zi, form="tdf2") on the cascade kernel
+// with b and a read where they lie (phs_biquad_fwd): b (nb,) or (batch, nb),
+// nb <= 3; a (2,) or (batch, 2), the denominator after its leading 1, each
+// with unit inner stride (any row stride: a column slice of a coefficient
+// table needs no copy); zi None or (batch, 2).  Returns (y, zf, ckpt), ckpt
+// the forward's state checkpoints for the backward.
+void check_biquad(const char *op, const Tensor &b, const Tensor &a, const Tensor &x) {
+  TORCH_CHECK(x.dim() == 2, "philtorch::", op, ": x must be a 2D tensor (batch, time)");
+  TORCH_CHECK(b.dim() == a.dim() && (b.dim() == 1 || b.dim() == 2), "philtorch::", op,
+              ": b and a must both be 1D (shared) or both 2D (batch, taps)");
+  TORCH_CHECK(b.size(-1) >= 1 && b.size(-1) <= 3 && a.size(-1) == 2, "philtorch::", op,
+              ": a biquad: b of 1 to 3 taps, a of 2 after the leading 1");
+  if (b.dim() == 2)
+    TORCH_CHECK(b.size(0) == x.size(0) && a.size(0) == x.size(0), "philtorch::", op,
+                ": 2D b and a must have x's batch size");
+  TORCH_CHECK(b.scalar_type() == x.scalar_type() && a.scalar_type() == x.scalar_type(), "philtorch::", op,
+              ": b, a and x must have the same scalar type");
+  TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble, "philtorch::", op,
+              ": float32 or float64 only, got ", x.scalar_type());
+  TORCH_CHECK(x.is_cuda() && b.device() == x.device() && a.device() == x.device(), "philtorch::", op,
+              ": philtorch_amd runs on HIP devices only, all tensors on one device");
+}
+
+// b or a with unit inner stride (a copy only where the taps are strided);
+// its row stride in elements, 0 for a shared (1D) one
+Tensor rows_unit_inner(const Tensor &t, int64_t &row_stride) {
+  Tensor u = t;
+  if (u.stride(-1) != 1 || (u.dim() == 2 && u.size(0) > 1 && u.stride(0) == 0)) u = u.contiguous();
+  row_stride = (u.dim() == 2 && u.size(0) > 1) ? u.stride(0) : 0;
+  return u;
+}
+
+Triple biquad_hip(const Tensor &b, const Tensor &a, const std::optional<Tensor> &zi, const Tensor &x) {
+  check_biquad("biquad", b, a, x);
+  const int64_t B = x.size(0), T = x.size(1);
+  if (zi)
+    TORCH_CHECK(zi->dim() == 2 && zi->size(0) == B && zi->size(1) == 2 && zi->scalar_type() == x.scalar_type() &&
+                    zi->device() == x.device(),
+                "philtorch::biquad: zi must be (batch, 2) with x's scalar type");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  int64_t bs = 0, as = 0;
+  Tensor bu = rows_unit_inner(b, bs), au = rows_unit_inner(a, as), xc = x.contiguous();
+  Tensor zc = zi ? zi->contiguous() : Tensor();
+  Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  Tensor zf = at::empty({B, 2}, x.options());
+  Tensor ckpt = at::empty({B, 1, sos_n_ckpt(T), 2}, x.options().dtype(at::kDouble));
+  if (B == 0 || T == 0) {
+    if (zi) zf.copy_(zc); else zf.zero_();
+    return {y, zf, ckpt};
+  }
+  void *stream = stream_of(x);
+  const Workspace ws = workspace_for(x, phs_sosfilt_workspace_size(dt, B, T, 1, 0), stream);
+  check_status(phs_biquad_fwd(dt, B, T, bu.const_data_ptr(), int(b.size(-1)), bs, au.const_data_ptr(), as,
+                              zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(), y.mutable_data_ptr(),
+                              zf.mutable_data_ptr(), ckpt.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+               "biquad");
+  return {y, zf, ckpt};
+}
+
+// Gradients of biquad (phs_biquad_bwd): (grad_x, grad_b, grad_a, grad_zi);
+// grad_b, grad_a shaped like b and a (zero unless need_coef); grad_zf None is
+// zero.
+std::vector<Tensor> biquad_backward_hip(const Tensor &b, const Tensor &a, const Tensor &x, const Tensor &ckpt,
+                                        const Tensor &gy, const std::optional<Tensor> &gzf, bool need_coef) {
+  check_biquad("biquad_backward", b, a, x);
+  const int64_t B = x.size(0), T = x.size(1);
+  TORCH_CHECK(gy.sizes() == x.sizes() && gy.device() == x.device(),
+              "philtorch::biquad_backward: grad_y must have x's shape and device");
+  if (gzf)
+    TORCH_CHECK(gzf->dim() == 2 && gzf->size(0) == B && gzf->size(1) == 2 && gzf->device() == x.device(),
+                "philtorch::biquad_backward: grad_zf must be (batch, 2)");
+  TORCH_CHECK(ckpt.scalar_type() == at::kDouble && ckpt.dim() == 4 && ckpt.size(0) == B && ckpt.size(1) == 1 &&
+                  ckpt.size(2) == sos_n_ckpt(T) && ckpt.size(3) == 2 && ckpt.device() == x.device(),
+              "philtorch::biquad_backward: ckpt must be the forward's checkpoint tensor");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  int64_t bs = 0, as = 0;
+  Tensor bu = rows_unit_inner(b, bs), au = rows_unit_inner(a, as), xc = x.contiguous();
+  Tensor gc = gy.to(x.scalar_type()).contiguous(), cc = ckpt.contiguous();
+  Tensor gzc = gzf ? gzf->to(x.scalar_type()).contiguous() : Tensor();
+  Tensor gx = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  Tensor gb = need_coef ? at::empty(b.sizes(), b.options()) : at::zeros(b.sizes(), b.options());
+  Tensor ga = need_coef ? at::empty(a.sizes(), a.options()) : at::zeros(a.sizes(), a.options());
+  Tensor gzi = at::empty({B, 2}, x.options());
+  if (B == 0 || T == 0) {
+    if (need_coef) gb.zero_(), ga.zero_();
+    if (gzf) gzi.copy_(gzc); else gzi.zero_();
+    return {gx, gb, ga, gzi};
+  }
+  void *stream = stream_of(x);
+  const Workspace ws = workspace_for(x, phs_sosfilt_workspace_size(dt, B, T, 1, 1), stream);
+  check_status(phs_biquad_bwd(dt, B, T, bu.const_data_ptr(), int(b.size(-1)), bs, au.const_data_ptr(), as,
+                              need_coef ? xc.const_data_ptr() : nullptr, need_coef ? cc.const_data_ptr() : nullptr,
+                              gc.const_data_ptr(), gzf ? gzc.const_data_ptr() : nullptr, gx.mutable_data_ptr(),
+                              need_coef ? gb.mutable_data_ptr() : nullptr, need_coef ? ga.mutable_data_ptr() : nullptr,
+                              gzi.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+               "biquad_backward");
+  return {gx, gb, ga, gzi};
+}
+
 // Zero-phase filter of order 4 at most (phs_filtfilt_fwd;
 // philtorch/lti/filtering.py:413-484): b (nb,) or (batch, nb), nb <= 5; a
 // (na,) or (batch, na), the denominator after its leading 1, na <= 4;
@@ -1052,6 +1153,11 @@ TORCH_LIBRARY(philtorch, m) {
   m.def("sosfilt_backward(Tensor sos, Tensor x, Tensor ckpt, Tensor grad_y, Tensor? grad_zf, bool need_sos)"
         " -> (Tensor, Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
+  // new: one biquad on the cascade kernel from lfilter's b and a, and its backward
+  m.def("biquad(Tensor b, Tensor a, Tensor? zi, Tensor x) -> (Tensor, Tensor, Tensor)", {at::Tag::pt2_compliant_tag});
+  m.def("biquad_backward(Tensor b, Tensor a, Tensor x, Tensor ckpt, Tensor grad_y, Tensor? grad_zf, bool need_coef)"
+        " -> Tensor[]",
+        {at::Tag::pt2_compliant_tag});
   // new: zero-phase filtering, filters of second order at most (forward only)
   m.def("filtfilt(Tensor b, Tensor a, Tensor x, int padmode, int padlen) -> Tensor", {at::Tag::pt2_compliant_tag});
   // new: single-input single-output LTI state space of order <= 4, fused: (y, zf)
@@ -1089,6 +1195,8 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("sosfilt", &sosfilt_hip);
   m.impl("sosfilt_backward", &sosfilt_backward_hip);
   m.impl("filtfilt", &filtfilt_hip);
+  m.impl("biquad", &biquad_hip);
+  m.impl("biquad_backward", &biquad_backward_hip);
   m.impl("lti_ss", &lti_ss_hip);
   m.impl("lfilter_ss", &lfilter_ss_hip);
   m.impl("lti_ss_backward", &lti_ss_backward_hip);

@@ -93,7 +93,7 @@ def _fused_biquad_applies(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor],
         return False
     if zi is not None and not (zi.dim() == 1 or (zi.dim() == 2 and zi.size(0) == x.size(0))):
         return False
-    if not hasattr(torch.ops.philtorch, "sosfilt"):
+    if not hasattr(torch.ops.philtorch, "biquad"):
         return False
     import torch.autograd.forward_ad as fwad
 
@@ -101,11 +101,13 @@ def _fused_biquad_applies(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor],
 
 
 def _fused_biquad(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor]):
-    """lfilter(b, a, x, zi, form="tdf2") of one biquad through philtorch::sosfilt."""
-    sos = torch.cat([F.pad(b, (0, 3 - b.size(-1))), torch.ones_like(a[..., :1]), a], dim=-1).unsqueeze(-2)
-    zb = None if zi is None else zi.expand(x.size(0), 2).unsqueeze(1).contiguous()
-    y, zf, _ = torch.ops.philtorch.sosfilt(sos.contiguous(), zb, x.contiguous())
-    return y if zi is None else (y, zf[:, 0])
+    """lfilter(b, a, x, zi, form="tdf2") of one biquad on the cascade kernel:
+    philtorch::biquad reads b and a where they lie (a column of a
+    coefficient table needs no copy) and keeps checkpoints for its fused
+    backward."""
+    zb = None if zi is None else zi.expand(x.size(0), 2).contiguous()
+    y, zf, _ = torch.ops.philtorch.biquad(b, a, zb, x)
+    return y if zi is None else (y, zf)
 
 
 def _fused_lfilter_applies(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor], form: str, kwargs) -> bool:

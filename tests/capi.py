@@ -86,6 +86,13 @@ def load() -> ctypes.CDLL:
                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                     ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.phs_sosfilt_bwd.restype = ctypes.c_int
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.phs_biquad_fwd.argtypes = [ctypes.c_int, i64, i64, vp, ctypes.c_int, i64, vp, i64, vp, vp, vp, vp, vp, vp,
+                                   ctypes.c_size_t, vp]
+    lib.phs_biquad_fwd.restype = ctypes.c_int
+    lib.phs_biquad_bwd.argtypes = [ctypes.c_int, i64, i64, vp, ctypes.c_int, i64, vp, i64, vp, vp, vp, vp, vp, vp,
+                                   vp, vp, vp, ctypes.c_size_t, vp]
+    lib.phs_biquad_bwd.restype = ctypes.c_int
     # zero-phase biquad filter
     lib.phs_filtfilt_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
     lib.phs_filtfilt_workspace_size.restype = ctypes.c_size_t

@@ -357,3 +357,84 @@ def test_sosfilt_capi_aggregates_only_multi_window(api, dtype):
     finally:
         lib.phs_debug_set_aggregates_only(0)
     _check_all(got, *case, dtype, "aggregates only")
+
+
+# ---------------------------------------------------------------- one biquad from b and a
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("layout", ["table", "rows", "shared"])
+@pytest.mark.parametrize("nb", [1, 2, 3])
+def test_biquad_capi_reads_b_and_a_in_place(api, dtype, layout, nb):
+    """phs_biquad_fwd/bwd: b and a read where they lie (columns of a
+    [B, S, 3] / [B, S, 2] coefficient table at row stride S*3 / S*2,
+    contiguous rows, or one shared filter) against the oracle's cascade at
+    S = 1, with initial and final states and the coefficient gradients."""
+    import torch
+
+    lib, ws, capi = api
+    g = D.rng(D.seed_of("biquad-capi", np.dtype(dtype).str, layout, nb))
+    B, T = 3, 13001
+    dt = capi.DTYPES[np.dtype(dtype)]
+    sos = D.sos_coefs(g, (B, 4), 1, dtype)[..., 0, :] if layout == "table" else \
+        D.sos_coefs(g, () if layout == "shared" else (B,), 1, dtype)[..., 0, :]
+    if nb < 3:
+        sos[..., nb:3] = 0
+    x, gy = D.normal(g, (B, T), dtype), D.normal(g, (B, T), dtype)
+    zi, gzf = D.normal(g, (B, 2), dtype), D.normal(g, (B, 2), dtype)
+    tsos = _dev(sos)
+    if layout == "table":  # column s = 2 of the table: row stride 4 * 6 elements
+        tb, ta = tsos[:, 2, 0:nb], tsos[:, 2, 4:6]
+        sos_rows = sos[:, 2]
+    else:
+        tb, ta = tsos[..., 0:nb], tsos[..., 4:6]
+        sos_rows = sos
+    bs = 0 if tb.dim() == 1 else tb.stride(0)
+    as_ = 0 if ta.dim() == 1 else ta.stride(0)
+    tx, tg, tz, tgz = _dev(x), _dev(gy), _dev(zi), _dev(gzf)
+    need = lib.phs_sosfilt_workspace_size(dt, B, T, 1, 1)
+    ck = torch.empty(lib.phs_sosfilt_ckpt_size(dt, B, T, 1), dtype=torch.uint8, device="cuda")
+    y, zf = torch.empty_like(tx), torch.empty((B, 2), dtype=tx.dtype, device="cuda")
+    print(f"biquad capi {np.dtype(dtype).name} layout={layout} nb={nb}", flush=True)
+    rc = lib.phs_biquad_fwd(dt, B, T, _p(tb), nb, bs, _p(ta), as_, _p(tz), _p(tx), _p(y), _p(zf), _p(ck), _p(ws),
+                            need, _stream())
+    assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+    rows = 1 if layout == "shared" else B
+    gx, gzi = torch.empty_like(tx), torch.empty((B, 2), dtype=tx.dtype, device="cuda")
+    gb = torch.full((rows, nb), float("nan"), dtype=tx.dtype, device="cuda")
+    ga = torch.full((rows, 2), float("nan"), dtype=tx.dtype, device="cuda")
+    rc = lib.phs_biquad_bwd(dt, B, T, _p(tb), nb, bs, _p(ta), as_, _p(tx), _p(ck), _p(tg), _p(tgz), _p(gx), _p(gb),
+                            _p(ga), _p(gzi), _p(ws), need, _stream())
+    assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+    torch.cuda.synchronize()
+    full = np.asarray(sos_rows, np.float64)[..., None, :]  # (B|., 1, 6)
+    got = [y.cpu().numpy(), zf.cpu().numpy()[:, None, :], None, gzi.cpu().numpy()[:, None, :], gx.cpu().numpy()]
+    _check_all(got, full, x, zi[:, None, :], gy, gzf[:, None, :], dtype, f"biquad {layout}")
+    rgs, _, _ = oracle.sosfilt_bwd(*_exact(full, x, zi[:, None, :], gy, gzf[:, None, :]))
+    rgs = rgs.reshape(rows, 6)
+    D.check(gb.cpu().numpy(), rgs[:, 0:nb], "grad_b", dtype=dtype)
+    D.check(ga.cpu().numpy(), rgs[:, 4:6], "grad_a", dtype=dtype)
+
+
+def test_biquad_op_gradients_and_opcheck(hip):
+    """philtorch::biquad through autograd: strided columns of a coefficient
+    table (the C4 caller pattern), gradcheck (the fused backward),
+    gradgradcheck (the composite), opcheck."""
+    import torch
+
+    g = D.rng(D.seed_of("biquad-op"))
+    B, T = 2, 40
+    sos = torch.tensor(D.sos_coefs(g, (B, 3), 1, np.float64)[..., 0, :], device="cuda")
+    b = sos[:, 1, 0:3].clone().requires_grad_(True)
+    a = sos[:, 1, 4:6].clone().requires_grad_(True)
+    x = torch.tensor(g.standard_normal((B, T)), device="cuda", requires_grad=True)
+    zi = torch.tensor(g.standard_normal((B, 2)), device="cuda", requires_grad=True)
+    f = lambda b_, a_, z_, x_: torch.ops.philtorch.biquad(b_, a_, z_, x_)[:2]  # noqa: E731
+    assert torch.autograd.gradcheck(f, (b, a, zi, x))
+    assert torch.autograd.gradgradcheck(f, (b, a, zi, x))
+    tab_b = torch.tensor(g.standard_normal((B, 4, 3)), device="cuda", requires_grad=True)
+    tab_a = (torch.tensor(D.sos_coefs(g, (B, 4), 1, np.float64)[..., 0, 4:6], device="cuda")).requires_grad_(True)
+    f2 = lambda tb_, ta_, x_: torch.ops.philtorch.biquad(tb_[:, 2], ta_[:, 2], None, x_)[0]  # noqa: E731
+    assert torch.autograd.gradcheck(f2, (tab_b, tab_a, x))
+    s = lambda v: torch.tensor(np.asarray(v, np.float32), device="cuda")  # noqa: E731
+    torch.library.opcheck(torch.ops.philtorch.biquad.default,
+                          (s(g.standard_normal(3)), s([-0.5, 0.2]), None, s(g.standard_normal((B, 700)))),
+                          test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
