@@ -144,7 +144,7 @@ int lpv_ss_bwd(int64_t B, int64_t T, const void *A, bool A_sh, bool A_tr, LpvOpe
     if (o->row_stride < 0 || o->t_stride < 0) return PHS_ERR_INVALID;
   if ((gb && !bv.p) || (gc && !cv.p) || (gd && !d.p)) return PHS_ERR_INVALID;
   if (B == 0) return PHS_OK;
-  if (!A || (T > 0 && (!x || !gy))) return PHS_ERR_INVALID;
+  if (T > 0 && (!A || !x || !gy)) return PHS_ERR_INVALID;
   const int64_t tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
   if (double(B) * double(tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
   const int shared = lpv_step_shared<E>(A_sh, bv, cv, d);

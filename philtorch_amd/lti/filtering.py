@@ -101,10 +101,15 @@ def _fused_biquad_applies(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor],
 
 
 def _fused_biquad(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor]):
-    """lfilter(b, a, x, zi, form="tdf2") of one biquad on the cascade kernel:
-    philtorch::biquad reads b and a where they lie (a column of a
-    coefficient table needs no copy) and keeps checkpoints for its fused
-    backward."""
+    """lfilter(b, a, x, zi, form="tdf2") of one biquad.  Where b or a needs
+    a gradient, the cascade kernel at one section: philtorch::biquad reads b
+    and a where they lie (a column of a coefficient table needs no copy) and
+    keeps checkpoints for its fused coefficient gradients.  Otherwise the
+    state-space kernel (philtorch::lfilter_ss), whose forward and x/zi
+    adjoint passes are the shorter ones at one section."""
+    if not (torch.is_grad_enabled() and (b.requires_grad or a.requires_grad)) and hasattr(torch.ops.philtorch,
+                                                                                          "lfilter_ss"):
+        return _fused_lfilter(b, a, x, zi, "tdf2")
     zb = None if zi is None else zi.expand(x.size(0), 2).contiguous()
     y, zf, _ = torch.ops.philtorch.biquad(b, a, zb, x)
     return y if zi is None else (y, zf)

@@ -249,3 +249,33 @@ def test_api_takes_fused_route_with_coefficient_gradients(hip, monkeypatch):
         for rev in (False, True):
             fl = lambda b_, a_, x_: torch.ops.philtorch.lfilter_ss(b_, a_, None, x_, form, rev)[0]  # noqa: E731
             assert torch.autograd.gradcheck(fl, (bf, af, xs))
+
+
+def test_backward_ops_on_empty_inputs(hip):
+    """The fused coefficient-gradient ops on rows of no steps (T = 0: zero
+    coefficient gradients, grad_zi = grad_zf) and on no rows (B = 0)."""
+    import torch
+
+    g = D.rng(D.seed_of("grad-empty"))
+    for B in (3, 0):
+        M = 2
+        A = _t(np.asarray(_normal_model(g, M, ()), np.float32))
+        b, c = _t(g.standard_normal(M).astype(np.float32)), _t(g.standard_normal((B, M)).astype(np.float32))
+        d = _t(g.standard_normal(B).astype(np.float32))
+        zi, gzf = _t(g.standard_normal((B, M)).astype(np.float32)), _t(g.standard_normal((B, M)).astype(np.float32))
+        x = torch.zeros(B, 0, device="cuda")
+        gA, gb, gc, gd, gzi, gx = torch.ops.philtorch.lti_ss_backward(A, b, c, d, zi, x, x, gzf, 0, False)
+        assert gx.shape == (B, 0) and gzi.shape == (B, M)
+        assert torch.equal(gzi, gzf)
+        for t in (gA, gb, gc, gd):
+            assert t.numel() == 0 or torch.count_nonzero(t).item() == 0
+        fb = _t(g.standard_normal((B, 3)).astype(np.float32))
+        fa = _t(np.tile(np.asarray([-0.5, 0.2], np.float32), (B, 1)))
+        gb2, ga2, gzi2, gx2 = torch.ops.philtorch.lfilter_ss_backward(fb, fa, zi, x, x, gzf, 0, False)
+        assert torch.equal(gzi2, gzf) and gx2.shape == (B, 0)
+        assert torch.count_nonzero(gb2).item() == 0 and torch.count_nonzero(ga2).item() == 0
+        Al = torch.zeros(B, 0, M, M, device="cuda")
+        bl = _t(g.standard_normal((B, 1, M)).astype(np.float32))
+        res = torch.ops.philtorch.lpv_ss_backward(Al, bl, None, None, zi, x, x, gzf, 0, False, False)
+        assert torch.equal(res[4], gzf) and res[0].shape == (B, 0, M, M)
+        assert torch.count_nonzero(res[1]).item() == 0
