@@ -19,10 +19,12 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c4      8 x (philtorch::lti_recur2 + lti_recurN_backward) (LTI biquad cascade)
   c4_fused  philtorch::sosfilt + sosfilt_backward              (the same cascade, fused)
   c4_api  8 x lti.lfilter(tdf2, unroll_factor=1) + autograd   (the caller pattern, API level)
+  c4_lfilter_inf  the same 8 lfilter calls under torch.no_grad (philtorch::lfilter_ss)
   c4_filtfilt  8 x lti.filtfilt(replicate, padlen 9), forward only (philtorch::filtfilt)
+  c4_filtfilt_grad  the same plus the gradient w.r.t. x (philtorch::filtfilt_backward)
   c4_lfilter4  4 x lti.lfilter of order 4 (tdf2), forward only (philtorch::lti_ss)
   c4_lfilter4_grad  the same plus gradients w.r.t. x, b and a (philtorch::lfilter_ss_backward)
---composed runs an API config (c3_lpv_ss*, c4_api, c4_filtfilt, c4_lfilter4)
+--composed runs an API config (c3_lpv_ss*, c4_api, c4_lfilter*, c4_filtfilt*)
 through the reference's composed route instead of the fused kernels, for the
 comparison.
 Before every step a 512 MiB buffer is read end to end so the 256 MB Infinity
@@ -365,6 +367,43 @@ class SosApi(SosFused):
         return torch.autograd.grad(y, inputs, self.dev[2])
 
 
+class LfilterInfApi(SosApi):
+    """c4_lfilter_inf: the C4 caller pattern's forward at inference, under
+    torch.no_grad: ``for s in range(8): y = lti.lfilter(b[:, s], a[:, s], y,
+    form="tdf2", unroll_factor=1)`` with b and a columns of the C4 tables.
+    Every call runs philtorch::lfilter_ss (B x, the scan, the state shift
+    and C h + D x in one pass of the state-space kernel)."""
+
+    def __init__(self):
+        super().__init__()
+        self.name = "c4_lfilter_inf"
+        self.metric = (f"GSamples/s fwd (no_grad), lti.lfilter cascade x{self.S} (tdf2) B={self.B} T={self.T} "
+                       "fp32 (API)")
+        self.fwd_bytes = 8 * self.B * self.T  # per lfilter: read x, write y
+        self.bwd_bytes = 0
+
+    def step_fwd(self):
+        import torch
+        from philtorch_amd import lti
+
+        sos, x, _ = self.dev
+        b, a = sos[..., 0:3], sos[..., 4:6]
+        with torch.no_grad():
+            y = x
+            for s in range(self.S):
+                y = lti.lfilter(b[:, s], a[:, s], y, form="tdf2", unroll_factor=1)
+        return y
+
+    def step_bwd(self, out):
+        return out
+
+    def cpu_step(self, rows, steps, nthreads):
+        import oracle
+
+        sos, x, _ = (v.numpy() for v in self.cpu)
+        oracle.sosfilt(sos[:rows], x[:rows, :steps], nthreads=nthreads)
+
+
 class FiltfiltApi(SosFused):
     """c4_filtfilt: the filtfilt half of the C4 caller pattern, forward only,
     ``for s in range(8): y = lti.filtfilt(b[:, s], a[:, s], y,
@@ -402,6 +441,38 @@ class FiltfiltApi(SosFused):
         y = x[:rows, :steps]
         for s in range(self.S):
             y = oracle.filtfilt(sos[:rows, s], y, padmode="replicate", padlen=9, nthreads=nthreads)
+
+
+class FiltfiltGrad(FiltfiltApi):
+    """c4_filtfilt_grad: c4_filtfilt with the gradient w.r.t. x
+    (torch.autograd.grad against a seeded upstream gradient).  Each
+    filtfilt's backward is philtorch::filtfilt_backward: the two passes'
+    adjoints, each a state-space launch of the DF-II model in the opposite
+    time direction, plus the per-row pad and edge terms."""
+
+    def __init__(self):
+        super().__init__()
+        self.name = "c4_filtfilt_grad"
+        self.metric = (f"GSamples/s fwd+bwd(x), lti.filtfilt x{self.S} sections (replicate, padlen 9) "
+                       f"B={self.B} T={self.T} fp32 (API)")
+        self.bwd_bytes = 16 * self.B * self.T  # per filtfilt: two adjoint passes, each reads and writes the row
+
+    def step_fwd(self):
+        from philtorch_amd import lti
+
+        x = self.dev[1].detach().requires_grad_(True)
+        y = x
+        for s in range(self.S):
+            y = lti.filtfilt(self.b[s], self.a[s], y, padmode="replicate", padlen=9, unroll_factor=1)
+        return y, x
+
+    def step_bwd(self, out):
+        import torch
+
+        y, x = out
+        return torch.autograd.grad(y, x, self.dev[2])
+
+    cpu_step = None  # the oracle restates filtfilt's forward only
 
 
 class Lfilter4Api(SosFused):
@@ -650,6 +721,10 @@ def make_workload(name):
         return SosApi()
     if name == "c4_filtfilt":
         return FiltfiltApi()
+    if name == "c4_filtfilt_grad":
+        return FiltfiltGrad()
+    if name == "c4_lfilter_inf":
+        return LfilterInfApi()
     if name == "c4_lfilter4":
         return Lfilter4Api()
     if name == "c3_lpv_ss":
@@ -663,9 +738,10 @@ def make_workload(name):
     raise ValueError(name)
 
 
-API_CONFIGS = ("c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4_api", "c4_filtfilt", "c4_lfilter4",
-               "c4_lfilter4_grad")
-CONFIGS = ("c1", "c2", "c3", "c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4", "c4_lfilter4_grad", "c4_fused", "c4_api", "c4_filtfilt", "c4_lfilter4", "c5", "c5_f64")
+API_CONFIGS = ("c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4_api", "c4_lfilter_inf", "c4_filtfilt",
+               "c4_filtfilt_grad", "c4_lfilter4", "c4_lfilter4_grad")
+CONFIGS = ("c1", "c2", "c3", "c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4", "c4_fused", "c4_api",
+           "c4_lfilter_inf", "c4_filtfilt", "c4_filtfilt_grad", "c4_lfilter4", "c4_lfilter4_grad", "c5", "c5_f64")
 
 
 # ----------------------------------------------------------------------------
@@ -953,6 +1029,8 @@ def main() -> int:
                 "c4_fused": "lti_sos8_cascade_fused_fwd_bwd_B16_T480000_f32",
                 "c4_api": "lti_lfilter8_cascade_api_fwd_bwd_B16_T480000_f32",
                 "c4_filtfilt": "lti_filtfilt8_api_fwd_B16_T480000_f32",
+                "c4_filtfilt_grad": "lti_filtfilt8_api_fwd_bwd_x_B16_T480000_f32",
+                "c4_lfilter_inf": "lti_lfilter8_cascade_api_fwd_nograd_B16_T480000_f32",
                 "c4_lfilter4": "lti_lfilter_order4_x4_api_fwd_B16_T480000_f32",
                 "c3_lpv_ss": "lpv_biquad_state_space_api_fwd_B32_T1048576_f32",
                 "c3_lpv_ss_grad": "lpv_biquad_state_space_api_fwd_bwd_x_zi_B32_T1048576_f32",

@@ -274,9 +274,10 @@ int phs_biquad_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64
                    void *grad_x, void *grad_b, void *grad_a, void *grad_zi, void *workspace, size_t workspace_bytes,
                    void *stream);
 
-/* ---- Zero-phase filtering with a filter of order 1..4 per row (forward
- * only).  Replaces philtorch.lti.filtering.filtfilt (philtorch/lti/
- * filtering.py:413-484, with lfilter_zi :107-142) for a filter b / a:
+/* ---- Zero-phase filtering with a filter of order 1..4 per row (its
+ * input gradient: phs_filtfilt_bwd below).  Replaces philtorch.lti.
+ * filtering.filtfilt (philtorch/lti/filtering.py:413-484, with lfilter_zi
+ * :107-142) for a filter b / a:
  *     ext = F.pad(x, (padlen, padlen), mode=padmode)
  *     y1  = lfilter(b, a, ext, zi = lfilter_zi(a, b) * ext[:, 0])
  *     y2  = lfilter(b, a, flip(y1), zi = lfilter_zi(a, b) * y1[:, -1])
@@ -307,6 +308,25 @@ size_t phs_filtfilt_mid_size(int dtype, int64_t B, int64_t T);
 int phs_filtfilt_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
                      int coef_shared, int padmode, int64_t padlen, const void *x, void *y, void *mid, void *workspace,
                      size_t workspace_bytes, void *stream);
+
+/* ---- Gradient of the zero-phase filter w.r.t. its input: grad_x = J^T
+ * grad_y of the linear map x -> phs_filtfilt_fwd(x) (same b, a, padmode,
+ * padlen).  Replaces the autograd of philtorch.lti.filtering.filtfilt's
+ * composed graph (philtorch/lti/filtering.py:413-484: F.pad, lfilter_zi
+ * * ext[:, :1], two lfilter passes with their flips, the trim) for inputs
+ * whose b and a need no gradient.  Two state-space launches of the adjoint
+ * model (the DF-II form of b and a, each in the direction opposite to its
+ * forward pass) and two one-thread-per-row kernels for the pad pieces and
+ * the steady-state edge terms (padlen serial steps per row); the padded,
+ * flipped and trimmed signals are never materialised.  Arguments as
+ * phs_filtfilt_fwd; grad_y, grad_x: [B,T]; workspace as
+ * phs_filtfilt_workspace_size; scratch: phs_filtfilt_bwd_scratch_size bytes
+ * (any contents, 16-byte aligned). */
+size_t phs_filtfilt_bwd_scratch_size(int dtype, int64_t B, int64_t T, int64_t padlen);
+
+int phs_filtfilt_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
+                     int coef_shared, int padmode, int64_t padlen, const void *grad_y, void *grad_x, void *scratch,
+                     size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- Single-input, single-output LTI state space of order M = 1..4, fused
  * (forward).  Replaces philtorch.lti.state_space (philtorch/lti/ssm.py:

@@ -378,15 +378,52 @@ if EXTENSION_LOADED and _has_op("biquad"):
     torch.library.register_autograd("philtorch::biquad", _biquad_backward, setup_context=_biquad_setup)
 
 if EXTENSION_LOADED and _has_op("filtfilt"):
-    # zero-phase biquad filter, forward only (lti.filtfilt takes it when no
-    # gradient is needed)
-    @torch.library.register_fake("philtorch::filtfilt")
-    def _(b, a, x, padmode, padlen):
+    # zero-phase filter of order 4 at most; lti.filtfilt takes it when b and
+    # a need no gradient.  Its input gradient is philtorch::filtfilt_backward
+    # (J^T of the linear map x -> y), whose own gradient is filtfilt again.
+    def _filtfilt_fake_check(b, a, x, padlen):
         torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
         torch._check(b.ndim == a.ndim and b.ndim in (1, 2), lambda: "b and a must both be 1D or both 2D")
         torch._check(1 <= b.shape[-1] <= 5 and 1 <= a.shape[-1] <= 4, lambda: "order 4 at most")
         torch._check(0 <= padlen < x.shape[1], lambda: "0 <= padlen < T")
+
+    @torch.library.register_fake("philtorch::filtfilt")
+    def _(b, a, x, padmode, padlen):
+        _filtfilt_fake_check(b, a, x, padlen)
         return _fake_like(x)
+
+    if _has_op("filtfilt_backward"):
+        @torch.library.register_fake("philtorch::filtfilt_backward")
+        def _(b, a, grad_y, padmode, padlen):
+            _filtfilt_fake_check(b, a, grad_y, padlen)
+            return _fake_like(grad_y)
+
+        def _filtfilt_setup(ctx, inputs, output):
+            b, a, _, padmode, padlen = inputs
+            ctx.save_for_backward(b, a)
+            ctx.pad = (padmode, padlen)
+            ctx.set_materialize_grads(False)
+
+        def _filtfilt_backward(ctx, gy):
+            if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
+                raise RuntimeError("philtorch::filtfilt has no gradient w.r.t. b and a: lti.filtfilt composes "
+                                   "lfilter passes when they need one")
+            if gy is None or not ctx.needs_input_grad[2]:
+                return None, None, None, None, None
+            b, a = ctx.saved_tensors
+            return None, None, torch.ops.philtorch.filtfilt_backward(b, a, gy, *ctx.pad), None, None
+
+        def _filtfilt_bwd_backward(ctx, ggx):
+            if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
+                raise RuntimeError("philtorch::filtfilt_backward has no gradient w.r.t. b and a")
+            if ggx is None or not ctx.needs_input_grad[2]:
+                return None, None, None, None, None
+            b, a = ctx.saved_tensors
+            return None, None, torch.ops.philtorch.filtfilt(b, a, ggx, *ctx.pad), None, None
+
+        torch.library.register_autograd("philtorch::filtfilt", _filtfilt_backward, setup_context=_filtfilt_setup)
+        torch.library.register_autograd("philtorch::filtfilt_backward", _filtfilt_bwd_backward,
+                                        setup_context=_filtfilt_setup)
 
 if EXTENSION_LOADED and _has_op("lti_ss"):
     # single-input single-output LTI state space of order <= 4: (y, zf)

@@ -254,6 +254,73 @@ int ss_filtfilt(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e, co
   return ss_launch<Alg, true>(p, stream);
 }
 
+// filtfilt backward's scratch: pass 1's adjoint input dL/dy1 over the
+// interior [B, T], the three [B, 4] adjoint states (after pass 2's interior,
+// entering and after pass 1's) and the back pad's values [B, padlen] in
+// double.
+struct FfBwdLayout {
+  size_t gy1 = 0, lam_a = 0, entry = 0, lam_b = 0, edge = 0, total = 0;
+};
+inline FfBwdLayout ff_bwd_layout(size_t esz, int64_t B, int64_t T, int64_t e) {
+  FfBwdLayout L;
+  L.lam_a = align_up(size_t(B) * size_t(T) * esz);
+  L.entry = L.lam_a + align_up(size_t(B) * 4 * esz);
+  L.lam_b = L.entry + align_up(size_t(B) * 4 * esz);
+  L.edge = L.lam_b + align_up(size_t(B) * 4 * esz);
+  L.total = L.edge + align_up(size_t(B) * size_t(e) * sizeof(double));
+  return L;
+}
+
+// dL/dx of the zero-phase filter (ff_bwd_edge_kernel's comment): pass 2's
+// adjoint over the interior, the back pad (edge kernel), pass 1's adjoint
+// over the interior in reversed time, the front pad and the fold (fold
+// kernel).  Both launches run the DF-II form of the same b and a, the
+// adjoint of the TDF-II model the forward runs.
+template <class Alg>
+int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e, const void *gy, void *gx,
+                    void *scratch, size_t scratch_bytes, void *workspace, size_t ws_bytes, hipStream_t stream) {
+  using E = typename Alg::elem;
+  constexpr int M = SsView<Alg>::M;
+  if (ws_bytes < filtfilt_ws_bytes<E>(B, T)) return PHS_ERR_WORKSPACE;
+  const FfBwdLayout L = ff_bwd_layout(sizeof(E), B, T, e);
+  if (!scratch || scratch_bytes < L.total) return PHS_ERR_WORKSPACE;
+  char *sc = static_cast<char *>(scratch);
+  FfBwdArgs<E> k{};
+  k.fb = static_cast<const E *>(f.b);
+  k.fa = static_cast<const E *>(f.a);
+  k.nb = f.nb;
+  k.na = f.na;
+  k.f_stride_b = f.shared ? 0 : f.nb;
+  k.f_stride_a = f.shared ? 0 : f.na;
+  k.B = B;
+  k.T = T;
+  k.e = e;
+  k.pad_mode = mode;
+  E *gy1 = reinterpret_cast<E *>(sc + L.gy1);
+  E *lam_a = reinterpret_cast<E *>(sc + L.lam_a);
+  E *entry = reinterpret_cast<E *>(sc + L.entry);
+  E *lam_b = reinterpret_cast<E *>(sc + L.lam_b);
+  k.lam_a = lam_a;
+  k.gy1 = gy1;
+  k.edge = reinterpret_cast<double *>(sc + L.edge);
+  k.entry = entry;
+  k.lam_b = lam_b;
+  k.gx = static_cast<E *>(gx);
+  SsFilter adj = f;
+  adj.form = 2;
+  SsArgs<Alg> p{};
+  if (!ss_args<Alg>(B, T, adj, nullptr, gy, gy1, lam_a, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+  int rc = ss_launch<Alg, false>(p, stream);
+  if (rc != PHS_OK) return rc;
+  const dim3 grid(unsigned((B + 63) / 64));
+  hipLaunchKernelGGL((ff_bwd_edge_kernel<E, M>), grid, dim3(64), 0, stream, k);
+  if (!ss_args<Alg>(B, T, adj, entry, gy1, gx, lam_b, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+  rc = ss_launch<Alg, true>(p, stream);
+  if (rc != PHS_OK) return rc;
+  hipLaunchKernelGGL((ff_bwd_fold_kernel<E, M>), grid, dim3(64), 0, stream, k);
+  return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
+}
+
 // f(Alg{}) for one of the eight (dtype, M) models
 template <class F>
 int ss_dispatch(int dtype, int M, F &&f) {
@@ -443,6 +510,41 @@ int phs_filtfilt_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, con
   f.shared = coef_shared != 0;
   return phs::ss_dispatch(dtype, M, [&](auto alg) {
     return phs::ss_filtfilt<decltype(alg)>(B, T, f, padmode, padlen, x, y, mid, workspace, workspace_bytes, st);
+  });
+}
+
+size_t phs_filtfilt_bwd_scratch_size(int dtype, int64_t B, int64_t T, int64_t padlen) {
+  if (B < 0 || T < 0 || padlen < 0) return 0;
+  switch (dtype) {
+    case PHS_F32: return phs::ff_bwd_layout(sizeof(float), B, T, padlen).total;
+    case PHS_F64: return phs::ff_bwd_layout(sizeof(double), B, T, padlen).total;
+    default: return 0;
+  }
+}
+
+int phs_filtfilt_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
+                     int coef_shared, int padmode, int64_t padlen, const void *grad_y, void *grad_x, void *scratch,
+                     size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream) {
+  if (dtype != PHS_F32 && dtype != PHS_F64) return PHS_ERR_DTYPE;
+  const int M = nb - 1 > na ? nb - 1 : na;
+  if (B < 0 || T < 1 || nb < 1 || nb > 5 || na < 1 || na > 4 || padlen < 0 || padlen >= T ||
+      padmode < PHS_PAD_CONSTANT || padmode > PHS_PAD_CIRCULAR)
+    return PHS_ERR_INVALID;
+  if (B == 0) return PHS_OK;
+  if (!b || !a || !grad_y || !grad_x) return PHS_ERR_INVALID;
+  const int64_t tile = dtype == PHS_F32 ? phs::SsShape<phs::Scalar<float>>::kTile : phs::SsShape<phs::Scalar<double>>::kTile;
+  if (!phs::ss_grid_ok(B, T, tile)) return PHS_ERR_INVALID;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  phs::SsFilter f;
+  f.b = b;
+  f.a = a;
+  f.nb = nb;
+  f.na = na;
+  f.form = 1;  // the forward's TDF-II model (ss_filtfilt_entry)
+  f.shared = coef_shared != 0;
+  return phs::ss_dispatch(dtype, M, [&](auto alg) {
+    return phs::ss_filtfilt_bwd<decltype(alg)>(B, T, f, padmode, padlen, grad_y, grad_x, scratch, scratch_bytes,
+                                               workspace, workspace_bytes, st);
   });
 }
 

@@ -309,6 +309,35 @@ __device__ __forceinline__ SsModel<Alg> ss_model(const SsArgs<Alg> &a, int64_t r
   return m;
 }
 
+// The TDF-II model of lfilter(fb, fa) of order M in double (filter form 1:
+// h' = A h + g u with A = companion(a)^T, g = b[1:] - b0 a, y = h0 + b0 u)
+// and its steady state for a unit input z = (I - A)^-1 g (lfilter_zi,
+// philtorch/lti/filtering.py:107-142), from the companion structure:
+// z0 = H(1) - b0 with H(1) = sum(b) / (1 + sum(a)), z(i+1) = z(i) + a_i z0
+// - g_i.
+template <int M>
+struct FfModel {
+  double am[M], g[M], z[M], b0;
+};
+template <int M, typename E>
+__device__ __forceinline__ FfModel<M> ff_model(const E *fb, int nb, const E *fa, int na) {
+  FfModel<M> f;
+  f.b0 = double(fb[0]);
+  double sb = f.b0, sa = 1.0;
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    f.am[i] = i < na ? double(fa[i]) : 0.0;
+    const double bi = i + 1 < nb ? double(fb[i + 1]) : 0.0;
+    f.g[i] = bi - f.b0 * f.am[i];
+    sb += bi;
+    sa += f.am[i];
+  }
+  f.z[0] = sb / sa - f.b0;
+#pragma unroll
+  for (int i = 0; i + 1 < M; ++i) f.z[i + 1] = f.z[i] + f.am[i] * f.z[0] - f.g[i];
+  return f;
+}
+
 // Entry state of row b for the two passes of a zero-phase filter
 // (virt_mode 1 and 2), in double, on the TDF-II model of lfilter(fb, fa) of
 // order M (filter form 1: h' = A h + g u with A = companion(a)^T, g = b[1:]
@@ -316,10 +345,7 @@ __device__ __forceinline__ SsModel<Alg> ss_model(const SsArgs<Alg> &a, int64_t r
 // caller names: each starts from the steady state of the same transfer
 // function, so the outputs are the same (the reference runs its `form`).
 //
-//  * steady state for a unit input, z = (I - A)^-1 g (lfilter_zi,
-//    philtorch/lti/filtering.py:107-142): from the companion structure,
-//    z0 = H(1) - b0 with H(1) = sum(b) / (1 + sum(a)), and
-//    z(i+1) = z(i) + a_i z0 - g_i;
+//  * z the steady state of a unit input (ff_model);
 //  * pass 1 starts at z ext[0] before the e front-pad samples of xpad, so
 //    its entry state is that stepped over them (filtering.py:466-470);
 //  * pass 2 filters the reversed pass-1 output over the padded row, whose
@@ -337,21 +363,12 @@ template <class Alg>
 __device__ __forceinline__ typename Alg::state ss_filtfilt_entry(const SsArgs<Alg> &a, int64_t b, int lane) {
   using E = typename Alg::elem;
   constexpr int M = SsView<Alg>::M;
-  const E *fb = a.fb + b * a.f_stride_b, *fa = a.fa + b * a.f_stride_a;
-  const double b0 = double(fb[0]);
-  double am[M], g[M], z[M], h[M];
-  double sb = b0, sa = 1.0;
-#pragma unroll
-  for (int i = 0; i < M; ++i) {
-    am[i] = i < a.na ? double(fa[i]) : 0.0;
-    const double bi = i + 1 < a.nb ? double(fb[i + 1]) : 0.0;
-    g[i] = bi - b0 * am[i];
-    sb += bi;
-    sa += am[i];
-  }
-  z[0] = sb / sa - b0;
-#pragma unroll
-  for (int i = 0; i + 1 < M; ++i) z[i + 1] = z[i] + am[i] * z[0] - g[i];
+  const FfModel<M> f = ff_model<M>(a.fb + b * a.f_stride_b, a.nb, a.fa + b * a.f_stride_a, a.na);
+  const double b0 = f.b0;
+  const double(&am)[M] = f.am;
+  const double(&g)[M] = f.g;
+  const double(&z)[M] = f.z;
+  double h[M];
   // h <- A h + g u (ascending i reads h[i+1] before it changes)
   auto step = [&](double (&v)[M], double u) {
     const double v0 = v[0];
@@ -1014,6 +1031,137 @@ __global__ __launch_bounds__(kSsReduceThreads) void ss_grad_finish_kernel(
       }
     }
   }
+}
+
+// ------------------------------------------------------ zero-phase filter backward
+// dL/dx of y = filtfilt(fb, fa, x), a map linear in x, over the padded row
+// ext of N = T + 2e samples: pass 1 runs the TDF-II model from z ext[0] over
+// ext, pass 2 the same model from z y1[N-1] over the reversed y1, and y is
+// pass 2's output at the T interior samples.  The adjoint model (DF-II of
+// the same b and a: A^T = companion(a), input vector e0, output vector g,
+// d = b0) runs twice, each time in the opposite direction of its pass:
+//  * pass 2's adjoint in ascending time over the upstream gradient padded
+//    with zeros: its state stays zero through the front pad; the interior is
+//    an ss_kernel launch from a zero state (dL/dy1 there, state lambda_A);
+//    the back pad continues from lambda_A with a zero input (dL/dy1 there);
+//    its final state dL/dh2[0] adds z . dL/dh2[0] to dL/dy1[N-1] (h2[0] =
+//    z y1[N-1]);
+//  * pass 1's adjoint in descending time over dL/dy1: the back pad from a
+//    zero state (dL/dext there, and the interior's entry state); the
+//    interior an ss_kernel launch in reversed time (dL/dx there, state
+//    lambda_B); the front pad continues from lambda_B with a zero input
+//    (dL/dy1 is zero there: pass 2's adjoint state is) (dL/dext there); its
+//    final state dL/dh1[0] adds z . dL/dh1[0] to dL/dext[0] (h1[0] = z
+//    ext[0]);
+//  * dL/dext of the pads folds into dL/dx through the pad's index map (the
+//    adjoint of F.pad; constant pads hold no x).
+// The pad pieces run serially per row in double, one thread per row:
+// ff_bwd_edge_kernel between the two launches, ff_bwd_fold_kernel after
+// them, e steps each (as the forward's entry states).
+template <typename E>
+struct FfBwdArgs {
+  const E *fb, *fa;
+  int nb, na;
+  int64_t f_stride_b, f_stride_a;  // 0 = shared
+  int64_t B, T, e;
+  int pad_mode;
+  const E *lam_a;  // [B, M] pass 2's adjoint state after the interior
+  E *gy1;          // [B, T] dL/dy1 of the interior (pass 1's adjoint input)
+  double *edge;    // [B, e] the back pad's dL/dy1, then its dL/dext
+  E *entry;        // [B, M] pass 1's adjoint state entering the interior
+  const E *lam_b;  // [B, M] pass 1's adjoint state after the interior
+  E *gx;           // [B, T]
+};
+
+// One step of the adjoint model from state s with input u; returns the
+// output (o = g . s + b0 u, s' = companion(a) s + e0 u).
+template <int M>
+__device__ __forceinline__ double ff_adj_step(const FfModel<M> &f, double (&s)[M], double u) {
+  double o = f.b0 * u, s0 = u;
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    o += f.g[i] * s[i];
+    s0 -= f.am[i] * s[i];
+  }
+#pragma unroll
+  for (int i = M - 1; i > 0; --i) s[i] = s[i - 1];
+  s[0] = s0;
+  return o;
+}
+
+template <int M>
+__device__ __forceinline__ double ff_dot_z(const FfModel<M> &f, const double (&s)[M]) {
+  double c = 0.0;
+#pragma unroll
+  for (int i = 0; i < M; ++i) c += f.z[i] * s[i];
+  return c;
+}
+
+// Between the launches: pass 2's adjoint over the back pad and its edge
+// term, then pass 1's adjoint over the back pad (its dL/dext, in place of
+// the dL/dy1 it consumes) up to the interior's entry state.  With no pad the
+// edge term lands on the interior's last dL/dy1.
+template <typename E, int M>
+__global__ __launch_bounds__(64) void ff_bwd_edge_kernel(FfBwdArgs<E> a) {
+  const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b >= a.B) return;
+  const FfModel<M> f = ff_model<M>(a.fb + b * a.f_stride_b, a.nb, a.fa + b * a.f_stride_a, a.na);
+  double s[M], r[M];
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    s[i] = double(a.lam_a[b * M + i]);
+    r[i] = 0.0;
+  }
+  double *u = a.edge + b * a.e;
+  for (int64_t j = 0; j < a.e; ++j) u[j] = ff_adj_step(f, s, 0.0);
+  const double c = ff_dot_z(f, s);
+  if (a.e > 0) {
+    u[a.e - 1] += c;
+  } else {
+    E *p = a.gy1 + b * a.T + (a.T - 1);
+    *p = E(double(*p) + c);
+  }
+  for (int64_t j = a.e - 1; j >= 0; --j) u[j] = ff_adj_step(f, r, u[j]);
+#pragma unroll
+  for (int i = 0; i < M; ++i) a.entry[b * M + i] = E(r[i]);
+}
+
+// After the launches: pass 1's adjoint over the front pad from lambda_B and
+// its edge term, then both pads' dL/dext folded into dL/dx (serial per row,
+// so pads that map onto one sample add up in order).
+template <typename E, int M>
+__global__ __launch_bounds__(64) void ff_bwd_fold_kernel(FfBwdArgs<E> a) {
+  const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b >= a.B) return;
+  const FfModel<M> f = ff_model<M>(a.fb + b * a.f_stride_b, a.nb, a.fa + b * a.f_stride_a, a.na);
+  const int64_t T = a.T, e = a.e;
+  E *gx = a.gx + b * T;
+  const double *ub = a.edge + b * e;
+  double r[M];
+#pragma unroll
+  for (int i = 0; i < M; ++i) r[i] = double(a.lam_b[b * M + i]);
+  auto add = [&](int64_t i, double v) { gx[i] = E(double(gx[i]) + v); };
+  if (e == 0) {  // ext is x
+    add(0, ff_dot_z(f, r));
+    return;
+  }
+  if (a.pad_mode == kPadConstant) return;
+  if (a.pad_mode == kPadReplicate) {
+    double sf = 0.0, sb = 0.0;
+    for (int64_t n = e - 1; n >= 0; --n) sf += ff_adj_step(f, r, 0.0);
+    sf += ff_dot_z(f, r);
+    for (int64_t j = 0; j < e; ++j) sb += ub[j];
+    add(0, sf);
+    add(T - 1, sb);
+    return;
+  }
+  const bool refl = a.pad_mode == kPadReflect;
+  for (int64_t n = e - 1; n >= 0; --n) {  // ext[n] is x[e - n] (reflect) or x[T - e + n]
+    double o = ff_adj_step(f, r, 0.0);
+    if (n == 0) o += ff_dot_z(f, r);
+    add(refl ? e - n : T - e + n, o);
+  }
+  for (int64_t j = 0; j < e; ++j) add(refl ? T - 2 - j : j, ub[j]);  // ext[T + e + j]
 }
 
 }  // namespace phs

@@ -576,27 +576,31 @@ std::vector<Tensor> biquad_backward_hip(const Tensor &b, const Tensor &a, const 
 // Zero-phase filter of order 4 at most (phs_filtfilt_fwd;
 // philtorch/lti/filtering.py:413-484): b (nb,) or (batch, nb), nb <= 5; a
 // (na,) or (batch, na), the denominator after its leading 1, na <= 4;
-// padmode a phs_padmode code.  Forward only: callers that need gradients
-// compose lfilter passes instead.
-Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t padmode, int64_t padlen) {
-  TORCH_CHECK(x.dim() == 2, "philtorch::filtfilt: x must be a 2D tensor (batch, time)");
-  TORCH_CHECK(b.dim() == a.dim() && (b.dim() == 1 || b.dim() == 2), "philtorch::filtfilt: b and a must both be 1D "
+// padmode a phs_padmode code.  Its input gradient is filtfilt_backward
+// below (the coefficients' gradients take the composed lfilter route).
+void filtfilt_check(const char *op, const Tensor &b, const Tensor &a, const Tensor &x, int64_t padmode,
+                    int64_t padlen) {
+  TORCH_CHECK(x.dim() == 2, op, ": x must be a 2D tensor (batch, time)");
+  TORCH_CHECK(b.dim() == a.dim() && (b.dim() == 1 || b.dim() == 2), op, ": b and a must both be 1D "
               "(shared) or both 2D (batch, taps)");
   const int64_t B = x.size(0), T = x.size(1);
-  if (b.dim() == 2)
-    TORCH_CHECK(b.size(0) == B && a.size(0) == B, "philtorch::filtfilt: 2D b and a must have x's batch size");
+  if (b.dim() == 2) TORCH_CHECK(b.size(0) == B && a.size(0) == B, op, ": 2D b and a must have x's batch size");
   const int64_t nb = b.size(-1), na = a.size(-1);
-  TORCH_CHECK(nb >= 1 && nb <= 5 && na >= 1 && na <= 4, "philtorch::filtfilt: filters of order 4 at most "
+  TORCH_CHECK(nb >= 1 && nb <= 5 && na >= 1 && na <= 4, op, ": filters of order 4 at most "
               "(b: 1 to 5 taps, a: 1 to 4 after the leading 1)");
-  TORCH_CHECK(b.scalar_type() == x.scalar_type() && a.scalar_type() == x.scalar_type(),
-              "philtorch::filtfilt: b, a and x must have the same scalar type");
-  TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,
-              "philtorch::filtfilt: float32 or float64 only, got ", x.scalar_type());
-  TORCH_CHECK(x.is_cuda() && b.device() == x.device() && a.device() == x.device(),
-              "philtorch::filtfilt: philtorch_amd runs on HIP devices only, all tensors on one device");
-  TORCH_CHECK(padmode >= PHS_PAD_CONSTANT && padmode <= PHS_PAD_CIRCULAR, "philtorch::filtfilt: unknown padmode ",
-              padmode);
+  TORCH_CHECK(b.scalar_type() == x.scalar_type() && a.scalar_type() == x.scalar_type(), op,
+              ": b, a and x must have the same scalar type");
+  TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble, op,
+              ": float32 or float64 only, got ", x.scalar_type());
+  TORCH_CHECK(x.is_cuda() && b.device() == x.device() && a.device() == x.device(), op,
+              ": philtorch_amd runs on HIP devices only, all tensors on one device");
+  TORCH_CHECK(padmode >= PHS_PAD_CONSTANT && padmode <= PHS_PAD_CIRCULAR, op, ": unknown padmode ", padmode);
   TORCH_CHECK(padlen >= 0 && T > padlen, "Input signal length ", T, " must be greater than pad length ", padlen, ".");
+}
+
+Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t padmode, int64_t padlen) {
+  filtfilt_check("philtorch::filtfilt", b, a, x, padmode, padlen);
+  const int64_t B = x.size(0), T = x.size(1), nb = b.size(-1), na = a.size(-1);
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
   const int dt = phs_dtype_of(x.scalar_type());
   Tensor bc = b.contiguous(), ac = a.contiguous(), xc = x.contiguous();
@@ -610,6 +614,28 @@ Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t p
                                 mid.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
                "filtfilt");
   return y;
+}
+
+// dL/dx of filtfilt (phs_filtfilt_bwd): grad_y (batch, time), b and a as
+// filtfilt's.  The map is linear in x, so x itself is not needed.
+Tensor filtfilt_backward_hip(const Tensor &b, const Tensor &a, const Tensor &grad_y, int64_t padmode,
+                             int64_t padlen) {
+  filtfilt_check("philtorch::filtfilt_backward", b, a, grad_y, padmode, padlen);
+  const int64_t B = grad_y.size(0), T = grad_y.size(1), nb = b.size(-1), na = a.size(-1);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(grad_y.device());
+  const int dt = phs_dtype_of(grad_y.scalar_type());
+  Tensor bc = b.contiguous(), ac = a.contiguous(), gy = grad_y.contiguous();
+  Tensor gx = at::empty_like(gy, at::MemoryFormat::Contiguous);
+  if (B == 0) return gx;
+  Tensor scratch =
+      at::empty({int64_t(phs_filtfilt_bwd_scratch_size(dt, B, T, padlen))}, gy.options().dtype(at::kByte));
+  void *stream = stream_of(gy);
+  const Workspace ws = workspace_for(gy, phs_filtfilt_workspace_size(dt, B, T), stream);
+  check_status(phs_filtfilt_bwd(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
+                                b.dim() == 1 ? 1 : 0, int(padmode), padlen, gy.const_data_ptr(), gx.mutable_data_ptr(),
+                                scratch.mutable_data_ptr(), size_t(scratch.numel()), ws.ptr, ws.bytes, stream),
+               "filtfilt_backward");
+  return gx;
 }
 
 // Single-input single-output LTI state space of order <= 4, fused
@@ -1160,6 +1186,8 @@ TORCH_LIBRARY(philtorch, m) {
         {at::Tag::pt2_compliant_tag});
   // new: zero-phase filtering, filters of second order at most (forward only)
   m.def("filtfilt(Tensor b, Tensor a, Tensor x, int padmode, int padlen) -> Tensor", {at::Tag::pt2_compliant_tag});
+  m.def("filtfilt_backward(Tensor b, Tensor a, Tensor grad_y, int padmode, int padlen) -> Tensor",
+        {at::Tag::pt2_compliant_tag});
   // new: single-input single-output LTI state space of order <= 4, fused: (y, zf)
   m.def("lti_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx, bool reverse=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
@@ -1195,6 +1223,7 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("sosfilt", &sosfilt_hip);
   m.impl("sosfilt_backward", &sosfilt_backward_hip);
   m.impl("filtfilt", &filtfilt_hip);
+  m.impl("filtfilt_backward", &filtfilt_backward_hip);
   m.impl("biquad", &biquad_hip);
   m.impl("biquad_backward", &biquad_backward_hip);
   m.impl("lti_ss", &lti_ss_hip);

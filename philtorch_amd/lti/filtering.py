@@ -203,10 +203,12 @@ _PAD_CODES = {"constant": 0, "replicate": 1, "reflect": 2, "circular": 3}
 
 def _fused_filtfilt_applies(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[str], form: str, kwargs) -> bool:
     """A filter of order 4 at most on a HIP device with the native route
-    requested (``unroll_factor=1``) and no gradient wanted: philtorch::filtfilt
-    runs both passes with the padding, the flips and the trim folded in.  Its
-    output is the same for the ``tdf2`` and ``df2`` forms (each pass starts
-    from the steady state of the same transfer function)."""
+    requested (``unroll_factor=1``) and no gradient wanted for b or a:
+    philtorch::filtfilt runs both passes with the padding, the flips and the
+    trim folded in, and its input gradient philtorch::filtfilt_backward the
+    two adjoint passes.  Its output is the same for the ``tdf2`` and ``df2``
+    forms (each pass starts from the steady state of the same transfer
+    function)."""
     from .. import EXTENSION_LOADED
 
     if not (EXTENSION_LOADED and x.is_cuda and form in ("tdf2", "df2") and set(kwargs) == {"unroll_factor"}
@@ -224,7 +226,9 @@ def _fused_filtfilt_applies(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[s
         return False
     if not hasattr(torch.ops.philtorch, "filtfilt"):
         return False
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (b, a, x)):
+    if torch.is_grad_enabled() and (b.requires_grad or a.requires_grad):
+        return False
+    if torch.is_grad_enabled() and x.requires_grad and not hasattr(torch.ops.philtorch, "filtfilt_backward"):
         return False
     import torch.autograd.forward_ad as fwad
 
@@ -256,8 +260,10 @@ def filtfilt(
     HIP device with ``unroll_factor=1`` and no gradient wanted runs
     philtorch::filtfilt (two state-space passes, the second in reversed time,
     their entry states derived in the kernel: no padded copy, no flips and no
-    host synchronisation); otherwise the passes are composed as in the
-    reference, each pass on the fused lfilter route."""
+    host synchronisation), also when x needs a gradient
+    (philtorch::filtfilt_backward); otherwise (b or a need one) the passes
+    are composed as in the reference, each pass on the fused lfilter
+    route."""
     assert method in ("pad", "gust"), "Method must be either 'pad' or 'gust'."
     if method == "gust":
         raise NotImplementedError("Gustafsson's method is not implemented yet.")

@@ -15,7 +15,14 @@ million steps; shared and per-row coefficients; the forced look-back fallback
 of both passes; a constant row and linearity at the benchmark's C4 size.
 Through the torch API: scipy (orders 1-4), the composed route (each pass an
 lfilter) at the C4 size, the route choice, and gradients (which take the
-composed route).
+composed route when b or a need one).
+
+The input gradient (phs_filtfilt_bwd, op philtorch::filtfilt_backward):
+J^T grad_y with J the oracle's filtfilt applied to unit impulses (exact, at
+small T, every pad mode, padlen 0 to T - 1), the adjoint identity
+<g, F x> = <F^T g, x> with F the oracle at rows of many tiles, the forced
+look-back fallback, the composed route's autograd (orders 1-4, every pad
+mode, 1D and 2D x, the C4 size), and gradcheck / gradgradcheck of the ops.
 """
 import ctypes
 
@@ -149,6 +156,95 @@ def test_filtfilt_capi_forced_fallback(api, dtype, order):
     _check(y, b, a, x, "replicate", 9, dtype, "fallback")
 
 
+def _run_bwd(api, b, a, gy, padmode, padlen, spin_limit=0):
+    """phs_filtfilt_bwd through the C ABI (scratch and output prefilled with
+    NaN bytes: every value must be written before it is read); numpy grad_x."""
+    import torch
+
+    lib, ws, capi = api
+    dt = capi.DTYPES[np.dtype(gy.dtype)]
+    B, T = gy.shape
+    need = lib.phs_filtfilt_workspace_size(dt, B, T)
+    assert 0 < need <= ws.numel()
+    sc = torch.full((lib.phs_filtfilt_bwd_scratch_size(dt, B, T, padlen),), 255, dtype=torch.uint8, device="cuda")
+    tb, ta, tg = _dev(b), _dev(a), _dev(gy)
+    gx = torch.full_like(tg, float("nan"))
+    print(f"filtfilt_bwd capi B={B} T={T} nb={b.shape[-1]} na={a.shape[-1]} {padmode} {padlen}", flush=True)
+    lib.phs_debug_set_spin_limit(spin_limit)
+    try:
+        rc = lib.phs_filtfilt_bwd(dt, B, T, _p(tb), b.shape[-1], _p(ta), a.shape[-1], int(b.ndim == 1),
+                                  capi.PADMODES[padmode], padlen, _p(tg), _p(gx), _p(sc), sc.numel(), _p(ws), need,
+                                  _stream())
+        assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+        torch.cuda.synchronize()
+    finally:
+        lib.phs_debug_set_spin_limit(0)
+    return gx.cpu().numpy()
+
+
+def _oracle_jt(b, a, T, padmode, padlen):
+    """The transposed Jacobian of the oracle's filtfilt for one filter (fp64):
+    row k of filtfilt_ba(I) is the response to e_k, the column J[:, k]."""
+    return oracle.filtfilt_ba(b, a, np.eye(T), padmode=padmode, padlen=padlen)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("order", ORDERS)
+@pytest.mark.parametrize("padmode", MODES)
+def test_filtfilt_bwd_capi_vs_oracle_jacobian(api, dtype, order, padmode):
+    """grad_x = J^T grad_y with J the oracle's own filtfilt applied to unit
+    impulses (exact for the linear map), shared and per-row filters, no pad,
+    a one-sample pad, 9, and the largest allowed (T - 1)."""
+    f64 = lambda v: np.asarray(v, np.float64)  # noqa: E731
+    for B, T in ((3, 40), (2, 13), (1, 1)):
+        for shared in (True, False):
+            b, a, _ = _case(dtype, B, T, shared, D.seed_of("filtfilt-bwd-jt", dtype, order, padmode, T, shared),
+                            order)
+            gy = D.normal(D.rng(D.seed_of("filtfilt-bwd-jt-g", T)), (B, T), dtype)
+            for padlen in sorted({0, min(1, T - 1), min(9, T - 1), T - 1}):
+                gx = _run_bwd(api, b, a, gy, padmode, padlen)
+                ref = np.stack([_oracle_jt(f64(b if shared else b[r]), f64(a if shared else a[r]), T, padmode,
+                                           padlen) @ f64(gy[r]) for r in range(B)])
+                D.check(gx, ref, f"B={B} T={T} shared={shared} padlen={padlen}", dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("order", ORDERS)
+@pytest.mark.parametrize("B,T", [(2, 3071), (3, 6145), (2, 12288), (1, 40000), (2, 30001)])
+def test_filtfilt_bwd_capi_adjoint_identity(api, dtype, order, B, T):
+    """<grad_y, F x> = <F^T grad_y, x> per row for two random x, F x the
+    oracle's filtfilt in fp64, around and over tiles, every pad mode at
+    padlen 9, T // 3 and T - 1."""
+    f64 = lambda v: np.asarray(v, np.float64)  # noqa: E731
+    b, a, _ = _case(dtype, B, T, False, D.seed_of("filtfilt-bwd-adj", dtype, order, T), order)
+    g = D.rng(D.seed_of("filtfilt-bwd-adj-g", dtype, order, T))
+    gy = D.normal(g, (B, T), dtype)
+    xs = [g.standard_normal((B, T)) for _ in range(2)]
+    for padmode in MODES:
+        for padlen in (9, T // 3, T - 1):
+            gx = f64(_run_bwd(api, b, a, gy, padmode, padlen))
+            assert np.isfinite(gx).all()
+            for x in xs:
+                y = oracle.filtfilt_ba(f64(b), f64(a), x, padmode=padmode, padlen=padlen)
+                lhs, rhs = np.sum(f64(gy) * y, axis=1), np.sum(gx * x, axis=1)
+                scale = np.sum(np.abs(f64(gy) * y), axis=1) + np.sum(np.abs(gx * x), axis=1)
+                tol = 1e-4 if dtype == np.float32 else 1e-11
+                assert np.all(np.abs(lhs - rhs) <= tol * scale), (padmode, padlen, lhs, rhs)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("order", ORDERS)
+def test_filtfilt_bwd_capi_forced_fallback(api, dtype, order):
+    """A one-poll budget: the tiles of both adjoint passes compute their
+    entry states from the row's prefix (pass 2's adjoint) or suffix (pass 1's)
+    themselves; equal to the look-back's result."""
+    b, a, _ = _case(dtype, 3, 40000, False, D.seed_of("filtfilt-bwd-fallback", dtype, order), order)
+    gy = D.normal(D.rng(D.seed_of("filtfilt-bwd-fallback-g", dtype)), (3, 40000), dtype)
+    ref = _run_bwd(api, b, a, gy, "reflect", 9)
+    got = _run_bwd(api, b, a, gy, "reflect", 9, spin_limit=1)
+    D.check(got, ref, "fallback", dtype=dtype)
+
+
 @pytest.mark.parametrize("order", [2, 4])
 def test_filtfilt_capi_constant_row_full_size(api, order):
     """At the C4 size a constant row comes out scaled by H(1)^2 for every
@@ -203,9 +299,13 @@ def test_filtfilt_route_choice(hip):
     assert filtering._fused_filtfilt_applies(torch.ones(3, 5, device="cuda"), a, x, "replicate", "tdf2", ok)
     assert not filtering._fused_filtfilt_applies(torch.ones(3, 6, device="cuda"), a, x, "replicate", "tdf2", ok)
     assert not filtering._fused_filtfilt_applies(b, torch.ones(3, 5, device="cuda"), x, "replicate", "tdf2", ok)
-    assert not filtering._fused_filtfilt_applies(b, a, x.requires_grad_(), "replicate", "tdf2", ok)
+    # an input gradient runs philtorch::filtfilt_backward; coefficient gradients the composed route
+    assert filtering._fused_filtfilt_applies(b, a, x.requires_grad_(), "replicate", "tdf2", ok)
+    bg = b.clone().requires_grad_()
+    assert not filtering._fused_filtfilt_applies(bg, a, x, "replicate", "tdf2", ok)
+    assert not filtering._fused_filtfilt_applies(b, a.clone().requires_grad_(), x, "replicate", "tdf2", ok)
     with torch.no_grad():
-        assert filtering._fused_filtfilt_applies(b, a, x, "replicate", "tdf2", ok)
+        assert filtering._fused_filtfilt_applies(bg, a, x, "replicate", "tdf2", ok)
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
@@ -237,24 +337,32 @@ def test_filtfilt_api_matches_scipy(hip, dtype):
                 D.check(y.cpu().numpy(), ref.astype(dtype), f"{shape} {batched} {padmode} {form}")
 
 
-def test_filtfilt_api_c4_size_matches_composed_route(hip):
+def test_filtfilt_api_c4_size_matches_composed_route(hip, monkeypatch):
     """The benchmark's filtfilt pattern at the C4 size (B=16, T=480000, fp32,
-    one filtfilt per section, padmode replicate, padlen 9): the fused route
-    against the composed one (padding, two lfilter passes, flips), which the
-    same call takes when x requires a gradient."""
+    one filtfilt per section, padmode replicate, padlen 9), output and input
+    gradient: the fused route against the composed one (padding, two lfilter
+    passes, flips, and their autograd)."""
     import torch
+
+    from philtorch_amd.lti import filtering
 
     g = D.rng(D.seed_of("filtfilt-c4"))
     B, T, S = 16, 480000, 8
     sos = torch.tensor(D.sos_coefs(g, (B,), S, np.float32, rhi=0.98), device="cuda")
     x = torch.tensor(g.standard_normal((B, T)).astype(np.float32), device="cuda")
+    gy = torch.tensor(g.standard_normal((B, T)).astype(np.float32), device="cuda")
     outs = []
-    for grad in (False, True):
-        y = x.clone().requires_grad_(grad)
+    for fused in (True, False):
+        if not fused:
+            monkeypatch.setattr(filtering, "_fused_filtfilt_applies", lambda *a, **k: False)
+        xr = x.clone().requires_grad_(True)
+        y = xr
         for s in range(S):
             y = hip.lti.filtfilt(sos[:, s, :3], sos[:, s, 4:], y, padmode="replicate", padlen=9, unroll_factor=1)
-        outs.append(y.detach().cpu().numpy())
-    D.check(outs[0], outs[1], "8 filtfilts")
+        (gx,) = torch.autograd.grad(y, xr, gy)
+        outs.append((y.detach().cpu().numpy(), gx.cpu().numpy()))
+    D.check(outs[0][0], outs[1][0], "8 filtfilts")
+    D.check(outs[0][1], outs[1][1], "8 filtfilts, grad x")
 
 
 def test_filtfilt_api_gradients_take_composed_route(hip):
@@ -268,6 +376,62 @@ def test_filtfilt_api_gradients_take_composed_route(hip):
     with torch.no_grad():
         fused = f(b, a, x)
     D.check(fused.cpu().numpy(), f(b, a, x).detach().cpu().numpy(), "no-grad vs grad route")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_filtfilt_api_input_gradient_fused_vs_composed(hip, dtype, monkeypatch):
+    """lti.filtfilt with x requiring a gradient (b and a not) takes the fused
+    route both ways and matches the composed route's autograd (every pad
+    mode, orders 1-4, shared and per-row filters, 1D and 2D x)."""
+    import torch
+
+    from philtorch_amd.lti import filtering
+
+    taken = []
+    orig = filtering._fused_filtfilt_applies
+    g = D.rng(D.seed_of("filtfilt-xgrad", dtype))
+    for shape, batched, order in (((3, 5000), True, 2), ((3, 5000), False, 1), ((777,), False, 2),
+                                  ((3, 5000), True, 3), ((2, 6145), False, 4), ((3, 4001), True, 4)):
+        b, a = D.ba_coefs(g, (shape[0],) if batched else (), order, dtype, rhi=0.98)
+        x = g.standard_normal(shape).astype(dtype)
+        gy = g.standard_normal(shape).astype(dtype)
+        tb, ta, tgy = (torch.tensor(v, device="cuda") for v in (b, a, gy))
+        for padmode, padlen in (("replicate", None), ("reflect", 100), ("constant", 7), ("circular", 31),
+                                (None, None)):
+            res = []
+            for fused in (True, False):
+                monkeypatch.setattr(filtering, "_fused_filtfilt_applies",
+                                    (lambda *a_: taken.append(orig(*a_)) or taken[-1]) if fused
+                                    else (lambda *a_, **k_: False))
+                tx = torch.tensor(x, device="cuda", requires_grad=True)
+                y = hip.lti.filtfilt(tb, ta, tx, padmode=padmode, padlen=padlen, unroll_factor=1)
+                if fused:
+                    assert taken[-1] is True
+                (gx,) = torch.autograd.grad(y, tx, tgy)
+                res.append((y.detach().cpu().numpy(), gx.cpu().numpy()))
+            nm = f"{shape} batched={batched} order={order} {padmode} {padlen}"
+            D.check(res[0][0], res[1][0], nm, dtype=dtype)
+            D.check(res[0][1], res[1][1], nm + " grad x", dtype=dtype)
+
+
+def test_filtfilt_op_gradcheck(hip):
+    """First and second order through the ops (fp64): filtfilt's gradient is
+    filtfilt_backward, whose own is filtfilt."""
+    import torch
+
+    g = D.rng(D.seed_of("filtfilt-gradcheck"))
+    for order, batched in ((1, False), (2, True), (3, False), (4, True)):
+        b, a = (torch.tensor(v, device="cuda") for v in D.ba_coefs(g, (2,) if batched else (), order, np.float64,
+                                                                     rhi=0.9))
+        x = torch.tensor(g.standard_normal((2, 30)), device="cuda", requires_grad=True)
+        for mode, padlen in ((1, 5), (2, 7), (3, 4), (0, 3), (1, 0), (2, 29)):
+            f = lambda x_: torch.ops.philtorch.filtfilt(b, a, x_, mode, padlen)  # noqa: E731
+            assert torch.autograd.gradcheck(f, (x,))
+            assert torch.autograd.gradgradcheck(f, (x,))
+    bg = b.clone().requires_grad_(True)
+    y = torch.ops.philtorch.filtfilt(bg, a, x, 1, 5)
+    with pytest.raises(RuntimeError, match="no gradient w.r.t. b and a"):
+        y.sum().backward()
 
 
 def test_filtfilt_api_errors(hip):
@@ -299,3 +463,9 @@ def test_filtfilt_opcheck(hip):
     b4, a4 = (torch.tensor(v, device="cuda") for v in D.ba_coefs(g, (2,), 4, np.float32))
     torch.library.opcheck(torch.ops.philtorch.filtfilt.default, (b4, a4, x, 3, 15),
                           test_utils=("test_schema", "test_faketensor"))
+    for args in ((b, a, x, 1, 9), (b4, a4, x, 2, 15), (b4, a4, x, 0, 0)):
+        torch.library.opcheck(torch.ops.philtorch.filtfilt_backward.default, args,
+                              test_utils=("test_schema", "test_faketensor"))
+        torch.library.opcheck(torch.ops.philtorch.filtfilt.default, (args[0], args[1], x.clone().requires_grad_(),
+                                                                     args[3], args[4]),
+                              test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))

@@ -22,7 +22,7 @@ def test_capi_exports_every_declared_symbol():
 
 def test_capi_host_only_calls():
     lib = capi.load()
-    assert lib.phs_abi_version() == 108
+    assert lib.phs_abi_version() == 109
     for op in capi.OPS.values():
         for dt in capi.DTYPES.values():
             fwd = lib.phs_workspace_size(op, dt, 64, 65536, 0, 0)
@@ -274,6 +274,42 @@ def test_capi_filtfilt_host_only_calls():
     for nb, na in ((3, 2), (2, 1), (5, 4)):
         assert call(wsb=need - 1, nb=nb, na=na) == capi.PHS_ERR_WORKSPACE
     assert lib.phs_filtfilt_fwd(0, 0, 100, None, 3, None, 2, 0, rep, 9, None, None, None, None, 0, None) == capi.PHS_OK
+
+
+def test_capi_filtfilt_bwd_host_only_calls():
+    """Sizes and argument errors of the zero-phase filter's input gradient
+    (nothing launches)."""
+    lib = capi.load()
+    for dt, esz in ((0, 4), (1, 8)):
+        # dL/dy1 of the interior, three [B, 4] states, the back pad in double
+        need = lib.phs_filtfilt_bwd_scratch_size(dt, 16, 480000, 9)
+        assert need >= 16 * 480000 * esz + 3 * 16 * 4 * esz + 16 * 9 * 8
+        assert lib.phs_filtfilt_bwd_scratch_size(dt, 16, 480000, 100) > need
+    for bad in ((2, 16, 100, 9), (0, -1, 100, 9), (0, 16, -1, 9), (0, 16, 100, -1)):
+        assert lib.phs_filtfilt_bwd_scratch_size(*bad) == 0
+    d = ctypes.c_void_p(16)
+    big = 1 << 30
+    rep = capi.PADMODES["replicate"]
+
+    def call(dt=0, T=100, nb=3, na=2, mode=rep, padlen=9, sc=d, scb=big, wsb=big, B=2, b=d, gy=d, gx=d):
+        return lib.phs_filtfilt_bwd(dt, B, T, b, nb, d, na, 0, mode, padlen, gy, gx, sc, scb, d, wsb, None)
+
+    assert call(dt=2) == capi.PHS_ERR_DTYPE
+    assert call(padlen=100) == capi.PHS_ERR_INVALID
+    assert call(padlen=-1) == capi.PHS_ERR_INVALID
+    assert call(T=0, padlen=0) == capi.PHS_ERR_INVALID
+    assert call(mode=4) == capi.PHS_ERR_INVALID
+    assert call(nb=6) == capi.PHS_ERR_INVALID and call(na=0) == capi.PHS_ERR_INVALID
+    assert call(b=None) == capi.PHS_ERR_INVALID and call(gy=None) == capi.PHS_ERR_INVALID
+    assert call(gx=None) == capi.PHS_ERR_INVALID
+    need_ws = lib.phs_filtfilt_workspace_size(0, 2, 100)
+    need_sc = lib.phs_filtfilt_bwd_scratch_size(0, 2, 100, 9)
+    for nb, na in ((3, 2), (2, 1), (5, 4)):
+        assert call(wsb=need_ws - 1, nb=nb, na=na) == capi.PHS_ERR_WORKSPACE
+        assert call(scb=need_sc - 1, nb=nb, na=na) == capi.PHS_ERR_WORKSPACE
+    assert call(sc=None) == capi.PHS_ERR_WORKSPACE
+    assert lib.phs_filtfilt_bwd(0, 0, 100, None, 3, None, 2, 0, rep, 9, None, None, None, 0, None, 0,
+                                None) == capi.PHS_OK
 
 
 def test_filtfilt_fused_route_not_taken_on_cpu():
