@@ -22,6 +22,7 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c4_lfilter_inf  the same 8 lfilter calls under torch.no_grad (philtorch::lfilter_ss)
   c4_filtfilt  8 x lti.filtfilt(replicate, padlen 9), forward only (philtorch::filtfilt)
   c4_filtfilt_grad  the same plus the gradient w.r.t. x (philtorch::filtfilt_backward)
+  c4_filtfilt_coef  the same plus the gradients w.r.t. x, b and a (its coefficient mode)
   c4_lfilter4  4 x lti.lfilter of order 4 (tdf2), forward only (philtorch::lti_ss)
   c4_lfilter4_grad  the same plus gradients w.r.t. x, b and a (philtorch::lfilter_ss_backward)
 --composed runs an API config (c3_lpv_ss*, c4_api, c4_lfilter*, c4_filtfilt*)
@@ -66,9 +67,14 @@ class Workload:
     metric = ""
     dtype_tag = "f32"
     samples = 0
-    fwd_bytes = 0  # algorithmic bytes of one forward launch
-    bwd_bytes = 0  # algorithmic bytes of one backward launch
-    launches = 1  # forward (and backward) launches per step
+    fwd_bytes = 0  # algorithmic bytes of one forward call (all its launches)
+    bwd_bytes = 0  # algorithmic bytes of one backward call
+    # algorithmic bytes of the first launch of a call, the one the launch hook
+    # times (None: the call is one launch, fwd_bytes / bwd_bytes)
+    fwd_launch_bytes = None
+    bwd_launch_bytes = None
+    kernel = "scan_kernel"  # the library kernel of those launches
+    launches = 1  # forward (and backward) calls per step
     # streaming-probe equivalents of one forward / backward launch: (names of
     # the arrays read, names of the arrays written, fp32 elements per array),
     # or None where the launch's traffic is not a set of equal-length arrays.
@@ -315,6 +321,7 @@ class SosFused(Workload):
         self.fwd_bytes = 8 * B * T  # read x, write y (state checkpoints: 1/32 of that)
         self.bwd_bytes = 12 * B * T  # read x and grad y, write grad x
         self.launches = 1
+        self.kernel = "sos_kernel"
 
     def step_fwd(self):
         import torch
@@ -377,6 +384,7 @@ class LfilterInfApi(SosApi):
     def __init__(self):
         super().__init__()
         self.name = "c4_lfilter_inf"
+        self.kernel = "ss_kernel"
         self.metric = (f"GSamples/s fwd (no_grad), lti.lfilter cascade x{self.S} (tdf2) B={self.B} T={self.T} "
                        "fp32 (API)")
         self.fwd_bytes = 8 * self.B * self.T  # per lfilter: read x, write y
@@ -417,8 +425,10 @@ class FiltfiltApi(SosFused):
         self.metric = (f"GSamples/s fwd, lti.filtfilt x{self.S} sections (replicate, padlen 9) "
                        f"B={self.B} T={self.T} fp32 (API)")
         self.fwd_bytes = 16 * self.B * self.T  # per filtfilt: two passes, each reads and writes the row
+        self.fwd_launch_bytes = 8 * self.B * self.T  # pass 1
         self.bwd_bytes = 0
         self.launches = self.S
+        self.kernel = "ss_kernel"
         sos = self.dev[0]
         self.b = [sos[:, s, 0:3].contiguous() for s in range(self.S)]
         self.a = [sos[:, s, 4:6].contiguous() for s in range(self.S)]
@@ -456,6 +466,7 @@ class FiltfiltGrad(FiltfiltApi):
         self.metric = (f"GSamples/s fwd+bwd(x), lti.filtfilt x{self.S} sections (replicate, padlen 9) "
                        f"B={self.B} T={self.T} fp32 (API)")
         self.bwd_bytes = 16 * self.B * self.T  # per filtfilt: two adjoint passes, each reads and writes the row
+        self.bwd_launch_bytes = 8 * self.B * self.T  # pass 2's adjoint: read g, write dL/dy1
 
     def step_fwd(self):
         from philtorch_amd import lti
@@ -475,6 +486,41 @@ class FiltfiltGrad(FiltfiltApi):
     cpu_step = None  # the oracle restates filtfilt's forward only
 
 
+class FiltfiltCoefGrad(FiltfiltGrad):
+    """c4_filtfilt_coef: c4_filtfilt with the gradients w.r.t. x and every
+    section's b and a.  Each filtfilt's backward is philtorch::
+    filtfilt_backward's coefficient mode: pass 1 again keeping its states
+    and output, pass 2 keeping its states, the two adjoint passes with the
+    model's gradient sums, the pads' sums and the steady state's in the
+    per-row kernels, the chain rule to b and a."""
+
+    def __init__(self):
+        super().__init__()
+        self.name = "c4_filtfilt_coef"
+        self.metric = (f"GSamples/s fwd+bwd(x, b, a), lti.filtfilt x{self.S} sections (replicate, padlen 9) "
+                       f"B={self.B} T={self.T} fp32 (API)")
+        # per filtfilt backward: pass 1 reads x, writes y1 and 2 states (16 B); pass 2 reads y1, writes 2 states
+        # (12 B); each adjoint reads its input, 2 states and the forward's input, writes its output (20 B)
+        self.bwd_bytes = 68 * self.B * self.T
+        self.bwd_launch_bytes = 16 * self.B * self.T  # pass 1 again: read x, write y1 and the states
+
+    def step_fwd(self):
+        from philtorch_amd import lti
+
+        x = self.dev[1].detach().requires_grad_(True)
+        coefs = [t.detach().requires_grad_(True) for t in self.b + self.a]
+        y = x
+        for s in range(self.S):
+            y = lti.filtfilt(coefs[s], coefs[self.S + s], y, padmode="replicate", padlen=9, unroll_factor=1)
+        return y, x, coefs
+
+    def step_bwd(self, out):
+        import torch
+
+        y, x, coefs = out
+        return torch.autograd.grad(y, [x] + coefs, self.dev[2])
+
+
 class Lfilter4Api(SosFused):
     """c4_lfilter4: the C4 signal through order-4 filters, forward only: the
     eight C4 biquads of each row multiplied pairwise into four order-4
@@ -488,6 +534,7 @@ class Lfilter4Api(SosFused):
 
         super().__init__()
         self.name = "c4_lfilter4"
+        self.kernel = "ss_kernel"
         self.S4 = self.S // 2
         self.metric = (f"GSamples/s fwd, lti.lfilter order-4 x{self.S4} (tdf2) B={self.B} T={self.T} fp32 (API)")
         sos = self.cpu[0].double()
@@ -544,6 +591,7 @@ class LpvSsApi(LpvBiquad):
         super().__init__()
         B, T = self.B, self.T
         self.name = "c3_lpv_ss"
+        self.kernel = "lpv_ss_kernel"
         self.metric = f"GSamples/s fwd, LPV biquad lpv.state_space (tdf2, one output) B={B} T={T} fp32 (API)"
         g = torch.Generator().manual_seed(33)
         rz = torch.rand(B, T + 63, generator=g, dtype=torch.float64) * 1.2
@@ -650,6 +698,7 @@ class Lfilter4Grad(Lfilter4Api):
         self.gy = torch.randn(self.B, self.T, generator=g).cuda()
         # per lfilter: states pass (read x, write 4 states) + adjoint (read g, x, 4 states; write grad_x)
         self.bwd_bytes = (4 + 16) * self.B * self.T + (4 + 4 + 16 + 4) * self.B * self.T
+        self.bwd_launch_bytes = (4 + 16) * self.B * self.T  # the states pass
 
     def step_fwd(self):
         from philtorch_amd import lti
@@ -685,6 +734,7 @@ class LpvSsCoefGrad(LpvSsGrad):
         # states pass: read A (16), x, b (8), write 2 states (8); adjoint: read A, b, d, g, x, states (8),
         # write grad_x, grad_A (16), grad_b (8), grad_d
         self.bwd_bytes = (16 + 4 + 8 + 8) * B * T + (16 + 8 + 4 + 4 + 4 + 8 + 4 + 16 + 8 + 4) * B * T
+        self.bwd_launch_bytes = (16 + 4 + 8 + 8) * B * T  # the states pass
 
     def step_fwd(self):
         from philtorch_amd import lpv
@@ -723,6 +773,8 @@ def make_workload(name):
         return FiltfiltApi()
     if name == "c4_filtfilt_grad":
         return FiltfiltGrad()
+    if name == "c4_filtfilt_coef":
+        return FiltfiltCoefGrad()
     if name == "c4_lfilter_inf":
         return LfilterInfApi()
     if name == "c4_lfilter4":
@@ -739,9 +791,10 @@ def make_workload(name):
 
 
 API_CONFIGS = ("c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4_api", "c4_lfilter_inf", "c4_filtfilt",
-               "c4_filtfilt_grad", "c4_lfilter4", "c4_lfilter4_grad")
+               "c4_filtfilt_grad", "c4_filtfilt_coef", "c4_lfilter4", "c4_lfilter4_grad")
 CONFIGS = ("c1", "c2", "c3", "c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4", "c4_fused", "c4_api",
-           "c4_lfilter_inf", "c4_filtfilt", "c4_filtfilt_grad", "c4_lfilter4", "c4_lfilter4_grad", "c5", "c5_f64")
+           "c4_lfilter_inf", "c4_filtfilt", "c4_filtfilt_grad", "c4_filtfilt_coef", "c4_lfilter4", "c4_lfilter4_grad",
+           "c5", "c5_f64")
 
 
 # ----------------------------------------------------------------------------
@@ -790,8 +843,8 @@ def cpu_baseline(w: Workload, budget_s=10.0):
 
 
 def _measured_traffic(config, direction="backward"):
-    """HBM bytes per launch of the dominant kernel (per call of the timed
-    unit where that is several kernels), from the rocprofv3 --pmc summary
+    """HBM bytes of one launch of the dominant kernel (the first launch of a
+    call, the one the launch hook times), from the rocprofv3 --pmc summary
     committed under profiles/ (FETCH_SIZE + WRITE_SIZE, each scaled by the
     same counter on a plain copy of known size), or None."""
     path = os.path.join(REPO, "profiles", f"traffic_{config}.json")
@@ -999,10 +1052,12 @@ def main() -> int:
     torch.cuda.synchronize()
     mean_fwd = sum(f[0].elapsed_time(f[1]) for f, _ in kev) / args.steps
     mean_bwd = sum(b[0].elapsed_time(b[1]) for _, b in kev) / args.steps if w.bwd_bytes else 0.0
+    fwd_lb = w.fwd_launch_bytes or w.fwd_bytes
+    bwd_lb = w.bwd_launch_bytes or w.bwd_bytes
     if w.bwd_bytes and mean_bwd >= mean_fwd:
-        dominant = ("backward", w.bwd_bytes, mean_bwd)
+        dominant = ("backward", bwd_lb, mean_bwd)
     else:
-        dominant = ("forward", w.fwd_bytes, mean_fwd)
+        dominant = ("forward", fwd_lb, mean_fwd)
     achieved = dominant[1] / (dominant[2] * 1e-3) / 1e9
     step_bytes = (w.fwd_bytes + w.bwd_bytes) * w.launches
     ceiling = _ceiling(lib, w, args.steps, evict_caches, dev)
@@ -1030,6 +1085,7 @@ def main() -> int:
                 "c4_api": "lti_lfilter8_cascade_api_fwd_bwd_B16_T480000_f32",
                 "c4_filtfilt": "lti_filtfilt8_api_fwd_B16_T480000_f32",
                 "c4_filtfilt_grad": "lti_filtfilt8_api_fwd_bwd_x_B16_T480000_f32",
+                "c4_filtfilt_coef": "lti_filtfilt8_api_fwd_bwd_x_b_a_B16_T480000_f32",
                 "c4_lfilter_inf": "lti_lfilter8_cascade_api_fwd_nograd_B16_T480000_f32",
                 "c4_lfilter4": "lti_lfilter_order4_x4_api_fwd_B16_T480000_f32",
                 "c3_lpv_ss": "lpv_biquad_state_space_api_fwd_B32_T1048576_f32",
@@ -1049,15 +1105,17 @@ def main() -> int:
             "ms_fwd_kernel": round(mean_fwd, 5),
             "ms_bwd_kernel": round(mean_bwd, 5) if w.bwd_bytes else None,
             "kernel_timing": "library launch hook: events recorded around the kernel by hipExtLaunchKernelGGL",
-            "fwd_GBs_algorithmic": round(w.fwd_bytes / (mean_fwd * 1e-3) / 1e9, 1),
-            "bwd_GBs_algorithmic": round(w.bwd_bytes / (mean_bwd * 1e-3) / 1e9, 1) if w.bwd_bytes else None,
-            "fwd_frac": round(w.fwd_bytes / (mean_fwd * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-            "bwd_frac": round(w.bwd_bytes / (mean_bwd * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if w.bwd_bytes else None,
+            "fwd_launch_bytes": fwd_lb,
+            "bwd_launch_bytes": bwd_lb if w.bwd_bytes else None,
+            "fwd_GBs_algorithmic": round(fwd_lb / (mean_fwd * 1e-3) / 1e9, 1),
+            "bwd_GBs_algorithmic": round(bwd_lb / (mean_bwd * 1e-3) / 1e9, 1) if w.bwd_bytes else None,
+            "fwd_frac": round(fwd_lb / (mean_fwd * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "bwd_frac": round(bwd_lb / (mean_bwd * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if w.bwd_bytes else None,
             "wall_s_timed_region": round(wall, 4),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{'ss_kernel' if w.name in ('c4_lfilter4', 'c4_filtfilt') else 'lpv_ss_kernel' if w.name.startswith('c3_lpv_ss') else 'sos_kernel' if w.name.startswith('c4_') else 'scan_kernel'} ({dominant[0]})",
+            "kernel": f"{w.kernel} ({dominant[0]}, first launch of a call)",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

@@ -275,7 +275,7 @@ int phs_biquad_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64
                    void *stream);
 
 /* ---- Zero-phase filtering with a filter of order 1..4 per row (its
- * input gradient: phs_filtfilt_bwd below).  Replaces philtorch.lti.
+ * gradients: phs_filtfilt_bwd below).  Replaces philtorch.lti.
  * filtering.filtfilt (philtorch/lti/filtering.py:413-484, with lfilter_zi
  * :107-142) for a filter b / a:
  *     ext = F.pad(x, (padlen, padlen), mode=padmode)
@@ -309,24 +309,32 @@ int phs_filtfilt_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, con
                      int coef_shared, int padmode, int64_t padlen, const void *x, void *y, void *mid, void *workspace,
                      size_t workspace_bytes, void *stream);
 
-/* ---- Gradient of the zero-phase filter w.r.t. its input: grad_x = J^T
- * grad_y of the linear map x -> phs_filtfilt_fwd(x) (same b, a, padmode,
- * padlen).  Replaces the autograd of philtorch.lti.filtering.filtfilt's
- * composed graph (philtorch/lti/filtering.py:413-484: F.pad, lfilter_zi
- * * ext[:, :1], two lfilter passes with their flips, the trim) for inputs
- * whose b and a need no gradient.  Two state-space launches of the adjoint
- * model (the DF-II form of b and a, each in the direction opposite to its
- * forward pass) and two one-thread-per-row kernels for the pad pieces and
- * the steady-state edge terms (padlen serial steps per row); the padded,
- * flipped and trimmed signals are never materialised.  Arguments as
- * phs_filtfilt_fwd; grad_y, grad_x: [B,T]; workspace as
- * phs_filtfilt_workspace_size; scratch: phs_filtfilt_bwd_scratch_size bytes
- * (any contents, 16-byte aligned). */
-size_t phs_filtfilt_bwd_scratch_size(int dtype, int64_t B, int64_t T, int64_t padlen);
+/* ---- Gradients of the zero-phase filter: grad_x = J^T grad_y of the
+ * linear map x -> phs_filtfilt_fwd(x) (same b, a, padmode, padlen) and,
+ * when grad_b and grad_a are given (both or neither), dL/db [nb] or [B,nb]
+ * and dL/da [na] or [B,na] (shared filters: summed over the rows), for
+ * L = <grad_y, y>.  Replaces the autograd of philtorch.lti.filtering.
+ * filtfilt's composed graph (philtorch/lti/filtering.py:413-484: F.pad,
+ * lfilter_zi * ext[:, :1] with its linalg.solve, two lfilter passes with
+ * their flips, the trim).  Input only: two state-space launches of the
+ * adjoint model (the DF-II form of b and a, each in the direction opposite
+ * to its forward pass) and two one-thread-per-row kernels for the pad
+ * pieces and the steady-state edge terms (padlen serial steps per row).
+ * With coefficient gradients: both passes again keeping their states, the
+ * adjoint launches also summing dL/dA, dL/dg, dL/db0 of the TDF-II model
+ * over the interior, the pads' sums and dL/dz (z = lfilter_zi) in the
+ * per-row kernels, the chain rule to b and a.  The padded, flipped and
+ * trimmed signals are never materialised.  Arguments as phs_filtfilt_fwd;
+ * x: [B,T], read only for coefficient gradients (may be NULL otherwise);
+ * grad_y, grad_x: [B,T]; workspace as phs_filtfilt_workspace_size;
+ * scratch: phs_filtfilt_bwd_scratch_size(dtype, M = max(nb - 1, na), B, T,
+ * padlen, need_coef) bytes (any contents, 16-byte aligned). */
+size_t phs_filtfilt_bwd_scratch_size(int dtype, int M, int64_t B, int64_t T, int64_t padlen, int need_coef);
 
 int phs_filtfilt_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
-                     int coef_shared, int padmode, int64_t padlen, const void *grad_y, void *grad_x, void *scratch,
-                     size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream);
+                     int coef_shared, int padmode, int64_t padlen, const void *x, const void *grad_y, void *grad_x,
+                     void *grad_b, void *grad_a, void *scratch, size_t scratch_bytes, void *workspace,
+                     size_t workspace_bytes, void *stream);
 
 /* ---- Single-input, single-output LTI state space of order M = 1..4, fused
  * (forward).  Replaces philtorch.lti.state_space (philtorch/lti/ssm.py:

@@ -378,9 +378,8 @@ if EXTENSION_LOADED and _has_op("biquad"):
     torch.library.register_autograd("philtorch::biquad", _biquad_backward, setup_context=_biquad_setup)
 
 if EXTENSION_LOADED and _has_op("filtfilt"):
-    # zero-phase filter of order 4 at most; lti.filtfilt takes it when b and
-    # a need no gradient.  Its input gradient is philtorch::filtfilt_backward
-    # (J^T of the linear map x -> y), whose own gradient is filtfilt again.
+    # zero-phase filter of order 4 at most (lti.filtfilt's fused route); its
+    # gradients are philtorch::filtfilt_backward
     def _filtfilt_fake_check(b, a, x, padlen):
         torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
         torch._check(b.ndim == a.ndim and b.ndim in (1, 2), lambda: "b and a must both be 1D or both 2D")
@@ -394,36 +393,65 @@ if EXTENSION_LOADED and _has_op("filtfilt"):
 
     if _has_op("filtfilt_backward"):
         @torch.library.register_fake("philtorch::filtfilt_backward")
-        def _(b, a, grad_y, padmode, padlen):
+        def _(b, a, x, grad_y, padmode, padlen, need_coef):
             _filtfilt_fake_check(b, a, grad_y, padlen)
-            return _fake_like(grad_y)
+            if need_coef:
+                return [_fake_like(grad_y), b.new_empty(b.shape), a.new_empty(a.shape)]
+            return [_fake_like(grad_y), b.new_empty((0,)), a.new_empty((0,))]
+
+        class _FiltfiltAdjoint(torch.autograd.Function):
+            """grad_x = J^T grad_y of filtfilt (b and a constant), whose own
+            gradient is J ggx: filtfilt again (second order)."""
+
+            @staticmethod
+            def forward(ctx, b, a, gy, padmode, padlen):
+                ctx.save_for_backward(b, a)
+                ctx.pad = (padmode, padlen)
+                return torch.ops.philtorch.filtfilt_backward(b, a, gy, gy, padmode, padlen, False)[0]
+
+            @staticmethod
+            def backward(ctx, ggx):
+                b, a = ctx.saved_tensors
+                return None, None, torch.ops.philtorch.filtfilt(b, a, ggx, *ctx.pad), None, None
 
         def _filtfilt_setup(ctx, inputs, output):
-            b, a, _, padmode, padlen = inputs
-            ctx.save_for_backward(b, a)
+            b, a, x, padmode, padlen = inputs
+            ctx.save_for_backward(b, a, x)
             ctx.pad = (padmode, padlen)
             ctx.set_materialize_grads(False)
 
         def _filtfilt_backward(ctx, gy):
-            if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
-                raise RuntimeError("philtorch::filtfilt has no gradient w.r.t. b and a: lti.filtfilt composes "
-                                   "lfilter passes when they need one")
-            if gy is None or not ctx.needs_input_grad[2]:
+            """x only: J^T gy (philtorch::filtfilt_backward, differentiable
+            again through filtfilt).  b or a too: the same op's coefficient
+            mode; under create_graph, the gradient of the composed route the
+            kernels replace (pad, lfilter_zi, two lfilter passes;
+            philtorch/lti/filtering.py:413-484), recomputed from the inputs."""
+            needs = ctx.needs_input_grad
+            if gy is None or not any(needs[:3]):
                 return None, None, None, None, None
-            b, a = ctx.saved_tensors
-            return None, None, torch.ops.philtorch.filtfilt_backward(b, a, gy, *ctx.pad), None, None
+            b, a, x = ctx.saved_tensors
+            need_coef = bool(needs[0] or needs[1])
+            if not need_coef:
+                if torch.is_grad_enabled():
+                    return None, None, _FiltfiltAdjoint.apply(b, a, gy, *ctx.pad), None, None
+                return None, None, torch.ops.philtorch.filtfilt_backward(b, a, x, gy, *ctx.pad, False)[0], None, None
+            if torch.is_grad_enabled():
+                from .lti.filtering import _PAD_CODES, _filtfilt_composed
 
-        def _filtfilt_bwd_backward(ctx, ggx):
-            if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
-                raise RuntimeError("philtorch::filtfilt_backward has no gradient w.r.t. b and a")
-            if ggx is None or not ctx.needs_input_grad[2]:
-                return None, None, None, None, None
-            b, a = ctx.saved_tensors
-            return None, None, torch.ops.philtorch.filtfilt(b, a, ggx, *ctx.pad), None, None
+                padmode = {v: k for k, v in _PAD_CODES.items()}[ctx.pad[0]]
+                inputs = (b, a, x)
+                wrt = [i for i in range(3) if needs[i]]
+                with torch.enable_grad():
+                    y = _filtfilt_composed(b, a, x, padmode, ctx.pad[1], unroll_factor=1)
+                    res = torch.autograd.grad(y, [inputs[i] for i in wrt], gy, create_graph=True, allow_unused=True)
+                out = [None] * 5
+                for i, g in zip(wrt, res):
+                    out[i] = g if g is not None else torch.zeros_like(inputs[i])
+                return tuple(out)
+            gx, gb, ga = torch.ops.philtorch.filtfilt_backward(b, a, x, gy, *ctx.pad, True)
+            return gb if needs[0] else None, ga if needs[1] else None, gx if needs[2] else None, None, None
 
         torch.library.register_autograd("philtorch::filtfilt", _filtfilt_backward, setup_context=_filtfilt_setup)
-        torch.library.register_autograd("philtorch::filtfilt_backward", _filtfilt_bwd_backward,
-                                        setup_context=_filtfilt_setup)
 
 if EXTENSION_LOADED and _has_op("lti_ss"):
     # single-input single-output LTI state space of order <= 4: (y, zf)

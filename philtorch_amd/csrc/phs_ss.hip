@@ -7,6 +7,8 @@
 // its own for the per-wave partial sums, the row sums and the forward's
 // states [B, T, M] (data must never land on the self-resetting status
 // words).
+#include <type_traits>
+
 #include "phs_launch.hpp"
 #include "phs_ss.hpp"
 
@@ -257,34 +259,71 @@ int ss_filtfilt(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e, co
 // filtfilt backward's scratch: pass 1's adjoint input dL/dy1 over the
 // interior [B, T], the three [B, 4] adjoint states (after pass 2's interior,
 // entering and after pass 1's) and the back pad's values [B, padlen] in
-// double.
+// double; with coefficient gradients also pass 1's output and final state,
+// both passes' interior states [B, T, M], the per-wave partial sums (one
+// buffer, used by each adjoint launch in turn), two [B, kN] row sums, dL/dz
+// [B, M] and the pads' forward states [B, padlen, 2M + 1] in double.
+template <class Alg>
 struct FfBwdLayout {
-  size_t gy1 = 0, lam_a = 0, entry = 0, lam_b = 0, edge = 0, total = 0;
+  size_t gy1 = 0, lam_a = 0, entry = 0, lam_b = 0, edge = 0;
+  size_t y1 = 0, zf1 = 0, h1 = 0, h2 = 0, gpart = 0, rowsum1 = 0, rowsum2 = 0, gz = 0, work = 0, total = 0;
 };
-inline FfBwdLayout ff_bwd_layout(size_t esz, int64_t B, int64_t T, int64_t e) {
-  FfBwdLayout L;
-  L.lam_a = align_up(size_t(B) * size_t(T) * esz);
-  L.entry = L.lam_a + align_up(size_t(B) * 4 * esz);
-  L.lam_b = L.entry + align_up(size_t(B) * 4 * esz);
-  L.edge = L.lam_b + align_up(size_t(B) * 4 * esz);
-  L.total = L.edge + align_up(size_t(B) * size_t(e) * sizeof(double));
+template <class Alg>
+FfBwdLayout<Alg> ff_bwd_layout(int64_t B, int64_t T, int64_t e, bool coef) {
+  using E = typename Alg::elem;
+  using C = typename Wide<E>::type;
+  constexpr int M = SsView<Alg>::M;
+  const size_t esz = sizeof(E), rows = size_t(B), n = size_t(B) * size_t(T);
+  FfBwdLayout<Alg> L;
+  L.lam_a = align_up(n * esz);
+  L.entry = L.lam_a + align_up(rows * 4 * esz);
+  L.lam_b = L.entry + align_up(rows * 4 * esz);
+  L.edge = L.lam_b + align_up(rows * 4 * esz);
+  L.total = L.edge + align_up(rows * size_t(e) * sizeof(double));
+  if (!coef) return L;
+  const int64_t tiles = (T + SsShape<Alg>::kTile - 1) / SsShape<Alg>::kTile;
+  constexpr int N = SsGrad<Alg>::kN;
+  L.y1 = L.total;
+  L.zf1 = L.y1 + align_up(n * esz);
+  L.h1 = L.zf1 + align_up(rows * M * esz);
+  L.h2 = L.h1 + align_up(n * sizeof(typename Alg::s_state));
+  L.gpart = L.h2 + align_up(n * sizeof(typename Alg::s_state));
+  L.rowsum1 = L.gpart + align_up(rows * size_t(tiles) * SsShape<Alg>::kWaves * N * sizeof(C));
+  L.rowsum2 = L.rowsum1 + align_up(rows * N * sizeof(C));
+  L.gz = L.rowsum2 + align_up(rows * N * sizeof(C));
+  L.work = L.gz + align_up(rows * M * sizeof(double));
+  L.total = L.work + align_up(rows * size_t(e) * (2 * M + 1) * sizeof(double));
   return L;
 }
 
-// dL/dx of the zero-phase filter (ff_bwd_edge_kernel's comment): pass 2's
-// adjoint over the interior, the back pad (edge kernel), pass 1's adjoint
-// over the interior in reversed time, the front pad and the fold (fold
-// kernel).  Both launches run the DF-II form of the same b and a, the
-// adjoint of the TDF-II model the forward runs.
+// Gradients of the zero-phase filter (ff_bwd_edge_kernel's comment).  Input
+// only: pass 2's adjoint over the interior, the back pad (edge kernel),
+// pass 1's adjoint over the interior in reversed time, the front pad and
+// the fold (fold kernel).  Both adjoint launches run the DF-II form of the
+// same b and a, the adjoint of the TDF-II model the forward runs.  With
+// coefficient gradients (gfb, gfa) first pass 1 again keeping its states,
+// output and final state (kSsStatesY) and pass 2 keeping its states
+// (kSsStates), then the adjoint launches in the gradient mode, each
+// followed by its row sums, the pads' sums and dL/dz in the edge and fold
+// kernels, and the filter chain rule (ss_grad_finish_kernel).
 template <class Alg>
-int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e, const void *gy, void *gx,
-                    void *scratch, size_t scratch_bytes, void *workspace, size_t ws_bytes, hipStream_t stream) {
+int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e, const void *x, const void *gy,
+                    void *gx, void *gfb, void *gfa, void *scratch, size_t scratch_bytes, void *workspace,
+                    size_t ws_bytes, hipStream_t stream) {
   using E = typename Alg::elem;
+  using C = typename Wide<E>::type;
+  using SS = typename Alg::s_state;
   constexpr int M = SsView<Alg>::M;
+  static_assert(std::is_same<C, double>::value, "row sums in double");
+  static_assert(FfSums<M>::kN == SsGrad<Alg>::kN && FfSums<M>::kB == SsGrad<Alg>::kB &&
+                    FfSums<M>::kD == SsGrad<Alg>::kD,
+                "the pads' sums in the kernels' layout");
+  const bool coef = gfb != nullptr;
   if (ws_bytes < filtfilt_ws_bytes<E>(B, T)) return PHS_ERR_WORKSPACE;
-  const FfBwdLayout L = ff_bwd_layout(sizeof(E), B, T, e);
+  const FfBwdLayout<Alg> L = ff_bwd_layout<Alg>(B, T, e, coef);
   if (!scratch || scratch_bytes < L.total) return PHS_ERR_WORKSPACE;
   char *sc = static_cast<char *>(scratch);
+  auto at = [&](size_t off) { return static_cast<void *>(sc + off); };
   FfBwdArgs<E> k{};
   k.fb = static_cast<const E *>(f.b);
   k.fa = static_cast<const E *>(f.a);
@@ -296,28 +335,107 @@ int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e
   k.T = T;
   k.e = e;
   k.pad_mode = mode;
-  E *gy1 = reinterpret_cast<E *>(sc + L.gy1);
-  E *lam_a = reinterpret_cast<E *>(sc + L.lam_a);
-  E *entry = reinterpret_cast<E *>(sc + L.entry);
-  E *lam_b = reinterpret_cast<E *>(sc + L.lam_b);
+  E *gy1 = static_cast<E *>(at(L.gy1));
+  E *lam_a = static_cast<E *>(at(L.lam_a));
+  E *entry = static_cast<E *>(at(L.entry));
+  E *lam_b = static_cast<E *>(at(L.lam_b));
   k.lam_a = lam_a;
   k.gy1 = gy1;
-  k.edge = reinterpret_cast<double *>(sc + L.edge);
+  k.edge = static_cast<double *>(at(L.edge));
   k.entry = entry;
   k.lam_b = lam_b;
   k.gx = static_cast<E *>(gx);
+  const int64_t tiles = (T + SsShape<Alg>::kTile - 1) / SsShape<Alg>::kTile;
+  const dim3 grid(unsigned((B + 63) / 64));
   SsFilter adj = f;
   adj.form = 2;
   SsArgs<Alg> p{};
+  int rc = PHS_OK;
+  E *y1 = nullptr, *zf1 = nullptr;
+  SS *h1 = nullptr, *h2 = nullptr;
+  C *gpart = nullptr, *rowsum1 = nullptr, *rowsum2 = nullptr;
+  auto vec_states = [&](const void *hs, const void *xf) {
+    return aligned16(hs) && (size_t(T) * sizeof(SS)) % 16 == 0 && aligned16(xf) && (size_t(T) * sizeof(E)) % 16 == 0;
+  };
+  if (coef) {
+    y1 = static_cast<E *>(at(L.y1));
+    zf1 = static_cast<E *>(at(L.zf1));
+    h1 = static_cast<SS *>(at(L.h1));
+    h2 = static_cast<SS *>(at(L.h2));
+    gpart = static_cast<C *>(at(L.gpart));
+    rowsum1 = static_cast<C *>(at(L.rowsum1));
+    rowsum2 = static_cast<C *>(at(L.rowsum2));
+    k.coef = 1;
+    k.x = static_cast<const E *>(x);
+    k.y1 = y1;
+    k.zf1 = zf1;
+    k.work = static_cast<double *>(at(L.work));
+    k.gz = static_cast<double *>(at(L.gz));
+    k.rowsum1 = rowsum1;
+    k.rowsum2 = rowsum2;
+    // pass 1 (states, output, final state), then pass 2 (states)
+    if (!ss_args<Alg>(B, T, f, nullptr, x, y1, zf1, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+    p.virt_mode = 1;
+    p.xpad = static_cast<const E *>(x);
+    p.pad_mode = mode;
+    p.pad_len = e;
+    p.hs = reinterpret_cast<E *>(h1);
+    p.vec_hs = vec_states(h1, x);
+    if ((rc = ss_launch<Alg, false, kSsStatesY>(p, stream)) != PHS_OK) return rc;
+    p = SsArgs<Alg>{};
+    if (!ss_args<Alg>(B, T, f, nullptr, y1, nullptr, nullptr, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+    p.virt_mode = 2;
+    p.xpad = static_cast<const E *>(x);
+    p.zf_prev = zf1;
+    p.pad_mode = mode;
+    p.pad_len = e;
+    p.hs = reinterpret_cast<E *>(h2);
+    p.vec_hs = vec_states(h2, y1);
+    if ((rc = ss_launch<Alg, true, kSsStates>(p, stream)) != PHS_OK) return rc;
+  }
+  // pass 2's adjoint over the interior (ascending time)
+  p = SsArgs<Alg>{};
   if (!ss_args<Alg>(B, T, adj, nullptr, gy, gy1, lam_a, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
-  int rc = ss_launch<Alg, false>(p, stream);
-  if (rc != PHS_OK) return rc;
-  const dim3 grid(unsigned((B + 63) / 64));
+  if (coef) {
+    p.hs_fwd = reinterpret_cast<const E *>(h2);
+    p.x_fwd = y1;
+    p.gpart = gpart;
+    p.vec_hs = vec_states(h2, y1);
+    if ((rc = ss_launch<Alg, false, kSsGrad>(p, stream)) != PHS_OK) return rc;
+    hipLaunchKernelGGL(ss_grad_rows_kernel<Alg>, dim3(unsigned(B)), dim3(kSsReduceThreads), 0, stream,
+                       static_cast<const C *>(gpart), tiles * SsShape<Alg>::kWaves, rowsum2);
+  } else if ((rc = ss_launch<Alg, false>(p, stream)) != PHS_OK) {
+    return rc;
+  }
   hipLaunchKernelGGL((ff_bwd_edge_kernel<E, M>), grid, dim3(64), 0, stream, k);
+  // pass 1's adjoint over the interior (descending time)
+  p = SsArgs<Alg>{};
   if (!ss_args<Alg>(B, T, adj, entry, gy1, gx, lam_b, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
-  rc = ss_launch<Alg, true>(p, stream);
-  if (rc != PHS_OK) return rc;
+  if (coef) {
+    p.hs_fwd = reinterpret_cast<const E *>(h1);
+    p.x_fwd = static_cast<const E *>(x);
+    p.gpart = gpart;
+    p.vec_hs = vec_states(h1, x);
+    if ((rc = ss_launch<Alg, true, kSsGrad>(p, stream)) != PHS_OK) return rc;
+    hipLaunchKernelGGL(ss_grad_rows_kernel<Alg>, dim3(unsigned(B)), dim3(kSsReduceThreads), 0, stream,
+                       static_cast<const C *>(gpart), tiles * SsShape<Alg>::kWaves, rowsum1);
+  } else if ((rc = ss_launch<Alg, true>(p, stream)) != PHS_OK) {
+    return rc;
+  }
   hipLaunchKernelGGL((ff_bwd_fold_kernel<E, M>), grid, dim3(64), 0, stream, k);
+  if (coef) {
+    SsGradOut<E> out{};
+    out.form = 1;
+    out.f_sh = f.shared;
+    out.fb = static_cast<const E *>(f.b);
+    out.fa = static_cast<const E *>(f.a);
+    out.nb = f.nb;
+    out.na = f.na;
+    out.gfb = static_cast<E *>(gfb);
+    out.gfa = static_cast<E *>(gfa);
+    hipLaunchKernelGGL(ss_grad_finish_kernel<Alg>, dim3(1), dim3(kSsReduceThreads), 0, stream,
+                       static_cast<const C *>(rowsum1), B, T, out);
+  }
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
@@ -513,25 +631,29 @@ int phs_filtfilt_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, con
   });
 }
 
-size_t phs_filtfilt_bwd_scratch_size(int dtype, int64_t B, int64_t T, int64_t padlen) {
-  if (B < 0 || T < 0 || padlen < 0) return 0;
-  switch (dtype) {
-    case PHS_F32: return phs::ff_bwd_layout(sizeof(float), B, T, padlen).total;
-    case PHS_F64: return phs::ff_bwd_layout(sizeof(double), B, T, padlen).total;
-    default: return 0;
-  }
+size_t phs_filtfilt_bwd_scratch_size(int dtype, int M, int64_t B, int64_t T, int64_t padlen, int need_coef) {
+  if (B < 0 || T < 0 || padlen < 0 || M < 1 || M > 4) return 0;
+  size_t n = 0;
+  if (phs::ss_dispatch(dtype, M, [&](auto alg) {
+        n = phs::ff_bwd_layout<decltype(alg)>(B, T, padlen, need_coef != 0).total;
+        return PHS_OK;
+      }) != PHS_OK)
+    return 0;
+  return n;
 }
 
 int phs_filtfilt_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
-                     int coef_shared, int padmode, int64_t padlen, const void *grad_y, void *grad_x, void *scratch,
-                     size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream) {
+                     int coef_shared, int padmode, int64_t padlen, const void *x, const void *grad_y, void *grad_x,
+                     void *grad_b, void *grad_a, void *scratch, size_t scratch_bytes, void *workspace,
+                     size_t workspace_bytes, void *stream) {
   if (dtype != PHS_F32 && dtype != PHS_F64) return PHS_ERR_DTYPE;
   const int M = nb - 1 > na ? nb - 1 : na;
   if (B < 0 || T < 1 || nb < 1 || nb > 5 || na < 1 || na > 4 || padlen < 0 || padlen >= T ||
       padmode < PHS_PAD_CONSTANT || padmode > PHS_PAD_CIRCULAR)
     return PHS_ERR_INVALID;
+  if ((grad_b == nullptr) != (grad_a == nullptr)) return PHS_ERR_INVALID;
   if (B == 0) return PHS_OK;
-  if (!b || !a || !grad_y || !grad_x) return PHS_ERR_INVALID;
+  if (!b || !a || !grad_y || !grad_x || (grad_b && !x)) return PHS_ERR_INVALID;
   const int64_t tile = dtype == PHS_F32 ? phs::SsShape<phs::Scalar<float>>::kTile : phs::SsShape<phs::Scalar<double>>::kTile;
   if (!phs::ss_grid_ok(B, T, tile)) return PHS_ERR_INVALID;
   const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -543,8 +665,8 @@ int phs_filtfilt_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, con
   f.form = 1;  // the forward's TDF-II model (ss_filtfilt_entry)
   f.shared = coef_shared != 0;
   return phs::ss_dispatch(dtype, M, [&](auto alg) {
-    return phs::ss_filtfilt_bwd<decltype(alg)>(B, T, f, padmode, padlen, grad_y, grad_x, scratch, scratch_bytes,
-                                               workspace, workspace_bytes, st);
+    return phs::ss_filtfilt_bwd<decltype(alg)>(B, T, f, padmode, padlen, x, grad_y, grad_x, grad_b, grad_a, scratch,
+                                               scratch_bytes, workspace, workspace_bytes, st);
   });
 }
 

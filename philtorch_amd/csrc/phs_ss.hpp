@@ -642,8 +642,10 @@ __device__ bool ss_lookback(const uint64_t *row_status, const typename Alg::stat
 
 // Kernel modes: the model's output (plain), the states of a forward for the
 // coefficient gradients (kSsStates: h[t] before every step, no y), the
-// adjoint pass with the coefficient-gradient sums (kSsGrad).
-constexpr int kSsPlain = 0, kSsStates = 1, kSsGrad = 2;
+// adjoint pass with the coefficient-gradient sums (kSsGrad), the states
+// and the output with the final state (kSsStatesY: a zero-phase filter's
+// first pass, whose output is the second pass's input).
+constexpr int kSsPlain = 0, kSsStates = 1, kSsGrad = 2, kSsStatesY = 3;
 
 // Coefficient-gradient sums of one model: dL/dA (M x M row-major), dL/db
 // (M), dL/dc (M), dL/dd; a lane sums its own steps in storage precision
@@ -829,6 +831,7 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
 #pragma unroll
   for (int r = 1; r < R; ++r) ent[r] = Alg::affine(s_tab.pw[6], ent[r - 1], tot[r - 1]);
   ss_pow_apply<Alg, 6, R>(s_tab.pw, sl, ent);
+  constexpr bool kStates = MODE == kSsStates || MODE == kSsStatesY;
   constexpr int G = MODE == kSsPlain ? K : ss_state_group<Alg>();
   const bool vh = a.vec_hs != 0;
   SsGrad<Alg, E> lacc;
@@ -851,9 +854,8 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
 #pragma unroll
       for (int k2 = 0; k2 < G; ++k2) {
         const int k = g0 + k2;
-        if constexpr (MODE == kSsStates) {
-          Hg[k2] = h;
-        } else {
+        if constexpr (kStates) Hg[k2] = h;
+        if constexpr (MODE != kSsStates) {
           O[k] = fma(m.d, X[r][k], V::dot(m.c, h));
           if constexpr (MODE == kSsGrad) ss_grad_step<Alg>(lacc, h, Hg[k2], Xg[k2], X[r][k]);
         }
@@ -868,10 +870,10 @@ __global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Al
           for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = u.e[i];
         }
       }
-      if constexpr (MODE == kSsStates)
-        ss_store<REV, SS, G>(reinterpret_cast<SS *>(a.hs) + b * T, t0s[r] + g0, T, vh, Hg);
+      if constexpr (kStates) ss_store<REV, SS, G>(reinterpret_cast<SS *>(a.hs) + b * T, t0s[r] + g0, T, vh, Hg);
     }
-    if (MODE == kSsPlain || (MODE == kSsGrad && a.y)) ss_store<REV, E, K>(a.y + b * T, t0s[r], T, vec, O);
+    if (MODE == kSsPlain || MODE == kSsStatesY || (MODE == kSsGrad && a.y))
+      ss_store<REV, E, K>(a.y + b * T, t0s[r], T, vec, O);
   }
   if constexpr (MODE == kSsGrad) {
     // the wave's sums, in a fixed order, one partial per (row, tile, wave)
@@ -1034,12 +1036,13 @@ __global__ __launch_bounds__(kSsReduceThreads) void ss_grad_finish_kernel(
 }
 
 // ------------------------------------------------------ zero-phase filter backward
-// dL/dx of y = filtfilt(fb, fa, x), a map linear in x, over the padded row
-// ext of N = T + 2e samples: pass 1 runs the TDF-II model from z ext[0] over
-// ext, pass 2 the same model from z y1[N-1] over the reversed y1, and y is
-// pass 2's output at the T interior samples.  The adjoint model (DF-II of
-// the same b and a: A^T = companion(a), input vector e0, output vector g,
-// d = b0) runs twice, each time in the opposite direction of its pass:
+// Gradients of y = filtfilt(fb, fa, x) over the padded row ext of N = T + 2e
+// samples: pass 1 runs the TDF-II model (A = companion(a)^T, g, c = e0,
+// d = b0) from h1[0] = z ext[0] over ext, pass 2 the same model from z
+// y1[N-1] over the reversed y1, and y is pass 2's output at the T interior
+// samples.  The adjoint model (DF-II of the same b and a: A^T =
+// companion(a), input vector e0, output vector g, d = b0) runs twice, each
+// time in the opposite direction of its pass:
 //  * pass 2's adjoint in ascending time over the upstream gradient padded
 //    with zeros: its state stays zero through the front pad; the interior is
 //    an ss_kernel launch from a zero state (dL/dy1 there, state lambda_A);
@@ -1051,13 +1054,21 @@ __global__ __launch_bounds__(kSsReduceThreads) void ss_grad_finish_kernel(
 //    interior an ss_kernel launch in reversed time (dL/dx there, state
 //    lambda_B); the front pad continues from lambda_B with a zero input
 //    (dL/dy1 is zero there: pass 2's adjoint state is) (dL/dext there); its
-//    final state dL/dh1[0] adds z . dL/dh1[0] to dL/dext[0] (h1[0] = z
-//    ext[0]);
+//    final state dL/dh1[0] adds z . dL/dh1[0] to dL/dext[0];
 //  * dL/dext of the pads folds into dL/dx through the pad's index map (the
 //    adjoint of F.pad; constant pads hold no x).
+// With coefficient gradients every step n of either pass also adds, with
+// lambda the adjoint state before the step (dL/d of the state after it), h
+// the forward state before it, u its input and gy its upstream gradient,
+//     dL/dA += lambda h^T,  dL/dg += lambda u,  dL/db0 += gy u
+// (the interiors in the ss_kernel launches' gradient mode, the pads here,
+// from the forward states the two passes take through them), the initial
+// states add dL/dz = dL/dh1[0] ext[0] + dL/dh2[0] y1[N-1], and z = (I -
+// A)^-1 g adds w z^T to dL/dA and w to dL/dg, w = (I - A)^-T dL/dz; the
+// filter chain rule maps (A, g, b0) to dL/dfb, dL/dfa.
 // The pad pieces run serially per row in double, one thread per row:
-// ff_bwd_edge_kernel between the two launches, ff_bwd_fold_kernel after
-// them, e steps each (as the forward's entry states).
+// ff_bwd_edge_kernel between the two adjoint launches, ff_bwd_fold_kernel
+// after them, a few passes of e steps each (as the forward's entry states).
 template <typename E>
 struct FfBwdArgs {
   const E *fb, *fa;
@@ -1071,6 +1082,15 @@ struct FfBwdArgs {
   E *entry;        // [B, M] pass 1's adjoint state entering the interior
   const E *lam_b;  // [B, M] pass 1's adjoint state after the interior
   E *gx;           // [B, T]
+  // coefficient gradients (coef != 0)
+  int coef;
+  const E *x;        // [B, T]
+  const E *y1;       // [B, T] pass 1's output over the interior
+  const E *zf1;      // [B, M] pass 1's state after the interior
+  double *work;      // [B, e, 2M + 1] forward states and outputs over a pad
+  double *gz;        // [B, M] dL/dz of the edge kernel's part
+  double *rowsum1;   // [B, kN] pass 1's interior sums (ss_grad_rows_kernel), the total on exit
+  double *rowsum2;   // [B, kN] pass 2's interior sums, the back pad's added by the edge kernel
 };
 
 // One step of the adjoint model from state s with input u; returns the
@@ -1089,6 +1109,15 @@ __device__ __forceinline__ double ff_adj_step(const FfModel<M> &f, double (&s)[M
   return o;
 }
 
+// One step of the TDF-II model: h' = A h + g u (A = companion(a)^T; the
+// ascending i reads h[i+1] before it changes).
+template <int M>
+__device__ __forceinline__ void ff_fwd_step(const FfModel<M> &f, double (&h)[M], double u) {
+  const double h0 = h[0];
+#pragma unroll
+  for (int i = 0; i < M; ++i) h[i] = -f.am[i] * h0 + (i + 1 < M ? h[i + 1] : 0.0) + f.g[i] * u;
+}
+
 template <int M>
 __device__ __forceinline__ double ff_dot_z(const FfModel<M> &f, const double (&s)[M]) {
   double c = 0.0;
@@ -1097,71 +1126,184 @@ __device__ __forceinline__ double ff_dot_z(const FfModel<M> &f, const double (&s
   return c;
 }
 
-// Between the launches: pass 2's adjoint over the back pad and its edge
-// term, then pass 1's adjoint over the back pad (its dL/dext, in place of
-// the dL/dy1 it consumes) up to the interior's entry state.  With no pad the
-// edge term lands on the interior's last dL/dy1.
+// The model's gradient sums of one step (the SsGrad layout: A row-major, g,
+// c (unused: c is e0), b0).
+template <int M>
+struct FfSums {
+  static constexpr int kB = M * M, kD = M * M + 2 * M, kN = M * M + 2 * M + 1;
+  double v[kN];
+  __device__ __forceinline__ void step(const double (&lam)[M], const double *h, double u, double gy) {
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+#pragma unroll
+      for (int j = 0; j < M; ++j) v[i * M + j] += lam[i] * h[j];
+      v[kB + i] += lam[i] * u;
+    }
+    v[kD] += gy * u;
+  }
+};
+
+// Between the adjoint launches: pass 2's adjoint over the back pad and its
+// edge term, then pass 1's adjoint over the back pad (its dL/dext, in place
+// of the dL/dy1 it consumes) up to the interior's entry state.  With no pad
+// the edge term lands on the interior's last dL/dy1.  With coefficient
+// gradients, first the forward states of both passes over the back pad
+// (pass 1 from zf1 over the pad's samples, pass 2 from z y1[N-1] back over
+// pass 1's outputs there), then both adjoints' sums over it, added to
+// rowsum2, and pass 2's part of dL/dz.
 template <typename E, int M>
 __global__ __launch_bounds__(64) void ff_bwd_edge_kernel(FfBwdArgs<E> a) {
   const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (b >= a.B) return;
   const FfModel<M> f = ff_model<M>(a.fb + b * a.f_stride_b, a.nb, a.fa + b * a.f_stride_a, a.na);
+  const int64_t T = a.T, e = a.e;
+  const bool coef = a.coef != 0;
+  const E *xr = coef ? a.x + b * T : nullptr;
+  double *const wk = coef ? a.work + b * e * (2 * M + 1) : nullptr;
+  double *const h1b = wk;                          // [e][M] pass 1's states
+  double *const h2b = coef ? wk + e * M : nullptr;  // [e][M] pass 2's states
+  double *const y1b = coef ? wk + 2 * e * M : nullptr;  // [e] pass 1's outputs
+  double ylast = 0.0;
+  if (coef) {
+    double h[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) h[i] = double(a.zf1[b * M + i]);
+    for (int64_t j = 0; j < e; ++j) {
+      const double u = double(pad_back(xr, T, a.pad_mode, j));
+#pragma unroll
+      for (int i = 0; i < M; ++i) h1b[j * M + i] = h[i];
+      y1b[j] = h[0] + f.b0 * u;
+      ff_fwd_step(f, h, u);
+    }
+    ylast = e > 0 ? y1b[e - 1] : double(a.y1[b * T + T - 1]);
+#pragma unroll
+    for (int i = 0; i < M; ++i) h[i] = f.z[i] * ylast;
+    for (int64_t j = e - 1; j >= 0; --j) {
+#pragma unroll
+      for (int i = 0; i < M; ++i) h2b[j * M + i] = h[i];
+      ff_fwd_step(f, h, y1b[j]);
+    }
+  }
+  FfSums<M> acc;
+#pragma unroll
+  for (int k = 0; k < FfSums<M>::kN; ++k) acc.v[k] = 0.0;
   double s[M], r[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) {
     s[i] = double(a.lam_a[b * M + i]);
     r[i] = 0.0;
   }
-  double *u = a.edge + b * a.e;
-  for (int64_t j = 0; j < a.e; ++j) u[j] = ff_adj_step(f, s, 0.0);
+  double *u = a.edge + b * e;
+  for (int64_t j = 0; j < e; ++j) {
+    if (coef) acc.step(s, h2b + j * M, y1b[j], 0.0);
+    u[j] = ff_adj_step(f, s, 0.0);
+  }
   const double c = ff_dot_z(f, s);
-  if (a.e > 0) {
-    u[a.e - 1] += c;
+  if (e > 0) {
+    u[e - 1] += c;
   } else {
-    E *p = a.gy1 + b * a.T + (a.T - 1);
+    E *p = a.gy1 + b * T + (T - 1);
     *p = E(double(*p) + c);
   }
-  for (int64_t j = a.e - 1; j >= 0; --j) u[j] = ff_adj_step(f, r, u[j]);
+  for (int64_t j = e - 1; j >= 0; --j) {
+    if (coef) acc.step(r, h1b + j * M, double(pad_back(xr, T, a.pad_mode, j)), u[j]);
+    u[j] = ff_adj_step(f, r, u[j]);
+  }
 #pragma unroll
   for (int i = 0; i < M; ++i) a.entry[b * M + i] = E(r[i]);
+  if (coef) {
+    double *rs = a.rowsum2 + b * FfSums<M>::kN;
+#pragma unroll
+    for (int k = 0; k < FfSums<M>::kN; ++k) rs[k] += acc.v[k];
+#pragma unroll
+    for (int i = 0; i < M; ++i) a.gz[b * M + i] = s[i] * ylast;
+  }
 }
 
-// After the launches: pass 1's adjoint over the front pad from lambda_B and
-// its edge term, then both pads' dL/dext folded into dL/dx (serial per row,
-// so pads that map onto one sample add up in order).
+// After the adjoint launches: pass 1's adjoint over the front pad from
+// lambda_B and its edge term, then both pads' dL/dext folded into dL/dx
+// (serial per row, so pads that map onto one sample add up in order).  With
+// coefficient gradients also pass 1's forward states over the front pad
+// (from z ext[0]), the adjoint's sums over it, dL/dz through z = (I -
+// A)^-1 g, and the row's total: rowsum1 += rowsum2 + the front pad's sums +
+// the steady state's.
 template <typename E, int M>
 __global__ __launch_bounds__(64) void ff_bwd_fold_kernel(FfBwdArgs<E> a) {
   const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (b >= a.B) return;
   const FfModel<M> f = ff_model<M>(a.fb + b * a.f_stride_b, a.nb, a.fa + b * a.f_stride_a, a.na);
   const int64_t T = a.T, e = a.e;
+  const bool coef = a.coef != 0;
+  const bool to_x = e == 0 || a.pad_mode != kPadConstant;  // pads that hold samples of x
+  const bool refl = a.pad_mode == kPadReflect, repl = a.pad_mode == kPadReplicate;
   E *gx = a.gx + b * T;
+  const E *xr = coef ? a.x + b * T : nullptr;
   const double *ub = a.edge + b * e;
+  double *h1f = coef ? a.work + b * e * (2 * M + 1) : nullptr;  // [e][M] pass 1's states over the front pad
+  double ext0 = 0.0;
+  if (coef) {
+    ext0 = double(e > 0 ? pad_front(xr, T, e, a.pad_mode, 0) : xr[0]);
+    double h[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) h[i] = f.z[i] * ext0;
+    for (int64_t n = 0; n < e; ++n) {
+#pragma unroll
+      for (int i = 0; i < M; ++i) h1f[n * M + i] = h[i];
+      ff_fwd_step(f, h, double(pad_front(xr, T, e, a.pad_mode, n)));
+    }
+  }
+  FfSums<M> acc;
+#pragma unroll
+  for (int k = 0; k < FfSums<M>::kN; ++k) acc.v[k] = 0.0;
   double r[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) r[i] = double(a.lam_b[b * M + i]);
   auto add = [&](int64_t i, double v) { gx[i] = E(double(gx[i]) + v); };
-  if (e == 0) {  // ext is x
-    add(0, ff_dot_z(f, r));
-    return;
-  }
-  if (a.pad_mode == kPadConstant) return;
-  if (a.pad_mode == kPadReplicate) {
-    double sf = 0.0, sb = 0.0;
-    for (int64_t n = e - 1; n >= 0; --n) sf += ff_adj_step(f, r, 0.0);
-    sf += ff_dot_z(f, r);
-    for (int64_t j = 0; j < e; ++j) sb += ub[j];
-    add(0, sf);
-    add(T - 1, sb);
-    return;
-  }
-  const bool refl = a.pad_mode == kPadReflect;
-  for (int64_t n = e - 1; n >= 0; --n) {  // ext[n] is x[e - n] (reflect) or x[T - e + n]
+  double sf = 0.0, sb = 0.0;  // replicate: everything lands on x[0] and x[T - 1]
+  for (int64_t n = e - 1; n >= 0; --n) {  // ext[n] is x[0], x[e - n] (reflect) or x[T - e + n]
+    if (coef) acc.step(r, h1f + n * M, double(pad_front(xr, T, e, a.pad_mode, n)), 0.0);
     double o = ff_adj_step(f, r, 0.0);
     if (n == 0) o += ff_dot_z(f, r);
-    add(refl ? e - n : T - e + n, o);
+    if (repl)
+      sf += o;
+    else if (to_x)
+      add(refl ? e - n : T - e + n, o);
   }
-  for (int64_t j = 0; j < e; ++j) add(refl ? T - 2 - j : j, ub[j]);  // ext[T + e + j]
+  if (e == 0) add(0, ff_dot_z(f, r));  // ext is x
+  for (int64_t j = 0; j < e; ++j) {  // ext[T + e + j]
+    if (repl)
+      sb += ub[j];
+    else if (to_x)
+      add(refl ? T - 2 - j : j, ub[j]);
+  }
+  if (repl && e > 0) {
+    add(0, sf);
+    add(T - 1, sb);
+  }
+  if (!coef) return;
+  // dL/dz, then w = (I - companion(a))^-1 dL/dz: rows 1.. give w_i = w_0 +
+  // p_i with p_i = sum_{k=1..i} gz_k, row 0 w_0 (1 + sum a) = gz_0 - sum a_i p_i
+  double gz[M], p[M], w[M];
+  double sa = 1.0, ap = 0.0;
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    gz[i] = a.gz[b * M + i] + r[i] * ext0;
+    p[i] = i == 0 ? 0.0 : p[i - 1] + gz[i];
+    sa += f.am[i];
+    ap += f.am[i] * p[i];
+  }
+  const double w0 = (gz[0] - ap) / sa;
+#pragma unroll
+  for (int i = 0; i < M; ++i) {
+    w[i] = w0 + p[i];
+#pragma unroll
+    for (int j = 0; j < M; ++j) acc.v[i * M + j] += w[i] * f.z[j];
+    acc.v[FfSums<M>::kB + i] += w[i];
+  }
+  double *rs = a.rowsum1 + b * FfSums<M>::kN;
+  const double *r2 = a.rowsum2 + b * FfSums<M>::kN;
+#pragma unroll
+  for (int k = 0; k < FfSums<M>::kN; ++k) rs[k] += r2[k] + acc.v[k];
 }
 
 }  // namespace phs

@@ -576,8 +576,7 @@ std::vector<Tensor> biquad_backward_hip(const Tensor &b, const Tensor &a, const 
 // Zero-phase filter of order 4 at most (phs_filtfilt_fwd;
 // philtorch/lti/filtering.py:413-484): b (nb,) or (batch, nb), nb <= 5; a
 // (na,) or (batch, na), the denominator after its leading 1, na <= 4;
-// padmode a phs_padmode code.  Its input gradient is filtfilt_backward
-// below (the coefficients' gradients take the composed lfilter route).
+// padmode a phs_padmode code.  Its gradients are filtfilt_backward below.
 void filtfilt_check(const char *op, const Tensor &b, const Tensor &a, const Tensor &x, int64_t padmode,
                     int64_t padlen) {
   TORCH_CHECK(x.dim() == 2, op, ": x must be a 2D tensor (batch, time)");
@@ -616,26 +615,36 @@ Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t p
   return y;
 }
 
-// dL/dx of filtfilt (phs_filtfilt_bwd): grad_y (batch, time), b and a as
-// filtfilt's.  The map is linear in x, so x itself is not needed.
-Tensor filtfilt_backward_hip(const Tensor &b, const Tensor &a, const Tensor &grad_y, int64_t padmode,
-                             int64_t padlen) {
+// Gradients of filtfilt (phs_filtfilt_bwd): [grad_x, grad_b, grad_a] for
+// grad_y (batch, time), b, a and x as filtfilt's; grad_b and grad_a are
+// empty unless need_coef (x is read only then: the map is linear in x).
+std::vector<Tensor> filtfilt_backward_hip(const Tensor &b, const Tensor &a, const Tensor &x, const Tensor &grad_y,
+                                          int64_t padmode, int64_t padlen, bool need_coef) {
   filtfilt_check("philtorch::filtfilt_backward", b, a, grad_y, padmode, padlen);
+  TORCH_CHECK(x.sizes() == grad_y.sizes() && x.scalar_type() == grad_y.scalar_type() &&
+                  x.device() == grad_y.device(),
+              "philtorch::filtfilt_backward: x and grad_y must have the same shape, type and device");
   const int64_t B = grad_y.size(0), T = grad_y.size(1), nb = b.size(-1), na = a.size(-1);
+  const int M = int(std::max(nb - 1, na));
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(grad_y.device());
   const int dt = phs_dtype_of(grad_y.scalar_type());
   Tensor bc = b.contiguous(), ac = a.contiguous(), gy = grad_y.contiguous();
+  Tensor xc = need_coef ? x.contiguous() : x;
   Tensor gx = at::empty_like(gy, at::MemoryFormat::Contiguous);
-  if (B == 0) return gx;
-  Tensor scratch =
-      at::empty({int64_t(phs_filtfilt_bwd_scratch_size(dt, B, T, padlen))}, gy.options().dtype(at::kByte));
+  Tensor gb = need_coef ? at::empty_like(bc) : at::empty({0}, b.options());
+  Tensor ga = need_coef ? at::empty_like(ac) : at::empty({0}, a.options());
+  if (B == 0) return {gx, gb, ga};
+  Tensor scratch = at::empty({int64_t(phs_filtfilt_bwd_scratch_size(dt, M, B, T, padlen, need_coef ? 1 : 0))},
+                             gy.options().dtype(at::kByte));
   void *stream = stream_of(gy);
   const Workspace ws = workspace_for(gy, phs_filtfilt_workspace_size(dt, B, T), stream);
   check_status(phs_filtfilt_bwd(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
-                                b.dim() == 1 ? 1 : 0, int(padmode), padlen, gy.const_data_ptr(), gx.mutable_data_ptr(),
-                                scratch.mutable_data_ptr(), size_t(scratch.numel()), ws.ptr, ws.bytes, stream),
+                                b.dim() == 1 ? 1 : 0, int(padmode), padlen, need_coef ? xc.const_data_ptr() : nullptr,
+                                gy.const_data_ptr(), gx.mutable_data_ptr(), need_coef ? gb.mutable_data_ptr() : nullptr,
+                                need_coef ? ga.mutable_data_ptr() : nullptr, scratch.mutable_data_ptr(),
+                                size_t(scratch.numel()), ws.ptr, ws.bytes, stream),
                "filtfilt_backward");
-  return gx;
+  return {gx, gb, ga};
 }
 
 // Single-input single-output LTI state space of order <= 4, fused
@@ -1186,7 +1195,8 @@ TORCH_LIBRARY(philtorch, m) {
         {at::Tag::pt2_compliant_tag});
   // new: zero-phase filtering, filters of second order at most (forward only)
   m.def("filtfilt(Tensor b, Tensor a, Tensor x, int padmode, int padlen) -> Tensor", {at::Tag::pt2_compliant_tag});
-  m.def("filtfilt_backward(Tensor b, Tensor a, Tensor grad_y, int padmode, int padlen) -> Tensor",
+  m.def("filtfilt_backward(Tensor b, Tensor a, Tensor x, Tensor grad_y, int padmode, int padlen, bool need_coef) "
+        "-> Tensor[]",
         {at::Tag::pt2_compliant_tag});
   // new: single-input single-output LTI state space of order <= 4, fused: (y, zf)
   m.def("lti_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx, bool reverse=False) -> (Tensor, Tensor)",

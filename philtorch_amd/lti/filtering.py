@@ -203,12 +203,11 @@ _PAD_CODES = {"constant": 0, "replicate": 1, "reflect": 2, "circular": 3}
 
 def _fused_filtfilt_applies(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[str], form: str, kwargs) -> bool:
     """A filter of order 4 at most on a HIP device with the native route
-    requested (``unroll_factor=1``) and no gradient wanted for b or a:
-    philtorch::filtfilt runs both passes with the padding, the flips and the
-    trim folded in, and its input gradient philtorch::filtfilt_backward the
-    two adjoint passes.  Its output is the same for the ``tdf2`` and ``df2``
-    forms (each pass starts from the steady state of the same transfer
-    function)."""
+    requested (``unroll_factor=1``): philtorch::filtfilt runs both passes
+    with the padding, the flips and the trim folded in, and its gradients
+    (x, b, a) philtorch::filtfilt_backward.  Its output is the same for the
+    ``tdf2`` and ``df2`` forms (each pass starts from the steady state of the
+    same transfer function)."""
     from .. import EXTENSION_LOADED
 
     if not (EXTENSION_LOADED and x.is_cuda and form in ("tdf2", "df2") and set(kwargs) == {"unroll_factor"}
@@ -226,13 +225,32 @@ def _fused_filtfilt_applies(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[s
         return False
     if not hasattr(torch.ops.philtorch, "filtfilt"):
         return False
-    if torch.is_grad_enabled() and (b.requires_grad or a.requires_grad):
-        return False
-    if torch.is_grad_enabled() and x.requires_grad and not hasattr(torch.ops.philtorch, "filtfilt_backward"):
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (b, a, x)) and not hasattr(torch.ops.philtorch,
+                                                                                          "filtfilt_backward"):
         return False
     import torch.autograd.forward_ad as fwad
 
     return all(fwad.unpack_dual(t).tangent is None for t in (b, a, x))
+
+
+def _filtfilt_composed(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[str], edge: int, form: str = "tdf2",
+                       **kwargs) -> Tensor:
+    """The reference's filtfilt steps (philtorch/lti/filtering.py:462-484):
+    pad, lfilter_zi, an lfilter pass from zi * ext[:, :1], a second over the
+    flipped output from zi * y[:, -1:], the trim and the flip back (each pass
+    on the fused lfilter route where it applies)."""
+    if edge > 0 and padmode is not None:
+        ext = F.pad(x.view(-1, x.size(-1)), (edge, edge), mode=padmode)
+        if x.dim() == 1:
+            ext = ext.squeeze(0)
+    else:
+        ext = x
+    zi = lfilter_zi(a, b, transpose=(form == "tdf2"))
+    y, _ = lfilter(b, a, ext, zi=zi * ext[..., :1], form=form, **kwargs)
+    y, _ = lfilter(b, a, y.flip(-1), zi=zi * y[..., -1:], form=form, **kwargs)
+    if edge > 0:
+        y = y[..., edge:-edge]
+    return y.flip(-1)
 
 
 def _fused_filtfilt(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[str], edge: int) -> Tensor:
@@ -260,10 +278,9 @@ def filtfilt(
     HIP device with ``unroll_factor=1`` and no gradient wanted runs
     philtorch::filtfilt (two state-space passes, the second in reversed time,
     their entry states derived in the kernel: no padded copy, no flips and no
-    host synchronisation), also when x needs a gradient
-    (philtorch::filtfilt_backward); otherwise (b or a need one) the passes
-    are composed as in the reference, each pass on the fused lfilter
-    route."""
+    host synchronisation; gradients w.r.t. x, b and a through
+    philtorch::filtfilt_backward); otherwise the passes are composed as in
+    the reference, each pass on the fused lfilter route."""
     assert method in ("pad", "gust"), "Method must be either 'pad' or 'gust'."
     if method == "gust":
         raise NotImplementedError("Gustafsson's method is not implemented yet.")
@@ -274,18 +291,7 @@ def filtfilt(
     assert x.size(-1) > edge, f"Input signal length {x.size(-1)} must be greater than pad length {edge}."
     if _fused_filtfilt_applies(b, a, x, padmode, form, kwargs):
         return _fused_filtfilt(b, a, x, padmode, edge)
-    if edge > 0 and padmode is not None:
-        ext = F.pad(x.view(-1, x.size(-1)), (edge, edge), mode=padmode)
-        if x.dim() == 1:
-            ext = ext.squeeze(0)
-    else:
-        ext = x
-    zi = lfilter_zi(a, b, transpose=(form == "tdf2"))
-    y, _ = lfilter(b, a, ext, zi=zi * ext[..., :1], form=form, **kwargs)
-    y, _ = lfilter(b, a, y.flip(-1), zi=zi * y[..., -1:], form=form, **kwargs)
-    if edge > 0:
-        y = y[..., edge:-edge]
-    return y.flip(-1)
+    return _filtfilt_composed(b, a, x, padmode, edge, form, **kwargs)
 
 
 # sections per fused launch (the backward keeps every section's lane states in LDS)

@@ -103,12 +103,14 @@ def load() -> ctypes.CDLL:
                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                      ctypes.c_size_t, ctypes.c_void_p]
     lib.phs_filtfilt_fwd.restype = ctypes.c_int
-    lib.phs_filtfilt_bwd_scratch_size.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]
+    lib.phs_filtfilt_bwd_scratch_size.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                                  ctypes.c_int64, ctypes.c_int]
     lib.phs_filtfilt_bwd_scratch_size.restype = ctypes.c_size_t
     lib.phs_filtfilt_bwd.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
                                      ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
-                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
-                                     ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                     ctypes.c_size_t, ctypes.c_void_p]
     lib.phs_filtfilt_bwd.restype = ctypes.c_int
     # single-input single-output state space and lfilter of order <= 4
     lib.phs_lti_ss_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64]

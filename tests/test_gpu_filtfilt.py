@@ -15,14 +15,18 @@ million steps; shared and per-row coefficients; the forced look-back fallback
 of both passes; a constant row and linearity at the benchmark's C4 size.
 Through the torch API: scipy (orders 1-4), the composed route (each pass an
 lfilter) at the C4 size, the route choice, and gradients (which take the
-composed route when b or a need one).
+fused route too).
 
-The input gradient (phs_filtfilt_bwd, op philtorch::filtfilt_backward):
+The gradients (phs_filtfilt_bwd, op philtorch::filtfilt_backward): grad_x as
 J^T grad_y with J the oracle's filtfilt applied to unit impulses (exact, at
-small T, every pad mode, padlen 0 to T - 1), the adjoint identity
-<g, F x> = <F^T g, x> with F the oracle at rows of many tiles, the forced
-look-back fallback, the composed route's autograd (orders 1-4, every pad
-mode, 1D and 2D x, the C4 size), and gradcheck / gradgradcheck of the ops.
+small T, every pad mode, padlen 0 to T - 1) and the adjoint identity
+<g, F x> = <F^T g, x> with F the oracle at rows of many tiles; grad_b and
+grad_a against central differences of the oracle in fp64 (every pad mode,
+orders 1-4, shared and per-row filters, b one tap short, rows of one and
+two tiles); the forced look-back fallback; the composed route's autograd
+(orders 1-4, every pad mode, 1D and 2D x, x, b and a together and apart,
+and the C4 size against the composed route in fp64); gradcheck /
+gradgradcheck of the op.
 """
 import ctypes
 
@@ -156,30 +160,40 @@ def test_filtfilt_capi_forced_fallback(api, dtype, order):
     _check(y, b, a, x, "replicate", 9, dtype, "fallback")
 
 
-def _run_bwd(api, b, a, gy, padmode, padlen, spin_limit=0):
-    """phs_filtfilt_bwd through the C ABI (scratch and output prefilled with
-    NaN bytes: every value must be written before it is read); numpy grad_x."""
+def _run_bwd(api, b, a, gy, padmode, padlen, spin_limit=0, x=None):
+    """phs_filtfilt_bwd through the C ABI (scratch and outputs prefilled with
+    NaN bytes: every value must be written before it is read); numpy
+    grad_x, or (grad_x, grad_b, grad_a) when x is given."""
     import torch
 
     lib, ws, capi = api
     dt = capi.DTYPES[np.dtype(gy.dtype)]
     B, T = gy.shape
+    coef = x is not None
+    M = max(b.shape[-1] - 1, a.shape[-1])
     need = lib.phs_filtfilt_workspace_size(dt, B, T)
     assert 0 < need <= ws.numel()
-    sc = torch.full((lib.phs_filtfilt_bwd_scratch_size(dt, B, T, padlen),), 255, dtype=torch.uint8, device="cuda")
+    sc = torch.full((lib.phs_filtfilt_bwd_scratch_size(dt, M, B, T, padlen, int(coef)),), 255, dtype=torch.uint8,
+                    device="cuda")
     tb, ta, tg = _dev(b), _dev(a), _dev(gy)
+    tx = _dev(x) if coef else None
     gx = torch.full_like(tg, float("nan"))
-    print(f"filtfilt_bwd capi B={B} T={T} nb={b.shape[-1]} na={a.shape[-1]} {padmode} {padlen}", flush=True)
+    gb = torch.full_like(tb, float("nan")) if coef else None
+    ga = torch.full_like(ta, float("nan")) if coef else None
+    print(f"filtfilt_bwd capi B={B} T={T} nb={b.shape[-1]} na={a.shape[-1]} {padmode} {padlen} coef={coef}",
+          flush=True)
     lib.phs_debug_set_spin_limit(spin_limit)
     try:
         rc = lib.phs_filtfilt_bwd(dt, B, T, _p(tb), b.shape[-1], _p(ta), a.shape[-1], int(b.ndim == 1),
-                                  capi.PADMODES[padmode], padlen, _p(tg), _p(gx), _p(sc), sc.numel(), _p(ws), need,
-                                  _stream())
+                                  capi.PADMODES[padmode], padlen, _p(tx), _p(tg), _p(gx), _p(gb), _p(ga), _p(sc),
+                                  sc.numel(), _p(ws), need, _stream())
         assert rc == capi.PHS_OK, lib.phs_error_string(rc)
         torch.cuda.synchronize()
     finally:
         lib.phs_debug_set_spin_limit(0)
-    return gx.cpu().numpy()
+    if not coef:
+        return gx.cpu().numpy()
+    return gx.cpu().numpy(), gb.cpu().numpy(), ga.cpu().numpy()
 
 
 def _oracle_jt(b, a, T, padmode, padlen):
@@ -234,6 +248,55 @@ def test_filtfilt_bwd_capi_adjoint_identity(api, dtype, order, B, T):
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
 @pytest.mark.parametrize("order", ORDERS)
+@pytest.mark.parametrize("padmode", MODES)
+def test_filtfilt_bwd_capi_coef_vs_oracle_fd(api, dtype, order, padmode):
+    """dL/db . V and dL/da . V for L = <grad_y, filtfilt(b, a, x)> against
+    the central difference of the oracle's filtfilt in fp64 (random
+    directions V), shared and per-row filters, b one tap short, padlen 0, 1,
+    9 and T - 1, a row shorter than a tile and one of two tiles; grad_x
+    against the oracle's Jacobian as above."""
+    f64 = lambda v: np.asarray(v, np.float64)  # noqa: E731
+    tile = 6144 if dtype == np.float32 else 3072
+    for B, T in ((3, 40), (2, tile + 9)):
+        for shared, short in ((True, False), (False, False), (False, True)):
+            g = D.rng(D.seed_of("filtfilt-bwd-coef", dtype, order, padmode, T, shared, short))
+            # poles within radius 0.9: nearer the circle, central differences lose the digits to pin with
+            b, a = D.ba_coefs(g, () if shared else (B,), order, dtype, rhi=0.9)
+            x = D.normal(g, (B, T), dtype)
+            if short:
+                b = np.ascontiguousarray(b[..., :-1])
+            gy = D.normal(g, (B, T), dtype)
+            for padlen in sorted({0, 1, 9, T - 1}):
+                gx, gb, ga = _run_bwd(api, b, a, gy, padmode, padlen, x=x)
+                assert np.isfinite(gb).all() and np.isfinite(ga).all()
+
+                def loss(bv, av):
+                    return float(np.sum(f64(gy) * oracle.filtfilt_ba(bv, av, f64(x), padmode=padmode, padlen=padlen)))
+
+                for which, grad in (("b", gb), ("a", ga)):
+                    V = g.standard_normal(grad.shape)
+                    if which == "b":
+                        L = lambda t: loss(f64(b) + t * V, f64(a))  # noqa: E731
+                    else:
+                        L = lambda t: loss(f64(b), f64(a) + t * V)  # noqa: E731
+                    eps = 1e-5  # fourth-order stencil: truncation ~eps^4, rounding ~1e-16 |L| / eps
+                    fd = (8 * (L(eps) - L(-eps)) - (L(2 * eps) - L(-2 * eps))) / (12 * eps)
+                    got = float(np.sum(f64(grad) * V))
+                    # the scale of the directional sum (its terms cancel where the loss's do)
+                    scale = max(1.0, abs(fd), float(np.sum(np.abs(f64(grad) * V))))
+                    rtol = 2e-4 if dtype == np.float32 else 1e-7
+                    assert abs(got - fd) <= rtol * scale, (which, B, T, shared, short, padlen, got, fd, scale)
+                if T <= 64:
+                    ref = np.stack([_oracle_jt(f64(b if shared else b[r]), f64(a if shared else a[r]), T, padmode,
+                                               padlen) @ f64(gy[r]) for r in range(B)])
+                    D.check(gx, ref, f"grad x B={B} T={T} padlen={padlen}", dtype=dtype)
+                else:
+                    D.check(gx, _run_bwd(api, b, a, gy, padmode, padlen), "grad x with and without coefficients",
+                            dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("order", ORDERS)
 def test_filtfilt_bwd_capi_forced_fallback(api, dtype, order):
     """A one-poll budget: the tiles of both adjoint passes compute their
     entry states from the row's prefix (pass 2's adjoint) or suffix (pass 1's)
@@ -243,6 +306,11 @@ def test_filtfilt_bwd_capi_forced_fallback(api, dtype, order):
     ref = _run_bwd(api, b, a, gy, "reflect", 9)
     got = _run_bwd(api, b, a, gy, "reflect", 9, spin_limit=1)
     D.check(got, ref, "fallback", dtype=dtype)
+    x = D.normal(D.rng(D.seed_of("filtfilt-bwd-fallback-x", dtype)), (3, 40000), dtype)
+    ref = _run_bwd(api, b, a, gy, "replicate", 9, x=x)
+    got = _run_bwd(api, b, a, gy, "replicate", 9, spin_limit=1, x=x)
+    for gg, rr, nm in zip(got, ref, ("x", "b", "a")):
+        D.check(gg, rr, f"fallback with coefficients, grad {nm}", dtype=dtype)
 
 
 @pytest.mark.parametrize("order", [2, 4])
@@ -299,13 +367,10 @@ def test_filtfilt_route_choice(hip):
     assert filtering._fused_filtfilt_applies(torch.ones(3, 5, device="cuda"), a, x, "replicate", "tdf2", ok)
     assert not filtering._fused_filtfilt_applies(torch.ones(3, 6, device="cuda"), a, x, "replicate", "tdf2", ok)
     assert not filtering._fused_filtfilt_applies(b, torch.ones(3, 5, device="cuda"), x, "replicate", "tdf2", ok)
-    # an input gradient runs philtorch::filtfilt_backward; coefficient gradients the composed route
+    # gradients w.r.t. x, b and a run philtorch::filtfilt_backward
     assert filtering._fused_filtfilt_applies(b, a, x.requires_grad_(), "replicate", "tdf2", ok)
-    bg = b.clone().requires_grad_()
-    assert not filtering._fused_filtfilt_applies(bg, a, x, "replicate", "tdf2", ok)
-    assert not filtering._fused_filtfilt_applies(b, a.clone().requires_grad_(), x, "replicate", "tdf2", ok)
-    with torch.no_grad():
-        assert filtering._fused_filtfilt_applies(bg, a, x, "replicate", "tdf2", ok)
+    assert filtering._fused_filtfilt_applies(b.clone().requires_grad_(), a, x, "replicate", "tdf2", ok)
+    assert filtering._fused_filtfilt_applies(b, a.clone().requires_grad_(), x, "replicate", "tdf2", ok)
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
@@ -339,9 +404,10 @@ def test_filtfilt_api_matches_scipy(hip, dtype):
 
 def test_filtfilt_api_c4_size_matches_composed_route(hip, monkeypatch):
     """The benchmark's filtfilt pattern at the C4 size (B=16, T=480000, fp32,
-    one filtfilt per section, padmode replicate, padlen 9), output and input
-    gradient: the fused route against the composed one (padding, two lfilter
-    passes, flips, and their autograd)."""
+    one filtfilt per section, padmode replicate, padlen 9), output and the
+    gradients w.r.t. x and every section's b and a: the fused route against
+    the composed one (padding, lfilter_zi, two lfilter passes, flips, and
+    their autograd) run in fp64 on the same fp32 values."""
     import torch
 
     from philtorch_amd.lti import filtering
@@ -355,34 +421,28 @@ def test_filtfilt_api_c4_size_matches_composed_route(hip, monkeypatch):
     for fused in (True, False):
         if not fused:
             monkeypatch.setattr(filtering, "_fused_filtfilt_applies", lambda *a, **k: False)
-        xr = x.clone().requires_grad_(True)
+        dt = torch.float32 if fused else torch.float64
+        xr = x.to(dt).requires_grad_(True)
+        sr = sos.to(dt).requires_grad_(True)
         y = xr
         for s in range(S):
-            y = hip.lti.filtfilt(sos[:, s, :3], sos[:, s, 4:], y, padmode="replicate", padlen=9, unroll_factor=1)
-        (gx,) = torch.autograd.grad(y, xr, gy)
-        outs.append((y.detach().cpu().numpy(), gx.cpu().numpy()))
-    D.check(outs[0][0], outs[1][0], "8 filtfilts")
-    D.check(outs[0][1], outs[1][1], "8 filtfilts, grad x")
-
-
-def test_filtfilt_api_gradients_take_composed_route(hip):
-    import torch
-
-    g = D.rng(D.seed_of("filtfilt-grad"))
-    b, a = (torch.tensor(v, device="cuda", requires_grad=True) for v in _biquad(g, (2,), np.float64))
-    x = torch.tensor(g.standard_normal((2, 40)), device="cuda", requires_grad=True)
-    f = lambda b_, a_, x_: hip.lti.filtfilt(b_, a_, x_, padlen=5, unroll_factor=1)  # noqa: E731
-    assert torch.autograd.gradcheck(f, (b, a, x))
-    with torch.no_grad():
-        fused = f(b, a, x)
-    D.check(fused.cpu().numpy(), f(b, a, x).detach().cpu().numpy(), "no-grad vs grad route")
+            y = hip.lti.filtfilt(sr[:, s, :3], sr[:, s, 4:], y, padmode="replicate", padlen=9, unroll_factor=1)
+        gx, gs = torch.autograd.grad(y, (xr, sr), gy.to(dt))
+        outs.append((y.detach().cpu().numpy(), gx.cpu().numpy(), gs.cpu().numpy()))
+    D.check(outs[0][0], outs[1][0], "8 filtfilts", dtype=np.float32)
+    D.check(outs[0][1], outs[1][1], "8 filtfilts, grad x", dtype=np.float32)
+    for s in range(S):
+        for cols, nm in ((slice(0, 3), "b"), (slice(4, 6), "a")):
+            D.check(outs[0][2][:, s, cols], outs[1][2][:, s, cols], f"8 filtfilts, grad {nm} of section {s}",
+                    dtype=np.float32)
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
-def test_filtfilt_api_input_gradient_fused_vs_composed(hip, dtype, monkeypatch):
-    """lti.filtfilt with x requiring a gradient (b and a not) takes the fused
-    route both ways and matches the composed route's autograd (every pad
-    mode, orders 1-4, shared and per-row filters, 1D and 2D x)."""
+def test_filtfilt_api_gradients_fused_vs_composed(hip, dtype, monkeypatch):
+    """lti.filtfilt with gradients wanted for x, b and a (together and
+    apart) takes the fused route both ways and matches the composed
+    route's autograd (every pad mode, orders 1-4, shared and per-row
+    filters, 1D and 2D x)."""
     import torch
 
     from philtorch_amd.lti import filtering
@@ -395,28 +455,46 @@ def test_filtfilt_api_input_gradient_fused_vs_composed(hip, dtype, monkeypatch):
         b, a = D.ba_coefs(g, (shape[0],) if batched else (), order, dtype, rhi=0.98)
         x = g.standard_normal(shape).astype(dtype)
         gy = g.standard_normal(shape).astype(dtype)
-        tb, ta, tgy = (torch.tensor(v, device="cuda") for v in (b, a, gy))
-        for padmode, padlen in (("replicate", None), ("reflect", 100), ("constant", 7), ("circular", 31),
-                                (None, None)):
+        tgy = torch.tensor(gy, device="cuda")
+        for (padmode, padlen), want in zip((("replicate", None), ("reflect", 100), ("constant", 7),
+                                            ("circular", 31), (None, None)),
+                                           ((1, 1, 1), (0, 0, 1), (1, 0, 0), (0, 1, 1), (1, 1, 1))):
             res = []
             for fused in (True, False):
                 monkeypatch.setattr(filtering, "_fused_filtfilt_applies",
                                     (lambda *a_: taken.append(orig(*a_)) or taken[-1]) if fused
                                     else (lambda *a_, **k_: False))
-                tx = torch.tensor(x, device="cuda", requires_grad=True)
-                y = hip.lti.filtfilt(tb, ta, tx, padmode=padmode, padlen=padlen, unroll_factor=1)
+                ts = [torch.tensor(v, device="cuda", requires_grad=bool(w)) for v, w in zip((b, a, x), want)]
+                y = hip.lti.filtfilt(*ts, padmode=padmode, padlen=padlen, unroll_factor=1)
                 if fused:
                     assert taken[-1] is True
-                (gx,) = torch.autograd.grad(y, tx, tgy)
-                res.append((y.detach().cpu().numpy(), gx.cpu().numpy()))
-            nm = f"{shape} batched={batched} order={order} {padmode} {padlen}"
+                grads = torch.autograd.grad(y, [t for t in ts if t.requires_grad], tgy)
+                res.append((y.detach().cpu().numpy(), [gg.cpu().numpy() for gg in grads]))
+            nm = f"{shape} batched={batched} order={order} {padmode} {padlen} want={want}"
             D.check(res[0][0], res[1][0], nm, dtype=dtype)
-            D.check(res[0][1], res[1][1], nm + " grad x", dtype=dtype)
+            for gf, gc, wn in zip(res[0][1], res[1][1], [n for n, w in zip("bax", want) if w]):
+                D.check(gf, gc, f"{nm} grad {wn}", dtype=dtype)
+
+
+def test_filtfilt_api_gradcheck(hip):
+    """gradcheck of lti.filtfilt w.r.t. b, a and x (the fused route's
+    coefficient mode), and the output with and without gradients."""
+    import torch
+
+    g = D.rng(D.seed_of("filtfilt-grad"))
+    b, a = (torch.tensor(v, device="cuda", requires_grad=True) for v in _biquad(g, (2,), np.float64))
+    x = torch.tensor(g.standard_normal((2, 40)), device="cuda", requires_grad=True)
+    f = lambda b_, a_, x_: hip.lti.filtfilt(b_, a_, x_, padlen=5, unroll_factor=1)  # noqa: E731
+    assert torch.autograd.gradcheck(f, (b, a, x))
+    with torch.no_grad():
+        fused = f(b, a, x)
+    D.check(fused.cpu().numpy(), f(b, a, x).detach().cpu().numpy(), "no-grad vs grad route")
 
 
 def test_filtfilt_op_gradcheck(hip):
-    """First and second order through the ops (fp64): filtfilt's gradient is
-    filtfilt_backward, whose own is filtfilt."""
+    """First and second order through the op (fp64): w.r.t. x alone
+    (filtfilt_backward, whose own gradient is filtfilt) and w.r.t. b, a and
+    x (the coefficient mode; second order through the composed route)."""
     import torch
 
     g = D.rng(D.seed_of("filtfilt-gradcheck"))
@@ -424,14 +502,16 @@ def test_filtfilt_op_gradcheck(hip):
         b, a = (torch.tensor(v, device="cuda") for v in D.ba_coefs(g, (2,) if batched else (), order, np.float64,
                                                                      rhi=0.9))
         x = torch.tensor(g.standard_normal((2, 30)), device="cuda", requires_grad=True)
+        bg, ag = b.clone().requires_grad_(True), a.clone().requires_grad_(True)
         for mode, padlen in ((1, 5), (2, 7), (3, 4), (0, 3), (1, 0), (2, 29)):
             f = lambda x_: torch.ops.philtorch.filtfilt(b, a, x_, mode, padlen)  # noqa: E731
             assert torch.autograd.gradcheck(f, (x,))
             assert torch.autograd.gradgradcheck(f, (x,))
-    bg = b.clone().requires_grad_(True)
-    y = torch.ops.philtorch.filtfilt(bg, a, x, 1, 5)
-    with pytest.raises(RuntimeError, match="no gradient w.r.t. b and a"):
-        y.sum().backward()
+            f3 = lambda b_, a_, x_: torch.ops.philtorch.filtfilt(b_, a_, x_, mode, padlen)  # noqa: E731
+            assert torch.autograd.gradcheck(f3, (bg, ag, x))
+            assert torch.autograd.gradcheck(f3, (bg, a, x.detach()))
+        # second order runs the composed route, whose F.pad backward accumulates with atomics on the GPU
+        assert torch.autograd.gradgradcheck(f3, (bg, ag, x), nondet_tol=1e-12)
 
 
 def test_filtfilt_api_errors(hip):
@@ -463,9 +543,11 @@ def test_filtfilt_opcheck(hip):
     b4, a4 = (torch.tensor(v, device="cuda") for v in D.ba_coefs(g, (2,), 4, np.float32))
     torch.library.opcheck(torch.ops.philtorch.filtfilt.default, (b4, a4, x, 3, 15),
                           test_utils=("test_schema", "test_faketensor"))
-    for args in ((b, a, x, 1, 9), (b4, a4, x, 2, 15), (b4, a4, x, 0, 0)):
-        torch.library.opcheck(torch.ops.philtorch.filtfilt_backward.default, args,
-                              test_utils=("test_schema", "test_faketensor"))
-        torch.library.opcheck(torch.ops.philtorch.filtfilt.default, (args[0], args[1], x.clone().requires_grad_(),
-                                                                     args[3], args[4]),
+    for bb, aa, mode, padlen in ((b, a, 1, 9), (b4, a4, 2, 15), (b4, a4, 0, 0)):
+        for need_coef in (False, True):
+            torch.library.opcheck(torch.ops.philtorch.filtfilt_backward.default,
+                                  (bb, aa, x, x.flip(-1).contiguous(), mode, padlen, need_coef),
+                                  test_utils=("test_schema", "test_faketensor"))
+        torch.library.opcheck(torch.ops.philtorch.filtfilt.default,
+                              (bb.clone().requires_grad_(), aa, x.clone().requires_grad_(), mode, padlen),
                               test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))

@@ -277,22 +277,29 @@ def test_capi_filtfilt_host_only_calls():
 
 
 def test_capi_filtfilt_bwd_host_only_calls():
-    """Sizes and argument errors of the zero-phase filter's input gradient
+    """Sizes and argument errors of the zero-phase filter's gradients
     (nothing launches)."""
     lib = capi.load()
     for dt, esz in ((0, 4), (1, 8)):
         # dL/dy1 of the interior, three [B, 4] states, the back pad in double
-        need = lib.phs_filtfilt_bwd_scratch_size(dt, 16, 480000, 9)
+        need = lib.phs_filtfilt_bwd_scratch_size(dt, 2, 16, 480000, 9, 0)
         assert need >= 16 * 480000 * esz + 3 * 16 * 4 * esz + 16 * 9 * 8
-        assert lib.phs_filtfilt_bwd_scratch_size(dt, 16, 480000, 100) > need
-    for bad in ((2, 16, 100, 9), (0, -1, 100, 9), (0, 16, -1, 9), (0, 16, 100, -1)):
+        assert lib.phs_filtfilt_bwd_scratch_size(dt, 2, 16, 480000, 100, 0) > need
+        # coefficients: pass 1's output, both passes' states [B, T, M], the sums
+        coef = lib.phs_filtfilt_bwd_scratch_size(dt, 2, 16, 480000, 9, 1)
+        assert coef >= need + 16 * 480000 * esz * (1 + 2 * 2)
+        assert lib.phs_filtfilt_bwd_scratch_size(dt, 4, 16, 480000, 9, 1) > coef
+    for bad in ((2, 2, 16, 100, 9, 0), (0, 2, -1, 100, 9, 0), (0, 2, 16, -1, 9, 0), (0, 2, 16, 100, -1, 0),
+                (0, 0, 16, 100, 9, 0), (0, 5, 16, 100, 9, 1)):
         assert lib.phs_filtfilt_bwd_scratch_size(*bad) == 0
     d = ctypes.c_void_p(16)
     big = 1 << 30
     rep = capi.PADMODES["replicate"]
 
-    def call(dt=0, T=100, nb=3, na=2, mode=rep, padlen=9, sc=d, scb=big, wsb=big, B=2, b=d, gy=d, gx=d):
-        return lib.phs_filtfilt_bwd(dt, B, T, b, nb, d, na, 0, mode, padlen, gy, gx, sc, scb, d, wsb, None)
+    def call(dt=0, T=100, nb=3, na=2, mode=rep, padlen=9, sc=d, scb=big, wsb=big, B=2, b=d, gy=d, gx=d, x=d,
+             gb=None, ga=None):
+        return lib.phs_filtfilt_bwd(dt, B, T, b, nb, d, na, 0, mode, padlen, x, gy, gx, gb, ga, sc, scb, d, wsb,
+                                    None)
 
     assert call(dt=2) == capi.PHS_ERR_DTYPE
     assert call(padlen=100) == capi.PHS_ERR_INVALID
@@ -302,15 +309,19 @@ def test_capi_filtfilt_bwd_host_only_calls():
     assert call(nb=6) == capi.PHS_ERR_INVALID and call(na=0) == capi.PHS_ERR_INVALID
     assert call(b=None) == capi.PHS_ERR_INVALID and call(gy=None) == capi.PHS_ERR_INVALID
     assert call(gx=None) == capi.PHS_ERR_INVALID
+    assert call(gb=d) == capi.PHS_ERR_INVALID and call(ga=d) == capi.PHS_ERR_INVALID  # both or neither
+    assert call(gb=d, ga=d, x=None) == capi.PHS_ERR_INVALID  # coefficient gradients read x
     need_ws = lib.phs_filtfilt_workspace_size(0, 2, 100)
-    need_sc = lib.phs_filtfilt_bwd_scratch_size(0, 2, 100, 9)
     for nb, na in ((3, 2), (2, 1), (5, 4)):
+        M = max(nb - 1, na)
+        need_sc = lib.phs_filtfilt_bwd_scratch_size(0, M, 2, 100, 9, 0)
+        need_cf = lib.phs_filtfilt_bwd_scratch_size(0, M, 2, 100, 9, 1)
         assert call(wsb=need_ws - 1, nb=nb, na=na) == capi.PHS_ERR_WORKSPACE
         assert call(scb=need_sc - 1, nb=nb, na=na) == capi.PHS_ERR_WORKSPACE
+        assert call(scb=need_cf - 1, nb=nb, na=na, gb=d, ga=d) == capi.PHS_ERR_WORKSPACE
     assert call(sc=None) == capi.PHS_ERR_WORKSPACE
-    assert lib.phs_filtfilt_bwd(0, 0, 100, None, 3, None, 2, 0, rep, 9, None, None, None, 0, None, 0,
-                                None) == capi.PHS_OK
-
+    assert lib.phs_filtfilt_bwd(0, 0, 100, None, 3, None, 2, 0, rep, 9, None, None, None, None, None, None, 0,
+                                None, 0, None) == capi.PHS_OK
 
 def test_filtfilt_fused_route_not_taken_on_cpu():
     from philtorch_amd.lti import filtering
