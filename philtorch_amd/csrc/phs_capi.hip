@@ -62,7 +62,7 @@ const char *phs_error_string(int status) {
   }
 }
 
-int phs_abi_version(void) { return 109; }
+int phs_abi_version(void) { return 110; }
 
 void phs_debug_set_spin_limit(unsigned polls) { phs::g_spin_limit.store(polls, std::memory_order_relaxed); }
 

@@ -262,7 +262,8 @@ int ss_filtfilt(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e, co
 // double; with coefficient gradients also pass 1's output and final state,
 // both passes' interior states [B, T, M], the per-wave partial sums (one
 // buffer, used by each adjoint launch in turn), two [B, kN] row sums, dL/dz
-// [B, M] and the pads' forward states [B, padlen, 2M + 1] in double.
+// [B, M] and, for pads longer than kFfPadLds, the pads' working values
+// [B, padlen, 2M + 2] in double.
 template <class Alg>
 struct FfBwdLayout {
   size_t gy1 = 0, lam_a = 0, entry = 0, lam_b = 0, edge = 0;
@@ -292,7 +293,7 @@ FfBwdLayout<Alg> ff_bwd_layout(int64_t B, int64_t T, int64_t e, bool coef) {
   L.rowsum2 = L.rowsum1 + align_up(rows * N * sizeof(C));
   L.gz = L.rowsum2 + align_up(rows * N * sizeof(C));
   L.work = L.gz + align_up(rows * M * sizeof(double));
-  L.total = L.work + align_up(rows * size_t(e) * (2 * M + 1) * sizeof(double));
+  L.total = L.work + align_up(rows * size_t(e > kFfPadLds ? e : 0) * FfPad<M>::kW * sizeof(double));
   return L;
 }
 
@@ -346,7 +347,8 @@ int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e
   k.lam_b = lam_b;
   k.gx = static_cast<E *>(gx);
   const int64_t tiles = (T + SsShape<Alg>::kTile - 1) / SsShape<Alg>::kTile;
-  const dim3 grid(unsigned((B + 63) / 64));
+  const dim3 grid(unsigned((B + kFfRows - 1) / kFfRows));
+  const bool lds = e <= kFfPadLds;
   SsFilter adj = f;
   adj.form = 2;
   SsArgs<Alg> p{};
@@ -407,7 +409,10 @@ int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e
   } else if ((rc = ss_launch<Alg, false>(p, stream)) != PHS_OK) {
     return rc;
   }
-  hipLaunchKernelGGL((ff_bwd_edge_kernel<E, M>), grid, dim3(64), 0, stream, k);
+  if (lds)
+    hipLaunchKernelGGL((ff_bwd_edge_kernel<E, M, kFfPadLds>), grid, dim3(kFfRows), 0, stream, k);
+  else
+    hipLaunchKernelGGL((ff_bwd_edge_kernel<E, M, 0>), grid, dim3(kFfRows), 0, stream, k);
   // pass 1's adjoint over the interior (descending time)
   p = SsArgs<Alg>{};
   if (!ss_args<Alg>(B, T, adj, entry, gy1, gx, lam_b, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
@@ -422,7 +427,10 @@ int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e
   } else if ((rc = ss_launch<Alg, true>(p, stream)) != PHS_OK) {
     return rc;
   }
-  hipLaunchKernelGGL((ff_bwd_fold_kernel<E, M>), grid, dim3(64), 0, stream, k);
+  if (lds)
+    hipLaunchKernelGGL((ff_bwd_fold_kernel<E, M, kFfPadLds>), grid, dim3(kFfRows), 0, stream, k);
+  else
+    hipLaunchKernelGGL((ff_bwd_fold_kernel<E, M, 0>), grid, dim3(kFfRows), 0, stream, k);
   if (coef) {
     SsGradOut<E> out{};
     out.form = 1;

@@ -659,7 +659,9 @@ struct SsGrad {
 
 // Steps per group of state loads and stores: at most 64 bytes of states
 // and whole 16-byte vectors of states and inputs (bounds the registers a
-// K-step chunk of order-4 states would take).
+// K-step chunk of order-4 states would take).  A 32-byte group in the
+// gradient mode removed the order-2 fp32 reversed adjoint's 9 spilled
+// registers but measured no faster there and 6% slower forward.
 template <class Alg>
 constexpr int ss_state_group() {
   constexpr int K = SsShape<Alg>::K;
@@ -1087,7 +1089,7 @@ struct FfBwdArgs {
   const E *x;        // [B, T]
   const E *y1;       // [B, T] pass 1's output over the interior
   const E *zf1;      // [B, M] pass 1's state after the interior
-  double *work;      // [B, e, 2M + 1] forward states and outputs over a pad
+  double *work;      // [B, e, 2M + 2] the pad steps' working values (pads longer than kFfPadLds)
   double *gz;        // [B, M] dL/dz of the edge kernel's part
   double *rowsum1;   // [B, kN] pass 1's interior sums (ss_grad_rows_kernel), the total on exit
   double *rowsum2;   // [B, kN] pass 2's interior sums, the back pad's added by the edge kernel
@@ -1143,72 +1145,127 @@ struct FfSums {
   }
 };
 
+// The per-row pad kernels' working values: for each pad step the forward
+// states of both passes, pass 1's output and the adjoint's value (kFfW
+// doubles).  Pads of at most kFfPadLds steps live in LDS, one column per
+// row (kFfRows rows a block); longer ones in the global work buffer
+// ([B, e, kFfW]), where every step would wait on a store's round trip.
+constexpr int kFfRows = 32;
+constexpr int kFfPadLds = 16;
+template <int M>
+struct FfPad {
+  static constexpr int kW = 2 * M + 2;  // h1 [0, M), h2 [M, 2M), y1 2M, u 2M + 1
+};
+
+// Pad-step loops: unrolled over at most EMAX steps (EMAX > 0: the LDS
+// path, whose indices are then compile-time) or over e.
+template <int EMAX, class F>
+__device__ __forceinline__ void ff_up(int64_t e, F &&f) {
+  if constexpr (EMAX > 0) {
+#pragma unroll
+    for (int j = 0; j < EMAX; ++j)
+      if (j < e) f(int64_t(j));
+  } else {
+    for (int64_t j = 0; j < e; ++j) f(j);
+  }
+}
+template <int EMAX, class F>
+__device__ __forceinline__ void ff_down(int64_t e, F &&f) {
+  if constexpr (EMAX > 0) {
+#pragma unroll
+    for (int j = EMAX - 1; j >= 0; --j)
+      if (j < e) f(int64_t(j));
+  } else {
+    for (int64_t j = e - 1; j >= 0; --j) f(j);
+  }
+}
+
 // Between the adjoint launches: pass 2's adjoint over the back pad and its
-// edge term, then pass 1's adjoint over the back pad (its dL/dext, in place
-// of the dL/dy1 it consumes) up to the interior's entry state.  With no pad
-// the edge term lands on the interior's last dL/dy1.  With coefficient
+// edge term, then pass 1's adjoint over the back pad (its dL/dext, the
+// fold kernel's input) up to the interior's entry state.  With no pad the
+// edge term lands on the interior's last dL/dy1.  With coefficient
 // gradients, first the forward states of both passes over the back pad
 // (pass 1 from zf1 over the pad's samples, pass 2 from z y1[N-1] back over
 // pass 1's outputs there), then both adjoints' sums over it, added to
 // rowsum2, and pass 2's part of dL/dz.
-template <typename E, int M>
-__global__ __launch_bounds__(64) void ff_bwd_edge_kernel(FfBwdArgs<E> a) {
-  const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+template <typename E, int M, int EMAX>
+__global__ __launch_bounds__(kFfRows) void ff_bwd_edge_kernel(FfBwdArgs<E> a) {
+  constexpr int W = FfPad<M>::kW;
+  __shared__ double lds[EMAX > 0 ? EMAX * W : 1][kFfRows];
+  const int tid = threadIdx.x;
+  const int64_t b = int64_t(blockIdx.x) * kFfRows + tid;
   if (b >= a.B) return;
   const FfModel<M> f = ff_model<M>(a.fb + b * a.f_stride_b, a.nb, a.fa + b * a.f_stride_a, a.na);
   const int64_t T = a.T, e = a.e;
   const bool coef = a.coef != 0;
   const E *xr = coef ? a.x + b * T : nullptr;
-  double *const wk = coef ? a.work + b * e * (2 * M + 1) : nullptr;
-  double *const h1b = wk;                          // [e][M] pass 1's states
-  double *const h2b = coef ? wk + e * M : nullptr;  // [e][M] pass 2's states
-  double *const y1b = coef ? wk + 2 * e * M : nullptr;  // [e] pass 1's outputs
+  auto w = [&](int64_t j, int k) -> double & {  // the forward values (coefficient gradients only)
+    if constexpr (EMAX > 0)
+      return lds[j * W + k][tid];
+    else
+      return a.work[(b * e + j) * W + k];
+  };
+  double *ub = a.edge + b * e;
+  auto u = [&](int64_t j) -> double & {  // dL/dy1 of the back pad, then its dL/dext in ub
+    if constexpr (EMAX > 0)
+      return lds[j * W + 2 * M + 1][tid];
+    else
+      return ub[j];
+  };
   double ylast = 0.0;
   if (coef) {
     double h[M];
 #pragma unroll
     for (int i = 0; i < M; ++i) h[i] = double(a.zf1[b * M + i]);
-    for (int64_t j = 0; j < e; ++j) {
-      const double u = double(pad_back(xr, T, a.pad_mode, j));
+    ff_up<EMAX>(e, [&](int64_t j) {
+      const double xj = double(pad_back(xr, T, a.pad_mode, j));
 #pragma unroll
-      for (int i = 0; i < M; ++i) h1b[j * M + i] = h[i];
-      y1b[j] = h[0] + f.b0 * u;
-      ff_fwd_step(f, h, u);
-    }
-    ylast = e > 0 ? y1b[e - 1] : double(a.y1[b * T + T - 1]);
+      for (int i = 0; i < M; ++i) w(j, i) = h[i];
+      w(j, 2 * M) = h[0] + f.b0 * xj;
+      ff_fwd_step(f, h, xj);
+    });
+    ylast = e > 0 ? w(e - 1, 2 * M) : double(a.y1[b * T + T - 1]);
 #pragma unroll
     for (int i = 0; i < M; ++i) h[i] = f.z[i] * ylast;
-    for (int64_t j = e - 1; j >= 0; --j) {
+    ff_down<EMAX>(e, [&](int64_t j) {
 #pragma unroll
-      for (int i = 0; i < M; ++i) h2b[j * M + i] = h[i];
-      ff_fwd_step(f, h, y1b[j]);
-    }
+      for (int i = 0; i < M; ++i) w(j, M + i) = h[i];
+      ff_fwd_step(f, h, w(j, 2 * M));
+    });
   }
   FfSums<M> acc;
 #pragma unroll
   for (int k = 0; k < FfSums<M>::kN; ++k) acc.v[k] = 0.0;
-  double s[M], r[M];
+  double s[M], r[M], hj[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) {
     s[i] = double(a.lam_a[b * M + i]);
     r[i] = 0.0;
   }
-  double *u = a.edge + b * e;
-  for (int64_t j = 0; j < e; ++j) {
-    if (coef) acc.step(s, h2b + j * M, y1b[j], 0.0);
-    u[j] = ff_adj_step(f, s, 0.0);
-  }
+  ff_up<EMAX>(e, [&](int64_t j) {
+    if (coef) {
+#pragma unroll
+      for (int i = 0; i < M; ++i) hj[i] = w(j, M + i);
+      acc.step(s, hj, w(j, 2 * M), 0.0);
+    }
+    u(j) = ff_adj_step(f, s, 0.0);
+  });
   const double c = ff_dot_z(f, s);
   if (e > 0) {
-    u[e - 1] += c;
+    u(e - 1) += c;
   } else {
     E *p = a.gy1 + b * T + (T - 1);
     *p = E(double(*p) + c);
   }
-  for (int64_t j = e - 1; j >= 0; --j) {
-    if (coef) acc.step(r, h1b + j * M, double(pad_back(xr, T, a.pad_mode, j)), u[j]);
-    u[j] = ff_adj_step(f, r, u[j]);
-  }
+  ff_down<EMAX>(e, [&](int64_t j) {
+    const double uj = u(j);
+    if (coef) {
+#pragma unroll
+      for (int i = 0; i < M; ++i) hj[i] = w(j, i);
+      acc.step(r, hj, double(pad_back(xr, T, a.pad_mode, j)), uj);
+    }
+    ub[j] = ff_adj_step(f, r, uj);
+  });
 #pragma unroll
   for (int i = 0; i < M; ++i) a.entry[b * M + i] = E(r[i]);
   if (coef) {
@@ -1227,9 +1284,12 @@ __global__ __launch_bounds__(64) void ff_bwd_edge_kernel(FfBwdArgs<E> a) {
 // (from z ext[0]), the adjoint's sums over it, dL/dz through z = (I -
 // A)^-1 g, and the row's total: rowsum1 += rowsum2 + the front pad's sums +
 // the steady state's.
-template <typename E, int M>
-__global__ __launch_bounds__(64) void ff_bwd_fold_kernel(FfBwdArgs<E> a) {
-  const int64_t b = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+template <typename E, int M, int EMAX>
+__global__ __launch_bounds__(kFfRows) void ff_bwd_fold_kernel(FfBwdArgs<E> a) {
+  constexpr int W = FfPad<M>::kW;
+  __shared__ double lds[EMAX > 0 ? EMAX * M : 1][kFfRows];
+  const int tid = threadIdx.x;
+  const int64_t b = int64_t(blockIdx.x) * kFfRows + tid;
   if (b >= a.B) return;
   const FfModel<M> f = ff_model<M>(a.fb + b * a.f_stride_b, a.nb, a.fa + b * a.f_stride_a, a.na);
   const int64_t T = a.T, e = a.e;
@@ -1239,36 +1299,45 @@ __global__ __launch_bounds__(64) void ff_bwd_fold_kernel(FfBwdArgs<E> a) {
   E *gx = a.gx + b * T;
   const E *xr = coef ? a.x + b * T : nullptr;
   const double *ub = a.edge + b * e;
-  double *h1f = coef ? a.work + b * e * (2 * M + 1) : nullptr;  // [e][M] pass 1's states over the front pad
+  auto h1f = [&](int64_t n, int i) -> double & {  // pass 1's states over the front pad
+    if constexpr (EMAX > 0)
+      return lds[n * M + i][tid];
+    else
+      return a.work[(b * e + n) * W + i];
+  };
   double ext0 = 0.0;
   if (coef) {
     ext0 = double(e > 0 ? pad_front(xr, T, e, a.pad_mode, 0) : xr[0]);
     double h[M];
 #pragma unroll
     for (int i = 0; i < M; ++i) h[i] = f.z[i] * ext0;
-    for (int64_t n = 0; n < e; ++n) {
+    ff_up<EMAX>(e, [&](int64_t n) {
 #pragma unroll
-      for (int i = 0; i < M; ++i) h1f[n * M + i] = h[i];
+      for (int i = 0; i < M; ++i) h1f(n, i) = h[i];
       ff_fwd_step(f, h, double(pad_front(xr, T, e, a.pad_mode, n)));
-    }
+    });
   }
   FfSums<M> acc;
 #pragma unroll
   for (int k = 0; k < FfSums<M>::kN; ++k) acc.v[k] = 0.0;
-  double r[M];
+  double r[M], hn[M];
 #pragma unroll
   for (int i = 0; i < M; ++i) r[i] = double(a.lam_b[b * M + i]);
   auto add = [&](int64_t i, double v) { gx[i] = E(double(gx[i]) + v); };
   double sf = 0.0, sb = 0.0;  // replicate: everything lands on x[0] and x[T - 1]
-  for (int64_t n = e - 1; n >= 0; --n) {  // ext[n] is x[0], x[e - n] (reflect) or x[T - e + n]
-    if (coef) acc.step(r, h1f + n * M, double(pad_front(xr, T, e, a.pad_mode, n)), 0.0);
+  ff_down<EMAX>(e, [&](int64_t n) {  // ext[n] is x[0], x[e - n] (reflect) or x[T - e + n]
+    if (coef) {
+#pragma unroll
+      for (int i = 0; i < M; ++i) hn[i] = h1f(n, i);
+      acc.step(r, hn, double(pad_front(xr, T, e, a.pad_mode, n)), 0.0);
+    }
     double o = ff_adj_step(f, r, 0.0);
     if (n == 0) o += ff_dot_z(f, r);
     if (repl)
       sf += o;
     else if (to_x)
       add(refl ? e - n : T - e + n, o);
-  }
+  });
   if (e == 0) add(0, ff_dot_z(f, r));  // ext is x
   for (int64_t j = 0; j < e; ++j) {  // ext[T + e + j]
     if (repl)
@@ -1283,7 +1352,7 @@ __global__ __launch_bounds__(64) void ff_bwd_fold_kernel(FfBwdArgs<E> a) {
   if (!coef) return;
   // dL/dz, then w = (I - companion(a))^-1 dL/dz: rows 1.. give w_i = w_0 +
   // p_i with p_i = sum_{k=1..i} gz_k, row 0 w_0 (1 + sum a) = gz_0 - sum a_i p_i
-  double gz[M], p[M], w[M];
+  double gz[M], p[M], wv[M];
   double sa = 1.0, ap = 0.0;
 #pragma unroll
   for (int i = 0; i < M; ++i) {
@@ -1295,10 +1364,10 @@ __global__ __launch_bounds__(64) void ff_bwd_fold_kernel(FfBwdArgs<E> a) {
   const double w0 = (gz[0] - ap) / sa;
 #pragma unroll
   for (int i = 0; i < M; ++i) {
-    w[i] = w0 + p[i];
+    wv[i] = w0 + p[i];
 #pragma unroll
-    for (int j = 0; j < M; ++j) acc.v[i * M + j] += w[i] * f.z[j];
-    acc.v[FfSums<M>::kB + i] += w[i];
+    for (int j = 0; j < M; ++j) acc.v[i * M + j] += wv[i] * f.z[j];
+    acc.v[FfSums<M>::kB + i] += wv[i];
   }
   double *rs = a.rowsum1 + b * FfSums<M>::kN;
   const double *r2 = a.rowsum2 + b * FfSums<M>::kN;

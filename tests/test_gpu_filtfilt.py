@@ -215,7 +215,8 @@ def test_filtfilt_bwd_capi_vs_oracle_jacobian(api, dtype, order, padmode):
             b, a, _ = _case(dtype, B, T, shared, D.seed_of("filtfilt-bwd-jt", dtype, order, padmode, T, shared),
                             order)
             gy = D.normal(D.rng(D.seed_of("filtfilt-bwd-jt-g", T)), (B, T), dtype)
-            for padlen in sorted({0, min(1, T - 1), min(9, T - 1), T - 1}):
+            # 16 and 17: the pad kernels' LDS path and its global-memory one
+            for padlen in sorted({0, min(1, T - 1), min(9, T - 1), min(16, T - 1), min(17, T - 1), T - 1}):
                 gx = _run_bwd(api, b, a, gy, padmode, padlen)
                 ref = np.stack([_oracle_jt(f64(b if shared else b[r]), f64(a if shared else a[r]), T, padmode,
                                            padlen) @ f64(gy[r]) for r in range(B)])
@@ -266,7 +267,7 @@ def test_filtfilt_bwd_capi_coef_vs_oracle_fd(api, dtype, order, padmode):
             if short:
                 b = np.ascontiguousarray(b[..., :-1])
             gy = D.normal(g, (B, T), dtype)
-            for padlen in sorted({0, 1, 9, T - 1}):
+            for padlen in sorted({0, 1, 9, 16, 17, T - 1}):
                 gx, gb, ga = _run_bwd(api, b, a, gy, padmode, padlen, x=x)
                 assert np.isfinite(gb).all() and np.isfinite(ga).all()
 
@@ -511,7 +512,8 @@ def test_filtfilt_op_gradcheck(hip):
             assert torch.autograd.gradcheck(f3, (bg, ag, x))
             assert torch.autograd.gradcheck(f3, (bg, a, x.detach()))
         # second order runs the composed route, whose F.pad backward accumulates with atomics on the GPU
-        assert torch.autograd.gradgradcheck(f3, (bg, ag, x), nondet_tol=1e-12)
+        # (run-to-run differences of ~1e-11 relative on gradients up to ~1e4)
+        assert torch.autograd.gradgradcheck(f3, (bg, ag, x), nondet_tol=1e-7)
 
 
 def test_filtfilt_api_errors(hip):
