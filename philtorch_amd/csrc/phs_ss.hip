@@ -15,9 +15,16 @@
 namespace phs {
 namespace {
 
+// The shortest tile of any launch mode (the gradient mode's at orders 3-4):
+// the workspace and the grid check cover every launch of a call.
+template <class Alg>
+constexpr int64_t ss_min_tile() {
+  return std::min<int64_t>(SsShape<Alg>::kTile, SsShape<Alg, kSsGrad>::kTile);
+}
+
 template <class Alg>
 size_t ss_ws_bytes(int64_t B, int64_t T) {
-  const int64_t tiles = (T + SsShape<Alg>::kTile - 1) / SsShape<Alg>::kTile;
+  const int64_t tiles = (T + ss_min_tile<Alg>() - 1) / ss_min_tile<Alg>();
   return align_up(align_up(kHeaderBytes) + size_t(B) * size_t(tiles) * SsStatus<Alg>::kStride * sizeof(uint64_t));
 }
 
@@ -29,13 +36,13 @@ struct SsFilter {
   bool shared = false;
 };
 
-// The launch arguments of one pass over [B, T] (workspace carved as above);
-// false if the workspace is short.
-template <class Alg>
+// The launch arguments of one pass over [B, T] in launch mode MODE
+// (workspace carved as above); false if the workspace is short.
+template <class Alg, int MODE = kSsPlain>
 bool ss_args(int64_t B, int64_t T, const SsFilter &f, const void *zi, const void *x, void *y, void *zf,
              void *workspace, size_t ws_bytes, SsArgs<Alg> &a) {
   using E = typename Alg::elem;
-  using Sh = SsShape<Alg>;
+  using Sh = SsShape<Alg, MODE>;
   const int64_t tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
   if (!workspace || ws_bytes < ss_ws_bytes<Alg>(B, T)) return false;
   char *ws = static_cast<char *>(workspace);
@@ -66,7 +73,7 @@ bool ss_args(int64_t B, int64_t T, const SsFilter &f, const void *zi, const void
 
 template <class Alg, bool REV, int MODE = kSsPlain>
 int ss_launch(const SsArgs<Alg> &a, hipStream_t stream) {
-  launch_kernel((ss_kernel<Alg, REV, MODE>), dim3(a.per_stripe * kStripes), dim3(SsShape<Alg>::kThreads), 0, stream,
+  launch_kernel((ss_kernel<Alg, REV, MODE>), dim3(a.per_stripe * kStripes), dim3(SsShape<Alg, MODE>::kThreads), 0, stream,
                 a);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
@@ -80,10 +87,11 @@ struct SsBwdLayout {
 template <class Alg>
 SsBwdLayout<Alg> ss_bwd_layout(int64_t B, int64_t T) {
   using C = typename Wide<typename Alg::elem>::type;
-  const int64_t tiles = (T + SsShape<Alg>::kTile - 1) / SsShape<Alg>::kTile;
+  using Sh = SsShape<Alg, kSsGrad>;  // the partials are the gradient launch's
+  const int64_t tiles = (T + Sh::kTile - 1) / Sh::kTile;
   SsBwdLayout<Alg> L;
   L.partials = 0;
-  L.rowsum = align_up(L.partials + size_t(B) * size_t(tiles) * SsShape<Alg>::kWaves * SsGrad<Alg>::kN * sizeof(C));
+  L.rowsum = align_up(L.partials + size_t(B) * size_t(tiles) * Sh::kWaves * SsGrad<Alg>::kN * sizeof(C));
   L.states = align_up(L.rowsum + size_t(B) * SsGrad<Alg>::kN * sizeof(C));
   L.total = align_up(L.states + size_t(B) * size_t(T) * sizeof(typename Alg::s_state));
   return L;
@@ -151,7 +159,7 @@ int ss_bwd(int64_t B, int64_t T, const SsModelArgs<typename Alg::elem> &mo, cons
   if (B == 0) return PHS_OK;
   if ((f.form == 0 ? !mo.A : (!f.b || !f.a)) || (T > 0 && (!x || !gy))) return PHS_ERR_INVALID;
   if (f.form == 0 && ((out.gb && !mo.b) || (out.gc && !mo.c) || (out.gd && !mo.d))) return PHS_ERR_INVALID;
-  if (!ss_grid_ok(B, T, SsShape<Alg>::kTile)) return PHS_ERR_INVALID;
+  if (!ss_grid_ok(B, T, ss_min_tile<Alg>())) return PHS_ERR_INVALID;
   const SsBwdLayout<Alg> L = ss_bwd_layout<Alg>(B, T);
   if (!scratch || scratch_bytes < L.total) return PHS_ERR_WORKSPACE;
   if (T > 0 && (!workspace || ws_bytes < ss_ws_bytes<Alg>(B, T))) return PHS_ERR_WORKSPACE;
@@ -159,7 +167,7 @@ int ss_bwd(int64_t B, int64_t T, const SsModelArgs<typename Alg::elem> &mo, cons
   C *gpart = reinterpret_cast<C *>(sc + L.partials);
   C *rowsum = reinterpret_cast<C *>(sc + L.rowsum);
   E *states = reinterpret_cast<E *>(sc + L.states);
-  const int64_t tiles = (T + SsShape<Alg>::kTile - 1) / SsShape<Alg>::kTile;
+  const int64_t tiles = (T + SsShape<Alg, kSsGrad>::kTile - 1) / SsShape<Alg, kSsGrad>::kTile;
   auto set_model = [&](SsArgs<Alg> &a, bool adjoint) {
     a.A = static_cast<const E *>(mo.A);
     a.A_stride = mo.A_sh ? 0 : M * M;
@@ -186,7 +194,7 @@ int ss_bwd(int64_t B, int64_t T, const SsModelArgs<typename Alg::elem> &mo, cons
     if (rc != PHS_OK) return rc;
     SsFilter fa = f;
     if (f.form != 0) fa.form = 3 - f.form;  // TDF-II <-> DF-II: the adjoint of a companion form
-    if (!ss_args<Alg>(B, T, fa, gzf, gy, gx, gzi, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+    if (!ss_args<Alg, kSsGrad>(B, T, fa, gzf, gy, gx, gzi, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
     set_model(p, true);
     p.hs_fwd = states;
     p.x_fwd = static_cast<const E *>(x);
@@ -205,7 +213,7 @@ int ss_bwd(int64_t B, int64_t T, const SsModelArgs<typename Alg::elem> &mo, cons
   out.gzi = T == 0 ? static_cast<E *>(gzi) : nullptr;
   out.gzf = static_cast<const E *>(gzf);
   hipLaunchKernelGGL(ss_grad_rows_kernel<Alg>, dim3(unsigned(B)), dim3(kSsReduceThreads), 0, stream,
-                     static_cast<const C *>(gpart), tiles * SsShape<Alg>::kWaves, rowsum);
+                     static_cast<const C *>(gpart), tiles * SsShape<Alg, kSsGrad>::kWaves, rowsum);
   hipLaunchKernelGGL(ss_grad_finish_kernel<Alg>, dim3(1), dim3(kSsReduceThreads), 0, stream,
                      static_cast<const C *>(rowsum), B, T, out);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
@@ -282,14 +290,14 @@ FfBwdLayout<Alg> ff_bwd_layout(int64_t B, int64_t T, int64_t e, bool coef) {
   L.edge = L.lam_b + align_up(rows * 4 * esz);
   L.total = L.edge + align_up(rows * size_t(e) * sizeof(double));
   if (!coef) return L;
-  const int64_t tiles = (T + SsShape<Alg>::kTile - 1) / SsShape<Alg>::kTile;
+  const int64_t tiles = (T + SsShape<Alg, kSsGrad>::kTile - 1) / SsShape<Alg, kSsGrad>::kTile;
   constexpr int N = SsGrad<Alg>::kN;
   L.y1 = L.total;
   L.zf1 = L.y1 + align_up(n * esz);
   L.h1 = L.zf1 + align_up(rows * M * esz);
   L.h2 = L.h1 + align_up(n * sizeof(typename Alg::s_state));
   L.gpart = L.h2 + align_up(n * sizeof(typename Alg::s_state));
-  L.rowsum1 = L.gpart + align_up(rows * size_t(tiles) * SsShape<Alg>::kWaves * N * sizeof(C));
+  L.rowsum1 = L.gpart + align_up(rows * size_t(tiles) * SsShape<Alg, kSsGrad>::kWaves * N * sizeof(C));
   L.rowsum2 = L.rowsum1 + align_up(rows * N * sizeof(C));
   L.gz = L.rowsum2 + align_up(rows * N * sizeof(C));
   L.work = L.gz + align_up(rows * M * sizeof(double));
@@ -320,6 +328,7 @@ int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e
                     FfSums<M>::kD == SsGrad<Alg>::kD,
                 "the pads' sums in the kernels' layout");
   const bool coef = gfb != nullptr;
+  if (!ss_grid_ok(B, T, ss_min_tile<Alg>())) return PHS_ERR_INVALID;
   if (ws_bytes < filtfilt_ws_bytes<E>(B, T)) return PHS_ERR_WORKSPACE;
   const FfBwdLayout<Alg> L = ff_bwd_layout<Alg>(B, T, e, coef);
   if (!scratch || scratch_bytes < L.total) return PHS_ERR_WORKSPACE;
@@ -346,7 +355,7 @@ int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e
   k.entry = entry;
   k.lam_b = lam_b;
   k.gx = static_cast<E *>(gx);
-  const int64_t tiles = (T + SsShape<Alg>::kTile - 1) / SsShape<Alg>::kTile;
+  const int64_t tiles = (T + SsShape<Alg, kSsGrad>::kTile - 1) / SsShape<Alg, kSsGrad>::kTile;
   const dim3 grid(unsigned((B + kFfRows - 1) / kFfRows));
   const bool lds = e <= kFfPadLds;
   SsFilter adj = f;
@@ -397,7 +406,9 @@ int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e
   }
   // pass 2's adjoint over the interior (ascending time)
   p = SsArgs<Alg>{};
-  if (!ss_args<Alg>(B, T, adj, nullptr, gy, gy1, lam_a, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+  const bool args_ok = coef ? ss_args<Alg, kSsGrad>(B, T, adj, nullptr, gy, gy1, lam_a, workspace, ws_bytes, p)
+                             : ss_args<Alg>(B, T, adj, nullptr, gy, gy1, lam_a, workspace, ws_bytes, p);
+  if (!args_ok) return PHS_ERR_WORKSPACE;
   if (coef) {
     p.hs_fwd = reinterpret_cast<const E *>(h2);
     p.x_fwd = y1;
@@ -405,7 +416,7 @@ int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e
     p.vec_hs = vec_states(h2, y1);
     if ((rc = ss_launch<Alg, false, kSsGrad>(p, stream)) != PHS_OK) return rc;
     hipLaunchKernelGGL(ss_grad_rows_kernel<Alg>, dim3(unsigned(B)), dim3(kSsReduceThreads), 0, stream,
-                       static_cast<const C *>(gpart), tiles * SsShape<Alg>::kWaves, rowsum2);
+                       static_cast<const C *>(gpart), tiles * SsShape<Alg, kSsGrad>::kWaves, rowsum2);
   } else if ((rc = ss_launch<Alg, false>(p, stream)) != PHS_OK) {
     return rc;
   }
@@ -415,7 +426,9 @@ int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e
     hipLaunchKernelGGL((ff_bwd_edge_kernel<E, M, 0>), grid, dim3(kFfRows), 0, stream, k);
   // pass 1's adjoint over the interior (descending time)
   p = SsArgs<Alg>{};
-  if (!ss_args<Alg>(B, T, adj, entry, gy1, gx, lam_b, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+  const bool args1_ok = coef ? ss_args<Alg, kSsGrad>(B, T, adj, entry, gy1, gx, lam_b, workspace, ws_bytes, p)
+                              : ss_args<Alg>(B, T, adj, entry, gy1, gx, lam_b, workspace, ws_bytes, p);
+  if (!args1_ok) return PHS_ERR_WORKSPACE;
   if (coef) {
     p.hs_fwd = reinterpret_cast<const E *>(h1);
     p.x_fwd = static_cast<const E *>(x);
@@ -423,7 +436,7 @@ int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e
     p.vec_hs = vec_states(h1, x);
     if ((rc = ss_launch<Alg, true, kSsGrad>(p, stream)) != PHS_OK) return rc;
     hipLaunchKernelGGL(ss_grad_rows_kernel<Alg>, dim3(unsigned(B)), dim3(kSsReduceThreads), 0, stream,
-                       static_cast<const C *>(gpart), tiles * SsShape<Alg>::kWaves, rowsum1);
+                       static_cast<const C *>(gpart), tiles * SsShape<Alg, kSsGrad>::kWaves, rowsum1);
   } else if ((rc = ss_launch<Alg, true>(p, stream)) != PHS_OK) {
     return rc;
   }

@@ -94,20 +94,33 @@ struct SsArgs {
   int vec_ok;
 };
 
+// Kernel modes: the model's output (plain), the states of a forward for the
+// coefficient gradients (kSsStates: h[t] before every step, no y), the
+// adjoint pass with the coefficient-gradient sums (kSsGrad), the states
+// and the output with the final state (kSsStatesY: a zero-phase filter's
+// first pass, whose output is the second pass's input).
+constexpr int kSsPlain = 0, kSsStates = 1, kSsGrad = 2, kSsStatesY = 3;
+
 // 3 data waves and a look-back wave.  Orders 1-2: 4 rounds of two 16-byte
 // vectors of inputs per lane (8 fp32 or 4 fp64 steps); orders 3-4: 2 rounds
 // of four vectors, which halves the scan levels per step where each level
 // is an M x M product (6144-step fp32 tiles either way; at the C4 shape,
 // order 4 takes 53 us per launch against 67 with the other split and 74
-// with 3072-step tiles, order 1 25 against 28).
-template <class Alg>
+// with 3072-step tiles, order 1 25 against 28).  The gradient mode runs
+// half the rounds (3072-step fp32 tiles): its sums and the forward's states
+// take the registers the other rounds' inputs would, and the order-4
+// adjoint spilled.  At the C4 shape a backward call with coefficient
+// gradients (states pass, adjoint, sums) went 279 -> 237 us at order 4,
+// 217 -> 188 at order 3, 134 -> 128.5 at order 2 and 86.5 -> 85.5 at
+// order 1; the other modes are slower with fewer rounds.
+template <class Alg, int MODE = kSsPlain>
 struct SsShape {
   using E = typename Alg::elem;
   static constexpr int M = int(sizeof(typename Alg::s_state) / sizeof(E));
   static constexpr int kWaves = 3;
   static constexpr int kThreads = 64 * (kWaves + 1);
   static constexpr int K = int((M <= 2 ? 32 : 64) / sizeof(E));
-  static constexpr int R = M <= 2 ? 4 : 2;
+  static constexpr int R = (M <= 2 ? 4 : 2) / (MODE == kSsGrad ? 2 : 1);
   static constexpr int kWaveSeg = 64 * K * R;
   static constexpr int kTile = kWaves * kWaveSeg;
   static_assert((K & (K - 1)) == 0, "K is a power of two (the lane matrix is A^K by squaring)");
@@ -640,13 +653,6 @@ __device__ bool ss_lookback(const uint64_t *row_status, const typename Alg::stat
   }
 }
 
-// Kernel modes: the model's output (plain), the states of a forward for the
-// coefficient gradients (kSsStates: h[t] before every step, no y), the
-// adjoint pass with the coefficient-gradient sums (kSsGrad), the states
-// and the output with the final state (kSsStatesY: a zero-phase filter's
-// first pass, whose output is the second pass's input).
-constexpr int kSsPlain = 0, kSsStates = 1, kSsGrad = 2, kSsStatesY = 3;
-
 // Coefficient-gradient sums of one model: dL/dA (M x M row-major), dL/db
 // (M), dL/dc (M), dL/dd; a lane sums its own steps in storage precision
 // (32 fp32 or 16 fp64 steps), everything above it in compute precision.
@@ -699,12 +705,12 @@ __device__ __forceinline__ void ss_grad_step(SsGrad<Alg, typename Alg::elem> &ac
 
 // At least two waves per SIMD (two workgroups per CU).
 template <class Alg, bool REV, int MODE>
-__global__ __launch_bounds__(SsShape<Alg>::kThreads, 2) void ss_kernel(SsArgs<Alg> a) {
+__global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), 2) void ss_kernel(SsArgs<Alg> a) {
   using E = typename Alg::elem;
   using S = typename Alg::state;
   using SS = typename Alg::s_state;
   using V = SsView<Alg>;
-  using Sh = SsShape<Alg>;
+  using Sh = SsShape<Alg, MODE>;
   using St = SsStatus<Alg>;
   constexpr int K = Sh::K, R = Sh::R, kWaves = Sh::kWaves;
   static_assert(Alg::kLookFirst == 8 || Alg::kLookFirst == 64, "window weights are table entries");
