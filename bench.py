@@ -45,6 +45,9 @@ Output: one JSON line (the driver's contract) with
   cpu_baseline the oracle (a C restatement of the reference CPU extension and
                its composite backward, OpenMP over the batch) on a bounded
                sample of the same workload, on this host's cores
+--phases adds detail.phases: where a scan launch's time goes, tile by tile
+(claim, loads and fold, look-back, pass 2 and stores), from one traced forward
+and one traced backward launch (phs_debug_trace_next_launch).
 """
 from __future__ import annotations
 
@@ -869,6 +872,8 @@ def _kernel_lib():
     lib.phs_stream_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p,
                                      ctypes.c_void_p, ctypes.c_void_p]
     lib.phs_stream_probe.restype = ctypes.c_int
+    lib.phs_debug_trace_next_launch.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    lib.phs_debug_trace_next_launch.restype = None
     return lib
 
 
@@ -959,6 +964,58 @@ def _ceiling(lib, w, steps, evict_caches, dev):
     }
 
 
+def _phases(lib, w, evict_caches, dev):
+    """Per-tile phase breakdown of the first forward and the first backward
+    scan launch of a step, from the tracing build of the scan kernel
+    (phs_debug_trace_next_launch): per tile, the tile claim, data wave 0's
+    loads and fold, the wait for the other waves' aggregates, the look-back
+    (entry state known) and pass 2 with its stores; percentiles in us over
+    the launch's tiles, and the failed look-back polls.  None for workloads
+    whose kernel is not scan_kernel."""
+    import numpy as np
+    import torch
+
+    if w.kernel != "scan_kernel":
+        return None
+    n = 1 << 18
+    rec = torch.zeros(n * 8, dtype=torch.int64, device=dev)
+    out = {}
+    for direction in ("forward", "backward"):
+        evict_caches()
+        rec.zero_()
+        torch.cuda.synchronize()
+        if direction == "forward":
+            lib.phs_debug_trace_next_launch(rec.data_ptr(), n)
+            w.step_fwd()
+        else:
+            y = w.step_fwd()
+            lib.phs_debug_trace_next_launch(rec.data_ptr(), n)
+            w.step_bwd(y)
+        torch.cuda.synchronize()
+        lib.phs_debug_trace_next_launch(None, 0)
+        r = rec.view(-1, 8).cpu().numpy()
+        r = r[r[:, 0] != 0].astype(np.float64)
+        if len(r) == 0:
+            out[direction] = None
+            continue
+        start, claimed, loaded, aggs, entry, stored = (r[:, i] * 0.01 for i in range(6))  # 100 MHz -> us
+        pct = lambda v: [round(float(np.percentile(v, p)), 2) for p in (10, 50, 90)]  # noqa: E731
+        out[direction] = {
+            "tiles": int(len(r)),
+            "percentiles": [10, 50, 90],
+            "claim_us": pct(claimed - start),
+            "load_fold_us": pct(loaded - claimed),
+            "wait_aggregates_us": pct(aggs - loaded),
+            "lookback_us": pct(entry - aggs),
+            "pass2_store_us": pct(stored - entry),
+            "tile_life_us": pct(stored - start),
+            "start_spread_us": round(float(start.max() - start.min()), 2),
+            "wave_span_us": round(float(stored.max() - start.min()), 2),
+            "failed_polls": [int(np.percentile(r[:, 6], p)) for p in (10, 50, 90)],
+        }
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -966,6 +1023,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c1", choices=CONFIGS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--phases", action="store_true",
+                    help="add the per-tile phase breakdown of a traced forward and backward scan launch")
     ap.add_argument("--no-evict", action="store_true", help="keep operands cache-resident (diagnostic)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="after timing, run one plain 256 MiB device copy (reads and writes 256 MiB) so "
@@ -1128,6 +1187,8 @@ def main() -> int:
     }
     if ceiling is not None:
         ceiling["scan_step_frac_of_ceiling"] = round(ceiling["ms_per_step"] / ms_per_step, 4)
+    if args.phases:
+        result["detail"]["phases"] = _phases(lib, w, evict_caches, dev)
     if args.calib_copy:
         csrc = torch.ones(64 << 20, dtype=torch.float32, device=dev)
         cdst = torch.empty_like(csrc)

@@ -108,6 +108,22 @@ void phs_debug_set_aggregates_only(int on);
  * consumed by that launch; NULL, NULL disarms it.  Process-wide. */
 void phs_debug_time_next_launch(void *start_event, void *stop_event);
 
+/* Measurement hook, no counterpart in the reference.  The next scan launch of
+ * phs_{recur,lti_recur,recur2,lti_recur2}_{fwd,bwd} in fp32, fp64 (scalar
+ * ops) or complex64 (scalar ops), and fp32 (2x2 ops) whose tile count is at
+ * most `n_records` runs the tracing build of the scan kernel and writes one
+ * record of 8 uint64 words per tile into `records` (device memory, tile id
+ * order; tile id = position along the row * B + row, backward positions
+ * counted from the row's end): s_memrealtime stamps (100 MHz) at the
+ * workgroup's start, after its tile claim, when data wave 0 has loaded and
+ * folded its segment, when the tile's look-back starts, when its entry state
+ * is known and when data wave 0 has issued its last stores; then the
+ * look-back's failed polls and the tile id.  Results are those of an
+ * untraced launch.  The hook is consumed by the next scan launch, traced or
+ * not (records untouched if it is not); NULL or 0 disarms it.
+ * Process-wide. */
+void phs_debug_trace_next_launch(void *records, size_t n_records);
+
 /* LPV scalar scan.  A: [B,T] (coef_shared=0) or [T] shared by all rows
  * (coef_shared=1); zi: [B]; x, y: [B,T].
  * Replaces philtorch::recurN with 1x1 matrices, the only native time-varying

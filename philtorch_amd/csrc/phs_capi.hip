@@ -7,6 +7,7 @@ namespace phs {
 std::atomic<unsigned> g_spin_limit{0};
 std::atomic<bool> g_agg_only{false};
 TimingHook g_timing;
+TraceHook g_trace;
 
 // ---- workspace of the allocation-free entry point (phs_recur_fwd_noalloc)
 // One array per device, held from the library's load until the process
@@ -62,7 +63,7 @@ const char *phs_error_string(int status) {
   }
 }
 
-int phs_abi_version(void) { return 110; }
+int phs_abi_version(void) { return 111; }
 
 void phs_debug_set_spin_limit(unsigned polls) { phs::g_spin_limit.store(polls, std::memory_order_relaxed); }
 
@@ -73,6 +74,13 @@ void phs_debug_time_next_launch(void *start_event, void *stop_event) {
   phs::g_timing.start = static_cast<hipEvent_t>(start_event);
   phs::g_timing.stop = static_cast<hipEvent_t>(stop_event);
   phs::g_timing.armed.store(start_event != nullptr || stop_event != nullptr, std::memory_order_release);
+}
+
+void phs_debug_trace_next_launch(void *records, size_t n_records) {
+  std::lock_guard<std::mutex> lock(phs::g_trace.mu);
+  phs::g_trace.records = static_cast<uint64_t *>(records);
+  phs::g_trace.n_records = n_records;
+  phs::g_trace.armed.store(records != nullptr && n_records > 0, std::memory_order_release);
 }
 
 #define PHS_FWD(NAME, ALGT, TV)                                                                    \

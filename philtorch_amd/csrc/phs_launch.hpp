@@ -2,8 +2,8 @@
 // phs_capi_n.hip: order-M entry points): argument checks, workspace carving,
 // and the launch of scan_kernel [-> reduce kernel] on the caller's stream.
 // No allocation and no synchronisation; the only global state is the
-// spin-limit testing hook and a per-device cache of how many workgroups of
-// each kernel are resident at once.
+// testing and measurement hooks and a per-device cache of how many
+// workgroups of each kernel are resident at once.
 // Workspace layout: [0, 2048) header (16 striped {epoch, claim count} words),
 // then the tile status words, then (backward only) per-tile partial sums or
 // per-step scratch.
@@ -50,6 +50,41 @@ inline bool take_timing(hipEvent_t &start, hipEvent_t &stop) {
   start = g_timing.start;
   stop = g_timing.stop;
   g_timing.armed.store(false, std::memory_order_relaxed);
+  return true;
+}
+
+// Measurement hook (phs_debug_trace_next_launch): a device buffer of
+// per-tile phase records that the next scan_kernel launch of a traceable
+// algebra (TraceableAlg) fills, if its tiles fit.  Taken (and cleared) by
+// that launch.
+struct TraceHook {
+  std::atomic<bool> armed{false};
+  std::mutex mu;
+  uint64_t *records = nullptr;
+  size_t n_records = 0;
+};
+extern TraceHook g_trace;  // phs_capi.hip
+
+// The algebras whose scans carry a tracing instantiation: those of the
+// benchmark configurations (fp32/fp64 scalar, complex64 scalar, fp32 2x2).
+template <class Alg>
+struct TraceableAlg : std::false_type {};
+template <>
+struct TraceableAlg<Scalar<float>> : std::true_type {};
+template <>
+struct TraceableAlg<Scalar<double>> : std::true_type {};
+template <>
+struct TraceableAlg<Scalar<c64>> : std::true_type {};
+template <>
+struct TraceableAlg<Block2<float>> : std::true_type {};
+
+inline bool take_trace(uint64_t *&records, size_t &n) {
+  if (!g_trace.armed.load(std::memory_order_acquire)) return false;
+  std::lock_guard<std::mutex> lock(g_trace.mu);
+  if (!g_trace.armed.load(std::memory_order_relaxed)) return false;
+  records = g_trace.records;
+  n = g_trace.n_records;
+  g_trace.armed.store(false, std::memory_order_relaxed);
   return true;
 }
 
@@ -113,7 +148,17 @@ inline int64_t resident_groups(const void *kernel, int threads) {
 }
 
 template <class Alg, bool TV, bool REV>
-void launch_scan(const ScanArgs<Alg> &a, unsigned grid, hipStream_t stream) {
+void launch_scan(ScanArgs<Alg> a, unsigned grid, hipStream_t stream) {
+  if constexpr (TraceableAlg<Alg>::value) {
+    uint64_t *records = nullptr;
+    size_t n = 0;
+    if (take_trace(records, n) && records && n >= a.tiles) {
+      a.trace = records;
+      a.trace_tiles = a.tiles;
+      launch_kernel(scan_kernel<Alg, TV, REV, true>, dim3(grid), dim3(Shape<Alg, TV>::kThreads), 0, stream, a);
+      return;
+    }
+  }
   launch_kernel(scan_kernel<Alg, TV, REV>, dim3(grid), dim3(Shape<Alg, TV>::kThreads), 0, stream, a);
 }
 
@@ -151,6 +196,8 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
   const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
   a.spin_limit = sl ? sl : kDefaultSpinLimit;
   a.agg_only = g_agg_only.load(std::memory_order_relaxed) ? 1u : 0u;
+  a.trace = nullptr;
+  a.trace_tiles = 0;
   if (backward && gcoef) {
     if (TV)
       a.gcoef = shared ? reinterpret_cast<E *>(ws + L.scratch_off) : static_cast<E *>(gcoef);

@@ -121,7 +121,23 @@ struct ScanArgs {
   unsigned agg_only;           // testing: tiles after a row's first publish no inclusive state
   uint64_t *status;          // status words of this call
   int vec_ok;
+  // tracing launches only (scan_kernel<..., TRACE = true>): per-tile phase
+  // records, kTraceWords 64-bit words per tile id, for ids below trace_tiles
+  uint64_t *trace;
+  unsigned trace_tiles;
 };
+
+// Per-tile phase record of a tracing launch (phs_debug_trace_next_launch):
+// s_memrealtime stamps (a constant 100 MHz clock shared by the whole chip)
+// at the workgroup's start, after its tile claim, when data wave 0 has
+// loaded and folded its segment, when the tile's wave aggregates are in
+// (the look-back starts), when its entry state is known, and when data wave
+// 0 has issued its last stores; then the look-back's failed polls and the
+// tile id.
+constexpr int kTraceWords = 8;
+enum TraceSlot { kTrStart, kTrClaimed, kTrLoaded, kTrAggregates, kTrEntry, kTrStored, kTrPolls, kTrId };
+
+__device__ __forceinline__ uint64_t trace_clock() { return __builtin_amdgcn_s_memrealtime(); }
 
 constexpr int kStripes = 16;
 constexpr int kStripeWords = 16;  // 128 bytes between claim words
@@ -500,7 +516,10 @@ __device__ __forceinline__ typename Alg::state tile_entry(const ScanArgs<Alg> &a
 // per tile costs more than it saves.  Either way the waves meet at the same
 // barriers: claim, wave aggregates ready, entry state ready (and, backward
 // for LTI, the gradient reduction).
-template <class Alg, bool TV, bool REV>
+//
+// TRACE: the instantiation a tracing launch runs; it also writes each
+// tile's phase record (kTraceWords words at trace + id * kTraceWords).
+template <class Alg, bool TV, bool REV, bool TRACE = false>
 __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) void scan_kernel(ScanArgs<Alg> a) {
   using S = typename Alg::state;     // compute type
   using SC = typename Alg::s_coef;   // storage types
@@ -521,6 +540,8 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
   // wave index as a scalar: the role branches below are scalar branches, so a
   // wave only ever executes the barriers of its own role
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  [[maybe_unused]] uint64_t tr_start = 0;
+  if constexpr (TRACE) tr_start = trace_clock();
   if (tid == 0) {
     claim_tile(a.claims, a.per_stripe, s_id, s_tag);
     s_ready = 0;
@@ -529,6 +550,15 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
   if (s_id >= a.tiles) return;  // padding of the last stripe round
   const int64_t id = s_id;
   const unsigned tag = s_tag;
+  uint64_t *tr = nullptr;  // this tile's phase record (tracing launches)
+  if constexpr (TRACE) {
+    if (id < a.trace_tiles) tr = a.trace + id * kTraceWords;
+    if (tr && tid == 0) {
+      tr[kTrStart] = tr_start;
+      tr[kTrClaimed] = trace_clock();
+      tr[kTrId] = uint64_t(id);
+    }
+  }
   const int64_t qs = id / a.B;         // position in scan order
   const int64_t b = id - qs * a.B;
   const int64_t qf = REV ? a.tiles_per_row - 1 - qs : qs;  // position along time
@@ -566,9 +596,18 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
       __builtin_amdgcn_s_sleep(1);
     }
     __syncthreads();  // wave aggregates are in s_wagg
+    if constexpr (TRACE) {
+      if (tr && lane == 0) tr[kTrAggregates] = trace_clock();
+    }
     const M tagg = tile_aggregate<Alg, kWaves>(s_wagg);
     if (!known && lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
     yin = tile_entry<Alg, TV, REV>(a, qs, b, tag, lane, tagg, known, yin, lb, s_look);
+    if constexpr (TRACE) {
+      if (tr && lane == 0) {
+        tr[kTrEntry] = trace_clock();
+        tr[kTrPolls] = lb.polls;
+      }
+    }
     if (lane == 0) s_in = yin;
     __syncthreads();  // entry state published to the data waves
     if (want_acc) __syncthreads();  // the data waves' gradient reduction
@@ -679,6 +718,9 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
     if (spec[r]) v = pass2(r, hs[r]);
     if constexpr (kAcc) acc_s[r] = v;
   }
+  if constexpr (TRACE) {
+    if (tr && tid == 0) tr[kTrLoaded] = trace_clock();
+  }
   if (lane == 0) {
     s_wagg[w] = carry;
     if (Sh::kLookbackWave) __hip_atomic_fetch_add(&s_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -686,11 +728,20 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
   __syncthreads();  // wave aggregates are in s_wagg
   if (!Sh::kLookbackWave && w == 0) {
     // look-back by data wave 0: publish the tile's aggregate, find its entry
+    if constexpr (TRACE) {
+      if (tr && lane == 0) tr[kTrAggregates] = trace_clock();
+    }
     const M tagg = tile_aggregate<Alg, kWaves>(s_wagg);
     if (qs > 0 && lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
     Lookback<Alg> lb = lookback_start<Alg>(qs);
     const S virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
     const S yin = tile_entry<Alg, TV, REV>(a, qs, b, tag, lane, tagg, qs == 0, virt, lb, s_look);
+    if constexpr (TRACE) {
+      if (tr && lane == 0) {
+        tr[kTrEntry] = trace_clock();
+        tr[kTrPolls] = lb.polls;
+      }
+    }
     if (lane == 0) s_in = yin;
   }
   // the wave's exclusive prefix in the tile, folded by every wave itself
@@ -707,6 +758,9 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
     AC v = kAcc ? acc_s[kAcc ? r : 0] : Alg::acc_zero();
     if (!(spec[r] && same_bits(h, hs[r]))) v = pass2(r, h);
     if constexpr (kAcc) acc = Alg::acc_sum(acc, v);
+  }
+  if constexpr (TRACE) {
+    if (tr && tid == 0) tr[kTrStored] = trace_clock();
   }
   if (want_acc) {
     // deterministic block reduction of the per-tile coefficient gradient

@@ -64,6 +64,8 @@ def load() -> ctypes.CDLL:
     lib.phs_debug_set_aggregates_only.restype = None
     lib.phs_debug_time_next_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     lib.phs_debug_time_next_launch.restype = None
+    lib.phs_debug_trace_next_launch.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    lib.phs_debug_trace_next_launch.restype = None
     lib.phs_stream_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p,
                                      ctypes.c_void_p, ctypes.c_void_p]
     lib.phs_stream_probe.restype = ctypes.c_int

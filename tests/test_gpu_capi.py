@@ -295,3 +295,53 @@ def test_capi_order_n_aggregates_only(api, op, M, B, T, dtype):
     finally:
         lib.phs_debug_set_aggregates_only(0)
     _check(got, _oracle_n(op, A, zi, x, gy))
+
+
+# Tracing launches (phs_debug_trace_next_launch): the traced scan gives the
+# untraced results bit for bit and one record per tile whose phase stamps
+# run in order.
+@pytest.mark.parametrize(
+    "op,dtype,B,T,shared",
+    [
+        ("recur", np.float32, 3, 50001, False),
+        ("recur", np.float64, 2, 30000, True),
+        ("lti_recur", np.complex64, 3, 20000, False),
+        ("recur2", np.float32, 2, 9000, False),
+        ("lti_recur2", np.float32, 3, 12000, False),
+    ],
+)
+def test_capi_trace_records(api, op, dtype, B, T, shared):
+    import torch
+
+    lib, ws, capi = api
+    A, zi, x, gy = _case(op, B, T, dtype, shared, D.seed_of("trace", op, np.dtype(dtype).str))
+    ref = _run(api, op, A, shared, zi, x, gy)
+    rec = torch.zeros(4096 * 8, dtype=torch.int64, device="cuda")
+    dt = capi.DTYPES[np.dtype(x.dtype)]
+    tA, tz, tx, tg = _dev(A), _dev(zi), _dev(x), _dev(gy)
+    y = torch.empty_like(tx)
+    gA, gz, gx = torch.empty_like(tA), torch.empty_like(tz), torch.empty_like(tx)
+    fwd = lambda: getattr(lib, f"phs_{op}_fwd")(dt, B, T, _p(tA), int(shared), _p(tz), _p(tx), _p(y),  # noqa: E731
+                                                _p(ws), ws.numel(), _stream())
+    bwd = lambda: getattr(lib, f"phs_{op}_bwd")(dt, B, T, _p(tA), int(shared), _p(tz), _p(y), _p(tg),  # noqa: E731
+                                                _p(gx), _p(gA), _p(gz), _p(ws), ws.numel(), _stream())
+    for direction in ("fwd", "bwd"):
+        rec.zero_()
+        if direction == "bwd":
+            assert fwd() == capi.PHS_OK
+        lib.phs_debug_trace_next_launch(_p(rec), rec.numel() // 8)
+        assert (fwd if direction == "fwd" else bwd)() == capi.PHS_OK
+        torch.cuda.synchronize()
+        r = rec.view(-1, 8).cpu().numpy()
+        tiles = int((r[:, 0] != 0).sum())
+        assert tiles >= 2 * B, (direction, tiles)
+        r = r[:tiles]
+        assert (r[:, 7] == np.arange(tiles)).all()
+        start, claimed, loaded, aggs, entry, stored = (r[:, i] for i in range(6))
+        assert (start <= claimed).all() and (claimed <= loaded).all() and (loaded <= aggs).all()
+        assert (aggs <= entry).all() and (entry <= stored).all()
+        assert ((stored - start) < 100_000_000).all()  # under a second of 100 MHz ticks
+    lib.phs_debug_trace_next_launch(None, 0)
+    got = [t.cpu().numpy() for t in (y, gA, gz, gx)]
+    for name, g, e in zip(("y", "grad_A", "grad_zi", "grad_x"), got, ref):
+        assert np.array_equal(g, e), name

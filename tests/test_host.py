@@ -22,7 +22,7 @@ def test_capi_exports_every_declared_symbol():
 
 def test_capi_host_only_calls():
     lib = capi.load()
-    assert lib.phs_abi_version() == 110
+    assert lib.phs_abi_version() == 111
     for op in capi.OPS.values():
         for dt in capi.DTYPES.values():
             fwd = lib.phs_workspace_size(op, dt, 64, 65536, 0, 0)
