@@ -145,7 +145,9 @@ int sos_bwd(int64_t B, int64_t T, int S, const SosCoefs &k, const void *x, const
   a.vec_ok = (size_t(T) * sizeof(E)) % 16 == 0 && aligned16(gy) && aligned16(gx) && (!grad || aligned16(x));
   const unsigned grid = a.per_stripe * kStripes;
   if (grad) {
-    const size_t lds = size_t(S) * Sh::kWaves * Sh::R * 64 * sizeof(Vec2<E>);
+    // lane entry states of every section, then the kept section's input
+    const size_t lds = size_t(S) * Sh::kWaves * Sh::R * 64 * sizeof(Vec2<E>) +
+                       (sos_kept_section(S) > 0 ? size_t(Sh::kWaves) * Sh::R * Sh::K * 64 * sizeof(E) : 0);
     launch_kernel((sos_kernel<E, Sh, true, true>), dim3(grid), dim3(Sh::kThreads), lds, stream, a);
     if (hipGetLastError() != hipSuccess) return PHS_ERR_LAUNCH;
     const int64_t rows = k.coef_shared() ? 1 : B;

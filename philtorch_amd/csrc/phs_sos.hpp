@@ -42,6 +42,13 @@ namespace phs {
 constexpr int kSosCkpt = 512;          // steps between forward state checkpoints
 constexpr int kSosMaxSections = 8;     // sections per launch (LDS of the gradient backward)
 
+// The gradient backward needs every section's forward input inside its tile.
+// Its forward recompute keeps the input of the middle section S/2 in LDS (for
+// S >= 2), so that re-deriving the input of section s runs sections
+// [0, s) or [S/2, s) from their lane states: at most S/2 sections instead of
+// s (C4's eight sections: 12 section runs per tile instead of 28).
+__host__ __device__ constexpr int sos_kept_section(int S) { return S >= 2 ? S / 2 : 0; }
+
 // Tile shape: W data waves plus one look-back wave; K steps per lane and
 // round (a power of two dividing kSosCkpt), R rounds (a power of two).
 template <typename E, int K_, int R_, int W_>
@@ -726,8 +733,11 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
   __shared__ uint64_t s_look[kSosLookWords];
   __shared__ M s_fagg[GRAD ? 2 : 1][W];  // forward recompute: wave aggregates, two visits in flight
   __shared__ SecPowers<C> s_pow[3];
-  extern __shared__ __align__(16) unsigned char sos_dyn[];  // GRAD: lane entry states [S][W][R][64]
+  // GRAD: lane entry states [S][W][R][64], then the kept section's input
+  // [W][R][K][64] (sos_kept_section)
+  extern __shared__ __align__(16) unsigned char sos_dyn[];
   SV *s_laneh = reinterpret_cast<SV *>(sos_dyn);
+  E *s_uin = reinterpret_cast<E *>(sos_dyn + size_t(a.S) * W * R * 64 * sizeof(SV));
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -835,8 +845,15 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
 #pragma unroll
       for (int k = 0; k < K; ++k) F[r][k] = X[r][k];
     const int64_t ck0 = (qf * Sh::kTile) / kSosCkpt;
+    const int kept = sos_kept_section(S);
     for (; v < S; ++v) {
       const int s = v;
+      if (kept > 0 && s == kept) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int k = 0; k < K; ++k) s_uin[((w * R + r) * K + k) * 64 + lane] = F[r][k];
+      }
       const SosSec<E> q = load_sec(a, b, s);
       const SecPowers<C> &t = s_pow[v % 3];
       V ex[R], tot[R], x[R];
@@ -872,15 +889,25 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
     const SecPowers<C> &t = s_pow[v % 3];
     const SV gzf = load_pair(a.virt + (b * S + s) * 2, REV && a.virt != nullptr);
 
-    // forward input of section s, recomputed from x through sections < s
-    // (F keeps its output, the previous visit's input)
+    // forward input of section s, recomputed from x or from the kept
+    // section's input through the sections between (F keeps its output, the
+    // previous visit's input)
     E Uf[GRAD ? R : 1][GRAD ? K : 1];
     if constexpr (GRAD) {
+      const int kept = sos_kept_section(S);
+      const int j0 = (kept > 0 && s >= kept) ? kept : 0;
+      if (j0 > 0) {
 #pragma unroll
-      for (int r = 0; r < R; ++r)
+        for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int k = 0; k < K; ++k) Uf[r][k] = X[r][k];
-      for (int j = 0; j < s; ++j) {
+          for (int k = 0; k < K; ++k) Uf[r][k] = s_uin[((w * R + r) * K + k) * 64 + lane];
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int k = 0; k < K; ++k) Uf[r][k] = X[r][k];
+      }
+      for (int j = j0; j < s; ++j) {
         const SosSec<E> qj = load_sec(a, b, j);
         SV hj[R];
 #pragma unroll
