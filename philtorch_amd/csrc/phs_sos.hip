@@ -58,6 +58,30 @@ size_t ws_bytes_for(int64_t B, int64_t T, int S, bool backward) {
 
 bool sizes_ok(int64_t B, int64_t T, int S) { return B >= 0 && T >= 0 && S >= 1 && S <= kSosMaxSections; }
 
+// Dynamic LDS a launch of `kernel` may take on the current device: the
+// device's LDS per workgroup less the kernel's static LDS (cached per kernel
+// and device; 64 KiB less static where the query fails).
+size_t lds_limit(const void *kernel) {
+  static std::mutex mu;
+  static std::map<std::pair<const void *, int>, size_t> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(kernel, dev);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int per_block = 0;
+  hipFuncAttributes attr{};
+  size_t stat = 0;
+  if (hipFuncGetAttributes(&attr, kernel) == hipSuccess) stat = attr.sharedSizeBytes;
+  if (dev < 0 || hipDeviceGetAttribute(&per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+      per_block <= 0)
+    per_block = 64 << 10;
+  const size_t out = size_t(per_block) > stat ? size_t(per_block) - stat : 0;
+  cache[key] = out;
+  return out;
+}
+
 // Where the coefficients lie: a [rows, S, 6] sos array (shared: one row
 // for all), or one biquad as lfilter's b [rows, nb] and a [rows, 2] at their
 // own row strides (0 = shared).
@@ -145,10 +169,19 @@ int sos_bwd(int64_t B, int64_t T, int S, const SosCoefs &k, const void *x, const
   a.vec_ok = (size_t(T) * sizeof(E)) % 16 == 0 && aligned16(gy) && aligned16(gx) && (!grad || aligned16(x));
   const unsigned grid = a.per_stripe * kStripes;
   if (grad) {
-    // lane entry states of every section, then the kept section's input
-    const size_t lds = size_t(S) * Sh::kWaves * Sh::R * 64 * sizeof(Vec2<E>) +
-                       (sos_kept_section(S) > 0 ? size_t(Sh::kWaves) * Sh::R * Sh::K * 64 * sizeof(E) : 0);
-    launch_kernel((sos_kernel<E, Sh, true, true>), dim3(grid), dim3(Sh::kThreads), lds, stream, a);
+    // lane entry states of every section, then the kept sections' inputs:
+    // every third section where the device's LDS per workgroup allows two
+    // slots (gfx950: 160 KiB), else every other
+    const auto kernel = sos_kernel<E, Sh, true, true>;
+    const size_t laneh = size_t(S) * Sh::kWaves * Sh::R * 64 * sizeof(Vec2<E>);
+    const size_t slot = size_t(Sh::kWaves) * Sh::R * Sh::K * 64 * sizeof(E);
+    const size_t limit = lds_limit(reinterpret_cast<const void *>(kernel));
+    int step = S >= 2 ? (S + 2) / 3 : 0;
+    if (step > 0 && laneh + sos_kept_slots(S, step) * slot > limit) step = (S + 1) / 2;
+    if (step > 0 && laneh + sos_kept_slots(S, step) * slot > limit) step = 0;
+    a.kept_step = step;
+    const size_t lds = laneh + sos_kept_slots(S, step) * slot;
+    launch_kernel(kernel, dim3(grid), dim3(Sh::kThreads), lds, stream, a);
     if (hipGetLastError() != hipSuccess) return PHS_ERR_LAUNCH;
     const int64_t rows = k.coef_shared() ? 1 : B;
     hipLaunchKernelGGL((sos_grad_reduce_kernel<E, Sh>), dim3(unsigned(rows * S)), dim3(kSosReduceThreads), 0,

@@ -43,11 +43,14 @@ constexpr int kSosCkpt = 512;          // steps between forward state checkpoint
 constexpr int kSosMaxSections = 8;     // sections per launch (LDS of the gradient backward)
 
 // The gradient backward needs every section's forward input inside its tile.
-// Its forward recompute keeps the input of the middle section S/2 in LDS (for
-// S >= 2), so that re-deriving the input of section s runs sections
-// [0, s) or [S/2, s) from their lane states: at most S/2 sections instead of
-// s (C4's eight sections: 12 section runs per tile instead of 28).
-__host__ __device__ constexpr int sos_kept_section(int S) { return S >= 2 ? S / 2 : 0; }
+// Its forward recompute keeps in LDS the inputs of sections kept_step and
+// 2 kept_step (those below S), so that re-deriving the input of section s
+// runs only the sections from the nearest kept one below it: C4's eight
+// sections with kept_step 3 take 7 section runs per tile instead of 28.
+constexpr int kSosKeptSlots = 2;
+__host__ __device__ constexpr int sos_kept_slots(int S, int step) {
+  return step <= 0 ? 0 : (step < S ? 1 : 0) + (2 * step < S ? 1 : 0);
+}
 
 // Tile shape: W data waves plus one look-back wave; K steps per lane and
 // round (a power of two dividing kSosCkpt), R rounds (a power of two).
@@ -93,6 +96,7 @@ struct SosArgs {
   unsigned agg_only;           // testing: tiles after a row's first publish no inclusive state
   uint64_t *status;            // [B, S, tiles, kStride] status words of this call
   int vec_ok;
+  int kept_step;               // gradient backward: sections whose input stays in LDS (0: none)
 };
 
 // One section, in the form the steps use.
@@ -733,8 +737,8 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
   __shared__ uint64_t s_look[kSosLookWords];
   __shared__ M s_fagg[GRAD ? 2 : 1][W];  // forward recompute: wave aggregates, two visits in flight
   __shared__ SecPowers<C> s_pow[3];
-  // GRAD: lane entry states [S][W][R][64], then the kept section's input
-  // [W][R][K][64] (sos_kept_section)
+  // GRAD: lane entry states [S][W][R][64], then the kept sections' inputs
+  // [slot][W][R][K][64] (slot i: section (i + 1) kept_step)
   extern __shared__ __align__(16) unsigned char sos_dyn[];
   SV *s_laneh = reinterpret_cast<SV *>(sos_dyn);
   E *s_uin = reinterpret_cast<E *>(sos_dyn + size_t(a.S) * W * R * 64 * sizeof(SV));
@@ -845,14 +849,15 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
 #pragma unroll
       for (int k = 0; k < K; ++k) F[r][k] = X[r][k];
     const int64_t ck0 = (qf * Sh::kTile) / kSosCkpt;
-    const int kept = sos_kept_section(S);
+    const int ks = a.kept_step;
     for (; v < S; ++v) {
       const int s = v;
-      if (kept > 0 && s == kept) {
+      if (ks > 0 && s > 0 && s % ks == 0 && s / ks <= kSosKeptSlots) {
+        E *dst = s_uin + size_t(s / ks - 1) * W * R * K * 64;
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int k = 0; k < K; ++k) s_uin[((w * R + r) * K + k) * 64 + lane] = F[r][k];
+          for (int k = 0; k < K; ++k) dst[((w * R + r) * K + k) * 64 + lane] = F[r][k];
       }
       const SosSec<E> q = load_sec(a, b, s);
       const SecPowers<C> &t = s_pow[v % 3];
@@ -894,13 +899,15 @@ __global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
     // previous visit's input)
     E Uf[GRAD ? R : 1][GRAD ? K : 1];
     if constexpr (GRAD) {
-      const int kept = sos_kept_section(S);
-      const int j0 = (kept > 0 && s >= kept) ? kept : 0;
+      const int ks = a.kept_step;
+      const int slot = ks > 0 ? (s / ks < kSosKeptSlots ? s / ks : kSosKeptSlots) : 0;  // kept sections <= s
+      const int j0 = slot * ks;
       if (j0 > 0) {
+        const E *src = s_uin + size_t(slot - 1) * W * R * K * 64;
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int k = 0; k < K; ++k) Uf[r][k] = s_uin[((w * R + r) * K + k) * 64 + lane];
+          for (int k = 0; k < K; ++k) Uf[r][k] = src[((w * R + r) * K + k) * 64 + lane];
       } else {
 #pragma unroll
         for (int r = 0; r < R; ++r)
