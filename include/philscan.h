@@ -272,9 +272,11 @@ int phs_sosfilt_bwd(int dtype, int64_t B, int64_t T, int S, const void *sos, int
                     const void *ckpt, const void *grad_y, const void *grad_zf, void *grad_x, void *grad_sos,
                     void *grad_zi, void *workspace, size_t workspace_bytes, void *stream);
 
-/* ---- One biquad given as lfilter's b and a where they lie (the cascade
- * kernel at S = 1 without an sos array; lfilter(b, a, x, form="tdf2"),
- * philtorch/lti/filtering.py:211-333, for a second-order filter): b [B, nb]
+/* ---- One biquad given as lfilter's b and a where they lie (no sos array;
+ * lfilter(b, a, x, form="tdf2"), philtorch/lti/filtering.py:211-333, for a
+ * second-order filter: the forward is the state-space kernel's pass of the
+ * TDF-II model, which also writes the checkpoints, the backward the cascade
+ * kernel at S = 1): b [B, nb]
  * (nb = 1..3, missing taps zero) and a [B, 2] (after the leading 1), each
  * row at its own stride in elements (0 = one filter for all rows, inner
  * stride 1); zi, zf [B, 2]; ckpt as phs_sosfilt_fwd's at S = 1; workspace

@@ -285,4 +285,12 @@ int launch_blockn(int dtype, int64_t B, int64_t T, bool TV, bool shared, bool ba
 template <int M>
 size_t ws_blockn(int dtype, int64_t B, int64_t T, bool TV, bool shared, bool backward);
 
+// One biquad's forward on the state-space kernel with the fused cascade's
+// checkpoints, and its workspace bytes (defined in phs_ss.hip; the biquad
+// entry points live in phs_sos.hip).
+int biquad_fwd_ss(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_t b_row_stride, const void *a,
+                  int64_t a_row_stride, const void *zi, const void *x, void *y, void *zf, void *ckpt, int64_t n_ckpt,
+                  int ckpt_every, void *workspace, size_t ws_bytes, hipStream_t stream);
+size_t biquad_ss_ws_bytes(int dtype, int64_t B, int64_t T);
+
 }  // namespace phs

@@ -51,7 +51,9 @@ inline int64_t n_ckpt(int64_t T) { return (T + kSosCkpt - 1) / kSosCkpt; }
 
 template <typename E>
 size_t ws_bytes_for(int64_t B, int64_t T, int S, bool backward) {
-  const size_t f = sos_layout<E, SosFwd<E>>(B, T, S, false).total;
+  size_t f = sos_layout<E, SosFwd<E>>(B, T, S, false).total;
+  // one section: the biquad forward runs the state-space kernel
+  if (S == 1) f = std::max(f, biquad_ss_ws_bytes(std::is_same<E, float>::value ? PHS_F32 : PHS_F64, B, T));
   if (!backward) return f;
   return std::max(f, sos_layout<E, SosBwd<E>>(B, T, S, true).total);
 }
@@ -258,13 +260,14 @@ phs::SosCoefs biquad_coefs(const void *b, int nb, int64_t b_row_stride, const vo
 int phs_biquad_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_t b_row_stride, const void *a,
                    int64_t a_row_stride, const void *zi, const void *x, void *y, void *zf, void *ckpt,
                    void *workspace, size_t workspace_bytes, void *stream) {
-  const hipStream_t st = static_cast<hipStream_t>(stream);
-  const phs::SosCoefs k = biquad_coefs(b, nb, b_row_stride, a, a_row_stride);
-  switch (dtype) {
-    case PHS_F32: return phs::sos_fwd<float>(B, T, 1, k, zi, x, y, zf, ckpt, workspace, workspace_bytes, st);
-    case PHS_F64: return phs::sos_fwd<double>(B, T, 1, k, zi, x, y, zf, ckpt, workspace, workspace_bytes, st);
-    default: return PHS_ERR_DTYPE;
-  }
+  // the plain state-space pass of the TDF-II model (shorter than the
+  // cascade kernel at one section), writing the cascade's checkpoints for
+  // phs_biquad_bwd
+  if (dtype != PHS_F32 && dtype != PHS_F64) return PHS_ERR_DTYPE;
+  if (nb < 1 || nb > 3) return PHS_ERR_INVALID;
+  return phs::biquad_fwd_ss(dtype, B, T, b, nb, b_row_stride, a, a_row_stride, zi, x, y, zf, ckpt,
+                            phs::n_ckpt(T), phs::kSosCkpt, workspace, workspace_bytes,
+                            static_cast<hipStream_t>(stream));
 }
 
 int phs_biquad_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_t b_row_stride, const void *a,

@@ -475,6 +475,48 @@ int ss_dispatch(int dtype, int M, F &&f) {
 }
 
 }  // namespace
+
+// One biquad, lfilter(b, a, form="tdf2") with b [rows, nb] and a [rows, 2] at
+// their own row strides (0 = shared), as the plain state-space pass, writing
+// the fused cascade's checkpoints at one section (the state entering every
+// ckpt_every-th step, [B, n_ckpt] in compute precision; nullable) for its
+// gradient backward (phs_biquad_fwd).
+int biquad_fwd_ss(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_t b_row_stride, const void *a,
+                  int64_t a_row_stride, const void *zi, const void *x, void *y, void *zf, void *ckpt, int64_t n_ckpt,
+                  int ckpt_every, void *workspace, size_t ws_bytes, hipStream_t stream) {
+  auto run = [&](auto alg) -> int {
+    using Alg = decltype(alg);
+    SsFilter f;
+    f.b = b, f.a = a, f.nb = nb, f.na = 2, f.form = 1;
+    if (B < 0 || T < 0 || b_row_stride < 0 || a_row_stride < 0 || !ss_filter_ok(f, 2)) return PHS_ERR_INVALID;
+    if (B == 0 || T == 0) return PHS_OK;
+    if (!b || !a || !x || !y || (ckpt && ckpt_every <= 0)) return PHS_ERR_INVALID;
+    if (!ss_grid_ok(B, T, SsShape<Alg>::kTile)) return PHS_ERR_INVALID;
+    SsArgs<Alg> p{};
+    if (!ss_args<Alg>(B, T, f, zi, x, y, zf, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
+    p.f_stride_b = b_row_stride;
+    p.f_stride_a = a_row_stride;
+    p.ckpt = ckpt;
+    p.n_ckpt = n_ckpt;
+    p.ckpt_every = ckpt_every;
+    return ss_launch<Alg, false>(p, stream);
+  };
+  switch (dtype) {
+    case PHS_F32: return run(Block2<float>{});
+    case PHS_F64: return run(Block2<double>{});
+    default: return PHS_ERR_DTYPE;
+  }
+}
+
+size_t biquad_ss_ws_bytes(int dtype, int64_t B, int64_t T) {
+  if (B <= 0 || T <= 0) return 0;
+  switch (dtype) {
+    case PHS_F32: return ss_ws_bytes<Block2<float>>(B, T);
+    case PHS_F64: return ss_ws_bytes<Block2<double>>(B, T);
+    default: return 0;
+  }
+}
+
 }  // namespace phs
 
 extern "C" {

@@ -92,6 +92,12 @@ struct SsArgs {
   unsigned agg_only;  // testing: tiles after a row's first publish no inclusive state
   uint64_t *status;
   int vec_ok;
+  // plain forward of a second-order model (nullable): the state entering
+  // every ckpt_every-th step, in compute precision, [B, n_ckpt] (the
+  // checkpoints the fused cascade's gradient backward reads at one section)
+  void *ckpt;
+  int64_t n_ckpt;
+  int ckpt_every;
 };
 
 // Kernel modes: the model's output (plain), the states of a forward for the
@@ -849,6 +855,10 @@ __global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), 2) void ss_kernel(S
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
+    if constexpr (MODE == kSsPlain && !REV && V::M == 2) {
+      if (a.ckpt && t0s[r] < T && t0s[r] % a.ckpt_every == 0)
+        reinterpret_cast<S *>(a.ckpt)[b * a.n_ckpt + t0s[r] / a.ckpt_every] = Alg::sadd(ent[r], ex[r]);
+    }
     SS h = Alg::store_s(Alg::sadd(ent[r], ex[r]));
     E O[K];
 #pragma unroll
