@@ -175,7 +175,7 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
   if (!workspace || ws_bytes < L.total) return PHS_ERR_WORKSPACE;
 
   char *ws = static_cast<char *>(workspace);
-  ScanArgs<Alg> a;
+  ScanArgs<Alg> a{};
   a.coef = static_cast<const E *>(coef);
   a.coef_row_stride = shared ? 0 : (TV ? T : 1);
   a.zi = static_cast<const E *>(zi);

@@ -719,8 +719,14 @@ __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const S
 // section's entry state.  Barriers: claim; powers of the first two visits; one per
 // forward-recompute visit (GRAD); two per look-back visit (wave aggregates
 // ready, entry state ready).
+// The fp32 forward is held to 128 VGPRs (four waves per SIMD: 103 against
+// 106.5 us at C4, 18 VGPRs spilled); the backward and fp64 keep their
+// registers (their spills at that bound would cost more than the waves gain).
+template <typename E, bool REV>
+constexpr int kSosMinWaves = (!REV && sizeof(E) == 4) ? 4 : 1;
+
 template <typename E, class Sh, bool REV, bool GRAD>
-__global__ __launch_bounds__(Sh::kThreads, 1) void sos_kernel(SosArgs<E> a) {
+__global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kernel(SosArgs<E> a) {
   using Alg = Block2<E>;
   using C = typename Wide<E>::type;
   using V = Vec2<C>;
