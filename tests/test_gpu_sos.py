@@ -414,6 +414,46 @@ def test_biquad_capi_reads_b_and_a_in_place(api, dtype, layout, nb):
     D.check(ga.cpu().numpy(), rgs[:, 4:6], "grad_a", dtype=dtype)
 
 
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_biquad_forward_checkpoints_match_cascade_kernel(api, dtype):
+    """phs_biquad_fwd runs the state-space kernel's pass and writes the
+    checkpoints the cascade backward reads: the state entering every 512th
+    step, the same values phs_sosfilt_fwd's cascade kernel at S = 1 writes
+    for the same filter (to the parity bar), with equal outputs and zf."""
+    import torch
+
+    lib, ws, capi = api
+    g = D.rng(D.seed_of("biquad-ckpt", np.dtype(dtype).str))
+    B, T = 3, 3 * 6144 + 77
+    dt = capi.DTYPES[np.dtype(dtype)]
+    sos = D.sos_coefs(g, (B,), 1, dtype)  # (B, 1, 6)
+    x, zi = D.normal(g, (B, T), dtype), D.normal(g, (B, 1, 2), dtype)
+    tsos, tx, tz = _dev(sos), _dev(x), _dev(zi)
+    need = lib.phs_sosfilt_workspace_size(dt, B, T, 1, 0)
+    nck = lib.phs_sosfilt_ckpt_size(dt, B, T, 1)
+    outs = []
+    for route in ("biquad", "sosfilt"):
+        ck = torch.full((nck // 8,), float("nan"), dtype=torch.float64, device="cuda")
+        y, zf = torch.empty_like(tx), torch.empty((B, 1, 2), dtype=tx.dtype, device="cuda")
+        print(f"biquad ckpt {np.dtype(dtype).name} {route}", flush=True)
+        if route == "biquad":
+            tb, ta = tsos[:, 0, 0:3], tsos[:, 0, 4:6]
+            rc = lib.phs_biquad_fwd(dt, B, T, _p(tb), 3, tb.stride(0), _p(ta), ta.stride(0), _p(tz), _p(tx), _p(y),
+                                    _p(zf), _p(ck), _p(ws), need, _stream())
+        else:
+            rc = lib.phs_sosfilt_fwd(dt, B, T, 1, _p(tsos), 0, _p(tz), _p(tx), _p(y), _p(zf), _p(ck), _p(ws), need,
+                                     _stream())
+        assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+        torch.cuda.synchronize()
+        outs.append([t.cpu().numpy() for t in (ck, y, zf)])
+    (ck1, y1, zf1), (ck2, y2, zf2) = outs
+    assert np.isfinite(ck1).all() and np.isfinite(ck2).all()
+    assert ck1.size == B * ((T + 511) // 512) * 2
+    D.check(ck1, ck2, "ckpt", dtype=dtype)
+    D.check(y1, y2, "y", dtype=dtype)
+    D.check(zf1, zf2, "zf", dtype=dtype)
+
+
 def test_biquad_op_gradients_and_opcheck(hip):
     """philtorch::biquad through autograd: strided columns of a coefficient
     table (the C4 caller pattern), gradcheck (the fused backward),
