@@ -292,11 +292,15 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
-  __syncthreads();
-  if (s_id >= a.tiles) return;  // padding of the last stripe round
-  const int64_t id = s_id;
-  const unsigned tag = s_tag;
+  // the tile is the workgroup's index (dispatch order puts a tile's row
+  // predecessors first); the look-back wave claims for the call's tag
+  // (claim_tag), so the data waves' loads do not wait for the claim
+  const int64_t id = blockIdx.x;
+  if (id >= a.tiles) {  // padding of the last stripe round: counted, then gone
+    if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
+    return;
+  }
+  unsigned tag = 0;
   const int64_t q = id / a.B;  // tile position along the row
   const int64_t b = id - q * a.B;
   const int64_t T = a.T_len;
@@ -305,6 +309,7 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
 
   if (w == kWaves) {
     // ================= look-back wave
+    tag = claim_tag(a.claims, a.per_stripe, lane);
     uint64_t *row_status = a.status + b * a.tiles_per_row * St::kStride;
     const S virt = a.zi ? Alg::load_s(V::load_vec(a.zi + b * V::M)) : Alg::szero();
     __syncthreads();  // wave aggregates are in s_wagg

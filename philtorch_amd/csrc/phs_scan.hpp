@@ -155,6 +155,16 @@ __device__ __forceinline__ void claim_tile(unsigned long long *claims, unsigned 
     __hip_atomic_store(w, (unsigned long long)(epoch + 1u) << 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The call's tag for a workgroup whose tile is its own index (kernels with a
+// look-back wave: the data waves load at once, the look-back wave claims
+// from the stripe, which counts the workgroup for the re-arming and gives the
+// tag).  Called by the whole look-back wave; lane 0 claims.
+__device__ __forceinline__ unsigned claim_tag(unsigned long long *claims, unsigned per_stripe, int lane) {
+  unsigned cid = 0, ctag = 0;
+  if (lane == 0) claim_tile(claims, per_stripe, cid, ctag);
+  return __builtin_amdgcn_readfirstlane(ctag);
+}
+
 // ------------------------------------------------------------ status words
 template <typename X>
 __device__ __forceinline__ void publish(uint64_t *dst, const X &v, unsigned tag) {

@@ -751,11 +751,15 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
-  __syncthreads();
-  if (s_id >= a.tiles) return;  // padding of the last stripe round
-  const int64_t id = s_id;
-  const unsigned tag = s_tag;
+  // the tile is the workgroup's index (dispatch order puts a tile's row
+  // predecessors first); the look-back wave claims for the call's tag
+  // (claim_tag), so the data waves' loads do not wait for the claim
+  const int64_t id = blockIdx.x;
+  if (id >= a.tiles) {  // padding of the last stripe round: counted, then gone
+    if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
+    return;
+  }
+  unsigned tag = 0;
   const int64_t qs = id / a.B;  // position in scan order
   const int64_t b = id - qs * a.B;
   const int64_t tiles = a.tiles_per_row;
@@ -775,6 +779,7 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
     build_powers<E, K, R>(&s_pow[0], load_sec(a, b, vis_sec(0)), lane);
     if (nvis > 1) build_powers<E, K, R>(&s_pow[1], load_sec(a, b, vis_sec(1)), lane);
     __syncthreads();  // powers of the first two visits
+    tag = claim_tag(a.claims, a.per_stripe, lane);
     int v = 0;
     if constexpr (GRAD) {
       for (; v < S; ++v) {

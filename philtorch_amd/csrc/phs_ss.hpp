@@ -730,11 +730,15 @@ __global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), 2) void ss_kernel(S
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
-  __syncthreads();
-  if (s_id >= a.tiles) return;  // padding of the last stripe round
-  const int64_t id = s_id;
-  const unsigned tag = s_tag;
+  // the tile is the workgroup's index (dispatch order puts a tile's row
+  // predecessors first); the look-back wave claims for the call's tag
+  // (claim_tag), so the data waves' loads do not wait for the claim
+  const int64_t id = blockIdx.x;
+  if (id >= a.tiles) {  // padding of the last stripe round: counted, then gone
+    if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
+    return;
+  }
+  unsigned tag = 0;
   const int64_t q = id / a.B;  // tile position along the row
   const int64_t b = id - q * a.B;
   const int64_t T = a.T_len;
@@ -761,6 +765,7 @@ __global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), 2) void ss_kernel(S
       }
     }
     __syncthreads();  // power tables
+    tag = claim_tag(a.claims, a.per_stripe, lane);
     uint64_t *row_status = a.status + b * a.tiles_per_row * St::kStride;
     // The row's entry state.  A zero-phase pass derives it from the row's
     // edge, which only tile 0 needs: tile 0 publishes inclusive states only,
