@@ -13,16 +13,21 @@
 namespace phs {
 namespace {
 
-// Forward tiles: fp32 16 steps per lane in two rounds (6144-step tiles:
-// 110 us for C4's eight sections against 120 with four rounds and 119-151
-// for 8- or 32-step lanes), fp64 8 steps in four rounds; a lane's rounds are
-// independent chains and run interleaved.  The gradient backward keeps four
+// Forward tiles: fp32 16 steps per lane in two rounds (against four rounds
+// and 8- or 32-step lanes, measured with 3 data waves), fp64 8 steps in four
+// rounds; a lane's rounds are independent chains and run interleaved.  The
+// forward holds few registers (fp32 128: four waves per SIMD), so its
+// workgroups are wide, 15 data waves (fp32; fp64 7) beside the look-back
+// wave: a CU's wave slots hold one tile, 15/16 of them signal, and C4's call
+// is 256 tiles of 30720 steps, all resident at once.  With 3 data waves it
+// was 1264 tiles on 1024 resident slots, two generations: 92.3 -> 77.0 us.
+// The gradient backward keeps four
 // arrays of a lane's steps live and an LDS table of lane states per lane and
 // round: fp32 takes 32 steps in one round (236 VGPRs, no spills; 4% faster
 // at C4 than 16 steps in two rounds, which cost a second table entry and a
 // second round of multipliers), fp64 8 steps in one round.
 template <typename E>
-using SosFwd = std::conditional_t<sizeof(E) == 4, SosShape<E, 16, 2, 3>, SosShape<E, 8, 4, 3>>;
+using SosFwd = std::conditional_t<sizeof(E) == 4, SosShape<E, 16, 2, 15>, SosShape<E, 8, 4, 7>>;
 template <typename E>
 using SosBwd = std::conditional_t<sizeof(E) == 4, SosShape<E, 32, 1, 3>, SosShape<E, 8, 1, 3>>;
 

@@ -169,18 +169,32 @@ struct SecPowers {
   Mat2<C> seg;
 };
 
-template <typename E, int K, int R>
-__device__ __forceinline__ void build_powers(SecPowers<typename Wide<E>::type> *t, const SosSec<E> &q, int lane) {
+// W > 0: also wm[j] = seg^j for j = 0..W (the matrix parts of the tile's
+// wave prefixes; wm[W] is the tile matrix).
+template <typename E, int K, int R, int W = 0>
+__device__ __forceinline__ void build_powers(SecPowers<typename Wide<E>::type> *t, const SosSec<E> &q, int lane,
+                                             Mat2<typename Wide<E>::type> *wm = nullptr) {
   using Alg = Block2<E>;
-  Mat2<typename Wide<E>::type> P[7];
+  using Mt = Mat2<typename Wide<E>::type>;
+  Mt P[7];
   sec_powers<E, K, 7>(sec_matrix(q), P);
   t->pw[lane] = lane_power<E, 7>(P, lane);
+  Mt seg = P[6];
+#pragma unroll
+  for (int r = 1; r < R; r <<= 1) seg = Alg::cmul(seg, seg);
   if (lane == 0) {
     t->pw[64] = P[6];
-    Mat2<typename Wide<E>::type> seg = P[6];
-#pragma unroll
-    for (int r = 1; r < R; r <<= 1) seg = Alg::cmul(seg, seg);
     t->seg = seg;
+  }
+  if constexpr (W > 0) {
+    static_assert(W < 64, "one lane per power");
+    Mt m = Alg::cone();
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      if (lane == j) wm[j] = m;
+      m = Alg::cmul(seg, m);
+    }
+    if (lane == W) wm[W] = m;
   }
 }
 
@@ -743,6 +757,11 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
   __shared__ uint64_t s_look[kSosLookWords];
   __shared__ M s_fagg[GRAD ? 2 : 1][W];  // forward recompute: wave aggregates, two visits in flight
   __shared__ SecPowers<C> s_pow[3];
+  // wide tiles: seg^j (j <= W) in LDS beside s_pow, built with it; narrow
+  // ones keep the W + 1 matrices in the look-back wave's registers
+  constexpr bool kWmatLds = W > 4;
+  constexpr int kWm = kWmatLds ? W : 0;
+  __shared__ Mt s_wmat[3][kWm + 1];
   // GRAD: lane entry states [S][W][R][64], then the kept sections' inputs
   // [slot][W][R][K][64] (slot i: section (i + 1) kept_step)
   extern __shared__ __align__(16) unsigned char sos_dyn[];
@@ -776,15 +795,16 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
 
   if (w == W) {
     // ================= look-back wave
-    build_powers<E, K, R>(&s_pow[0], load_sec(a, b, vis_sec(0)), lane);
-    if (nvis > 1) build_powers<E, K, R>(&s_pow[1], load_sec(a, b, vis_sec(1)), lane);
+    build_powers<E, K, R, kWm>(&s_pow[0], load_sec(a, b, vis_sec(0)), lane, s_wmat[0]);
+    if (nvis > 1) build_powers<E, K, R, kWm>(&s_pow[1], load_sec(a, b, vis_sec(1)), lane, s_wmat[1]);
     __syncthreads();  // powers of the first two visits
     tag = claim_tag(a.claims, a.per_stripe, lane);
     int v = 0;
     if constexpr (GRAD) {
       for (; v < S; ++v) {
         __syncthreads();  // forward recompute: wave aggregates of visit v
-        if (v + 2 < nvis) build_powers<E, K, R>(&s_pow[(v + 2) % 3], load_sec(a, b, vis_sec(v + 2)), lane);
+        if (v + 2 < nvis)
+          build_powers<E, K, R, kWm>(&s_pow[(v + 2) % 3], load_sec(a, b, vis_sec(v + 2)), lane, s_wmat[(v + 2) % 3]);
       }
     }
     for (; v < nvis; ++v) {
@@ -793,13 +813,16 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
       const SV vs = load_pair(a.virt + (b * S + s) * 2, a.virt != nullptr && row_virt);
       const V virt = {up(vs.v0), up(vs.v1)};
       // matrices of this section, before the aggregates are in: one wave
-      // segment (Mw), its powers up to the tile matrix G, and G's powers
+      // segment (Mw), the tile matrix G = Mw^W and G's powers
       const Mt Mw = maybe_transpose<REV>(s_pow[v % 3].seg);
-      Mt Mp[W + 1];
+      Mt Mp[kWmatLds ? 1 : W + 1];
       Mp[0] = Alg::cone();
+      if constexpr (!kWmatLds) {
 #pragma unroll
-      for (int j = 1; j <= W; ++j) Mp[j] = Alg::cmul(Mw, Mp[j - 1]);
-      const TilePowers<C> tp = tile_powers<E>(Mp[W], lane);
+        for (int j = 1; j <= W; ++j) Mp[j] = Alg::cmul(Mw, Mp[j - 1]);
+      }
+      const Mt G = kWmatLds ? maybe_transpose<REV>(s_wmat[v % 3][W]) : Mp[kWmatLds ? 0 : W];
+      const TilePowers<C> tp = tile_powers<E>(G, lane);
       // (polling for the predecessors before the aggregates are in measured
       // slower: a tile's predecessors reach each section about when it does)
       V yin = virt;
@@ -809,7 +832,7 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
       V pv = Alg::szero();
 #pragma unroll
       for (int j = 0; j < W; ++j) {
-        if (lane == 0) s_wpre[j] = M{Mp[j], pv};
+        if (lane == 0) s_wpre[j] = M{kWmatLds ? maybe_transpose<REV>(s_wmat[v % 3][j]) : Mp[kWmatLds ? 0 : j], pv};
         pv = Alg::affine(Mw, pv, s_wagg[j].x);
       }
       if (qs > 0) {
@@ -818,10 +841,11 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
           yin = sos_prefix_fallback<E, Sh, REV>(a, b, s, qs * Sh::kTile, lane, s_look);
       }
       if (qs + 1 < tiles && lane == 0 && !(a.agg_only && qs > 0))
-        publish(row_status + qs * kSosStatusWords, Alg::affine(Mp[W], yin, pv), tag);
+        publish(row_status + qs * kSosStatusWords, Alg::affine(G, yin, pv), tag);
       if (lane == 0) s_in = yin;
       __syncthreads();  // entry state is in s_in
-      if (v + 2 < nvis) build_powers<E, K, R>(&s_pow[(v + 2) % 3], load_sec(a, b, vis_sec(v + 2)), lane);
+      if (v + 2 < nvis)
+        build_powers<E, K, R, kWm>(&s_pow[(v + 2) % 3], load_sec(a, b, vis_sec(v + 2)), lane, s_wmat[(v + 2) % 3]);
     }
     return;
   }
