@@ -321,8 +321,9 @@ class SosFused(Workload):
         self.cpu = [v.float() for v in (sos, x, gy)]
         self.dev = [v.cuda() for v in self.cpu]
         self.samples = B * T
-        self.fwd_bytes = 8 * B * T  # read x, write y (state checkpoints: 1/32 of that)
-        self.bwd_bytes = 12 * B * T  # read x and grad y, write grad x
+        ck = 16 * B * T // 32  # per section: an fp64 state pair per 32 steps (the backward's lane chunk)
+        self.fwd_bytes = 8 * B * T + S * ck  # read x; write y and the state checkpoints
+        self.bwd_bytes = 12 * B * T + S * ck  # read x, grad y and the checkpoints; write grad x
         self.launches = 1
         self.kernel = "sos_kernel"
 
@@ -356,7 +357,9 @@ class SosApi(SosFused):
         self.name = "c4_api"
         self.metric = f"GSamples/s fwd+bwd, lti.lfilter cascade x{self.S} (grad x, b, a) B={self.B} T={self.T} fp32 (API)"
         self.launches = self.S
-
+        ck = 16 * self.B * self.T // 32  # one section's state checkpoints
+        self.fwd_bytes = 8 * self.B * self.T + ck  # per lfilter
+        self.bwd_bytes = 12 * self.B * self.T + ck
     def step_fwd(self):
         import torch
         from philtorch_amd import lti

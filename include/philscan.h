@@ -254,7 +254,8 @@ int phs_lti_recurN_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, in
 size_t phs_sosfilt_workspace_size(int dtype, int64_t B, int64_t T, int S, int backward);
 
 /* Bytes of the state checkpoints the forward writes for the backward's
- * coefficient gradients (every 512th step of every section, in fp64). */
+ * coefficient gradients: the state entering every 32nd step (PHS_F32; every
+ * 8th for PHS_F64) of every section, as fp64 pairs. */
 size_t phs_sosfilt_ckpt_size(int dtype, int64_t B, int64_t T, int S);
 
 /* Forward.  zi NULL = zero initial states; zf and ckpt are skipped when NULL.

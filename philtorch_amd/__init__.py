@@ -268,9 +268,16 @@ def _has_op(name: str) -> bool:
 
 # (a _C.so built before the cascade ops existed lacks them; the in-tree build
 # imports this package before it rebuilds that library)
+def _n_ckpt(x, T):
+    """Forward state checkpoints per row and section of the cascade ops."""
+    every = 32 if x.dtype == torch.float32 else 8
+    return (T + every - 1) // every
+
+
 if EXTENSION_LOADED and _has_op("sosfilt"):
     # fused cascade of second-order sections: (y, zf, ckpt); ckpt holds the
-    # forward's state checkpoints (every 512th step, fp64) for the backward
+    # forward's state checkpoints (fp64 pairs, every 32nd step for float32
+    # and every 8th for float64: the gradient backward's lane chunks)
     @torch.library.register_fake("philtorch::sosfilt")
     def _(sos, zi, x):
         torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
@@ -281,7 +288,7 @@ if EXTENSION_LOADED and _has_op("sosfilt"):
         B, T, S = x.shape[0], x.shape[1], sos.shape[-2]
         if zi is not None:
             torch._check(tuple(zi.shape) == (B, S, 2), lambda: "zi must be (batch, sections, 2)")
-        return (_fake_like(x), x.new_empty((B, S, 2)), x.new_empty((B, S, (T + 511) // 512, 2), dtype=torch.float64))
+        return (_fake_like(x), x.new_empty((B, S, 2)), x.new_empty((B, S, _n_ckpt(x, T), 2), dtype=torch.float64))
 
     @torch.library.register_fake("philtorch::sosfilt_backward")
     def _(sos, x, ckpt, grad_y, grad_zf, need_sos):
@@ -335,7 +342,7 @@ if EXTENSION_LOADED and _has_op("biquad"):
         torch._check(b.ndim == a.ndim and b.ndim in (1, 2), lambda: "b and a must both be 1D or both 2D")
         torch._check(1 <= b.shape[-1] <= 3 and a.shape[-1] == 2, lambda: "a biquad")
         B, T = x.shape
-        return _fake_like(x), x.new_empty((B, 2)), x.new_empty((B, 1, (T + 511) // 512, 2), dtype=torch.float64)
+        return _fake_like(x), x.new_empty((B, 2)), x.new_empty((B, 1, _n_ckpt(x, T), 2), dtype=torch.float64)
 
     @torch.library.register_fake("philtorch::biquad_backward")
     def _(b, a, x, ckpt, grad_y, grad_zf, need_coef):

@@ -63,7 +63,7 @@ const char *phs_error_string(int status) {
   }
 }
 
-int phs_abi_version(void) { return 111; }
+int phs_abi_version(void) { return 112; }
 
 void phs_debug_set_spin_limit(unsigned polls) { phs::g_spin_limit.store(polls, std::memory_order_relaxed); }
 

@@ -52,7 +52,12 @@ SosLayout sos_layout(int64_t B, int64_t T, int S, bool grad) {
   return L;
 }
 
-inline int64_t n_ckpt(int64_t T) { return (T + kSosCkpt - 1) / kSosCkpt; }
+template <typename E>
+int64_t n_ckpt(int64_t T) {
+  return (T + kSosCkptEvery<E> - 1) / kSosCkptEvery<E>;
+}
+inline int64_t n_ckpt_of(int dtype, int64_t T) { return dtype == PHS_F32 ? n_ckpt<float>(T) : n_ckpt<double>(T); }
+inline int ckpt_every_of(int dtype) { return dtype == PHS_F32 ? kSosCkptEvery<float> : kSosCkptEvery<double>; }
 
 template <typename E>
 size_t ws_bytes_for(int64_t B, int64_t T, int S, bool backward) {
@@ -114,7 +119,7 @@ void fill_common(SosArgs<E> &a, const SosLayout &L, int64_t B, int64_t T, int S,
   a.B = B;
   a.T_len = T;
   a.tiles_per_row = L.tiles_per_row;
-  a.n_ckpt = n_ckpt(T);
+  a.n_ckpt = n_ckpt<E>(T);
   a.S = S;
   a.claims = reinterpret_cast<unsigned long long *>(ws);
   a.status = reinterpret_cast<uint64_t *>(ws + L.status_off);
@@ -215,7 +220,7 @@ size_t phs_sosfilt_workspace_size(int dtype, int64_t B, int64_t T, int S, int ba
 
 size_t phs_sosfilt_ckpt_size(int dtype, int64_t B, int64_t T, int S) {
   if (!phs::sizes_ok(B, T, S) || (dtype != PHS_F32 && dtype != PHS_F64)) return 0;
-  return size_t(B) * size_t(S) * size_t(phs::n_ckpt(T)) * 2 * sizeof(double);
+  return size_t(B) * size_t(S) * size_t(phs::n_ckpt_of(dtype, T)) * 2 * sizeof(double);
 }
 
 int phs_sosfilt_fwd(int dtype, int64_t B, int64_t T, int S, const void *sos, int sos_shared, const void *zi,
@@ -271,7 +276,7 @@ int phs_biquad_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64
   if (dtype != PHS_F32 && dtype != PHS_F64) return PHS_ERR_DTYPE;
   if (nb < 1 || nb > 3) return PHS_ERR_INVALID;
   return phs::biquad_fwd_ss(dtype, B, T, b, nb, b_row_stride, a, a_row_stride, zi, x, y, zf, ckpt,
-                            phs::n_ckpt(T), phs::kSosCkpt, workspace, workspace_bytes,
+                            phs::n_ckpt_of(dtype, T), phs::ckpt_every_of(dtype), workspace, workspace_bytes,
                             static_cast<hipStream_t>(stream));
 }
 

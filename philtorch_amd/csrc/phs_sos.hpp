@@ -14,7 +14,8 @@
 // forward values, so one kernel template serves both directions.
 // Coefficient gradients pair mu with the forward input u and state h, which
 // the backward recomputes inside its tile from x and the states the forward
-// kernel checkpoints every kSosCkpt steps.
+// kernel checkpoints every kSosCkptEvery<E> steps: the entry state of every
+// lane chunk of the backward, so the recompute runs each lane on its own.
 //
 // Per tile and section (tile layout as in phs_scan.hpp: data waves own
 // contiguous segments of R rounds of 64*K steps; the backward mirrors waves,
@@ -39,7 +40,10 @@
 
 namespace phs {
 
-constexpr int kSosCkpt = 512;          // steps between forward state checkpoints
+// Steps between forward state checkpoints: the gradient backward's lane
+// chunk (fp32 32 steps, fp64 8), whose entry states the forward writes.
+template <typename E>
+constexpr int kSosCkptEvery = sizeof(E) == 4 ? 32 : 8;
 constexpr int kSosMaxSections = 8;     // sections per launch (LDS of the gradient backward)
 
 // The gradient backward needs every section's forward input inside its tile.
@@ -53,7 +57,8 @@ __host__ __device__ constexpr int sos_kept_slots(int S, int step) {
 }
 
 // Tile shape: W data waves plus one look-back wave; K steps per lane and
-// round (a power of two dividing kSosCkpt), R rounds (a power of two).
+// round (a power of two dividing kSosCkptEvery<E>), R rounds (a power of
+// two).
 template <typename E, int K_, int R_, int W_>
 struct SosShape {
   static constexpr int kWaves = W_;
@@ -63,8 +68,8 @@ struct SosShape {
   static constexpr int kWaveSeg = 64 * K * R;
   static constexpr int kTile = kWaves * kWaveSeg;
   static_assert(R >= 1 && (R & (R - 1)) == 0, "a power-of-two number of rounds");
-  static_assert((K & (K - 1)) == 0 && kSosCkpt % K == 0, "K must be a power of two dividing kSosCkpt");
-  static_assert(kTile % kSosCkpt == 0, "tiles start on checkpoints");
+  static_assert((K & (K - 1)) == 0 && kSosCkptEvery<E> % K == 0, "K must be a power of two dividing kSosCkptEvery");
+  static_assert(kTile % kSosCkptEvery<E> == 0, "tiles start on checkpoints");
   static_assert((K * sizeof(E)) % 16 == 0, "chunks must be whole 16-byte vectors");
 };
 
@@ -83,7 +88,7 @@ struct SosArgs {
   E *out;                  // forward: y;  backward: grad of x (nullable)
   const E *virt;           // forward: zi;  backward: grad of zf  ([B, S, 2], nullable = zeros)
   E *fin;                  // forward: zf;  backward: grad of zi  ([B, S, 2], nullable)
-  Vec2<C> *ckpt;           // [B, S, n_ckpt] states entering every kSosCkpt-th step:
+  Vec2<C> *ckpt;           // [B, S, n_ckpt] states entering every kSosCkptEvery-th step:
                            // written forward (nullable), read by the gradient backward
   const E *x;              // gradient backward: the forward input
   C *partials;             // gradient backward: [B, S, tiles, kWaves, 5] coefficient sums
@@ -727,12 +732,12 @@ __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const S
 // (backward only: recomputes the forward inside the tile from a.x and a.ckpt).
 //
 // The tile visits its sections in order (backward: in reverse order, after,
-// with GRAD, a forward visit of every section).  The look-back wave builds
-// each visit's matrix powers two visits ahead into one of three LDS buffers
+// with GRAD, a recompute of the forward cascade that every lane runs on its
+// own from its checkpointed entry states).  The look-back wave builds each
+// visit's matrix powers two visits ahead into one of three LDS buffers
 // (keeping the data waves' registers free of matrices) and resolves each
-// section's entry state.  Barriers: claim; powers of the first two visits; one per
-// forward-recompute visit (GRAD); two per look-back visit (wave aggregates
-// ready, entry state ready).
+// section's entry state.  Barriers: powers of the first two visits; two per
+// visit (wave aggregates ready, entry state ready).
 // The fp32 forward is held to 128 VGPRs (four waves per SIMD: 103 against
 // 106.5 us at C4, 18 VGPRs spilled); the backward and fp64 keep their
 // registers (their spills at that bound would cost more than the waves gain).
@@ -755,7 +760,6 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
   __shared__ V s_in;
   __shared__ unsigned s_id, s_tag;
   __shared__ uint64_t s_look[kSosLookWords];
-  __shared__ M s_fagg[GRAD ? 2 : 1][W];  // forward recompute: wave aggregates, two visits in flight
   __shared__ SecPowers<C> s_pow[3];
   // wide tiles: seg^j (j <= W) in LDS beside s_pow, built with it; narrow
   // ones keep the W + 1 matrices in the look-back wave's registers
@@ -789,9 +793,9 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
   // the row's state before its first step in scan order; backward it is
   // dL/dzf only when no padded step t = T carries it
   const bool row_virt = !REV || (T % Sh::kTile) == 0;
-  // visit v -> section: forward 0..S-1; backward S-1..0, after 0..S-1 with GRAD
-  const int nvis = GRAD ? 2 * S : S;
-  auto vis_sec = [S](int v) { return GRAD ? (v < S ? v : 2 * S - 1 - v) : (REV ? S - 1 - v : v); };
+  // visit v -> section: forward 0..S-1; backward S-1..0
+  const int nvis = S;
+  auto vis_sec = [S](int v) { return REV ? S - 1 - v : v; };
 
   if (w == W) {
     // ================= look-back wave
@@ -799,15 +803,7 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
     if (nvis > 1) build_powers<E, K, R, kWm>(&s_pow[1], load_sec(a, b, vis_sec(1)), lane, s_wmat[1]);
     __syncthreads();  // powers of the first two visits
     tag = claim_tag(a.claims, a.per_stripe, lane);
-    int v = 0;
-    if constexpr (GRAD) {
-      for (; v < S; ++v) {
-        __syncthreads();  // forward recompute: wave aggregates of visit v
-        if (v + 2 < nvis)
-          build_powers<E, K, R, kWm>(&s_pow[(v + 2) % 3], load_sec(a, b, vis_sec(v + 2)), lane, s_wmat[(v + 2) % 3]);
-      }
-    }
-    for (; v < nvis; ++v) {
+    for (int v = 0; v < nvis; ++v) {
       const int s = vis_sec(v);
       uint64_t *row_status = a.status + ((b * S + s) * tiles) * kSosStatusWords;
       const SV vs = load_pair(a.virt + (b * S + s) * 2, a.virt != nullptr && row_virt);
@@ -873,20 +869,20 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
     for (int r = 0; r < R; ++r) load_chunk<E, K>(a.x + b * T, chunk0(r), T, vec, X[r], zero);
   }
   __syncthreads();  // powers of the first two visits
-  int v = 0;
 
   // ---- backward with coefficient gradients: recompute the forward cascade
-  // over the tile from its checkpoints (time order is descending scan order),
-  // keeping every lane's entry state of every section in LDS
+  // over the lane's chunk from x and the forward's checkpoint of each
+  // section's entry state there (the chunk is one checkpoint interval), no
+  // scan and no barrier; every lane's entry state of every section stays in
+  // LDS for the re-derivations
   if constexpr (GRAD) {
+    static_assert(R == 1 && K == kSosCkptEvery<E>, "a lane chunk is one checkpoint interval");
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int k = 0; k < K; ++k) F[r][k] = X[r][k];
-    const int64_t ck0 = (qf * Sh::kTile) / kSosCkpt;
     const int ks = a.kept_step;
-    for (; v < S; ++v) {
-      const int s = v;
+    for (int s = 0; s < S; ++s) {
       if (ks > 0 && s > 0 && s % ks == 0 && s / ks <= kSosKeptSlots) {
         E *dst = s_uin + size_t(s / ks - 1) * W * R * K * 64;
 #pragma unroll
@@ -895,35 +891,19 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
           for (int k = 0; k < K; ++k) dst[((w * R + r) * K + k) * 64 + lane] = F[r][k];
       }
       const SosSec<E> q = load_sec(a, b, s);
-      const SecPowers<C> &t = s_pow[v % 3];
-      V ex[R], tot[R], x[R];
-      fold_fwd_n<E, K, R>(q, F, x);
-      lti_scan<false, false>(x, lane, t);
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        tot[r] = read_lane(x[r], 0);
-        ex[r] = lane_prev<false>(x[r], lane, Alg::szero());
-      }
-      V agg = tot[R - 1];
-#pragma unroll
-      for (int r = R - 2; r >= 0; --r) agg = mva<false>(t.pw[64], agg, tot[r]);
-      if (lane == 0) s_fagg[s & 1][w] = M{t.seg, agg};
-      __syncthreads();  // forward wave aggregates of visit v
-      V H = a.ckpt[(b * S + s) * a.n_ckpt + ck0];
-      for (int w2 = W - 1; w2 > w; --w2) H = apply<Alg>(s_fagg[s & 1][w2], H);
+      const Vec2<C> *ck = a.ckpt + (b * S + s) * a.n_ckpt;
       SV h[R];
 #pragma unroll
-      for (int r = R - 1; r >= 0; --r) {
-        h[r] = Alg::store_s(mva<false>(t.pw[63 - lane], H, ex[r]));
+      for (int r = 0; r < R; ++r) {
+        h[r] = t0s[r] < T ? Alg::store_s(ck[t0s[r] / kSosCkptEvery<E>]) : SV{zero, zero};
         s_laneh[((s * W + w) * R + r) * 64 + lane] = h[r];
-        H = mva<false>(t.pw[64], H, tot[r]);
       }
       run_fwd_n<E, K, R>(q, h, F, t0s, T, nullptr);
     }
     // F now holds the cascade output: the forward output of section S-1
   }
 
-  for (; v < nvis; ++v) {
+  for (int v = 0; v < nvis; ++v) {
     const int s = vis_sec(v);
     const SosSec<E> q = load_sec(a, b, s);
     const SecPowers<C> &t = s_pow[v % 3];
@@ -985,8 +965,8 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
       const V hc = mva<REV>(t.pw[lane], H, ex[r]);
       h[r] = Alg::store_s(hc);
       if constexpr (!REV) {
-        if (a.ckpt && (t0s[r] % kSosCkpt) == 0 && t0s[r] < T)
-          a.ckpt[(b * S + s) * a.n_ckpt + t0s[r] / kSosCkpt] = hc;
+        if (a.ckpt && (t0s[r] % kSosCkptEvery<E>) == 0 && t0s[r] < T)
+          a.ckpt[(b * S + s) * a.n_ckpt + t0s[r] / kSosCkptEvery<E>] = hc;
       }
       H = mva<REV>(t.pw[64], H, tot[r]);
     }

@@ -490,7 +490,7 @@ int biquad_fwd_ss(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_
     f.b = b, f.a = a, f.nb = nb, f.na = 2, f.form = 1;
     if (B < 0 || T < 0 || b_row_stride < 0 || a_row_stride < 0 || !ss_filter_ok(f, 2)) return PHS_ERR_INVALID;
     if (B == 0 || T == 0) return PHS_OK;
-    if (!b || !a || !x || !y || (ckpt && ckpt_every <= 0)) return PHS_ERR_INVALID;
+    if (!b || !a || !x || !y || (ckpt && (ckpt_every <= 0 || ckpt_every % SsShape<Alg>::K != 0))) return PHS_ERR_INVALID;
     if (!ss_grid_ok(B, T, SsShape<Alg>::kTile)) return PHS_ERR_INVALID;
     SsArgs<Alg> p{};
     if (!ss_args<Alg>(B, T, f, zi, x, y, zf, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;

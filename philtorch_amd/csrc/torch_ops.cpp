@@ -383,7 +383,6 @@ Triple lti_recurN_backward_hip(const Tensor &A, const Tensor &zi, const Tensor &
 // sosfilt: fused cascade of second-order sections (scipy.signal.sosfilt
 // semantics, phs_sosfilt_* in philscan.h); no counterpart op in the reference.
 constexpr int64_t kSosMaxSections = 8;
-constexpr int64_t kSosCkptInterval = 512;  // steps between forward checkpoints
 
 void check_sos(const char *op, const Tensor &sos, const Tensor &x) {
   TORCH_CHECK(x.dim() == 2, "philtorch::", op, ": x must be a 2D tensor (batch, time)");
@@ -409,7 +408,9 @@ void check_states(const char *op, const char *what, const Tensor &z, const Tenso
   TORCH_CHECK(z.device() == x.device(), "philtorch::", op, ": all tensors must be on the same device");
 }
 
-int64_t sos_n_ckpt(int64_t T) { return (T + kSosCkptInterval - 1) / kSosCkptInterval; }
+// forward checkpoints per row and section (one fp64 pair each; the
+// interval is the library's, per dtype)
+int64_t sos_n_ckpt(int dt, int64_t T) { return int64_t(phs_sosfilt_ckpt_size(dt, 1, T, 1) / (2 * sizeof(double))); }
 
 Triple sosfilt_hip(const Tensor &sos, const std::optional<Tensor> &zi, const Tensor &x) {
   check_sos("sosfilt", sos, x);
@@ -421,7 +422,7 @@ Triple sosfilt_hip(const Tensor &sos, const std::optional<Tensor> &zi, const Ten
   Tensor zc = zi ? zi->contiguous() : Tensor();
   Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
   Tensor zf = at::empty({B, S, 2}, x.options());
-  Tensor ckpt = at::empty({B, S, sos_n_ckpt(T), 2}, x.options().dtype(at::kDouble));
+  Tensor ckpt = at::empty({B, S, sos_n_ckpt(dt, T), 2}, x.options().dtype(at::kDouble));
   TORCH_CHECK(size_t(ckpt.numel()) * sizeof(double) == phs_sosfilt_ckpt_size(dt, B, T, int(S)),
               "philtorch::sosfilt: checkpoint layout mismatch with libphilscan");
   if (B == 0 || T == 0) {
@@ -445,8 +446,9 @@ Triple sosfilt_backward_hip(const Tensor &sos, const Tensor &x, const Tensor &ck
   TORCH_CHECK(gy.sizes() == x.sizes(), "philtorch::sosfilt_backward: grad_y must have x's shape");
   TORCH_CHECK(gy.device() == x.device(), "philtorch::sosfilt_backward: all tensors must be on the same device");
   if (gzf) check_states("sosfilt_backward", "grad_zf", *gzf, x, S);
+  const int64_t nck = sos_n_ckpt(phs_dtype_of(x.scalar_type()), T);
   TORCH_CHECK(ckpt.scalar_type() == at::kDouble && ckpt.dim() == 4 && ckpt.size(0) == B && ckpt.size(1) == S &&
-                  ckpt.size(2) == sos_n_ckpt(T) && ckpt.size(3) == 2 && ckpt.device() == x.device(),
+                  ckpt.size(2) == nck && ckpt.size(3) == 2 && ckpt.device() == x.device(),
               "philtorch::sosfilt_backward: ckpt must be the forward's checkpoint tensor");
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
   const int dt = phs_dtype_of(x.scalar_type());
@@ -518,7 +520,7 @@ Triple biquad_hip(const Tensor &b, const Tensor &a, const std::optional<Tensor> 
   Tensor zc = zi ? zi->contiguous() : Tensor();
   Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
   Tensor zf = at::empty({B, 2}, x.options());
-  Tensor ckpt = at::empty({B, 1, sos_n_ckpt(T), 2}, x.options().dtype(at::kDouble));
+  Tensor ckpt = at::empty({B, 1, sos_n_ckpt(dt, T), 2}, x.options().dtype(at::kDouble));
   if (B == 0 || T == 0) {
     if (zi) zf.copy_(zc); else zf.zero_();
     return {y, zf, ckpt};
@@ -544,8 +546,9 @@ std::vector<Tensor> biquad_backward_hip(const Tensor &b, const Tensor &a, const 
   if (gzf)
     TORCH_CHECK(gzf->dim() == 2 && gzf->size(0) == B && gzf->size(1) == 2 && gzf->device() == x.device(),
                 "philtorch::biquad_backward: grad_zf must be (batch, 2)");
+  const int64_t nck = sos_n_ckpt(phs_dtype_of(x.scalar_type()), T);
   TORCH_CHECK(ckpt.scalar_type() == at::kDouble && ckpt.dim() == 4 && ckpt.size(0) == B && ckpt.size(1) == 1 &&
-                  ckpt.size(2) == sos_n_ckpt(T) && ckpt.size(3) == 2 && ckpt.device() == x.device(),
+                  ckpt.size(2) == nck && ckpt.size(3) == 2 && ckpt.device() == x.device(),
               "philtorch::biquad_backward: ckpt must be the forward's checkpoint tensor");
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
   const int dt = phs_dtype_of(x.scalar_type());

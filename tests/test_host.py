@@ -22,7 +22,7 @@ def test_capi_exports_every_declared_symbol():
 
 def test_capi_host_only_calls():
     lib = capi.load()
-    assert lib.phs_abi_version() == 111
+    assert lib.phs_abi_version() == 112
     for op in capi.OPS.values():
         for dt in capi.DTYPES.values():
             fwd = lib.phs_workspace_size(op, dt, 64, 65536, 0, 0)
@@ -223,8 +223,11 @@ def test_capi_sosfilt_host_only_calls():
         fwd = lib.phs_sosfilt_workspace_size(dt, 16, 480000, 8, 0)
         bwd = lib.phs_sosfilt_workspace_size(dt, 16, 480000, 8, 1)
         assert 0 < fwd <= bwd
-        # one fp64 pair per section and every 512th step
-        assert lib.phs_sosfilt_ckpt_size(dt, 16, 480000, 8) == 16 * 8 * ((480000 + 511) // 512) * 16
+        # one fp64 pair per section and every 32nd step (float32) or every
+        # 8th (float64): the gradient backward's lane chunks
+        every = 32 if dt == 0 else 8
+        assert lib.phs_sosfilt_ckpt_size(dt, 16, 480000, 8) == 16 * 8 * ((480000 + every - 1) // every) * 16
+        assert lib.phs_sosfilt_ckpt_size(dt, 3, 100, 2) == 3 * 2 * ((100 + every - 1) // every) * 16
     for bad in ((0, 16, 100, 0), (0, 16, 100, 9), (2, 16, 100, 8), (0, -1, 100, 8)):
         assert lib.phs_sosfilt_workspace_size(*bad, 0) == 0
         assert lib.phs_sosfilt_ckpt_size(*bad) == 0
