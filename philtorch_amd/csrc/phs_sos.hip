@@ -8,6 +8,8 @@
 #include "phs_launch.hpp"
 #include "phs_sos.hpp"
 
+#include <algorithm>
+#include <tuple>
 #include <type_traits>
 
 namespace phs {
@@ -70,26 +72,33 @@ size_t ws_bytes_for(int64_t B, int64_t T, int S, bool backward) {
 
 bool sizes_ok(int64_t B, int64_t T, int S) { return B >= 0 && T >= 0 && S >= 1 && S <= kSosMaxSections; }
 
-// Dynamic LDS a launch of `kernel` may take on the current device: the
-// device's LDS per workgroup less the kernel's static LDS (cached per kernel
-// and device; 64 KiB less static where the query fails).
-size_t lds_limit(const void *kernel) {
+// Dynamic LDS a launch of `kernel` may take on the current device with
+// `wgs` of its workgroups resident per CU: the device's LDS per CU over wgs,
+// at most its LDS per workgroup, less the kernel's static LDS (cached per
+// kernel, device and wgs; 64 KiB per CU and per workgroup where the queries
+// fail).
+size_t lds_limit(const void *kernel, int wgs) {
   static std::mutex mu;
-  static std::map<std::pair<const void *, int>, size_t> cache;
+  static std::map<std::tuple<const void *, int, int>, size_t> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = -1;
   std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_pair(kernel, dev);
+  const auto key = std::make_tuple(kernel, dev, wgs);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
-  int per_block = 0;
+  int per_block = 0, per_cu = 0;
   hipFuncAttributes attr{};
   size_t stat = 0;
   if (hipFuncGetAttributes(&attr, kernel) == hipSuccess) stat = attr.sharedSizeBytes;
   if (dev < 0 || hipDeviceGetAttribute(&per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
       per_block <= 0)
     per_block = 64 << 10;
-  const size_t out = size_t(per_block) > stat ? size_t(per_block) - stat : 0;
+  if (dev < 0 ||
+      hipDeviceGetAttribute(&per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess ||
+      per_cu <= 0)
+    per_cu = 64 << 10;
+  const size_t avail = std::min(size_t(per_block), size_t(per_cu) / size_t(wgs > 0 ? wgs : 1));
+  const size_t out = avail > stat ? avail - stat : 0;
   cache[key] = out;
   return out;
 }
@@ -182,12 +191,13 @@ int sos_bwd(int64_t B, int64_t T, int S, const SosCoefs &k, const void *x, const
   const unsigned grid = a.per_stripe * kStripes;
   if (grad) {
     // lane entry states of every section, then the kept sections' inputs:
-    // every third section where the device's LDS per workgroup allows two
-    // slots (gfx950: 160 KiB), else every other
+    // every third section where the LDS left to each of the workgroups the
+    // kernel's registers let a CU hold allows two slots, else every other
+    // (fp32 on gfx950: three workgroups per CU, one slot), else none
     const auto kernel = sos_kernel<E, Sh, true, true>;
     const size_t laneh = size_t(S) * Sh::kWaves * Sh::R * 64 * sizeof(Vec2<E>);
     const size_t slot = size_t(Sh::kWaves) * Sh::R * Sh::K * 64 * sizeof(E);
-    const size_t limit = lds_limit(reinterpret_cast<const void *>(kernel));
+    const size_t limit = lds_limit(reinterpret_cast<const void *>(kernel), kSosWgsPerCu<E, Sh, true>);
     int step = S >= 2 ? (S + 2) / 3 : 0;
     if (step > 0 && laneh + sos_kept_slots(S, step) * slot > limit) step = (S + 1) / 2;
     if (step > 0 && laneh + sos_kept_slots(S, step) * slot > limit) step = 0;

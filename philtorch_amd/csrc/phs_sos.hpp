@@ -656,11 +656,14 @@ __device__ bool sos_lookback(const uint64_t *row_status, const Vec2<typename Wid
 // State entering scan positions [span, ...) of section s_target in row b,
 // computed by one wave straight from the inputs: the cascade (forward) or the
 // adjoint cascade (REV) over the whole row prefix in scan order, 64*K steps
-// per iteration, every section up to s_target carrying its state across
-// iterations.  `lds` (the look-back staging area, free by then) holds the
-// carries and the section's powers.  Taken only when predecessors did not
-// publish within the poll budget.  The arguments come by value: a reference
-// would make every thread of the kernel keep a private copy of them.
+// per iteration (K = 4 whatever the tile's lane chunk: the kernel's VGPR
+// count is the largest of its own and its callees', and at the tile's K this
+// function set it, 229 against 111 for the fp32 backward), every section up
+// to s_target carrying its state across iterations.  `lds` (the look-back
+// staging area, free by then) holds the carries and the section's powers.
+// Taken only when predecessors did not publish within the poll budget.  The
+// arguments come by value: a reference would make every thread of the kernel
+// keep a private copy of them.
 template <typename E, class Sh, bool REV>
 __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const SosArgs<E> a, int64_t b,
                                                                         int s_target, int64_t span, int lane,
@@ -668,7 +671,8 @@ __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const S
   using Alg = Block2<E>;
   using C = typename Wide<E>::type;
   using V = Vec2<C>;
-  constexpr int K = Sh::K;
+  constexpr int K = Sh::K < 4 ? Sh::K : 4;
+  static_assert(Sh::kTile % (64 * K) == 0, "tiles are whole fallback iterations");
   V *carry = reinterpret_cast<V *>(lds);
   SecPowers<C> *tab = reinterpret_cast<SecPowers<C> *>(lds + kSosMaxSections * (sizeof(V) / sizeof(uint64_t)));
   const int S = a.S;
@@ -738,11 +742,16 @@ __device__ __noinline__ Vec2<typename Wide<E>::type> sos_prefix_fallback(const S
 // (keeping the data waves' registers free of matrices) and resolves each
 // section's entry state.  Barriers: powers of the first two visits; two per
 // visit (wave aggregates ready, entry state ready).
-// The fp32 forward is held to 128 VGPRs (four waves per SIMD: 103 against
-// 106.5 us at C4, 18 VGPRs spilled); the backward and fp64 keep their
-// registers (their spills at that bound would cost more than the waves gain).
+// Waves per SIMD the launch bounds ask for: the fp32 forward 4 (128 VGPRs,
+// a 15-wave tile and its look-back wave fill a CU), the fp32 backward 3 (168
+// VGPRs: three workgroups per CU, so C4's 1264 backward tiles run in two
+// generations instead of three); fp64 keeps its registers.
 template <typename E, bool REV>
-constexpr int kSosMinWaves = (!REV && sizeof(E) == 4) ? 4 : 1;
+constexpr int kSosMinWaves = sizeof(E) == 4 ? (REV ? 3 : 4) : 1;
+
+// Workgroups of shape Sh a CU holds at those bounds (four SIMDs).
+template <typename E, class Sh, bool REV>
+constexpr int kSosWgsPerCu = sizeof(E) == 4 ? 4 * kSosMinWaves<E, REV> / (Sh::kThreads / 64) : 1;
 
 template <typename E, class Sh, bool REV, bool GRAD>
 __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kernel(SosArgs<E> a) {
@@ -862,11 +871,12 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
   E U[R][K];  // forward: input of the current section;  backward: its upstream gradient
 #pragma unroll
   for (int r = 0; r < R; ++r) load_chunk<E, K>(a.in + b * T, chunk0(r), T, vec, U[r], zero);
-  E X[GRAD ? R : 1][GRAD ? K : 1];
-  E F[GRAD ? R : 1][GRAD ? K : 1];  // forward values of the current section
+  // forward values of the current section (x is read again from memory
+  // where a re-derivation starts from it, not held in registers)
+  E F[GRAD ? R : 1][GRAD ? K : 1];
   if constexpr (GRAD) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) load_chunk<E, K>(a.x + b * T, chunk0(r), T, vec, X[r], zero);
+    for (int r = 0; r < R; ++r) load_chunk<E, K>(a.x + b * T, chunk0(r), T, vec, F[r], zero);
   }
   __syncthreads();  // powers of the first two visits
 
@@ -877,10 +887,6 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
   // LDS for the re-derivations
   if constexpr (GRAD) {
     static_assert(R == 1 && K == kSosCkptEvery<E>, "a lane chunk is one checkpoint interval");
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int k = 0; k < K; ++k) F[r][k] = X[r][k];
     const int ks = a.kept_step;
     for (int s = 0; s < S; ++s) {
       if (ks > 0 && s > 0 && s % ks == 0 && s / ks <= kSosKeptSlots) {
@@ -909,34 +915,7 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
     const SecPowers<C> &t = s_pow[v % 3];
     const SV gzf = load_pair(a.virt + (b * S + s) * 2, REV && a.virt != nullptr);
 
-    // forward input of section s, recomputed from x or from the kept
-    // section's input through the sections between (F keeps its output, the
-    // previous visit's input)
     E Uf[GRAD ? R : 1][GRAD ? K : 1];
-    if constexpr (GRAD) {
-      const int ks = a.kept_step;
-      const int slot = ks > 0 ? (s / ks < kSosKeptSlots ? s / ks : kSosKeptSlots) : 0;  // kept sections <= s
-      const int j0 = slot * ks;
-      if (j0 > 0) {
-        const E *src = s_uin + size_t(slot - 1) * W * R * K * 64;
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int k = 0; k < K; ++k) Uf[r][k] = src[((w * R + r) * K + k) * 64 + lane];
-      } else {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int k = 0; k < K; ++k) Uf[r][k] = X[r][k];
-      }
-      for (int j = j0; j < s; ++j) {
-        const SosSec<E> qj = load_sec(a, b, j);
-        SV hj[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) hj[r] = s_laneh[((j * W + w) * R + r) * 64 + lane];
-        run_fwd_n<E, K, R>(qj, hj, Uf, t0s, T, nullptr);
-      }
-    }
 
     // ---- pass 1: lane folds, wave scan, round chaining
     V ex[R], tot[R], x[R];
@@ -955,6 +934,32 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
     for (int r = 1; r < R; ++r) agg = mva<REV>(t.pw[64], agg, tot[r]);
     if (lane == 0) s_wagg[w] = M{maybe_transpose<REV>(t.seg), agg};
     __syncthreads();  // wave aggregates are in s_wagg
+    // forward input of section s, recomputed from x or from the kept
+    // section's input through the sections between (F keeps its output, the
+    // previous visit's input), while the look-back wave resolves the entry
+    // state (the adjoint's pass 1 does not read it)
+    if constexpr (GRAD) {
+      const int ks = a.kept_step;
+      const int slot = ks > 0 ? (s / ks < kSosKeptSlots ? s / ks : kSosKeptSlots) : 0;  // kept sections <= s
+      const int j0 = slot * ks;
+      if (j0 > 0) {
+        const E *src = s_uin + size_t(slot - 1) * W * R * K * 64;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int k = 0; k < K; ++k) Uf[r][k] = src[((w * R + r) * K + k) * 64 + lane];
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) load_chunk<E, K>(a.x + b * T, chunk0(r), T, vec, Uf[r], zero);
+      }
+      for (int j = j0; j < s; ++j) {
+        const SosSec<E> qj = load_sec(a, b, j);
+        SV hj[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) hj[r] = s_laneh[((j * W + w) * R + r) * 64 + lane];
+        run_fwd_n<E, K, R>(qj, hj, Uf, t0s, T, nullptr);
+      }
+    }
     __syncthreads();  // entry state is in s_in
     V H = apply<Alg>(s_wpre[w], s_in);
 
