@@ -71,10 +71,15 @@ bool ss_args(int64_t B, int64_t T, const SsFilter &f, const void *zi, const void
   return true;
 }
 
+// The tile grid is the launched mode's (modes differ in tile length; the
+// workspace's status words cover the shortest tiles).
 template <class Alg, bool REV, int MODE = kSsPlain>
-int ss_launch(const SsArgs<Alg> &a, hipStream_t stream) {
-  launch_kernel((ss_kernel<Alg, REV, MODE>), dim3(a.per_stripe * kStripes), dim3(SsShape<Alg, MODE>::kThreads), 0, stream,
-                a);
+int ss_launch(SsArgs<Alg> a, hipStream_t stream) {
+  using Sh = SsShape<Alg, MODE>;
+  a.tiles_per_row = (a.T_len + Sh::kTile - 1) / Sh::kTile;
+  a.tiles = unsigned(a.B * a.tiles_per_row);
+  a.per_stripe = (a.tiles + kStripes - 1) / kStripes;
+  launch_kernel((ss_kernel<Alg, REV, MODE>), dim3(a.per_stripe * kStripes), dim3(Sh::kThreads), 0, stream, a);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 

@@ -119,14 +119,22 @@ constexpr int kSsPlain = 0, kSsStates = 1, kSsGrad = 2, kSsStatesY = 3;
 // gradients (states pass, adjoint, sums) went 279 -> 237 us at order 4,
 // 217 -> 188 at order 3, 134 -> 128.5 at order 2 and 86.5 -> 85.5 at
 // order 1; the other modes are slower with fewer rounds.
+//
+// The fp32 order-2 plain pass is a wide tile instead: 15 data waves of 16
+// steps in 2 rounds (30720 steps) beside the look-back wave, held to 128
+// VGPRs (four waves per SIMD, 9 spilled), so one tile fills a CU's wave
+// slots and a C4 call is 256 tiles all resident at once, where 3-wave tiles
+// at 158 VGPRs were 1264 tiles on 768 resident slots (two generations).
 template <class Alg, int MODE = kSsPlain>
 struct SsShape {
   using E = typename Alg::elem;
   static constexpr int M = int(sizeof(typename Alg::s_state) / sizeof(E));
-  static constexpr int kWaves = 3;
+  static constexpr bool kWide = MODE == kSsPlain && M == 2 && sizeof(E) == 4;
+  static constexpr int kWaves = kWide ? 15 : 3;
+  static constexpr int kMinWaves = kWide ? 4 : 2;  // waves per SIMD the launch bounds ask for
   static constexpr int kThreads = 64 * (kWaves + 1);
-  static constexpr int K = int((M <= 2 ? 32 : 64) / sizeof(E));
-  static constexpr int R = (M <= 2 ? 4 : 2) / (MODE == kSsGrad ? 2 : 1);
+  static constexpr int K = kWide ? 16 : int((M <= 2 ? 32 : 64) / sizeof(E));
+  static constexpr int R = kWide ? 2 : (M <= 2 ? 4 : 2) / (MODE == kSsGrad ? 2 : 1);
   static constexpr int kWaveSeg = 64 * K * R;
   static constexpr int kTile = kWaves * kWaveSeg;
   static_assert((K & (K - 1)) == 0, "K is a power of two (the lane matrix is A^K by squaring)");
@@ -709,9 +717,10 @@ __device__ __forceinline__ void ss_grad_step(SsGrad<Alg, typename Alg::elem> &ac
   acc.v[G::kD] = fma(g, xf, acc.v[G::kD]);
 }
 
-// At least two waves per SIMD (two workgroups per CU).
+// At least two waves per SIMD (two workgroups per CU; wide tiles four).
 template <class Alg, bool REV, int MODE>
-__global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), 2) void ss_kernel(SsArgs<Alg> a) {
+__global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), (SsShape<Alg, MODE>::kMinWaves)) void ss_kernel(
+    SsArgs<Alg> a) {
   using E = typename Alg::elem;
   using S = typename Alg::state;
   using SS = typename Alg::s_state;
@@ -756,8 +765,12 @@ __global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), 2) void ss_kernel(S
 #pragma unroll
       for (int r = 1; r < R; r <<= 1) P = Alg::cmul(P, P);
       if (lane == 0) s_tab.pw[7] = P;
-      P = Alg::cmul(P, Alg::cmul(P, P));  // G = A^(3 * 64 K R)
-      static_assert(kWaves == 3, "G is the wave power cubed");
+      {  // G = A^(kWaves * 64 K R)
+        typename Alg::coef G = P;
+#pragma unroll
+        for (int j = 1; j < kWaves; ++j) G = Alg::cmul(P, G);
+        P = G;
+      }
 #pragma unroll
       for (int j = 0; j < 7; ++j) {
         if (lane == 0) s_tab.gp[j] = P;
