@@ -20,7 +20,7 @@ from tests import _data as D
 
 pytestmark = pytest.mark.gpu
 
-# tiles: float32 6144 steps forward and backward; float64 6144 / 1536
+# tiles: float32 30720 steps forward, 6144 backward; float64 14336 / 1536
 SHAPES = [(1, 1), (2, 17), (3, 1536), (2, 3071), (2, 6144), (3, 6145), (2, 12288), (2, 20000), (1, 40000)]
 SECTIONS = [1, 3, 8]
 FLOATS = [np.float32, np.float64]
@@ -151,7 +151,8 @@ def test_sosfilt_capi_forced_fallback(api, dtype):
     """A one-poll budget makes tiles compute their entry states from the row
     prefix (forward cascade) or suffix (adjoint cascade) themselves."""
     lib = api[0]
-    case = _case(dtype, 2, 20000, 5, False, True, True, D.seed_of("sos-fallback", dtype))
+    # three forward tiles a row at float32's 30720-step tile
+    case = _case(dtype, 2, 2 * 30720 + 5, 5, False, True, True, D.seed_of("sos-fallback", dtype))
     lib.phs_debug_set_spin_limit(1)
     try:
         got = _run(api, *case)
@@ -348,9 +349,11 @@ def test_lfilter_fused_route_second_order_gradients(hip):
 def test_sosfilt_capi_aggregates_only_multi_window(api, dtype):
     """Tiles after a row's first publish aggregates only (testing hook): every
     section's look-back folds back to tile 0 through windows of 64 entries
-    (110+ tiles per row), forward cascade and adjoint cascade."""
+    (70+ tiles per row at the forward's tile, more at the backward's),
+    forward cascade and adjoint cascade."""
     lib = api[0]
-    case = _case(dtype, 2, 110 * 6144 + 3, 3, False, True, True, D.seed_of("sos-agg-only", dtype))
+    T = 70 * (30720 if dtype == np.float32 else 14336) + 3
+    case = _case(dtype, 2, T, 3, False, True, True, D.seed_of("sos-agg-only", dtype))
     lib.phs_debug_set_aggregates_only(1)
     try:
         got = _run(api, *case)

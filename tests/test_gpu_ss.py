@@ -139,7 +139,8 @@ def test_lti_ss_capi_reversed(api, dtype, M, Bn, T):
 @pytest.mark.parametrize("M", [2, 4])
 def test_lti_ss_capi_reversed_forced_fallback(api, dtype, M):
     lib = api[0]
-    A, b, c, d, zi, x = _case(dtype, M, 3, 20000, False, D.seed_of("ss-rev-fallback", dtype, M))
+    # three tiles a row at the order-2 fp32 plain pass's 30720-step tile
+    A, b, c, d, zi, x = _case(dtype, M, 3, 2 * 30720 + 5, False, D.seed_of("ss-rev-fallback", dtype, M))
     lib.phs_debug_set_spin_limit(1)
     try:
         got = _run(api, A, b, c, d, zi, x, rev=True)
@@ -159,7 +160,7 @@ def test_lti_ss_capi_long_rows(api, dtype, M):
 @pytest.mark.parametrize("M", [2, 3])
 def test_lti_ss_capi_forced_fallback(api, dtype, M):
     lib = api[0]
-    A, b, c, d, zi, x = _case(dtype, M, 3, 20000, False, D.seed_of("ss-fallback", dtype, M))
+    A, b, c, d, zi, x = _case(dtype, M, 3, 2 * 30720 + 5, False, D.seed_of("ss-fallback", dtype, M))
     lib.phs_debug_set_spin_limit(1)
     try:
         got = _run(api, A, b, c, d, zi, x)
@@ -510,7 +511,8 @@ def test_lti_ss_capi_aggregates_only_multi_window(api, dtype, M):
     every look-back folds back to tile 0 through windows of 64 entries: 110
     tiles of 6144 (fp32) or fewer steps per row, both time directions."""
     lib = api[0]
-    A, b, c, d, zi, x = _case(dtype, M, 2, 110 * 6144 + 5, False, D.seed_of("ss-agg-only", dtype, M))
+    # 70+ tiles a row at the widest tile (order-2 fp32 plain: 30720 steps)
+    A, b, c, d, zi, x = _case(dtype, M, 2, 70 * 30720 + 5, False, D.seed_of("ss-agg-only", dtype, M))
     lib.phs_debug_set_aggregates_only(1)
     try:
         got = _run(api, A, b, c, d, zi, x)
