@@ -21,7 +21,8 @@ from tests import _data as D
 pytestmark = pytest.mark.gpu
 
 # tiles: float32 30720 steps forward, 6144 backward; float64 14336 / 1536
-SHAPES = [(1, 1), (2, 17), (3, 1536), (2, 3071), (2, 6144), (3, 6145), (2, 12288), (2, 20000), (1, 40000)]
+SHAPES = [(1, 1), (2, 17), (3, 1536), (2, 3071), (2, 6144), (3, 6145), (2, 12288), (2, 20000), (2, 30720), (1, 40000),
+          (2, 61441)]
 SECTIONS = [1, 3, 8]
 FLOATS = [np.float32, np.float64]
 
