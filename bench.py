@@ -956,6 +956,25 @@ def _ceiling(lib, w, steps, evict_caches, dev):
     best = min(results, key=lambda sh: results[sh][0])
     ms_step, ms_f, ms_b = results[best]
     step_bytes = (w.fwd_bytes + w.bwd_bytes) * w.launches
+    del bufs, calls
+    # a plain device copy (torch's copy_, the runtime's own copy kernel)
+    # moving the same bytes as each launch: half of them read, half written
+    copies = {}
+    for nm, nbytes in (("fwd", w.fwd_bytes), ("bwd", w.bwd_bytes)):
+        src = torch.ones(nbytes // 8, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            evict_caches()
+            dst.copy_(src)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        for i in range(steps):
+            evict_caches()
+            ev[i][0].record()
+            dst.copy_(src)
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        copies[nm] = sum(a.elapsed_time(b) for a, b in ev) / steps
+        del src, dst
     return {
         "kernel": f"phs_stream_probe shape {best} ({'scan tile geometry' if best == 0 else 'one float4 per lane'})",
         "ms_per_step": round(ms_step, 5),
@@ -964,6 +983,14 @@ def _ceiling(lib, w, steps, evict_caches, dev):
         "step_GBs": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
         "step_frac_of_peak": round(step_bytes / (ms_step * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
         "shapes_ms_per_step": {str(k): round(v[0], 5) for k, v in results.items()},
+        "device_copy": {
+            "what": "torch copy_ of a buffer of half each launch's bytes (reads + writes = the launch's bytes), "
+                    "one event pair around each copy, same cache eviction",
+            "ms_fwd_equivalent": round(copies["fwd"], 5),
+            "ms_bwd_equivalent": round(copies["bwd"], 5),
+            "GBs_fwd_equivalent": round(w.fwd_bytes / (copies["fwd"] * 1e-3) / 1e9, 1),
+            "GBs_bwd_equivalent": round(w.bwd_bytes / (copies["bwd"] * 1e-3) / 1e9, 1),
+        },
     }
 
 

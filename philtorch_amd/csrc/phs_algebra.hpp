@@ -153,38 +153,6 @@ __device__ __forceinline__ T down(typename Wide<T>::type v) {
   return o;
 }
 
-// Speculative pass 2 (phs_scan.hpp): a lane whose entry map from the tile's
-// start has a coefficient below these magnitudes writes its outputs from a
-// zero entry state before the tile's entry state is known, and rewrites them
-// only if the true entry state then moves its start state in storage
-// precision.  The bounds only decide how often that rewrite happens, never
-// the result: fp32 storage rounds at 2^-24 relative, fp64 at 2^-53, so for
-// states and entry states of comparable size a coefficient below 2^-32
-// (2^-62) leaves the rounded start state unchanged; int64 is exact only for
-// a zero coefficient.
-__device__ __forceinline__ bool tiny_for(double v, float) { return __builtin_fabs(v) < 0x1p-32; }
-__device__ __forceinline__ bool tiny_for(double v, double) { return __builtin_fabs(v) < 0x1p-62; }
-__device__ __forceinline__ bool tiny_for(int64_t v, int64_t) { return v == 0; }
-__device__ __forceinline__ bool tiny_for(c128 v, c64) { return tiny_for(v.re, 0.f) && tiny_for(v.im, 0.f); }
-__device__ __forceinline__ bool tiny_for(c128 v, c128) { return tiny_for(v.re, 0.0) && tiny_for(v.im, 0.0); }
-
-// Bitwise equality of two stored values (whole 32-bit words).
-template <typename X>
-__device__ __forceinline__ bool same_bits(const X &p, const X &q) {
-  static_assert(sizeof(X) % 4 == 0, "stored values are whole words");
-  union U {
-    X x;
-    uint32_t w[sizeof(X) / 4];
-  };
-  U u, v;
-  u.x = p;
-  v.x = q;
-  bool eq = true;
-#pragma unroll
-  for (int i = 0; i < int(sizeof(X) / 4); ++i) eq = eq & (u.w[i] == v.w[i]);
-  return eq;
-}
-
 // Scalar first-order scan: coefficient and state are both one scalar.
 template <typename T>
 struct Scalar {
@@ -197,11 +165,15 @@ struct Scalar {
   using acc_coef = ct;
   static constexpr int kCoefElems = 1;
   static constexpr int kStateElems = 1;
-  static constexpr int kVecsPerLane = 2;
+  // Real scans: one 16-byte vector per lane, array and round, in four
+  // rounds (fp32: 4 steps x 4 rounds, a 8192-step tile).  Folding a round as
+  // soon as its vectors arrive, with four rounds in flight, beat two rounds
+  // of two vectors (C1 step 33.90 -> 32.37 us, same-box A/B).
   // LTI scans load no coefficients: complex lanes then carry twice the steps
   // in the registers the coefficients would take
-  static constexpr int kVecsPerLaneLTI = Num<T>::kComplex ? 4 : 2;
-  static constexpr int kRounds = 2;
+  static constexpr int kVecsPerLane = Num<T>::kComplex ? 2 : 1;
+  static constexpr int kVecsPerLaneLTI = Num<T>::kComplex ? 4 : 1;
+  static constexpr int kRounds = Num<T>::kComplex ? 2 : 4;
 
   // Real scans: 8 data waves that also do the look-back, with a floor of 4
   // waves per SIMD (at most 128 VGPRs): two tiles resident per CU.  Complex
@@ -216,9 +188,6 @@ struct Scalar {
   // among the last 8 tiles (C5 fp32: 8 tiles 134, 16 tiles 125, 64 tiles 128
   // GSamples/s)
   static constexpr int kLookFirst = 8;
-  // writes each round's outputs before the entry state is known where it
-  // cannot reach them (phs_scan.hpp); complex scans keep the plain pass 2
-  static constexpr bool kSpeculate = !Num<T>::kComplex;
 
   static __device__ __forceinline__ coef load_c(s_coef v) { return up(v); }
   static __device__ __forceinline__ state load_s(s_state v) { return up(v); }
@@ -236,7 +205,6 @@ struct Scalar {
 
   static __device__ __forceinline__ coef cone() { return Num<ct>::one(); }
   static __device__ __forceinline__ state szero() { return Num<ct>::zero(); }
-  static __device__ __forceinline__ bool negligible(coef A) { return tiny_for(A, T{}); }
   // q * p  (apply p first)
   static __device__ __forceinline__ coef cmul(coef q, coef p) { return mul(q, p); }
   // A h + x
@@ -275,7 +243,6 @@ struct Block2 {
   // a full first look-back window: a short one costs 2x2 scans a second poll
   // too often (C3: 8 tiles 40.7, 16 tiles 38.8, 64 tiles 45.5 GSamples/s)
   static constexpr int kLookFirst = 64;
-  static constexpr bool kSpeculate = false;  // its maps would add to the register budget
 
   static __device__ __forceinline__ coef load_c(s_coef v) {
     return {up(v.m00), up(v.m01), up(v.m10), up(v.m11)};
@@ -312,9 +279,6 @@ struct Block2 {
     return {Num<ct>::one(), Num<ct>::zero(), Num<ct>::zero(), Num<ct>::one()};
   }
   static __device__ __forceinline__ state szero() { return {Num<ct>::zero(), Num<ct>::zero()}; }
-  static __device__ __forceinline__ bool negligible(const coef &A) {
-    return tiny_for(A.m00, T{}) && tiny_for(A.m01, T{}) && tiny_for(A.m10, T{}) && tiny_for(A.m11, T{});
-  }
   static __device__ __forceinline__ coef cmul(coef q, coef p) {
     coef r;
     r.m00 = mad(q.m00, p.m00, mul(q.m01, p.m10));
@@ -382,7 +346,6 @@ struct BlockN {
   static constexpr int kWavesPerBlock = 3;
   static constexpr int kMinWavesPerEU = 1;
   static constexpr int kLookFirst = 64;  // as Block2
-  static constexpr bool kSpeculate = false;
 
   template <typename D, typename S, int N>
   static __device__ __forceinline__ void conv_up(D (&d)[N], const S (&s)[N]) {
@@ -503,12 +466,6 @@ struct BlockN {
     return r;
   }
   static __device__ __forceinline__ state szero() { return vec_zero<ct>(); }
-  static __device__ __forceinline__ bool negligible(const coef &A) {
-    bool r = true;
-#pragma unroll
-    for (int i = 0; i < M * M; ++i) r = r && tiny_for(A.m[i], T{});
-    return r;
-  }
   static __device__ __forceinline__ coef cmul(const coef &q, const coef &p) { return mat_mul<ct>(q, p); }
   static __device__ __forceinline__ state affine(const coef &A, const state &h, const state &x) {
     return mat_affine<ct>(A, h, x);

@@ -9,16 +9,21 @@
 // runs serially in time with the reference's arithmetic: per step and state
 // component, the products A[i][j] h[j] summed from zero in j order, then
 // added to x[i] (so a scalar step is x + a h_prev).  The forward results are
-// therefore the reference CPU results bit for bit (no fused multiply-add:
+// therefore the reference CPU results bit for bit, in every dtype the
+// reference dispatches, half and bfloat16 included (no fused multiply-add:
 // this file is built for the baseline x86-64 target).  The backward runs the
 // adjoint lambda[t] = g[t] + A[t+1]^H lambda[t+1] directly, in one pass per
 // row, instead of the reference's flipped, rolled and conjugated copies.
 //
 // No device code and no torch types in the kernels: element types are
-// float, double, c10::complex<float>, c10::complex<double> and int64_t; the
+// float, double, c10::complex<float>, c10::complex<double>, int64_t and the
+// 16-bit c10::Half and c10::BFloat16, whose operators round to the type after
+// every multiply and add, as the reference's loops in those dtypes do; the
 // caller passes contiguous buffers and a `parallel_rows(n, fn)` runner.
 #pragma once
 
+#include <c10/util/BFloat16.h>
+#include <c10/util/Half.h>
 #include <c10/util/complex.h>
 
 #include <cstdint>
@@ -30,6 +35,28 @@ namespace phs_cpu {
 template <typename T>
 inline T conj_of(T v) {
   return v;
+}
+
+// Accumulator of the backward's sums over steps or rows (coefficient
+// gradients of shared or time-invariant coefficients, grad_zi): float for
+// the 16-bit types, as the reference's closures form those sums with
+// matmul / vecdot, which accumulate 16-bit operands in float; the element
+// type otherwise.
+template <typename S>
+struct AccOf {
+  using type = S;
+};
+template <>
+struct AccOf<c10::Half> {
+  using type = float;
+};
+template <>
+struct AccOf<c10::BFloat16> {
+  using type = float;
+};
+template <typename S>
+inline typename AccOf<S>::type acc_of(S v) {
+  return typename AccOf<S>::type(v);
 }
 template <typename R>
 inline c10::complex<R> conj_of(c10::complex<R> v) {
@@ -108,10 +135,11 @@ inline void adjoint_row(const Layout &L, int64_t b, const S *A, const S *zi, con
     on_step(t, lam, t == 0 ? zi + b * M : yb + (t - 1) * M);
   }
   if (gzi && T > 0) {
+    using Acc = typename AccOf<S>::type;
     for (int64_t i = 0; i < M; ++i) {
-      S sum = S(0);
-      for (int64_t j = 0; j < M; ++j) sum += conj_of(Ab[j * M + i]) * lb[j];
-      gzi[b * M + i] = sum;
+      Acc sum = Acc(0);
+      for (int64_t j = 0; j < M; ++j) sum += acc_of(conj_of(Ab[j * M + i])) * acc_of(lb[j]);
+      gzi[b * M + i] = S(sum);
     }
   }
 }
@@ -125,6 +153,7 @@ inline void adjoint_row(const Layout &L, int64_t b, const S *A, const S *zi, con
 template <typename S, class Par>
 void scan_bwd(const Layout &L, const S *A, const S *zi, const S *y, const S *g, S *gx, S *gA, S *gzi,
               Par &&parallel_rows) {
+  using Acc = typename AccOf<S>::type;
   const int64_t B = L.B, T = L.T, M = L.M, MM = M * M;
   const bool tv = L.a_step != 0, shared = L.a_row == 0;
   if (gA && tv && !shared) {
@@ -139,20 +168,23 @@ void scan_bwd(const Layout &L, const S *A, const S *zi, const S *y, const S *g, 
   }
   if (gA && !tv) {
     // per-row sums over time, then (shared A) over rows in row order
-    std::vector<S> rows(shared ? size_t(B * MM) : size_t(0));
-    S *dst_all = shared ? rows.data() : gA;
+    std::vector<Acc> rows(size_t(B * MM));
     parallel_rows(B, [&](int64_t b) {
-      S *dst = dst_all + b * MM;
-      for (int64_t k = 0; k < MM; ++k) dst[k] = S(0);
+      Acc *dst = rows.data() + b * MM;
+      for (int64_t k = 0; k < MM; ++k) dst[k] = Acc(0);
       adjoint_row(L, b, A, zi, y, g, gx, gzi, [&](int64_t, const S *lam, const S *hp) {
         for (int64_t i = 0; i < M; ++i)
-          for (int64_t j = 0; j < M; ++j) dst[i * M + j] += lam[i] * conj_of(hp[j]);
+          for (int64_t j = 0; j < M; ++j) dst[i * M + j] += acc_of(lam[i]) * acc_of(conj_of(hp[j]));
       });
+      if (!shared)
+        for (int64_t k = 0; k < MM; ++k) gA[b * MM + k] = S(dst[k]);
     });
     if (shared) {
-      for (int64_t k = 0; k < MM; ++k) gA[k] = S(0);
-      for (int64_t b = 0; b < B; ++b)
-        for (int64_t k = 0; k < MM; ++k) gA[k] += rows[b * MM + k];
+      for (int64_t k = 0; k < MM; ++k) {
+        Acc sum = Acc(0);
+        for (int64_t b = 0; b < B; ++b) sum += rows[b * MM + k];
+        gA[k] = S(sum);
+      }
     }
     return;
   }
@@ -161,14 +193,15 @@ void scan_bwd(const Layout &L, const S *A, const S *zi, const S *y, const S *g, 
   parallel_rows(B, [&](int64_t b) { adjoint_row(L, b, A, zi, y, g, gx, gzi, [](int64_t, const S *, const S *) {}); });
   if (!gA) return;
   parallel_rows(T, [&](int64_t t) {
-    S *dst = gA + t * MM;
-    for (int64_t k = 0; k < MM; ++k) dst[k] = S(0);
+    thread_local std::vector<Acc> dst;
+    dst.assign(size_t(MM), Acc(0));
     for (int64_t b = 0; b < B; ++b) {
       const S *lam = gx + (b * T + t) * M;
       const S *hp = t == 0 ? zi + b * M : y + (b * T + t - 1) * M;
       for (int64_t i = 0; i < M; ++i)
-        for (int64_t j = 0; j < M; ++j) dst[i * M + j] += lam[i] * conj_of(hp[j]);
+        for (int64_t j = 0; j < M; ++j) dst[i * M + j] += acc_of(lam[i]) * acc_of(conj_of(hp[j]));
     }
+    for (int64_t k = 0; k < MM; ++k) gA[t * MM + k] = S(dst[k]);
   });
 }
 

@@ -196,6 +196,15 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
   const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
   a.spin_limit = sl ? sl : kDefaultSpinLimit;
   a.agg_only = g_agg_only.load(std::memory_order_relaxed) ? 1u : 0u;
+  // tile id -> row by multiply and shift: with l = ceil(log2 B) and
+  // s = 31 + l, m = floor(2^s / B) + 1 gives floor(id m / 2^s) = floor(id / B)
+  // for every id below 2^31 (m B - 2^s lies in (0, B], and B <= 2^l)
+  {
+    unsigned l = 0;
+    while ((uint64_t(1) << l) < uint64_t(B)) ++l;
+    a.b_shift = 31u + l;
+    a.b_magic = ((uint64_t(1) << a.b_shift) / uint64_t(B)) + 1u;
+  }
   a.trace = nullptr;
   a.trace_tiles = 0;
   if (backward && gcoef) {

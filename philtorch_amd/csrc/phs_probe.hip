@@ -4,8 +4,9 @@
 // launch comes to a plain kernel of the same traffic and launch shape.
 //
 //   shape 0  the fp32 scalar scan's tile geometry: 8 waves of 64 lanes, a
-//            lane holding 8 consecutive floats per array in each of two
-//            rounds (8192 elements per workgroup, one tile per workgroup)
+//            lane holding 4 consecutive floats (one float4) per array in
+//            each of four rounds (8192 elements per workgroup, one tile per
+//            workgroup), every load issued before the first store
 //   shape 1  one float4 per lane and array, 2048 elements per workgroup
 //   shape 2  shape 0's grid with no memory access: launch and drain only
 //
@@ -23,35 +24,30 @@ struct ProbeArgs {
 
 template <int NIN, int NOUT>
 __global__ __launch_bounds__(512) void probe_tile_kernel(ProbeArgs a) {
+  constexpr int kRounds = 4;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int64_t base = int64_t(blockIdx.x) * 8192 + w * 1024 + l * 8;
-  float4 v[NIN][2][2];
+  const int64_t base = int64_t(blockIdx.x) * 8192 + w * 1024 + l * 4;
+  float4 v[NIN][kRounds];
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+  for (int r = 0; r < kRounds; ++r)
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) {
-      const float4 *p = reinterpret_cast<const float4 *>(a.in[k] + base + r * 512);
-      v[k][r][0] = p[0];
-      v[k][r][1] = p[1];
+    for (int k = 0; k < NIN; ++k) v[k][r] = *reinterpret_cast<const float4 *>(a.in[k] + base + r * 256);
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    float4 s = v[0][r];
+#pragma unroll
+    for (int k = 1; k < NIN; ++k) {
+      s.x += v[k][r].x;
+      s.y += v[k][r].y;
+      s.z += v[k][r].z;
+      s.w += v[k][r].w;
     }
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float4 s = v[0][r][h];
-#pragma unroll
-      for (int k = 1; k < NIN; ++k) {
-        s.x += v[k][r][h].x;
-        s.y += v[k][r][h].y;
-        s.z += v[k][r][h].z;
-        s.w += v[k][r][h].w;
-      }
-#pragma unroll
-      for (int j = 0; j < NOUT; ++j) {
-        const float c = float(j + 1);
-        reinterpret_cast<float4 *>(a.out[j] + base + r * 512)[h] = make_float4(c * s.x, c * s.y, c * s.z, c * s.w);
-      }
+    for (int j = 0; j < NOUT; ++j) {
+      const float c = float(j + 1);
+      *reinterpret_cast<float4 *>(a.out[j] + base + r * 256) = make_float4(c * s.x, c * s.y, c * s.z, c * s.w);
     }
+  }
 }
 
 template <int NIN, int NOUT>

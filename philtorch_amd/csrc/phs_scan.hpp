@@ -34,9 +34,11 @@
 // Self-resetting workspace: the workspace starts with kStripes 64-bit claim
 // words {epoch (high 32 bits), claim count (low 32 bits)}, one per 128-byte
 // line.  Workgroup g claims from stripe g % kStripes with one atomic add,
-// which returns its claim index c and the epoch; its tile is c*kStripes + g%
-// kStripes (the grid is padded to whole stripes, surplus workgroups exit).
-// Striping keeps same-address atomics from serialising the launch.  The call
+// which returns its claim index c and the epoch (the grid is padded to whole
+// stripes, surplus workgroups exit).  Its tile is g itself (workgroups are
+// dispatched in index order), except in the 2x2 time-varying backward, which
+// takes c*kStripes + g%kStripes, the order of the claims.  Striping keeps
+// same-address atomics from serialising the launch.  The call
 // tags its status words with epoch+1.  The last claimer of each stripe
 // re-arms it with {epoch+1, 0}: every claim on that stripe has happened by
 // then.  Words left by earlier calls carry older tags and are ignored, so the
@@ -49,9 +51,11 @@
 // workgroups: the look-back polls a bounded number of times, and a tile whose
 // predecessors have not all published by then computes its entry state
 // itself, folding every earlier step of its row straight from the inputs.
-// Claims are mapped q-major (id = q*B + b), so in practice predecessors are
-// claimed first and that path is only taken by the tests that force it.
+// Tiles are mapped q-major (id = q*B + b), so in practice predecessors start
+// first and that path is only taken by the tests that force it.
 #pragma once
+
+#include <type_traits>
 
 #include "phs_algebra.hpp"
 
@@ -119,6 +123,10 @@ struct ScanArgs {
   unsigned per_stripe;         // claims per stripe (grid = per_stripe * kStripes)
   unsigned spin_limit;         // look-back polls before the self-compute fallback
   unsigned agg_only;           // testing: tiles after a row's first publish no inclusive state
+  // tile id -> (scan position, row) without a 64-bit division: for ids
+  // below 2^31, id / B == (id * b_magic) >> b_shift (set by the host)
+  uint64_t b_magic;
+  unsigned b_shift;
   uint64_t *status;          // status words of this call
   int vec_ok;
   // tracing launches only (scan_kernel<..., TRACE = true>): per-tile phase
@@ -163,6 +171,29 @@ __device__ __forceinline__ unsigned claim_tag(unsigned long long *claims, unsign
   unsigned cid = 0, ctag = 0;
   if (lane == 0) claim_tile(claims, per_stripe, cid, ctag);
   return __builtin_amdgcn_readfirstlane(ctag);
+}
+
+// The same claim split in two for a workgroup whose tile is its own index
+// and whose data wave 0 looks back: the atomic is issued before the tile's
+// loads and its result is read only at the look-back, so its round trip
+// overlaps the loads.  claim_issue: one lane; claim_finish: the whole wave
+// (lane 0 holds the claim word), returns the tag and re-arms the stripe if
+// this was its last claim.
+__device__ __forceinline__ unsigned long long claim_issue(unsigned long long *claims) {
+  return __hip_atomic_fetch_add(claims + (blockIdx.x % kStripes) * kStripeWords, 1ull, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned claim_finish(unsigned long long *claims, unsigned per_stripe,
+                                                 unsigned long long v, int lane) {
+  unsigned tag = 0;
+  if (lane == 0) {
+    const unsigned epoch = unsigned(v >> 32), c = unsigned(v);
+    tag = epoch + 1u;
+    if (c == per_stripe - 1u)
+      __hip_atomic_store(claims + (blockIdx.x % kStripes) * kStripeWords, (unsigned long long)(epoch + 1u) << 32,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return __builtin_amdgcn_readfirstlane(tag);
 }
 
 // ------------------------------------------------------------ status words
@@ -333,11 +364,13 @@ __device__ bool lookback(const uint64_t *row_status, const typename Alg::state &
 // The bounds-checked tail assigns in branches: `c ? row[t] : fill` with both
 // operands lvalues is an lvalue, compiled as a select between a global and a
 // private address, and every thread of the kernel then keeps a copy of
-// `fill` in scratch memory.
-template <typename X, int K>
+// `fill` in scratch memory.  kFull: the caller knows the chunk is in range
+// and 16-byte aligned, so only the vector path is compiled (no branch
+// between the forms; see the kernel's full-tile path).
+template <typename X, int K, bool kFull = false>
 __device__ __forceinline__ void load_chunk(const X *row, int64_t t0, int64_t T, bool vec, X (&out)[K],
                                            const X fill) {
-  if (vec && t0 + K <= T) {
+  if (kFull || (vec && t0 + K <= T)) {
     constexpr int nv = int(K * sizeof(X) / 16);
     static_assert(K * sizeof(X) % 16 == 0, "chunk must be 16-byte granular");
     union {
@@ -360,9 +393,9 @@ __device__ __forceinline__ void load_chunk(const X *row, int64_t t0, int64_t T, 
   }
 }
 
-template <typename X, int K>
+template <typename X, int K, bool kFull = false>
 __device__ __forceinline__ void store_chunk(X *row, int64_t t0, int64_t T, bool vec, const X (&v)[K]) {
-  if (vec && t0 + K <= T) {
+  if (kFull || (vec && t0 + K <= T)) {
     constexpr int nv = int(K * sizeof(X) / 16);
     union {
       X x[K];
@@ -468,17 +501,17 @@ __device__ __forceinline__ Map<Alg> tile_aggregate(const Map<Alg> *s_wagg) {
 // tile's aggregate `tagg` is known: publish it, look back over the
 // predecessors (or fold the row prefix from the inputs once the poll budget
 // is spent), publish the inclusive state.  `known`: the state is already in
-// `yin` (the row's first tile, or an early look-back that resolved).
+// `yin` (the row's first tile, or an early look-back that resolved).  `virt`:
+// the state entering the row (zi forward, zero backward).
 template <class Alg, bool TV, bool REV>
 __device__ __forceinline__ typename Alg::state tile_entry(const ScanArgs<Alg> &a, int64_t qs, int64_t b,
                                                           unsigned tag, int lane, const Map<Alg> &tagg, bool known,
                                                           typename Alg::state yin, Lookback<Alg> &lb,
-                                                          uint64_t *s_look) {
+                                                          uint64_t *s_look, const typename Alg::state &virt) {
   using SC = typename Alg::s_coef;
   using SS = typename Alg::s_state;
   using Sh = Shape<Alg, TV>;
   uint64_t *row_status = a.status + b * a.tiles_per_row * Sh::kStride;
-  const typename Alg::state virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
   if (!known) {
     if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
       yin = row_prefix_fallback<Alg, TV, REV>(reinterpret_cast<const SS *>(a.x) + b * a.T_len,
@@ -501,21 +534,19 @@ __device__ __forceinline__ typename Alg::state tile_entry(const ScanArgs<Alg> &a
 // placement of waves, rounds and lanes in memory instead, so one DPP scan
 // serves both directions.  Inside a lane's K steps REV walks downwards.
 //
-// Speculative pass 2 (Alg::kSpeculate).  Right after round r's wave scan a
-// lane knows the map E from the start of its wave's segment to the start of
-// its chunk; the true start state is store_s(E.A h + E.x) for the state h
-// entering the segment, which the look-back and the other waves' aggregates
-// fix only later.  Where E.A is negligible (Alg::negligible: below the
-// storage precision's rounding for states of ordinary size) the lane runs
-// pass 2 from store_s(E.x) at once and writes the round's outputs while the
-// later rounds are still loading; once h is known it recomputes only its
-// start state and runs pass 2 again, rewriting its outputs, if and only if
-// that start state differs in any bit.  The memory then holds exactly what
-// pass 2 from the true entry state writes, whatever was speculated.  For
-// contractive recurrences (|a| < 1, products decaying along the segment)
-// only the first steps of each wave's segment wait for the look-back, so
-// the tile streams: round r's stores overlap round r+1's loads, and the
-// look-back's latency overlaps both.
+// Every output is written after the tile's entry state is known, so a tile
+// reads all of its inputs before it writes anything.  Writing the outputs a
+// lane's entry state cannot reach early (from the in-wave prefix, before the
+// look-back resolves) was measured slower on every real scalar config: the
+// early writes mix into the co-resident tiles' reads (C1 backward 14.8 ->
+// 16.6 us, C5 fp64 step 1.80 -> 1.85 ms, same-box A/B).
+//
+// Full tiles (in range and 16-byte aligned) of real scalar scans and of
+// every backward run a copy of the data path with
+// only vector loads and stores, so the compiler's memory-counter waits see
+// one straight-line sequence of loads and each round's fold waits for its
+// own vectors only; with the bounds-checked form in the same code it waited
+// for every load of the tile before the first fold.
 //
 // Where the algebra asks for it (Alg::kLookbackWave), the look-back runs in
 // a wave of its own that holds no tile data.  Run by data wave 0 instead, its
@@ -524,8 +555,8 @@ __device__ __forceinline__ typename Alg::state tile_entry(const ScanArgs<Alg> &a
 // register sets, not their sum.  That pays where the data path is
 // register-heavy (2x2 and complex scans); for real scalar scans a ninth wave
 // per tile costs more than it saves.  Either way the waves meet at the same
-// barriers: claim, wave aggregates ready, entry state ready (and, backward
-// for LTI, the gradient reduction).
+// barriers: wave aggregates ready, entry state ready (and, backward for LTI,
+// the gradient reduction).
 //
 // TRACE: the instantiation a tracing launch runs; it also writes each
 // tile's phase record (kTraceWords words at trace + id * kTraceWords).
@@ -552,27 +583,33 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   [[maybe_unused]] uint64_t tr_start = 0;
   if constexpr (TRACE) tr_start = trace_clock();
-  // Tile ids.  Where a look-back wave holds the tag (Sh::kLookbackWave), the
-  // tile is the workgroup's own index: workgroups are dispatched in index
-  // order, so a tile's row predecessors start first, as claimed tiles do, and
-  // the data waves issue their loads at once instead of after the claim's
-  // round trip; the look-back wave still claims from its stripe, which
-  // counts the workgroup for the stripe's re-arming and gives it the call's
-  // tag.  Otherwise the claimed index is the tile (data wave 0 needs the tag
-  // only after its loads anyway).  Measured at the C4 op level (2x2 LTI,
-  // both directions) 8.8 -> 9.6 GSamples/s, C2 +1 %, C3's forward 258 ->
-  // 240 us; C3's backward (2x2, time-varying) ran 452 -> 471 us, and keeps
-  // the claimed order.
-  constexpr bool kStaticIds = Sh::kLookbackWave && !(TV && REV);
+  // Tile ids.  The tile is the workgroup's own index: workgroups are
+  // dispatched in index order, so a tile's row predecessors start first, as
+  // claimed tiles do, and the data waves issue their loads at once instead of
+  // after a claim's round trip.  The workgroup still claims from its stripe,
+  // which counts it for the stripe's re-arming and gives it the call's tag:
+  // the look-back wave claims, or, without one, data wave 0 issues the claim
+  // before its loads and reads the result at the look-back.  Measured: C4 op
+  // level (2x2 LTI) 8.8 -> 9.6 GSamples/s, C2 +1 %, C3's forward 258 -> 240
+  // us; C3's backward (2x2 with a look-back wave, time-varying) ran 452 ->
+  // 471 us and keeps the claimed order.
+  constexpr bool kStaticIds = !(Sh::kLookbackWave && TV && REV);
+  constexpr bool kOwnClaim = kStaticIds && !Sh::kLookbackWave;  // data wave 0 claims
   int64_t id = 0;
   unsigned tag = 0;
+  [[maybe_unused]] unsigned long long claim_v = 0;
   if constexpr (kStaticIds) {
-    if (tid == 0) s_ready = 0;
-    __syncthreads();
+    if constexpr (Sh::kLookbackWave) {
+      if (tid == 0) s_ready = 0;
+      __syncthreads();
+    }
     id = blockIdx.x;
     if (id >= a.tiles) {  // padding of the last stripe round: counted, then gone
       if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
       return;
+    }
+    if constexpr (kOwnClaim) {
+      if (tid == 0) claim_v = claim_issue(a.claims);
     }
   } else {
     if (tid == 0) {
@@ -593,8 +630,10 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
       tr[kTrId] = uint64_t(id);
     }
   }
-  const int64_t qs = id / a.B;         // position in scan order
-  const int64_t b = id - qs * a.B;
+  // id = qs * B + b, by multiply and shift (ids are below 2^31)
+  const unsigned uq = unsigned((uint64_t(unsigned(id)) * a.b_magic) >> a.b_shift);
+  const int64_t qs = uq;  // position in scan order
+  const int64_t b = int64_t(unsigned(id) - uq * unsigned(a.B));
   const int64_t qf = REV ? a.tiles_per_row - 1 - qs : qs;  // position along time
   const int64_t T = a.T_len;
   const bool vec = a.vec_ok != 0;
@@ -616,11 +655,7 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
 
   if (Sh::kLookbackWave && w == kWaves) {
     // ================= look-back wave
-    if constexpr (kStaticIds) {
-      unsigned cid = 0, ctag = 0;
-      if (lane == 0) claim_tile(a.claims, a.per_stripe, cid, ctag);
-      tag = __builtin_amdgcn_readfirstlane(ctag);
-    }
+    if constexpr (kStaticIds) tag = claim_tag(a.claims, a.per_stripe, lane);
     const S virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
     Lookback<Alg> lb = lookback_start<Alg>(qs);
     S yin = virt;
@@ -640,7 +675,7 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
     }
     const M tagg = tile_aggregate<Alg, kWaves>(s_wagg);
     if (!known && lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
-    yin = tile_entry<Alg, TV, REV>(a, qs, b, tag, lane, tagg, known, yin, lb, s_look);
+    yin = tile_entry<Alg, TV, REV>(a, qs, b, tag, lane, tagg, known, yin, lb, s_look, virt);
     if constexpr (TRACE) {
       if (tr && lane == 0) {
         tr[kTrEntry] = trace_clock();
@@ -654,6 +689,11 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
   }
 
   // ================= data waves
+  // forward without a look-back wave: the state entering the row, read with
+  // the tile's data (data wave 0's look-back needs it; one line per wave,
+  // converted only where it is used)
+  [[maybe_unused]] SS virt_raw = zero_ss;
+  if constexpr (!REV && !Sh::kLookbackWave) virt_raw = reinterpret_cast<const SS *>(a.zi)[b];
   // memory placement of this wave's segment and of this lane's chunk
   const int pw = REV ? kWaves - 1 - w : w;
   const int pl = REV ? 63 - lane : lane;
@@ -663,157 +703,161 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
     return seg0 + int64_t(pr) * 64 * K + int64_t(pl) * K;
   };
   const SS *yrow_in = reinterpret_cast<const SS *>(a.y) + b * T;
-
-  // ---- loads (all rounds issued up front)
-  SS X[R][K];
-  SC A[TV ? R : 1][TV ? K : 1];
-  SS Y[REV ? R : 1][REV ? K : 1];
-  SS Ylow[REV ? R : 1];  // backward: y[t0-1] below the chunk of lane 63
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t t0 = chunk0(r);
-    load_chunk<SS, K>(xrow, t0, T, vec, X[r], zero_ss);
-    if constexpr (TV) load_chunk<SC, K>(crow, t0, T, vec, A[r], zero_sc);
-    if constexpr (REV) {
-      load_chunk<SS, K>(yrow_in, t0, T, vec, Y[r], zero_ss);
-      Ylow[r] = zero_ss;
-      if (lane == 63) {
-        if (t0 == 0)
-          Ylow[r] = reinterpret_cast<const SS *>(a.zi)[b];
-        else if (t0 - 1 < T)
-          Ylow[r] = yrow_in[t0 - 1];
-      }
-    }
-  }
-
-  // ---- pass 2 of round r from the stored start state h, writing its outputs
   SS *yrow = REV ? nullptr : reinterpret_cast<SS *>(a.out) + b * T;
   SS *gxrow = (REV && a.out) ? reinterpret_cast<SS *>(a.out) + b * T : nullptr;
   SC *gcrow = (REV && a.gcoef) ? reinterpret_cast<SC *>(a.gcoef) + b * T : nullptr;
-  // backward: y[t0-1] of each round sits in the last step of the next lane's
-  // chunk (lanes are mirrored), or below the round for lane 63 (set, by a
-  // shuffle, outside the per-lane branches of pass 2)
-  SS Ybelow[REV ? R : 1];
-  auto pass2 = [&](int r, SS h) -> AC {
-    AC acc = Alg::acc_zero();
-    const int64_t t0 = chunk0(r);
-    if constexpr (!REV) {
-      SS O[K];
+
+  // The data path, compiled twice: kFull for tiles wholly inside the row
+  // with aligned rows (vector loads and stores only), and the bounds-checked
+  // form for the rest.
+  auto data_path = [&](auto full_c) {
+    constexpr bool kFull = decltype(full_c)::value;
+    // ---- loads (all rounds issued up front)
+    SS X[R][K];
+    SC A[TV ? R : 1][TV ? K : 1];
+    SS Y[REV ? R : 1][REV ? K : 1];
+    SS Ylow[REV ? R : 1];  // backward: y[t0-1] below the chunk of lane 63
 #pragma unroll
-      for (int k = 0; k < K; ++k) {
-        h = Alg::s_affine(TV ? A[r][TV ? k : 0] : a_row_s, h, X[r][k]);
-        O[k] = h;
-      }
-      store_chunk<SS, K>(yrow, t0, T, vec, O);
-    } else {
-      SS nu = h;
-      SS GX[K];
-      SC GC[K];
-#pragma unroll
-      for (int kk = 0; kk < K; ++kk) {
-        const int k = K - 1 - kk;
-        const SC c = Alg::s_adjoint(TV ? A[r][TV ? k : 0] : a_row_s);
-        const SS lam = Alg::s_add(X[r][k], nu);
-        GX[k] = lam;
-        const SC g = Alg::s_outer(lam, k == 0 ? Ybelow[r] : Y[r][k > 0 ? k - 1 : 0]);
-        GC[k] = g;
-        if constexpr (kAcc) {
-          if (want_acc && t0 + k < T) acc = Alg::acc_add(acc, Alg::load_c(g));
+    for (int r = 0; r < R; ++r) {
+      const int64_t t0 = chunk0(r);
+      load_chunk<SS, K, kFull>(xrow, t0, T, vec, X[r], zero_ss);
+      if constexpr (TV) load_chunk<SC, K, kFull>(crow, t0, T, vec, A[r], zero_sc);
+      if constexpr (REV) {
+        load_chunk<SS, K, kFull>(yrow_in, t0, T, vec, Y[r], zero_ss);
+        Ylow[r] = zero_ss;
+        if (lane == 63) {
+          if (t0 == 0)
+            Ylow[r] = reinterpret_cast<const SS *>(a.zi)[b];
+          else if (kFull || t0 - 1 < T)
+            Ylow[r] = yrow_in[t0 - 1];
         }
-        nu = Alg::s_affine(c, lam, zero_ss);
-        if (t0 + k == 0 && a.gzi) reinterpret_cast<SS *>(a.gzi)[b] = nu;
-      }
-      if (gxrow) store_chunk<SS, K>(gxrow, t0, T, vec, GX);
-      if constexpr (TV) {
-        if (gcrow) store_chunk<SC, K>(gcrow, t0, T, vec, GC);
       }
     }
-    return acc;
+
+    // ---- pass 2 of round r from the start state h, writing its outputs
+    // backward: y[t0-1] of each round sits in the last step of the next
+    // lane's chunk (lanes are mirrored), or below the round for lane 63 (set,
+    // by a shuffle, outside the per-lane branches of pass 2)
+    SS Ybelow[REV ? R : 1];
+    auto pass2 = [&](int r, SS h) -> AC {
+      AC acc = Alg::acc_zero();
+      const int64_t t0 = chunk0(r);
+      if constexpr (!REV) {
+        SS O[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          h = Alg::s_affine(TV ? A[r][TV ? k : 0] : a_row_s, h, X[r][k]);
+          O[k] = h;
+        }
+        store_chunk<SS, K, kFull>(yrow, t0, T, vec, O);
+      } else {
+        SS nu = h;
+        SS GX[K];
+        SC GC[K];
+#pragma unroll
+        for (int kk = 0; kk < K; ++kk) {
+          const int k = K - 1 - kk;
+          const SC c = Alg::s_adjoint(TV ? A[r][TV ? k : 0] : a_row_s);
+          const SS lam = Alg::s_add(X[r][k], nu);
+          GX[k] = lam;
+          const SC g = Alg::s_outer(lam, k == 0 ? Ybelow[r] : Y[r][k > 0 ? k - 1 : 0]);
+          GC[k] = g;
+          if constexpr (kAcc) {
+            if (want_acc && (kFull || t0 + k < T)) acc = Alg::acc_add(acc, Alg::load_c(g));
+          }
+          nu = Alg::s_affine(c, lam, zero_ss);
+          if (t0 + k == 0 && a.gzi) reinterpret_cast<SS *>(a.gzi)[b] = nu;
+        }
+        if (gxrow) store_chunk<SS, K, kFull>(gxrow, t0, T, vec, GX);
+        if constexpr (TV) {
+          if (gcrow) store_chunk<SC, K, kFull>(gcrow, t0, T, vec, GC);
+        }
+      }
+      return acc;
+    };
+
+    // ---- pass 1: lane maps, wave scans (each round as soon as its vectors
+    // are in), round chaining
+    M E[R];  // map from the wave's start to this lane's chunk of round r
+    M carry = map_identity<Alg>();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      M m = lane_map<Alg, TV, REV, K>(A[TV ? r : 0], X[r], a_row_s);
+      m = wave_scan_incl(m, lane, op);
+      const M ex = wave_shift_up(m, lane, map_identity<Alg>());
+      const M tot = read_lane(m, 63);
+      E[r] = compose<Alg>(carry, ex);
+      carry = compose<Alg>(carry, tot);
+      if constexpr (REV) {
+        Ybelow[r] = shfl_from(Y[r][K - 1], lane + 1);
+        if (lane == 63) Ybelow[r] = Ylow[r];
+      }
+    }
+    if constexpr (TRACE) {
+      if (tr && tid == 0) tr[kTrLoaded] = trace_clock();
+    }
+    if (lane == 0) {
+      s_wagg[w] = carry;
+      if (Sh::kLookbackWave) __hip_atomic_fetch_add(&s_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    __syncthreads();  // wave aggregates are in s_wagg
+    if (!Sh::kLookbackWave && w == 0) {
+      // look-back by data wave 0: publish the tile's aggregate, find its entry
+      if constexpr (kOwnClaim) tag = claim_finish(a.claims, a.per_stripe, claim_v, lane);
+      if constexpr (TRACE) {
+        if (tr && lane == 0) tr[kTrAggregates] = trace_clock();
+      }
+      const M tagg = tile_aggregate<Alg, kWaves>(s_wagg);
+      if (qs > 0 && lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
+      Lookback<Alg> lb = lookback_start<Alg>(qs);
+      const S virt = REV ? Alg::szero() : Alg::load_s(virt_raw);
+      const S yin = tile_entry<Alg, TV, REV>(a, qs, b, tag, lane, tagg, qs == 0, virt, lb, s_look, virt);
+      if constexpr (TRACE) {
+        if (tr && lane == 0) {
+          tr[kTrEntry] = trace_clock();
+          tr[kTrPolls] = lb.polls;
+        }
+      }
+      if (lane == 0) s_in = yin;
+    }
+    // the wave's exclusive prefix in the tile, folded by every wave itself
+    M wpre = map_identity<Alg>();
+    for (int j = 0; j < w; ++j) wpre = compose<Alg>(wpre, s_wagg[j]);
+    __syncthreads();  // entry state is in s_in
+
+    // ---- pass 2 from the entry state
+    const S hin = apply<Alg>(wpre, s_in);  // state entering this wave's segment
+    AC acc = Alg::acc_zero();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const AC v = pass2(r, Alg::store_s(apply<Alg>(E[r], hin)));
+      if constexpr (kAcc) acc = Alg::acc_sum(acc, v);
+    }
+    if constexpr (TRACE) {
+      if (tr && tid == 0) tr[kTrStored] = trace_clock();
+    }
+    if (want_acc) {
+      // deterministic block reduction of the per-tile coefficient gradient
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) acc = Alg::acc_sum(acc, shfl_from(acc, lane ^ d));
+      if (lane == 0) s_acc[w] = acc;
+      __syncthreads();
+      if (tid == 0) {
+        AC sum = s_acc[0];
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) sum = Alg::acc_sum(sum, s_acc[i]);
+        reinterpret_cast<AC *>(a.partials)[b * a.tiles_per_row + qf] = sum;
+      }
+    }
   };
-
-  // ---- pass 1: lane maps, wave scans, round chaining; speculative pass 2
-  // of each round as soon as its wave scan is done
-  constexpr bool kSpec = Alg::kSpeculate;
-  M E[R];  // map from the wave's start to this lane's chunk of round r
-  bool spec[R];
-  SS hs[R];
-  AC acc_s[kAcc ? R : 1];
-  M carry = map_identity<Alg>();
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    M m = lane_map<Alg, TV, REV, K>(A[TV ? r : 0], X[r], a_row_s);
-    m = wave_scan_incl(m, lane, op);
-    const M ex = wave_shift_up(m, lane, map_identity<Alg>());
-    const M tot = read_lane(m, 63);
-    E[r] = compose<Alg>(carry, ex);
-    carry = compose<Alg>(carry, tot);
-    if constexpr (REV) {
-      Ybelow[r] = shfl_from(Y[r][K - 1], lane + 1);
-      if (lane == 63) Ybelow[r] = Ylow[r];
-    }
-    spec[r] = kSpec && Alg::negligible(E[r].A);
-    hs[r] = Alg::store_s(E[r].x);
-    AC v = Alg::acc_zero();
-    if (spec[r]) v = pass2(r, hs[r]);
-    if constexpr (kAcc) acc_s[r] = v;
-  }
-  if constexpr (TRACE) {
-    if (tr && tid == 0) tr[kTrLoaded] = trace_clock();
-  }
-  if (lane == 0) {
-    s_wagg[w] = carry;
-    if (Sh::kLookbackWave) __hip_atomic_fetch_add(&s_ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  __syncthreads();  // wave aggregates are in s_wagg
-  if (!Sh::kLookbackWave && w == 0) {
-    // look-back by data wave 0: publish the tile's aggregate, find its entry
-    if constexpr (TRACE) {
-      if (tr && lane == 0) tr[kTrAggregates] = trace_clock();
-    }
-    const M tagg = tile_aggregate<Alg, kWaves>(s_wagg);
-    if (qs > 0 && lane == 0) publish(row_status + qs * Sh::kStride + Sh::kIncWords, tagg, tag);
-    Lookback<Alg> lb = lookback_start<Alg>(qs);
-    const S virt = REV ? Alg::szero() : Alg::load_s(reinterpret_cast<const SS *>(a.zi)[b]);
-    const S yin = tile_entry<Alg, TV, REV>(a, qs, b, tag, lane, tagg, qs == 0, virt, lb, s_look);
-    if constexpr (TRACE) {
-      if (tr && lane == 0) {
-        tr[kTrEntry] = trace_clock();
-        tr[kTrPolls] = lb.polls;
-      }
-    }
-    if (lane == 0) s_in = yin;
-  }
-  // the wave's exclusive prefix in the tile, folded by every wave itself
-  M wpre = map_identity<Alg>();
-  for (int j = 0; j < w; ++j) wpre = compose<Alg>(wpre, s_wagg[j]);
-  __syncthreads();  // entry state is in s_in
-
-  // ---- pass 2 from the true entry state where the speculation missed
-  const S hin = apply<Alg>(wpre, s_in);  // state entering this wave's segment
-  AC acc = Alg::acc_zero();
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const SS h = Alg::store_s(apply<Alg>(E[r], hin));
-    AC v = kAcc ? acc_s[kAcc ? r : 0] : Alg::acc_zero();
-    if (!(spec[r] && same_bits(h, hs[r]))) v = pass2(r, h);
-    if constexpr (kAcc) acc = Alg::acc_sum(acc, v);
-  }
-  if constexpr (TRACE) {
-    if (tr && tid == 0) tr[kTrStored] = trace_clock();
-  }
-  if (want_acc) {
-    // deterministic block reduction of the per-tile coefficient gradient
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) acc = Alg::acc_sum(acc, shfl_from(acc, lane ^ d));
-    if (lane == 0) s_acc[w] = acc;
-    __syncthreads();
-    if (tid == 0) {
-      AC sum = s_acc[0];
-#pragma unroll
-      for (int i = 1; i < kWaves; ++i) sum = Alg::acc_sum(sum, s_acc[i]);
-      reinterpret_cast<AC *>(a.partials)[b * a.tiles_per_row + qf] = sum;
-    }
-  }
+  // The forwards of algebras with a look-back wave (complex, 2x2, order M)
+  // keep the single bounds-checked form: with the vector-only copy beside it
+  // they measured slower (C2 forward 0.852 -> 0.861 ms, same-box A/B).
+  constexpr bool kSplit = !Sh::kLookbackWave || REV;
+  if (kSplit && vec && (qf + 1) * Sh::kTile <= T)
+    data_path(std::true_type{});
+  else
+    data_path(std::false_type{});
 }
 
 // ------------------------------------------------------------ helpers

@@ -1023,7 +1023,10 @@ std::vector<Tensor> lpv_ss_backward_hip(const Tensor &A, const std::optional<Ten
 // ------------------------------------------------------------ CPU key
 // The reference's CPU extension registers its ops for the CPU key; these
 // run phs_cpu.hpp on contiguous copies, in parallel over rows (torch's
-// intra-op thread pool), serially in time.  Half and bfloat16 compute in fp32.
+// intra-op thread pool), serially in time.  Half and bfloat16 compute in their
+// own type, rounding after every operation, as the reference's CPU loops do
+// (its AT_DISPATCH ..._AND2/AND3(kHalf, kBFloat16) kernels); the backward's
+// sums over steps or rows accumulate them in float.
 template <class F>
 void parallel_rows(int64_t n, F &&f) {
   at::parallel_for(0, n, 1, [&](int64_t begin, int64_t end) {
@@ -1040,7 +1043,7 @@ Tensor cpu_fwd(const Tensor &A, const Tensor &zi, const Tensor &x, phs_cpu::Layo
   Tensor Ac = A.contiguous(), zc = zi.contiguous(), xc = x.contiguous();
   Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
   if (L.B == 0 || L.T == 0) return y;
-  AT_DISPATCH_FLOATING_AND_COMPLEX_TYPES_AND1(at::kLong, x.scalar_type(), "philtorch_cpu_fwd", [&] {
+  AT_DISPATCH_FLOATING_AND_COMPLEX_TYPES_AND3(at::kLong, at::kHalf, at::kBFloat16, x.scalar_type(), "philtorch_cpu_fwd", [&] {
     phs_cpu::scan_fwd<scalar_t>(L, Ac.const_data_ptr<scalar_t>(), zc.const_data_ptr<scalar_t>(),
                                 xc.const_data_ptr<scalar_t>(), y.mutable_data_ptr<scalar_t>(),
                                 [](int64_t n, auto &&f) { parallel_rows(n, f); });
@@ -1055,7 +1058,7 @@ Triple cpu_bwd(const Tensor &A, const Tensor &zi, const Tensor &y, const Tensor 
   Tensor gzi = at::empty(zi.sizes(), zi.options());
   Tensor gx = at::empty(y.sizes(), y.options());
   if (L.B == 0 || L.T == 0) return {gA.zero_(), gzi.zero_(), gx.zero_()};
-  AT_DISPATCH_FLOATING_AND_COMPLEX_TYPES_AND1(at::kLong, y.scalar_type(), "philtorch_cpu_bwd", [&] {
+  AT_DISPATCH_FLOATING_AND_COMPLEX_TYPES_AND3(at::kLong, at::kHalf, at::kBFloat16, y.scalar_type(), "philtorch_cpu_bwd", [&] {
     phs_cpu::scan_bwd<scalar_t>(L, Ac.const_data_ptr<scalar_t>(), zc.const_data_ptr<scalar_t>(),
                                 yc.const_data_ptr<scalar_t>(), gc.const_data_ptr<scalar_t>(),
                                 gx.mutable_data_ptr<scalar_t>(), gA.mutable_data_ptr<scalar_t>(),
@@ -1069,8 +1072,6 @@ Tensor recur_cpu(const Tensor &A, const Tensor &zi, const Tensor &x) {
   check_common("recur", A, zi, x);
   check_recur(A, zi, x);
   check_cpu("recur", x);
-  if (is_half(x.scalar_type()))
-    return recur_cpu(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
   const int64_t B = x.size(0), T = x.size(1);
   return cpu_fwd(A, zi, x, {B, T, 1, A.dim() == 1 ? 0 : T, 1, false});
 }
@@ -1080,9 +1081,6 @@ Triple recur_backward_cpu(const Tensor &A, const Tensor &zi, const Tensor &y, co
   check_recur(A, zi, y);
   check_cpu("recur_backward", y);
   TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
-  if (is_half(y.scalar_type()))
-    return to_dtype(recur_backward_cpu(A.to(at::kFloat), zi.to(at::kFloat), y.to(at::kFloat), gy.to(at::kFloat)),
-                    y.scalar_type());
   const int64_t B = y.size(0), T = y.size(1);
   return cpu_bwd(A, zi, y, gy.to(y.scalar_type()), {B, T, 1, A.dim() == 1 ? 0 : T, 1, false});
 }
@@ -1091,8 +1089,6 @@ Tensor recurN_cpu(const Tensor &A, const Tensor &zi, const Tensor &x) {
   check_common("recurN", A, zi, x);
   check_recurN(A, zi, x);
   check_cpu("recurN", x);
-  if (is_half(x.scalar_type()))
-    return recurN_cpu(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
   const int64_t B = x.size(0), T = x.size(1), M = A.size(-1);
   return cpu_fwd(A, zi, x, {B, T, M, A.dim() == 3 ? 0 : T * M * M, M * M, false});
 }
@@ -1107,9 +1103,6 @@ Triple recurN_backward_cpu(const Tensor &A, const Tensor &zi, const Tensor &y, c
   check_recurN(A, zi, y);
   check_cpu("recurN_backward", y);
   TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
-  if (is_half(y.scalar_type()))
-    return to_dtype(recurN_backward_cpu(A.to(at::kFloat), zi.to(at::kFloat), y.to(at::kFloat), gy.to(at::kFloat)),
-                    y.scalar_type());
   const int64_t B = y.size(0), T = y.size(1), M = A.size(-1);
   return cpu_bwd(A, zi, y, gy.to(y.scalar_type()), {B, T, M, A.dim() == 3 ? 0 : T * M * M, M * M, false});
 }
@@ -1118,8 +1111,6 @@ Tensor lti_recur_cpu(const Tensor &A, const Tensor &zi, const Tensor &x) {
   check_common("lti_recur", A, zi, x);
   check_lti_recur(A, zi, x);
   check_cpu("lti_recur", x);
-  if (is_half(x.scalar_type()))
-    return lti_recur_cpu(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
   const int64_t B = x.size(0), T = x.size(1);
   return cpu_fwd(A, zi, x, {B, T, 1, lti_shared(A, x) ? 0 : 1, 0, true});
 }
@@ -1129,10 +1120,6 @@ Triple lti_recur_backward_cpu(const Tensor &A, const Tensor &zi, const Tensor &y
   check_lti_recur(A, zi, y);
   check_cpu("lti_recur_backward", y);
   TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
-  if (is_half(y.scalar_type()))
-    return to_dtype(lti_recur_backward_cpu(A.to(at::kFloat), zi.to(at::kFloat), y.to(at::kFloat),
-                                           gy.to(at::kFloat)),
-                    y.scalar_type());
   const int64_t B = y.size(0), T = y.size(1);
   return cpu_bwd(A, zi, y, gy.to(y.scalar_type()), {B, T, 1, lti_shared(A, y) ? 0 : 1, 0, true});
 }
@@ -1141,8 +1128,6 @@ Tensor lti_recurN_cpu(const Tensor &A, const Tensor &zi, const Tensor &x) {
   check_common("lti_recurN", A, zi, x);
   check_lti_recurN(A, zi, x);
   check_cpu("lti_recurN", x);
-  if (is_half(x.scalar_type()))
-    return lti_recurN_cpu(A.to(at::kFloat), zi.to(at::kFloat), x.to(at::kFloat)).to(x.scalar_type());
   const int64_t B = x.size(0), T = x.size(1), M = A.size(-1);
   return cpu_fwd(A, zi, x, {B, T, M, A.dim() == 2 ? 0 : M * M, 0, false});
 }
@@ -1157,10 +1142,6 @@ Triple lti_recurN_backward_cpu(const Tensor &A, const Tensor &zi, const Tensor &
   check_lti_recurN(A, zi, y);
   check_cpu("lti_recurN_backward", y);
   TORCH_CHECK(gy.sizes() == y.sizes(), "grad_y must have y's shape");
-  if (is_half(y.scalar_type()))
-    return to_dtype(lti_recurN_backward_cpu(A.to(at::kFloat), zi.to(at::kFloat), y.to(at::kFloat),
-                                            gy.to(at::kFloat)),
-                    y.scalar_type());
   const int64_t B = y.size(0), T = y.size(1), M = A.size(-1);
   return cpu_bwd(A, zi, y, gy.to(y.scalar_type()), {B, T, M, A.dim() == 2 ? 0 : M * M, 0, false});
 }

@@ -38,8 +38,10 @@ def linear_recurrence(a: Tensor, init: Tensor, x: Tensor, *, unroll_factor: int 
         a: ``[N]`` (shared by the batch) or ``[B, N]`` coefficients.
         init: scalar or ``[B]`` initial state.
         x: ``[B, N]`` input.
-        unroll_factor: 1 = native scan on HIP devices (per-step loop on CPU);
-            ``k > 1`` = blocked PyTorch scan with blocks of ``k`` steps.
+        unroll_factor: 1 = the native scan (``philtorch::recur``) on CPU and
+            HIP tensors alike (the per-step PyTorch loop only without the
+            extension); ``k > 1`` = blocked PyTorch scan with blocks of ``k``
+            steps.
     Returns:
         ``[B, N]`` states.
     """

@@ -139,8 +139,10 @@ def state_space_recursion(
         A: ``[N, M, M]`` or ``[B, N, M, M]``.
         zi: ``[B, M]`` initial states.
         x: ``[B, N, M]`` or ``[B, N]`` (drives the first state).
-        unroll_factor: 1 = native scan on a HIP device (per-step loop on the
-            CPU); ``k > 1`` = blocked PyTorch scan with blocks of ``k`` steps.
+        unroll_factor: 1 = the native scan where the backend indicator
+            allows it (CPU tensors of any order, HIP tensors of order <= 4;
+            the per-step PyTorch loop otherwise); ``k > 1`` = blocked PyTorch
+            scan with blocks of ``k`` steps.
         out_idx: return only this state index.
     Returns:
         ``[B, N, M]`` (or ``[B, N]`` with ``out_idx``).

@@ -124,9 +124,10 @@ def state_space_recursion(
 ) -> Tensor:
     """States of ``h[t] = A h[t-1] + x[t]`` (philtorch/lti/ssm.py:198-383).
 
-    ``unroll_factor = 1`` runs the native scan on a HIP device (per-step loop
-    on the CPU); ``k > 1`` a blocked PyTorch scan whose block gains are the
-    powers ``A^1 .. A^k``.
+    ``unroll_factor = 1`` runs the native scan: on the CPU for any order, on
+    a HIP device for orders M <= 4 (the per-step PyTorch loop otherwise, or
+    without the extension); ``k > 1`` a blocked PyTorch scan whose block
+    gains are the powers ``A^1 .. A^k``.
     """
     assert x.dim() in (2, 3), f"Input signal must be 2D or 3D (batch, time, [features]), got {x.shape}"
     assert A.dim() in (2, 3), f"State matrix A must be 2D or 3D, got {A.shape}"

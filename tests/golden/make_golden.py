@@ -81,18 +81,49 @@ def cases():
             out.append(("recurN", coef3(M, T, M, M), rnd3(B, M), rnd3(B, T, M)))
             out.append(("lti_recurN", coef3(M, B, M, M), rnd3(B, M), rnd3(B, T, M)))
             out.append(("lti_recurN", coef3(M, M, M), rnd3(B, M), rnd3(B, T, M)))
+    # half and bfloat16: the reference's CPU loops run in those types, rounding
+    # after every operation; bfloat16 arrays are stored as their 16-bit
+    # patterns (uint16) with a dtype tag
+    import torch
+
+    g16 = np.random.default_rng(20261203)
+    for dt in ("float16", "bfloat16"):
+
+        def cast(v, dt=dt):
+            t = torch.from_numpy(np.ascontiguousarray(v, dtype=np.float32)).to(getattr(torch, dt))
+            return t.view(torch.uint16).numpy() if dt == "bfloat16" else t.numpy()
+
+        def rnd16(*shape):
+            return cast(g16.standard_normal(shape))
+
+        def coef16(*shape):
+            return cast(g16.uniform(-0.95, 0.95, shape))
+
+        B, T = 3, 37
+        out.append(("recurN", coef16(B, T, 1, 1), rnd16(B, 1), rnd16(B, T, 1), dt))
+        out.append(("recurN", coef16(T, 1, 1), rnd16(B, 1), rnd16(B, T, 1), dt))
+        out.append(("recurN", cast(0.6 * g16.uniform(-0.95, 0.95, (B, T, 2, 2))), rnd16(B, 2), rnd16(B, T, 2), dt))
+        out.append(("recurN", cast(0.6 * g16.uniform(-0.95, 0.95, (T, 2, 2))), rnd16(B, 2), rnd16(B, T, 2), dt))
+        out.append(("lti_recur", coef16(B), rnd16(B), rnd16(B, T), dt))
+        out.append(("lti_recur", coef16(1), rnd16(B), rnd16(B, T), dt))
+        out.append(("lti_recurN", cast(0.6 * g16.uniform(-0.95, 0.95, (B, 2, 2))), rnd16(B, 2), rnd16(B, T, 2), dt))
+        out.append(("lti_recurN", cast(0.6 * g16.uniform(-0.95, 0.95, (2, 2))), rnd16(B, 2), rnd16(B, T, 2), dt))
     return out
 
 
 def main() -> None:
     arrays = {}
-    for i, (op, A, zi, x) in enumerate(cases()):
-        y = ref_runner.run(op, A, zi, x)
+    for i, case in enumerate(cases()):
+        op, A, zi, x = case[:4]
+        dt = case[4] if len(case) > 4 else ""
+        y = ref_runner.run(op, A, zi, x, dt)
         arrays[f"{i}_op"] = np.array(op)
         arrays[f"{i}_A"], arrays[f"{i}_zi"], arrays[f"{i}_x"], arrays[f"{i}_y"] = A, zi, x, y
+        if dt:
+            arrays[f"{i}_dt"] = np.array(dt)
     path = os.path.join(HERE, "ref_vectors.npz")
     np.savez_compressed(path, **arrays)
-    print(f"wrote {len(arrays) // 5} cases to {path}")
+    print(f"wrote {sum(1 for k in arrays if k.endswith('_op'))} cases to {path}")
 
 
 if __name__ == "__main__":

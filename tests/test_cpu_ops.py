@@ -44,7 +44,8 @@ def _t(v):
 def _golden():
     data = np.load(GOLDEN)
     n = len([k for k in data.files if k.endswith("_op")])
-    return [(str(data[f"{i}_op"]), data[f"{i}_A"], data[f"{i}_zi"], data[f"{i}_x"], data[f"{i}_y"]) for i in range(n)]
+    return [(str(data[f"{i}_op"]), data[f"{i}_A"], data[f"{i}_zi"], data[f"{i}_x"], data[f"{i}_y"],
+             str(data[f"{i}_dt"]) if f"{i}_dt" in data.files else "") for i in range(n)]
 
 
 N_GOLDEN = len([k for k in np.load(GOLDEN).files if k.endswith("_op")])
@@ -52,8 +53,14 @@ N_GOLDEN = len([k for k in np.load(GOLDEN).files if k.endswith("_op")])
 
 @pytest.mark.parametrize("case", range(N_GOLDEN))
 def test_cpu_op_reproduces_reference_golden_vectors(ops, case):
-    op, A, zi, x, y = _golden()[case]
-    got = getattr(ops, op)(_t(A), _t(zi), _t(x)).numpy()
+    """Every golden case bit for bit, half and bfloat16 included (bfloat16
+    arrays are stored as their 16-bit patterns)."""
+    op, A, zi, x, y, dt = _golden()[case]
+    args = [_t(v) for v in (A, zi, x)]
+    if dt == "bfloat16":
+        args = [v.view(torch.bfloat16) for v in args]
+    out = getattr(ops, op)(*args)
+    got = (out.view(torch.uint16) if dt == "bfloat16" else out).numpy()
     assert got.dtype == y.dtype and got.shape == y.shape
     np.testing.assert_array_equal(got, y)
 
@@ -144,10 +151,23 @@ def test_cpu_empty_and_half(ops):
     a = torch.tensor(D.coef(g, (2, 300), np.float32))
     x, zi = torch.randn(2, 300), torch.randn(2)
     for dt in (torch.float16, torch.bfloat16):
-        y = ops.recur(a.to(dt), zi.to(dt), x.to(dt))
+        a16, zi16, x16 = a.to(dt), zi.to(dt), x.to(dt)
+        y = ops.recur(a16, zi16, x16)
         assert y.dtype == dt
-        ref = ops.recur(a.to(dt).float(), zi.to(dt).float(), x.to(dt).float()).to(dt)
-        assert torch.equal(y, ref)  # computed in fp32, rounded once
+        # the reference's loop in the 16-bit type: every product and sum
+        # rounded to it (philtorch/csrc/host_recurN.cpp:81-140 with scalar_t
+        # = Half / BFloat16)
+        h, ref = zi16.clone(), torch.empty_like(x16)
+        for t in range(x16.shape[1]):
+            h = x16[:, t] + (torch.zeros_like(h) + a16[:, t] * h)
+            ref[:, t] = h
+        assert torch.equal(y, ref)
+        # backward: the adjoint in the 16-bit type, within its rounding of the fp32 adjoint
+        gA, gz, gx = ops.recur_backward(a16, zi16, y, torch.ones_like(y))
+        gA32, gz32, gx32 = ops.recur_backward(a16.float(), zi16.float(), y.float(), torch.ones(2, 300))
+        for got, want in ((gA, gA32), (gz, gz32), (gx, gx32)):
+            assert got.dtype == dt
+            assert float((got.float() - want).abs().max()) <= 0.05 * float(want.abs().max())
 
 
 def test_cpu_errors(ops):

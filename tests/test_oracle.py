@@ -38,12 +38,16 @@ def _oracle_fwd(op, A, zi, x):
 
 
 def _golden_cases():
+    """The golden cases in the oracle's dtypes (fp32, fp64, complex, int64);
+    the half and bfloat16 cases pin the CPU key only (tests/test_cpu_ops.py):
+    the oracle restates the arithmetic of the wider types."""
     data = np.load(GOLDEN)
     n = len([k for k in data.files if k.endswith("_op")])
-    return [(str(data[f"{i}_op"]), data[f"{i}_A"], data[f"{i}_zi"], data[f"{i}_x"], data[f"{i}_y"]) for i in range(n)]
+    return [(str(data[f"{i}_op"]), data[f"{i}_A"], data[f"{i}_zi"], data[f"{i}_x"], data[f"{i}_y"]) for i in range(n)
+            if f"{i}_dt" not in data.files and data[f"{i}_A"].dtype != np.float16]
 
 
-N_GOLDEN = len([k for k in np.load(GOLDEN).files if k.endswith("_op")])
+N_GOLDEN = len(_golden_cases())
 
 
 @pytest.mark.parametrize("case", range(N_GOLDEN))
