@@ -12,8 +12,9 @@ exact tensors the bench times), checked against the oracle.
 * C3  LPV 2x2 fp32, B=32, T=2^20 (683 look-back tiles per row): all rows on
       the GPU, three checked.
 * C4  the 8-section SOS cascade, B=16, T=480000: op level (one lti_recur2 and
-      its backward per section, every section's gradients) and fused
-      (sosfilt), two rows checked.
+      its backward per section, every section's gradients), fused (sosfilt)
+      and the caller pattern (8 x lti.lfilter + autograd w.r.t. x, b, a),
+      two rows checked.
 
 The oracle restates the reference CPU loops (philtorch/csrc/host_recurN.cpp:
 81-111, host_lti_recur.cpp:4-80, host_lti_recurN.cpp:4-108) and the backward
@@ -186,3 +187,30 @@ def test_c4_fused_config(bench_mod):
     D.check(got[0], y_ref, "c4_fused y", dtype=np.float32)
     D.check(got[1], gx_ref, "c4_fused grad_x", dtype=np.float32)
     D.check(got[2], gsos_ref, "c4_fused grad_sos", dtype=np.float32)
+
+
+def test_c4_api_config(bench_mod):
+    """The C4 caller pattern exactly as the bench times it, ``for s in
+    range(8): y = lti.lfilter(b[:, s], a[:, s], y, form="tdf2",
+    unroll_factor=1)`` at B=16, T=480000 (every call the biquad kernels),
+    then autograd w.r.t. x, b and a; two rows against the oracle's
+    per-section chain evaluated in fp64 on the same fp32 inputs
+    (philtorch/lti/filtering.py:211-333 per call)."""
+    import oracle
+
+    w = bench_mod.make_workload("c4_api")
+    print(f"[c4_api] B={w.B} T={w.T} S={w.S} f32", flush=True)
+    rows = [0, w.B - 1]
+    out = w.step_fwd()
+    gx, gb, ga = w.step_bwd(out)
+    got = [_np(out[0][rows]), _np(gx[rows]), _np(gb[rows]), _np(ga[rows])]
+    del out, gx, gb, ga
+    w.dev = None
+    _free()
+    sos, x, gy = (np.ascontiguousarray(v.numpy()[rows]).astype(np.float64) for v in w.cpu)
+    y_ref, _ = oracle.sosfilt(sos, x)
+    gsos_ref, _, gx_ref = oracle.sosfilt_bwd(sos, x, None, gy)
+    D.check(got[0], y_ref, "c4_api y", dtype=np.float32)
+    D.check(got[1], gx_ref, "c4_api grad_x", dtype=np.float32)
+    D.check(got[2], gsos_ref[..., 0:3], "c4_api grad_b", dtype=np.float32)
+    D.check(got[3], gsos_ref[..., 4:6], "c4_api grad_a", dtype=np.float32)

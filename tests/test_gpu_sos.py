@@ -252,8 +252,11 @@ def test_sosfilt_opcheck(hip):
 
 def test_sosfilt_c4_size_matches_lfilter_chain(hip):
     """At the benchmark's C4 size (B=16, T=480000, 8 sections, fp32) the fused
-    cascade agrees with one lfilter(tdf2) per section on the native 2x2 scan,
-    forward and backward."""
+    cascade agrees with one lfilter(tdf2) per section (each a biquad on the
+    state-space kernel forward and the cascade kernel at one section
+    backward), forward and backward: the two HIP routes against each other;
+    tests/test_gpu_configs.py::test_c4_api_config checks the lfilter route
+    against the oracle at this size."""
     import torch
 
     g = D.rng(D.seed_of("sos-c4"))

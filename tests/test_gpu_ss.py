@@ -9,7 +9,8 @@ scipy.signal.dlsim in tests/test_oracle.py), evaluated in fp64 on the GPU's
 exact inputs.  Orders 1 to 4; dense stable A (a companion matrix in a random
 basis); shared and per-row A, b, c, d; b absent (input into state 0), c
 absent (out_idx), d absent; initial and final states; rows shorter than a
-lane's chunk, on and around a tile (6144 fp32 steps, 3072 fp64), of odd
+lane's chunk, on and around a tile (6144 fp32 steps, 3072 fp64; the
+order-2 fp32 plain pass's 30720-step wide tile, both directions), of odd
 length and of a million steps; the forced look-back fallback.  Through the
 torch API: lfilter of orders 1, 3 and 4 in both forms against the CPU
 (reference) route, state_space against its composed route, gradients
@@ -133,6 +134,25 @@ def test_lti_ss_capi_reversed(api, dtype, M, Bn, T):
         idx = M - 1
         _check(_run(api, A, None, None, None, None, x, out_idx=idx, rev=True), A, None, None, None, None, x, idx,
                dtype, name + " e0/out_idx", rev=True)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("M", ORDERS)
+@pytest.mark.parametrize("T", [30719, 30720, 30721, 61441])
+def test_lti_ss_capi_wide_tile_edges(api, dtype, M, T):
+    """Rows on and around the order-2 fp32 plain pass's wide tile (30720
+    steps: 15 data waves of 2 x 16 steps per lane) with the normal look-back,
+    both time directions: one tile, one tile and one step, three tiles
+    (61441 steps, two look-backs per row).  The other orders and fp64 run
+    their own tiles over the same rows."""
+    for shared in (False, True):
+        A, b, c, d, zi, x = _case(dtype, M, 3, T, shared, D.seed_of("ss-wide", dtype, M, T, shared))
+        for rev in (False, True):
+            name = f"wide M={M} T={T} shared={shared} rev={rev}"
+            _check(_run(api, A, b, c, d, zi, x, rev=rev), A, b, c, d, zi, x, None, dtype, name, rev=rev)
+        idx = M - 1
+        _check(_run(api, A, None, None, None, None, x, out_idx=idx), A, None, None, None, None, x, idx, dtype,
+               f"wide M={M} T={T} shared={shared} e0/out_idx")
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
