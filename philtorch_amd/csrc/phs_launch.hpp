@@ -127,6 +127,17 @@ Layout make_layout(int64_t B, int64_t T, bool TV, bool shared, bool backward) {
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Tile id -> row by multiply and shift (the kernels' `id / B` without a
+// 64-bit division): with l = ceil(log2 B) and s = 31 + l, m = floor(2^s / B)
+// + 1 gives floor(id m / 2^s) = floor(id / B) for every id below 2^31
+// (m B - 2^s lies in (0, B], and B <= 2^l).
+inline void row_split(int64_t B, uint64_t &magic, unsigned &shift) {
+  unsigned l = 0;
+  while ((uint64_t(1) << l) < uint64_t(B)) ++l;
+  shift = 31u + l;
+  magic = ((uint64_t(1) << shift) / uint64_t(B)) + 1u;
+}
+
 // Workgroups of `kernel` resident at once on the current device (occupancy
 // per CU times CUs), cached per (kernel, device); 0 if the query fails.
 inline int64_t resident_groups(const void *kernel, int threads) {
@@ -196,15 +207,7 @@ int launch(int64_t B, int64_t T, bool TV, bool shared, bool backward, const void
   const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
   a.spin_limit = sl ? sl : kDefaultSpinLimit;
   a.agg_only = g_agg_only.load(std::memory_order_relaxed) ? 1u : 0u;
-  // tile id -> row by multiply and shift: with l = ceil(log2 B) and
-  // s = 31 + l, m = floor(2^s / B) + 1 gives floor(id m / 2^s) = floor(id / B)
-  // for every id below 2^31 (m B - 2^s lies in (0, B], and B <= 2^l)
-  {
-    unsigned l = 0;
-    while ((uint64_t(1) << l) < uint64_t(B)) ++l;
-    a.b_shift = 31u + l;
-    a.b_magic = ((uint64_t(1) << a.b_shift) / uint64_t(B)) + 1u;
-  }
+  row_split(B, a.b_magic, a.b_shift);
   a.trace = nullptr;
   a.trace_tiles = 0;
   if (backward && gcoef) {

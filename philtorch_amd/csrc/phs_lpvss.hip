@@ -47,6 +47,7 @@ LpvSsArgs<Alg> lpv_args(int64_t B, int64_t T, const void *A, bool A_sh, bool A_t
   a.claims = reinterpret_cast<unsigned long long *>(ws);
   a.status = reinterpret_cast<uint64_t *>(ws + align_up(kHeaderBytes));
   a.tiles = unsigned(B * tiles_per_row);
+  row_split(B, a.b_magic, a.b_shift);
   a.per_stripe = (a.tiles + kStripes - 1) / kStripes;
   const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
   a.spin_limit = sl ? sl : kDefaultSpinLimit;

@@ -65,6 +65,8 @@ struct LpvSsArgs {
   int sum_b, sum_c, sum_d;
   typename Wide<E>::type *gpart;
   int64_t B, T_len, tiles_per_row;
+  uint64_t b_magic;  // tile id -> row by multiply and shift (row_split)
+  unsigned b_shift;
   unsigned long long *claims;
   unsigned tiles, per_stripe, spin_limit;
   unsigned agg_only;  // testing: tiles after a row's first publish no inclusive state
@@ -301,8 +303,8 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
     return;
   }
   unsigned tag = 0;
-  const int64_t q = id / a.B;  // tile position along the row
-  const int64_t b = id - q * a.B;
+  int64_t q, b;  // tile position along the row, row
+  split_tile(id, a.B, a.b_magic, a.b_shift, q, b);
   const int64_t T = a.T_len;
   const bool vec = a.vec_ok != 0;
   auto op = [](const M &p, const M &q2) { return compose<Alg>(p, q2); };

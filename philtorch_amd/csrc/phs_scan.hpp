@@ -196,6 +196,14 @@ __device__ __forceinline__ unsigned claim_finish(unsigned long long *claims, uns
   return __builtin_amdgcn_readfirstlane(tag);
 }
 
+// (q, b) of tile id = q * B + b with the host's row_split constants.
+__device__ __forceinline__ void split_tile(int64_t id, int64_t B, uint64_t magic, unsigned shift, int64_t &q,
+                                           int64_t &b) {
+  const unsigned uq = unsigned((uint64_t(unsigned(id)) * magic) >> shift);
+  q = uq;
+  b = int64_t(unsigned(id) - uq * unsigned(B));
+}
+
 // ------------------------------------------------------------ status words
 template <typename X>
 __device__ __forceinline__ void publish(uint64_t *dst, const X &v, unsigned tag) {
@@ -630,10 +638,8 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
       tr[kTrId] = uint64_t(id);
     }
   }
-  // id = qs * B + b, by multiply and shift (ids are below 2^31)
-  const unsigned uq = unsigned((uint64_t(unsigned(id)) * a.b_magic) >> a.b_shift);
-  const int64_t qs = uq;  // position in scan order
-  const int64_t b = int64_t(unsigned(id) - uq * unsigned(a.B));
+  int64_t qs, b;  // position in scan order, row: id = qs * B + b
+  split_tile(id, a.B, a.b_magic, a.b_shift, qs, b);
   const int64_t qf = REV ? a.tiles_per_row - 1 - qs : qs;  // position along time
   const int64_t T = a.T_len;
   const bool vec = a.vec_ok != 0;

@@ -133,6 +133,7 @@ void fill_common(SosArgs<E> &a, const SosLayout &L, int64_t B, int64_t T, int S,
   a.claims = reinterpret_cast<unsigned long long *>(ws);
   a.status = reinterpret_cast<uint64_t *>(ws + L.status_off);
   a.tiles = unsigned(B * L.tiles_per_row);
+  row_split(B, a.b_magic, a.b_shift);
   a.per_stripe = (a.tiles + kStripes - 1) / kStripes;
   const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
   a.spin_limit = sl ? sl : kDefaultSpinLimit;

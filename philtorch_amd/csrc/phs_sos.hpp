@@ -94,6 +94,8 @@ struct SosArgs {
   C *partials;             // gradient backward: [B, S, tiles, kWaves, 5] coefficient sums
   int64_t B, T_len, tiles_per_row, n_ckpt;
   int S;
+  uint64_t b_magic;            // tile id -> row by multiply and shift (row_split)
+  unsigned b_shift;
   unsigned long long *claims;  // kStripes claim words (workspace offset 0)
   unsigned tiles;              // B * tiles_per_row
   unsigned per_stripe;         // claims per stripe (grid = per_stripe * kStripes)
@@ -792,8 +794,8 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
     return;
   }
   unsigned tag = 0;
-  const int64_t qs = id / a.B;  // position in scan order
-  const int64_t b = id - qs * a.B;
+  int64_t qs, b;  // position in scan order, row
+  split_tile(id, a.B, a.b_magic, a.b_shift, qs, b);
   const int64_t tiles = a.tiles_per_row;
   const int64_t qf = REV ? tiles - 1 - qs : qs;  // position along time
   const int64_t T = a.T_len;

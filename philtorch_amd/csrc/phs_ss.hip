@@ -79,6 +79,7 @@ int ss_launch(SsArgs<Alg> a, hipStream_t stream) {
   a.tiles_per_row = (a.T_len + Sh::kTile - 1) / Sh::kTile;
   a.tiles = unsigned(a.B * a.tiles_per_row);
   a.per_stripe = (a.tiles + kStripes - 1) / kStripes;
+  row_split(a.B, a.b_magic, a.b_shift);
   launch_kernel((ss_kernel<Alg, REV, MODE>), dim3(a.per_stripe * kStripes), dim3(Sh::kThreads), 0, stream, a);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }

@@ -90,6 +90,8 @@ struct SsArgs {
   unsigned long long *claims;
   unsigned tiles, per_stripe, spin_limit;
   unsigned agg_only;  // testing: tiles after a row's first publish no inclusive state
+  uint64_t b_magic;   // tile id -> row by multiply and shift (row_split)
+  unsigned b_shift;
   uint64_t *status;
   int vec_ok;
   // plain forward of a second-order model (nullable): the state entering
@@ -122,7 +124,7 @@ constexpr int kSsPlain = 0, kSsStates = 1, kSsGrad = 2, kSsStatesY = 3;
 //
 // The fp32 order-2 plain pass is a wide tile instead: 15 data waves of 16
 // steps in 2 rounds (30720 steps) beside the look-back wave, held to 128
-// VGPRs (four waves per SIMD, 9 spilled), so one tile fills a CU's wave
+// VGPRs (four waves per SIMD; 98 used), so one tile fills a CU's wave
 // slots and a C4 call is 256 tiles all resident at once, where 3-wave tiles
 // at 158 VGPRs were 1264 tiles on 768 resident slots (two generations).
 template <class Alg, int MODE = kSsPlain>
@@ -137,6 +139,12 @@ struct SsShape {
   static constexpr int R = kWide ? 2 : (M <= 2 ? 4 : 2) / (MODE == kSsGrad ? 2 : 1);
   static constexpr int kWaveSeg = 64 * K * R;
   static constexpr int kTile = kWaves * kWaveSeg;
+  // The last kLdsRounds rounds' inputs wait in LDS between the passes.  The
+  // wide tile's second round (61 KB of the CU's 160) took it from 128 VGPRs
+  // with 32 (reversed 48) bytes a lane spilled to scratch, whose traffic
+  // reached HBM, to 98 (92) and none: 26.5 -> 25.7 us forward at the C4
+  // shape, reversed unchanged.  Both rounds measured no faster.
+  static constexpr int kLdsRounds = kWide ? 1 : 0;
   static_assert((K & (K - 1)) == 0, "K is a power of two (the lane matrix is A^K by squaring)");
 };
 
@@ -144,14 +152,15 @@ struct SsShape {
 // (REV), it is time T-1-s, so a lane's K steps are the K samples below
 // T - s0, read (and written) in descending time.  Positions past the row
 // read 0 and are not written.  The bounds-checked paths assign in branches
-// (no select between a global and a private address).
-template <bool REV, typename E, int K>
+// (no select between a global and a private address).  kFull: the chunk
+// is known to be in range and aligned, only the vector form is compiled.
+template <bool REV, typename E, int K, bool kFull = false>
 __device__ __forceinline__ void ss_load(const E *row, int64_t s0, int64_t T, bool vec, E (&out)[K]) {
   if constexpr (!REV) {
-    load_chunk<E, K>(row, s0, T, vec, out, E{});
+    load_chunk<E, K, kFull>(row, s0, T, vec, out, E{});
   } else {
     const int64_t base = T - s0 - K;  // lowest time of the chunk
-    if (vec && base >= 0) {
+    if (kFull || (vec && base >= 0)) {
       E tmp[K];
       load_chunk<E, K>(row, base, T, true, tmp, E{});
 #pragma unroll
@@ -169,13 +178,14 @@ __device__ __forceinline__ void ss_load(const E *row, int64_t s0, int64_t T, boo
   }
 }
 
-template <bool REV, typename E, int K>
+template <bool REV, typename E, int K, bool kFull = false>
 __device__ __forceinline__ void ss_store(E *row, int64_t s0, int64_t T, bool vec, const E (&v)[K]) {
+  static_assert(K * sizeof(E) % 16 == 0, "whole 16-byte vectors");
   if constexpr (!REV) {
-    store_chunk<E, K>(row, s0, T, vec, v);
+    store_chunk<E, K, kFull>(row, s0, T, vec, v);
   } else {
     const int64_t base = T - s0 - K;
-    if (vec && base >= 0) {
+    if (kFull || (vec && base >= 0)) {
       E tmp[K];
 #pragma unroll
       for (int k = 0; k < K; ++k) tmp[k] = v[K - 1 - k];
@@ -298,15 +308,34 @@ __device__ __forceinline__ SsModel<Alg> ss_model(const SsArgs<Alg> &a, int64_t r
   using E = typename Alg::elem;
   constexpr int M = V::M;
   SsModel<Alg> m;
+  // Every coefficient is read before any is used, with no branch around a
+  // read (absent operands read an in-bounds stand-in and are selected away
+  // after), so the reads overlap in one round trip instead of one each.
   if (a.filt_form == 0) {
-    m.A = V::load_mat(a.A + row * a.A_stride);
+    const E *pA = a.A + row * a.A_stride;
+    const E *pb = a.bv ? a.bv + row * a.b_stride : pA;
+    const E *pc = a.cv ? a.cv + row * a.c_stride : pA;
+    const E *pd = a.d ? a.d + row * a.d_stride : pA;
+    const typename Alg::s_coef Am = V::load_mat(pA);
+    const typename Alg::s_state bl = V::load_vec(pb), cl = V::load_vec(pc);
+    const E dl = pd[0];
+    m.A = Am;
     if (kAdjoint && a.A_trans) m.A = Alg::s_adjoint(m.A);  // real: the transpose
-    m.b = a.bv ? V::load_vec(a.bv + row * a.b_stride) : V::unit(kAdjoint ? a.in_idx : 0);
-    m.c = a.cv ? V::load_vec(a.cv + row * a.c_stride) : V::unit(a.out_idx);
-    m.d = a.d ? a.d[row * a.d_stride] : E(0);
+    m.b = a.bv ? bl : V::unit(kAdjoint ? a.in_idx : 0);
+    m.c = a.cv ? cl : V::unit(a.out_idx);
+    m.d = a.d ? dl : E(0);
     return m;
   }
   const E *fb = a.fb + row * a.f_stride_b, *fa = a.fa + row * a.f_stride_a;
+  E fav[M], fbv[M + 1];  // nb >= 1 and na >= 1: index 0 is always in range
+#pragma unroll
+  for (int i = 0; i < M; ++i) fav[i] = fa[i < a.na ? i : 0];
+#pragma unroll
+  for (int i = 0; i <= M; ++i) fbv[i] = fb[i < a.nb ? i : 0];
+#pragma unroll
+  for (int i = 0; i < M; ++i) fav[i] = i < a.na ? fav[i] : E(0);
+#pragma unroll
+  for (int i = 0; i <= M; ++i) fbv[i] = i < a.nb ? fbv[i] : E(0);
   union {
     typename Alg::s_coef s;
     E e[M * M];
@@ -315,17 +344,15 @@ __device__ __forceinline__ SsModel<Alg> ss_model(const SsArgs<Alg> &a, int64_t r
     typename Alg::s_state s;
     E e[M];
   } g;
-  const E b0 = fb[0];
+  const E b0 = fbv[0];
 #pragma unroll
   for (int i = 0; i < M; ++i) {
-    const E ai = i < a.na ? fa[i] : E(0);
-    const E bi = i + 1 < a.nb ? fb[i + 1] : E(0);
-    g.e[i] = bi - b0 * ai;
+    g.e[i] = fbv[i + 1] - b0 * fav[i];
 #pragma unroll
     for (int j = 0; j < M; ++j) {
       // companion(a): row 0 = -a, ones below the diagonal
-      const E comp_ij = i == 0 ? -(j < a.na ? fa[j] : E(0)) : (j == i - 1 ? E(1) : E(0));
-      const E comp_ji = j == 0 ? -ai : (i == j - 1 ? E(1) : E(0));
+      const E comp_ij = i == 0 ? -fav[j] : (j == i - 1 ? E(1) : E(0));
+      const E comp_ji = j == 0 ? -fav[i] : (i == j - 1 ? E(1) : E(0));
       A.e[i * M + j] = a.filt_form == 1 ? comp_ji : comp_ij;
     }
   }
@@ -718,6 +745,61 @@ __device__ __forceinline__ void ss_grad_step(SsGrad<Alg, typename Alg::elem> &ac
 }
 
 // At least two waves per SIMD (two workgroups per CU; wide tiles four).
+// Slot swizzle of a lane-blocked LDS buffer of NV 16-byte vectors a lane:
+// lane L's vector v sits at L NV + (v ^ ss_swizzle<NV>(L)), so that both the
+// lanes' writes of one vector and the reads of 64 consecutive vectors fall
+// in distinct banks within each group of 16 lanes.
+template <int NV>
+__device__ __forceinline__ int ss_swizzle(int L) {
+  static_assert(NV >= 1 && NV <= 16 && (NV & (NV - 1)) == 0, "a power of two up to 16");
+  constexpr int p = NV >= 16 ? 4 : NV >= 8 ? 3 : NV >= 4 ? 2 : NV >= 2 ? 1 : 0;
+  return (L >> (4 - p)) & (NV - 1);
+}
+
+// Group g0 .. g0+G-1 of a lane's K steps (items of type X, whole 16-byte
+// vectors) into the wave's lane-blocked buffer `wb`, in ascending time (a
+// reversed pass walks its chunk downwards).
+template <int NV, bool REV, int K, typename X, int G>
+__device__ __forceinline__ void ss_lds_put(uint4 *wb, int lane, int g0, const X (&items)[G]) {
+  constexpr int NG = int(G * sizeof(X) / 16);
+  static_assert(G * sizeof(X) % 16 == 0 && K % G == 0, "whole vectors");
+  union {
+    X x[G];
+    uint4 u[NG];
+  } t;
+#pragma unroll
+  for (int i = 0; i < G; ++i) t.x[i] = items[REV ? G - 1 - i : i];
+  const int v0 = int((REV ? K - g0 - G : g0) * sizeof(X) / 16);
+  const int sw = ss_swizzle<NV>(lane);
+#pragma unroll
+  for (int i = 0; i < NG; ++i) wb[lane * NV + ((v0 + i) ^ sw)] = t.u[i];
+}
+
+// The wave's buffer to the round's block at dst (16-byte aligned, in range):
+// vector c of the block is lane c / NV's vector c % NV, so each store
+// instruction writes 64 consecutive vectors.
+template <int NV>
+__device__ __forceinline__ void ss_lds_flush(uint4 *dst, const uint4 *wb, int lane, bool write) {
+  wave_sync();
+  if (write) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = j * 64 + lane, L = c / NV, v = c % NV;
+      dst[c] = wb[L * NV + (v ^ ss_swizzle<NV>(L))];
+    }
+  }
+  wave_sync();  // the next round's writes follow these reads
+}
+
+// A workgroup barrier with no wait for outstanding memory operations, whose
+// memory accesses stay on their side of it: memory operations issued before
+// it by one wave are queued ahead of those the others issue after it.
+__device__ __forceinline__ void issue_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <class Alg, bool REV, int MODE>
 __global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), (SsShape<Alg, MODE>::kMinWaves)) void ss_kernel(
     SsArgs<Alg> a) {
@@ -736,6 +818,34 @@ __global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), (SsShape<Alg, MODE>
   __shared__ unsigned s_id, s_tag;
   __shared__ uint64_t s_look[St::kLookWords];
   __shared__ SsPowers<Alg> s_tab;
+  __shared__ SsModel<Alg> s_model;  // the row's model, from the look-back wave
+  // inputs of the rounds that wait in LDS, 16 bytes a lane at a time, lanes
+  // adjacent: [wave][round][vector][lane]
+  constexpr int kLR = Sh::kLdsRounds;
+  constexpr int kEV = int(16 / sizeof(E));  // elements per 16-byte vector
+  struct alignas(16) Vec16 {
+    E e[kEV];
+  };
+  __shared__ Vec16 s_xin[kLR > 0 ? kWaves * kLR * (K / kEV) * 64 : 1];
+  // Outputs and states of full tiles leave through LDS: a lane's K steps
+  // are K consecutive samples, so a 16-byte store instruction of the lanes
+  // themselves touches 64 separate segments; transposed, each instruction
+  // writes 1 KB of the row in one piece.  [wave][lane-blocked vectors,
+  // swizzled], one round at a time.  At the C4 shape (fp32): order-2
+  // lfilter 25.7 -> 22.3 us forward and 26.5 -> 22.0 reversed (a plain
+  // copy in the wide tile's geometry takes 26.6 us lane-blocked, 21.7
+  // transposed), the order-2 states pass 38.2 -> 29.5, order 4's 69.6 ->
+  // 57.2, order 1 23.0 -> 22.2.  The plain pass of orders 3-4 (2.5
+  // generations of tiles, 4 x 4 steps) ran 49 -> 53 us forward with it and
+  // keeps its lanes' stores.
+  constexpr bool kStates = MODE == kSsStates || MODE == kSsStatesY;
+  constexpr int kNVy = int(K * sizeof(E) / 16);   // 16-byte vectors of outputs per lane and round
+  constexpr int kNVh = int(K * sizeof(SS) / 16);  // of states
+  constexpr bool kYLds = MODE != kSsStates && !(MODE == kSsPlain && V::M >= 3) && kNVy > 1;
+  constexpr bool kHLds = kStates && kNVh > 1 && (kNVh & (kNVh - 1)) == 0 && kNVh <= 16 &&
+                         int(K * sizeof(SS)) % 16 == 0;
+  __shared__ uint4 s_yt[kYLds ? kWaves * 64 * kNVy : 1];
+  __shared__ uint4 s_ht[kHLds ? kWaves * 64 * kNVh : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -748,14 +858,20 @@ __global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), (SsShape<Alg, MODE>
     return;
   }
   unsigned tag = 0;
-  const int64_t q = id / a.B;  // tile position along the row
-  const int64_t b = id - q * a.B;
+  int64_t q, b;  // tile position along the row, row
+  split_tile(id, a.B, a.b_magic, a.b_shift, q, b);
   const int64_t T = a.T_len;
 
   if (w == kWaves) {
     // ================= look-back wave: power tables, then the look-back
     {
-      typename Alg::coef P = ss_pow2<Alg>(ss_model<Alg, MODE == kSsGrad>(a, b).A, __builtin_ctz(K));
+      // the model's reads go out before the data waves' input loads (the
+      // barrier below, without a wait, releases them): the power tables,
+      // which the data waves wait for, start as soon as the model is in
+      const SsModel<Alg> mrow = ss_model<Alg, MODE == kSsGrad>(a, b);
+      issue_barrier();
+      if (lane == 0) s_model = mrow;
+      typename Alg::coef P = ss_pow2<Alg>(mrow.A, __builtin_ctz(K));
 #pragma unroll
       for (int i = 0; i < 6; ++i) {
         if (lane == 0) s_tab.pw[i] = P;
@@ -812,123 +928,187 @@ __global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), (SsShape<Alg, MODE>
   }
 
   // ================= data waves
-  const SsModel<Alg> m = ss_model<Alg, MODE == kSsGrad>(a, b);
   const bool vec = a.vec_ok != 0;
   const E *xrow = a.x + b * T;
   const int64_t seg0 = q * Sh::kTile + int64_t(w) * Sh::kWaveSeg;
   const int sl = ss_scan_lane<REV>(lane);
-  int64_t t0s[R];
-  E X[R][K];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    t0s[r] = seg0 + int64_t(r) * 64 * K + int64_t(sl) * K;
-    ss_load<REV, E, K>(xrow, t0s[r], T, vec, X[r]);
-  }
-  __syncthreads();  // power tables
-
-  // ---- pass 1: every map's matrix part is a known power of A, so only the
-  // vector parts are scanned.  Steps past the row's end take a zero input
-  // and only touch the aggregate of its last tile, which nobody reads.
-  S ex[R], tot[R];
-  {
-    S v[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) v[r] = ss_lane_fold<Alg, K>(m, X[r]);
-    ss_lane_scan<Alg, R, REV>(v, lane, s_tab.pw);
+  // fp32 orders 3-4: the data waves read the model themselves and fold
+  // before the power tables are in (the look-back wave's 4 x 4 products take
+  // longer than the loads): 52.5 -> 49.1 us forward and 52.9 -> 49.7
+  // reversed at order 4 on the C4 shape.  Orders 1-2 (a short table build)
+  // and fp64 (register spills at order 4) take the model from LDS.
+  constexpr bool kOwnModel = V::M >= 3 && sizeof(E) == 4;
+  // The data path, compiled twice: kFull for tiles wholly inside the row
+  // with aligned rows (vector loads and stores only, so each round's fold
+  // waits for its own loads), and the bounds-checked form.
+  auto data_path = [&](auto full_c) {
+    constexpr bool kFull = decltype(full_c)::value;
+    issue_barrier();  // the look-back wave has issued the model's reads
+    SsModel<Alg> mown;
+    if constexpr (kOwnModel) mown = ss_model<Alg, MODE == kSsGrad>(a, b);
+    int64_t t0s[R];
+    E X[R][K];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      tot[r] = read_lane(v[r], ss_last_lane<REV>());
-      const S prev = shfl_from(v[r], REV ? lane + 1 : lane - 1);
-      ex[r] = sl > 0 ? prev : Alg::szero();
+      t0s[r] = seg0 + int64_t(r) * 64 * K + int64_t(sl) * K;
+      ss_load<REV, E, K, kFull>(xrow, t0s[r], T, vec, X[r]);
     }
-  }
-  if (lane == 0) {
-    S agg = tot[0];
+    // ---- pass 1: every map's matrix part is a known power of A, so only the
+    // vector parts are scanned.  Steps past the row's end take a zero input
+    // and only touch the aggregate of its last tile, which nobody reads.
+    S v[R];
+    if constexpr (kOwnModel) {
 #pragma unroll
-    for (int r = 1; r < R; ++r) agg = Alg::affine(s_tab.pw[6], agg, tot[r]);
-    s_wagg[w] = agg;
-  }
-  __syncthreads();  // wave aggregates are in s_wagg
-  __syncthreads();  // entry state is in s_in
-  // the wave's entry state: A^(64 K R w) s_in + its exclusive prefix
-  S st = s_in;
-  for (int j = 0; j < w; ++j) st = Alg::affine(s_tab.pw[7], st, Alg::szero());
-  st = Alg::sadd(st, s_wpre[w]);
+      for (int r = 0; r < R; ++r) v[r] = ss_lane_fold<Alg, K>(mown, X[r]);
+    }
+    __syncthreads();  // power tables and the model
+    // Otherwise the model comes from LDS as wave-uniform values, and the
+    // data waves issue no global load but the inputs' before pass 1.
+    const SsModel<Alg> m = kOwnModel ? mown : read_lane(s_model, 0);
+    S ex[R];
+    S tot[R];
+    {
+      if constexpr (!kOwnModel) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] = ss_lane_fold<Alg, K>(m, X[r]);
+      }
+#pragma unroll
+      for (int r = R - kLR; r < R; ++r) {
+#pragma unroll
+        for (int j = 0; j < K / kEV; ++j) {
+          Vec16 t;
+#pragma unroll
+          for (int i = 0; i < kEV; ++i) t.e[i] = X[r][j * kEV + i];
+          s_xin[((w * kLR + r - (R - kLR)) * (K / kEV) + j) * 64 + lane] = t;
+        }
+      }
+      ss_lane_scan<Alg, R, REV>(v, lane, s_tab.pw);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        tot[r] = read_lane(v[r], ss_last_lane<REV>());
+        const S prev = shfl_from(v[r], REV ? lane + 1 : lane - 1);
+        ex[r] = sl > 0 ? prev : Alg::szero();
+      }
+    }
+    if (lane == 0) {
+      S agg = tot[0];
+#pragma unroll
+      for (int r = 1; r < R; ++r) agg = Alg::affine(s_tab.pw[6], agg, tot[r]);
+      s_wagg[w] = agg;
+    }
+    __syncthreads();  // wave aggregates are in s_wagg
+    __syncthreads();  // entry state is in s_in
+    // the wave's entry state: A^(64 K R w) s_in + its exclusive prefix
+    S st = s_in;
+    for (int j = 0; j < w; ++j) st = Alg::affine(s_tab.pw[7], st, Alg::szero());
+    st = Alg::sadd(st, s_wpre[w]);
 
-  // ---- pass 2: round r of the wave starts at st[r] (st[r+1] = A^(64 K)
-  // st[r] + tot[r]); a lane enters it at A^(K sl) st[r] + ex[r], then
-  // y = c . h + d x and the step
-  S ent[R];
-  ent[0] = st;
+    // ---- pass 2: round r of the wave starts at st[r] (st[r+1] = A^(64 K)
+    // st[r] + tot[r]); a lane enters it at A^(K sl) st[r] + ex[r], then
+    // y = c . h + d x and the step
+    S ent[R];
+    ent[0] = st;
 #pragma unroll
-  for (int r = 1; r < R; ++r) ent[r] = Alg::affine(s_tab.pw[6], ent[r - 1], tot[r - 1]);
-  ss_pow_apply<Alg, 6, R>(s_tab.pw, sl, ent);
-  constexpr bool kStates = MODE == kSsStates || MODE == kSsStatesY;
-  constexpr int G = MODE == kSsPlain ? K : ss_state_group<Alg>();
-  const bool vh = a.vec_hs != 0;
-  SsGrad<Alg, E> lacc;
-  if constexpr (MODE == kSsGrad) {
+    for (int r = 1; r < R; ++r) ent[r] = Alg::affine(s_tab.pw[6], ent[r - 1], tot[r - 1]);
+    ss_pow_apply<Alg, 6, R>(s_tab.pw, sl, ent);
+    // steps per group: plain outputs are written a 16-byte vector at a time
+    // (not held for the whole chunk); the state modes group whole state
+    // vectors
+    constexpr int G = MODE == kSsPlain ? int(16 / sizeof(E)) : ss_state_group<Alg>();
+    static_assert(K % G == 0 && G * sizeof(E) % 16 == 0, "groups of whole output vectors");
+    const bool vh = a.vec_hs != 0;
+    SsGrad<Alg, E> lacc;
+    if constexpr (MODE == kSsGrad) {
 #pragma unroll
-    for (int j = 0; j < SsGrad<Alg>::kN; ++j) lacc.v[j] = E(0);
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if constexpr (MODE == kSsPlain && !REV && V::M == 2) {
-      if (a.ckpt && t0s[r] < T && t0s[r] % a.ckpt_every == 0)
-        reinterpret_cast<S *>(a.ckpt)[b * a.n_ckpt + t0s[r] / a.ckpt_every] = Alg::sadd(ent[r], ex[r]);
+      for (int j = 0; j < SsGrad<Alg>::kN; ++j) lacc.v[j] = E(0);
     }
-    SS h = Alg::store_s(Alg::sadd(ent[r], ex[r]));
-    E O[K];
+    const bool want_y = MODE == kSsPlain || MODE == kSsStatesY || (MODE == kSsGrad && a.y);
 #pragma unroll
-    for (int g0 = 0; g0 < K; g0 += G) {
-      SS Hg[G];
-      E Xg[G];
-      if constexpr (MODE == kSsGrad) {
-        ss_load<REV, SS, G>(reinterpret_cast<const SS *>(a.hs_fwd) + b * T, t0s[r] + g0, T, vh, Hg);
-        ss_load<REV, E, G>(a.x_fwd + b * T, t0s[r] + g0, T, vh, Xg);
-      }
+    for (int r = 0; r < R; ++r) {
+      if (r >= R - kLR) {
 #pragma unroll
-      for (int k2 = 0; k2 < G; ++k2) {
-        const int k = g0 + k2;
-        if constexpr (kStates) Hg[k2] = h;
-        if constexpr (MODE != kSsStates) {
-          O[k] = fma(m.d, X[r][k], V::dot(m.c, h));
-          if constexpr (MODE == kSsGrad) ss_grad_step<Alg>(lacc, h, Hg[k2], Xg[k2], X[r][k]);
-        }
-        h = Alg::s_affine(m.A, h, V::scale(m.b, X[r][k]));
-        if (MODE != kSsStates && a.zf && t0s[r] + k == T - 1) {
-          union {
-            SS s;
-            E e[V::M];
-          } u;
-          u.s = h;
+        for (int j = 0; j < K / kEV; ++j) {
+          const Vec16 t = s_xin[((w * kLR + r - (R - kLR)) * (K / kEV) + j) * 64 + lane];
 #pragma unroll
-          for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = u.e[i];
+          for (int i = 0; i < kEV; ++i) X[r][j * kEV + i] = t.e[i];
         }
       }
-      if constexpr (kStates) ss_store<REV, SS, G>(reinterpret_cast<SS *>(a.hs) + b * T, t0s[r] + g0, T, vh, Hg);
+      const S h0 = Alg::sadd(ent[r], ex[r]);
+      if constexpr (MODE == kSsPlain && !REV && V::M == 2) {
+        if (a.ckpt && t0s[r] < T && t0s[r] % a.ckpt_every == 0)
+          reinterpret_cast<S *>(a.ckpt)[b * a.n_ckpt + t0s[r] / a.ckpt_every] = h0;
+      }
+      SS h = Alg::store_s(h0);
+#pragma unroll
+      for (int g0 = 0; g0 < K; g0 += G) {
+        SS Hg[G];
+        E Xg[G];
+        E Og[G];
+        if constexpr (MODE == kSsGrad) {
+          ss_load<REV, SS, G>(reinterpret_cast<const SS *>(a.hs_fwd) + b * T, t0s[r] + g0, T, vh, Hg);
+          ss_load<REV, E, G>(a.x_fwd + b * T, t0s[r] + g0, T, vh, Xg);
+        }
+#pragma unroll
+        for (int k2 = 0; k2 < G; ++k2) {
+          const int k = g0 + k2;
+          if constexpr (kStates) Hg[k2] = h;
+          if constexpr (MODE != kSsStates) {
+            Og[k2] = fma(m.d, X[r][k], V::dot(m.c, h));
+            if constexpr (MODE == kSsGrad) ss_grad_step<Alg>(lacc, h, Hg[k2], Xg[k2], X[r][k]);
+          }
+          h = Alg::s_affine(m.A, h, V::scale(m.b, X[r][k]));
+          if (MODE != kSsStates && a.zf && t0s[r] + k == T - 1) {
+            union {
+              SS s;
+              E e[V::M];
+            } u;
+            u.s = h;
+#pragma unroll
+            for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = u.e[i];
+          }
+        }
+        if constexpr (kFull && kHLds)
+          ss_lds_put<kNVh, REV, K>(s_ht + w * 64 * kNVh, lane, g0, Hg);
+        else if constexpr (kStates)
+          ss_store<REV, SS, G>(reinterpret_cast<SS *>(a.hs) + b * T, t0s[r] + g0, T, vh, Hg);
+        if constexpr (kFull && kYLds)
+          ss_lds_put<kNVy, REV, K>(s_yt + w * 64 * kNVy, lane, g0, Og);
+        else if (want_y)
+          ss_store<REV, E, G, kFull>(a.y + b * T, t0s[r] + g0, T, vec, Og);
+      }
+      // the round's block, lowest time first
+      const int64_t p0 = seg0 + int64_t(r) * 64 * K;  // first scan position of the round
+      const int64_t tb = REV ? T - p0 - 64 * K : p0;
+      if constexpr (kFull && kHLds)
+        ss_lds_flush<kNVh>(reinterpret_cast<uint4 *>(reinterpret_cast<SS *>(a.hs) + b * T + tb),
+                           s_ht + w * 64 * kNVh, lane, true);
+      if constexpr (kFull && kYLds)
+        ss_lds_flush<kNVy>(reinterpret_cast<uint4 *>(a.y + b * T + tb), s_yt + w * 64 * kNVy, lane, want_y);
     }
-    if (MODE == kSsPlain || MODE == kSsStatesY || (MODE == kSsGrad && a.y))
-      ss_store<REV, E, K>(a.y + b * T, t0s[r], T, vec, O);
-  }
-  if constexpr (MODE == kSsGrad) {
-    // the wave's sums, in a fixed order, one partial per (row, tile, wave)
-    auto add = [](const SsGrad<Alg> &p, const SsGrad<Alg> &o) {
-      SsGrad<Alg> r;
+    if constexpr (MODE == kSsGrad) {
+      // the wave's sums, in a fixed order, one partial per (row, tile, wave)
+      auto add = [](const SsGrad<Alg> &p, const SsGrad<Alg> &o) {
+        SsGrad<Alg> r;
 #pragma unroll
-      for (int j = 0; j < SsGrad<Alg>::kN; ++j) r.v[j] = p.v[j] + o.v[j];
-      return r;
-    };
-    SsGrad<Alg> gacc;
+        for (int j = 0; j < SsGrad<Alg>::kN; ++j) r.v[j] = p.v[j] + o.v[j];
+        return r;
+      };
+      SsGrad<Alg> gacc;
 #pragma unroll
-    for (int j = 0; j < SsGrad<Alg>::kN; ++j) gacc.v[j] = up(lacc.v[j]);
-    gacc = wave_scan_incl(gacc, lane, add);
-    if (lane == 63) {
-      auto *dst = a.gpart + ((b * a.tiles_per_row + q) * kWaves + w) * SsGrad<Alg>::kN;
+      for (int j = 0; j < SsGrad<Alg>::kN; ++j) gacc.v[j] = up(lacc.v[j]);
+      gacc = wave_scan_incl(gacc, lane, add);
+      if (lane == 63) {
+        auto *dst = a.gpart + ((b * a.tiles_per_row + q) * kWaves + w) * SsGrad<Alg>::kN;
 #pragma unroll
-      for (int j = 0; j < SsGrad<Alg>::kN; ++j) dst[j] = gacc.v[j];
+        for (int j = 0; j < SsGrad<Alg>::kN; ++j) dst[j] = gacc.v[j];
+      }
     }
-  }
+  };
+  // the state modes' full path also needs 16-byte state rows (vec_hs)
+  if (vec && (!kStates || a.vec_hs) && (q + 1) * Sh::kTile <= T)
+    data_path(std::true_type{});
+  else
+    data_path(std::false_type{});
 }
 
 // ------------------------------------------------------------ coefficient gradients
