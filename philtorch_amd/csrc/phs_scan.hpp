@@ -247,6 +247,57 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// ------------------------------------------------------------ coalesced stores
+// A lane that owns K consecutive steps writes them as NV 16-byte vectors of
+// its own, so one store instruction of the wave touches 64 separate
+// segments.  Through a lane-blocked LDS buffer of the wave (64 NV vectors)
+// the same block leaves as NV instructions of 64 consecutive vectors each
+// (1 KB in one piece).  Slot swizzle: block lane L's vector v sits at
+// L NV + (v ^ lds_swizzle<NV>(L)), so both the lanes' writes of one vector
+// and the reads of 64 consecutive vectors fall in distinct banks within
+// each group of 16 lanes.
+template <int NV>
+__device__ __forceinline__ int lds_swizzle(int L) {
+  static_assert(NV >= 1 && NV <= 16 && (NV & (NV - 1)) == 0, "a power of two up to 16");
+  constexpr int p = NV >= 16 ? 4 : NV >= 8 ? 3 : NV >= 4 ? 2 : NV >= 2 ? 1 : 0;
+  return (L >> (4 - p)) & (NV - 1);
+}
+
+// NV vectors a lane, block lane count 64 and a power of two up to 16.
+template <typename X, int K>
+constexpr bool kLdsBlocked = int(K * sizeof(X)) % 16 == 0 && int(K * sizeof(X) / 16) > 1 &&
+                             int(K * sizeof(X) / 16) <= 16 && (int(K * sizeof(X) / 16) & (int(K * sizeof(X) / 16) - 1)) == 0;
+
+// Block lane L's chunk (ascending) into the wave's buffer.
+template <typename X, int K>
+__device__ __forceinline__ void lds_put_chunk(uint4 *wb, int L, const X (&v)[K]) {
+  constexpr int NV = int(K * sizeof(X) / 16);
+  union {
+    X x[K];
+    uint4 u[NV];
+  } t;
+#pragma unroll
+  for (int k = 0; k < K; ++k) t.x[k] = v[k];
+  const int sw = lds_swizzle<NV>(L);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) wb[L * NV + (i ^ sw)] = t.u[i];
+}
+
+// The wave's buffer to its block at dst (16-byte aligned, in range): vector
+// c of the block is block lane c / NV's vector c % NV.
+template <int NV>
+__device__ __forceinline__ void lds_flush(uint4 *dst, const uint4 *wb, int lane, bool write) {
+  wave_sync();
+  if (write) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = j * 64 + lane, L = c / NV, v = c % NV;
+      dst[c] = wb[L * NV + (v ^ lds_swizzle<NV>(L))];
+    }
+  }
+  wave_sync();  // later writes to the buffer follow these reads
+}
+
 // Wave-level look-back.  `row_status` points at tile 0 of this row's status;
 // `virt` is the state entering the row (zi forward, 0 backward); `s_look` is
 // LDS for one window.
@@ -584,6 +635,15 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
   __shared__ AC s_acc[kWaves];
   __shared__ uint64_t s_look[Sh::kLookWords];
   __shared__ unsigned s_ready;  // data waves whose aggregate is in s_wagg
+  // Outputs of whole rounds leave through LDS (lds_flush) where a lane's
+  // chunk is more than one 16-byte vector: states (forward y, backward
+  // grad_x) and per-step coefficient gradients, one buffer per wave
+  constexpr bool kSLds = kLdsBlocked<SS, K>;
+  constexpr bool kCLds = TV && REV && kLdsBlocked<SC, K>;
+  constexpr int kNVs = kSLds ? int(K * sizeof(SS) / 16) : 1;
+  constexpr int kNVc = kCLds ? int(K * sizeof(SC) / 16) : 1;
+  constexpr int kNVb = kNVs > kNVc ? kNVs : kNVc;
+  __shared__ uint4 s_out[(kSLds || kCLds) ? kWaves * 64 * kNVb : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   // wave index as a scalar: the role branches below are scalar branches, so a
@@ -748,6 +808,10 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
     auto pass2 = [&](int r, SS h) -> AC {
       AC acc = Alg::acc_zero();
       const int64_t t0 = chunk0(r);
+      // the round's block (lowest time first) and whether it is whole and aligned
+      const int64_t blk0 = t0 - int64_t(pl) * K;
+      const bool blk_full = kFull || (vec && blk0 + 64 * K <= T);
+      uint4 *wb = s_out + w * 64 * kNVb;
       if constexpr (!REV) {
         SS O[K];
 #pragma unroll
@@ -755,7 +819,14 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
           h = Alg::s_affine(TV ? A[r][TV ? k : 0] : a_row_s, h, X[r][k]);
           O[k] = h;
         }
-        store_chunk<SS, K, kFull>(yrow, t0, T, vec, O);
+        if (kSLds && blk_full) {
+          if constexpr (kSLds) {
+            lds_put_chunk<SS, K>(wb, pl, O);
+            lds_flush<kNVs>(reinterpret_cast<uint4 *>(yrow + blk0), wb, lane, true);
+          }
+        } else {
+          store_chunk<SS, K, kFull>(yrow, t0, T, vec, O);
+        }
       } else {
         SS nu = h;
         SS GX[K];
@@ -774,9 +845,23 @@ __global__ __launch_bounds__((Shape<Alg, TV>::kThreads), Alg::kMinWavesPerEU) vo
           nu = Alg::s_affine(c, lam, zero_ss);
           if (t0 + k == 0 && a.gzi) reinterpret_cast<SS *>(a.gzi)[b] = nu;
         }
-        if (gxrow) store_chunk<SS, K, kFull>(gxrow, t0, T, vec, GX);
+        if (kSLds && blk_full) {
+          if constexpr (kSLds) {
+            lds_put_chunk<SS, K>(wb, pl, GX);
+            lds_flush<kNVs>(reinterpret_cast<uint4 *>(gxrow + blk0), wb, lane, gxrow != nullptr);
+          }
+        } else if (gxrow) {
+          store_chunk<SS, K, kFull>(gxrow, t0, T, vec, GX);
+        }
         if constexpr (TV) {
-          if (gcrow) store_chunk<SC, K, kFull>(gcrow, t0, T, vec, GC);
+          if (kCLds && blk_full) {
+            if constexpr (kCLds) {
+              lds_put_chunk<SC, K>(wb, pl, GC);
+              lds_flush<kNVc>(reinterpret_cast<uint4 *>(gcrow + blk0), wb, lane, gcrow != nullptr);
+            }
+          } else if (gcrow) {
+            store_chunk<SC, K, kFull>(gcrow, t0, T, vec, GC);
+          }
         }
       }
       return acc;

@@ -745,20 +745,9 @@ __device__ __forceinline__ void ss_grad_step(SsGrad<Alg, typename Alg::elem> &ac
 }
 
 // At least two waves per SIMD (two workgroups per CU; wide tiles four).
-// Slot swizzle of a lane-blocked LDS buffer of NV 16-byte vectors a lane:
-// lane L's vector v sits at L NV + (v ^ ss_swizzle<NV>(L)), so that both the
-// lanes' writes of one vector and the reads of 64 consecutive vectors fall
-// in distinct banks within each group of 16 lanes.
-template <int NV>
-__device__ __forceinline__ int ss_swizzle(int L) {
-  static_assert(NV >= 1 && NV <= 16 && (NV & (NV - 1)) == 0, "a power of two up to 16");
-  constexpr int p = NV >= 16 ? 4 : NV >= 8 ? 3 : NV >= 4 ? 2 : NV >= 2 ? 1 : 0;
-  return (L >> (4 - p)) & (NV - 1);
-}
-
 // Group g0 .. g0+G-1 of a lane's K steps (items of type X, whole 16-byte
-// vectors) into the wave's lane-blocked buffer `wb`, in ascending time (a
-// reversed pass walks its chunk downwards).
+// vectors) into the wave's lane-blocked buffer `wb` (lds_flush's layout), in
+// ascending time (a reversed pass walks its chunk downwards).
 template <int NV, bool REV, int K, typename X, int G>
 __device__ __forceinline__ void ss_lds_put(uint4 *wb, int lane, int g0, const X (&items)[G]) {
   constexpr int NG = int(G * sizeof(X) / 16);
@@ -770,26 +759,11 @@ __device__ __forceinline__ void ss_lds_put(uint4 *wb, int lane, int g0, const X 
 #pragma unroll
   for (int i = 0; i < G; ++i) t.x[i] = items[REV ? G - 1 - i : i];
   const int v0 = int((REV ? K - g0 - G : g0) * sizeof(X) / 16);
-  const int sw = ss_swizzle<NV>(lane);
+  const int sw = lds_swizzle<NV>(lane);
 #pragma unroll
   for (int i = 0; i < NG; ++i) wb[lane * NV + ((v0 + i) ^ sw)] = t.u[i];
 }
 
-// The wave's buffer to the round's block at dst (16-byte aligned, in range):
-// vector c of the block is lane c / NV's vector c % NV, so each store
-// instruction writes 64 consecutive vectors.
-template <int NV>
-__device__ __forceinline__ void ss_lds_flush(uint4 *dst, const uint4 *wb, int lane, bool write) {
-  wave_sync();
-  if (write) {
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int c = j * 64 + lane, L = c / NV, v = c % NV;
-      dst[c] = wb[L * NV + (v ^ ss_swizzle<NV>(L))];
-    }
-  }
-  wave_sync();  // the next round's writes follow these reads
-}
 
 // A workgroup barrier with no wait for outstanding memory operations, whose
 // memory accesses stay on their side of it: memory operations issued before
@@ -1080,10 +1054,10 @@ __global__ __launch_bounds__((SsShape<Alg, MODE>::kThreads), (SsShape<Alg, MODE>
       const int64_t p0 = seg0 + int64_t(r) * 64 * K;  // first scan position of the round
       const int64_t tb = REV ? T - p0 - 64 * K : p0;
       if constexpr (kFull && kHLds)
-        ss_lds_flush<kNVh>(reinterpret_cast<uint4 *>(reinterpret_cast<SS *>(a.hs) + b * T + tb),
+        lds_flush<kNVh>(reinterpret_cast<uint4 *>(reinterpret_cast<SS *>(a.hs) + b * T + tb),
                            s_ht + w * 64 * kNVh, lane, true);
       if constexpr (kFull && kYLds)
-        ss_lds_flush<kNVy>(reinterpret_cast<uint4 *>(a.y + b * T + tb), s_yt + w * 64 * kNVy, lane, want_y);
+        lds_flush<kNVy>(reinterpret_cast<uint4 *>(a.y + b * T + tb), s_yt + w * 64 * kNVy, lane, want_y);
     }
     if constexpr (MODE == kSsGrad) {
       // the wave's sums, in a fixed order, one partial per (row, tile, wave)
