@@ -203,7 +203,16 @@ int sos_bwd(int64_t B, int64_t T, int S, const SosCoefs &k, const void *x, const
     if (step > 0 && laneh + sos_kept_slots(S, step) * slot > limit) step = (S + 1) / 2;
     if (step > 0 && laneh + sos_kept_slots(S, step) * slot > limit) step = 0;
     a.kept_step = step;
-    const size_t lds = laneh + sos_kept_slots(S, step) * slot;
+    size_t lds = laneh + sos_kept_slots(S, step) * slot;
+    // kept slot 0 also takes the output's LDS transpose at the end; without
+    // kept inputs, one slot is added for it where the LDS allows
+    a.out_lds = 0;
+    if (sos_kept_slots(S, step) >= 1) {
+      a.out_lds = 1;
+    } else if (laneh + slot <= limit) {
+      lds = laneh + slot;
+      a.out_lds = 1;
+    }
     launch_kernel(kernel, dim3(grid), dim3(Sh::kThreads), lds, stream, a);
     if (hipGetLastError() != hipSuccess) return PHS_ERR_LAUNCH;
     const int64_t rows = k.coef_shared() ? 1 : B;

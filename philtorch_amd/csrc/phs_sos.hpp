@@ -104,6 +104,7 @@ struct SosArgs {
   uint64_t *status;            // [B, S, tiles, kStride] status words of this call
   int vec_ok;
   int kept_step;               // gradient backward: sections whose input stays in LDS (0: none)
+  int out_lds;                 // gradient backward: kept slot 0 holds the output's LDS transpose
 };
 
 // One section, in the form the steps use.
@@ -782,6 +783,13 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
   extern __shared__ __align__(16) unsigned char sos_dyn[];
   SV *s_laneh = reinterpret_cast<SV *>(sos_dyn);
   E *s_uin = reinterpret_cast<E *>(sos_dyn + size_t(a.S) * W * R * 64 * sizeof(SV));
+  // Whole rounds of the output leave through a lane-blocked LDS buffer of
+  // the wave as 1 KB rows (lds_flush): static for the forward and the plain
+  // backward; the gradient backward reuses the wave's part of kept slot 0
+  // (a.out_lds), whose inputs are dead by then
+  constexpr bool kOutLds = kLdsBlocked<E, K>;
+  constexpr int kNVo = kOutLds ? int(K * sizeof(E) / 16) : 1;
+  __shared__ uint4 s_out[(kOutLds && !GRAD) ? W * 64 * kNVo : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1018,8 +1026,25 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
   }
 
   if (a.out) {
+    uint4 *wb = nullptr;
+    if constexpr (kOutLds) {
+      if constexpr (GRAD)
+        wb = a.out_lds ? reinterpret_cast<uint4 *>(s_uin + size_t(w) * R * K * 64) : nullptr;
+      else
+        wb = s_out + w * 64 * kNVo;
+    }
 #pragma unroll
-    for (int r = 0; r < R; ++r) store_chunk<E, K>(a.out + b * T, chunk0(r), T, vec, U[r]);
+    for (int r = 0; r < R; ++r) {
+      const int64_t blk0 = chunk0(r) - int64_t(pl) * K;  // the round's block, lowest time first
+      if (kOutLds && wb != nullptr && vec && blk0 + 64 * K <= T) {
+        if constexpr (kOutLds) {
+          lds_put_chunk<E, K>(wb, pl, U[r]);
+          lds_flush<kNVo>(reinterpret_cast<uint4 *>(a.out + b * T + blk0), wb, lane, true);
+        }
+      } else {
+        store_chunk<E, K>(a.out + b * T, chunk0(r), T, vec, U[r]);
+      }
+    }
   }
 }
 
