@@ -293,6 +293,21 @@ int phs_biquad_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64
                    void *grad_x, void *grad_b, void *grad_a, void *grad_zi, void *workspace, size_t workspace_bytes,
                    void *stream);
 
+/* phs_biquad_bwd for a biquad whose b and a are columns of coefficient
+ * tables (the C4 caller pattern's b[:, s] of a [B, S, 3] table): the
+ * gradient reduction writes the whole tables, grad_b_table [B|1, b_cols, nb]
+ * with dL/db at column b_col and zeros in the other columns, grad_a_table
+ * [B|1, a_cols, 2] likewise (contiguous; b_cols = a_cols = 1 and column 0
+ * are phs_biquad_bwd's grad_b and grad_a).  No counterpart in the
+ * reference: it replaces autograd's zero-filled table and column copy per
+ * call of the caller pattern over philtorch/lti/filtering.py:211-333
+ * (torch's select backward). */
+int phs_biquad_bwd_cols(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_t b_row_stride, const void *a,
+                        int64_t a_row_stride, const void *x, const void *ckpt, const void *grad_y,
+                        const void *grad_zf, void *grad_x, void *grad_b_table, int b_cols, int b_col,
+                        void *grad_a_table, int a_cols, int a_col, void *grad_zi, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
 /* ---- Zero-phase filtering with a filter of order 1..4 per row (its
  * gradients: phs_filtfilt_bwd below).  Replaces philtorch.lti.
  * filtering.filtfilt (philtorch/lti/filtering.py:413-484, with lfilter_zi

@@ -384,6 +384,66 @@ if EXTENSION_LOADED and _has_op("biquad"):
 
     torch.library.register_autograd("philtorch::biquad", _biquad_backward, setup_context=_biquad_setup)
 
+if EXTENSION_LOADED and _has_op("biquad_cols"):
+    # biquad with b and a as columns of coefficient tables (col -1: b or a
+    # itself): the backward writes the tables' gradients whole, the column's
+    # in place and zeros elsewhere
+    def _table_col(t, col):
+        return t if col < 0 else t.select(-2, col)
+
+    @torch.library.register_fake("philtorch::biquad_cols")
+    def _(bt, b_col, at, a_col, zi, x):
+        b, a = _table_col(bt, b_col), _table_col(at, a_col)
+        torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
+        torch._check(b.ndim == a.ndim and b.ndim in (1, 2), lambda: "b and a must both be 1D or both 2D")
+        torch._check(1 <= b.shape[-1] <= 3 and a.shape[-1] == 2, lambda: "a biquad")
+        B, T = x.shape
+        return _fake_like(x), x.new_empty((B, 2)), x.new_empty((B, 1, _n_ckpt(x, T), 2), dtype=torch.float64)
+
+    @torch.library.register_fake("philtorch::biquad_cols_backward")
+    def _(bt, b_col, at, a_col, x, ckpt, grad_y, grad_zf, need_coef):
+        return [_fake_like(x), bt.new_empty(bt.shape), at.new_empty(at.shape), x.new_empty((x.shape[0], 2))]
+
+    def _biquad_cols_setup(ctx, inputs, output):
+        bt, b_col, at, a_col, zi, x = inputs
+        ctx.save_for_backward(bt, at, x, output[2], zi)
+        ctx.cols = (b_col, a_col)
+        ctx.has_zi = zi is not None
+        ctx.set_materialize_grads(False)
+
+    def _biquad_cols_backward(ctx, gy, gzf, _gckpt):
+        """philtorch::biquad_cols_backward: biquad_backward whose coefficient
+        gradients are the tables' (the caller's b[:, s] costs autograd no
+        zero-filled table and column copy).  Under create_graph: the
+        section's composite gradient scattered into the table's column."""
+        bt, at, x, ckpt, zi = ctx.saved_tensors
+        b_col, a_col = ctx.cols
+        needs = ctx.needs_input_grad  # bt, b_col, at, a_col, zi, x
+        if gy is None:
+            gy = torch.zeros_like(x)
+        if torch.is_grad_enabled():
+            b, a = _table_col(bt, b_col), _table_col(at, a_col)
+            sos = torch.cat([torch.nn.functional.pad(b, (0, 3 - b.size(-1))), torch.ones_like(a[..., :1]), a],
+                            dim=-1).unsqueeze(-2)
+            zs = None if zi is None else zi.unsqueeze(1)
+            gsos, gz, gx = _sosfilt_composite(sos, zs, x, gy, None if gzf is None else gzf.unsqueeze(1),
+                                              (needs[0] or needs[2], needs[4], needs[5]))
+            gbt = gat = None
+            if gsos is not None:
+                gb, ga = gsos[..., 0, : b.size(-1)], gsos[..., 0, 4:6]
+                gbt = gb if b_col < 0 else torch.select_scatter(torch.zeros_like(bt), gb, -2, b_col)
+                gat = ga if a_col < 0 else torch.select_scatter(torch.zeros_like(at), ga, -2, a_col)
+            return (gbt if needs[0] else None, None, gat if needs[2] else None, None,
+                    gz[:, 0] if (gz is not None and ctx.has_zi and needs[4]) else None, gx if needs[5] else None)
+        need_coef = bool(needs[0] or needs[2])
+        gx, gbt, gat, gzi = torch.ops.philtorch.biquad_cols_backward(bt, b_col, at, a_col, x, ckpt, gy, gzf,
+                                                                     need_coef)
+        return (gbt if needs[0] else None, None, gat if needs[2] else None, None,
+                gzi if ctx.has_zi and needs[4] else None, gx if needs[5] else None)
+
+    torch.library.register_autograd("philtorch::biquad_cols", _biquad_cols_backward,
+                                    setup_context=_biquad_cols_setup)
+
 if EXTENSION_LOADED and _has_op("filtfilt"):
     # zero-phase filter of order 4 at most (lti.filtfilt's fused route); its
     # gradients are philtorch::filtfilt_backward

@@ -168,7 +168,7 @@ int sos_fwd(int64_t B, int64_t T, int S, const SosCoefs &k, const void *zi, cons
 template <typename E>
 int sos_bwd(int64_t B, int64_t T, int S, const SosCoefs &k, const void *x, const void *ckpt, const void *gy,
             const void *gzf, void *gx, void *gsos, void *gb, void *ga, void *gzi, void *workspace, size_t ws_bytes,
-            hipStream_t stream) {
+            hipStream_t stream, int b_cols = 1, int b_col = 0, int a_cols = 1, int a_col = 0) {
   using Sh = SosBwd<E>;
   if (!sizes_ok(B, T, S) || (k.b && S != 1)) return PHS_ERR_INVALID;
   if (B == 0 || T == 0) return PHS_OK;
@@ -217,7 +217,8 @@ int sos_bwd(int64_t B, int64_t T, int S, const SosCoefs &k, const void *x, const
     if (hipGetLastError() != hipSuccess) return PHS_ERR_LAUNCH;
     const int64_t rows = k.coef_shared() ? 1 : B;
     hipLaunchKernelGGL((sos_grad_reduce_kernel<E, Sh>), dim3(unsigned(rows * S)), dim3(kSosReduceThreads), 0,
-                       stream, a, static_cast<E *>(gsos), rows, static_cast<E *>(gb), static_cast<E *>(ga));
+                       stream, a, static_cast<E *>(gsos), rows, static_cast<E *>(gb), static_cast<E *>(ga), b_cols,
+                       b_col, a_cols, a_col);
   } else {
     launch_kernel((sos_kernel<E, Sh, true, false>), dim3(grid), dim3(Sh::kThreads), 0, stream, a);
   }
@@ -298,6 +299,27 @@ int phs_biquad_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64
   return phs::biquad_fwd_ss(dtype, B, T, b, nb, b_row_stride, a, a_row_stride, zi, x, y, zf, ckpt,
                             phs::n_ckpt_of(dtype, T), phs::ckpt_every_of(dtype), workspace, workspace_bytes,
                             static_cast<hipStream_t>(stream));
+}
+
+int phs_biquad_bwd_cols(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_t b_row_stride, const void *a,
+                        int64_t a_row_stride, const void *x, const void *ckpt, const void *grad_y,
+                        const void *grad_zf, void *grad_x, void *grad_b_table, int b_cols, int b_col,
+                        void *grad_a_table, int a_cols, int a_col, void *grad_zi, void *workspace,
+                        size_t workspace_bytes, void *stream) {
+  if (b_cols < 1 || b_col < 0 || b_col >= b_cols || a_cols < 1 || a_col < 0 || a_col >= a_cols)
+    return PHS_ERR_INVALID;
+  if ((grad_b_table == nullptr) != (grad_a_table == nullptr)) return PHS_ERR_INVALID;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const phs::SosCoefs k = biquad_coefs(b, nb, b_row_stride, a, a_row_stride);
+  switch (dtype) {
+    case PHS_F32:
+      return phs::sos_bwd<float>(B, T, 1, k, x, ckpt, grad_y, grad_zf, grad_x, nullptr, grad_b_table, grad_a_table,
+                                 grad_zi, workspace, workspace_bytes, st, b_cols, b_col, a_cols, a_col);
+    case PHS_F64:
+      return phs::sos_bwd<double>(B, T, 1, k, x, ckpt, grad_y, grad_zf, grad_x, nullptr, grad_b_table, grad_a_table,
+                                  grad_zi, workspace, workspace_bytes, st, b_cols, b_col, a_cols, a_col);
+    default: return PHS_ERR_DTYPE;
+  }
 }
 
 int phs_biquad_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, int64_t b_row_stride, const void *a,

@@ -1054,15 +1054,21 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
 // order and applies the chain rule to (b0, b1, b2, a0, a1, a2):
 //   d c0/d b1 = 1, d c0/d b0 = -a1, d c0/d a1 = -b0, d A00/d a1 = -1 (same
 //   pattern for c1, a2), d y/d b0 = u; a0 is not a free parameter (zero).
-// gsos: [coef_rows, S, 6]; for a biquad given as b and a (a.fb), gb
-// [coef_rows, nb] and ga [coef_rows, 2] instead (gsos unused).
+// gsos: [coef_rows, S, 6]; for a biquad given as b and a (a.fb), the
+// gradients of whole coefficient tables instead (gsos unused): gb
+// [coef_rows, b_cols, nb] with the biquad's b at column b_col and zeros in
+// the others, ga [coef_rows, a_cols, 2] likewise (b_cols = a_cols = 1,
+// column 0: plain [coef_rows, nb] and [coef_rows, 2]).
 constexpr int kSosReduceThreads = 256;
 
 template <typename E, class Sh>
 __global__ __launch_bounds__(kSosReduceThreads) void sos_grad_reduce_kernel(const SosArgs<E> a, E *gsos,
-                                                                         int64_t coef_rows, E *gb, E *ga) {
+                                                                         int64_t coef_rows, E *gb, E *ga,
+                                                                         int b_cols, int b_col, int a_cols,
+                                                                         int a_col) {
   using C = typename Wide<E>::type;
   __shared__ C s_sum[5][kSosReduceThreads];
+  __shared__ C s_g[6];
   const int64_t row = blockIdx.x / a.S;
   const int s = int(blockIdx.x - row * a.S);
   const int64_t per_b = a.tiles_per_row * Sh::kWaves;
@@ -1089,13 +1095,27 @@ __global__ __launch_bounds__(kSosReduceThreads) void sos_grad_reduce_kernel(cons
     const C Sa1 = s_sum[0][0], Sa2 = s_sum[1][0], Sc0 = s_sum[2][0], Sc1 = s_sum[3][0], Sb0 = s_sum[4][0];
     const C g[6] = {Sb0 - a1 * Sc0 - a2 * Sc1, Sc0, Sc1, C(0), -Sa1 - b0 * Sc0, -Sa2 - b0 * Sc1};
     if (a.fb) {
-      for (int j = 0; j < a.nb; ++j) gb[row * a.nb + j] = down<E>(g[j]);
-      ga[row * 2] = down<E>(g[4]);
-      ga[row * 2 + 1] = down<E>(g[5]);
+#pragma unroll
+      for (int j = 0; j < 6; ++j) s_g[j] = g[j];
     } else {
       E *o = gsos + row * int64_t(a.S) * 6 + 6 * s;
 #pragma unroll
       for (int j = 0; j < 6; ++j) o[j] = down<E>(g[j]);
+    }
+  }
+  if (a.fb) {
+    // the row's tables: the biquad's column, zeros elsewhere
+    __syncthreads();
+    const int nb = a.nb;
+    E *gbr = gb + row * int64_t(b_cols) * nb;
+    for (int i = threadIdx.x; i < b_cols * nb; i += kSosReduceThreads) {
+      const int col = i / nb;
+      gbr[i] = col == b_col ? down<E>(s_g[i - col * nb]) : E(0);
+    }
+    E *gar = ga + row * int64_t(a_cols) * 2;
+    for (int i = threadIdx.x; i < a_cols * 2; i += kSosReduceThreads) {
+      const int col = i >> 1;
+      gar[i] = col == a_col ? down<E>(s_g[4 + (i & 1)]) : E(0);
     }
   }
 }

@@ -534,12 +534,25 @@ Triple biquad_hip(const Tensor &b, const Tensor &a, const std::optional<Tensor> 
   return {y, zf, ckpt};
 }
 
-// Gradients of biquad (phs_biquad_bwd): (grad_x, grad_b, grad_a, grad_zi);
-// grad_b, grad_a shaped like b and a (zero unless need_coef); grad_zf None is
+// Column `col` of a coefficient table along its second-to-last dimension
+// (b [B, C, nb] or [C, nb]: the C4 caller's b[:, s]); col -1: t itself.
+Tensor table_column(const Tensor &t, int64_t col, const char *op) {
+  if (col < 0) return t;
+  TORCH_CHECK(t.dim() >= 2 && col < t.size(-2), "philtorch::", op, ": column ", col, " of a table of ",
+              t.dim() >= 2 ? t.size(-2) : 0, " columns");
+  return t.select(-2, col);
+}
+
+// Gradients of biquad (phs_biquad_bwd_cols): (grad_x, grad_bt, grad_at,
+// grad_zi) for b = bt's column b_col (bt itself for -1) and a likewise;
+// grad_bt, grad_at shaped like bt and at, the biquad's gradient in its
+// column and zeros elsewhere (all zero unless need_coef); grad_zf None is
 // zero.
-std::vector<Tensor> biquad_backward_hip(const Tensor &b, const Tensor &a, const Tensor &x, const Tensor &ckpt,
-                                        const Tensor &gy, const std::optional<Tensor> &gzf, bool need_coef) {
-  check_biquad("biquad_backward", b, a, x);
+std::vector<Tensor> biquad_backward_impl(const char *op, const Tensor &bt, int64_t b_col, const Tensor &at_,
+                                         int64_t a_col, const Tensor &x, const Tensor &ckpt, const Tensor &gy,
+                                         const std::optional<Tensor> &gzf, bool need_coef) {
+  const Tensor b = table_column(bt, b_col, op), a = table_column(at_, a_col, op);
+  check_biquad(op, b, a, x);
   const int64_t B = x.size(0), T = x.size(1);
   TORCH_CHECK(gy.sizes() == x.sizes() && gy.device() == x.device(),
               "philtorch::biquad_backward: grad_y must have x's shape and device");
@@ -557,8 +570,8 @@ std::vector<Tensor> biquad_backward_hip(const Tensor &b, const Tensor &a, const 
   Tensor gc = gy.to(x.scalar_type()).contiguous(), cc = ckpt.contiguous();
   Tensor gzc = gzf ? gzf->to(x.scalar_type()).contiguous() : Tensor();
   Tensor gx = at::empty_like(xc, at::MemoryFormat::Contiguous);
-  Tensor gb = need_coef ? at::empty(b.sizes(), b.options()) : at::zeros(b.sizes(), b.options());
-  Tensor ga = need_coef ? at::empty(a.sizes(), a.options()) : at::zeros(a.sizes(), a.options());
+  Tensor gb = need_coef ? at::empty(bt.sizes(), bt.options()) : at::zeros(bt.sizes(), bt.options());
+  Tensor ga = need_coef ? at::empty(at_.sizes(), at_.options()) : at::zeros(at_.sizes(), at_.options());
   Tensor gzi = at::empty({B, 2}, x.options());
   if (B == 0 || T == 0) {
     if (need_coef) gb.zero_(), ga.zero_();
@@ -567,13 +580,35 @@ std::vector<Tensor> biquad_backward_hip(const Tensor &b, const Tensor &a, const 
   }
   void *stream = stream_of(x);
   const Workspace ws = workspace_for(x, phs_sosfilt_workspace_size(dt, B, T, 1, 1), stream);
-  check_status(phs_biquad_bwd(dt, B, T, bu.const_data_ptr(), int(b.size(-1)), bs, au.const_data_ptr(), as,
-                              need_coef ? xc.const_data_ptr() : nullptr, need_coef ? cc.const_data_ptr() : nullptr,
-                              gc.const_data_ptr(), gzf ? gzc.const_data_ptr() : nullptr, gx.mutable_data_ptr(),
-                              need_coef ? gb.mutable_data_ptr() : nullptr, need_coef ? ga.mutable_data_ptr() : nullptr,
-                              gzi.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
-               "biquad_backward");
+  const int b_cols = b_col >= 0 ? int(bt.size(-2)) : 1, a_cols = a_col >= 0 ? int(at_.size(-2)) : 1;
+  check_status(phs_biquad_bwd_cols(dt, B, T, bu.const_data_ptr(), int(b.size(-1)), bs, au.const_data_ptr(), as,
+                                   need_coef ? xc.const_data_ptr() : nullptr,
+                                   need_coef ? cc.const_data_ptr() : nullptr, gc.const_data_ptr(),
+                                   gzf ? gzc.const_data_ptr() : nullptr, gx.mutable_data_ptr(),
+                                   need_coef ? gb.mutable_data_ptr() : nullptr, b_cols, int(b_col < 0 ? 0 : b_col),
+                                   need_coef ? ga.mutable_data_ptr() : nullptr, a_cols, int(a_col < 0 ? 0 : a_col),
+                                   gzi.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+               op);
   return {gx, gb, ga, gzi};
+}
+
+std::vector<Tensor> biquad_backward_hip(const Tensor &b, const Tensor &a, const Tensor &x, const Tensor &ckpt,
+                                        const Tensor &gy, const std::optional<Tensor> &gzf, bool need_coef) {
+  return biquad_backward_impl("biquad_backward", b, -1, a, -1, x, ckpt, gy, gzf, need_coef);
+}
+
+// biquad with b and a given as columns of coefficient tables (col -1: the
+// coefficients themselves), so that autograd's gradient of a table needs no
+// zero-filled copy and column write per call: (y, zf, ckpt)
+Triple biquad_cols_hip(const Tensor &bt, int64_t b_col, const Tensor &at_, int64_t a_col,
+                       const std::optional<Tensor> &zi, const Tensor &x) {
+  return biquad_hip(table_column(bt, b_col, "biquad_cols"), table_column(at_, a_col, "biquad_cols"), zi, x);
+}
+
+std::vector<Tensor> biquad_cols_backward_hip(const Tensor &bt, int64_t b_col, const Tensor &at_, int64_t a_col,
+                                             const Tensor &x, const Tensor &ckpt, const Tensor &gy,
+                                             const std::optional<Tensor> &gzf, bool need_coef) {
+  return biquad_backward_impl("biquad_cols_backward", bt, b_col, at_, a_col, x, ckpt, gy, gzf, need_coef);
 }
 
 // Zero-phase filter of order 4 at most (phs_filtfilt_fwd;
@@ -1177,6 +1212,13 @@ TORCH_LIBRARY(philtorch, m) {
   m.def("biquad_backward(Tensor b, Tensor a, Tensor x, Tensor ckpt, Tensor grad_y, Tensor? grad_zf, bool need_coef)"
         " -> Tensor[]",
         {at::Tag::pt2_compliant_tag});
+  // new: the same with b and a as columns of coefficient tables (col -1: b or a itself);
+  // the backward's coefficient gradients are the whole tables'
+  m.def("biquad_cols(Tensor bt, int b_col, Tensor at, int a_col, Tensor? zi, Tensor x) -> (Tensor, Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
+  m.def("biquad_cols_backward(Tensor bt, int b_col, Tensor at, int a_col, Tensor x, Tensor ckpt, Tensor grad_y, "
+        "Tensor? grad_zf, bool need_coef) -> Tensor[]",
+        {at::Tag::pt2_compliant_tag});
   // new: zero-phase filtering, filters of second order at most (forward only)
   m.def("filtfilt(Tensor b, Tensor a, Tensor x, int padmode, int padlen) -> Tensor", {at::Tag::pt2_compliant_tag});
   m.def("filtfilt_backward(Tensor b, Tensor a, Tensor x, Tensor grad_y, int padmode, int padlen, bool need_coef) "
@@ -1220,6 +1262,8 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("filtfilt_backward", &filtfilt_backward_hip);
   m.impl("biquad", &biquad_hip);
   m.impl("biquad_backward", &biquad_backward_hip);
+  m.impl("biquad_cols", &biquad_cols_hip);
+  m.impl("biquad_cols_backward", &biquad_cols_backward_hip);
   m.impl("lti_ss", &lti_ss_hip);
   m.impl("lfilter_ss", &lfilter_ss_hip);
   m.impl("lti_ss_backward", &lti_ss_backward_hip);

@@ -111,8 +111,44 @@ def _fused_biquad(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor]):
                                                                                           "lfilter_ss"):
         return _fused_lfilter(b, a, x, zi, "tdf2")
     zb = None if zi is None else zi.expand(x.size(0), 2).contiguous()
-    y, zf, _ = torch.ops.philtorch.biquad(b, a, zb, x)
+    bt, b_col = _table_column(b)
+    at, a_col = _table_column(a)
+    if (b_col >= 0 or a_col >= 0) and hasattr(torch.ops.philtorch, "biquad_cols"):
+        # b or a is a column of a coefficient table (the caller's b[:, s]):
+        # the table takes its gradient directly
+        y, zf, _ = torch.ops.philtorch.biquad_cols(bt, b_col, at, a_col, zb, x)
+    else:
+        y, zf, _ = torch.ops.philtorch.biquad(b, a, zb, x)
     return y if zi is None else (y, zf)
+
+
+def _table_column(t: Tensor) -> tuple[Tensor, int]:
+    """``(table, s)`` when ``t`` is ``table.select(-2, s)`` of the tensor its
+    view chain starts from (the C4 caller's ``b[:, s]`` of a ``(B, S, 3)``
+    coefficient table), judged by memory placement; else ``(t, -1)``.
+
+    A column routed this way hands its gradient to the table directly:
+    autograd then allocates no zero-filled table and writes no column per
+    call (torch's select backward), but the gradient of the column view
+    object itself is no longer recorded (``autograd.grad(y, column)`` with
+    that very view, its ``retain_grad`` or its hooks).  Views that retain
+    their gradient or carry hooks keep the plain route."""
+    base = getattr(t, "_base", None)
+    if base is None or t.grad_fn is None or not base.requires_grad or t.retains_grad:
+        return t, -1
+    if getattr(t, "_backward_hooks", None):
+        return t, -1
+    if base.dim() != t.dim() + 1 or t.dim() not in (1, 2) or base.dtype != t.dtype:
+        return t, -1
+    if tuple(t.shape) != tuple(base.shape[:-2]) + tuple(base.shape[-1:]):
+        return t, -1
+    if tuple(t.stride()) != tuple(base.stride()[:-2]) + tuple(base.stride()[-1:]):
+        return t, -1
+    step = base.stride(-2)
+    off = t.storage_offset() - base.storage_offset()
+    if step <= 0 or off < 0 or off % step != 0 or off // step >= base.size(-2):
+        return t, -1
+    return base, off // step
 
 
 def _fused_lfilter_applies(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor], form: str, kwargs) -> bool:

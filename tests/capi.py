@@ -95,6 +95,10 @@ def load() -> ctypes.CDLL:
     lib.phs_biquad_bwd.argtypes = [ctypes.c_int, i64, i64, vp, ctypes.c_int, i64, vp, i64, vp, vp, vp, vp, vp, vp,
                                    vp, vp, vp, ctypes.c_size_t, vp]
     lib.phs_biquad_bwd.restype = ctypes.c_int
+    ci = ctypes.c_int
+    lib.phs_biquad_bwd_cols.argtypes = [ci, i64, i64, vp, ci, i64, vp, i64, vp, vp, vp, vp, vp, vp, ci, ci, vp, ci,
+                                        ci, vp, vp, ctypes.c_size_t, vp]
+    lib.phs_biquad_bwd_cols.restype = ctypes.c_int
     # zero-phase biquad filter
     lib.phs_filtfilt_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
     lib.phs_filtfilt_workspace_size.restype = ctypes.c_size_t

@@ -419,6 +419,26 @@ def test_biquad_capi_reads_b_and_a_in_place(api, dtype, layout, nb):
     rgs = rgs.reshape(rows, 6)
     D.check(gb.cpu().numpy(), rgs[:, 0:nb], "grad_b", dtype=dtype)
     D.check(ga.cpu().numpy(), rgs[:, 4:6], "grad_a", dtype=dtype)
+    # phs_biquad_bwd_cols: the same gradients written as whole tables, the
+    # biquad's column in place (bit-identical: the same reduction) and zeros
+    # in every other column
+    gbt = torch.full((rows, 5, nb), float("nan"), dtype=tx.dtype, device="cuda")
+    gat = torch.full((rows, 2, 2), float("nan"), dtype=tx.dtype, device="cuda")
+    gx2, gzi2 = torch.empty_like(tx), torch.empty((B, 2), dtype=tx.dtype, device="cuda")
+    print(f"biquad capi cols {np.dtype(dtype).name} layout={layout} nb={nb}", flush=True)
+    rc = lib.phs_biquad_bwd_cols(dt, B, T, _p(tb), nb, bs, _p(ta), as_, _p(tx), _p(ck), _p(tg), _p(tgz), _p(gx2),
+                                 _p(gbt), 5, 3, _p(gat), 2, 1, _p(gzi2), _p(ws), need, _stream())
+    assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+    torch.cuda.synchronize()
+    assert torch.equal(gbt[:, 3], gb) and torch.equal(gat[:, 1], ga)
+    assert torch.equal(gx2, gx) and torch.equal(gzi2, gzi)
+    others = torch.cat([gbt[:, [0, 1, 2, 4]].flatten(), gat[:, 0].flatten()])
+    assert torch.equal(others, torch.zeros_like(others))
+    for bc, bcol, ac, acol in ((5, 5, 2, 1), (5, -1, 2, 1), (0, 0, 2, 1), (5, 3, 2, 2)):
+        rc = lib.phs_biquad_bwd_cols(dt, B, T, _p(tb), nb, bs, _p(ta), as_, _p(tx), _p(ck), _p(tg), _p(tgz),
+                                     _p(gx2), _p(gbt), bc, bcol, _p(gat), ac, acol, _p(gzi2), _p(ws), need,
+                                     _stream())
+        assert rc == capi.PHS_ERR_INVALID
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
@@ -461,6 +481,82 @@ def test_biquad_forward_checkpoints_match_cascade_kernel(api, dtype):
     D.check(ck1, ck2, "ckpt", dtype=dtype)
     D.check(y1, y2, "y", dtype=dtype)
     D.check(zf1, zf2, "zf", dtype=dtype)
+
+
+def test_lfilter_columns_hand_gradients_to_tables(hip):
+    """The C4 caller pattern's b[:, s] / a[:, s] of coefficient tables
+    take philtorch::biquad_cols, whose backward writes the tables' gradients
+    whole: the gradients w.r.t. x and the tables are bit-identical to the
+    plain route's (the same columns passed as fresh tensors), also for 1-D
+    shared tables and for a table of b beside a plain a; views that retain
+    their gradient keep the plain route."""
+    import torch
+
+    from philtorch_amd import lti
+    from philtorch_amd.lti import filtering
+
+    g = D.rng(D.seed_of("biquad-cols-route"))
+    B, T, S = 3, 7001, 4
+    for shared in (False, True):
+        lead = (S,) if shared else (B, S)
+        sos = D.sos_coefs(g, lead, 1, np.float64)[..., 0, :]
+        x0 = torch.tensor(g.standard_normal((B, T)), device="cuda")
+        gy = torch.tensor(g.standard_normal((B, T)), device="cuda")
+        grads = {}
+        for route in ("cols", "plain", "mixed"):
+            print(f"biquad cols route={route} shared={shared}", flush=True)
+            bt = torch.tensor(sos[..., 0:3], device="cuda").requires_grad_(True)
+            at = torch.tensor(sos[..., 4:6], device="cuda").requires_grad_(True)
+            x = x0.clone().requires_grad_(True)
+            y = x
+            for s in range(S):
+                bs, as_ = bt[..., s, :], at[..., s, :]
+                if route == "cols":
+                    assert filtering._table_column(bs)[1] == s and filtering._table_column(as_)[1] == s
+                if route in ("plain", "mixed"):
+                    as_ = as_ * 1.0  # not a view: the plain route for a
+                if route == "plain":
+                    bs = bs * 1.0
+                y = lti.lfilter(bs, as_, y, form="tdf2", unroll_factor=1)
+            grads[route] = torch.autograd.grad(y, (x, bt, at), gy)
+        for route in ("plain", "mixed"):
+            for got, ref in zip(grads[route], grads["cols"]):
+                assert torch.equal(got, ref), route
+        # against the oracle's cascade (every section a column of the tables)
+        full = np.broadcast_to(sos, (B, S, 6)) if shared else sos
+        rgs, _, rgx = oracle.sosfilt_bwd(*_exact(full, x0.cpu().numpy(), None, gy.cpu().numpy(), None))
+        gsum = rgs.sum(0) if shared else rgs
+        D.check(grads["cols"][0].cpu().numpy(), rgx, "grad_x", dtype=np.float64)
+        D.check(grads["cols"][1].cpu().numpy(), gsum[..., 0:3], "grad_b table", dtype=np.float64)
+        D.check(grads["cols"][2].cpu().numpy(), gsum[..., 4:6], "grad_a table", dtype=np.float64)
+    bt = torch.zeros((B, S, 3), device="cuda", requires_grad=True)
+    v = bt[:, 1]
+    v.retain_grad()
+    assert filtering._table_column(v)[1] == -1
+
+
+def test_biquad_cols_op_gradients_and_opcheck(hip):
+    """philtorch::biquad_cols: gradcheck of the fused table gradients,
+    gradgradcheck of the composite, opcheck."""
+    import torch
+
+    g = D.rng(D.seed_of("biquad-cols-op"))
+    B, T = 2, 40
+    tab_b = torch.tensor(g.standard_normal((B, 4, 3)), device="cuda", requires_grad=True)
+    tab_a = torch.tensor(D.sos_coefs(g, (B, 4), 1, np.float64)[..., 0, 4:6], device="cuda").requires_grad_(True)
+    a_row = torch.tensor(D.sos_coefs(g, (B,), 1, np.float64)[..., 0, 4:6], device="cuda").requires_grad_(True)
+    x = torch.tensor(g.standard_normal((B, T)), device="cuda", requires_grad=True)
+    zi = torch.tensor(g.standard_normal((B, 2)), device="cuda", requires_grad=True)
+    f = lambda tb_, ta_, z_, x_: torch.ops.philtorch.biquad_cols(tb_, 2, ta_, 1, z_, x_)[:2]  # noqa: E731
+    assert torch.autograd.gradcheck(f, (tab_b, tab_a, zi, x))
+    assert torch.autograd.gradgradcheck(f, (tab_b, tab_a, zi, x))
+    f2 = lambda tb_, a_, x_: torch.ops.philtorch.biquad_cols(tb_, 0, a_, -1, None, x_)[0]  # noqa: E731
+    assert torch.autograd.gradcheck(f2, (tab_b, a_row, x))
+    s = lambda v: torch.tensor(np.asarray(v, np.float32), device="cuda")  # noqa: E731
+    torch.library.opcheck(torch.ops.philtorch.biquad_cols.default,
+                          (s(g.standard_normal((3, 3))), 1, s([[-0.5, 0.2]] * 3), 2, None,
+                           s(g.standard_normal((B, 700)))),
+                          test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
 
 
 def test_biquad_op_gradients_and_opcheck(hip):

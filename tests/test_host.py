@@ -360,3 +360,34 @@ def test_capi_state_space_host_only_calls():
     assert lf(nb=6) == capi.PHS_ERR_INVALID and lf(na=5) == capi.PHS_ERR_INVALID and lf(na=0) == capi.PHS_ERR_INVALID
     assert lf(b=None) == capi.PHS_ERR_INVALID
     assert lf(wsb=lib.phs_lti_ss_workspace_size(0, 2, 2, 100) - 1) == capi.PHS_ERR_WORKSPACE
+
+
+def test_table_column_detects_only_exact_columns():
+    """lfilter's column route (philtorch::biquad_cols) takes b[:, s] of a
+    (B, S, 3) table and table[s] of a shared (S, 3) one, by memory
+    placement; copies, slices of wider tables, transposed tables, views
+    that retain their gradient and tables without a gradient keep the plain
+    route."""
+    import torch
+
+    from philtorch_amd.lti.filtering import _table_column
+
+    t3 = torch.randn(4, 8, 3, requires_grad=True)
+    for s in (0, 5, 7):
+        base, col = _table_column(t3[:, s])
+        assert base is t3 and col == s
+    t2 = torch.randn(8, 2, requires_grad=True)
+    base, col = _table_column(t2[3])
+    assert base is t2 and col == 3
+    assert _table_column(t3[:, 2].clone())[1] == -1
+    assert _table_column(t3[:, 2] * 1.0)[1] == -1
+    wide = torch.randn(4, 8, 6, requires_grad=True)
+    assert _table_column(wide[..., 0:3][:, 1])[1] == -1  # a column of a slice of a wider table
+    tt = torch.randn(4, 3, 8, requires_grad=True).transpose(1, 2)  # (4, 8, 3), not the root's layout
+    assert _table_column(tt[:, 1])[1] == -1
+    v = t3[:, 1]
+    v.retain_grad()
+    assert _table_column(v)[1] == -1
+    assert _table_column(torch.randn(4, 8, 3)[:, 1])[1] == -1  # no gradient wanted
+    plain = torch.randn(4, 3, requires_grad=True)
+    assert _table_column(plain) == (plain, -1)
