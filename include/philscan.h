@@ -98,6 +98,17 @@ void phs_debug_set_spin_limit(unsigned polls);
  * Process-wide; takes effect for calls issued afterwards. */
 void phs_debug_set_aggregates_only(int on);
 
+/* Testing hook, no counterpart in the reference.  Forces the cascade
+ * gradient backward's kept_step (phs_sosfilt_bwd and phs_biquad_bwd with
+ * coefficient gradients): the sections whose forward input stays in LDS, so
+ * that re-deriving a section's input runs from the nearest kept one (0: none
+ * kept, every re-derivation runs from x).  step < 0 restores the automatic
+ * choice, which this device's LDS and register counts decide; a forced
+ * value whose kept inputs exceed the LDS left to the kernel makes the call
+ * return PHS_ERR_INVALID.  Results are identical for every value.
+ * Process-wide; takes effect for calls issued afterwards. */
+void phs_debug_set_sos_kept_step(int step);
+
 /* Measurement hook, no counterpart in the reference.  The next main-kernel
  * launch of this library (the scan, cascade, state-space or probe kernel of
  * the next call; not a follow-up reduction) records `start_event` and

@@ -575,6 +575,7 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
             return (None, None, None, None, gzi if zi is not None and needs[4] else None,
                     gx if needs[5] else None, None, None)
         wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
+        create = torch.is_grad_enabled()  # create_graph, read before enable_grad
         with torch.enable_grad():
             if ctx.reverse:
                 y, zf = _state_space_composite(A, B, C, D, zi, x.flip(-1), out_idx=ctx.out_idx)
@@ -585,7 +586,7 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
             if gzf is not None:
                 outs.append(zf)
                 grads.append(gzf)
-            res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=torch.is_grad_enabled(),
+            res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=create,
                                       allow_unused=True)
         out = [None] * 8
         for i, g in zip(wrt, res):
@@ -643,6 +644,7 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
             gx, gzi = torch.ops.philtorch.lfilter_ss(b, a, gzf, g, 1 - ctx.form, not ctx.reverse)
             return (None, None, gzi if zi is not None and needs[2] else None, gx if needs[3] else None, None, None)
         wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
+        create = torch.is_grad_enabled()  # create_graph, read before enable_grad
         with torch.enable_grad():
             z = zi if zi is not None else x.new_zeros(x.size(0), max(b.size(-1) - 1, a.size(-1)))
             xs = x.flip(-1) if ctx.reverse else x
@@ -653,7 +655,7 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
             if gzf is not None:
                 outs.append(zf)
                 grads.append(gzf)
-            res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=torch.is_grad_enabled(),
+            res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=create,
                                       allow_unused=True)
         out = [None] * 6
         for i, g in zip(wrt, res):
@@ -693,17 +695,23 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         a coefficient gradient wanted: philtorch::lpv_ss_backward (the
         forward again keeping its states, then the adjoint pass writing
         lambda[t+1] h[t]^T, lambda[t+1] x[t], g[t] h[t], g[t] x[t] per step,
-        summed over the axes an operand shares).  Under create_graph: the
-        gradient of the composite the fused kernel replaces (B x, the native
-        LPV scan, the state shift, C h + D x; philtorch/lpv/ssm.py:337-581),
-        recomputed from the inputs and differentiable again."""
-        from .lpv.ssm import _lpv_state_space_composite
+        summed over the axes an operand shares).  Under create_graph, or
+        where the fused backward's per-row step gradients of operands the
+        rows share would exceed lpv.ssm._LPV_ROW_SCRATCH_LIMIT: the gradient
+        of the composite the fused kernel replaces (B x, the native LPV
+        scan, the state shift, C h + D x; philtorch/lpv/ssm.py:337-581),
+        recomputed from the inputs (and differentiable again)."""
+        from .lpv import ssm as _lpv_ssm
 
+        _lpv_state_space_composite = _lpv_ssm._lpv_state_space_composite
         inputs = ctx.saved_tensors
         needs = ctx.needs_input_grad
         A, B, C, D, zi, x = inputs
         out = [None] * 9
-        if any(needs[:4]) and not torch.is_grad_enabled() and _has_op("lpv_ss_backward"):
+        # the fused backward, unless its per-row step gradients of shared
+        # operands would exceed _LPV_ROW_SCRATCH_LIMIT (then the composite)
+        fits = _lpv_ssm._lpv_row_scratch_bytes(A, B, C, D, x, needs[:4]) <= _lpv_ssm._LPV_ROW_SCRATCH_LIMIT
+        if any(needs[:4]) and not torch.is_grad_enabled() and _has_op("lpv_ss_backward") and fits:
             g = gy if gy is not None else torch.zeros_like(x)
             res = torch.ops.philtorch.lpv_ss_backward(A, B, C, D, zi, x, g, gzf, ctx.out_idx, ctx.reverse,
                                                       ctx.transpose_A)
@@ -728,6 +736,7 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
         if not wrt:
             return tuple(out)
+        create = torch.is_grad_enabled()  # create_graph, read before enable_grad
         with torch.enable_grad():
             Am = A.mT if ctx.transpose_A else A  # the model's matrices
             if ctx.reverse:
@@ -742,7 +751,7 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
             if gzf is not None:
                 outs.append(zf)
                 grads.append(gzf)
-            res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=torch.is_grad_enabled(),
+            res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=create,
                                       allow_unused=True)
         for i, g in zip(wrt, res):
             out[i] = g if g is not None else torch.zeros_like(inputs[i])

@@ -6,6 +6,7 @@
 namespace phs {
 std::atomic<unsigned> g_spin_limit{0};
 std::atomic<bool> g_agg_only{false};
+std::atomic<int> g_sos_kept_step{-1};
 TimingHook g_timing;
 TraceHook g_trace;
 
@@ -68,6 +69,8 @@ int phs_abi_version(void) { return 112; }
 void phs_debug_set_spin_limit(unsigned polls) { phs::g_spin_limit.store(polls, std::memory_order_relaxed); }
 
 void phs_debug_set_aggregates_only(int on) { phs::g_agg_only.store(on != 0, std::memory_order_relaxed); }
+
+void phs_debug_set_sos_kept_step(int step) { phs::g_sos_kept_step.store(step, std::memory_order_relaxed); }
 
 void phs_debug_time_next_launch(void *start_event, void *stop_event) {
   std::lock_guard<std::mutex> lock(phs::g_timing.mu);

@@ -29,6 +29,7 @@ inline constexpr size_t kAlign = 256;
 inline constexpr unsigned kDefaultSpinLimit = 1u << 16;
 extern std::atomic<unsigned> g_spin_limit;  // testing hook, 0 = default (phs_capi.hip)
 extern std::atomic<bool> g_agg_only;        // testing hook (phs_capi.hip)
+extern std::atomic<int> g_sos_kept_step;    // testing hook, < 0 = automatic (phs_capi.hip)
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 // Measurement hook (phs_debug_time_next_launch): a pair of events that the

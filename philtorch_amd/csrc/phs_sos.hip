@@ -202,6 +202,11 @@ int sos_bwd(int64_t B, int64_t T, int S, const SosCoefs &k, const void *x, const
     int step = S >= 2 ? (S + 2) / 3 : 0;
     if (step > 0 && laneh + sos_kept_slots(S, step) * slot > limit) step = (S + 1) / 2;
     if (step > 0 && laneh + sos_kept_slots(S, step) * slot > limit) step = 0;
+    const int forced = g_sos_kept_step.load(std::memory_order_relaxed);  // testing hook
+    if (forced >= 0) {
+      if (laneh + sos_kept_slots(S, forced) * slot > limit) return PHS_ERR_INVALID;
+      step = forced;
+    }
     a.kept_step = step;
     size_t lds = laneh + sos_kept_slots(S, step) * slot;
     // kept slot 0 also takes the output's LDS transpose at the end; without

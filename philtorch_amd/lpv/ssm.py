@@ -368,6 +368,31 @@ def _lpv_state_space_composite(A, B, C, D, zi, x, out_idx=0):
     return y, zf
 
 
+# Above this many bytes of per-row, per-step gradients of the operands that
+# the rows share but that vary along time (A (T, M, M); B, C, D with one row
+# and T steps), which philtorch::lpv_ss_backward writes for every row before
+# it sums them, the coefficient gradients take the composed route's autograd
+# instead, which reduces over the rows as it goes (the reference's
+# algorithm, philtorch/lpv/ssm.py:337-581).  At B = 32, T = 2^20, M = 4 fp32
+# the scratch for A alone is 2 GiB.
+_LPV_ROW_SCRATCH_LIMIT = 512 << 20
+
+
+def _lpv_row_scratch_bytes(A: Tensor, B, C, D, x: Tensor, needs) -> int:
+    """Bytes of per-row step gradients philtorch::lpv_ss_backward would
+    write for operands shared by the rows and varying along time, for the
+    gradients `needs` asks for (A, B, C, D order)."""
+    batch, T = x.shape
+    M = A.size(-1)
+    per_step = 0
+    if needs[0] and A.dim() == 3:
+        per_step += M * M
+    for t, width, need in ((B, M, needs[1]), (C, M, needs[2]), (D, 1, needs[3])):
+        if need and t is not None and (t.size(0) == 1 or t.stride(0) == 0) and t.size(1) > 1 and t.stride(1) != 0:
+            per_step += width
+    return batch * T * per_step * x.element_size()
+
+
 def _fused_lpv_ss_applies(A: Tensor, x: Tensor, zi: Optional[Tensor], ops, native: bool) -> bool:
     """A model of order <= 4 with one input and one output on a HIP device,
     the native route requested and no tangent: philtorch::lpv_ss runs it in

@@ -62,6 +62,8 @@ def load() -> ctypes.CDLL:
     lib.phs_debug_set_spin_limit.restype = None
     lib.phs_debug_set_aggregates_only.argtypes = [ctypes.c_int]
     lib.phs_debug_set_aggregates_only.restype = None
+    lib.phs_debug_set_sos_kept_step.argtypes = [ctypes.c_int]
+    lib.phs_debug_set_sos_kept_step.restype = None
     lib.phs_debug_time_next_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     lib.phs_debug_time_next_launch.restype = None
     lib.phs_debug_trace_next_launch.argtypes = [ctypes.c_void_p, ctypes.c_size_t]

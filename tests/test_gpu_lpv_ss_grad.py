@@ -182,3 +182,35 @@ def test_lpv_api_takes_fused_route_with_coefficient_gradients(hip, monkeypatch):
             assert torch.autograd.gradcheck(f, (As, bs, cs, ds, zs, xs))
     f = lambda *a: torch.ops.philtorch.lpv_ss(*a, 0)  # noqa: E731
     assert torch.autograd.gradgradcheck(f, (As, bs, cs, ds, zs, xs))
+
+
+def test_lpv_shared_step_gradients_above_scratch_limit_take_composite(hip, monkeypatch):
+    """Operands shared by the rows and varying along time (A (T, M, M); b, d
+    with one row): the fused backward would first write every row's
+    per-step gradient.  Above lpv.ssm._LPV_ROW_SCRATCH_LIMIT bytes of that
+    scratch the gradients come from the composed route's autograd instead;
+    both routes' gradients agree (fp64), and the byte count is the fused
+    backward's."""
+    import torch
+
+    from philtorch_amd import lpv
+    from philtorch_amd.lpv import ssm
+
+    g = D.rng(D.seed_of("lpv-scratch-limit"))
+    Bn, T, M = 3, 7000, 3
+    A0 = _model(g, M, Bn, T, True)
+    b0, c0 = g.standard_normal((1, T, M)), g.standard_normal((Bn, 1, M))
+    d0, x0, z0 = g.standard_normal((1, T)), g.standard_normal((Bn, T)), g.standard_normal((Bn, M))
+    gy, gzf = g.standard_normal((Bn, T)), g.standard_normal((Bn, M))
+    assert ssm._lpv_row_scratch_bytes(_t(A0), _t(b0), _t(c0), _t(d0), _t(x0), (True,) * 4) == Bn * T * (M * M + M + 1) * 8
+    grads = {}
+    for limit in (ssm._LPV_ROW_SCRATCH_LIMIT, 0):
+        print(f"lpv scratch limit={limit}", flush=True)
+        monkeypatch.setattr(ssm, "_LPV_ROW_SCRATCH_LIMIT", limit)
+        # the API's shapes: B (T, M) and D (T,) shared by the rows, C (batch, M)
+        ins = [_t(v, rg=True) for v in (A0, b0.reshape(T, M), c0.reshape(Bn, M), d0.reshape(T), z0, x0)]
+        A, b, c, d, zi, x = ins
+        y, zf = lpv.state_space(A, x, B=b, C=c, D=d, zi=zi, unroll_factor=1)
+        grads[limit] = torch.autograd.grad((y, zf), ins, (_t(gy), _t(gzf)))
+    for nm, a, r in zip(("A", "B", "C", "D", "zi", "x"), grads[0], grads[ssm._LPV_ROW_SCRATCH_LIMIT]):
+        D.check(a.cpu().numpy(), r.cpu().numpy(), f"composite vs fused grad {nm}", dtype=np.float64)

@@ -162,6 +162,33 @@ def test_sosfilt_capi_forced_fallback(api, dtype):
     _check_all(got, *case, dtype, "fallback")
 
 
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+def test_sosfilt_capi_forced_kept_step(api, dtype):
+    """Every kept_step branch of the eight-section gradient backward
+    (phs_debug_set_sos_kept_step): none kept, so every re-derivation of a
+    section's input runs from x through all sections below it; one and two
+    kept slots at the steps the LDS allows (others return PHS_ERR_INVALID).
+    grad_sos, grad_x and grad_zi against the oracle each time."""
+    lib, _, capi = api
+    case = _case(dtype, 3, 2 * 6144 + 77, 8, False, True, True, D.seed_of("sos-kept-step", dtype))
+    ran = []
+    try:
+        for step in (0, 1, 2, 3, 4, 5, 7, 8):
+            lib.phs_debug_set_sos_kept_step(step)
+            print(f"sos kept_step={step} {np.dtype(dtype).name}", flush=True)
+            try:
+                got = _run(api, *case)
+            except AssertionError as e:
+                assert "invalid" in str(e).lower(), e  # the forced slots exceed this device's LDS
+                assert step != 0
+                continue
+            _check_all(got, *case, dtype, f"kept_step={step}")
+            ran.append(step)
+    finally:
+        lib.phs_debug_set_sos_kept_step(-1)
+    assert 0 in ran and any(s not in (0, 8) for s in ran), ran
+
+
 def test_sosfilt_capi_errors(api):
     import torch
 

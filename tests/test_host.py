@@ -391,3 +391,26 @@ def test_table_column_detects_only_exact_columns():
     assert _table_column(torch.randn(4, 8, 3)[:, 1])[1] == -1  # no gradient wanted
     plain = torch.randn(4, 3, requires_grad=True)
     assert _table_column(plain) == (plain, -1)
+
+
+def test_lpv_row_scratch_bytes_counts_shared_time_varying_operands():
+    """The fused LPV backward's per-row step-gradient scratch: A shared by the
+    rows (T, M, M) and b, c, d with one row and T steps count; per-row or
+    constant-in-time operands and gradients not wanted do not.  B = 32,
+    T = 2^20, M = 4 fp32 (A alone: 2 GiB) is above the limit."""
+    import torch
+
+    from philtorch_amd.lpv import ssm
+
+    B, T, M = 32, 1 << 20, 4
+    meta = lambda *s: torch.empty(*s, device="meta")  # noqa: E731
+    x = meta(B, T)
+    need = (True,) * 4
+    assert ssm._lpv_row_scratch_bytes(meta(T, M, M), None, None, None, x, need) == B * T * M * M * 4 == 2 << 30
+    assert ssm._lpv_row_scratch_bytes(meta(T, M, M), None, None, None, x, need) > ssm._LPV_ROW_SCRATCH_LIMIT
+    assert ssm._lpv_row_scratch_bytes(meta(B, T, M, M), None, None, None, x, need) == 0
+    assert ssm._lpv_row_scratch_bytes(meta(T, M, M), None, None, None, x, (False, True, True, True)) == 0
+    b_step, b_row = meta(1, T, M), meta(B, 1, M)
+    d_step = meta(1, T)
+    assert ssm._lpv_row_scratch_bytes(meta(B, T, M, M), b_step, b_row, d_step, x, need) == B * T * (M + 1) * 4
+    assert ssm._lpv_row_scratch_bytes(meta(B, T, M, M), meta(B, T, M), None, meta(1, 1), x, need) == 0
