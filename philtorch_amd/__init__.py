@@ -411,14 +411,13 @@ if EXTENSION_LOADED and _has_op("biquad_cols"):
         ctx.has_zi = zi is not None
         ctx.set_materialize_grads(False)
 
-    def _biquad_cols_backward(ctx, gy, gzf, _gckpt):
-        """philtorch::biquad_cols_backward: biquad_backward whose coefficient
-        gradients are the tables' (the caller's b[:, s] costs autograd no
-        zero-filled table and column copy).  Under create_graph: the
-        section's composite gradient scattered into the table's column."""
-        bt, at, x, ckpt, zi = ctx.saved_tensors
-        b_col, a_col = ctx.cols
-        needs = ctx.needs_input_grad  # bt, b_col, at, a_col, zi, x
+    def _biquad_cols_grads(bt, b_col, at, a_col, x, ckpt, zi, has_zi, needs, gy, gzf):
+        """(grad bt, grad at, grad zi, grad x) of philtorch::biquad_cols for
+        `needs` (bt, at, zi, x): biquad_backward whose coefficient gradients
+        are the tables' (the caller's b[:, s] costs autograd no zero-filled
+        table and column copy), called below the Autograd dispatch key.
+        Under create_graph: the section's composite gradient scattered into
+        the table's column."""
         if gy is None:
             gy = torch.zeros_like(x)
         if torch.is_grad_enabled():
@@ -427,19 +426,55 @@ if EXTENSION_LOADED and _has_op("biquad_cols"):
                             dim=-1).unsqueeze(-2)
             zs = None if zi is None else zi.unsqueeze(1)
             gsos, gz, gx = _sosfilt_composite(sos, zs, x, gy, None if gzf is None else gzf.unsqueeze(1),
-                                              (needs[0] or needs[2], needs[4], needs[5]))
+                                              (needs[0] or needs[1], needs[2], needs[3]))
             gbt = gat = None
             if gsos is not None:
                 gb, ga = gsos[..., 0, : b.size(-1)], gsos[..., 0, 4:6]
                 gbt = gb if b_col < 0 else torch.select_scatter(torch.zeros_like(bt), gb, -2, b_col)
                 gat = ga if a_col < 0 else torch.select_scatter(torch.zeros_like(at), ga, -2, a_col)
-            return (gbt if needs[0] else None, None, gat if needs[2] else None, None,
-                    gz[:, 0] if (gz is not None and ctx.has_zi and needs[4]) else None, gx if needs[5] else None)
-        need_coef = bool(needs[0] or needs[2])
-        gx, gbt, gat, gzi = torch.ops.philtorch.biquad_cols_backward(bt, b_col, at, a_col, x, ckpt, gy, gzf,
-                                                                     need_coef)
-        return (gbt if needs[0] else None, None, gat if needs[2] else None, None,
-                gzi if ctx.has_zi and needs[4] else None, gx if needs[5] else None)
+            return (gbt if needs[0] else None, gat if needs[1] else None,
+                    gz[:, 0] if (gz is not None and has_zi and needs[2]) else None, gx if needs[3] else None)
+        need_coef = bool(needs[0] or needs[1])
+        with torch._C._AutoDispatchBelowAutograd():
+            gx, gbt, gat, gzi = torch.ops.philtorch.biquad_cols_backward(bt, b_col, at, a_col, x, ckpt, gy, gzf,
+                                                                         need_coef)
+        return (gbt if needs[0] else None, gat if needs[1] else None, gzi if has_zi and needs[2] else None,
+                gx if needs[3] else None)
+
+    def _biquad_cols_backward(ctx, gy, gzf, _gckpt):
+        bt, at, x, ckpt, zi = ctx.saved_tensors
+        b_col, a_col = ctx.cols
+        n = ctx.needs_input_grad  # bt, b_col, at, a_col, zi, x
+        gbt, gat, gzi, gx = _biquad_cols_grads(bt, b_col, at, a_col, x, ckpt, zi, ctx.has_zi,
+                                               (n[0], n[2], n[4], n[5]), gy, gzf)
+        return gbt, None, gat, None, gzi, gx
+
+    class _BiquadColumns(torch.autograd.Function):
+        """lfilter's route for a biquad whose b or a is a column of a
+        coefficient table: philtorch::biquad_cols and its backward, called
+        below the Autograd dispatch key.  The op's own registered autograd
+        (torch.library) runs the same gradients; this Function skips that
+        layer's Python per call (about half of the C4 caller pattern's host
+        time per lfilter, where the step is bound by the host)."""
+
+        @staticmethod
+        def forward(ctx, bt, at, zi, x, b_col, a_col):
+            with torch._C._AutoDispatchBelowAutograd():
+                y, zf, ckpt = torch.ops.philtorch.biquad_cols(bt, b_col, at, a_col, zi, x)
+            ctx.save_for_backward(bt, at, x, ckpt, zi)
+            ctx.cols = (b_col, a_col)
+            ctx.has_zi = zi is not None
+            ctx.set_materialize_grads(False)
+            return y, zf
+
+        @staticmethod
+        def backward(ctx, gy, gzf):
+            bt, at, x, ckpt, zi = ctx.saved_tensors
+            b_col, a_col = ctx.cols
+            n = ctx.needs_input_grad  # bt, at, zi, x, b_col, a_col
+            gbt, gat, gzi, gx = _biquad_cols_grads(bt, b_col, at, a_col, x, ckpt, zi, ctx.has_zi,
+                                                   (n[0], n[1], n[2], n[3]), gy, gzf)
+            return gbt, gat, gzi, gx, None, None
 
     torch.library.register_autograd("philtorch::biquad_cols", _biquad_cols_backward,
                                     setup_context=_biquad_cols_setup)

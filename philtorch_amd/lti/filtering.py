@@ -116,7 +116,9 @@ def _fused_biquad(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor]):
     if (b_col >= 0 or a_col >= 0) and hasattr(torch.ops.philtorch, "biquad_cols"):
         # b or a is a column of a coefficient table (the caller's b[:, s]):
         # the table takes its gradient directly
-        y, zf, _ = torch.ops.philtorch.biquad_cols(bt, b_col, at, a_col, zb, x)
+        from .. import _BiquadColumns
+
+        y, zf = _BiquadColumns.apply(bt, at, zb, x, b_col, a_col)
     else:
         y, zf, _ = torch.ops.philtorch.biquad(b, a, zb, x)
     return y if zi is None else (y, zf)

@@ -579,6 +579,13 @@ def test_biquad_cols_op_gradients_and_opcheck(hip):
     assert torch.autograd.gradgradcheck(f, (tab_b, tab_a, zi, x))
     f2 = lambda tb_, a_, x_: torch.ops.philtorch.biquad_cols(tb_, 0, a_, -1, None, x_)[0]  # noqa: E731
     assert torch.autograd.gradcheck(f2, (tab_b, a_row, x))
+    # the same through lti.lfilter, whose column route is its own autograd
+    # Function over the same ops (first and second order)
+    from philtorch_amd import lti
+
+    f3 = lambda tb_, ta_, z_, x_: lti.lfilter(tb_[:, 2], ta_[:, 1], x_, zi=z_, form="tdf2", unroll_factor=1)  # noqa: E731
+    assert torch.autograd.gradcheck(f3, (tab_b, tab_a, zi, x))
+    assert torch.autograd.gradgradcheck(f3, (tab_b, tab_a, zi, x))
     s = lambda v: torch.tensor(np.asarray(v, np.float32), device="cuda")  # noqa: E731
     torch.library.opcheck(torch.ops.philtorch.biquad_cols.default,
                           (s(g.standard_normal((3, 3))), 1, s([[-0.5, 0.2]] * 3), 2, None,
