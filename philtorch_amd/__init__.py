@@ -266,6 +266,18 @@ def _has_op(name: str) -> bool:
         return False
 
 
+def _op_ctx(*tensors):
+    """The context of a philtorch op call: as it is where autograd records a
+    graph (grad mode on and an input wanting a gradient); else below the
+    Autograd dispatch key, which skips the Python layer of the op's
+    registered autograd (torch.library) on every call."""
+    import contextlib
+
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        return contextlib.nullcontext()
+    return torch._C._AutoDispatchBelowAutograd()
+
+
 # (a _C.so built before the cascade ops existed lacks them; the in-tree build
 # imports this package before it rebuilds that library)
 def _n_ckpt(x, T):
@@ -329,7 +341,8 @@ if EXTENSION_LOADED and _has_op("sosfilt"):
         if torch.is_grad_enabled():  # create_graph: a differentiable gradient
             return _sosfilt_composite(sos, zi, x, gy, gzf, needs)
         need_sos = bool(needs[0])
-        gx, gsos, gzi = torch.ops.philtorch.sosfilt_backward(sos, x, ckpt, gy, gzf, need_sos)
+        with _op_ctx(sos, x, gy):
+            gx, gsos, gzi = torch.ops.philtorch.sosfilt_backward(sos, x, ckpt, gy, gzf, need_sos)
         return (gsos if needs[0] else None, gzi if ctx.has_zi and needs[1] else None, gx if needs[2] else None)
 
     torch.library.register_autograd("philtorch::sosfilt", _sosfilt_backward, setup_context=_sosfilt_setup)
@@ -378,7 +391,8 @@ if EXTENSION_LOADED and _has_op("biquad"):
             return (gb if needs[0] else None, ga if needs[1] else None,
                     gz[:, 0] if (gz is not None and ctx.has_zi and needs[2]) else None, gx if needs[3] else None)
         need_coef = bool(needs[0] or needs[1])
-        gx, gb, ga, gzi = torch.ops.philtorch.biquad_backward(b, a, x, ckpt, gy, gzf, need_coef)
+        with _op_ctx(b, a, x, gy):
+            gx, gb, ga, gzi = torch.ops.philtorch.biquad_backward(b, a, x, ckpt, gy, gzf, need_coef)
         return (gb if needs[0] else None, ga if needs[1] else None, gzi if ctx.has_zi and needs[2] else None,
                 gx if needs[3] else None)
 
@@ -536,7 +550,9 @@ if EXTENSION_LOADED and _has_op("filtfilt"):
             if not need_coef:
                 if torch.is_grad_enabled():
                     return None, None, _FiltfiltAdjoint.apply(b, a, gy, *ctx.pad), None, None
-                return None, None, torch.ops.philtorch.filtfilt_backward(b, a, x, gy, *ctx.pad, False)[0], None, None
+                with _op_ctx(b, a, x, gy):
+                    gx = torch.ops.philtorch.filtfilt_backward(b, a, x, gy, *ctx.pad, False)[0]
+                return None, None, gx, None, None
             if torch.is_grad_enabled():
                 from .lti.filtering import _PAD_CODES, _filtfilt_composed
 
@@ -550,7 +566,8 @@ if EXTENSION_LOADED and _has_op("filtfilt"):
                 for i, g in zip(wrt, res):
                     out[i] = g if g is not None else torch.zeros_like(inputs[i])
                 return tuple(out)
-            gx, gb, ga = torch.ops.philtorch.filtfilt_backward(b, a, x, gy, *ctx.pad, True)
+            with _op_ctx(b, a, x, gy):
+                gx, gb, ga = torch.ops.philtorch.filtfilt_backward(b, a, x, gy, *ctx.pad, True)
             return gb if needs[0] else None, ga if needs[1] else None, gx if needs[2] else None, None, None
 
         torch.library.register_autograd("philtorch::filtfilt", _filtfilt_backward, setup_context=_filtfilt_setup)
@@ -595,7 +612,8 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
         A, B, C, D, zi, x = inputs
         if any(needs[:4]) and not torch.is_grad_enabled() and _has_op("lti_ss_backward"):
             g = gy if gy is not None else torch.zeros_like(x)
-            res = torch.ops.philtorch.lti_ss_backward(A, B, C, D, zi, x, g, gzf, ctx.out_idx, ctx.reverse)
+            with _op_ctx(A, B, C, D, zi, x, g):
+                res = torch.ops.philtorch.lti_ss_backward(A, B, C, D, zi, x, g, gzf, ctx.out_idx, ctx.reverse)
             out = [None] * 8
             for i, t in enumerate(inputs[:5] + (x,)):
                 if t is not None and needs[i]:
@@ -605,8 +623,9 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
             M = A.size(-1)
             unit = lambda i: torch.nn.functional.one_hot(torch.tensor(i, device=x.device), M).to(x.dtype)  # noqa: E731
             g = gy if gy is not None else torch.zeros_like(x)
-            gx, gzi = torch.ops.philtorch.lti_ss(A.mT.contiguous(), C if C is not None else unit(ctx.out_idx),
-                                                 B if B is not None else unit(0), D, gzf, g, 0, not ctx.reverse)
+            with _op_ctx(A, B, C, D, gzf, g):
+                gx, gzi = torch.ops.philtorch.lti_ss(A.mT.contiguous(), C if C is not None else unit(ctx.out_idx),
+                                                     B if B is not None else unit(0), D, gzf, g, 0, not ctx.reverse)
             return (None, None, None, None, gzi if zi is not None and needs[4] else None,
                     gx if needs[5] else None, None, None)
         wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
@@ -671,12 +690,14 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
         needs = ctx.needs_input_grad
         if (needs[0] or needs[1]) and not torch.is_grad_enabled() and _has_op("lfilter_ss_backward"):
             g = gy if gy is not None else torch.zeros_like(x)
-            gb, ga, gzi, gx = torch.ops.philtorch.lfilter_ss_backward(b, a, zi, x, g, gzf, ctx.form, ctx.reverse)
+            with _op_ctx(b, a, zi, x, g):
+                gb, ga, gzi, gx = torch.ops.philtorch.lfilter_ss_backward(b, a, zi, x, g, gzf, ctx.form, ctx.reverse)
             return (gb if needs[0] else None, ga if needs[1] else None,
                     gzi if zi is not None and needs[2] else None, gx if needs[3] else None, None, None)
         if not (needs[0] or needs[1]):
             g = gy if gy is not None else torch.zeros_like(x)
-            gx, gzi = torch.ops.philtorch.lfilter_ss(b, a, gzf, g, 1 - ctx.form, not ctx.reverse)
+            with _op_ctx(b, a, gzf, g):
+                gx, gzi = torch.ops.philtorch.lfilter_ss(b, a, gzf, g, 1 - ctx.form, not ctx.reverse)
             return (None, None, gzi if zi is not None and needs[2] else None, gx if needs[3] else None, None, None)
         wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
         create = torch.is_grad_enabled()  # create_graph, read before enable_grad
@@ -748,8 +769,9 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         fits = _lpv_ssm._lpv_row_scratch_bytes(A, B, C, D, x, needs[:4]) <= _lpv_ssm._LPV_ROW_SCRATCH_LIMIT
         if any(needs[:4]) and not torch.is_grad_enabled() and _has_op("lpv_ss_backward") and fits:
             g = gy if gy is not None else torch.zeros_like(x)
-            res = torch.ops.philtorch.lpv_ss_backward(A, B, C, D, zi, x, g, gzf, ctx.out_idx, ctx.reverse,
-                                                      ctx.transpose_A)
+            with _op_ctx(A, B, C, D, zi, x, g):
+                res = torch.ops.philtorch.lpv_ss_backward(A, B, C, D, zi, x, g, gzf, ctx.out_idx, ctx.reverse,
+                                                          ctx.transpose_A)
             for i, t in enumerate(inputs):
                 if t is not None and needs[i]:
                     out[i] = res[i]
@@ -761,8 +783,9 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
                 c_in = x.new_zeros(1, 1, M)
                 c_in[..., ctx.out_idx] = 1
             g = gy if gy is not None else torch.zeros_like(x)
-            gx, gzi = torch.ops.philtorch.lpv_ss(A, c_in, B, D, gzf, g, 0, not ctx.reverse,
-                                              not ctx.transpose_A)
+            with _op_ctx(A, c_in, B, D, gzf, g):
+                gx, gzi = torch.ops.philtorch.lpv_ss(A, c_in, B, D, gzf, g, 0, not ctx.reverse,
+                                                  not ctx.transpose_A)
             if zi is not None and needs[4]:
                 out[4] = gzi
             if needs[5]:

@@ -456,8 +456,11 @@ def state_space(
     native = extension_backend_indicator(x, M) and unroll_factor in (None, 1)
     ops = _lpv_siso_operands(x, B, C, D, out_idx, batch, N, M)
     if _fused_lpv_ss_applies(A, x, zi if return_zf else None, ops, native):
-        y, zf = torch.ops.philtorch.lpv_ss(A, ops[0], ops[1], ops[2], zi.contiguous() if return_zf else None, x,
-                                           0 if out_idx is None else out_idx)
+        from .. import _op_ctx
+
+        with _op_ctx(A, *ops, zi, x):
+            y, zf = torch.ops.philtorch.lpv_ss(A, ops[0], ops[1], ops[2], zi.contiguous() if return_zf else None, x,
+                                               0 if out_idx is None else out_idx)
         return (y, zf) if return_zf else y
     Bx = _apply_B(x, B, batch, N, M, features)
 

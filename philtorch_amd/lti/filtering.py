@@ -120,7 +120,10 @@ def _fused_biquad(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor]):
 
         y, zf = _BiquadColumns.apply(bt, at, zb, x, b_col, a_col)
     else:
-        y, zf, _ = torch.ops.philtorch.biquad(b, a, zb, x)
+        from .. import _op_ctx
+
+        with _op_ctx(b, a, zb, x):
+            y, zf, _ = torch.ops.philtorch.biquad(b, a, zb, x)
     return y if zi is None else (y, zf)
 
 
@@ -186,7 +189,10 @@ def _fused_lfilter(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor], form: 
     """lfilter(b, a, x, zi, form) through philtorch::lfilter_ss."""
     M = max(b.size(-1) - 1, a.size(-1))
     zb = None if zi is None else zi.expand(x.size(0), M).contiguous()
-    y, zf = torch.ops.philtorch.lfilter_ss(b, a, zb, x, 0 if form == "tdf2" else 1)
+    from .. import _op_ctx
+
+    with _op_ctx(b, a, zb, x):
+        y, zf = torch.ops.philtorch.lfilter_ss(b, a, zb, x, 0 if form == "tdf2" else 1)
     return y if zi is None else (y, zf)
 
 
@@ -295,7 +301,10 @@ def _fused_filtfilt(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[str], edg
     """filtfilt of a filter of order 4 at most through philtorch::filtfilt."""
     x2 = x.reshape(-1, x.size(-1))
     code = _PAD_CODES[padmode] if padmode is not None else 0
-    y = torch.ops.philtorch.filtfilt(b, a, x2, code, edge if padmode is not None else 0)
+    from .. import _op_ctx
+
+    with _op_ctx(b, a, x2):
+        y = torch.ops.philtorch.filtfilt(b, a, x2, code, edge if padmode is not None else 0)
     return y.reshape(x.shape)
 
 
@@ -391,11 +400,14 @@ def _sosfilt_fused(sos: Tensor, x: Tensor, zi: Optional[Tensor]) -> tuple[Tensor
         zi = None if zi is None else zi.float()
     else:
         sos = sos.to(dtype)
+    from .. import _op_ctx
+
     y, zfs = x, []
     for s0 in range(0, sos.size(-2), _SOS_SECTIONS_PER_CALL):
         part = sos[..., s0:s0 + _SOS_SECTIONS_PER_CALL, :]
         zpart = None if zi is None else zi[:, s0:s0 + part.size(-2)].contiguous()
-        y, zf, _ = torch.ops.philtorch.sosfilt(part.contiguous(), zpart, y.contiguous())
+        with _op_ctx(part, zpart, y):
+            y, zf, _ = torch.ops.philtorch.sosfilt(part.contiguous(), zpart, y.contiguous())
         zfs.append(zf)
     return y.to(dtype), torch.cat(zfs, dim=1).to(dtype)
 

@@ -304,8 +304,11 @@ def _state_space(A, x, B, C, D, zi, unroll_factor, out_idx, fused):
     if unroll_factor is None:
         unroll_factor = round(N**0.5)
     if fused and _fused_ss_applies(A, x, B, C, D, zi, unroll_factor, out_idx):
-        y, zf = torch.ops.philtorch.lti_ss(A, B, C, D, zi.contiguous() if return_zf else None, x,
-                                           out_idx if C is None else 0)
+        from .. import _op_ctx
+
+        with _op_ctx(A, B, C, D, zi, x):
+            y, zf = torch.ops.philtorch.lti_ss(A, B, C, D, zi.contiguous() if return_zf else None, x,
+                                               out_idx if C is None else 0)
         return (y, zf) if return_zf else y
     features = -1 if x.dim() == 2 else x.size(-1)
     if B is not None:
