@@ -538,6 +538,43 @@ int phs_lpv_ss_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
                    void *gd, int reverse, void *scratch, size_t scratch_bytes, void *workspace,
                    size_t workspace_bytes, void *stream);
 
+/* Bits of the `shared` argument of phs_mimo_ss_fwd / phs_mimo_ss_rev: an
+ * operand with its bit set is one matrix for every row (else one per row). */
+#define PHS_MIMO_A_SHARED 1
+#define PHS_MIMO_B_SHARED 2
+#define PHS_MIMO_C_SHARED 4
+#define PHS_MIMO_D_SHARED 8
+
+/* ---- Multi-input, multi-output LTI state space of order M = 1..4 with
+ * F = 1..4 inputs and P = 1..4 outputs per step, fused (forward).  Replaces
+ * philtorch.lti.state_space (philtorch/lti/ssm.py:386-589) for a 3D input
+ * x (batch, time, features) or matrix-valued B, C, D: the composed route's
+ * B x (:460-485), recurrence (_ext_ss_recur, :487-491), state shift
+ * (:493-504) and _ssm_C_D (:506, :513-589) in one pass:
+ *     h[0] = zi,  y[t] = C h[t] + D x[t],  h[t+1] = A h[t] + B x[t],  zf = h[T]
+ * dtype PHS_F32 or PHS_F64; A [B,M,M], Bm [B,M,F], Cm [B,P,M], Dm [B,P,F]
+ * (row-major; an operand with its PHS_MIMO_*_SHARED bit in `shared` is one
+ * matrix, without the row axis); Dm NULL: no feedthrough; zi [B,M] (NULL =
+ * zeros); x [B,T,F] and y [B,T,P], features innermost; zf [B,M] (skipped
+ * when NULL; zi when T = 0).  `workspace`: phs_mimo_ss_workspace_size
+ * bytes, under the conventions above. */
+size_t phs_mimo_ss_workspace_size(int dtype, int M, int64_t B, int64_t T);
+
+int phs_mimo_ss_fwd(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *A, const void *Bm,
+                    const void *Cm, const void *Dm, int shared, const void *zi, const void *x, void *y, void *zf,
+                    void *workspace, size_t workspace_bytes, void *stream);
+
+/* The same model run backwards in time (no counterpart in the reference,
+ * which flips): h[T] = zi, y[t] = C h[t+1] + D x[t], h[t] = A h[t+1] +
+ * B x[t], zf = h[0].  The adjoint of the forward model is this one on
+ * (A^T, C^T, B^T, D^T) from dL/dzf: y = grad_x, zf = grad_zi; with C the
+ * identity and no D, y[t] is the adjoint state dL/dh[t+1] that the
+ * coefficient gradients sum against (dL/dA = sum lambda[t+1] h[t]^T,
+ * dL/dB = sum lambda[t+1] x[t]^T). */
+int phs_mimo_ss_rev(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *A, const void *Bm,
+                    const void *Cm, const void *Dm, int shared, const void *zi, const void *x, void *y, void *zf,
+                    void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- Measurement helper, no counterpart in the reference.  A streaming
  * kernel with no scan: out_j[i] = (j + 1) * sum_k in_k[i] over n fp32
  * elements, n_in = 1..3 input arrays and n_out = 1..2 output arrays (16-byte

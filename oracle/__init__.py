@@ -317,7 +317,7 @@ def lpv_state_space(A, x, B=None, C=None, D=None, zi=None, out_idx=None, nthread
         Bx = x[..., None] * np.broadcast_to(np.asarray(B, dtype=dt), (Bn, T, M))
     h = recurN(A, zi, _c(Bx, dt), nthreads)
     zf = h[:, -1] if T > 0 else zi.copy()
-    hprev = np.concatenate([zi[:, None, :], h[:, :-1]], axis=1)
+    hprev = np.concatenate([zi[:, None, :], h[:, :-1]], axis=1)[:, :T]
     if C is None:
         y = hprev[..., out_idx].copy()
     else:
@@ -382,6 +382,34 @@ def filtfilt_ba(b, a, x, padmode="replicate", padlen=None, nthreads=None):
     return np.ascontiguousarray(y[:, ::-1])
 
 
+def lti_state_space_mimo(A, x, B, C, D=None, zi=None, nthreads=None):
+    """philtorch.lti.state_space with matrix operands (philtorch/lti/ssm.py:
+    386-589 for a 3D input (batch, time, features)): x [Bn,T,F]; A [M,M] or
+    [Bn,M,M]; B [M,F] or [Bn,M,F]; C [P,M] or [Bn,P,M]; D None, [P,F] or
+    [Bn,P,F].  Bx[t] = B x[t] (:478-482), the scan lti_recurN, the state
+    sequence shifted one step behind zi (:493-504), then y = C h + D x
+    (_ssm_C_D :513-589, its (_, M) / (batch, _, M) and (_, features) /
+    (batch, _, features) branches).  Returns (y [Bn,T,P], zf [Bn,M])."""
+    dt = np.asarray(x).dtype
+    x = _c(x, dt)
+    Bn, T, F = x.shape
+    A = _c(np.broadcast_to(A, (Bn,) + np.shape(A)[-2:]), dt)
+    M = A.shape[-1]
+    Bm = np.broadcast_to(np.asarray(B, dtype=dt), (Bn, M, F))
+    Cm = np.asarray(C, dtype=dt)
+    P = Cm.shape[-2]
+    Cm = np.broadcast_to(Cm, (Bn, P, M))
+    zi = np.zeros((Bn, M), dtype=dt) if zi is None else _c(np.broadcast_to(zi, (Bn, M)), dt)
+    Bx = np.einsum("bmf,btf->btm", Bm, x)
+    h = lti_recurN(A, zi, _c(Bx, dt), nthreads)
+    zf = h[:, -1] if T > 0 else zi.copy()
+    hprev = np.concatenate([zi[:, None, :], h[:, :-1]], axis=1)[:, :T]
+    y = np.einsum("bpm,btm->btp", Cm, hprev)
+    if D is not None:
+        y = y + np.einsum("bpf,btf->btp", np.broadcast_to(np.asarray(D, dtype=dt), (Bn, P, F)), x)
+    return _c(y, dt), _c(zf, dt)
+
+
 def lti_state_space(A, x, B=None, C=None, D=None, zi=None, out_idx=None, nthreads=None):
     """philtorch.lti.state_space for a 2D input and a single output
     (philtorch/lti/ssm.py:386-589): Bx = x b (b an M-vector per row or shared;
@@ -402,7 +430,7 @@ def lti_state_space(A, x, B=None, C=None, D=None, zi=None, out_idx=None, nthread
         Bx = x[..., None] * np.broadcast_to(np.asarray(B, dtype=dt), (Bn, M))[:, None, :]
     h = lti_recurN(A, zi, _c(Bx, dt), nthreads)
     zf = h[:, -1] if T > 0 else zi.copy()
-    hprev = np.concatenate([zi[:, None, :], h[:, :-1]], axis=1)
+    hprev = np.concatenate([zi[:, None, :], h[:, :-1]], axis=1)[:, :T]
     if C is None:
         y = hprev[..., out_idx].copy()
     else:

@@ -10,9 +10,11 @@ counterpart; ``lti.sosfilt`` is its API), the forward-only zero-phase
 ``filtfilt`` of filters up to order 4 (behind ``lti.filtfilt``) and the
 fused single-input single-output state space ``lti_ss`` (behind
 ``lti.state_space``), ``lfilter_ss``, ``lfilter`` of order <= 4 from b and
-a in one pass (behind ``lti.lfilter``), and ``lpv_ss``, the time-varying
+a in one pass (behind ``lti.lfilter``), ``lpv_ss``, the time-varying
 single-input single-output state space of order <= 4 (behind
-``lpv.state_space``).  This module then
+``lpv.state_space``), and ``mimo_ss``, the LTI state space of order <= 4
+with up to four inputs and outputs per step (behind ``lti.state_space``
+for a 3D x or matrix-valued B, C, D).  This module then
 registers fake (meta) kernels and autograd formulas for them, as
 philtorch/__init__.py:157-268 does for its ops.
 
@@ -816,6 +818,88 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         return tuple(out)
 
     torch.library.register_autograd("philtorch::lpv_ss", _lpv_ss_backward, setup_context=_lpv_ss_setup)
+
+if EXTENSION_LOADED and _has_op("mimo_ss"):
+    # LTI state space with F inputs and P outputs per step (F, P <= 4): (y, zf)
+    @torch.library.register_fake("philtorch::mimo_ss")
+    def _(A, B, C, D, zi, x, reverse=False):
+        torch._check(x.ndim == 3, lambda: "x must be 3D (batch, time, features)")
+        torch._check(A.ndim in (2, 3) and A.shape[-1] == A.shape[-2], lambda: "A must be (M, M) or (batch, M, M)")
+        torch._check(C.ndim in (2, 3), lambda: "C must be (P, M) or (batch, P, M)")
+        return x.new_empty((x.shape[0], x.shape[1], C.shape[-2])), x.new_empty((x.shape[0], A.shape[-1]))
+
+    def _mimo_ss_setup(ctx, inputs, output):
+        ctx.reverse = bool(inputs[6]) if len(inputs) > 6 else False
+        ctx.save_for_backward(*inputs[:6])
+        ctx.set_materialize_grads(False)
+
+    def _mimo_row_sums(left, right, shared):
+        """sum over t of left[b, t]^T right[b, t] per row (batch, L, R), or
+        over the rows too (L, R) for an operand the rows share: one GEMM
+        with time (and the rows) as its inner dimension."""
+        if shared:
+            return left.reshape(-1, left.size(-1)).mT @ right.reshape(-1, right.size(-1))
+        return torch.bmm(left.mT, right)
+
+    def _mimo_ss_backward(ctx, gy, gzf):
+        """The adjoint model (A^T, input matrix C^T, output matrix B^T, D^T)
+        run in the opposite time direction from dL/dzf gives grad_x and
+        grad_zi in one more mimo_ss pass.  The coefficient gradients
+            dL/dA = sum_t lambda[t+1] h[t]^T,  dL/dB = sum_t lambda[t+1] x[t]^T,
+            dL/dC = sum_t g[t] h[t]^T,         dL/dD = sum_t g[t] x[t]^T
+        take the states h[t] (the forward again with C = I and no D) and the
+        adjoint states lambda[t+1] (the adjoint pass with output matrix I),
+        each one more mimo_ss pass, and one GEMM per operand over time (and
+        the rows, for a shared operand).  Under create_graph: the gradient
+        of the composite the fused kernel replaces (B x, the native scan,
+        the state shift, C h + D x; philtorch/lti/ssm.py:386-589),
+        recomputed from the inputs and differentiable again."""
+        from .lti.ssm import _mimo_composite
+
+        inputs = ctx.saved_tensors
+        A, B, C, D, zi, x = inputs
+        needs = ctx.needs_input_grad
+        out = [None] * 7
+        if torch.is_grad_enabled():  # create_graph
+            wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
+            with torch.enable_grad():
+                y, zf = _mimo_composite(*inputs, reverse=ctx.reverse)
+                outs, grads = [y], [gy if gy is not None else torch.zeros_like(y)]
+                if gzf is not None:
+                    outs.append(zf)
+                    grads.append(gzf)
+                res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=True,
+                                          allow_unused=True)
+            for i, g in zip(wrt, res):
+                out[i] = g if g is not None else torch.zeros_like(inputs[i])
+            return tuple(out)
+        M = A.size(-1)
+        g = gy if gy is not None else x.new_zeros(x.size(0), x.size(1), C.size(-2))
+        At, Ct = A.mT.contiguous(), C.mT.contiguous()
+        eye = torch.eye(M, dtype=x.dtype, device=x.device)
+        with _op_ctx():
+            if needs[5] or (needs[4] and zi is not None):
+                gx, gzi = torch.ops.philtorch.mimo_ss(At, Ct, B.mT.contiguous(),
+                                                      D.mT.contiguous() if D is not None else None, gzf, g,
+                                                      not ctx.reverse)
+                out[5] = gx if needs[5] else None
+                out[4] = gzi if needs[4] and zi is not None else None
+            hs = lam = None
+            if needs[0] or needs[2]:
+                hs, _ = torch.ops.philtorch.mimo_ss(A, B, eye, None, zi, x, ctx.reverse)
+            if needs[0] or needs[1]:
+                lam, _ = torch.ops.philtorch.mimo_ss(At, Ct, eye, None, gzf, g, not ctx.reverse)
+        if needs[0]:
+            out[0] = _mimo_row_sums(lam, hs, A.dim() == 2)
+        if needs[1]:
+            out[1] = _mimo_row_sums(lam, x, B.dim() == 2)
+        if needs[2]:
+            out[2] = _mimo_row_sums(g, hs, C.dim() == 2)
+        if needs[3] and D is not None:
+            out[3] = _mimo_row_sums(g, x, D.dim() == 2)
+        return tuple(out)
+
+    torch.library.register_autograd("philtorch::mimo_ss", _mimo_ss_backward, setup_context=_mimo_ss_setup)
 
 from . import mat  # noqa: E402,F401
 from . import lti  # noqa: E402,F401

@@ -75,6 +75,7 @@ KERNEL_UNITS = (
     ("phs_sos.hip", [], "phs_sos.o"),
     ("phs_ss.hip", [], "phs_ss.o"),
     ("phs_lpvss.hip", [], "phs_lpvss.o"),
+    ("phs_mimo.hip", [], "phs_mimo.o"),
     ("phs_probe.hip", [], "phs_probe.o"),
 )
 

@@ -1,0 +1,437 @@
+// Fused multi-input, multi-output LTI state space of order M <= 4 with up to
+// four inputs and four outputs per step, in one pass (philtorch/lti/ssm.py:
+// 386-589: state_space with a 3D input (batch, time, features), B an M x F
+// matrix, C a P x M matrix, D a P x F matrix, each per row or shared; the
+// glue of lti/ssm.py:467-471, 493-506 and _ssm_C_D :513-589 folded into the
+// scan):
+//     h[0] = zi,  y[t] = C h[t] + D x[t],  h[t+1] = A h[t] + B x[t],  zf = h[T]
+// x is [rows, T, F] and y [rows, T, P], both with the features innermost.
+// Per step F inputs and P outputs move; the reference route writes and reads
+// B x, the state sequence, its shifted copy, C h and D x.
+//
+// The scan is the generic one (phs_scan.hpp) with one matrix per row: a lane
+// folds its K steps (A, B x[t]) into a map in compute precision (A^K and a
+// Horner sum, mimo_lane_map), wave scans chain the lanes, a
+// look-back wave resolves the tile's entry state over the row's status
+// words, and pass 2 re-runs the steps from each lane's entry state, writing
+// C h + D x.  F and P are arguments, not template parameters: a wave stages
+// its span of x through LDS as F planes of one feature each (a lane then
+// reads its K steps of feature f at a fixed offset), and its outputs leave
+// through P planes the same way, so the global side of both moves is the
+// span's contiguous block, one element per lane and instruction.  The
+// reversed mode (REV) runs the model backwards in time: the gradients w.r.t.
+// x and zi are that mode on the adjoint model (A^T, input matrix C^T, output
+// matrix B^T, feedthrough D^T); with C = I and no D the output is the state
+// before every step, which the coefficient gradients reduce against.
+#pragma once
+
+#include "phs_ss.hpp"
+
+namespace phs {
+
+// Largest F and P of a call (the register arrays of the model and of a
+// lane's per-step inputs and outputs are this wide).
+constexpr int kMimoMaxIO = 4;
+
+template <class Alg>
+struct MimoArgs {
+  using E = typename Alg::elem;
+  const E *A;  // [rows, M, M] row-major
+  int64_t A_stride;  // elements between rows (0 = shared)
+  const E *Bm;  // [rows, M, F]
+  int64_t b_stride;
+  const E *Cm;  // [rows, P, M]
+  int64_t c_stride;
+  const E *Dm;  // [rows, P, F]; nullptr: no feedthrough
+  int64_t d_stride;
+  int F, P;
+  uint64_t f_magic, p_magic;  // ceil(2^32 / F), ceil(2^32 / P): e / F = (e * f_magic) >> 32 for small e
+  const E *zi;  // [B, M]; nullptr: zeros
+  const E *x;   // [B, T, F]
+  E *y;         // [B, T, P]
+  E *zf;        // [B, M]; nullable (the state after the last step scanned)
+  int64_t B, T_len, tiles_per_row;
+  uint64_t b_magic;  // tile id -> row by multiply and shift (row_split)
+  unsigned b_shift;
+  unsigned long long *claims;
+  unsigned tiles, per_stripe, spin_limit;
+  unsigned agg_only;  // testing: tiles after a row's first publish no inclusive state
+  uint64_t *status;
+};
+
+// 3 data waves and a look-back wave; a lane owns K consecutive steps (32
+// bytes of one feature), a wave 64 K steps.  LDS per data wave: kMimoMaxIO
+// input planes and kMimoMaxIO output planes of 64 K elements, each padded by
+// 16 bytes so that the lanes of a staging instruction, which write
+// consecutive elements of different planes, spread over the banks.
+template <class Alg>
+struct MimoShape {
+  using E = typename Alg::elem;
+  static constexpr int kWaves = 3;
+  static constexpr int kThreads = 64 * (kWaves + 1);
+  static constexpr int K = 32 / int(sizeof(E));
+  static constexpr int kSpan = 64 * K;
+  static constexpr int kTile = kWaves * kSpan;
+  static constexpr int kPlane = kSpan + 16 / int(sizeof(E));
+  static constexpr int kWaveElems = 2 * kMimoMaxIO * kPlane;
+};
+
+// The model of row b in two halves, each loaded where it is first needed
+// (a half that lives across the wave scan holds registers the scan's maps
+// want): the input side, A and the columns of B as state vectors; the output
+// side, the rows of C as state vectors and D by element.  Zero past F and P,
+// so that every step runs the same arithmetic whatever the widths.
+template <class Alg>
+struct MimoIn {
+  typename Alg::s_coef A;
+  typename Alg::s_state b[kMimoMaxIO];
+};
+template <class Alg>
+struct MimoOut {
+  using E = typename Alg::elem;
+  typename Alg::s_state c[kMimoMaxIO];
+  E d[kMimoMaxIO][kMimoMaxIO];
+};
+
+template <class Alg>
+__device__ __forceinline__ MimoIn<Alg> mimo_in(const MimoArgs<Alg> &a, int64_t row) {
+  using E = typename Alg::elem;
+  using V = SsView<Alg>;
+  constexpr int M = V::M;
+  MimoIn<Alg> m;
+  m.A = V::load_mat(a.A + row * a.A_stride);
+  const E *bp = a.Bm + row * a.b_stride;
+#pragma unroll
+  for (int j = 0; j < kMimoMaxIO; ++j) {
+    union {
+      typename Alg::s_state s;
+      E e[M];
+    } u;
+#pragma unroll
+    for (int i = 0; i < M; ++i) u.e[i] = j < a.F ? bp[i * a.F + j] : E(0);
+    m.b[j] = u.s;
+  }
+  return m;
+}
+
+template <class Alg>
+__device__ __forceinline__ MimoOut<Alg> mimo_out(const MimoArgs<Alg> &a, int64_t row) {
+  using E = typename Alg::elem;
+  using V = SsView<Alg>;
+  constexpr int M = V::M;
+  MimoOut<Alg> m;
+  const E *cp = a.Cm + row * a.c_stride;
+  const E *dp = a.Dm ? a.Dm + row * a.d_stride : nullptr;
+#pragma unroll
+  for (int j = 0; j < kMimoMaxIO; ++j) {
+    union {
+      typename Alg::s_state s;
+      E e[M];
+    } u;
+#pragma unroll
+    for (int i = 0; i < M; ++i) u.e[i] = j < a.P ? cp[j * M + i] : E(0);
+    m.c[j] = u.s;
+#pragma unroll
+    for (int f = 0; f < kMimoMaxIO; ++f) m.d[j][f] = (dp && j < a.P && f < a.F) ? dp[j * a.F + f] : E(0);
+  }
+  return m;
+}
+
+// B u for one step's inputs u (zero past F)
+template <class Alg>
+__device__ __forceinline__ typename Alg::s_state mimo_bx(const MimoIn<Alg> &m, const typename Alg::elem (&u)[kMimoMaxIO]) {
+  using E = typename Alg::elem;
+  constexpr int M = SsView<Alg>::M;
+  union {
+    typename Alg::s_state s;
+    E e[M];
+  } o, ub;
+#pragma unroll
+  for (int i = 0; i < M; ++i) o.e[i] = E(0);
+#pragma unroll
+  for (int f = 0; f < kMimoMaxIO; ++f) {
+    ub.s = m.b[f];
+#pragma unroll
+    for (int i = 0; i < M; ++i) o.e[i] = fma(ub.e[i], u[f], o.e[i]);
+  }
+  return o.s;
+}
+
+// A lane's K steps (A, B x[k]) folded into one map in compute precision:
+// the matrix part is A^K for every lane (AK, from squarings of A), the
+// vector part sum_k A^(K-1-k) B x[k] by Horner's rule.  Folding in storage
+// precision instead (as a time-varying scan must) let float32 rounding in
+// the lane maps of a model with a large transient gain reach 3e-4 of the
+// output's range, ten times a sequential float32 loop's error; from an
+// exact entry state, pass 2's K float32 steps add only a few ulps.
+template <class Alg, int K>
+__device__ __forceinline__ Map<Alg> mimo_lane_map(const typename Alg::coef &A, const typename Alg::coef &AK,
+                                                  const typename Alg::s_state (&X)[K]) {
+  Map<Alg> m;
+  m.A = AK;
+  m.x = Alg::load_s(X[0]);
+#pragma unroll
+  for (int k = 1; k < K; ++k) m.x = Alg::affine(A, m.x, Alg::load_s(X[k]));
+  return m;
+}
+
+// A^K for K a power of two, in compute precision.
+template <class Alg, int K>
+__device__ __forceinline__ typename Alg::coef mimo_pow(const typename Alg::coef &A) {
+  static_assert((K & (K - 1)) == 0, "K must be a power of two");
+  typename Alg::coef p = A;
+#pragma unroll
+  for (int n = 1; n < K; n *= 2) p = Alg::cmul(p, p);
+  return p;
+}
+
+// The elements [lo, hi) of a block of `len` elements starting at element
+// `base` of a row of `lim` elements that lie inside the row (clamped to
+// [0, len]; lo >= hi when none do).  One bounds test per element serves
+// every span: a separate unchecked path for whole spans made the compiler
+// keep both paths' loads live (2.9 KB of scratch per lane).
+__device__ __forceinline__ void mimo_block_range(int64_t base, int64_t lim, int len, int &lo, int &hi) {
+  const int64_t l = base < 0 ? -base : 0, h = lim - base;
+  lo = int(l < len ? l : len);
+  hi = int(h < 0 ? 0 : (h < len ? h : len));
+}
+
+// Stages a wave's span of one [T, W] row block into W LDS planes: plane j
+// holds feature j of the span's 64 K steps in scan order (forward: scan
+// position s0 + s is time s0 + s; REV: time T-1-s0-s).  Steps outside the
+// row read 0.  The global side is the span's contiguous block of 64 K W
+// elements, lane-strided (element e = i 64 + lane is step e / W, feature
+// e % W of the block).
+template <class Alg, bool REV>
+__device__ __forceinline__ void mimo_stage_in(const typename Alg::elem *row, int64_t s0, int64_t T, int W,
+                                              uint64_t w_magic, typename Alg::elem *lds, int lane) {
+  using E = typename Alg::elem;
+  using Sh = MimoShape<Alg>;
+  constexpr int S = Sh::kSpan, K = Sh::K, kMax = K * kMimoMaxIO;
+  // the block starts at element `base` of the row (negative or past the row
+  // for the spans that leave it); its elements [lo, hi) lie inside the row
+  const int64_t base = (REV ? T - s0 - S : s0) * W;
+  const int n = K * W;  // elements per lane
+  int lo, hi;
+  mimo_block_range(base, T * W, S * W, lo, hi);
+  E v[kMax];
+#pragma unroll
+  for (int i = 0; i < kMax; ++i) {
+    const int e = i * 64 + lane;
+    v[i] = E(0);
+    if (i < n && e >= lo && e < hi) v[i] = row[base + e];
+  }
+#pragma unroll
+  for (int i = 0; i < kMax; ++i) {
+    if (i < n) {
+      const unsigned e = unsigned(i * 64 + lane);
+      const unsigned s = unsigned((uint64_t(e) * w_magic) >> 32);
+      const unsigned j = e - s * unsigned(W);
+      lds[j * Sh::kPlane + (REV ? S - 1 - int(s) : int(s))] = v[i];
+    }
+  }
+}
+
+// The inverse of mimo_stage_in for a wave's outputs: W planes out to the
+// span's block of the [T, W] row; steps outside the row are not written.
+template <class Alg, bool REV>
+__device__ __forceinline__ void mimo_stage_out(typename Alg::elem *row, int64_t s0, int64_t T, int W,
+                                               uint64_t w_magic, const typename Alg::elem *lds, int lane) {
+  using E = typename Alg::elem;
+  using Sh = MimoShape<Alg>;
+  constexpr int S = Sh::kSpan, K = Sh::K, kMax = K * kMimoMaxIO;
+  const int64_t base = (REV ? T - s0 - S : s0) * W;
+  const int n = K * W;
+  int lo, hi;
+  mimo_block_range(base, T * W, S * W, lo, hi);
+  E v[kMax];
+#pragma unroll
+  for (int i = 0; i < kMax; ++i) {
+    if (i < n) {
+      const unsigned e = unsigned(i * 64 + lane);
+      const unsigned s = unsigned((uint64_t(e) * w_magic) >> 32);
+      const unsigned j = e - s * unsigned(W);
+      v[i] = lds[j * Sh::kPlane + (REV ? S - 1 - int(s) : int(s))];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kMax; ++i) {
+    const int e = i * 64 + lane;
+    if (i < n && e >= lo && e < hi) row[base + e] = v[i];
+  }
+}
+
+// Time of scan position s in a row of T steps.
+template <bool REV>
+__device__ __forceinline__ int64_t mimo_time(int64_t s, int64_t T) {
+  return REV ? T - 1 - s : s;
+}
+
+// State entering tile position `span` of a row, folded from the inputs (the
+// look-back's bounded-wait fallback; out of line, cold): 64 K steps at a
+// time, each lane reading its K steps' features straight from the row.
+template <class Alg, bool REV>
+__device__ __noinline__ typename Alg::state mimo_prefix_fallback(const MimoArgs<Alg> *ap, int64_t b, int64_t span,
+                                                                int lane, typename Alg::state virt) {
+  const MimoArgs<Alg> &a = *ap;
+  using E = typename Alg::elem;
+  using SC = typename Alg::s_coef;
+  using SS = typename Alg::s_state;
+  using M = Map<Alg>;
+  constexpr int K = MimoShape<Alg>::K;
+  auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
+  const MimoIn<Alg> mdl = mimo_in<Alg>(a, b);
+  const E *xrow = a.x + b * a.T_len * a.F;
+  const typename Alg::coef Ac = Alg::load_c(mdl.A), AK = mimo_pow<Alg, K>(Ac);
+  M acc = map_identity<Alg>();
+  for (int64_t off = 0; off < span; off += 64 * K) {
+    SS xs[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int64_t s = off + int64_t(lane) * K + k;
+      E u[kMimoMaxIO];
+#pragma unroll
+      for (int f = 0; f < kMimoMaxIO; ++f) {
+        u[f] = E(0);
+        if (f < a.F && s < a.T_len) u[f] = xrow[mimo_time<REV>(s, a.T_len) * a.F + f];
+      }
+      xs[k] = mimo_bx<Alg>(mdl, u);
+    }
+    M m = mimo_lane_map<Alg, K>(Ac, AK, xs);
+    m = wave_scan_incl(m, lane, op);
+    acc = compose<Alg>(acc, read_lane(m, 63));
+  }
+  return apply<Alg>(acc, virt);
+}
+
+template <class Alg, bool REV>
+__global__ __launch_bounds__(MimoShape<Alg>::kThreads, 2) void mimo_ss_kernel(MimoArgs<Alg> a) {
+  using E = typename Alg::elem;
+  using S = typename Alg::state;
+  using SC = typename Alg::s_coef;
+  using SS = typename Alg::s_state;
+  using M = Map<Alg>;
+  using V = SsView<Alg>;
+  using Sh = MimoShape<Alg>;
+  using St = StatusShape<Alg>;
+  constexpr int K = Sh::K, kWaves = Sh::kWaves, kP = Sh::kPlane;
+
+  __shared__ M s_wagg[kWaves];
+  __shared__ M s_wpre[kWaves];
+  __shared__ S s_in;
+  __shared__ unsigned s_id, s_tag;
+  __shared__ uint64_t s_look[St::kLookWords];
+  __shared__ E s_io[kWaves * Sh::kWaveElems];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the tile is the workgroup's index; the look-back wave claims for the
+  // call's tag (claim_tag), so the data waves' loads do not wait for it
+  const int64_t id = blockIdx.x;
+  if (id >= a.tiles) {  // padding of the last stripe round: counted, then gone
+    if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
+    return;
+  }
+  unsigned tag = 0;
+  int64_t q, b;  // tile position along the row, row
+  split_tile(id, a.B, a.b_magic, a.b_shift, q, b);
+  const int64_t T = a.T_len;
+  auto op = [](const M &p, const M &q2) { return compose<Alg>(p, q2); };
+
+  if (w == kWaves) {
+    // ================= look-back wave
+    tag = claim_tag(a.claims, a.per_stripe, lane);
+    uint64_t *row_status = a.status + b * a.tiles_per_row * St::kStride;
+    const S virt = a.zi ? Alg::load_s(V::load_vec(a.zi + b * V::M)) : Alg::szero();
+    __syncthreads();  // wave aggregates are in s_wagg
+    M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
+    v = wave_scan_incl(v, lane, op);
+    const M wex = wave_shift_up(v, lane, map_identity<Alg>());
+    if (lane < kWaves) s_wpre[lane] = wex;
+    const M tagg = read_lane(v, kWaves - 1);
+    S yin = virt;
+    if (q > 0) {
+      if (lane == 0) publish(row_status + q * St::kStride + St::kIncWords, tagg, tag);
+      Lookback<Alg> lb = lookback_start<Alg>(q);
+      if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
+        yin = mimo_prefix_fallback<Alg, REV>(kernel_args<MimoArgs<Alg>>(), b, q * Sh::kTile, lane, virt);
+    }
+    if (q + 1 < a.tiles_per_row && lane == 0 && !(a.agg_only && q > 0))
+      publish(row_status + q * St::kStride, apply<Alg>(tagg, yin), tag);
+    if (lane == 0) s_in = yin;
+    __syncthreads();  // entry state is in s_in
+    return;
+  }
+
+  // ================= data waves
+  E *xin = s_io + w * Sh::kWaveElems;  // F input planes
+  E *yout = xin + kMimoMaxIO * kP;     // P output planes
+  const int64_t s0 = q * Sh::kTile + int64_t(w) * Sh::kSpan;  // the wave's first scan position
+  mimo_stage_in<Alg, REV>(a.x + b * T * a.F, s0, T, a.F, a.f_magic, xin, lane);
+  const MimoIn<Alg> mi = mimo_in<Alg>(a, b);
+  wave_sync();  // the span's inputs are in the planes
+
+  // one step's inputs from the planes (zero past F)
+  auto inputs = [&](int k, E (&u)[kMimoMaxIO]) {
+#pragma unroll
+    for (int f = 0; f < kMimoMaxIO; ++f) u[f] = f < a.F ? xin[f * kP + lane * K + k] : E(0);
+  };
+
+  // ---- pass 1: the lane map of (A, B x[t]) over its K steps, the wave scan.
+  // Steps past the row's end carry a zero input and only touch the
+  // aggregate of its last tile, which nobody reads.
+  M m;
+  {
+    SS X[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      E u[kMimoMaxIO];
+      inputs(k, u);
+      X[k] = mimo_bx<Alg>(mi, u);
+    }
+    const typename Alg::coef Ac = Alg::load_c(mi.A);
+    m = mimo_lane_map<Alg, K>(Ac, mimo_pow<Alg, K>(Ac), X);
+  }
+  m = wave_scan_incl(m, lane, op);
+  const M ex = wave_shift_up(m, lane, map_identity<Alg>());
+  if (lane == 63) s_wagg[w] = m;
+  __syncthreads();  // wave aggregates are in s_wagg
+  __syncthreads();  // entry state is in s_in
+  SS h = Alg::store_s(apply<Alg>(ex, apply<Alg>(s_wpre[w], s_in)));
+
+  // ---- pass 2: y = C h + D x, then the step (B x again from the planes:
+  // keeping the K products from pass 1 held their registers across the scan)
+  const MimoOut<Alg> mo = mimo_out<Alg>(a, b);
+  const int64_t l0 = s0 + int64_t(lane) * K;  // the lane's first scan position
+  const bool has_d = a.Dm != nullptr;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    E u[kMimoMaxIO];
+    inputs(k, u);
+#pragma unroll
+    for (int p = 0; p < kMimoMaxIO; ++p) {
+      if (p < a.P) {
+        E o = V::dot(mo.c[p], h);
+        if (has_d) {
+#pragma unroll
+          for (int f = 0; f < kMimoMaxIO; ++f) o = fma(mo.d[p][f], u[f], o);
+        }
+        yout[p * kP + lane * K + k] = o;
+      }
+    }
+    h = Alg::s_affine(mi.A, h, mimo_bx<Alg>(mi, u));
+    if (a.zf && l0 + k == T - 1) {
+      union {
+        SS s;
+        E e[V::M];
+      } zu;
+      zu.s = h;
+#pragma unroll
+      for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = zu.e[i];
+    }
+  }
+  wave_sync();  // the span's outputs are in the planes
+  mimo_stage_out<Alg, REV>(a.y + b * T * a.P, s0, T, a.P, a.p_magic, yout, lane);
+}
+
+}  // namespace phs

@@ -257,6 +257,136 @@ def _fused_ss_applies(A: Tensor, x: Tensor, B, C, D, zi, unroll_factor, out_idx)
     return all(t is None or fwad.unpack_dual(t).tangent is None for t in (A, B, C, D, zi, x))
 
 
+def _mimo_operands(A: Tensor, x: Tensor, B, C, D, out_idx, batch: int, M: int):
+    """The per-row matrices of philtorch::mimo_ss for a call of state_space,
+    or None where the shapes fall outside it: ``(x3, Bm, Cm, Dm, vec)`` with
+    x3 (batch, N, F), Bm (M, F) or (batch, M, F), Cm (P, M) or
+    (batch, P, M), Dm None, (P, F) or (batch, P, F), and ``vec`` true where
+    the reference's y is 2D (one output: C an M-vector or out_idx, D a
+    feature vector or one value per row; y is then mimo_ss's squeezed).
+
+    Each case mirrors a branch of the composed route (B:
+    philtorch/lti/ssm.py:460-485; C and D: _ssm_C_D :513-589), tested in the
+    same order, so the fused call reads every operand as the composed one
+    does; B, C, D enter through views or products that autograd carries
+    back to them.  A sum of a 2D and a 3D term (which the reference
+    broadcasts) and shapes the composed route rejects stay with it."""
+    two_d = x.dim() == 2
+    Fn = 1 if two_d else x.size(-1)
+    features = -1 if two_d else Fn
+    eye = lambda n: torch.eye(n, dtype=x.dtype, device=x.device)  # noqa: E731
+    if B is None:
+        if two_d or Fn != M:
+            return None
+        Bm = eye(M)
+    else:
+        shape = tuple(B.shape)
+        if shape == (M,):
+            if not two_d:
+                return None
+            Bm = B.reshape(M, 1)
+        elif len(shape) == 2 and shape == (batch, M) and two_d:
+            Bm = B.reshape(batch, M, 1)
+        elif len(shape) == 2 and shape == (M, features):
+            Bm = B
+        elif len(shape) == 3 and shape == (batch, M, features):
+            Bm = B
+        else:
+            return None
+    if C is None:
+        if out_idx is None:
+            Cm, c_vec = eye(M), False
+        else:
+            Cm, c_vec = eye(M)[out_idx].reshape(1, M), True
+    else:
+        shape = tuple(C.shape)
+        if shape == (M,):
+            Cm, c_vec = C.reshape(1, M), True
+        elif len(shape) == 2 and shape == (batch, M):
+            Cm, c_vec = C.reshape(batch, 1, M), True
+        elif len(shape) == 2 and shape[1] == M:
+            Cm, c_vec = C, False
+        elif len(shape) == 3 and shape[0] == batch and shape[2] == M:
+            Cm, c_vec = C, False
+        else:
+            return None
+    Dm, d_vec = None, None
+    if D is not None:
+        shape = tuple(D.shape)
+        if len(shape) == 1 and shape[0] == features:
+            Dm, d_vec = D.reshape(1, Fn), True
+        elif len(shape) == 1 and shape[0] == batch:
+            if not two_d:
+                return None
+            Dm, d_vec = D.reshape(batch, 1, 1), True
+        elif shape in ((), (1,)):
+            if two_d:
+                Dm, d_vec = D.reshape(1, 1), True
+            else:
+                Dm, d_vec = D.reshape(()) * eye(Fn), False
+        elif len(shape) == 1:
+            if not two_d:
+                return None
+            Dm, d_vec = D.reshape(shape[0], 1), False
+        elif len(shape) == 2 and shape == (batch, features):
+            Dm, d_vec = D.reshape(batch, 1, Fn), True
+        elif len(shape) == 2 and shape[0] == batch:
+            if not two_d:
+                return None
+            Dm, d_vec = D.reshape(batch, shape[1], 1), False
+        elif len(shape) == 2 and shape[1] == features:
+            Dm, d_vec = D, False
+        elif len(shape) == 3 and shape[0] == batch and shape[2] == features:
+            Dm, d_vec = D, False
+        else:
+            return None
+        if d_vec != c_vec or Dm.size(-2) != Cm.size(-2):
+            return None
+    x3 = x.unsqueeze(-1) if two_d else x
+    return x3, Bm, Cm, Dm, c_vec
+
+
+def _mimo_applies(A: Tensor, x: Tensor, B, C, D, zi, unroll_factor) -> bool:
+    """Whether a call outside the single-input single-output fused path can
+    take philtorch::mimo_ss: order <= 4, float32 or float64 on a HIP device,
+    the native route requested (``unroll_factor=1``), no forward-mode
+    tangent (those keep the composed route); the widths are checked on the
+    operands _mimo_operands builds."""
+    from .. import EXTENSION_LOADED
+
+    if not (EXTENSION_LOADED and x.is_cuda and unroll_factor == 1 and x.dim() in (2, 3)):
+        return False
+    if not hasattr(torch.ops.philtorch, "mimo_ss"):
+        return False
+    if A.size(-1) > 4 or x.dtype not in (torch.float32, torch.float64):
+        return False
+    if any(t is not None and t.dtype != x.dtype for t in (A, B, C, D, zi)):
+        return False
+    import torch.autograd.forward_ad as fwad
+
+    return all(t is None or fwad.unpack_dual(t).tangent is None for t in (A, B, C, D, zi, x))
+
+
+def _mimo_composite(A, Bm, Cm, Dm, zi, x, reverse=False):
+    """(y, zf) of the composed route for philtorch::mimo_ss's operands (B x,
+    the native scan, the shifted state sequence, C h + D x, in time-reversed
+    order with ``reverse``): its autograd formula differentiates this under
+    create_graph."""
+    if reverse:
+        y, zf = _mimo_composite(A, Bm, Cm, Dm, zi, x.flip(1))
+        return y.flip(1), zf
+    M = A.size(-1)
+    zi = x.new_zeros(x.size(0), M) if zi is None else zi
+    Bx = torch.matmul(x, Bm.mT)  # (batch, N, M)
+    h = _ext_ss_recur(A, zi, Bx)
+    zf = h[:, -1] if h.size(1) > 0 else zi
+    h = torch.cat([zi.unsqueeze(1), h[:, :-1]], dim=1)
+    y = torch.matmul(h, Cm.mT)
+    if Dm is not None:
+        y = y + torch.matmul(x, Dm.mT)
+    return y, zf
+
+
 def _state_space_composite(A, B, C, D, zi, x, out_idx=None):
     """(y, zf) of the composed route (B x, the native scan, the shifted state
     sequence, C h + D x) for what philtorch::lti_ss computes fused: its
@@ -280,8 +410,10 @@ def state_space(
     Mirrors philtorch/lti/ssm.py:386-510; returns ``(y, zf)`` when ``zi`` is
     given.  ``unroll_factor=None`` means ``round(sqrt(N))`` (blocked PyTorch
     route) as in the reference; ``unroll_factor=1`` on a HIP device runs the
-    native scan, and a single-input single-output model of order <= 4 the
-    fused philtorch::lti_ss.
+    native scan, a single-input single-output model of order <= 4 the fused
+    philtorch::lti_ss, and other models of order <= 4 with at most four
+    inputs and outputs per step (a 3D x, matrix-valued B, C, D) the fused
+    philtorch::mimo_ss.
     """
     return _state_space(A, x, B, C, D, zi, unroll_factor, out_idx, fused=True)
 
@@ -309,6 +441,16 @@ def _state_space(A, x, B, C, D, zi, unroll_factor, out_idx, fused):
         with _op_ctx(A, B, C, D, zi, x):
             y, zf = torch.ops.philtorch.lti_ss(A, B, C, D, zi.contiguous() if return_zf else None, x,
                                                out_idx if C is None else 0)
+        return (y, zf) if return_zf else y
+    ops = _mimo_operands(A, x, B, C, D, out_idx, batch, M) if fused and _mimo_applies(
+        A, x, B, C, D, zi, unroll_factor) else None
+    if ops is not None and ops[0].size(-1) <= 4 and ops[2].size(-2) <= 4:
+        from .. import _op_ctx
+
+        x3, Bm, Cm, Dm, vec = ops
+        with _op_ctx(A, Bm, Cm, Dm, zi, x3):
+            y, zf = torch.ops.philtorch.mimo_ss(A, Bm, Cm, Dm, zi.contiguous() if return_zf else None, x3)
+        y = y.squeeze(-1) if vec else y
         return (y, zf) if return_zf else y
     features = -1 if x.dim() == 2 else x.size(-1)
     if B is not None:

@@ -16,6 +16,7 @@ HEADER = os.path.join(REPO, "include", "philscan.h")
 
 PHS_OK, PHS_ERR_INVALID, PHS_ERR_WORKSPACE, PHS_ERR_LAUNCH, PHS_ERR_DTYPE, PHS_ERR_TOO_LARGE = range(6)
 PHS_LPV_A_SHARED, PHS_LPV_A_TRANSPOSED = 1, 2
+PHS_MIMO_A_SHARED, PHS_MIMO_B_SHARED, PHS_MIMO_C_SHARED, PHS_MIMO_D_SHARED = 1, 2, 4, 8
 # phs_padmode codes (torch.nn.functional.pad modes)
 PADMODES = {"constant": 0, "replicate": 1, "reflect": 2, "circular": 3}
 OPS = {"recur": 0, "lti_recur": 1, "recur2": 2, "lti_recur2": 3}
@@ -145,4 +146,11 @@ def load() -> ctypes.CDLL:
     for rev, fwd in (("phs_lti_ss_rev", "phs_lti_ss_fwd"), ("phs_lfilter_rev", "phs_lfilter_fwd")):
         getattr(lib, rev).argtypes = getattr(lib, fwd).argtypes
         getattr(lib, rev).restype = ctypes.c_int
+    lib.phs_mimo_ss_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int, i64, i64]
+    lib.phs_mimo_ss_workspace_size.restype = ctypes.c_size_t
+    ci = ctypes.c_int
+    for name in ("phs_mimo_ss_fwd", "phs_mimo_ss_rev"):
+        getattr(lib, name).argtypes = [ci, ci, ci, ci, i64, i64, vp, vp, vp, vp, ci, vp, vp, vp, vp, vp,
+                                       ctypes.c_size_t, vp]
+        getattr(lib, name).restype = ci
     return lib

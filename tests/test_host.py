@@ -414,3 +414,90 @@ def test_lpv_row_scratch_bytes_counts_shared_time_varying_operands():
     d_step = meta(1, T)
     assert ssm._lpv_row_scratch_bytes(meta(B, T, M, M), b_step, b_row, d_step, x, need) == B * T * (M + 1) * 4
     assert ssm._lpv_row_scratch_bytes(meta(B, T, M, M), meta(B, T, M), None, meta(1, 1), x, need) == 0
+
+
+def test_capi_mimo_state_space_host_only_calls():
+    """Sizes and argument errors of the multi-input multi-output state space
+    (nothing launches; an empty batch returns at once)."""
+    lib = capi.load()
+    for dt in (0, 1):
+        for M in (1, 2, 3, 4):
+            assert lib.phs_mimo_ss_workspace_size(dt, M, 16, 480000) > 0
+    for bad in ((2, 2, 16, 100), (0, 5, 16, 100), (0, 0, 16, 100), (0, 2, -1, 100)):
+        assert lib.phs_mimo_ss_workspace_size(*bad) == 0
+    d = ctypes.c_void_p(16)
+    ws = 1 << 30
+
+    def mimo(dt=0, M=2, F=2, P=3, B=2, shared=0, a=d, wsb=ws):
+        return lib.phs_mimo_ss_fwd(dt, M, F, P, B, 100, a, d, d, None, shared, None, d, d, None, d, wsb, None)
+
+    assert mimo(dt=2) == capi.PHS_ERR_DTYPE
+    for bad in (dict(M=5), dict(M=0), dict(F=0), dict(F=5), dict(P=0), dict(P=5), dict(B=-1), dict(shared=16),
+                dict(a=None)):
+        assert mimo(**bad) == capi.PHS_ERR_INVALID, bad
+    assert mimo(wsb=lib.phs_mimo_ss_workspace_size(0, 2, 2, 100) - 1) == capi.PHS_ERR_WORKSPACE
+    assert mimo(B=0) == capi.PHS_OK
+
+
+def _mimo_shape_cases(batch, M):
+    """(x features or None for 2D x, B, C, D, out_idx) of every branch of the
+    reference's B, C and D shape rules that the fused multi-output route
+    takes (philtorch/lti/ssm.py:460-485, 513-589)."""
+    F, P = 3, 2
+    return [
+        (F, (M, F), (P, M), (P, F), None),
+        (F, (batch, M, F), (batch, P, M), (batch, P, F), None),
+        (F, (M, F), (M,), (F,), None),
+        (F, (M, F), (batch, M), (batch, F), None),
+        (F, (M, F), None, (F,), 1),
+        (F, (M, F), (F, M), (), None),
+        (M, None, None, None, None),
+        (M, None, (P, M), None, None),
+        (None, (M,), (P, M), (P,), None),
+        (None, (batch, M), (batch, P, M), (batch, P), None),
+        (None, (M,), (P, M), None, None),
+        (None, (batch, M), None, None, None),
+    ]
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_mimo_operands_reproduce_composed_route(case):
+    """Each shape case's per-row matrices (lti.ssm._mimo_operands) run through
+    the composite of mimo_ss (B x, the scan, the shift, C h + D x) give the
+    composed route's y and zf on CPU, for every branch of the reference's
+    shape rules the fused route takes."""
+    from philtorch_amd.lti import ssm
+
+    batch, N, M = 4, 40, 3  # (batch != M != F: no shape reads two ways)
+    F, bs, cs, ds, out_idx = _mimo_shape_cases(batch, M)[case]
+    g = torch.Generator().manual_seed(1000 + case)
+    rnd = lambda *s: torch.randn(tuple(s), generator=g, dtype=torch.float64)  # noqa: E731
+    A = 0.4 * rnd(M, M)
+    x = rnd(batch, N) if F is None else rnd(batch, N, F)
+    B = None if bs is None else rnd(*bs)
+    C = None if cs is None else rnd(*cs)
+    D = None if ds is None else rnd(*ds)
+    zi = rnd(batch, M)
+    ops = ssm._mimo_operands(A, x, B, C, D, out_idx, batch, M)
+    assert ops is not None
+    x3, Bm, Cm, Dm, vec = ops
+    y, zf = ssm._mimo_composite(A, Bm, Cm, Dm, zi, x3)
+    y = y.squeeze(-1) if vec else y
+    ref, rzf = ssm._state_space(A, x, B, C, D, zi, 1, out_idx, fused=False)
+    assert y.shape == ref.shape
+    torch.testing.assert_close(y, ref, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(zf, rzf, rtol=1e-12, atol=1e-12)
+
+
+def test_mimo_operands_leave_mixed_and_rejected_shapes():
+    """Shapes whose reference result broadcasts a one-output term against a
+    multi-output one, or that the reference rejects, get no fused operands."""
+    from philtorch_amd.lti import ssm
+
+    batch, N, M, F = 4, 10, 2, 3
+    A, x = torch.eye(M), torch.randn(batch, N, F)
+    assert ssm._mimo_operands(A, x, torch.randn(M, F), torch.randn(M), torch.randn(2, F), None, batch, M) is None
+    assert ssm._mimo_operands(A, x, torch.randn(M, F), torch.randn(2, M), torch.randn(F), None, batch, M) is None
+    assert ssm._mimo_operands(A, x, torch.randn(M), torch.randn(M), None, None, batch, M) is None
+    assert ssm._mimo_operands(A, x, None, torch.randn(M), None, None, batch, M) is None  # B None needs F == M
+    assert ssm._mimo_operands(A, x, torch.randn(M, F), torch.randn(M), torch.randn(batch), None, batch, M) is None

@@ -468,6 +468,50 @@ def test_lti_state_space_matches_scipy_dlsim(M):
         D.check(y2[r], ry[:, 0], f"out_idx row {r}")
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("F,P", [(1, 1), (2, 3), (4, 4), (3, 1)])
+def test_lti_state_space_mimo_matches_scipy_dlsim(M, F, P):
+    """oracle.lti_state_space_mimo (B x per step, lti_recurN, shift, C h + D x)
+    against scipy.signal.dlsim's multi-input multi-output simulation, per row,
+    with per-row and shared operands and initial states: a transposed B, C or
+    D, or a state shift off by one, fails it."""
+    g = D.rng(D.seed_of("oracle-ss-mimo", M, F, P))
+    Bn, T = 3, 300
+    A, _, _, _ = _stable_model(g, M, (Bn,))
+    Bm, Cm, Dm = g.standard_normal((Bn, M, F)), g.standard_normal((P, M)), g.standard_normal((Bn, P, F))
+    x = g.standard_normal((Bn, T, F))
+    zi = g.standard_normal((Bn, M))
+    y, zf = oracle.lti_state_space_mimo(A, x, Bm, Cm, Dm, zi)
+    assert y.shape == (Bn, T, P) and zf.shape == (Bn, M)
+    for r in range(Bn):
+        _, ry, rx = scipy.signal.dlsim((A[r], Bm[r], Cm, Dm[r], 1), x[r], x0=zi[r])
+        D.check(y[r], ry.reshape(T, P), f"y row {r}")
+        D.check(zf[r], A[r] @ rx[-1] + Bm[r] @ x[r, -1], f"zf row {r}", scale=np.max(np.abs(ry)))
+    # shared A and B, no D, no zi: the zero-state response
+    y2, _ = oracle.lti_state_space_mimo(A[0], x, Bm[0], Cm)
+    for r in range(Bn):
+        _, ry, _ = scipy.signal.dlsim((A[0], Bm[0], Cm, np.zeros((P, F)), 1), x[r])
+        D.check(y2[r], ry.reshape(T, P), f"shared row {r}")
+
+
+def test_lti_state_space_mimo_reduces_to_siso():
+    """With one input and one output the matrix form is the single-input
+    single-output oracle (pinned to dlsim above) on the same operands; and an
+    empty row returns zi as its final state."""
+    g = D.rng(D.seed_of("oracle-ss-mimo-siso"))
+    Bn, T, M = 2, 90, 3
+    A, Bv, Cv, Dv = _stable_model(g, M, (Bn,))
+    x = g.standard_normal((Bn, T))
+    zi = g.standard_normal((Bn, M))
+    y1, zf1 = oracle.lti_state_space(A, x, Bv, Cv, Dv, zi)
+    y2, zf2 = oracle.lti_state_space_mimo(A, x[..., None], Bv[..., None], Cv[:, None, :], Dv[:, None, None], zi)
+    np.testing.assert_allclose(y2[..., 0], y1, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(zf2, zf1, rtol=1e-12, atol=1e-12)
+    y0, zf0 = oracle.lti_state_space_mimo(A, np.zeros((Bn, 0, 2)), np.ones((M, 2)), np.ones((1, M)), None, zi)
+    assert y0.shape == (Bn, 0, 1)
+    np.testing.assert_array_equal(zf0, zi)
+
+
 # ---------------------------------------------------------------- LPV SISO state space
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_lpv_state_space_matches_loop_and_lti(M):
