@@ -25,7 +25,10 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c4_filtfilt_coef  the same plus the gradients w.r.t. x, b and a (its coefficient mode)
   c4_lfilter4  4 x lti.lfilter of order 4 (tdf2), forward only (philtorch::lti_ss)
   c4_lfilter4_grad  the same plus gradients w.r.t. x, b and a (philtorch::lfilter_ss_backward)
---composed runs an API config (c3_lpv_ss*, c4_api, c4_lfilter*, c4_filtfilt*)
+  c4_mimo  lti.state_space of order 4, 2 inputs and 2 outputs per step (philtorch::mimo_ss)
+  c4_mimo_grad  the same plus gradients w.r.t. x and zi (the adjoint mimo_ss pass)
+  c4_mimo_coef  the same plus gradients w.r.t. A, B, C, D (two states passes and GEMM sums)
+--composed runs an API config (c3_lpv_ss*, c4_api, c4_lfilter*, c4_filtfilt*, c4_mimo*)
 through the reference's composed route instead of the fused kernels, for the
 comparison.
 Before every step a 512 MiB buffer is read end to end so the 256 MB Infinity
@@ -758,6 +761,140 @@ class LpvSsCoefGrad(LpvSsGrad):
     cpu_step = None  # the oracle restates no coefficient gradients of the LPV state space
 
 
+class MimoSsApi(Workload):
+    """c4_mimo: a two-channel LTI state space on the C4 shape (16 rows of
+    480000 steps, fp32): per row an order-4 model (A block-diagonal of the
+    TDF-II companion matrices of the row's first two C4 biquads), two inputs
+    and two outputs per step, B (4, 2), C (2, 4), D (2, 2) shared by the
+    rows, ``lti.state_space(A, x, B, C, D, zi=zi, unroll_factor=1)`` on
+    x (16, 480000, 2).  Runs philtorch::mimo_ss: B x, the scan, the state
+    shift and C h + D x in one pass; forward only."""
+
+    def __init__(self):
+        import torch
+
+        B, T, M, F, P = 16, 480000, 4, 2, 2
+        self.name, self.B, self.T, self.M, self.F, self.P = "c4_mimo", B, T, M, F, P
+        self.kernel = "mimo_ss_kernel"
+        self.metric = (f"GSamples/s fwd, lti.state_space order {M}, {F} inputs, {P} outputs per step "
+                       f"B={B} T={T} fp32 (API)")
+        g = torch.Generator().manual_seed(45)
+        r = torch.rand(B, 2, generator=g, dtype=torch.float64) * 0.48 + 0.5
+        th = torch.rand(B, 2, generator=g, dtype=torch.float64) * torch.pi
+        A = torch.zeros(B, M, M, dtype=torch.float64)
+        for s in range(2):  # companion(1, -2 r cos th, r^2)^T per block
+            A[:, 2 * s, 2 * s] = 2 * r[:, s] * torch.cos(th[:, s])
+            A[:, 2 * s + 1, 2 * s] = -r[:, s] ** 2
+            A[:, 2 * s, 2 * s + 1] = 1.0
+        Bm = torch.randn(M, F, generator=g, dtype=torch.float64) / F ** 0.5
+        Cm = torch.randn(P, M, generator=g, dtype=torch.float64)
+        Dm = torch.randn(P, F, generator=g, dtype=torch.float64)
+        x = torch.randn(B, T, F, generator=g, dtype=torch.float64)
+        zi = torch.randn(B, M, generator=g, dtype=torch.float64)
+        self.cpu = [v.float().contiguous() for v in (A, x, Bm, Cm, Dm, zi)]
+        self.dev = [v.cuda() for v in self.cpu]
+        self.samples = B * T
+        self.fwd_bytes = 4 * (F + P) * B * T  # read x, write y
+        self.bwd_bytes = 0
+
+    def step_fwd(self):
+        from philtorch_amd import lti
+
+        A, x, Bm, Cm, Dm, zi = self.dev
+        return lti.state_space(A, x, Bm, Cm, Dm, zi=zi, unroll_factor=1)
+
+    def step_bwd(self, out):
+        return out
+
+    def cpu_step(self, rows, steps, nthreads):
+        import oracle
+
+        A, x, Bm, Cm, Dm, zi = (v.numpy() for v in self.cpu)
+        oracle.lti_state_space_mimo(A[:rows], x[:rows, :steps], Bm, Cm, Dm, zi[:rows], nthreads=nthreads)
+
+
+class MimoSsGrad(MimoSsApi):
+    """c4_mimo_grad: c4_mimo plus the gradients w.r.t. x and zi
+    (torch.autograd.grad against a seeded upstream gradient): one more
+    philtorch::mimo_ss pass, the adjoint model (A^T, input matrix C^T,
+    output matrix B^T, D^T) in reversed time."""
+
+    def __init__(self):
+        import torch
+
+        super().__init__()
+        B, T, F, P = self.B, self.T, self.F, self.P
+        self.name = "c4_mimo_grad"
+        self.metric = (f"GSamples/s fwd+bwd(x, zi), lti.state_space order {self.M}, {F} inputs, {P} outputs per step "
+                       f"B={B} T={T} fp32 (API)")
+        g = torch.Generator().manual_seed(46)
+        self.gy_cpu = torch.randn(B, T, P, generator=g)
+        self.gy = self.gy_cpu.cuda()
+        self.bwd_bytes = 4 * (P + F) * B * T  # read g, write grad_x
+
+    def step_fwd(self):
+        from philtorch_amd import lti
+
+        A, x, Bm, Cm, Dm, zi = self.dev
+        x, zi = x.detach().requires_grad_(True), zi.detach().requires_grad_(True)
+        y, _ = lti.state_space(A, x, Bm, Cm, Dm, zi=zi, unroll_factor=1)
+        return y, x, zi
+
+    def step_bwd(self, out):
+        import torch
+
+        y, x, zi = out
+        return torch.autograd.grad(y, (x, zi), self.gy)
+
+    def cpu_step(self, rows, steps, nthreads):
+        import numpy as np
+
+        import oracle
+
+        A, x, Bm, Cm, Dm, zi = (v.numpy() for v in self.cpu)
+        A, x, zi = A[:rows], x[:rows, :steps], zi[:rows]
+        gy = self.gy_cpu.numpy()[:rows, :steps]
+        oracle.lti_state_space_mimo(A, x, Bm, Cm, Dm, zi, nthreads=nthreads)
+        # the adjoint model over reversed time
+        fl = lambda v: np.ascontiguousarray(v[:, ::-1])  # noqa: E731
+        oracle.lti_state_space_mimo(np.ascontiguousarray(np.swapaxes(A, -1, -2)), fl(gy), Cm.T.copy(), Bm.T.copy(),
+                                    Dm.T.copy(), None, nthreads=nthreads)
+
+
+class MimoSsCoefGrad(MimoSsGrad):
+    """c4_mimo_coef: c4_mimo_grad with the gradients of A, B, C and D too:
+    the adjoint pass, the forward again writing its states (C = I), the
+    adjoint again writing its states, and one GEMM over time (and rows, for
+    the shared B, C, D) per operand."""
+
+    def __init__(self):
+        super().__init__()
+        B, T, M, F, P = self.B, self.T, self.M, self.F, self.P
+        self.name = "c4_mimo_coef"
+        self.metric = (f"GSamples/s fwd+bwd(x, zi, A, B, C, D), lti.state_space order {M}, {F} inputs, {P} outputs "
+                       f"per step B={B} T={T} fp32 (API)")
+        # adjoint (read g, write grad_x), states (read x, write h), adjoint states (read g, write lambda),
+        # then the sums read lambda and h (A), lambda and x (B), g and h (C), g and x (D)
+        self.bwd_bytes = 4 * ((P + F) + (F + M) + (P + M) + (2 * M) + (M + F) + (P + M) + (P + F)) * B * T
+        self.bwd_launch_bytes = 4 * (P + F) * B * T  # the adjoint pass
+
+    def step_fwd(self):
+        from philtorch_amd import lti
+
+        leaves = [t.detach().requires_grad_(True) for t in self.dev]
+        A, x, Bm, Cm, Dm, zi = leaves
+        y, _ = lti.state_space(A, x, Bm, Cm, Dm, zi=zi, unroll_factor=1)
+        return y, leaves
+
+    def step_bwd(self, out):
+        import torch
+
+        y, leaves = out
+        return torch.autograd.grad(y, leaves, self.gy)
+
+    cpu_step = None  # the oracle restates no coefficient gradients of the state space
+
+
 def make_workload(name):
     if name == "c1":
         return LpvScalar("c1", 64, 65536, "float32")
@@ -793,14 +930,21 @@ def make_workload(name):
         return LpvSsCoefGrad()
     if name == "c4_lfilter4_grad":
         return Lfilter4Grad()
+    if name == "c4_mimo":
+        return MimoSsApi()
+    if name == "c4_mimo_grad":
+        return MimoSsGrad()
+    if name == "c4_mimo_coef":
+        return MimoSsCoefGrad()
     raise ValueError(name)
 
 
 API_CONFIGS = ("c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4_api", "c4_lfilter_inf", "c4_filtfilt",
-               "c4_filtfilt_grad", "c4_filtfilt_coef", "c4_lfilter4", "c4_lfilter4_grad")
+               "c4_filtfilt_grad", "c4_filtfilt_coef", "c4_lfilter4", "c4_lfilter4_grad", "c4_mimo", "c4_mimo_grad",
+               "c4_mimo_coef")
 CONFIGS = ("c1", "c2", "c3", "c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4", "c4_fused", "c4_api",
            "c4_lfilter_inf", "c4_filtfilt", "c4_filtfilt_grad", "c4_filtfilt_coef", "c4_lfilter4", "c4_lfilter4_grad",
-           "c5", "c5_f64")
+           "c4_mimo", "c4_mimo_grad", "c4_mimo_coef", "c5", "c5_f64")
 
 
 # ----------------------------------------------------------------------------
@@ -1091,8 +1235,8 @@ def main() -> int:
 
         off = lambda *a, **k: False  # noqa: E731
         for mod, fn in ((lpv_ssm, "_fused_lpv_ss_applies"), (lti_ssm, "_fused_ss_applies"),
-                        (filtering, "_fused_biquad_applies"), (filtering, "_fused_lfilter_applies"),
-                        (filtering, "_fused_filtfilt_applies")):
+                        (lti_ssm, "_mimo_applies"), (filtering, "_fused_biquad_applies"),
+                        (filtering, "_fused_lfilter_applies"), (filtering, "_fused_filtfilt_applies")):
             setattr(mod, fn, off)
         w.metric += " [composed route]"
     dev = torch.device("cuda", 0)
@@ -1181,6 +1325,9 @@ def main() -> int:
                 "c3_lpv_ss_grad": "lpv_biquad_state_space_api_fwd_bwd_x_zi_B32_T1048576_f32",
                 "c3_lpv_ss_coef": "lpv_biquad_state_space_api_fwd_bwd_all_B32_T1048576_f32",
                 "c4_lfilter4_grad": "lti_lfilter_order4_x4_api_fwd_bwd_x_b_a_B16_T480000_f32",
+                "c4_mimo": "lti_state_space_order4_2in_2out_api_fwd_B16_T480000_f32",
+                "c4_mimo_grad": "lti_state_space_order4_2in_2out_api_fwd_bwd_x_zi_B16_T480000_f32",
+                "c4_mimo_coef": "lti_state_space_order4_2in_2out_api_fwd_bwd_all_B16_T480000_f32",
                 "c5": "lpv_scan_fwd_bwd_B8_T16777216_f32",
                 "c5_f64": "lpv_scan_fwd_bwd_B8_T16777216_f64",
             }[w.name],

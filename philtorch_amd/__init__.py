@@ -833,13 +833,20 @@ if EXTENSION_LOADED and _has_op("mimo_ss"):
         ctx.save_for_backward(*inputs[:6])
         ctx.set_materialize_grads(False)
 
+    if _has_op("outer_sums"):
+
+        @torch.library.register_fake("philtorch::outer_sums")
+        def _(L, R, shared):
+            return L.new_empty((1 if shared else L.shape[0], L.shape[2], R.shape[2]))
+
     def _mimo_row_sums(left, right, shared):
-        """sum over t of left[b, t]^T right[b, t] per row (batch, L, R), or
-        over the rows too (L, R) for an operand the rows share: one GEMM
-        with time (and the rows) as its inner dimension."""
-        if shared:
-            return left.reshape(-1, left.size(-1)).mT @ right.reshape(-1, right.size(-1))
-        return torch.bmm(left.mT, right)
+        """sum over t of left[b, t] right[b, t]^T per row (batch, L, R), or
+        over the rows too (L, R) for an operand the rows share
+        (philtorch::outer_sums: a GEMM with time as its inner dimension and
+        outputs of 4 x 4 at most gets one workgroup from the BLAS library,
+        8 ms at 7.7 million steps)."""
+        out = torch.ops.philtorch.outer_sums(left, right, shared)
+        return out[0] if shared else out
 
     def _mimo_ss_backward(ctx, gy, gzf):
         """The adjoint model (A^T, input matrix C^T, output matrix B^T, D^T)
@@ -849,8 +856,8 @@ if EXTENSION_LOADED and _has_op("mimo_ss"):
             dL/dC = sum_t g[t] h[t]^T,         dL/dD = sum_t g[t] x[t]^T
         take the states h[t] (the forward again with C = I and no D) and the
         adjoint states lambda[t+1] (the adjoint pass with output matrix I),
-        each one more mimo_ss pass, and one GEMM per operand over time (and
-        the rows, for a shared operand).  Under create_graph: the gradient
+        each one more mimo_ss pass, and one philtorch::outer_sums per
+        operand (over time, and the rows for a shared operand).  Under create_graph: the gradient
         of the composite the fused kernel replaces (B x, the native scan,
         the state shift, C h + D x; philtorch/lti/ssm.py:386-589),
         recomputed from the inputs and differentiable again."""

@@ -9,12 +9,13 @@
 // Per step F inputs and P outputs move; the reference route writes and reads
 // B x, the state sequence, its shifted copy, C h and D x.
 //
-// The scan is the generic one (phs_scan.hpp) with one matrix per row: a lane
-// folds its K steps (A, B x[t]) into a map in compute precision (A^K and a
-// Horner sum, mimo_lane_map), wave scans chain the lanes, a
-// look-back wave resolves the tile's entry state over the row's status
-// words, and pass 2 re-runs the steps from each lane's entry state, writing
-// C h + D x.  F and P are arguments, not template parameters: a wave stages
+// The decomposition and the look-back are the LTI state space's
+// (phs_ss.hpp): a lane folds its K steps of B x[t] from a zero state in
+// compute precision, the data waves scan these vectors against a table of
+// A^(K 2^i) in LDS (every map's matrix part is a known power of A, so a level
+// is M^2 work on a vector, not M^3 on a map), a look-back wave resolves the
+// tile's entry state over vector status words, and pass 2 re-runs the steps
+// from each lane's entry state, writing C h + D x.  F and P are arguments, not template parameters: a wave stages
 // its span of x through LDS as F planes of one feature each (a lane then
 // reads its K steps of feature f at a fixed offset), and its outputs leave
 // through P planes the same way, so the global side of both moves is the
@@ -157,32 +158,19 @@ __device__ __forceinline__ typename Alg::s_state mimo_bx(const MimoIn<Alg> &m, c
   return o.s;
 }
 
-// A lane's K steps (A, B x[k]) folded into one map in compute precision:
-// the matrix part is A^K for every lane (AK, from squarings of A), the
-// vector part sum_k A^(K-1-k) B x[k] by Horner's rule.  Folding in storage
-// precision instead (as a time-varying scan must) let float32 rounding in
-// the lane maps of a model with a large transient gain reach 3e-4 of the
-// output's range, ten times a sequential float32 loop's error; from an
-// exact entry state, pass 2's K float32 steps add only a few ulps.
+// A lane's K steps from a zero state, sum_k A^(K-1-k) B x[k], in compute
+// precision (the vector part of its map; the matrix part is A^K).  Folding
+// in storage precision let float32 rounding in the lane maps of a model
+// with a large transient gain reach 3e-4 of the output's range, ten times a
+// sequential float32 loop's error; from an exact entry state, pass 2's K
+// float32 steps add only a few ulps.
 template <class Alg, int K>
-__device__ __forceinline__ Map<Alg> mimo_lane_map(const typename Alg::coef &A, const typename Alg::coef &AK,
-                                                  const typename Alg::s_state (&X)[K]) {
-  Map<Alg> m;
-  m.A = AK;
-  m.x = Alg::load_s(X[0]);
+__device__ __forceinline__ typename Alg::state mimo_lane_fold(const typename Alg::coef &A,
+                                                              const typename Alg::s_state (&X)[K]) {
+  typename Alg::state v = Alg::load_s(X[0]);
 #pragma unroll
-  for (int k = 1; k < K; ++k) m.x = Alg::affine(A, m.x, Alg::load_s(X[k]));
-  return m;
-}
-
-// A^K for K a power of two, in compute precision.
-template <class Alg, int K>
-__device__ __forceinline__ typename Alg::coef mimo_pow(const typename Alg::coef &A) {
-  static_assert((K & (K - 1)) == 0, "K must be a power of two");
-  typename Alg::coef p = A;
-#pragma unroll
-  for (int n = 1; n < K; n *= 2) p = Alg::cmul(p, p);
-  return p;
+  for (int k = 1; k < K; ++k) v = Alg::affine(A, v, Alg::load_s(X[k]));
+  return v;
 }
 
 // The elements [lo, hi) of a block of `len` elements starting at element
@@ -269,22 +257,20 @@ __device__ __forceinline__ int64_t mimo_time(int64_t s, int64_t T) {
 
 // State entering tile position `span` of a row, folded from the inputs (the
 // look-back's bounded-wait fallback; out of line, cold): 64 K steps at a
-// time, each lane reading its K steps' features straight from the row.
+// time, each lane reading its K steps' features straight from the row,
+// st <- A^(64 K) st + the chunk's total.
 template <class Alg, bool REV>
 __device__ __noinline__ typename Alg::state mimo_prefix_fallback(const MimoArgs<Alg> *ap, int64_t b, int64_t span,
-                                                                int lane, typename Alg::state virt) {
+                                                                int lane, typename Alg::state st,
+                                                                const SsPowers<Alg> *tab) {
   const MimoArgs<Alg> &a = *ap;
   using E = typename Alg::elem;
-  using SC = typename Alg::s_coef;
   using SS = typename Alg::s_state;
-  using M = Map<Alg>;
   constexpr int K = MimoShape<Alg>::K;
-  auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
   const MimoIn<Alg> mdl = mimo_in<Alg>(a, b);
   const E *xrow = a.x + b * a.T_len * a.F;
-  const typename Alg::coef Ac = Alg::load_c(mdl.A), AK = mimo_pow<Alg, K>(Ac);
-  M acc = map_identity<Alg>();
   for (int64_t off = 0; off < span; off += 64 * K) {
+    ss_reload_tables();
     SS xs[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -297,30 +283,29 @@ __device__ __noinline__ typename Alg::state mimo_prefix_fallback(const MimoArgs<
       }
       xs[k] = mimo_bx<Alg>(mdl, u);
     }
-    M m = mimo_lane_map<Alg, K>(Ac, AK, xs);
-    m = wave_scan_incl(m, lane, op);
-    acc = compose<Alg>(acc, read_lane(m, 63));
+    typename Alg::state v[1] = {mimo_lane_fold<Alg, K>(Alg::load_c(mdl.A), xs)};
+    ss_lane_scan<Alg, 1, false>(v, lane, tab->pw);
+    st = Alg::affine(tab->pw[6], st, read_lane(v[0], 63));
   }
-  return apply<Alg>(acc, virt);
+  return st;
 }
 
 template <class Alg, bool REV>
 __global__ __launch_bounds__(MimoShape<Alg>::kThreads, 2) void mimo_ss_kernel(MimoArgs<Alg> a) {
   using E = typename Alg::elem;
   using S = typename Alg::state;
-  using SC = typename Alg::s_coef;
   using SS = typename Alg::s_state;
-  using M = Map<Alg>;
   using V = SsView<Alg>;
   using Sh = MimoShape<Alg>;
-  using St = StatusShape<Alg>;
+  using St = SsStatus<Alg>;
   constexpr int K = Sh::K, kWaves = Sh::kWaves, kP = Sh::kPlane;
 
-  __shared__ M s_wagg[kWaves];
-  __shared__ M s_wpre[kWaves];
+  __shared__ S s_wagg[kWaves];  // wave aggregates (matrix part A^(64 K))
+  __shared__ S s_wpre[kWaves];  // exclusive wave prefixes (matrix part A^(64 K w))
   __shared__ S s_in;
   __shared__ unsigned s_id, s_tag;
   __shared__ uint64_t s_look[St::kLookWords];
+  __shared__ SsPowers<Alg> s_tab;
   __shared__ E s_io[kWaves * Sh::kWaveElems];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -336,28 +321,48 @@ __global__ __launch_bounds__(MimoShape<Alg>::kThreads, 2) void mimo_ss_kernel(Mi
   int64_t q, b;  // tile position along the row, row
   split_tile(id, a.B, a.b_magic, a.b_shift, q, b);
   const int64_t T = a.T_len;
-  auto op = [](const M &p, const M &q2) { return compose<Alg>(p, q2); };
 
   if (w == kWaves) {
-    // ================= look-back wave
+    // ================= look-back wave: power tables, then the look-back
+    {
+      const typename Alg::s_coef Arow = V::load_mat(a.A + b * a.A_stride);
+      typename Alg::coef P = ss_pow2<Alg>(Arow, __builtin_ctz(K));
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        if (lane == 0) s_tab.pw[i] = P;
+        P = Alg::cmul(P, P);
+      }
+      if (lane == 0) s_tab.pw[6] = P;  // A^(64 K), a wave's span
+      if (lane == 0) s_tab.pw[7] = P;
+      typename Alg::coef G = P;  // A^(kWaves 64 K), a tile
+#pragma unroll
+      for (int j = 1; j < kWaves; ++j) G = Alg::cmul(P, G);
+#pragma unroll
+      for (int j = 0; j < 7; ++j) {
+        if (lane == 0) s_tab.gp[j] = G;
+        G = Alg::cmul(G, G);
+      }
+    }
+    __syncthreads();  // power tables
     tag = claim_tag(a.claims, a.per_stripe, lane);
     uint64_t *row_status = a.status + b * a.tiles_per_row * St::kStride;
     const S virt = a.zi ? Alg::load_s(V::load_vec(a.zi + b * V::M)) : Alg::szero();
-    __syncthreads();  // wave aggregates are in s_wagg
-    M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
-    v = wave_scan_incl(v, lane, op);
-    const M wex = wave_shift_up(v, lane, map_identity<Alg>());
-    if (lane < kWaves) s_wpre[lane] = wex;
-    const M tagg = read_lane(v, kWaves - 1);
     S yin = virt;
+    __syncthreads();  // wave aggregates are in s_wagg
+    // exclusive wave prefixes and the tile aggregate (every lane, uniformly)
+    S tagg = Alg::szero();
+#pragma unroll
+    for (int j = 0; j < kWaves; ++j) {
+      if (lane == 0) s_wpre[j] = tagg;
+      tagg = Alg::affine(s_tab.pw[7], tagg, s_wagg[j]);
+    }
     if (q > 0) {
-      if (lane == 0) publish(row_status + q * St::kStride + St::kIncWords, tagg, tag);
-      Lookback<Alg> lb = lookback_start<Alg>(q);
-      if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
-        yin = mimo_prefix_fallback<Alg, REV>(kernel_args<MimoArgs<Alg>>(), b, q * Sh::kTile, lane, virt);
+      if (lane == 0) publish(row_status + q * St::kStride + St::kVecWords, tagg, tag);
+      if (!ss_lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, &s_tab, q, yin))
+        yin = mimo_prefix_fallback<Alg, REV>(kernel_args<MimoArgs<Alg>>(), b, q * Sh::kTile, lane, virt, &s_tab);
     }
     if (q + 1 < a.tiles_per_row && lane == 0 && !(a.agg_only && q > 0))
-      publish(row_status + q * St::kStride, apply<Alg>(tagg, yin), tag);
+      publish(row_status + q * St::kStride, Alg::affine(s_tab.gp[0], yin, tagg), tag);
     if (lane == 0) s_in = yin;
     __syncthreads();  // entry state is in s_in
     return;
@@ -377,10 +382,10 @@ __global__ __launch_bounds__(MimoShape<Alg>::kThreads, 2) void mimo_ss_kernel(Mi
     for (int f = 0; f < kMimoMaxIO; ++f) u[f] = f < a.F ? xin[f * kP + lane * K + k] : E(0);
   };
 
-  // ---- pass 1: the lane map of (A, B x[t]) over its K steps, the wave scan.
-  // Steps past the row's end carry a zero input and only touch the
-  // aggregate of its last tile, which nobody reads.
-  M m;
+  // ---- pass 1: the lane's K steps of B x[t] folded from a zero state, then
+  // the wave's vector scan.  Steps past the row's end carry a zero input and
+  // only touch the aggregate of its last tile, which nobody reads.
+  S v[1];
   {
     SS X[K];
 #pragma unroll
@@ -389,15 +394,26 @@ __global__ __launch_bounds__(MimoShape<Alg>::kThreads, 2) void mimo_ss_kernel(Mi
       inputs(k, u);
       X[k] = mimo_bx<Alg>(mi, u);
     }
-    const typename Alg::coef Ac = Alg::load_c(mi.A);
-    m = mimo_lane_map<Alg, K>(Ac, mimo_pow<Alg, K>(Ac), X);
+    v[0] = mimo_lane_fold<Alg, K>(Alg::load_c(mi.A), X);
   }
-  m = wave_scan_incl(m, lane, op);
-  const M ex = wave_shift_up(m, lane, map_identity<Alg>());
-  if (lane == 63) s_wagg[w] = m;
+  __syncthreads();  // power tables
+  ss_lane_scan<Alg, 1, false>(v, lane, s_tab.pw);
+  const S prev = shfl_from(v[0], lane - 1);
+  S ent[1] = {lane > 0 ? prev : Alg::szero()};
+  if (lane == 63) s_wagg[w] = v[0];
   __syncthreads();  // wave aggregates are in s_wagg
   __syncthreads();  // entry state is in s_in
-  SS h = Alg::store_s(apply<Alg>(ex, apply<Alg>(s_wpre[w], s_in)));
+  // the wave's entry state A^(64 K w) s_in + its exclusive prefix; a lane
+  // enters at A^(K lane) of that plus its own exclusive prefix
+  {
+    S st = s_in;
+    for (int j = 0; j < w; ++j) st = Alg::affine(s_tab.pw[6], st, Alg::szero());
+    st = Alg::sadd(st, s_wpre[w]);
+    S sv[1] = {st};
+    ss_pow_apply<Alg, 6, 1>(s_tab.pw, lane, sv);
+    ent[0] = Alg::sadd(sv[0], ent[0]);
+  }
+  SS h = Alg::store_s(ent[0]);
 
   // ---- pass 2: y = C h + D x, then the step (B x again from the planes:
   // keeping the K products from pass 1 held their registers across the scan)

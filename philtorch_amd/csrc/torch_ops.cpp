@@ -1055,6 +1055,36 @@ std::vector<Tensor> lpv_ss_backward_hip(const Tensor &A, const std::optional<Ten
   return {gA, gB, gC, gD, gzi, gx};
 }
 
+// sum over time (and the rows, with shared) of L[b, t] R[b, t]^T
+// (phs_outer_sums): L (batch, T, nl), R (batch, T, nr), nl and nr 1-4;
+// returns (batch or 1, nl, nr) in their type.  The coefficient gradients of
+// mimo_ss reduce the forward's and the adjoint's states with it.
+Tensor outer_sums_hip(const Tensor &L, const Tensor &R, bool shared) {
+  TORCH_CHECK(L.dim() == 3 && R.dim() == 3 && L.size(0) == R.size(0) && L.size(1) == R.size(1),
+              "philtorch::outer_sums: L and R must be (batch, T, n) with equal batch and T");
+  TORCH_CHECK(L.size(2) >= 1 && L.size(2) <= 4 && R.size(2) >= 1 && R.size(2) <= 4,
+              "philtorch::outer_sums: widths 1 to 4");
+  TORCH_CHECK(L.scalar_type() == R.scalar_type() && (L.scalar_type() == at::kFloat || L.scalar_type() == at::kDouble),
+              "philtorch::outer_sums: float32 or float64 operands of one type");
+  TORCH_CHECK(L.is_cuda() && R.device() == L.device(), "philtorch::outer_sums: HIP tensors on one device");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(L.device());
+  const int64_t B = L.size(0), T = L.size(1), nl = L.size(2), nr = R.size(2);
+  const int dt = phs_dtype_of(L.scalar_type());
+  Tensor Lc = L.contiguous(), Rc = R.contiguous();
+  Tensor out = at::empty({shared ? 1 : B, nl, nr}, L.options());
+  if (B == 0) {
+    out.zero_();
+    return out;
+  }
+  Tensor scratch = at::empty({int64_t(std::max<size_t>(phs_outer_sums_scratch_size(dt, B, T), 8))},
+                             L.options().dtype(at::kByte));
+  check_status(phs_outer_sums(dt, B, T, Lc.const_data_ptr(), int(nl), Rc.const_data_ptr(), int(nr), shared ? 1 : 0,
+                              out.mutable_data_ptr(), scratch.mutable_data_ptr(), size_t(scratch.numel()),
+                              stream_of(L)),
+               "outer_sums");
+  return out;
+}
+
 // Multi-input, multi-output LTI state space of order <= 4 with 1-4 inputs and
 // 1-4 outputs per step, fused (phs_mimo_ss_fwd; philtorch/lti/ssm.py:386-589
 // for a 3D x or matrix-valued B, C, D): returns (y, zf).  x (batch, T, F);
@@ -1307,6 +1337,7 @@ TORCH_LIBRARY(philtorch, m) {
         {at::Tag::pt2_compliant_tag});
   m.def("mimo_ss(Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? zi, Tensor x, bool reverse=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
+  m.def("outer_sums(Tensor L, Tensor R, bool shared) -> Tensor", {at::Tag::pt2_compliant_tag});
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
@@ -1335,6 +1366,7 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("lpv_ss", &lpv_ss_hip);
   m.impl("lpv_ss_backward", &lpv_ss_backward_hip);
   m.impl("mimo_ss", &mimo_ss_hip);
+  m.impl("outer_sums", &outer_sums_hip);
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CPU, m) {

@@ -193,6 +193,46 @@ def test_mimo_ss_capi_errors(api):
     assert call(wsb=16) == capi.PHS_ERR_WORKSPACE
 
 
+@pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("nl,nr", [(1, 1), (4, 4), (3, 2), (2, 4)])
+@pytest.mark.parametrize("Bn,T", [(1, 1), (3, 700), (2, 16384), (2, 16385), (3, 100003)])
+def test_outer_sums_capi(api, dtype, nl, nr, Bn, T):
+    """phs_outer_sums (the coefficient gradients' reductions) against numpy's
+    einsum in fp64, per row and over the rows, across its 16384-step blocks."""
+    import torch
+
+    lib, ws, capi = api
+    g = D.rng(D.seed_of("outer", np.dtype(dtype).name, nl, nr, Bn, T))
+    Lh, Rh = g.standard_normal((Bn, T, nl)).astype(dtype), g.standard_normal((Bn, T, nr)).astype(dtype)
+    L, R = _dev(Lh), _dev(Rh)
+    dt = capi.DTYPES[np.dtype(dtype)]
+    need = lib.phs_outer_sums_scratch_size(dt, Bn, T)
+    assert 0 < need <= ws.numel()
+    ref = np.einsum("bti,btj->bij", Lh.astype(np.float64), Rh.astype(np.float64))
+    for shared in (0, 1):
+        out = torch.full((1 if shared else Bn, nl, nr), float("nan"), dtype=L.dtype, device="cuda")
+        print(f"outer_sums nl={nl} nr={nr} B={Bn} T={T} shared={shared}", flush=True)
+        rc = lib.phs_outer_sums(dt, Bn, T, _p(L), nl, _p(R), nr, shared, _p(out), _p(ws), need,
+                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == capi.PHS_OK, lib.phs_error_string(rc)
+        torch.cuda.synchronize()
+        want = ref.sum(0, keepdims=True) if shared else ref
+        # sums of T products: the bound scales with sqrt(T) times the terms' size
+        D.check(out.cpu().numpy(), want, f"outer shared={shared}", dtype=dtype, scale=np.sqrt(Bn * T))
+
+
+def test_outer_sums_op_and_empty_rows(hip):
+    import torch
+
+    L = torch.randn(3, 5000, 2, device="cuda", dtype=torch.float64)
+    R = torch.randn(3, 5000, 3, device="cuda", dtype=torch.float64)
+    torch.testing.assert_close(torch.ops.philtorch.outer_sums(L, R, False), torch.einsum("bti,btj->bij", L, R))
+    torch.testing.assert_close(torch.ops.philtorch.outer_sums(L, R, True)[0], torch.einsum("bti,btj->ij", L, R))
+    E = torch.empty(2, 0, 3, device="cuda")
+    assert torch.ops.philtorch.outer_sums(E, torch.empty(2, 0, 1, device="cuda"), False).abs().sum() == 0
+    torch.library.opcheck(torch.ops.philtorch.outer_sums.default, (L.float(), R.float(), True))
+
+
 # ---------------------------------------------------------------- torch API
 def _api_cases(batch, M):
     from tests.test_host import _mimo_shape_cases

@@ -437,6 +437,17 @@ def test_capi_mimo_state_space_host_only_calls():
         assert mimo(**bad) == capi.PHS_ERR_INVALID, bad
     assert mimo(wsb=lib.phs_mimo_ss_workspace_size(0, 2, 2, 100) - 1) == capi.PHS_ERR_WORKSPACE
     assert mimo(B=0) == capi.PHS_OK
+    # outer-product sums: sizes and argument errors
+    assert lib.phs_outer_sums_scratch_size(0, 16, 480000) >= 16 * 30 * 16 * 8
+    assert lib.phs_outer_sums_scratch_size(2, 16, 100) == 0
+
+    def osum(dt=0, nl=2, nr=3, shared=0, sb=1 << 20, out=d):
+        return lib.phs_outer_sums(dt, 2, 100, d, nl, d, nr, shared, out, d, sb, None)
+
+    assert osum(dt=2) == capi.PHS_ERR_DTYPE
+    for bad in (dict(nl=0), dict(nr=5), dict(shared=2), dict(out=None)):
+        assert osum(**bad) == capi.PHS_ERR_INVALID, bad
+    assert osum(sb=8) == capi.PHS_ERR_WORKSPACE
 
 
 def _mimo_shape_cases(batch, M):
