@@ -195,9 +195,14 @@ int sos_bwd(int64_t B, int64_t T, int S, const SosCoefs &k, const void *x, const
     // every third section where the LDS left to each of the workgroups the
     // kernel's registers let a CU hold allows two slots, else every other
     // (fp32 on gfx950: three workgroups per CU, one slot), else none
-    const auto kernel = sos_kernel<E, Sh, true, true>;
     const size_t laneh = size_t(S) * Sh::kWaves * Sh::R * 64 * sizeof(Vec2<E>);
     const size_t slot = size_t(Sh::kWaves) * Sh::R * Sh::K * 64 * sizeof(E);
+    // one section with room for the output's slot: the form that parks x
+    // there (ONE in sos_kernel)
+    const auto kernel_one = sos_kernel<E, Sh, true, true, true>;
+    const bool one = S == 1 && laneh + slot <= lds_limit(reinterpret_cast<const void *>(kernel_one),
+                                                         kSosWgsPerCu<E, Sh, true>);
+    const auto kernel = one ? kernel_one : sos_kernel<E, Sh, true, true>;
     const size_t limit = lds_limit(reinterpret_cast<const void *>(kernel), kSosWgsPerCu<E, Sh, true>);
     int step = S >= 2 ? (S + 2) / 3 : 0;
     if (step > 0 && laneh + sos_kept_slots(S, step) * slot > limit) step = (S + 1) / 2;

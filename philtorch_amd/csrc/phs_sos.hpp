@@ -756,7 +756,13 @@ constexpr int kSosMinWaves = sizeof(E) == 4 ? (REV ? 3 : 4) : 1;
 template <typename E, class Sh, bool REV>
 constexpr int kSosWgsPerCu = sizeof(E) == 4 ? 4 * kSosMinWaves<E, REV> / (Sh::kThreads / 64) : 1;
 
-template <typename E, class Sh, bool REV, bool GRAD>
+// ONE (gradient backward of a single section, the biquad op's, with the
+// output's LDS slot): the prologue's load of x also goes to that slot, and
+// the one visit reads its section's input from there instead of loading x a
+// second time (the slot takes the output's transpose only after the visit
+// has read it).  Holding x in registers instead spilled 124 VGPRs: it lives
+// across the visit's fold and scan, where its input does not.
+template <typename E, class Sh, bool REV, bool GRAD, bool ONE = false>
 __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kernel(SosArgs<E> a) {
   using Alg = Block2<E>;
   using C = typename Wide<E>::type;
@@ -766,6 +772,7 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
   constexpr int K = Sh::K, R = Sh::R, W = Sh::kWaves;
   using Mt = Mat2<C>;
   static_assert(!GRAD || REV, "coefficient gradients come with the backward");
+  static_assert(!ONE || GRAD, "the single-section form is the gradient backward's");
 
   __shared__ M s_wagg[W];
   __shared__ M s_wpre[W];
@@ -888,6 +895,12 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
 #pragma unroll
     for (int r = 0; r < R; ++r) load_chunk<E, K>(a.x + b * T, chunk0(r), T, vec, F[r], zero);
   }
+  if constexpr (ONE) {  // x into the output's slot, for the visit
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int k = 0; k < K; ++k) s_uin[((w * R + r) * K + k) * 64 + lane] = F[r][k];
+  }
   __syncthreads();  // powers of the first two visits
 
   // ---- backward with coefficient gradients: recompute the forward cascade
@@ -952,8 +965,8 @@ __global__ __launch_bounds__(Sh::kThreads, (kSosMinWaves<E, REV>)) void sos_kern
       const int ks = a.kept_step;
       const int slot = ks > 0 ? (s / ks < kSosKeptSlots ? s / ks : kSosKeptSlots) : 0;  // kept sections <= s
       const int j0 = slot * ks;
-      if (j0 > 0) {
-        const E *src = s_uin + size_t(slot - 1) * W * R * K * 64;
+      if (ONE || j0 > 0) {
+        const E *src = s_uin + size_t(ONE ? 0 : slot - 1) * W * R * K * 64;
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
