@@ -62,9 +62,13 @@ struct MimoArgs {
 
 // 3 data waves and a look-back wave; a lane owns K consecutive steps (32
 // bytes of one feature), a wave 64 K steps.  LDS per data wave: kMimoMaxIO
-// input planes and kMimoMaxIO output planes of 64 K elements, each padded by
-// 16 bytes so that the lanes of a staging instruction, which write
-// consecutive elements of different planes, spread over the banks.
+// planes of 64 K elements, each padded by 16 bytes so that the lanes of a
+// staging instruction, which write consecutive elements of different
+// planes, spread over the banks.  The outputs overwrite the inputs in the
+// same planes: a lane writes step k's outputs after reading its inputs, and
+// no other lane reads them.  With separate output planes (60 KB of LDS per
+// workgroup at order 4) and 200 VGPRs a CU held two workgroups; at 35 KB and
+// 168 VGPRs it holds three.
 template <class Alg>
 struct MimoShape {
   using E = typename Alg::elem;
@@ -74,7 +78,10 @@ struct MimoShape {
   static constexpr int kSpan = 64 * K;
   static constexpr int kTile = kWaves * kSpan;
   static constexpr int kPlane = kSpan + 16 / int(sizeof(E));
-  static constexpr int kWaveElems = 2 * kMimoMaxIO * kPlane;
+  static constexpr int kWaveElems = kMimoMaxIO * kPlane;
+  // waves per SIMD of the launch bounds: 3 (168 VGPRs), but 2 for order-4
+  // fp64, which spilled 14 VGPRs at 168
+  static constexpr int kMinWaves = sizeof(E) == 8 && sizeof(typename Alg::s_state) == 4 * sizeof(E) ? 2 : 3;
 };
 
 // The model of row b in two halves, each loaded where it is first needed
@@ -291,7 +298,7 @@ __device__ __noinline__ typename Alg::state mimo_prefix_fallback(const MimoArgs<
 }
 
 template <class Alg, bool REV>
-__global__ __launch_bounds__(MimoShape<Alg>::kThreads, 2) void mimo_ss_kernel(MimoArgs<Alg> a) {
+__global__ __launch_bounds__(MimoShape<Alg>::kThreads, MimoShape<Alg>::kMinWaves) void mimo_ss_kernel(MimoArgs<Alg> a) {
   using E = typename Alg::elem;
   using S = typename Alg::state;
   using SS = typename Alg::s_state;
@@ -369,8 +376,8 @@ __global__ __launch_bounds__(MimoShape<Alg>::kThreads, 2) void mimo_ss_kernel(Mi
   }
 
   // ================= data waves
-  E *xin = s_io + w * Sh::kWaveElems;  // F input planes
-  E *yout = xin + kMimoMaxIO * kP;     // P output planes
+  E *xin = s_io + w * Sh::kWaveElems;  // F input planes, then P output planes
+  E *yout = xin;
   const int64_t s0 = q * Sh::kTile + int64_t(w) * Sh::kSpan;  // the wave's first scan position
   mimo_stage_in<Alg, REV>(a.x + b * T * a.F, s0, T, a.F, a.f_magic, xin, lane);
   const MimoIn<Alg> mi = mimo_in<Alg>(a, b);
