@@ -575,20 +575,24 @@ int phs_mimo_ss_rev(int dtype, int M, int F, int P, int64_t B, int64_t T, const 
                     const void *Cm, const void *Dm, int shared, const void *zi, const void *x, void *y, void *zf,
                     void *workspace, size_t workspace_bytes, void *stream);
 
-/* ---- Sums over time of outer products, for the coefficient gradients of
- * phs_mimo_ss_fwd (no counterpart in the reference, whose autograd forms
- * them as matmuls over the composed route's tensors; philtorch/lti/ssm.py:
- * 467-589): out[b] = sum_t L[b,t,:] R[b,t,:]^T, or with shared = 1 out[0] =
- * the sum over every row too.  dtype PHS_F32 or PHS_F64 (sums in fp64);
- * L [B,T,nl] and R [B,T,nr] contiguous, nl and nr 1..4; out [B or 1, nl,
- * nr].  dL/dA = sum lambda[t+1] h[t]^T, dL/dB = sum lambda[t+1] x[t]^T,
- * dL/dC = sum g[t] h[t]^T, dL/dD = sum g[t] x[t]^T, with h the forward's
- * states and lambda the adjoint's (both phs_mimo_ss passes with C = I).
- * `scratch`: phs_outer_sums_scratch_size bytes, any contents. */
-size_t phs_outer_sums_scratch_size(int dtype, int64_t B, int64_t T);
+/* ---- The coefficient gradients of phs_mimo_ss_fwd summed over time in one
+ * pass (no counterpart in the reference, whose autograd forms them as
+ * matmuls over the composed route's tensors; philtorch/lti/ssm.py:460-589):
+ *     gA = sum_t lam[t] h[t]^T (M x M),  gB = sum_t lam[t] x[t]^T (M x F),
+ *     gC = sum_t g[t] h[t]^T (P x M),    gD = sum_t g[t] x[t]^T (P x F),
+ * per row [B, ...], or with the operand's PHS_MIMO_*_SHARED bit in `shared`
+ * summed over the rows too (no row axis).  lam [B,T,M] are the adjoint
+ * states dL/dh[t+1] and h [B,T,M] the forward's states h[t] (both
+ * phs_mimo_ss passes with C the identity), x [B,T,F] the input, g [B,T,P]
+ * the upstream gradient; every output is nullable (not wanted), and an input
+ * no wanted output reads may be NULL.  dtype PHS_F32 or PHS_F64, sums in
+ * fp64.  `scratch`: phs_mimo_ss_grad_sums_scratch_size bytes, any
+ * contents. */
+size_t phs_mimo_ss_grad_sums_scratch_size(int dtype, int64_t B, int64_t T);
 
-int phs_outer_sums(int dtype, int64_t B, int64_t T, const void *L, int nl, const void *R, int nr, int shared,
-                   void *out, void *scratch, size_t scratch_bytes, void *stream);
+int phs_mimo_ss_grad_sums(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *lam, const void *hs,
+                          const void *x, const void *g, int shared, void *gA, void *gB, void *gC, void *gD,
+                          void *scratch, size_t scratch_bytes, void *stream);
 
 /* ---- Measurement helper, no counterpart in the reference.  A streaming
  * kernel with no scan: out_j[i] = (j + 1) * sum_k in_k[i] over n fp32

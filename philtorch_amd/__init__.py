@@ -833,20 +833,15 @@ if EXTENSION_LOADED and _has_op("mimo_ss"):
         ctx.save_for_backward(*inputs[:6])
         ctx.set_materialize_grads(False)
 
-    if _has_op("outer_sums"):
+    if _has_op("mimo_ss_grad_sums"):
 
-        @torch.library.register_fake("philtorch::outer_sums")
-        def _(L, R, shared):
-            return L.new_empty((1 if shared else L.shape[0], L.shape[2], R.shape[2]))
-
-    def _mimo_row_sums(left, right, shared):
-        """sum over t of left[b, t] right[b, t]^T per row (batch, L, R), or
-        over the rows too (L, R) for an operand the rows share
-        (philtorch::outer_sums: a GEMM with time as its inner dimension and
-        outputs of 4 x 4 at most gets one workgroup from the BLAS library,
-        8 ms at 7.7 million steps)."""
-        out = torch.ops.philtorch.outer_sums(left, right, shared)
-        return out[0] if shared else out
+        @torch.library.register_fake("philtorch::mimo_ss_grad_sums")
+        def _(lam, hs, x, g, shared, want):
+            st = lam if lam is not None else hs
+            M = st.shape[2] if st is not None else 1
+            dims = ((M, M), (M, x.shape[2]), (g.shape[2], M), (g.shape[2], x.shape[2]))
+            return [x.new_empty(((1 if (shared >> i) & 1 else x.shape[0]),) + dims[i]) if (want >> i) & 1
+                    else x.new_empty((0,)) for i in range(4)]
 
     def _mimo_ss_backward(ctx, gy, gzf):
         """The adjoint model (A^T, input matrix C^T, output matrix B^T, D^T)
@@ -856,8 +851,9 @@ if EXTENSION_LOADED and _has_op("mimo_ss"):
             dL/dC = sum_t g[t] h[t]^T,         dL/dD = sum_t g[t] x[t]^T
         take the states h[t] (the forward again with C = I and no D) and the
         adjoint states lambda[t+1] (the adjoint pass with output matrix I),
-        each one more mimo_ss pass, and one philtorch::outer_sums per
-        operand (over time, and the rows for a shared operand).  Under create_graph: the gradient
+        each one more mimo_ss pass, and philtorch::mimo_ss_grad_sums: the
+        four sums over time (and the rows, for a shared operand) in one pass
+        over lambda, h, x and g.  Under create_graph: the gradient
         of the composite the fused kernel replaces (B x, the native scan,
         the state shift, C h + D x; philtorch/lti/ssm.py:386-589),
         recomputed from the inputs and differentiable again."""
@@ -896,14 +892,14 @@ if EXTENSION_LOADED and _has_op("mimo_ss"):
                 hs, _ = torch.ops.philtorch.mimo_ss(A, B, eye, None, zi, x, ctx.reverse)
             if needs[0] or needs[1]:
                 lam, _ = torch.ops.philtorch.mimo_ss(At, Ct, eye, None, gzf, g, not ctx.reverse)
-        if needs[0]:
-            out[0] = _mimo_row_sums(lam, hs, A.dim() == 2)
-        if needs[1]:
-            out[1] = _mimo_row_sums(lam, x, B.dim() == 2)
-        if needs[2]:
-            out[2] = _mimo_row_sums(g, hs, C.dim() == 2)
-        if needs[3] and D is not None:
-            out[3] = _mimo_row_sums(g, x, D.dim() == 2)
+        want = sum(1 << i for i in range(4) if needs[i] and inputs[i] is not None)
+        if want:
+            shared = sum(1 << i for i, t in enumerate((A, B, C, D)) if t is not None and t.dim() == 2)
+            with _op_ctx():
+                sums = torch.ops.philtorch.mimo_ss_grad_sums(lam, hs, x, g, shared, want)
+            for i in range(4):
+                if (want >> i) & 1:
+                    out[i] = sums[i][0] if (shared >> i) & 1 else sums[i]
         return tuple(out)
 
     torch.library.register_autograd("philtorch::mimo_ss", _mimo_ss_backward, setup_context=_mimo_ss_setup)

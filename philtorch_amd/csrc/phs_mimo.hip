@@ -86,117 +86,175 @@ int mimo_ss(int F, int P, int64_t B, int64_t T, const void *A, const void *Bm, c
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
-// ---- sums over time of outer products (the coefficient gradients of the
-// model: dL/dA = sum lambda h^T, dL/dB = sum lambda x^T, dL/dC = sum g h^T,
-// dL/dD = sum g x^T).  A block sums `chunk` steps of one row: each thread
-// its strided steps in compute precision, then the block through LDS, one
-// partial per (row, block); the second kernel sums the partials in row and
-// block order (and over the rows for a shared operand).
-constexpr int kOuterThreads = 256;
-constexpr int kOuterSteps = 64;  // steps per thread and block
-constexpr int kOuterMax = kMimoMaxIO * kMimoMaxIO;
+// ---- the coefficient gradients, summed over time in one pass over the
+// forward's states h, the adjoint states lambda, x and g:
+//   dL/dA = sum lambda h^T (M x M), dL/dB = sum lambda x^T (M x F),
+//   dL/dC = sum g h^T (P x M),      dL/dD = sum g x^T (P x F),
+// each wanted or not.  A block sums `chunk` steps of one row: each thread its
+// strided steps in compute precision, then the block through LDS, one
+// partial (the four products as 4 x 4 blocks) per (row, block); the second
+// kernel sums the partials in row and block order, over the rows too for a
+// shared operand.  (Four separate sums of one product each read lambda, h,
+// x and g twice: 372 against 93 us for one of them at the c4_mimo shape.)
+constexpr int kSumThreads = 256;
+constexpr int kSumSteps = 64;  // steps per thread and block
+constexpr int kSumBlock = kMimoMaxIO * kMimoMaxIO;
+constexpr int kSumN = 4 * kSumBlock;  // A, B, C, D
 
 template <typename E>
-__global__ __launch_bounds__(kOuterThreads) void mimo_outer_partial_kernel(const E *L, int nl, const E *R, int nr,
-                                                                         int64_t T, typename Wide<E>::type *part) {
+struct GradSumIn {
+  const E *lam, *hs, *x, *g;  // [B, T, M], [B, T, M], [B, T, F], [B, T, P]
+  int M, F, P;
+  unsigned want;  // bit i: product i (A, B, C, D)
+};
+
+template <typename E>
+__global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumIn<E> in, int64_t T,
+                                                                        typename Wide<E>::type *part) {
   using C = typename Wide<E>::type;
-  __shared__ C s_red[kOuterThreads / 64][kOuterMax];
+  __shared__ C s_red[kSumThreads / 64][kSumN];
   const int64_t b = blockIdx.y, blk = blockIdx.x;
-  const int64_t chunk = int64_t(kOuterThreads) * kOuterSteps;
+  const int64_t chunk = int64_t(kSumThreads) * kSumSteps;
   const int64_t t0 = blk * chunk, t1 = t0 + chunk < T ? t0 + chunk : T;
-  const E *lrow = L + b * T * nl;
-  const E *rrow = R + b * T * nr;
-  C acc[kMimoMaxIO][kMimoMaxIO];
+  const int M = in.M, F = in.F, P = in.P;
+  const bool wA = in.want & 1, wB = in.want & 2, wC = in.want & 4, wD = in.want & 8;
+  const bool need_l = wA || wB, need_h = wA || wC, need_x = wB || wD, need_g = wC || wD;
+  C acc[4][kMimoMaxIO][kMimoMaxIO];
 #pragma unroll
-  for (int i = 0; i < kMimoMaxIO; ++i)
+  for (int p = 0; p < 4; ++p)
 #pragma unroll
-    for (int j = 0; j < kMimoMaxIO; ++j) acc[i][j] = C(0);
-  for (int64_t t = t0 + threadIdx.x; t < t1; t += kOuterThreads) {
-    E l[kMimoMaxIO], r[kMimoMaxIO];
+    for (int i = 0; i < kMimoMaxIO; ++i)
+#pragma unroll
+      for (int j = 0; j < kMimoMaxIO; ++j) acc[p][i][j] = C(0);
+  for (int64_t t = t0 + threadIdx.x; t < t1; t += kSumThreads) {
+    const int64_t bt = b * T + t;
+    C l[kMimoMaxIO], h[kMimoMaxIO], u[kMimoMaxIO], g[kMimoMaxIO];
 #pragma unroll
     for (int i = 0; i < kMimoMaxIO; ++i) {
-      l[i] = i < nl ? lrow[t * nl + i] : E(0);
-      r[i] = i < nr ? rrow[t * nr + i] : E(0);
+      l[i] = h[i] = u[i] = g[i] = C(0);
+      if (need_l && i < M) l[i] = C(in.lam[bt * M + i]);
+      if (need_h && i < M) h[i] = C(in.hs[bt * M + i]);
+      if (need_x && i < F) u[i] = C(in.x[bt * F + i]);
+      if (need_g && i < P) g[i] = C(in.g[bt * P + i]);
     }
 #pragma unroll
     for (int i = 0; i < kMimoMaxIO; ++i)
 #pragma unroll
-      for (int j = 0; j < kMimoMaxIO; ++j) acc[i][j] = fma(C(l[i]), C(r[j]), acc[i][j]);
+      for (int j = 0; j < kMimoMaxIO; ++j) {
+        acc[0][i][j] = fma(l[i], h[j], acc[0][i][j]);
+        acc[1][i][j] = fma(l[i], u[j], acc[1][i][j]);
+        acc[2][i][j] = fma(g[i], h[j], acc[2][i][j]);
+        acc[3][i][j] = fma(g[i], u[j], acc[3][i][j]);
+      }
   }
   // the wave's sums by DPP scans, then the block's through LDS
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   auto add = [](const C &p, const C &o) { return p + o; };
 #pragma unroll
-  for (int i = 0; i < kMimoMaxIO; ++i)
+  for (int p = 0; p < 4; ++p) {
+    if (!((in.want >> p) & 1)) continue;
 #pragma unroll
-    for (int j = 0; j < kMimoMaxIO; ++j) {
-      const C v = read_lane(wave_scan_incl(acc[i][j], lane, add), 63);
-      if (lane == 0) s_red[wv][i * kMimoMaxIO + j] = v;
-    }
+    for (int i = 0; i < kMimoMaxIO; ++i)
+#pragma unroll
+      for (int j = 0; j < kMimoMaxIO; ++j) {
+        const C v = read_lane(wave_scan_incl(acc[p][i][j], lane, add), 63);
+        if (lane == 0) s_red[wv][p * kSumBlock + i * kMimoMaxIO + j] = v;
+      }
+  }
   __syncthreads();
-  if (threadIdx.x < kOuterMax) {
+  if (threadIdx.x < kSumN && ((in.want >> (threadIdx.x / kSumBlock)) & 1)) {
     C v = C(0);
 #pragma unroll
-    for (int k = 0; k < kOuterThreads / 64; ++k) v += s_red[k][threadIdx.x];
-    part[(b * gridDim.x + blk) * kOuterMax + threadIdx.x] = v;
+    for (int k = 0; k < kSumThreads / 64; ++k) v += s_red[k][threadIdx.x];
+    part[(b * gridDim.x + blk) * kSumN + threadIdx.x] = v;
   }
 }
 
-// out[row or 0][i][j] (i < nl, j < nr) from the partials of `blocks` blocks
-// per row; shared: one sum over every row.  A block per output row, its
-// threads strided over the partials, then the block's sums through LDS.
 template <typename E>
-__global__ __launch_bounds__(kOuterThreads) void mimo_outer_finish_kernel(const typename Wide<E>::type *part,
-                                                                        int64_t rows, int64_t blocks, int nl, int nr,
-                                                                        int shared, E *out) {
+struct GradSumOut {
+  E *out[4];      // A [B|1, M, M], B [B|1, M, F], C [B|1, P, M], D [B|1, P, F]; nullptr: not wanted
+  int rows[4], cols[4];
+  int shared;     // bit i: product i summed over the rows too
+};
+
+// Block o < B: the per-row products of row o; block B: the shared ones over
+// every row.  Threads strided over the partials, then the block's sums
+// through LDS.
+template <typename E>
+__global__ __launch_bounds__(kSumThreads) void mimo_grad_finish_kernel(const typename Wide<E>::type *part,
+                                                                       int64_t B, int64_t blocks, GradSumOut<E> o) {
   using C = typename Wide<E>::type;
-  __shared__ C s_red[kOuterThreads / 64][kOuterMax];
-  const int64_t o = blockIdx.x;  // output row
-  const int64_t p0 = shared ? 0 : o * blocks, n = shared ? rows * blocks : blocks;
-  C acc[kOuterMax];
+  __shared__ C s_red[kSumThreads / 64][kSumN];
+  const int64_t r = blockIdx.x;
+  const bool shared_block = r == B;
+  unsigned mine = 0;  // the products this block writes
 #pragma unroll
-  for (int k = 0; k < kOuterMax; ++k) acc[k] = C(0);
-  for (int64_t p = threadIdx.x; p < n; p += kOuterThreads) {
+  for (int p = 0; p < 4; ++p)
+    if (o.out[p] && (((o.shared >> p) & 1) != 0) == shared_block) mine |= 1u << p;
+  if (!mine) return;
+  const int64_t p0 = shared_block ? 0 : r * blocks, n = shared_block ? B * blocks : blocks;
+  C acc[kSumN];
 #pragma unroll
-    for (int k = 0; k < kOuterMax; ++k) acc[k] += part[(p0 + p) * kOuterMax + k];
+  for (int k = 0; k < kSumN; ++k) acc[k] = C(0);
+  for (int64_t q = threadIdx.x; q < n; q += kSumThreads) {
+#pragma unroll
+    for (int k = 0; k < kSumN; ++k)
+      if ((mine >> (k / kSumBlock)) & 1) acc[k] += part[(p0 + q) * kSumN + k];
   }
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   auto add = [](const C &a, const C &b) { return a + b; };
 #pragma unroll
-  for (int k = 0; k < kOuterMax; ++k) {
+  for (int k = 0; k < kSumN; ++k) {
+    if (!((mine >> (k / kSumBlock)) & 1)) continue;
     const C v = read_lane(wave_scan_incl(acc[k], lane, add), 63);
     if (lane == 0) s_red[wv][k] = v;
   }
   __syncthreads();
-  const int i = threadIdx.x / kMimoMaxIO, j = threadIdx.x % kMimoMaxIO;
-  if (threadIdx.x < kOuterMax && i < nl && j < nr) {
+  const int k = threadIdx.x, p = k / kSumBlock, i = (k % kSumBlock) / kMimoMaxIO, j = k % kMimoMaxIO;
+  if (k < kSumN && ((mine >> p) & 1) && i < o.rows[p] && j < o.cols[p]) {
     C v = C(0);
 #pragma unroll
-    for (int k = 0; k < kOuterThreads / 64; ++k) v += s_red[k][threadIdx.x];
-    out[(o * nl + i) * nr + j] = down<E>(v);
+    for (int w = 0; w < kSumThreads / 64; ++w) v += s_red[w][k];
+    const int64_t row = shared_block ? 0 : r;
+    o.out[p][(row * o.rows[p] + i) * o.cols[p] + j] = down<E>(v);
   }
 }
 
 template <typename E>
-int outer_sums(int64_t B, int64_t T, const void *L, int nl, const void *R, int nr, int shared, void *out,
-               void *scratch, size_t scratch_bytes, hipStream_t stream) {
+int grad_sums(int M, int F, int P, int64_t B, int64_t T, const void *lam, const void *hs, const void *x,
+              const void *g, int shared, void *gA, void *gB, void *gC, void *gD, void *scratch, size_t scratch_bytes,
+              hipStream_t stream) {
   using C = typename Wide<E>::type;
-  if (B < 0 || T < 0 || nl < 1 || nl > kMimoMaxIO || nr < 1 || nr > kMimoMaxIO || (shared & ~1)) return PHS_ERR_INVALID;
-  if (!out) return PHS_ERR_INVALID;
-  const int64_t orows = shared ? 1 : B;
-  if (orows == 0) return PHS_OK;
-  const int64_t chunk = int64_t(kOuterThreads) * kOuterSteps;
-  const int64_t blocks = (T + chunk - 1) / chunk;
-  if (B * blocks > 0) {
-    if (!L || !R) return PHS_ERR_INVALID;
-    if (B > 65535) return PHS_ERR_INVALID;
-    if (!scratch || scratch_bytes < size_t(B) * size_t(blocks) * kOuterMax * sizeof(C)) return PHS_ERR_WORKSPACE;
-    hipLaunchKernelGGL(mimo_outer_partial_kernel<E>, dim3(unsigned(blocks), unsigned(B)), dim3(kOuterThreads), 0,
-                       stream, static_cast<const E *>(L), nl, static_cast<const E *>(R), nr, T,
-                       static_cast<C *>(scratch));
+  if (B < 0 || T < 0 || M < 1 || M > kMimoMaxIO || F < 1 || F > kMimoMaxIO || P < 1 || P > kMimoMaxIO)
+    return PHS_ERR_INVALID;
+  if (shared & ~(PHS_MIMO_A_SHARED | PHS_MIMO_B_SHARED | PHS_MIMO_C_SHARED | PHS_MIMO_D_SHARED))
+    return PHS_ERR_INVALID;
+  GradSumIn<E> in{static_cast<const E *>(lam), static_cast<const E *>(hs), static_cast<const E *>(x),
+                  static_cast<const E *>(g), M, F, P, 0u};
+  GradSumOut<E> o{};
+  void *outs[4] = {gA, gB, gC, gD};
+  const int rows[4] = {M, M, P, P}, cols[4] = {M, F, M, F};
+  for (int p = 0; p < 4; ++p) {
+    o.out[p] = static_cast<E *>(outs[p]);
+    o.rows[p] = rows[p];
+    o.cols[p] = cols[p];
+    if (outs[p]) in.want |= 1u << p;
   }
-  hipLaunchKernelGGL(mimo_outer_finish_kernel<E>, dim3(unsigned(orows)), dim3(kOuterThreads), 0, stream,
-                     static_cast<const C *>(scratch), B, blocks, nl, nr, shared, static_cast<E *>(out));
+  o.shared = shared;
+  if (!in.want || B == 0) return PHS_OK;
+  if (T > 0 && (((in.want & 3) && !lam) || ((in.want & 5) && !hs) || ((in.want & 10) && !x) ||
+                ((in.want & 12) && !g)))
+    return PHS_ERR_INVALID;
+  if (B > 65535) return PHS_ERR_INVALID;
+  const int64_t chunk = int64_t(kSumThreads) * kSumSteps;
+  const int64_t blocks = (T + chunk - 1) / chunk;
+  if (blocks > 0) {
+    if (!scratch || scratch_bytes < size_t(B) * size_t(blocks) * kSumN * sizeof(C)) return PHS_ERR_WORKSPACE;
+    hipLaunchKernelGGL(mimo_grad_partial_kernel<E>, dim3(unsigned(blocks), unsigned(B)), dim3(kSumThreads), 0,
+                       stream, in, T, static_cast<C *>(scratch));
+  }
+  hipLaunchKernelGGL(mimo_grad_finish_kernel<E>, dim3(unsigned(B + 1)), dim3(kSumThreads), 0, stream,
+                     static_cast<const C *>(scratch), B, blocks, o);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
@@ -252,17 +310,20 @@ int phs_mimo_ss_rev(int dtype, int M, int F, int P, int64_t B, int64_t T, const 
                         stream);
 }
 
-size_t phs_outer_sums_scratch_size(int dtype, int64_t B, int64_t T) {
+size_t phs_mimo_ss_grad_sums_scratch_size(int dtype, int64_t B, int64_t T) {
   if (B < 0 || T < 0 || (dtype != PHS_F32 && dtype != PHS_F64)) return 0;
-  const int64_t chunk = int64_t(phs::kOuterThreads) * phs::kOuterSteps;
-  return size_t(B) * size_t((T + chunk - 1) / chunk) * phs::kOuterMax * sizeof(double);
+  const int64_t chunk = int64_t(phs::kSumThreads) * phs::kSumSteps;
+  return size_t(B) * size_t((T + chunk - 1) / chunk) * phs::kSumN * sizeof(double);
 }
 
-int phs_outer_sums(int dtype, int64_t B, int64_t T, const void *L, int nl, const void *R, int nr, int shared,
-                   void *out, void *scratch, size_t scratch_bytes, void *stream) {
+int phs_mimo_ss_grad_sums(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *lam, const void *hs,
+                          const void *x, const void *g, int shared, void *gA, void *gB, void *gC, void *gD,
+                          void *scratch, size_t scratch_bytes, void *stream) {
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == PHS_F32) return phs::outer_sums<float>(B, T, L, nl, R, nr, shared, out, scratch, scratch_bytes, st);
-  if (dtype == PHS_F64) return phs::outer_sums<double>(B, T, L, nl, R, nr, shared, out, scratch, scratch_bytes, st);
+  if (dtype == PHS_F32)
+    return phs::grad_sums<float>(M, F, P, B, T, lam, hs, x, g, shared, gA, gB, gC, gD, scratch, scratch_bytes, st);
+  if (dtype == PHS_F64)
+    return phs::grad_sums<double>(M, F, P, B, T, lam, hs, x, g, shared, gA, gB, gC, gD, scratch, scratch_bytes, st);
   return PHS_ERR_DTYPE;
 }
 

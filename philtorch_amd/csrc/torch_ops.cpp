@@ -1055,33 +1055,56 @@ std::vector<Tensor> lpv_ss_backward_hip(const Tensor &A, const std::optional<Ten
   return {gA, gB, gC, gD, gzi, gx};
 }
 
-// sum over time (and the rows, with shared) of L[b, t] R[b, t]^T
-// (phs_outer_sums): L (batch, T, nl), R (batch, T, nr), nl and nr 1-4;
-// returns (batch or 1, nl, nr) in their type.  The coefficient gradients of
-// mimo_ss reduce the forward's and the adjoint's states with it.
-Tensor outer_sums_hip(const Tensor &L, const Tensor &R, bool shared) {
-  TORCH_CHECK(L.dim() == 3 && R.dim() == 3 && L.size(0) == R.size(0) && L.size(1) == R.size(1),
-              "philtorch::outer_sums: L and R must be (batch, T, n) with equal batch and T");
-  TORCH_CHECK(L.size(2) >= 1 && L.size(2) <= 4 && R.size(2) >= 1 && R.size(2) <= 4,
-              "philtorch::outer_sums: widths 1 to 4");
-  TORCH_CHECK(L.scalar_type() == R.scalar_type() && (L.scalar_type() == at::kFloat || L.scalar_type() == at::kDouble),
-              "philtorch::outer_sums: float32 or float64 operands of one type");
-  TORCH_CHECK(L.is_cuda() && R.device() == L.device(), "philtorch::outer_sums: HIP tensors on one device");
-  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(L.device());
-  const int64_t B = L.size(0), T = L.size(1), nl = L.size(2), nr = R.size(2);
-  const int dt = phs_dtype_of(L.scalar_type());
-  Tensor Lc = L.contiguous(), Rc = R.contiguous();
-  Tensor out = at::empty({shared ? 1 : B, nl, nr}, L.options());
-  if (B == 0) {
-    out.zero_();
-    return out;
+// The coefficient gradients of mimo_ss summed over time in one pass
+// (phs_mimo_ss_grad_sums): lam, hs (batch, T, M) (None where no wanted
+// output reads them), x (batch, T, F), g (batch, T, P); `want` and `shared`
+// bit i for A, B, C, D.  Returns [gA, gB, gC, gD], each (batch or 1, rows,
+// cols) as its bit in `shared` says, an empty tensor where not wanted.
+std::vector<Tensor> mimo_ss_grad_sums_hip(const std::optional<Tensor> &lam, const std::optional<Tensor> &hs,
+                                          const Tensor &x, const Tensor &g, int64_t shared, int64_t want) {
+  TORCH_CHECK(x.dim() == 3 && g.dim() == 3 && g.size(0) == x.size(0) && g.size(1) == x.size(1),
+              "philtorch::mimo_ss_grad_sums: x and g must be (batch, T, F) and (batch, T, P)");
+  TORCH_CHECK((want & ~15) == 0 && (shared & ~15) == 0, "philtorch::mimo_ss_grad_sums: want and shared are 4-bit masks");
+  const int64_t B = x.size(0), T = x.size(1), F = x.size(2), P = g.size(2);
+  const bool need_l = want & 3, need_h = want & 5;
+  TORCH_CHECK(!need_l || lam, "philtorch::mimo_ss_grad_sums: gradients of A or B need lam");
+  TORCH_CHECK(!need_h || hs, "philtorch::mimo_ss_grad_sums: gradients of A or C need hs");
+  const Tensor &ref = lam ? *lam : *hs;
+  const int64_t M = (lam || hs) ? ref.size(2) : 1;
+  for (const Tensor *t : {lam ? &*lam : nullptr, hs ? &*hs : nullptr, &x, &g}) {
+    if (!t) continue;
+    TORCH_CHECK(t->dim() == 3 && t->size(0) == B && t->size(1) == T, "philtorch::mimo_ss_grad_sums: (batch, T, n) operands");
+    TORCH_CHECK(t->scalar_type() == x.scalar_type() && t->device() == x.device(),
+                "philtorch::mimo_ss_grad_sums: one dtype and device");
   }
-  Tensor scratch = at::empty({int64_t(std::max<size_t>(phs_outer_sums_scratch_size(dt, B, T), 8))},
-                             L.options().dtype(at::kByte));
-  check_status(phs_outer_sums(dt, B, T, Lc.const_data_ptr(), int(nl), Rc.const_data_ptr(), int(nr), shared ? 1 : 0,
-                              out.mutable_data_ptr(), scratch.mutable_data_ptr(), size_t(scratch.numel()),
-                              stream_of(L)),
-               "outer_sums");
+  if (lam) TORCH_CHECK(lam->size(2) == M, "philtorch::mimo_ss_grad_sums: lam and hs must both have M states");
+  if (hs) TORCH_CHECK(hs->size(2) == M, "philtorch::mimo_ss_grad_sums: lam and hs must both have M states");
+  TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,
+              "philtorch::mimo_ss_grad_sums: float32 or float64 only");
+  TORCH_CHECK(x.is_cuda(), "philtorch::mimo_ss_grad_sums: HIP tensors only");
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor lc = lam ? lam->contiguous() : Tensor(), hc = hs ? hs->contiguous() : Tensor();
+  Tensor xc = x.contiguous(), gc = g.contiguous();
+  const int64_t rows[4] = {M, M, P, P}, cols[4] = {M, F, M, F};
+  std::vector<Tensor> out(4);
+  for (int p = 0; p < 4; ++p) {
+    if ((want >> p) & 1) {
+      out[p] = at::empty({((shared >> p) & 1) ? int64_t(1) : B, rows[p], cols[p]}, x.options());
+      if (B == 0 || T == 0) out[p].zero_();
+    } else {
+      out[p] = at::empty({0}, x.options());
+    }
+  }
+  if (B == 0 || T == 0 || want == 0) return out;
+  Tensor scratch = at::empty({int64_t(std::max<size_t>(phs_mimo_ss_grad_sums_scratch_size(dt, B, T), 8))},
+                             x.options().dtype(at::kByte));
+  auto ptr = [&](int p) { return ((want >> p) & 1) ? out[p].mutable_data_ptr() : nullptr; };
+  check_status(phs_mimo_ss_grad_sums(dt, int(M), int(F), int(P), B, T, lam ? lc.const_data_ptr() : nullptr,
+                                     hs ? hc.const_data_ptr() : nullptr, xc.const_data_ptr(), gc.const_data_ptr(),
+                                     int(shared), ptr(0), ptr(1), ptr(2), ptr(3), scratch.mutable_data_ptr(),
+                                     size_t(scratch.numel()), stream_of(x)),
+               "mimo_ss_grad_sums");
   return out;
 }
 
@@ -1337,7 +1360,8 @@ TORCH_LIBRARY(philtorch, m) {
         {at::Tag::pt2_compliant_tag});
   m.def("mimo_ss(Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? zi, Tensor x, bool reverse=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
-  m.def("outer_sums(Tensor L, Tensor R, bool shared) -> Tensor", {at::Tag::pt2_compliant_tag});
+  m.def("mimo_ss_grad_sums(Tensor? lam, Tensor? hs, Tensor x, Tensor g, int shared, int want) -> Tensor[]",
+        {at::Tag::pt2_compliant_tag});
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
@@ -1366,7 +1390,7 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("lpv_ss", &lpv_ss_hip);
   m.impl("lpv_ss_backward", &lpv_ss_backward_hip);
   m.impl("mimo_ss", &mimo_ss_hip);
-  m.impl("outer_sums", &outer_sums_hip);
+  m.impl("mimo_ss_grad_sums", &mimo_ss_grad_sums_hip);
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CPU, m) {

@@ -14,7 +14,7 @@ steps; both time directions; the forced look-back fallback and
 aggregates-only publishing; empty rows.  Through the torch API: every shape
 branch of the reference's B, C, D rules that the fused route takes, against
 the composed route; gradients (the adjoint pass, the states passes and the
-row sums) against the composed route's and by gradcheck, second order
+fused sums over time) against the composed route's and by gradcheck, second order
 through the composite formula; opcheck.
 """
 import ctypes
@@ -194,43 +194,59 @@ def test_mimo_ss_capi_errors(api):
 
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
-@pytest.mark.parametrize("nl,nr", [(1, 1), (4, 4), (3, 2), (2, 4)])
+@pytest.mark.parametrize("M,F,P", [(1, 1, 1), (4, 4, 4), (3, 2, 1), (2, 4, 3)])
 @pytest.mark.parametrize("Bn,T", [(1, 1), (3, 700), (2, 16384), (2, 16385), (3, 100003)])
-def test_outer_sums_capi(api, dtype, nl, nr, Bn, T):
-    """phs_outer_sums (the coefficient gradients' reductions) against numpy's
-    einsum in fp64, per row and over the rows, across its 16384-step blocks."""
+def test_mimo_ss_grad_sums_capi(api, dtype, M, F, P, Bn, T):
+    """phs_mimo_ss_grad_sums (the coefficient gradients' sums over time)
+    against numpy's einsum in fp64: every product per row and over the rows,
+    subsets of the products, across its 16384-step blocks."""
     import torch
 
     lib, ws, capi = api
-    g = D.rng(D.seed_of("outer", np.dtype(dtype).name, nl, nr, Bn, T))
-    Lh, Rh = g.standard_normal((Bn, T, nl)).astype(dtype), g.standard_normal((Bn, T, nr)).astype(dtype)
-    L, R = _dev(Lh), _dev(Rh)
+    g = D.rng(D.seed_of("grad-sums", np.dtype(dtype).name, M, F, P, Bn, T))
+    hl = {n: g.standard_normal((Bn, T, w)).astype(dtype) for n, w in (("lam", M), ("hs", M), ("x", F), ("g", P))}
+    dv = {n: _dev(v) for n, v in hl.items()}
+    w64 = {n: v.astype(np.float64) for n, v in hl.items()}
+    refs = [np.einsum("bti,btj->bij", w64[l], w64[r]) for l, r in (("lam", "hs"), ("lam", "x"), ("g", "hs"), ("g", "x"))]
+    dims = [(M, M), (M, F), (P, M), (P, F)]
     dt = capi.DTYPES[np.dtype(dtype)]
-    need = lib.phs_outer_sums_scratch_size(dt, Bn, T)
+    need = lib.phs_mimo_ss_grad_sums_scratch_size(dt, Bn, T)
     assert 0 < need <= ws.numel()
-    ref = np.einsum("bti,btj->bij", Lh.astype(np.float64), Rh.astype(np.float64))
-    for shared in (0, 1):
-        out = torch.full((1 if shared else Bn, nl, nr), float("nan"), dtype=L.dtype, device="cuda")
-        print(f"outer_sums nl={nl} nr={nr} B={Bn} T={T} shared={shared}", flush=True)
-        rc = lib.phs_outer_sums(dt, Bn, T, _p(L), nl, _p(R), nr, shared, _p(out), _p(ws), need,
-                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    for want, shared in ((15, 0), (15, 15), (9, 1), (6, 4)):
+        outs = [torch.full(((1 if (shared >> i) & 1 else Bn),) + dims[i], float("nan"), dtype=dv["x"].dtype,
+                           device="cuda") if (want >> i) & 1 else None for i in range(4)]
+        print(f"grad_sums M={M} F={F} P={P} B={Bn} T={T} want={want} shared={shared}", flush=True)
+        rc = lib.phs_mimo_ss_grad_sums(dt, M, F, P, Bn, T, _p(dv["lam"]), _p(dv["hs"]), _p(dv["x"]), _p(dv["g"]),
+                                       shared, *(_p(o) for o in outs), _p(ws), need,
+                                       ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         assert rc == capi.PHS_OK, lib.phs_error_string(rc)
         torch.cuda.synchronize()
-        want = ref.sum(0, keepdims=True) if shared else ref
-        # sums of T products: the bound scales with sqrt(T) times the terms' size
-        D.check(out.cpu().numpy(), want, f"outer shared={shared}", dtype=dtype, scale=np.sqrt(Bn * T))
+        for i in range(4):
+            if outs[i] is None:
+                continue
+            want_i = refs[i].sum(0, keepdims=True) if (shared >> i) & 1 else refs[i]
+            # sums of T products: the bound scales with sqrt(T) times the terms' size
+            D.check(outs[i].cpu().numpy(), want_i, f"product {i} shared={shared}", dtype=dtype,
+                    scale=np.sqrt(Bn * T))
 
 
-def test_outer_sums_op_and_empty_rows(hip):
+def test_mimo_ss_grad_sums_op_and_empty_rows(hip):
     import torch
 
-    L = torch.randn(3, 5000, 2, device="cuda", dtype=torch.float64)
-    R = torch.randn(3, 5000, 3, device="cuda", dtype=torch.float64)
-    torch.testing.assert_close(torch.ops.philtorch.outer_sums(L, R, False), torch.einsum("bti,btj->bij", L, R))
-    torch.testing.assert_close(torch.ops.philtorch.outer_sums(L, R, True)[0], torch.einsum("bti,btj->ij", L, R))
-    E = torch.empty(2, 0, 3, device="cuda")
-    assert torch.ops.philtorch.outer_sums(E, torch.empty(2, 0, 1, device="cuda"), False).abs().sum() == 0
-    torch.library.opcheck(torch.ops.philtorch.outer_sums.default, (L.float(), R.float(), True))
+    t = lambda *s: torch.randn(*s, device="cuda", dtype=torch.float64)  # noqa: E731
+    lam, hs, x, g = t(3, 5000, 2), t(3, 5000, 2), t(3, 5000, 3), t(3, 5000, 4)
+    gA, gB, gC, gD = torch.ops.philtorch.mimo_ss_grad_sums(lam, hs, x, g, 0b1010, 15)
+    torch.testing.assert_close(gA, torch.einsum("bti,btj->bij", lam, hs))
+    torch.testing.assert_close(gB[0], torch.einsum("bti,btj->ij", lam, x))
+    torch.testing.assert_close(gC, torch.einsum("bti,btj->bij", g, hs))
+    torch.testing.assert_close(gD[0], torch.einsum("bti,btj->ij", g, x))
+    none = torch.ops.philtorch.mimo_ss_grad_sums(None, None, x, g, 0, 8)
+    assert [v.numel() for v in none[:3]] == [0, 0, 0]
+    torch.testing.assert_close(none[3], torch.einsum("bti,btj->bij", g, x))
+    e = torch.ops.philtorch.mimo_ss_grad_sums(None, None, x[:, :0], g[:, :0], 8, 8)
+    assert e[3].shape == (1, 4, 3) and e[3].abs().sum() == 0
+    f = lambda v: v.float()  # noqa: E731
+    torch.library.opcheck(torch.ops.philtorch.mimo_ss_grad_sums.default, (f(lam), f(hs), f(x), f(g), 5, 15))
 
 
 # ---------------------------------------------------------------- torch API

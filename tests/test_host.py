@@ -437,17 +437,18 @@ def test_capi_mimo_state_space_host_only_calls():
         assert mimo(**bad) == capi.PHS_ERR_INVALID, bad
     assert mimo(wsb=lib.phs_mimo_ss_workspace_size(0, 2, 2, 100) - 1) == capi.PHS_ERR_WORKSPACE
     assert mimo(B=0) == capi.PHS_OK
-    # outer-product sums: sizes and argument errors
-    assert lib.phs_outer_sums_scratch_size(0, 16, 480000) >= 16 * 30 * 16 * 8
-    assert lib.phs_outer_sums_scratch_size(2, 16, 100) == 0
+    # the coefficient-gradient sums: sizes and argument errors
+    assert lib.phs_mimo_ss_grad_sums_scratch_size(0, 16, 480000) >= 16 * 30 * 64 * 8
+    assert lib.phs_mimo_ss_grad_sums_scratch_size(2, 16, 100) == 0
 
-    def osum(dt=0, nl=2, nr=3, shared=0, sb=1 << 20, out=d):
-        return lib.phs_outer_sums(dt, 2, 100, d, nl, d, nr, shared, out, d, sb, None)
+    def gsum(dt=0, M=2, F=2, P=3, shared=0, sb=1 << 20, lam=d, gA=d, gD=None):
+        return lib.phs_mimo_ss_grad_sums(dt, M, F, P, 2, 100, lam, d, d, d, shared, gA, None, None, gD, d, sb, None)
 
-    assert osum(dt=2) == capi.PHS_ERR_DTYPE
-    for bad in (dict(nl=0), dict(nr=5), dict(shared=2), dict(out=None)):
-        assert osum(**bad) == capi.PHS_ERR_INVALID, bad
-    assert osum(sb=8) == capi.PHS_ERR_WORKSPACE
+    assert gsum(dt=2) == capi.PHS_ERR_DTYPE
+    for bad in (dict(M=0), dict(F=5), dict(P=0), dict(shared=16), dict(lam=None)):
+        assert gsum(**bad) == capi.PHS_ERR_INVALID, bad
+    assert gsum(sb=8) == capi.PHS_ERR_WORKSPACE
+    assert gsum(gA=None) == capi.PHS_OK  # nothing wanted: nothing launched
 
 
 def _mimo_shape_cases(batch, M):
