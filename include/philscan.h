@@ -575,6 +575,30 @@ int phs_mimo_ss_rev(int dtype, int M, int F, int P, int64_t B, int64_t T, const 
                     const void *Cm, const void *Dm, int shared, const void *zi, const void *x, void *y, void *zf,
                     void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- Multi-input, multi-output LPV (time-varying A) state space of order
+ * M = 1..4 with F = 1..4 inputs and P = 1..4 outputs per step, fused.
+ * Replaces philtorch.lpv.state_space (philtorch/lpv/ssm.py:337-581) for a
+ * 3D x or matrix-valued B, C, D constant in time: the composed route's B x
+ * (:413-454), the LPV scan (_ext_ss_recur), the state shift (:462-474) and
+ * C h + D x (:480-577) in one pass:
+ *     h[0] = zi,  y[t] = C h[t] + D x[t],  h[t+1] = A[t] h[t] + B x[t],  zf = h[T]
+ * A [B,T,M,M], or [T,M,M] with PHS_LPV_A_SHARED in A_flags
+ * (PHS_LPV_A_TRANSPOSED: use A[t]^T); Bm [B,M,F], Cm [B,P,M], Dm [B,P,F]
+ * with their PHS_MIMO_{B,C,D}_SHARED bits in `shared` (one matrix, no row
+ * axis); Dm NULL: no feedthrough; zi [B,M] (NULL = zeros); x [B,T,F], y
+ * [B,T,P]; zf [B,M] (skipped when NULL; zi when T = 0).  reverse != 0 runs
+ * the model backwards in time (no counterpart in the reference, which
+ * flips): h[T] = zi, y[t] = C h[t+1] + D x[t], h[t] = A[t] h[t+1] + B x[t],
+ * zf = h[0]; on the adjoint model (A[t]^T, C^T, B^T, D^T) from dL/dzf it
+ * gives grad_x and grad_zi, and with C the identity the adjoint states.
+ * `workspace`: phs_lpv_mimo_ss_workspace_size bytes, under the conventions
+ * above. */
+size_t phs_lpv_mimo_ss_workspace_size(int dtype, int M, int64_t B, int64_t T);
+
+int phs_lpv_mimo_ss(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *A, int A_flags,
+                    const void *Bm, const void *Cm, const void *Dm, int shared, const void *zi, const void *x,
+                    void *y, void *zf, int reverse, void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- The coefficient gradients of phs_mimo_ss_fwd summed over time in one
  * pass (no counterpart in the reference, whose autograd forms them as
  * matmuls over the composed route's tensors; philtorch/lti/ssm.py:460-589):

@@ -327,6 +327,33 @@ def lpv_state_space(A, x, B=None, C=None, D=None, zi=None, out_idx=None, nthread
     return _c(y, dt), _c(zf, dt)
 
 
+def lpv_state_space_mimo(A, x, B, C, D=None, zi=None, nthreads=None):
+    """philtorch.lpv.state_space with matrix operands constant in time
+    (philtorch/lpv/ssm.py:337-581 for a 3D input): x [Bn,T,F]; A [T,M,M] or
+    [Bn,T,M,M]; B [M,F] or [Bn,M,F]; C [P,M] or [Bn,P,M]; D None, [P,F] or
+    [Bn,P,F].  Bx[t] = B x[t] (:413-454), the LPV scan recurN, the state
+    sequence shifted one step behind zi (:462-474), then y = C h + D x
+    (:480-577).  Returns (y [Bn,T,P], zf [Bn,M])."""
+    dt = np.asarray(x).dtype
+    x = _c(x, dt)
+    Bn, T, F = x.shape
+    M = np.shape(A)[-1]
+    A = _c(np.broadcast_to(A, (Bn, T, M, M)), dt)
+    Bm = np.broadcast_to(np.asarray(B, dtype=dt), (Bn, M, F))
+    Cm = np.asarray(C, dtype=dt)
+    P = Cm.shape[-2]
+    Cm = np.broadcast_to(Cm, (Bn, P, M))
+    zi = np.zeros((Bn, M), dtype=dt) if zi is None else _c(np.broadcast_to(zi, (Bn, M)), dt)
+    Bx = np.einsum("bmf,btf->btm", Bm, x)
+    h = recurN(A, zi, _c(Bx, dt), nthreads)
+    zf = h[:, -1] if T > 0 else zi.copy()
+    hprev = np.concatenate([zi[:, None, :], h[:, :-1]], axis=1)[:, :T]
+    y = np.einsum("bpm,btm->btp", Cm, hprev)
+    if D is not None:
+        y = y + np.einsum("bpf,btf->btp", np.broadcast_to(np.asarray(D, dtype=dt), (Bn, P, F)), x)
+    return _c(y, dt), _c(zf, dt)
+
+
 def _tdf2_companion(b, a):
     """TDF-II model of lfilter(b, a) per row (philtorch/lti/filtering.py:
     107-142 and :273-333, transpose=True): b [R,nb], a [R,na] (after the

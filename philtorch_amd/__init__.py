@@ -12,9 +12,10 @@ fused single-input single-output state space ``lti_ss`` (behind
 ``lti.state_space``), ``lfilter_ss``, ``lfilter`` of order <= 4 from b and
 a in one pass (behind ``lti.lfilter``), ``lpv_ss``, the time-varying
 single-input single-output state space of order <= 4 (behind
-``lpv.state_space``), and ``mimo_ss``, the LTI state space of order <= 4
+``lpv.state_space``), ``mimo_ss``, the LTI state space of order <= 4
 with up to four inputs and outputs per step (behind ``lti.state_space``
-for a 3D x or matrix-valued B, C, D).  This module then
+for a 3D x or matrix-valued B, C, D), and ``lpv_mimo_ss``, its LPV form
+(behind ``lpv.state_space``).  This module then
 registers fake (meta) kernels and autograd formulas for them, as
 philtorch/__init__.py:157-268 does for its ops.
 
@@ -903,6 +904,87 @@ if EXTENSION_LOADED and _has_op("mimo_ss"):
         return tuple(out)
 
     torch.library.register_autograd("philtorch::mimo_ss", _mimo_ss_backward, setup_context=_mimo_ss_setup)
+
+if EXTENSION_LOADED and _has_op("lpv_mimo_ss"):
+    # LPV state space (A[t]) with F inputs and P outputs per step (F, P <= 4),
+    # B, C, D constant in time: (y, zf)
+    @torch.library.register_fake("philtorch::lpv_mimo_ss")
+    def _(A, B, C, D, zi, x, reverse=False, transpose_A=False):
+        torch._check(x.ndim == 3, lambda: "x must be 3D (batch, time, features)")
+        torch._check(A.ndim in (3, 4) and A.shape[-1] == A.shape[-2], lambda: "A must be (T, M, M) or (batch, T, M, M)")
+        torch._check(C.ndim in (2, 3), lambda: "C must be (P, M) or (batch, P, M)")
+        return x.new_empty((x.shape[0], x.shape[1], C.shape[-2])), x.new_empty((x.shape[0], A.shape[-1]))
+
+    def _lpv_mimo_ss_setup(ctx, inputs, output):
+        ctx.reverse = bool(inputs[6]) if len(inputs) > 6 else False
+        ctx.transpose_A = bool(inputs[7]) if len(inputs) > 7 else False
+        ctx.save_for_backward(*inputs[:6])
+        ctx.set_materialize_grads(False)
+
+    def _lpv_mimo_ss_backward(ctx, gy, gzf):
+        """The adjoint model (A[t]^T read in place, input matrix C^T, output
+        matrix B^T, D^T) in the opposite time direction from dL/dzf gives
+        grad_x and grad_zi in one more lpv_mimo_ss pass.  The coefficients:
+        the states h[t] (the forward again with C = I, no D) and the adjoint
+        states lambda[t+1] (the adjoint pass with output matrix I), then
+        dL/dA[t] = lambda[t+1] h[t]^T per step (summed over the rows for a
+        shared A) and the sums over time of lambda x^T, g h^T, g x^T for B,
+        C, D (philtorch::mimo_ss_grad_sums).  Under create_graph: the
+        gradient of the composite the fused kernel replaces (B x, the native
+        LPV scan, the state shift, C h + D x; philtorch/lpv/ssm.py:337-581),
+        recomputed from the inputs and differentiable again."""
+        from .lpv.ssm import _lpv_mimo_composite
+
+        inputs = ctx.saved_tensors
+        A, B, C, D, zi, x = inputs
+        needs = ctx.needs_input_grad
+        out = [None] * 8
+        if torch.is_grad_enabled():  # create_graph
+            wrt = [i for i, t in enumerate(inputs) if t is not None and needs[i]]
+            with torch.enable_grad():
+                y, zf = _lpv_mimo_composite(*inputs, reverse=ctx.reverse, transpose_A=ctx.transpose_A)
+                outs, grads = [y], [gy if gy is not None else torch.zeros_like(y)]
+                if gzf is not None:
+                    outs.append(zf)
+                    grads.append(gzf)
+                res = torch.autograd.grad(outs, [inputs[i] for i in wrt], grads, create_graph=True,
+                                          allow_unused=True)
+            for i, g in zip(wrt, res):
+                out[i] = g if g is not None else torch.zeros_like(inputs[i])
+            return tuple(out)
+        M = A.size(-1)
+        g = gy if gy is not None else x.new_zeros(x.size(0), x.size(1), C.size(-2))
+        Ct = C.mT.contiguous()
+        eye = torch.eye(M, dtype=x.dtype, device=x.device)
+        rev, tr = ctx.reverse, ctx.transpose_A
+        op = torch.ops.philtorch.lpv_mimo_ss
+        with _op_ctx():
+            if needs[5] or (needs[4] and zi is not None):
+                gx, gzi = op(A, Ct, B.mT.contiguous(), D.mT.contiguous() if D is not None else None, gzf, g,
+                             not rev, not tr)
+                out[5] = gx if needs[5] else None
+                out[4] = gzi if needs[4] and zi is not None else None
+            hs = lam = None
+            if needs[0] or needs[2]:
+                hs, _ = op(A, B, eye, None, zi, x, rev, tr)
+            if needs[0] or needs[1]:
+                lam, _ = op(A, Ct, eye, None, gzf, g, not rev, not tr)
+            if needs[0]:
+                gA = lam.unsqueeze(-1) * hs.unsqueeze(-2)  # dL/dA[t] = lambda[t+1] h[t]^T
+                if tr:
+                    gA = gA.mT
+                out[0] = gA.sum(0) if A.dim() == 3 else gA
+            want = sum(1 << i for i in (1, 2, 3) if needs[i] and inputs[i] is not None)
+            if want:
+                shared = sum(1 << i for i, t in enumerate((A, B, C, D)) if i > 0 and t is not None and t.dim() == 2)
+                sums = torch.ops.philtorch.mimo_ss_grad_sums(lam, hs, x, g, shared, want)
+                for i in (1, 2, 3):
+                    if (want >> i) & 1:
+                        out[i] = sums[i][0] if (shared >> i) & 1 else sums[i]
+        return tuple(out)
+
+    torch.library.register_autograd("philtorch::lpv_mimo_ss", _lpv_mimo_ss_backward,
+                                    setup_context=_lpv_mimo_ss_setup)
 
 from . import mat  # noqa: E402,F401
 from . import lti  # noqa: E402,F401

@@ -1,6 +1,6 @@
-// C ABI of the fused multi-input, multi-output LTI state space (declared in
-// include/philscan.h): argument checks, workspace carving and the launch of
-// mimo_ss_kernel on the caller's stream.  No allocation and no
+// C ABI of the fused multi-input, multi-output state spaces, LTI and LPV
+// (declared in include/philscan.h): argument checks, workspace carving and
+// the launches of mimo_ss_kernel and lpv_mimo_kernel on the caller's stream.  No allocation and no
 // synchronisation.  Workspace layout: [0, 2048) claim header, then the status
 // words of every (row, tile).
 #include "phs_launch.hpp"
@@ -258,6 +258,77 @@ int grad_sums(int M, int F, int P, int64_t B, int64_t T, const void *lam, const 
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
+// ---- the time-varying model (lpv_mimo_kernel)
+template <class Alg>
+size_t lpv_mimo_ws_bytes(int64_t B, int64_t T) {
+  const int64_t tiles = (T + LpvMimoShape<Alg>::kTile - 1) / LpvMimoShape<Alg>::kTile;
+  return align_up(align_up(kHeaderBytes) + size_t(B) * size_t(tiles) * StatusShape<Alg>::kStride * sizeof(uint64_t));
+}
+
+template <class Alg>
+int lpv_mimo_ss(int F, int P, int64_t B, int64_t T, const void *A, int A_flags, const void *Bm, const void *Cm,
+                const void *Dm, int shared, const void *zi, const void *x, void *y, void *zf, void *workspace,
+                size_t ws_bytes, bool rev, hipStream_t stream) {
+  using E = typename Alg::elem;
+  using Sh = LpvMimoShape<Alg>;
+  constexpr int M = SsView<Alg>::M;
+  if (B < 0 || T < 0 || F < 1 || F > kMimoMaxIO || P < 1 || P > kMimoMaxIO) return PHS_ERR_INVALID;
+  if ((shared & ~(PHS_MIMO_B_SHARED | PHS_MIMO_C_SHARED | PHS_MIMO_D_SHARED)) ||
+      (A_flags & ~(PHS_LPV_A_SHARED | PHS_LPV_A_TRANSPOSED)))
+    return PHS_ERR_INVALID;
+  if (B == 0) return PHS_OK;
+  if (T == 0) {
+    if (zf) {
+      const int64_t n = B * M;
+      hipLaunchKernelGGL(mimo_empty_zf_kernel<E>, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
+                         static_cast<const E *>(zi), n, static_cast<E *>(zf));
+      return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
+    }
+    return PHS_OK;
+  }
+  if (!A || !Bm || !Cm || !x || !y) return PHS_ERR_INVALID;
+  const int64_t tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
+  if (double(B) * double(tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
+  if (!workspace || ws_bytes < lpv_mimo_ws_bytes<Alg>(B, T)) return PHS_ERR_WORKSPACE;
+  char *ws = static_cast<char *>(workspace);
+  MimoArgs<Alg> a{};
+  a.A = static_cast<const E *>(A);
+  a.A_stride = (A_flags & PHS_LPV_A_SHARED) ? 0 : T * M * M;
+  a.A_trans = (A_flags & PHS_LPV_A_TRANSPOSED) ? 1 : 0;
+  a.A_vec = aligned16(A) && (size_t(T) * M * M * sizeof(E)) % 16 == 0;
+  a.Bm = static_cast<const E *>(Bm);
+  a.b_stride = (shared & PHS_MIMO_B_SHARED) ? 0 : int64_t(M) * F;
+  a.Cm = static_cast<const E *>(Cm);
+  a.c_stride = (shared & PHS_MIMO_C_SHARED) ? 0 : int64_t(P) * M;
+  a.Dm = static_cast<const E *>(Dm);
+  a.d_stride = (shared & PHS_MIMO_D_SHARED) ? 0 : int64_t(P) * F;
+  a.F = F;
+  a.P = P;
+  a.f_magic = io_magic(F);
+  a.p_magic = io_magic(P);
+  a.zi = static_cast<const E *>(zi);
+  a.x = static_cast<const E *>(x);
+  a.y = static_cast<E *>(y);
+  a.zf = static_cast<E *>(zf);
+  a.B = B;
+  a.T_len = T;
+  a.tiles_per_row = tiles_per_row;
+  row_split(B, a.b_magic, a.b_shift);
+  a.claims = reinterpret_cast<unsigned long long *>(ws);
+  a.status = reinterpret_cast<uint64_t *>(ws + align_up(kHeaderBytes));
+  a.tiles = unsigned(B * tiles_per_row);
+  a.per_stripe = (a.tiles + kStripes - 1) / kStripes;
+  const unsigned sl = g_spin_limit.load(std::memory_order_relaxed);
+  a.spin_limit = sl ? sl : kDefaultSpinLimit;
+  a.agg_only = g_agg_only.load(std::memory_order_relaxed) ? 1u : 0u;
+  const dim3 grid(a.per_stripe * kStripes), block(Sh::kThreads);
+  if (rev)
+    launch_kernel((lpv_mimo_kernel<Alg, true>), grid, block, 0, stream, a);
+  else
+    launch_kernel((lpv_mimo_kernel<Alg, false>), grid, block, 0, stream, a);
+  return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
+}
+
 template <class Fn>
 int mimo_dispatch(int dtype, int M, Fn &&f) {
   if (dtype != PHS_F32 && dtype != PHS_F64) return PHS_ERR_DTYPE;
@@ -308,6 +379,26 @@ int phs_mimo_ss_rev(int dtype, int M, int F, int P, int64_t B, int64_t T, const 
                     void *workspace, size_t workspace_bytes, void *stream) {
   return phs::mimo_call(dtype, M, F, P, B, T, A, Bm, Cm, Dm, shared, zi, x, y, zf, workspace, workspace_bytes, true,
                         stream);
+}
+
+size_t phs_lpv_mimo_ss_workspace_size(int dtype, int M, int64_t B, int64_t T) {
+  if (B < 0 || T < 0) return 0;
+  size_t out = 0;
+  const int rc = phs::mimo_dispatch(dtype, M, [&](auto alg) {
+    out = phs::lpv_mimo_ws_bytes<decltype(alg)>(B, T);
+    return PHS_OK;
+  });
+  return rc == PHS_OK ? out : 0;
+}
+
+int phs_lpv_mimo_ss(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *A, int A_flags,
+                    const void *Bm, const void *Cm, const void *Dm, int shared, const void *zi, const void *x,
+                    void *y, void *zf, int reverse, void *workspace, size_t workspace_bytes, void *stream) {
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return phs::mimo_dispatch(dtype, M, [&](auto alg) {
+    return phs::lpv_mimo_ss<decltype(alg)>(F, P, B, T, A, A_flags, Bm, Cm, Dm, shared, zi, x, y, zf, workspace,
+                                           workspace_bytes, reverse != 0, st);
+  });
 }
 
 size_t phs_mimo_ss_grad_sums_scratch_size(int dtype, int64_t B, int64_t T) {

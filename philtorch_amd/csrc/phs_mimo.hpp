@@ -26,7 +26,7 @@
 // before every step, which the coefficient gradients reduce against.
 #pragma once
 
-#include "phs_ss.hpp"
+#include "phs_lpvss.hpp"
 
 namespace phs {
 
@@ -37,8 +37,10 @@ constexpr int kMimoMaxIO = 4;
 template <class Alg>
 struct MimoArgs {
   using E = typename Alg::elem;
-  const E *A;  // [rows, M, M] row-major
+  const E *A;  // [rows, M, M] row-major; time-varying (lpv_mimo_kernel): [rows, T, M, M]
   int64_t A_stride;  // elements between rows (0 = shared)
+  int A_trans;       // time-varying: read each step's matrix transposed (the adjoint model's A[t]^T)
+  int A_vec;         // time-varying: a row's matrices lie in whole 16-byte vectors
   const E *Bm;  // [rows, M, F]
   int64_t b_stride;
   const E *Cm;  // [rows, P, M]
@@ -197,11 +199,10 @@ __device__ __forceinline__ void mimo_block_range(int64_t base, int64_t lim, int 
 // row read 0.  The global side is the span's contiguous block of 64 K W
 // elements, lane-strided (element e = i 64 + lane is step e / W, feature
 // e % W of the block).
-template <class Alg, bool REV>
+template <class Alg, bool REV, class Sh = MimoShape<Alg>>
 __device__ __forceinline__ void mimo_stage_in(const typename Alg::elem *row, int64_t s0, int64_t T, int W,
                                               uint64_t w_magic, typename Alg::elem *lds, int lane) {
   using E = typename Alg::elem;
-  using Sh = MimoShape<Alg>;
   constexpr int S = Sh::kSpan, K = Sh::K, kMax = K * kMimoMaxIO;
   // the block starts at element `base` of the row (negative or past the row
   // for the spans that leave it); its elements [lo, hi) lie inside the row
@@ -229,11 +230,10 @@ __device__ __forceinline__ void mimo_stage_in(const typename Alg::elem *row, int
 
 // The inverse of mimo_stage_in for a wave's outputs: W planes out to the
 // span's block of the [T, W] row; steps outside the row are not written.
-template <class Alg, bool REV>
+template <class Alg, bool REV, class Sh = MimoShape<Alg>>
 __device__ __forceinline__ void mimo_stage_out(typename Alg::elem *row, int64_t s0, int64_t T, int W,
                                                uint64_t w_magic, const typename Alg::elem *lds, int lane) {
   using E = typename Alg::elem;
-  using Sh = MimoShape<Alg>;
   constexpr int S = Sh::kSpan, K = Sh::K, kMax = K * kMimoMaxIO;
   const int64_t base = (REV ? T - s0 - S : s0) * W;
   const int n = K * W;
@@ -455,6 +455,209 @@ __global__ __launch_bounds__(MimoShape<Alg>::kThreads, MimoShape<Alg>::kMinWaves
   }
   wave_sync();  // the span's outputs are in the planes
   mimo_stage_out<Alg, REV>(a.y + b * T * a.P, s0, T, a.P, a.p_magic, yout, lane);
+}
+
+// ---------------------------------------------------------------- time-varying A
+// The LPV (parameter-varying) model with several inputs and outputs
+// (philtorch/lpv/ssm.py:337-581 with a 3D x or matrix-valued B, C, D that
+// are constant in time):
+//     h[0] = zi,  y[t] = C h[t] + D x[t],  h[t+1] = A[t] h[t] + B x[t],  zf = h[T]
+// A is [rows, T, M, M]; B, C, D and the staging of x and y are the LTI
+// kernel's.  Every step has its own matrix, so the scan is the generic
+// time-varying one (phs_scan.hpp), as in lpv_ss_kernel: a lane folds its K
+// steps (A[t], B x[t]) into a map, wave scans of maps chain the lanes, and
+// the look-back resolves map status words.  K is 32 bytes of state-order-2
+// coefficients' worth (fp32 8, fp64 4 steps; orders 3-4 half that: a lane
+// holds its K matrices).
+template <class Alg>
+struct LpvMimoShape {
+  using E = typename Alg::elem;
+  static constexpr int kM = SsView<Alg>::M;
+  static constexpr int kWaves = 3;
+  static constexpr int kThreads = 64 * (kWaves + 1);
+  static constexpr int K = (kM <= 2 ? 32 : 16) / int(sizeof(E));
+  static constexpr int kSpan = 64 * K;
+  static constexpr int kTile = kWaves * kSpan;
+  static constexpr int kPlane = kSpan + 16 / int(sizeof(E));
+  static constexpr int kWaveElems = kMimoMaxIO * kPlane;
+};
+
+// A lane's K matrices A[t] in scan order from scan position s0 (past the
+// row: zero), transposed where the adjoint reads them so.
+template <class Alg, bool REV, int K>
+__device__ __forceinline__ void lpv_mimo_load_A(const MimoArgs<Alg> &a, int64_t b, int64_t s0,
+                                                typename Alg::s_coef (&Ak)[K]) {
+  using SC = typename Alg::s_coef;
+  const SC *row = reinterpret_cast<const SC *>(a.A + b * a.A_stride);
+  lpv_load<REV, SC, K>(row, s0, a.T_len, a.A_vec != 0, Ak, Alg::s_czero());
+  if (a.A_trans) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) Ak[k] = Alg::s_adjoint(Ak[k]);  // real: the transpose
+  }
+}
+
+// State entering tile position `span` of a row, folded from the inputs (the
+// look-back's bounded-wait fallback; out of line, cold).
+template <class Alg, bool REV>
+__device__ __noinline__ typename Alg::state lpv_mimo_prefix_fallback(const MimoArgs<Alg> *ap, int64_t b,
+                                                                    int64_t span, int lane,
+                                                                    typename Alg::state virt) {
+  const MimoArgs<Alg> &a = *ap;
+  using E = typename Alg::elem;
+  using SC = typename Alg::s_coef;
+  using SS = typename Alg::s_state;
+  using M = Map<Alg>;
+  constexpr int K = LpvMimoShape<Alg>::K;
+  auto op = [](const M &p, const M &q) { return compose<Alg>(p, q); };
+  const MimoIn<Alg> mdl = mimo_in<Alg>(a, b);  // (its A is not read)
+  const E *xrow = a.x + b * a.T_len * a.F;
+  const SC dummy = Alg::s_czero();
+  M acc = map_identity<Alg>();
+  for (int64_t off = 0; off < span; off += 64 * K) {
+    const int64_t c0 = off + int64_t(lane) * K;
+    SC Ak[K];
+    lpv_mimo_load_A<Alg, REV, K>(a, b, c0, Ak);
+    SS xs[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int64_t s = c0 + k;
+      E u[kMimoMaxIO];
+#pragma unroll
+      for (int f = 0; f < kMimoMaxIO; ++f) {
+        u[f] = E(0);
+        if (f < a.F && s < a.T_len) u[f] = xrow[mimo_time<REV>(s, a.T_len) * a.F + f];
+      }
+      xs[k] = mimo_bx<Alg>(mdl, u);
+    }
+    M m = lane_map<Alg, true, false, K>(Ak, xs, dummy);
+    m = wave_scan_incl(m, lane, op);
+    acc = compose<Alg>(acc, read_lane(m, 63));
+  }
+  return apply<Alg>(acc, virt);
+}
+
+template <class Alg, bool REV>
+__global__ __launch_bounds__(LpvMimoShape<Alg>::kThreads, 2) void lpv_mimo_kernel(MimoArgs<Alg> a) {
+  using E = typename Alg::elem;
+  using S = typename Alg::state;
+  using SC = typename Alg::s_coef;
+  using SS = typename Alg::s_state;
+  using M = Map<Alg>;
+  using V = SsView<Alg>;
+  using Sh = LpvMimoShape<Alg>;
+  using St = StatusShape<Alg>;
+  constexpr int K = Sh::K, kWaves = Sh::kWaves, kP = Sh::kPlane;
+
+  __shared__ M s_wagg[kWaves];
+  __shared__ M s_wpre[kWaves];
+  __shared__ S s_in;
+  __shared__ unsigned s_id, s_tag;
+  __shared__ uint64_t s_look[St::kLookWords];
+  __shared__ E s_io[kWaves * Sh::kWaveElems];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t id = blockIdx.x;
+  if (id >= a.tiles) {  // padding of the last stripe round: counted, then gone
+    if (tid == 0) claim_tile(a.claims, a.per_stripe, s_id, s_tag);
+    return;
+  }
+  unsigned tag = 0;
+  int64_t q, b;  // tile position along the row, row
+  split_tile(id, a.B, a.b_magic, a.b_shift, q, b);
+  const int64_t T = a.T_len;
+  auto op = [](const M &p, const M &q2) { return compose<Alg>(p, q2); };
+
+  if (w == kWaves) {
+    // ================= look-back wave
+    tag = claim_tag(a.claims, a.per_stripe, lane);
+    uint64_t *row_status = a.status + b * a.tiles_per_row * St::kStride;
+    const S virt = a.zi ? Alg::load_s(V::load_vec(a.zi + b * V::M)) : Alg::szero();
+    __syncthreads();  // wave aggregates are in s_wagg
+    M v = lane < kWaves ? s_wagg[lane] : map_identity<Alg>();
+    v = wave_scan_incl(v, lane, op);
+    const M wex = wave_shift_up(v, lane, map_identity<Alg>());
+    if (lane < kWaves) s_wpre[lane] = wex;
+    const M tagg = read_lane(v, kWaves - 1);
+    S yin = virt;
+    if (q > 0) {
+      if (lane == 0) publish(row_status + q * St::kStride + St::kIncWords, tagg, tag);
+      Lookback<Alg> lb = lookback_start<Alg>(q);
+      if (!lookback<Alg>(row_status, virt, lane, tag, a.spin_limit, s_look, lb, yin))
+        yin = lpv_mimo_prefix_fallback<Alg, REV>(kernel_args<MimoArgs<Alg>>(), b, q * Sh::kTile, lane, virt);
+    }
+    if (q + 1 < a.tiles_per_row && lane == 0 && !(a.agg_only && q > 0))
+      publish(row_status + q * St::kStride, apply<Alg>(tagg, yin), tag);
+    if (lane == 0) s_in = yin;
+    __syncthreads();  // entry state is in s_in
+    return;
+  }
+
+  // ================= data waves
+  E *io = s_io + w * Sh::kWaveElems;  // F input planes, then P output planes
+  const int64_t s0 = q * Sh::kTile + int64_t(w) * Sh::kSpan;  // the wave's first scan position
+  mimo_stage_in<Alg, REV, Sh>(a.x + b * T * a.F, s0, T, a.F, a.f_magic, io, lane);
+  SC Ak[K];
+  lpv_mimo_load_A<Alg, REV, K>(a, b, s0 + int64_t(lane) * K, Ak);
+  const MimoIn<Alg> mi = mimo_in<Alg>(a, b);  // (its A is not read)
+  wave_sync();  // the span's inputs are in the planes
+
+  auto inputs = [&](int k, E (&u)[kMimoMaxIO]) {
+#pragma unroll
+    for (int f = 0; f < kMimoMaxIO; ++f) u[f] = f < a.F ? io[f * kP + lane * K + k] : E(0);
+  };
+
+  // ---- pass 1: the lane map of (A[t], B x[t]) over its K steps, the wave
+  // scan.  Steps past the row's end carry a zero matrix and input and only
+  // touch the aggregate of its last tile, which nobody reads.
+  SS X[K];  // B x[t], kept for pass 2
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    E u[kMimoMaxIO];
+    inputs(k, u);
+    X[k] = mimo_bx<Alg>(mi, u);
+  }
+  const SC dummy = Alg::s_czero();
+  M m = lane_map<Alg, true, false, K>(Ak, X, dummy);
+  m = wave_scan_incl(m, lane, op);
+  const M ex = wave_shift_up(m, lane, map_identity<Alg>());
+  if (lane == 63) s_wagg[w] = m;
+  __syncthreads();  // wave aggregates are in s_wagg
+  __syncthreads();  // entry state is in s_in
+  SS h = Alg::store_s(apply<Alg>(ex, apply<Alg>(s_wpre[w], s_in)));
+
+  // ---- pass 2: y = C h + D x, then the step
+  const MimoOut<Alg> mo = mimo_out<Alg>(a, b);
+  const int64_t l0 = s0 + int64_t(lane) * K;
+  const bool has_d = a.Dm != nullptr;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    E u[kMimoMaxIO];
+    if (has_d) inputs(k, u);
+#pragma unroll
+    for (int p = 0; p < kMimoMaxIO; ++p) {
+      if (p < a.P) {
+        E o = V::dot(mo.c[p], h);
+        if (has_d) {
+#pragma unroll
+          for (int f = 0; f < kMimoMaxIO; ++f) o = fma(mo.d[p][f], u[f], o);
+        }
+        io[p * kP + lane * K + k] = o;
+      }
+    }
+    h = Alg::s_affine(Ak[k], h, X[k]);
+    if (a.zf && l0 + k == T - 1) {
+      union {
+        SS s;
+        E e[V::M];
+      } zu;
+      zu.s = h;
+#pragma unroll
+      for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = zu.e[i];
+    }
+  }
+  wave_sync();  // the span's outputs are in the planes
+  mimo_stage_out<Alg, REV, Sh>(a.y + b * T * a.P, s0, T, a.P, a.p_magic, io, lane);
 }
 
 }  // namespace phs

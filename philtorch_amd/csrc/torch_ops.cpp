@@ -1,7 +1,7 @@
 // torch.library layer of philtorch_amd: owns the `philtorch` operator
 // namespace with the reference's schemas (philtorch/csrc/host_recur2.cpp:162-171)
 // plus the new LPV scalar op `recur`, four fused backward ops and the fused
-// filter ops (`sosfilt`, `filtfilt`, `lti_ss`, `lfilter_ss`, `lpv_ss`, `mimo_ss`), and
+// filter ops (`sosfilt`, `filtfilt`, `lti_ss`, `lfilter_ss`, `lpv_ss`, `mimo_ss`, `lpv_mimo_ss`), and
 // binds the HIP device key (PyTorch-ROCm names it CUDA) to the C ABI of
 // libphilscan.  The CPU key serves the reference's five ops, `recur` and the
 // backward ops with the CPU kernels of phs_cpu.hpp, as the reference's CPU
@@ -1055,6 +1055,73 @@ std::vector<Tensor> lpv_ss_backward_hip(const Tensor &A, const std::optional<Ten
   return {gA, gB, gC, gD, gzi, gx};
 }
 
+// Multi-input, multi-output LPV state space (time-varying A) of order <= 4
+// with 1-4 inputs and outputs per step, B, C, D constant in time, fused
+// (phs_lpv_mimo_ss; philtorch/lpv/ssm.py:337-581 for a 3D x or matrix
+// B, C, D): returns (y, zf).  x (batch, T, F); A (T, M, M) or
+// (batch, T, M, M); B (M, F) or (batch, M, F); C (P, M) or (batch, P, M);
+// D None, (P, F) or (batch, P, F); zi None or (batch, M); y (batch, T, P).
+// reverse runs the model backwards in time; transpose_A uses A[t]^T (the
+// adjoint model, read without a transposed copy).
+std::tuple<Tensor, Tensor> lpv_mimo_ss_hip(const Tensor &A, const Tensor &Bm, const Tensor &Cm,
+                                           const std::optional<Tensor> &Dm, const std::optional<Tensor> &zi,
+                                           const Tensor &x, bool reverse, bool transpose_A) {
+  TORCH_CHECK(x.dim() == 3, "philtorch::lpv_mimo_ss: x must be a 3D tensor (batch, time, features)");
+  const int64_t B = x.size(0), T = x.size(1), F = x.size(2);
+  TORCH_CHECK((A.dim() == 3 || A.dim() == 4) && A.size(-1) == A.size(-2) && A.size(-3) == T,
+              "philtorch::lpv_mimo_ss: A must be (T, M, M) or (batch, T, M, M)");
+  if (A.dim() == 4) TORCH_CHECK(A.size(0) == B, "philtorch::lpv_mimo_ss: a 4D A must have x's batch size");
+  const int64_t M = A.size(-1);
+  TORCH_CHECK(M >= 1 && M <= kMaxOrder, "philtorch::lpv_mimo_ss: state order 1 to ", kMaxOrder, ", got ", M);
+  TORCH_CHECK(F >= 1 && F <= 4, "philtorch::lpv_mimo_ss: 1 to 4 input features, got ", F);
+  TORCH_CHECK(Cm.dim() == 2 || Cm.dim() == 3, "philtorch::lpv_mimo_ss: C must be (P, M) or (batch, P, M)");
+  const int64_t P = Cm.size(-2);
+  TORCH_CHECK(P >= 1 && P <= 4, "philtorch::lpv_mimo_ss: 1 to 4 outputs, got ", P);
+  TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,
+              "philtorch::lpv_mimo_ss: float32 or float64 only, got ", x.scalar_type());
+  TORCH_CHECK(x.is_cuda(), "philtorch::lpv_mimo_ss: philtorch_amd runs on HIP devices only (got ", x.device(), ")");
+  TORCH_CHECK(A.scalar_type() == x.scalar_type() && A.device() == x.device(),
+              "philtorch::lpv_mimo_ss: A must have x's scalar type and device");
+  auto check = [&](const Tensor &t, const char *what, int64_t r, int64_t c) {
+    TORCH_CHECK(t.scalar_type() == x.scalar_type(), "philtorch::lpv_mimo_ss: ", what, " must have x's scalar type");
+    TORCH_CHECK(t.device() == x.device(), "philtorch::lpv_mimo_ss: all tensors must be on the same device");
+    TORCH_CHECK((t.dim() == 2 || (t.dim() == 3 && t.size(0) == B)) && t.size(-2) == r && t.size(-1) == c,
+                "philtorch::lpv_mimo_ss: ", what, " must be (", r, ", ", c, ") or (batch, ", r, ", ", c, "), got ",
+                t.sizes());
+  };
+  check(Bm, "B", M, F);
+  check(Cm, "C", P, M);
+  if (Dm) check(*Dm, "D", P, F);
+  if (zi) {
+    TORCH_CHECK(zi->scalar_type() == x.scalar_type() && zi->device() == x.device(),
+                "philtorch::lpv_mimo_ss: zi must have x's scalar type and device");
+    TORCH_CHECK(zi->dim() == 2 && zi->size(0) == B && zi->size(1) == M,
+                "philtorch::lpv_mimo_ss: zi must be (batch, M)");
+  }
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor Ac = A.contiguous(), bc = Bm.contiguous(), cc = Cm.contiguous(), xc = x.contiguous();
+  Tensor dc = Dm ? Dm->contiguous() : Tensor(), zc = zi ? zi->contiguous() : Tensor();
+  Tensor y = at::empty({B, T, P}, x.options());
+  Tensor zf = at::empty({B, M}, x.options());
+  if (B == 0) return {y, zf};
+  if (T == 0) {
+    if (zi) zf.copy_(zc); else zf.zero_();
+    return {y, zf};
+  }
+  const int A_flags = (A.dim() == 3 ? PHS_LPV_A_SHARED : 0) | (transpose_A ? PHS_LPV_A_TRANSPOSED : 0);
+  const int shared = (Bm.dim() == 2 ? PHS_MIMO_B_SHARED : 0) | (Cm.dim() == 2 ? PHS_MIMO_C_SHARED : 0) |
+                     (Dm && Dm->dim() == 2 ? PHS_MIMO_D_SHARED : 0);
+  void *stream = stream_of(x);
+  const Workspace ws = workspace_for(x, phs_lpv_mimo_ss_workspace_size(dt, int(M), B, T), stream);
+  check_status(phs_lpv_mimo_ss(dt, int(M), int(F), int(P), B, T, Ac.const_data_ptr(), A_flags, bc.const_data_ptr(),
+                               cc.const_data_ptr(), Dm ? dc.const_data_ptr() : nullptr, shared,
+                               zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(), y.mutable_data_ptr(),
+                               zf.mutable_data_ptr(), reverse ? 1 : 0, ws.ptr, ws.bytes, stream),
+               "lpv_mimo_ss");
+  return {y, zf};
+}
+
 // The coefficient gradients of mimo_ss summed over time in one pass
 // (phs_mimo_ss_grad_sums): lam, hs (batch, T, M) (None where no wanted
 // output reads them), x (batch, T, F), g (batch, T, P); `want` and `shared`
@@ -1362,6 +1429,9 @@ TORCH_LIBRARY(philtorch, m) {
         {at::Tag::pt2_compliant_tag});
   m.def("mimo_ss_grad_sums(Tensor? lam, Tensor? hs, Tensor x, Tensor g, int shared, int want) -> Tensor[]",
         {at::Tag::pt2_compliant_tag});
+  m.def("lpv_mimo_ss(Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? zi, Tensor x, bool reverse=False, "
+        "bool transpose_A=False) -> (Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
@@ -1391,6 +1461,7 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("lpv_ss_backward", &lpv_ss_backward_hip);
   m.impl("mimo_ss", &mimo_ss_hip);
   m.impl("mimo_ss_grad_sums", &mimo_ss_grad_sums_hip);
+  m.impl("lpv_mimo_ss", &lpv_mimo_ss_hip);
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CPU, m) {

@@ -368,6 +368,159 @@ def _lpv_state_space_composite(A, B, C, D, zi, x, out_idx=0):
     return y, zf
 
 
+def _lpv_mimo_operands(x: Tensor, B, C, D, out_idx, batch: int, N: int, M: int):
+    """The per-row (or shared) matrices of philtorch::lpv_mimo_ss for a call
+    of state_space whose B, C, D are constant in time, or None where they
+    are not or the shapes fall outside it: ``(x3, Bm, Cm, Dm, vec)`` with x3
+    (batch, N, F), Bm (M, F) or (batch, M, F), Cm (P, M) or (batch, P, M),
+    Dm None, (P, F) or (batch, P, F), and ``vec`` true where the
+    reference's y is 2D (one output).  Each case mirrors a branch of the
+    composed route (_apply_B: philtorch/lpv/ssm.py:413-454; _apply_D
+    :480-547; _apply_C :549-573), tested in the same order, so a shape is
+    read as the composed route reads it; a branch whose operand varies along
+    time (an N axis) returns None, as does a one-output term added to a
+    multi-output one (which the reference broadcasts)."""
+    two_d = x.dim() == 2
+    Fn = 1 if two_d else x.size(-1)
+    features = -1 if two_d else Fn
+    eye = lambda n: torch.eye(n, dtype=x.dtype, device=x.device)  # noqa: E731
+    if B is None:
+        if two_d or Fn != M:
+            return None
+        Bm = eye(M)
+    else:
+        s = tuple(B.shape)
+        if s == (M,):
+            if not two_d:
+                return None
+            Bm = B.reshape(M, 1)
+        elif len(s) == 2 and s == (M, features):
+            Bm = B
+        elif len(s) == 2 and s == (N, M):
+            return None
+        elif len(s) == 2 and s == (batch, M):
+            if not two_d:
+                return None
+            Bm = B.reshape(batch, M, 1)
+        elif len(s) == 3 and s == (N, M, features):
+            return None
+        elif len(s) == 3 and s == (batch, N, M):
+            return None
+        elif len(s) == 3 and s == (batch, M, features):
+            Bm = B
+        else:
+            return None
+    if C is None:
+        if out_idx is None:
+            Cm, c_vec = eye(M), False
+        else:
+            Cm, c_vec = eye(M)[out_idx].reshape(1, M), True
+    else:
+        s = tuple(C.shape)
+        if s == (M,):
+            Cm, c_vec = C.reshape(1, M), True
+        elif len(s) == 2 and s == (N, M):
+            return None
+        elif len(s) == 2 and s == (batch, M):
+            Cm, c_vec = C.reshape(batch, 1, M), True
+        elif len(s) == 2 and s[1] == M:
+            Cm, c_vec = C, False
+        elif len(s) == 3 and s[0] == N and s[2] == M:
+            return None
+        elif len(s) == 3 and s == (batch, N, M):
+            return None
+        elif len(s) == 3 and s[0] == batch and s[2] == M:
+            Cm, c_vec = C, False
+        else:
+            return None
+    Dm, d_vec = None, None
+    if D is not None:
+        s = tuple(D.shape)
+        if s in ((), (1,)):
+            if two_d:
+                Dm, d_vec = D.reshape(1, 1), True
+            else:
+                Dm, d_vec = D.reshape(()) * eye(Fn), False
+        elif len(s) == 1:
+            if s[0] == features:
+                Dm, d_vec = D.reshape(1, Fn), True
+            elif not two_d or s[0] == N:
+                return None
+            elif s[0] == batch:
+                Dm, d_vec = D.reshape(batch, 1, 1), True
+            else:
+                Dm, d_vec = D.reshape(s[0], 1), False
+        elif len(s) == 2:
+            if s == (N, features):
+                return None
+            if s == (batch, features):
+                Dm, d_vec = D.reshape(batch, 1, Fn), True
+            elif s[0] == N or (s == (batch, N) and two_d):
+                return None
+            elif s[0] == batch and two_d:
+                Dm, d_vec = D.reshape(batch, s[1], 1), False
+            elif s[1] == features:
+                Dm, d_vec = D, False
+            else:
+                return None
+        elif len(s) == 3:
+            if s == (batch, N, features):
+                return None
+            if s[0] == batch and s[2] == features:
+                Dm, d_vec = D, False
+            else:
+                return None
+        else:
+            return None
+        if d_vec != c_vec or Dm.size(-2) != Cm.size(-2):
+            return None
+    return (x.unsqueeze(-1) if two_d else x), Bm, Cm, Dm, c_vec
+
+
+def _lpv_mimo_applies(A: Tensor, x: Tensor, zi: Optional[Tensor], ops, native: bool) -> bool:
+    """Whether _lpv_mimo_operands' matrices run philtorch::lpv_mimo_ss:
+    order <= 4, at most four inputs and outputs per step, float32 or float64
+    on a HIP device with the native route requested, no forward-mode
+    tangent."""
+    from .. import EXTENSION_LOADED
+
+    if not (native and EXTENSION_LOADED and x.is_cuda and ops is not None and hasattr(torch.ops.philtorch, "lpv_mimo_ss")):
+        return False
+    x3, Bm, Cm, Dm, _ = ops
+    if x.dtype not in (torch.float32, torch.float64) or A.size(-1) > 4 or x3.size(-1) > 4 or Cm.size(-2) > 4:
+        return False
+    tensors = [A, x, Bm, Cm] + [t for t in (Dm, zi) if t is not None]
+    if any(t.dtype != x.dtype or t.device != x.device for t in tensors):
+        return False
+    if A.dim() == 4 and A.size(0) != x.size(0):
+        return False
+    import torch.autograd.forward_ad as fwad
+
+    return all(fwad.unpack_dual(t).tangent is None for t in tensors)
+
+
+def _lpv_mimo_composite(A, Bm, Cm, Dm, zi, x, reverse=False, transpose_A=False):
+    """(y, zf) of the composed route for philtorch::lpv_mimo_ss's operands (B
+    x, the native LPV scan, the shifted state sequence, C h + D x; A[t]^T
+    with ``transpose_A``, in time-reversed order with ``reverse``): its
+    autograd formula differentiates this under create_graph."""
+    if transpose_A:
+        A = A.mT
+    if reverse:
+        y, zf = _lpv_mimo_composite(A.flip(-3), Bm, Cm, Dm, zi, x.flip(1))
+        return y.flip(1), zf
+    M = A.size(-1)
+    zi = x.new_zeros(x.size(0), M) if zi is None else zi
+    Bx = torch.matmul(x, Bm.mT)  # (batch, N, M)
+    h = _ext_ss_recur(A.contiguous(), zi, Bx)
+    zf = h[:, -1] if h.size(1) > 0 else zi
+    h = torch.cat([zi.unsqueeze(1), h[:, :-1]], dim=1)
+    y = torch.matmul(h, Cm.mT)
+    if Dm is not None:
+        y = y + torch.matmul(x, Dm.mT)
+    return y, zf
+
+
 # Above this many bytes of per-row, per-step gradients of the operands that
 # the rows share but that vary along time (A (T, M, M); B, C, D with one row
 # and T steps), which philtorch::lpv_ss_backward writes for every row before
@@ -433,7 +586,9 @@ def state_space(
     B, C per row and/or per step or absent / out_idx; D per row and/or per
     step) runs philtorch::lpv_ss: B x, the scan, the state shift and
     C h + D x in one pass; its adjoint gives the gradients w.r.t. x and zi,
-    and philtorch::lpv_ss_backward those of A, B, C, D.
+    and philtorch::lpv_ss_backward those of A, B, C, D.  A model with up to
+    four inputs and outputs per step (3D x, matrix-valued B, C, D) whose B,
+    C, D are constant in time runs philtorch::lpv_mimo_ss the same way.
     """
     assert x.dim() in (2, 3), f"Input signal must be 2D or 3D (batch, time, [features]), got {x.shape}"
     assert A.dim() in (3, 4), f"State matrix A must be 3D or 4D, got {A.shape}"
@@ -461,6 +616,15 @@ def state_space(
         with _op_ctx(A, *ops, zi, x):
             y, zf = torch.ops.philtorch.lpv_ss(A, ops[0], ops[1], ops[2], zi.contiguous() if return_zf else None, x,
                                                0 if out_idx is None else out_idx)
+        return (y, zf) if return_zf else y
+    mops = _lpv_mimo_operands(x, B, C, D, out_idx, batch, N, M) if native else None
+    if _lpv_mimo_applies(A, x, zi if return_zf else None, mops, native):
+        from .. import _op_ctx
+
+        x3, Bm, Cm, Dm, vec = mops
+        with _op_ctx(A, Bm, Cm, Dm, zi, x3):
+            y, zf = torch.ops.philtorch.lpv_mimo_ss(A, Bm, Cm, Dm, zi.contiguous() if return_zf else None, x3)
+        y = y.squeeze(-1) if vec else y
         return (y, zf) if return_zf else y
     Bx = _apply_B(x, B, batch, N, M, features)
 

@@ -149,6 +149,11 @@ def load() -> ctypes.CDLL:
     lib.phs_mimo_ss_workspace_size.argtypes = [ctypes.c_int, ctypes.c_int, i64, i64]
     lib.phs_mimo_ss_workspace_size.restype = ctypes.c_size_t
     ci = ctypes.c_int
+    lib.phs_lpv_mimo_ss_workspace_size.argtypes = [ci, ci, i64, i64]
+    lib.phs_lpv_mimo_ss_workspace_size.restype = ctypes.c_size_t
+    lib.phs_lpv_mimo_ss.argtypes = [ci, ci, ci, ci, i64, i64, vp, ci, vp, vp, vp, ci, vp, vp, vp, vp, ci, vp,
+                                    ctypes.c_size_t, vp]
+    lib.phs_lpv_mimo_ss.restype = ci
     lib.phs_mimo_ss_grad_sums_scratch_size.argtypes = [ci, i64, i64]
     lib.phs_mimo_ss_grad_sums_scratch_size.restype = ctypes.c_size_t
     lib.phs_mimo_ss_grad_sums.argtypes = [ci, ci, ci, ci, i64, i64, vp, vp, vp, vp, ci, vp, vp, vp, vp, vp,

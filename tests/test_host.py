@@ -449,6 +449,21 @@ def test_capi_mimo_state_space_host_only_calls():
         assert gsum(**bad) == capi.PHS_ERR_INVALID, bad
     assert gsum(sb=8) == capi.PHS_ERR_WORKSPACE
     assert gsum(gA=None) == capi.PHS_OK  # nothing wanted: nothing launched
+    # the LPV form: sizes and argument errors
+    for dt in (0, 1):
+        for M in (1, 2, 3, 4):
+            assert lib.phs_lpv_mimo_ss_workspace_size(dt, M, 32, 1 << 20) > 0
+    assert lib.phs_lpv_mimo_ss_workspace_size(2, 2, 16, 100) == 0
+
+    def lpv(dt=0, M=2, F=2, P=3, B=2, a_flags=0, shared=0, a=d, wsb=ws):
+        return lib.phs_lpv_mimo_ss(dt, M, F, P, B, 100, a, a_flags, d, d, None, shared, None, d, d, None, 0, d, wsb,
+                                   None)
+
+    assert lpv(dt=2) == capi.PHS_ERR_DTYPE
+    for bad in (dict(M=5), dict(F=0), dict(P=5), dict(B=-1), dict(a_flags=4), dict(shared=1), dict(a=None)):
+        assert lpv(**bad) == capi.PHS_ERR_INVALID, bad
+    assert lpv(wsb=lib.phs_lpv_mimo_ss_workspace_size(0, 2, 2, 100) - 1) == capi.PHS_ERR_WORKSPACE
+    assert lpv(B=0) == capi.PHS_OK
 
 
 def _mimo_shape_cases(batch, M):
@@ -513,3 +528,74 @@ def test_mimo_operands_leave_mixed_and_rejected_shapes():
     assert ssm._mimo_operands(A, x, torch.randn(M), torch.randn(M), None, None, batch, M) is None
     assert ssm._mimo_operands(A, x, None, torch.randn(M), None, None, batch, M) is None  # B None needs F == M
     assert ssm._mimo_operands(A, x, torch.randn(M, F), torch.randn(M), torch.randn(batch), None, batch, M) is None
+
+
+def _lpv_mimo_shape_cases(batch, N, M, F, P):
+    """(x features or None for 2D x, B, C, D, out_idx) of every branch of the
+    reference's LPV B, C and D shape rules with operands constant in time
+    that the fused multi-output route takes (philtorch/lpv/ssm.py:413-577)."""
+    return [
+        (F, (M, F), (P, M), (P, F), None),
+        (F, (batch, M, F), (batch, P, M), (batch, P, F), None),
+        (F, (M, F), (M,), (F,), None),
+        (F, (M, F), (batch, M), (batch, F), None),
+        (F, (M, F), None, (F,), 1),
+        (F, (M, F), (F, M), (), None),
+        (M, None, None, None, None),
+        (M, None, (P, M), None, None),
+        (None, (M,), (P, M), (P,), None),
+        (None, (batch, M), (batch, P, M), (batch, P), None),
+        (None, (M,), (P, M), None, None),
+        (None, (batch, M), None, None, None),
+    ]
+
+
+@pytest.mark.parametrize("case", range(12))
+@pytest.mark.parametrize("shared_A", [False, True])
+def test_lpv_mimo_operands_reproduce_composed_route(case, shared_A):
+    """Each LPV shape case's matrices (lpv.ssm._lpv_mimo_operands) run
+    through the composite of lpv_mimo_ss (B x, the LPV scan, the shift,
+    C h + D x) give the composed route's y and zf on CPU."""
+    from philtorch_amd.lpv import ssm
+
+    batch, N, M, F, P = 5, 40, 3, 2, 4  # (no two sizes equal: no shape reads two ways)
+    Fx, bs, cs, ds, out_idx = _lpv_mimo_shape_cases(batch, N, M, F, P)[case]
+    g = torch.Generator().manual_seed(3000 + case)
+    rnd = lambda *s: torch.randn(tuple(s), generator=g, dtype=torch.float64)  # noqa: E731
+    A = 0.5 * rnd(*((N, M, M) if shared_A else (batch, N, M, M))) / M ** 0.5
+    x = rnd(batch, N) if Fx is None else rnd(batch, N, Fx)
+    B = None if bs is None else rnd(*bs)
+    C = None if cs is None else rnd(*cs)
+    D = None if ds is None else rnd(*ds)
+    zi = rnd(batch, M)
+    ops = ssm._lpv_mimo_operands(x, B, C, D, out_idx, batch, N, M)
+    assert ops is not None
+    x3, Bm, Cm, Dm, vec = ops
+    y, zf = ssm._lpv_mimo_composite(A, Bm, Cm, Dm, zi, x3)
+    y = y.squeeze(-1) if vec else y
+    ref, rzf = ssm.state_space(A, x, B, C, D, zi=zi, unroll_factor=1, out_idx=out_idx)
+    assert y.shape == ref.shape
+    torch.testing.assert_close(y, ref, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(zf, rzf, rtol=1e-12, atol=1e-12)
+    # reversed and transposed forms against the composite's definition
+    yr, _ = ssm._lpv_mimo_composite(A, Bm, Cm, Dm, zi, x3, reverse=True, transpose_A=True)
+    At = A.mT.flip(-3)
+    yf, _ = ssm._lpv_mimo_composite(At, Bm, Cm, Dm, zi, x3.flip(1))
+    torch.testing.assert_close(yr, yf.flip(1), rtol=1e-12, atol=1e-12)
+
+
+def test_lpv_mimo_operands_leave_time_varying_and_mixed_shapes():
+    """Operands that vary along time, shapes whose one-output term the
+    reference broadcasts against a multi-output one, and shapes the reference
+    rejects get no fused operands."""
+    from philtorch_amd.lpv import ssm
+
+    batch, N, M, F = 5, 40, 3, 2
+    x3, x2 = torch.randn(batch, N, F), torch.randn(batch, N)
+    o = ssm._lpv_mimo_operands
+    assert o(x3, torch.randn(N, M, F), torch.randn(2, M), None, None, batch, N, M) is None  # B (N, M, F)
+    assert o(x3, torch.randn(M, F), torch.randn(N, 2, M), None, None, batch, N, M) is None  # C (N, P, M)
+    assert o(x2, torch.randn(M), torch.randn(2, M), torch.randn(N), None, batch, N, M) is None  # D (N,)
+    assert o(x2, torch.randn(N, M), torch.randn(2, M), None, None, batch, N, M) is None  # B (N, M)
+    assert o(x3, torch.randn(M, F), torch.randn(M), torch.randn(2, F), None, batch, N, M) is None  # 1 + 2 outputs
+    assert o(x3, torch.randn(M), torch.randn(M), None, None, batch, N, M) is None  # B (M,) with 3D x

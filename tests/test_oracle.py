@@ -512,6 +512,38 @@ def test_lti_state_space_mimo_reduces_to_siso():
     np.testing.assert_array_equal(zf0, zi)
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_lpv_state_space_mimo_matches_loop_and_lti(M):
+    """oracle.lpv_state_space_mimo against the textbook per-step loop of
+    h[t+1] = A[t] h[t] + B x[t], y[t] = C h[t] + D x[t] (per-row and shared
+    operands, 2 inputs and 3 outputs), against lti_state_space_mimo (pinned
+    to dlsim) when A does not vary along time, and against the
+    single-input single-output LPV oracle at F = P = 1."""
+    g = D.rng(D.seed_of("oracle-lpv-mimo", M))
+    Bn, T, F, P = 3, 50, 2, 3
+    A = 0.6 * g.standard_normal((Bn, T, M, M)) / np.sqrt(M)
+    Bm, Cm, Dm = g.standard_normal((M, F)), g.standard_normal((Bn, P, M)), g.standard_normal((P, F))
+    x = g.standard_normal((Bn, T, F))
+    zi = g.standard_normal((Bn, M))
+    y, zf = oracle.lpv_state_space_mimo(A, x, Bm, Cm, Dm, zi)
+    for r in range(Bn):
+        h = zi[r].copy()
+        for t in range(T):
+            ref = Cm[r] @ h + Dm @ x[r, t]
+            np.testing.assert_allclose(y[r, t], ref, rtol=1e-12, atol=1e-12)
+            h = A[r, t] @ h + Bm @ x[r, t]
+        np.testing.assert_allclose(zf[r], h, rtol=1e-12, atol=1e-12)
+    A0 = A[:, 0]
+    yl, zl = oracle.lpv_state_space_mimo(np.broadcast_to(A0[:, None], (Bn, T, M, M)), x, Bm, Cm, Dm, zi)
+    ym, zm = oracle.lti_state_space_mimo(A0, x, Bm, Cm, Dm, zi)
+    np.testing.assert_allclose(yl, ym, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(zl, zm, rtol=1e-12, atol=1e-12)
+    ys, zs = oracle.lpv_state_space(A, x[..., 0], Bm[:, 0], Cm[:, 0][:, None, :], Dm[0, 0], zi)
+    y1, z1 = oracle.lpv_state_space_mimo(A, x[..., :1], Bm[:, :1], Cm[:, :1], Dm[:1, :1], zi)
+    np.testing.assert_allclose(y1[..., 0], ys, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(z1, zs, rtol=1e-12, atol=1e-12)
+
+
 # ---------------------------------------------------------------- LPV SISO state space
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_lpv_state_space_matches_loop_and_lti(M):
