@@ -27,8 +27,10 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c4_lfilter4_grad  the same plus gradients w.r.t. x, b and a (philtorch::lfilter_ss_backward)
   c4_mimo  lti.state_space of order 4, 2 inputs and 2 outputs per step (philtorch::mimo_ss)
   c4_mimo_grad  the same plus gradients w.r.t. x and zi (the adjoint mimo_ss pass)
-  c4_mimo_coef  the same plus gradients w.r.t. A, B, C, D (two states passes and GEMM sums)
---composed runs an API config (c3_lpv_ss*, c4_api, c4_lfilter*, c4_filtfilt*, c4_mimo*)
+  c4_mimo_coef  the same plus gradients w.r.t. A, B, C, D (two states passes and the fused sums)
+  c3_lpv_mimo  lpv.state_space on C3's A[t], 2 inputs and 2 outputs per step (philtorch::lpv_mimo_ss)
+  c3_lpv_mimo_grad  the same plus gradients w.r.t. x and zi; c3_lpv_mimo_coef: and A[t], B, C, D
+--composed runs an API config (c3_lpv_ss*, c3_lpv_mimo*, c4_api, c4_lfilter*, c4_filtfilt*, c4_mimo*)
 through the reference's composed route instead of the fused kernels, for the
 comparison.
 Before every step a 512 MiB buffer is read end to end so the 256 MB Infinity
@@ -895,6 +897,128 @@ class MimoSsCoefGrad(MimoSsGrad):
     cpu_step = None  # the oracle restates no coefficient gradients of the state space
 
 
+class LpvMimoApi(LpvBiquad):
+    """c3_lpv_mimo: the C3 time-varying biquad dynamics A[t] (32 rows of 2^20
+    steps, fp32) with two inputs and two outputs per step, B (2, 2), C (2, 2),
+    D (2, 2) shared by the rows: ``lpv.state_space(A, x, B, C, D, zi=zi,
+    unroll_factor=1)`` on x (32, 2^20, 2).  Runs philtorch::lpv_mimo_ss: B x,
+    the scan, the state shift and C h + D x in one pass; forward only."""
+
+    def __init__(self):
+        import torch
+
+        super().__init__()
+        B, T = self.B, self.T
+        self.name = "c3_lpv_mimo"
+        self.kernel = "lpv_mimo_kernel"
+        self.metric = f"GSamples/s fwd, LPV lpv.state_space order 2, 2 inputs, 2 outputs per step B={B} T={T} fp32 (API)"
+        g = torch.Generator().manual_seed(35)
+        A = self.cpu[0]
+        x = torch.randn(B, T, 2, generator=g)
+        Bm = torch.randn(2, 2, generator=g) / 2 ** 0.5
+        Cm, Dm = torch.randn(2, 2, generator=g), torch.randn(2, 2, generator=g)
+        zi = torch.randn(B, 2, generator=g)
+        self.cpu = [v.contiguous() for v in (A, x, Bm, Cm, Dm, zi)]
+        self.dev = [v.cuda() for v in self.cpu]
+        self.fwd_bytes = 32 * B * T  # read A (16), x (8); write y (8)
+        self.bwd_bytes = 0
+
+    def step_fwd(self):
+        from philtorch_amd import lpv
+
+        A, x, Bm, Cm, Dm, zi = self.dev
+        return lpv.state_space(A, x, Bm, Cm, Dm, zi=zi, unroll_factor=1)
+
+    def step_bwd(self, out):
+        return out
+
+    def cpu_step(self, rows, steps, nthreads):
+        import oracle
+
+        A, x, Bm, Cm, Dm, zi = (v.numpy() for v in self.cpu)
+        oracle.lpv_state_space_mimo(A[:rows, :steps], x[:rows, :steps], Bm, Cm, Dm, zi[:rows], nthreads=nthreads)
+
+
+class LpvMimoGrad(LpvMimoApi):
+    """c3_lpv_mimo_grad: c3_lpv_mimo plus the gradients w.r.t. x and zi: one
+    more philtorch::lpv_mimo_ss pass, the adjoint model (A[t]^T read in
+    place, input matrix C^T, output matrix B^T, D^T) in reversed time."""
+
+    def __init__(self):
+        import torch
+
+        super().__init__()
+        B, T = self.B, self.T
+        self.name = "c3_lpv_mimo_grad"
+        self.metric = (f"GSamples/s fwd+bwd(x, zi), LPV lpv.state_space order 2, 2 inputs, 2 outputs per step "
+                       f"B={B} T={T} fp32 (API)")
+        g = torch.Generator().manual_seed(36)
+        self.gy_cpu = torch.randn(B, T, 2, generator=g)
+        self.gy = self.gy_cpu.cuda()
+        self.bwd_bytes = 32 * B * T  # read A (16), g (8); write grad_x (8)
+
+    def step_fwd(self):
+        from philtorch_amd import lpv
+
+        A, x, Bm, Cm, Dm, zi = self.dev
+        x, zi = x.detach().requires_grad_(True), zi.detach().requires_grad_(True)
+        y, _ = lpv.state_space(A, x, Bm, Cm, Dm, zi=zi, unroll_factor=1)
+        return y, x, zi
+
+    def step_bwd(self, out):
+        import torch
+
+        y, x, zi = out
+        return torch.autograd.grad(y, (x, zi), self.gy)
+
+    def cpu_step(self, rows, steps, nthreads):
+        import numpy as np
+
+        import oracle
+
+        A, x, Bm, Cm, Dm, zi = (v.numpy() for v in self.cpu)
+        A, x, zi = A[:rows, :steps], x[:rows, :steps], zi[:rows]
+        gy = self.gy_cpu.numpy()[:rows, :steps]
+        oracle.lpv_state_space_mimo(A, x, Bm, Cm, Dm, zi, nthreads=nthreads)
+        fl = lambda v: np.ascontiguousarray(v[:, ::-1])  # noqa: E731
+        oracle.lpv_state_space_mimo(fl(np.swapaxes(A, -1, -2)), fl(gy), Cm.T.copy(), Bm.T.copy(), Dm.T.copy(), None,
+                                    nthreads=nthreads)
+
+
+class LpvMimoCoefGrad(LpvMimoGrad):
+    """c3_lpv_mimo_coef: c3_lpv_mimo_grad with the gradients of A[t], B, C and
+    D too: the adjoint pass, the forward again writing its states, the
+    adjoint again writing its states, dL/dA[t] = lambda[t+1] h[t]^T per step
+    and the sums over time for B, C, D (philtorch::mimo_ss_grad_sums)."""
+
+    def __init__(self):
+        super().__init__()
+        B, T = self.B, self.T
+        self.name = "c3_lpv_mimo_coef"
+        self.metric = (f"GSamples/s fwd+bwd(x, zi, A, B, C, D), LPV lpv.state_space order 2, 2 inputs, 2 outputs "
+                       f"per step B={B} T={T} fp32 (API)")
+        # adjoint, states and adjoint-states passes (32 each: A, one signal in, one out), dL/dA (read
+        # lambda and h, write 16), the sums (read lambda, h, x, g)
+        self.bwd_bytes = (32 + 32 + 32 + 32 + 32) * B * T
+        self.bwd_launch_bytes = 32 * B * T  # the adjoint pass
+
+    def step_fwd(self):
+        from philtorch_amd import lpv
+
+        leaves = [t.detach().requires_grad_(True) for t in self.dev]
+        A, x, Bm, Cm, Dm, zi = leaves
+        y, _ = lpv.state_space(A, x, Bm, Cm, Dm, zi=zi, unroll_factor=1)
+        return y, leaves
+
+    def step_bwd(self, out):
+        import torch
+
+        y, leaves = out
+        return torch.autograd.grad(y, leaves, self.gy)
+
+    cpu_step = None  # the oracle restates no coefficient gradients of the state space
+
+
 def make_workload(name):
     if name == "c1":
         return LpvScalar("c1", 64, 65536, "float32")
@@ -936,15 +1060,22 @@ def make_workload(name):
         return MimoSsGrad()
     if name == "c4_mimo_coef":
         return MimoSsCoefGrad()
+    if name == "c3_lpv_mimo":
+        return LpvMimoApi()
+    if name == "c3_lpv_mimo_grad":
+        return LpvMimoGrad()
+    if name == "c3_lpv_mimo_coef":
+        return LpvMimoCoefGrad()
     raise ValueError(name)
 
 
 API_CONFIGS = ("c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4_api", "c4_lfilter_inf", "c4_filtfilt",
                "c4_filtfilt_grad", "c4_filtfilt_coef", "c4_lfilter4", "c4_lfilter4_grad", "c4_mimo", "c4_mimo_grad",
-               "c4_mimo_coef")
+               "c4_mimo_coef", "c3_lpv_mimo", "c3_lpv_mimo_grad", "c3_lpv_mimo_coef")
 CONFIGS = ("c1", "c2", "c3", "c3_lpv_ss", "c3_lpv_ss_grad", "c3_lpv_ss_coef", "c4", "c4_fused", "c4_api",
            "c4_lfilter_inf", "c4_filtfilt", "c4_filtfilt_grad", "c4_filtfilt_coef", "c4_lfilter4", "c4_lfilter4_grad",
-           "c4_mimo", "c4_mimo_grad", "c4_mimo_coef", "c5", "c5_f64")
+           "c4_mimo", "c4_mimo_grad", "c4_mimo_coef", "c3_lpv_mimo", "c3_lpv_mimo_grad", "c3_lpv_mimo_coef", "c5",
+           "c5_f64")
 
 
 # ----------------------------------------------------------------------------
@@ -1234,8 +1365,8 @@ def main() -> int:
         from philtorch_amd.lti import filtering, ssm as lti_ssm
 
         off = lambda *a, **k: False  # noqa: E731
-        for mod, fn in ((lpv_ssm, "_fused_lpv_ss_applies"), (lti_ssm, "_fused_ss_applies"),
-                        (lti_ssm, "_mimo_applies"), (filtering, "_fused_biquad_applies"),
+        for mod, fn in ((lpv_ssm, "_fused_lpv_ss_applies"), (lpv_ssm, "_lpv_mimo_applies"),
+                        (lti_ssm, "_fused_ss_applies"), (lti_ssm, "_mimo_applies"), (filtering, "_fused_biquad_applies"),
                         (filtering, "_fused_lfilter_applies"), (filtering, "_fused_filtfilt_applies")):
             setattr(mod, fn, off)
         w.metric += " [composed route]"
@@ -1328,6 +1459,9 @@ def main() -> int:
                 "c4_mimo": "lti_state_space_order4_2in_2out_api_fwd_B16_T480000_f32",
                 "c4_mimo_grad": "lti_state_space_order4_2in_2out_api_fwd_bwd_x_zi_B16_T480000_f32",
                 "c4_mimo_coef": "lti_state_space_order4_2in_2out_api_fwd_bwd_all_B16_T480000_f32",
+                "c3_lpv_mimo": "lpv_state_space_order2_2in_2out_api_fwd_B32_T1048576_f32",
+                "c3_lpv_mimo_grad": "lpv_state_space_order2_2in_2out_api_fwd_bwd_x_zi_B32_T1048576_f32",
+                "c3_lpv_mimo_coef": "lpv_state_space_order2_2in_2out_api_fwd_bwd_all_B32_T1048576_f32",
                 "c5": "lpv_scan_fwd_bwd_B8_T16777216_f32",
                 "c5_f64": "lpv_scan_fwd_bwd_B8_T16777216_f64",
             }[w.name],

@@ -480,6 +480,9 @@ struct LpvMimoShape {
   static constexpr int kTile = kWaves * kSpan;
   static constexpr int kPlane = kSpan + 16 / int(sizeof(E));
   static constexpr int kWaveElems = kMimoMaxIO * kPlane;
+  // waves per SIMD of the launch bounds: orders 1-2 fit 168 VGPRs (3 waves,
+  // three workgroups per CU), orders 3-4 take 256 (2)
+  static constexpr int kMinWaves = kM <= 2 ? 3 : 2;
 };
 
 // A lane's K matrices A[t] in scan order from scan position s0 (past the
@@ -537,7 +540,8 @@ __device__ __noinline__ typename Alg::state lpv_mimo_prefix_fallback(const MimoA
 }
 
 template <class Alg, bool REV>
-__global__ __launch_bounds__(LpvMimoShape<Alg>::kThreads, 2) void lpv_mimo_kernel(MimoArgs<Alg> a) {
+__global__ __launch_bounds__(LpvMimoShape<Alg>::kThreads, LpvMimoShape<Alg>::kMinWaves) void lpv_mimo_kernel(
+    MimoArgs<Alg> a) {
   using E = typename Alg::elem;
   using S = typename Alg::state;
   using SC = typename Alg::s_coef;
