@@ -93,8 +93,8 @@ int mimo_ss(int F, int P, int64_t B, int64_t T, const void *A, const void *Bm, c
 // each wanted or not.  A block sums `chunk` steps of one row: each thread its
 // strided steps in compute precision, then the block through LDS, one
 // partial (the four products as 4 x 4 blocks) per (row, block); the second
-// kernel sums the partials in row and block order, over the rows too for a
-// shared operand.  (Four separate sums of one product each read lambda, h,
+// kernel sums each row's partials, the third the row totals of a product
+// shared by the rows, each in a fixed order.  (Four separate sums of one product each read lambda, h,
 // x and g twice: 372 against 93 us for one of them at the c4_mimo shape.)
 constexpr int kSumThreads = 256;
 constexpr int kSumSteps = 64;  // steps per thread and block
@@ -108,10 +108,23 @@ struct GradSumIn {
   unsigned want;  // bit i: product i (A, B, C, D)
 };
 
-template <typename E>
+// One step's operands in compute precision, each padded to W with zeros.
+template <typename C, int W>
+struct SumStep {
+  C l[W], h[W], u[W], g[W];
+};
+
+// The partial kernel at a padded width W = max(M, F, P): the four products'
+// accumulators take 4 W^2 registers (16 doubles at W = 2; padding every
+// model to 4 took 64 and 180 VGPRs, two waves per SIMD: 717 us at the C3
+// shape), and each thread keeps U steps' loads in flight per iteration.
+// (Staging a block's steps through LDS with two barriers per 256 steps
+// measured slower still: 1111 us.)
+template <typename E, int W, bool ALL>
 __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumIn<E> in, int64_t T,
                                                                         typename Wide<E>::type *part) {
   using C = typename Wide<E>::type;
+  constexpr int U = W <= 2 ? 4 : 2;
   __shared__ C s_red[kSumThreads / 64][kSumN];
   const int64_t b = blockIdx.y, blk = blockIdx.x;
   const int64_t chunk = int64_t(kSumThreads) * kSumSteps;
@@ -119,44 +132,84 @@ __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumI
   const int M = in.M, F = in.F, P = in.P;
   const bool wA = in.want & 1, wB = in.want & 2, wC = in.want & 4, wD = in.want & 8;
   const bool need_l = wA || wB, need_h = wA || wC, need_x = wB || wD, need_g = wC || wD;
-  C acc[4][kMimoMaxIO][kMimoMaxIO];
+  const E *__restrict__ lrow = need_l ? in.lam + b * T * M : nullptr;
+  const E *__restrict__ hrow = need_h ? in.hs + b * T * M : nullptr;
+  const E *__restrict__ xrow = need_x ? in.x + b * T * F : nullptr;
+  const E *__restrict__ grow = need_g ? in.g + b * T * P : nullptr;
+  auto load = [&](int64_t t, SumStep<C, W> &s) {
+    if constexpr (ALL) {
+      // every operand there: unconditional loads (an index past the width
+      // reads its last element, zeroed after), so a thread's U steps of
+      // loads are all in flight before the first use
+      E l[W], h[W], u[W], g[W];
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        l[i] = lrow[t * M + (i < M ? i : M - 1)];
+        h[i] = hrow[t * M + (i < M ? i : M - 1)];
+        u[i] = xrow[t * F + (i < F ? i : F - 1)];
+        g[i] = grow[t * P + (i < P ? i : P - 1)];
+      }
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        s.l[i] = i < M ? C(l[i]) : C(0);
+        s.h[i] = i < M ? C(h[i]) : C(0);
+        s.u[i] = i < F ? C(u[i]) : C(0);
+        s.g[i] = i < P ? C(g[i]) : C(0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        s.l[i] = s.h[i] = s.u[i] = s.g[i] = C(0);
+        if (need_l && i < M) s.l[i] = C(lrow[t * M + i]);
+        if (need_h && i < M) s.h[i] = C(hrow[t * M + i]);
+        if (need_x && i < F) s.u[i] = C(xrow[t * F + i]);
+        if (need_g && i < P) s.g[i] = C(grow[t * P + i]);
+      }
+    }
+  };
+  C acc[4][W][W];
 #pragma unroll
   for (int p = 0; p < 4; ++p)
 #pragma unroll
-    for (int i = 0; i < kMimoMaxIO; ++i)
+    for (int i = 0; i < W; ++i)
 #pragma unroll
-      for (int j = 0; j < kMimoMaxIO; ++j) acc[p][i][j] = C(0);
-  for (int64_t t = t0 + threadIdx.x; t < t1; t += kSumThreads) {
-    const int64_t bt = b * T + t;
-    C l[kMimoMaxIO], h[kMimoMaxIO], u[kMimoMaxIO], g[kMimoMaxIO];
+      for (int j = 0; j < W; ++j) acc[p][i][j] = C(0);
+  auto add_step = [&](const SumStep<C, W> &s) {
 #pragma unroll
-    for (int i = 0; i < kMimoMaxIO; ++i) {
-      l[i] = h[i] = u[i] = g[i] = C(0);
-      if (need_l && i < M) l[i] = C(in.lam[bt * M + i]);
-      if (need_h && i < M) h[i] = C(in.hs[bt * M + i]);
-      if (need_x && i < F) u[i] = C(in.x[bt * F + i]);
-      if (need_g && i < P) g[i] = C(in.g[bt * P + i]);
-    }
+    for (int i = 0; i < W; ++i)
 #pragma unroll
-    for (int i = 0; i < kMimoMaxIO; ++i)
-#pragma unroll
-      for (int j = 0; j < kMimoMaxIO; ++j) {
-        acc[0][i][j] = fma(l[i], h[j], acc[0][i][j]);
-        acc[1][i][j] = fma(l[i], u[j], acc[1][i][j]);
-        acc[2][i][j] = fma(g[i], h[j], acc[2][i][j]);
-        acc[3][i][j] = fma(g[i], u[j], acc[3][i][j]);
+      for (int j = 0; j < W; ++j) {
+        acc[0][i][j] = fma(s.l[i], s.h[j], acc[0][i][j]);
+        acc[1][i][j] = fma(s.l[i], s.u[j], acc[1][i][j]);
+        acc[2][i][j] = fma(s.g[i], s.h[j], acc[2][i][j]);
+        acc[3][i][j] = fma(s.g[i], s.u[j], acc[3][i][j]);
       }
+  };
+  int64_t t = t0 + threadIdx.x;
+  for (; t + (U - 1) * kSumThreads < t1; t += U * kSumThreads) {
+    SumStep<C, W> s[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) load(t + k * kSumThreads, s[k]);
+#pragma unroll
+    for (int k = 0; k < U; ++k) add_step(s[k]);
   }
-  // the wave's sums by DPP scans, then the block's through LDS
+  for (; t < t1; t += kSumThreads) {
+    SumStep<C, W> s;
+    load(t, s);
+    add_step(s);
+  }
+  // the wave's sums by DPP scans, then the block's through LDS (entries
+  // past W: zeros)
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   auto add = [](const C &p, const C &o) { return p + o; };
+  if (lane < kSumN) s_red[wv][lane] = C(0);
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
     if (!((in.want >> p) & 1)) continue;
 #pragma unroll
-    for (int i = 0; i < kMimoMaxIO; ++i)
+    for (int i = 0; i < W; ++i)
 #pragma unroll
-      for (int j = 0; j < kMimoMaxIO; ++j) {
+      for (int j = 0; j < W; ++j) {
         const C v = read_lane(wave_scan_incl(acc[p][i][j], lane, add), 63);
         if (lane == 0) s_red[wv][p * kSumBlock + i * kMimoMaxIO + j] = v;
       }
@@ -177,47 +230,72 @@ struct GradSumOut {
   int shared;     // bit i: product i summed over the rows too
 };
 
-// Block o < B: the per-row products of row o; block B: the shared ones over
-// every row.  Threads strided over the partials, then the block's sums
-// through LDS.
+// Block r: row r's partials summed, thread (entry k, lane group q0) over
+// every fourth partial (coalesced: a wave reads 64 consecutive entries),
+// then the four groups through LDS.  A product not summed over the rows is
+// written out; a shared one leaves the row's total in `rows` for the next
+// kernel.  (One block summing a shared product over every row's partials
+// took 66 us at the C3 shape.)
 template <typename E>
-__global__ __launch_bounds__(kSumThreads) void mimo_grad_finish_kernel(const typename Wide<E>::type *part,
-                                                                       int64_t B, int64_t blocks, GradSumOut<E> o) {
+__global__ __launch_bounds__(kSumThreads) void mimo_grad_rows_kernel(const typename Wide<E>::type *part,
+                                                                     int64_t blocks, GradSumOut<E> o,
+                                                                     typename Wide<E>::type *rows) {
   using C = typename Wide<E>::type;
-  __shared__ C s_red[kSumThreads / 64][kSumN];
+  constexpr int G = kSumThreads / kSumN;
+  __shared__ C s_red[G][kSumN];
   const int64_t r = blockIdx.x;
-  const bool shared_block = r == B;
-  unsigned mine = 0;  // the products this block writes
+  const int k = threadIdx.x % kSumN, q0 = threadIdx.x / kSumN;
+  const C *src = part + r * blocks * kSumN + k;
+  C v[4] = {C(0), C(0), C(0), C(0)};
+  int64_t q = q0;
+  for (; q + 3 * G < blocks; q += 4 * G) {
 #pragma unroll
-  for (int p = 0; p < 4; ++p)
-    if (o.out[p] && (((o.shared >> p) & 1) != 0) == shared_block) mine |= 1u << p;
-  if (!mine) return;
-  const int64_t p0 = shared_block ? 0 : r * blocks, n = shared_block ? B * blocks : blocks;
-  C acc[kSumN];
-#pragma unroll
-  for (int k = 0; k < kSumN; ++k) acc[k] = C(0);
-  for (int64_t q = threadIdx.x; q < n; q += kSumThreads) {
-#pragma unroll
-    for (int k = 0; k < kSumN; ++k)
-      if ((mine >> (k / kSumBlock)) & 1) acc[k] += part[(p0 + q) * kSumN + k];
+    for (int u = 0; u < 4; ++u) v[u] += src[(q + u * G) * kSumN];
   }
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  auto add = [](const C &a, const C &b) { return a + b; };
-#pragma unroll
-  for (int k = 0; k < kSumN; ++k) {
-    if (!((mine >> (k / kSumBlock)) & 1)) continue;
-    const C v = read_lane(wave_scan_incl(acc[k], lane, add), 63);
-    if (lane == 0) s_red[wv][k] = v;
-  }
+  for (; q < blocks; q += G) v[0] += src[q * kSumN];
+  s_red[q0][k] = (v[0] + v[1]) + (v[2] + v[3]);
   __syncthreads();
-  const int k = threadIdx.x, p = k / kSumBlock, i = (k % kSumBlock) / kMimoMaxIO, j = k % kMimoMaxIO;
-  if (k < kSumN && ((mine >> p) & 1) && i < o.rows[p] && j < o.cols[p]) {
-    C v = C(0);
+  if (threadIdx.x >= kSumN) return;
+  C t = C(0);
 #pragma unroll
-    for (int w = 0; w < kSumThreads / 64; ++w) v += s_red[w][k];
-    const int64_t row = shared_block ? 0 : r;
-    o.out[p][(row * o.rows[p] + i) * o.cols[p] + j] = down<E>(v);
+  for (int w = 0; w < G; ++w) t += s_red[w][k];
+  const int p = k / kSumBlock, i = (k % kSumBlock) / kMimoMaxIO, j = k % kMimoMaxIO;
+  if (!o.out[p] || i >= o.rows[p] || j >= o.cols[p]) return;
+  if ((o.shared >> p) & 1)
+    rows[r * kSumN + k] = t;
+  else
+    o.out[p][(r * o.rows[p] + i) * o.cols[p] + j] = down<E>(t);
+}
+
+// One block: the shared products, the row totals summed by thread (entry
+// k, row group q0) over every G-th row, then the groups through LDS.
+constexpr int kSharedThreads = 1024;
+
+template <typename E>
+__global__ __launch_bounds__(kSharedThreads) void mimo_grad_shared_kernel(const typename Wide<E>::type *rows,
+                                                                          int64_t B, GradSumOut<E> o) {
+  using C = typename Wide<E>::type;
+  constexpr int G = kSharedThreads / kSumN;
+  __shared__ C s_red[G][kSumN];
+  const int k = threadIdx.x % kSumN, q0 = threadIdx.x / kSumN;
+  const int p = k / kSumBlock, i = (k % kSumBlock) / kMimoMaxIO, j = k % kMimoMaxIO;
+  const bool mine = o.out[p] && ((o.shared >> p) & 1) && i < o.rows[p] && j < o.cols[p];
+  C v[4] = {C(0), C(0), C(0), C(0)};
+  if (mine) {
+    int64_t q = q0;
+    for (; q + 3 * G < B; q += 4 * G) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] += rows[(q + u * G) * kSumN + k];
+    }
+    for (; q < B; q += G) v[0] += rows[q * kSumN + k];
   }
+  s_red[q0][k] = (v[0] + v[1]) + (v[2] + v[3]);
+  __syncthreads();
+  if (threadIdx.x >= kSumN || !mine) return;
+  C t = C(0);
+#pragma unroll
+  for (int w = 0; w < G; ++w) t += s_red[w][k];
+  o.out[p][i * o.cols[p] + j] = down<E>(t);
 }
 
 template <typename E>
@@ -248,13 +326,29 @@ int grad_sums(int M, int F, int P, int64_t B, int64_t T, const void *lam, const 
   if (B > 65535) return PHS_ERR_INVALID;
   const int64_t chunk = int64_t(kSumThreads) * kSumSteps;
   const int64_t blocks = (T + chunk - 1) / chunk;
+  if (!scratch || scratch_bytes < size_t(B) * size_t(blocks + 1) * kSumN * sizeof(C)) return PHS_ERR_WORKSPACE;
   if (blocks > 0) {
-    if (!scratch || scratch_bytes < size_t(B) * size_t(blocks) * kSumN * sizeof(C)) return PHS_ERR_WORKSPACE;
-    hipLaunchKernelGGL(mimo_grad_partial_kernel<E>, dim3(unsigned(blocks), unsigned(B)), dim3(kSumThreads), 0,
-                       stream, in, T, static_cast<C *>(scratch));
+    const int W = M > F ? (M > P ? M : P) : (F > P ? F : P);
+    // all: the wanted products read every one of lambda, h, x and g
+    const bool all = (in.want & 3) && (in.want & 5) && (in.want & 10) && (in.want & 12);
+    auto pick = [&](auto w) {
+      constexpr int Wc = decltype(w)::value;
+      return all ? mimo_grad_partial_kernel<E, Wc, true> : mimo_grad_partial_kernel<E, Wc, false>;
+    };
+    auto kern = W == 1   ? pick(std::integral_constant<int, 1>{})
+                : W == 2 ? pick(std::integral_constant<int, 2>{})
+                : W == 3 ? pick(std::integral_constant<int, 3>{})
+                         : pick(std::integral_constant<int, 4>{});
+    hipLaunchKernelGGL(kern, dim3(unsigned(blocks), unsigned(B)), dim3(kSumThreads), 0, stream, in, T,
+                       static_cast<C *>(scratch));
   }
-  hipLaunchKernelGGL(mimo_grad_finish_kernel<E>, dim3(unsigned(B + 1)), dim3(kSumThreads), 0, stream,
-                     static_cast<const C *>(scratch), B, blocks, o);
+  C *part = static_cast<C *>(scratch), *row_tot = part + B * blocks * kSumN;
+  hipLaunchKernelGGL(mimo_grad_rows_kernel<E>, dim3(unsigned(B)), dim3(kSumThreads), 0, stream, part, blocks, o,
+                     row_tot);
+  bool any_shared = false;
+  for (int p = 0; p < 4; ++p) any_shared |= o.out[p] && ((shared >> p) & 1);
+  if (any_shared)
+    hipLaunchKernelGGL(mimo_grad_shared_kernel<E>, dim3(1), dim3(kSharedThreads), 0, stream, row_tot, B, o);
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
@@ -404,7 +498,8 @@ int phs_lpv_mimo_ss(int dtype, int M, int F, int P, int64_t B, int64_t T, const 
 size_t phs_mimo_ss_grad_sums_scratch_size(int dtype, int64_t B, int64_t T) {
   if (B < 0 || T < 0 || (dtype != PHS_F32 && dtype != PHS_F64)) return 0;
   const int64_t chunk = int64_t(phs::kSumThreads) * phs::kSumSteps;
-  return size_t(B) * size_t((T + chunk - 1) / chunk) * phs::kSumN * sizeof(double);
+  // the partials of every (row, block), then one total per row
+  return size_t(B) * size_t((T + chunk - 1) / chunk + 1) * phs::kSumN * sizeof(double);
 }
 
 int phs_mimo_ss_grad_sums(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *lam, const void *hs,

@@ -195,11 +195,13 @@ def test_mimo_ss_capi_errors(api):
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
 @pytest.mark.parametrize("M,F,P", [(1, 1, 1), (4, 4, 4), (3, 2, 1), (2, 4, 3)])
-@pytest.mark.parametrize("Bn,T", [(1, 1), (3, 700), (2, 16384), (2, 16385), (3, 100003)])
+@pytest.mark.parametrize("Bn,T", [(1, 1), (3, 700), (2, 16384), (2, 16385), (3, 100003), (1, 200003), (70, 5)])
 def test_mimo_ss_grad_sums_capi(api, dtype, M, F, P, Bn, T):
     """phs_mimo_ss_grad_sums (the coefficient gradients' sums over time)
     against numpy's einsum in fp64: every product per row and over the rows,
-    subsets of the products, across its 16384-step blocks."""
+    subsets of the products (those reading all four signals and those
+    reading two or three), across its 16384-step blocks, past the unrolled
+    sums of a row's 13 blocks and of 70 rows' totals."""
     import torch
 
     lib, ws, capi = api
@@ -212,7 +214,7 @@ def test_mimo_ss_grad_sums_capi(api, dtype, M, F, P, Bn, T):
     dt = capi.DTYPES[np.dtype(dtype)]
     need = lib.phs_mimo_ss_grad_sums_scratch_size(dt, Bn, T)
     assert 0 < need <= ws.numel()
-    for want, shared in ((15, 0), (15, 15), (9, 1), (6, 4)):
+    for want, shared in ((15, 0), (15, 15), (9, 1), (6, 4), (8, 8), (3, 2), (1, 0)):
         outs = [torch.full(((1 if (shared >> i) & 1 else Bn),) + dims[i], float("nan"), dtype=dv["x"].dtype,
                            device="cuda") if (want >> i) & 1 else None for i in range(4)]
         print(f"grad_sums M={M} F={F} P={P} B={Bn} T={T} want={want} shared={shared}", flush=True)
