@@ -108,23 +108,25 @@ struct GradSumIn {
   unsigned want;  // bit i: product i (A, B, C, D)
 };
 
-// One step's operands in compute precision, each padded to W with zeros.
-template <typename C, int W>
+// One step's operands in compute precision: lambda and h padded to WM with
+// zeros, x and g to WI.
+template <typename C, int WM, int WI>
 struct SumStep {
-  C l[W], h[W], u[W], g[W];
+  C l[WM], h[WM], u[WI], g[WI];
 };
 
-// The partial kernel at a padded width W = max(M, F, P): the four products'
-// accumulators take 4 W^2 registers (16 doubles at W = 2; padding every
-// model to 4 took 64 and 180 VGPRs, two waves per SIMD: 717 us at the C3
-// shape), and each thread keeps U steps' loads in flight per iteration.
-// (Staging a block's steps through LDS with two barriers per 256 steps
-// measured slower still: 1111 us.)
-template <typename E, int W, bool ALL>
+// The partial kernel at padded widths WM >= M (the state) and WI >= F, P
+// (the input and output): the four products' accumulators take WM^2 +
+// 2 WM WI + WI^2 registers (16 doubles at WM = WI = 2; padding every model
+// to 4 took 64 and 180 VGPRs, two waves per SIMD: 717 us at the C3 shape),
+// and each thread keeps U steps' loads in flight per iteration.  (Staging
+// a block's steps through LDS with two barriers per 256 steps measured
+// slower still: 1111 us.)
+template <typename E, int WM, int WI, bool ALL>
 __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumIn<E> in, int64_t T,
                                                                         typename Wide<E>::type *part) {
   using C = typename Wide<E>::type;
-  constexpr int U = W <= 2 ? 4 : 2;
+  constexpr int U = WM + WI <= 6 ? 4 : 2;
   __shared__ C s_red[kSumThreads / 64][kSumN];
   const int64_t b = blockIdx.y, blk = blockIdx.x;
   const int64_t chunk = int64_t(kSumThreads) * kSumSteps;
@@ -136,65 +138,87 @@ __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumI
   const E *__restrict__ hrow = need_h ? in.hs + b * T * M : nullptr;
   const E *__restrict__ xrow = need_x ? in.x + b * T * F : nullptr;
   const E *__restrict__ grow = need_g ? in.g + b * T * P : nullptr;
-  auto load = [&](int64_t t, SumStep<C, W> &s) {
+  auto load = [&](int64_t t, SumStep<C, WM, WI> &s) {
     if constexpr (ALL) {
       // every operand there: unconditional loads (an index past the width
       // reads its last element, zeroed after), so a thread's U steps of
       // loads are all in flight before the first use
-      E l[W], h[W], u[W], g[W];
+      E l[WM], h[WM], u[WI], g[WI];
 #pragma unroll
-      for (int i = 0; i < W; ++i) {
+      for (int i = 0; i < WM; ++i) {
         l[i] = lrow[t * M + (i < M ? i : M - 1)];
         h[i] = hrow[t * M + (i < M ? i : M - 1)];
+      }
+#pragma unroll
+      for (int i = 0; i < WI; ++i) {
         u[i] = xrow[t * F + (i < F ? i : F - 1)];
         g[i] = grow[t * P + (i < P ? i : P - 1)];
       }
 #pragma unroll
-      for (int i = 0; i < W; ++i) {
+      for (int i = 0; i < WM; ++i) {
         s.l[i] = i < M ? C(l[i]) : C(0);
         s.h[i] = i < M ? C(h[i]) : C(0);
+      }
+#pragma unroll
+      for (int i = 0; i < WI; ++i) {
         s.u[i] = i < F ? C(u[i]) : C(0);
         s.g[i] = i < P ? C(g[i]) : C(0);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < W; ++i) {
-        s.l[i] = s.h[i] = s.u[i] = s.g[i] = C(0);
+      for (int i = 0; i < WM; ++i) {
+        s.l[i] = s.h[i] = C(0);
         if (need_l && i < M) s.l[i] = C(lrow[t * M + i]);
         if (need_h && i < M) s.h[i] = C(hrow[t * M + i]);
+      }
+#pragma unroll
+      for (int i = 0; i < WI; ++i) {
+        s.u[i] = s.g[i] = C(0);
         if (need_x && i < F) s.u[i] = C(xrow[t * F + i]);
         if (need_g && i < P) s.g[i] = C(grow[t * P + i]);
       }
     }
   };
-  C acc[4][W][W];
+  C aA[WM][WM], aB[WM][WI], aC[WI][WM], aD[WI][WI];
 #pragma unroll
-  for (int p = 0; p < 4; ++p)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int i = 0; i < W; ++i)
+    for (int j = 0; j < WM; ++j) aA[i][j] = C(0);
 #pragma unroll
-      for (int j = 0; j < W; ++j) acc[p][i][j] = C(0);
-  auto add_step = [&](const SumStep<C, W> &s) {
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int i = 0; i < W; ++i)
+    for (int j = 0; j < WI; ++j) aB[i][j] = aC[j][i] = C(0);
 #pragma unroll
-      for (int j = 0; j < W; ++j) {
-        acc[0][i][j] = fma(s.l[i], s.h[j], acc[0][i][j]);
-        acc[1][i][j] = fma(s.l[i], s.u[j], acc[1][i][j]);
-        acc[2][i][j] = fma(s.g[i], s.h[j], acc[2][i][j]);
-        acc[3][i][j] = fma(s.g[i], s.u[j], acc[3][i][j]);
+  for (int i = 0; i < WI; ++i)
+#pragma unroll
+    for (int j = 0; j < WI; ++j) aD[i][j] = C(0);
+  auto add_step = [&](const SumStep<C, WM, WI> &s) {
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WM; ++j) aA[i][j] = fma(s.l[i], s.h[j], aA[i][j]);
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WI; ++j) {
+        aB[i][j] = fma(s.l[i], s.u[j], aB[i][j]);
+        aC[j][i] = fma(s.g[j], s.h[i], aC[j][i]);
       }
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+      for (int j = 0; j < WI; ++j) aD[i][j] = fma(s.g[i], s.u[j], aD[i][j]);
   };
   int64_t t = t0 + threadIdx.x;
   for (; t + (U - 1) * kSumThreads < t1; t += U * kSumThreads) {
-    SumStep<C, W> s[U];
+    SumStep<C, WM, WI> s[U];
 #pragma unroll
     for (int k = 0; k < U; ++k) load(t + k * kSumThreads, s[k]);
 #pragma unroll
     for (int k = 0; k < U; ++k) add_step(s[k]);
   }
   for (; t < t1; t += kSumThreads) {
-    SumStep<C, W> s;
+    SumStep<C, WM, WI> s;
     load(t, s);
     add_step(s);
   }
@@ -203,17 +227,30 @@ __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumI
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   auto add = [](const C &p, const C &o) { return p + o; };
   if (lane < kSumN) s_red[wv][lane] = C(0);
+  auto put = [&](int p, int i, int j, const C &a) {
+    const C v = read_lane(wave_scan_incl(a, lane, add), 63);
+    if (lane == 0) s_red[wv][p * kSumBlock + i * kMimoMaxIO + j] = v;
+  };
+  if (wA)
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    if (!((in.want >> p) & 1)) continue;
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int i = 0; i < W; ++i)
+      for (int j = 0; j < WM; ++j) put(0, i, j, aA[i][j]);
+  if (wB)
 #pragma unroll
-      for (int j = 0; j < W; ++j) {
-        const C v = read_lane(wave_scan_incl(acc[p][i][j], lane, add), 63);
-        if (lane == 0) s_red[wv][p * kSumBlock + i * kMimoMaxIO + j] = v;
-      }
-  }
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WI; ++j) put(1, i, j, aB[i][j]);
+  if (wC)
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+      for (int j = 0; j < WM; ++j) put(2, i, j, aC[i][j]);
+  if (wD)
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+      for (int j = 0; j < WI; ++j) put(3, i, j, aD[i][j]);
   __syncthreads();
   if (threadIdx.x < kSumN && ((in.want >> (threadIdx.x / kSumBlock)) & 1)) {
     C v = C(0);
@@ -328,16 +365,18 @@ int grad_sums(int M, int F, int P, int64_t B, int64_t T, const void *lam, const 
   const int64_t blocks = (T + chunk - 1) / chunk;
   if (!scratch || scratch_bytes < size_t(B) * size_t(blocks + 1) * kSumN * sizeof(C)) return PHS_ERR_WORKSPACE;
   if (blocks > 0) {
-    const int W = M > F ? (M > P ? M : P) : (F > P ? F : P);
+    // the state's width exact, the input's and output's rounded to 2 or 4;
     // all: the wanted products read every one of lambda, h, x and g
+    const int WI = (F > P ? F : P) <= 2 ? 2 : 4;
     const bool all = (in.want & 3) && (in.want & 5) && (in.want & 10) && (in.want & 12);
-    auto pick = [&](auto w) {
-      constexpr int Wc = decltype(w)::value;
-      return all ? mimo_grad_partial_kernel<E, Wc, true> : mimo_grad_partial_kernel<E, Wc, false>;
+    auto pick = [&](auto wm) {
+      constexpr int WMc = decltype(wm)::value;
+      if (WI == 2) return all ? mimo_grad_partial_kernel<E, WMc, 2, true> : mimo_grad_partial_kernel<E, WMc, 2, false>;
+      return all ? mimo_grad_partial_kernel<E, WMc, 4, true> : mimo_grad_partial_kernel<E, WMc, 4, false>;
     };
-    auto kern = W == 1   ? pick(std::integral_constant<int, 1>{})
-                : W == 2 ? pick(std::integral_constant<int, 2>{})
-                : W == 3 ? pick(std::integral_constant<int, 3>{})
+    auto kern = M == 1   ? pick(std::integral_constant<int, 1>{})
+                : M == 2 ? pick(std::integral_constant<int, 2>{})
+                : M == 3 ? pick(std::integral_constant<int, 3>{})
                          : pick(std::integral_constant<int, 4>{});
     hipLaunchKernelGGL(kern, dim3(unsigned(blocks), unsigned(B)), dim3(kSumThreads), 0, stream, in, T,
                        static_cast<C *>(scratch));
