@@ -544,6 +544,13 @@ int phs_lpv_ss_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
 #define PHS_MIMO_B_SHARED 2
 #define PHS_MIMO_C_SHARED 4
 #define PHS_MIMO_D_SHARED 8
+/* Bits of phs_mimo_ss_grad_sums' `shared` only: gA receives lam[t] h[t]^T
+ * per step, [B,T,M,M], instead of its sum (the gradient of a time-varying
+ * A[t], phs_lpv_mimo_ss); with PHS_MIMO_A_STEPS_T too, its transpose h[t]
+ * lam[t]^T (the gradient of the A[t] a PHS_LPV_A_TRANSPOSED pass read).
+ * Not with PHS_MIMO_A_SHARED. */
+#define PHS_MIMO_A_STEPS 16
+#define PHS_MIMO_A_STEPS_T 32
 
 /* ---- Multi-input, multi-output LTI state space of order M = 1..4 with
  * F = 1..4 inputs and P = 1..4 outputs per step, fused (forward).  Replaces
@@ -610,8 +617,10 @@ int phs_lpv_mimo_ss(int dtype, int M, int F, int P, int64_t B, int64_t T, const 
  * phs_mimo_ss passes with C the identity), x [B,T,F] the input, g [B,T,P]
  * the upstream gradient; every output is nullable (not wanted), and an input
  * no wanted output reads may be NULL.  dtype PHS_F32 or PHS_F64, sums in
- * fp64.  `scratch`: phs_mimo_ss_grad_sums_scratch_size bytes, any
- * contents. */
+ * fp64.  PHS_MIMO_A_STEPS in `shared`: gA is the per-step product instead
+ * (each element rounded once from the exact product, as an fp32 or fp64
+ * multiply gives it).  `scratch`: phs_mimo_ss_grad_sums_scratch_size
+ * bytes, any contents. */
 size_t phs_mimo_ss_grad_sums_scratch_size(int dtype, int64_t B, int64_t T);
 
 int phs_mimo_ss_grad_sums(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *lam, const void *hs,

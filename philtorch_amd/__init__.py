@@ -841,8 +841,11 @@ if EXTENSION_LOADED and _has_op("mimo_ss"):
             st = lam if lam is not None else hs
             M = st.shape[2] if st is not None else 1
             dims = ((M, M), (M, x.shape[2]), (g.shape[2], M), (g.shape[2], x.shape[2]))
-            return [x.new_empty(((1 if (shared >> i) & 1 else x.shape[0]),) + dims[i]) if (want >> i) & 1
-                    else x.new_empty((0,)) for i in range(4)]
+            out = [x.new_empty(((1 if (shared >> i) & 1 else x.shape[0]),) + dims[i]) if (want >> i) & 1
+                   else x.new_empty((0,)) for i in range(4)]
+            if shared & 16 and want & 1:  # A per step
+                out[0] = x.new_empty((x.shape[0], x.shape[1], M, M))
+            return out
 
     def _mimo_ss_backward(ctx, gy, gzf):
         """The adjoint model (A^T, input matrix C^T, output matrix B^T, D^T)
@@ -926,10 +929,10 @@ if EXTENSION_LOADED and _has_op("lpv_mimo_ss"):
         matrix B^T, D^T) in the opposite time direction from dL/dzf gives
         grad_x and grad_zi in one more lpv_mimo_ss pass.  The coefficients:
         the states h[t] (the forward again with C = I, no D) and the adjoint
-        states lambda[t+1] (the adjoint pass with output matrix I), then
-        dL/dA[t] = lambda[t+1] h[t]^T per step (summed over the rows for a
-        shared A) and the sums over time of lambda x^T, g h^T, g x^T for B,
-        C, D (philtorch::mimo_ss_grad_sums).  Under create_graph: the
+        states lambda[t+1] (the adjoint pass with output matrix I), then one
+        pass of philtorch::mimo_ss_grad_sums writing dL/dA[t] = lambda[t+1]
+        h[t]^T per step (summed over the rows after, for a shared A) and
+        summing lambda x^T, g h^T, g x^T over time for B, C, D.  Under create_graph: the
         gradient of the composite the fused kernel replaces (B x, the native
         LPV scan, the state shift, C h + D x; philtorch/lpv/ssm.py:337-581),
         recomputed from the inputs and differentiable again."""
@@ -969,15 +972,13 @@ if EXTENSION_LOADED and _has_op("lpv_mimo_ss"):
                 hs, _ = op(A, B, eye, None, zi, x, rev, tr)
             if needs[0] or needs[1]:
                 lam, _ = op(A, Ct, eye, None, gzf, g, not rev, not tr)
-            if needs[0]:
-                gA = lam.unsqueeze(-1) * hs.unsqueeze(-2)  # dL/dA[t] = lambda[t+1] h[t]^T
-                if tr:
-                    gA = gA.mT
-                out[0] = gA.sum(0) if A.dim() == 3 else gA
-            want = sum(1 << i for i in (1, 2, 3) if needs[i] and inputs[i] is not None)
+            want = sum(1 << i for i in (0, 1, 2, 3) if needs[i] and inputs[i] is not None)
             if want:
                 shared = sum(1 << i for i, t in enumerate((A, B, C, D)) if i > 0 and t is not None and t.dim() == 2)
+                shared |= 16 | (32 if tr else 0)  # dL/dA[t] per step (transposed for A[t]^T)
                 sums = torch.ops.philtorch.mimo_ss_grad_sums(lam, hs, x, g, shared, want)
+                if want & 1:
+                    out[0] = sums[0].sum(0) if A.dim() == 3 else sums[0]
                 for i in (1, 2, 3):
                     if (want >> i) & 1:
                         out[i] = sums[i][0] if (shared >> i) & 1 else sums[i]

@@ -106,6 +106,9 @@ struct GradSumIn {
   const E *lam, *hs, *x, *g;  // [B, T, M], [B, T, M], [B, T, F], [B, T, P]
   int M, F, P;
   unsigned want;  // bit i: product i (A, B, C, D)
+  E *a_steps;     // non-null: lambda h^T per step [B, T, M, M] here, A not summed
+  int a_trans;    // a_steps holds h lambda^T
+  int a_vec;      // a_steps is 16-byte aligned
 };
 
 // One step's operands in compute precision: lambda and h padded to WM with
@@ -192,7 +195,8 @@ __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumI
   for (int i = 0; i < WI; ++i)
 #pragma unroll
     for (int j = 0; j < WI; ++j) aD[i][j] = C(0);
-  auto add_step = [&](const SumStep<C, WM, WI> &s) {
+  E *const arow = in.a_steps ? in.a_steps + b * T * M * M : nullptr;
+  auto add_sums = [&](const SumStep<C, WM, WI> &s) {
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -209,18 +213,47 @@ __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumI
 #pragma unroll
       for (int j = 0; j < WI; ++j) aD[i][j] = fma(s.g[i], s.u[j], aD[i][j]);
   };
+  auto add_step = [&](const SumStep<C, WM, WI> &s, int64_t t) {
+    if (arow) {
+      // the per-step product, rounded once (exact in compute precision);
+      // M = WM here.  A step's block in 16-byte stores where it is a whole
+      // number of them and the buffer 16-byte aligned
+      E v[WM * WM];
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WM; ++j) v[in.a_trans ? j * WM + i : i * WM + j] = down<E>(s.l[i] * s.h[j]);
+      E *dst = arow + t * WM * WM;
+      constexpr int kPer16 = 16 / int(sizeof(E));
+      if constexpr ((WM * WM) % kPer16 == 0) {
+        using V16 = typename std::conditional<sizeof(E) == 4, float4, double2>::type;
+        if (in.a_vec) {
+#pragma unroll
+          for (int k = 0; k < WM * WM / kPer16; ++k) {
+            V16 w;
+            __builtin_memcpy(&w, v + k * kPer16, 16);
+            reinterpret_cast<V16 *>(dst)[k] = w;
+          }
+          return add_sums(s);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < WM * WM; ++k) dst[k] = v[k];
+    }
+    add_sums(s);
+  };
   int64_t t = t0 + threadIdx.x;
   for (; t + (U - 1) * kSumThreads < t1; t += U * kSumThreads) {
     SumStep<C, WM, WI> s[U];
 #pragma unroll
     for (int k = 0; k < U; ++k) load(t + k * kSumThreads, s[k]);
 #pragma unroll
-    for (int k = 0; k < U; ++k) add_step(s[k]);
+    for (int k = 0; k < U; ++k) add_step(s[k], t + k * kSumThreads);
   }
   for (; t < t1; t += kSumThreads) {
     SumStep<C, WM, WI> s;
     load(t, s);
-    add_step(s);
+    add_step(s, t);
   }
   // the wave's sums by DPP scans, then the block's through LDS (entries
   // past W: zeros)
@@ -231,7 +264,7 @@ __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumI
     const C v = read_lane(wave_scan_incl(a, lane, add), 63);
     if (lane == 0) s_red[wv][p * kSumBlock + i * kMimoMaxIO + j] = v;
   };
-  if (wA)
+  if (wA && !arow)
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -252,7 +285,8 @@ __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumI
 #pragma unroll
       for (int j = 0; j < WI; ++j) put(3, i, j, aD[i][j]);
   __syncthreads();
-  if (threadIdx.x < kSumN && ((in.want >> (threadIdx.x / kSumBlock)) & 1)) {
+  const unsigned summed = arow ? in.want & ~1u : in.want;
+  if (threadIdx.x < kSumN && ((summed >> (threadIdx.x / kSumBlock)) & 1)) {
     C v = C(0);
 #pragma unroll
     for (int k = 0; k < kSumThreads / 64; ++k) v += s_red[k][threadIdx.x];
@@ -342,12 +376,15 @@ int grad_sums(int M, int F, int P, int64_t B, int64_t T, const void *lam, const 
   using C = typename Wide<E>::type;
   if (B < 0 || T < 0 || M < 1 || M > kMimoMaxIO || F < 1 || F > kMimoMaxIO || P < 1 || P > kMimoMaxIO)
     return PHS_ERR_INVALID;
-  if (shared & ~(PHS_MIMO_A_SHARED | PHS_MIMO_B_SHARED | PHS_MIMO_C_SHARED | PHS_MIMO_D_SHARED))
+  if (shared & ~(PHS_MIMO_A_SHARED | PHS_MIMO_B_SHARED | PHS_MIMO_C_SHARED | PHS_MIMO_D_SHARED | PHS_MIMO_A_STEPS |
+                 PHS_MIMO_A_STEPS_T))
     return PHS_ERR_INVALID;
+  const bool steps = shared & PHS_MIMO_A_STEPS;
+  if ((steps && (shared & PHS_MIMO_A_SHARED)) || (!steps && (shared & PHS_MIMO_A_STEPS_T))) return PHS_ERR_INVALID;
   GradSumIn<E> in{static_cast<const E *>(lam), static_cast<const E *>(hs), static_cast<const E *>(x),
-                  static_cast<const E *>(g), M, F, P, 0u};
+                  static_cast<const E *>(g), M, F, P, 0u, nullptr, (shared & PHS_MIMO_A_STEPS_T) ? 1 : 0, 0};
   GradSumOut<E> o{};
-  void *outs[4] = {gA, gB, gC, gD};
+  void *outs[4] = {steps ? nullptr : gA, gB, gC, gD};
   const int rows[4] = {M, M, P, P}, cols[4] = {M, F, M, F};
   for (int p = 0; p < 4; ++p) {
     o.out[p] = static_cast<E *>(outs[p]);
@@ -355,7 +392,12 @@ int grad_sums(int M, int F, int P, int64_t B, int64_t T, const void *lam, const 
     o.cols[p] = cols[p];
     if (outs[p]) in.want |= 1u << p;
   }
-  o.shared = shared;
+  if (steps && gA) {
+    in.want |= 1u;  // reads lambda and h
+    in.a_steps = static_cast<E *>(gA);
+    in.a_vec = aligned16(gA);
+  }
+  o.shared = shared & 15;
   if (!in.want || B == 0) return PHS_OK;
   if (T > 0 && (((in.want & 3) && !lam) || ((in.want & 5) && !hs) || ((in.want & 10) && !x) ||
                 ((in.want & 12) && !g)))

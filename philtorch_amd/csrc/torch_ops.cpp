@@ -1126,12 +1126,18 @@ std::tuple<Tensor, Tensor> lpv_mimo_ss_hip(const Tensor &A, const Tensor &Bm, co
 // (phs_mimo_ss_grad_sums): lam, hs (batch, T, M) (None where no wanted
 // output reads them), x (batch, T, F), g (batch, T, P); `want` and `shared`
 // bit i for A, B, C, D.  Returns [gA, gB, gC, gD], each (batch or 1, rows,
-// cols) as its bit in `shared` says, an empty tensor where not wanted.
+// cols) as its bit in `shared` says, an empty tensor where not wanted;
+// with PHS_MIMO_A_STEPS (and _T) in `shared`, gA is (batch, T, M, M), the
+// per-step product lam[t] h[t]^T (transposed).
 std::vector<Tensor> mimo_ss_grad_sums_hip(const std::optional<Tensor> &lam, const std::optional<Tensor> &hs,
                                           const Tensor &x, const Tensor &g, int64_t shared, int64_t want) {
   TORCH_CHECK(x.dim() == 3 && g.dim() == 3 && g.size(0) == x.size(0) && g.size(1) == x.size(1),
               "philtorch::mimo_ss_grad_sums: x and g must be (batch, T, F) and (batch, T, P)");
-  TORCH_CHECK((want & ~15) == 0 && (shared & ~15) == 0, "philtorch::mimo_ss_grad_sums: want and shared are 4-bit masks");
+  TORCH_CHECK((want & ~15) == 0 && (shared & ~63) == 0,
+              "philtorch::mimo_ss_grad_sums: want is a 4-bit mask, shared a 6-bit one");
+  const bool steps = shared & PHS_MIMO_A_STEPS;
+  TORCH_CHECK(!(steps && (shared & PHS_MIMO_A_SHARED)) && (steps || !(shared & PHS_MIMO_A_STEPS_T)),
+              "philtorch::mimo_ss_grad_sums: A per step is neither shared nor transposed without A_STEPS");
   const int64_t B = x.size(0), T = x.size(1), F = x.size(2), P = g.size(2);
   const bool need_l = want & 3, need_h = want & 5;
   TORCH_CHECK(!need_l || lam, "philtorch::mimo_ss_grad_sums: gradients of A or B need lam");
@@ -1156,7 +1162,9 @@ std::vector<Tensor> mimo_ss_grad_sums_hip(const std::optional<Tensor> &lam, cons
   const int64_t rows[4] = {M, M, P, P}, cols[4] = {M, F, M, F};
   std::vector<Tensor> out(4);
   for (int p = 0; p < 4; ++p) {
-    if ((want >> p) & 1) {
+    if (p == 0 && steps && (want & 1)) {
+      out[p] = at::empty({B, T, M, M}, x.options());
+    } else if ((want >> p) & 1) {
       out[p] = at::empty({((shared >> p) & 1) ? int64_t(1) : B, rows[p], cols[p]}, x.options());
       if (B == 0 || T == 0) out[p].zero_();
     } else {

@@ -17,6 +17,7 @@ HEADER = os.path.join(REPO, "include", "philscan.h")
 PHS_OK, PHS_ERR_INVALID, PHS_ERR_WORKSPACE, PHS_ERR_LAUNCH, PHS_ERR_DTYPE, PHS_ERR_TOO_LARGE = range(6)
 PHS_LPV_A_SHARED, PHS_LPV_A_TRANSPOSED = 1, 2
 PHS_MIMO_A_SHARED, PHS_MIMO_B_SHARED, PHS_MIMO_C_SHARED, PHS_MIMO_D_SHARED = 1, 2, 4, 8
+PHS_MIMO_A_STEPS, PHS_MIMO_A_STEPS_T = 16, 32
 # phs_padmode codes (torch.nn.functional.pad modes)
 PADMODES = {"constant": 0, "replicate": 1, "reflect": 2, "circular": 3}
 OPS = {"recur": 0, "lti_recur": 1, "recur2": 2, "lti_recur2": 3}

@@ -201,7 +201,9 @@ def test_mimo_ss_grad_sums_capi(api, dtype, M, F, P, Bn, T):
     against numpy's einsum in fp64: every product per row and over the rows,
     subsets of the products (those reading all four signals and those
     reading two or three), across its 16384-step blocks, past the unrolled
-    sums of a row's 13 blocks and of 70 rows' totals."""
+    sums of a row's 13 blocks and of 70 rows' totals; A's product per step
+    (PHS_MIMO_A_STEPS, transposed or not) bit-exact against numpy's
+    product in the same dtype."""
     import torch
 
     lib, ws, capi = api
@@ -214,9 +216,13 @@ def test_mimo_ss_grad_sums_capi(api, dtype, M, F, P, Bn, T):
     dt = capi.DTYPES[np.dtype(dtype)]
     need = lib.phs_mimo_ss_grad_sums_scratch_size(dt, Bn, T)
     assert 0 < need <= ws.numel()
-    for want, shared in ((15, 0), (15, 15), (9, 1), (6, 4), (8, 8), (3, 2), (1, 0)):
+    steps_ref = hl["lam"][..., :, None] * hl["hs"][..., None, :]  # per-step products, rounded once
+    for want, shared in ((15, 0), (15, 15), (9, 1), (6, 4), (8, 8), (3, 2), (1, 0), (1, 16), (15, 16 | 32 | 2),
+                         (11, 16 | 8)):
         outs = [torch.full(((1 if (shared >> i) & 1 else Bn),) + dims[i], float("nan"), dtype=dv["x"].dtype,
                            device="cuda") if (want >> i) & 1 else None for i in range(4)]
+        if shared & 16:
+            outs[0] = torch.full((Bn, T, M, M), float("nan"), dtype=dv["x"].dtype, device="cuda")
         print(f"grad_sums M={M} F={F} P={P} B={Bn} T={T} want={want} shared={shared}", flush=True)
         rc = lib.phs_mimo_ss_grad_sums(dt, M, F, P, Bn, T, _p(dv["lam"]), _p(dv["hs"]), _p(dv["x"]), _p(dv["g"]),
                                        shared, *(_p(o) for o in outs), _p(ws), need,
@@ -225,6 +231,10 @@ def test_mimo_ss_grad_sums_capi(api, dtype, M, F, P, Bn, T):
         torch.cuda.synchronize()
         for i in range(4):
             if outs[i] is None:
+                continue
+            if i == 0 and shared & 16:  # A per step: bit-exact
+                ref = np.swapaxes(steps_ref, -1, -2) if shared & 32 else steps_ref
+                np.testing.assert_array_equal(outs[0].cpu().numpy(), ref, err_msg=f"A per step shared={shared}")
                 continue
             want_i = refs[i].sum(0, keepdims=True) if (shared >> i) & 1 else refs[i]
             # sums of T products: the bound scales with sqrt(T) times the terms' size

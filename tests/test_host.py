@@ -445,7 +445,9 @@ def test_capi_mimo_state_space_host_only_calls():
         return lib.phs_mimo_ss_grad_sums(dt, M, F, P, 2, 100, lam, d, d, d, shared, gA, None, None, gD, d, sb, None)
 
     assert gsum(dt=2) == capi.PHS_ERR_DTYPE
-    for bad in (dict(M=0), dict(F=5), dict(P=0), dict(shared=16), dict(lam=None)):
+    steps, steps_t = capi.PHS_MIMO_A_STEPS, capi.PHS_MIMO_A_STEPS_T
+    for bad in (dict(M=0), dict(F=5), dict(P=0), dict(shared=64), dict(lam=None), dict(shared=steps | 1),
+                dict(shared=steps_t), dict(shared=steps | steps_t, lam=None)):
         assert gsum(**bad) == capi.PHS_ERR_INVALID, bad
     assert gsum(sb=8) == capi.PHS_ERR_WORKSPACE
     assert gsum(gA=None) == capi.PHS_OK  # nothing wanted: nothing launched
