@@ -988,8 +988,9 @@ class LpvMimoGrad(LpvMimoApi):
 class LpvMimoCoefGrad(LpvMimoGrad):
     """c3_lpv_mimo_coef: c3_lpv_mimo_grad with the gradients of A[t], B, C and
     D too: the adjoint pass, the forward again writing its states, the
-    adjoint again writing its states, dL/dA[t] = lambda[t+1] h[t]^T per step
-    and the sums over time for B, C, D (philtorch::mimo_ss_grad_sums)."""
+    adjoint again writing its states, and one philtorch::mimo_ss_grad_sums
+    pass writing dL/dA[t] = lambda[t+1] h[t]^T per step and summing over
+    time for B, C, D."""
 
     def __init__(self):
         super().__init__()
@@ -997,9 +998,9 @@ class LpvMimoCoefGrad(LpvMimoGrad):
         self.name = "c3_lpv_mimo_coef"
         self.metric = (f"GSamples/s fwd+bwd(x, zi, A, B, C, D), LPV lpv.state_space order 2, 2 inputs, 2 outputs "
                        f"per step B={B} T={T} fp32 (API)")
-        # adjoint, states and adjoint-states passes (32 each: A, one signal in, one out), dL/dA (read
-        # lambda and h, write 16), the sums (read lambda, h, x, g)
-        self.bwd_bytes = (32 + 32 + 32 + 32 + 32) * B * T
+        # adjoint, states and adjoint-states passes (32 each: A, one signal in, one out), the sums pass
+        # (read lambda, h, x, g: 32; write dL/dA[t]: 16)
+        self.bwd_bytes = (32 + 32 + 32 + 48) * B * T
         self.bwd_launch_bytes = 32 * B * T  # the adjoint pass
 
     def step_fwd(self):
