@@ -126,12 +126,13 @@ struct SumStep {
 // a block's steps through LDS with two barriers per 256 steps measured
 // slower still: 1111 us.)
 template <typename E, int WM, int WI, bool ALL>
-__global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumIn<E> in, int64_t T,
+__global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumIn<E> in, int64_t T, unsigned nblk,
                                                                         typename Wide<E>::type *part) {
   using C = typename Wide<E>::type;
   constexpr int U = WM + WI <= 6 ? 4 : 2;
   __shared__ C s_red[kSumThreads / 64][kSumN];
-  const int64_t b = blockIdx.y, blk = blockIdx.x;
+  // one workgroup per (row, block of steps), row-major
+  const int64_t b = blockIdx.x / nblk, blk = blockIdx.x - unsigned(b) * nblk;
   const int64_t chunk = int64_t(kSumThreads) * kSumSteps;
   const int64_t t0 = blk * chunk, t1 = t0 + chunk < T ? t0 + chunk : T;
   const int M = in.M, F = in.F, P = in.P;
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumI
     C v = C(0);
 #pragma unroll
     for (int k = 0; k < kSumThreads / 64; ++k) v += s_red[k][threadIdx.x];
-    part[(b * gridDim.x + blk) * kSumN + threadIdx.x] = v;
+    part[(b * nblk + blk) * kSumN + threadIdx.x] = v;
   }
 }
 
@@ -402,9 +403,9 @@ int grad_sums(int M, int F, int P, int64_t B, int64_t T, const void *lam, const 
   if (T > 0 && (((in.want & 3) && !lam) || ((in.want & 5) && !hs) || ((in.want & 10) && !x) ||
                 ((in.want & 12) && !g)))
     return PHS_ERR_INVALID;
-  if (B > 65535) return PHS_ERR_INVALID;
   const int64_t chunk = int64_t(kSumThreads) * kSumSteps;
   const int64_t blocks = (T + chunk - 1) / chunk;
+  if (double(B) * double(blocks) >= 2147483648.0 || B >= 2147483648LL) return PHS_ERR_INVALID;
   if (!scratch || scratch_bytes < size_t(B) * size_t(blocks + 1) * kSumN * sizeof(C)) return PHS_ERR_WORKSPACE;
   if (blocks > 0) {
     // the state's width exact, the input's and output's rounded to 2 or 4;
@@ -420,7 +421,7 @@ int grad_sums(int M, int F, int P, int64_t B, int64_t T, const void *lam, const 
                 : M == 2 ? pick(std::integral_constant<int, 2>{})
                 : M == 3 ? pick(std::integral_constant<int, 3>{})
                          : pick(std::integral_constant<int, 4>{});
-    hipLaunchKernelGGL(kern, dim3(unsigned(blocks), unsigned(B)), dim3(kSumThreads), 0, stream, in, T,
+    hipLaunchKernelGGL(kern, dim3(unsigned(B * blocks)), dim3(kSumThreads), 0, stream, in, T, unsigned(blocks),
                        static_cast<C *>(scratch));
   }
   C *part = static_cast<C *>(scratch), *row_tot = part + B * blocks * kSumN;

@@ -195,13 +195,15 @@ def test_mimo_ss_capi_errors(api):
 
 @pytest.mark.parametrize("dtype", FLOATS, ids=lambda d: np.dtype(d).name)
 @pytest.mark.parametrize("M,F,P", [(1, 1, 1), (4, 4, 4), (3, 2, 1), (2, 4, 3)])
-@pytest.mark.parametrize("Bn,T", [(1, 1), (3, 700), (2, 16384), (2, 16385), (3, 100003), (1, 200003), (70, 5)])
+@pytest.mark.parametrize("Bn,T", [(1, 1), (3, 700), (2, 16384), (2, 16385), (3, 100003), (1, 200003), (70, 5),
+                                  (70001, 3)])
 def test_mimo_ss_grad_sums_capi(api, dtype, M, F, P, Bn, T):
     """phs_mimo_ss_grad_sums (the coefficient gradients' sums over time)
     against numpy's einsum in fp64: every product per row and over the rows,
     subsets of the products (those reading all four signals and those
     reading two or three), across its 16384-step blocks, past the unrolled
-    sums of a row's 13 blocks and of 70 rows' totals; A's product per step
+    sums of a row's 13 blocks and of 70 rows' totals, more rows than a
+    grid dimension of 65535 holds; A's product per step
     (PHS_MIMO_A_STEPS, transposed or not) bit-exact against numpy's
     product in the same dtype."""
     import torch
@@ -215,7 +217,8 @@ def test_mimo_ss_grad_sums_capi(api, dtype, M, F, P, Bn, T):
     dims = [(M, M), (M, F), (P, M), (P, F)]
     dt = capi.DTYPES[np.dtype(dtype)]
     need = lib.phs_mimo_ss_grad_sums_scratch_size(dt, Bn, T)
-    assert 0 < need <= ws.numel()
+    assert 0 < need
+    scratch = ws if need <= ws.numel() else torch.empty(need, dtype=torch.uint8, device="cuda")
     steps_ref = hl["lam"][..., :, None] * hl["hs"][..., None, :]  # per-step products, rounded once
     for want, shared in ((15, 0), (15, 15), (9, 1), (6, 4), (8, 8), (3, 2), (1, 0), (1, 16), (15, 16 | 32 | 2),
                          (11, 16 | 8)):
@@ -225,7 +228,7 @@ def test_mimo_ss_grad_sums_capi(api, dtype, M, F, P, Bn, T):
             outs[0] = torch.full((Bn, T, M, M), float("nan"), dtype=dv["x"].dtype, device="cuda")
         print(f"grad_sums M={M} F={F} P={P} B={Bn} T={T} want={want} shared={shared}", flush=True)
         rc = lib.phs_mimo_ss_grad_sums(dt, M, F, P, Bn, T, _p(dv["lam"]), _p(dv["hs"]), _p(dv["x"]), _p(dv["g"]),
-                                       shared, *(_p(o) for o in outs), _p(ws), need,
+                                       shared, *(_p(o) for o in outs), _p(scratch), need,
                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         assert rc == capi.PHS_OK, lib.phs_error_string(rc)
         torch.cuda.synchronize()
