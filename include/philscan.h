@@ -619,13 +619,18 @@ int phs_lpv_mimo_ss(int dtype, int M, int F, int P, int64_t B, int64_t T, const 
  * no wanted output reads may be NULL.  dtype PHS_F32 or PHS_F64, sums in
  * fp64.  PHS_MIMO_A_STEPS in `shared`: gA is the per-step product instead
  * (each element rounded once from the exact product, as an fp32 or fp64
- * multiply gives it).  `scratch`: phs_mimo_ss_grad_sums_scratch_size
- * bytes, any contents. */
+ * multiply gives it).  gx (nullable) [B,T,F]: the input's gradient
+ * gx[t] = Bm^T lam[t] + Dm^T g[t] per step, from the model's Bm [B,M,F] and
+ * Dm [B,P,F] (NULL: no feedthrough), each one matrix with its
+ * PHS_MIMO_{B,D}_SHARED bit, summed in fp64 and rounded once: the adjoint
+ * pass that gives lam would give it with output matrix Bm^T, so one pass
+ * serves both.  `scratch`: phs_mimo_ss_grad_sums_scratch_size bytes, any
+ * contents. */
 size_t phs_mimo_ss_grad_sums_scratch_size(int dtype, int64_t B, int64_t T);
 
 int phs_mimo_ss_grad_sums(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *lam, const void *hs,
-                          const void *x, const void *g, int shared, void *gA, void *gB, void *gC, void *gD,
-                          void *scratch, size_t scratch_bytes, void *stream);
+                          const void *x, const void *g, const void *Bm, const void *Dm, int shared, void *gA,
+                          void *gB, void *gC, void *gD, void *gx, void *scratch, size_t scratch_bytes, void *stream);
 
 /* ---- Measurement helper, no counterpart in the reference.  A streaming
  * kernel with no scan: out_j[i] = (j + 1) * sum_k in_k[i] over n fp32

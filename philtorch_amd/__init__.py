@@ -837,7 +837,7 @@ if EXTENSION_LOADED and _has_op("mimo_ss"):
     if _has_op("mimo_ss_grad_sums"):
 
         @torch.library.register_fake("philtorch::mimo_ss_grad_sums")
-        def _(lam, hs, x, g, shared, want):
+        def _(lam, hs, x, g, shared, want, Bm=None, Dm=None):
             st = lam if lam is not None else hs
             M = st.shape[2] if st is not None else 1
             dims = ((M, M), (M, x.shape[2]), (g.shape[2], M), (g.shape[2], x.shape[2]))
@@ -845,12 +845,17 @@ if EXTENSION_LOADED and _has_op("mimo_ss"):
                    else x.new_empty((0,)) for i in range(4)]
             if shared & 16 and want & 1:  # A per step
                 out[0] = x.new_empty((x.shape[0], x.shape[1], M, M))
+            if want & 16:  # the input's gradient
+                out.append(x.new_empty(x.shape))
             return out
 
     def _mimo_ss_backward(ctx, gy, gzf):
         """The adjoint model (A^T, input matrix C^T, output matrix B^T, D^T)
         run in the opposite time direction from dL/dzf gives grad_x and
-        grad_zi in one more mimo_ss pass.  The coefficient gradients
+        grad_zi in one more mimo_ss pass; where the coefficient gradients
+        take the adjoint states (A or B wanted), their pass gives grad_zi and
+        the sums pass writes grad_x = B^T lambda[t+1] + D^T g[t] instead.
+        The coefficient gradients
             dL/dA = sum_t lambda[t+1] h[t]^T,  dL/dB = sum_t lambda[t+1] x[t]^T,
             dL/dC = sum_t g[t] h[t]^T,         dL/dD = sum_t g[t] x[t]^T
         take the states h[t] (the forward again with C = I and no D) and the
@@ -884,8 +889,11 @@ if EXTENSION_LOADED and _has_op("mimo_ss"):
         g = gy if gy is not None else x.new_zeros(x.size(0), x.size(1), C.size(-2))
         At, Ct = A.mT.contiguous(), C.mT.contiguous()
         eye = torch.eye(M, dtype=x.dtype, device=x.device)
+        # lambda is wanted for A or B: its pass also gives grad_zi, and the
+        # sums pass writes grad_x = B^T lambda + D^T g beside the sums
+        lam_pass = needs[0] or needs[1]
         with _op_ctx():
-            if needs[5] or (needs[4] and zi is not None):
+            if not lam_pass and (needs[5] or (needs[4] and zi is not None)):
                 gx, gzi = torch.ops.philtorch.mimo_ss(At, Ct, B.mT.contiguous(),
                                                       D.mT.contiguous() if D is not None else None, gzf, g,
                                                       not ctx.reverse)
@@ -894,16 +902,21 @@ if EXTENSION_LOADED and _has_op("mimo_ss"):
             hs = lam = None
             if needs[0] or needs[2]:
                 hs, _ = torch.ops.philtorch.mimo_ss(A, B, eye, None, zi, x, ctx.reverse)
-            if needs[0] or needs[1]:
-                lam, _ = torch.ops.philtorch.mimo_ss(At, Ct, eye, None, gzf, g, not ctx.reverse)
+            if lam_pass:
+                lam, gzi = torch.ops.philtorch.mimo_ss(At, Ct, eye, None, gzf, g, not ctx.reverse)
+                out[4] = gzi if needs[4] and zi is not None else None
         want = sum(1 << i for i in range(4) if needs[i] and inputs[i] is not None)
+        if lam_pass and needs[5]:
+            want |= 16
         if want:
             shared = sum(1 << i for i, t in enumerate((A, B, C, D)) if t is not None and t.dim() == 2)
             with _op_ctx():
-                sums = torch.ops.philtorch.mimo_ss_grad_sums(lam, hs, x, g, shared, want)
+                sums = torch.ops.philtorch.mimo_ss_grad_sums(lam, hs, x, g, shared, want, B, D)
             for i in range(4):
                 if (want >> i) & 1:
                     out[i] = sums[i][0] if (shared >> i) & 1 else sums[i]
+            if want & 16:
+                out[5] = sums[4]
         return tuple(out)
 
     torch.library.register_autograd("philtorch::mimo_ss", _mimo_ss_backward, setup_context=_mimo_ss_setup)
@@ -927,13 +940,15 @@ if EXTENSION_LOADED and _has_op("lpv_mimo_ss"):
     def _lpv_mimo_ss_backward(ctx, gy, gzf):
         """The adjoint model (A[t]^T read in place, input matrix C^T, output
         matrix B^T, D^T) in the opposite time direction from dL/dzf gives
-        grad_x and grad_zi in one more lpv_mimo_ss pass.  The coefficients:
-        the states h[t] (the forward again with C = I, no D) and the adjoint
-        states lambda[t+1] (the adjoint pass with output matrix I), then one
-        pass of philtorch::mimo_ss_grad_sums writing dL/dA[t] = lambda[t+1]
-        h[t]^T per step (summed over the rows after, for a shared A) and
-        summing lambda x^T, g h^T, g x^T over time for B, C, D.  Under create_graph: the
-        gradient of the composite the fused kernel replaces (B x, the native
+        grad_x and grad_zi in one more lpv_mimo_ss pass (where the
+        coefficient gradients take the adjoint states, their pass gives
+        grad_zi and the sums pass grad_x = B^T lambda[t+1] + D^T g[t]).
+        The coefficients: the states h[t] (the forward again with C = I, no
+        D) and the adjoint states lambda[t+1] (the adjoint pass with output
+        matrix I), then one pass of philtorch::mimo_ss_grad_sums writing
+        dL/dA[t] = lambda[t+1] h[t]^T per step (summed over the rows after,
+        for a shared A) and summing lambda x^T, g h^T, g x^T over time for
+        B, C, D.  Under create_graph: the gradient of the composite the fused kernel replaces (B x, the native
         LPV scan, the state shift, C h + D x; philtorch/lpv/ssm.py:337-581),
         recomputed from the inputs and differentiable again."""
         from .lpv.ssm import _lpv_mimo_composite
@@ -961,8 +976,11 @@ if EXTENSION_LOADED and _has_op("lpv_mimo_ss"):
         eye = torch.eye(M, dtype=x.dtype, device=x.device)
         rev, tr = ctx.reverse, ctx.transpose_A
         op = torch.ops.philtorch.lpv_mimo_ss
+        # lambda is wanted for A[t] or B: its pass also gives grad_zi, and
+        # the sums pass writes grad_x = B^T lambda + D^T g beside the sums
+        lam_pass = needs[0] or needs[1]
         with _op_ctx():
-            if needs[5] or (needs[4] and zi is not None):
+            if not lam_pass and (needs[5] or (needs[4] and zi is not None)):
                 gx, gzi = op(A, Ct, B.mT.contiguous(), D.mT.contiguous() if D is not None else None, gzf, g,
                              not rev, not tr)
                 out[5] = gx if needs[5] else None
@@ -970,18 +988,23 @@ if EXTENSION_LOADED and _has_op("lpv_mimo_ss"):
             hs = lam = None
             if needs[0] or needs[2]:
                 hs, _ = op(A, B, eye, None, zi, x, rev, tr)
-            if needs[0] or needs[1]:
-                lam, _ = op(A, Ct, eye, None, gzf, g, not rev, not tr)
+            if lam_pass:
+                lam, gzi = op(A, Ct, eye, None, gzf, g, not rev, not tr)
+                out[4] = gzi if needs[4] and zi is not None else None
             want = sum(1 << i for i in (0, 1, 2, 3) if needs[i] and inputs[i] is not None)
+            if lam_pass and needs[5]:
+                want |= 16
             if want:
                 shared = sum(1 << i for i, t in enumerate((A, B, C, D)) if i > 0 and t is not None and t.dim() == 2)
                 shared |= 16 | (32 if tr else 0)  # dL/dA[t] per step (transposed for A[t]^T)
-                sums = torch.ops.philtorch.mimo_ss_grad_sums(lam, hs, x, g, shared, want)
+                sums = torch.ops.philtorch.mimo_ss_grad_sums(lam, hs, x, g, shared, want, B, D)
                 if want & 1:
                     out[0] = sums[0].sum(0) if A.dim() == 3 else sums[0]
                 for i in (1, 2, 3):
                     if (want >> i) & 1:
                         out[i] = sums[i][0] if (shared >> i) & 1 else sums[i]
+                if want & 16:
+                    out[5] = sums[4]
         return tuple(out)
 
     torch.library.register_autograd("philtorch::lpv_mimo_ss", _lpv_mimo_ss_backward,

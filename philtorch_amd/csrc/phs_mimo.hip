@@ -109,6 +109,11 @@ struct GradSumIn {
   E *a_steps;     // non-null: lambda h^T per step [B, T, M, M] here, A not summed
   int a_trans;    // a_steps holds h lambda^T
   int a_vec;      // a_steps is 16-byte aligned
+  // non-null gx: B^T lambda[t] + D^T g[t] per step [B, T, F] (the input's
+  // gradient); Bm [B|1, M, F], Dm [B|1, P, F] or null, row strides 0 when shared
+  E *gx;
+  const E *Bm, *Dm;
+  int64_t b_stride, d_stride;
 };
 
 // One step's operands in compute precision: lambda and h padded to WM with
@@ -131,13 +136,14 @@ __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumI
   using C = typename Wide<E>::type;
   constexpr int U = WM + WI <= 6 ? 4 : 2;
   __shared__ C s_red[kSumThreads / 64][kSumN];
+  __shared__ C s_bd[2 * kSumBlock];  // gx: this row's B (M x F), then D (P x F), zero past them
   // one workgroup per (row, block of steps), row-major
   const int64_t b = blockIdx.x / nblk, blk = blockIdx.x - unsigned(b) * nblk;
   const int64_t chunk = int64_t(kSumThreads) * kSumSteps;
   const int64_t t0 = blk * chunk, t1 = t0 + chunk < T ? t0 + chunk : T;
   const int M = in.M, F = in.F, P = in.P;
-  const bool wA = in.want & 1, wB = in.want & 2, wC = in.want & 4, wD = in.want & 8;
-  const bool need_l = wA || wB, need_h = wA || wC, need_x = wB || wD, need_g = wC || wD;
+  const bool wA = in.want & 1, wB = in.want & 2, wC = in.want & 4, wD = in.want & 8, wx = in.gx != nullptr;
+  const bool need_l = wA || wB || wx, need_h = wA || wC, need_x = wB || wD, need_g = wC || wD || wx;
   const E *__restrict__ lrow = need_l ? in.lam + b * T * M : nullptr;
   const E *__restrict__ hrow = need_h ? in.hs + b * T * M : nullptr;
   const E *__restrict__ xrow = need_x ? in.x + b * T * F : nullptr;
@@ -197,6 +203,17 @@ __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumI
 #pragma unroll
     for (int j = 0; j < WI; ++j) aD[i][j] = C(0);
   E *const arow = in.a_steps ? in.a_steps + b * T * M * M : nullptr;
+  E *const gxrow = in.gx ? in.gx + b * T * F : nullptr;
+  if (in.gx) {
+    if (threadIdx.x < 2 * kSumBlock) {
+      const int k = threadIdx.x % kSumBlock;
+      C v = C(0);
+      if (threadIdx.x < kSumBlock && k < M * F) v = C(in.Bm[b * in.b_stride + k]);
+      if (threadIdx.x >= kSumBlock && in.Dm && k < P * F) v = C(in.Dm[b * in.d_stride + k]);
+      s_bd[threadIdx.x] = v;
+    }
+    __syncthreads();
+  }
   auto add_sums = [&](const SumStep<C, WM, WI> &s) {
 #pragma unroll
     for (int i = 0; i < WM; ++i)
@@ -215,15 +232,36 @@ __global__ __launch_bounds__(kSumThreads) void mimo_grad_partial_kernel(GradSumI
       for (int j = 0; j < WI; ++j) aD[i][j] = fma(s.g[i], s.u[j], aD[i][j]);
   };
   auto add_step = [&](const SumStep<C, WM, WI> &s, int64_t t) {
+    if (gxrow) {
+      // the input's gradient, rounded once: lambda and g are zero past M
+      // and P, and so are the entries of B and D past them
+#pragma unroll
+      for (int f = 0; f < WI; ++f) {
+        if (f >= F) break;
+        C v = C(0);
+#pragma unroll
+        for (int m = 0; m < WM; ++m) v = fma(s_bd[m * F + f], s.l[m], v);
+#pragma unroll
+        for (int q = 0; q < WI; ++q) v = fma(s_bd[kSumBlock + q * F + f], s.g[q], v);
+        gxrow[t * F + f] = down<E>(v);
+      }
+    }
     if (arow) {
       // the per-step product, rounded once (exact in compute precision);
       // M = WM here.  A step's block in 16-byte stores where it is a whole
       // number of them and the buffer 16-byte aligned
-      E v[WM * WM];
+      E v[WM * WM];  // compile-time indices on both branches: registers, not scratch
+      if (in.a_trans) {
 #pragma unroll
-      for (int i = 0; i < WM; ++i)
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < WM; ++j) v[in.a_trans ? j * WM + i : i * WM + j] = down<E>(s.l[i] * s.h[j]);
+          for (int j = 0; j < WM; ++j) v[j * WM + i] = down<E>(s.l[i] * s.h[j]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+          for (int j = 0; j < WM; ++j) v[i * WM + j] = down<E>(s.l[i] * s.h[j]);
+      }
       E *dst = arow + t * WM * WM;
       constexpr int kPer16 = 16 / int(sizeof(E));
       if constexpr ((WM * WM) % kPer16 == 0) {
@@ -372,8 +410,8 @@ __global__ __launch_bounds__(kSharedThreads) void mimo_grad_shared_kernel(const 
 
 template <typename E>
 int grad_sums(int M, int F, int P, int64_t B, int64_t T, const void *lam, const void *hs, const void *x,
-              const void *g, int shared, void *gA, void *gB, void *gC, void *gD, void *scratch, size_t scratch_bytes,
-              hipStream_t stream) {
+              const void *g, const void *Bm, const void *Dm, int shared, void *gA, void *gB, void *gC, void *gD,
+              void *gx, void *scratch, size_t scratch_bytes, hipStream_t stream) {
   using C = typename Wide<E>::type;
   if (B < 0 || T < 0 || M < 1 || M > kMimoMaxIO || F < 1 || F > kMimoMaxIO || P < 1 || P > kMimoMaxIO)
     return PHS_ERR_INVALID;
@@ -398,11 +436,18 @@ int grad_sums(int M, int F, int P, int64_t B, int64_t T, const void *lam, const 
     in.a_steps = static_cast<E *>(gA);
     in.a_vec = aligned16(gA);
   }
+  if (gx) {
+    if (!Bm) return PHS_ERR_INVALID;
+    in.gx = static_cast<E *>(gx);
+    in.Bm = static_cast<const E *>(Bm);
+    in.Dm = static_cast<const E *>(Dm);
+    in.b_stride = (shared & PHS_MIMO_B_SHARED) ? 0 : int64_t(M) * F;
+    in.d_stride = (shared & PHS_MIMO_D_SHARED) ? 0 : int64_t(P) * F;
+  }
   o.shared = shared & 15;
-  if (!in.want || B == 0) return PHS_OK;
-  if (T > 0 && (((in.want & 3) && !lam) || ((in.want & 5) && !hs) || ((in.want & 10) && !x) ||
-                ((in.want & 12) && !g)))
-    return PHS_ERR_INVALID;
+  if ((!in.want && !gx) || B == 0) return PHS_OK;
+  const bool need_l = (in.want & 3) || gx, need_h = in.want & 5, need_x = in.want & 10, need_g = (in.want & 12) || gx;
+  if (T > 0 && ((need_l && !lam) || (need_h && !hs) || (need_x && !x) || (need_g && !g))) return PHS_ERR_INVALID;
   const int64_t chunk = int64_t(kSumThreads) * kSumSteps;
   const int64_t blocks = (T + chunk - 1) / chunk;
   if (double(B) * double(blocks) >= 2147483648.0 || B >= 2147483648LL) return PHS_ERR_INVALID;
@@ -411,7 +456,7 @@ int grad_sums(int M, int F, int P, int64_t B, int64_t T, const void *lam, const 
     // the state's width exact, the input's and output's rounded to 2 or 4;
     // all: the wanted products read every one of lambda, h, x and g
     const int WI = (F > P ? F : P) <= 2 ? 2 : 4;
-    const bool all = (in.want & 3) && (in.want & 5) && (in.want & 10) && (in.want & 12);
+    const bool all = need_l && need_h && need_x && need_g;
     auto pick = [&](auto wm) {
       constexpr int WMc = decltype(wm)::value;
       if (WI == 2) return all ? mimo_grad_partial_kernel<E, WMc, 2, true> : mimo_grad_partial_kernel<E, WMc, 2, false>;
@@ -585,13 +630,15 @@ size_t phs_mimo_ss_grad_sums_scratch_size(int dtype, int64_t B, int64_t T) {
 }
 
 int phs_mimo_ss_grad_sums(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *lam, const void *hs,
-                          const void *x, const void *g, int shared, void *gA, void *gB, void *gC, void *gD,
-                          void *scratch, size_t scratch_bytes, void *stream) {
+                          const void *x, const void *g, const void *Bm, const void *Dm, int shared, void *gA,
+                          void *gB, void *gC, void *gD, void *gx, void *scratch, size_t scratch_bytes, void *stream) {
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == PHS_F32)
-    return phs::grad_sums<float>(M, F, P, B, T, lam, hs, x, g, shared, gA, gB, gC, gD, scratch, scratch_bytes, st);
+    return phs::grad_sums<float>(M, F, P, B, T, lam, hs, x, g, Bm, Dm, shared, gA, gB, gC, gD, gx, scratch,
+                                 scratch_bytes, st);
   if (dtype == PHS_F64)
-    return phs::grad_sums<double>(M, F, P, B, T, lam, hs, x, g, shared, gA, gB, gC, gD, scratch, scratch_bytes, st);
+    return phs::grad_sums<double>(M, F, P, B, T, lam, hs, x, g, Bm, Dm, shared, gA, gB, gC, gD, gx, scratch,
+                                  scratch_bytes, st);
   return PHS_ERR_DTYPE;
 }
 

@@ -1128,13 +1128,18 @@ std::tuple<Tensor, Tensor> lpv_mimo_ss_hip(const Tensor &A, const Tensor &Bm, co
 // bit i for A, B, C, D.  Returns [gA, gB, gC, gD], each (batch or 1, rows,
 // cols) as its bit in `shared` says, an empty tensor where not wanted;
 // with PHS_MIMO_A_STEPS (and _T) in `shared`, gA is (batch, T, M, M), the
-// per-step product lam[t] h[t]^T (transposed).
+// per-step product lam[t] h[t]^T (transposed).  want bit 4: a fifth tensor,
+// the input's gradient (batch, T, F) = Bm^T lam[t] + Dm^T g[t] from the
+// model's Bm (M, F) / (batch, M, F) and Dm None / (P, F) / (batch, P, F).
 std::vector<Tensor> mimo_ss_grad_sums_hip(const std::optional<Tensor> &lam, const std::optional<Tensor> &hs,
-                                          const Tensor &x, const Tensor &g, int64_t shared, int64_t want) {
+                                          const Tensor &x, const Tensor &g, int64_t shared, int64_t want,
+                                          const std::optional<Tensor> &Bm, const std::optional<Tensor> &Dm) {
   TORCH_CHECK(x.dim() == 3 && g.dim() == 3 && g.size(0) == x.size(0) && g.size(1) == x.size(1),
               "philtorch::mimo_ss_grad_sums: x and g must be (batch, T, F) and (batch, T, P)");
-  TORCH_CHECK((want & ~15) == 0 && (shared & ~63) == 0,
-              "philtorch::mimo_ss_grad_sums: want is a 4-bit mask, shared a 6-bit one");
+  TORCH_CHECK((want & ~31) == 0 && (shared & ~63) == 0,
+              "philtorch::mimo_ss_grad_sums: want is a 5-bit mask, shared a 6-bit one");
+  const bool want_gx = want & 16;
+  TORCH_CHECK(!want_gx || (lam && Bm), "philtorch::mimo_ss_grad_sums: the input's gradient needs lam and Bm");
   const bool steps = shared & PHS_MIMO_A_STEPS;
   TORCH_CHECK(!(steps && (shared & PHS_MIMO_A_SHARED)) && (steps || !(shared & PHS_MIMO_A_STEPS_T)),
               "philtorch::mimo_ss_grad_sums: A per step is neither shared nor transposed without A_STEPS");
@@ -1152,6 +1157,19 @@ std::vector<Tensor> mimo_ss_grad_sums_hip(const std::optional<Tensor> &lam, cons
   }
   if (lam) TORCH_CHECK(lam->size(2) == M, "philtorch::mimo_ss_grad_sums: lam and hs must both have M states");
   if (hs) TORCH_CHECK(hs->size(2) == M, "philtorch::mimo_ss_grad_sums: lam and hs must both have M states");
+  Tensor bc, dc;
+  if (want_gx) {
+    auto model = [&](const Tensor &t, int64_t r, int bit, const char *what) {
+      TORCH_CHECK(t.scalar_type() == x.scalar_type() && t.device() == x.device(),
+                  "philtorch::mimo_ss_grad_sums: ", what, " must have x's dtype and device");
+      const bool sh = (shared >> bit) & 1;
+      TORCH_CHECK(t.dim() == (sh ? 2 : 3) && (sh || t.size(0) == B) && t.size(-2) == r && t.size(-1) == F,
+                  "philtorch::mimo_ss_grad_sums: ", what, " must be (", r, ", ", F, "), or per row as its shared bit says");
+      return t.contiguous();
+    };
+    bc = model(*Bm, M, 1, "Bm");
+    if (Dm) dc = model(*Dm, P, 3, "Dm");
+  }
   TORCH_CHECK(x.scalar_type() == at::kFloat || x.scalar_type() == at::kDouble,
               "philtorch::mimo_ss_grad_sums: float32 or float64 only");
   TORCH_CHECK(x.is_cuda(), "philtorch::mimo_ss_grad_sums: HIP tensors only");
@@ -1160,7 +1178,8 @@ std::vector<Tensor> mimo_ss_grad_sums_hip(const std::optional<Tensor> &lam, cons
   Tensor lc = lam ? lam->contiguous() : Tensor(), hc = hs ? hs->contiguous() : Tensor();
   Tensor xc = x.contiguous(), gc = g.contiguous();
   const int64_t rows[4] = {M, M, P, P}, cols[4] = {M, F, M, F};
-  std::vector<Tensor> out(4);
+  std::vector<Tensor> out(want_gx ? 5 : 4);
+  if (want_gx) out[4] = at::empty({B, T, F}, x.options());
   for (int p = 0; p < 4; ++p) {
     if (p == 0 && steps && (want & 1)) {
       out[p] = at::empty({B, T, M, M}, x.options());
@@ -1177,8 +1196,10 @@ std::vector<Tensor> mimo_ss_grad_sums_hip(const std::optional<Tensor> &lam, cons
   auto ptr = [&](int p) { return ((want >> p) & 1) ? out[p].mutable_data_ptr() : nullptr; };
   check_status(phs_mimo_ss_grad_sums(dt, int(M), int(F), int(P), B, T, lam ? lc.const_data_ptr() : nullptr,
                                      hs ? hc.const_data_ptr() : nullptr, xc.const_data_ptr(), gc.const_data_ptr(),
-                                     int(shared), ptr(0), ptr(1), ptr(2), ptr(3), scratch.mutable_data_ptr(),
-                                     size_t(scratch.numel()), stream_of(x)),
+                                     want_gx ? bc.const_data_ptr() : nullptr,
+                                     want_gx && Dm ? dc.const_data_ptr() : nullptr, int(shared), ptr(0), ptr(1),
+                                     ptr(2), ptr(3), ptr(4), scratch.mutable_data_ptr(), size_t(scratch.numel()),
+                                     stream_of(x)),
                "mimo_ss_grad_sums");
   return out;
 }
@@ -1435,7 +1456,8 @@ TORCH_LIBRARY(philtorch, m) {
         {at::Tag::pt2_compliant_tag});
   m.def("mimo_ss(Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? zi, Tensor x, bool reverse=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
-  m.def("mimo_ss_grad_sums(Tensor? lam, Tensor? hs, Tensor x, Tensor g, int shared, int want) -> Tensor[]",
+  m.def("mimo_ss_grad_sums(Tensor? lam, Tensor? hs, Tensor x, Tensor g, int shared, int want, Tensor? Bm=None, "
+        "Tensor? Dm=None) -> Tensor[]",
         {at::Tag::pt2_compliant_tag});
   m.def("lpv_mimo_ss(Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? zi, Tensor x, bool reverse=False, "
         "bool transpose_A=False) -> (Tensor, Tensor)",

@@ -157,8 +157,8 @@ def load() -> ctypes.CDLL:
     lib.phs_lpv_mimo_ss.restype = ci
     lib.phs_mimo_ss_grad_sums_scratch_size.argtypes = [ci, i64, i64]
     lib.phs_mimo_ss_grad_sums_scratch_size.restype = ctypes.c_size_t
-    lib.phs_mimo_ss_grad_sums.argtypes = [ci, ci, ci, ci, i64, i64, vp, vp, vp, vp, ci, vp, vp, vp, vp, vp,
-                                          ctypes.c_size_t, vp]
+    lib.phs_mimo_ss_grad_sums.argtypes = [ci, ci, ci, ci, i64, i64, vp, vp, vp, vp, vp, vp, ci, vp, vp, vp, vp, vp,
+                                          vp, ctypes.c_size_t, vp]
     lib.phs_mimo_ss_grad_sums.restype = ci
     for name in ("phs_mimo_ss_fwd", "phs_mimo_ss_rev"):
         getattr(lib, name).argtypes = [ci, ci, ci, ci, i64, i64, vp, vp, vp, vp, ci, vp, vp, vp, vp, vp,

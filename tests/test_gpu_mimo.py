@@ -205,7 +205,8 @@ def test_mimo_ss_grad_sums_capi(api, dtype, M, F, P, Bn, T):
     sums of a row's 13 blocks and of 70 rows' totals, more rows than a
     grid dimension of 65535 holds; A's product per step
     (PHS_MIMO_A_STEPS, transposed or not) bit-exact against numpy's
-    product in the same dtype."""
+    product in the same dtype; the input's gradient B^T lambda + D^T g per
+    step (B and D per row, B shared without D, alone or beside the sums)."""
     import torch
 
     lib, ws, capi = api
@@ -220,18 +221,34 @@ def test_mimo_ss_grad_sums_capi(api, dtype, M, F, P, Bn, T):
     assert 0 < need
     scratch = ws if need <= ws.numel() else torch.empty(need, dtype=torch.uint8, device="cuda")
     steps_ref = hl["lam"][..., :, None] * hl["hs"][..., None, :]  # per-step products, rounded once
-    for want, shared in ((15, 0), (15, 15), (9, 1), (6, 4), (8, 8), (3, 2), (1, 0), (1, 16), (15, 16 | 32 | 2),
-                         (11, 16 | 8)):
+    # the model's B and D for the input's gradient, per row and shared
+    Bm_rows, Dm_rows = g.standard_normal((Bn, M, F)), g.standard_normal((Bn, P, F))
+    model = {n: _dev(v.astype(dtype)) for n, v in (("B", Bm_rows), ("D", Dm_rows), ("B1", Bm_rows[:1, :, :]),
+                                                       ("D1", Dm_rows[:1, :, :]))}
+    # (want, shared, input's gradient: None, "rows" (B, D per row), "shared" (one B, no D))
+    cases = ((15, 0, None), (15, 15, None), (9, 1, None), (6, 4, None), (8, 8, None), (3, 2, None), (1, 0, None),
+             (1, 16, None), (15, 16 | 32 | 2, None), (11, 16 | 8, None), (15, 0, "rows"), (0, 2 | 8, "shared"),
+             (1, 16, "rows"))
+    for want, shared, gxm in cases:
         outs = [torch.full(((1 if (shared >> i) & 1 else Bn),) + dims[i], float("nan"), dtype=dv["x"].dtype,
                            device="cuda") if (want >> i) & 1 else None for i in range(4)]
         if shared & 16:
             outs[0] = torch.full((Bn, T, M, M), float("nan"), dtype=dv["x"].dtype, device="cuda")
-        print(f"grad_sums M={M} F={F} P={P} B={Bn} T={T} want={want} shared={shared}", flush=True)
+        gx = torch.full((Bn, T, F), float("nan"), dtype=dv["x"].dtype, device="cuda") if gxm else None
+        bm = model["B"] if gxm == "rows" else model["B1"] if gxm else None
+        dm = model["D"] if gxm == "rows" else None
+        print(f"grad_sums M={M} F={F} P={P} B={Bn} T={T} want={want} shared={shared} gx={gxm}", flush=True)
         rc = lib.phs_mimo_ss_grad_sums(dt, M, F, P, Bn, T, _p(dv["lam"]), _p(dv["hs"]), _p(dv["x"]), _p(dv["g"]),
-                                       shared, *(_p(o) for o in outs), _p(scratch), need,
+                                       _p(bm), _p(dm), shared, *(_p(o) for o in outs), _p(gx), _p(scratch), need,
                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         assert rc == capi.PHS_OK, lib.phs_error_string(rc)
         torch.cuda.synchronize()
+        if gxm:  # B^T lambda + D^T g per step, from the model as the kernel read it, in fp64
+            bref = (Bm_rows if gxm == "rows" else np.broadcast_to(Bm_rows[:1], Bm_rows.shape)).astype(dtype)
+            gx_ref = np.einsum("bmf,btm->btf", bref.astype(np.float64), w64["lam"])
+            if gxm == "rows":
+                gx_ref += np.einsum("bpf,btp->btf", Dm_rows.astype(dtype).astype(np.float64), w64["g"])
+            D.check(gx.cpu().numpy(), gx_ref, f"input's gradient {gxm}", dtype=dtype, scale=1.0)
         for i in range(4):
             if outs[i] is None:
                 continue
@@ -260,8 +277,14 @@ def test_mimo_ss_grad_sums_op_and_empty_rows(hip):
     torch.testing.assert_close(none[3], torch.einsum("bti,btj->bij", g, x))
     e = torch.ops.philtorch.mimo_ss_grad_sums(None, None, x[:, :0], g[:, :0], 8, 8)
     assert e[3].shape == (1, 4, 3) and e[3].abs().sum() == 0
+    # the input's gradient beside the sums: B per row, D shared (bit 3)
+    Bm, Dm = t(3, 2, 3), t(4, 3)
+    *_, gx = torch.ops.philtorch.mimo_ss_grad_sums(lam, hs, x, g, 0b1000, 31, Bm, Dm)
+    torch.testing.assert_close(gx, torch.einsum("bmf,btm->btf", Bm, lam) + torch.einsum("pf,btp->btf", Dm, g))
     f = lambda v: v.float()  # noqa: E731
     torch.library.opcheck(torch.ops.philtorch.mimo_ss_grad_sums.default, (f(lam), f(hs), f(x), f(g), 5, 15))
+    torch.library.opcheck(torch.ops.philtorch.mimo_ss_grad_sums.default,
+                          (f(lam), f(hs), f(x), f(g), 8, 31, f(Bm), f(Dm)))
 
 
 # ---------------------------------------------------------------- torch API

@@ -441,13 +441,15 @@ def test_capi_mimo_state_space_host_only_calls():
     assert lib.phs_mimo_ss_grad_sums_scratch_size(0, 16, 480000) >= 16 * 30 * 64 * 8
     assert lib.phs_mimo_ss_grad_sums_scratch_size(2, 16, 100) == 0
 
-    def gsum(dt=0, M=2, F=2, P=3, shared=0, sb=1 << 20, lam=d, gA=d, gD=None):
-        return lib.phs_mimo_ss_grad_sums(dt, M, F, P, 2, 100, lam, d, d, d, shared, gA, None, None, gD, d, sb, None)
+    def gsum(dt=0, M=2, F=2, P=3, shared=0, sb=1 << 20, lam=d, gA=d, gD=None, bm=None, gx=None):
+        return lib.phs_mimo_ss_grad_sums(dt, M, F, P, 2, 100, lam, d, d, d, bm, None, shared, gA, None, None, gD, gx,
+                                         d, sb, None)
 
     assert gsum(dt=2) == capi.PHS_ERR_DTYPE
     steps, steps_t = capi.PHS_MIMO_A_STEPS, capi.PHS_MIMO_A_STEPS_T
     for bad in (dict(M=0), dict(F=5), dict(P=0), dict(shared=64), dict(lam=None), dict(shared=steps | 1),
-                dict(shared=steps_t), dict(shared=steps | steps_t, lam=None)):
+                dict(shared=steps_t), dict(shared=steps | steps_t, lam=None), dict(gx=d),
+                dict(gx=d, bm=d, lam=None)):
         assert gsum(**bad) == capi.PHS_ERR_INVALID, bad
     assert gsum(sb=8) == capi.PHS_ERR_WORKSPACE
     assert gsum(gA=None) == capi.PHS_OK  # nothing wanted: nothing launched
