@@ -865,9 +865,10 @@ class MimoSsGrad(MimoSsApi):
 
 class MimoSsCoefGrad(MimoSsGrad):
     """c4_mimo_coef: c4_mimo_grad with the gradients of A, B, C and D too:
-    the adjoint pass, the forward again writing its states (C = I), the
-    adjoint again writing its states, and one GEMM over time (and rows, for
-    the shared B, C, D) per operand."""
+    the forward again writing its states (C = I), the adjoint writing its
+    states (which also gives grad_zi), and one philtorch::mimo_ss_grad_sums
+    pass that sums the four products over time (and rows, for the shared B,
+    C, D) and writes grad_x = B^T lambda + D^T g."""
 
     def __init__(self):
         super().__init__()
@@ -875,10 +876,10 @@ class MimoSsCoefGrad(MimoSsGrad):
         self.name = "c4_mimo_coef"
         self.metric = (f"GSamples/s fwd+bwd(x, zi, A, B, C, D), lti.state_space order {M}, {F} inputs, {P} outputs "
                        f"per step B={B} T={T} fp32 (API)")
-        # adjoint (read g, write grad_x), states (read x, write h), adjoint states (read g, write lambda),
-        # then the sums read lambda and h (A), lambda and x (B), g and h (C), g and x (D)
-        self.bwd_bytes = 4 * ((P + F) + (F + M) + (P + M) + (2 * M) + (M + F) + (P + M) + (P + F)) * B * T
-        self.bwd_launch_bytes = 4 * (P + F) * B * T  # the adjoint pass
+        # states (read x, write h), adjoint states (read g, write lambda), then the sums pass (read
+        # lambda, h, x, g; write grad_x)
+        self.bwd_bytes = 4 * ((F + M) + (P + M) + (M + M + F + P + F)) * B * T
+        self.bwd_launch_bytes = 4 * (F + M) * B * T  # the states pass
 
     def step_fwd(self):
         from philtorch_amd import lti
@@ -987,10 +988,10 @@ class LpvMimoGrad(LpvMimoApi):
 
 class LpvMimoCoefGrad(LpvMimoGrad):
     """c3_lpv_mimo_coef: c3_lpv_mimo_grad with the gradients of A[t], B, C and
-    D too: the adjoint pass, the forward again writing its states, the
-    adjoint again writing its states, and one philtorch::mimo_ss_grad_sums
-    pass writing dL/dA[t] = lambda[t+1] h[t]^T per step and summing over
-    time for B, C, D."""
+    D too: the forward again writing its states, the adjoint writing its
+    states (which also gives grad_zi), and one philtorch::mimo_ss_grad_sums
+    pass writing dL/dA[t] = lambda[t+1] h[t]^T and grad_x = B^T lambda + D^T
+    g per step and summing over time for B, C, D."""
 
     def __init__(self):
         super().__init__()
@@ -998,10 +999,10 @@ class LpvMimoCoefGrad(LpvMimoGrad):
         self.name = "c3_lpv_mimo_coef"
         self.metric = (f"GSamples/s fwd+bwd(x, zi, A, B, C, D), LPV lpv.state_space order 2, 2 inputs, 2 outputs "
                        f"per step B={B} T={T} fp32 (API)")
-        # adjoint, states and adjoint-states passes (32 each: A, one signal in, one out), the sums pass
-        # (read lambda, h, x, g: 32; write dL/dA[t]: 16)
-        self.bwd_bytes = (32 + 32 + 32 + 48) * B * T
-        self.bwd_launch_bytes = 32 * B * T  # the adjoint pass
+        # states and adjoint-states passes (32 each: A, one signal in, one out), the sums pass (read
+        # lambda, h, x, g: 32; write dL/dA[t]: 16, grad_x: 8)
+        self.bwd_bytes = (32 + 32 + 56) * B * T
+        self.bwd_launch_bytes = 32 * B * T  # the states pass
 
     def step_fwd(self):
         from philtorch_amd import lpv
