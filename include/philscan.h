@@ -538,6 +538,27 @@ int phs_lpv_ss_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
                    void *gd, int reverse, void *scratch, size_t scratch_bytes, void *workspace,
                    size_t workspace_bytes, void *stream);
 
+/* ---- The same pair split for a caller that keeps the forward's states (no
+ * counterpart in the reference, whose autograd saves the composed route's
+ * tensors; philtorch/lpv/ssm.py:337-581).  phs_lpv_ss_fwd_hs: phs_lpv_ss_fwd
+ * (reverse = 0) or phs_lpv_ss_rev (reverse = 1) that also writes hs [B,T,M],
+ * the state before every step, in the same pass.  phs_lpv_ss_bwd_hs:
+ * phs_lpv_ss_bwd given those states (the same model's, same reverse), so it
+ * runs the adjoint pass only; hs NULL: it recomputes them, as
+ * phs_lpv_ss_bwd.  Results equal phs_lpv_ss_bwd's bit for bit. */
+int phs_lpv_ss_fwd_hs(int dtype, int M, int64_t B, int64_t T, const void *A, int A_flags, const void *b,
+                      int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride,
+                      int64_t c_t_stride, int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride,
+                      const void *zi, const void *x, void *y, void *zf, void *hs, int reverse, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
+int phs_lpv_ss_bwd_hs(int dtype, int M, int64_t B, int64_t T, const void *A, int A_flags, const void *b,
+                      int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride,
+                      int64_t c_t_stride, int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride,
+                      const void *zi, const void *x, const void *hs, const void *gy, const void *gzf, void *gx,
+                      void *gzi, void *gA, void *gb, void *gc, void *gd, int reverse, void *scratch,
+                      size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Bits of the `shared` argument of phs_mimo_ss_fwd / phs_mimo_ss_rev: an
  * operand with its bit set is one matrix for every row (else one per row). */
 #define PHS_MIMO_A_SHARED 1

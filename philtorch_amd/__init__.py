@@ -734,7 +734,7 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
     if _has_op("lpv_ss_backward"):
 
         @torch.library.register_fake("philtorch::lpv_ss_backward")
-        def _(A, B, C, D, zi, x, grad_y, grad_zf, out_idx, reverse=False, transpose_A=False):
+        def _(A, B, C, D, zi, x, grad_y, grad_zf, out_idx, reverse=False, transpose_A=False, hs=None):
             e = lambda t: x.new_empty(t.shape) if t is not None else x.new_empty((0,))  # noqa: E731
             return [e(A), e(B), e(C), e(D), x.new_empty((x.shape[0], A.shape[-1])), _fake_like(x)]
 
@@ -743,7 +743,11 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         ctx.out_idx = out_idx
         ctx.reverse = bool(inputs[7]) if len(inputs) > 7 else False
         ctx.transpose_A = bool(inputs[8]) if len(inputs) > 8 else False
-        ctx.save_for_backward(A, B, C, D, zi, x)
+        # lpv_ss_states: the forward's states too, for the coefficient backward
+        hs = output[2] if len(output) > 2 else None
+        if hs is not None:
+            ctx.mark_non_differentiable(hs)
+        ctx.save_for_backward(A, B, C, D, zi, x, hs)
         ctx.set_materialize_grads(False)
 
     def _lpv_ss_backward(ctx, gy, gzf):
@@ -763,7 +767,8 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         from .lpv import ssm as _lpv_ssm
 
         _lpv_state_space_composite = _lpv_ssm._lpv_state_space_composite
-        inputs = ctx.saved_tensors
+        saved = ctx.saved_tensors
+        inputs, hs = saved[:6], saved[6]
         needs = ctx.needs_input_grad
         A, B, C, D, zi, x = inputs
         out = [None] * 9
@@ -774,7 +779,7 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
             g = gy if gy is not None else torch.zeros_like(x)
             with _op_ctx(A, B, C, D, zi, x, g):
                 res = torch.ops.philtorch.lpv_ss_backward(A, B, C, D, zi, x, g, gzf, ctx.out_idx, ctx.reverse,
-                                                          ctx.transpose_A)
+                                                          ctx.transpose_A, hs)
             for i, t in enumerate(inputs):
                 if t is not None and needs[i]:
                     out[i] = res[i]
@@ -819,6 +824,23 @@ if EXTENSION_LOADED and _has_op("lpv_ss"):
         return tuple(out)
 
     torch.library.register_autograd("philtorch::lpv_ss", _lpv_ss_backward, setup_context=_lpv_ss_setup)
+
+    if _has_op("lpv_ss_states"):
+
+        @torch.library.register_fake("philtorch::lpv_ss_states")
+        def _(A, B, C, D, zi, x, out_idx, reverse=False, transpose_A=False):
+            torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
+            M = A.shape[-1]
+            return _fake_like(x), x.new_empty((x.shape[0], M)), x.new_empty((x.shape[0], x.shape[1], M))
+
+        def _lpv_ss_states_backward(ctx, gy, gzf, ghs):
+            """lpv_ss's backward with the states the forward kept (hs is not
+            differentiable): the coefficient backward runs its adjoint pass
+            only, instead of the forward again first."""
+            return _lpv_ss_backward(ctx, gy, gzf)
+
+        torch.library.register_autograd("philtorch::lpv_ss_states", _lpv_ss_states_backward,
+                                        setup_context=_lpv_ss_setup)
 
 if EXTENSION_LOADED and _has_op("mimo_ss"):
     # LTI state space with F inputs and P outputs per step (F, P <= 4): (y, zf)

@@ -63,10 +63,14 @@ int lpv_launch(const LpvSsArgs<Alg> &a, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
+// hs (nullable): the state before every step [B, T, M] as well (the states
+// the coefficient backward reads), written in the same pass as y.
 template <class Alg>
 int lpv_ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, bool A_tr, LpvOperand<typename Alg::elem> bv,
                LpvOperand<typename Alg::elem> cv, int out_idx, LpvOperand<typename Alg::elem> d, const void *zi,
-               const void *x, void *y, void *zf, void *workspace, size_t ws_bytes, bool rev, hipStream_t stream) {
+               const void *x, void *y, void *zf, void *workspace, size_t ws_bytes, bool rev, hipStream_t stream,
+               void *hs = nullptr) {
+  using E = typename Alg::elem;
   using Sh = LpvSsShape<Alg>;
   constexpr int M = SsView<Alg>::M;
   if (B < 0 || T < 0) return PHS_ERR_INVALID;
@@ -78,7 +82,13 @@ int lpv_ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, bool A_tr, LpvOpe
   const int64_t tiles_per_row = (T + Sh::kTile - 1) / Sh::kTile;
   if (double(B) * double(tiles_per_row) >= 2147483648.0) return PHS_ERR_INVALID;
   if (!workspace || ws_bytes < lpv_ss_ws_bytes<Alg>(B, T)) return PHS_ERR_WORKSPACE;
-  const LpvSsArgs<Alg> a = lpv_args<Alg>(B, T, A, A_sh, A_tr, bv, cv, out_idx, 0, d, zi, x, y, zf, workspace);
+  LpvSsArgs<Alg> a = lpv_args<Alg>(B, T, A, A_sh, A_tr, bv, cv, out_idx, 0, d, zi, x, y, zf, workspace);
+  if (hs) {
+    a.hs = static_cast<E *>(hs);
+    a.vec_hs = aligned16(hs) && (size_t(T) * sizeof(typename Alg::s_state)) % 16 == 0 && aligned16(x) &&
+               (size_t(T) * sizeof(E)) % 16 == 0;
+    return rev ? lpv_launch<Alg, true, kSsStatesY>(a, stream) : lpv_launch<Alg, false, kSsStatesY>(a, stream);
+  }
   return rev ? lpv_launch<Alg, true>(a, stream) : lpv_launch<Alg, false>(a, stream);
 }
 
@@ -123,7 +133,7 @@ LpvBwdLayout<Alg> lpv_bwd_layout(int64_t B, int64_t T, int step_shared) {
 }
 
 // Gradients of the model w.r.t. x, zi and A, b, c, d: the forward again
-// writing its states, the adjoint model (A[t]^T, input vector c[t], output
+// writing its states (unless the forward gave them, hs_in), the adjoint model (A[t]^T, input vector c[t], output
 // vector b[t], d[t]) in the opposite time direction from grad_zf with the
 // coefficient gradients, the row sums of those constant in time and the
 // batch sums of those the rows share.  The outputs are contiguous, shaped
@@ -133,7 +143,7 @@ int lpv_ss_bwd(int64_t B, int64_t T, const void *A, bool A_sh, bool A_tr, LpvOpe
                LpvOperand<typename Alg::elem> cv, int out_idx, LpvOperand<typename Alg::elem> d, const void *zi,
                const void *x, const void *gy, const void *gzf, void *gx, void *gzi, void *gA, void *gb, void *gc,
                void *gd, void *scratch, size_t scratch_bytes, void *workspace, size_t ws_bytes, bool rev,
-               hipStream_t stream) {
+               hipStream_t stream, const void *hs_in = nullptr) {
   using E = typename Alg::elem;
   using C = typename Wide<E>::type;
   using SS = typename Alg::s_state;
@@ -153,7 +163,7 @@ int lpv_ss_bwd(int64_t B, int64_t T, const void *A, bool A_sh, bool A_tr, LpvOpe
   if (!scratch || scratch_bytes < L.total) return PHS_ERR_WORKSPACE;
   if (T > 0 && (!workspace || ws_bytes < lpv_ss_ws_bytes<Alg>(B, T))) return PHS_ERR_WORKSPACE;
   char *sc = static_cast<char *>(scratch);
-  E *states = reinterpret_cast<E *>(sc + L.states);
+  E *states = hs_in ? const_cast<E *>(static_cast<const E *>(hs_in)) : reinterpret_cast<E *>(sc + L.states);
   C *gpart = reinterpret_cast<C *>(sc + L.partials);
   C *rowsum = reinterpret_cast<C *>(sc + L.rowsum);
   // where each per-step gradient goes: the output, or the per-row scratch
@@ -169,8 +179,11 @@ int lpv_ss_bwd(int64_t B, int64_t T, const void *A, bool A_sh, bool A_tr, LpvOpe
     p.hs = states;
     p.vec_hs = aligned16(states) && (size_t(T) * sizeof(SS)) % 16 == 0 && aligned16(x) &&
                (size_t(T) * sizeof(E)) % 16 == 0;
-    int rc = rev ? lpv_launch<Alg, true, kSsStates>(p, stream) : lpv_launch<Alg, false, kSsStates>(p, stream);
-    if (rc != PHS_OK) return rc;
+    int rc = PHS_OK;
+    if (!hs_in) {
+      rc = rev ? lpv_launch<Alg, true, kSsStates>(p, stream) : lpv_launch<Alg, false, kSsStates>(p, stream);
+      if (rc != PHS_OK) return rc;
+    }
     // the adjoint: A^T, input vector c (e_out_idx), output vector b (e_0)
     LpvSsArgs<Alg> q = lpv_args<Alg>(B, T, A, A_sh, !A_tr, cv, bv, 0, out_idx, d, gzf, gy, gx, gzi, workspace);
     q.hs_fwd = states;
@@ -247,6 +260,17 @@ int phs_lpv_ss_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
                    const void *x, const void *gy, const void *gzf, void *gx, void *gzi, void *gA, void *gb, void *gc,
                    void *gd, int reverse, void *scratch, size_t scratch_bytes, void *workspace,
                    size_t workspace_bytes, void *stream) {
+  return phs_lpv_ss_bwd_hs(dtype, M, B, T, A, A_flags, b, b_row_stride, b_t_stride, c, c_row_stride, c_t_stride,
+                           out_idx, d, d_row_stride, d_t_stride, zi, x, nullptr, gy, gzf, gx, gzi, gA, gb, gc, gd,
+                           reverse, scratch, scratch_bytes, workspace, workspace_bytes, stream);
+}
+
+int phs_lpv_ss_bwd_hs(int dtype, int M, int64_t B, int64_t T, const void *A, int A_flags, const void *b,
+                      int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride,
+                      int64_t c_t_stride, int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride,
+                      const void *zi, const void *x, const void *hs, const void *gy, const void *gzf, void *gx,
+                      void *gzi, void *gA, void *gb, void *gc, void *gd, int reverse, void *scratch,
+                      size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream) {
   if (A_flags & ~(PHS_LPV_A_SHARED | PHS_LPV_A_TRANSPOSED)) return PHS_ERR_INVALID;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return phs::lpv_dispatch(dtype, M, [&](auto alg) {
@@ -257,7 +281,7 @@ int phs_lpv_ss_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
     return phs::lpv_ss_bwd<decltype(alg)>(B, T, A, (A_flags & PHS_LPV_A_SHARED) != 0,
                                           (A_flags & PHS_LPV_A_TRANSPOSED) != 0, bo, co, out_idx, dd, zi, x, gy, gzf,
                                           gx, gzi, gA, gb, gc, gd, scratch, scratch_bytes, workspace, workspace_bytes,
-                                          reverse != 0, st);
+                                          reverse != 0, st, hs);
   });
 }
 
@@ -276,7 +300,8 @@ namespace {
 int lpv_ss_call(int dtype, int M, int64_t B, int64_t T, const void *A, int A_flags, const void *b,
                 int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride, int64_t c_t_stride,
                 int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride, const void *zi, const void *x,
-                void *y, void *zf, void *workspace, size_t workspace_bytes, bool rev, void *stream) {
+                void *y, void *zf, void *workspace, size_t workspace_bytes, bool rev, void *stream,
+                void *hs = nullptr) {
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (A_flags & ~(PHS_LPV_A_SHARED | PHS_LPV_A_TRANSPOSED)) return PHS_ERR_INVALID;
   return phs::lpv_dispatch(dtype, M, [&](auto alg) {
@@ -286,7 +311,7 @@ int lpv_ss_call(int dtype, int M, int64_t B, int64_t T, const void *A, int A_fla
     const phs::LpvOperand<E> dd{static_cast<const E *>(d), d_row_stride, d_t_stride};
     return phs::lpv_ss_fwd<decltype(alg)>(B, T, A, (A_flags & PHS_LPV_A_SHARED) != 0,
                                           (A_flags & PHS_LPV_A_TRANSPOSED) != 0, bo, co, out_idx, dd, zi, x, y, zf,
-                                          workspace, workspace_bytes, rev, st);
+                                          workspace, workspace_bytes, rev, st, hs);
   });
 }
 
@@ -306,6 +331,16 @@ int phs_lpv_ss_rev(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
                    const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes, void *stream) {
   return lpv_ss_call(dtype, M, B, T, A, A_flags, b, b_row_stride, b_t_stride, c, c_row_stride, c_t_stride, out_idx,
                      d, d_row_stride, d_t_stride, zi, x, y, zf, workspace, workspace_bytes, true, stream);
+}
+
+int phs_lpv_ss_fwd_hs(int dtype, int M, int64_t B, int64_t T, const void *A, int A_flags, const void *b,
+                      int64_t b_row_stride, int64_t b_t_stride, const void *c, int64_t c_row_stride,
+                      int64_t c_t_stride, int out_idx, const void *d, int64_t d_row_stride, int64_t d_t_stride,
+                      const void *zi, const void *x, void *y, void *zf, void *hs, int reverse, void *workspace,
+                      size_t workspace_bytes, void *stream) {
+  if (!hs && B > 0 && T > 0) return PHS_ERR_INVALID;
+  return lpv_ss_call(dtype, M, B, T, A, A_flags, b, b_row_stride, b_t_stride, c, c_row_stride, c_t_stride, out_idx,
+                     d, d_row_stride, d_t_stride, zi, x, y, zf, workspace, workspace_bytes, reverse != 0, stream, hs);
 }
 
 }  // extern "C"

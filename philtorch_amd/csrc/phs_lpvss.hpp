@@ -398,9 +398,8 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int64_t t = lpv_time<REV>(t0 + k, T);
-      if constexpr (MODE == kSsStates) {
-        Hf[k] = h;
-      } else {
+      if constexpr (MODE == kSsStates || MODE == kSsStatesY) Hf[k] = h;
+      if constexpr (MODE != kSsStates) {
         const SS c = cp ? V::load_vec(cp + t * a.cv.t_stride) : c_fixed;
         const E dv = dp ? dp[t * a.d.t_stride] : E(0);
         O[k] = fma(dv, U[r][k], V::dot(c, h));
@@ -417,9 +416,11 @@ __global__ __launch_bounds__(LpvSsShape<Alg>::kThreads, 2) void lpv_ss_kernel(Lp
         for (int i = 0; i < V::M; ++i) a.zf[b * V::M + i] = zu.e[i];
       }
     }
-    if constexpr (MODE == kSsStates)
+    if constexpr (MODE == kSsStates || MODE == kSsStatesY)
       lpv_store<REV, SS, K>(reinterpret_cast<SS *>(a.hs) + b * T, t0, T, vh, Hf);
-    else if (MODE == kSsPlain || a.y)
+    if constexpr (MODE == kSsPlain || MODE == kSsStatesY)
+      lpv_store<REV, E, K>(a.y + b * T, t0, T, vec, O);
+    else if (MODE == kSsGrad && a.y)
       lpv_store<REV, E, K>(a.y + b * T, t0, T, vec, O);
   }
   if constexpr (MODE == kSsGrad) {

@@ -964,10 +964,12 @@ int64_t lpv_ss_meta_check(const Tensor &A, const std::optional<Tensor> &Bm, cons
 int64_t lpv_row_stride(const Tensor &t, int64_t width) { return t.size(0) == 1 ? int64_t(0) : t.size(1) * width; }
 int64_t lpv_t_stride(const Tensor &t, int64_t width) { return t.size(1) == 1 ? int64_t(0) : width; }
 
-std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
-                                      const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
-                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
-                                      bool reverse, bool transpose_A) {
+// keep_states: also the state before every step, hs (batch, T, M), written
+// by the same pass (phs_lpv_ss_fwd_hs) for the coefficient backward.
+std::tuple<Tensor, Tensor, Tensor> lpv_ss_impl(const Tensor &A, const std::optional<Tensor> &Bm,
+                                               const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
+                                               const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
+                                               bool reverse, bool transpose_A, bool keep_states) {
   const int64_t M = lpv_ss_meta_check(A, Bm, Cm, Dm, zi, x, out_idx);
   const int64_t B = x.size(0), T = x.size(1);
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
@@ -977,23 +979,51 @@ std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tenso
   Tensor dc = Dm ? Dm->contiguous() : Tensor(), zc = zi ? zi->contiguous() : Tensor();
   Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
   Tensor zf = at::empty({B, M}, x.options());
-  if (B == 0) return {y, zf};
+  Tensor hs = at::empty({keep_states ? B : 0, keep_states ? T : 0, M}, x.options());
+  if (B == 0) return {y, zf, hs};
   if (T == 0) {
     if (zi) zf.copy_(zc); else zf.zero_();
-    return {y, zf};
+    return {y, zf, hs};
   }
   const auto rs = lpv_row_stride, ts = lpv_t_stride;
   void *stream = stream_of(x);
   const Workspace ws = workspace_for(x, phs_lpv_ss_workspace_size(dt, int(M), B, T), stream);
   const int A_flags = (A.dim() == 3 ? PHS_LPV_A_SHARED : 0) | (transpose_A ? PHS_LPV_A_TRANSPOSED : 0);
-  check_status((reverse ? phs_lpv_ss_rev : phs_lpv_ss_fwd)(dt, int(M), B, T, Ac.const_data_ptr(), A_flags,
-                              Bm ? bc.const_data_ptr() : nullptr, Bm ? rs(bc, M) : 0, Bm ? ts(bc, M) : 0,
-                              Cm ? cc.const_data_ptr() : nullptr, Cm ? rs(cc, M) : 0, Cm ? ts(cc, M) : 0,
-                              int(out_idx), Dm ? dc.const_data_ptr() : nullptr, Dm ? rs(dc, 1) : 0,
-                              Dm ? ts(dc, 1) : 0, zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(),
-                              y.mutable_data_ptr(), zf.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
-               "lpv_ss");
+  const void *bp = Bm ? bc.const_data_ptr() : nullptr, *cp = Cm ? cc.const_data_ptr() : nullptr;
+  const void *dp = Dm ? dc.const_data_ptr() : nullptr, *zp = zi ? zc.const_data_ptr() : nullptr;
+  const int64_t brs = Bm ? rs(bc, M) : 0, bts = Bm ? ts(bc, M) : 0, crs = Cm ? rs(cc, M) : 0,
+                cts = Cm ? ts(cc, M) : 0, drs = Dm ? rs(dc, 1) : 0, dts = Dm ? ts(dc, 1) : 0;
+  if (keep_states)
+    check_status(phs_lpv_ss_fwd_hs(dt, int(M), B, T, Ac.const_data_ptr(), A_flags, bp, brs, bts, cp, crs, cts,
+                                   int(out_idx), dp, drs, dts, zp, xc.const_data_ptr(), y.mutable_data_ptr(),
+                                   zf.mutable_data_ptr(), hs.mutable_data_ptr(), reverse ? 1 : 0, ws.ptr, ws.bytes,
+                                   stream),
+                 "lpv_ss_states");
+  else
+    check_status((reverse ? phs_lpv_ss_rev : phs_lpv_ss_fwd)(dt, int(M), B, T, Ac.const_data_ptr(), A_flags, bp, brs,
+                                                             bts, cp, crs, cts, int(out_idx), dp, drs, dts, zp,
+                                                             xc.const_data_ptr(), y.mutable_data_ptr(),
+                                                             zf.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+                 "lpv_ss");
+  return {y, zf, hs};
+}
+
+std::tuple<Tensor, Tensor> lpv_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
+                                      const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
+                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
+                                      bool reverse, bool transpose_A) {
+  auto [y, zf, hs] = lpv_ss_impl(A, Bm, Cm, Dm, zi, x, out_idx, reverse, transpose_A, false);
   return {y, zf};
+}
+
+// lpv_ss that also returns hs (batch, T, M), the state before every step:
+// what lpv_ss_backward would recompute for the coefficient gradients.
+std::tuple<Tensor, Tensor, Tensor> lpv_ss_states_hip(const Tensor &A, const std::optional<Tensor> &Bm,
+                                                     const std::optional<Tensor> &Cm,
+                                                     const std::optional<Tensor> &Dm,
+                                                     const std::optional<Tensor> &zi, const Tensor &x,
+                                                     int64_t out_idx, bool reverse, bool transpose_A) {
+  return lpv_ss_impl(A, Bm, Cm, Dm, zi, x, out_idx, reverse, transpose_A, true);
 }
 
 // Gradients of lpv_ss w.r.t. every input (phs_lpv_ss_bwd): returns (grad_A,
@@ -1006,11 +1036,16 @@ std::vector<Tensor> lpv_ss_backward_hip(const Tensor &A, const std::optional<Ten
                                         const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
                                         const std::optional<Tensor> &zi, const Tensor &x, const Tensor &gy,
                                         const std::optional<Tensor> &gzf, int64_t out_idx, bool reverse,
-                                        bool transpose_A) {
+                                        bool transpose_A, const std::optional<Tensor> &hs) {
   const int64_t M = lpv_ss_meta_check(A, Bm, Cm, Dm, zi, x, out_idx);
   const int64_t B = x.size(0), T = x.size(1);
   TORCH_CHECK(gy.sizes() == x.sizes() && gy.device() == x.device(),
               "philtorch::lpv_ss_backward: grad_y must have x's shape and device");
+  if (hs)
+    TORCH_CHECK(hs->dim() == 3 && hs->size(0) == B && hs->size(1) == T && hs->size(2) == M &&
+                    hs->scalar_type() == x.scalar_type() && hs->device() == x.device(),
+                "philtorch::lpv_ss_backward: hs must be the forward's states (batch, T, M)");
+  Tensor hc = hs ? hs->contiguous() : Tensor();
   if (gzf)
     TORCH_CHECK(gzf->dim() == 2 && gzf->size(0) == B && gzf->size(1) == M && gzf->device() == x.device(),
                 "philtorch::lpv_ss_backward: grad_zf must be (batch, M)");
@@ -1041,11 +1076,12 @@ std::vector<Tensor> lpv_ss_backward_hip(const Tensor &A, const std::optional<Ten
       at::empty({int64_t(phs_lpv_ss_bwd_scratch_size(dt, int(M), B, T, step_shared))}, x.options().dtype(at::kByte));
   const Workspace ws = workspace_for(x, phs_lpv_ss_workspace_size(dt, int(M), B, T), stream);
   const int A_flags = (A.dim() == 3 ? PHS_LPV_A_SHARED : 0) | (transpose_A ? PHS_LPV_A_TRANSPOSED : 0);
-  check_status(phs_lpv_ss_bwd(dt, int(M), B, T, Ac.const_data_ptr(), A_flags, Bm ? bc.const_data_ptr() : nullptr,
+  check_status(phs_lpv_ss_bwd_hs(dt, int(M), B, T, Ac.const_data_ptr(), A_flags, Bm ? bc.const_data_ptr() : nullptr,
                               Bm ? rs(bc, M) : 0, Bm ? ts(bc, M) : 0, Cm ? cc.const_data_ptr() : nullptr,
                               Cm ? rs(cc, M) : 0, Cm ? ts(cc, M) : 0, int(out_idx),
                               Dm ? dc.const_data_ptr() : nullptr, Dm ? rs(dc, 1) : 0, Dm ? ts(dc, 1) : 0,
-                              zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(), gc.const_data_ptr(),
+                              zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(),
+                              hs ? hc.const_data_ptr() : nullptr, gc.const_data_ptr(),
                               gzf ? gzc.const_data_ptr() : nullptr, gx.mutable_data_ptr(), gzi.mutable_data_ptr(),
                               gA.mutable_data_ptr(), Bm ? gB.mutable_data_ptr() : nullptr,
                               Cm ? gC.mutable_data_ptr() : nullptr, Dm ? gD.mutable_data_ptr() : nullptr,
@@ -1452,7 +1488,10 @@ TORCH_LIBRARY(philtorch, m) {
         "bool transpose_A=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
   m.def("lpv_ss_backward(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, Tensor grad_y, "
-        "Tensor? grad_zf, int out_idx, bool reverse=False, bool transpose_A=False) -> Tensor[]",
+        "Tensor? grad_zf, int out_idx, bool reverse=False, bool transpose_A=False, Tensor? hs=None) -> Tensor[]",
+        {at::Tag::pt2_compliant_tag});
+  m.def("lpv_ss_states(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx, "
+        "bool reverse=False, bool transpose_A=False) -> (Tensor, Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
   m.def("mimo_ss(Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? zi, Tensor x, bool reverse=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
@@ -1489,6 +1528,7 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("lfilter_ss_backward", &lfilter_ss_backward_hip);
   m.impl("lpv_ss", &lpv_ss_hip);
   m.impl("lpv_ss_backward", &lpv_ss_backward_hip);
+  m.impl("lpv_ss_states", &lpv_ss_states_hip);
   m.impl("mimo_ss", &mimo_ss_hip);
   m.impl("mimo_ss_grad_sums", &mimo_ss_grad_sums_hip);
   m.impl("lpv_mimo_ss", &lpv_mimo_ss_hip);

@@ -611,11 +611,18 @@ def state_space(
     native = extension_backend_indicator(x, M) and unroll_factor in (None, 1)
     ops = _lpv_siso_operands(x, B, C, D, out_idx, batch, N, M)
     if _fused_lpv_ss_applies(A, x, zi if return_zf else None, ops, native):
-        from .. import _op_ctx
+        from .. import _has_op, _op_ctx
 
+        # a coefficient with a gradient to come: the forward keeps its states
+        # (lpv_ss_states), which the coefficient backward would compute again
+        keep = torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (A, *ops))
         with _op_ctx(A, *ops, zi, x):
-            y, zf = torch.ops.philtorch.lpv_ss(A, ops[0], ops[1], ops[2], zi.contiguous() if return_zf else None, x,
-                                               0 if out_idx is None else out_idx)
+            args = (A, ops[0], ops[1], ops[2], zi.contiguous() if return_zf else None, x,
+                    0 if out_idx is None else out_idx)
+            if keep and _has_op("lpv_ss_states"):
+                y, zf, _ = torch.ops.philtorch.lpv_ss_states(*args)
+            else:
+                y, zf = torch.ops.philtorch.lpv_ss(*args)
         return (y, zf) if return_zf else y
     mops = _lpv_mimo_operands(x, B, C, D, out_idx, batch, N, M) if native else None
     if _lpv_mimo_applies(A, x, zi if return_zf else None, mops, native):

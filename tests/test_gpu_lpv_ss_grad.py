@@ -16,7 +16,9 @@ Pins:
   and per-row A, A read transposed, forward and reversed calls, rows of one
   step, on and around a tile and of many tiles;
 * the API: lpv.state_space keeps the fused route when coefficients need
-  gradients; gradcheck (the fused op) and gradgradcheck (the composite).
+  gradients (its forward then keeps its states, philtorch::lpv_ss_states,
+  whose outputs and backward are checked bit-exact against lpv_ss's);
+  gradcheck (the fused ops) and gradgradcheck (the composite).
 """
 import numpy as np
 import pytest
@@ -135,6 +137,15 @@ def test_lpv_ss_backward_vs_composed_route(hip, dtype, M, Bn, T):
                   f"transpose_A={tr}", flush=True)
             res = torch.ops.philtorch.lpv_ss_backward(*[_t(v) for v in ops], _t(gy), _t(gzf), out_idx, rev, tr)
             got = [r.cpu().numpy() for r in res]
+            # the forward keeping its states (phs_lpv_ss_fwd_hs) gives lpv_ss's outputs, and the
+            # backward given them (phs_lpv_ss_bwd_hs) the same gradients, bit for bit
+            y1, zf1 = torch.ops.philtorch.lpv_ss(*[_t(v) for v in ops], out_idx, rev, tr)
+            y2, zf2, hs = torch.ops.philtorch.lpv_ss_states(*[_t(v) for v in ops], out_idx, rev, tr)
+            assert hs.shape == (Bn, T, M) and torch.equal(y1, y2) and torch.equal(zf1, zf2)
+            res_hs = torch.ops.philtorch.lpv_ss_backward(*[_t(v) for v in ops], _t(gy), _t(gzf), out_idx, rev, tr,
+                                                         hs)
+            for r0, r1 in zip(res, res_hs):
+                assert torch.equal(r0, r1)
             ref = _composite_grads([None if v is None else v.astype(np.float64) for v in ops],
                                    gy.astype(np.float64), gzf.astype(np.float64), out_idx, rev, tr)
             for i, nm in enumerate(("grad_A", "grad_B", "grad_C", "grad_D", "grad_zi", "grad_x")):
@@ -182,6 +193,12 @@ def test_lpv_api_takes_fused_route_with_coefficient_gradients(hip, monkeypatch):
             assert torch.autograd.gradcheck(f, (As, bs, cs, ds, zs, xs))
     f = lambda *a: torch.ops.philtorch.lpv_ss(*a, 0)  # noqa: E731
     assert torch.autograd.gradgradcheck(f, (As, bs, cs, ds, zs, xs))
+    # the states-keeping forward the API takes here: gradcheck of its (y, zf), and opcheck
+    for rev in (False, True):
+        f = lambda *a: torch.ops.philtorch.lpv_ss_states(*a, 0, rev)[:2]  # noqa: E731
+        assert torch.autograd.gradcheck(f, (As, bs, cs, ds, zs, xs))
+    det = [t.detach() for t in (As, bs, cs, ds, zs, xs)]
+    torch.library.opcheck(torch.ops.philtorch.lpv_ss_states.default, (*det, 0, True, False))
 
 
 def test_lpv_shared_step_gradients_above_scratch_limit_take_composite(hip, monkeypatch):
