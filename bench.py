@@ -15,7 +15,8 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c3      philtorch::recur2 + recurN_backward               (LPV 2x2)
   c3_lpv_ss  lpv.state_space of a time-varying biquad (tdf2, one output), forward only (philtorch::lpv_ss)
   c3_lpv_ss_grad  the same plus gradients w.r.t. x and zi (a reversed lpv_ss pass over the adjoint model)
-  c3_lpv_ss_coef  the same plus gradients w.r.t. A[t], b[t], d[t] too (philtorch::lpv_ss_backward)
+  c3_lpv_ss_coef  the same plus gradients w.r.t. A[t], b[t], d[t] too (philtorch::lpv_ss_states forward,
+                  philtorch::lpv_ss_backward given its states)
   c4      8 x (philtorch::lti_recur2 + lti_recurN_backward) (LTI biquad cascade)
   c4_fused  philtorch::sosfilt + sosfilt_backward              (the same cascade, fused)
   c4_api  8 x lti.lfilter(tdf2, unroll_factor=1) + autograd   (the caller pattern, API level)
@@ -732,9 +733,9 @@ class Lfilter4Grad(Lfilter4Api):
 
 class LpvSsCoefGrad(LpvSsGrad):
     """c3_lpv_ss_coef: c3_lpv_ss_grad with the gradients of the time-varying
-    A[t], b[t] and d[t] too (philtorch::lpv_ss_backward: the forward again
-    keeping its states, then the adjoint pass writing the per-step
-    coefficient gradients)."""
+    A[t], b[t] and d[t] too: the forward keeps its states
+    (philtorch::lpv_ss_states), and philtorch::lpv_ss_backward runs the
+    adjoint pass writing the per-step coefficient gradients from them."""
 
     def __init__(self):
         super().__init__()
@@ -742,10 +743,10 @@ class LpvSsCoefGrad(LpvSsGrad):
         self.name = "c3_lpv_ss_coef"
         self.metric = (f"GSamples/s fwd+bwd(x, zi, A, b, d), LPV biquad lpv.state_space (tdf2, one output) B={B} "
                        f"T={T} fp32 (API)")
-        # states pass: read A (16), x, b (8), write 2 states (8); adjoint: read A, b, d, g, x, states (8),
-        # write grad_x, grad_A (16), grad_b (8), grad_d
-        self.bwd_bytes = (16 + 4 + 8 + 8) * B * T + (16 + 8 + 4 + 4 + 4 + 8 + 4 + 16 + 8 + 4) * B * T
-        self.bwd_launch_bytes = (16 + 4 + 8 + 8) * B * T  # the states pass
+        # the forward also writes its 2 states (8); adjoint: read A, b, d, g, x, states (8), write grad_x,
+        # grad_A (16), grad_b (8), grad_d
+        self.fwd_bytes += 8 * B * T
+        self.bwd_bytes = (16 + 8 + 4 + 4 + 4 + 8 + 4 + 16 + 8 + 4) * B * T
 
     def step_fwd(self):
         from philtorch_amd import lpv
