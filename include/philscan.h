@@ -470,6 +470,35 @@ int phs_lfilter_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, cons
                     void *gb, void *ga, int reverse, void *scratch, size_t scratch_bytes, void *workspace,
                     size_t workspace_bytes, void *stream);
 
+/* ---- The LTI pairs split for a caller that keeps the forward's states (no
+ * counterpart in the reference, whose autograd saves the composed route's
+ * tensors; philtorch/lti/ssm.py:386-589, philtorch/lti/filtering.py:273-333):
+ * the forward (reverse = 0) or reversed pass that also writes hs [B,T,M],
+ * the state before every step, in the same pass (its y may differ from the
+ * plain pass's in the last bits: the states-and-output mode scans other tile
+ * lengths), and the backward given those states, which runs the adjoint pass
+ * only (hs NULL: recomputed, as phs_lti_ss_bwd / phs_lfilter_bwd; the
+ * gradients equal theirs bit for bit). */
+int phs_lti_ss_fwd_hs(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+                      int b_shared, const void *c, int c_shared, int out_idx, const void *d, int d_shared,
+                      const void *zi, const void *x, void *y, void *zf, void *hs, int reverse, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
+int phs_lti_ss_bwd_hs(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+                      int b_shared, const void *c, int c_shared, int out_idx, const void *d, int d_shared,
+                      const void *zi, const void *x, const void *hs, const void *gy, const void *gzf, void *gx,
+                      void *gzi, void *gA, void *gb, void *gc, void *gd, int reverse, void *scratch,
+                      size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream);
+
+int phs_lfilter_fwd_hs(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
+                       int coef_shared, int form, const void *zi, const void *x, void *y, void *zf, void *hs,
+                       int reverse, void *workspace, size_t workspace_bytes, void *stream);
+
+int phs_lfilter_bwd_hs(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
+                       int coef_shared, int form, const void *zi, const void *x, const void *hs, const void *gy,
+                       const void *gzf, void *gx, void *gzi, void *gb, void *ga, int reverse, void *scratch,
+                       size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Flags of the A argument of phs_lpv_ss_fwd / phs_lpv_ss_rev (A_flags):
  * PHS_LPV_A_SHARED, A is [T,M,M] and shared by the rows; PHS_LPV_A_TRANSPOSED,
  * every step's matrix is read transposed, so the adjoint model's A[t]^T

@@ -586,7 +586,7 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
     if _has_op("lti_ss_backward"):
 
         @torch.library.register_fake("philtorch::lti_ss_backward")
-        def _(A, B, C, D, zi, x, grad_y, grad_zf, out_idx, reverse=False):
+        def _(A, B, C, D, zi, x, grad_y, grad_zf, out_idx, reverse=False, hs=None):
             e = lambda t: x.new_empty(t.shape) if t is not None else x.new_empty((0,))  # noqa: E731
             return [e(A), e(B), e(C), e(D), x.new_empty((x.shape[0], A.shape[-1])), _fake_like(x)]
 
@@ -594,7 +594,11 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
         A, B, C, D, zi, x, out_idx = inputs[:7]
         ctx.out_idx = out_idx
         ctx.reverse = bool(inputs[7]) if len(inputs) > 7 else False
-        ctx.save_for_backward(A, B, C, D, zi, x)
+        # lti_ss_states: the forward's states too, for the coefficient backward
+        hs = output[2] if len(output) > 2 else None
+        if hs is not None:
+            ctx.mark_non_differentiable(hs)
+        ctx.save_for_backward(A, B, C, D, zi, x, hs)
         ctx.set_materialize_grads(False)
 
     def _lti_ss_backward(ctx, gy, gzf):
@@ -610,13 +614,14 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
         recomputed from the inputs and differentiable again."""
         from .lti.ssm import _state_space_composite
 
-        inputs = ctx.saved_tensors
+        saved = ctx.saved_tensors
+        inputs, hs = saved[:6], saved[6]
         needs = ctx.needs_input_grad
         A, B, C, D, zi, x = inputs
         if any(needs[:4]) and not torch.is_grad_enabled() and _has_op("lti_ss_backward"):
             g = gy if gy is not None else torch.zeros_like(x)
             with _op_ctx(A, B, C, D, zi, x, g):
-                res = torch.ops.philtorch.lti_ss_backward(A, B, C, D, zi, x, g, gzf, ctx.out_idx, ctx.reverse)
+                res = torch.ops.philtorch.lti_ss_backward(A, B, C, D, zi, x, g, gzf, ctx.out_idx, ctx.reverse, hs)
             out = [None] * 8
             for i, t in enumerate(inputs[:5] + (x,)):
                 if t is not None and needs[i]:
@@ -652,6 +657,23 @@ if EXTENSION_LOADED and _has_op("lti_ss"):
 
     torch.library.register_autograd("philtorch::lti_ss", _lti_ss_backward, setup_context=_lti_ss_setup)
 
+    if _has_op("lti_ss_states"):
+
+        @torch.library.register_fake("philtorch::lti_ss_states")
+        def _(A, B, C, D, zi, x, out_idx, reverse=False):
+            torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
+            M = A.shape[-1]
+            return _fake_like(x), x.new_empty((x.shape[0], M)), x.new_empty((x.shape[0], x.shape[1], M))
+
+        def _lti_ss_states_backward(ctx, gy, gzf, ghs):
+            """lti_ss's backward with the states the forward kept (hs is not
+            differentiable): the coefficient backward runs its adjoint pass
+            only."""
+            return _lti_ss_backward(ctx, gy, gzf)
+
+        torch.library.register_autograd("philtorch::lti_ss_states", _lti_ss_states_backward,
+                                        setup_context=_lti_ss_setup)
+
 if EXTENSION_LOADED and _has_op("lfilter_ss"):
     # lfilter of order <= 4 from b and a in one pass: (y, zf)
     @torch.library.register_fake("philtorch::lfilter_ss")
@@ -664,7 +686,7 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
     if _has_op("lfilter_ss_backward"):
 
         @torch.library.register_fake("philtorch::lfilter_ss_backward")
-        def _(b, a, zi, x, grad_y, grad_zf, form, reverse=False):
+        def _(b, a, zi, x, grad_y, grad_zf, form, reverse=False, hs=None):
             M = max(b.shape[-1] - 1, a.shape[-1])
             return [b.new_empty(b.shape), a.new_empty(a.shape), x.new_empty((x.shape[0], M)), _fake_like(x)]
 
@@ -672,7 +694,11 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
         b, a, zi, x, form = inputs[:5]
         ctx.form = form
         ctx.reverse = bool(inputs[5]) if len(inputs) > 5 else False
-        ctx.save_for_backward(b, a, zi, x)
+        # lfilter_ss_states: the forward's states too, for the coefficient backward
+        hs = output[2] if len(output) > 2 else None
+        if hs is not None:
+            ctx.mark_non_differentiable(hs)
+        ctx.save_for_backward(b, a, zi, x, hs)
         ctx.set_materialize_grads(False)
 
     def _lfilter_ss_backward(ctx, gy, gzf):
@@ -689,12 +715,15 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
         filtering.py:273-333), recomputed from the inputs."""
         from .lti.filtering import _ssm_lfilter
 
-        b, a, zi, x = inputs = ctx.saved_tensors
+        saved = ctx.saved_tensors
+        b, a, zi, x = inputs = saved[:4]
+        hs = saved[4]
         needs = ctx.needs_input_grad
         if (needs[0] or needs[1]) and not torch.is_grad_enabled() and _has_op("lfilter_ss_backward"):
             g = gy if gy is not None else torch.zeros_like(x)
             with _op_ctx(b, a, zi, x, g):
-                gb, ga, gzi, gx = torch.ops.philtorch.lfilter_ss_backward(b, a, zi, x, g, gzf, ctx.form, ctx.reverse)
+                gb, ga, gzi, gx = torch.ops.philtorch.lfilter_ss_backward(b, a, zi, x, g, gzf, ctx.form, ctx.reverse,
+                                                                          hs)
             return (gb if needs[0] else None, ga if needs[1] else None,
                     gzi if zi is not None and needs[2] else None, gx if needs[3] else None, None, None)
         if not (needs[0] or needs[1]):
@@ -722,6 +751,23 @@ if EXTENSION_LOADED and _has_op("lfilter_ss"):
         return tuple(out)
 
     torch.library.register_autograd("philtorch::lfilter_ss", _lfilter_ss_backward, setup_context=_lfilter_ss_setup)
+
+    if _has_op("lfilter_ss_states"):
+
+        @torch.library.register_fake("philtorch::lfilter_ss_states")
+        def _(b, a, zi, x, form, reverse=False):
+            torch._check(x.ndim == 2, lambda: "x must be 2D (batch, time)")
+            M = max(b.shape[-1] - 1, a.shape[-1])
+            return _fake_like(x), x.new_empty((x.shape[0], M)), x.new_empty((x.shape[0], x.shape[1], M))
+
+        def _lfilter_ss_states_backward(ctx, gy, gzf, ghs):
+            """lfilter_ss's backward with the states the forward kept (hs is
+            not differentiable): the gradients of b and a take the adjoint
+            pass only."""
+            return _lfilter_ss_backward(ctx, gy, gzf)
+
+        torch.library.register_autograd("philtorch::lfilter_ss_states", _lfilter_ss_states_backward,
+                                        setup_context=_lfilter_ss_setup)
 
 if EXTENSION_LOADED and _has_op("lpv_ss"):
     # single-input single-output LPV state space of order <= 4: (y, zf)

@@ -114,7 +114,7 @@ bool ss_filter_ok(const SsFilter &f, int M) {
 template <class Alg>
 int ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, const void *bv, bool b_sh, const void *cv, bool c_sh,
            int out_idx, const void *d, bool d_sh, const SsFilter &f, const void *zi, const void *x, void *y, void *zf,
-           void *workspace, size_t ws_bytes, bool rev, hipStream_t stream) {
+           void *workspace, size_t ws_bytes, bool rev, hipStream_t stream, void *hs = nullptr) {
   using E = typename Alg::elem;
   constexpr int M = SsView<Alg>::M;
   if (B < 0 || T < 0) return PHS_ERR_INVALID;
@@ -134,6 +134,12 @@ int ss_fwd(int64_t B, int64_t T, const void *A, bool A_sh, const void *bv, bool 
   a.d = static_cast<const E *>(d);
   a.d_stride = d_sh ? 0 : 1;
   a.out_idx = out_idx;
+  if (hs) {  // the states as well, in the same pass (the states-and-output mode)
+    a.hs = static_cast<E *>(hs);
+    a.vec_hs = aligned16(hs) && (size_t(T) * sizeof(typename Alg::s_state)) % 16 == 0 && aligned16(x) &&
+               (size_t(T) * sizeof(E)) % 16 == 0;
+    return rev ? ss_launch<Alg, true, kSsStatesY>(a, stream) : ss_launch<Alg, false, kSsStatesY>(a, stream);
+  }
   return rev ? ss_launch<Alg, true>(a, stream) : ss_launch<Alg, false>(a, stream);
 }
 
@@ -146,7 +152,8 @@ struct SsModelArgs {
 };
 
 // Gradients of y = model(x) (and zf) w.r.t. x, zi and the coefficients:
-// the forward again writing its states (kSsStates), the adjoint model in
+// the forward again writing its states (kSsStates; skipped when the forward
+// kept them, hs_in), the adjoint model in
 // the opposite time direction from grad_zf with the coefficient sums
 // (kSsGrad; explicit model: A^T, input vector c, output vector b; filter:
 // the other companion form of the same b and a), then the row sums and the
@@ -154,7 +161,8 @@ struct SsModelArgs {
 template <class Alg>
 int ss_bwd(int64_t B, int64_t T, const SsModelArgs<typename Alg::elem> &mo, const SsFilter &f, const void *zi,
            const void *x, const void *gy, const void *gzf, void *gx, void *gzi, SsGradOut<typename Alg::elem> out,
-           void *scratch, size_t scratch_bytes, void *workspace, size_t ws_bytes, bool rev, hipStream_t stream) {
+           void *scratch, size_t scratch_bytes, void *workspace, size_t ws_bytes, bool rev, hipStream_t stream,
+           const void *hs_in = nullptr) {
   using E = typename Alg::elem;
   using C = typename Wide<E>::type;
   using SS = typename Alg::s_state;
@@ -172,7 +180,7 @@ int ss_bwd(int64_t B, int64_t T, const SsModelArgs<typename Alg::elem> &mo, cons
   char *sc = static_cast<char *>(scratch);
   C *gpart = reinterpret_cast<C *>(sc + L.partials);
   C *rowsum = reinterpret_cast<C *>(sc + L.rowsum);
-  E *states = reinterpret_cast<E *>(sc + L.states);
+  E *states = hs_in ? const_cast<E *>(static_cast<const E *>(hs_in)) : reinterpret_cast<E *>(sc + L.states);
   const int64_t tiles = (T + SsShape<Alg, kSsGrad>::kTile - 1) / SsShape<Alg, kSsGrad>::kTile;
   auto set_model = [&](SsArgs<Alg> &a, bool adjoint) {
     a.A = static_cast<const E *>(mo.A);
@@ -196,8 +204,11 @@ int ss_bwd(int64_t B, int64_t T, const SsModelArgs<typename Alg::elem> &mo, cons
     p.hs = states;
     p.vec_hs = aligned16(states) && (size_t(T) * sizeof(SS)) % 16 == 0 && aligned16(x) &&
                (size_t(T) * sizeof(E)) % 16 == 0;
-    int rc = rev ? ss_launch<Alg, true, kSsStates>(p, stream) : ss_launch<Alg, false, kSsStates>(p, stream);
-    if (rc != PHS_OK) return rc;
+    int rc = PHS_OK;
+    if (!hs_in) {
+      rc = rev ? ss_launch<Alg, true, kSsStates>(p, stream) : ss_launch<Alg, false, kSsStates>(p, stream);
+      if (rc != PHS_OK) return rc;
+    }
     SsFilter fa = f;
     if (f.form != 0) fa.form = 3 - f.form;  // TDF-II <-> DF-II: the adjoint of a companion form
     if (!ss_args<Alg, kSsGrad>(B, T, fa, gzf, gy, gx, gzi, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
@@ -541,18 +552,19 @@ namespace {
 
 int lti_ss_call(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b, int b_shared,
                 const void *c, int c_shared, int out_idx, const void *d, int d_shared, const void *zi, const void *x,
-                void *y, void *zf, void *workspace, size_t workspace_bytes, bool rev, void *stream) {
+                void *y, void *zf, void *workspace, size_t workspace_bytes, bool rev, void *stream,
+                void *hs = nullptr) {
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return phs::ss_dispatch(dtype, M, [&](auto alg) {
     return phs::ss_fwd<decltype(alg)>(B, T, A, A_shared != 0, b, b_shared != 0, c, c_shared != 0, out_idx, d,
                                       d_shared != 0, phs::SsFilter{}, zi, x, y, zf, workspace, workspace_bytes, rev,
-                                      st);
+                                      st, hs);
   });
 }
 
 int lfilter_call(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na, int coef_shared,
                  int form, const void *zi, const void *x, void *y, void *zf, void *workspace, size_t workspace_bytes,
-                 bool rev, void *stream) {
+                 bool rev, void *stream, void *hs = nullptr) {
   if (form != PHS_FORM_TDF2 && form != PHS_FORM_DF2) return PHS_ERR_INVALID;
   const int M = nb - 1 > na ? nb - 1 : na;
   if (M < 1 || M > 4) return PHS_ERR_INVALID;
@@ -566,7 +578,7 @@ int lfilter_call(int dtype, int64_t B, int64_t T, const void *b, int nb, const v
   f.shared = coef_shared != 0;
   return phs::ss_dispatch(dtype, M, [&](auto alg) {
     return phs::ss_fwd<decltype(alg)>(B, T, nullptr, false, nullptr, false, nullptr, false, 0, nullptr, false, f, zi,
-                                      x, y, zf, workspace, workspace_bytes, rev, st);
+                                      x, y, zf, workspace, workspace_bytes, rev, st, hs);
   });
 }
 
@@ -600,6 +612,23 @@ int phs_lfilter_rev(int dtype, int64_t B, int64_t T, const void *b, int nb, cons
                       stream);
 }
 
+int phs_lti_ss_fwd_hs(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+                      int b_shared, const void *c, int c_shared, int out_idx, const void *d, int d_shared,
+                      const void *zi, const void *x, void *y, void *zf, void *hs, int reverse, void *workspace,
+                      size_t workspace_bytes, void *stream) {
+  if (!hs && B > 0 && T > 0) return PHS_ERR_INVALID;
+  return lti_ss_call(dtype, M, B, T, A, A_shared, b, b_shared, c, c_shared, out_idx, d, d_shared, zi, x, y, zf,
+                     workspace, workspace_bytes, reverse != 0, stream, hs);
+}
+
+int phs_lfilter_fwd_hs(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
+                       int coef_shared, int form, const void *zi, const void *x, void *y, void *zf, void *hs,
+                       int reverse, void *workspace, size_t workspace_bytes, void *stream) {
+  if (!hs && B > 0 && T > 0) return PHS_ERR_INVALID;
+  return lfilter_call(dtype, B, T, b, nb, a, na, coef_shared, form, zi, x, y, zf, workspace, workspace_bytes,
+                      reverse != 0, stream, hs);
+}
+
 size_t phs_lti_ss_bwd_scratch_size(int dtype, int M, int64_t B, int64_t T) {
   if (B < 0 || T < 0) return 0;
   size_t out = 0;
@@ -615,6 +644,16 @@ int phs_lti_ss_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
                    const void *x, const void *gy, const void *gzf, void *gx, void *gzi, void *gA, void *gb, void *gc,
                    void *gd, int reverse, void *scratch, size_t scratch_bytes, void *workspace,
                    size_t workspace_bytes, void *stream) {
+  return phs_lti_ss_bwd_hs(dtype, M, B, T, A, A_shared, b, b_shared, c, c_shared, out_idx, d, d_shared, zi, x,
+                           nullptr, gy, gzf, gx, gzi, gA, gb, gc, gd, reverse, scratch, scratch_bytes, workspace,
+                           workspace_bytes, stream);
+}
+
+int phs_lti_ss_bwd_hs(int dtype, int M, int64_t B, int64_t T, const void *A, int A_shared, const void *b,
+                      int b_shared, const void *c, int c_shared, int out_idx, const void *d, int d_shared,
+                      const void *zi, const void *x, const void *hs, const void *gy, const void *gzf, void *gx,
+                      void *gzi, void *gA, void *gb, void *gc, void *gd, int reverse, void *scratch,
+                      size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream) {
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return phs::ss_dispatch(dtype, M, [&](auto alg) {
     using Alg = decltype(alg);
@@ -627,7 +666,7 @@ int phs_lti_ss_bwd(int dtype, int M, int64_t B, int64_t T, const void *A, int A_
     o.gA = static_cast<E *>(gA), o.gb = static_cast<E *>(gb), o.gc = static_cast<E *>(gc), o.gd = static_cast<E *>(gd);
     o.A_sh = mo.A_sh, o.b_sh = mo.b_sh, o.c_sh = mo.c_sh, o.d_sh = mo.d_sh;
     return phs::ss_bwd<Alg>(B, T, mo, phs::SsFilter{}, zi, x, gy, gzf, gx, gzi, o, scratch, scratch_bytes, workspace,
-                            workspace_bytes, reverse != 0, st);
+                            workspace_bytes, reverse != 0, st, hs);
   });
 }
 
@@ -635,6 +674,14 @@ int phs_lfilter_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, cons
                     int form, const void *zi, const void *x, const void *gy, const void *gzf, void *gx, void *gzi,
                     void *gb, void *ga, int reverse, void *scratch, size_t scratch_bytes, void *workspace,
                     size_t workspace_bytes, void *stream) {
+  return phs_lfilter_bwd_hs(dtype, B, T, b, nb, a, na, coef_shared, form, zi, x, nullptr, gy, gzf, gx, gzi, gb, ga,
+                            reverse, scratch, scratch_bytes, workspace, workspace_bytes, stream);
+}
+
+int phs_lfilter_bwd_hs(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
+                       int coef_shared, int form, const void *zi, const void *x, const void *hs, const void *gy,
+                       const void *gzf, void *gx, void *gzi, void *gb, void *ga, int reverse, void *scratch,
+                       size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream) {
   if (form != PHS_FORM_TDF2 && form != PHS_FORM_DF2) return PHS_ERR_INVALID;
   const int M = nb - 1 > na ? nb - 1 : na;
   if (M < 1 || M > 4 || !gb || !ga) return PHS_ERR_INVALID;
@@ -653,7 +700,7 @@ int phs_lfilter_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, cons
     o.gfb = static_cast<E *>(gb);
     o.gfa = static_cast<E *>(ga);
     return phs::ss_bwd<Alg>(B, T, phs::SsModelArgs<E>{}, f, zi, x, gy, gzf, gx, gzi, o, scratch, scratch_bytes,
-                            workspace, workspace_bytes, reverse != 0, st);
+                            workspace, workspace_bytes, reverse != 0, st, hs);
   });
 }
 

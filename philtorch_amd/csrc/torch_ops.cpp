@@ -731,10 +731,20 @@ int64_t lti_ss_meta_check(const Tensor &A, const std::optional<Tensor> &Bm, cons
   return M;
 }
 
-std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
-                                      const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
-                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
-                                      bool reverse) {
+// A backward's optional states argument: the forward's (batch, T, M).
+void check_states(const std::optional<Tensor> &hs, const Tensor &x, int64_t M, const char *op) {
+  if (hs)
+    TORCH_CHECK(hs->dim() == 3 && hs->size(0) == x.size(0) && hs->size(1) == x.size(1) && hs->size(2) == M &&
+                    hs->scalar_type() == x.scalar_type() && hs->device() == x.device(),
+                "philtorch::", op, ": hs must be the forward's states (batch, T, M)");
+}
+
+// keep_states: also hs (batch, T, M), the state before every step, from the
+// same pass (phs_lti_ss_fwd_hs) for the coefficient backward.
+std::tuple<Tensor, Tensor, Tensor> lti_ss_impl(const Tensor &A, const std::optional<Tensor> &Bm,
+                                               const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
+                                               const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
+                                               bool reverse, bool keep_states) {
   const int64_t M = lti_ss_meta_check(A, Bm, Cm, Dm, zi, x, out_idx);
   const int64_t B = x.size(0), T = x.size(1);
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
@@ -744,21 +754,48 @@ std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tenso
   Tensor dc = Dm ? Dm->contiguous() : Tensor(), zc = zi ? zi->contiguous() : Tensor();
   Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
   Tensor zf = at::empty({B, M}, x.options());
-  if (B == 0) return {y, zf};
+  Tensor hs = at::empty({keep_states ? B : 0, keep_states ? T : 0, M}, x.options());
+  if (B == 0) return {y, zf, hs};
   if (T == 0) {
     if (zi) zf.copy_(zc); else zf.zero_();
-    return {y, zf};
+    return {y, zf, hs};
   }
   void *stream = stream_of(x);
   const Workspace ws = workspace_for(x, phs_lti_ss_workspace_size(dt, int(M), B, T), stream);
-  check_status((reverse ? phs_lti_ss_rev : phs_lti_ss_fwd)(dt, int(M), B, T, Ac.const_data_ptr(), A.dim() == 2 ? 1 : 0,
-                              Bm ? bc.const_data_ptr() : nullptr, Bm && Bm->dim() == 1 ? 1 : 0,
-                              Cm ? cc.const_data_ptr() : nullptr, Cm && Cm->dim() == 1 ? 1 : 0, int(out_idx),
-                              Dm ? dc.const_data_ptr() : nullptr, Dm && Dm->numel() == 1 ? 1 : 0,
-                              zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(), y.mutable_data_ptr(),
-                              zf.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
-               "lti_ss");
+  const void *bp = Bm ? bc.const_data_ptr() : nullptr, *cp = Cm ? cc.const_data_ptr() : nullptr;
+  const void *dp = Dm ? dc.const_data_ptr() : nullptr, *zp = zi ? zc.const_data_ptr() : nullptr;
+  const int ash = A.dim() == 2 ? 1 : 0, bsh = Bm && Bm->dim() == 1 ? 1 : 0, csh = Cm && Cm->dim() == 1 ? 1 : 0;
+  const int dsh = Dm && Dm->numel() == 1 ? 1 : 0;
+  if (keep_states)
+    check_status(phs_lti_ss_fwd_hs(dt, int(M), B, T, Ac.const_data_ptr(), ash, bp, bsh, cp, csh, int(out_idx), dp,
+                                   dsh, zp, xc.const_data_ptr(), y.mutable_data_ptr(), zf.mutable_data_ptr(),
+                                   hs.mutable_data_ptr(), reverse ? 1 : 0, ws.ptr, ws.bytes, stream),
+                 "lti_ss_states");
+  else
+    check_status((reverse ? phs_lti_ss_rev : phs_lti_ss_fwd)(dt, int(M), B, T, Ac.const_data_ptr(), ash, bp, bsh, cp,
+                                                             csh, int(out_idx), dp, dsh, zp, xc.const_data_ptr(),
+                                                             y.mutable_data_ptr(), zf.mutable_data_ptr(), ws.ptr,
+                                                             ws.bytes, stream),
+                 "lti_ss");
+  return {y, zf, hs};
+}
+
+std::tuple<Tensor, Tensor> lti_ss_hip(const Tensor &A, const std::optional<Tensor> &Bm,
+                                      const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
+                                      const std::optional<Tensor> &zi, const Tensor &x, int64_t out_idx,
+                                      bool reverse) {
+  auto [y, zf, hs] = lti_ss_impl(A, Bm, Cm, Dm, zi, x, out_idx, reverse, false);
   return {y, zf};
+}
+
+// lti_ss that also returns hs (batch, T, M), the states lti_ss_backward
+// would compute again.
+std::tuple<Tensor, Tensor, Tensor> lti_ss_states_hip(const Tensor &A, const std::optional<Tensor> &Bm,
+                                                     const std::optional<Tensor> &Cm,
+                                                     const std::optional<Tensor> &Dm,
+                                                     const std::optional<Tensor> &zi, const Tensor &x,
+                                                     int64_t out_idx, bool reverse) {
+  return lti_ss_impl(A, Bm, Cm, Dm, zi, x, out_idx, reverse, true);
 }
 
 // lfilter of order <= 4 from b and a directly (phs_lfilter_fwd;
@@ -793,8 +830,9 @@ int64_t lfilter_ss_meta_check(const Tensor &b, const Tensor &a, const std::optio
   return M;
 }
 
-std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, const std::optional<Tensor> &zi,
-                                          const Tensor &x, int64_t form, bool reverse) {
+std::tuple<Tensor, Tensor, Tensor> lfilter_ss_impl(const Tensor &b, const Tensor &a,
+                                                   const std::optional<Tensor> &zi, const Tensor &x, int64_t form,
+                                                   bool reverse, bool keep_states) {
   const int64_t M = lfilter_ss_meta_check(b, a, zi, x, form);
   const int64_t B = x.size(0), T = x.size(1), nb = b.size(-1), na = a.size(-1);
   const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
@@ -802,19 +840,41 @@ std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, cons
   Tensor bc = b.contiguous(), ac = a.contiguous(), xc = x.contiguous(), zc = zi ? zi->contiguous() : Tensor();
   Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
   Tensor zf = at::empty({B, M}, x.options());
-  if (B == 0) return {y, zf};
+  Tensor hs = at::empty({keep_states ? B : 0, keep_states ? T : 0, M}, x.options());
+  if (B == 0) return {y, zf, hs};
   if (T == 0) {
     if (zi) zf.copy_(zc); else zf.zero_();
-    return {y, zf};
+    return {y, zf, hs};
   }
   void *stream = stream_of(x);
   const Workspace ws = workspace_for(x, phs_lti_ss_workspace_size(dt, int(M), B, T), stream);
-  check_status((reverse ? phs_lfilter_rev : phs_lfilter_fwd)(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
-                               b.dim() == 1 ? 1 : 0, int(form), zi ? zc.const_data_ptr() : nullptr,
-                               xc.const_data_ptr(), y.mutable_data_ptr(), zf.mutable_data_ptr(), ws.ptr, ws.bytes,
-                               stream),
-               "lfilter_ss");
+  if (keep_states)
+    check_status(phs_lfilter_fwd_hs(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
+                                    b.dim() == 1 ? 1 : 0, int(form), zi ? zc.const_data_ptr() : nullptr,
+                                    xc.const_data_ptr(), y.mutable_data_ptr(), zf.mutable_data_ptr(),
+                                    hs.mutable_data_ptr(), reverse ? 1 : 0, ws.ptr, ws.bytes, stream),
+                 "lfilter_ss_states");
+  else
+    check_status((reverse ? phs_lfilter_rev : phs_lfilter_fwd)(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
+                                 b.dim() == 1 ? 1 : 0, int(form), zi ? zc.const_data_ptr() : nullptr,
+                                 xc.const_data_ptr(), y.mutable_data_ptr(), zf.mutable_data_ptr(), ws.ptr, ws.bytes,
+                                 stream),
+                 "lfilter_ss");
+  return {y, zf, hs};
+}
+
+std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, const std::optional<Tensor> &zi,
+                                          const Tensor &x, int64_t form, bool reverse) {
+  auto [y, zf, hs] = lfilter_ss_impl(b, a, zi, x, form, reverse, false);
   return {y, zf};
+}
+
+// lfilter_ss that also returns hs (batch, T, order), the states
+// lfilter_ss_backward would compute again.
+std::tuple<Tensor, Tensor, Tensor> lfilter_ss_states_hip(const Tensor &b, const Tensor &a,
+                                                         const std::optional<Tensor> &zi, const Tensor &x,
+                                                         int64_t form, bool reverse) {
+  return lfilter_ss_impl(b, a, zi, x, form, reverse, true);
 }
 
 // Gradients of lti_ss w.r.t. every input (phs_lti_ss_bwd): returns
@@ -826,10 +886,13 @@ std::tuple<Tensor, Tensor> lfilter_ss_hip(const Tensor &b, const Tensor &a, cons
 std::vector<Tensor> lti_ss_backward_hip(const Tensor &A, const std::optional<Tensor> &Bm,
                                         const std::optional<Tensor> &Cm, const std::optional<Tensor> &Dm,
                                         const std::optional<Tensor> &zi, const Tensor &x, const Tensor &gy,
-                                        const std::optional<Tensor> &gzf, int64_t out_idx, bool reverse) {
+                                        const std::optional<Tensor> &gzf, int64_t out_idx, bool reverse,
+                                        const std::optional<Tensor> &hs) {
   // the forward's argument checks
   (void)lti_ss_meta_check(A, Bm, Cm, Dm, zi, x, out_idx);
   const int64_t B = x.size(0), T = x.size(1), M = A.size(-1);
+  check_states(hs, x, M, "lti_ss_backward");
+  Tensor hc = hs ? hs->contiguous() : Tensor();
   TORCH_CHECK(gy.sizes() == x.sizes() && gy.device() == x.device(),
               "philtorch::lti_ss_backward: grad_y must have x's shape and device");
   if (gzf)
@@ -854,11 +917,12 @@ std::vector<Tensor> lti_ss_backward_hip(const Tensor &A, const std::optional<Ten
   void *stream = stream_of(x);
   Tensor scratch = at::empty({int64_t(phs_lti_ss_bwd_scratch_size(dt, int(M), B, T))}, x.options().dtype(at::kByte));
   const Workspace ws = workspace_for(x, phs_lti_ss_workspace_size(dt, int(M), B, T), stream);
-  check_status(phs_lti_ss_bwd(dt, int(M), B, T, Ac.const_data_ptr(), A.dim() == 2 ? 1 : 0,
+  check_status(phs_lti_ss_bwd_hs(dt, int(M), B, T, Ac.const_data_ptr(), A.dim() == 2 ? 1 : 0,
                               Bm ? bc.const_data_ptr() : nullptr, Bm && Bm->dim() == 1 ? 1 : 0,
                               Cm ? cc.const_data_ptr() : nullptr, Cm && Cm->dim() == 1 ? 1 : 0, int(out_idx),
                               Dm ? dc.const_data_ptr() : nullptr, Dm && Dm->numel() == 1 ? 1 : 0,
-                              zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(), gc.const_data_ptr(),
+                              zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(),
+                              hs ? hc.const_data_ptr() : nullptr, gc.const_data_ptr(),
                               gzf ? gzc.const_data_ptr() : nullptr, gx.mutable_data_ptr(), gzi.mutable_data_ptr(),
                               gA.mutable_data_ptr(), Bm ? gB.mutable_data_ptr() : nullptr,
                               Cm ? gC.mutable_data_ptr() : nullptr, Dm ? gD.mutable_data_ptr() : nullptr,
@@ -874,10 +938,12 @@ std::vector<Tensor> lti_ss_backward_hip(const Tensor &A, const std::optional<Ten
 // autograd of the companion-form route (philtorch/lti/filtering.py:273-333).
 std::vector<Tensor> lfilter_ss_backward_hip(const Tensor &b, const Tensor &a, const std::optional<Tensor> &zi,
                                             const Tensor &x, const Tensor &gy, const std::optional<Tensor> &gzf,
-                                            int64_t form, bool reverse) {
+                                            int64_t form, bool reverse, const std::optional<Tensor> &hs) {
   (void)lfilter_ss_meta_check(b, a, zi, x, form);
   const int64_t B = x.size(0), T = x.size(1), nb = b.size(-1), na = a.size(-1);
   const int64_t M = std::max(nb - 1, na);
+  check_states(hs, x, M, "lfilter_ss_backward");
+  Tensor hc = hs ? hs->contiguous() : Tensor();
   TORCH_CHECK(gy.sizes() == x.sizes() && gy.device() == x.device(),
               "philtorch::lfilter_ss_backward: grad_y must have x's shape and device");
   if (gzf)
@@ -898,9 +964,10 @@ std::vector<Tensor> lfilter_ss_backward_hip(const Tensor &b, const Tensor &a, co
   void *stream = stream_of(x);
   Tensor scratch = at::empty({int64_t(phs_lti_ss_bwd_scratch_size(dt, int(M), B, T))}, x.options().dtype(at::kByte));
   const Workspace ws = workspace_for(x, phs_lti_ss_workspace_size(dt, int(M), B, T), stream);
-  check_status(phs_lfilter_bwd(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
+  check_status(phs_lfilter_bwd_hs(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
                                b.dim() == 1 ? 1 : 0, int(form), zi ? zc.const_data_ptr() : nullptr,
-                               xc.const_data_ptr(), gc.const_data_ptr(), gzf ? gzc.const_data_ptr() : nullptr,
+                               xc.const_data_ptr(), hs ? hc.const_data_ptr() : nullptr, gc.const_data_ptr(),
+                               gzf ? gzc.const_data_ptr() : nullptr,
                                gx.mutable_data_ptr(), gzi.mutable_data_ptr(), gb.mutable_data_ptr(),
                                ga.mutable_data_ptr(), reverse ? 1 : 0, scratch.mutable_data_ptr(),
                                size_t(scratch.numel()), ws.ptr, ws.bytes, stream),
@@ -1479,10 +1546,17 @@ TORCH_LIBRARY(philtorch, m) {
         {at::Tag::pt2_compliant_tag});
   // new: their fused gradients w.r.t. every input (coefficients included)
   m.def("lti_ss_backward(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, Tensor grad_y, "
-        "Tensor? grad_zf, int out_idx, bool reverse=False) -> Tensor[]",
+        "Tensor? grad_zf, int out_idx, bool reverse=False, Tensor? hs=None) -> Tensor[]",
         {at::Tag::pt2_compliant_tag});
   m.def("lfilter_ss_backward(Tensor b, Tensor a, Tensor? zi, Tensor x, Tensor grad_y, Tensor? grad_zf, int form, "
-        "bool reverse=False) -> Tensor[]",
+        "bool reverse=False, Tensor? hs=None) -> Tensor[]",
+        {at::Tag::pt2_compliant_tag});
+  // new: the forwards that also return their states, for the coefficient backward
+  m.def("lti_ss_states(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx, "
+        "bool reverse=False) -> (Tensor, Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
+  m.def("lfilter_ss_states(Tensor b, Tensor a, Tensor? zi, Tensor x, int form, bool reverse=False) -> "
+        "(Tensor, Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
   m.def("lpv_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx, bool reverse=False, "
         "bool transpose_A=False) -> (Tensor, Tensor)",
@@ -1524,6 +1598,8 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("biquad_cols_backward", &biquad_cols_backward_hip);
   m.impl("lti_ss", &lti_ss_hip);
   m.impl("lfilter_ss", &lfilter_ss_hip);
+  m.impl("lti_ss_states", &lti_ss_states_hip);
+  m.impl("lfilter_ss_states", &lfilter_ss_states_hip);
   m.impl("lti_ss_backward", &lti_ss_backward_hip);
   m.impl("lfilter_ss_backward", &lfilter_ss_backward_hip);
   m.impl("lpv_ss", &lpv_ss_hip);

@@ -189,10 +189,16 @@ def _fused_lfilter(b: Tensor, a: Tensor, x: Tensor, zi: Optional[Tensor], form: 
     """lfilter(b, a, x, zi, form) through philtorch::lfilter_ss."""
     M = max(b.size(-1) - 1, a.size(-1))
     zb = None if zi is None else zi.expand(x.size(0), M).contiguous()
-    from .. import _op_ctx
+    from .. import _has_op, _op_ctx
 
+    # b or a with a gradient to come: the forward keeps its states
+    # (lfilter_ss_states), which their backward would compute again
+    keep = torch.is_grad_enabled() and (b.requires_grad or a.requires_grad) and _has_op("lfilter_ss_states")
     with _op_ctx(b, a, zb, x):
-        y, zf = torch.ops.philtorch.lfilter_ss(b, a, zb, x, 0 if form == "tdf2" else 1)
+        if keep:
+            y, zf, _ = torch.ops.philtorch.lfilter_ss_states(b, a, zb, x, 0 if form == "tdf2" else 1)
+        else:
+            y, zf = torch.ops.philtorch.lfilter_ss(b, a, zb, x, 0 if form == "tdf2" else 1)
     return y if zi is None else (y, zf)
 
 

@@ -436,11 +436,18 @@ def _state_space(A, x, B, C, D, zi, unroll_factor, out_idx, fused):
     if unroll_factor is None:
         unroll_factor = round(N**0.5)
     if fused and _fused_ss_applies(A, x, B, C, D, zi, unroll_factor, out_idx):
-        from .. import _op_ctx
+        from .. import _has_op, _op_ctx
 
+        # a coefficient with a gradient to come: the forward keeps its states
+        # (lti_ss_states), which the coefficient backward would compute again
+        keep = (torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (A, B, C, D))
+                and _has_op("lti_ss_states"))
         with _op_ctx(A, B, C, D, zi, x):
-            y, zf = torch.ops.philtorch.lti_ss(A, B, C, D, zi.contiguous() if return_zf else None, x,
-                                               out_idx if C is None else 0)
+            args = (A, B, C, D, zi.contiguous() if return_zf else None, x, out_idx if C is None else 0)
+            if keep:
+                y, zf, _ = torch.ops.philtorch.lti_ss_states(*args)
+            else:
+                y, zf = torch.ops.philtorch.lti_ss(*args)
         return (y, zf) if return_zf else y
     ops = _mimo_operands(A, x, B, C, D, out_idx, batch, M) if fused and _mimo_applies(
         A, x, B, C, D, zi, unroll_factor) else None

@@ -144,6 +144,16 @@ def test_lti_ss_backward_vs_composed_route(hip, dtype, M, Bn, T):
             print(f"lti_ss_backward {np.dtype(dtype).name} M={M} B={Bn} T={T} layout={layout} rev={rev}", flush=True)
             res = torch.ops.philtorch.lti_ss_backward(*[_t(v) for v in ops], _t(gy), _t(gzf), out_idx, rev)
             got = [r.cpu().numpy() for r in res]
+            # the forward keeping its states (phs_lti_ss_fwd_hs; other tile lengths, so y within
+            # tolerance of lti_ss's) and the backward given them: the same gradients, bit for bit
+            y1, zf1 = torch.ops.philtorch.lti_ss(*[_t(v) for v in ops], out_idx, rev)
+            y2, zf2, hs = torch.ops.philtorch.lti_ss_states(*[_t(v) for v in ops], out_idx, rev)
+            assert hs.shape == (Bn, T, M)
+            D.check(y2.cpu().numpy(), y1.cpu().numpy(), "lti_ss_states y", dtype=dtype)
+            D.check(zf2.cpu().numpy(), zf1.cpu().numpy(), "lti_ss_states zf", dtype=dtype)
+            res_hs = torch.ops.philtorch.lti_ss_backward(*[_t(v) for v in ops], _t(gy), _t(gzf), out_idx, rev, hs)
+            for r0, r1 in zip(res, res_hs):
+                assert torch.equal(r0, r1)
             ref = _composite_grads([None if v is None else v.astype(np.float64) for v in ops],
                                    gy.astype(np.float64), gzf.astype(np.float64), out_idx, rev, "cpu")
             names = ("grad_A", "grad_B", "grad_C", "grad_D", "grad_zi", "grad_x")
@@ -188,8 +198,16 @@ def test_lfilter_ss_backward_vs_composed_route(hip, dtype, nb, na, form, shared)
         gy, gzf = g.standard_normal((Bn, T)).astype(dtype), g.standard_normal((Bn, M)).astype(dtype)
         print(f"lfilter_ss_backward {np.dtype(dtype).name} nb={nb} na={na} form={form} shared={shared} rev={rev}",
               flush=True)
-        got = [r.cpu().numpy() for r in torch.ops.philtorch.lfilter_ss_backward(
-            _t(b), _t(a), _t(zi), _t(x), _t(gy), _t(gzf), form, rev)]
+        res = torch.ops.philtorch.lfilter_ss_backward(_t(b), _t(a), _t(zi), _t(x), _t(gy), _t(gzf), form, rev)
+        got = [r.cpu().numpy() for r in res]
+        # the states-keeping forward, and the backward given its states: bit for bit
+        y1, zf1 = torch.ops.philtorch.lfilter_ss(_t(b), _t(a), _t(zi), _t(x), form, rev)
+        y2, zf2, hs = torch.ops.philtorch.lfilter_ss_states(_t(b), _t(a), _t(zi), _t(x), form, rev)
+        D.check(y2.cpu().numpy(), y1.cpu().numpy(), "lfilter_ss_states y", dtype=dtype)
+        D.check(zf2.cpu().numpy(), zf1.cpu().numpy(), "lfilter_ss_states zf", dtype=dtype)
+        res_hs = torch.ops.philtorch.lfilter_ss_backward(_t(b), _t(a), _t(zi), _t(x), _t(gy), _t(gzf), form, rev, hs)
+        for r0, r1 in zip(res, res_hs):
+            assert torch.equal(r0, r1)
         tb, ta, tz, tx = (_t(v.astype(np.float64), "cpu", True) for v in (b, a, zi, x))
         xs = tx.flip(-1) if rev else tx
         y, zf = _ssm_lfilter(tb, ta, xs, tz, form=("tdf2", "df2")[form], unroll_factor=1)
@@ -249,6 +267,15 @@ def test_api_takes_fused_route_with_coefficient_gradients(hip, monkeypatch):
         for rev in (False, True):
             fl = lambda b_, a_, x_: torch.ops.philtorch.lfilter_ss(b_, a_, None, x_, form, rev)[0]  # noqa: E731
             assert torch.autograd.gradcheck(fl, (bf, af, xs))
+            # the states-keeping forwards the API takes with coefficient gradients
+            fs = lambda b_, a_, x_: torch.ops.philtorch.lfilter_ss_states(b_, a_, None, x_, form, rev)[0]  # noqa: E731
+            assert torch.autograd.gradcheck(fs, (bf, af, xs))
+    fs = lambda A_, b_, c_, d_, x_: torch.ops.philtorch.lti_ss_states(A_, b_, c_, d_, None, x_, 0)[0]  # noqa: E731
+    assert torch.autograd.gradcheck(fs, (As, bs, cs, ds, xs))
+    det = [t.detach() for t in (bf, af)]
+    torch.library.opcheck(torch.ops.philtorch.lfilter_ss_states.default, (*det, None, xs.detach(), 0, False))
+    torch.library.opcheck(torch.ops.philtorch.lti_ss_states.default,
+                          (As.detach(), bs.detach(), cs.detach(), ds.detach(), None, xs.detach(), 0, False))
 
 
 def test_backward_ops_on_empty_inputs(hip):
