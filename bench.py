@@ -25,7 +25,8 @@ adjoint op (grads w.r.t. the coefficients, the input and the initial state):
   c4_filtfilt_grad  the same plus the gradient w.r.t. x (philtorch::filtfilt_backward)
   c4_filtfilt_coef  the same plus the gradients w.r.t. x, b and a (its coefficient mode)
   c4_lfilter4  4 x lti.lfilter of order 4 (tdf2), forward only (philtorch::lti_ss)
-  c4_lfilter4_grad  the same plus gradients w.r.t. x, b and a (philtorch::lfilter_ss_backward)
+  c4_lfilter4_grad  the same plus gradients w.r.t. x, b and a (philtorch::lfilter_ss_states forward,
+                    philtorch::lfilter_ss_backward given its states)
   c4_mimo  lti.state_space of order 4, 2 inputs and 2 outputs per step (philtorch::mimo_ss)
   c4_mimo_grad  the same plus gradients w.r.t. x and zi (the adjoint mimo_ss pass)
   c4_mimo_coef  the same plus gradients w.r.t. A, B, C, D (two states passes and the fused sums)
@@ -695,8 +696,9 @@ class LpvSsGrad(LpvSsApi):
 class Lfilter4Grad(Lfilter4Api):
     """c4_lfilter4_grad: c4_lfilter4 with the gradients w.r.t. x and every
     filter's b and a (torch.autograd.grad against a seeded upstream
-    gradient).  Each lfilter's backward is philtorch::lfilter_ss_backward:
-    the forward again keeping its states, then the adjoint pass with the
+    gradient).  Each lfilter's forward keeps its states
+    (philtorch::lfilter_ss_states) and its backward is
+    philtorch::lfilter_ss_backward given them: the adjoint pass with the
     coefficient sums."""
 
     def __init__(self):
@@ -708,9 +710,9 @@ class Lfilter4Grad(Lfilter4Api):
                        "fp32 (API)")
         g = torch.Generator().manual_seed(44)
         self.gy = torch.randn(self.B, self.T, generator=g).cuda()
-        # per lfilter: states pass (read x, write 4 states) + adjoint (read g, x, 4 states; write grad_x)
-        self.bwd_bytes = (4 + 16) * self.B * self.T + (4 + 4 + 16 + 4) * self.B * self.T
-        self.bwd_launch_bytes = (4 + 16) * self.B * self.T  # the states pass
+        # per lfilter: the forward also writes its 4 states; the adjoint reads g, x, 4 states, writes grad_x
+        self.fwd_bytes += 16 * self.B * self.T
+        self.bwd_bytes = (4 + 4 + 16 + 4) * self.B * self.T
 
     def step_fwd(self):
         from philtorch_amd import lti
