@@ -381,6 +381,25 @@ int phs_filtfilt_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, con
                      void *grad_b, void *grad_a, void *scratch, size_t scratch_bytes, void *workspace,
                      size_t workspace_bytes, void *stream);
 
+/* ---- The filtfilt pair split for a caller that keeps the forward's states
+ * (no counterpart in the reference, whose autograd saves the composed
+ * route's tensors; philtorch/lti/filtering.py:107-142, 413-484).
+ * phs_filtfilt_fwd_hs: phs_filtfilt_fwd whose two passes also write their
+ * states, h1 and h2 [B,T,M] each (M = max(nb - 1, na)), beside pass 1's
+ * output in `mid` (its y agrees with phs_filtfilt_fwd's to rounding: the
+ * states-and-output mode scans other tile lengths).  phs_filtfilt_bwd_hs:
+ * phs_filtfilt_bwd given that mid, h1 and h2 (all three, or none: then it
+ * computes them again); with grad_b/grad_a it skips both passes' recompute,
+ * with the same results bit for bit. */
+int phs_filtfilt_fwd_hs(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
+                        int coef_shared, int padmode, int64_t padlen, const void *x, void *y, void *mid, void *h1,
+                        void *h2, void *workspace, size_t workspace_bytes, void *stream);
+
+int phs_filtfilt_bwd_hs(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
+                        int coef_shared, int padmode, int64_t padlen, const void *x, const void *mid, const void *h1,
+                        const void *h2, const void *grad_y, void *grad_x, void *grad_b, void *grad_a, void *scratch,
+                        size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- Single-input, single-output LTI state space of order M = 1..4, fused
  * (forward).  Replaces philtorch.lti.state_space (philtorch/lti/ssm.py:
  * 386-510 with _ssm_C_D :513-589) for a 2D input x, B an M-vector (or

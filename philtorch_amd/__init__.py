@@ -512,7 +512,7 @@ if EXTENSION_LOADED and _has_op("filtfilt"):
 
     if _has_op("filtfilt_backward"):
         @torch.library.register_fake("philtorch::filtfilt_backward")
-        def _(b, a, x, grad_y, padmode, padlen, need_coef):
+        def _(b, a, x, grad_y, padmode, padlen, need_coef, mid=None, h1=None, h2=None):
             _filtfilt_fake_check(b, a, grad_y, padlen)
             if need_coef:
                 return [_fake_like(grad_y), b.new_empty(b.shape), a.new_empty(a.shape)]
@@ -535,7 +535,11 @@ if EXTENSION_LOADED and _has_op("filtfilt"):
 
         def _filtfilt_setup(ctx, inputs, output):
             b, a, x, padmode, padlen = inputs
-            ctx.save_for_backward(b, a, x)
+            # filtfilt_states: pass 1's output and both passes' states too
+            kept = tuple(output[1:]) if isinstance(output, (tuple, list)) else ()
+            for t in kept:
+                ctx.mark_non_differentiable(t)
+            ctx.save_for_backward(b, a, x, *kept)
             ctx.pad = (padmode, padlen)
             ctx.set_materialize_grads(False)
 
@@ -548,7 +552,9 @@ if EXTENSION_LOADED and _has_op("filtfilt"):
             needs = ctx.needs_input_grad
             if gy is None or not any(needs[:3]):
                 return None, None, None, None, None
-            b, a, x = ctx.saved_tensors
+            saved = ctx.saved_tensors
+            b, a, x = saved[:3]
+            kept = saved[3:]  # mid, h1, h2 from filtfilt_states, or none
             need_coef = bool(needs[0] or needs[1])
             if not need_coef:
                 if torch.is_grad_enabled():
@@ -570,10 +576,31 @@ if EXTENSION_LOADED and _has_op("filtfilt"):
                     out[i] = g if g is not None else torch.zeros_like(inputs[i])
                 return tuple(out)
             with _op_ctx(b, a, x, gy):
-                gx, gb, ga = torch.ops.philtorch.filtfilt_backward(b, a, x, gy, *ctx.pad, True)
+                gx, gb, ga = torch.ops.philtorch.filtfilt_backward(b, a, x, gy, *ctx.pad, True, *kept)
             return gb if needs[0] else None, ga if needs[1] else None, gx if needs[2] else None, None, None
 
         torch.library.register_autograd("philtorch::filtfilt", _filtfilt_backward, setup_context=_filtfilt_setup)
+
+        if _has_op("filtfilt_states"):
+
+            @torch.library.register_fake("philtorch::filtfilt_states")
+            def _(b, a, x, padmode, padlen):
+                _filtfilt_fake_check(b, a, x, padlen)
+                B, T = x.shape
+                M = max(b.shape[-1] - 1, a.shape[-1])
+                al = lambda n: (n + 255) // 256 * 256  # noqa: E731  (the library's 256-byte alignment)
+                mid = al(B * T * x.element_size()) + al(B * 4 * x.element_size()) if B else 0
+                return (_fake_like(x), x.new_empty((mid,), dtype=torch.uint8), x.new_empty((B, T, M)),
+                        x.new_empty((B, T, M)))
+
+            def _filtfilt_states_backward(ctx, gy, gmid, gh1, gh2):
+                """filtfilt's backward with pass 1's output and both passes'
+                states from the forward (not differentiable): the coefficient
+                mode skips computing them again."""
+                return _filtfilt_backward(ctx, gy)
+
+            torch.library.register_autograd("philtorch::filtfilt_states", _filtfilt_states_backward,
+                                            setup_context=_filtfilt_setup)
 
 if EXTENSION_LOADED and _has_op("lti_ss"):
     # single-input single-output LTI state space of order <= 4: (y, zf)

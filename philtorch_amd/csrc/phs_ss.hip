@@ -256,10 +256,17 @@ size_t filtfilt_ws_bytes(int64_t B, int64_t T) {
 
 // Zero-phase filter: pass 1 forward over x from the edge-derived state into
 // mid (output and final state), pass 2 in reversed time over mid into y.
+// With h1 and h2: both passes also write their states [B, T, M] (the
+// states-and-output mode, as the coefficient backward computes them again).
 template <class Alg>
 int ss_filtfilt(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e, const void *x, void *y, void *mid,
-                void *workspace, size_t ws_bytes, hipStream_t stream) {
+                void *workspace, size_t ws_bytes, hipStream_t stream, void *h1 = nullptr, void *h2 = nullptr) {
   using E = typename Alg::elem;
+  using SS = typename Alg::s_state;
+  const bool keep = h1 && h2;
+  auto vec_states = [&](const void *hs, const void *xf) {
+    return aligned16(hs) && (size_t(T) * sizeof(SS)) % 16 == 0 && aligned16(xf) && (size_t(T) * sizeof(E)) % 16 == 0;
+  };
   if (ws_bytes < filtfilt_ws_bytes<E>(B, T)) return PHS_ERR_WORKSPACE;  // the documented size, any order
   char *m = static_cast<char *>(mid);
   E *y1 = reinterpret_cast<E *>(m);
@@ -270,7 +277,11 @@ int ss_filtfilt(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e, co
   p.xpad = static_cast<const E *>(x);
   p.pad_mode = mode;
   p.pad_len = e;
-  int rc = ss_launch<Alg, false>(p, stream);
+  if (keep) {
+    p.hs = static_cast<E *>(h1);
+    p.vec_hs = vec_states(h1, x);
+  }
+  int rc = keep ? ss_launch<Alg, false, kSsStatesY>(p, stream) : ss_launch<Alg, false>(p, stream);
   if (rc != PHS_OK) return rc;
   if (!ss_args<Alg>(B, T, f, nullptr, y1, y, nullptr, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
   p.virt_mode = 2;
@@ -278,6 +289,11 @@ int ss_filtfilt(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e, co
   p.zf_prev = zf1;
   p.pad_mode = mode;
   p.pad_len = e;
+  if (keep) {
+    p.hs = static_cast<E *>(h2);
+    p.vec_hs = vec_states(h2, y1);
+    return ss_launch<Alg, true, kSsStatesY>(p, stream);
+  }
   return ss_launch<Alg, true>(p, stream);
 }
 
@@ -335,7 +351,8 @@ FfBwdLayout<Alg> ff_bwd_layout(int64_t B, int64_t T, int64_t e, bool coef) {
 template <class Alg>
 int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e, const void *x, const void *gy,
                     void *gx, void *gfb, void *gfa, void *scratch, size_t scratch_bytes, void *workspace,
-                    size_t ws_bytes, hipStream_t stream) {
+                    size_t ws_bytes, hipStream_t stream, const void *mid_in = nullptr, const void *h1_in = nullptr,
+                    const void *h2_in = nullptr) {
   using E = typename Alg::elem;
   using C = typename Wide<E>::type;
   using SS = typename Alg::s_state;
@@ -401,6 +418,17 @@ int ss_filtfilt_bwd(int64_t B, int64_t T, const SsFilter &f, int mode, int64_t e
     k.gz = static_cast<double *>(at(L.gz));
     k.rowsum1 = rowsum1;
     k.rowsum2 = rowsum2;
+  }
+  if (coef && mid_in && h1_in && h2_in) {
+    // the forward kept pass 1's output and final state and both passes' states
+    char *m = static_cast<char *>(const_cast<void *>(mid_in));
+    y1 = reinterpret_cast<E *>(m);
+    zf1 = reinterpret_cast<E *>(m + filtfilt_zf_offset(sizeof(E), B, T));
+    h1 = static_cast<SS *>(const_cast<void *>(h1_in));
+    h2 = static_cast<SS *>(const_cast<void *>(h2_in));
+    k.y1 = y1;
+    k.zf1 = zf1;
+  } else if (coef) {
     // pass 1 (states, output, final state), then pass 2 (states)
     if (!ss_args<Alg>(B, T, f, nullptr, x, y1, zf1, workspace, ws_bytes, p)) return PHS_ERR_WORKSPACE;
     p.virt_mode = 1;
@@ -725,7 +753,15 @@ size_t phs_filtfilt_mid_size(int dtype, int64_t B, int64_t T) {
 int phs_filtfilt_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
                      int coef_shared, int padmode, int64_t padlen, const void *x, void *y, void *mid, void *workspace,
                      size_t workspace_bytes, void *stream) {
+  return phs_filtfilt_fwd_hs(dtype, B, T, b, nb, a, na, coef_shared, padmode, padlen, x, y, mid, nullptr, nullptr,
+                             workspace, workspace_bytes, stream);
+}
+
+int phs_filtfilt_fwd_hs(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
+                        int coef_shared, int padmode, int64_t padlen, const void *x, void *y, void *mid, void *h1,
+                        void *h2, void *workspace, size_t workspace_bytes, void *stream) {
   if (dtype != PHS_F32 && dtype != PHS_F64) return PHS_ERR_DTYPE;
+  if ((h1 == nullptr) != (h2 == nullptr)) return PHS_ERR_INVALID;
   const int M = nb - 1 > na ? nb - 1 : na;
   if (B < 0 || T < 1 || nb < 1 || nb > 5 || na < 1 || na > 4 || padlen < 0 || padlen >= T ||
       padmode < PHS_PAD_CONSTANT || padmode > PHS_PAD_CIRCULAR)
@@ -743,7 +779,8 @@ int phs_filtfilt_fwd(int dtype, int64_t B, int64_t T, const void *b, int nb, con
   f.form = 1;  // TDF-II (ss_filtfilt_entry)
   f.shared = coef_shared != 0;
   return phs::ss_dispatch(dtype, M, [&](auto alg) {
-    return phs::ss_filtfilt<decltype(alg)>(B, T, f, padmode, padlen, x, y, mid, workspace, workspace_bytes, st);
+    return phs::ss_filtfilt<decltype(alg)>(B, T, f, padmode, padlen, x, y, mid, workspace, workspace_bytes, st, h1,
+                                           h2);
   });
 }
 
@@ -762,7 +799,17 @@ int phs_filtfilt_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, con
                      int coef_shared, int padmode, int64_t padlen, const void *x, const void *grad_y, void *grad_x,
                      void *grad_b, void *grad_a, void *scratch, size_t scratch_bytes, void *workspace,
                      size_t workspace_bytes, void *stream) {
+  return phs_filtfilt_bwd_hs(dtype, B, T, b, nb, a, na, coef_shared, padmode, padlen, x, nullptr, nullptr, nullptr,
+                             grad_y, grad_x, grad_b, grad_a, scratch, scratch_bytes, workspace, workspace_bytes,
+                             stream);
+}
+
+int phs_filtfilt_bwd_hs(int dtype, int64_t B, int64_t T, const void *b, int nb, const void *a, int na,
+                        int coef_shared, int padmode, int64_t padlen, const void *x, const void *mid, const void *h1,
+                        const void *h2, const void *grad_y, void *grad_x, void *grad_b, void *grad_a, void *scratch,
+                        size_t scratch_bytes, void *workspace, size_t workspace_bytes, void *stream) {
   if (dtype != PHS_F32 && dtype != PHS_F64) return PHS_ERR_DTYPE;
+  if ((mid == nullptr) != (h1 == nullptr) || (h1 == nullptr) != (h2 == nullptr)) return PHS_ERR_INVALID;
   const int M = nb - 1 > na ? nb - 1 : na;
   if (B < 0 || T < 1 || nb < 1 || nb > 5 || na < 1 || na > 4 || padlen < 0 || padlen >= T ||
       padmode < PHS_PAD_CONSTANT || padmode > PHS_PAD_CIRCULAR)
@@ -782,7 +829,7 @@ int phs_filtfilt_bwd(int dtype, int64_t B, int64_t T, const void *b, int nb, con
   f.shared = coef_shared != 0;
   return phs::ss_dispatch(dtype, M, [&](auto alg) {
     return phs::ss_filtfilt_bwd<decltype(alg)>(B, T, f, padmode, padlen, x, grad_y, grad_x, grad_b, grad_a, scratch,
-                                               scratch_bytes, workspace, workspace_bytes, st);
+                                               scratch_bytes, workspace, workspace_bytes, st, mid, h1, h2);
   });
 }
 

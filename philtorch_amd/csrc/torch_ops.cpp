@@ -635,6 +635,32 @@ void filtfilt_check(const char *op, const Tensor &b, const Tensor &a, const Tens
   TORCH_CHECK(padlen >= 0 && T > padlen, "Input signal length ", T, " must be greater than pad length ", padlen, ".");
 }
 
+// filtfilt that also returns what its coefficient backward would compute
+// again (phs_filtfilt_fwd_hs): (y, mid, h1, h2) with mid pass 1's output and
+// final state (bytes, phs_filtfilt_mid_size) and h1, h2 (batch, T, order)
+// both passes' states.
+std::tuple<Tensor, Tensor, Tensor, Tensor> filtfilt_states_hip(const Tensor &b, const Tensor &a, const Tensor &x,
+                                                               int64_t padmode, int64_t padlen) {
+  filtfilt_check("philtorch::filtfilt_states", b, a, x, padmode, padlen);
+  const int64_t B = x.size(0), T = x.size(1), nb = b.size(-1), na = a.size(-1);
+  const int64_t M = std::max(nb - 1, na);
+  const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(x.device());
+  const int dt = phs_dtype_of(x.scalar_type());
+  Tensor bc = b.contiguous(), ac = a.contiguous(), xc = x.contiguous();
+  Tensor y = at::empty_like(xc, at::MemoryFormat::Contiguous);
+  Tensor mid = at::empty({int64_t(B == 0 ? 0 : phs_filtfilt_mid_size(dt, B, T))}, x.options().dtype(at::kByte));
+  Tensor h1 = at::empty({B, T, M}, x.options()), h2 = at::empty({B, T, M}, x.options());
+  if (B == 0) return {y, mid, h1, h2};
+  void *stream = stream_of(x);
+  const Workspace ws = workspace_for(x, phs_filtfilt_workspace_size(dt, B, T), stream);
+  check_status(phs_filtfilt_fwd_hs(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
+                                   b.dim() == 1 ? 1 : 0, int(padmode), padlen, xc.const_data_ptr(),
+                                   y.mutable_data_ptr(), mid.mutable_data_ptr(), h1.mutable_data_ptr(),
+                                   h2.mutable_data_ptr(), ws.ptr, ws.bytes, stream),
+               "filtfilt_states");
+  return {y, mid, h1, h2};
+}
+
 Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t padmode, int64_t padlen) {
   filtfilt_check("philtorch::filtfilt", b, a, x, padmode, padlen);
   const int64_t B = x.size(0), T = x.size(1), nb = b.size(-1), na = a.size(-1);
@@ -657,7 +683,11 @@ Tensor filtfilt_hip(const Tensor &b, const Tensor &a, const Tensor &x, int64_t p
 // grad_y (batch, time), b, a and x as filtfilt's; grad_b and grad_a are
 // empty unless need_coef (x is read only then: the map is linear in x).
 std::vector<Tensor> filtfilt_backward_hip(const Tensor &b, const Tensor &a, const Tensor &x, const Tensor &grad_y,
-                                          int64_t padmode, int64_t padlen, bool need_coef) {
+                                          int64_t padmode, int64_t padlen, bool need_coef,
+                                          const std::optional<Tensor> &mid, const std::optional<Tensor> &h1,
+                                          const std::optional<Tensor> &h2) {
+  TORCH_CHECK(bool(mid) == bool(h1) && bool(h1) == bool(h2),
+              "philtorch::filtfilt_backward: mid, h1 and h2 come together (filtfilt_states) or not at all");
   filtfilt_check("philtorch::filtfilt_backward", b, a, grad_y, padmode, padlen);
   TORCH_CHECK(x.sizes() == grad_y.sizes() && x.scalar_type() == grad_y.scalar_type() &&
                   x.device() == grad_y.device(),
@@ -676,8 +706,17 @@ std::vector<Tensor> filtfilt_backward_hip(const Tensor &b, const Tensor &a, cons
                              gy.options().dtype(at::kByte));
   void *stream = stream_of(gy);
   const Workspace ws = workspace_for(gy, phs_filtfilt_workspace_size(dt, B, T), stream);
-  check_status(phs_filtfilt_bwd(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
+  const bool kept = need_coef && mid && h1 && h2;
+  if (kept)
+    TORCH_CHECK(mid->numel() == int64_t(phs_filtfilt_mid_size(dt, B, T)) && h1->dim() == 3 && h1->size(0) == B &&
+                    h1->size(1) == T && h1->size(2) == M && h2->sizes() == h1->sizes() &&
+                    h1->scalar_type() == grad_y.scalar_type() && h2->scalar_type() == grad_y.scalar_type() &&
+                    mid->is_contiguous() && h1->is_contiguous() && h2->is_contiguous(),
+                "philtorch::filtfilt_backward: mid, h1, h2 must be filtfilt_states' outputs for these shapes");
+  check_status(phs_filtfilt_bwd_hs(dt, B, T, bc.const_data_ptr(), int(nb), ac.const_data_ptr(), int(na),
                                 b.dim() == 1 ? 1 : 0, int(padmode), padlen, need_coef ? xc.const_data_ptr() : nullptr,
+                                kept ? mid->const_data_ptr() : nullptr, kept ? h1->const_data_ptr() : nullptr,
+                                kept ? h2->const_data_ptr() : nullptr,
                                 gy.const_data_ptr(), gx.mutable_data_ptr(), need_coef ? gb.mutable_data_ptr() : nullptr,
                                 need_coef ? ga.mutable_data_ptr() : nullptr, scratch.mutable_data_ptr(),
                                 size_t(scratch.numel()), ws.ptr, ws.bytes, stream),
@@ -1535,8 +1574,10 @@ TORCH_LIBRARY(philtorch, m) {
         {at::Tag::pt2_compliant_tag});
   // new: zero-phase filtering, filters of second order at most (forward only)
   m.def("filtfilt(Tensor b, Tensor a, Tensor x, int padmode, int padlen) -> Tensor", {at::Tag::pt2_compliant_tag});
-  m.def("filtfilt_backward(Tensor b, Tensor a, Tensor x, Tensor grad_y, int padmode, int padlen, bool need_coef) "
-        "-> Tensor[]",
+  m.def("filtfilt_backward(Tensor b, Tensor a, Tensor x, Tensor grad_y, int padmode, int padlen, bool need_coef, "
+        "Tensor? mid=None, Tensor? h1=None, Tensor? h2=None) -> Tensor[]",
+        {at::Tag::pt2_compliant_tag});
+  m.def("filtfilt_states(Tensor b, Tensor a, Tensor x, int padmode, int padlen) -> (Tensor, Tensor, Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
   // new: single-input single-output LTI state space of order <= 4, fused: (y, zf)
   m.def("lti_ss(Tensor A, Tensor? B, Tensor? C, Tensor? D, Tensor? zi, Tensor x, int out_idx, bool reverse=False) -> (Tensor, Tensor)",
@@ -1592,6 +1633,7 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("sosfilt_backward", &sosfilt_backward_hip);
   m.impl("filtfilt", &filtfilt_hip);
   m.impl("filtfilt_backward", &filtfilt_backward_hip);
+  m.impl("filtfilt_states", &filtfilt_states_hip);
   m.impl("biquad", &biquad_hip);
   m.impl("biquad_backward", &biquad_backward_hip);
   m.impl("biquad_cols", &biquad_cols_hip);

@@ -307,10 +307,17 @@ def _fused_filtfilt(b: Tensor, a: Tensor, x: Tensor, padmode: Optional[str], edg
     """filtfilt of a filter of order 4 at most through philtorch::filtfilt."""
     x2 = x.reshape(-1, x.size(-1))
     code = _PAD_CODES[padmode] if padmode is not None else 0
-    from .. import _op_ctx
+    from .. import _has_op, _op_ctx
 
+    # b or a with a gradient to come: the forward keeps pass 1's output and
+    # both passes' states (filtfilt_states), which their backward would
+    # compute again
+    keep = torch.is_grad_enabled() and (b.requires_grad or a.requires_grad) and _has_op("filtfilt_states")
     with _op_ctx(b, a, x2):
-        y = torch.ops.philtorch.filtfilt(b, a, x2, code, edge if padmode is not None else 0)
+        if keep:
+            y = torch.ops.philtorch.filtfilt_states(b, a, x2, code, edge if padmode is not None else 0)[0]
+        else:
+            y = torch.ops.philtorch.filtfilt(b, a, x2, code, edge if padmode is not None else 0)
     return y.reshape(x.shape)
 
 

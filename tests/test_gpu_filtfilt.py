@@ -511,6 +511,17 @@ def test_filtfilt_op_gradcheck(hip):
             f3 = lambda b_, a_, x_: torch.ops.philtorch.filtfilt(b_, a_, x_, mode, padlen)  # noqa: E731
             assert torch.autograd.gradcheck(f3, (bg, ag, x))
             assert torch.autograd.gradcheck(f3, (bg, a, x.detach()))
+            # the states-keeping forward (what lti.filtfilt takes with coefficient gradients)
+            fs = lambda b_, a_, x_: torch.ops.philtorch.filtfilt_states(b_, a_, x_, mode, padlen)[0]  # noqa: E731
+            assert torch.autograd.gradcheck(fs, (bg, ag, x))
+            # its kept buffers give the coefficient backward's results bit for bit
+            y0 = torch.ops.philtorch.filtfilt(b, a, x.detach(), mode, padlen)
+            ys, mid, h1, h2 = torch.ops.philtorch.filtfilt_states(b, a, x.detach(), mode, padlen)
+            torch.testing.assert_close(ys, y0, rtol=1e-12, atol=1e-12)
+            gy = torch.randn_like(y0)
+            r0 = torch.ops.philtorch.filtfilt_backward(b, a, x.detach(), gy, mode, padlen, True)
+            r1 = torch.ops.philtorch.filtfilt_backward(b, a, x.detach(), gy, mode, padlen, True, mid, h1, h2)
+            assert all(torch.equal(u, v) for u, v in zip(r0, r1))
         # second order runs the composed route, whose F.pad backward accumulates with atomics on the GPU
         # (run-to-run differences of ~1e-11 relative on gradients up to ~1e4)
         assert torch.autograd.gradgradcheck(f3, (bg, ag, x), nondet_tol=1e-7)
@@ -538,6 +549,8 @@ def test_filtfilt_opcheck(hip):
     x = torch.tensor(g.standard_normal((2, 700)).astype(np.float32), device="cuda")
     b, a = sos[0, :3].contiguous(), sos[0, 4:].contiguous()
     torch.library.opcheck(torch.ops.philtorch.filtfilt.default, (b, a, x, 1, 9),
+                          test_utils=("test_schema", "test_faketensor"))
+    torch.library.opcheck(torch.ops.philtorch.filtfilt_states.default, (b, a, x, 1, 9),
                           test_utils=("test_schema", "test_faketensor"))
     torch.library.opcheck(torch.ops.philtorch.filtfilt.default,
                           (b.expand(2, 3).contiguous(), a[:1].expand(2, 1).contiguous(), x, 2, 0),
