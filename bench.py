@@ -501,21 +501,23 @@ class FiltfiltGrad(FiltfiltApi):
 
 class FiltfiltCoefGrad(FiltfiltGrad):
     """c4_filtfilt_coef: c4_filtfilt with the gradients w.r.t. x and every
-    section's b and a.  Each filtfilt's backward is philtorch::
-    filtfilt_backward's coefficient mode: pass 1 again keeping its states
-    and output, pass 2 keeping its states, the two adjoint passes with the
-    model's gradient sums, the pads' sums and the steady state's in the
-    per-row kernels, the chain rule to b and a."""
+    section's b and a.  Each filtfilt's forward keeps pass 1's output and
+    both passes' states (philtorch::filtfilt_states); its backward is
+    philtorch::filtfilt_backward's coefficient mode given them: the two
+    adjoint passes with the model's gradient sums, the pads' sums and the
+    steady state's in the per-row kernels, the chain rule to b and a."""
 
     def __init__(self):
         super().__init__()
         self.name = "c4_filtfilt_coef"
         self.metric = (f"GSamples/s fwd+bwd(x, b, a), lti.filtfilt x{self.S} sections (replicate, padlen 9) "
                        f"B={self.B} T={self.T} fp32 (API)")
-        # per filtfilt backward: pass 1 reads x, writes y1 and 2 states (16 B); pass 2 reads y1, writes 2 states
-        # (12 B); each adjoint reads its input, 2 states and the forward's input, writes its output (20 B)
-        self.bwd_bytes = 68 * self.B * self.T
-        self.bwd_launch_bytes = 16 * self.B * self.T  # pass 1 again: read x, write y1 and the states
+        # per filtfilt: each forward pass also writes its 2 states (8 B more each); backward: each adjoint
+        # reads its input, 2 states and the forward's input, writes its output (20 B)
+        self.fwd_bytes += 16 * self.B * self.T
+        self.fwd_launch_bytes = 16 * self.B * self.T  # pass 1: read x, write y1 and its states
+        self.bwd_bytes = 40 * self.B * self.T
+        self.bwd_launch_bytes = 20 * self.B * self.T  # pass 2's adjoint
 
     def step_fwd(self):
         from philtorch_amd import lti
