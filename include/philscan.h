@@ -675,6 +675,18 @@ int phs_lpv_mimo_ss(int dtype, int M, int F, int P, int64_t B, int64_t T, const 
                     const void *Bm, const void *Cm, const void *Dm, int shared, const void *zi, const void *x,
                     void *y, void *zf, int reverse, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- phs_lpv_mimo_ss that also writes hs [B,T,M], the state before every
+ * step, in the same pass (no counterpart in the reference, whose autograd
+ * saves the composed route's tensors; philtorch/lpv/ssm.py:337-581): the
+ * states the coefficient gradients read (phs_mimo_ss_grad_sums), so a
+ * caller need not run the model again with C the identity.  Needs
+ * P + M <= 4 (the states take output planes); y, zf as phs_lpv_mimo_ss's
+ * bit for bit. */
+int phs_lpv_mimo_ss_hs(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *A, int A_flags,
+                       const void *Bm, const void *Cm, const void *Dm, int shared, const void *zi, const void *x,
+                       void *y, void *zf, void *hs, int reverse, void *workspace, size_t workspace_bytes,
+                       void *stream);
+
 /* ---- The coefficient gradients of phs_mimo_ss_fwd summed over time in one
  * pass (no counterpart in the reference, whose autograd forms them as
  * matmuls over the composed route's tensors; philtorch/lti/ssm.py:460-589):

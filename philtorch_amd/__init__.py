@@ -1029,7 +1029,11 @@ if EXTENSION_LOADED and _has_op("lpv_mimo_ss"):
     def _lpv_mimo_ss_setup(ctx, inputs, output):
         ctx.reverse = bool(inputs[6]) if len(inputs) > 6 else False
         ctx.transpose_A = bool(inputs[7]) if len(inputs) > 7 else False
-        ctx.save_for_backward(*inputs[:6])
+        # lpv_mimo_ss_states: the forward's states too, for the coefficient backward
+        hs = output[2] if len(output) > 2 else None
+        if hs is not None:
+            ctx.mark_non_differentiable(hs)
+        ctx.save_for_backward(*inputs[:6], hs)
         ctx.set_materialize_grads(False)
 
     def _lpv_mimo_ss_backward(ctx, gy, gzf):
@@ -1048,7 +1052,8 @@ if EXTENSION_LOADED and _has_op("lpv_mimo_ss"):
         recomputed from the inputs and differentiable again."""
         from .lpv.ssm import _lpv_mimo_composite
 
-        inputs = ctx.saved_tensors
+        saved = ctx.saved_tensors
+        inputs, kept_hs = saved[:6], saved[6]
         A, B, C, D, zi, x = inputs
         needs = ctx.needs_input_grad
         out = [None] * 8
@@ -1082,7 +1087,8 @@ if EXTENSION_LOADED and _has_op("lpv_mimo_ss"):
                 out[4] = gzi if needs[4] and zi is not None else None
             hs = lam = None
             if needs[0] or needs[2]:
-                hs, _ = op(A, B, eye, None, zi, x, rev, tr)
+                # the forward's states, kept by lpv_mimo_ss_states or computed again
+                hs = kept_hs if kept_hs is not None else op(A, B, eye, None, zi, x, rev, tr)[0]
             if lam_pass:
                 lam, gzi = op(A, Ct, eye, None, gzf, g, not rev, not tr)
                 out[4] = gzi if needs[4] and zi is not None else None
@@ -1104,6 +1110,22 @@ if EXTENSION_LOADED and _has_op("lpv_mimo_ss"):
 
     torch.library.register_autograd("philtorch::lpv_mimo_ss", _lpv_mimo_ss_backward,
                                     setup_context=_lpv_mimo_ss_setup)
+
+    if _has_op("lpv_mimo_ss_states"):
+
+        @torch.library.register_fake("philtorch::lpv_mimo_ss_states")
+        def _(A, B, C, D, zi, x, reverse=False, transpose_A=False):
+            M = A.shape[-1]
+            return (x.new_empty((x.shape[0], x.shape[1], C.shape[-2])), x.new_empty((x.shape[0], M)),
+                    x.new_empty((x.shape[0], x.shape[1], M)))
+
+        def _lpv_mimo_ss_states_backward(ctx, gy, gzf, ghs):
+            """lpv_mimo_ss's backward with the states the forward kept (hs is
+            not differentiable): no states pass."""
+            return _lpv_mimo_ss_backward(ctx, gy, gzf)
+
+        torch.library.register_autograd("philtorch::lpv_mimo_ss_states", _lpv_mimo_ss_states_backward,
+                                        setup_context=_lpv_mimo_ss_setup)
 
 from . import mat  # noqa: E402,F401
 from . import lti  # noqa: E402,F401

@@ -489,11 +489,12 @@ size_t lpv_mimo_ws_bytes(int64_t B, int64_t T) {
 template <class Alg>
 int lpv_mimo_ss(int F, int P, int64_t B, int64_t T, const void *A, int A_flags, const void *Bm, const void *Cm,
                 const void *Dm, int shared, const void *zi, const void *x, void *y, void *zf, void *workspace,
-                size_t ws_bytes, bool rev, hipStream_t stream) {
+                size_t ws_bytes, bool rev, hipStream_t stream, void *hs = nullptr) {
   using E = typename Alg::elem;
   using Sh = LpvMimoShape<Alg>;
   constexpr int M = SsView<Alg>::M;
   if (B < 0 || T < 0 || F < 1 || F > kMimoMaxIO || P < 1 || P > kMimoMaxIO) return PHS_ERR_INVALID;
+  if (hs && P + M > kMimoMaxIO) return PHS_ERR_INVALID;  // the states share the outputs' LDS planes
   if ((shared & ~(PHS_MIMO_B_SHARED | PHS_MIMO_C_SHARED | PHS_MIMO_D_SHARED)) ||
       (A_flags & ~(PHS_LPV_A_SHARED | PHS_LPV_A_TRANSPOSED)))
     return PHS_ERR_INVALID;
@@ -527,6 +528,8 @@ int lpv_mimo_ss(int F, int P, int64_t B, int64_t T, const void *A, int A_flags, 
   a.P = P;
   a.f_magic = io_magic(F);
   a.p_magic = io_magic(P);
+  a.hs = static_cast<E *>(hs);
+  a.m_magic = io_magic(M);
   a.zi = static_cast<const E *>(zi);
   a.x = static_cast<const E *>(x);
   a.y = static_cast<E *>(y);
@@ -543,10 +546,16 @@ int lpv_mimo_ss(int F, int P, int64_t B, int64_t T, const void *A, int A_flags, 
   a.spin_limit = sl ? sl : kDefaultSpinLimit;
   a.agg_only = g_agg_only.load(std::memory_order_relaxed) ? 1u : 0u;
   const dim3 grid(a.per_stripe * kStripes), block(Sh::kThreads);
-  if (rev)
+  if (hs) {
+    if (rev)
+      launch_kernel((lpv_mimo_kernel<Alg, true, true>), grid, block, 0, stream, a);
+    else
+      launch_kernel((lpv_mimo_kernel<Alg, false, true>), grid, block, 0, stream, a);
+  } else if (rev) {
     launch_kernel((lpv_mimo_kernel<Alg, true>), grid, block, 0, stream, a);
-  else
+  } else {
     launch_kernel((lpv_mimo_kernel<Alg, false>), grid, block, 0, stream, a);
+  }
   return hipGetLastError() == hipSuccess ? PHS_OK : PHS_ERR_LAUNCH;
 }
 
@@ -615,10 +624,18 @@ size_t phs_lpv_mimo_ss_workspace_size(int dtype, int M, int64_t B, int64_t T) {
 int phs_lpv_mimo_ss(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *A, int A_flags,
                     const void *Bm, const void *Cm, const void *Dm, int shared, const void *zi, const void *x,
                     void *y, void *zf, int reverse, void *workspace, size_t workspace_bytes, void *stream) {
+  return phs_lpv_mimo_ss_hs(dtype, M, F, P, B, T, A, A_flags, Bm, Cm, Dm, shared, zi, x, y, zf, nullptr, reverse,
+                            workspace, workspace_bytes, stream);
+}
+
+int phs_lpv_mimo_ss_hs(int dtype, int M, int F, int P, int64_t B, int64_t T, const void *A, int A_flags,
+                       const void *Bm, const void *Cm, const void *Dm, int shared, const void *zi, const void *x,
+                       void *y, void *zf, void *hs, int reverse, void *workspace, size_t workspace_bytes,
+                       void *stream) {
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return phs::mimo_dispatch(dtype, M, [&](auto alg) {
     return phs::lpv_mimo_ss<decltype(alg)>(F, P, B, T, A, A_flags, Bm, Cm, Dm, shared, zi, x, y, zf, workspace,
-                                           workspace_bytes, reverse != 0, st);
+                                           workspace_bytes, reverse != 0, st, hs);
   });
 }
 

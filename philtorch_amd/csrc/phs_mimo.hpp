@@ -49,6 +49,10 @@ struct MimoArgs {
   int64_t d_stride;
   int F, P;
   uint64_t f_magic, p_magic;  // ceil(2^32 / F), ceil(2^32 / P): e / F = (e * f_magic) >> 32 for small e
+  // lpv_mimo_kernel: the state before every step [B, T, M] as well
+  // (nullable; P + M <= kMimoMaxIO planes), m_magic = ceil(2^32 / M)
+  E *hs;
+  uint64_t m_magic;
   const E *zi;  // [B, M]; nullptr: zeros
   const E *x;   // [B, T, F]
   E *y;         // [B, T, P]
@@ -539,7 +543,9 @@ __device__ __noinline__ typename Alg::state lpv_mimo_prefix_fallback(const MimoA
   return apply<Alg>(acc, virt);
 }
 
-template <class Alg, bool REV>
+// HS: also the state before every step into a.hs (a separate instance, so
+// the plain forward carries none of it).
+template <class Alg, bool REV, bool HS = false>
 __global__ __launch_bounds__(LpvMimoShape<Alg>::kThreads, LpvMimoShape<Alg>::kMinWaves) void lpv_mimo_kernel(
     MimoArgs<Alg> a) {
   using E = typename Alg::elem;
@@ -649,6 +655,15 @@ __global__ __launch_bounds__(LpvMimoShape<Alg>::kThreads, LpvMimoShape<Alg>::kMi
         io[p * kP + lane * K + k] = o;
       }
     }
+    if constexpr (HS) {  // the state before the step into planes P.., the lane's own (already read) slots
+      union {
+        SS s;
+        E e[V::M];
+      } hu;
+      hu.s = h;
+#pragma unroll
+      for (int i = 0; i < V::M; ++i) io[(a.P + i) * kP + lane * K + k] = hu.e[i];
+    }
     h = Alg::s_affine(Ak[k], h, X[k]);
     if (a.zf && l0 + k == T - 1) {
       union {
@@ -662,6 +677,7 @@ __global__ __launch_bounds__(LpvMimoShape<Alg>::kThreads, LpvMimoShape<Alg>::kMi
   }
   wave_sync();  // the span's outputs are in the planes
   mimo_stage_out<Alg, REV, Sh>(a.y + b * T * a.P, s0, T, a.P, a.p_magic, io, lane);
+  if constexpr (HS) mimo_stage_out<Alg, REV, Sh>(a.hs + b * T * V::M, s0, T, V::M, a.m_magic, io + a.P * kP, lane);
 }
 
 }  // namespace phs

@@ -1205,9 +1205,10 @@ std::vector<Tensor> lpv_ss_backward_hip(const Tensor &A, const std::optional<Ten
 // D None, (P, F) or (batch, P, F); zi None or (batch, M); y (batch, T, P).
 // reverse runs the model backwards in time; transpose_A uses A[t]^T (the
 // adjoint model, read without a transposed copy).
-std::tuple<Tensor, Tensor> lpv_mimo_ss_hip(const Tensor &A, const Tensor &Bm, const Tensor &Cm,
-                                           const std::optional<Tensor> &Dm, const std::optional<Tensor> &zi,
-                                           const Tensor &x, bool reverse, bool transpose_A) {
+std::tuple<Tensor, Tensor, Tensor> lpv_mimo_ss_impl(const Tensor &A, const Tensor &Bm, const Tensor &Cm,
+                                                    const std::optional<Tensor> &Dm,
+                                                    const std::optional<Tensor> &zi, const Tensor &x, bool reverse,
+                                                    bool transpose_A, bool keep_states) {
   TORCH_CHECK(x.dim() == 3, "philtorch::lpv_mimo_ss: x must be a 3D tensor (batch, time, features)");
   const int64_t B = x.size(0), T = x.size(1), F = x.size(2);
   TORCH_CHECK((A.dim() == 3 || A.dim() == 4) && A.size(-1) == A.size(-2) && A.size(-3) == T,
@@ -1246,22 +1247,42 @@ std::tuple<Tensor, Tensor> lpv_mimo_ss_hip(const Tensor &A, const Tensor &Bm, co
   Tensor dc = Dm ? Dm->contiguous() : Tensor(), zc = zi ? zi->contiguous() : Tensor();
   Tensor y = at::empty({B, T, P}, x.options());
   Tensor zf = at::empty({B, M}, x.options());
-  if (B == 0) return {y, zf};
+  Tensor hs = at::empty({keep_states ? B : 0, keep_states ? T : 0, M}, x.options());
+  if (keep_states)
+    TORCH_CHECK(P + M <= 4, "philtorch::lpv_mimo_ss_states: outputs plus states at most 4 per step, got ", P, " + ", M);
+  if (B == 0) return {y, zf, hs};
   if (T == 0) {
     if (zi) zf.copy_(zc); else zf.zero_();
-    return {y, zf};
+    return {y, zf, hs};
   }
   const int A_flags = (A.dim() == 3 ? PHS_LPV_A_SHARED : 0) | (transpose_A ? PHS_LPV_A_TRANSPOSED : 0);
   const int shared = (Bm.dim() == 2 ? PHS_MIMO_B_SHARED : 0) | (Cm.dim() == 2 ? PHS_MIMO_C_SHARED : 0) |
                      (Dm && Dm->dim() == 2 ? PHS_MIMO_D_SHARED : 0);
   void *stream = stream_of(x);
   const Workspace ws = workspace_for(x, phs_lpv_mimo_ss_workspace_size(dt, int(M), B, T), stream);
-  check_status(phs_lpv_mimo_ss(dt, int(M), int(F), int(P), B, T, Ac.const_data_ptr(), A_flags, bc.const_data_ptr(),
-                               cc.const_data_ptr(), Dm ? dc.const_data_ptr() : nullptr, shared,
-                               zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(), y.mutable_data_ptr(),
-                               zf.mutable_data_ptr(), reverse ? 1 : 0, ws.ptr, ws.bytes, stream),
+  check_status(phs_lpv_mimo_ss_hs(dt, int(M), int(F), int(P), B, T, Ac.const_data_ptr(), A_flags,
+                                  bc.const_data_ptr(), cc.const_data_ptr(), Dm ? dc.const_data_ptr() : nullptr, shared,
+                                  zi ? zc.const_data_ptr() : nullptr, xc.const_data_ptr(), y.mutable_data_ptr(),
+                                  zf.mutable_data_ptr(), keep_states ? hs.mutable_data_ptr() : nullptr,
+                                  reverse ? 1 : 0, ws.ptr, ws.bytes, stream),
                "lpv_mimo_ss");
+  return {y, zf, hs};
+}
+
+std::tuple<Tensor, Tensor> lpv_mimo_ss_hip(const Tensor &A, const Tensor &Bm, const Tensor &Cm,
+                                           const std::optional<Tensor> &Dm, const std::optional<Tensor> &zi,
+                                           const Tensor &x, bool reverse, bool transpose_A) {
+  auto [y, zf, hs] = lpv_mimo_ss_impl(A, Bm, Cm, Dm, zi, x, reverse, transpose_A, false);
   return {y, zf};
+}
+
+// lpv_mimo_ss that also returns hs (batch, T, M), the state before every
+// step (the states the coefficient gradients read), from the same pass.
+std::tuple<Tensor, Tensor, Tensor> lpv_mimo_ss_states_hip(const Tensor &A, const Tensor &Bm, const Tensor &Cm,
+                                                          const std::optional<Tensor> &Dm,
+                                                          const std::optional<Tensor> &zi, const Tensor &x,
+                                                          bool reverse, bool transpose_A) {
+  return lpv_mimo_ss_impl(A, Bm, Cm, Dm, zi, x, reverse, transpose_A, true);
 }
 
 // The coefficient gradients of mimo_ss summed over time in one pass
@@ -1616,6 +1637,9 @@ TORCH_LIBRARY(philtorch, m) {
   m.def("lpv_mimo_ss(Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? zi, Tensor x, bool reverse=False, "
         "bool transpose_A=False) -> (Tensor, Tensor)",
         {at::Tag::pt2_compliant_tag});
+  m.def("lpv_mimo_ss_states(Tensor A, Tensor B, Tensor C, Tensor? D, Tensor? zi, Tensor x, bool reverse=False, "
+        "bool transpose_A=False) -> (Tensor, Tensor, Tensor)",
+        {at::Tag::pt2_compliant_tag});
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
@@ -1650,6 +1674,7 @@ TORCH_LIBRARY_IMPL(philtorch, CUDA, m) {
   m.impl("mimo_ss", &mimo_ss_hip);
   m.impl("mimo_ss_grad_sums", &mimo_ss_grad_sums_hip);
   m.impl("lpv_mimo_ss", &lpv_mimo_ss_hip);
+  m.impl("lpv_mimo_ss_states", &lpv_mimo_ss_states_hip);
 }
 
 TORCH_LIBRARY_IMPL(philtorch, CPU, m) {

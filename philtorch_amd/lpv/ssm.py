@@ -626,11 +626,19 @@ def state_space(
         return (y, zf) if return_zf else y
     mops = _lpv_mimo_operands(x, B, C, D, out_idx, batch, N, M) if native else None
     if _lpv_mimo_applies(A, x, zi if return_zf else None, mops, native):
-        from .. import _op_ctx
+        from .. import _has_op, _op_ctx
 
         x3, Bm, Cm, Dm, vec = mops
+        # a coefficient with a gradient to come: the forward keeps its states
+        # (lpv_mimo_ss_states, where outputs and states fit four planes)
+        keep = (torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (A, Bm, Cm, Dm))
+                and Cm.size(-2) + M <= 4 and _has_op("lpv_mimo_ss_states"))
         with _op_ctx(A, Bm, Cm, Dm, zi, x3):
-            y, zf = torch.ops.philtorch.lpv_mimo_ss(A, Bm, Cm, Dm, zi.contiguous() if return_zf else None, x3)
+            args = (A, Bm, Cm, Dm, zi.contiguous() if return_zf else None, x3)
+            if keep:
+                y, zf, _ = torch.ops.philtorch.lpv_mimo_ss_states(*args)
+            else:
+                y, zf = torch.ops.philtorch.lpv_mimo_ss(*args)
         y = y.squeeze(-1) if vec else y
         return (y, zf) if return_zf else y
     Bx = _apply_B(x, B, batch, N, M, features)

@@ -273,3 +273,35 @@ def test_lpv_mimo_ss_gradcheck_and_opcheck(hip):
     f32 = lambda v: v.detach().float()  # noqa: E731
     torch.library.opcheck(op.default, tuple(f32(v) for v in (A, Bm, Cm, Dm, zi, x)))
     torch.library.opcheck(op.default, (f32(A[0]), f32(Bm), f32(Cm[0]), None, None, f32(x), True, True))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64], ids=lambda d: np.dtype(d).name)
+@pytest.mark.parametrize("M,F,P", [(1, 2, 3), (2, 2, 2), (2, 3, 1), (3, 1, 1)])
+@pytest.mark.parametrize("rev,trans", [(False, False), (True, False), (False, True)])
+def test_lpv_mimo_ss_states_op(hip, dtype, M, F, P, rev, trans):
+    """philtorch::lpv_mimo_ss_states (phs_lpv_mimo_ss_hs): y and zf bit for
+    bit lpv_mimo_ss's, hs bit for bit the states pass the coefficient
+    backward would run (the model again with C the identity, no D), across
+    spans and tiles; gradcheck of its (y, zf) and opcheck."""
+    import torch
+
+    g = D.rng(D.seed_of("lpv-mimo-states", np.dtype(dtype).name, M, F, P, rev, trans))
+    Bn, T = 3, 5003
+    t = lambda v: torch.tensor(np.ascontiguousarray(v, dtype=dtype), device="cuda")  # noqa: E731
+    A = t(_contractive_A(g, (Bn,), T, M))
+    Bm, Cm, Dm = t(g.standard_normal((M, F))), t(g.standard_normal((Bn, P, M))), t(g.standard_normal((P, F)))
+    zi, x = t(g.standard_normal((Bn, M))), t(g.standard_normal((Bn, T, F)))
+    print(f"lpv_mimo_ss_states {np.dtype(dtype).name} M={M} F={F} P={P} rev={rev} trans={trans}", flush=True)
+    y0, zf0 = torch.ops.philtorch.lpv_mimo_ss(A, Bm, Cm, Dm, zi, x, rev, trans)
+    y1, zf1, hs = torch.ops.philtorch.lpv_mimo_ss_states(A, Bm, Cm, Dm, zi, x, rev, trans)
+    eye = torch.eye(M, dtype=x.dtype, device="cuda")
+    h_ref, _ = torch.ops.philtorch.lpv_mimo_ss(A, Bm, eye, None, zi, x, rev, trans)
+    assert torch.equal(y0, y1) and torch.equal(zf0, zf1) and torch.equal(hs, h_ref)
+    if dtype == np.float64:
+        small = [v.detach()[:, :40].contiguous() if v.dim() == 3 and v.size(1) == T else v.detach()
+                 for v in (A, Bm, Cm, Dm, zi, x)]
+        small[0] = small[0][:, :40].contiguous()
+        leaves = [v.clone().requires_grad_(True) for v in small]
+        f = lambda *a: torch.ops.philtorch.lpv_mimo_ss_states(*a, rev, trans)[:2]  # noqa: E731
+        assert torch.autograd.gradcheck(f, tuple(leaves))
+        torch.library.opcheck(torch.ops.philtorch.lpv_mimo_ss_states.default, (*small, rev, trans))
