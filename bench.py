@@ -993,10 +993,11 @@ class LpvMimoGrad(LpvMimoApi):
 
 class LpvMimoCoefGrad(LpvMimoGrad):
     """c3_lpv_mimo_coef: c3_lpv_mimo_grad with the gradients of A[t], B, C and
-    D too: the forward again writing its states, the adjoint writing its
-    states (which also gives grad_zi), and one philtorch::mimo_ss_grad_sums
-    pass writing dL/dA[t] = lambda[t+1] h[t]^T and grad_x = B^T lambda + D^T
-    g per step and summing over time for B, C, D."""
+    D too: the forward keeps its states (philtorch::lpv_mimo_ss_states), the
+    adjoint writes its states (which also gives grad_zi), and one
+    philtorch::mimo_ss_grad_sums pass writes dL/dA[t] = lambda[t+1] h[t]^T
+    and grad_x = B^T lambda + D^T g per step and sums over time for B, C,
+    D."""
 
     def __init__(self):
         super().__init__()
@@ -1004,10 +1005,11 @@ class LpvMimoCoefGrad(LpvMimoGrad):
         self.name = "c3_lpv_mimo_coef"
         self.metric = (f"GSamples/s fwd+bwd(x, zi, A, B, C, D), LPV lpv.state_space order 2, 2 inputs, 2 outputs "
                        f"per step B={B} T={T} fp32 (API)")
-        # states and adjoint-states passes (32 each: A, one signal in, one out), the sums pass (read
-        # lambda, h, x, g: 32; write dL/dA[t]: 16, grad_x: 8)
-        self.bwd_bytes = (32 + 32 + 56) * B * T
-        self.bwd_launch_bytes = 32 * B * T  # the states pass
+        # the forward also writes its 2 states (8); backward: the adjoint-states pass (32: A, g in,
+        # lambda out) and the sums pass (read lambda, h, x, g: 32; write dL/dA[t]: 16, grad_x: 8)
+        self.fwd_bytes += 8 * B * T
+        self.bwd_bytes = (32 + 56) * B * T
+        self.bwd_launch_bytes = 32 * B * T  # the adjoint-states pass
 
     def step_fwd(self):
         from philtorch_amd import lpv
